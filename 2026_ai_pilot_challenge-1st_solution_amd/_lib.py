@@ -1,0 +1,68 @@
+"""ctypes binding of libf16hip.so (C ABI declared in include/f16_fdm.h).
+
+torch is imported first so that the process's HIP runtime is torch's; the library then binds
+to that same runtime (libamdhip64.so.7) and launches on torch's streams.  There is no CPU
+fallback: if the library is missing or fails to load, every call raises.
+"""
+import ctypes
+import os
+
+import torch  # noqa: F401  (loads the HIP runtime the library binds to)
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libf16hip.so")
+
+F16_EINVAL = -1
+F16_ERATE = -2
+F16_ETOOBIG = -3
+
+_vp, _i, _l, _d = ctypes.c_void_p, ctypes.c_int, ctypes.c_long, ctypes.c_double
+_SIGNATURES = {
+    "f16_fdm_step_batch": (_i, [_vp, _l, _vp, _i, _i, _i, _vp, _l, _vp]),
+    "f16_seed_batch": (_i, [_vp, _i, _i, _vp, _l, _vp, _vp]),
+    "f16_fdm_kernel_info": (_i, [_i, ctypes.POINTER(_i)]),
+}
+
+_lib = None
+
+
+def lib():
+    """Load (once) and return the library; raise if it is not built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with __graft_entry__.build() or "
+                "python -m <package>.build; there is no CPU fallback")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def exported_symbols():
+    return sorted(_SIGNATURES)
+
+
+def check(rc, what):
+    """Map a C-ABI return code to the reference's error classes (cuda_rt.py:36-44)."""
+    if rc == 0:
+        return
+    if rc == F16_EINVAL:
+        raise ValueError(f"{what}: invalid size, stride or pointer")
+    if rc == F16_ERATE:
+        raise ValueError(f"{what}: unsupported FCS rate (120 or 60 Hz)")
+    if rc == F16_ETOOBIG:
+        raise ValueError(f"{what}: size exceeds the entry point's limit")
+    raise RuntimeError(f"HIP error {-(rc + 1000)} in {what}")
+
+
+def ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def stream_handle(device=None):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)

@@ -1,0 +1,50 @@
+"""Build the HIP library (libf16hip.so) in-tree for gfx950.
+
+Compiled with hipcc straight from csrc/; no torch extension machinery, no JIT cache: the .so
+sits next to this file so that it travels with the repository snapshot to the GPU box.
+
+Flags:
+  -ffp-contract=off    keep every add and multiply separately rounded (parity with the
+                       reference's --fmad=false build and with the CPU restatement);
+  -packed-fp32-ops off no packed FP32 instructions (they are avoided on this fleet).
+"""
+import os
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+CSRC = os.path.join(HERE, "csrc")
+ROOT = os.path.dirname(HERE)
+LIB = os.path.join(HERE, "libf16hip.so")
+SOURCES = ["fdm_kernels.hip"]
+ARCH = os.environ.get("F16_OFFLOAD_ARCH", "gfx950")
+
+
+def hipcc():
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", "hipcc"):
+        if cand and (os.path.sep not in cand or os.path.exists(cand)):
+            return cand
+    raise RuntimeError("hipcc not found")
+
+
+def build(verbose=False):
+    """Compile every HIP source into libf16hip.so (always recompiles)."""
+    srcs = [os.path.join(CSRC, s) for s in SOURCES]
+    tmp = LIB + ".tmp"
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
+           "-ffp-contract=off", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+           "-I", os.path.join(ROOT, "include"), "-I", CSRC, "-o", tmp] + srcs
+    if verbose:
+        cmd.append("-Rpass-analysis=kernel-resource-usage")
+    p = subprocess.run(cmd, capture_output=True, text=True)
+    if p.returncode != 0:
+        sys.stderr.write(p.stdout + p.stderr)
+        raise RuntimeError("hipcc failed building libf16hip.so")
+    if verbose:
+        sys.stderr.write("\n".join(l for l in p.stderr.splitlines() if "remark" in l) + "\n")
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(verbose="-v" in sys.argv))

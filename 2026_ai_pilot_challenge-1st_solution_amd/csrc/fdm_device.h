@@ -1,0 +1,695 @@
+// fdm_device.h -- device-side F-16 six-degree-of-freedom model for gfx950.
+//
+// One lane owns one aircraft.  Its integrator state lives in VGPRs for all substeps of a
+// launch; the aero/engine/FCS/ISA tables are one flat image staged in LDS per workgroup.
+// The model is the reference's JSBSim-v1.0.0 restatement (cuda_fdm/ref, model order of
+// cuda_fdm/ref/jsb_fdm.py:212-244): propagate -> kinematics -> atmosphere -> mass -> FCS ->
+// auxiliary -> engine -> aero -> gravity -> accelerations.
+//
+// Numerics.  All arithmetic is IEEE double with contraction disabled (-ffp-contract=off).
+// Where the reference evaluates a trigonometric function of an angle that was itself produced
+// by atan2/asin from a vector, this code uses the vector ratio directly (e.g. sin(atan2(z,rxy))
+// = z/r, cos(alpha) = u/sqrt(u^2+w^2)); the angles are still produced wherever they are state
+// or output.  These substitutions change results at the last-ulp level only (the per-step
+// tolerance against the CPU restatement is 1e-10 relative).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "f16_model_gen.h"
+#include "f16_state.h"
+
+// Every model function is host+device so the identical algorithm can also be built for the CPU
+// (debugging and unit checks); the kernels are the only production callers.
+#define F16_HD __host__ __device__ __forceinline__
+
+namespace f16 {
+
+// ------------------------------------------------------------------ constants
+constexpr double kDt = 1.0 / 60.0;                 // integration step (jsb_fdm.py:18)
+constexpr double kRot = 0.00007292115;             // Earth rotation, rad/s (jsb_frames.py:14)
+constexpr double kSemiMajor = 20925646.32546;      // WGS84 a, ft (jsb_frames.py:10)
+constexpr double kGM = 14.0764417572E15;           // ft^3/s^2 (jsb_frames.py:12)
+constexpr double kJ2 = 1.08262982E-03;             // (jsb_frames.py:13)
+constexpr double kInToFt = 1.0 / 12;               // jsb_const.py:10
+constexpr double kLbToSlug = 1.0 / 32.174049;      // jsb_const.py:13
+constexpr double kEarthRadiusIsa = F16M_EARTH_RADIUS_ISA;
+constexpr double kHbMac = 765.0;                   // aero/h_b-mac-ft (jsb_fdm.py:86)
+constexpr double kGearForce = 0.30;                // externally forced gear position (jsb_fdm.py:84)
+
+// ------------------------------------------------------------------ table interpolation
+// Bracket for a 1-D table: value = f * (y[hi] - y[lo]) + y[lo].  Keys at or beyond the ends
+// select the end value exactly (lo = hi, f = 0), as the reference's Table1D does.
+struct F16Br1 { int lo, hi; double f; };
+// Bracket for one axis of a 2-D table: upper index r in [1, n-1] and the factor clamped to
+// [0, 1] (the reference's Table2D has no end special case, so the clamped factor is kept).
+struct F16Br2 { int r; double f; };
+
+F16_HD F16Br1 f16_br1(const double* T, int off, int n, int r, double key,
+                                          double x0, double xn) {
+  const double xl = T[off + r - 1], xh = T[off + r];
+  double f = (key - xl) / (xh - xl);
+  f = (f > 1.0) ? 1.0 : f;
+  F16Br1 b;
+  const bool lo_end = key <= x0, hi_end = key >= xn;
+  b.lo = lo_end ? 0 : (hi_end ? n - 1 : r - 1);
+  b.hi = lo_end ? 0 : (hi_end ? n - 1 : r);
+  b.f = (lo_end || hi_end) ? 0.0 : f;
+  return b;
+}
+
+F16_HD F16Br2 f16_br2(const double* T, int off, int r, double key) {
+  const double xl = T[off + r - 1], xh = T[off + r];
+  double f = (key - xl) / (xh - xl);
+  f = (f > 1.0) ? 1.0 : ((f < 0.0) ? 0.0 : f);
+  F16Br2 b;
+  b.r = r;
+  b.f = f;
+  return b;
+}
+
+F16_HD double f16_lerp1(const double* T, int off, const F16Br1& b) {
+  const double ylo = T[off + b.lo], yhi = T[off + b.hi];
+  return b.f * (yhi - ylo) + ylo;
+}
+
+F16_HD double f16_lerp2(const double* T, int off, int nc, const F16Br2& br,
+                                            const F16Br2& bc) {
+  const int i0 = off + (br.r - 1) * nc + bc.r - 1;
+  const double d00 = T[i0], d01 = T[i0 + 1], d10 = T[i0 + nc], d11 = T[i0 + nc + 1];
+  const double col1 = br.f * (d10 - d00) + d00;
+  const double col2 = br.f * (d11 - d01) + d01;
+  return col1 + bc.f * (col2 - col1);
+}
+
+#include "f16_grid_gen.inc"
+
+#define F16_BR1_(g, key) \
+  f16_br1(T, F16M_##g##_OFF, F16M_##g##_LEN, f16m_upper_##g(key), (key), F16M_##g##_X0, F16M_##g##_XN)
+#define F16_BR1(g, key) F16_BR1_(g, key)
+#define F16_BR2_(g, key) f16_br2(T, F16M_##g##_OFF, f16m_upper_##g(key), (key))
+#define F16_BR2(g, key) F16_BR2_(g, key)
+
+// ------------------------------------------------------------------ small helpers
+F16_HD double clampd(double x, double lo, double hi) {
+  return x < lo ? lo : (x > hi ? hi : x);
+}
+
+// |a-b| <= 1e-9 * max(1, |a|, |b|)  (jsb_fcs.py:28-30)
+F16_HD bool near_equal(double a, double b) {
+  double m = 1.0;
+  const double fa = fabs(a), fb = fabs(b);
+  m = fa > m ? fa : m;
+  m = fb > m ? fb : m;
+  return fabs(a - b) <= 1e-9 * m;
+}
+
+// Rate-limited actuator with two detents (lo, hi) and one travel time t: the general
+// kinematic (jsb_fcs.py:42-78) always brackets into segment 1 for two detents, so it reduces to
+// one clipped step of at most dt0.
+F16_HD double kinemat2(double input, double output, double lo, double hi,
+                                           double t, double dt0) {
+  input = clampd(input * hi, lo, hi);
+  if (dt0 > 0.0 && !near_equal(input, output)) {
+    const double rate = (hi - lo) / t;
+    const double this_in = clampd(input, lo, hi);
+    const double this_dt = fabs((this_in - output) / rate);
+    if (dt0 < this_dt)
+      output = (output < input) ? output + dt0 * rate : output - dt0 * rate;
+    else
+      output = this_in;
+  }
+  return output;
+}
+
+// Trailing-edge-flap kinematic: detents (-1, 0, 1), times (3, 0, 3).  Same loop as the
+// reference with an iteration cap; three passes always suffice for three detents.
+F16_HD double kinemat_tef(double input, double output, double dt0) {
+  const double det[3] = {-1.0, 0.0, 1.0}, tim[3] = {3.0, 0.0, 3.0};
+  input = clampd(input * det[2], det[0], det[2]);
+  for (int it = 0; it < 4 && dt0 > 0.0 && !near_equal(input, output); ++it) {
+    int ind = 1;
+    const bool down = input < output;
+    if (down ? (det[1] < output) : (det[1] <= output)) ind = 2;
+    const double dlo = ind == 1 ? det[0] : det[1], dhi = ind == 1 ? det[1] : det[2];
+    const double t = ind == 1 ? tim[1] : tim[2];
+    if (t <= 0.0) { output = input; break; }
+    const double rate = (dhi - dlo) / t;
+    const double this_in = clampd(input, dlo, dhi);
+    double this_dt = fabs((this_in - output) / rate);
+    if (dt0 < this_dt) {
+      this_dt = dt0;
+      output = (output < input) ? output + this_dt * rate : output - this_dt * rate;
+    } else {
+      output = this_in;
+    }
+    dt0 -= this_dt;
+  }
+  return output;
+}
+
+// AEROSURFACE_SCALE, zero-centred (jsb_fcs.py:107-113)
+F16_HD double surface_scale(double in, double in_min, double in_max,
+                                                double out_min, double out_max) {
+  if (in == 0.0) return 0.0;
+  return in > 0.0 ? (in / in_max) * out_max : (in / in_min) * out_min;
+}
+
+F16_HD double seek(double v, double target, double accel, double decel) {
+  if (v > target) {
+    v -= kDt * decel;
+    v = v < target ? target : v;
+  } else if (v < target) {
+    v += kDt * accel;
+    v = v > target ? target : v;
+  }
+  return v;
+}
+
+// ------------------------------------------------------------------ register-resident state
+// The 66 state doubles a substep reads.  The remaining 35 of the 101 are outputs only
+// (history slots, PID input_prev2, the rudder and gear kinematic outputs) and are written by
+// the kernel straight to memory.
+struct Aircraft {
+  double p[3], v[3], q[4], wi[3], epa, fuel;
+  double ai[3], wdi[3], qd[4];
+  double vh1[3], vh2[3];   // velocity history slots 0 and 1 at substep start
+  double ah1[3];           // acceleration history slot 0 at substep start
+  double pba[3], ppd[3], ppq[3];
+  double pa[9];            // alpha, mach, vc_kts, vg_fps, n_py, n_pz, p, q, r (previous frame)
+  double n1, n2, n2n, ff;
+  double k_tef, k_ail, k_ele, k_lef;
+  double pid_ip[3], pid_io[3];
+};
+
+// Per-substep results that are not carried state.
+struct SubstepOut {
+  double k_rud, k_gear;
+  double euler[3], uvw[3];
+  double alpha, beta, mach, vt, alt;
+};
+
+// Atmosphere at geometric altitude h (ft): jsb_atmos.py:43-111.
+struct Atmos { double T, P, rho, a, sigma, densalt; };
+
+F16_HD Atmos isa(double h, const double* T) {
+  constexpr double kER = kEarthRadiusIsa;
+  constexpr double lapse[8] = F16M_ATM_LAPSE_INIT;
+  constexpr double alts[9] = F16M_ATM_ALT_INIT;
+  constexpr double temps[9] = F16M_ATM_TMP_INIT;
+  constexpr double pbrk[9] = F16M_ATM_PBRK_INIT;
+  constexpr double dbrk[9] = F16M_ATM_DBRK_INIT;
+  constexpr double tmbp[8] = F16M_ATM_TMB_P_INIT;
+  constexpr double g0Mair = F16M_G0 * F16M_MAIR;
+  constexpr double ng0Mair = -F16M_G0 * F16M_MAIR;
+  Atmos o;
+  const double gp = (h * kER) / (kER + h);
+  if (gp >= 0.0) {
+    const F16Br1 b = F16_BR1(F16M_TG_ISA_TEMP_R, gp);
+    o.T = f16_lerp1(T, F16M_T_ISA_TEMP_OFF, b);
+  } else {
+    o.T = temps[0] + gp * lapse[0];
+  }
+  // pressure layer: first b with gp < alt[b+1] (b <= 7)
+  int b = 0;
+#pragma unroll
+  for (int i = 1; i < 8; ++i) b += !(gp < alts[i]);
+  double Lmb = 0.0, Tmb = 0.0, base = 0.0, pb = 0.0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    if (b == i) { Lmb = lapse[i]; Tmb = tmbp[i]; base = alts[i]; pb = pbrk[i]; }
+  const double dH = gp - base;
+  if (Lmb != 0.0) {
+    const double ex = g0Mair / (F16M_RSTAR * Lmb);
+    o.P = pb * pow(Tmb / (Tmb + Lmb * dH), ex);
+  } else {
+    o.P = pb * exp(ng0Mair * dH / (F16M_RSTAR * Tmb));
+  }
+  o.rho = o.P / (F16M_RENG * o.T);
+  o.a = sqrt(F16M_GAMMA_R * o.T);
+  o.sigma = o.rho / F16M_RHO_SL;
+  // density altitude: first b with rho >= dbrk[b+1]
+  int d = 0;
+#pragma unroll
+  for (int i = 1; i < 8; ++i) d += !(o.rho >= dbrk[i]);
+  double dT = 0.0, dHb = 0.0, dL = 0.0, dpb = 1.0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    if (d == i) { dT = temps[i]; dHb = alts[i]; dL = lapse[i]; dpb = dbrk[i]; }
+  double da;
+  if (dL != 0.0) {
+    const double ex = -1.0 / (1.0 + g0Mair / (F16M_RSTAR * dL));
+    da = dHb + (dT / dL) * (pow(o.rho / dpb, ex) - 1.0);
+  } else {
+    const double fac = -(F16M_RSTAR * dT) / g0Mair;
+    da = dHb + fac * log(o.rho / dpb);
+  }
+  o.densalt = (da * kER) / (kER - da);
+  return o;
+}
+
+// Mass, CG, inertia and its inverse for a fuel load (jsb_massbalance.py:49-83); the two
+// internal tanks share the fuel equally.
+struct Mass { double cg[3], mass, J[6], Jinv[6], rp[3]; };   // J, Jinv: xx yy zz xy xz yz (symmetric)
+
+F16_HD void add_pointmass(double m, double rx, double ry, double rz,
+                                              const double cg[3], double mJ[3][3]) {
+  const double vx = kInToFt * (cg[0] - rx), vy = kInToFt * (ry - cg[1]), vz = kInToFt * (cg[2] - rz);
+  const double sx = m * vx, sy = m * vy, sz = m * vz;
+  const double xx = sx * vx, yy = sy * vy, zz = sz * vz;
+  const double xy = -sx * vy, xz = -sx * vz, yz = -sy * vz;
+  mJ[0][0] = mJ[0][0] + (yy + zz); mJ[0][1] = mJ[0][1] + xy; mJ[0][2] = mJ[0][2] + xz;
+  mJ[1][0] = mJ[1][0] + xy; mJ[1][1] = mJ[1][1] + (xx + zz); mJ[1][2] = mJ[1][2] + yz;
+  mJ[2][0] = mJ[2][0] + xz; mJ[2][1] = mJ[2][1] + yz; mJ[2][2] = mJ[2][2] + (xx + yy);
+}
+
+F16_HD Mass mass_props(double fuel) {
+  constexpr double ew = F16M_EMPTYWT, pw = F16M_PILOT_WT;
+  constexpr double bcg[3] = {F16M_BASECG_X, F16M_BASECG_Y, F16M_BASECG_Z};
+  constexpr double pl[3] = {F16M_PILOT_X, F16M_PILOT_Y, F16M_PILOT_Z};
+  constexpr double t0l[3] = {F16M_TANK0_X, F16M_TANK0_Y, F16M_TANK0_Z};
+  constexpr double t1l[3] = {F16M_TANK1_X, F16M_TANK1_Y, F16M_TANK1_Z};
+  Mass o;
+  const double t = fuel / 2.0;
+  const double weight = ew + (t + t) + pw;
+#pragma unroll
+  for (int i = 0; i < 3; ++i)
+    o.cg[i] = (ew * bcg[i] + pw * pl[i] + t * t0l[i] + t * t1l[i]) / weight;
+  double mJ[3][3] = {{F16M_IXX, -F16M_IXY, F16M_IXZ},
+                     {-F16M_IXY, F16M_IYY, -F16M_IYZ},
+                     {F16M_IXZ, -F16M_IYZ, F16M_IZZ}};
+  add_pointmass(kLbToSlug * ew, bcg[0], bcg[1], bcg[2], o.cg, mJ);
+  add_pointmass(kLbToSlug * pw, pl[0], pl[1], pl[2], o.cg, mJ);
+  const double mt = kLbToSlug * t;
+  add_pointmass(mt, t0l[0], t0l[1], t0l[2], o.cg, mJ);
+  add_pointmass(mt, t1l[0], t1l[1], t1l[2], o.cg, mJ);
+  const double Ixx = mJ[0][0], Iyy = mJ[1][1], Izz = mJ[2][2];
+  const double Ixy = -mJ[0][1], Ixz = -mJ[0][2], Iyz = -mJ[1][2];
+  double k1 = Iyy * Izz - Iyz * Iyz, k2 = Iyz * Ixz + Ixy * Izz, k3 = Ixy * Iyz + Iyy * Ixz;
+  const double den = 1.0 / (Ixx * k1 - Ixy * k2 - Ixz * k3);
+  k1 *= den; k2 *= den; k3 *= den;
+  o.Jinv[0] = k1; o.Jinv[1] = (Izz * Ixx - Ixz * Ixz) * den; o.Jinv[2] = (Ixx * Iyy - Ixy * Ixy) * den;
+  o.Jinv[3] = k2; o.Jinv[4] = k3; o.Jinv[5] = (Ixy * Ixz + Iyz * Ixx) * den;
+  o.J[0] = Ixx; o.J[1] = Iyy; o.J[2] = Izz; o.J[3] = -Ixy; o.J[4] = -Ixz; o.J[5] = -Iyz;
+  o.mass = kLbToSlug * weight;
+  o.rp[0] = kInToFt * (o.cg[0] - F16M_AERORP_X);
+  o.rp[1] = kInToFt * (F16M_AERORP_Y - o.cg[1]);
+  o.rp[2] = kInToFt * (o.cg[2] - F16M_AERORP_Z);
+  return o;
+}
+
+// Pitot total pressure and its inverse (jsb_auxiliary.py:20-42) -> calibrated airspeed, ft/s.
+F16_HD double vcal_from_mach(double mach, double p) {
+  double pt;
+  if (mach < 0.0) {
+    pt = p;
+  } else if (mach < 1.0) {
+    const double m2 = 1.0 + 0.2 * mach * mach;   // m2^3.5 = m2^3 sqrt(m2)
+    pt = p * (m2 * m2 * m2 * sqrt(m2));
+  } else {
+    pt = p * 166.92158009316827 * pow(mach, 7.0) / pow(7.0 * mach * mach - 1.0, 2.5);
+  }
+  const double qc = pt - p;
+  const double A = qc / 2116.228 + 1.0;          // StdDaySLpressure (jsb_const.py:24)
+  double M = sqrt(5.0 * (pow(A, 1.0 / 3.5) - 1.0));
+  if (M > 1.0) {
+    for (int i = 0; i < 10; ++i) {
+      const double t = 1.0 - 1.0 / (7.0 * M * M);
+      M = 0.8812848543473311 * sqrt(A * (t * t * sqrt(t)));
+    }
+  }
+  return F16M_STD_SL_SOUNDSPEED * M;
+}
+
+
+
+// ------------------------------------------------------------------ kinematics
+// Frames derived from the ECI state (FDM._kinematics_from_state, jsb_fdm.py:121-140).
+struct Kin {
+  double ce, se;              // cos/sin of the Earth position angle
+  double ex, ey, ez, radius, sLat;
+  double B[3][3];             // Ti2b: rows are the body axes in ECI
+  double uvw[3], wpqr[3];     // body velocity w.r.t. the Earth, body rates w.r.t. the Earth
+  double vn, ve;              // local north/east ground velocity
+  double ctcp;                // cos(theta) * cos(phi) of the local-NED Euler angles
+};
+
+// `want_euler` (wave-uniform) also produces the Euler angles (mat_to_euler,
+// jsb_frames.py:140-163) for the output row; the FCS only needs cos(theta)cos(phi), which is
+// formed from the DCM without the inverse trigonometry.
+F16_HD void kinematics(const double p[3], const double v[3], const double q[4],
+                                           const double wi[3], double epa, bool want_euler,
+                                           Kin& k, double euler[3]) {
+  sincos(epa, &k.se, &k.ce);
+  const double ce = k.ce, se = k.se;
+  k.ex = ce * p[0] + se * p[1];
+  k.ey = ce * p[1] - se * p[0];
+  k.ez = p[2];
+  const double rxy2 = k.ex * k.ex + k.ey * k.ey;
+  k.radius = sqrt(rxy2 + k.ez * k.ez);
+  const double rxy = sqrt(rxy2);
+  double sLon = 0.0, cLon = 1.0, sLat = 0.0, cLat = 1.0;
+  if (rxy != 0.0) { sLon = k.ey / rxy; cLon = k.ex / rxy; }
+  if (k.radius != 0.0) { sLat = k.ez / k.radius; cLat = rxy / k.radius; }
+  k.sLat = sLat;
+  // local N, E, D axes in ECI (columns of Tl2i = Tec2i * Tl2ec; Tec2l rows from
+  // location_derived, jsb_frames.py:48-51)
+  const double n0 = -cLon * sLat, n1 = -sLon * sLat;
+  const double d0 = -cLon * cLat, d1 = -sLon * cLat;
+  const double N[3] = {ce * n0 - se * n1, se * n0 + ce * n1, cLat};
+  const double E[2] = {ce * (-sLon) - se * cLon, se * (-sLon) + ce * cLon};
+  const double D[3] = {ce * d0 - se * d1, se * d0 + ce * d1, -sLat};
+  {
+    const double q0 = q[0], q1 = q[1], q2 = q[2], q3 = q[3];
+    const double q0q0 = q0 * q0, q1q1 = q1 * q1, q2q2 = q2 * q2, q3q3 = q3 * q3;
+    const double q0q1 = q0 * q1, q0q2 = q0 * q2, q0q3 = q0 * q3;
+    const double q1q2 = q1 * q2, q1q3 = q1 * q3, q2q3 = q2 * q3;
+    k.B[0][0] = q0q0 + q1q1 - q2q2 - q3q3; k.B[0][1] = 2.0 * (q1q2 + q0q3); k.B[0][2] = 2.0 * (q1q3 - q0q2);
+    k.B[1][0] = 2.0 * (q1q2 - q0q3); k.B[1][1] = q0q0 - q1q1 + q2q2 - q3q3; k.B[1][2] = 2.0 * (q2q3 + q0q1);
+    k.B[2][0] = 2.0 * (q1q3 + q0q2); k.B[2][1] = 2.0 * (q2q3 - q0q1); k.B[2][2] = q0q0 - q1q1 - q2q2 + q3q3;
+  }
+  // Tl2b[i][j] = body_i . local_j
+  double L[3][3];
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    L[i][0] = k.B[i][0] * N[0] + k.B[i][1] * N[1] + k.B[i][2] * N[2];
+    L[i][1] = k.B[i][0] * E[0] + k.B[i][1] * E[1];
+    L[i][2] = k.B[i][0] * D[0] + k.B[i][1] * D[1] + k.B[i][2] * D[2];
+  }
+  // body velocity relative to the rotating Earth: Ti2b (v - omega x p)
+  const double dv[3] = {v[0] + kRot * p[1], v[1] - kRot * p[0], v[2]};
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    k.uvw[i] = k.B[i][0] * dv[0] + k.B[i][1] * dv[1] + k.B[i][2] * dv[2];
+    k.wpqr[i] = wi[i] - k.B[i][2] * kRot;   // vPQR = vPQRi - Ti2b * omega
+  }
+  k.vn = L[0][0] * k.uvw[0] + L[1][0] * k.uvw[1] + L[2][0] * k.uvw[2];
+  k.ve = L[0][1] * k.uvw[0] + L[1][1] * k.uvw[1] + L[2][1] * k.uvw[2];
+  const double d6 = L[0][2];
+  const bool gimbal = d6 <= -1.0 || d6 >= 1.0;
+  if (gimbal) {
+    k.ctcp = 6.123233995736766e-17 * cos(atan2(-L[2][1], L[1][1]));   // cos(+-pi/2) in double
+  } else {
+    const double h = sqrt(L[1][2] * L[1][2] + L[2][2] * L[2][2]);
+    k.ctcp = sqrt(1.0 - d6 * d6) * (h != 0.0 ? L[2][2] / h : 1.0);
+  }
+  if (want_euler) {
+    if (gimbal) {
+      euler[1] = d6 <= -1.0 ? 0.5 * M_PI : -0.5 * M_PI;
+      euler[0] = atan2(-L[2][1], L[1][1]);
+      euler[2] = 0.0;
+    } else {
+      euler[1] = asin(-d6);
+      euler[0] = atan2(L[1][2], L[2][2]);
+      double ps = atan2(L[0][1], L[0][0]);
+      euler[2] = ps < 0.0 ? ps + 2.0 * M_PI : ps;
+    }
+  }
+}
+
+// ------------------------------------------------------------------ force path
+// FDM._force_path (jsb_fdm.py:76-119): atmosphere -> mass -> FCS (previous-frame auxiliary
+// values, current attitude) -> auxiliary -> engine -> aero -> gravity -> accelerations.
+// Reads and updates the FCS and engine state in `a`; writes the new derivatives to `d`.
+struct ForceOut {
+  double ai[3], wdi[3], pba[3], ppq[3];   // vUVWidot, vPQRidot, vBodyAccel, vPQRi
+  double alpha, beta, vt, mach, vc_kts, vg, npy, npz;
+  double fuel_burn, alt, k_rud;
+};
+
+template <int FCS_RATE>
+F16_HD void force_path(Aircraft& a, double c_ail, double c_ele, double c_rud,
+                                           double c_thr, const Kin& k,
+                                           const double* __restrict__ T, ForceOut& o) {
+  constexpr double fdt = 1.0 / (double)FCS_RATE;
+  const double alt = k.radius - kSemiMajor;
+  const Atmos at = isa(alt, T);
+  const Mass mb = mass_props(a.fuel);
+
+  // ---- FCS (jsb_fcs.py:143-268) ----
+  const double pa_alpha = a.pa[0], pa_mach = a.pa[1], vc = a.pa[2], vg = a.pa[3];
+  double ail_rad, elev_rad, rud_rad, lef_rad, flap_rad;
+  // gear kinematic from its forced seed 0.30 toward command 0: one rate-limited step
+  constexpr double gear = kGearForce - fdt * ((1.0 - 0.0) / 5.0);
+  {
+    const double tef_rad = (vc < 250.0) ? 0.349 : ((pa_mach > 0.9) ? -0.0349 : 0.0);
+    const double tef = kinemat_tef(2.864789 * tef_rad, a.k_tef, fdt);
+    a.k_tef = tef;
+    // roll: PID (3, 5e-4, -1.25e-3), integrating only when its trigger is 0 (vc < 20 kt)
+    const double rte = c_ail - 0.31821 * a.pa[6];
+    double rpid;
+    {
+      const double ip = a.pid_ip[0];
+      const double dval = (rte - ip) / fdt;
+      a.pid_io[0] += 0.00050 * fdt * ((vc < 20.0) ? (1.5 * rte - 0.5 * ip) : 0.0);
+      a.pid_ip[0] = rte;
+      rpid = 3.00000 * rte + a.pid_io[0] + -0.00125 * dval;
+    }
+    const double rrc = clampd(rpid + c_ail, -1.0, 1.0);
+    ail_rad = surface_scale(rrc, -1.0, 1.0, -0.375, 0.375);
+    const double lapn = kinemat2(rrc, a.k_ail, -1.0, 1.0, 0.3, fdt);
+    a.k_ail = lapn;
+    const F16Br1 bm = F16_BR1(F16M_TG_FCS_AIL_SPEED_R, pa_mach);
+    const double asc = f16_lerp1(T, F16M_T_FCS_AIL_SPEED_OFF, bm) * lapn;
+    const double lf = clampd(-tef - asc, -1.0, 1.0), rf = clampd(tef - asc, -1.0, 1.0);
+    flap_rad = 1.4324 * (lf + rf);
+    // pitch: g-load PID (0.3, 0.025, 0) clipped to +-1, trigger 0 below 5 kt
+    const double gcorr = a.pa[5] - k.ctcp;
+    const double ecl = clampd(c_ele + 0.0, -1.0, 0.44);
+    const F16Br1 ba = F16_BR1(F16M_TG_FCS_ELEV_SCHED_R, pa_alpha);
+    const double esch = f16_lerp1(T, F16M_T_FCS_ELEV_SCHED_OFF, ba) * ecl;
+    const double pte = esch + 6.2 * a.pa[7] - 0.020 * gcorr;
+    double gpid;
+    {
+      const double ip = a.pid_ip[1];
+      const double dval = (pte - ip) / fdt;
+      a.pid_io[1] += 0.0250 * fdt * ((vc < 5.0) ? (1.5 * pte - 0.5 * ip) : 0.0);
+      a.pid_ip[1] = pte;
+      gpid = clampd(0.3000 * pte + a.pid_io[1] + 0.0000 * dval, -1.0, 1.0);
+    }
+    const double psch = clampd(esch + 1.0472 * pa_alpha + gpid, -1.0, 1.0);
+    const double epn = kinemat2(psch, a.k_ele, -1.0, 1.0, 0.3, fdt);
+    a.k_ele = epn;
+    elev_rad = surface_scale(epn, -1.0, 1.0, -0.436, 0.436);
+    // yaw: PID (0.1055, 1e-5, 5e-5) clipped to +-1, trigger 0 below 10 kt; its output seeds
+    // the rudder kinematic
+    const F16Br1 bv = F16_BR1(F16M_TG_FCS_YAW_RATE_R, vg);
+    const double yrn = f16_lerp1(T, F16M_T_FCS_YAW_RATE_OFF, bv) * a.pa[8];
+    const double yte = c_rud + yrn + 0.25 * a.pa[4];
+    double ypid;
+    {
+      const double ip = a.pid_ip[2];
+      const double dval = (yte - ip) / fdt;
+      a.pid_io[2] += 0.000010 * fdt * ((vc < 10.0) ? (1.5 * yte - 0.5 * ip) : 0.0);
+      a.pid_ip[2] = yte;
+      ypid = clampd(0.105500 * yte + a.pid_io[2] + 0.00005 * dval, -1.0, 1.0);
+    }
+    const double ysch = clampd(c_rud + 0.0 + ypid, -1.0, 1.0);
+    const double rpn = kinemat2(ysch, ypid, -1.0, 1.0, 0.4, fdt);
+    o.k_rud = rpn;
+    rud_rad = surface_scale(rpn, -1.0, 1.0, -0.524, 0.524);
+    // leading-edge flap switch: the gear is never at 0 and weight-on-wheels is never set
+    lef_rad = (pa_alpha > 0.0873) ? 0.262 : ((pa_mach > 0.9) ? -0.0349 : 0.0);
+    a.k_lef = kinemat2(2.293578 * lef_rad, a.k_lef, -1.0, 1.0, 3.0, fdt);
+  }
+
+  // ---- auxiliary (jsb_auxiliary.py:45-73) ----
+  const double u = k.uvw[0], v = k.uvw[1], w = k.uvw[2];
+  const double muw = u * u + w * w;
+  const double vt2 = muw + v * v;
+  const double vt = sqrt(vt2);
+  double alpha = 0.0, beta = 0.0, ca = 1.0, sa = 0.0, cb = 1.0, sb = 0.0;
+  if (vt > 0.001) {
+    const double suw = sqrt(muw);
+    beta = atan2(v, suw);
+    cb = suw / vt;
+    sb = v / vt;
+    if (muw >= 1e-6) {
+      alpha = atan2(w, u);
+      ca = u / suw;
+      sa = w / suw;
+    }
+  }
+  const double qbar = 0.5 * at.rho * vt2;
+  const double mach = vt / at.a;
+  {
+    const double eye[3] = {kInToFt * (mb.cg[0] - F16M_EYEPOINT_X), kInToFt * (F16M_EYEPOINT_Y - mb.cg[1]),
+                           kInToFt * (mb.cg[2] - F16M_EYEPOINT_Z)};
+    const double* wd = a.ppd;
+    const double* wq = a.ppq;
+    const double c1y = wd[2] * eye[0] - wd[0] * eye[2], c1z = wd[0] * eye[1] - wd[1] * eye[0];
+    const double c2x = wq[1] * eye[2] - wq[2] * eye[1], c2y = wq[2] * eye[0] - wq[0] * eye[2];
+    const double c2z = wq[0] * eye[1] - wq[1] * eye[0];
+    const double c3y = wq[2] * c2x - wq[0] * c2z, c3z = wq[0] * c2y - wq[1] * c2x;
+    o.npy = (a.pba[1] + c1y + c3y) / F16M_SLGRAVITY;
+    o.npz = (a.pba[2] + c1z + c3z) / F16M_SLGRAVITY;
+  }
+  o.vc_kts = (fabs(mach) > 0.0) ? vcal_from_mach(mach, at.P) * F16M_FPSTOKTS : 0.0;
+  o.vg = sqrt(k.vn * k.vn + k.ve * k.ve);
+  o.alpha = alpha; o.beta = beta; o.vt = vt; o.mach = mach; o.alt = alt;
+
+  // ---- engine (jsb_propulsion.py:89-128); throttle position = 2 * throttle command ----
+  double thrust;
+  {
+    double thr = 2.0 * c_thr, aug = 0.0;
+    if (thr > 1.0) { aug = thr - 1.0; thr -= aug; }
+    // spool-time constants as the reference forms them: k * 90 / (bypass + 3)
+    constexpr double d_up = 1.0 * 90.0 / (F16M_ENG_BYPASSRATIO + 3.0);
+    constexpr double d_n2dn = 3.0 * 90.0 / (F16M_ENG_BYPASSRATIO + 3.0);
+    constexpr double d_n1dn = 2.4 * 90.0 / (F16M_ENG_BYPASSRATIO + 3.0);
+    const double nx = a.n2n + 0.1;
+    const double om = 1.0 - (nx < 1.0 ? nx : 1.0);
+    const double den = 1.0 + 3.0 * (om * om * om) + (1.0 - at.sigma);
+    const double up = d_up / den, n2dn = d_n2dn / den, n1dn = d_n1dn / den;
+    a.n2 = seek(a.n2, F16M_ENG_IDLEN2 + thr * (F16M_ENG_MAXN2 - F16M_ENG_IDLEN2), up, n2dn);
+    a.n1 = seek(a.n1, F16M_ENG_IDLEN1 + thr * (F16M_ENG_MAXN1 - F16M_ENG_IDLEN1), up, n1dn);
+    a.n2n = (a.n2 - F16M_ENG_IDLEN2) / (F16M_ENG_MAXN2 - F16M_ENG_IDLEN2);
+    const F16Br2 bm = F16_BR2(F16M_TG_ENG_IDLE_R, mach);
+    const F16Br2 bd = F16_BR2(F16M_TG_ENG_IDLE_C, at.densalt);
+    const F16Br2 bm2 = F16_BR2(F16M_TG_ENG_MIL_R, mach);
+    const double idle = F16M_ENG_MILTHRUST * f16_lerp2(T, F16M_T_ENG_IDLE_OFF, F16M_T_ENG_IDLE_NC, bm, bd);
+    const double mil = (F16M_ENG_MILTHRUST - idle) * f16_lerp2(T, F16M_T_ENG_MIL_OFF, F16M_T_ENG_MIL_NC, bm2, bd);
+    thrust = idle + mil * a.n2n * a.n2n;
+    const double on = 1.0 - a.n2n;
+    const double tsfc = F16M_ENG_TSFC * sqrt(at.T / 389.7) * (0.84 + on * on);
+    a.ff = seek(a.ff, thrust * tsfc, 1000.0, 10000.0);
+    a.ff = a.ff < F16M_IDLEFF ? F16M_IDLEFF : a.ff;
+    if (aug > 0.0) {   // afterburner, AugMethod 2
+      const F16Br2 bm3 = F16_BR2(F16M_TG_ENG_AUG_R, mach);
+      const double tdiff = F16M_ENG_MAXTHRUST * f16_lerp2(T, F16M_T_ENG_AUG_OFF, F16M_T_ENG_AUG_NC, bm3, bd) - thrust;
+      thrust += tdiff * aug;
+      a.ff = seek(a.ff, thrust * F16M_ENG_ATSFC, 5000.0, 10000.0);
+    }
+    o.fuel_burn = a.ff / 3600.0 * kDt;
+  }
+
+  // ---- aerodynamics (jsb_aero.py:75-107): 40 coefficient functions ----
+  double ax_drag, ax_side, ax_lift, ax_roll, ax_pitch, ax_yaw;
+  {
+    const double twovel = 2.0 * vt;
+    const double bi2vel = twovel != 0.0 ? F16M_BW / twovel : 0.0;
+    const double ci2vel = twovel != 0.0 ? F16M_CBAR / twovel : 0.0;
+    constexpr double kclge = 1.0;   // kCLge(765 ft): beyond the table's last breakpoint (1.1 -> 1.0)
+    const double p = k.wpqr[0], q = k.wpqr[1], r = k.wpqr[2];
+    const double ail = ail_rad, elev = elev_rad, rud = rud_rad, lef = lef_rad, flap = flap_rad;
+    constexpr double sb = 0.0;      // speedbrake position is never driven
+#include "f16_aero_gen.inc"
+  }
+  // wind -> body forces, moments about the CG, then the engine's thrust at the structural origin
+  double F[3], M[3];
+  {
+    const double drag = -ax_drag, side = ax_side, lift = -ax_lift;
+    F[0] = ca * cb * drag + (-ca * sb) * side + (-sa) * lift;
+    F[1] = sb * drag + cb * side;
+    F[2] = sa * cb * drag + (-sa * sb) * side + ca * lift;
+    const double rx = mb.rp[0], ry = mb.rp[1], rz = mb.rp[2];
+    M[0] = ax_roll + (ry * F[2] - rz * F[1]);
+    M[1] = ax_pitch + (rz * F[0] - rx * F[2]);
+    M[2] = ax_yaw + (rx * F[1] - ry * F[0]);
+    const double mz = kInToFt * (mb.cg[2] - 0.0), my = kInToFt * (0.0 - mb.cg[1]);
+    F[0] = F[0] + thrust;
+    M[1] = M[1] + mz * thrust;
+    M[2] = M[2] + (-my) * thrust;
+  }
+
+  // ---- J2 gravity (jsb_frames.py:69-80), then accelerations (jsb_accel.py:10-31) ----
+  double gi[3];
+  {
+    const double adivr = kSemiMajor / k.radius;
+    const double pc = 1.5 * kJ2 * adivr * adivr;
+    const double s2 = k.sLat * k.sLat;   // sin(geocentric latitude) = z / r
+    const double kxy = 1.0 + pc * (1.0 - 5.0 * s2), kz = 1.0 + pc * (3.0 - 5.0 * s2);
+    const double g = -(kGM / (k.radius * k.radius)) / k.radius;
+    const double gx = g * (kxy * k.ex), gy = g * (kxy * k.ey), gz = g * (kz * k.ez);
+    gi[0] = k.ce * gx - k.se * gy;   // Tec2i * g_ecef
+    gi[1] = k.se * gx + k.ce * gy;
+    gi[2] = gz;
+  }
+  {
+    double wq[3];   // vPQRi re-formed from vPQR, as the reference's accelerations do
+#pragma unroll
+    for (int i = 0; i < 3; ++i) wq[i] = k.wpqr[i] + k.B[i][2] * kRot;
+    const double* J = mb.J;
+    const double Jw0 = J[0] * wq[0] + J[3] * wq[1] + J[4] * wq[2];
+    const double Jw1 = J[3] * wq[0] + J[1] * wq[1] + J[5] * wq[2];
+    const double Jw2 = J[4] * wq[0] + J[5] * wq[1] + J[2] * wq[2];
+    const double m0 = M[0] - (wq[1] * Jw2 - wq[2] * Jw1);
+    const double m1 = M[1] - (wq[2] * Jw0 - wq[0] * Jw2);
+    const double m2 = M[2] - (wq[0] * Jw1 - wq[1] * Jw0);
+    const double* Ji = mb.Jinv;
+    o.wdi[0] = Ji[0] * m0 + Ji[3] * m1 + Ji[4] * m2;
+    o.wdi[1] = Ji[3] * m0 + Ji[1] * m1 + Ji[5] * m2;
+    o.wdi[2] = Ji[4] * m0 + Ji[5] * m1 + Ji[2] * m2;
+    const double sm = 1.0 / mb.mass;
+#pragma unroll
+    for (int i = 0; i < 3; ++i) o.pba[i] = F[i] * sm;
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+      o.ai[i] = (k.B[0][i] * o.pba[0] + k.B[1][i] * o.pba[1] + k.B[2][i] * o.pba[2]) + gi[i];
+      o.ppq[i] = wq[i];
+    }
+  }
+}
+
+// ------------------------------------------------------------------ one integration step
+// FDM.step (jsb_fdm.py:212-244).  FCS_RATE: the FCS components' dt is 1/FCS_RATE s (120 for
+// cuda_fdm/ref/jsb_fcs.py:19, 60 for the 184-D runtime's copy of that file).
+template <int FCS_RATE>
+F16_HD void substep(Aircraft& a, double c_ail, double c_ele, double c_rud,
+                                        double c_thr, const double* __restrict__ T,
+                                        bool want_euler, SubstepOut& out) {
+  // ---- propagate: quaternion rect-Euler + normalize, vPQRi rect-Euler, ECI position AB3 on the
+  // velocity history, ECI velocity AB2 on the acceleration history ----
+  {
+    double q0 = a.q[0] + kDt * a.qd[0], q1 = a.q[1] + kDt * a.qd[1];
+    double q2 = a.q[2] + kDt * a.qd[2], q3 = a.q[3] + kDt * a.qd[3];
+    const double mag = sqrt(q0 * q0 + q1 * q1 + q2 * q2 + q3 * q3);
+    if (mag != 0.0) {
+      const double inv = 1.0 / mag;
+      q0 = q0 * inv; q1 = q1 * inv; q2 = q2 * inv; q3 = q3 * inv;
+    }
+    a.q[0] = q0; a.q[1] = q1; a.q[2] = q2; a.q[3] = q3;
+  }
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    a.wi[i] = a.wi[i] + kDt * a.wdi[i];
+    const double v0 = a.v[i];
+    a.p[i] = a.p[i] + (kDt / 12.0) * (23.0 * v0 - 16.0 * a.vh1[i] + 5.0 * a.vh2[i]);
+    a.v[i] = v0 + kDt * (1.5 * a.ai[i] - 0.5 * a.ah1[i]);
+    a.vh2[i] = a.vh1[i];
+    a.vh1[i] = v0;
+    a.ah1[i] = a.ai[i];
+  }
+  a.epa += kRot * kDt;
+
+  Kin k;
+  kinematics(a.p, a.v, a.q, a.wi, a.epa, want_euler, k, out.euler);
+  {   // quaternion derivative for the next step (quat_qdot, jsb_frames.py:170-176)
+    const double p = a.wi[0], qq = a.wi[1], r = a.wi[2];
+    const double q0 = a.q[0], q1 = a.q[1], q2 = a.q[2], q3 = a.q[3];
+    a.qd[0] = -0.5 * (q1 * p + q2 * qq + q3 * r);
+    a.qd[1] = 0.5 * (q0 * p - q3 * qq + q2 * r);
+    a.qd[2] = 0.5 * (q3 * p + q0 * qq - q1 * r);
+    a.qd[3] = 0.5 * (-q2 * p + q1 * qq + q0 * r);
+  }
+  ForceOut f;
+  force_path<FCS_RATE>(a, c_ail, c_ele, c_rud, c_thr, k, T, f);
+  a.fuel -= f.fuel_burn;
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    a.ai[i] = f.ai[i];
+    a.wdi[i] = f.wdi[i];
+    a.pba[i] = f.pba[i];
+    a.ppd[i] = f.wdi[i];
+    a.ppq[i] = f.ppq[i];
+  }
+  a.pa[0] = f.alpha; a.pa[1] = f.mach; a.pa[2] = f.vc_kts; a.pa[3] = f.vg;
+  a.pa[4] = f.npy; a.pa[5] = f.npz; a.pa[6] = k.wpqr[0]; a.pa[7] = k.wpqr[1]; a.pa[8] = k.wpqr[2];
+  out.k_rud = f.k_rud;
+  out.k_gear = kGearForce - (1.0 / (double)FCS_RATE) * ((1.0 - 0.0) / 5.0);
+#pragma unroll
+  for (int i = 0; i < 3; ++i) out.uvw[i] = k.uvw[i];
+  out.alpha = f.alpha; out.beta = f.beta; out.mach = f.mach; out.vt = f.vt; out.alt = f.alt;
+}
+
+}  // namespace f16

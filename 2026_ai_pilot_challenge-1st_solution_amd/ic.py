@@ -1,0 +1,109 @@
+"""Initial-condition sampling and the discrete action grid.
+
+* ``ned_to_geodetic`` places an aircraft given in the contest's N/E/D frame about the official
+  origin (37.240778 N, 131.869556 E, cuda_fdm/rl_env.py:33-37) at a geodetic latitude and
+  longitude, with altitude MSL = -D (cuda_fdm/rl_env.py:165-173).  The reference uses pymap3d
+  for the horizontal inverse; this is an independent WGS84 implementation (tangent-plane ->
+  ECEF, then Bowring's iteration to convergence).  IC sampling is not on the parity path: the
+  same IC rows feed the GPU and the CPU restatement.
+* samplers for the BASELINE workloads (head-on and tail-chase engagements);
+* ``action_grid`` / ``bins_to_controls``: 21 bins on [-1, 1], throttle = 0.5 z + 0.5
+  (research/competition_36500/runtime/cuda_fdm/ppo_gpu.py:178-181, 361-370).
+"""
+import math
+
+import numpy as np
+
+ORIGIN_LAT_DEG = 37.240778
+ORIGIN_LON_DEG = 131.869556
+WGS84_A_M = 6378137.0
+WGS84_E2 = 0.0066943799901411
+FT2M = 0.3048
+M2FT = 1.0 / FT2M
+
+
+def _geodetic_to_ecef_m(lat, lon, h):
+    s, c = np.sin(lat), np.cos(lat)
+    n = WGS84_A_M / np.sqrt(1.0 - WGS84_E2 * s * s)
+    return ((n + h) * c * np.cos(lon), (n + h) * c * np.sin(lon), (n * (1.0 - WGS84_E2) + h) * s)
+
+
+def ned_to_geodetic(n, e, d, lat0=ORIGIN_LAT_DEG, lon0=ORIGIN_LON_DEG, h0=0.0):
+    """N/E/D metres about (lat0, lon0, h0) -> (lat_deg, lon_deg, alt_ft) with alt = -D."""
+    n, e, d = (np.asarray(v, dtype=np.float64) for v in (n, e, d))
+    la0, lo0 = math.radians(lat0), math.radians(lon0)
+    x0, y0, z0 = _geodetic_to_ecef_m(la0, lo0, h0)
+    sl, cl, so, co = math.sin(la0), math.cos(la0), math.sin(lo0), math.cos(lo0)
+    u = -d
+    x = x0 - sl * co * n - so * e + cl * co * u
+    y = y0 - sl * so * n + co * e + cl * so * u
+    z = z0 + cl * n + sl * u
+    lon = np.arctan2(y, x)
+    p = np.hypot(x, y)
+    lat = np.arctan2(z, p * (1.0 - WGS84_E2))
+    for _ in range(8):
+        s = np.sin(lat)
+        nn = WGS84_A_M / np.sqrt(1.0 - WGS84_E2 * s * s)
+        lat = np.arctan2(z + WGS84_E2 * nn * s, p)
+    return np.degrees(lat), np.degrees(lon), -d * M2FT
+
+
+def ic_row(lat_deg, lon_deg, alt_ft, vt_fps, psi_deg, fuel_lbs, phi_deg=0.0, theta_deg=0.0,
+           alpha_deg=0.0, beta_deg=0.0):
+    return [lat_deg, lon_deg, alt_ft, vt_fps, phi_deg, theta_deg, psi_deg, alpha_deg, beta_deg,
+            fuel_lbs]
+
+
+def sample_headon(nenv, seed=0, fuel_lbs=6972.0):
+    """BASELINE C1: alt U[3,10] km, speed U[150,300] m/s, separation U[5,15] km, opposing
+    headings on the north axis about N = 3500 m (rl_env.py:252-258 pattern).  Returns (2*nenv, 10)
+    IC rows, plane 0 at N = c + d/2 heading 180 deg, plane 1 at N = c - d/2 heading 0 deg."""
+    rng = np.random.default_rng(seed)
+    alt = rng.uniform(3000.0, 10000.0, nenv)
+    spd = rng.uniform(150.0, 300.0, nenv)
+    sep = rng.uniform(5000.0, 15000.0, nenv)
+    c = 3500.0
+    rows = np.zeros((2 * nenv, 10))
+    for plane, sign, psi in ((0, 1.0, 180.0), (1, -1.0, 0.0)):
+        la, lo, h = ned_to_geodetic(c + sign * 0.5 * sep, np.zeros(nenv), -alt)
+        for k in range(nenv):
+            rows[2 * k + plane] = ic_row(la[k], lo[k], h[k], spd[k] * M2FT, psi, fuel_lbs)
+    return rows
+
+
+def sample_tailchase(nenv, seed=0, fuel_lbs=6972.0):
+    """BASELINE C2: both aircraft share a random heading; the pursuer (plane 0) sits 1-3 km
+    behind the target (plane 1); alt U[4,8] km, speed U[200,280] m/s.  Returns (2*nenv, 10)."""
+    rng = np.random.default_rng(seed)
+    alt = rng.uniform(4000.0, 8000.0, nenv)
+    spd = rng.uniform(200.0, 280.0, nenv)
+    gap = rng.uniform(1000.0, 3000.0, nenv)
+    psi = rng.uniform(0.0, 360.0, nenv)
+    cn, ce = 3500.0, 0.0
+    hn, he = np.cos(np.radians(psi)), np.sin(np.radians(psi))
+    rows = np.zeros((2 * nenv, 10))
+    lt, ot, ht = ned_to_geodetic(cn + 0.5 * gap * hn, ce + 0.5 * gap * he, -alt)
+    lp, op, hp = ned_to_geodetic(cn - 0.5 * gap * hn, ce - 0.5 * gap * he, -alt)
+    for k in range(nenv):
+        rows[2 * k] = ic_row(lp[k], op[k], hp[k], spd[k] * M2FT, psi[k], fuel_lbs)
+        rows[2 * k + 1] = ic_row(lt[k], ot[k], ht[k], spd[k] * M2FT, psi[k], fuel_lbs)
+    return rows
+
+
+def action_grid(num_bins=21):
+    """linspace(-1, 1, num_bins) (ppo_gpu.py:178-181)."""
+    return np.linspace(-1.0, 1.0, num_bins)
+
+
+def bins_to_controls(idx, num_bins=21):
+    """(..., 4) integer bins -> (..., 4) controls; throttle = 0.5 z + 0.5 (ppo_gpu.py:361-370)."""
+    g = action_grid(num_bins)
+    u = g[np.asarray(idx)]
+    u[..., 3] = 0.5 * u[..., 3] + 0.5
+    return u
+
+
+def random_bin_actions(ndec, nac, seed=0, num_bins=21):
+    """(ndec, nac, 4) controls from i.i.d. uniform bins (BASELINE C1/C2 action model)."""
+    rng = np.random.default_rng(seed)
+    return bins_to_controls(rng.integers(0, num_bins, size=(ndec, nac, 4)), num_bins)

@@ -1,0 +1,166 @@
+#!/usr/bin/env python3
+"""Benchmark of the batched F-16 step on one MI355X (see DESIGN.md for the workload and the
+roofline accounting).
+
+A "step" is one decision of the batched flight model: every aircraft of 16,384 tail-chase
+engagements (32,768 aircraft) advances 6 substeps of 1/60 s with its random 21-bin action
+held (BASELINE configs[1] model at the metric's 16k-engagement size).  Inputs are resident in
+HBM before the timed region.  Prints one JSON line.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--nenv 16384] [--substeps 6]
+                    [--cpu-seconds 10] [--no-cpu]
+"""
+import argparse
+import ctypes
+import importlib
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = "2026_ai_pilot_challenge-1st_solution_amd"
+
+# Algorithmic FP64 work of one aircraft-substep: static count of the reference's model
+# (adds, subs, muls, divs, sqrts and libm calls each 1), SURVEY 8(d): ~1.55 kFLOP.
+FLOP_PER_SUBSTEP = 1550.0
+PEAK_FP64_TFLOPS = 78.6
+PEAK_HBM_GBS = 8000.0
+# reference's published GpuDogfight.step rate at 16k envs (RTX 3070 Ti, cuda_fdm/README.md:130)
+REF_PUBLISHED_SUBSTEPS = 37.0e6
+
+
+def cpu_baseline(states0_aos, actions_host, substeps, cpu_seconds):
+    """Time the reference's own C model (oracle/_ref, fdm.cuh built from its sources) on the
+    host cores; fall back to the C restatement (oracle/liborc.so).  Bounded sample."""
+    D = ctypes.POINTER(ctypes.c_double)
+    ref = os.path.join(ROOT, "oracle", "_ref", "libf16ref_120.so")
+    if os.path.exists(ref):
+        L = ctypes.CDLL(ref)
+        fn = L.ref_fdm_rollout
+        fn.argtypes = [D, D, ctypes.c_long, ctypes.c_int, ctypes.c_int, ctypes.c_int]
+        kind = "reference"
+
+        def run(st, act, nac, ndec, nth):
+            fn(st.ctypes.data_as(D), act.ctypes.data_as(D), nac, ndec, substeps, nth)
+    else:
+        L = ctypes.CDLL(os.path.join(ROOT, "oracle", "liborc.so"))
+        fn = L.orc_fdm_rollout
+        fn.argtypes = [D, D, ctypes.c_long, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int]
+        kind = "port"
+
+        def run(st, act, nac, ndec, nth):
+            fn(st.ctypes.data_as(D), act.ctypes.data_as(D), nac, ndec, substeps, 120, nth)
+    cores = len(os.sched_getaffinity(0))
+    nac = states0_aos.shape[0]
+    # the same decisions as the GPU's timed steps, cycled until ~cpu_seconds of wall time
+    st = states0_aos.copy()
+    acts = np.ascontiguousarray(actions_host)
+    ndec = 0
+    t0 = time.perf_counter()
+    while True:
+        run(st, acts, nac, acts.shape[0], cores)
+        ndec += acts.shape[0]
+        dt = time.perf_counter() - t0
+        if dt >= cpu_seconds:
+            break
+    # single-thread figure on a slice
+    n1 = min(nac, 256)
+    st1 = np.ascontiguousarray(states0_aos[:n1])
+    a1 = np.ascontiguousarray(actions_host[:1, :n1])
+    t1 = time.perf_counter()
+    run(st1, a1, n1, 1, 1)
+    dt1 = time.perf_counter() - t1
+    return {"value": nac * substeps * ndec / dt, "unit": "aircraft-substeps/s", "cores": cores,
+            "kind": kind,
+            "sample": f"{nac} aircraft x {ndec} decisions x {substeps} substeps, fp64, OpenMP "
+                      f"over aircraft on {cores} host threads ({dt:.1f} s)",
+            "single_thread": n1 * substeps / dt1}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--nenv", type=int, default=16384)
+    ap.add_argument("--substeps", type=int, default=6)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        sys.stderr.write("bench.py measures one GPU only: this build has no multi-GPU path "
+                         "(engagements shard with zero communication; see DESIGN.md).\n")
+        sys.exit(2)
+
+    import torch
+    sys.path.insert(0, ROOT)
+    pkg = importlib.import_module(PKG)
+    icm = importlib.import_module(PKG + ".ic")
+
+    nenv, S = args.nenv, args.substeps
+    nac = 2 * nenv
+    sim = pkg.GpuDogfight(nenv, substeps=S, fcs_rate=120)
+    ic = icm.sample_tailchase(nenv, seed=0)
+    sim.seed_rows(torch.as_tensor(ic, device="cuda"))
+    ndec = args.warmup + args.steps
+    acts_host = icm.random_bin_actions(ndec, nac, seed=0)
+    acts = torch.as_tensor(acts_host, device="cuda").contiguous()
+    torch.cuda.synchronize()
+    states0 = sim.states.cpu().numpy().copy()
+
+    for k in range(args.warmup):
+        sim.step(acts[k], want_obs=False)
+    torch.cuda.synchronize()
+    sim.kernel_events = []
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    e0.record()
+    for k in range(args.steps):
+        sim.step(acts[args.warmup + k], want_obs=False)
+    e1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    kev, sim.kernel_events = sim.kernel_events, None
+    ms_step = e0.elapsed_time(e1) / args.steps
+    kern_ms = float(np.mean([s.elapsed_time(e) for s, e in kev]))
+    if not bool(torch.isfinite(sim.states).all()):
+        raise FloatingPointError("non-finite state after the timed steps")
+
+    value = nac * S / (ms_step * 1e-3)
+    flop_launch = FLOP_PER_SUBSTEP * nac * S
+    achieved = flop_launch / (kern_ms * 1e-3) / 1e12
+    line = {
+        "metric": "aircraft FDM substeps/s + env transitions/s at 16k engagements; % vector roofline",
+        "value": value,
+        "unit": "aircraft-substeps/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": value / REF_PUBLISHED_SUBSTEPS,
+        "dtype": "f64",
+        "data": "synthetic",
+        "config": {"workload": "fdm_tailchase_16k", "engagements": nenv, "aircraft": nac,
+                   "substeps_per_step": S, "fcs_rate_hz": 120,
+                   "actions": "i.i.d. uniform 21-bin per channel, held per decision"},
+        "env_transitions_per_s": nenv / (ms_step * 1e-3),
+        "roofline": {"bound": "valu", "achieved": achieved, "peak": PEAK_FP64_TFLOPS,
+                     "unit": "TFLOP/s", "frac": achieved / PEAK_FP64_TFLOPS, "traffic": None,
+                     "kernel": "fdm_step_kernel<120>", "kernel_ms": kern_ms,
+                     "flop_per_launch": flop_launch},
+        "wall_s": wall,
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(states0, acts_host[args.warmup:], S, args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

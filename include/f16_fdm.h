@@ -1,0 +1,44 @@
+/* f16_fdm.h -- C ABI of the MI355X F-16 flight-dynamics path (libf16hip.so).
+ *
+ * Plain pointers and sizes only.  All pointers are device pointers unless stated otherwise;
+ * `stream` is a hipStream_t (the caller's current stream; nothing is synchronised).
+ * Return value: 0 on success, F16_EINVAL (-1) for bad sizes/strides/null pointers,
+ * F16_ERATE (-2) for an unsupported FCS rate, -(1000 + hipError_t) for a launch error.
+ *
+ * State layout: structure-of-arrays, field k (0..100, the reference's FdmState order,
+ * cuda_fdm/ic.py:92-114) of aircraft a at states[k * ld + a]; ld >= nac.
+ */
+#ifndef F16_FDM_H
+#define F16_FDM_H
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Advance nac aircraft by `substeps` 1/60-s steps with each aircraft's action held.
+ * actions: (nac, 4) row-major [aileron, elevator, rudder in -1..1, throttle in 0..1].
+ * obs (optional, may be NULL): (17, obs_ld) structure-of-arrays FDM output of the last substep:
+ *   eci_pos(3) eci_vel(3) euler(3) vUVW(3) alpha beta mach Vt alt_asl.
+ * fcs_rate: FCS component rate in Hz, 120 (root lineage) or 60 (184-D lineage).
+ * Replaces the NVRTC kernel `fdm_step_batch(FdmState*, const double* actions, int nac,
+ * int substeps, double* obs)` (cuda_fdm/gen/fdm_kernel.cu:32) as launched by
+ * GpuDogfight.step (cuda_fdm/gpu_env.py:95-106). */
+int f16_fdm_step_batch(double* states, long ld, const double* actions, int nac, int substeps,
+                       int fcs_rate, double* obs, long obs_ld, void* stream);
+
+/* Seed aircraft states from initial conditions on the device.
+ * ic: (n, 10) rows [lat_deg, lon_deg, alt_ft, vt_fps, phi_deg, theta_deg, psi_deg, alpha_deg,
+ *     beta_deg, fuel_lbs] (geodetic latitude, epa = 0, fuel-flow 0).
+ * rows (optional): (n,) int64 target aircraft index per IC row; NULL seeds rows 0..n-1.
+ * Replaces the host-side build_seed_vector (cuda_fdm/ic.py:117-138) used by
+ * GpuDogfight.reset_ic (cuda_fdm/gpu_env.py:78-92) and the env's IC pools. */
+int f16_seed_batch(const double* ic, int n, int fcs_rate, double* states, long ld,
+                   const long* rows, void* stream);
+
+/* Host pointer out4 <- {registers per lane, static LDS bytes, scratch bytes per lane,
+ * max threads per block} of the step kernel (cf. cuda_fdm/tests/profile_kernel.py:23-33). */
+int f16_fdm_kernel_info(int fcs_rate, int* out4);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* F16_FDM_H */

@@ -1,0 +1,152 @@
+"""ctypes view of the CPU checkers under oracle/ (test infrastructure only).
+
+liborc.so is the C restatement of the reference's Python model; oracle/_ref/libf16ref_*.so
+is the reference's own host-compilable C model built from its sources (present only where the
+reference checkout was available at build time)."""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+ORACLE = os.path.join(ROOT, "oracle")
+D = ctypes.POINTER(ctypes.c_double)
+_c, _i, _l = ctypes.c_double, ctypes.c_int, ctypes.c_long
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data_as(D)
+
+
+class Oracle:
+    def __init__(self, L):
+        self.L = L
+        sig = {
+            "orc_table1d": (_c, [D, D, _i, _c]),
+            "orc_table2d": (_c, [D, _i, D, _i, D, _c, _c]),
+            "orc_model_image": (D, []),
+            "orc_mass": (None, [_c, D]),
+            "orc_atmos": (None, [_c, D]),
+            "orc_fdm_step1": (None, [D, D, _i, _i, D]),
+            "orc_fdm_step_batch": (None, [D, D, _l, _i, _i, D, _i]),
+            "orc_fdm_rollout": (None, [D, D, _l, _i, _i, _i, _i]),
+            "orc_build_seed": (None, [D, _i, D]),
+            "orc_euler_to_quat": (None, [_c, _c, _c, D]),
+            "orc_quat_to_T": (None, [D, D]),
+            "orc_mat_to_quat": (None, [D, D]),
+            "orc_mat_to_euler": (None, [D, D]),
+            "orc_gravity_j2": (None, [D, _c, D]),
+            "orc_vcal_from_mach": (_c, [_c, _c]),
+            "orc_idleff": (_c, []),
+            "orc_geodetic_to_ecef": (None, [_c, _c, _c, D]),
+            "orc_num_threads": (_i, []),
+        }
+        for name, (res, args) in sig.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+
+    def table1d(self, x, y, key):
+        x = np.ascontiguousarray(x, dtype=np.float64); y = np.ascontiguousarray(y, dtype=np.float64)
+        return self.L.orc_table1d(_p(x), _p(y), len(x), key)
+
+    def table2d(self, rx, cx, d, r, c):
+        rx, cx, d = (np.ascontiguousarray(a, dtype=np.float64) for a in (rx, cx, d))
+        return self.L.orc_table2d(_p(rx), len(rx), _p(cx), len(cx), _p(d), r, c)
+
+    def mass(self, fuel):
+        o = np.zeros(25)
+        self.L.orc_mass(fuel, _p(o))
+        return dict(cg=o[0:3], mass=o[3], J=o[4:13].reshape(3, 3), Jinv=o[13:22].reshape(3, 3), rp=o[22:25])
+
+    def atmos(self, alt_ft):
+        o = np.zeros(6)
+        self.L.orc_atmos(alt_ft, _p(o))
+        return dict(zip(("T", "P", "rho", "a", "sigma", "densalt"), o))
+
+    def seed(self, ic_rows, fcs_rate=120):
+        ic_rows = np.ascontiguousarray(ic_rows, dtype=np.float64).reshape(-1, 10)
+        out = np.zeros((len(ic_rows), 101))
+        for i, r in enumerate(ic_rows):
+            r = np.ascontiguousarray(r)
+            self.L.orc_build_seed(_p(r), fcs_rate, _p(out[i]))
+        return out
+
+    def step(self, states, actions, substeps, fcs_rate=120, want_obs=True, nthreads=0):
+        """In place on a C-contiguous (nac, 101) array; returns the (nac, 17) output."""
+        assert states.flags.c_contiguous and states.dtype == np.float64
+        actions = np.ascontiguousarray(actions, dtype=np.float64)
+        obs = np.zeros((states.shape[0], 17)) if want_obs else None
+        self.L.orc_fdm_step_batch(_p(states), _p(actions), states.shape[0], substeps, fcs_rate,
+                                  _p(obs), nthreads)
+        return obs
+
+    def rollout(self, states, actions, substeps, fcs_rate=120, nthreads=0):
+        actions = np.ascontiguousarray(actions, dtype=np.float64)
+        self.L.orc_fdm_rollout(_p(states), _p(actions), states.shape[0], actions.shape[0],
+                               substeps, fcs_rate, nthreads)
+
+
+class RefModel:
+    """The reference's own fdm.cuh compiled for the host (oracle/_ref)."""
+
+    def __init__(self, path):
+        self.L = ctypes.CDLL(path)
+        self.L.ref_fdm_step_batch.argtypes = [D, D, _l, _i, D, _i]
+        self.L.ref_fdm_rollout.argtypes = [D, D, _l, _i, _i, _i]
+        self.L.ref_fcs_rate.restype = _i
+
+    def step(self, states, actions, substeps, nthreads=0):
+        actions = np.ascontiguousarray(actions, dtype=np.float64)
+        obs = np.zeros((states.shape[0], 17))
+        self.L.ref_fdm_step_batch(_p(states), _p(actions), states.shape[0], substeps, _p(obs), nthreads)
+        return obs
+
+
+def build():
+    subprocess.run(["make", "-s", "-C", ORACLE], check=True)
+
+
+def load():
+    path = os.path.join(ORACLE, "liborc.so")
+    if not os.path.exists(path):
+        build()
+    return Oracle(ctypes.CDLL(path))
+
+
+def load_ref(fcs_rate=120):
+    path = os.path.join(ORACLE, "_ref", f"libf16ref_{fcs_rate}.so")
+    return RefModel(path) if os.path.exists(path) else None
+
+
+def golden(name):
+    return np.load(os.path.join(ROOT, "tests", "golden", name))
+
+
+# Column groups whose members share one physical scale: the components of one vector or
+# quaternion of the 101-double state (cuda_fdm/ic.py:92-114) and of the 17-value output.
+def _spans(*bounds):
+    return [list(range(a, b)) for a, b in zip(bounds, bounds[1:])]
+
+
+STATE_GROUPS = (_spans(0, 3, 6, 10, 13, 14, 15, 18, 21, 25, 29, 33, 37, 40, 43, 46, 49, 52,
+                       55, 58, 61, 64, 67, 70, 73, 74, 75, 76, 77, 79, 82)
+                + [[k] for k in range(82, 101)])
+OBS_GROUPS = _spans(0, 3, 6, 9, 12, 14, 15, 16, 17)
+
+
+def rel_err(got, want, floor_frac=1e-3):
+    """Per-state-variable relative error |got - want| / max(|want|, floor), where the floor is
+    floor_frac times the largest magnitude of the variable's group (the vector it belongs to)
+    over the batch.  Components that are zero by symmetry (e.g. the roll acceleration of a
+    wings-level aircraft, pure rounding noise) are judged on their vector's scale."""
+    got = np.asarray(got, dtype=np.float64); want = np.asarray(want, dtype=np.float64)
+    groups = {101: STATE_GROUPS, 17: OBS_GROUPS}.get(want.shape[-1])
+    if groups is None:
+        groups = [[k] for k in range(want.shape[-1])]
+    scale = np.zeros(want.shape[-1])
+    for g in groups:
+        scale[g] = np.max(np.abs(want[..., g])) if want.size else 0.0
+    den = np.maximum(np.abs(want), np.maximum(floor_frac * scale, 1e-300))
+    return np.abs(got - want) / den
