@@ -32,6 +32,18 @@ PEAK_HBM_GBS = 8000.0
 REF_PUBLISHED_SUBSTEPS = 37.0e6
 
 
+def profiled_traffic(name="fdm_step_kernel_tailchase16k.md"):
+    """HBM bytes per launch measured by rocprofv3 FETCH_SIZE/WRITE_SIZE (copy-calibrated) and
+    recorded in the kernel's profile summary; None when no summary is present."""
+    path = os.path.join(ROOT, "profiles", name)
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("traffic_bytes_per_launch:"):
+            return float(line.split(":")[1])
+    return None
+
+
 def cpu_baseline(states0_aos, actions_host, substeps, cpu_seconds):
     """Time the reference's own C model (oracle/_ref, fdm.cuh built from its sources) on the
     host cores; fall back to the C restatement (oracle/liborc.so).  Bounded sample."""
@@ -165,7 +177,7 @@ def main():
                    "actions": "i.i.d. uniform 21-bin per channel, held per decision"},
         "env_transitions_per_s": nenv / (ms_step * 1e-3),
         "roofline": {"bound": "valu", "achieved": achieved, "peak": PEAK_FP64_TFLOPS,
-                     "unit": "TFLOP/s", "frac": achieved / PEAK_FP64_TFLOPS, "traffic": None,
+                     "unit": "TFLOP/s", "frac": achieved / PEAK_FP64_TFLOPS, "traffic": profiled_traffic(),
                      "kernel": "fdm_step_kernel<120>", "kernel_ms": kern_ms,
                      "flop_per_launch": flop_launch},
         "wall_s": wall,

@@ -38,6 +38,16 @@ int f16_seed_batch(const double* ic, int n, int fcs_rate, double* states, long l
  * max threads per block} of the step kernel (cf. cuda_fdm/tests/profile_kernel.py:23-33). */
 int f16_fdm_kernel_info(int fcs_rate, int* out4);
 
+/* Generalized advantage estimation over a rollout buffer (fp32).
+ * rew, val, adv, ret: (T, nenv*nagents) time-major, column = env*nagents + agent;
+ * done: (T, nenv), done[t] = done flag entering step t; last_val: (nenv*nagents);
+ * next_done: (nenv).  gamma_lambda = gamma*lambda rounded once to float.
+ * Replaces the reverse Python loop of PPOGPUTrainer.collect_rollout
+ * (research/competition_36500/runtime/cuda_fdm/ppo_gpu.py:1979-1995). */
+int f16_gae(const float* rew, const float* val, const float* done, const float* last_val,
+            const float* next_done, int T, int nenv, int nagents, float gamma,
+            float gamma_lambda, float* adv, float* ret, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -150,3 +150,88 @@ def rel_err(got, want, floor_frac=1e-3):
         scale[g] = np.max(np.abs(want[..., g])) if want.size else 0.0
     den = np.maximum(np.abs(want), np.maximum(floor_frac * scale, 1e-300))
     return np.abs(got - want) / den
+
+
+# ------------------------------------------------------------------ observation / reward oracle
+class _OrcObrStruct(ctypes.Structure):
+    _fields_ = [("nenv", ctypes.c_long)] + [
+        (n, ctypes.c_void_p) for n in ("hp", "fuel", "t_sec", "prev_att", "prev_valid", "pqr",
+                                      "dealt", "taken", "hp_loss", "act_hist", "prev_x",
+                                      "prev_x_valid", "prev_alt_log", "prev_vel_ned", "accel")]
+
+
+REWARD_CFG = np.array([1.0, 10.0, 0.0001, 5.0, -5.0, 5.0, -5.0, -4.0])  # MY_REWARD_CONFIG
+REWARD_CFG_KEYS = ("own_damage_weight", "damage_scale", "shaping_reward_scale", "win_reward",
+                   "loss_reward", "timeout_win_reward", "timeout_loss_reward",
+                   "timeout_draw_reward")
+
+
+class ObrOracle:
+    """Numpy-backed reconstructor state + the C restatement of BatchObsReward."""
+
+    def __init__(self, orc, nenv, accel=False):
+        self.L = orc.L
+        n = 2 * nenv
+        self.nenv = nenv
+        self.hp = np.ones(n); self.fuel = np.ones(n); self.t_sec = np.zeros(nenv)
+        self.prev_att = np.zeros((n, 3)); self.prev_valid = np.zeros(n, np.uint8)
+        self.pqr = np.zeros((n, 3)); self.dealt = np.zeros(n); self.taken = np.zeros(n)
+        self.hp_loss = np.zeros(n); self.act_hist = np.zeros((n, 5, 4)); self.prev_x = np.zeros(n)
+        self.prev_x_valid = np.zeros(n, np.uint8); self.prev_alt_log = np.zeros(n)
+        self.prev_vel_ned = np.zeros((n, 3)) if accel else None
+        self.accel = np.zeros((n, 3)) if accel else None
+        L = self.L
+        L.orc_state9.argtypes = [D, D]
+        L.orc_obr_reset_envs.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        L.orc_obr_init_reward.argtypes = [ctypes.c_void_p, D, ctypes.c_void_p]
+        L.orc_obr_step.argtypes = [ctypes.c_void_p, D, D, D, ctypes.c_int, ctypes.c_double,
+                                   ctypes.c_double, ctypes.c_double, D, ctypes.c_void_p,
+                                   ctypes.c_void_p]
+        L.orc_obr_build_obs.argtypes = [ctypes.c_void_p, D, ctypes.c_int, ctypes.c_void_p,
+                                        ctypes.c_void_p]
+
+    def _struct(self):
+        s = _OrcObrStruct()
+        s.nenv = self.nenv
+        for name, _ in _OrcObrStruct._fields_[1:]:
+            arr = getattr(self, name)
+            setattr(s, name, None if arr is None else arr.ctypes.data)
+        return s
+
+    def state9(self, states):
+        states = np.ascontiguousarray(states, dtype=np.float64)
+        out = np.zeros((states.shape[0], 9))
+        for i in range(states.shape[0]):
+            self.L.orc_state9(_p(np.ascontiguousarray(states[i])), _p(out[i]))
+        return out
+
+    def reset_envs(self, mask=None):
+        s = self._struct()
+        m = None if mask is None else np.ascontiguousarray(mask, np.uint8)
+        self.L.orc_obr_reset_envs(ctypes.byref(s), None if m is None else m.ctypes.data)
+
+    def init_reward(self, s9, mask=None):
+        s = self._struct()
+        s9 = np.ascontiguousarray(s9, np.float64)
+        m = None if mask is None else np.ascontiguousarray(mask, np.uint8)
+        self.L.orc_obr_init_reward(ctypes.byref(s), _p(s9), None if m is None else m.ctypes.data)
+
+    def step(self, s9, actions, mode=0, coef=5.0, cfg=REWARD_CFG, min_alt=304.8, max_time=200.0):
+        s = self._struct()
+        s9 = np.ascontiguousarray(s9, np.float64)
+        actions = np.ascontiguousarray(actions, np.float64)
+        cfg = np.ascontiguousarray(cfg, np.float64)
+        reward = np.zeros(2 * self.nenv)
+        term = np.zeros(self.nenv, np.uint8); trunc = np.zeros(self.nenv, np.uint8)
+        self.L.orc_obr_step(ctypes.byref(s), _p(s9), _p(actions), _p(cfg), mode, coef, min_alt,
+                            max_time, _p(reward), term.ctypes.data, trunc.ctypes.data)
+        return reward, term.astype(bool), trunc.astype(bool)
+
+    def build_obs(self, s9, obs_dim=184, mask=None):
+        s = self._struct()
+        s9 = np.ascontiguousarray(s9, np.float64)
+        obs = np.zeros((2 * self.nenv, obs_dim), np.float32)
+        m = None if mask is None else np.ascontiguousarray(mask, np.uint8)
+        self.L.orc_obr_build_obs(ctypes.byref(s), _p(s9), obs_dim,
+                                 None if m is None else m.ctypes.data, obs.ctypes.data)
+        return obs
