@@ -1,4 +1,4 @@
-"""ctypes binding of libf16hip.so (C ABI declared in include/f16_fdm.h).
+"""ctypes binding of libf16hip.so (C ABI declared in include/f16_fdm.h and include/f16_obs.h).
 
 torch is imported first so that the process's HIP runtime is torch's; the library then binds
 to that same runtime (libamdhip64.so.7) and launches on torch's streams.  There is no CPU
@@ -17,12 +17,38 @@ F16_ERATE = -2
 F16_ETOOBIG = -3
 
 _vp, _i, _l, _d = ctypes.c_void_p, ctypes.c_int, ctypes.c_long, ctypes.c_double
+
+
+class F16Recon(ctypes.Structure):
+    """include/f16_obs.h F16Recon: device pointers of the reconstructor buffers."""
+    _fields_ = [("hp", _vp), ("fuel", _vp), ("t_sec", _vp), ("prev_att", _vp),
+                ("prev_valid", _vp), ("pqr", _vp), ("dealt", _vp), ("taken", _vp),
+                ("hp_loss", _vp), ("act_hist", _vp), ("prev_x", _vp), ("prev_x_valid", _vp),
+                ("prev_alt_log", _vp), ("prev_vel_ned", _vp), ("accel", _vp), ("ld", _l),
+                ("nenv", _i)]
+
+
+class F16RewardCfg(ctypes.Structure):
+    """include/f16_obs.h F16RewardCfg."""
+    _fields_ = [("own_damage_weight", _d), ("damage_scale", _d), ("shaping_reward_scale", _d),
+                ("win_reward", _d), ("loss_reward", _d), ("timeout_win_reward", _d),
+                ("timeout_loss_reward", _d), ("timeout_draw_reward", _d), ("min_alt_m", _d),
+                ("max_time_s", _d), ("alt_hunt_coef", _d), ("mode", _i)]
+
+
+_RP, _CP = ctypes.POINTER(F16Recon), ctypes.POINTER(F16RewardCfg)
 _SIGNATURES = {
     "f16_fdm_step_batch": (_i, [_vp, _l, _vp, _i, _i, _i, _vp, _l, _vp]),
     "f16_seed_batch": (_i, [_vp, _i, _i, _vp, _l, _vp, _vp]),
     "f16_fdm_kernel_info": (_i, [_i, ctypes.POINTER(_i)]),
     "f16_gae": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, ctypes.c_float, ctypes.c_float, _vp,
                      _vp, _vp]),
+    "f16_obr_advance": (_i, [_vp, _l, _vp, _RP, _CP, _vp, _vp, _vp, _vp]),
+    "f16_obr_init_reward": (_i, [_vp, _l, _vp, _RP, _vp]),
+    "f16_obr_build_obs": (_i, [_vp, _l, _vp, _RP, _i, _vp, _vp]),
+    "f16_env_post_step": (_i, [_vp, _l, _vp, _RP, _CP, _vp, _l, _vp, _i, _vp, _vp, _vp, _vp, _vp,
+                               _vp, _vp, _vp, _vp, _vp]),
+    "f16_state9": (_i, [_vp, _l, _i, _vp, _vp]),
 }
 
 _lib = None

@@ -1,0 +1,683 @@
+// obs_kernels.hip -- observation, reward, termination and autoreset kernels (gfx950).
+//
+// One lane per aircraft; the two aircraft of an engagement sit in adjacent lanes (2e, 2e+1) of
+// one wavefront and trade what each computed about itself (state9, attitude, NED velocity,
+// damage rate, geometry score, ...) through __shfl_xor(x, 1).  So every aircraft's state9 and
+// attitude trigonometry is evaluated once per launch, where the reference evaluates each of
+// them in both the advance thread (one per engagement) and both observation threads.
+//
+// Kernels mirror the reference's launch set (research/competition_36500/runtime/cuda_fdm/
+// obs_reward.py:410-469: advance, init_reward, build_obs; external_observation.cu for the 214-D
+// variant) and add env_post_step, which is GpuDogfightVecEnv.step's whole post-physics sequence
+// (cuda_fdm/rl_env.py:540-580) in one launch.
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+
+#include "f16_capi_common.h"
+#include "f16_obs.h"
+#include "f16_state.h"
+#include "obs_device.h"
+
+namespace f16obs {
+
+constexpr int kObsBlock = 256;
+constexpr double kFuelBurn = 8.0e-5;          // fuel proxy burn per second at 300 m/s
+constexpr double kFuelRef = 300.0;
+constexpr double kSeaLevelRadiusFtT = 20925646.32546;
+
+__device__ __forceinline__ double xch(double v) { return __shfl_xor(v, 1); }
+__device__ __forceinline__ int xchi(int v) { return __shfl_xor(v, 1); }
+
+F16_HD void attitude_rpy(double roll, double pitch, double yaw, Att& A) {
+  const double s9[9] = {0.0, 0.0, 0.0, roll, pitch, yaw, 0.0, 0.0, 0.0};
+  attitude(s9, A);
+}
+
+// This aircraft's kinematics as the observation sees them.
+struct Kin9 {
+  double s9[9];
+  Att A;
+  double vn[3];    // NED velocity R^T (u, v, w)
+  double spd;      // |(u, v, w)|
+};
+
+// The partner aircraft's, received through the lane exchange.
+struct Peer {
+  double s9[9];
+  double R[3][3];
+  double sr, cr, sp, cp, sy, cy;
+  double vn[3];
+  double spd;
+};
+
+// Geometry from this aircraft to its partner.
+struct Geo {
+  double delta[3];  // partner - own position, NED m
+  double dist;
+  double b[3];      // own body-frame unit line of sight R (delta / |delta|)
+  double ata;       // antenna train angle, deg
+};
+
+// Reconstructor values the observation reads for one aircraft.
+struct ObsIn {
+  double hp, fuel, dealt, taken, t;
+  double pqr[3];
+  double accel[3];
+};
+
+__device__ __forceinline__ void make_kin(const double* st, long ld, const Origin& O, Kin9& k) {
+  state9(st, ld, O, k.s9);
+  attitude(k.s9, k.A);
+  mtv3(k.A.R, k.s9 + 6, k.vn);
+  k.spd = norm3(k.s9 + 6);
+}
+
+__device__ __forceinline__ void exchange(const Kin9& k, Peer& p) {
+#pragma unroll
+  for (int i = 0; i < 9; ++i) p.s9[i] = xch(k.s9[i]);
+#pragma unroll
+  for (int i = 0; i < 3; ++i)
+#pragma unroll
+    for (int j = 0; j < 3; ++j) p.R[i][j] = xch(k.A.R[i][j]);
+  p.sr = xch(k.A.sr); p.cr = xch(k.A.cr); p.sp = xch(k.A.sp);
+  p.cp = xch(k.A.cp); p.sy = xch(k.A.sy); p.cy = xch(k.A.cy);
+#pragma unroll
+  for (int i = 0; i < 3; ++i) p.vn[i] = xch(k.vn[i]);
+  p.spd = xch(k.spd);
+}
+
+__device__ __forceinline__ void pair_geo(const Kin9& k, const Peer& p, Geo& g) {
+#pragma unroll
+  for (int i = 0; i < 3; ++i) g.delta[i] = p.s9[i] - k.s9[i];
+  g.dist = norm3(g.delta);
+  double u[3];
+  unit_or_self(g.delta, u);
+  mv3(k.A.R, u, g.b);
+  g.ata = acos(clampd(g.b[0], -1.0, 1.0)) * kR2D;
+}
+
+__device__ __forceinline__ bool finite9(const double s[9]) {
+  bool ok = true;
+#pragma unroll
+  for (int i = 0; i < 9; ++i) ok = ok && isfinite(s[i]);
+  return ok;
+}
+
+__device__ __forceinline__ double safe_side(const Kin9& k, const Peer& p, const Geo& g, double t) {
+  return final_safe_side(k.s9, k.A.R, k.vn, p.s9, p.vn, g.ata, t);
+}
+
+// obs_reward.py:727-744: re-anchor G and the log altitude at time t.
+__device__ __forceinline__ void lane_init_reward(const Kin9& k, const Peer& p, const Geo& g,
+                                                 long a, double t, const F16Recon& r) {
+  const double s_own = safe_side(k, p, g, t);
+  const double s_opp = xch(s_own);
+  r.prev_x[a] = clampd(s_own - s_opp, -1.0, 1.0);
+  r.prev_x_valid[a] = 1;
+  r.prev_alt_log[a] = altitude_log(-k.s9[2]);
+}
+
+struct AdvOut {
+  double reward;
+  bool term, trunc;
+  ObsIn obs;        // this aircraft's reconstructor values after the update
+};
+
+// One decision of the reconstructor, termination and reward for this aircraft
+// (obs_reward.py:571-614 push_actions/advance, 747-819 compute_reward; rl_env.py:467-484).
+__device__ __forceinline__ AdvOut lane_advance(const Kin9& k, const Peer& p, const Geo& g, long a,
+                                               long e, const double* __restrict__ act,
+                                               const F16Recon& r, const F16RewardCfg& c) {
+  const long ld = r.ld;
+  AdvOut out;
+  // action history: roll by one decision, newest first
+  {
+    double h[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) h[i] = r.act_hist[i * ld + a];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) r.act_hist[(i + 4) * ld + a] = h[i];
+#pragma unroll
+    for (int ch = 0; ch < 4; ++ch) r.act_hist[ch * ld + a] = act[4 * a + ch];
+  }
+  // damage exchanged inside the cones, rated at the time entering the decision
+  const double t_old = r.t_sec[e];
+  const double dealt = damage_rate(g.dist * kM2FtObs, g.ata, t_old);
+  const double taken = xch(dealt);
+  const double hp_before = r.hp[a];
+  double hp = hp_before - taken * kDtStep;
+  hp = hp < 0.0 ? 0.0 : hp;
+  const double hp_loss = hp_before - hp;
+  r.hp_loss[a] = hp_loss;
+  r.hp[a] = hp;
+  const double burn = kFuelBurn * (k.spd / kFuelRef);
+  double fuel = r.fuel[a] - burn * kDtStep;
+  fuel = fuel < 0.0 ? 0.0 : fuel;
+  r.fuel[a] = fuel;
+  // body rates from the attitude change since the previous decision
+  const bool prev_valid = r.prev_valid[a] != 0;
+  double pqr[3] = {0.0, 0.0, 0.0};
+  if (prev_valid) {
+    Att P;
+    attitude_rpy(r.prev_att[a], r.prev_att[ld + a], r.prev_att[2 * ld + a], P);
+    so3_rates(P.R, k.A.R, pqr);
+  }
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    r.pqr[i * ld + a] = pqr[i];
+    r.prev_att[i * ld + a] = k.s9[3 + i];
+  }
+  double acc[3] = {0.0, 0.0, 0.0};
+  if (r.accel) {   // 214-D lineage: NED acceleration from the velocity difference
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+      if (prev_valid) acc[i] = (k.vn[i] - r.prev_vel_ned[i * ld + a]) / kDtStep;
+      r.accel[i * ld + a] = acc[i];
+      r.prev_vel_ned[i * ld + a] = k.vn[i];
+    }
+  }
+  r.prev_valid[a] = 1;
+  r.dealt[a] = dealt;
+  r.taken[a] = taken;
+  const double t_new = t_old + kDtStep;
+  if (!(a & 1)) r.t_sec[e] = t_new;
+  // termination (rl_env.py:467-484): hard deck, HP, non-finite; truncation at the time limit
+  const double alt_o = -k.s9[2], alt_t = -p.s9[2];
+  const double hp_t = xch(hp);
+  const bool finite = finite9(k.s9) && finite9(p.s9);
+  const bool te = (alt_o < c.min_alt_m) || (alt_t < c.min_alt_m) || (hp <= 0.0) || (hp_t <= 0.0) ||
+                  !finite;
+  const bool tr = !te && (t_new >= c.max_time_s - kTimeTol);
+  // reward: damage + potential shaping (or altitude hunting) + terminal
+  const double s_own = safe_side(k, p, g, t_new);
+  const double s_opp = xch(s_own);
+  const double G = clampd(s_own - s_opp, -1.0, 1.0);
+  const double alt_log = altitude_log(alt_o);
+  const double alt_log_t = xch(alt_log);
+  const bool pxv = r.prev_x_valid[a] != 0;
+  const double prev_x = r.prev_x[a];
+  const double pxv_t = xch(pxv ? 1.0 : 0.0);
+  const double prev_alt_log_t = xch(r.prev_alt_log[a]);
+  double r_shape;
+  if (c.mode == 1) {
+    r_shape = pxv_t != 0.0 ? (prev_alt_log_t - alt_log_t) * c.alt_hunt_coef : 0.0;
+  } else {
+    const double prev = pxv ? prev_x : G;
+    r_shape = c.shaping_reward_scale / 0.0001 * 5.0 / 200.0 * 0.5 * (prev + G) * kDtStep;
+  }
+  const double loss_t = xch(hp_loss);
+  double r_dmg;
+  if (c.mode == 2) r_dmg = loss_t * c.damage_scale;
+  else if (c.mode == 3) r_dmg = -(hp_loss * c.own_damage_weight) * c.damage_scale;
+  else r_dmg = (loss_t - hp_loss * c.own_damage_weight) * c.damage_scale;
+  const bool own_below = alt_o < kMinAltM, tgt_below = alt_t < kMinAltM;
+  double r_term = 0.0;
+  if (te && own_below) r_term = -(hp > 0.0 ? hp : 0.0) * c.damage_scale;
+  if (te && !own_below && tgt_below) r_term = (hp_t > 0.0 ? hp_t : 0.0) * c.damage_scale;
+  const bool hp_only = te && !own_below && !tgt_below;
+  if (hp_only && hp_t <= 0.0) r_term = r_term + c.win_reward;
+  if (hp_only && hp <= 0.0) r_term = r_term + c.loss_reward;
+  if (tr) r_term = hp > hp_t ? c.timeout_win_reward
+                             : (hp < hp_t ? c.timeout_loss_reward : c.timeout_draw_reward);
+  r.prev_x[a] = G;
+  r.prev_x_valid[a] = 1;
+  r.prev_alt_log[a] = alt_log;
+  out.reward = r_dmg + r_shape + r_term;
+  out.term = te;
+  out.trunc = tr;
+  out.obs.hp = hp; out.obs.fuel = fuel; out.obs.dealt = dealt; out.obs.taken = taken;
+  out.obs.t = t_new;
+#pragma unroll
+  for (int i = 0; i < 3; ++i) { out.obs.pqr[i] = pqr[i]; out.obs.accel[i] = acc[i]; }
+  return out;
+}
+
+__device__ __forceinline__ void put(float* o1, float* o2, int j, double v) {
+  const float f = obs_value(v);
+  o1[j] = f;
+  if (o2) o2[j] = f;
+}
+
+// frames a vector is expressed in (rows = frame axes in NED)
+struct Frames {
+  const double (&Ro)[3][3];
+  const double (&Rt)[3][3];
+  const double (&Fmv)[3][3];
+  const double (&Fov)[3][3];
+  const double (&Flos)[3][3];
+};
+enum VecKind { kRaw = 0, kVel = 1, kRate = 2, kAcc = 3 };
+
+__device__ __forceinline__ void emit3(float* o1, float* o2, int& j, const double F[3][3],
+                                      const double v[3], int kind) {
+  double comp[3];
+  mv3(F, v, comp);
+#pragma unroll
+  for (int q = 0; q < 3; ++q) {
+    double val = comp[q];
+    if (kind == kVel) val = normz(val, -600.0, 600.0);
+    else if (kind == kRate) val = tanh(val / 4.0);
+    else if (kind == kAcc) val = normz(val, -150.0, 150.0);
+    put(o1, o2, j++, val);
+  }
+}
+
+// one vector in the six frames minus `skip` (-1: none), NED first
+__device__ __forceinline__ void emit_vec(float* o1, float* o2, int& j, const Frames& Fr,
+                                         const double v[3], int kind, int skip) {
+  if (skip != 0) {   // NED: the identity, applied as a product like the other frames
+    const double I3[3][3] = {{1.0, 0.0, 0.0}, {0.0, 1.0, 0.0}, {0.0, 0.0, 1.0}};
+    emit3(o1, o2, j, I3, v, kind);
+  }
+  if (skip != 1) emit3(o1, o2, j, Fr.Ro, v, kind);
+  if (skip != 2) emit3(o1, o2, j, Fr.Rt, v, kind);
+  if (skip != 3) emit3(o1, o2, j, Fr.Fmv, v, kind);
+  if (skip != 4) emit3(o1, o2, j, Fr.Fov, v, kind);
+  if (skip != 5) emit3(o1, o2, j, Fr.Flos, v, kind);
+}
+
+// bank angle of the body y axis about the direction-of-motion frame (obs_reward.py:159-166)
+__device__ __forceinline__ void bank_of(const double R[3][3], const double F[3][3], double& s,
+                                        double& co) {
+  const double by[3] = {R[1][0], R[1][1], R[1][2]};
+  const double y1 = F[1][0] * by[0] + F[1][1] * by[1] + F[1][2] * by[2];
+  const double y2 = F[2][0] * by[0] + F[2][1] * by[1] + F[2][2] * by[2];
+  sincos(atan2(y2, y1), &s, &co);
+}
+
+// One observation row (obs_reward.py:617-723; 214-D: cuda_fdm/external_observation.cu).
+// Writes to o1 and, if non-null, o2.  All lanes of a pair must call it together.
+__device__ __forceinline__ void lane_build_obs(const Kin9& k, const Peer& p, const Geo& g,
+                                               const ObsIn& own, long a, const F16Recon& r,
+                                               int obs_dim, float* o1, float* o2) {
+  const long ld = r.ld;
+  // partner's reconstructor values and partner-side geometry
+  ObsIn tgt;
+  tgt.hp = xch(own.hp); tgt.fuel = xch(own.fuel);
+  double pb[3];
+#pragma unroll
+  for (int i = 0; i < 3; ++i) pb[i] = xch(g.b[i]);
+  const double en_ata = xch(g.ata);
+  // own direction-of-motion frame and bank; the partner's arrive by exchange
+  double Fmv[3][3];
+  dir_frame(k.vn, Fmv);
+  double bs, bc;
+  bank_of(k.A.R, Fmv, bs, bc);
+  const double tbs = xch(bs), tbc = xch(bc);
+  double Fov[3][3];
+#pragma unroll
+  for (int i = 0; i < 3; ++i)
+#pragma unroll
+    for (int j = 0; j < 3; ++j) Fov[i][j] = xch(Fmv[i][j]);
+  // body rates in NED (partner's by exchange), accelerations
+  double om_o[3];
+  mtv3(k.A.R, own.pqr, om_o);
+  double om_t[3], acc_t[3];
+#pragma unroll
+  for (int i = 0; i < 3; ++i) { om_t[i] = xch(om_o[i]); acc_t[i] = xch(own.accel[i]); }
+
+  const double own_alt = -k.s9[2], tgt_alt = -p.s9[2];
+  double los_u[3] = {0.0, 0.0, 0.0}, closure = 0.0;
+  if (g.dist > 1e-6) {
+#pragma unroll
+    for (int i = 0; i < 3; ++i) los_u[i] = g.delta[i] / g.dist;
+    closure = (k.vn[0] - p.vn[0]) * los_u[0] + (k.vn[1] - p.vn[1]) * los_u[1] +
+              (k.vn[2] - p.vn[2]) * los_u[2];
+  }
+  // aspect angle from the partner's body-frame line of sight, signed by its body y
+  const double pt1 = -pb[1], pt2 = pb[2];
+  const double sgn = pt1 > 0.0 ? 1.0 : (pt1 < 0.0 ? -1.0 : (pt2 >= 0.0 ? 1.0 : -1.0));
+  const double aa = sgn * acos(clampd(-pb[0], -1.0, 1.0)) * kR2D;
+  const double az = atan2(g.b[1], g.b[0]) * kR2D;
+  const double el = -asin(clampd(g.b[2], -1.0, 1.0)) * kR2D;
+  const double u = k.s9[6], v = k.s9[7], w = k.s9[8];
+  double aoa = 0.0, ss = 0.0;
+  if (!(k.spd < 1.0)) {
+    aoa = atan2(w, u) * kR2D;
+    ss = atan2(v, sqrt(u * u + w * w)) * kR2D;
+  }
+  const double e_adv = (own_alt + k.spd * k.spd / (2.0 * kGacc)) -
+                       (tgt_alt + p.spd * p.spd / (2.0 * kGacc));
+  const double t = own.t;
+  const double cone = t >= 150.0 ? 3.0 : (t >= 100.0 ? 2.0 : 1.0);
+  const double maxr_ft = t >= 150.0 ? 4000.0 : (t >= 100.0 ? 3500.0 : 3000.0);
+  const double cc = cone > 1e-6 ? cone : 1e-6;
+  const double min_r = 500.0 * kFt2M, max_r = maxr_ft * kFt2M;
+  double span = max_r - min_r;
+  span = span < 1e-6 ? 1e-6 : span;
+  double pf_ata = 1.0 - fabs(g.ata) / 30.0;
+  pf_ata = pf_ata < 0.0 ? 0.0 : pf_ata;
+  double pf_rng = 1.0 - g.dist / 3000.0;
+  pf_rng = pf_rng < 0.0 ? 0.0 : pf_rng;
+  double s_, c_;
+  int j = 0;
+  put(o1, o2, j++, normz(k.spd, 0.0, 600.0));
+  put(o1, o2, j++, normz(p.spd, 0.0, 600.0));
+  put(o1, o2, j++, tanh(aoa / 30.0));
+  put(o1, o2, j++, tanh(ss / 15.0));
+  put(o1, o2, j++, tanh((own_alt - kMinAltM) / 300.0));
+  put(o1, o2, j++, normz(-k.vn[2], -100.0, 100.0));
+  put(o1, o2, j++, normz(own.hp, 0.0, 1.0));
+  put(o1, o2, j++, normz(tgt.hp, 0.0, 1.0));
+  put(o1, o2, j++, own.hp - tgt.hp);
+  put(o1, o2, j++, e_adv / (fabs(e_adv) + 5000.0));
+  put(o1, o2, j++, normz(g.dist, 0.0, 2500.0));
+  put(o1, o2, j++, normz(closure, -1000.0, 1000.0));
+  sincos(g.ata * kD2R, &s_, &c_); put(o1, o2, j++, s_); put(o1, o2, j++, c_);
+  sincos(aa * kD2R, &s_, &c_); put(o1, o2, j++, s_); put(o1, o2, j++, c_);
+  sincos(az * kD2R, &s_, &c_); put(o1, o2, j++, s_); put(o1, o2, j++, c_);
+  sincos(el * kD2R, &s_, &c_); put(o1, o2, j++, s_); put(o1, o2, j++, c_);
+  put(o1, o2, j++, 2.0 * exp(-((g.ata / 3.0) * (g.ata / 3.0))) - 1.0);
+  put(o1, o2, j++, tanh((cone - fabs(g.ata)) / cc));
+  put(o1, o2, j++, 2.0 * exp(-((en_ata / 3.0) * (en_ata / 3.0))) - 1.0);
+  put(o1, o2, j++, tanh((cone - fabs(en_ata)) / cc));
+  put(o1, o2, j++, tanh((g.dist - min_r) / span));
+  put(o1, o2, j++, tanh((max_r - g.dist) / span));
+  put(o1, o2, j++, normz(t, 0.0, 200.0));
+  put(o1, o2, j++, k.A.sr); put(o1, o2, j++, k.A.cr);
+  put(o1, o2, j++, k.A.sp); put(o1, o2, j++, k.A.cp);
+  put(o1, o2, j++, k.A.sy); put(o1, o2, j++, k.A.cy);
+  put(o1, o2, j++, p.sr); put(o1, o2, j++, p.cr);
+  put(o1, o2, j++, p.sp); put(o1, o2, j++, p.cp);
+  put(o1, o2, j++, p.sy); put(o1, o2, j++, p.cy);
+  put(o1, o2, j++, bs); put(o1, o2, j++, bc);
+  put(o1, o2, j++, tbs); put(o1, o2, j++, tbc);
+  put(o1, o2, j++, normz(own.fuel, 0.0, 1.0));
+  put(o1, o2, j++, normz(tgt.fuel, 0.0, 1.0));
+  put(o1, o2, j++, clampd(2.0 * own.dealt - 1.0, -1.0, 1.0));
+  put(o1, o2, j++, clampd(2.0 * own.taken - 1.0, -1.0, 1.0));
+  put(o1, o2, j++, 2.0 * (pf_ata * pf_rng) - 1.0);
+  put(o1, o2, j++, normz(own_alt, 0.0, 15000.0));
+  put(o1, o2, j++, normz(tgt_alt, 0.0, 15000.0));
+  // 38 (vector, frame) pairs x 3 (my_observation.py _VEC_LAYOUT), then 10 more for 214-D.
+  // Frames: 0 NED, 1 own body, 2 partner body, 3 own motion, 4 partner motion, 5 line of sight.
+  double Flos[3][3];
+  dir_frame(g.delta, Flos);
+  const Frames Fr{k.A.R, p.R, Fmv, Fov, Flos};
+  double rel_vn[3];
+#pragma unroll
+  for (int i = 0; i < 3; ++i) rel_vn[i] = p.vn[i] - k.vn[i];
+  const double grav[3] = {0.0, 0.0, 1.0};
+  emit_vec(o1, o2, j, Fr, grav, kRaw, 0);
+  emit_vec(o1, o2, j, Fr, los_u, kRaw, 5);
+  emit_vec(o1, o2, j, Fr, k.vn, kVel, 3);
+  emit_vec(o1, o2, j, Fr, p.vn, kVel, 4);
+  emit_vec(o1, o2, j, Fr, rel_vn, kVel, -1);
+  emit_vec(o1, o2, j, Fr, om_o, kRate, -1);
+  emit_vec(o1, o2, j, Fr, om_t, kRate, -1);
+  if (obs_dim == 214) {
+    emit_vec(o1, o2, j, Fr, own.accel, kAcc, 3);
+    emit_vec(o1, o2, j, Fr, acc_t, kAcc, 4);
+  }
+#pragma unroll
+  for (int i = 0; i < kActHist; ++i) put(o1, o2, j++, r.act_hist[i * ld + a]);
+}
+
+__device__ __forceinline__ ObsIn load_obs_in(const F16Recon& r, long a, long e) {
+  ObsIn o;
+  const long ld = r.ld;
+  o.hp = r.hp[a]; o.fuel = r.fuel[a]; o.dealt = r.dealt[a]; o.taken = r.taken[a];
+  o.t = r.t_sec[e];
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    o.pqr[i] = r.pqr[i * ld + a];
+    o.accel[i] = r.accel ? r.accel[i * ld + a] : 0.0;
+  }
+  return o;
+}
+
+// ------------------------------------------------------------------------------ kernels
+__global__ __launch_bounds__(kObsBlock) void advance_kernel(
+    const double* __restrict__ st, long ld, const double* __restrict__ act, F16Recon r,
+    F16RewardCfg c, Origin O, double* __restrict__ reward, unsigned char* __restrict__ term,
+    unsigned char* __restrict__ trunc) {
+  const long a = (long)blockIdx.x * kObsBlock + threadIdx.x;
+  if (a >= 2L * r.nenv) return;     // nac is even: both lanes of a pair leave together
+  const long e = a >> 1;
+  Kin9 k;
+  make_kin(st + a, ld, O, k);
+  Peer p;
+  exchange(k, p);
+  Geo g;
+  pair_geo(k, p, g);
+  const AdvOut o = lane_advance(k, p, g, a, e, act, r, c);
+  reward[a] = o.reward;
+  if (!(a & 1)) { term[e] = o.term; trunc[e] = o.trunc; }
+}
+
+__global__ __launch_bounds__(kObsBlock) void init_reward_kernel(
+    const double* __restrict__ st, long ld, const unsigned char* __restrict__ mask, F16Recon r,
+    Origin O) {
+  const long a = (long)blockIdx.x * kObsBlock + threadIdx.x;
+  if (a >= 2L * r.nenv) return;
+  const long e = a >> 1;
+  if (mask && !mask[e]) return;      // per engagement: the pair leaves together
+  Kin9 k;
+  make_kin(st + a, ld, O, k);
+  Peer p;
+  exchange(k, p);
+  Geo g;
+  pair_geo(k, p, g);
+  lane_init_reward(k, p, g, a, r.t_sec[e], r);
+}
+
+__global__ __launch_bounds__(kObsBlock) void build_obs_kernel(
+    const double* __restrict__ st, long ld, const unsigned char* __restrict__ mask, F16Recon r,
+    Origin O, int obs_dim, float* __restrict__ obs) {
+  const long a = (long)blockIdx.x * kObsBlock + threadIdx.x;
+  if (a >= 2L * r.nenv) return;
+  const long e = a >> 1;
+  if (mask && !mask[e]) return;
+  Kin9 k;
+  make_kin(st + a, ld, O, k);
+  Peer p;
+  exchange(k, p);
+  Geo g;
+  pair_geo(k, p, g);
+  const ObsIn in = load_obs_in(r, a, e);
+  lane_build_obs(k, p, g, in, a, r, obs_dim, obs + a * obs_dim, nullptr);
+}
+
+__global__ __launch_bounds__(kObsBlock) void env_post_step_kernel(
+    double* __restrict__ st, long ld, const double* __restrict__ act, F16Recon r, F16RewardCfg c,
+    Origin O, const double* __restrict__ pool, long pool_size, const long* __restrict__ pick,
+    int obs_dim, float* __restrict__ obs, float* __restrict__ tobs, double* __restrict__ reward,
+    unsigned char* __restrict__ term, unsigned char* __restrict__ trunc,
+    unsigned char* __restrict__ done, double* __restrict__ thp, double* __restrict__ talt,
+    unsigned char* __restrict__ tfin) {
+  const long a = (long)blockIdx.x * kObsBlock + threadIdx.x;
+  if (a >= 2L * r.nenv) return;
+  const long e = a >> 1;
+  const int odd = (int)(a & 1);
+  if (tfin) {   // rl_env.py:545: every state value of both aircraft finite after the physics
+    int fin = 1;
+    for (int f = 0; f < F16S_N; ++f) fin &= isfinite(st[f * ld + a]) ? 1 : 0;
+    fin &= xchi(fin);
+    if (!odd) tfin[e] = (unsigned char)fin;
+  }
+  Kin9 k;
+  make_kin(st + a, ld, O, k);
+  Peer p;
+  exchange(k, p);
+  Geo g;
+  pair_geo(k, p, g);
+  const AdvOut o = lane_advance(k, p, g, a, e, act, r, c);
+  reward[a] = o.reward;
+  const bool d = o.term || o.trunc;
+  if (!odd) { term[e] = o.term; trunc[e] = o.trunc; done[e] = d; }
+  if (thp) thp[a] = o.obs.hp;
+  if (talt) {
+    const double x = st[a], y = st[ld + a], z = st[2 * ld + a];
+    talt[a] = (sqrt(x * x + y * y + z * z) - kSeaLevelRadiusFtT) * kFt2M;
+  }
+  float* row = obs + a * obs_dim;
+  // terminal observation (rl_env.py:552-554); live engagements keep it as their observation
+  lane_build_obs(k, p, g, o.obs, a, r, obs_dim, tobs ? tobs + a * obs_dim : row,
+                 (tobs && !d) ? row : nullptr);
+  if (!d) return;                    // per engagement: the pair leaves together
+  // autoreset from the initial-condition pool (rl_env.py:559-577)
+  const long pk = pick[e];
+  const bool ok = pk >= 0 && pk < pool_size;
+  const double* src = pool + (ok ? pk * 2 + odd : 0) * F16S_N;
+  const double qnan = __builtin_nan("");
+  if (ok) {
+    for (int f = 0; f < F16S_N; ++f) st[f * ld + a] = src[f];
+  } else {
+    for (int f = 0; f < F16S_N; ++f) st[f * ld + a] = qnan;
+  }
+  r.hp[a] = 1.0; r.fuel[a] = 1.0;
+  r.prev_valid[a] = 0; r.prev_x_valid[a] = 0;
+  r.dealt[a] = 0.0; r.taken[a] = 0.0; r.hp_loss[a] = 0.0; r.prev_x[a] = 0.0;
+  r.prev_alt_log[a] = 0.0;
+  for (int i = 0; i < 3; ++i) {
+    r.prev_att[i * ld + a] = 0.0;
+    r.pqr[i * ld + a] = 0.0;
+    if (r.accel) { r.accel[i * ld + a] = 0.0; r.prev_vel_ned[i * ld + a] = 0.0; }
+  }
+  for (int i = 0; i < kActHist; ++i) r.act_hist[i * ld + a] = 0.0;
+  if (!odd) r.t_sec[e] = 0.0;
+  Kin9 k2;
+  if (ok) {
+    make_kin(src, 1, O, k2);
+  } else {
+    const double nan14[14] = {qnan, qnan, qnan, qnan, qnan, qnan, qnan,
+                              qnan, qnan, qnan, qnan, qnan, qnan, qnan};   // fields 0..13
+    make_kin(nan14, 1, O, k2);
+  }
+  Peer p2;
+  exchange(k2, p2);
+  Geo g2;
+  pair_geo(k2, p2, g2);
+  lane_init_reward(k2, p2, g2, a, 0.0, r);
+  ObsIn fresh;
+  fresh.hp = 1.0; fresh.fuel = 1.0; fresh.dealt = 0.0; fresh.taken = 0.0; fresh.t = 0.0;
+  for (int i = 0; i < 3; ++i) { fresh.pqr[i] = 0.0; fresh.accel[i] = 0.0; }
+  lane_build_obs(k2, p2, g2, fresh, a, r, obs_dim, row, nullptr);
+}
+
+// rl_env.py:583-592 state9_flat: (nac, 9) float64 rows N/E/D m, roll/pitch/yaw deg, u/v/w m/s
+__global__ __launch_bounds__(kObsBlock) void state9_kernel(const double* __restrict__ st, long ld,
+                                                            int nac, Origin O,
+                                                            double* __restrict__ out) {
+  const long a = (long)blockIdx.x * kObsBlock + threadIdx.x;
+  if (a >= nac) return;
+  double s9[9];
+  state9(st + a, ld, O, s9);
+#pragma unroll
+  for (int i = 0; i < 9; ++i) out[a * 9 + i] = s9[i];
+}
+
+// ------------------------------------------------------------------------------ host side
+static Origin make_origin() {
+  // official BaseLat/BaseLon (cuda_fdm/obs_reward.py:376-384), same expressions as the checker
+  const double la = 37.240778 * kD2R, lo = 131.869556 * kD2R;
+  Origin O;
+  O.slat = sin(la); O.clat = cos(la); O.slon = sin(lo); O.clon = cos(lo);
+  const double N = kWgsA / sqrt(1.0 - kWgsE2 * O.slat * O.slat);
+  O.ox = (N + 0.0) * O.clat * O.clon;
+  O.oy = (N + 0.0) * O.clat * O.slon;
+  O.oz = (N * (1.0 - kWgsE2) + 0.0) * O.slat;
+  O.b = kWgsA * sqrt(1.0 - kWgsE2);
+  O.ep2 = (kWgsA * kWgsA - O.b * O.b) / (O.b * O.b);
+  return O;
+}
+
+static const Origin& origin() {
+  static const Origin O = make_origin();
+  return O;
+}
+
+static int check_recon(const F16Recon* r, bool need_accel) {
+  if (!r || r->nenv < 0) return F16_EINVAL;
+  if (r->nenv == 0) return 0;
+  if ((long)r->nenv * 2 > 0x7fffffffL || r->ld < 2L * r->nenv) return F16_EINVAL;
+  if (!r->hp || !r->fuel || !r->t_sec || !r->prev_att || !r->prev_valid || !r->pqr || !r->dealt ||
+      !r->taken || !r->hp_loss || !r->act_hist || !r->prev_x || !r->prev_x_valid ||
+      !r->prev_alt_log)
+    return F16_EINVAL;
+  if ((r->accel == nullptr) != (r->prev_vel_ned == nullptr)) return F16_EINVAL;
+  if (need_accel && !r->accel) return F16_EINVAL;
+  return 0;
+}
+
+static int check_cfg(const F16RewardCfg* c) {
+  if (!c || c->mode < 0 || c->mode > 3) return F16_EINVAL;
+  return 0;
+}
+
+static dim3 grid_for(int nenv) {
+  return dim3((unsigned)((2L * nenv + kObsBlock - 1) / kObsBlock));
+}
+
+}  // namespace f16obs
+
+using namespace f16obs;
+
+extern "C" int f16_obr_advance(const double* states, long ld, const double* actions,
+                               const F16Recon* rec, const F16RewardCfg* cfg, double* reward,
+                               unsigned char* term, unsigned char* trunc, void* stream) {
+  int rc = check_recon(rec, false);
+  if (rc) return rc;
+  if ((rc = check_cfg(cfg))) return rc;
+  if (rec->nenv == 0) return 0;
+  if (!states || !actions || !reward || !term || !trunc || ld < 2L * rec->nenv) return F16_EINVAL;
+  hipLaunchKernelGGL(advance_kernel, grid_for(rec->nenv), dim3(kObsBlock), 0,
+                     (hipStream_t)stream, states, ld, actions, *rec, *cfg, origin(), reward,
+                     term, trunc);
+  return f16_last_error();
+}
+
+extern "C" int f16_obr_init_reward(const double* states, long ld, const unsigned char* env_mask,
+                                   const F16Recon* rec, void* stream) {
+  int rc = check_recon(rec, false);
+  if (rc) return rc;
+  if (rec->nenv == 0) return 0;
+  if (!states || ld < 2L * rec->nenv) return F16_EINVAL;
+  hipLaunchKernelGGL(init_reward_kernel, grid_for(rec->nenv), dim3(kObsBlock), 0,
+                     (hipStream_t)stream, states, ld, env_mask, *rec, origin());
+  return f16_last_error();
+}
+
+extern "C" int f16_obr_build_obs(const double* states, long ld, const unsigned char* env_mask,
+                                 const F16Recon* rec, int obs_dim, float* obs, void* stream) {
+  if (obs_dim != 184 && obs_dim != 214) return F16_EINVAL;
+  int rc = check_recon(rec, obs_dim == 214);
+  if (rc) return rc;
+  if (rec->nenv == 0) return 0;
+  if (!states || !obs || ld < 2L * rec->nenv) return F16_EINVAL;
+  hipLaunchKernelGGL(build_obs_kernel, grid_for(rec->nenv), dim3(kObsBlock), 0,
+                     (hipStream_t)stream, states, ld, env_mask, *rec, origin(), obs_dim, obs);
+  return f16_last_error();
+}
+
+extern "C" int f16_env_post_step(double* states, long ld, const double* actions,
+                                 const F16Recon* rec, const F16RewardCfg* cfg,
+                                 const double* ic_pool, long pool_size, const long* pick,
+                                 int obs_dim, float* obs, float* terminal_obs, double* reward,
+                                 unsigned char* term, unsigned char* trunc, unsigned char* done,
+                                 double* terminal_hp, double* terminal_alt_m,
+                                 unsigned char* terminal_finite, void* stream) {
+  if (obs_dim != 184 && obs_dim != 214) return F16_EINVAL;
+  int rc = check_recon(rec, obs_dim == 214);
+  if (rc) return rc;
+  if ((rc = check_cfg(cfg))) return rc;
+  if (rec->nenv == 0) return 0;
+  if (!states || !actions || !obs || !reward || !term || !trunc || !done || !ic_pool || !pick ||
+      pool_size < 1 || ld < 2L * rec->nenv)
+    return F16_EINVAL;
+  hipLaunchKernelGGL(env_post_step_kernel, grid_for(rec->nenv), dim3(kObsBlock), 0,
+                     (hipStream_t)stream, states, ld, actions, *rec, *cfg, origin(), ic_pool,
+                     pool_size, pick, obs_dim, obs, terminal_obs, reward, term, trunc, done,
+                     terminal_hp, terminal_alt_m, terminal_finite);
+  return f16_last_error();
+}
+
+extern "C" int f16_state9(const double* states, long ld, int nac, double* s9, void* stream) {
+  if (nac < 0 || ld < nac) return F16_EINVAL;
+  if (nac == 0) return 0;
+  if (!states || !s9) return F16_EINVAL;
+  hipLaunchKernelGGL(state9_kernel, dim3((unsigned)((nac + kObsBlock - 1) / kObsBlock)),
+                     dim3(kObsBlock), 0, (hipStream_t)stream, states, ld, nac, origin(), s9);
+  return f16_last_error();
+}

@@ -107,3 +107,48 @@ def random_bin_actions(ndec, nac, seed=0, num_bins=21):
     """(ndec, nac, 4) controls from i.i.d. uniform bins (BASELINE C1/C2 action model)."""
     rng = np.random.default_rng(seed)
     return bins_to_controls(rng.integers(0, num_bins, size=(ndec, nac, 4)), num_bins)
+
+
+# contest distribution (research/competition_36500/runtime/cuda_fdm/rl_env.py:199-212)
+CONTEST_CENTER_N = 3500.0
+CONTEST_CENTER_E = 0.0
+CONTEST_ALT_FT = (2000.0, 30000.0)
+CONTEST_SPEED_MPS = (200.0, 300.0)
+CONTEST_DIST_A_FT = (2000.0, 2500.0, 3000.0)
+CONTEST_DIST_HEADON_FT = 5539.0 / FT2M
+CONTEST_FUEL_LBS = 3000.0
+
+
+def contest_pair(rng, scenario_b_prob=0.0, alt_ft=None, speed=None, side_swap=None,
+                 scenario_b=None, head_swap=None, dist_ft=None):
+    """One engagement's (own, target) IC rows from the contest distribution, drawing from the
+    numpy Generator in the reference's order (rl_env.py:218-250): altitude, speed, side swap,
+    scenario B, then heading swap and 3-9 distance.  Scenario A puts the two aircraft abeam on
+    the north axis with opposite east/west headings; B is head-on."""
+    alt_ft = float(rng.uniform(*CONTEST_ALT_FT) if alt_ft is None else alt_ft)
+    speed = float(rng.uniform(*CONTEST_SPEED_MPS) if speed is None else speed)
+    side_swap = bool(rng.integers(0, 2) if side_swap is None else side_swap)
+    scenario_b = bool(rng.random() < scenario_b_prob if scenario_b is None else scenario_b)
+    if scenario_b:
+        half = 0.5 * CONTEST_DIST_HEADON_FT * FT2M
+        own_hdg, tgt_hdg = (0.0, 180.0) if side_swap else (180.0, 0.0)
+    else:
+        head_swap = bool(rng.integers(0, 2) if head_swap is None else head_swap)
+        dist_ft = float(rng.choice(np.asarray(CONTEST_DIST_A_FT)) if dist_ft is None else dist_ft)
+        half = 0.5 * dist_ft * FT2M
+        own_hdg, tgt_hdg = (270.0, 90.0) if head_swap else (90.0, 270.0)
+    own_n = CONTEST_CENTER_N + (-half if side_swap else half)
+    tgt_n = CONTEST_CENTER_N + (half if side_swap else -half)
+    d = -alt_ft * FT2M
+    la, lo, h = ned_to_geodetic(np.array([own_n, tgt_n]), np.array([CONTEST_CENTER_E] * 2),
+                                np.array([d, d]))
+    return [ic_row(la[0], lo[0], h[0], speed * M2FT, own_hdg, CONTEST_FUEL_LBS),
+            ic_row(la[1], lo[1], h[1], speed * M2FT, tgt_hdg, CONTEST_FUEL_LBS)]
+
+
+def contest_rows(rng, npairs, scenario_b_prob=0.0):
+    """(2*npairs, 10) IC rows, plane 0 = ownship, plane 1 = target."""
+    rows = []
+    for _ in range(npairs):
+        rows += contest_pair(rng, scenario_b_prob)
+    return np.asarray(rows, dtype=np.float64).reshape(-1, 10)

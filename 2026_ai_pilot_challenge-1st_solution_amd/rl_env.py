@@ -1,0 +1,276 @@
+"""GpuDogfightVecEnv: batched 1v1 engagements (physics + observation + reward) on one GPU.
+
+Mirror of the reference's ``GpuDogfightVecEnv`` (research/competition_36500/runtime/cuda_fdm/
+rl_env.py:175-592): same constructor, attributes, reset / reset_evaluation / step / state9
+contract and ``info`` keys.  The post-physics half of ``step`` (advance, reward, termination,
+terminal observation, autoreset from the GPU initial-condition pool, re-anchoring and the new
+observation) is one kernel launch (f16_env_post_step) instead of three kernels and about ten
+torch operations; nothing inside ``step`` synchronises with the host.
+"""
+import numpy as np
+import torch
+
+from . import _lib
+from . import ic as icm
+from .gpu_env import GpuDogfight, STATE_N
+from .obs_reward import (MY_REWARD_CONFIG, OBS_SIZE, OBS_SIZE_EXT, BatchObsReward,
+                         reward_cfg_struct, validate_reward_mode)
+
+FT2M = 0.3048
+SEA_LEVEL_RADIUS_FT = 20925646.32546
+HARD_DECK_M = 1000.0 * FT2M
+NEUTRAL_ACTION = (0.0, 0.0, 0.0, 1.0)
+
+
+class GpuDogfightVecEnv:
+    """nenv engagements x 2 aircraft.  obs_dim 184 (default) or 214 (with NED accelerations)."""
+
+    def __init__(self, nenv, substeps=6, precision="fp64", block=128, seed=None, device="cuda",
+                 min_altitude_m=304.8, max_engage_time_s=200.0, reward_cfg=None, reward_mode=0,
+                 alt_hunt_coef=5.0, scenario="mixed", headon_distance_m=5539.0, fcs_rate=60,
+                 obs_dim=OBS_SIZE, ic_pool_size=4096):
+        if precision != "fp64":
+            raise ValueError("GpuDogfightVecEnv supports precision='fp64' only")
+        if obs_dim not in (OBS_SIZE, OBS_SIZE_EXT):
+            raise ValueError("obs_dim must be 184 or 214")
+        self.sim = GpuDogfight(nenv, substeps=substeps, planes_per_env=2, precision=precision,
+                               block=block, fcs_rate=fcs_rate, device=device)
+        self.nenv = int(nenv)
+        self.nac = self.sim.nac
+        self.substeps = int(substeps)
+        self.device = torch.device(device)
+        self.seed = 0 if seed is None else int(seed)
+        self.rng = np.random.default_rng(seed)
+        self.scenario = scenario
+        self.headon_distance_m = float(headon_distance_m)
+        self.scenario_b_prob = 0.0
+        self.min_altitude_m = float(min_altitude_m)
+        self.max_engage_time_s = float(max_engage_time_s)
+        self.reward_cfg = dict(MY_REWARD_CONFIG if reward_cfg is None else reward_cfg)
+        self.reward_mode = validate_reward_mode(reward_mode, alt_hunt_coef)
+        self.alt_hunt_coef = float(alt_hunt_coef)
+        self.OBS_SIZE = int(obs_dim)
+        self.obr = BatchObsReward(nenv, device=device)
+        if self.OBS_SIZE == OBS_SIZE_EXT:
+            self.obr.enable_external_observations()
+        self.ic_pool = None
+        self.ic_pool_size = int(ic_pool_size)
+        self._evaluation_seed_bank = None
+        self._evaluation_seed_bank_key = None
+        self._evaluation_seed_metadata = None
+        n, ne, dev = self.nac, self.nenv, self.device
+        self._obs = torch.zeros(n, self.OBS_SIZE, dtype=torch.float32, device=dev)
+        self._term = torch.zeros(ne, dtype=torch.uint8, device=dev)
+        self._trunc = torch.zeros(ne, dtype=torch.uint8, device=dev)
+        self._done = torch.zeros(ne, dtype=torch.uint8, device=dev)
+        self._tfin = torch.zeros(ne, dtype=torch.uint8, device=dev)
+        self._neutral = torch.tensor([NEUTRAL_ACTION], dtype=torch.float64,
+                                     device=dev).expand(n, 4).contiguous()
+        # When set to a list, step() appends (start, end) events around its post-physics launch.
+        self.kernel_events = None
+
+    # ---- initial conditions (rl_env.py:218-375) ----
+    def _sample_pairs(self, npairs):
+        return icm.contest_rows(self.rng, npairs, self.scenario_b_prob)
+
+    def _initialize_physical_seeds(self, rows):
+        """(2P, 10) IC rows -> (P, 2, 101) float64 states after the neutral tick."""
+        count = rows.shape[0]
+        init = GpuDogfight(count // 2, precision=self.sim.precision, fcs_rate=self.sim.fcs_rate,
+                           device=self.device)
+        init.seed_rows(torch.as_tensor(rows, dtype=torch.float64, device=self.device))
+        init.step(torch.tensor([NEUTRAL_ACTION] * count, dtype=torch.float64, device=self.device),
+                  substeps=1, want_obs=False)
+        return init.states.reshape(count // 2, 2, STATE_N).contiguous()
+
+    def _ensure_ic_pool(self):
+        if self.ic_pool is None:
+            self.ic_pool = self._initialize_physical_seeds(self._sample_pairs(self.ic_pool_size))
+
+    def _seed_envs(self, env_indices):
+        """Re-seed the given engagements with fresh contest ICs (no neutral tick, rl_env.py:436-451)."""
+        if not len(env_indices):
+            return
+        rows = self._sample_pairs(len(env_indices))
+        ac = torch.tensor([[2 * e, 2 * e + 1] for e in env_indices], dtype=torch.int64,
+                          device=self.device).flatten()
+        self.sim.seed_rows(torch.as_tensor(rows, dtype=torch.float64, device=self.device), ac)
+
+    # ---- reset (rl_env.py:362-434) ----
+    def reset(self, stagger=True, max_stagger_steps=256, warmup_action_fn=None):
+        """Fresh contest ICs for every engagement; with stagger, each engagement is advanced a
+        random number of valid decisions so episode phases are spread.  Returns obs (nenv,2,D)."""
+        seeds = self._initialize_physical_seeds(self._sample_pairs(self.nenv))
+        if not bool(torch.isfinite(seeds).all()):
+            raise FloatingPointError("non-finite initial physical states")
+        self.sim.load_seed(seeds)
+        self.obr.reset_all()
+        self.obr.kernel_init_reward_state(self.sim.states)
+        if stagger and max_stagger_steps > 0:
+            self._staggered_warmup(max_stagger_steps, warmup_action_fn)
+        return self._build_obs_all()
+
+    def _build_obs_all(self, env_mask=None):
+        out = self.obr._build(self.sim.states, env_mask, self.OBS_SIZE, self._obs)
+        return out.view(self.nenv, 2, self.OBS_SIZE)
+
+    def _random_actions(self):
+        a = torch.empty(self.nac, 4, dtype=torch.float64, device=self.device)
+        a[:, 0:3].uniform_(-0.2, 0.2)
+        a[:, 3].uniform_(0.6, 0.9)
+        return a
+
+    def _staggered_warmup(self, max_steps, action_fn):
+        """rl_env.py:386-434: advance engagement e by p_e ~ U[0, max_steps) valid decisions,
+        re-seeding any that depart first, and capture physics + reconstructor at that phase."""
+        targ = torch.tensor(self.rng.integers(0, max_steps, size=self.nenv), device=self.device)
+        age = torch.zeros(self.nenv, dtype=torch.long, device=self.device)
+        captured_mask = targ == 0
+        captured = self.sim.states.clone()
+        obr_buf = self.obr.clone_state()
+        warm_finite = torch.ones((), dtype=torch.bool, device=self.device)
+        for _ in range(max_steps):
+            if action_fn is None:
+                a = self._random_actions()
+            else:
+                a = action_fn(self._build_obs_all().reshape(self.nac, self.OBS_SIZE))
+                a = torch.as_tensor(a, dtype=torch.float64, device=self.device).reshape(self.nac, 4)
+            self.sim.step(a, substeps=self.substeps, want_obs=False)
+            fin = torch.isfinite(self.sim.states).reshape(self.nenv, -1).all(dim=1)
+            warm_finite.logical_and_((fin | captured_mask).all())
+            # push + advance (the kernel's reward side effects are re-anchored after capture)
+            self.obr.kernel_advance(self.sim.states, a, cfg=self.reward_cfg,
+                                    min_alt=self.min_altitude_m, max_time=self.max_engage_time_s,
+                                    reward_mode=self.reward_mode, alt_hunt_coef=self.alt_hunt_coef)
+            dep = self._departed_envs(self.state9_flat()) & (~captured_mask)
+            if bool(dep.any()):
+                self._seed_envs(torch.nonzero(dep).flatten().tolist())
+                self.obr.reset_envs(dep)
+                self.obr.kernel_init_reward_state(self.sim.states, dep)
+                age[dep] = 0
+            age = age + (~captured_mask).long()
+            hit = (~captured_mask) & (age == targ)
+            if bool(hit.any()):
+                hac = hit.repeat_interleave(2)
+                captured[hac] = self.sim.states[hac]
+                self.obr.capture_into(obr_buf, hit)
+                captured_mask |= hit
+            if bool(captured_mask.all()):
+                break
+        if not bool(captured_mask.all()):
+            rest = ~captured_mask
+            self._seed_envs(torch.nonzero(rest).flatten().tolist())
+            self.obr.reset_envs(rest)
+            self.obr.kernel_init_reward_state(self.sim.states, rest)
+            rac = rest.repeat_interleave(2)
+            captured[rac] = self.sim.states[rac]
+            self.obr.capture_into(obr_buf, rest)
+        if not bool(warm_finite):
+            raise FloatingPointError("non-finite physical trajectory during staggered initialization")
+        self.sim.states.copy_(captured)
+        self.obr.restore(obr_buf)
+        self.obr.kernel_init_reward_state(self.sim.states)
+
+    def _departed_envs(self, s9_flat=None, floor_m=100.0):
+        s9 = (self.state9() if s9_flat is None else s9_flat.view(self.nenv, 2, 9))
+        alt = -s9[:, :, 2]
+        bad = (alt < floor_m) | (~torch.isfinite(s9).all(dim=2))
+        return bad.any(dim=1)
+
+    def reset_evaluation(self, *, paired=False, seed_block=0):
+        """Deterministic stratified contest bank, no warm-up (rl_env.py:260-327, 343-356)."""
+        key = (bool(paired), int(seed_block))
+        if self._evaluation_seed_bank is None or self._evaluation_seed_bank_key != key:
+            self._evaluation_seed_bank = self._build_evaluation_seed_bank(paired, seed_block)
+            self._evaluation_seed_bank_key = key
+        self.sim.load_seed(self._evaluation_seed_bank)
+        self.obr.reset_all()
+        self.obr.kernel_init_reward_state(self.sim.states)
+        return self._build_obs_all()
+
+    def _build_evaluation_seed_bank(self, paired, seed_block):
+        if paired and self.nenv % 8:
+            raise ValueError("mirrored 3:1 evaluation requires nenv divisible by 8")
+        base = self.nenv // 2 if paired else self.nenv
+        rng = np.random.default_rng((self.seed + 19_870_331 + int(seed_block) * 1_000_003)
+                                    % (2 ** 63 - 1))
+        alt_order, spd_order = rng.permutation(base), rng.permutation(base)
+        lo_a, hi_a = icm.CONTEST_ALT_FT
+        lo_s, hi_s = icm.CONTEST_SPEED_MPS
+        rows = np.zeros((self.nac, 10))
+        counts = {str(int(d)): 0 for d in icm.CONTEST_DIST_A_FT}
+        for e in range(base):
+            alt = lo_a + (alt_order[e] + 0.5) / base * (hi_a - lo_a)
+            spd = lo_s + (spd_order[e] + 0.5) / base * (hi_s - lo_s)
+            dist = icm.CONTEST_DIST_A_FT[e % len(icm.CONTEST_DIST_A_FT)]
+            counts[str(int(dist))] += 1
+            rows[2 * e:2 * e + 2] = icm.contest_pair(
+                self.rng, alt_ft=alt, speed=spd, side_swap=(e % 2) == 1, scenario_b=False,
+                head_swap=((e // 2) % 2) == 1, dist_ft=dist)
+        if paired:
+            rows[2 * base:] = rows[:2 * base]
+        self._evaluation_seed_metadata = {
+            "paired": bool(paired), "seed_block": int(seed_block), "base_count": int(base),
+            "three_nine": int(base), "headon": 0, "three_nine_distance_counts": counts}
+        return self._initialize_physical_seeds(rows)
+
+    # ---- step (rl_env.py:529-580) ----
+    def _to_nac4(self, actions):
+        a = torch.as_tensor(actions, dtype=torch.float64, device=self.device)
+        return a.reshape(self.nac, 4)
+
+    def step(self, actions, *, reset_indices=None):
+        """actions (nenv,2,4) or (nac,4) [aileron, elevator, rudder, throttle].
+        Returns (obs (nenv,2,D) f32, reward (nenv,2) f64, done (nenv,) bool, info)."""
+        a = self._to_nac4(actions)
+        self._ensure_ic_pool()
+        self.sim.step(a, substeps=self.substeps, want_obs=False)
+        if reset_indices is None:
+            pick = torch.randint(0, self.ic_pool_size, (self.nenv,), device=self.device)
+        else:
+            if (reset_indices.shape != (self.nenv,) or reset_indices.dtype != torch.long
+                    or reset_indices.device != self.sim.states.device):
+                raise ValueError("reset indices must be one device int64 index per environment")
+            pick = reset_indices.contiguous()
+        n, dev = self.nac, self.device
+        reward = torch.empty(n, dtype=torch.float64, device=dev)
+        terminal_obs = torch.empty(n, self.OBS_SIZE, dtype=torch.float32, device=dev)
+        terminal_hp = torch.empty(n, dtype=torch.float64, device=dev)
+        terminal_alt = torch.empty(n, dtype=torch.float64, device=dev)
+        c = reward_cfg_struct(self.reward_cfg, self.min_altitude_m, self.max_engage_time_s,
+                              self.reward_mode, self.alt_hunt_coef)
+        rec = self.obr._recon()
+        ev = self.kernel_events
+        if ev is not None:
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+        rc = self.obr._lib.f16_env_post_step(
+            _lib.ptr(self.sim._state_soa), self.nac, _lib.ptr(self.sim.actions),
+            _lib.ctypes.byref(rec), _lib.ctypes.byref(c), _lib.ptr(self.ic_pool),
+            self.ic_pool.shape[0], _lib.ptr(pick), self.OBS_SIZE, _lib.ptr(self._obs),
+            _lib.ptr(terminal_obs), _lib.ptr(reward), _lib.ptr(self._term), _lib.ptr(self._trunc),
+            _lib.ptr(self._done), _lib.ptr(terminal_hp), _lib.ptr(terminal_alt),
+            _lib.ptr(self._tfin), _lib.stream_handle(dev))
+        if ev is not None:
+            e1.record()
+            ev.append((e0, e1))
+        _lib.check(rc, "f16_env_post_step")
+        term, trunc, done = self._term.bool(), self._trunc.bool(), self._done.bool()
+        info = {"terminated": term, "truncated": trunc,
+                "terminal_obs": terminal_obs.view(self.nenv, 2, self.OBS_SIZE),
+                "terminal_hp": terminal_hp.view(self.nenv, 2),
+                "terminal_alt_m": terminal_alt.view(self.nenv, 2), "done": done,
+                "terminal_state_finite": self._tfin.bool()}
+        return (self._obs.view(self.nenv, 2, self.OBS_SIZE), reward.view(self.nenv, 2), done,
+                info)
+
+    # ---- state export (rl_env.py:583-592) ----
+    def state9_flat(self):
+        out = torch.empty(self.nac, 9, dtype=torch.float64, device=self.device)
+        rc = self.obr._lib.f16_state9(_lib.ptr(self.sim._state_soa), self.nac, self.nac,
+                                      _lib.ptr(out), _lib.stream_handle(self.device))
+        _lib.check(rc, "f16_state9")
+        return out
+
+    def state9(self):
+        return self.state9_flat().view(self.nenv, 2, 9)

@@ -1,0 +1,101 @@
+/* f16_obs.h -- C ABI of the observation / reward / termination kernels and of the fused
+ * post-physics environment step (libf16hip.so).
+ *
+ * Every function launches on `stream` (a hipStream_t, NULL = the default stream), never
+ * synchronises and never allocates.  Device pointers only.  Return 0 on success, a negative
+ * F16_E* code for a rejected argument, or -(1000 + hipError_t) for a launch failure.
+ *
+ * Layout.  Aircraft a of engagement e is a = 2e (plane 0) or 2e + 1 (plane 1).  The aircraft
+ * state is the structure-of-arrays buffer of f16_fdm.h: field k of aircraft a at
+ * states[k * ld + a].  Per-aircraft reconstructor vectors are structure-of-arrays too:
+ * component k of aircraft a at X[k * rec->ld + a]; the action history holds the five most
+ * recent (aileron, elevator, rudder, throttle) rows, newest first, as component 4*step + channel.
+ * Observations are row-major float32, obs[a * obs_dim + j], obs_dim 184 or 214.
+ */
+#ifndef F16_OBS_H
+#define F16_OBS_H
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Reconstructor state of BatchObsReward (research/competition_36500/runtime/cuda_fdm/
+ * obs_reward.py:338-353, 471-486): what the observation needs beyond the aircraft states. */
+typedef struct F16Recon {
+    double *hp;            /* (nac)      hit points, 1 at reset                              */
+    double *fuel;          /* (nac)      fuel proxy, 1 at reset                              */
+    double *t_sec;         /* (nenv)     engagement time [s]                                 */
+    double *prev_att;      /* (3, ld)    roll/pitch/yaw [deg] at the previous decision       */
+    unsigned char *prev_valid;   /* (nac) prev_att holds a value                          */
+    double *pqr;           /* (3, ld)    attitude-difference body rates [rad/s]              */
+    double *dealt;         /* (nac)      damage rate dealt this decision                     */
+    double *taken;         /* (nac)      damage rate taken this decision                     */
+    double *hp_loss;       /* (nac)      HP lost this decision                               */
+    double *act_hist;      /* (20, ld)   action history, newest first                        */
+    double *prev_x;        /* (nac)      previous geometry advantage G                       */
+    unsigned char *prev_x_valid; /* (nac)                                                    */
+    double *prev_alt_log;  /* (nac)      previous log(altitude / 304.8 m)                    */
+    double *prev_vel_ned;  /* (3, ld)    214-D only (else NULL): previous NED velocity [m/s] */
+    double *accel;         /* (3, ld)    214-D only (else NULL): NED acceleration [m/s^2]    */
+    long ld;               /* column stride of the (k, ld) arrays, >= nac                   */
+    int nenv;
+} F16Recon;
+
+/* MY_REWARD_CONFIG scalars (claude_code/my_reward.py:45-103) and the kernel_advance options
+ * (obs_reward.py:410-441).  mode: 0 final-safe geometry, 1 altitude hunt, 2 attack, 3 defence
+ * (cuda_fdm/reward_modes.py). */
+typedef struct F16RewardCfg {
+    double own_damage_weight, damage_scale, shaping_reward_scale;
+    double win_reward, loss_reward;
+    double timeout_win_reward, timeout_loss_reward, timeout_draw_reward;
+    double min_alt_m, max_time_s, alt_hunt_coef;
+    int mode;
+} F16RewardCfg;
+
+/* BatchObsReward.kernel_advance (obs_reward.py:410-441; obs_kernel.cu advance_kernel, and
+ * external_observation.cu external_acceleration when rec->accel is set): push `actions`
+ * ((nac, 4) float64 rows) into the history, integrate HP / fuel / body rates / time from the
+ * post-physics states, decide termination (term) and truncation (trunc) per engagement
+ * (uint8), and write the reward of every aircraft (float64). */
+int f16_obr_advance(const double *states, long ld, const double *actions, const F16Recon *rec,
+                    const F16RewardCfg *cfg, double *reward, unsigned char *term,
+                    unsigned char *trunc, void *stream);
+
+/* BatchObsReward.kernel_init_reward_state (obs_reward.py:443-452): re-anchor the geometry
+ * advantage and log-altitude of the engagements whose env_mask byte is non-zero (NULL = all). */
+int f16_obr_init_reward(const double *states, long ld, const unsigned char *env_mask,
+                        const F16Recon *rec, void *stream);
+
+/* BatchObsReward.kernel_build_obs (obs_reward.py:454-469) and, for obs_dim 214, the external
+ * 214-D observation (obs_reward.py:487-496, external_observation.cu): write the observation rows
+ * of the engagements selected by env_mask (NULL = all).  214 needs rec->accel. */
+int f16_obr_build_obs(const double *states, long ld, const unsigned char *env_mask,
+                      const F16Recon *rec, int obs_dim, float *obs, void *stream);
+
+/* GpuDogfightVecEnv.step after the physics launch (research/competition_36500/runtime/
+ * cuda_fdm/rl_env.py:540-580), one launch: terminal_state_finite (may be NULL), advance +
+ * reward + termination, the terminal observation (terminal_obs, may be NULL), terminal HP and
+ * MSL altitude (either may be NULL), then for every engagement with term|trunc: the state rows
+ * of ic_pool[pick[e]] ((pool_size, 2, 101) float64) are copied into states, the reconstructor
+ * is reset, the reward state re-anchored and the observation rebuilt; live engagements keep
+ * the terminal observation in `obs`.  `done` (uint8 per engagement) = term | trunc.  A pick
+ * outside [0, pool_size) fills that engagement's states with NaN so the error surfaces as a
+ * non-finite state instead of an out-of-bounds read. */
+int f16_env_post_step(double *states, long ld, const double *actions, const F16Recon *rec,
+                      const F16RewardCfg *cfg, const double *ic_pool, long pool_size,
+                      const long *pick, int obs_dim, float *obs, float *terminal_obs,
+                      double *reward, unsigned char *term, unsigned char *trunc,
+                      unsigned char *done, double *terminal_hp, double *terminal_alt_m,
+                      unsigned char *terminal_finite, void *stream);
+
+/* GpuDogfightVecEnv.state9_flat (cuda_fdm/rl_env.py:583-592 with kinematics_state and
+ * ned_from_ecef_altasl, :88-163): per aircraft N, E, D [m] (D = -MSL altitude; N/E the tangent
+ * plane about the official origin of the point at the aircraft's geodetic latitude/longitude),
+ * roll, pitch, yaw [deg], body u, v, w [m/s].  s9: (nac, 9) row-major float64. */
+int f16_state9(const double *states, long ld, int nac, double *s9, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* F16_OBS_H */

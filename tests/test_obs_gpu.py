@@ -1,0 +1,388 @@
+"""GPU parity of the observation / reward / termination kernels and of the fused post-physics
+environment step (include/f16_obs.h, through the C ABI) against the CPU restatement of the
+reference (oracle/obs_oracle.c, itself pinned to the reference's torch path by
+tests/golden/obs_golden.npz) and against those golden vectors directly.
+
+Tolerances (observations and rewards within 1e-5, termination flags
+bit-exact): observations <= 1e-5 absolute (float32 outputs of unit-scale features); rewards
+and reconstructor doubles <= 1e-8 absolute (the GPU and host transcendentals differ by an ulp,
+which the geometry score's smoothsteps amplify by at most ~1e3); flags, action history, time,
+autoreset state rows: exact.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle_lib
+from conftest import import_pkg
+
+pytestmark = pytest.mark.gpu
+OBS_TOL = 1e-5
+VAL_TOL = 1e-8
+FT2M = 0.3048
+
+
+def _obr(nenv, ext=False):
+    obr = import_pkg("obs_reward").BatchObsReward(nenv)
+    if ext:
+        obr.enable_external_observations()
+    return obr
+
+
+def _to_oracle(obr, orc, ext=False):
+    """An oracle reconstructor holding a copy of the GPU reconstructor's state."""
+    ob = oracle_lib.ObrOracle(orc, obr.nenv, accel=ext)
+    c = lambda t: t.detach().cpu().numpy()
+    ob.hp[:] = c(obr.hp); ob.fuel[:] = c(obr.fuel); ob.t_sec[:] = c(obr.t_sec)
+    ob.prev_att[:] = c(obr.prev_att); ob.prev_valid[:] = c(obr.prev_valid)
+    ob.pqr[:] = c(obr.pqr); ob.dealt[:] = c(obr.last_dmg_dealt)
+    ob.taken[:] = c(obr.last_dmg_taken); ob.hp_loss[:] = c(obr.hp_loss)
+    ob.act_hist[:] = c(obr.act_hist); ob.prev_x[:] = c(obr.prev_x)
+    ob.prev_x_valid[:] = c(obr.prev_x_valid); ob.prev_alt_log[:] = c(obr.prev_alt_log)
+    if ext:
+        ob.prev_vel_ned[:] = c(obr.external_previous_velocity)
+        ob.accel[:] = c(obr.external_accel)
+    return ob
+
+
+def _cmp_recon(obr, ob, ext=False):
+    c = lambda t: t.detach().cpu().numpy().astype(np.float64)
+    pairs = [("hp", obr.hp, ob.hp), ("fuel", obr.fuel, ob.fuel), ("pqr", obr.pqr, ob.pqr),
+             ("dealt", obr.last_dmg_dealt, ob.dealt), ("taken", obr.last_dmg_taken, ob.taken),
+             ("hp_loss", obr.hp_loss, ob.hp_loss), ("prev_x", obr.prev_x, ob.prev_x),
+             ("prev_alt_log", obr.prev_alt_log, ob.prev_alt_log),
+             ("prev_att", obr.prev_att, ob.prev_att)]
+    if ext:
+        pairs += [("accel", obr.external_accel, ob.accel),
+                  ("prev_vel", obr.external_previous_velocity, ob.prev_vel_ned)]
+    for name, g, o in pairs:
+        err = np.abs(c(g) - o).max() if o.size else 0.0
+        assert err <= VAL_TOL * max(1.0, np.abs(o).max()), (name, err)
+    np.testing.assert_array_equal(c(obr.t_sec), ob.t_sec)
+    np.testing.assert_array_equal(c(obr.act_hist), ob.act_hist)
+    np.testing.assert_array_equal(c(obr.prev_valid), ob.prev_valid)
+    np.testing.assert_array_equal(c(obr.prev_x_valid), ob.prev_x_valid)
+
+
+def _soa(gpu, states_aos):
+    """A (nac, 101) transposed view of a structure-of-arrays device buffer."""
+    st = torch.as_tensor(np.ascontiguousarray(states_aos).T.copy(), device=gpu)
+    return st.t()
+
+
+# ------------------------------------------------------------------------ golden replay
+@pytest.mark.parametrize("mode", [0, 1, 2, 3])
+def test_golden_replay_matches_reference(gpu, mode):
+    """The scripted reference sequence (damage, hard deck, HP death, timeout, masked resets)
+    through the GPU kernels against the reference's own outputs."""
+    g = oracle_lib.golden("obs_golden.npz")
+    nenv = g["in_reset"].shape[1]
+    obr = _obr(nenv)
+    obr.hp.copy_(torch.as_tensor(g["in_hp0"], device=gpu))
+    obr.t_sec.copy_(torch.as_tensor(g["in_t0"], device=gpu))
+    obr.kernel_init_reward_state(_soa(gpu, g["in_states"][0]))
+    key = lambda n: g[f"m{mode}_{n}"] if f"m{mode}_{n}" in g else g[f"m0_{n}"]
+    for k in range(g["in_actions"].shape[0]):
+        st = _soa(gpu, g["in_states"][k])
+        act = torch.as_tensor(g["in_actions"][k], device=gpu)
+        r, te, tr = obr.kernel_advance(st, act, reward_mode=mode)
+        obs = obr.kernel_build_obs(st).cpu().numpy()
+        assert np.abs(r.cpu().numpy() - key("reward")[k]).max() <= VAL_TOL, (k, "reward")
+        np.testing.assert_array_equal(te.cpu().numpy().astype(bool), g["m0_term"][k].astype(bool))
+        np.testing.assert_array_equal(tr.cpu().numpy().astype(bool), g["m0_trunc"][k].astype(bool))
+        assert np.abs(obs - g["m0_obs"][k]).max() <= OBS_TOL, (k, "obs")
+        assert np.abs(obr.hp.cpu().numpy() - g["m0_hp"][k]).max() <= VAL_TOL
+        assert np.abs(obr.prev_x.cpu().numpy() - key("prev_x")[k]).max() <= VAL_TOL
+        np.testing.assert_array_equal(obr.t_sec.cpu().numpy(), g["m0_t_sec"][k])
+        mask = torch.as_tensor(g["in_reset"][k], device=gpu)
+        str_ = _soa(gpu, g["in_states_reset"][k])
+        if g["in_reset"][k].any():
+            obr.reset_envs(mask)
+            obr.kernel_init_reward_state(str_, mask)
+            obs = obr.kernel_build_obs(str_, mask).cpu().numpy()
+        assert np.abs(obs - g["m0_obs_reset"][k]).max() <= OBS_TOL, (k, "obs_reset")
+
+
+# ------------------------------------------------------------------------ random engagements
+def _random_states(gpu, nenv, seed, rate=60):
+    """Seeded valid aircraft states: positions within +-20 km of the contest centre, altitude
+    150 m - 12 km (some below the hard deck), 100-350 m/s, any attitude; a third of the
+    engagements put the partner 150-1300 m in front of the nose so damage cones engage."""
+    icm = import_pkg("ic")
+    rng = np.random.default_rng(seed)
+    n = 2 * nenv
+    north = 3500.0 + rng.uniform(-20000, 20000, n)
+    east = rng.uniform(-20000, 20000, n)
+    alt = rng.uniform(150.0, 12000.0, n)
+    spd = rng.uniform(100.0, 350.0, n)
+    phi = rng.uniform(-180, 180, n)
+    theta = rng.uniform(-80, 80, n)
+    psi = rng.uniform(0, 360, n)
+    alpha = rng.uniform(-5, 15, n)
+    beta = rng.uniform(-5, 5, n)
+    close = rng.random(nenv) < 0.35
+    for e in np.nonzero(close)[0]:
+        a, b = 2 * e, 2 * e + 1
+        th, ps = np.radians(theta[a]), np.radians(psi[a])
+        r = rng.uniform(150.0, 1300.0)
+        fwd = np.array([np.cos(th) * np.cos(ps), np.cos(th) * np.sin(ps), -np.sin(th)])
+        off = rng.normal(0.0, 0.004 * r, 3)
+        north[b], east[b] = north[a] + r * fwd[0] + off[0], east[a] + r * fwd[1] + off[1]
+        alt[b] = alt[a] - r * fwd[2] - off[2]
+        alt[a] = max(alt[a], 2000.0)
+        alt[b] = max(alt[b], 1500.0)
+        alpha[a] = beta[a] = 0.0
+    la, lo, h = icm.ned_to_geodetic(north, east, -alt)
+    rows = np.array([icm.ic_row(la[i], lo[i], h[i], spd[i] / FT2M, psi[i], 3000.0, phi[i],
+                                theta[i], alpha[i], beta[i]) for i in range(n)])
+    sim = import_pkg().GpuDogfight(nenv, fcs_rate=rate)
+    sim.seed_rows(torch.as_tensor(rows, device=gpu))
+    return sim
+
+
+def _random_recon(gpu, obr, seed, s9=None):
+    """Reconstructor mid-episode: random HP (some nearly dead), times (some at the limit),
+    previous attitudes, histories, anchors and validity flags.  With s9, the previous attitude
+    is the current one perturbed by 8 deg (sd) per axis, as one 0.1 s decision of fast
+    manoeuvring; log_SO3 is ill-conditioned for rotations near pi, which no decision makes."""
+    rng = np.random.default_rng(seed)
+    n, ne = obr.nac, obr.nenv
+    t = lambda x, dt=torch.float64: torch.as_tensor(x, dtype=dt, device=gpu)
+    hp = rng.uniform(0.05, 1.0, n)
+    hp[rng.random(n) < 0.1] = 1e-3
+    obr.hp.copy_(t(hp))
+    obr.fuel.copy_(t(rng.uniform(0.0, 1.0, n)))
+    ts = rng.uniform(0.0, 199.0, ne)
+    ts[rng.random(ne) < 0.1] = 199.95
+    ts[rng.random(ne) < 0.2] = rng.choice([99.95, 120.0, 149.95, 160.0])
+    obr.t_sec.copy_(t(ts))
+    if s9 is None:
+        att = np.stack([rng.uniform(-180, 180, n), rng.uniform(-80, 80, n),
+                        rng.uniform(0, 360, n)], 1)
+    else:
+        att = s9[:, 3:6] + rng.normal(0.0, 8.0, (n, 3))
+    obr.prev_att.copy_(t(att))
+    obr.prev_valid.copy_(t(rng.random(n) < 0.8, torch.bool))
+    obr.pqr.copy_(t(rng.normal(0, 0.3, (n, 3))))
+    obr.last_dmg_dealt.copy_(t(rng.uniform(0, 1, n)))
+    obr.last_dmg_taken.copy_(t(rng.uniform(0, 1, n)))
+    obr.hp_loss.copy_(t(rng.uniform(0, 0.01, n)))
+    obr.act_hist.copy_(t(rng.uniform(-1, 1, (n, 5, 4))))
+    obr.prev_x.copy_(t(rng.uniform(-1, 1, n)))
+    obr.prev_x_valid.copy_(t(rng.random(n) < 0.8, torch.bool))
+    obr.prev_alt_log.copy_(t(rng.normal(2.0, 1.0, n)))
+    if obr._acc_soa is not None:
+        obr.external_previous_velocity.copy_(t(rng.normal(0, 200, (n, 3))))
+        obr.external_accel.copy_(t(rng.normal(0, 20, (n, 3))))
+
+
+@pytest.mark.parametrize("mode", [0, 1, 2, 3])
+def test_random_engagements_match_oracle(gpu, orc, mode):
+    nenv = 1024
+    sim = _random_states(gpu, nenv, 10 + mode)
+    obr = _obr(nenv)
+    s9 = oracle_lib.ObrOracle(orc, nenv).state9(sim.states.cpu().numpy())
+    _random_recon(gpu, obr, 20 + mode, s9)
+    ob = _to_oracle(obr, orc)
+    act = np.random.default_rng(30 + mode).uniform(-1, 1, (2 * nenv, 4))
+    r, te, tr = obr.kernel_advance(sim.states, torch.as_tensor(act, device=gpu), reward_mode=mode)
+    r_o, te_o, tr_o = ob.step(s9, act, mode=mode)
+    np.testing.assert_array_equal(te.cpu().numpy().astype(bool), te_o)
+    np.testing.assert_array_equal(tr.cpu().numpy().astype(bool), tr_o)
+    assert np.abs(r.cpu().numpy() - r_o).max() <= VAL_TOL
+    _cmp_recon(obr, ob)
+    obs = obr.kernel_build_obs(sim.states).cpu().numpy()
+    assert np.abs(obs - ob.build_obs(s9)).max() <= OBS_TOL
+    # the workload must exercise what it claims to
+    assert te_o.any() and (~te_o).any() and tr_o.any()
+    assert (ob.dealt > 0).any() and (ob.hp <= 0).any()
+
+
+def test_init_reward_masked(gpu, orc):
+    nenv = 512
+    sim = _random_states(gpu, nenv, 41)
+    obr = _obr(nenv)
+    _random_recon(gpu, obr, 42)
+    ob = _to_oracle(obr, orc)
+    mask = np.random.default_rng(43).random(nenv) < 0.5
+    obr.kernel_init_reward_state(sim.states, torch.as_tensor(mask, device=gpu))
+    ob.init_reward(ob.state9(sim.states.cpu().numpy()), mask)
+    _cmp_recon(obr, ob)
+
+
+def test_external_214_matches_oracle(gpu, orc):
+    """214-D variant: acceleration vectors spliced in before the action history."""
+    nenv = 512
+    sim = _random_states(gpu, nenv, 51)
+    obr = _obr(nenv, ext=True)
+    s9 = oracle_lib.ObrOracle(orc, nenv).state9(sim.states.cpu().numpy())
+    _random_recon(gpu, obr, 52, s9)
+    ob = _to_oracle(obr, orc, ext=True)
+    act = np.random.default_rng(53).uniform(-1, 1, (2 * nenv, 4))
+    obr.kernel_advance(sim.states, torch.as_tensor(act, device=gpu))
+    ob.step(s9, act)
+    _cmp_recon(obr, ob, ext=True)
+    obs = obr.build_external_obs(sim.states).cpu().numpy()
+    ref = ob.build_obs(s9, obs_dim=214)
+    assert obs.shape == (2 * nenv, 214)
+    assert np.abs(obs - ref).max() <= OBS_TOL
+    # the 184-D layout is the 214-D one without the acceleration block
+    obs184 = obr.kernel_build_obs(sim.states).cpu().numpy()
+    np.testing.assert_array_equal(obs184[:, :164], obs[:, :164])
+    np.testing.assert_array_equal(obs184[:, 164:], obs[:, 194:])
+
+
+def test_state9_kernel(gpu, orc):
+    nenv = 256
+    sim = _random_states(gpu, nenv, 61)
+    out = torch.empty(2 * nenv, 9, dtype=torch.float64, device=gpu)
+    L = import_pkg("_lib")
+    rc = L.lib().f16_state9(L.ptr(sim._state_soa), sim.nac, sim.nac, L.ptr(out),
+                            L.stream_handle(gpu))
+    L.check(rc, "f16_state9")
+    ref = oracle_lib.ObrOracle(orc, nenv).state9(sim.states.cpu().numpy())
+    got = out.cpu().numpy()
+    assert np.abs(got[:, :3] - ref[:, :3]).max() <= 1e-6          # metres
+    assert np.abs(got[:, 3:6] - ref[:, 3:6]).max() <= 1e-9        # degrees
+    assert np.abs(got[:, 6:] - ref[:, 6:]).max() <= 1e-10         # m/s
+
+
+# ------------------------------------------------------------------------ fused env step
+@pytest.mark.parametrize("obs_dim", [184, 214])
+def test_env_post_step_matches_reference_sequence(gpu, orc, obs_dim):
+    """f16_env_post_step against the reference's sequence (rl_env.py:540-580) replayed on the
+    oracle: advance -> terminal obs -> pool autoreset -> reset_envs -> init_reward -> masked
+    build_obs."""
+    ext = obs_dim == 214
+    nenv = 1024
+    sim = _random_states(gpu, nenv, 71)
+    pool_sim = _random_states(gpu, 64, 72)
+    pool = pool_sim.states.reshape(64, 2, 101).contiguous()
+    obr = _obr(nenv, ext)
+    st0 = sim.states.cpu().numpy()
+    _random_recon(gpu, obr, 73, oracle_lib.ObrOracle(orc, nenv).state9(st0))
+    ob = _to_oracle(obr, orc, ext)
+    act = np.random.default_rng(74).uniform(-1, 1, (2 * nenv, 4))
+    pick = torch.as_tensor(np.random.default_rng(75).integers(0, 64, nenv), device=gpu)
+    sim.actions.copy_(torch.as_tensor(act, device=gpu))
+    L = import_pkg("_lib")
+    R = import_pkg("obs_reward")
+    n = 2 * nenv
+    obs = torch.full((n, obs_dim), -7.0, dtype=torch.float32, device=gpu)
+    tobs = torch.empty_like(obs)
+    rew = torch.empty(n, dtype=torch.float64, device=gpu)
+    te, tr, dn, fin = (torch.empty(nenv, dtype=torch.uint8, device=gpu) for _ in range(4))
+    thp = torch.empty(n, dtype=torch.float64, device=gpu)
+    talt = torch.empty(n, dtype=torch.float64, device=gpu)
+    c = R.reward_cfg_struct(R.MY_REWARD_CONFIG, 304.8, 200.0, 0, 5.0)
+    rec = obr._recon()
+    rc = L.lib().f16_env_post_step(
+        L.ptr(sim._state_soa), sim.nac, L.ptr(sim.actions), L.ctypes.byref(rec), L.ctypes.byref(c),
+        L.ptr(pool), 64, L.ptr(pick), obs_dim, L.ptr(obs), L.ptr(tobs), L.ptr(rew), L.ptr(te),
+        L.ptr(tr), L.ptr(dn), L.ptr(thp), L.ptr(talt), L.ptr(fin), L.stream_handle(gpu))
+    L.check(rc, "f16_env_post_step")
+    # oracle replay of the reference sequence
+    s9 = ob.state9(st0)
+    r_o, te_o, tr_o = ob.step(s9, act)
+    tobs_o = ob.build_obs(s9, obs_dim)
+    thp_o = ob.hp.copy()
+    done_o = te_o | tr_o
+    st1 = st0.copy()
+    pk = pick.cpu().numpy()
+    pool_np = pool.cpu().numpy()
+    for e in np.nonzero(done_o)[0]:
+        st1[2 * e:2 * e + 2] = pool_np[pk[e]]
+    ob.reset_envs(done_o)
+    s9r = ob.state9(st1)
+    ob.init_reward(s9r, done_o)
+    obs_o = tobs_o.copy()
+    obs_o[np.repeat(done_o, 2)] = ob.build_obs(s9r, obs_dim)[np.repeat(done_o, 2)]
+    # compare
+    np.testing.assert_array_equal(te.cpu().numpy().astype(bool), te_o)
+    np.testing.assert_array_equal(tr.cpu().numpy().astype(bool), tr_o)
+    np.testing.assert_array_equal(dn.cpu().numpy().astype(bool), done_o)
+    np.testing.assert_array_equal(fin.cpu().numpy().astype(bool),
+                                  np.isfinite(st0).all(1).reshape(nenv, 2).all(1))
+    assert np.abs(rew.cpu().numpy() - r_o).max() <= VAL_TOL
+    assert np.abs(thp.cpu().numpy() - thp_o).max() <= VAL_TOL
+    alt_o = (np.linalg.norm(st0[:, 0:3], axis=1) - 20925646.32546) * FT2M
+    assert np.abs(talt.cpu().numpy() - alt_o).max() <= 1e-6
+    assert np.abs(tobs.cpu().numpy() - tobs_o).max() <= OBS_TOL
+    assert np.abs(obs.cpu().numpy() - obs_o).max() <= OBS_TOL
+    np.testing.assert_array_equal(sim.states.cpu().numpy(), st1)
+    _cmp_recon(obr, ob, ext)
+    assert done_o.any() and (~done_o).any()
+
+
+def test_env_post_step_bad_pick_poisons_state(gpu):
+    """A pool index out of range never reads out of bounds: the engagement becomes NaN."""
+    nenv = 4
+    sim = _random_states(gpu, nenv, 81)
+    obr = _obr(nenv)
+    obr.t_sec.fill_(199.95)          # every engagement truncates -> autoreset for all
+    pool = sim.states.reshape(nenv, 2, 101).contiguous()
+    pick = torch.tensor([0, 4, -1, 1], dtype=torch.int64, device=gpu)
+    L = import_pkg("_lib")
+    R = import_pkg("obs_reward")
+    n = 2 * nenv
+    obs = torch.zeros(n, 184, dtype=torch.float32, device=gpu)
+    rew = torch.empty(n, dtype=torch.float64, device=gpu)
+    te, tr, dn = (torch.empty(nenv, dtype=torch.uint8, device=gpu) for _ in range(3))
+    c = R.reward_cfg_struct(R.MY_REWARD_CONFIG, 0.0, 200.0, 0, 5.0)
+    rec = obr._recon()
+    rc = L.lib().f16_env_post_step(
+        L.ptr(sim._state_soa), sim.nac, L.ptr(sim.actions), L.ctypes.byref(rec), L.ctypes.byref(c),
+        L.ptr(pool), nenv, L.ptr(pick), 184, L.ptr(obs), None, L.ptr(rew), L.ptr(te), L.ptr(tr),
+        L.ptr(dn), None, None, None, L.stream_handle(gpu))
+    L.check(rc, "f16_env_post_step")
+    st = sim.states.cpu().numpy().reshape(nenv, 2, 101)
+    assert dn.cpu().numpy().all()
+    assert np.isfinite(st[[0, 3]]).all()
+    assert np.isnan(st[[1, 2]]).all()
+
+
+# ------------------------------------------------------------------------ the env object
+def test_vec_env_contract(gpu):
+    """GpuDogfightVecEnv reset()/step() shapes, dtypes, info keys, autoreset bookkeeping."""
+    E = import_pkg("rl_env").GpuDogfightVecEnv
+    env = E(64, seed=3, ic_pool_size=32)
+    obs = env.reset(stagger=True, max_stagger_steps=6)
+    assert obs.shape == (64, 2, 184) and obs.dtype == torch.float32
+    assert torch.isfinite(obs).all()
+    rng = torch.Generator(device=gpu).manual_seed(0)
+    for k in range(40):
+        a = torch.rand(64, 2, 4, generator=rng, device=gpu, dtype=torch.float64) * 2 - 1
+        a[..., 3] = (a[..., 3] + 1) / 2
+        obs, rew, done, info = env.step(a)
+        assert obs.shape == (64, 2, 184) and rew.shape == (64, 2) and done.shape == (64,)
+        assert rew.dtype == torch.float64 and done.dtype == torch.bool
+        assert set(info) == {"terminated", "truncated", "terminal_obs", "terminal_hp",
+                             "terminal_alt_m", "done", "terminal_state_finite"}
+        assert torch.equal(done, info["terminated"] | info["truncated"])
+        if done.any():
+            # autoreset engagements restart the clock and full HP
+            assert (env.obr.t_sec[done] == 0).all()
+            assert (env.obr.hp.view(64, 2)[done] == 1).all()
+        live = ~done
+        assert torch.equal(obs[live], info["terminal_obs"][live])
+    s9 = env.state9()
+    assert s9.shape == (64, 2, 9)
+    ev = env.reset_evaluation(paired=True, seed_block=1)
+    assert ev.shape == (64, 2, 184)
+    np.testing.assert_array_equal(env.sim.states[:64].cpu().numpy(),
+                                  env.sim.states[64:].cpu().numpy())
+
+
+def test_obs_argument_errors(gpu):
+    obr = _obr(8)
+    st = torch.zeros(16, 101, dtype=torch.float64, device=gpu)
+    with pytest.raises(TypeError):
+        obr.kernel_build_obs(st.float())
+    with pytest.raises(ValueError):
+        obr.kernel_build_obs(st[:8])
+    with pytest.raises(ValueError):
+        obr.kernel_advance(st, torch.zeros(16, 4, dtype=torch.float64, device=gpu), reward_mode=7)
+    with pytest.raises(TypeError):
+        obr.kernel_advance(st, torch.zeros(16, 4, dtype=torch.float32, device=gpu))
+    with pytest.raises(ValueError):
+        obr._build(st, None, 200, obr.obs_buf)
