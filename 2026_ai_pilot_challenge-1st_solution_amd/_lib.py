@@ -1,4 +1,5 @@
-"""ctypes binding of libf16hip.so (C ABI declared in include/f16_fdm.h and include/f16_obs.h).
+"""ctypes binding of libf16hip.so (C ABI declared in include/f16_fdm.h, include/f16_obs.h and
+include/f16_policy.h).
 
 torch is imported first so that the process's HIP runtime is torch's; the library then binds
 to that same runtime (libamdhip64.so.7) and launches on torch's streams.  There is no CPU
@@ -36,6 +37,21 @@ class F16RewardCfg(ctypes.Structure):
                 ("max_time_s", _d), ("alt_hunt_coef", _d), ("mode", _i)]
 
 
+class F16PolicyGroup(ctypes.Structure):
+    """include/f16_policy.h F16PolicyGroup."""
+    _fields_ = [("wbf", _vp), ("wf", _vp), ("row_begin", _i), ("row_end", _i)]
+
+
+class F16PolicyArgs(ctypes.Structure):
+    """include/f16_policy.h F16PolicyArgs."""
+    _fields_ = [("obs", _vp), ("obs_ld", _l), ("obs_dim", _i), ("mean", _vp), ("var", _vp),
+                ("clip", ctypes.c_float), ("eps", ctypes.c_float), ("rows", _vp),
+                ("ngroups", _i), ("group", F16PolicyGroup * 16), ("seed", ctypes.c_ulonglong),
+                ("step", ctypes.c_uint), ("salt", ctypes.c_uint), ("deterministic", _i),
+                ("grid", _vp), ("nobs_out", _vp), ("nobs_ld", _l), ("act_idx", _vp),
+                ("logp", _vp), ("value", _vp), ("env_actions", _vp), ("logits_out", _vp)]
+
+
 _RP, _CP = ctypes.POINTER(F16Recon), ctypes.POINTER(F16RewardCfg)
 _SIGNATURES = {
     "f16_fdm_step_batch": (_i, [_vp, _l, _vp, _i, _i, _i, _vp, _l, _vp]),
@@ -49,6 +65,10 @@ _SIGNATURES = {
     "f16_env_post_step": (_i, [_vp, _l, _vp, _RP, _CP, _vp, _l, _vp, _i, _vp, _vp, _vp, _vp, _vp,
                                _vp, _vp, _vp, _vp, _vp]),
     "f16_state9": (_i, [_vp, _l, _i, _vp, _vp]),
+    "f16_policy_step": (_i, [ctypes.POINTER(F16PolicyArgs), _vp]),
+    "f16_norm_workspace_bytes": (_l, [_i, _i]),
+    "f16_abi_struct_sizes": (_i, [ctypes.POINTER(_l), _i]),
+    "f16_norm_update": (_i, [_vp, _l, _vp, _i, _i, _vp, _vp, _vp, _vp, _vp]),
 }
 
 _lib = None

@@ -1,0 +1,33 @@
+// sample_math.h -- softmax numerators for the categorical draw, from IEEE basic operations only,
+// so that the draw is reproducible bit-for-bit by any IEEE-754 single-precision implementation of
+// the same expression sequence (compiled without contraction).
+//
+// e^x for x <= 0: Cody-Waite reduction x = n ln2 + r with ln2 split into a 16-bit head (n * head
+// exact for |n| < 256) and a tail, |r| <= ln2/2; e^r by its degree-7 Taylor polynomial in Horner
+// form (truncation < 2e-8 relative); scaling by 2^n with ldexp.  Below -87, 0.
+#pragma once
+
+#include <math.h>
+
+#ifndef F16_HD
+#define F16_HD __host__ __device__ __forceinline__
+#endif
+
+namespace f16rng {
+
+F16_HD float exp_nonpos(float x) {
+  if (!(x >= -87.0f)) return 0.0f;
+  const float n = rintf(x * 1.44269504f);
+  const float r = (x - n * 0.693145751953125f) - n * 1.42860677e-6f;
+  float p = 1.0f / 5040.0f;
+  p = p * r + 1.0f / 720.0f;
+  p = p * r + 1.0f / 120.0f;
+  p = p * r + 1.0f / 24.0f;
+  p = p * r + 1.0f / 6.0f;
+  p = p * r + 0.5f;
+  p = p * r + 1.0f;
+  p = p * r + 1.0f;
+  return ldexpf(p, (int)n);
+}
+
+}  // namespace f16rng

@@ -92,6 +92,53 @@ def cpu_baseline(states0_aos, actions_host, substeps, cpu_seconds):
             "single_thread": n1 * substeps / dt1}
 
 
+# Algorithmic HBM bytes of one aircraft in the fused post-physics kernel: reads 11 state doubles
+# + reconstructor (hp, fuel, prev_att 3, pqr-free, act_hist 16, prev_x, prev_alt_log, flags, t)
+# + actions 4; writes reconstructor (hp, hp_loss, fuel, pqr 3, prev_att 3, act_hist 20, dealt,
+# taken, prev_x, prev_alt_log, flags, t) + reward + terminal and live observations (2 x 184 f32)
+# + terminal HP/altitude + the 101 state doubles read for the finite flag.
+POST_BYTES_PER_AIRCRAFT = (11 + 101 + 4 + 27) * 8 + 2 + (34 + 3) * 8 + 2 * 184 * 4 + 4
+
+
+def env_step_bench(pkg, nenv, steps, warmup):
+    """Full environment transitions: GpuDogfightVecEnv.step = FDM decision (6 substeps, FCS 60 Hz)
+    + the fused post-physics kernel (advance, reward, termination, terminal observation, pool
+    autoreset, new observation), contest ICs, random 4-channel actions resident on the device."""
+    import torch
+    env_mod = importlib.import_module(PKG + ".rl_env")
+    env = env_mod.GpuDogfightVecEnv(nenv, seed=0)
+    env.reset(stagger=False)
+    g = torch.Generator(device="cuda").manual_seed(0)
+    acts = torch.rand(warmup + steps, 2 * nenv, 4, generator=g, device="cuda",
+                      dtype=torch.float64) * 2 - 1
+    acts[..., 3] = (acts[..., 3] + 1) / 2
+    for k in range(warmup):
+        env.step(acts[k])
+    torch.cuda.synchronize()
+    env.kernel_events, env.sim.kernel_events = [], []
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    done_total = torch.zeros((), dtype=torch.int64, device="cuda")
+    e0.record()
+    for k in range(steps):
+        _, _, done, _ = env.step(acts[warmup + k])
+        done_total += done.sum()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    post_ms = float(np.mean([a.elapsed_time(b) for a, b in env.kernel_events]))
+    fdm_ms = float(np.mean([a.elapsed_time(b) for a, b in env.sim.kernel_events]))
+    env.kernel_events = env.sim.kernel_events = None
+    post_bytes = POST_BYTES_PER_AIRCRAFT * 2 * nenv
+    return {"workload": "contest_env_step_16k", "engagements": nenv, "obs_dim": 184,
+            "substeps": env.substeps, "fcs_rate_hz": env.sim.fcs_rate,
+            "transitions_per_s": nenv / (ms * 1e-3), "ms_per_step": ms,
+            "fdm_kernel_ms": fdm_ms, "post_kernel_ms": post_ms,
+            "episodes_done": int(done_total.item()),
+            "post_kernel": {"kernel": "env_post_step_kernel", "algorithmic_bytes": post_bytes,
+                            "achieved_GBs": post_bytes / (post_ms * 1e-3) / 1e9,
+                            "hbm_frac": post_bytes / (post_ms * 1e-3) / 1e9 / PEAK_HBM_GBS}}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -156,6 +203,8 @@ def main():
     if not bool(torch.isfinite(sim.states).all()):
         raise FloatingPointError("non-finite state after the timed steps")
 
+    env_line = env_step_bench(pkg, nenv, args.steps, args.warmup)
+
     value = nac * S / (ms_step * 1e-3)
     flop_launch = FLOP_PER_SUBSTEP * nac * S
     achieved = flop_launch / (kern_ms * 1e-3) / 1e12
@@ -175,7 +224,8 @@ def main():
         "config": {"workload": "fdm_tailchase_16k", "engagements": nenv, "aircraft": nac,
                    "substeps_per_step": S, "fcs_rate_hz": 120,
                    "actions": "i.i.d. uniform 21-bin per channel, held per decision"},
-        "env_transitions_per_s": nenv / (ms_step * 1e-3),
+        "env_transitions_per_s": env_line["transitions_per_s"],
+        "env_step": env_line,
         "roofline": {"bound": "valu", "achieved": achieved, "peak": PEAK_FP64_TFLOPS,
                      "unit": "TFLOP/s", "frac": achieved / PEAK_FP64_TFLOPS, "traffic": profiled_traffic(),
                      "kernel": "fdm_step_kernel<120>", "kernel_ms": kern_ms,

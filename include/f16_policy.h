@@ -1,0 +1,84 @@
+/* f16_policy.h -- C ABI of the rollout-side policy kernels (libf16hip.so): observation
+ * running-normalisation update and the fused actor/critic MLP step with categorical sampling.
+ *
+ * Launch on `stream` (hipStream_t, NULL = default), no synchronisation, no allocation; device
+ * pointers only; 0 on success, F16_E* (< 0) for a rejected argument, -(1000 + hipError_t) for a
+ * launch failure.
+ */
+#ifndef F16_POLICY_H
+#define F16_POLICY_H
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Packed network of the reference's MLPDiscreteActorCritic with hidden (256, 256), tanh
+ * (research/competition_36500/runtime/claude_code/model.py:162-205; BASELINE C4/C5 sizes).
+ * bf16 part, row-major [out][in] with the input width padded to kp = round_up(obs_dim, 32):
+ *   W1 [512][kp]   actor layer-1 rows 0..255, critic layer-1 rows 256..511 (pad columns 0)
+ *   W2a [256][256] actor layer 2,  W2c [256][256] critic layer 2
+ *   W3a [96][256]  actor logits head, rows 84..95 zero
+ * f32 part: b1 [512], b2a [256], b2c [256], b3a [96] (84..95 zero), w3c [256] critic head
+ * weights, b3c [1]  (F16_POLICY_NF = 1377 floats). */
+#define F16_POLICY_HID 256
+#define F16_POLICY_BINS 21
+#define F16_POLICY_CHANNELS 4
+#define F16_POLICY_NF 1377
+
+typedef struct F16PolicyGroup {
+    const void *wbf;        /* bf16 weight blob of this group's network */
+    const float *wf;        /* f32 bias/head blob */
+    int row_begin, row_end; /* logical rows [begin, end) evaluated by this network */
+} F16PolicyGroup;
+
+#define F16_POLICY_MAX_GROUPS 16
+
+typedef struct F16PolicyArgs {
+    const float *obs;       /* physical observation rows, row stride obs_ld floats */
+    long obs_ld;
+    int obs_dim;            /* 184 or 214 */
+    const float *mean, *var;/* RunningNorm statistics (obs_dim), NULL = no normalisation */
+    float clip, eps;        /* normalisation clip (10) and epsilon (1e-8) */
+    const int *rows;        /* logical row -> physical row; NULL = identity */
+    int ngroups;            /* networks, each over its own logical row range */
+    F16PolicyGroup group[F16_POLICY_MAX_GROUPS];
+    unsigned long long seed;/* Philox4x32-10 key */
+    unsigned int step;      /* counter word 1 (rollout step) */
+    unsigned int salt;      /* counter word 3 (separates independent draws at one step) */
+    int deterministic;      /* 1: per-channel argmax instead of sampling */
+    const float *grid;      /* 21 control values of linspace(-1, 1, 21) in float32 */
+    float *nobs_out;        /* normalised observations at logical rows (ld nobs_ld), or NULL */
+    long nobs_ld;
+    long long *act_idx;     /* (logical, 4) sampled bins, or NULL */
+    float *logp;            /* (logical) summed log-probability of the sampled bins, or NULL */
+    float *value;           /* (logical) critic value, or NULL */
+    double *env_actions;    /* (physical, 4) float64 controls [ail, ele, rud, thr], or NULL */
+    float *logits_out;      /* (logical, 84) actor logits, or NULL */
+} F16PolicyArgs;
+
+/* One policy step for every logical row: optional RunningNorm.normalize with clip
+ * (cuda_fdm/ppo_gpu.py:210-214), actor logits and critic value of the MLP
+ * (claude_code/model.py:195-205), per-channel categorical draw, its summed log-probability
+ * (model.py:221-233 / ppo_gpu.py:266-276 actor_step, value_step), and action_to_env
+ * (ppo_gpu.py:361-370).  The draw for (physical row r, channel c) inverts the CDF of the
+ * channel's softmax at u = (x0 >> 8) * 2^-24, x0 the first word of Philox4x32-10 with key `seed`
+ * and counter (r, step, c, salt).  kp = round_up(obs_dim, 32) of the packed weights. */
+int f16_policy_step(const F16PolicyArgs *args, void *stream);
+
+/* sizeof(F16PolicyGroup), sizeof(F16PolicyArgs) as compiled into the library (out[0..1]), so
+ * that a binding can check its struct layout; no counterpart in the reference. */
+int f16_abi_struct_sizes(long *out, int n);
+
+/* RunningNorm.update (cuda_fdm/ppo_gpu.py:194-207) from the batch of `nrows` physical rows
+ * (rows[i], or i when rows is NULL) of obs (row stride obs_ld): batch mean and population
+ * variance per column, then the parallel-variance merge into mean/var/count (float32, in
+ * place).  `work` is device scratch of at least f16_norm_workspace_bytes(nrows, obs_dim). */
+long f16_norm_workspace_bytes(int nrows, int obs_dim);
+int f16_norm_update(const float *obs, long obs_ld, const int *rows, int nrows, int obs_dim,
+                    float *mean, float *var, float *count, void *work, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* F16_POLICY_H */
