@@ -41,6 +41,9 @@ class GpuDogfightVecEnv:
         self.device = torch.device(device)
         self.seed = 0 if seed is None else int(seed)
         self.rng = np.random.default_rng(seed)
+        # device-side draws (warm-up actions, autoreset pool picks) come from the env's own
+        # generator rather than torch's global one, so an env is reproducible from its seed
+        self.torch_gen = torch.Generator(device=self.device).manual_seed(self.seed)
         self.scenario = scenario
         self.headon_distance_m = float(headon_distance_m)
         self.scenario_b_prob = 0.0
@@ -116,8 +119,8 @@ class GpuDogfightVecEnv:
 
     def _random_actions(self):
         a = torch.empty(self.nac, 4, dtype=torch.float64, device=self.device)
-        a[:, 0:3].uniform_(-0.2, 0.2)
-        a[:, 3].uniform_(0.6, 0.9)
+        a[:, 0:3].uniform_(-0.2, 0.2, generator=self.torch_gen)
+        a[:, 3].uniform_(0.6, 0.9, generator=self.torch_gen)
         return a
 
     def _staggered_warmup(self, max_steps, action_fn):
@@ -219,14 +222,17 @@ class GpuDogfightVecEnv:
         a = torch.as_tensor(actions, dtype=torch.float64, device=self.device)
         return a.reshape(self.nac, 4)
 
-    def step(self, actions, *, reset_indices=None):
+    def step(self, actions, *, reset_indices=None, terminal_obs=True):
         """actions (nenv,2,4) or (nac,4) [aileron, elevator, rudder, throttle].
-        Returns (obs (nenv,2,D) f32, reward (nenv,2) f64, done (nenv,) bool, info)."""
+        Returns (obs (nenv,2,D) f32, reward (nenv,2) f64, done (nenv,) bool, info).
+        terminal_obs=False skips the terminal-observation copy (info["terminal_obs"] is None):
+        the rollout collector reads only the terminal HP and altitude."""
         a = self._to_nac4(actions)
         self._ensure_ic_pool()
         self.sim.step(a, substeps=self.substeps, want_obs=False)
         if reset_indices is None:
-            pick = torch.randint(0, self.ic_pool_size, (self.nenv,), device=self.device)
+            pick = torch.randint(0, self.ic_pool_size, (self.nenv,), device=self.device,
+                                 generator=self.torch_gen)
         else:
             if (reset_indices.shape != (self.nenv,) or reset_indices.dtype != torch.long
                     or reset_indices.device != self.sim.states.device):
@@ -234,7 +240,8 @@ class GpuDogfightVecEnv:
             pick = reset_indices.contiguous()
         n, dev = self.nac, self.device
         reward = torch.empty(n, dtype=torch.float64, device=dev)
-        terminal_obs = torch.empty(n, self.OBS_SIZE, dtype=torch.float32, device=dev)
+        tobs = (torch.empty(n, self.OBS_SIZE, dtype=torch.float32, device=dev) if terminal_obs
+                else None)
         terminal_hp = torch.empty(n, dtype=torch.float64, device=dev)
         terminal_alt = torch.empty(n, dtype=torch.float64, device=dev)
         c = reward_cfg_struct(self.reward_cfg, self.min_altitude_m, self.max_engage_time_s,
@@ -248,7 +255,7 @@ class GpuDogfightVecEnv:
             _lib.ptr(self.sim._state_soa), self.nac, _lib.ptr(self.sim.actions),
             _lib.ctypes.byref(rec), _lib.ctypes.byref(c), _lib.ptr(self.ic_pool),
             self.ic_pool.shape[0], _lib.ptr(pick), self.OBS_SIZE, _lib.ptr(self._obs),
-            _lib.ptr(terminal_obs), _lib.ptr(reward), _lib.ptr(self._term), _lib.ptr(self._trunc),
+            _lib.ptr(tobs), _lib.ptr(reward), _lib.ptr(self._term), _lib.ptr(self._trunc),
             _lib.ptr(self._done), _lib.ptr(terminal_hp), _lib.ptr(terminal_alt),
             _lib.ptr(self._tfin), _lib.stream_handle(dev))
         if ev is not None:
@@ -257,7 +264,7 @@ class GpuDogfightVecEnv:
         _lib.check(rc, "f16_env_post_step")
         term, trunc, done = self._term.bool(), self._trunc.bool(), self._done.bool()
         info = {"terminated": term, "truncated": trunc,
-                "terminal_obs": terminal_obs.view(self.nenv, 2, self.OBS_SIZE),
+                "terminal_obs": tobs.view(self.nenv, 2, self.OBS_SIZE) if tobs is not None else None,
                 "terminal_hp": terminal_hp.view(self.nenv, 2),
                 "terminal_alt_m": terminal_alt.view(self.nenv, 2), "done": done,
                 "terminal_state_finite": self._tfin.bool()}

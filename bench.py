@@ -139,6 +139,47 @@ def env_step_bench(pkg, nenv, steps, warmup):
                             "hbm_frac": post_bytes / (post_ms * 1e-3) / 1e9 / PEAK_HBM_GBS}}
 
 
+PEAK_BF16_TFLOPS = 2500.0
+
+
+def rollout_bench(nenv, T=64, reps=2):
+    """BASELINE C4: nenv engagements x T-step self-play rollout (FDM + fused obs/reward + norm
+    update + fused bf16 actor/critic with Philox draw) then GAE (gamma 0.99, lambda 0.95) over
+    [T, nenv, 2].  Weights N(0, 0.02), draw seed 0."""
+    import torch
+    env_mod = importlib.import_module(PKG + ".rl_env")
+    pol = importlib.import_module(PKG + ".policy")
+    ppo = importlib.import_module(PKG + ".ppo")
+    env = env_mod.GpuDogfightVecEnv(nenv, seed=0)
+    net = pol.MLPActorCritic(184, init="normal", init_std=0.02,
+                             generator=torch.Generator().manual_seed(0)).to("cuda")
+    ro = ppo.SelfPlayRollout(env, net, T=T, gamma=0.99, lam=0.95, seed=0)
+    ro.reset(stagger=False)
+    ro.collect()                                    # warm-up rollout
+    torch.cuda.synchronize()
+    ro.policy_events = []
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        adv, ret, stats = ro.collect()
+    e1.record()
+    torch.cuda.synchronize()
+    if not bool(stats["trajectory_finite"]) or not bool(torch.isfinite(adv).all()):
+        raise FloatingPointError("non-finite rollout")
+    ms = e0.elapsed_time(e1) / reps
+    pol_ms = float(np.mean([a.elapsed_time(b) for a, b in ro.policy_events]))
+    ro.policy_events = None
+    flop = ppo.POLICY_FLOP_PER_ROW[184] * 2 * nenv
+    return {"workload": "selfplay_rollout_16k_T64", "engagements": nenv, "T": T,
+            "ms_per_rollout": ms, "transitions_per_s": nenv * T / (ms * 1e-3),
+            "aircraft_transitions_per_s": 2 * nenv * T / (ms * 1e-3),
+            "policy_kernel_ms": pol_ms,
+            "policy_mfma": {"kernel": "policy_kernel<192>", "flop_per_launch": flop,
+                            "achieved_TFLOPs": flop / (pol_ms * 1e-3) / 1e12,
+                            "peak_TFLOPs": PEAK_BF16_TFLOPS,
+                            "frac": flop / (pol_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS}}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -148,6 +189,7 @@ def main():
     ap.add_argument("--substeps", type=int, default=6)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-rollout", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run 5 device-to-device copies of MIB MiB (rocprof counter "
                          "calibration: FETCH_SIZE/WRITE_SIZE of a copy of known size)")
@@ -204,6 +246,7 @@ def main():
         raise FloatingPointError("non-finite state after the timed steps")
 
     env_line = env_step_bench(pkg, nenv, args.steps, args.warmup)
+    rollout_line = None if args.no_rollout else rollout_bench(nenv)
 
     value = nac * S / (ms_step * 1e-3)
     flop_launch = FLOP_PER_SUBSTEP * nac * S
@@ -226,6 +269,7 @@ def main():
                    "actions": "i.i.d. uniform 21-bin per channel, held per decision"},
         "env_transitions_per_s": env_line["transitions_per_s"],
         "env_step": env_line,
+        "rollout": rollout_line,
         "roofline": {"bound": "valu", "achieved": achieved, "peak": PEAK_FP64_TFLOPS,
                      "unit": "TFLOP/s", "frac": achieved / PEAK_FP64_TFLOPS, "traffic": profiled_traffic(),
                      "kernel": "fdm_step_kernel<120>", "kernel_ms": kern_ms,
