@@ -1,14 +1,17 @@
 // policy_kernels.hip -- rollout policy step on gfx950: RunningNorm update and the fused
 // normalise -> actor/critic MLP (bf16 MFMA, fp32 accumulate) -> categorical draw -> controls.
 //
-// Policy workgroup: 64 observation rows, 4 waves.  The rows are normalised once, rounded to bf16
-// and kept in LDS; the actor's and critic's first layers run as one 512-wide GEMM over them,
-// each wave owning 128 output columns (2 x 4 tiles of v_mfma_f32_32x32x16_bf16).  Hidden layers
-// stay in LDS (bf16, row pitch = width + 8 so the 16-byte fragment reads of 16 consecutive rows
-// hit 64 distinct banks); layer 2 runs actor and critic halves on two waves each; the logits
-// head (84 columns padded to 96) runs on three waves while the fourth forms the critic's
-// 256-long dot products.  Weights stream from L2 (every workgroup reads the same 0.5 MB).
-// Sampling is one lane per (row, channel).
+// Policy workgroup: 64 observation rows, 8 waves (two per SIMD, so one wave's tanh epilogue
+// overlaps another's matrix work).  The rows are loaded with every load in flight at once,
+// normalised with per-column statistics staged in LDS, rounded to bf16 and kept in LDS; the
+// actor's and critic's first layers run as one 512-unit GEMM over them, each wave owning 64 units
+// (2 x 2 tiles of v_mfma_f32_32x32x16_bf16 with units as the matrix rows, so a lane's results
+// are 4 consecutive units of one observation row: one 8-byte LDS store per 4 activations).
+// Hidden layers stay in LDS (bf16, row pitch width + 8: 16-byte fragment reads of 16
+// consecutive rows hit 64 distinct banks); layer 2 runs actor and critic halves on four waves
+// each; the logits head (84 units padded to 96) runs on six waves while a seventh forms the
+// critic's 256-long dot products.  Weights stream from L2 two K-slices ahead (every workgroup
+// reads the same 0.55 MB).  Sampling is one lane per (row, channel).
 #include <hip/hip_runtime.h>
 
 #include <stdint.h>
@@ -21,10 +24,13 @@
 namespace f16pol {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kRows = 64;               // observation rows per workgroup
-constexpr int kThreads = 256;
+constexpr int kWaves = 8;
+constexpr int kThreads = 64 * kWaves;
 constexpr int kHid = F16_POLICY_HID;    // 256
 constexpr int kH2 = 2 * kHid;           // actor | critic
 constexpr int kHPitch = kH2 + 8;        // bf16 per LDS row of the hidden activations
@@ -32,7 +38,7 @@ constexpr int kBins = F16_POLICY_BINS;  // 21
 constexpr int kChan = F16_POLICY_CHANNELS;
 constexpr int kLogits = kBins * kChan;  // 84
 constexpr int kLogitsPad = 96;
-constexpr int kLPitch = kLogitsPad + 1; // f32 per LDS row of logits
+constexpr int kLPitch = 100;            // f32 per LDS row of logits (16-byte rows)
 
 // offsets (elements) inside the packed blobs
 template <int KP>
@@ -46,69 +52,92 @@ struct Blob {
 constexpr int kB1 = 0, kB2A = 512, kB2C = 768, kB3A = 1024, kW3C = 1120, kB3C = 1376;
 static_assert(kB3C + 1 == F16_POLICY_NF, "f32 blob layout");
 
+// tanh for the bf16 hidden activations: 1 - 2/(e^{2|x|} + 1) from the hardware exp2 and
+// reciprocal (each ~1 ulp), odd Taylor series below |x| = 1/16 where 1 - e^{-2|x|} cancels;
+// relative error ~1e-6, far inside the bf16 rounding step (2^-8) the result is stored with.
+__device__ __forceinline__ float tanh_act(float x) {
+  const float ax = fabsf(x);
+  const float t = __builtin_amdgcn_exp2f(ax * -2.8853900817779268f);   // e^{-2|x|}
+  float y = (1.0f - t) * __builtin_amdgcn_rcpf(1.0f + t);
+  const float x2 = x * x;
+  const float ys = ax * (1.0f + x2 * (-1.0f / 3.0f + x2 * (2.0f / 15.0f)));
+  y = ax < 0.0625f ? ys : y;
+  return copysignf(y, x);
+}
+
 __device__ __forceinline__ f32x16 mfma(const bf16x8& a, const bf16x8& b, const f32x16& c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
-// Output element r (0..15) of a 32x32 tile held by `lane`: row and column inside the tile.
-__device__ __forceinline__ int tile_row(int lane, int r) { return (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3); }
-
-// acc[i][j] += A(rows 32i.., LDS, pitch) x B(cols cb+32j.., global [col][K])^T over K.
-template <int NI, int NJ, int K>
-__device__ __forceinline__ void gemm_tiles(f32x16 (&acc)[NI][NJ], const __bf16* __restrict__ As,
-                                           int a_pitch, int a_col0,
-                                           const __bf16* __restrict__ Bg, int col0, int lane) {
+// acc[u][r] += W(units u0+32u.., global [unit][K]) x A(rows 32r.., LDS [row][pitch])^T over K.
+// Units are the MFMA rows, observation rows the MFMA columns: element e of a tile's result held
+// by `lane` is unit 8(e/4) + 4(lane/32) + e%4, row lane%32.  Weights are prefetched two K slices
+// ahead.
+template <int NU, int NR, int K>
+__device__ __forceinline__ void gemm_t(f32x16 (&acc)[NU][NR], const __bf16* __restrict__ Wg,
+                                       int u0, const __bf16* __restrict__ As, int a_pitch,
+                                       int a_col0, int lane) {
   const int lr = lane & 31, lk = (lane >> 5) * 8;
-  bf16x8 b[NJ], bn[NJ];
+  constexpr int NK = K / 16;
+  bf16x8 w0[NU], w1[NU];
+  const __bf16* wp[NU];
 #pragma unroll
-  for (int j = 0; j < NJ; ++j)
-    b[j] = *reinterpret_cast<const bf16x8*>(Bg + (long)(col0 + 32 * j + lr) * K + lk);
-#pragma unroll 2
-  for (int k0 = 0; k0 < K; k0 += 16) {
-    if (k0 + 16 < K) {                // prefetch the next K slice of the weights
+  for (int u = 0; u < NU; ++u) {
+    wp[u] = Wg + (long)(u0 + 32 * u + lr) * K + lk;
+    w0[u] = *reinterpret_cast<const bf16x8*>(wp[u]);
+    w1[u] = *reinterpret_cast<const bf16x8*>(wp[u] + 16);
+  }
 #pragma unroll
-      for (int j = 0; j < NJ; ++j)
-        bn[j] = *reinterpret_cast<const bf16x8*>(Bg + (long)(col0 + 32 * j + lr) * K + k0 + 16 + lk);
+  for (int s = 0; s < NK; ++s) {
+    bf16x8 w2[NU];
+    if (s + 2 < NK) {
+#pragma unroll
+      for (int u = 0; u < NU; ++u) w2[u] = *reinterpret_cast<const bf16x8*>(wp[u] + 16 * (s + 2));
     }
-    bf16x8 a[NI];
+    bf16x8 a[NR];
 #pragma unroll
-    for (int i = 0; i < NI; ++i)
-      a[i] = *reinterpret_cast<const bf16x8*>(As + (32 * i + lr) * a_pitch + a_col0 + k0 + lk);
+    for (int r = 0; r < NR; ++r)
+      a[r] = *reinterpret_cast<const bf16x8*>(As + (32 * r + lr) * a_pitch + a_col0 + 16 * s + lk);
 #pragma unroll
-    for (int i = 0; i < NI; ++i)
+    for (int u = 0; u < NU; ++u)
 #pragma unroll
-      for (int j = 0; j < NJ; ++j) acc[i][j] = mfma(a[i], b[j], acc[i][j]);
-    if (k0 + 16 < K) {
+      for (int r = 0; r < NR; ++r) acc[u][r] = mfma(w0[u], a[r], acc[u][r]);
 #pragma unroll
-      for (int j = 0; j < NJ; ++j) b[j] = bn[j];
-    }
+    for (int u = 0; u < NU; ++u) { w0[u] = w1[u]; w1[u] = w2[u]; }
   }
 }
 
-template <int NI, int NJ>
-__device__ __forceinline__ void zero(f32x16 (&acc)[NI][NJ]) {
+template <int NU, int NR>
+__device__ __forceinline__ void zero(f32x16 (&acc)[NU][NR]) {
 #pragma unroll
-  for (int i = 0; i < NI; ++i)
+  for (int u = 0; u < NU; ++u)
 #pragma unroll
-    for (int j = 0; j < NJ; ++j)
+    for (int r = 0; r < NR; ++r)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+      for (int e = 0; e < 16; ++e) acc[u][r][e] = 0.0f;
 }
 
-// bias + tanh, rounded to bf16, into the LDS activation rows
-template <int NI, int NJ>
-__device__ __forceinline__ void store_tanh(const f32x16 (&acc)[NI][NJ], const float* __restrict__ bias,
-                                           __bf16* Hs, int col0, int lane) {
-  const int lr = lane & 31;
+// bias + tanh, rounded to bf16, 4 consecutive units per 8-byte LDS store at Hs[row][col0 + unit]
+template <int NU, int NR>
+__device__ __forceinline__ void store_tanh(const f32x16 (&acc)[NU][NR], const float* __restrict__ bias,
+                                           __bf16* Hs, int u0, int col0, int lane) {
+  const int lr = lane & 31, lh = (lane >> 5) * 4;
 #pragma unroll
-  for (int j = 0; j < NJ; ++j) {
-    const float bj = bias[col0 + 32 * j + lr];
+  for (int u = 0; u < NU; ++u)
 #pragma unroll
-    for (int i = 0; i < NI; ++i)
+    for (int g = 0; g < 4; ++g) {
+      const int unit = u0 + 32 * u + 8 * g + lh;
+      const float4 b = *reinterpret_cast<const float4*>(bias + unit);
 #pragma unroll
-      for (int r = 0; r < 16; ++r)
-        Hs[(32 * i + tile_row(lane, r)) * kHPitch + col0 + 32 * j + lr] = (__bf16)tanhf(acc[i][j][r] + bj);
-  }
+      for (int r = 0; r < NR; ++r) {
+        bf16x4 v;
+        v[0] = (__bf16)tanh_act(acc[u][r][4 * g + 0] + b.x);
+        v[1] = (__bf16)tanh_act(acc[u][r][4 * g + 1] + b.y);
+        v[2] = (__bf16)tanh_act(acc[u][r][4 * g + 2] + b.z);
+        v[3] = (__bf16)tanh_act(acc[u][r][4 * g + 3] + b.w);
+        *reinterpret_cast<bf16x4*>(Hs + (32 * r + lr) * kHPitch + col0 + unit) = v;
+      }
+    }
 }
 
 template <int KP>
@@ -117,6 +146,7 @@ __global__ __launch_bounds__(kThreads) void policy_kernel(const F16PolicyArgs p)
   static_assert(kRows * kLPitch * 4 <= kRows * XP * 2, "logits reuse the input rows' LDS");
   __shared__ __align__(16) __bf16 Xs[kRows * XP];
   __shared__ __align__(16) __bf16 Hs[kRows * kHPitch];
+  __shared__ float col_mean[KP], col_sd[KP];
   const int gi = blockIdx.y;
   if (gi >= p.ngroups) return;
   const F16PolicyGroup G = p.group[gi];
@@ -126,61 +156,103 @@ __global__ __launch_bounds__(kThreads) void policy_kernel(const F16PolicyArgs p)
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const __bf16* wbf = static_cast<const __bf16*>(G.wbf);
   const float* wf = G.wf;
+  const int D = p.obs_dim;
 
   // ---- normalise (RunningNorm.normalize, ppo_gpu.py:210-214) and stage bf16 rows in LDS
-  for (int idx = tid; idx < kRows * KP; idx += kThreads) {
-    const int r = idx / KP, k = idx - (idx / KP) * KP;
-    float v = 0.0f;
-    if (r < nr && k < p.obs_dim) {
-      const int li = r0 + r;
-      const long pr = p.rows ? p.rows[li] : li;
-      float x = p.obs[pr * p.obs_ld + k];
-      if (p.mean) {
-        x = (x - p.mean[k]) / sqrtf(p.var[k] + p.eps);
-        x = x < -p.clip ? -p.clip : (x > p.clip ? p.clip : x);
+  if (tid < KP) {
+    const bool on = p.mean && tid < D;
+    col_mean[tid] = on ? p.mean[tid] : 0.0f;
+    col_sd[tid] = on ? sqrtf(p.var[tid] + p.eps) : 1.0f;
+  }
+  __syncthreads();
+  {
+    const int half = D >> 1;                          // float2 per row (obs_dim is even)
+    constexpr int kPer = (kRows * (KP / 2) + kThreads - 1) / kThreads;
+    float2 x[kPer];
+#pragma unroll
+    for (int q = 0; q < kPer; ++q) {                   // issue every load before using any
+      const int idx = tid + q * kThreads;
+      const int r = idx / half, c = idx - r * half;
+      x[q] = make_float2(0.0f, 0.0f);
+      if (r < nr) {
+        const int li = r0 + r;
+        const long pr = p.rows ? p.rows[li] : li;
+        x[q] = *reinterpret_cast<const float2*>(p.obs + pr * p.obs_ld + 2 * c);
       }
-      if (p.nobs_out) p.nobs_out[(long)li * p.nobs_ld + k] = x;
-      v = x;
     }
-    Xs[r * XP + k] = (__bf16)v;
+#pragma unroll
+    for (int q = 0; q < kPer; ++q) {
+      const int idx = tid + q * kThreads;
+      const int r = idx / half, c = idx - r * half;
+      if (r < kRows) {
+        float v0 = x[q].x, v1 = x[q].y;
+        if (r < nr) {
+          if (p.mean) {
+            v0 = (v0 - col_mean[2 * c]) / col_sd[2 * c];
+            v1 = (v1 - col_mean[2 * c + 1]) / col_sd[2 * c + 1];
+            v0 = v0 < -p.clip ? -p.clip : (v0 > p.clip ? p.clip : v0);
+            v1 = v1 < -p.clip ? -p.clip : (v1 > p.clip ? p.clip : v1);
+          }
+          if (p.nobs_out)
+            *reinterpret_cast<float2*>(p.nobs_out + (long)(r0 + r) * p.nobs_ld + 2 * c) =
+                make_float2(v0, v1);
+        }
+        bf16x2 b;
+        b[0] = (__bf16)v0;
+        b[1] = (__bf16)v1;
+        *reinterpret_cast<bf16x2*>(Xs + r * XP + 2 * c) = b;
+      }
+    }
+    for (int idx = tid; idx < kRows * (KP - D); idx += kThreads) {   // zero the K padding
+      const int r = idx / (KP - D);
+      Xs[r * XP + D + (idx - r * (KP - D))] = (__bf16)0.0f;
+    }
   }
   __syncthreads();
 
-  // ---- layer 1: [actor | critic] = tanh(X W1^T + b1), wave owns 128 of the 512 columns
+  // ---- layer 1: [actor | critic] = tanh(W1 X^T + b1), wave owns 64 of the 512 units
   {
-    f32x16 acc[2][4];
+    f32x16 acc[2][2];
     zero(acc);
-    gemm_tiles<2, 4, KP>(acc, Xs, XP, 0, wbf + Blob<KP>::W1, 128 * wave, lane);
-    store_tanh(acc, wf + kB1, Hs, 128 * wave, lane);
+    gemm_t<2, 2, KP>(acc, wbf + Blob<KP>::W1, 64 * wave, Xs, XP, 0, lane);
+    store_tanh(acc, wf + kB1, Hs, 64 * wave, 0, lane);
   }
   __syncthreads();
 
-  // ---- layer 2: waves 0-1 actor, 2-3 critic; each 128 columns over its half's 256 inputs
+  // ---- layer 2: waves 0-3 actor, 4-7 critic; 64 units each over the half's 256 inputs
   {
-    const int half = wave >> 1;
-    const int ocol = (wave & 1) * 128;
-    f32x16 acc[2][4];
+    const int half = wave >> 2;
+    const int u0 = (wave & 3) * 64;
+    f32x16 acc[2][2];
     zero(acc);
-    gemm_tiles<2, 4, kHid>(acc, Hs, kHPitch, half * kHid,
-                           wbf + (half ? Blob<KP>::W2C : Blob<KP>::W2A), ocol, lane);
+    gemm_t<2, 2, kHid>(acc, wbf + (half ? Blob<KP>::W2C : Blob<KP>::W2A), u0, Hs, kHPitch,
+                       half * kHid, lane);
     __syncthreads();                                    // every wave has read layer 1
-    store_tanh(acc, wf + (half ? kB2C : kB2A) - half * kHid, Hs, half * kHid + ocol, lane);
+    store_tanh(acc, wf + (half ? kB2C : kB2A), Hs, u0, half * kHid, lane);
   }
   __syncthreads();
 
-  // ---- heads: logits on waves 0-2 (32 columns each), critic value on wave 3
+  // ---- heads: logits on waves 0-5 (32 units x 32 rows each), critic value on wave 6
   float* Ls = reinterpret_cast<float*>(Xs);
-  if (wave < 3) {
-    f32x16 acc[2][1];
+  if (wave < 6) {
+    const int ut = wave % 3, rt = wave / 3;
+    f32x16 acc[1][1];
     zero(acc);
-    gemm_tiles<2, 1, kHid>(acc, Hs, kHPitch, 0, wbf + Blob<KP>::W3A, 32 * wave, lane);
-    const int col = 32 * wave + (lane & 31);
-    const float bc = wf[kB3A + col];
+    gemm_t<1, 1, kHid>(acc, wbf + Blob<KP>::W3A, 32 * ut, Hs + 32 * rt * kHPitch, kHPitch, 0,
+                       lane);
+    const int row = 32 * rt + (lane & 31);
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) Ls[(32 * i + tile_row(lane, r)) * kLPitch + col] = acc[i][0][r] + bc;
-  } else {
+    for (int g = 0; g < 4; ++g) {
+      const int unit = 32 * ut + 8 * g + (lane >> 5) * 4;
+      const float4 b = *reinterpret_cast<const float4*>(wf + kB3A + unit);
+      float4 v;
+      v.x = acc[0][0][4 * g + 0] + b.x;
+      v.y = acc[0][0][4 * g + 1] + b.y;
+      v.z = acc[0][0][4 * g + 2] + b.z;
+      v.w = acc[0][0][4 * g + 3] + b.w;
+      *reinterpret_cast<float4*>(Ls + row * kLPitch + unit) = v;
+    }
+  } else if (wave == 6) {
     const int row = lane;
     const float* w3 = wf + kW3C;
     float s = 0.0f;
@@ -194,7 +266,8 @@ __global__ __launch_bounds__(kThreads) void policy_kernel(const F16PolicyArgs p)
   }
   __syncthreads();
 
-  // ---- per (row, channel): softmax, draw, log-probability, control
+  // ---- per (row, channel): softmax, draw, log-probability, control (waves 0-3)
+  if (tid >= kRows * kChan) return;
   const int row = tid >> 2, ch = tid & 3;
   const float* l = Ls + row * kLPitch + ch * kBins;
   float lg[kBins];
@@ -315,6 +388,8 @@ extern "C" int f16_policy_step(const F16PolicyArgs* a, void* stream) {
   }
   if (max_rows == 0) return 0;
   const dim3 grid((unsigned)((max_rows + kRows - 1) / kRows), (unsigned)a->ngroups), block(kThreads);
+  if (a->obs_ld % 2 || ((uintptr_t)a->obs & 7) || (a->nobs_out && (a->nobs_ld % 2 || ((uintptr_t)a->nobs_out & 7))))
+    return F16_EINVAL;                                   // rows are moved as float2
   if (a->obs_dim == 184)
     hipLaunchKernelGGL(policy_kernel<192>, grid, block, 0, (hipStream_t)stream, *a);
   else
