@@ -1,16 +1,16 @@
 // policy_kernels.hip -- rollout policy step on gfx950: RunningNorm update and the fused
 // normalise -> actor/critic MLP (bf16 MFMA, fp32 accumulate) -> categorical draw -> controls.
 //
-// Policy workgroup: 64 observation rows, 8 waves (two per SIMD, so one wave's tanh epilogue
-// overlaps another's matrix work).  The rows are loaded with every load in flight at once,
-// normalised with per-column statistics staged in LDS, rounded to bf16 and kept in LDS; the
-// actor's and critic's first layers run as one 512-unit GEMM over them, each wave owning 64 units
-// (2 x 2 tiles of v_mfma_f32_32x32x16_bf16 with units as the matrix rows, so a lane's results
-// are 4 consecutive units of one observation row: one 8-byte LDS store per 4 activations).
-// Hidden layers stay in LDS (bf16, row pitch width + 8: 16-byte fragment reads of 16
-// consecutive rows hit 64 distinct banks); layer 2 runs actor and critic halves on four waves
-// each; the logits head (84 units padded to 96) runs on six waves while a seventh forms the
-// critic's 256-long dot products.  Weights stream from L2 two K-slices ahead (every workgroup
+// Policy workgroup: 64 observation rows, 8 waves; 59 KB of LDS, so two workgroups share a CU and
+// one's loads, matrix work and tanh epilogues overlap the other's.  The rows are loaded with
+// every load in flight at once, normalised with per-column statistics staged in LDS, rounded to
+// bf16 and kept in LDS.  Actor, then critic: each runs its two 256-unit tanh layers through one
+// LDS activation buffer, every wave owning 32 units (2 tiles of v_mfma_f32_32x32x16_bf16 with
+// units as the matrix rows, so a lane's results are 4 consecutive units of one observation row:
+// one 8-byte LDS store per 4 activations; row pitch width + 8, so 16-byte fragment reads of 16
+// consecutive rows hit 64 distinct banks).  The logits head (84 units padded to 96) runs on six
+// waves and its results overlay the activation buffer for the draw; the critic's value is one
+// 256-long dot product per row.  Weights stream from L2 three K-slices ahead (every workgroup
 // reads the same 0.55 MB).  Sampling is one lane per (row, channel).
 #include <hip/hip_runtime.h>
 
@@ -32,19 +32,20 @@ constexpr int kRows = 64;               // observation rows per workgroup
 constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kHid = F16_POLICY_HID;    // 256
-constexpr int kH2 = 2 * kHid;           // actor | critic
-constexpr int kHPitch = kH2 + 8;        // bf16 per LDS row of the hidden activations
+constexpr int kHPitch = kHid + 8;       // bf16 per LDS row of one network's hidden activations
 constexpr int kBins = F16_POLICY_BINS;  // 21
 constexpr int kChan = F16_POLICY_CHANNELS;
 constexpr int kLogits = kBins * kChan;  // 84
 constexpr int kLogitsPad = 96;
 constexpr int kLPitch = 100;            // f32 per LDS row of logits (16-byte rows)
+constexpr int kPrefetch = 3;            // weight K-slices in flight ahead of the MFMAs
 
 // offsets (elements) inside the packed blobs
 template <int KP>
 struct Blob {
   static constexpr long W1 = 0;
-  static constexpr long W2A = W1 + (long)kH2 * KP;
+  static constexpr long W1C = (long)kHid * KP;     // critic rows of W1
+  static constexpr long W2A = 2L * kHid * KP;
   static constexpr long W2C = W2A + (long)kHid * kHid;
   static constexpr long W3A = W2C + (long)kHid * kHid;
   static constexpr long NBF = W3A + (long)kLogitsPad * kHid;
@@ -52,98 +53,115 @@ struct Blob {
 constexpr int kB1 = 0, kB2A = 512, kB2C = 768, kB3A = 1024, kW3C = 1120, kB3C = 1376;
 static_assert(kB3C + 1 == F16_POLICY_NF, "f32 blob layout");
 
-// tanh for the bf16 hidden activations: 1 - 2/(e^{2|x|} + 1) from the hardware exp2 and
-// reciprocal (each ~1 ulp), odd Taylor series below |x| = 1/16 where 1 - e^{-2|x|} cancels;
-// relative error ~1e-6, far inside the bf16 rounding step (2^-8) the result is stored with.
+// tanh for the bf16 hidden activations: sign(x) (1 - t) / (1 + t), t = e^{-2|x|}, from the
+// hardware exp2 and reciprocal (~1 ulp each).  Near 0 the subtraction cancels, but the absolute
+// error stays below 2.5e-7 everywhere, far inside the bf16 rounding step the result is stored with.
 __device__ __forceinline__ float tanh_act(float x) {
-  const float ax = fabsf(x);
-  const float t = __builtin_amdgcn_exp2f(ax * -2.8853900817779268f);   // e^{-2|x|}
-  float y = (1.0f - t) * __builtin_amdgcn_rcpf(1.0f + t);
-  const float x2 = x * x;
-  const float ys = ax * (1.0f + x2 * (-1.0f / 3.0f + x2 * (2.0f / 15.0f)));
-  y = ax < 0.0625f ? ys : y;
-  return copysignf(y, x);
+  const float t = __builtin_amdgcn_exp2f(fabsf(x) * -2.8853900817779268f);
+  return copysignf((1.0f - t) * __builtin_amdgcn_rcpf(1.0f + t), x);
 }
 
 __device__ __forceinline__ f32x16 mfma(const bf16x8& a, const bf16x8& b, const f32x16& c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
-// acc[u][r] += W(units u0+32u.., global [unit][K]) x A(rows 32r.., LDS [row][pitch])^T over K.
+// acc[r] += W(units u0..u0+31, global [unit][K]) x A(rows 32r.., LDS [row][pitch])^T over K.
 // Units are the MFMA rows, observation rows the MFMA columns: element e of a tile's result held
-// by `lane` is unit 8(e/4) + 4(lane/32) + e%4, row lane%32.  Weights are prefetched two K slices
-// ahead.
-template <int NU, int NR, int K>
-__device__ __forceinline__ void gemm_t(f32x16 (&acc)[NU][NR], const __bf16* __restrict__ Wg,
-                                       int u0, const __bf16* __restrict__ As, int a_pitch,
-                                       int a_col0, int lane) {
+// by `lane` is unit 8(e/4) + 4(lane/32) + e%4, row lane%32.  Weights run kPrefetch K-slices
+// ahead, the LDS activation fragments one slice ahead.
+template <int NR, int K>
+__device__ __forceinline__ void gemm_t(f32x16 (&acc)[NR], const __bf16* __restrict__ Wg, int u0,
+                                       const __bf16* __restrict__ As, int a_pitch, int a_col0,
+                                       int lane) {
   const int lr = lane & 31, lk = (lane >> 5) * 8;
   constexpr int NK = K / 16;
-  bf16x8 w0[NU], w1[NU];
-  const __bf16* wp[NU];
+  const __bf16* wp = Wg + (long)(u0 + lr) * K + lk;
+  const __bf16* ap = As + lr * a_pitch + a_col0 + lk;
+  bf16x8 w[kPrefetch + 1];
 #pragma unroll
-  for (int u = 0; u < NU; ++u) {
-    wp[u] = Wg + (long)(u0 + 32 * u + lr) * K + lk;
-    w0[u] = *reinterpret_cast<const bf16x8*>(wp[u]);
-    w1[u] = *reinterpret_cast<const bf16x8*>(wp[u] + 16);
-  }
+  for (int q = 0; q < kPrefetch; ++q) w[q] = *reinterpret_cast<const bf16x8*>(wp + 16 * q);
+  bf16x8 a[NR], an[NR];
+#pragma unroll
+  for (int r = 0; r < NR; ++r) a[r] = *reinterpret_cast<const bf16x8*>(ap + 32 * r * a_pitch);
 #pragma unroll
   for (int s = 0; s < NK; ++s) {
-    bf16x8 w2[NU];
-    if (s + 2 < NK) {
+    if (s + kPrefetch < NK) w[(s + kPrefetch) % (kPrefetch + 1)] =
+        *reinterpret_cast<const bf16x8*>(wp + 16 * (s + kPrefetch));
+    if (s + 1 < NK) {
 #pragma unroll
-      for (int u = 0; u < NU; ++u) w2[u] = *reinterpret_cast<const bf16x8*>(wp[u] + 16 * (s + 2));
+      for (int r = 0; r < NR; ++r)
+        an[r] = *reinterpret_cast<const bf16x8*>(ap + 32 * r * a_pitch + 16 * (s + 1));
     }
-    bf16x8 a[NR];
 #pragma unroll
-    for (int r = 0; r < NR; ++r)
-      a[r] = *reinterpret_cast<const bf16x8*>(As + (32 * r + lr) * a_pitch + a_col0 + 16 * s + lk);
+    for (int r = 0; r < NR; ++r) acc[r] = mfma(w[s % (kPrefetch + 1)], a[r], acc[r]);
 #pragma unroll
-    for (int u = 0; u < NU; ++u)
-#pragma unroll
-      for (int r = 0; r < NR; ++r) acc[u][r] = mfma(w0[u], a[r], acc[u][r]);
-#pragma unroll
-    for (int u = 0; u < NU; ++u) { w0[u] = w1[u]; w1[u] = w2[u]; }
+    for (int r = 0; r < NR; ++r) a[r] = an[r];
   }
 }
 
-template <int NU, int NR>
-__device__ __forceinline__ void zero(f32x16 (&acc)[NU][NR]) {
+// accumulators start at the layer's bias: element e of a tile is unit u0 + 8(e/4) + 4(lane/32) + e%4
+template <int NR>
+__device__ __forceinline__ void init_bias(f32x16 (&acc)[NR], const float* __restrict__ bias, int u0,
+                                          int lane) {
+  const int lh = (lane >> 5) * 4;
 #pragma unroll
-  for (int u = 0; u < NU; ++u)
+  for (int g = 0; g < 4; ++g) {
+    const float4 b = *reinterpret_cast<const float4*>(bias + u0 + 8 * g + lh);
 #pragma unroll
-    for (int r = 0; r < NR; ++r)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc[u][r][e] = 0.0f;
+    for (int r = 0; r < NR; ++r) {
+      acc[r][4 * g + 0] = b.x;
+      acc[r][4 * g + 1] = b.y;
+      acc[r][4 * g + 2] = b.z;
+      acc[r][4 * g + 3] = b.w;
+    }
+  }
 }
 
-// bias + tanh, rounded to bf16, 4 consecutive units per 8-byte LDS store at Hs[row][col0 + unit]
-template <int NU, int NR>
-__device__ __forceinline__ void store_tanh(const f32x16 (&acc)[NU][NR], const float* __restrict__ bias,
-                                           __bf16* Hs, int u0, int col0, int lane) {
+// tanh, rounded to bf16, 4 consecutive units per 8-byte LDS store at Hs[row][unit]
+template <int NR>
+__device__ __forceinline__ void store_tanh(const f32x16 (&acc)[NR], __bf16* Hs, int u0, int lane) {
   const int lr = lane & 31, lh = (lane >> 5) * 4;
 #pragma unroll
-  for (int u = 0; u < NU; ++u)
+  for (int g = 0; g < 4; ++g) {
+    const int unit = u0 + 8 * g + lh;
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int unit = u0 + 32 * u + 8 * g + lh;
-      const float4 b = *reinterpret_cast<const float4*>(bias + unit);
-#pragma unroll
-      for (int r = 0; r < NR; ++r) {
-        bf16x4 v;
-        v[0] = (__bf16)tanh_act(acc[u][r][4 * g + 0] + b.x);
-        v[1] = (__bf16)tanh_act(acc[u][r][4 * g + 1] + b.y);
-        v[2] = (__bf16)tanh_act(acc[u][r][4 * g + 2] + b.z);
-        v[3] = (__bf16)tanh_act(acc[u][r][4 * g + 3] + b.w);
-        *reinterpret_cast<bf16x4*>(Hs + (32 * r + lr) * kHPitch + col0 + unit) = v;
-      }
+    for (int r = 0; r < NR; ++r) {
+      bf16x4 v;
+      v[0] = (__bf16)tanh_act(acc[r][4 * g + 0]);
+      v[1] = (__bf16)tanh_act(acc[r][4 * g + 1]);
+      v[2] = (__bf16)tanh_act(acc[r][4 * g + 2]);
+      v[3] = (__bf16)tanh_act(acc[r][4 * g + 3]);
+      *reinterpret_cast<bf16x4*>(Hs + (32 * r + lr) * kHPitch + unit) = v;
     }
+  }
+}
+
+// One network's two tanh layers for the workgroup's 64 rows: X (LDS) -> Hs -> Hs.  Wave w owns
+// units [32w, 32w + 32) of each layer.
+template <int KP>
+__device__ __forceinline__ void hidden_layers(const __bf16* Xs, __bf16* Hs, const __bf16* W1,
+                                              const float* b1, const __bf16* W2, const float* b2,
+                                              int wave, int lane) {
+  constexpr int XP = KP + 8;
+  {
+    f32x16 acc[2];
+    init_bias(acc, b1, 32 * wave, lane);
+    gemm_t<2, KP>(acc, W1, 32 * wave, Xs, XP, 0, lane);
+    store_tanh(acc, Hs, 32 * wave, lane);
+  }
+  __syncthreads();
+  f32x16 acc[2];
+  init_bias(acc, b2, 32 * wave, lane);
+  gemm_t<2, kHid>(acc, W2, 32 * wave, Hs, kHPitch, 0, lane);
+  __syncthreads();                                    // every wave has read layer 1
+  store_tanh(acc, Hs, 32 * wave, lane);
+  __syncthreads();
 }
 
 template <int KP>
-__global__ __launch_bounds__(kThreads) void policy_kernel(const F16PolicyArgs p) {
+__global__ __launch_bounds__(kThreads, 2) void policy_kernel(const F16PolicyArgs p) {
   constexpr int XP = KP + 8;
-  static_assert(kRows * kLPitch * 4 <= kRows * XP * 2, "logits reuse the input rows' LDS");
+  static_assert(kRows * kLPitch * 4 <= kRows * kHPitch * 2, "logits reuse the hidden rows' LDS");
   __shared__ __align__(16) __bf16 Xs[kRows * XP];
   __shared__ __align__(16) __bf16 Hs[kRows * kHPitch];
   __shared__ float col_mean[KP], col_sd[KP];
@@ -156,7 +174,7 @@ __global__ __launch_bounds__(kThreads) void policy_kernel(const F16PolicyArgs p)
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const __bf16* wbf = static_cast<const __bf16*>(G.wbf);
   const float* wf = G.wf;
-  const int D = p.obs_dim;
+  constexpr int D = KP == 192 ? 184 : 214;              // observation width of this kernel
 
   // ---- normalise (RunningNorm.normalize, ppo_gpu.py:210-214) and stage bf16 rows in LDS
   if (tid < KP) {
@@ -166,7 +184,7 @@ __global__ __launch_bounds__(kThreads) void policy_kernel(const F16PolicyArgs p)
   }
   __syncthreads();
   {
-    const int half = D >> 1;                          // float2 per row (obs_dim is even)
+    constexpr int half = D / 2;                       // float2 per row
     constexpr int kPer = (kRows * (KP / 2) + kThreads - 1) / kThreads;
     float2 x[kPer];
 #pragma unroll
@@ -210,111 +228,98 @@ __global__ __launch_bounds__(kThreads) void policy_kernel(const F16PolicyArgs p)
   }
   __syncthreads();
 
-  // ---- layer 1: [actor | critic] = tanh(W1 X^T + b1), wave owns 64 of the 512 units
+  // ---- actor: two tanh layers, then the logits head on waves 0-5 (32 units x 32 rows each)
+  hidden_layers<KP>(Xs, Hs, wbf + Blob<KP>::W1, wf + kB1, wbf + Blob<KP>::W2A, wf + kB2A, wave,
+                    lane);
+  float* Ls = reinterpret_cast<float*>(Hs);
   {
-    f32x16 acc[2][2];
-    zero(acc);
-    gemm_t<2, 2, KP>(acc, wbf + Blob<KP>::W1, 64 * wave, Xs, XP, 0, lane);
-    store_tanh(acc, wf + kB1, Hs, 64 * wave, 0, lane);
-  }
-  __syncthreads();
-
-  // ---- layer 2: waves 0-3 actor, 4-7 critic; 64 units each over the half's 256 inputs
-  {
-    const int half = wave >> 2;
-    const int u0 = (wave & 3) * 64;
-    f32x16 acc[2][2];
-    zero(acc);
-    gemm_t<2, 2, kHid>(acc, wbf + (half ? Blob<KP>::W2C : Blob<KP>::W2A), u0, Hs, kHPitch,
-                       half * kHid, lane);
-    __syncthreads();                                    // every wave has read layer 1
-    store_tanh(acc, wf + (half ? kB2C : kB2A), Hs, u0, half * kHid, lane);
-  }
-  __syncthreads();
-
-  // ---- heads: logits on waves 0-5 (32 units x 32 rows each), critic value on wave 6
-  float* Ls = reinterpret_cast<float*>(Xs);
-  if (wave < 6) {
     const int ut = wave % 3, rt = wave / 3;
-    f32x16 acc[1][1];
-    zero(acc);
-    gemm_t<1, 1, kHid>(acc, wbf + Blob<KP>::W3A, 32 * ut, Hs + 32 * rt * kHPitch, kHPitch, 0,
-                       lane);
-    const int row = 32 * rt + (lane & 31);
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int unit = 32 * ut + 8 * g + (lane >> 5) * 4;
-      const float4 b = *reinterpret_cast<const float4*>(wf + kB3A + unit);
-      float4 v;
-      v.x = acc[0][0][4 * g + 0] + b.x;
-      v.y = acc[0][0][4 * g + 1] + b.y;
-      v.z = acc[0][0][4 * g + 2] + b.z;
-      v.w = acc[0][0][4 * g + 3] + b.w;
-      *reinterpret_cast<float4*>(Ls + row * kLPitch + unit) = v;
+    f32x16 acc[1];
+    if (wave < 6) {
+      init_bias(acc, wf + kB3A, 32 * ut, lane);
+      gemm_t<1, kHid>(acc, wbf + Blob<KP>::W3A, 32 * ut, Hs + 32 * rt * kHPitch, kHPitch, 0,
+                      lane);
     }
-  } else if (wave == 6) {
+    __syncthreads();                                  // every wave has read actor layer 2
+    if (wave < 6) {
+      const int row = 32 * rt + (lane & 31);
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int unit = 32 * ut + 8 * g + (lane >> 5) * 4;
+        *reinterpret_cast<float4*>(Ls + row * kLPitch + unit) =
+            make_float4(acc[0][4 * g + 0], acc[0][4 * g + 1], acc[0][4 * g + 2], acc[0][4 * g + 3]);
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- per (row, channel): softmax, draw, log-probability, control (waves 0-3)
+  if (tid < kRows * kChan) {
+    const int row = tid >> 2, ch = tid & 3;
+    const float* l = Ls + row * kLPitch + ch * kBins;
+    float lg[kBins];
+#pragma unroll
+    for (int k = 0; k < kBins; ++k) lg[k] = l[k];
+    float m = lg[0];
+    int amax = 0;
+#pragma unroll
+    for (int k = 1; k < kBins; ++k)
+      if (lg[k] > m) { m = lg[k]; amax = k; }
+    float e[kBins], s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kBins; ++k) { e[k] = f16rng::exp_nonpos(lg[k] - m); s += e[k]; }
+    const int li = r0 + row;
+    const long pr = (row < nr) ? (p.rows ? p.rows[li] : li) : 0;
+    int idx = amax;
+    if (!p.deterministic) {
+      uint32_t c[4] = {(uint32_t)pr, p.step, (uint32_t)ch, p.salt};
+      f16rng::philox4x32_10(c, (uint32_t)p.seed, (uint32_t)(p.seed >> 32));
+      const float u = (float)(c[0] >> 8) * 0x1p-24f;
+      const float target = u * s;
+      float cum = 0.0f;
+      idx = kBins - 1;
+#pragma unroll
+      for (int k = 0; k < kBins; ++k) {
+        cum += e[k];
+        if (cum > target) { idx = k; break; }
+      }
+    }
+    float lp = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kBins; ++k)
+      if (k == idx) lp = (lg[k] - m) - logf(s);
+    lp += __shfl_xor(lp, 1);
+    lp += __shfl_xor(lp, 2);
+    if (row < nr) {
+      if (p.act_idx) p.act_idx[(long)li * kChan + ch] = idx;
+      if (p.logp && ch == 0) p.logp[li] = lp;
+      if (p.env_actions) {
+        float g = p.grid[idx];
+        if (ch == 3) g = 0.5f * g + 0.5f;
+        p.env_actions[pr * kChan + ch] = (double)g;
+      }
+      if (p.logits_out) {
+#pragma unroll
+        for (int k = 0; k < kBins; ++k) p.logits_out[(long)li * kLogits + ch * kBins + k] = lg[k];
+      }
+    }
+  }
+  __syncthreads();                                    // the logits are consumed
+
+  // ---- critic: two tanh layers, then the value dot products (one row per lane of wave 0)
+  hidden_layers<KP>(Xs, Hs, wbf + Blob<KP>::W1C, wf + kB1 + kHid, wbf + Blob<KP>::W2C,
+                    wf + kB2C, wave, lane);
+  if (wave == 0) {
     const int row = lane;
     const float* w3 = wf + kW3C;
     float s = 0.0f;
 #pragma unroll 4
     for (int k0 = 0; k0 < kHid; k0 += 8) {
-      const bf16x8 h = *reinterpret_cast<const bf16x8*>(Hs + row * kHPitch + kHid + k0);
+      const bf16x8 h = *reinterpret_cast<const bf16x8*>(Hs + row * kHPitch + k0);
 #pragma unroll
       for (int q = 0; q < 8; ++q) s += (float)h[q] * w3[k0 + q];
     }
     if (row < nr && p.value) p.value[r0 + row] = s + wf[kB3C];
-  }
-  __syncthreads();
-
-  // ---- per (row, channel): softmax, draw, log-probability, control (waves 0-3)
-  if (tid >= kRows * kChan) return;
-  const int row = tid >> 2, ch = tid & 3;
-  const float* l = Ls + row * kLPitch + ch * kBins;
-  float lg[kBins];
-#pragma unroll
-  for (int k = 0; k < kBins; ++k) lg[k] = l[k];
-  float m = lg[0];
-  int amax = 0;
-#pragma unroll
-  for (int k = 1; k < kBins; ++k)
-    if (lg[k] > m) { m = lg[k]; amax = k; }
-  float e[kBins], s = 0.0f;
-#pragma unroll
-  for (int k = 0; k < kBins; ++k) { e[k] = f16rng::exp_nonpos(lg[k] - m); s += e[k]; }
-  const int li = r0 + row;
-  const long pr = (row < nr) ? (p.rows ? p.rows[li] : li) : 0;
-  int idx = amax;
-  if (!p.deterministic) {
-    uint32_t c[4] = {(uint32_t)pr, p.step, (uint32_t)ch, p.salt};
-    f16rng::philox4x32_10(c, (uint32_t)p.seed, (uint32_t)(p.seed >> 32));
-    const float u = (float)(c[0] >> 8) * 0x1p-24f;
-    const float target = u * s;
-    float cum = 0.0f;
-    idx = kBins - 1;
-#pragma unroll
-    for (int k = 0; k < kBins; ++k) {
-      cum += e[k];
-      if (cum > target) { idx = k; break; }
-    }
-  }
-  float lp = 0.0f;
-#pragma unroll
-  for (int k = 0; k < kBins; ++k)
-    if (k == idx) lp = (lg[k] - m) - logf(s);
-  lp += __shfl_xor(lp, 1);
-  lp += __shfl_xor(lp, 2);
-  if (row < nr) {
-    if (p.act_idx) p.act_idx[(long)li * kChan + ch] = idx;
-    if (p.logp && ch == 0) p.logp[li] = lp;
-    if (p.env_actions) {
-      float g = p.grid[idx];
-      if (ch == 3) g = 0.5f * g + 0.5f;
-      p.env_actions[pr * kChan + ch] = (double)g;
-    }
-    if (p.logits_out) {
-#pragma unroll
-      for (int k = 0; k < kBins; ++k) p.logits_out[(long)li * kLogits + ch * kBins + k] = lg[k];
-    }
   }
 }
 
