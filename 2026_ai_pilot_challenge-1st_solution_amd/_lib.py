@@ -37,6 +37,16 @@ class F16RewardCfg(ctypes.Structure):
                 ("max_time_s", _d), ("alt_hunt_coef", _d), ("mode", _i)]
 
 
+class F16EnvStepIO(ctypes.Structure):
+    """include/f16_obs.h F16EnvStepIO."""
+    _fields_ = [("states", _vp), ("ld", _l), ("actions", _vp), ("ic_pool", _vp),
+                ("pool_size", _l), ("pick", _vp), ("seed", ctypes.c_ulonglong),
+                ("step", ctypes.c_uint), ("obs_dim", _i), ("obs", _vp), ("terminal_obs", _vp),
+                ("reward", _vp), ("reward_f32", _vp), ("term", _vp), ("trunc", _vp),
+                ("done", _vp), ("done_f32", _vp), ("terminal_hp", _vp),
+                ("terminal_alt_m", _vp), ("terminal_finite", _vp), ("finite_acc", _vp)]
+
+
 class F16PolicyGroup(ctypes.Structure):
     """include/f16_policy.h F16PolicyGroup."""
     _fields_ = [("wbf", _vp), ("wf", _vp), ("row_begin", _i), ("row_end", _i)]
@@ -62,8 +72,7 @@ _SIGNATURES = {
     "f16_obr_advance": (_i, [_vp, _l, _vp, _RP, _CP, _vp, _vp, _vp, _vp]),
     "f16_obr_init_reward": (_i, [_vp, _l, _vp, _RP, _vp]),
     "f16_obr_build_obs": (_i, [_vp, _l, _vp, _RP, _i, _vp, _vp]),
-    "f16_env_post_step": (_i, [_vp, _l, _vp, _RP, _CP, _vp, _l, _vp, _i, _vp, _vp, _vp, _vp, _vp,
-                               _vp, _vp, _vp, _vp, _vp]),
+    "f16_env_post_step": (_i, [ctypes.POINTER(F16EnvStepIO), _RP, _CP, _vp]),
     "f16_state9": (_i, [_vp, _l, _i, _vp, _vp]),
     "f16_policy_step": (_i, [ctypes.POINTER(F16PolicyArgs), _vp]),
     "f16_norm_workspace_bytes": (_l, [_i, _i]),

@@ -18,6 +18,7 @@
 #include "f16_obs.h"
 #include "f16_state.h"
 #include "obs_device.h"
+#include "philox.h"
 
 namespace f16obs {
 
@@ -479,22 +480,23 @@ __global__ __launch_bounds__(kObsBlock) void build_obs_kernel(
   lane_build_obs(k, p, g, in, a, r, obs_dim, obs + a * obs_dim, nullptr);
 }
 
-__global__ __launch_bounds__(kObsBlock) void env_post_step_kernel(
-    double* __restrict__ st, long ld, const double* __restrict__ act, F16Recon r, F16RewardCfg c,
-    Origin O, const double* __restrict__ pool, long pool_size, const long* __restrict__ pick,
-    int obs_dim, float* __restrict__ obs, float* __restrict__ tobs, double* __restrict__ reward,
-    unsigned char* __restrict__ term, unsigned char* __restrict__ trunc,
-    unsigned char* __restrict__ done, double* __restrict__ thp, double* __restrict__ talt,
-    unsigned char* __restrict__ tfin) {
+__global__ __launch_bounds__(kObsBlock) void env_post_step_kernel(const F16EnvStepIO io,
+                                                                   F16Recon r, F16RewardCfg c,
+                                                                   Origin O) {
   const long a = (long)blockIdx.x * kObsBlock + threadIdx.x;
   if (a >= 2L * r.nenv) return;
   const long e = a >> 1;
   const int odd = (int)(a & 1);
-  if (tfin) {   // rl_env.py:545: every state value of both aircraft finite after the physics
+  double* __restrict__ st = io.states;
+  const long ld = io.ld;
+  if (io.terminal_finite || io.finite_acc) {   // rl_env.py:545: every state value finite
     int fin = 1;
     for (int f = 0; f < F16S_N; ++f) fin &= isfinite(st[f * ld + a]) ? 1 : 0;
     fin &= xchi(fin);
-    if (!odd) tfin[e] = (unsigned char)fin;
+    if (!odd) {
+      if (io.terminal_finite) io.terminal_finite[e] = (unsigned char)fin;
+      if (io.finite_acc && !fin) io.finite_acc[e] = 0;
+    }
   }
   Kin9 k;
   make_kin(st + a, ld, O, k);
@@ -502,24 +504,38 @@ __global__ __launch_bounds__(kObsBlock) void env_post_step_kernel(
   exchange(k, p);
   Geo g;
   pair_geo(k, p, g);
-  const AdvOut o = lane_advance(k, p, g, a, e, act, r, c);
-  reward[a] = o.reward;
+  const AdvOut o = lane_advance(k, p, g, a, e, io.actions, r, c);
+  if (io.reward) io.reward[a] = o.reward;
+  if (io.reward_f32) io.reward_f32[a] = (float)o.reward;
   const bool d = o.term || o.trunc;
-  if (!odd) { term[e] = o.term; trunc[e] = o.trunc; done[e] = d; }
-  if (thp) thp[a] = o.obs.hp;
-  if (talt) {
-    const double x = st[a], y = st[ld + a], z = st[2 * ld + a];
-    talt[a] = (sqrt(x * x + y * y + z * z) - kSeaLevelRadiusFtT) * kFt2M;
+  if (!odd) {
+    if (io.term) io.term[e] = o.term;
+    if (io.trunc) io.trunc[e] = o.trunc;
+    if (io.done) io.done[e] = d;
+    if (io.done_f32) io.done_f32[e] = d ? 1.0f : 0.0f;
   }
-  float* row = obs + a * obs_dim;
+  if (io.terminal_hp) io.terminal_hp[a] = o.obs.hp;
+  if (io.terminal_alt_m) {
+    const double x = st[a], y = st[ld + a], z = st[2 * ld + a];
+    io.terminal_alt_m[a] = (sqrt(x * x + y * y + z * z) - kSeaLevelRadiusFtT) * kFt2M;
+  }
+  const int D = io.obs_dim;
+  float* row = io.obs + a * D;
   // terminal observation (rl_env.py:552-554); live engagements keep it as their observation
-  lane_build_obs(k, p, g, o.obs, a, r, obs_dim, tobs ? tobs + a * obs_dim : row,
-                 (tobs && !d) ? row : nullptr);
+  lane_build_obs(k, p, g, o.obs, a, r, D, io.terminal_obs ? io.terminal_obs + a * D : row,
+                 (io.terminal_obs && !d) ? row : nullptr);
   if (!d) return;                    // per engagement: the pair leaves together
   // autoreset from the initial-condition pool (rl_env.py:559-577)
-  const long pk = pick[e];
-  const bool ok = pk >= 0 && pk < pool_size;
-  const double* src = pool + (ok ? pk * 2 + odd : 0) * F16S_N;
+  long pk;
+  if (io.pick) {
+    pk = io.pick[e];
+  } else {
+    uint32_t ctr[4] = {(uint32_t)e, io.step, 0u, 0x5EED5EEDu};
+    f16rng::philox4x32_10(ctr, (uint32_t)io.seed, (uint32_t)(io.seed >> 32));
+    pk = (long)(((uint64_t)ctr[0] * (uint64_t)io.pool_size) >> 32);
+  }
+  const bool ok = pk >= 0 && pk < io.pool_size;
+  const double* src = io.ic_pool + (ok ? pk * 2 + odd : 0) * F16S_N;
   const double qnan = __builtin_nan("");
   if (ok) {
     for (int f = 0; f < F16S_N; ++f) st[f * ld + a] = src[f];
@@ -531,11 +547,11 @@ __global__ __launch_bounds__(kObsBlock) void env_post_step_kernel(
   r.dealt[a] = 0.0; r.taken[a] = 0.0; r.hp_loss[a] = 0.0; r.prev_x[a] = 0.0;
   r.prev_alt_log[a] = 0.0;
   for (int i = 0; i < 3; ++i) {
-    r.prev_att[i * ld + a] = 0.0;
-    r.pqr[i * ld + a] = 0.0;
-    if (r.accel) { r.accel[i * ld + a] = 0.0; r.prev_vel_ned[i * ld + a] = 0.0; }
+    r.prev_att[i * r.ld + a] = 0.0;
+    r.pqr[i * r.ld + a] = 0.0;
+    if (r.accel) { r.accel[i * r.ld + a] = 0.0; r.prev_vel_ned[i * r.ld + a] = 0.0; }
   }
-  for (int i = 0; i < kActHist; ++i) r.act_hist[i * ld + a] = 0.0;
+  for (int i = 0; i < kActHist; ++i) r.act_hist[i * r.ld + a] = 0.0;
   if (!odd) r.t_sec[e] = 0.0;
   Kin9 k2;
   if (ok) {
@@ -553,7 +569,7 @@ __global__ __launch_bounds__(kObsBlock) void env_post_step_kernel(
   ObsIn fresh;
   fresh.hp = 1.0; fresh.fuel = 1.0; fresh.dealt = 0.0; fresh.taken = 0.0; fresh.t = 0.0;
   for (int i = 0; i < 3; ++i) { fresh.pqr[i] = 0.0; fresh.accel[i] = 0.0; }
-  lane_build_obs(k2, p2, g2, fresh, a, r, obs_dim, row, nullptr);
+  lane_build_obs(k2, p2, g2, fresh, a, r, D, row, nullptr);
 }
 
 // rl_env.py:583-592 state9_flat: (nac, 9) float64 rows N/E/D m, roll/pitch/yaw deg, u/v/w m/s
@@ -651,25 +667,19 @@ extern "C" int f16_obr_build_obs(const double* states, long ld, const unsigned c
   return f16_last_error();
 }
 
-extern "C" int f16_env_post_step(double* states, long ld, const double* actions,
-                                 const F16Recon* rec, const F16RewardCfg* cfg,
-                                 const double* ic_pool, long pool_size, const long* pick,
-                                 int obs_dim, float* obs, float* terminal_obs, double* reward,
-                                 unsigned char* term, unsigned char* trunc, unsigned char* done,
-                                 double* terminal_hp, double* terminal_alt_m,
-                                 unsigned char* terminal_finite, void* stream) {
-  if (obs_dim != 184 && obs_dim != 214) return F16_EINVAL;
-  int rc = check_recon(rec, obs_dim == 214);
+extern "C" int f16_env_post_step(const F16EnvStepIO* io, const F16Recon* rec,
+                                 const F16RewardCfg* cfg, void* stream) {
+  if (!io) return F16_EINVAL;
+  if (io->obs_dim != 184 && io->obs_dim != 214) return F16_EINVAL;
+  int rc = check_recon(rec, io->obs_dim == 214);
   if (rc) return rc;
   if ((rc = check_cfg(cfg))) return rc;
   if (rec->nenv == 0) return 0;
-  if (!states || !actions || !obs || !reward || !term || !trunc || !done || !ic_pool || !pick ||
-      pool_size < 1 || ld < 2L * rec->nenv)
+  if (!io->states || !io->actions || !io->obs || !io->ic_pool || io->pool_size < 1 ||
+      io->pool_size > 0xffffffffL || io->ld < 2L * rec->nenv || rec->ld != io->ld)
     return F16_EINVAL;
   hipLaunchKernelGGL(env_post_step_kernel, grid_for(rec->nenv), dim3(kObsBlock), 0,
-                     (hipStream_t)stream, states, ld, actions, *rec, *cfg, origin(), ic_pool,
-                     pool_size, pick, obs_dim, obs, terminal_obs, reward, term, trunc, done,
-                     terminal_hp, terminal_alt_m, terminal_finite);
+                     (hipStream_t)stream, *io, *rec, *cfg, origin());
   return f16_last_error();
 }
 

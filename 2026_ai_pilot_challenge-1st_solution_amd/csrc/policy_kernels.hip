@@ -323,9 +323,10 @@ __global__ __launch_bounds__(kThreads, 2) void policy_kernel(const F16PolicyArgs
   }
 }
 
-// ---- RunningNorm.update: per-block column partial sums, then one fixed-order merge
+// ---- RunningNorm.update: column partial sums over 32-row slabs (every load of a slab in flight
+// at once), a per-column fixed-order tree merge (deterministic), and the count update last.
 constexpr int kNormThreads = 256;
-constexpr int kNormRowsPerBlock = 128;
+constexpr int kNormRowsPerBlock = 32;
 
 __global__ __launch_bounds__(kNormThreads) void norm_partial_kernel(
     const float* __restrict__ obs, long ld, const int* __restrict__ rows, int nrows, int dim,
@@ -333,33 +334,48 @@ __global__ __launch_bounds__(kNormThreads) void norm_partial_kernel(
   const int c = threadIdx.x;
   const int b = blockIdx.x;
   if (c >= dim) return;
-  const int i0 = b * kNormRowsPerBlock, i1 = min(nrows, i0 + kNormRowsPerBlock);
+  const int i0 = b * kNormRowsPerBlock;
+  float x[kNormRowsPerBlock];
+#pragma unroll
+  for (int i = 0; i < kNormRowsPerBlock; ++i) {
+    const int ri = i0 + i;
+    x[i] = 0.0f;
+    if (ri < nrows) x[i] = obs[(rows ? (long)rows[ri] : (long)ri) * ld + c];
+  }
   double s = 0.0, q = 0.0;
-  for (int i = i0; i < i1; ++i) {
-    const long pr = rows ? rows[i] : i;
-    const double x = obs[pr * ld + c];
-    s += x;
-    q += x * x;
+#pragma unroll
+  for (int i = 0; i < kNormRowsPerBlock; ++i) {
+    const double v = x[i];
+    s += v;
+    q += v * v;
   }
   work[(long)b * 2 * dim + c] = s;
   work[(long)b * 2 * dim + dim + c] = q;
 }
 
+// one block per column: thread t sums partials t, t + 256, ... in order, then a fixed tree
 __global__ __launch_bounds__(kNormThreads) void norm_merge_kernel(
     const double* __restrict__ work, int nblocks, int nrows, int dim, float* __restrict__ mean,
-    float* __restrict__ var, float* __restrict__ count) {
-  const int c = threadIdx.x;
-  const float cnt = *count;
-  __syncthreads();                      // every lane has read the shared count
-  if (c < dim) {
-    double s = 0.0, q = 0.0;
-    for (int b = 0; b < nblocks; ++b) {
-      s += work[(long)b * 2 * dim + c];
-      q += work[(long)b * 2 * dim + dim + c];
-    }
-    const double mu = s / nrows;
-    double v = q / nrows - mu * mu;
+    float* __restrict__ var, const float* __restrict__ count) {
+  __shared__ double ss[kNormThreads], sq[kNormThreads];
+  const int c = blockIdx.x, t = threadIdx.x;
+  double s = 0.0, q = 0.0;
+  for (int b = t; b < nblocks; b += kNormThreads) {
+    s += work[(long)b * 2 * dim + c];
+    q += work[(long)b * 2 * dim + dim + c];
+  }
+  ss[t] = s;
+  sq[t] = q;
+  __syncthreads();
+  for (int w = kNormThreads / 2; w > 0; w >>= 1) {
+    if (t < w) { ss[t] += ss[t + w]; sq[t] += sq[t + w]; }
+    __syncthreads();
+  }
+  if (t == 0) {
+    const double mu = ss[0] / nrows;
+    double v = sq[0] / nrows - mu * mu;
     v = v < 0.0 ? 0.0 : v;
+    const float cnt = *count;
     const float b_mean = (float)mu, b_var = (float)v, b_count = (float)nrows;
     const float delta = b_mean - mean[c];
     const float tot = cnt + b_count;
@@ -369,7 +385,10 @@ __global__ __launch_bounds__(kNormThreads) void norm_merge_kernel(
     const float M2 = m_a + m_b + (delta * delta) * (cnt * b_count / tot);
     var[c] = M2 / tot;
   }
-  if (c == 0) *count = cnt + (float)nrows;
+}
+
+__global__ void norm_count_kernel(float* __restrict__ count, int nrows) {
+  if (threadIdx.x == 0) *count = *count + (float)nrows;
 }
 
 static int norm_blocks(int nrows) { return (nrows + kNormRowsPerBlock - 1) / kNormRowsPerBlock; }
@@ -423,7 +442,8 @@ extern "C" int f16_norm_update(const float* obs, long obs_ld, const int* rows, i
   const int nb = norm_blocks(nrows);
   hipLaunchKernelGGL(norm_partial_kernel, dim3(nb), dim3(kNormThreads), 0, (hipStream_t)stream,
                      obs, obs_ld, rows, nrows, obs_dim, (double*)work);
-  hipLaunchKernelGGL(norm_merge_kernel, dim3(1), dim3(kNormThreads), 0, (hipStream_t)stream,
+  hipLaunchKernelGGL(norm_merge_kernel, dim3(obs_dim), dim3(kNormThreads), 0, (hipStream_t)stream,
                      (const double*)work, nb, nrows, obs_dim, mean, var, count);
+  hipLaunchKernelGGL(norm_count_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream, count, nrows);
   return f16_last_error();
 }

@@ -59,8 +59,10 @@ class SelfPlayRollout:
     (ppo_gpu.py:1971-1995) over (T, nenv, 2).  The learner's rows are both planes here, so every
     buffer carries nac = 2 nenv rows per step.
 
-    Per step: f16_norm_update (2 launches), f16_policy_step, the FDM decision and
-    f16_env_post_step, plus a reward cast and the done cast; no host synchronisation."""
+    Per step: f16_norm_update (3 small launches), f16_policy_step, the FDM decision and
+    f16_env_post_step (which writes the float32 rewards and done flags straight into the
+    buffers and draws autoreset pool rows itself); no host synchronisation.  stats=True adds the
+    reference's episode-return bookkeeping (a few small torch launches per step)."""
 
     def __init__(self, env, net, T=64, gamma=0.99, lam=0.95, seed=0, update_norm=True,
                  stats=True):
@@ -84,6 +86,7 @@ class SelfPlayRollout:
         self.next_done = torch.zeros(ne, dtype=f32, device=dev)
         self.ep_ret = torch.zeros(nac, dtype=f32, device=dev)
         self.ep_len = torch.zeros(ne, dtype=f32, device=dev)
+        self.finite_acc = torch.ones(ne, dtype=torch.uint8, device=dev)
         self.global_step = 0
         # When set to a list, collect() appends (start, end) events around each policy launch.
         self.policy_events = None
@@ -110,31 +113,31 @@ class SelfPlayRollout:
             raise RuntimeError("call reset() first")
         env, T = self.env, self.T
         dev = self.device
-        finite = torch.ones((), dtype=torch.bool, device=dev)
-        ret_sum = torch.zeros((), device=dev)
-        ep_count = torch.zeros((), device=dev)
+        self.finite_acc.fill_(1)
+        self.b_done[0].copy_(self.next_done)
+        if self.want_stats:
+            ret_sum = torch.zeros((), device=dev)
+            ep_count = torch.zeros((), device=dev)
         for t in range(T):
             obs = self.next_obs
             if self.update_norm:
                 self.norm.update(obs)
-            self.b_done[t].copy_(self.next_done)
             self._policy(obs, nobs_out=self.b_obs[t], act_idx=self.b_act[t], logp=self.b_logp[t],
                          value=self.b_val[t], env_actions=env.sim.actions)
-            o, rew, done, info = env.step(env.sim.actions, terminal_obs=False)
-            self.b_rew[t].copy_(rew.view(-1))
-            finite.logical_and_(info["terminal_state_finite"].all())
-            self.next_obs = o.view(self.nac, self.D)
-            self.next_done = done.float()
+            done_t = self.b_done[t + 1] if t + 1 < T else self.next_done
+            self.next_obs = env.step_rollout(self.b_rew[t], done_t, self.finite_acc)
             if self.want_stats:
-                d2 = self.next_done.repeat_interleave(2)
+                d2 = done_t.repeat_interleave(2)
                 self.ep_ret += self.b_rew[t]
                 ret_sum += (self.ep_ret * d2).sum()
-                ep_count += self.next_done.sum()
+                ep_count += done_t.sum()
                 self.ep_ret *= 1.0 - d2
             self.global_step += 1
         self._policy(self.next_obs, value=self.last_val)
         shape = (T, self.nenv, 2)
         adv, ret = gae(self.b_rew.view(shape), self.b_val.view(shape), self.b_done,
                        self.last_val.view(self.nenv, 2), self.next_done, self.gamma, self.lam)
-        stats = {"ret_sum": ret_sum, "ep_count": ep_count, "trajectory_finite": finite}
+        stats = {"trajectory_finite": self.finite_acc.all()}
+        if self.want_stats:
+            stats.update(ret_sum=ret_sum, ep_count=ep_count)
         return adv, ret, stats

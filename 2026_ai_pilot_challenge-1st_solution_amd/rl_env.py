@@ -63,14 +63,13 @@ class GpuDogfightVecEnv:
         self._evaluation_seed_metadata = None
         n, ne, dev = self.nac, self.nenv, self.device
         self._obs = torch.zeros(n, self.OBS_SIZE, dtype=torch.float32, device=dev)
-        self._term = torch.zeros(ne, dtype=torch.uint8, device=dev)
-        self._trunc = torch.zeros(ne, dtype=torch.uint8, device=dev)
-        self._done = torch.zeros(ne, dtype=torch.uint8, device=dev)
-        self._tfin = torch.zeros(ne, dtype=torch.uint8, device=dev)
         self._neutral = torch.tensor([NEUTRAL_ACTION], dtype=torch.float64,
                                      device=dev).expand(n, 4).contiguous()
         # When set to a list, step() appends (start, end) events around its post-physics launch.
         self.kernel_events = None
+        self._rec = self.obr._recon()
+        self._cfg, self._cfg_key = None, None
+        self._post_steps = 0
 
     # ---- initial conditions (rl_env.py:218-375) ----
     def _sample_pairs(self, npairs):
@@ -222,11 +221,45 @@ class GpuDogfightVecEnv:
         a = torch.as_tensor(actions, dtype=torch.float64, device=self.device)
         return a.reshape(self.nac, 4)
 
+    def _io(self, pick):
+        """F16EnvStepIO with the env's persistent pointers; per-call outputs set by the caller."""
+        io = _lib.F16EnvStepIO()
+        io.states, io.ld = self.sim._state_soa.data_ptr(), self.nac
+        io.actions = self.sim.actions.data_ptr()
+        io.ic_pool, io.pool_size = self.ic_pool.data_ptr(), self.ic_pool.shape[0]
+        io.pick = pick.data_ptr() if pick is not None else None
+        io.seed, io.step = self.seed, self._post_steps & 0xffffffff
+        io.obs_dim, io.obs = self.OBS_SIZE, self._obs.data_ptr()
+        return io
+
+    def _post(self, io):
+        c = self._cfg_struct()
+        ev = self.kernel_events
+        if ev is not None:
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+        rc = self.obr._lib.f16_env_post_step(_lib.ctypes.byref(io), _lib.ctypes.byref(self._rec),
+                                             _lib.ctypes.byref(c), _lib.stream_handle(self.device))
+        if ev is not None:
+            e1.record()
+            ev.append((e0, e1))
+        _lib.check(rc, "f16_env_post_step")
+        self._post_steps += 1
+
+    def _cfg_struct(self):
+        key = (tuple(sorted(self.reward_cfg.items())), self.min_altitude_m, self.max_engage_time_s,
+               self.reward_mode, self.alt_hunt_coef)
+        if self._cfg_key != key:
+            self._cfg = reward_cfg_struct(self.reward_cfg, self.min_altitude_m,
+                                          self.max_engage_time_s, self.reward_mode,
+                                          self.alt_hunt_coef)
+            self._cfg_key = key
+        return self._cfg
+
     def step(self, actions, *, reset_indices=None, terminal_obs=True):
         """actions (nenv,2,4) or (nac,4) [aileron, elevator, rudder, throttle].
         Returns (obs (nenv,2,D) f32, reward (nenv,2) f64, done (nenv,) bool, info).
-        terminal_obs=False skips the terminal-observation copy (info["terminal_obs"] is None):
-        the rollout collector reads only the terminal HP and altitude."""
+        terminal_obs=False skips the terminal-observation copy (info["terminal_obs"] is None)."""
         a = self._to_nac4(actions)
         self._ensure_ic_pool()
         self.sim.step(a, substeps=self.substeps, want_obs=False)
@@ -238,38 +271,39 @@ class GpuDogfightVecEnv:
                     or reset_indices.device != self.sim.states.device):
                 raise ValueError("reset indices must be one device int64 index per environment")
             pick = reset_indices.contiguous()
-        n, dev = self.nac, self.device
+        n, ne, dev = self.nac, self.nenv, self.device
         reward = torch.empty(n, dtype=torch.float64, device=dev)
         tobs = (torch.empty(n, self.OBS_SIZE, dtype=torch.float32, device=dev) if terminal_obs
                 else None)
         terminal_hp = torch.empty(n, dtype=torch.float64, device=dev)
         terminal_alt = torch.empty(n, dtype=torch.float64, device=dev)
-        c = reward_cfg_struct(self.reward_cfg, self.min_altitude_m, self.max_engage_time_s,
-                              self.reward_mode, self.alt_hunt_coef)
-        rec = self.obr._recon()
-        ev = self.kernel_events
-        if ev is not None:
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record()
-        rc = self.obr._lib.f16_env_post_step(
-            _lib.ptr(self.sim._state_soa), self.nac, _lib.ptr(self.sim.actions),
-            _lib.ctypes.byref(rec), _lib.ctypes.byref(c), _lib.ptr(self.ic_pool),
-            self.ic_pool.shape[0], _lib.ptr(pick), self.OBS_SIZE, _lib.ptr(self._obs),
-            _lib.ptr(tobs), _lib.ptr(reward), _lib.ptr(self._term), _lib.ptr(self._trunc),
-            _lib.ptr(self._done), _lib.ptr(terminal_hp), _lib.ptr(terminal_alt),
-            _lib.ptr(self._tfin), _lib.stream_handle(dev))
-        if ev is not None:
-            e1.record()
-            ev.append((e0, e1))
-        _lib.check(rc, "f16_env_post_step")
-        term, trunc, done = self._term.bool(), self._trunc.bool(), self._done.bool()
+        term, trunc, done, fin = (torch.empty(ne, dtype=torch.bool, device=dev) for _ in range(4))
+        io = self._io(pick)
+        p = lambda t: t.data_ptr() if t is not None else None
+        io.terminal_obs, io.reward = p(tobs), p(reward)
+        io.term, io.trunc, io.done, io.terminal_finite = p(term), p(trunc), p(done), p(fin)
+        io.terminal_hp, io.terminal_alt_m = p(terminal_hp), p(terminal_alt)
+        self._post(io)
         info = {"terminated": term, "truncated": trunc,
-                "terminal_obs": tobs.view(self.nenv, 2, self.OBS_SIZE) if tobs is not None else None,
-                "terminal_hp": terminal_hp.view(self.nenv, 2),
-                "terminal_alt_m": terminal_alt.view(self.nenv, 2), "done": done,
-                "terminal_state_finite": self._tfin.bool()}
-        return (self._obs.view(self.nenv, 2, self.OBS_SIZE), reward.view(self.nenv, 2), done,
-                info)
+                "terminal_obs": tobs.view(ne, 2, self.OBS_SIZE) if tobs is not None else None,
+                "terminal_hp": terminal_hp.view(ne, 2),
+                "terminal_alt_m": terminal_alt.view(ne, 2), "done": done,
+                "terminal_state_finite": fin}
+        return self._obs.view(ne, 2, self.OBS_SIZE), reward.view(ne, 2), done, info
+
+    def step_rollout(self, reward_f32, done_f32, finite_acc):
+        """The rollout collector's step: the controls already sit in sim.actions (written by the
+        policy kernel); one FDM launch and one post-physics launch that writes the float32
+        rewards (nac,) and done flags (nenv,) straight into the caller's buffers and clears
+        finite_acc (nenv,) bytes of engagements whose state went non-finite.  Autoreset pool rows
+        are drawn inside the kernel (Philox keyed by the env seed and a per-env step counter)."""
+        self._ensure_ic_pool()
+        self.sim.step(self.sim.actions, substeps=self.substeps, want_obs=False)
+        io = self._io(None)
+        io.reward_f32, io.done_f32 = reward_f32.data_ptr(), done_f32.data_ptr()
+        io.finite_acc = finite_acc.data_ptr()
+        self._post(io)
+        return self._obs.view(self.nac, self.OBS_SIZE)
 
     # ---- state export (rl_env.py:583-592) ----
     def state9_flat(self):

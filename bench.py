@@ -153,7 +153,7 @@ def rollout_bench(nenv, T=64, reps=2):
     env = env_mod.GpuDogfightVecEnv(nenv, seed=0)
     net = pol.MLPActorCritic(184, init="normal", init_std=0.02,
                              generator=torch.Generator().manual_seed(0)).to("cuda")
-    ro = ppo.SelfPlayRollout(env, net, T=T, gamma=0.99, lam=0.95, seed=0)
+    ro = ppo.SelfPlayRollout(env, net, T=T, gamma=0.99, lam=0.95, seed=0, stats=False)
     ro.reset(stagger=False)
     ro.collect()                                    # warm-up rollout
     torch.cuda.synchronize()

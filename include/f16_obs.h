@@ -72,21 +72,43 @@ int f16_obr_init_reward(const double *states, long ld, const unsigned char *env_
 int f16_obr_build_obs(const double *states, long ld, const unsigned char *env_mask,
                       const F16Recon *rec, int obs_dim, float *obs, void *stream);
 
+/* Inputs and outputs of the fused post-physics step.  Output pointers may be NULL unless noted;
+ * byte flags are 0/1 (torch.bool compatible). */
+typedef struct F16EnvStepIO {
+    double *states;              /* SoA states (field k of aircraft a at states[k*ld + a]);
+                                    autoreset rewrites finished engagements in place (required) */
+    long ld;
+    const double *actions;       /* (nac, 4) controls of this decision (required) */
+    const double *ic_pool;       /* (pool_size, 2, 101) initial-condition rows (required) */
+    long pool_size;
+    const long *pick;            /* (nenv) pool row per engagement; NULL: drawn in the kernel as
+                                    floor(pool_size x0 / 2^32), x0 = Philox4x32-10 word 0 with key
+                                    `seed` and counter (e, step, 0, 0x5EED5EED) */
+    unsigned long long seed;
+    unsigned int step;
+    int obs_dim;                 /* 184 or 214 */
+    float *obs;                  /* (nac, obs_dim) observations after autoreset (required) */
+    float *terminal_obs;         /* (nac, obs_dim) observations before autoreset */
+    double *reward;              /* (nac) */
+    float *reward_f32;           /* (nac) the same rewards rounded to float32 */
+    unsigned char *term, *trunc, *done;   /* (nenv) */
+    float *done_f32;             /* (nenv) term|trunc as 0.0 / 1.0 */
+    double *terminal_hp;         /* (nac) HP after the decision, before autoreset */
+    double *terminal_alt_m;      /* (nac) (|ECI position| - sea-level radius) in metres */
+    unsigned char *terminal_finite;  /* (nenv) every state value of both aircraft finite */
+    unsigned char *finite_acc;   /* (nenv) cleared to 0 where terminal_finite is 0, else untouched */
+} F16EnvStepIO;
+
 /* GpuDogfightVecEnv.step after the physics launch (research/competition_36500/runtime/
- * cuda_fdm/rl_env.py:540-580), one launch: terminal_state_finite (may be NULL), advance +
- * reward + termination, the terminal observation (terminal_obs, may be NULL), terminal HP and
- * MSL altitude (either may be NULL), then for every engagement with term|trunc: the state rows
- * of ic_pool[pick[e]] ((pool_size, 2, 101) float64) are copied into states, the reconstructor
- * is reset, the reward state re-anchored and the observation rebuilt; live engagements keep
- * the terminal observation in `obs`.  `done` (uint8 per engagement) = term | trunc.  A pick
- * outside [0, pool_size) fills that engagement's states with NaN so the error surfaces as a
- * non-finite state instead of an out-of-bounds read. */
-int f16_env_post_step(double *states, long ld, const double *actions, const F16Recon *rec,
-                      const F16RewardCfg *cfg, const double *ic_pool, long pool_size,
-                      const long *pick, int obs_dim, float *obs, float *terminal_obs,
-                      double *reward, unsigned char *term, unsigned char *trunc,
-                      unsigned char *done, double *terminal_hp, double *terminal_alt_m,
-                      unsigned char *terminal_finite, void *stream);
+ * cuda_fdm/rl_env.py:540-580), one launch: the finite flag over the post-physics states,
+ * advance + reward + termination, the terminal observation, terminal HP and MSL altitude, then
+ * for every engagement with term|trunc: the state rows of ic_pool[pick] are copied into states,
+ * the reconstructor is reset, the reward state re-anchored and the observation rebuilt; live
+ * engagements keep the terminal observation in `obs`.  A pick outside [0, pool_size) fills that
+ * engagement's states with NaN so the error surfaces as a non-finite state instead of an
+ * out-of-bounds read. */
+int f16_env_post_step(const F16EnvStepIO *io, const F16Recon *rec, const F16RewardCfg *cfg,
+                      void *stream);
 
 /* GpuDogfightVecEnv.state9_flat (cuda_fdm/rl_env.py:583-592 with kinematics_state and
  * ned_from_ecef_altasl, :88-163): per aircraft N, E, D [m] (D = -MSL altitude; N/E the tangent

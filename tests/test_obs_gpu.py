@@ -271,15 +271,24 @@ def test_env_post_step_matches_reference_sequence(gpu, orc, obs_dim):
     obs = torch.full((n, obs_dim), -7.0, dtype=torch.float32, device=gpu)
     tobs = torch.empty_like(obs)
     rew = torch.empty(n, dtype=torch.float64, device=gpu)
+    rew32 = torch.empty(n, dtype=torch.float32, device=gpu)
     te, tr, dn, fin = (torch.empty(nenv, dtype=torch.uint8, device=gpu) for _ in range(4))
+    dn32 = torch.empty(nenv, dtype=torch.float32, device=gpu)
+    facc = torch.ones(nenv, dtype=torch.uint8, device=gpu)
     thp = torch.empty(n, dtype=torch.float64, device=gpu)
     talt = torch.empty(n, dtype=torch.float64, device=gpu)
     c = R.reward_cfg_struct(R.MY_REWARD_CONFIG, 304.8, 200.0, 0, 5.0)
     rec = obr._recon()
-    rc = L.lib().f16_env_post_step(
-        L.ptr(sim._state_soa), sim.nac, L.ptr(sim.actions), L.ctypes.byref(rec), L.ctypes.byref(c),
-        L.ptr(pool), 64, L.ptr(pick), obs_dim, L.ptr(obs), L.ptr(tobs), L.ptr(rew), L.ptr(te),
-        L.ptr(tr), L.ptr(dn), L.ptr(thp), L.ptr(talt), L.ptr(fin), L.stream_handle(gpu))
+    io = L.F16EnvStepIO(states=sim._state_soa.data_ptr(), ld=sim.nac,
+                        actions=sim.actions.data_ptr(), ic_pool=pool.data_ptr(), pool_size=64,
+                        pick=pick.data_ptr(), obs_dim=obs_dim, obs=obs.data_ptr(),
+                        terminal_obs=tobs.data_ptr(), reward=rew.data_ptr(),
+                        reward_f32=rew32.data_ptr(), term=te.data_ptr(), trunc=tr.data_ptr(),
+                        done=dn.data_ptr(), done_f32=dn32.data_ptr(),
+                        terminal_hp=thp.data_ptr(), terminal_alt_m=talt.data_ptr(),
+                        terminal_finite=fin.data_ptr(), finite_acc=facc.data_ptr())
+    rc = L.lib().f16_env_post_step(L.ctypes.byref(io), L.ctypes.byref(rec), L.ctypes.byref(c),
+                                   L.stream_handle(gpu))
     L.check(rc, "f16_env_post_step")
     # oracle replay of the reference sequence
     s9 = ob.state9(st0)
@@ -304,6 +313,9 @@ def test_env_post_step_matches_reference_sequence(gpu, orc, obs_dim):
     np.testing.assert_array_equal(fin.cpu().numpy().astype(bool),
                                   np.isfinite(st0).all(1).reshape(nenv, 2).all(1))
     assert np.abs(rew.cpu().numpy() - r_o).max() <= VAL_TOL
+    np.testing.assert_array_equal(rew32.cpu().numpy(), rew.cpu().numpy().astype(np.float32))
+    np.testing.assert_array_equal(dn32.cpu().numpy(), done_o.astype(np.float32))
+    np.testing.assert_array_equal(facc.cpu().numpy().astype(bool), fin.cpu().numpy().astype(bool))
     assert np.abs(thp.cpu().numpy() - thp_o).max() <= VAL_TOL
     alt_o = (np.linalg.norm(st0[:, 0:3], axis=1) - 20925646.32546) * FT2M
     assert np.abs(talt.cpu().numpy() - alt_o).max() <= 1e-6
@@ -326,19 +338,46 @@ def test_env_post_step_bad_pick_poisons_state(gpu):
     R = import_pkg("obs_reward")
     n = 2 * nenv
     obs = torch.zeros(n, 184, dtype=torch.float32, device=gpu)
-    rew = torch.empty(n, dtype=torch.float64, device=gpu)
-    te, tr, dn = (torch.empty(nenv, dtype=torch.uint8, device=gpu) for _ in range(3))
+    dn = torch.empty(nenv, dtype=torch.uint8, device=gpu)
     c = R.reward_cfg_struct(R.MY_REWARD_CONFIG, 0.0, 200.0, 0, 5.0)
     rec = obr._recon()
-    rc = L.lib().f16_env_post_step(
-        L.ptr(sim._state_soa), sim.nac, L.ptr(sim.actions), L.ctypes.byref(rec), L.ctypes.byref(c),
-        L.ptr(pool), nenv, L.ptr(pick), 184, L.ptr(obs), None, L.ptr(rew), L.ptr(te), L.ptr(tr),
-        L.ptr(dn), None, None, None, L.stream_handle(gpu))
+    io = L.F16EnvStepIO(states=sim._state_soa.data_ptr(), ld=sim.nac,
+                        actions=sim.actions.data_ptr(), ic_pool=pool.data_ptr(), pool_size=nenv,
+                        pick=pick.data_ptr(), obs_dim=184, obs=obs.data_ptr(), done=dn.data_ptr())
+    rc = L.lib().f16_env_post_step(L.ctypes.byref(io), L.ctypes.byref(rec), L.ctypes.byref(c),
+                                   L.stream_handle(gpu))
     L.check(rc, "f16_env_post_step")
     st = sim.states.cpu().numpy().reshape(nenv, 2, 101)
     assert dn.cpu().numpy().all()
     assert np.isfinite(st[[0, 3]]).all()
     assert np.isnan(st[[1, 2]]).all()
+
+
+def test_env_post_step_kernel_picks(gpu, orc):
+    """pick = NULL: finished engagements take pool row floor(P x0 / 2^32) of Philox4x32-10
+    (key = seed, counter = (e, step, 0, 0x5EED5EED))."""
+    from test_policy import philox
+    nenv, P = 64, 48
+    sim = _random_states(gpu, nenv, 91)
+    pool = _random_states(gpu, P, 92).states.reshape(P, 2, 101).contiguous()
+    obr = _obr(nenv)
+    obr.t_sec.fill_(199.95)                              # all truncate
+    L = import_pkg("_lib")
+    R = import_pkg("obs_reward")
+    obs = torch.zeros(2 * nenv, 184, dtype=torch.float32, device=gpu)
+    c = R.reward_cfg_struct(R.MY_REWARD_CONFIG, 0.0, 200.0, 0, 5.0)
+    rec = obr._recon()
+    seed, step = 0x1234_5678_9ABC, 17
+    io = L.F16EnvStepIO(states=sim._state_soa.data_ptr(), ld=sim.nac,
+                        actions=sim.actions.data_ptr(), ic_pool=pool.data_ptr(), pool_size=P,
+                        pick=None, seed=seed, step=step, obs_dim=184, obs=obs.data_ptr())
+    L.check(L.lib().f16_env_post_step(L.ctypes.byref(io), L.ctypes.byref(rec), L.ctypes.byref(c),
+                                      L.stream_handle(gpu)), "f16_env_post_step")
+    st = sim.states.cpu().numpy().reshape(nenv, 2, 101)
+    pn = pool.cpu().numpy()
+    for e in range(nenv):
+        x0 = philox(orc, [e, step, 0, 0x5EED5EED], [seed & 0xffffffff, seed >> 32])[0]
+        np.testing.assert_array_equal(st[e], pn[(x0 * P) >> 32])
 
 
 # ------------------------------------------------------------------------ the env object
