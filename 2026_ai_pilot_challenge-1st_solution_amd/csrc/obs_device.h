@@ -62,10 +62,30 @@ F16_HD void cross3(const double a[3], const double b[3], double o[3]) {
 }
 
 // ---------------------------------------------------------------- state9 bridge
+// Attitude of one aircraft: R = Tx(roll) Ty(pitch) Tz(yaw) (NED -> body, GeometryInfo
+// convention) and the sin/cos of roll, pitch, yaw (observation scalars 27-38 reuse them).
+struct Att { double R[3][3]; double sr, cr, sp, cp, sy, cy; };
+
+F16_HD void att_from_trig(Att& A) {
+  const double cr = A.cr, sr = A.sr, cp = A.cp, sp = A.sp, cy = A.cy, sy = A.sy;
+  A.R[0][0] = cp * cy;                  A.R[0][1] = cp * sy;                  A.R[0][2] = -sp;
+  A.R[1][0] = sr * (sp * cy) - cr * sy; A.R[1][1] = sr * (sp * sy) + cr * cy; A.R[1][2] = sr * cp;
+  A.R[2][0] = cr * (sp * cy) + sr * sy; A.R[2][1] = cr * (sp * sy) - sr * cy; A.R[2][2] = cr * cp;
+}
+
+// sin and cos of atan2(y, x) without the angle (atan2(0, 0) = 0)
+F16_HD void sc_atan2(double y, double x, double& s, double& c) {
+  const double h = sqrt(x * x + y * y);
+  if (h > 0.0) { s = y / h; c = x / h; } else { s = 0.0; c = 1.0; }
+}
+
 // 101-double state (field k at st[k*ld]) -> N/E/D m (D = -MSL), roll/pitch/yaw deg, body u/v/w
 // m/s.  N/E are the tangent projection about the origin of the point at the aircraft's
-// geodetic latitude/longitude (Bowring) and MSL altitude (rl_env.py:64-85).
-F16_HD void state9(const double* st, long ld, const Origin& O, double s9[9]) {
+// geodetic latitude/longitude (Bowring) and MSL altitude (rl_env.py:64-85).  The sines and
+// cosines of the Bowring angles and, when `att` is given, of the Euler angles come from the
+// ratios they are atan2'd from (sin atan2(y, x) = y / hypot(x, y)); the angles themselves are
+// produced only where they are outputs.
+F16_HD void state9(const double* st, long ld, const Origin& O, double s9[9], Att* att = nullptr) {
   const double px = st[0], py = st[ld], pz = st[2 * ld];
   const double vx = st[3 * ld], vy = st[4 * ld], vz = st[5 * ld];
   const double q0 = st[6 * ld], q1 = st[7 * ld], q2 = st[8 * ld], q3 = st[9 * ld];
@@ -91,10 +111,18 @@ F16_HD void state9(const double* st, long ld, const Origin& O, double s9[9]) {
   const double L02 = B[0][0] * Dn[0] + B[0][1] * Dn[1] + B[0][2] * Dn[2];
   const double L12 = B[1][0] * Dn[0] + B[1][1] * Dn[1] + B[1][2] * Dn[2];
   const double L22 = B[2][0] * Dn[0] + B[2][1] * Dn[1] + B[2][2] * Dn[2];
-  const double theta = asin(-clampd(L02, -1.0, 1.0));
+  const double sp = -clampd(L02, -1.0, 1.0);
+  const double theta = asin(sp);
   const double phi = atan2(L12, L22);
   double psi = atan2(L01, L00);
   psi = psi < 0.0 ? psi + 2.0 * 3.141592653589793 : psi;
+  if (att) {
+    att->sp = sp;
+    att->cp = sqrt((1.0 - sp) * (1.0 + sp));
+    sc_atan2(L12, L22, att->sr, att->cr);
+    sc_atan2(L01, L00, att->sy, att->cy);
+    att_from_trig(*att);
+  }
   const double dv[3] = {vx + kRot * py, vy - kRot * px, vz};
   double vb[3];
   mv3(B, dv, vb);
@@ -103,14 +131,10 @@ F16_HD void state9(const double* st, long ld, const Origin& O, double s9[9]) {
   const double exm = ex * kFt2M, eym = ey * kFt2M, ezm = ez * kFt2M;
   const double b = O.b, ep2 = O.ep2;
   const double p = sqrt(exm * exm + eym * eym);
-  const double lon = atan2(eym, exm);
-  const double th = atan2(ezm * kWgsA, p * b);
-  double sth, cth;
-  sincos(th, &sth, &cth);
-  const double lat = atan2(ezm + ep2 * b * (sth * sth * sth), p - kWgsE2 * kWgsA * (cth * cth * cth));
-  double slat, clat, slon, clon;
-  sincos(lat, &slat, &clat);
-  sincos(lon, &slon, &clon);
+  double sth, cth, slat, clat, slon, clon;
+  sc_atan2(ezm * kWgsA, p * b, sth, cth);
+  sc_atan2(ezm + ep2 * b * (sth * sth * sth), p - kWgsE2 * kWgsA * (cth * cth * cth), slat, clat);
+  sc_atan2(eym, exm, slon, clon);
   const double Nr = kWgsA / sqrt(1.0 - kWgsE2 * slat * slat);
   const double dx = (Nr + alt_m) * clat * clon - O.ox, dy = (Nr + alt_m) * clat * slon - O.oy;
   const double dz = (Nr * (1.0 - kWgsE2) + alt_m) * slat - O.oz;
@@ -122,18 +146,11 @@ F16_HD void state9(const double* st, long ld, const Origin& O, double s9[9]) {
 }
 
 // ---------------------------------------------------------------- attitude helpers
-// Attitude of one aircraft: R = Tx(roll) Ty(pitch) Tz(yaw) (NED -> body, GeometryInfo
-// convention) and the sin/cos of roll, pitch, yaw (observation scalars 27-38 reuse them).
-struct Att { double R[3][3]; double sr, cr, sp, cp, sy, cy; };
-
 F16_HD void attitude(const double s9[9], Att& A) {
   sincos(s9[3] * kD2R, &A.sr, &A.cr);
   sincos(s9[4] * kD2R, &A.sp, &A.cp);
   sincos(s9[5] * kD2R, &A.sy, &A.cy);
-  const double cr = A.cr, sr = A.sr, cp = A.cp, sp = A.sp, cy = A.cy, sy = A.sy;
-  A.R[0][0] = cp * cy;                A.R[0][1] = cp * sy;                A.R[0][2] = -sp;
-  A.R[1][0] = sr * (sp * cy) - cr * sy; A.R[1][1] = sr * (sp * sy) + cr * cy; A.R[1][2] = sr * cp;
-  A.R[2][0] = cr * (sp * cy) + sr * sy; A.R[2][1] = cr * (sp * sy) - sr * cy; A.R[2][2] = cr * cp;
+  att_from_trig(A);
 }
 
 F16_HD void unit_or_self(const double v[3], double o[3]) {
@@ -150,21 +167,22 @@ F16_HD double ata_deg(const double own[9], const double R[3][3], const double tg
   return acos(clampd(R[0][0] * u[0] + R[0][1] * u[1] + R[0][2] * u[2], -1.0, 1.0)) * kR2D;
 }
 
-// x axis along `x`, roll fixed by gravity; north, then east, when x is vertical (dir_frame)
+// x axis along `x`, roll fixed by gravity; north, then east, when x is vertical (dir_frame);
+// the identity for |x| < 1e-8.  Branch-free (both results formed, then selected), which keeps
+// the frame in registers.
 F16_HD void dir_frame(const double x[3], double F[3][3]) {
   const double nx = norm3(x);
-  if (!(nx >= 1e-8)) {
-    F[0][0] = 1; F[0][1] = 0; F[0][2] = 0; F[1][0] = 0; F[1][1] = 1; F[1][2] = 0;
-    F[2][0] = 0; F[2][1] = 0; F[2][2] = 1;
-    return;
-  }
-  const double xn[3] = {x[0] / nx, x[1] / nx, x[2] / nx};
-  // projections of down, north, east off x
-  double z[3] = {-xn[2] * xn[0], -xn[2] * xn[1], 1.0 - xn[2] * xn[2]};
-  if (!(norm3(z) >= 1e-6)) {
-    z[0] = 1.0 - xn[0] * xn[0]; z[1] = -xn[0] * xn[1]; z[2] = -xn[0] * xn[2];
-    if (!(norm3(z) >= 1e-6)) { z[0] = -xn[1] * xn[0]; z[1] = 1.0 - xn[1] * xn[1]; z[2] = -xn[1] * xn[2]; }
-  }
+  const bool ok = nx >= 1e-8;
+  const double nxs = ok ? nx : 1.0;
+  const double xn[3] = {x[0] / nxs, x[1] / nxs, x[2] / nxs};
+  // projections of down, north, east off x; the first with norm >= 1e-6 is used
+  const double zd[3] = {-xn[2] * xn[0], -xn[2] * xn[1], 1.0 - xn[2] * xn[2]};
+  const double zn[3] = {1.0 - xn[0] * xn[0], -xn[0] * xn[1], -xn[0] * xn[2]};
+  const double ze[3] = {-xn[1] * xn[0], 1.0 - xn[1] * xn[1], -xn[1] * xn[2]};
+  const bool use_d = norm3(zd) >= 1e-6, use_n = norm3(zn) >= 1e-6;
+  double z[3];
+#pragma unroll
+  for (int i = 0; i < 3; ++i) z[i] = use_d ? zd[i] : (use_n ? zn[i] : ze[i]);
   double n = norm3(z);
   n = n > 1e-300 ? n : 1e-300;
   z[0] /= n; z[1] /= n; z[2] /= n;
@@ -174,12 +192,17 @@ F16_HD void dir_frame(const double x[3], double F[3][3]) {
   n = n > 1e-300 ? n : 1e-300;
   y[0] /= n; y[1] /= n; y[2] /= n;
   cross3(xn, y, z);
-  for (int i = 0; i < 3; ++i) { F[0][i] = xn[i]; F[1][i] = y[i]; F[2][i] = z[i]; }
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    F[0][i] = ok ? xn[i] : (i == 0 ? 1.0 : 0.0);
+    F[1][i] = ok ? y[i] : (i == 1 ? 1.0 : 0.0);
+    F[2][i] = ok ? z[i] : (i == 2 ? 1.0 : 0.0);
+  }
 }
 
 F16_HD double normz(double x, double lo, double hi) {
-  const double mid = (hi + lo) * 0.5, half = (hi - lo) * 0.5;
-  return (clampd(x, lo, hi) - mid) / half;
+  const double mid = (hi + lo) * 0.5, inv_half = 1.0 / ((hi - lo) * 0.5);
+  return (clampd(x, lo, hi) - mid) * inv_half;
 }
 
 // three-tier cone damage rate, tier 1 first (obs_reward.py:206-218)

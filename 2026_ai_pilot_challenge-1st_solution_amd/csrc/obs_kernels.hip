@@ -23,6 +23,12 @@
 namespace f16obs {
 
 constexpr int kObsBlock = 256;
+// Kernels that write observation rows run one wave per workgroup: each lane builds its row in a
+// wave-private LDS tile (odd pitch: lane-per-row stores hit distinct banks), then the wave copies
+// the tile out as consecutive 8-byte pieces -- its 64 rows are one contiguous range of the
+// row-major observation matrix, so the stores coalesce instead of striding by a row per lane.
+constexpr int kRowBlock = 64;
+constexpr int kStagePitch = 215;     // >= 214, odd
 constexpr double kFuelBurn = 8.0e-5;          // fuel proxy burn per second at 300 m/s
 constexpr double kFuelRef = 300.0;
 constexpr double kSeaLevelRadiusFtT = 20925646.32546;
@@ -68,8 +74,7 @@ struct ObsIn {
 };
 
 __device__ __forceinline__ void make_kin(const double* st, long ld, const Origin& O, Kin9& k) {
-  state9(st, ld, O, k.s9);
-  attitude(k.s9, k.A);
+  state9(st, ld, O, k.s9, &k.A);
   mtv3(k.A.R, k.s9 + 6, k.vn);
   k.spd = norm3(k.s9 + 6);
 }
@@ -234,48 +239,59 @@ __device__ __forceinline__ AdvOut lane_advance(const Kin9& k, const Peer& p, con
   return out;
 }
 
+// Feature transforms stored as float32: tanh and a Gaussian from the hardware exp2/reciprocal
+// (absolute error < 3e-7, far inside the float32 output's tolerance).
+__device__ __forceinline__ double tanh_feat(double x) {
+  const float xf = (float)x;
+  const float t = __builtin_amdgcn_exp2f(fabsf(xf) * -2.8853900817779268f);
+  return copysignf((1.0f - t) * __builtin_amdgcn_rcpf(1.0f + t), xf);
+}
+__device__ __forceinline__ double gauss_feat(double z) {      // e^{-z^2}
+  const float zf = (float)z;
+  return __builtin_amdgcn_exp2f(-(zf * zf) * 1.4426950408889634f);
+}
+
 __device__ __forceinline__ void put(float* o1, float* o2, int j, double v) {
   const float f = obs_value(v);
   o1[j] = f;
   if (o2) o2[j] = f;
 }
 
-// frames a vector is expressed in (rows = frame axes in NED)
-struct Frames {
-  const double (&Ro)[3][3];
-  const double (&Rt)[3][3];
-  const double (&Fmv)[3][3];
-  const double (&Fov)[3][3];
-  const double (&Flos)[3][3];
-};
 enum VecKind { kRaw = 0, kVel = 1, kRate = 2, kAcc = 3 };
 
-__device__ __forceinline__ void emit3(float* o1, float* o2, int& j, const double F[3][3],
-                                      const double v[3], int kind) {
-  double comp[3];
-  mv3(F, v, comp);
-#pragma unroll
-  for (int q = 0; q < 3; ++q) {
-    double val = comp[q];
-    if (kind == kVel) val = normz(val, -600.0, 600.0);
-    else if (kind == kRate) val = tanh(val / 4.0);
-    else if (kind == kAcc) val = normz(val, -150.0, 150.0);
-    put(o1, o2, j++, val);
-  }
+// The observation's vector block (my_observation.py _VEC_LAYOUT): vectors in order, each in the
+// six frames 0 NED, 1 own body, 2 partner body, 3 own motion, 4 partner motion, 5 line of sight,
+// minus one skipped frame.  Column of (vector s, frame f) in the row:
+struct VecSlot { int kind, skip; };
+constexpr VecSlot kVecs[9] = {{kRaw, 0}, {kRaw, 5}, {kVel, 3}, {kVel, 4}, {kVel, -1},
+                              {kRate, -1}, {kRate, -1}, {kAcc, 3}, {kAcc, 4}};
+__host__ __device__ constexpr int vec_base(int s) {
+  return s == 0 ? 50 : vec_base(s - 1) + 3 * (kVecs[s - 1].skip >= 0 ? 5 : 6);
+}
+__host__ __device__ constexpr int vec_col(int s, int f) {
+  return vec_base(s) + 3 * (f - ((kVecs[s].skip >= 0 && f > kVecs[s].skip) ? 1 : 0));
+}
+static_assert(vec_base(7) == 164 && vec_base(9) == 194, "184/214-D layout");
+
+__device__ __forceinline__ double vec_feature(double x, int kind) {
+  if (kind == kVel) return normz(x, -600.0, 600.0);
+  if (kind == kRate) return tanh_feat(x * 0.25);
+  if (kind == kAcc) return normz(x, -150.0, 150.0);
+  return x;
 }
 
-// one vector in the six frames minus `skip` (-1: none), NED first
-__device__ __forceinline__ void emit_vec(float* o1, float* o2, int& j, const Frames& Fr,
-                                         const double v[3], int kind, int skip) {
-  if (skip != 0) {   // NED: the identity, applied as a product like the other frames
-    const double I3[3][3] = {{1.0, 0.0, 0.0}, {0.0, 1.0, 0.0}, {0.0, 0.0, 1.0}};
-    emit3(o1, o2, j, I3, v, kind);
+// Frame f applied to every vector that uses it (frame-major, so only one frame is live at a time)
+template <int F>
+__device__ __forceinline__ void emit_frame(float* o1, float* o2, const double Fm[3][3],
+                                           const double (&V)[9][3], int nvec) {
+#pragma unroll
+  for (int s = 0; s < 9; ++s) {
+    if (s >= nvec || kVecs[s].skip == F) continue;
+    double comp[3];
+    mv3(Fm, V[s], comp);
+#pragma unroll
+    for (int q = 0; q < 3; ++q) put(o1, o2, vec_col(s, F) + q, vec_feature(comp[q], kVecs[s].kind));
   }
-  if (skip != 1) emit3(o1, o2, j, Fr.Ro, v, kind);
-  if (skip != 2) emit3(o1, o2, j, Fr.Rt, v, kind);
-  if (skip != 3) emit3(o1, o2, j, Fr.Fmv, v, kind);
-  if (skip != 4) emit3(o1, o2, j, Fr.Fov, v, kind);
-  if (skip != 5) emit3(o1, o2, j, Fr.Flos, v, kind);
 }
 
 // bank angle of the body y axis about the direction-of-motion frame (obs_reward.py:159-166)
@@ -284,7 +300,7 @@ __device__ __forceinline__ void bank_of(const double R[3][3], const double F[3][
   const double by[3] = {R[1][0], R[1][1], R[1][2]};
   const double y1 = F[1][0] * by[0] + F[1][1] * by[1] + F[1][2] * by[2];
   const double y2 = F[2][0] * by[0] + F[2][1] * by[1] + F[2][2] * by[2];
-  sincos(atan2(y2, y1), &s, &co);
+  sc_atan2(y2, y1, s, co);                   // sin, cos of atan2(y2, y1)
 }
 
 // One observation row (obs_reward.py:617-723; 214-D: cuda_fdm/external_observation.cu).
@@ -293,45 +309,65 @@ __device__ __forceinline__ void lane_build_obs(const Kin9& k, const Peer& p, con
                                                const ObsIn& own, long a, const F16Recon& r,
                                                int obs_dim, float* o1, float* o2) {
   const long ld = r.ld;
-  // partner's reconstructor values and partner-side geometry
+  const int nvec = obs_dim == 214 ? 9 : 7;
+  // ---- vector block, frame by frame
+  double V[9][3];
+  const bool los_ok = g.dist > 1e-6;
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    V[0][i] = i == 2 ? 1.0 : 0.0;                                  // gravity direction
+    V[1][i] = los_ok ? g.delta[i] / g.dist : 0.0;                 // line of sight
+    V[2][i] = k.vn[i];
+    V[3][i] = p.vn[i];
+    V[4][i] = p.vn[i] - k.vn[i];
+    V[7][i] = own.accel[i];
+  }
+  mtv3(k.A.R, own.pqr, V[5]);                                      // own body rates in NED
+#pragma unroll
+  for (int i = 0; i < 3; ++i) { V[6][i] = xch(V[5][i]); V[8][i] = xch(own.accel[i]); }
+  {
+    const double I3[3][3] = {{1.0, 0.0, 0.0}, {0.0, 1.0, 0.0}, {0.0, 0.0, 1.0}};
+    emit_frame<0>(o1, o2, I3, V, nvec);
+  }
+  emit_frame<1>(o1, o2, k.A.R, V, nvec);
+  emit_frame<2>(o1, o2, p.R, V, nvec);
+  double bs, bc, tbs, tbc;
+  {
+    double Fm[3][3];
+    dir_frame(k.vn, Fm);                                           // own motion frame
+    bank_of(k.A.R, Fm, bs, bc);
+    emit_frame<3>(o1, o2, Fm, V, nvec);
+    tbs = xch(bs); tbc = xch(bc);
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+#pragma unroll
+      for (int q = 0; q < 3; ++q) Fm[i][q] = xch(Fm[i][q]);           // partner's motion frame
+    emit_frame<4>(o1, o2, Fm, V, nvec);
+    dir_frame(g.delta, Fm);                                        // line-of-sight frame
+    emit_frame<5>(o1, o2, Fm, V, nvec);
+  }
+  // ---- scalars [0, 50)
   ObsIn tgt;
   tgt.hp = xch(own.hp); tgt.fuel = xch(own.fuel);
   double pb[3];
 #pragma unroll
   for (int i = 0; i < 3; ++i) pb[i] = xch(g.b[i]);
   const double en_ata = xch(g.ata);
-  // own direction-of-motion frame and bank; the partner's arrive by exchange
-  double Fmv[3][3];
-  dir_frame(k.vn, Fmv);
-  double bs, bc;
-  bank_of(k.A.R, Fmv, bs, bc);
-  const double tbs = xch(bs), tbc = xch(bc);
-  double Fov[3][3];
-#pragma unroll
-  for (int i = 0; i < 3; ++i)
-#pragma unroll
-    for (int j = 0; j < 3; ++j) Fov[i][j] = xch(Fmv[i][j]);
-  // body rates in NED (partner's by exchange), accelerations
-  double om_o[3];
-  mtv3(k.A.R, own.pqr, om_o);
-  double om_t[3], acc_t[3];
-#pragma unroll
-  for (int i = 0; i < 3; ++i) { om_t[i] = xch(om_o[i]); acc_t[i] = xch(own.accel[i]); }
-
   const double own_alt = -k.s9[2], tgt_alt = -p.s9[2];
-  double los_u[3] = {0.0, 0.0, 0.0}, closure = 0.0;
-  if (g.dist > 1e-6) {
-#pragma unroll
-    for (int i = 0; i < 3; ++i) los_u[i] = g.delta[i] / g.dist;
-    closure = (k.vn[0] - p.vn[0]) * los_u[0] + (k.vn[1] - p.vn[1]) * los_u[1] +
-              (k.vn[2] - p.vn[2]) * los_u[2];
-  }
-  // aspect angle from the partner's body-frame line of sight, signed by its body y
+  const double closure = (k.vn[0] - p.vn[0]) * V[1][0] + (k.vn[1] - p.vn[1]) * V[1][1] +
+                         (k.vn[2] - p.vn[2]) * V[1][2];
+  // sines and cosines of the line-of-sight angles straight from the unit vectors they are
+  // acos'd/atan2'd/asin'd from: ATA = acos(b0); aspect = +-acos(-pb0), signed by the partner's
+  // body y; azimuth = atan2(b1, b0); elevation = -asin(b2)
   const double pt1 = -pb[1], pt2 = pb[2];
   const double sgn = pt1 > 0.0 ? 1.0 : (pt1 < 0.0 ? -1.0 : (pt2 >= 0.0 ? 1.0 : -1.0));
-  const double aa = sgn * acos(clampd(-pb[0], -1.0, 1.0)) * kR2D;
-  const double az = atan2(g.b[1], g.b[0]) * kR2D;
-  const double el = -asin(clampd(g.b[2], -1.0, 1.0)) * kR2D;
+  const double cb0 = clampd(g.b[0], -1.0, 1.0), cpb0 = clampd(-pb[0], -1.0, 1.0);
+  const double cb2 = clampd(g.b[2], -1.0, 1.0);
+  const double s_ata = sqrt((1.0 - cb0) * (1.0 + cb0)), c_ata = cb0;
+  const double s_aa = sgn * sqrt((1.0 - cpb0) * (1.0 + cpb0)), c_aa = cpb0;
+  double s_az, c_az;
+  sc_atan2(g.b[1], g.b[0], s_az, c_az);
+  const double s_el = -cb2, c_el = sqrt((1.0 - cb2) * (1.0 + cb2));
   const double u = k.s9[6], v = k.s9[7], w = k.s9[8];
   double aoa = 0.0, ss = 0.0;
   if (!(k.spd < 1.0)) {
@@ -351,13 +387,12 @@ __device__ __forceinline__ void lane_build_obs(const Kin9& k, const Peer& p, con
   pf_ata = pf_ata < 0.0 ? 0.0 : pf_ata;
   double pf_rng = 1.0 - g.dist / 3000.0;
   pf_rng = pf_rng < 0.0 ? 0.0 : pf_rng;
-  double s_, c_;
   int j = 0;
   put(o1, o2, j++, normz(k.spd, 0.0, 600.0));
   put(o1, o2, j++, normz(p.spd, 0.0, 600.0));
-  put(o1, o2, j++, tanh(aoa / 30.0));
-  put(o1, o2, j++, tanh(ss / 15.0));
-  put(o1, o2, j++, tanh((own_alt - kMinAltM) / 300.0));
+  put(o1, o2, j++, tanh_feat(aoa / 30.0));
+  put(o1, o2, j++, tanh_feat(ss / 15.0));
+  put(o1, o2, j++, tanh_feat((own_alt - kMinAltM) / 300.0));
   put(o1, o2, j++, normz(-k.vn[2], -100.0, 100.0));
   put(o1, o2, j++, normz(own.hp, 0.0, 1.0));
   put(o1, o2, j++, normz(tgt.hp, 0.0, 1.0));
@@ -365,16 +400,16 @@ __device__ __forceinline__ void lane_build_obs(const Kin9& k, const Peer& p, con
   put(o1, o2, j++, e_adv / (fabs(e_adv) + 5000.0));
   put(o1, o2, j++, normz(g.dist, 0.0, 2500.0));
   put(o1, o2, j++, normz(closure, -1000.0, 1000.0));
-  sincos(g.ata * kD2R, &s_, &c_); put(o1, o2, j++, s_); put(o1, o2, j++, c_);
-  sincos(aa * kD2R, &s_, &c_); put(o1, o2, j++, s_); put(o1, o2, j++, c_);
-  sincos(az * kD2R, &s_, &c_); put(o1, o2, j++, s_); put(o1, o2, j++, c_);
-  sincos(el * kD2R, &s_, &c_); put(o1, o2, j++, s_); put(o1, o2, j++, c_);
-  put(o1, o2, j++, 2.0 * exp(-((g.ata / 3.0) * (g.ata / 3.0))) - 1.0);
-  put(o1, o2, j++, tanh((cone - fabs(g.ata)) / cc));
-  put(o1, o2, j++, 2.0 * exp(-((en_ata / 3.0) * (en_ata / 3.0))) - 1.0);
-  put(o1, o2, j++, tanh((cone - fabs(en_ata)) / cc));
-  put(o1, o2, j++, tanh((g.dist - min_r) / span));
-  put(o1, o2, j++, tanh((max_r - g.dist) / span));
+  put(o1, o2, j++, s_ata); put(o1, o2, j++, c_ata);
+  put(o1, o2, j++, s_aa); put(o1, o2, j++, c_aa);
+  put(o1, o2, j++, s_az); put(o1, o2, j++, c_az);
+  put(o1, o2, j++, s_el); put(o1, o2, j++, c_el);
+  put(o1, o2, j++, 2.0 * gauss_feat(g.ata / 3.0) - 1.0);
+  put(o1, o2, j++, tanh_feat((cone - fabs(g.ata)) / cc));
+  put(o1, o2, j++, 2.0 * gauss_feat(en_ata / 3.0) - 1.0);
+  put(o1, o2, j++, tanh_feat((cone - fabs(en_ata)) / cc));
+  put(o1, o2, j++, tanh_feat((g.dist - min_r) / span));
+  put(o1, o2, j++, tanh_feat((max_r - g.dist) / span));
   put(o1, o2, j++, normz(t, 0.0, 200.0));
   put(o1, o2, j++, k.A.sr); put(o1, o2, j++, k.A.cr);
   put(o1, o2, j++, k.A.sp); put(o1, o2, j++, k.A.cp);
@@ -391,28 +426,25 @@ __device__ __forceinline__ void lane_build_obs(const Kin9& k, const Peer& p, con
   put(o1, o2, j++, 2.0 * (pf_ata * pf_rng) - 1.0);
   put(o1, o2, j++, normz(own_alt, 0.0, 15000.0));
   put(o1, o2, j++, normz(tgt_alt, 0.0, 15000.0));
-  // 38 (vector, frame) pairs x 3 (my_observation.py _VEC_LAYOUT), then 10 more for 214-D.
-  // Frames: 0 NED, 1 own body, 2 partner body, 3 own motion, 4 partner motion, 5 line of sight.
-  double Flos[3][3];
-  dir_frame(g.delta, Flos);
-  const Frames Fr{k.A.R, p.R, Fmv, Fov, Flos};
-  double rel_vn[3];
 #pragma unroll
-  for (int i = 0; i < 3; ++i) rel_vn[i] = p.vn[i] - k.vn[i];
-  const double grav[3] = {0.0, 0.0, 1.0};
-  emit_vec(o1, o2, j, Fr, grav, kRaw, 0);
-  emit_vec(o1, o2, j, Fr, los_u, kRaw, 5);
-  emit_vec(o1, o2, j, Fr, k.vn, kVel, 3);
-  emit_vec(o1, o2, j, Fr, p.vn, kVel, 4);
-  emit_vec(o1, o2, j, Fr, rel_vn, kVel, -1);
-  emit_vec(o1, o2, j, Fr, om_o, kRate, -1);
-  emit_vec(o1, o2, j, Fr, om_t, kRate, -1);
-  if (obs_dim == 214) {
-    emit_vec(o1, o2, j, Fr, own.accel, kAcc, 3);
-    emit_vec(o1, o2, j, Fr, acc_t, kAcc, 4);
+  for (int i = 0; i < kActHist; ++i) put(o1, o2, vec_base(nvec) + i, r.act_hist[i * ld + a]);
+}
+
+// copy staged rows [0, n) of the tile to out[(a0 + row) * D ...], rows with keep[row] != 0 only
+// (keep == nullptr: all rows): row by row, the wave's lanes striding across the row in 8-byte
+// pieces (one contiguous 512-byte store per instruction)
+template <int D>
+__device__ __forceinline__ void flush_rows(const float* S, long a0, int n,
+                                           const unsigned char* keep, float* __restrict__ out,
+                                           int lane) {
+  for (int r = 0; r < n; ++r) {
+    if (keep && !keep[r]) continue;                   // uniform across the wave
+    float* dst = out + (a0 + r) * D;
+    const float* src = S + r * kStagePitch;
+#pragma unroll
+    for (int c = 2 * lane; c < D; c += 2 * kRowBlock)
+      *reinterpret_cast<float2*>(dst + c) = make_float2(src[c], src[c + 1]);
   }
-#pragma unroll
-  for (int i = 0; i < kActHist; ++i) put(o1, o2, j++, r.act_hist[i * ld + a]);
 }
 
 __device__ __forceinline__ ObsIn load_obs_in(const F16Recon& r, long a, long e) {
@@ -463,113 +495,143 @@ __global__ __launch_bounds__(kObsBlock) void init_reward_kernel(
   lane_init_reward(k, p, g, a, r.t_sec[e], r);
 }
 
-__global__ __launch_bounds__(kObsBlock) void build_obs_kernel(
+template <int D>
+__global__ __launch_bounds__(kRowBlock) void build_obs_kernel(
     const double* __restrict__ st, long ld, const unsigned char* __restrict__ mask, F16Recon r,
-    Origin O, int obs_dim, float* __restrict__ obs) {
-  const long a = (long)blockIdx.x * kObsBlock + threadIdx.x;
-  if (a >= 2L * r.nenv) return;
+    Origin O, float* __restrict__ obs) {
+  __shared__ float S[kRowBlock * kStagePitch];
+  __shared__ unsigned char keep[kRowBlock];
+  const int lane = threadIdx.x;
+  const long a0 = (long)blockIdx.x * kRowBlock, a = a0 + lane;
+  const long nac = 2L * r.nenv;
+  const int n = (int)min((long)kRowBlock, nac - a0);
   const long e = a >> 1;
-  if (mask && !mask[e]) return;
-  Kin9 k;
-  make_kin(st + a, ld, O, k);
-  Peer p;
-  exchange(k, p);
-  Geo g;
-  pair_geo(k, p, g);
-  const ObsIn in = load_obs_in(r, a, e);
-  lane_build_obs(k, p, g, in, a, r, obs_dim, obs + a * obs_dim, nullptr);
+  const bool on = a < nac && (!mask || mask[e]);      // per engagement: pairs agree
+  if (on) {
+    Kin9 k;
+    make_kin(st + a, ld, O, k);
+    Peer p;
+    exchange(k, p);
+    Geo g;
+    pair_geo(k, p, g);
+    const ObsIn in = load_obs_in(r, a, e);
+    lane_build_obs(k, p, g, in, a, r, D, S + lane * kStagePitch, nullptr);
+  }
+  keep[lane] = on ? 1 : 0;
+  __syncthreads();
+  flush_rows<D>(S, a0, n, keep, obs, lane);
 }
 
-__global__ __launch_bounds__(kObsBlock) void env_post_step_kernel(const F16EnvStepIO io,
+template <int D>
+__global__ __launch_bounds__(kRowBlock) void env_post_step_kernel(const F16EnvStepIO io,
                                                                    F16Recon r, F16RewardCfg c,
                                                                    Origin O) {
-  const long a = (long)blockIdx.x * kObsBlock + threadIdx.x;
-  if (a >= 2L * r.nenv) return;
+  __shared__ float S[kRowBlock * kStagePitch];
+  __shared__ unsigned char live[kRowBlock], fresh_row[kRowBlock];
+  const int lane = threadIdx.x;
+  const long a0 = (long)blockIdx.x * kRowBlock, a = a0 + lane;
+  const long nac = 2L * r.nenv;
+  const int n = (int)min((long)kRowBlock, nac - a0);
+  const bool on = a < nac;                              // nac is even: pairs agree
   const long e = a >> 1;
   const int odd = (int)(a & 1);
   double* __restrict__ st = io.states;
   const long ld = io.ld;
-  if (io.terminal_finite || io.finite_acc) {   // rl_env.py:545: every state value finite
-    int fin = 1;
-    for (int f = 0; f < F16S_N; ++f) fin &= isfinite(st[f * ld + a]) ? 1 : 0;
-    fin &= xchi(fin);
-    if (!odd) {
-      if (io.terminal_finite) io.terminal_finite[e] = (unsigned char)fin;
-      if (io.finite_acc && !fin) io.finite_acc[e] = 0;
-    }
-  }
+  bool d = false;
   Kin9 k;
-  make_kin(st + a, ld, O, k);
   Peer p;
-  exchange(k, p);
   Geo g;
-  pair_geo(k, p, g);
-  const AdvOut o = lane_advance(k, p, g, a, e, io.actions, r, c);
-  if (io.reward) io.reward[a] = o.reward;
-  if (io.reward_f32) io.reward_f32[a] = (float)o.reward;
-  const bool d = o.term || o.trunc;
-  if (!odd) {
-    if (io.term) io.term[e] = o.term;
-    if (io.trunc) io.trunc[e] = o.trunc;
-    if (io.done) io.done[e] = d;
-    if (io.done_f32) io.done_f32[e] = d ? 1.0f : 0.0f;
+  AdvOut o;
+  if (on) {
+    if (io.terminal_finite || io.finite_acc) {   // rl_env.py:545: every state value finite
+      int fin = 1;
+      for (int f = 0; f < F16S_N; ++f) fin &= isfinite(st[f * ld + a]) ? 1 : 0;
+      fin &= xchi(fin);
+      if (!odd) {
+        if (io.terminal_finite) io.terminal_finite[e] = (unsigned char)fin;
+        if (io.finite_acc && !fin) io.finite_acc[e] = 0;
+      }
+    }
+    make_kin(st + a, ld, O, k);
+    exchange(k, p);
+    pair_geo(k, p, g);
+    o = lane_advance(k, p, g, a, e, io.actions, r, c);
+    if (io.reward) io.reward[a] = o.reward;
+    if (io.reward_f32) io.reward_f32[a] = (float)o.reward;
+    d = o.term || o.trunc;
+    if (!odd) {
+      if (io.term) io.term[e] = o.term;
+      if (io.trunc) io.trunc[e] = o.trunc;
+      if (io.done) io.done[e] = d;
+      if (io.done_f32) io.done_f32[e] = d ? 1.0f : 0.0f;
+    }
+    if (io.terminal_hp) io.terminal_hp[a] = o.obs.hp;
+    if (io.terminal_alt_m) {
+      const double x = st[a], y = st[ld + a], z = st[2 * ld + a];
+      io.terminal_alt_m[a] = (sqrt(x * x + y * y + z * z) - kSeaLevelRadiusFtT) * kFt2M;
+    }
+    // terminal observation (rl_env.py:552-554)
+    lane_build_obs(k, p, g, o.obs, a, r, D, S + lane * kStagePitch, nullptr);
   }
-  if (io.terminal_hp) io.terminal_hp[a] = o.obs.hp;
-  if (io.terminal_alt_m) {
-    const double x = st[a], y = st[ld + a], z = st[2 * ld + a];
-    io.terminal_alt_m[a] = (sqrt(x * x + y * y + z * z) - kSeaLevelRadiusFtT) * kFt2M;
-  }
-  const int D = io.obs_dim;
-  float* row = io.obs + a * D;
-  // terminal observation (rl_env.py:552-554); live engagements keep it as their observation
-  lane_build_obs(k, p, g, o.obs, a, r, D, io.terminal_obs ? io.terminal_obs + a * D : row,
-                 (io.terminal_obs && !d) ? row : nullptr);
-  if (!d) return;                    // per engagement: the pair leaves together
-  // autoreset from the initial-condition pool (rl_env.py:559-577)
-  long pk;
-  if (io.pick) {
-    pk = io.pick[e];
+  live[lane] = (on && !d) ? 1 : 0;
+  fresh_row[lane] = (on && d) ? 1 : 0;
+  __syncthreads();
+  // every terminal row to terminal_obs; the live engagements' rows are also their observation
+  if (io.terminal_obs) {
+    flush_rows<D>(S, a0, n, nullptr, io.terminal_obs, lane);
+    flush_rows<D>(S, a0, n, live, io.obs, lane);
   } else {
-    uint32_t ctr[4] = {(uint32_t)e, io.step, 0u, 0x5EED5EEDu};
-    f16rng::philox4x32_10(ctr, (uint32_t)io.seed, (uint32_t)(io.seed >> 32));
-    pk = (long)(((uint64_t)ctr[0] * (uint64_t)io.pool_size) >> 32);
+    flush_rows<D>(S, a0, n, nullptr, io.obs, lane);
   }
-  const bool ok = pk >= 0 && pk < io.pool_size;
-  const double* src = io.ic_pool + (ok ? pk * 2 + odd : 0) * F16S_N;
-  const double qnan = __builtin_nan("");
-  if (ok) {
-    for (int f = 0; f < F16S_N; ++f) st[f * ld + a] = src[f];
-  } else {
-    for (int f = 0; f < F16S_N; ++f) st[f * ld + a] = qnan;
+  __syncthreads();
+  if (on && d) {           // autoreset from the initial-condition pool (rl_env.py:559-577)
+    long pk;
+    if (io.pick) {
+      pk = io.pick[e];
+    } else {
+      uint32_t ctr[4] = {(uint32_t)e, io.step, 0u, 0x5EED5EEDu};
+      f16rng::philox4x32_10(ctr, (uint32_t)io.seed, (uint32_t)(io.seed >> 32));
+      pk = (long)(((uint64_t)ctr[0] * (uint64_t)io.pool_size) >> 32);
+    }
+    const bool ok = pk >= 0 && pk < io.pool_size;
+    const double* src = io.ic_pool + (ok ? pk * 2 + odd : 0) * F16S_N;
+    const double qnan = __builtin_nan("");
+    if (ok) {
+      for (int f = 0; f < F16S_N; ++f) st[f * ld + a] = src[f];
+    } else {
+      for (int f = 0; f < F16S_N; ++f) st[f * ld + a] = qnan;
+    }
+    r.hp[a] = 1.0; r.fuel[a] = 1.0;
+    r.prev_valid[a] = 0; r.prev_x_valid[a] = 0;
+    r.dealt[a] = 0.0; r.taken[a] = 0.0; r.hp_loss[a] = 0.0; r.prev_x[a] = 0.0;
+    r.prev_alt_log[a] = 0.0;
+    for (int i = 0; i < 3; ++i) {
+      r.prev_att[i * r.ld + a] = 0.0;
+      r.pqr[i * r.ld + a] = 0.0;
+      if (r.accel) { r.accel[i * r.ld + a] = 0.0; r.prev_vel_ned[i * r.ld + a] = 0.0; }
+    }
+    for (int i = 0; i < kActHist; ++i) r.act_hist[i * r.ld + a] = 0.0;
+    if (!odd) r.t_sec[e] = 0.0;
+    Kin9 k2;
+    if (ok) {
+      make_kin(src, 1, O, k2);
+    } else {
+      const double nan14[14] = {qnan, qnan, qnan, qnan, qnan, qnan, qnan,
+                                qnan, qnan, qnan, qnan, qnan, qnan, qnan};   // fields 0..13
+      make_kin(nan14, 1, O, k2);
+    }
+    Peer p2;
+    exchange(k2, p2);
+    Geo g2;
+    pair_geo(k2, p2, g2);
+    lane_init_reward(k2, p2, g2, a, 0.0, r);
+    ObsIn fresh;
+    fresh.hp = 1.0; fresh.fuel = 1.0; fresh.dealt = 0.0; fresh.taken = 0.0; fresh.t = 0.0;
+    for (int i = 0; i < 3; ++i) { fresh.pqr[i] = 0.0; fresh.accel[i] = 0.0; }
+    lane_build_obs(k2, p2, g2, fresh, a, r, D, S + lane * kStagePitch, nullptr);
   }
-  r.hp[a] = 1.0; r.fuel[a] = 1.0;
-  r.prev_valid[a] = 0; r.prev_x_valid[a] = 0;
-  r.dealt[a] = 0.0; r.taken[a] = 0.0; r.hp_loss[a] = 0.0; r.prev_x[a] = 0.0;
-  r.prev_alt_log[a] = 0.0;
-  for (int i = 0; i < 3; ++i) {
-    r.prev_att[i * r.ld + a] = 0.0;
-    r.pqr[i * r.ld + a] = 0.0;
-    if (r.accel) { r.accel[i * r.ld + a] = 0.0; r.prev_vel_ned[i * r.ld + a] = 0.0; }
-  }
-  for (int i = 0; i < kActHist; ++i) r.act_hist[i * r.ld + a] = 0.0;
-  if (!odd) r.t_sec[e] = 0.0;
-  Kin9 k2;
-  if (ok) {
-    make_kin(src, 1, O, k2);
-  } else {
-    const double nan14[14] = {qnan, qnan, qnan, qnan, qnan, qnan, qnan,
-                              qnan, qnan, qnan, qnan, qnan, qnan, qnan};   // fields 0..13
-    make_kin(nan14, 1, O, k2);
-  }
-  Peer p2;
-  exchange(k2, p2);
-  Geo g2;
-  pair_geo(k2, p2, g2);
-  lane_init_reward(k2, p2, g2, a, 0.0, r);
-  ObsIn fresh;
-  fresh.hp = 1.0; fresh.fuel = 1.0; fresh.dealt = 0.0; fresh.taken = 0.0; fresh.t = 0.0;
-  for (int i = 0; i < 3; ++i) { fresh.pqr[i] = 0.0; fresh.accel[i] = 0.0; }
-  lane_build_obs(k2, p2, g2, fresh, a, r, D, row, nullptr);
+  __syncthreads();
+  flush_rows<D>(S, a0, n, fresh_row, io.obs, lane);
 }
 
 // rl_env.py:583-592 state9_flat: (nac, 9) float64 rows N/E/D m, roll/pitch/yaw deg, u/v/w m/s
@@ -626,6 +688,10 @@ static dim3 grid_for(int nenv) {
   return dim3((unsigned)((2L * nenv + kObsBlock - 1) / kObsBlock));
 }
 
+static dim3 grid_rows(int nenv) {
+  return dim3((unsigned)((2L * nenv + kRowBlock - 1) / kRowBlock));
+}
+
 }  // namespace f16obs
 
 using namespace f16obs;
@@ -662,8 +728,12 @@ extern "C" int f16_obr_build_obs(const double* states, long ld, const unsigned c
   if (rc) return rc;
   if (rec->nenv == 0) return 0;
   if (!states || !obs || ld < 2L * rec->nenv) return F16_EINVAL;
-  hipLaunchKernelGGL(build_obs_kernel, grid_for(rec->nenv), dim3(kObsBlock), 0,
-                     (hipStream_t)stream, states, ld, env_mask, *rec, origin(), obs_dim, obs);
+  if (obs_dim == 184)
+    hipLaunchKernelGGL(build_obs_kernel<184>, grid_rows(rec->nenv), dim3(kRowBlock), 0,
+                       (hipStream_t)stream, states, ld, env_mask, *rec, origin(), obs);
+  else
+    hipLaunchKernelGGL(build_obs_kernel<214>, grid_rows(rec->nenv), dim3(kRowBlock), 0,
+                       (hipStream_t)stream, states, ld, env_mask, *rec, origin(), obs);
   return f16_last_error();
 }
 
@@ -678,8 +748,12 @@ extern "C" int f16_env_post_step(const F16EnvStepIO* io, const F16Recon* rec,
   if (!io->states || !io->actions || !io->obs || !io->ic_pool || io->pool_size < 1 ||
       io->pool_size > 0xffffffffL || io->ld < 2L * rec->nenv || rec->ld != io->ld)
     return F16_EINVAL;
-  hipLaunchKernelGGL(env_post_step_kernel, grid_for(rec->nenv), dim3(kObsBlock), 0,
-                     (hipStream_t)stream, *io, *rec, *cfg, origin());
+  if (io->obs_dim == 184)
+    hipLaunchKernelGGL(env_post_step_kernel<184>, grid_rows(rec->nenv), dim3(kRowBlock), 0,
+                       (hipStream_t)stream, *io, *rec, *cfg, origin());
+  else
+    hipLaunchKernelGGL(env_post_step_kernel<214>, grid_rows(rec->nenv), dim3(kRowBlock), 0,
+                       (hipStream_t)stream, *io, *rec, *cfg, origin());
   return f16_last_error();
 }
 
