@@ -34,7 +34,8 @@ class F16RewardCfg(ctypes.Structure):
     _fields_ = [("own_damage_weight", _d), ("damage_scale", _d), ("shaping_reward_scale", _d),
                 ("win_reward", _d), ("loss_reward", _d), ("timeout_win_reward", _d),
                 ("timeout_loss_reward", _d), ("timeout_draw_reward", _d), ("min_alt_m", _d),
-                ("max_time_s", _d), ("alt_hunt_coef", _d), ("mode", _i)]
+                ("max_time_s", _d), ("alt_hunt_coef", _d), ("mode", _i),
+                ("fuel_exhaustion", _i)]
 
 
 class F16EnvStepIO(ctypes.Structure):
@@ -44,19 +45,22 @@ class F16EnvStepIO(ctypes.Structure):
                 ("step", ctypes.c_uint), ("obs_dim", _i), ("obs", _vp), ("terminal_obs", _vp),
                 ("reward", _vp), ("reward_f32", _vp), ("term", _vp), ("trunc", _vp),
                 ("done", _vp), ("done_f32", _vp), ("terminal_hp", _vp),
-                ("terminal_alt_m", _vp), ("terminal_finite", _vp), ("finite_acc", _vp)]
+                ("terminal_alt_m", _vp), ("terminal_finite", _vp), ("finite_acc", _vp),
+                ("opp_assign", _vp), ("opp_cdf", _vp), ("n_opp", _i)]
 
 
 class F16PolicyGroup(ctypes.Structure):
     """include/f16_policy.h F16PolicyGroup."""
-    _fields_ = [("wbf", _vp), ("wf", _vp), ("row_begin", _i), ("row_end", _i)]
+    _fields_ = [("wbf", _vp), ("wf", _vp), ("mean", _vp), ("var", _vp), ("row_begin", _i),
+                ("row_end", _i)]
 
 
 class F16PolicyArgs(ctypes.Structure):
     """include/f16_policy.h F16PolicyArgs."""
     _fields_ = [("obs", _vp), ("obs_ld", _l), ("obs_dim", _i), ("mean", _vp), ("var", _vp),
                 ("clip", ctypes.c_float), ("eps", ctypes.c_float), ("rows", _vp),
-                ("ngroups", _i), ("group", F16PolicyGroup * 16), ("seed", ctypes.c_ulonglong),
+                ("ngroups", _i), ("group", F16PolicyGroup * 16), ("group_offsets", _vp),
+                ("max_group_rows", _i), ("seed", ctypes.c_ulonglong),
                 ("step", ctypes.c_uint), ("salt", ctypes.c_uint), ("deterministic", _i),
                 ("grid", _vp), ("nobs_out", _vp), ("nobs_ld", _l), ("act_idx", _vp),
                 ("logp", _vp), ("value", _vp), ("env_actions", _vp), ("logits_out", _vp)]
@@ -77,6 +81,7 @@ _SIGNATURES = {
     "f16_policy_step": (_i, [ctypes.POINTER(F16PolicyArgs), _vp]),
     "f16_norm_workspace_bytes": (_l, [_i, _i]),
     "f16_abi_struct_sizes": (_i, [ctypes.POINTER(_l), _i]),
+    "f16_group_rows": (_i, [_vp, _i, _i, _i, _i, _vp, _vp, _vp]),
     "f16_norm_update": (_i, [_vp, _l, _vp, _i, _i, _vp, _vp, _vp, _vp, _vp]),
 }
 

@@ -134,7 +134,8 @@ struct AdvOut {
 // (obs_reward.py:571-614 push_actions/advance, 747-819 compute_reward; rl_env.py:467-484).
 __device__ __forceinline__ AdvOut lane_advance(const Kin9& k, const Peer& p, const Geo& g, long a,
                                                long e, const double* __restrict__ act,
-                                               const F16Recon& r, const F16RewardCfg& c) {
+                                               const F16Recon& r, const F16RewardCfg& c,
+                                               double phys_fuel = 1.0) {
   const long ld = r.ld;
   AdvOut out;
   // action history: roll by one decision, newest first
@@ -192,8 +193,10 @@ __device__ __forceinline__ AdvOut lane_advance(const Kin9& k, const Peer& p, con
   const double alt_o = -k.s9[2], alt_t = -p.s9[2];
   const double hp_t = xch(hp);
   const bool finite = finite9(k.s9) && finite9(p.s9);
+  const double phys_fuel_t = xch(phys_fuel);
+  const bool fuel_out = c.fuel_exhaustion && (phys_fuel <= 0.0 || phys_fuel_t <= 0.0);
   const bool te = (alt_o < c.min_alt_m) || (alt_t < c.min_alt_m) || (hp <= 0.0) || (hp_t <= 0.0) ||
-                  !finite;
+                  !finite || fuel_out;
   const bool tr = !te && (t_new >= c.max_time_s - kTimeTol);
   // reward: damage + potential shaping (or altitude hunting) + terminal
   const double s_own = safe_side(k, p, g, t_new);
@@ -474,7 +477,7 @@ __global__ __launch_bounds__(kObsBlock) void advance_kernel(
   exchange(k, p);
   Geo g;
   pair_geo(k, p, g);
-  const AdvOut o = lane_advance(k, p, g, a, e, act, r, c);
+  const AdvOut o = lane_advance(k, p, g, a, e, act, r, c, st[F16S_FUEL * ld + a]);
   reward[a] = o.reward;
   if (!(a & 1)) { term[e] = o.term; trunc[e] = o.trunc; }
 }
@@ -555,7 +558,7 @@ __global__ __launch_bounds__(kRowBlock) void env_post_step_kernel(const F16EnvSt
     make_kin(st + a, ld, O, k);
     exchange(k, p);
     pair_geo(k, p, g);
-    o = lane_advance(k, p, g, a, e, io.actions, r, c);
+    o = lane_advance(k, p, g, a, e, io.actions, r, c, st[F16S_FUEL * ld + a]);
     if (io.reward) io.reward[a] = o.reward;
     if (io.reward_f32) io.reward_f32[a] = (float)o.reward;
     d = o.term || o.trunc;
@@ -605,6 +608,15 @@ __global__ __launch_bounds__(kRowBlock) void env_post_step_kernel(const F16EnvSt
     r.prev_valid[a] = 0; r.prev_x_valid[a] = 0;
     r.dealt[a] = 0.0; r.taken[a] = 0.0; r.hp_loss[a] = 0.0; r.prev_x[a] = 0.0;
     r.prev_alt_log[a] = 0.0;
+    if (io.opp_assign && !odd) {                     // league: draw this engagement's opponent
+      uint32_t ctr[4] = {(uint32_t)e, io.step, 1u, 0x0FF0A55Eu};
+      f16rng::philox4x32_10(ctr, (uint32_t)io.seed, (uint32_t)(io.seed >> 32));
+      const float u = (float)(ctr[0] >> 8) * 0x1p-24f;
+      int kk = io.n_opp - 1;
+      for (int q = io.n_opp - 1; q >= 0; --q)
+        if (io.opp_cdf[q] > u) kk = q;
+      io.opp_assign[e] = kk;
+    }
     for (int i = 0; i < 3; ++i) {
       r.prev_att[i * r.ld + a] = 0.0;
       r.pqr[i * r.ld + a] = 0.0;
@@ -748,6 +760,7 @@ extern "C" int f16_env_post_step(const F16EnvStepIO* io, const F16Recon* rec,
   if (!io->states || !io->actions || !io->obs || !io->ic_pool || io->pool_size < 1 ||
       io->pool_size > 0xffffffffL || io->ld < 2L * rec->nenv || rec->ld != io->ld)
     return F16_EINVAL;
+  if (io->opp_assign && (!io->opp_cdf || io->n_opp < 1)) return F16_EINVAL;
   if (io->obs_dim == 184)
     hipLaunchKernelGGL(env_post_step_kernel<184>, grid_rows(rec->nenv), dim3(kRowBlock), 0,
                        (hipStream_t)stream, *io, *rec, *cfg, origin());

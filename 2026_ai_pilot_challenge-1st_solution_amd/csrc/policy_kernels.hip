@@ -168,9 +168,13 @@ __global__ __launch_bounds__(kThreads, 2) void policy_kernel(const F16PolicyArgs
   const int gi = blockIdx.y;
   if (gi >= p.ngroups) return;
   const F16PolicyGroup G = p.group[gi];
-  const int r0 = G.row_begin + blockIdx.x * kRows;
-  if (r0 >= G.row_end) return;                        // uniform per workgroup
-  const int nr = min(kRows, G.row_end - r0);
+  const int gb = p.group_offsets ? p.group_offsets[gi] : G.row_begin;
+  const int ge = p.group_offsets ? p.group_offsets[gi + 1] : G.row_end;
+  const int r0 = gb + blockIdx.x * kRows;
+  if (r0 >= ge) return;                               // uniform per workgroup
+  const int nr = min(kRows, ge - r0);
+  const float* g_mean = G.mean ? G.mean : p.mean;
+  const float* g_var = G.mean ? G.var : p.var;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const __bf16* wbf = static_cast<const __bf16*>(G.wbf);
   const float* wf = G.wf;
@@ -178,9 +182,9 @@ __global__ __launch_bounds__(kThreads, 2) void policy_kernel(const F16PolicyArgs
 
   // ---- normalise (RunningNorm.normalize, ppo_gpu.py:210-214) and stage bf16 rows in LDS
   if (tid < KP) {
-    const bool on = p.mean && tid < D;
-    col_mean[tid] = on ? p.mean[tid] : 0.0f;
-    col_sd[tid] = on ? sqrtf(p.var[tid] + p.eps) : 1.0f;
+    const bool on = g_mean && tid < D;
+    col_mean[tid] = on ? g_mean[tid] : 0.0f;
+    col_sd[tid] = on ? sqrtf(g_var[tid] + p.eps) : 1.0f;
   }
   __syncthreads();
   {
@@ -205,7 +209,7 @@ __global__ __launch_bounds__(kThreads, 2) void policy_kernel(const F16PolicyArgs
       if (r < kRows) {
         float v0 = x[q].x, v1 = x[q].y;
         if (r < nr) {
-          if (p.mean) {
+          if (g_mean) {
             v0 = (v0 - col_mean[2 * c]) / col_sd[2 * c];
             v1 = (v1 - col_mean[2 * c + 1]) / col_sd[2 * c + 1];
             v0 = v0 < -p.clip ? -p.clip : (v0 > p.clip ? p.clip : v0);
@@ -393,9 +397,79 @@ __global__ void norm_count_kernel(float* __restrict__ count, int nrows) {
 
 static int norm_blocks(int nrows) { return (nrows + kNormRowsPerBlock - 1) / kNormRowsPerBlock; }
 
+// ---- stable counting sort of items by group (one workgroup; per-thread contiguous chunks)
+constexpr int kGroupThreads = 1024;
+constexpr int kGroupWaves = kGroupThreads / 64;
+
+// exclusive prefix of v over the workgroup's threads (in thread order) and the total
+__device__ __forceinline__ int block_exclusive_scan(int v, int* wave_sum, int& total) {
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  int x = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(x, o);
+    if (lane >= o) x += y;
+  }
+  if (lane == 63) wave_sum[w] = x;
+  __syncthreads();
+  int before = 0, all = 0;
+#pragma unroll
+  for (int u = 0; u < kGroupWaves; ++u) {
+    const int sw = wave_sum[u];
+    before += u < w ? sw : 0;
+    all += sw;
+  }
+  __syncthreads();                                   // wave_sum is reused by the next call
+  total = all;
+  return before + x - v;
+}
+
+__global__ __launch_bounds__(kGroupThreads) void group_rows_kernel(
+    const int* __restrict__ assign, int n, int ngroups, int stride, int offset,
+    int* __restrict__ rows, int* __restrict__ offsets) {
+  __shared__ int wave_sum[kGroupWaves];
+  const int t = threadIdx.x;
+  const int chunk = (n + kGroupThreads - 1) / kGroupThreads;
+  const int i0 = min(n, t * chunk), i1 = min(n, i0 + chunk);
+  int c[F16_POLICY_MAX_GROUPS];
+#pragma unroll
+  for (int g = 0; g < F16_POLICY_MAX_GROUPS; ++g) c[g] = 0;
+  for (int i = i0; i < i1; ++i) {
+    const int g = assign[i];
+#pragma unroll
+    for (int q = 0; q < F16_POLICY_MAX_GROUPS; ++q) c[q] += (g == q && q < ngroups) ? 1 : 0;
+  }
+  int pos[F16_POLICY_MAX_GROUPS];
+  int base = 0;
+#pragma unroll
+  for (int g = 0; g < F16_POLICY_MAX_GROUPS; ++g) {
+    if (g >= ngroups) { pos[g] = 0; continue; }        // uniform
+    int total;
+    pos[g] = base + block_exclusive_scan(c[g], wave_sum, total);
+    if (t == 0) offsets[g] = base;
+    base += total;
+  }
+  if (t == 0) offsets[ngroups] = base;
+  for (int i = i0; i < i1; ++i) {
+    const int g = assign[i];
+#pragma unroll
+    for (int q = 0; q < F16_POLICY_MAX_GROUPS; ++q)
+      if (g == q && q < ngroups) rows[pos[q]++] = stride * i + offset;
+  }
+}
+
 }  // namespace f16pol
 
 using namespace f16pol;
+
+extern "C" int f16_group_rows(const int* assign, int n, int ngroups, int stride, int offset,
+                              int* rows, int* group_offsets, void* stream) {
+  if (n < 0 || n > (1 << 24) || ngroups < 1 || ngroups > F16_POLICY_MAX_GROUPS) return F16_EINVAL;
+  if (!group_offsets || (n > 0 && (!assign || !rows))) return F16_EINVAL;
+  hipLaunchKernelGGL(group_rows_kernel, dim3(1), dim3(kGroupThreads), 0, (hipStream_t)stream,
+                     assign, n, ngroups, stride, offset, rows, group_offsets);
+  return f16_last_error();
+}
 
 extern "C" int f16_policy_step(const F16PolicyArgs* a, void* stream) {
   if (!a || !a->obs || a->ngroups < 1 || a->ngroups > F16_POLICY_MAX_GROUPS) return F16_EINVAL;
@@ -406,9 +480,16 @@ extern "C" int f16_policy_step(const F16PolicyArgs* a, void* stream) {
   int max_rows = 0;
   for (int g = 0; g < a->ngroups; ++g) {
     const F16PolicyGroup& G = a->group[g];
-    if (G.row_begin < 0 || G.row_end < G.row_begin || !G.wbf || !G.wf) return F16_EINVAL;
-    if (((uintptr_t)G.wbf & 15) != 0) return F16_EINVAL;
-    max_rows = max(max_rows, G.row_end - G.row_begin);
+    if (!G.wbf || !G.wf || ((uintptr_t)G.wbf & 15) != 0) return F16_EINVAL;
+    if ((G.mean == nullptr) != (G.var == nullptr)) return F16_EINVAL;
+    if (!a->group_offsets) {
+      if (G.row_begin < 0 || G.row_end < G.row_begin) return F16_EINVAL;
+      max_rows = max(max_rows, G.row_end - G.row_begin);
+    }
+  }
+  if (a->group_offsets) {
+    if (a->max_group_rows < 0) return F16_EINVAL;
+    max_rows = a->max_group_rows;
   }
   if (max_rows == 0) return 0;
   const dim3 grid((unsigned)((max_rows + kRows - 1) / kRows), (unsigned)a->ngroups), block(kThreads);

@@ -120,7 +120,7 @@ CONTEST_FUEL_LBS = 3000.0
 
 
 def contest_pair(rng, scenario_b_prob=0.0, alt_ft=None, speed=None, side_swap=None,
-                 scenario_b=None, head_swap=None, dist_ft=None):
+                 scenario_b=None, head_swap=None, dist_ft=None, fuel_range=None):
     """One engagement's (own, target) IC rows from the contest distribution, drawing from the
     numpy Generator in the reference's order (rl_env.py:218-250): altitude, speed, side swap,
     scenario B, then heading swap and 3-9 distance.  Scenario A puts the two aircraft abeam on
@@ -142,13 +142,17 @@ def contest_pair(rng, scenario_b_prob=0.0, alt_ft=None, speed=None, side_swap=No
     d = -alt_ft * FT2M
     la, lo, h = ned_to_geodetic(np.array([own_n, tgt_n]), np.array([CONTEST_CENTER_E] * 2),
                                 np.array([d, d]))
-    return [ic_row(la[0], lo[0], h[0], speed * M2FT, own_hdg, CONTEST_FUEL_LBS),
-            ic_row(la[1], lo[1], h[1], speed * M2FT, tgt_hdg, CONTEST_FUEL_LBS)]
+    # fuel_range (lb): per-aircraft fuel drawn after the reference's draws (league workload with
+    # fuel exhaustion); None keeps the contest's 3000 lb
+    f = (rng.uniform(*fuel_range, size=2) if fuel_range is not None
+         else (CONTEST_FUEL_LBS, CONTEST_FUEL_LBS))
+    return [ic_row(la[0], lo[0], h[0], speed * M2FT, own_hdg, float(f[0])),
+            ic_row(la[1], lo[1], h[1], speed * M2FT, tgt_hdg, float(f[1]))]
 
 
-def contest_rows(rng, npairs, scenario_b_prob=0.0):
+def contest_rows(rng, npairs, scenario_b_prob=0.0, fuel_range=None):
     """(2*npairs, 10) IC rows, plane 0 = ownship, plane 1 = target."""
     rows = []
     for _ in range(npairs):
-        rows += contest_pair(rng, scenario_b_prob)
+        rows += contest_pair(rng, scenario_b_prob, fuel_range=fuel_range)
     return np.asarray(rows, dtype=np.float64).reshape(-1, 10)

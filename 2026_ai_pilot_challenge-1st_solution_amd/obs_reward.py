@@ -42,7 +42,7 @@ def validate_reward_mode(mode, coefficient=5.0):
     return int(mode)
 
 
-def reward_cfg_struct(cfg, min_alt, max_time, mode, alt_hunt_coef):
+def reward_cfg_struct(cfg, min_alt, max_time, mode, alt_hunt_coef, fuel_exhaustion=False):
     c = _lib.F16RewardCfg()
     c.own_damage_weight = float(cfg.get("own_damage_weight", 0.5))
     for key in ("damage_scale", "shaping_reward_scale", "win_reward", "loss_reward",
@@ -51,6 +51,7 @@ def reward_cfg_struct(cfg, min_alt, max_time, mode, alt_hunt_coef):
     c.min_alt_m, c.max_time_s = float(min_alt), float(max_time)
     c.alt_hunt_coef = float(alt_hunt_coef)
     c.mode = int(mode)
+    c.fuel_exhaustion = int(bool(fuel_exhaustion))
     return c
 
 

@@ -176,24 +176,40 @@ class PolicyStep:
 
     def __call__(self, obs, groups, *, norm=None, rows=None, step=0, salt=0, deterministic=False,
                  nobs_out=None, act_idx=None, logp=None, value=None, env_actions=None,
-                 logits_out=None):
+                 logits_out=None, group_offsets=None, max_group_rows=None, nphys=None):
+        """groups: (net, row_begin, row_end) or (net, row_begin, row_end, norm) -- a per-network
+        RunningNorm overrides `norm` for that network.  group_offsets: device int32 (ngroups+1)
+        row boundaries computed on the device (f16_group_rows); then row_begin/row_end are
+        ignored, max_group_rows bounds any group's size and nphys bounds the physical rows.
+        nphys given with a row map skips the (host-synchronising) row-map validation: the caller
+        guarantees 0 <= rows < nphys."""
         if obs.dtype != torch.float32 or obs.dim() != 2 or obs.shape[1] != self.obs_dim:
             raise ValueError(f"obs must be (N, {self.obs_dim}) float32")
         if obs.stride(1) != 1:
             raise ValueError("obs rows must be contiguous")
         if len(groups) > 16:
             raise ValueError("at most 16 networks per launch")
-        nlog = max([int(e) for _, _, e in groups] + [0])
-        if any(int(b) < 0 or int(e) < int(b) for _, b, e in groups):
-            raise ValueError("group row ranges must satisfy 0 <= begin <= end")
+        groups = [tuple(g) + (None,) * (4 - len(g)) for g in groups]
+        if group_offsets is not None:
+            # device-side ranges: the caller bounds them (rows, outputs sized for every row)
+            if rows is None or max_group_rows is None or nphys is None:
+                raise ValueError("group_offsets needs rows, max_group_rows and nphys")
+            if group_offsets.dtype != torch.int32 or group_offsets.numel() < len(groups) + 1:
+                raise ValueError("group_offsets must be int32 with ngroups + 1 entries")
+            nlog = rows.numel()
+        else:
+            nlog = max([int(g[2]) for g in groups] + [0])
+            if any(int(g[1]) < 0 or int(g[2]) < int(g[1]) for g in groups):
+                raise ValueError("group row ranges must satisfy 0 <= begin <= end")
         if rows is not None:
             if rows.dtype != torch.int32 or rows.dim() != 1 or not rows.is_contiguous():
                 raise ValueError("rows must be a contiguous int32 vector")
             if rows.numel() < nlog:
                 raise ValueError("rows shorter than the groups' logical range")
-            nphys = int(rows[:nlog].max().item()) + 1 if nlog else 0
-            if nlog and int(rows[:nlog].min().item()) < 0:
-                raise ValueError("negative physical row")
+            if group_offsets is None and nphys is None:     # validate (host synchronisation)
+                nphys = int(rows[:nlog].max().item()) + 1 if nlog else 0
+                if nlog and int(rows[:nlog].min().item()) < 0:
+                    raise ValueError("negative physical row")
         else:
             nphys = nlog
         if obs.shape[0] < nphys:
@@ -217,16 +233,23 @@ class PolicyStep:
         if norm is not None:
             a.mean, a.var = norm.mean.data_ptr(), norm.var.data_ptr()
             a.clip, a.eps = norm.clip, norm.eps
+        else:
+            per = [g[3] for g in groups if len(g) > 3 and g[3] is not None]
+            a.clip, a.eps = (per[0].clip, per[0].eps) if per else (10.0, 1e-8)
         a.rows = rows.data_ptr() if rows is not None else None
         a.ngroups = len(groups)
         keep = []
-        for i, (net, b, e) in enumerate(groups):
+        for i, (net, b, e, gnorm) in enumerate(groups):
             if net.obs_dim != self.obs_dim:
                 raise ValueError("network obs_dim differs from the step's")
             wbf, wf = net.packed()
             keep.append((wbf, wf))
             a.group[i].wbf, a.group[i].wf = wbf.data_ptr(), wf.data_ptr()
-            a.group[i].row_begin, a.group[i].row_end = int(b), int(e)
+            if gnorm is not None:
+                a.group[i].mean, a.group[i].var = gnorm.mean.data_ptr(), gnorm.var.data_ptr()
+            a.group[i].row_begin, a.group[i].row_end = int(b or 0), int(e or 0)
+        if group_offsets is not None:
+            a.group_offsets, a.max_group_rows = group_offsets.data_ptr(), int(max_group_rows)
         a.seed, a.step, a.salt = self.seed, int(step) & 0xffffffff, int(salt) & 0xffffffff
         a.deterministic = int(bool(deterministic))
         a.grid = self.grid.data_ptr()

@@ -141,3 +141,129 @@ class SelfPlayRollout:
         if self.want_stats:
             stats.update(ret_sum=ret_sum, ep_count=ep_count)
         return adv, ret, stats
+
+
+def zipf_weights(n, s=1.1):
+    """Opponent weights proportional to k^-s, k = 1..n (BASELINE league: Zipf(1.1) over 8)."""
+    w = [float(k) ** -float(s) for k in range(1, int(n) + 1)]
+    tot = sum(w)
+    return [x / tot for x in w]
+
+
+class LeagueRollout:
+    """League-scale collection (BASELINE C5): the learner on plane 0 of every engagement and
+    frozen opponent networks on plane 1, each engagement's opponent drawn from categorical
+    weights (Zipf(1.1) by default) and redrawn when the engagement autoresets -- the
+    ``opp_kind="pool"`` branch of PPOGPUTrainer.collect_rollout (research/competition_36500/
+    runtime/cuda_fdm/ppo_gpu.py:1876-1908, 536-592), with the opponents evaluated as one grouped
+    launch over rows sorted by opponent on the device (no host synchronisation, no per-opponent
+    loop).  Buffers are per engagement (the learner's plane); GAE over (T, nenv).
+
+    Per step: f16_norm_update over the learner's rows, f16_policy_step for the learner,
+    f16_group_rows + one grouped f16_policy_step for all opponents, the FDM decision,
+    f16_env_post_step (rewards, termination incl. optional fuel exhaustion, autoreset and the
+    opponent redraw), and a strided copy of the learner's rewards."""
+
+    def __init__(self, env, net, opponents, T=128, gamma=0.99, lam=0.95, seed=0,
+                 update_norm=True, opp_weights=None, opp_norms=None):
+        from .policy import PolicyStep, RunningNorm
+        if len(opponents) < 1 or len(opponents) > 16:
+            raise ValueError("1..16 opponent networks")
+        self.env, self.net, self.opponents, self.T = env, net, list(opponents), int(T)
+        self.gamma, self.lam, self.update_norm = float(gamma), float(lam), bool(update_norm)
+        D, ne, nac, dev = env.OBS_SIZE, env.nenv, env.nac, env.device
+        self.D, self.nenv, self.nac, self.device = D, ne, nac, dev
+        self.seed = int(seed)
+        self.norm = RunningNorm(D, dev)
+        self.opp_norms = list(opp_norms) if opp_norms is not None else \
+            [RunningNorm(D, dev) for _ in self.opponents]
+        self.policy = PolicyStep(D, dev, seed)
+        w = opp_weights if opp_weights is not None else zipf_weights(len(self.opponents))
+        cdf, acc = [], 0.0
+        for x in w:
+            acc += float(x)
+            cdf.append(acc)
+        cdf = [c / acc for c in cdf]
+        cdf[-1] = 1.0
+        self.opp_weights = [float(x) / acc for x in w]
+        env.opp_cdf = torch.tensor(cdf, dtype=torch.float32, device=dev)
+        env.opp_assign = torch.zeros(ne, dtype=torch.int32, device=dev)
+        self.main_rows = torch.arange(0, nac, 2, dtype=torch.int32, device=dev)
+        self.opp_rows = torch.empty(ne, dtype=torch.int32, device=dev)
+        self.opp_offsets = torch.empty(len(self.opponents) + 1, dtype=torch.int32, device=dev)
+        f32 = torch.float32
+        self.b_obs = torch.empty(self.T, ne, D, dtype=f32, device=dev)
+        self.b_act = torch.empty(self.T, ne, 4, dtype=torch.int64, device=dev)
+        self.b_logp = torch.empty(self.T, ne, dtype=f32, device=dev)
+        self.b_rew = torch.empty(self.T, ne, dtype=f32, device=dev)
+        self.b_val = torch.empty(self.T, ne, dtype=f32, device=dev)
+        self.b_done = torch.empty(self.T, ne, dtype=f32, device=dev)
+        self.rew_all = torch.empty(nac, dtype=f32, device=dev)
+        self.last_val = torch.empty(ne, dtype=f32, device=dev)
+        self.next_obs = None
+        self.next_done = torch.zeros(ne, dtype=f32, device=dev)
+        self.finite_acc = torch.ones(ne, dtype=torch.uint8, device=dev)
+        self.global_step = 0
+        self._lib = _lib.lib()
+        # When set to lists, collect() appends (start, end) events around the policy launches.
+        self.policy_events = None
+        self.opp_events = None
+
+    def reset(self, **kw):
+        """Reset the env and draw every engagement's opponent from the weights (seeded)."""
+        import numpy as np
+        obs = self.env.reset(**kw)
+        rng = np.random.default_rng(self.seed + 7919)
+        ids = rng.choice(len(self.opponents), size=self.nenv, p=np.asarray(self.opp_weights))
+        self.env.opp_assign.copy_(torch.as_tensor(ids, dtype=torch.int32))
+        self.next_obs = obs.reshape(self.nac, self.D)
+        self.next_done.zero_()
+        return obs
+
+    def _timed(self, events, fn):
+        if events is None:
+            return fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        out = fn()
+        e1.record()
+        events.append((e0, e1))
+        return out
+
+    def _opponents(self, obs):
+        rc = self._lib.f16_group_rows(_lib.ptr(self.env.opp_assign), self.nenv,
+                                      len(self.opponents), 2, 1, _lib.ptr(self.opp_rows),
+                                      _lib.ptr(self.opp_offsets), _lib.stream_handle(self.device))
+        _lib.check(rc, "f16_group_rows")
+        groups = [(net, None, None, nrm) for net, nrm in zip(self.opponents, self.opp_norms)]
+        self.policy(obs, groups, rows=self.opp_rows, group_offsets=self.opp_offsets,
+                    max_group_rows=self.nenv, nphys=self.nac, step=self.global_step, salt=1,
+                    env_actions=self.env.sim.actions)
+
+    def collect(self):
+        """One rollout of T steps; returns (adv, ret) as (T, nenv) and a stats dict."""
+        if self.next_obs is None:
+            raise RuntimeError("call reset() first")
+        env, T = self.env, self.T
+        self.finite_acc.fill_(1)
+        self.b_done[0].copy_(self.next_done)
+        for t in range(T):
+            obs = self.next_obs
+            if self.update_norm:
+                self.norm.update(obs, rows=self.main_rows)
+            self._timed(self.policy_events, lambda: self.policy(
+                obs, [(self.net, 0, self.nenv)], norm=self.norm, rows=self.main_rows,
+                nphys=self.nac, step=self.global_step, salt=0, nobs_out=self.b_obs[t],
+                act_idx=self.b_act[t], logp=self.b_logp[t], value=self.b_val[t],
+                env_actions=env.sim.actions))
+            self._timed(self.opp_events, lambda: self._opponents(obs))
+            done_t = self.b_done[t + 1] if t + 1 < T else self.next_done
+            self.next_obs = env.step_rollout(self.rew_all, done_t, self.finite_acc)
+            self.b_rew[t].copy_(self.rew_all[0::2])
+            self.global_step += 1
+        self.policy(self.next_obs, [(self.net, 0, self.nenv)], norm=self.norm,
+                    rows=self.main_rows, nphys=self.nac, step=self.global_step,
+                    value=self.last_val)
+        adv, ret = gae(self.b_rew, self.b_val, self.b_done, self.last_val, self.next_done,
+                       self.gamma, self.lam)
+        return adv, ret, {"trajectory_finite": self.finite_acc.all()}

@@ -28,7 +28,7 @@ class GpuDogfightVecEnv:
     def __init__(self, nenv, substeps=6, precision="fp64", block=128, seed=None, device="cuda",
                  min_altitude_m=304.8, max_engage_time_s=200.0, reward_cfg=None, reward_mode=0,
                  alt_hunt_coef=5.0, scenario="mixed", headon_distance_m=5539.0, fcs_rate=60,
-                 obs_dim=OBS_SIZE, ic_pool_size=4096):
+                 obs_dim=OBS_SIZE, ic_pool_size=4096, fuel_exhaustion=False, fuel_lbs_range=None):
         if precision != "fp64":
             raise ValueError("GpuDogfightVecEnv supports precision='fp64' only")
         if obs_dim not in (OBS_SIZE, OBS_SIZE_EXT):
@@ -52,7 +52,13 @@ class GpuDogfightVecEnv:
         self.reward_cfg = dict(MY_REWARD_CONFIG if reward_cfg is None else reward_cfg)
         self.reward_mode = validate_reward_mode(reward_mode, alt_hunt_coef)
         self.alt_hunt_coef = float(alt_hunt_coef)
+        self.fuel_exhaustion = bool(fuel_exhaustion)
+        self.fuel_lbs_range = None if fuel_lbs_range is None else tuple(map(float, fuel_lbs_range))
         self.OBS_SIZE = int(obs_dim)
+        # league: per-engagement opponent ids redrawn at autoreset from this CDF (set by the
+        # league collector; None otherwise)
+        self.opp_assign = None
+        self.opp_cdf = None
         self.obr = BatchObsReward(nenv, device=device)
         if self.OBS_SIZE == OBS_SIZE_EXT:
             self.obr.enable_external_observations()
@@ -73,7 +79,7 @@ class GpuDogfightVecEnv:
 
     # ---- initial conditions (rl_env.py:218-375) ----
     def _sample_pairs(self, npairs):
-        return icm.contest_rows(self.rng, npairs, self.scenario_b_prob)
+        return icm.contest_rows(self.rng, npairs, self.scenario_b_prob, self.fuel_lbs_range)
 
     def _initialize_physical_seeds(self, rows):
         """(2P, 10) IC rows -> (P, 2, 101) float64 states after the neutral tick."""
@@ -230,6 +236,9 @@ class GpuDogfightVecEnv:
         io.pick = pick.data_ptr() if pick is not None else None
         io.seed, io.step = self.seed, self._post_steps & 0xffffffff
         io.obs_dim, io.obs = self.OBS_SIZE, self._obs.data_ptr()
+        if self.opp_assign is not None:
+            io.opp_assign, io.opp_cdf = self.opp_assign.data_ptr(), self.opp_cdf.data_ptr()
+            io.n_opp = self.opp_cdf.numel()
         return io
 
     def _post(self, io):
@@ -248,11 +257,11 @@ class GpuDogfightVecEnv:
 
     def _cfg_struct(self):
         key = (tuple(sorted(self.reward_cfg.items())), self.min_altitude_m, self.max_engage_time_s,
-               self.reward_mode, self.alt_hunt_coef)
+               self.reward_mode, self.alt_hunt_coef, self.fuel_exhaustion)
         if self._cfg_key != key:
             self._cfg = reward_cfg_struct(self.reward_cfg, self.min_altitude_m,
                                           self.max_engage_time_s, self.reward_mode,
-                                          self.alt_hunt_coef)
+                                          self.alt_hunt_coef, self.fuel_exhaustion)
             self._cfg_key = key
         return self._cfg
 

@@ -180,6 +180,47 @@ def rollout_bench(nenv, T=64, reps=2):
                             "frac": flop / (pol_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS}}
 
 
+def league_bench(nenv=65536, T=128, nopp=8, reps=2):
+    """BASELINE C5: nenv engagements x T-step league rollout with the 214-D observation: the
+    learner (plane 0) and 8 frozen random-init opponents (plane 1, bf16 N(0, 0.02)) assigned per
+    engagement from Zipf(1.1) weights, evaluated as one grouped launch; fuel exhaustion and
+    ground-collision (hard deck) terminations, autoreset with opponent redraw inside the step
+    kernel; GAE over [T, nenv]."""
+    import torch
+    env_mod = importlib.import_module(PKG + ".rl_env")
+    pol = importlib.import_module(PKG + ".policy")
+    ppo = importlib.import_module(PKG + ".ppo")
+    env = env_mod.GpuDogfightVecEnv(nenv, seed=0, obs_dim=214, fuel_exhaustion=True,
+                                    fuel_lbs_range=(100.0, 3000.0))
+    mk = lambda s: pol.MLPActorCritic(214, init="normal", init_std=0.02,
+                                      generator=torch.Generator().manual_seed(s)).to("cuda")
+    net, opps = mk(0), [mk(100 + k) for k in range(nopp)]
+    ro = ppo.LeagueRollout(env, net, opps, T=T, gamma=0.99, lam=0.95, seed=0)
+    ro.reset(stagger=False)
+    ro.collect()
+    torch.cuda.synchronize()
+    ro.policy_events, ro.opp_events, env.kernel_events, env.sim.kernel_events = [], [], [], []
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        adv, ret, stats = ro.collect()
+    e1.record()
+    torch.cuda.synchronize()
+    if not bool(stats["trajectory_finite"]) or not bool(torch.isfinite(adv).all()):
+        raise FloatingPointError("non-finite league rollout")
+    ms = e0.elapsed_time(e1) / reps
+    avg = lambda ev: float(np.mean([a.elapsed_time(b) for a, b in ev]))
+    out = {"workload": "league_rollout_64k_T128_214d_8opp", "engagements": nenv, "T": T,
+           "opponents": nopp, "opponent_weights": "zipf(1.1)", "ms_per_rollout": ms,
+           "transitions_per_s": nenv * T / (ms * 1e-3),
+           "aircraft_transitions_per_s": 2 * nenv * T / (ms * 1e-3),
+           "learner_policy_ms": avg(ro.policy_events), "opponents_policy_ms": avg(ro.opp_events),
+           "fdm_kernel_ms": avg(env.sim.kernel_events), "post_kernel_ms": avg(env.kernel_events),
+           "episodes_done_per_rollout": float(ro.b_done[1:].sum().item() + ro.next_done.sum().item())}
+    ro.policy_events = ro.opp_events = env.kernel_events = env.sim.kernel_events = None
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -190,6 +231,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-rollout", action="store_true")
+    ap.add_argument("--no-league", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run 5 device-to-device copies of MIB MiB (rocprof counter "
                          "calibration: FETCH_SIZE/WRITE_SIZE of a copy of known size)")
@@ -247,6 +289,7 @@ def main():
 
     env_line = env_step_bench(pkg, nenv, args.steps, args.warmup)
     rollout_line = None if args.no_rollout else rollout_bench(nenv)
+    league_line = None if args.no_league else league_bench()
 
     value = nac * S / (ms_step * 1e-3)
     flop_launch = FLOP_PER_SUBSTEP * nac * S
@@ -270,6 +313,7 @@ def main():
         "env_transitions_per_s": env_line["transitions_per_s"],
         "env_step": env_line,
         "rollout": rollout_line,
+        "league": league_line,
         "roofline": {"bound": "valu", "achieved": achieved, "peak": PEAK_FP64_TFLOPS,
                      "unit": "TFLOP/s", "frac": achieved / PEAK_FP64_TFLOPS, "traffic": profiled_traffic(),
                      "kernel": "fdm_step_kernel<120>", "kernel_ms": kern_ms,

@@ -50,6 +50,9 @@ typedef struct F16RewardCfg {
     double timeout_win_reward, timeout_loss_reward, timeout_draw_reward;
     double min_alt_m, max_time_s, alt_hunt_coef;
     int mode;
+    int fuel_exhaustion;         /* 1: an engagement also terminates when either aircraft's
+                                    physical fuel (state field 14) is <= 0 (BASELINE league
+                                    workload; the reference's rule set has no such term) */
 } F16RewardCfg;
 
 /* BatchObsReward.kernel_advance (obs_reward.py:410-441; obs_kernel.cu advance_kernel, and
@@ -97,6 +100,11 @@ typedef struct F16EnvStepIO {
     double *terminal_alt_m;      /* (nac) (|ECI position| - sea-level radius) in metres */
     unsigned char *terminal_finite;  /* (nenv) every state value of both aircraft finite */
     unsigned char *finite_acc;   /* (nenv) cleared to 0 where terminal_finite is 0, else untouched */
+    int *opp_assign;             /* (nenv) opponent id per engagement, redrawn at autoreset as the
+                                    first k with opp_cdf[k] > u, u = (x0 >> 8) 2^-24, x0 = Philox
+                                    word 0 with counter (e, step, 1, 0x0FF0A55E); or NULL */
+    const float *opp_cdf;        /* (n_opp) cumulative opponent weights, last = 1 */
+    int n_opp;
 } F16EnvStepIO;
 
 /* GpuDogfightVecEnv.step after the physics launch (research/competition_36500/runtime/

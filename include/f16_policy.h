@@ -28,7 +28,9 @@ extern "C" {
 typedef struct F16PolicyGroup {
     const void *wbf;        /* bf16 weight blob of this group's network */
     const float *wf;        /* f32 bias/head blob */
-    int row_begin, row_end; /* logical rows [begin, end) evaluated by this network */
+    const float *mean, *var;/* this network's RunningNorm statistics, or NULL for the launch's */
+    int row_begin, row_end; /* logical rows [begin, end) evaluated by this network (ignored when
+                               F16PolicyArgs.group_offsets is set) */
 } F16PolicyGroup;
 
 #define F16_POLICY_MAX_GROUPS 16
@@ -42,6 +44,9 @@ typedef struct F16PolicyArgs {
     const int *rows;        /* logical row -> physical row; NULL = identity */
     int ngroups;            /* networks, each over its own logical row range */
     F16PolicyGroup group[F16_POLICY_MAX_GROUPS];
+    const int *group_offsets;  /* device (ngroups + 1) row offsets: group g evaluates logical rows
+                                  [offsets[g], offsets[g+1]); NULL = the groups' row_begin/end */
+    int max_group_rows;     /* with group_offsets: upper bound of any group's row count */
     unsigned long long seed;/* Philox4x32-10 key */
     unsigned int step;      /* counter word 1 (rollout step) */
     unsigned int salt;      /* counter word 3 (separates independent draws at one step) */
@@ -64,6 +69,14 @@ typedef struct F16PolicyArgs {
  * channel's softmax at u = (x0 >> 8) * 2^-24, x0 the first word of Philox4x32-10 with key `seed`
  * and counter (r, step, c, salt).  kp = round_up(obs_dim, 32) of the packed weights. */
 int f16_policy_step(const F16PolicyArgs *args, void *stream);
+
+/* Stable counting sort of n items by group id (the reference's per-opponent lane partition,
+ * R/cuda_fdm/ppo_gpu.py:536-592, without its host synchronisation): item i with id assign[i] in
+ * [0, ngroups) gets physical row stride*i + offset; rows[] lists the physical rows group by group
+ * in increasing i, group_offsets[0..ngroups] the group boundaries.  Ids outside the range are
+ * dropped (counted nowhere).  One workgroup; n <= 2^24, ngroups <= F16_POLICY_MAX_GROUPS. */
+int f16_group_rows(const int *assign, int n, int ngroups, int stride, int offset, int *rows,
+                   int *group_offsets, void *stream);
 
 /* sizeof(F16PolicyGroup), sizeof(F16PolicyArgs) as compiled into the library (out[0..1]), so
  * that a binding can check its struct layout; no counterpart in the reference. */
