@@ -81,7 +81,8 @@ _SIGNATURES = {
     "f16_policy_step": (_i, [ctypes.POINTER(F16PolicyArgs), _vp]),
     "f16_norm_workspace_bytes": (_l, [_i, _i]),
     "f16_abi_struct_sizes": (_i, [ctypes.POINTER(_l), _i]),
-    "f16_group_rows": (_i, [_vp, _i, _i, _i, _i, _vp, _vp, _vp]),
+    "f16_group_rows": (_i, [_vp, _i, _i, _i, _i, _vp, _vp, _vp, _vp]),
+    "f16_group_workspace_bytes": (_l, [_i]),
     "f16_norm_update": (_i, [_vp, _l, _vp, _i, _i, _vp, _vp, _vp, _vp, _vp]),
 }
 

@@ -424,33 +424,67 @@ __device__ __forceinline__ int block_exclusive_scan(int v, int* wave_sum, int& t
   return before + x - v;
 }
 
-__global__ __launch_bounds__(kGroupThreads) void group_rows_kernel(
-    const int* __restrict__ assign, int n, int ngroups, int stride, int offset,
-    int* __restrict__ rows, int* __restrict__ offsets) {
-  __shared__ int wave_sum[kGroupWaves];
-  const int t = threadIdx.x;
-  const int chunk = (n + kGroupThreads - 1) / kGroupThreads;
-  const int i0 = min(n, t * chunk), i1 = min(n, i0 + chunk);
-  int c[F16_POLICY_MAX_GROUPS];
+// Three passes over blocks of kGroupItems items: (A) per-block group counts, (B) one small
+// scan giving each (block, group) its output base -- groups in order, blocks in order within a
+// group -- and the group offsets, (C) per-block stable scatter.  Deterministic, no atomics.
+constexpr int kGroupItems = 4096;                 // items per block: 4 per thread
+
+__device__ __forceinline__ void block_counts(const int* __restrict__ assign, int n, int ngroups,
+                                             int i0, int (&c)[F16_POLICY_MAX_GROUPS], int& j0,
+                                             int& j1) {
+  constexpr int per = kGroupItems / kGroupThreads;
+  j0 = min(n, i0 + threadIdx.x * per);
+  j1 = min(n, j0 + per);
 #pragma unroll
   for (int g = 0; g < F16_POLICY_MAX_GROUPS; ++g) c[g] = 0;
-  for (int i = i0; i < i1; ++i) {
+  for (int i = j0; i < j1; ++i) {
     const int g = assign[i];
 #pragma unroll
     for (int q = 0; q < F16_POLICY_MAX_GROUPS; ++q) c[q] += (g == q && q < ngroups) ? 1 : 0;
   }
+}
+
+__global__ __launch_bounds__(kGroupThreads) void group_count_kernel(
+    const int* __restrict__ assign, int n, int ngroups, int* __restrict__ counts) {
+  __shared__ int wave_sum[kGroupWaves];
+  int c[F16_POLICY_MAX_GROUPS], j0, j1;
+  block_counts(assign, n, ngroups, blockIdx.x * kGroupItems, c, j0, j1);
+  for (int g = 0; g < ngroups; ++g) {              // uniform
+    int total;
+    block_exclusive_scan(c[g], wave_sum, total);
+    if (threadIdx.x == 0) counts[blockIdx.x * F16_POLICY_MAX_GROUPS + g] = total;
+  }
+}
+
+__global__ void group_base_kernel(int* __restrict__ counts, int nblocks, int ngroups,
+                                  int* __restrict__ offsets) {
+  if (threadIdx.x != 0) return;
+  int s = 0;
+  for (int g = 0; g < ngroups; ++g) {
+    offsets[g] = s;
+    for (int b = 0; b < nblocks; ++b) {            // counts become bases in place
+      const int v = counts[b * F16_POLICY_MAX_GROUPS + g];
+      counts[b * F16_POLICY_MAX_GROUPS + g] = s;
+      s += v;
+    }
+  }
+  offsets[ngroups] = s;
+}
+
+__global__ __launch_bounds__(kGroupThreads) void group_scatter_kernel(
+    const int* __restrict__ assign, int n, int ngroups, int stride, int offset,
+    const int* __restrict__ bases, int* __restrict__ rows) {
+  __shared__ int wave_sum[kGroupWaves];
+  int c[F16_POLICY_MAX_GROUPS], j0, j1;
+  block_counts(assign, n, ngroups, blockIdx.x * kGroupItems, c, j0, j1);
   int pos[F16_POLICY_MAX_GROUPS];
-  int base = 0;
 #pragma unroll
   for (int g = 0; g < F16_POLICY_MAX_GROUPS; ++g) {
-    if (g >= ngroups) { pos[g] = 0; continue; }        // uniform
+    if (g >= ngroups) { pos[g] = 0; continue; }    // uniform
     int total;
-    pos[g] = base + block_exclusive_scan(c[g], wave_sum, total);
-    if (t == 0) offsets[g] = base;
-    base += total;
+    pos[g] = bases[blockIdx.x * F16_POLICY_MAX_GROUPS + g] + block_exclusive_scan(c[g], wave_sum, total);
   }
-  if (t == 0) offsets[ngroups] = base;
-  for (int i = i0; i < i1; ++i) {
+  for (int i = j0; i < j1; ++i) {
     const int g = assign[i];
 #pragma unroll
     for (int q = 0; q < F16_POLICY_MAX_GROUPS; ++q)
@@ -462,12 +496,26 @@ __global__ __launch_bounds__(kGroupThreads) void group_rows_kernel(
 
 using namespace f16pol;
 
+extern "C" long f16_group_workspace_bytes(int n) {
+  if (n < 0) return -1;
+  return (long)((n + kGroupItems - 1) / kGroupItems + 1) * F16_POLICY_MAX_GROUPS * (long)sizeof(int);
+}
+
 extern "C" int f16_group_rows(const int* assign, int n, int ngroups, int stride, int offset,
-                              int* rows, int* group_offsets, void* stream) {
+                              int* rows, int* group_offsets, void* work, void* stream) {
   if (n < 0 || n > (1 << 24) || ngroups < 1 || ngroups > F16_POLICY_MAX_GROUPS) return F16_EINVAL;
-  if (!group_offsets || (n > 0 && (!assign || !rows))) return F16_EINVAL;
-  hipLaunchKernelGGL(group_rows_kernel, dim3(1), dim3(kGroupThreads), 0, (hipStream_t)stream,
-                     assign, n, ngroups, stride, offset, rows, group_offsets);
+  if (!group_offsets || !work || (n > 0 && (!assign || !rows))) return F16_EINVAL;
+  const int nb = (n + kGroupItems - 1) / kGroupItems;
+  int* counts = static_cast<int*>(work);
+  hipStream_t s = (hipStream_t)stream;
+  if (nb > 0)
+    hipLaunchKernelGGL(group_count_kernel, dim3(nb), dim3(kGroupThreads), 0, s, assign, n,
+                       ngroups, counts);
+  hipLaunchKernelGGL(group_base_kernel, dim3(1), dim3(64), 0, s, counts, nb, ngroups,
+                     group_offsets);
+  if (nb > 0)
+    hipLaunchKernelGGL(group_scatter_kernel, dim3(nb), dim3(kGroupThreads), 0, s, assign, n,
+                       ngroups, stride, offset, counts, rows);
   return f16_last_error();
 }
 

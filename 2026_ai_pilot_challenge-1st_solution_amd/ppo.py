@@ -191,6 +191,8 @@ class LeagueRollout:
         self.main_rows = torch.arange(0, nac, 2, dtype=torch.int32, device=dev)
         self.opp_rows = torch.empty(ne, dtype=torch.int32, device=dev)
         self.opp_offsets = torch.empty(len(self.opponents) + 1, dtype=torch.int32, device=dev)
+        self._group_work = torch.empty(max(8, _lib.lib().f16_group_workspace_bytes(ne)),
+                                       dtype=torch.uint8, device=dev)
         f32 = torch.float32
         self.b_obs = torch.empty(self.T, ne, D, dtype=f32, device=dev)
         self.b_act = torch.empty(self.T, ne, 4, dtype=torch.int64, device=dev)
@@ -233,7 +235,8 @@ class LeagueRollout:
     def _opponents(self, obs):
         rc = self._lib.f16_group_rows(_lib.ptr(self.env.opp_assign), self.nenv,
                                       len(self.opponents), 2, 1, _lib.ptr(self.opp_rows),
-                                      _lib.ptr(self.opp_offsets), _lib.stream_handle(self.device))
+                                      _lib.ptr(self.opp_offsets), _lib.ptr(self._group_work),
+                                      _lib.stream_handle(self.device))
         _lib.check(rc, "f16_group_rows")
         groups = [(net, None, None, nrm) for net, nrm in zip(self.opponents, self.opp_norms)]
         self.policy(obs, groups, rows=self.opp_rows, group_offsets=self.opp_offsets,

@@ -74,9 +74,11 @@ int f16_policy_step(const F16PolicyArgs *args, void *stream);
  * R/cuda_fdm/ppo_gpu.py:536-592, without its host synchronisation): item i with id assign[i] in
  * [0, ngroups) gets physical row stride*i + offset; rows[] lists the physical rows group by group
  * in increasing i, group_offsets[0..ngroups] the group boundaries.  Ids outside the range are
- * dropped (counted nowhere).  One workgroup; n <= 2^24, ngroups <= F16_POLICY_MAX_GROUPS. */
+ * dropped (counted nowhere).  n <= 2^24, ngroups <= F16_POLICY_MAX_GROUPS; `work` is device
+ * scratch of f16_group_workspace_bytes(n). */
+long f16_group_workspace_bytes(int n);
 int f16_group_rows(const int *assign, int n, int ngroups, int stride, int offset, int *rows,
-                   int *group_offsets, void *stream);
+                   int *group_offsets, void *work, void *stream);
 
 /* sizeof(F16PolicyGroup), sizeof(F16PolicyArgs) as compiled into the library (out[0..1]), so
  * that a binding can check its struct layout; no counterpart in the reference. */

@@ -29,7 +29,7 @@ def test_zipf_weights():
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("n,ng", [(65536, 8), (1000, 3), (5, 16), (0, 2)])
+@pytest.mark.parametrize("n,ng", [(65536, 8), (70001, 5), (1000, 3), (5, 16), (0, 2)])
 def test_group_rows_is_stable_sort(gpu, n, ng):
     L = import_pkg("_lib")
     rng = np.random.default_rng(n + ng)
@@ -39,8 +39,10 @@ def test_group_rows_is_stable_sort(gpu, n, ng):
     rows = torch.full((max(n, 1),), -1, dtype=torch.int32, device=gpu)
     offs = torch.full((ng + 1,), -1, dtype=torch.int32, device=gpu)
     at = torch.as_tensor(a, device=gpu)
+    work = torch.empty(max(8, L.lib().f16_group_workspace_bytes(n)), dtype=torch.uint8,
+                       device=gpu)
     rc = L.lib().f16_group_rows(L.ptr(at) if n else None, n, ng, 2, 1, L.ptr(rows), L.ptr(offs),
-                                L.stream_handle(gpu))
+                                L.ptr(work), L.stream_handle(gpu))
     L.check(rc, "f16_group_rows")
     valid = a < ng
     order = np.argsort(np.where(valid, a, ng), kind="stable")[:int(valid.sum())]
@@ -74,8 +76,10 @@ def test_grouped_launch_with_device_offsets(gpu, orc):
     assign = torch.as_tensor(rng.integers(0, ng, nenv).astype(np.int32), device=gpu)
     rows = torch.empty(nenv, dtype=torch.int32, device=gpu)
     offs = torch.empty(ng + 1, dtype=torch.int32, device=gpu)
+    work = torch.empty(max(8, L.lib().f16_group_workspace_bytes(nenv)), dtype=torch.uint8,
+                       device=gpu)
     L.check(L.lib().f16_group_rows(L.ptr(assign), nenv, ng, 2, 1, L.ptr(rows), L.ptr(offs),
-                                   L.stream_handle(gpu)), "f16_group_rows")
+                                   L.ptr(work), L.stream_handle(gpu)), "f16_group_rows")
     step = P.PolicyStep(D, device=gpu, seed=9)
     acts = torch.zeros(2 * nenv, 4, dtype=torch.float64, device=gpu)
     lg = torch.empty(nenv, 84, dtype=torch.float32, device=gpu)
