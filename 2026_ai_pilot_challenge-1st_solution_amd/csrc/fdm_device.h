@@ -39,16 +39,18 @@ constexpr double kGearForce = 0.30;                // externally forced gear pos
 
 // ------------------------------------------------------------------ table interpolation
 // Bracket for a 1-D table: value = f * (y[hi] - y[lo]) + y[lo].  Keys at or beyond the ends
-// select the end value exactly (lo = hi, f = 0), as the reference's Table1D does.
+// select the end value exactly (lo = hi, f = 0), as the reference's Table1D does.  The factor
+// is (key - x[r-1]) times the interval's reciprocal width (stored in the image at `riv`), which
+// differs from the reference's division by at most one rounding.
 struct F16Br1 { int lo, hi; double f; };
 // Bracket for one axis of a 2-D table: upper index r in [1, n-1] and the factor clamped to
 // [0, 1] (the reference's Table2D has no end special case, so the clamped factor is kept).
 struct F16Br2 { int r; double f; };
 
-F16_HD F16Br1 f16_br1(const double* T, int off, int n, int r, double key,
-                                          double x0, double xn) {
-  const double xl = T[off + r - 1], xh = T[off + r];
-  double f = (key - xl) / (xh - xl);
+F16_HD F16Br1 f16_br1(const double* T, int off, int riv, int n, int r, double key,
+                      double x0, double xn) {
+  const double xl = T[off + r - 1];
+  double f = (key - xl) * T[riv + r - 1];
   f = (f > 1.0) ? 1.0 : f;
   F16Br1 b;
   const bool lo_end = key <= x0, hi_end = key >= xn;
@@ -58,9 +60,9 @@ F16_HD F16Br1 f16_br1(const double* T, int off, int n, int r, double key,
   return b;
 }
 
-F16_HD F16Br2 f16_br2(const double* T, int off, int r, double key) {
-  const double xl = T[off + r - 1], xh = T[off + r];
-  double f = (key - xl) / (xh - xl);
+F16_HD F16Br2 f16_br2(const double* T, int off, int riv, int r, double key) {
+  const double xl = T[off + r - 1];
+  double f = (key - xl) * T[riv + r - 1];
   f = (f > 1.0) ? 1.0 : ((f < 0.0) ? 0.0 : f);
   F16Br2 b;
   b.r = r;
@@ -83,11 +85,13 @@ F16_HD double f16_lerp2(const double* T, int off, int nc, const F16Br2& br,
 }
 
 #include "f16_grid_gen.inc"
+#include "f16_aero_gen.inc"
 
-#define F16_BR1_(g, key) \
-  f16_br1(T, F16M_##g##_OFF, F16M_##g##_LEN, f16m_upper_##g(key), (key), F16M_##g##_X0, F16M_##g##_XN)
+#define F16_BR1_(g, key)                                                                    \
+  f16_br1(T, F16M_##g##_OFF, F16M_##g##_RIV, F16M_##g##_LEN, f16m_upper_##g(key), (key),        \
+          F16M_##g##_X0, F16M_##g##_XN)
 #define F16_BR1(g, key) F16_BR1_(g, key)
-#define F16_BR2_(g, key) f16_br2(T, F16M_##g##_OFF, f16m_upper_##g(key), (key))
+#define F16_BR2_(g, key) f16_br2(T, F16M_##g##_OFF, F16M_##g##_RIV, f16m_upper_##g(key), (key))
 #define F16_BR2(g, key) F16_BR2_(g, key)
 
 // ------------------------------------------------------------------ small helpers
@@ -113,8 +117,9 @@ F16_HD double kinemat2(double input, double output, double lo, double hi,
   if (dt0 > 0.0 && !near_equal(input, output)) {
     const double rate = (hi - lo) / t;
     const double this_in = clampd(input, lo, hi);
-    const double this_dt = fabs((this_in - output) / rate);
-    if (dt0 < this_dt)
+    // dt0 < |this_in - output| / rate, without the division (a constant product for the
+    // callers' literal arguments)
+    if (dt0 * rate < fabs(this_in - output))
       output = (output < input) ? output + dt0 * rate : output - dt0 * rate;
     else
       output = this_in;
@@ -197,11 +202,7 @@ F16_HD Atmos isa(double h, const double* T) {
   constexpr double lapse[8] = F16M_ATM_LAPSE_INIT;
   constexpr double alts[9] = F16M_ATM_ALT_INIT;
   constexpr double temps[9] = F16M_ATM_TMP_INIT;
-  constexpr double pbrk[9] = F16M_ATM_PBRK_INIT;
   constexpr double dbrk[9] = F16M_ATM_DBRK_INIT;
-  constexpr double tmbp[8] = F16M_ATM_TMB_P_INIT;
-  constexpr double g0Mair = F16M_G0 * F16M_MAIR;
-  constexpr double ng0Mair = -F16M_G0 * F16M_MAIR;
   Atmos o;
   const double gp = (h * kER) / (kER + h);
   if (gp >= 0.0) {
@@ -210,40 +211,28 @@ F16_HD Atmos isa(double h, const double* T) {
   } else {
     o.T = temps[0] + gp * lapse[0];
   }
-  // pressure layer: first b with gp < alt[b+1] (b <= 7)
+  // pressure layer: first b with gp < alt[b+1] (b <= 7).  pow(Tb / (Tb + L dH), g0 M / (R* L))
+  // is exp(e * log(1 + (L / Tb) dH)); an isothermal layer is exp(e * dH).  Both forms are
+  // evaluated with one log and one exp for every lane.
   int b = 0;
 #pragma unroll
   for (int i = 1; i < 8; ++i) b += !(gp < alts[i]);
-  double Lmb = 0.0, Tmb = 0.0, base = 0.0, pb = 0.0;
-#pragma unroll
-  for (int i = 0; i < 8; ++i)
-    if (b == i) { Lmb = lapse[i]; Tmb = tmbp[i]; base = alts[i]; pb = pbrk[i]; }
-  const double dH = gp - base;
-  if (Lmb != 0.0) {
-    const double ex = g0Mair / (F16M_RSTAR * Lmb);
-    o.P = pb * pow(Tmb / (Tmb + Lmb * dH), ex);
-  } else {
-    o.P = pb * exp(ng0Mair * dH / (F16M_RSTAR * Tmb));
-  }
+  const double* lb = T + F16M_ATM_LAYER_OFF + F16M_ATM_LAYER_STRIDE * b;
+  const double dH = gp - lb[0];
+  const double kb = lb[2];
+  const double lg = log(1.0 + kb * dH);
+  o.P = lb[1] * exp(lb[3] * (kb != 0.0 ? lg : dH));
   o.rho = o.P / (F16M_RENG * o.T);
   o.a = sqrt(F16M_GAMMA_R * o.T);
-  o.sigma = o.rho / F16M_RHO_SL;
-  // density altitude: first b with rho >= dbrk[b+1]
+  o.sigma = o.rho * (1.0 / F16M_RHO_SL);
+  // density altitude: first d with rho >= dbrk[d+1]; pow(rho / rb, x) is exp(x log(rho / rb))
   int d = 0;
 #pragma unroll
   for (int i = 1; i < 8; ++i) d += !(o.rho >= dbrk[i]);
-  double dT = 0.0, dHb = 0.0, dL = 0.0, dpb = 1.0;
-#pragma unroll
-  for (int i = 0; i < 8; ++i)
-    if (d == i) { dT = temps[i]; dHb = alts[i]; dL = lapse[i]; dpb = dbrk[i]; }
-  double da;
-  if (dL != 0.0) {
-    const double ex = -1.0 / (1.0 + g0Mair / (F16M_RSTAR * dL));
-    da = dHb + (dT / dL) * (pow(o.rho / dpb, ex) - 1.0);
-  } else {
-    const double fac = -(F16M_RSTAR * dT) / g0Mair;
-    da = dHb + fac * log(o.rho / dpb);
-  }
+  const double* ld = T + F16M_ATM_LAYER_OFF + F16M_ATM_LAYER_STRIDE * d;
+  const double lr = log(o.rho * ld[5]);
+  const double xd = ld[6];
+  const double da = ld[4] + ld[7] * (xd != 0.0 ? exp(xd * lr) - 1.0 : lr);
   o.densalt = (da * kER) / (kER - da);
   return o;
 }
@@ -272,9 +261,10 @@ F16_HD Mass mass_props(double fuel) {
   Mass o;
   const double t = fuel / 2.0;
   const double weight = ew + (t + t) + pw;
+  const double iw = 1.0 / weight;
 #pragma unroll
   for (int i = 0; i < 3; ++i)
-    o.cg[i] = (ew * bcg[i] + pw * pl[i] + t * t0l[i] + t * t1l[i]) / weight;
+    o.cg[i] = (ew * bcg[i] + pw * pl[i] + t * t0l[i] + t * t1l[i]) * iw;
   double mJ[3][3] = {{F16M_IXX, -F16M_IXY, F16M_IXZ},
                      {-F16M_IXY, F16M_IYY, -F16M_IYZ},
                      {F16M_IXZ, -F16M_IYZ, F16M_IZZ}};
@@ -307,11 +297,12 @@ F16_HD double vcal_from_mach(double mach, double p) {
     const double m2 = 1.0 + 0.2 * mach * mach;   // m2^3.5 = m2^3 sqrt(m2)
     pt = p * (m2 * m2 * m2 * sqrt(m2));
   } else {
-    pt = p * 166.92158009316827 * pow(mach, 7.0) / pow(7.0 * mach * mach - 1.0, 2.5);
+    const double m2 = mach * mach, m7 = m2 * m2 * m2 * mach, d = 7.0 * m2 - 1.0;
+    pt = p * 166.92158009316827 * m7 / (d * d * sqrt(d));
   }
   const double qc = pt - p;
-  const double A = qc / 2116.228 + 1.0;          // StdDaySLpressure (jsb_const.py:24)
-  double M = sqrt(5.0 * (pow(A, 1.0 / 3.5) - 1.0));
+  const double A = qc * (1.0 / 2116.228) + 1.0;  // StdDaySLpressure (jsb_const.py:24)
+  double M = sqrt(5.0 * (exp(log(A) * (1.0 / 3.5)) - 1.0));
   if (M > 1.0) {
     for (int i = 0; i < 10; ++i) {
       const double t = 1.0 - 1.0 / (7.0 * M * M);
@@ -327,7 +318,7 @@ F16_HD double vcal_from_mach(double mach, double p) {
 // Frames derived from the ECI state (FDM._kinematics_from_state, jsb_fdm.py:121-140).
 struct Kin {
   double ce, se;              // cos/sin of the Earth position angle
-  double ex, ey, ez, radius, sLat;
+  double ex, ey, ez, radius, irad, sLat;
   double B[3][3];             // Ti2b: rows are the body axes in ECI
   double uvw[3], wpqr[3];     // body velocity w.r.t. the Earth, body rates w.r.t. the Earth
   double vn, ve;              // local north/east ground velocity
@@ -338,10 +329,10 @@ struct Kin {
 // jsb_frames.py:140-163) for the output row; the FCS only needs cos(theta)cos(phi), which is
 // formed from the DCM without the inverse trigonometry.
 F16_HD void kinematics(const double p[3], const double v[3], const double q[4],
-                                           const double wi[3], double epa, bool want_euler,
-                                           Kin& k, double euler[3]) {
-  sincos(epa, &k.se, &k.ce);
-  const double ce = k.ce, se = k.se;
+                       const double wi[3], double ce, double se, bool want_euler, Kin& k,
+                       double euler[3]) {
+  k.ce = ce;
+  k.se = se;
   k.ex = ce * p[0] + se * p[1];
   k.ey = ce * p[1] - se * p[0];
   k.ez = p[2];
@@ -349,8 +340,9 @@ F16_HD void kinematics(const double p[3], const double v[3], const double q[4],
   k.radius = sqrt(rxy2 + k.ez * k.ez);
   const double rxy = sqrt(rxy2);
   double sLon = 0.0, cLon = 1.0, sLat = 0.0, cLat = 1.0;
-  if (rxy != 0.0) { sLon = k.ey / rxy; cLon = k.ex / rxy; }
-  if (k.radius != 0.0) { sLat = k.ez / k.radius; cLat = rxy / k.radius; }
+  if (rxy != 0.0) { const double ir = 1.0 / rxy; sLon = k.ey * ir; cLon = k.ex * ir; }
+  k.irad = 1.0 / k.radius;
+  if (k.radius != 0.0) { sLat = k.ez * k.irad; cLat = rxy * k.irad; }
   k.sLat = sLat;
   // local N, E, D axes in ECI (columns of Tl2i = Tec2i * Tl2ec; Tec2l rows from
   // location_derived, jsb_frames.py:48-51)
@@ -440,7 +432,7 @@ F16_HD void force_path(Aircraft& a, double c_ail, double c_ele, double c_rud,
     double rpid;
     {
       const double ip = a.pid_ip[0];
-      const double dval = (rte - ip) / fdt;
+      const double dval = (rte - ip) * (double)FCS_RATE;   // / fdt
       a.pid_io[0] += 0.00050 * fdt * ((vc < 20.0) ? (1.5 * rte - 0.5 * ip) : 0.0);
       a.pid_ip[0] = rte;
       rpid = 3.00000 * rte + a.pid_io[0] + -0.00125 * dval;
@@ -462,7 +454,7 @@ F16_HD void force_path(Aircraft& a, double c_ail, double c_ele, double c_rud,
     double gpid;
     {
       const double ip = a.pid_ip[1];
-      const double dval = (pte - ip) / fdt;
+      const double dval = (pte - ip) * (double)FCS_RATE;
       a.pid_io[1] += 0.0250 * fdt * ((vc < 5.0) ? (1.5 * pte - 0.5 * ip) : 0.0);
       a.pid_ip[1] = pte;
       gpid = clampd(0.3000 * pte + a.pid_io[1] + 0.0000 * dval, -1.0, 1.0);
@@ -479,7 +471,7 @@ F16_HD void force_path(Aircraft& a, double c_ail, double c_ele, double c_rud,
     double ypid;
     {
       const double ip = a.pid_ip[2];
-      const double dval = (yte - ip) / fdt;
+      const double dval = (yte - ip) * (double)FCS_RATE;
       a.pid_io[2] += 0.000010 * fdt * ((vc < 10.0) ? (1.5 * yte - 0.5 * ip) : 0.0);
       a.pid_ip[2] = yte;
       ypid = clampd(0.105500 * yte + a.pid_io[2] + 0.00005 * dval, -1.0, 1.0);
@@ -500,14 +492,15 @@ F16_HD void force_path(Aircraft& a, double c_ail, double c_ele, double c_rud,
   const double vt = sqrt(vt2);
   double alpha = 0.0, beta = 0.0, ca = 1.0, sa = 0.0, cb = 1.0, sb = 0.0;
   if (vt > 0.001) {
-    const double suw = sqrt(muw);
+    const double suw = sqrt(muw), ivt = 1.0 / vt;
     beta = atan2(v, suw);
-    cb = suw / vt;
-    sb = v / vt;
+    cb = suw * ivt;
+    sb = v * ivt;
     if (muw >= 1e-6) {
+      const double isuw = 1.0 / suw;
       alpha = atan2(w, u);
-      ca = u / suw;
-      sa = w / suw;
+      ca = u * isuw;
+      sa = w * isuw;
     }
   }
   const double qbar = 0.5 * at.rho * vt2;
@@ -521,8 +514,8 @@ F16_HD void force_path(Aircraft& a, double c_ail, double c_ele, double c_rud,
     const double c2x = wq[1] * eye[2] - wq[2] * eye[1], c2y = wq[2] * eye[0] - wq[0] * eye[2];
     const double c2z = wq[0] * eye[1] - wq[1] * eye[0];
     const double c3y = wq[2] * c2x - wq[0] * c2z, c3z = wq[0] * c2y - wq[1] * c2x;
-    o.npy = (a.pba[1] + c1y + c3y) / F16M_SLGRAVITY;
-    o.npz = (a.pba[2] + c1z + c3z) / F16M_SLGRAVITY;
+    o.npy = (a.pba[1] + c1y + c3y) * (1.0 / F16M_SLGRAVITY);
+    o.npz = (a.pba[2] + c1z + c3z) * (1.0 / F16M_SLGRAVITY);
   }
   o.vc_kts = (fabs(mach) > 0.0) ? vcal_from_mach(mach, at.P) * F16M_FPSTOKTS : 0.0;
   o.vg = sqrt(k.vn * k.vn + k.ve * k.ve);
@@ -540,10 +533,11 @@ F16_HD void force_path(Aircraft& a, double c_ail, double c_ele, double c_rud,
     const double nx = a.n2n + 0.1;
     const double om = 1.0 - (nx < 1.0 ? nx : 1.0);
     const double den = 1.0 + 3.0 * (om * om * om) + (1.0 - at.sigma);
-    const double up = d_up / den, n2dn = d_n2dn / den, n1dn = d_n1dn / den;
+    const double iden = 1.0 / den;
+    const double up = d_up * iden, n2dn = d_n2dn * iden, n1dn = d_n1dn * iden;
     a.n2 = seek(a.n2, F16M_ENG_IDLEN2 + thr * (F16M_ENG_MAXN2 - F16M_ENG_IDLEN2), up, n2dn);
     a.n1 = seek(a.n1, F16M_ENG_IDLEN1 + thr * (F16M_ENG_MAXN1 - F16M_ENG_IDLEN1), up, n1dn);
-    a.n2n = (a.n2 - F16M_ENG_IDLEN2) / (F16M_ENG_MAXN2 - F16M_ENG_IDLEN2);
+    a.n2n = (a.n2 - F16M_ENG_IDLEN2) * (1.0 / (F16M_ENG_MAXN2 - F16M_ENG_IDLEN2));
     const F16Br2 bm = F16_BR2(F16M_TG_ENG_IDLE_R, mach);
     const F16Br2 bd = F16_BR2(F16M_TG_ENG_IDLE_C, at.densalt);
     const F16Br2 bm2 = F16_BR2(F16M_TG_ENG_MIL_R, mach);
@@ -551,7 +545,7 @@ F16_HD void force_path(Aircraft& a, double c_ail, double c_ele, double c_rud,
     const double mil = (F16M_ENG_MILTHRUST - idle) * f16_lerp2(T, F16M_T_ENG_MIL_OFF, F16M_T_ENG_MIL_NC, bm2, bd);
     thrust = idle + mil * a.n2n * a.n2n;
     const double on = 1.0 - a.n2n;
-    const double tsfc = F16M_ENG_TSFC * sqrt(at.T / 389.7) * (0.84 + on * on);
+    const double tsfc = F16M_ENG_TSFC * sqrt(at.T * (1.0 / 389.7)) * (0.84 + on * on);
     a.ff = seek(a.ff, thrust * tsfc, 1000.0, 10000.0);
     a.ff = a.ff < F16M_IDLEFF ? F16M_IDLEFF : a.ff;
     if (aug > 0.0) {   // afterburner, AugMethod 2
@@ -560,20 +554,25 @@ F16_HD void force_path(Aircraft& a, double c_ail, double c_ele, double c_rud,
       thrust += tdiff * aug;
       a.ff = seek(a.ff, thrust * F16M_ENG_ATSFC, 5000.0, 10000.0);
     }
-    o.fuel_burn = a.ff / 3600.0 * kDt;
+    o.fuel_burn = a.ff * (kDt / 3600.0);
   }
 
   // ---- aerodynamics (jsb_aero.py:75-107): 40 coefficient functions ----
   double ax_drag, ax_side, ax_lift, ax_roll, ax_pitch, ax_yaw;
   {
     const double twovel = 2.0 * vt;
-    const double bi2vel = twovel != 0.0 ? F16M_BW / twovel : 0.0;
-    const double ci2vel = twovel != 0.0 ? F16M_CBAR / twovel : 0.0;
+    const double i2v = twovel != 0.0 ? 1.0 / twovel : 0.0;
+    const double bi2vel = F16M_BW * i2v, ci2vel = F16M_CBAR * i2v;
     constexpr double kclge = 1.0;   // kCLge(765 ft): beyond the table's last breakpoint (1.1 -> 1.0)
     const double p = k.wpqr[0], q = k.wpqr[1], r = k.wpqr[2];
     const double ail = ail_rad, elev = elev_rad, rud = rud_rad, lef = lef_rad, flap = flap_rad;
-    constexpr double sb = 0.0;      // speedbrake position is never driven
-#include "f16_aero_gen.inc"
+    F16_AERO_BRACKETS;
+    ax_drag = F16_AERO_DRAG_FREE + F16_AERO_DRAG_CTL;
+    ax_side = F16_AERO_SIDE_FREE + F16_AERO_SIDE_CTL;
+    ax_lift = F16_AERO_LIFT_FREE + F16_AERO_LIFT_CTL;
+    ax_roll = F16_AERO_ROLL_FREE + F16_AERO_ROLL_CTL;
+    ax_pitch = F16_AERO_PITCH_FREE + F16_AERO_PITCH_CTL;
+    ax_yaw = F16_AERO_YAW_FREE + F16_AERO_YAW_CTL;
   }
   // wind -> body forces, moments about the CG, then the engine's thrust at the structural origin
   double F[3], M[3];
@@ -595,11 +594,11 @@ F16_HD void force_path(Aircraft& a, double c_ail, double c_ele, double c_rud,
   // ---- J2 gravity (jsb_frames.py:69-80), then accelerations (jsb_accel.py:10-31) ----
   double gi[3];
   {
-    const double adivr = kSemiMajor / k.radius;
+    const double adivr = kSemiMajor * k.irad;
     const double pc = 1.5 * kJ2 * adivr * adivr;
     const double s2 = k.sLat * k.sLat;   // sin(geocentric latitude) = z / r
     const double kxy = 1.0 + pc * (1.0 - 5.0 * s2), kz = 1.0 + pc * (3.0 - 5.0 * s2);
-    const double g = -(kGM / (k.radius * k.radius)) / k.radius;
+    const double g = -(kGM * k.irad * k.irad) * k.irad;
     const double gx = g * (kxy * k.ex), gy = g * (kxy * k.ey), gz = g * (kz * k.ez);
     gi[0] = k.ce * gx - k.se * gy;   // Tec2i * g_ecef
     gi[1] = k.se * gx + k.ce * gy;
@@ -661,9 +660,13 @@ F16_HD void substep(Aircraft& a, double c_ail, double c_ele, double c_rud,
     a.ah1[i] = a.ai[i];
   }
   a.epa += kRot * kDt;
+  // sin/cos of the Earth position angle: evaluated every step (a rotation recurrence would
+  // bias cos by one rounding per step, which the altitude-dependent terms amplify)
+  double ce, se;
+  sincos(a.epa, &se, &ce);
 
   Kin k;
-  kinematics(a.p, a.v, a.q, a.wi, a.epa, want_euler, k, out.euler);
+  kinematics(a.p, a.v, a.q, a.wi, ce, se, want_euler, k, out.euler);
   {   // quaternion derivative for the next step (quat_qdot, jsb_frames.py:170-176)
     const double p = a.wi[0], qq = a.wi[1], r = a.wi[2];
     const double q0 = a.q[0], q1 = a.q[1], q2 = a.q[2], q3 = a.q[3];

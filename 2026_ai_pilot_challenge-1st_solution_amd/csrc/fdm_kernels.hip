@@ -154,7 +154,7 @@ __global__ __launch_bounds__(kBlock) void seed_kernel(const double* __restrict__
   s.k_tef = s.k_ail = s.k_ele = s.k_lef = 0.0;
   Kin k;
   double eul[3];
-  kinematics(s.p, s.v, s.q, s.wi, 0.0, false, k, eul);
+  kinematics(s.p, s.v, s.q, s.wi, 1.0, 0.0, false, k, eul);
   ForceOut f;
   force_path<FCS_RATE>(s, 0.0, 0.0, 0.0, 0.8, k, T, f);   // throwaway FCS/engine (reset below)
   double qd[4];

@@ -304,6 +304,36 @@ def main():
             rec = add_table("AERO_" + short, f["table"]) if f["table"] else None
             terms.append((ai, short, f, rec))
     assert len(terms) == 40, len(terms)
+    # Reciprocal interval widths, one vector per grid, after every table body (the offsets
+    # above are unchanged): a bracket factor is (key - x[i]) * riv[i] instead of a division by
+    # x[i+1] - x[i].  The widths are differenced in IEEE double exactly as the kernel would.
+    riv_off = {}
+    for key, (name, _, _) in img.grids.items():
+        riv_off[name] = img.body([1.0 / (b - a) for a, b in zip(key, key[1:])])
+    # ISA layer constants, 8 per layer, so the atmosphere reads its layer's numbers with one
+    # indexed load each (jsb_atmos.py:52-111 written as exp/log):
+    #   pressure layer b:  [0] base altitude, [1] base pressure, [2] lapse / base temperature,
+    #                      [3] exponent (-g0 M / (R* lapse), or -g0 M / (R* T) when isothermal);
+    #                      P = pb * exp(e * log(1 + k dH)), or pb * exp(e * dH);
+    #   density layer d:   [4] base altitude, [5] 1 / base density, [6] density exponent
+    #                      (-1 / (1 + g0 M / (R* lapse)), 0 when isothermal), [7] T / lapse
+    #                      (or -R* T / (g0 M)); da = base + c (exp(x log(rho/rb)) - 1), or
+    #                      base + c log(rho/rb).
+    atm = dict(dc0["arrays"])
+    sca = dict(dc0["scalars"])
+    g0m = sca["F16M_G0"] * sca["F16M_MAIR"]
+    rst = sca["F16M_RSTAR"]
+    layer = []
+    for i in range(8):
+        lap, tmb, tmp = atm["F16M_ATM_LAPSE"][i], atm["F16M_ATM_TMB_P"][i], atm["F16M_ATM_TMP"][i]
+        iso = lap == 0.0
+        layer += [atm["F16M_ATM_ALT"][i], atm["F16M_ATM_PBRK"][i],
+                  0.0 if iso else lap / tmb,
+                  -(g0m / (rst * tmb)) if iso else -(g0m / (rst * lap)),
+                  atm["F16M_ATM_ALT"][i], 1.0 / atm["F16M_ATM_DBRK"][i],
+                  0.0 if iso else -1.0 / (1.0 + g0m / (rst * lap)),
+                  -(rst * tmp) / g0m if iso else tmp / lap]
+    atm_layer_off = img.body(layer)
 
     # ------------------------------------------------------------------ header
     out = []
@@ -330,6 +360,7 @@ def main():
     for key, (name, off, ln) in img.grids.items():
         w(f"#define F16M_{name}_OFF {off}")
         w(f"#define F16M_{name}_LEN {ln}")
+        w(f"#define F16M_{name}_RIV {riv_off[name]}")
     w("")
     w("/* ---- tables: body offset, grids ---- */")
     for tname, rec in tables:
@@ -343,6 +374,8 @@ def main():
             w(f"#define F16M_T_{tname}_CG {rec['cg'][1]}")
             w(f"#define F16M_T_{tname}_NC {rec['cg'][2]}")
     w("")
+    w(f"#define F16M_ATM_LAYER_OFF {atm_layer_off}")
+    w("#define F16M_ATM_LAYER_STRIDE 8")
     w(f"#define F16M_IMAGE_LEN {len(img.vals)}")
     w("#define F16M_IMAGE_INIT { \\")
     for i in range(0, len(img.vals), 6):
@@ -416,26 +449,43 @@ def main():
     with open(os.path.join(args.out_dir, "f16_grid_gen.inc"), "w") as fh:
         fh.write("\n".join(g) + "\n")
 
+    # The speedbrake is never driven (its position is identically +0), so the four terms with
+    # that factor are exactly +-0 for every finite state and are omitted.  Every axis is split
+    # into the terms that involve no control-surface position, as a factor or as a table
+    # variable ("free": they need only the flow state), and the terms that do ("ctl"); each part is a left-to-right sum from 0 in XML
+    # order, and the axis is free + ctl.  Callers can evaluate the parts at different times
+    # (the free part before the FCS has run) and get the same bits.
+    CTL = {"fcs/aileron-pos-rad", "fcs/elevator-pos-rad", "fcs/rudder-pos-rad",
+           "fcs/lef-pos-rad", "fcs/flaperon-mix-rad"}
+    SB = "fcs/speedbrake-pos-rad"
     d = []
     dw = d.append
     dw("// f16_aero_gen.inc -- GENERATED by gen_f16_model.py; do not edit.")
-    dw("// Body of the 40-function F-16 aero build-up.  Expects in scope: `const double* T` (the")
-    dw("// model image, usually in LDS), the inputs qbar alpha beta bi2vel ci2vel mach kclge p q r")
-    dw("// ail elev rud lef flap sb gear, and the helpers f16_br1/f16_br2/f16_lerp1/f16_lerp2.")
-    dw("// Writes ax_drag ax_side ax_lift ax_roll ax_pitch ax_yaw.")
+    dw("// The 40-function F-16 aero build-up as expression macros over names in scope: `T` (the")
+    dw("// model image), qbar alpha beta bi2vel ci2vel mach kclge p q r ail elev rud lef flap gear,")
+    dw("// and the brackets F16_AERO_BRACKETS declares (b1_<grid>, b2_<grid>).")
+    dw("// F16_AERO_<AXIS>_FREE sums the terms without a control-surface factor, F16_AERO_<AXIS>_CTL")
+    dw("// the terms with one; each is a left-to-right sum from 0 in XML order; axis = FREE + CTL.")
+    dw("// Terms with the speedbrake factor (identically 0) are omitted.")
+    brk = []
     for gr, var in sorted(used1.items(), key=lambda kv: kv[0][1]):
-        dw(f"const F16Br1 b1_{gr[0]} = F16_BR1({gr[0]}, {var_expr[var]});")
+        brk.append(f"const F16Br1 b1_{gr[0]} = F16_BR1({gr[0]}, {var_expr[var]})")
     for gr, var in sorted(used2.items(), key=lambda kv: kv[0][1]):
-        dw(f"const F16Br2 b2_{gr[0]} = F16_BR2({gr[0]}, {var_expr[var]});")
-    axvar = {a: "ax_" + a.lower() for a in AXES}
+        brk.append(f"const F16Br2 b2_{gr[0]} = F16_BR2({gr[0]}, {var_expr[var]})")
+    dw("#define F16_AERO_BRACKETS \\")
+    for i, b in enumerate(brk):
+        dw(f"  {b}" + ("; \\" if i + 1 < len(brk) else ""))
     for ai, ax in enumerate(AXES):
-        dw(f"{{ double s = 0.0;")
+        parts_of = {"FREE": [], "CTL": []}
         for aj, short, f, rec in terms:
             if aj != ai:
                 continue
+            if SB in f["factors"]:
+                dw(f"// {ax.lower()}: {short} omitted (speedbrake factor)")
+                continue
             parts = []
-            for p in f["factors"]:
-                parts.append(fnum(const_of[p]) if p in const_of else var_expr[p])
+            for pp in f["factors"]:
+                parts.append(fnum(const_of[pp]) if pp in const_of else var_expr[pp])
             if f["value"] is not None:
                 parts.append(fnum(f["value"]))
             if rec is not None:
@@ -444,8 +494,18 @@ def main():
                 else:
                     parts.append(f"f16_lerp2(T, F16M_T_AERO_{short}_OFF, F16M_T_AERO_{short}_NC, "
                                  f"b2_{rec['rg'][0]}, b2_{rec['cg'][0]})")
-            dw(f"  s += {' * '.join(parts)};  // {short}")
-        dw(f"  {axvar[ax]} = s; }}")
+            uses = set(f["factors"])
+            if rec is not None:
+                uses |= {rec["row_var"], rec.get("col_var")}
+            kind = "CTL" if CTL & uses else "FREE"
+            parts_of[kind].append((short, " * ".join(parts)))
+        for kind in ("FREE", "CTL"):
+            lst = parts_of[kind]
+            dw(f"#define F16_AERO_{ax}_{kind} ( \\")
+            dw("  0.0 \\")
+            for short, expr in lst:
+                dw(f"  + {expr} /* {short} */ \\")
+            dw("  )")
     with open(os.path.join(args.out_dir, "f16_aero_gen.inc"), "w") as fh:
         fh.write("\n".join(d) + "\n")
     print(f"image {len(img.vals)} doubles, {len(img.grids)} grids, {len(tables)} tables")

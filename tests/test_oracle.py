@@ -186,6 +186,54 @@ def test_isa_troposphere_textbook(orc):
     assert abs(a["densalt"] - h) < 1e-5
 
 
+def test_image_reciprocal_widths(orc):
+    """Every breakpoint grid carries 1 / (x[i+1] - x[i]) per interval (the kernels' bracket
+    factor multiplies by it instead of dividing)."""
+    img = image(orc)
+    hd = header_defines()
+    grids = [k[:-4] for k in hd if re.match(r"F16M_G\d+_\w+_OFF$", k)]
+    assert len(grids) == 20
+    for g in grids:
+        off, n, riv = hd[g + "_OFF"], hd[g + "_LEN"], hd[g + "_RIV"]
+        x = img[off:off + n]
+        assert np.all(np.diff(x) > 0), g
+        assert list(img[riv:riv + n - 1]) == [1.0 / (b - a) for a, b in zip(x, x[1:])], g
+
+
+def test_image_isa_layer_constants(orc):
+    """The per-layer atmosphere constants, used the way the kernels use them (pressure as
+    exp(e log(1 + k dH)) or exp(e dH); density altitude as base + c (exp(x log(rho / rb)) - 1)
+    or base + c log(rho / rb)), reproduce the oracle's pressure and density altitude over the
+    whole table, and the standard day's density altitude is the altitude itself."""
+    img = image(orc)
+    hd = header_defines()
+    L0, K = hd["F16M_ATM_LAYER_OFF"], hd["F16M_ATM_LAYER_STRIDE"]
+    lay = img[L0:L0 + 8 * K].reshape(8, K)
+    hdr = open(IMG_HDR).read()
+
+    def harr(name):
+        m = re.search(r"#define " + name + r"_INIT \{([^}]*)\}", hdr)
+        return [float(v) for v in m.group(1).split(",")]
+    alts, dbrk = harr("F16M_ATM_ALT"), harr("F16M_ATM_DBRK")
+    ER = hd["F16M_EARTH_RADIUS_ISA"]
+    for h in np.concatenate([np.linspace(-2000.0, 280000.0, 2001), [0.0, 36089.0, 65617.0]]):
+        a = orc.atmos(h)
+        gp = (h * ER) / (ER + h)
+        b = sum(not (gp < alts[i]) for i in range(1, 8))
+        base, pb, k, e = lay[b, :4]
+        dH = gp - base
+        P = pb * math.exp(e * (math.log(1.0 + k * dH) if k != 0.0 else dH))
+        assert abs(P / a["P"] - 1) < 1e-13, h
+        d = sum(not (a["rho"] >= dbrk[i]) for i in range(1, 8))
+        dbase, irb, x, c = lay[d, 4:]
+        lr = math.log(a["rho"] * irb)
+        da = dbase + c * (math.exp(x * lr) - 1.0 if x != 0.0 else lr)
+        da = (da * ER) / (ER - da)
+        assert abs(da - a["densalt"]) < 1e-8 * max(1.0, abs(h)), h
+        if 0.0 <= h <= 250000.0:
+            assert abs(da - h) < 1e-6 * max(1.0, abs(h)), h
+
+
 # ------------------------------------------------------------------ mass balance
 def test_mass_closed_forms(orc):
     for fuel in (0.0, 3000.0, 6000.0, 6972.0):
