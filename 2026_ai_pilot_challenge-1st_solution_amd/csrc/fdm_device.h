@@ -399,246 +399,252 @@ F16_HD void kinematics(const double p[3], const double v[3], const double q[4],
   }
 }
 
-// ------------------------------------------------------------------ force path
+// ------------------------------------------------------------------ force path components
 // FDM._force_path (jsb_fdm.py:76-119): atmosphere -> mass -> FCS (previous-frame auxiliary
-// values, current attitude) -> auxiliary -> engine -> aero -> gravity -> accelerations.
-// Reads and updates the FCS and engine state in `a`; writes the new derivatives to `d`.
-struct ForceOut {
-  double ai[3], wdi[3], pba[3], ppq[3];   // vUVWidot, vPQRidot, vBodyAccel, vPQRi
-  double alpha, beta, vt, mach, vc_kts, vg, npy, npz;
-  double fuel_burn, alt, k_rud;
-};
+// values, current attitude) -> auxiliary -> engine -> aero -> gravity -> accelerations.  Each
+// stage is a function of exactly what it reads, so the same arithmetic can run as one sequence
+// (force_path) or spread over cooperating wavefronts (fdm_split.h) with identical results.
 
+// ---- FCS (jsb_fcs.py:143-268) ----
+struct FcsOut { double ail, elev, rud, lef, flap, k_rud; };
+// Gear kinematic from its forced seed 0.30 toward command 0: one rate-limited step.
 template <int FCS_RATE>
-F16_HD void force_path(Aircraft& a, double c_ail, double c_ele, double c_rud,
-                                           double c_thr, const Kin& k,
-                                           const double* __restrict__ T, ForceOut& o) {
+constexpr double kGearPos = kGearForce - (1.0 / (double)FCS_RATE) * ((1.0 - 0.0) / 5.0);
+
+// Every channel that reads only previous-frame values: trailing-edge flap, roll loop, flaperon
+// mix, yaw loop and rudder kinematic, leading-edge flap, and the pitch schedule (elevator
+// command times the alpha schedule), which it returns.  Updates the FCS state in `a`.
+template <int FCS_RATE>
+F16_HD double fcs_prev_frame(Aircraft& a, double c_ail, double c_ele, double c_rud,
+                             const double* __restrict__ T, FcsOut& o) {
   constexpr double fdt = 1.0 / (double)FCS_RATE;
-  const double alt = k.radius - kSemiMajor;
-  const Atmos at = isa(alt, T);
-  const Mass mb = mass_props(a.fuel);
-
-  // ---- FCS (jsb_fcs.py:143-268) ----
   const double pa_alpha = a.pa[0], pa_mach = a.pa[1], vc = a.pa[2], vg = a.pa[3];
-  double ail_rad, elev_rad, rud_rad, lef_rad, flap_rad;
-  // gear kinematic from its forced seed 0.30 toward command 0: one rate-limited step
-  constexpr double gear = kGearForce - fdt * ((1.0 - 0.0) / 5.0);
+  const double tef_rad = (vc < 250.0) ? 0.349 : ((pa_mach > 0.9) ? -0.0349 : 0.0);
+  const double tef = kinemat_tef(2.864789 * tef_rad, a.k_tef, fdt);
+  a.k_tef = tef;
+  // roll: PID (3, 5e-4, -1.25e-3), integrating only when its trigger is 0 (vc < 20 kt)
+  const double rte = c_ail - 0.31821 * a.pa[6];
+  double rpid;
   {
-    const double tef_rad = (vc < 250.0) ? 0.349 : ((pa_mach > 0.9) ? -0.0349 : 0.0);
-    const double tef = kinemat_tef(2.864789 * tef_rad, a.k_tef, fdt);
-    a.k_tef = tef;
-    // roll: PID (3, 5e-4, -1.25e-3), integrating only when its trigger is 0 (vc < 20 kt)
-    const double rte = c_ail - 0.31821 * a.pa[6];
-    double rpid;
-    {
-      const double ip = a.pid_ip[0];
-      const double dval = (rte - ip) * (double)FCS_RATE;   // / fdt
-      a.pid_io[0] += 0.00050 * fdt * ((vc < 20.0) ? (1.5 * rte - 0.5 * ip) : 0.0);
-      a.pid_ip[0] = rte;
-      rpid = 3.00000 * rte + a.pid_io[0] + -0.00125 * dval;
-    }
-    const double rrc = clampd(rpid + c_ail, -1.0, 1.0);
-    ail_rad = surface_scale(rrc, -1.0, 1.0, -0.375, 0.375);
-    const double lapn = kinemat2(rrc, a.k_ail, -1.0, 1.0, 0.3, fdt);
-    a.k_ail = lapn;
-    const F16Br1 bm = F16_BR1(F16M_TG_FCS_AIL_SPEED_R, pa_mach);
-    const double asc = f16_lerp1(T, F16M_T_FCS_AIL_SPEED_OFF, bm) * lapn;
-    const double lf = clampd(-tef - asc, -1.0, 1.0), rf = clampd(tef - asc, -1.0, 1.0);
-    flap_rad = 1.4324 * (lf + rf);
-    // pitch: g-load PID (0.3, 0.025, 0) clipped to +-1, trigger 0 below 5 kt
-    const double gcorr = a.pa[5] - k.ctcp;
-    const double ecl = clampd(c_ele + 0.0, -1.0, 0.44);
-    const F16Br1 ba = F16_BR1(F16M_TG_FCS_ELEV_SCHED_R, pa_alpha);
-    const double esch = f16_lerp1(T, F16M_T_FCS_ELEV_SCHED_OFF, ba) * ecl;
-    const double pte = esch + 6.2 * a.pa[7] - 0.020 * gcorr;
-    double gpid;
-    {
-      const double ip = a.pid_ip[1];
-      const double dval = (pte - ip) * (double)FCS_RATE;
-      a.pid_io[1] += 0.0250 * fdt * ((vc < 5.0) ? (1.5 * pte - 0.5 * ip) : 0.0);
-      a.pid_ip[1] = pte;
-      gpid = clampd(0.3000 * pte + a.pid_io[1] + 0.0000 * dval, -1.0, 1.0);
-    }
-    const double psch = clampd(esch + 1.0472 * pa_alpha + gpid, -1.0, 1.0);
-    const double epn = kinemat2(psch, a.k_ele, -1.0, 1.0, 0.3, fdt);
-    a.k_ele = epn;
-    elev_rad = surface_scale(epn, -1.0, 1.0, -0.436, 0.436);
-    // yaw: PID (0.1055, 1e-5, 5e-5) clipped to +-1, trigger 0 below 10 kt; its output seeds
-    // the rudder kinematic
-    const F16Br1 bv = F16_BR1(F16M_TG_FCS_YAW_RATE_R, vg);
-    const double yrn = f16_lerp1(T, F16M_T_FCS_YAW_RATE_OFF, bv) * a.pa[8];
-    const double yte = c_rud + yrn + 0.25 * a.pa[4];
-    double ypid;
-    {
-      const double ip = a.pid_ip[2];
-      const double dval = (yte - ip) * (double)FCS_RATE;
-      a.pid_io[2] += 0.000010 * fdt * ((vc < 10.0) ? (1.5 * yte - 0.5 * ip) : 0.0);
-      a.pid_ip[2] = yte;
-      ypid = clampd(0.105500 * yte + a.pid_io[2] + 0.00005 * dval, -1.0, 1.0);
-    }
-    const double ysch = clampd(c_rud + 0.0 + ypid, -1.0, 1.0);
-    const double rpn = kinemat2(ysch, ypid, -1.0, 1.0, 0.4, fdt);
-    o.k_rud = rpn;
-    rud_rad = surface_scale(rpn, -1.0, 1.0, -0.524, 0.524);
-    // leading-edge flap switch: the gear is never at 0 and weight-on-wheels is never set
-    lef_rad = (pa_alpha > 0.0873) ? 0.262 : ((pa_mach > 0.9) ? -0.0349 : 0.0);
-    a.k_lef = kinemat2(2.293578 * lef_rad, a.k_lef, -1.0, 1.0, 3.0, fdt);
+    const double ip = a.pid_ip[0];
+    const double dval = (rte - ip) * (double)FCS_RATE;   // / fdt
+    a.pid_io[0] += 0.00050 * fdt * ((vc < 20.0) ? (1.5 * rte - 0.5 * ip) : 0.0);
+    a.pid_ip[0] = rte;
+    rpid = 3.00000 * rte + a.pid_io[0] + -0.00125 * dval;
   }
+  const double rrc = clampd(rpid + c_ail, -1.0, 1.0);
+  o.ail = surface_scale(rrc, -1.0, 1.0, -0.375, 0.375);
+  const double lapn = kinemat2(rrc, a.k_ail, -1.0, 1.0, 0.3, fdt);
+  a.k_ail = lapn;
+  const F16Br1 bm = F16_BR1(F16M_TG_FCS_AIL_SPEED_R, pa_mach);
+  const double asc = f16_lerp1(T, F16M_T_FCS_AIL_SPEED_OFF, bm) * lapn;
+  const double lf = clampd(-tef - asc, -1.0, 1.0), rf = clampd(tef - asc, -1.0, 1.0);
+  o.flap = 1.4324 * (lf + rf);
+  // pitch schedule
+  const double ecl = clampd(c_ele + 0.0, -1.0, 0.44);
+  const F16Br1 ba = F16_BR1(F16M_TG_FCS_ELEV_SCHED_R, pa_alpha);
+  const double esch = f16_lerp1(T, F16M_T_FCS_ELEV_SCHED_OFF, ba) * ecl;
+  // yaw: PID (0.1055, 1e-5, 5e-5) clipped to +-1, trigger 0 below 10 kt; its output seeds
+  // the rudder kinematic
+  const F16Br1 bv = F16_BR1(F16M_TG_FCS_YAW_RATE_R, vg);
+  const double yrn = f16_lerp1(T, F16M_T_FCS_YAW_RATE_OFF, bv) * a.pa[8];
+  const double yte = c_rud + yrn + 0.25 * a.pa[4];
+  double ypid;
+  {
+    const double ip = a.pid_ip[2];
+    const double dval = (yte - ip) * (double)FCS_RATE;
+    a.pid_io[2] += 0.000010 * fdt * ((vc < 10.0) ? (1.5 * yte - 0.5 * ip) : 0.0);
+    a.pid_ip[2] = yte;
+    ypid = clampd(0.105500 * yte + a.pid_io[2] + 0.00005 * dval, -1.0, 1.0);
+  }
+  const double ysch = clampd(c_rud + 0.0 + ypid, -1.0, 1.0);
+  const double rpn = kinemat2(ysch, ypid, -1.0, 1.0, 0.4, fdt);
+  o.k_rud = rpn;
+  o.rud = surface_scale(rpn, -1.0, 1.0, -0.524, 0.524);
+  // leading-edge flap switch: the gear is never at 0 and weight-on-wheels is never set
+  o.lef = (pa_alpha > 0.0873) ? 0.262 : ((pa_mach > 0.9) ? -0.0349 : 0.0);
+  a.k_lef = kinemat2(2.293578 * o.lef, a.k_lef, -1.0, 1.0, 3.0, fdt);
+  return esch;
+}
 
-  // ---- auxiliary (jsb_auxiliary.py:45-73) ----
-  const double u = k.uvw[0], v = k.uvw[1], w = k.uvw[2];
+// The pitch loop: g-load PID (0.3, 0.025, 0) clipped to +-1, trigger 0 below 5 kt, on the
+// schedule plus the current attitude's gravity correction (cos(theta) cos(phi)).
+template <int FCS_RATE>
+F16_HD void fcs_pitch(Aircraft& a, double esch, double ctcp, FcsOut& o) {
+  constexpr double fdt = 1.0 / (double)FCS_RATE;
+  const double vc = a.pa[2];
+  const double gcorr = a.pa[5] - ctcp;
+  const double pte = esch + 6.2 * a.pa[7] - 0.020 * gcorr;
+  double gpid;
+  {
+    const double ip = a.pid_ip[1];
+    const double dval = (pte - ip) * (double)FCS_RATE;
+    a.pid_io[1] += 0.0250 * fdt * ((vc < 5.0) ? (1.5 * pte - 0.5 * ip) : 0.0);
+    a.pid_ip[1] = pte;
+    gpid = clampd(0.3000 * pte + a.pid_io[1] + 0.0000 * dval, -1.0, 1.0);
+  }
+  const double psch = clampd(esch + 1.0472 * a.pa[0] + gpid, -1.0, 1.0);
+  const double epn = kinemat2(psch, a.k_ele, -1.0, 1.0, 0.3, fdt);
+  a.k_ele = epn;
+  o.elev = surface_scale(epn, -1.0, 1.0, -0.436, 0.436);
+}
+
+// ---- auxiliary (jsb_auxiliary.py:45-73) ----
+struct AuxGeo { double vt2, vt, alpha, beta, ca, sa, cb, sb; };
+
+F16_HD AuxGeo aux_geometry(const double uvw[3]) {
+  AuxGeo g;
+  const double u = uvw[0], v = uvw[1], w = uvw[2];
   const double muw = u * u + w * w;
-  const double vt2 = muw + v * v;
-  const double vt = sqrt(vt2);
-  double alpha = 0.0, beta = 0.0, ca = 1.0, sa = 0.0, cb = 1.0, sb = 0.0;
-  if (vt > 0.001) {
-    const double suw = sqrt(muw), ivt = 1.0 / vt;
-    beta = atan2(v, suw);
-    cb = suw * ivt;
-    sb = v * ivt;
+  g.vt2 = muw + v * v;
+  g.vt = sqrt(g.vt2);
+  g.alpha = 0.0; g.beta = 0.0; g.ca = 1.0; g.sa = 0.0; g.cb = 1.0; g.sb = 0.0;
+  if (g.vt > 0.001) {
+    const double suw = sqrt(muw), ivt = 1.0 / g.vt;
+    g.beta = atan2(v, suw);
+    g.cb = suw * ivt;
+    g.sb = v * ivt;
     if (muw >= 1e-6) {
       const double isuw = 1.0 / suw;
-      alpha = atan2(w, u);
-      ca = u * isuw;
-      sa = w * isuw;
+      g.alpha = atan2(w, u);
+      g.ca = u * isuw;
+      g.sa = w * isuw;
     }
   }
-  const double qbar = 0.5 * at.rho * vt2;
-  const double mach = vt / at.a;
-  {
-    const double eye[3] = {kInToFt * (mb.cg[0] - F16M_EYEPOINT_X), kInToFt * (F16M_EYEPOINT_Y - mb.cg[1]),
-                           kInToFt * (mb.cg[2] - F16M_EYEPOINT_Z)};
-    const double* wd = a.ppd;
-    const double* wq = a.ppq;
-    const double c1y = wd[2] * eye[0] - wd[0] * eye[2], c1z = wd[0] * eye[1] - wd[1] * eye[0];
-    const double c2x = wq[1] * eye[2] - wq[2] * eye[1], c2y = wq[2] * eye[0] - wq[0] * eye[2];
-    const double c2z = wq[0] * eye[1] - wq[1] * eye[0];
-    const double c3y = wq[2] * c2x - wq[0] * c2z, c3z = wq[0] * c2y - wq[1] * c2x;
-    o.npy = (a.pba[1] + c1y + c3y) * (1.0 / F16M_SLGRAVITY);
-    o.npz = (a.pba[2] + c1z + c3z) * (1.0 / F16M_SLGRAVITY);
-  }
-  o.vc_kts = (fabs(mach) > 0.0) ? vcal_from_mach(mach, at.P) * F16M_FPSTOKTS : 0.0;
-  o.vg = sqrt(k.vn * k.vn + k.ve * k.ve);
-  o.alpha = alpha; o.beta = beta; o.vt = vt; o.mach = mach; o.alt = alt;
+  return g;
+}
 
-  // ---- engine (jsb_propulsion.py:89-128); throttle position = 2 * throttle command ----
-  double thrust;
-  {
-    double thr = 2.0 * c_thr, aug = 0.0;
-    if (thr > 1.0) { aug = thr - 1.0; thr -= aug; }
-    // spool-time constants as the reference forms them: k * 90 / (bypass + 3)
-    constexpr double d_up = 1.0 * 90.0 / (F16M_ENG_BYPASSRATIO + 3.0);
-    constexpr double d_n2dn = 3.0 * 90.0 / (F16M_ENG_BYPASSRATIO + 3.0);
-    constexpr double d_n1dn = 2.4 * 90.0 / (F16M_ENG_BYPASSRATIO + 3.0);
-    const double nx = a.n2n + 0.1;
-    const double om = 1.0 - (nx < 1.0 ? nx : 1.0);
-    const double den = 1.0 + 3.0 * (om * om * om) + (1.0 - at.sigma);
-    const double iden = 1.0 / den;
-    const double up = d_up * iden, n2dn = d_n2dn * iden, n1dn = d_n1dn * iden;
-    a.n2 = seek(a.n2, F16M_ENG_IDLEN2 + thr * (F16M_ENG_MAXN2 - F16M_ENG_IDLEN2), up, n2dn);
-    a.n1 = seek(a.n1, F16M_ENG_IDLEN1 + thr * (F16M_ENG_MAXN1 - F16M_ENG_IDLEN1), up, n1dn);
-    a.n2n = (a.n2 - F16M_ENG_IDLEN2) * (1.0 / (F16M_ENG_MAXN2 - F16M_ENG_IDLEN2));
-    const F16Br2 bm = F16_BR2(F16M_TG_ENG_IDLE_R, mach);
-    const F16Br2 bd = F16_BR2(F16M_TG_ENG_IDLE_C, at.densalt);
-    const F16Br2 bm2 = F16_BR2(F16M_TG_ENG_MIL_R, mach);
-    const double idle = F16M_ENG_MILTHRUST * f16_lerp2(T, F16M_T_ENG_IDLE_OFF, F16M_T_ENG_IDLE_NC, bm, bd);
-    const double mil = (F16M_ENG_MILTHRUST - idle) * f16_lerp2(T, F16M_T_ENG_MIL_OFF, F16M_T_ENG_MIL_NC, bm2, bd);
-    thrust = idle + mil * a.n2n * a.n2n;
-    const double on = 1.0 - a.n2n;
-    const double tsfc = F16M_ENG_TSFC * sqrt(at.T * (1.0 / 389.7)) * (0.84 + on * on);
-    a.ff = seek(a.ff, thrust * tsfc, 1000.0, 10000.0);
-    a.ff = a.ff < F16M_IDLEFF ? F16M_IDLEFF : a.ff;
-    if (aug > 0.0) {   // afterburner, AugMethod 2
-      const F16Br2 bm3 = F16_BR2(F16M_TG_ENG_AUG_R, mach);
-      const double tdiff = F16M_ENG_MAXTHRUST * f16_lerp2(T, F16M_T_ENG_AUG_OFF, F16M_T_ENG_AUG_NC, bm3, bd) - thrust;
-      thrust += tdiff * aug;
-      a.ff = seek(a.ff, thrust * F16M_ENG_ATSFC, 5000.0, 10000.0);
-    }
-    o.fuel_burn = a.ff * (kDt / 3600.0);
-  }
+// Pilot-station load factors from the previous frame's body acceleration, angular
+// acceleration and rates, about the current CG.
+F16_HD void load_factors(const Aircraft& a, const double cg[3], double& npy, double& npz) {
+  const double eye[3] = {kInToFt * (cg[0] - F16M_EYEPOINT_X), kInToFt * (F16M_EYEPOINT_Y - cg[1]),
+                         kInToFt * (cg[2] - F16M_EYEPOINT_Z)};
+  const double* wd = a.ppd;
+  const double* wq = a.ppq;
+  const double c1y = wd[2] * eye[0] - wd[0] * eye[2], c1z = wd[0] * eye[1] - wd[1] * eye[0];
+  const double c2x = wq[1] * eye[2] - wq[2] * eye[1], c2y = wq[2] * eye[0] - wq[0] * eye[2];
+  const double c2z = wq[0] * eye[1] - wq[1] * eye[0];
+  const double c3y = wq[2] * c2x - wq[0] * c2z, c3z = wq[0] * c2y - wq[1] * c2x;
+  npy = (a.pba[1] + c1y + c3y) * (1.0 / F16M_SLGRAVITY);
+  npz = (a.pba[2] + c1z + c3z) * (1.0 / F16M_SLGRAVITY);
+}
 
-  // ---- aerodynamics (jsb_aero.py:75-107): 40 coefficient functions ----
-  double ax_drag, ax_side, ax_lift, ax_roll, ax_pitch, ax_yaw;
-  {
-    const double twovel = 2.0 * vt;
-    const double i2v = twovel != 0.0 ? 1.0 / twovel : 0.0;
-    const double bi2vel = F16M_BW * i2v, ci2vel = F16M_CBAR * i2v;
-    constexpr double kclge = 1.0;   // kCLge(765 ft): beyond the table's last breakpoint (1.1 -> 1.0)
-    const double p = k.wpqr[0], q = k.wpqr[1], r = k.wpqr[2];
-    const double ail = ail_rad, elev = elev_rad, rud = rud_rad, lef = lef_rad, flap = flap_rad;
-    F16_AERO_BRACKETS;
-    ax_drag = F16_AERO_DRAG_FREE + F16_AERO_DRAG_CTL;
-    ax_side = F16_AERO_SIDE_FREE + F16_AERO_SIDE_CTL;
-    ax_lift = F16_AERO_LIFT_FREE + F16_AERO_LIFT_CTL;
-    ax_roll = F16_AERO_ROLL_FREE + F16_AERO_ROLL_CTL;
-    ax_pitch = F16_AERO_PITCH_FREE + F16_AERO_PITCH_CTL;
-    ax_yaw = F16_AERO_YAW_FREE + F16_AERO_YAW_CTL;
-  }
-  // wind -> body forces, moments about the CG, then the engine's thrust at the structural origin
-  double F[3], M[3];
-  {
-    const double drag = -ax_drag, side = ax_side, lift = -ax_lift;
-    F[0] = ca * cb * drag + (-ca * sb) * side + (-sa) * lift;
-    F[1] = sb * drag + cb * side;
-    F[2] = sa * cb * drag + (-sa * sb) * side + ca * lift;
-    const double rx = mb.rp[0], ry = mb.rp[1], rz = mb.rp[2];
-    M[0] = ax_roll + (ry * F[2] - rz * F[1]);
-    M[1] = ax_pitch + (rz * F[0] - rx * F[2]);
-    M[2] = ax_yaw + (rx * F[1] - ry * F[0]);
-    const double mz = kInToFt * (mb.cg[2] - 0.0), my = kInToFt * (0.0 - mb.cg[1]);
-    F[0] = F[0] + thrust;
-    M[1] = M[1] + mz * thrust;
-    M[2] = M[2] + (-my) * thrust;
-  }
+F16_HD double vc_knots(double mach, double P) {
+  return (fabs(mach) > 0.0) ? vcal_from_mach(mach, P) * F16M_FPSTOKTS : 0.0;
+}
 
-  // ---- J2 gravity (jsb_frames.py:69-80), then accelerations (jsb_accel.py:10-31) ----
-  double gi[3];
-  {
-    const double adivr = kSemiMajor * k.irad;
-    const double pc = 1.5 * kJ2 * adivr * adivr;
-    const double s2 = k.sLat * k.sLat;   // sin(geocentric latitude) = z / r
-    const double kxy = 1.0 + pc * (1.0 - 5.0 * s2), kz = 1.0 + pc * (3.0 - 5.0 * s2);
-    const double g = -(kGM * k.irad * k.irad) * k.irad;
-    const double gx = g * (kxy * k.ex), gy = g * (kxy * k.ey), gz = g * (kz * k.ez);
-    gi[0] = k.ce * gx - k.se * gy;   // Tec2i * g_ecef
-    gi[1] = k.se * gx + k.ce * gy;
-    gi[2] = gz;
+// ---- engine (jsb_propulsion.py:89-128); throttle position = 2 * throttle command ----
+// Updates the spool and fuel-flow state in `a`; returns the thrust, and the fuel burnt this
+// step in `burn`.
+F16_HD double engine(Aircraft& a, double c_thr, const Atmos& at, double mach,
+                     const double* __restrict__ T, double& burn) {
+  double thr = 2.0 * c_thr, aug = 0.0;
+  if (thr > 1.0) { aug = thr - 1.0; thr -= aug; }
+  // spool-time constants as the reference forms them: k * 90 / (bypass + 3)
+  constexpr double d_up = 1.0 * 90.0 / (F16M_ENG_BYPASSRATIO + 3.0);
+  constexpr double d_n2dn = 3.0 * 90.0 / (F16M_ENG_BYPASSRATIO + 3.0);
+  constexpr double d_n1dn = 2.4 * 90.0 / (F16M_ENG_BYPASSRATIO + 3.0);
+  const double nx = a.n2n + 0.1;
+  const double om = 1.0 - (nx < 1.0 ? nx : 1.0);
+  const double den = 1.0 + 3.0 * (om * om * om) + (1.0 - at.sigma);
+  const double iden = 1.0 / den;
+  const double up = d_up * iden, n2dn = d_n2dn * iden, n1dn = d_n1dn * iden;
+  a.n2 = seek(a.n2, F16M_ENG_IDLEN2 + thr * (F16M_ENG_MAXN2 - F16M_ENG_IDLEN2), up, n2dn);
+  a.n1 = seek(a.n1, F16M_ENG_IDLEN1 + thr * (F16M_ENG_MAXN1 - F16M_ENG_IDLEN1), up, n1dn);
+  a.n2n = (a.n2 - F16M_ENG_IDLEN2) * (1.0 / (F16M_ENG_MAXN2 - F16M_ENG_IDLEN2));
+  const F16Br2 bm = F16_BR2(F16M_TG_ENG_IDLE_R, mach);
+  const F16Br2 bd = F16_BR2(F16M_TG_ENG_IDLE_C, at.densalt);
+  const F16Br2 bm2 = F16_BR2(F16M_TG_ENG_MIL_R, mach);
+  const double idle = F16M_ENG_MILTHRUST * f16_lerp2(T, F16M_T_ENG_IDLE_OFF, F16M_T_ENG_IDLE_NC, bm, bd);
+  const double mil = (F16M_ENG_MILTHRUST - idle) * f16_lerp2(T, F16M_T_ENG_MIL_OFF, F16M_T_ENG_MIL_NC, bm2, bd);
+  double thrust = idle + mil * a.n2n * a.n2n;
+  const double on = 1.0 - a.n2n;
+  const double tsfc = F16M_ENG_TSFC * sqrt(at.T * (1.0 / 389.7)) * (0.84 + on * on);
+  a.ff = seek(a.ff, thrust * tsfc, 1000.0, 10000.0);
+  a.ff = a.ff < F16M_IDLEFF ? F16M_IDLEFF : a.ff;
+  if (aug > 0.0) {   // afterburner, AugMethod 2
+    const F16Br2 bm3 = F16_BR2(F16M_TG_ENG_AUG_R, mach);
+    const double tdiff = F16M_ENG_MAXTHRUST * f16_lerp2(T, F16M_T_ENG_AUG_OFF, F16M_T_ENG_AUG_NC, bm3, bd) - thrust;
+    thrust += tdiff * aug;
+    a.ff = seek(a.ff, thrust * F16M_ENG_ATSFC, 5000.0, 10000.0);
   }
-  {
-    double wq[3];   // vPQRi re-formed from vPQR, as the reference's accelerations do
+  burn = a.ff * (kDt / 3600.0);
+  return thrust;
+}
+
+// ---- aerodynamics (jsb_aero.py:75-107): 40 coefficient functions ----
+F16_HD void aero_rates(double vt, double& bi2vel, double& ci2vel) {
+  const double twovel = 2.0 * vt;
+  const double i2v = twovel != 0.0 ? 1.0 / twovel : 0.0;
+  bi2vel = F16M_BW * i2v;
+  ci2vel = F16M_CBAR * i2v;
+}
+constexpr double kCLge = 1.0;   // kCLge(765 ft): beyond the table's last breakpoint (1.1 -> 1.0)
+
+// Wind-axis aero forces to body forces, moments about the CG, then the engine's thrust at the
+// structural origin.
+F16_HD void forces_moments(const double ax[6], const AuxGeo& g, const Mass& mb, double thrust,
+                           double F[3], double M[3]) {
+  const double ca = g.ca, sa = g.sa, cb = g.cb, sb = g.sb;
+  const double drag = -ax[0], side = ax[1], lift = -ax[2];
+  F[0] = ca * cb * drag + (-ca * sb) * side + (-sa) * lift;
+  F[1] = sb * drag + cb * side;
+  F[2] = sa * cb * drag + (-sa * sb) * side + ca * lift;
+  const double rx = mb.rp[0], ry = mb.rp[1], rz = mb.rp[2];
+  M[0] = ax[3] + (ry * F[2] - rz * F[1]);
+  M[1] = ax[4] + (rz * F[0] - rx * F[2]);
+  M[2] = ax[5] + (rx * F[1] - ry * F[0]);
+  const double mz = kInToFt * (mb.cg[2] - 0.0), my = kInToFt * (0.0 - mb.cg[1]);
+  F[0] = F[0] + thrust;
+  M[1] = M[1] + mz * thrust;
+  M[2] = M[2] + (-my) * thrust;
+}
+
+// ---- J2 gravity (jsb_frames.py:69-80) ----
+F16_HD void gravity(const Kin& k, double gi[3]) {
+  const double adivr = kSemiMajor * k.irad;
+  const double pc = 1.5 * kJ2 * adivr * adivr;
+  const double s2 = k.sLat * k.sLat;   // sin(geocentric latitude) = z / r
+  const double kxy = 1.0 + pc * (1.0 - 5.0 * s2), kz = 1.0 + pc * (3.0 - 5.0 * s2);
+  const double g = -(kGM * k.irad * k.irad) * k.irad;
+  const double gx = g * (kxy * k.ex), gy = g * (kxy * k.ey), gz = g * (kz * k.ez);
+  gi[0] = k.ce * gx - k.se * gy;   // Tec2i * g_ecef
+  gi[1] = k.se * gx + k.ce * gy;
+  gi[2] = gz;
+}
+
+// ---- accelerations (jsb_accel.py:10-31) ----
+struct Accel { double ai[3], wdi[3], pba[3], ppq[3]; };   // vUVWidot, vPQRidot, vBodyAccel, vPQRi
+
+F16_HD void accelerations(const Kin& k, const Mass& mb, const double F[3], const double M[3],
+                          const double gi[3], Accel& o) {
+  double wq[3];   // vPQRi re-formed from vPQR, as the reference's accelerations do
 #pragma unroll
-    for (int i = 0; i < 3; ++i) wq[i] = k.wpqr[i] + k.B[i][2] * kRot;
-    const double* J = mb.J;
-    const double Jw0 = J[0] * wq[0] + J[3] * wq[1] + J[4] * wq[2];
-    const double Jw1 = J[3] * wq[0] + J[1] * wq[1] + J[5] * wq[2];
-    const double Jw2 = J[4] * wq[0] + J[5] * wq[1] + J[2] * wq[2];
-    const double m0 = M[0] - (wq[1] * Jw2 - wq[2] * Jw1);
-    const double m1 = M[1] - (wq[2] * Jw0 - wq[0] * Jw2);
-    const double m2 = M[2] - (wq[0] * Jw1 - wq[1] * Jw0);
-    const double* Ji = mb.Jinv;
-    o.wdi[0] = Ji[0] * m0 + Ji[3] * m1 + Ji[4] * m2;
-    o.wdi[1] = Ji[3] * m0 + Ji[1] * m1 + Ji[5] * m2;
-    o.wdi[2] = Ji[4] * m0 + Ji[5] * m1 + Ji[2] * m2;
-    const double sm = 1.0 / mb.mass;
+  for (int i = 0; i < 3; ++i) wq[i] = k.wpqr[i] + k.B[i][2] * kRot;
+  const double* J = mb.J;
+  const double Jw0 = J[0] * wq[0] + J[3] * wq[1] + J[4] * wq[2];
+  const double Jw1 = J[3] * wq[0] + J[1] * wq[1] + J[5] * wq[2];
+  const double Jw2 = J[4] * wq[0] + J[5] * wq[1] + J[2] * wq[2];
+  const double m0 = M[0] - (wq[1] * Jw2 - wq[2] * Jw1);
+  const double m1 = M[1] - (wq[2] * Jw0 - wq[0] * Jw2);
+  const double m2 = M[2] - (wq[0] * Jw1 - wq[1] * Jw0);
+  const double* Ji = mb.Jinv;
+  o.wdi[0] = Ji[0] * m0 + Ji[3] * m1 + Ji[4] * m2;
+  o.wdi[1] = Ji[3] * m0 + Ji[1] * m1 + Ji[5] * m2;
+  o.wdi[2] = Ji[4] * m0 + Ji[5] * m1 + Ji[2] * m2;
+  const double sm = 1.0 / mb.mass;
 #pragma unroll
-    for (int i = 0; i < 3; ++i) o.pba[i] = F[i] * sm;
+  for (int i = 0; i < 3; ++i) o.pba[i] = F[i] * sm;
 #pragma unroll
-    for (int i = 0; i < 3; ++i) {
-      o.ai[i] = (k.B[0][i] * o.pba[0] + k.B[1][i] * o.pba[1] + k.B[2][i] * o.pba[2]) + gi[i];
-      o.ppq[i] = wq[i];
-    }
+  for (int i = 0; i < 3; ++i) {
+    o.ai[i] = (k.B[0][i] * o.pba[0] + k.B[1][i] * o.pba[1] + k.B[2][i] * o.pba[2]) + gi[i];
+    o.ppq[i] = wq[i];
   }
 }
 
-// ------------------------------------------------------------------ one integration step
-// FDM.step (jsb_fdm.py:212-244).  FCS_RATE: the FCS components' dt is 1/FCS_RATE s (120 for
-// cuda_fdm/ref/jsb_fcs.py:19, 60 for the 184-D runtime's copy of that file).
-template <int FCS_RATE>
-F16_HD void substep(Aircraft& a, double c_ail, double c_ele, double c_rud,
-                                        double c_thr, const double* __restrict__ T,
-                                        bool want_euler, SubstepOut& out) {
-  // ---- propagate: quaternion rect-Euler + normalize, vPQRi rect-Euler, ECI position AB3 on the
-  // velocity history, ECI velocity AB2 on the acceleration history ----
+// ---- propagate: quaternion rect-Euler + normalize, vPQRi rect-Euler, ECI position AB3 on the
+// velocity history, ECI velocity AB2 on the acceleration history, Earth position angle ----
+F16_HD void propagate(Aircraft& a) {
   {
     double q0 = a.q[0] + kDt * a.qd[0], q1 = a.q[1] + kDt * a.qd[1];
     double q2 = a.q[2] + kDt * a.qd[2], q3 = a.q[3] + kDt * a.qd[3];
@@ -660,21 +666,92 @@ F16_HD void substep(Aircraft& a, double c_ail, double c_ele, double c_rud,
     a.ah1[i] = a.ai[i];
   }
   a.epa += kRot * kDt;
-  // sin/cos of the Earth position angle: evaluated every step (a rotation recurrence would
-  // bias cos by one rounding per step, which the altitude-dependent terms amplify)
+}
+
+// Quaternion derivative for the next step (quat_qdot, jsb_frames.py:170-176).
+F16_HD void quat_rate(Aircraft& a) {
+  const double p = a.wi[0], qq = a.wi[1], r = a.wi[2];
+  const double q0 = a.q[0], q1 = a.q[1], q2 = a.q[2], q3 = a.q[3];
+  a.qd[0] = -0.5 * (q1 * p + q2 * qq + q3 * r);
+  a.qd[1] = 0.5 * (q0 * p - q3 * qq + q2 * r);
+  a.qd[2] = 0.5 * (q3 * p + q0 * qq - q1 * r);
+  a.qd[3] = 0.5 * (-q2 * p + q1 * qq + q0 * r);
+}
+
+// Frames at the propagated state; sin/cos of the Earth position angle are evaluated every step
+// (a rotation recurrence would bias cos by one rounding per step, which the altitude-dependent
+// terms amplify).
+F16_HD void frames(const Aircraft& a, bool want_euler, Kin& k, double euler[3]) {
   double ce, se;
   sincos(a.epa, &se, &ce);
+  kinematics(a.p, a.v, a.q, a.wi, ce, se, want_euler, k, euler);
+}
 
-  Kin k;
-  kinematics(a.p, a.v, a.q, a.wi, ce, se, want_euler, k, out.euler);
-  {   // quaternion derivative for the next step (quat_qdot, jsb_frames.py:170-176)
-    const double p = a.wi[0], qq = a.wi[1], r = a.wi[2];
-    const double q0 = a.q[0], q1 = a.q[1], q2 = a.q[2], q3 = a.q[3];
-    a.qd[0] = -0.5 * (q1 * p + q2 * qq + q3 * r);
-    a.qd[1] = 0.5 * (q0 * p - q3 * qq + q2 * r);
-    a.qd[2] = 0.5 * (q3 * p + q0 * qq - q1 * r);
-    a.qd[3] = 0.5 * (-q2 * p + q1 * qq + q0 * r);
+// ------------------------------------------------------------------ force path (one lane)
+struct ForceOut {
+  double ai[3], wdi[3], pba[3], ppq[3];   // vUVWidot, vPQRidot, vBodyAccel, vPQRi
+  double alpha, beta, vt, mach, vc_kts, vg, npy, npz;
+  double fuel_burn, alt, k_rud;
+};
+
+template <int FCS_RATE>
+F16_HD void force_path(Aircraft& a, double c_ail, double c_ele, double c_rud,
+                       double c_thr, const Kin& k, const double* __restrict__ T, ForceOut& o) {
+  const double alt = k.radius - kSemiMajor;
+  const Atmos at = isa(alt, T);
+  const Mass mb = mass_props(a.fuel);
+  FcsOut fc;
+  const double esch = fcs_prev_frame<FCS_RATE>(a, c_ail, c_ele, c_rud, T, fc);
+  fcs_pitch<FCS_RATE>(a, esch, k.ctcp, fc);
+  o.k_rud = fc.k_rud;
+  const AuxGeo g = aux_geometry(k.uvw);
+  const double qbar = 0.5 * at.rho * g.vt2;
+  const double mach = g.vt / at.a;
+  load_factors(a, mb.cg, o.npy, o.npz);
+  o.vc_kts = vc_knots(mach, at.P);
+  o.vg = sqrt(k.vn * k.vn + k.ve * k.ve);
+  o.alpha = g.alpha; o.beta = g.beta; o.vt = g.vt; o.mach = mach; o.alt = alt;
+  const double thrust = engine(a, c_thr, at, mach, T, o.fuel_burn);
+  double ax[6];
+  {
+    const double alpha = g.alpha, beta = g.beta;
+    double bi2vel, ci2vel;
+    aero_rates(g.vt, bi2vel, ci2vel);
+    constexpr double kclge = kCLge;
+    constexpr double gear = kGearPos<FCS_RATE>;
+    const double p = k.wpqr[0], q = k.wpqr[1], r = k.wpqr[2];
+    const double ail = fc.ail, elev = fc.elev, rud = fc.rud, lef = fc.lef, flap = fc.flap;
+    F16_AERO_BRACKETS;
+    F16_AERO_LOOKUPS;
+    ax[0] = F16_AERO_DRAG_FREE + F16_AERO_DRAG_CTL;
+    ax[1] = F16_AERO_SIDE_FREE + F16_AERO_SIDE_CTL;
+    ax[2] = F16_AERO_LIFT_FREE + F16_AERO_LIFT_CTL;
+    ax[3] = F16_AERO_ROLL_FREE + F16_AERO_ROLL_CTL;
+    ax[4] = F16_AERO_PITCH_FREE + F16_AERO_PITCH_CTL;
+    ax[5] = F16_AERO_YAW_FREE + F16_AERO_YAW_CTL;
   }
+  double F[3], M[3], gi[3];
+  forces_moments(ax, g, mb, thrust, F, M);
+  gravity(k, gi);
+  Accel ac;
+  accelerations(k, mb, F, M, gi, ac);
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    o.ai[i] = ac.ai[i]; o.wdi[i] = ac.wdi[i]; o.pba[i] = ac.pba[i]; o.ppq[i] = ac.ppq[i];
+  }
+}
+
+// ------------------------------------------------------------------ one integration step
+// FDM.step (jsb_fdm.py:212-244).  FCS_RATE: the FCS components' dt is 1/FCS_RATE s (120 for
+// cuda_fdm/ref/jsb_fcs.py:19, 60 for the 184-D runtime's copy of that file).
+template <int FCS_RATE>
+F16_HD void substep(Aircraft& a, double c_ail, double c_ele, double c_rud,
+                                        double c_thr, const double* __restrict__ T,
+                                        bool want_euler, SubstepOut& out) {
+  propagate(a);
+  Kin k;
+  frames(a, want_euler, k, out.euler);
+  quat_rate(a);
   ForceOut f;
   force_path<FCS_RATE>(a, c_ail, c_ele, c_rud, c_thr, k, T, f);
   a.fuel -= f.fuel_burn;
@@ -689,7 +766,7 @@ F16_HD void substep(Aircraft& a, double c_ail, double c_ele, double c_rud,
   a.pa[0] = f.alpha; a.pa[1] = f.mach; a.pa[2] = f.vc_kts; a.pa[3] = f.vg;
   a.pa[4] = f.npy; a.pa[5] = f.npz; a.pa[6] = k.wpqr[0]; a.pa[7] = k.wpqr[1]; a.pa[8] = k.wpqr[2];
   out.k_rud = f.k_rud;
-  out.k_gear = kGearForce - (1.0 / (double)FCS_RATE) * ((1.0 - 0.0) / 5.0);
+  out.k_gear = kGearPos<FCS_RATE>;
 #pragma unroll
   for (int i = 0; i < 3; ++i) out.uvw[i] = k.uvw[i];
   out.alpha = f.alpha; out.beta = f.beta; out.mach = f.mach; out.vt = f.vt; out.alt = f.alt;

@@ -7,6 +7,7 @@
 #include <hip/hip_runtime.h>
 
 #include "fdm_advance.h"
+#include "fdm_split.h"
 #include "f16_capi_common.h"
 
 namespace f16 {
@@ -33,6 +34,28 @@ __global__ __launch_bounds__(kBlock) void fdm_step_kernel(double* __restrict__ s
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= nac) return;
   advance_aircraft<FCS_RATE>(st + i, ld, act + 4L * i, S, obs ? obs + i : nullptr, obs_ld, T);
+}
+
+// Two wavefronts per 64 aircraft (fdm_split.h): even waves fly, odd waves run the systems.
+// The role is wave-uniform (a scalar branch), so each role's loop issues its own barriers and
+// the two loops' barrier counts match (3 per substep each).
+template <int FCS_RATE>
+__global__ __launch_bounds__(kSplitBlock) void fdm_step_split_kernel(
+    double* __restrict__ st, long ld, const double* __restrict__ act, int nac, int S,
+    double* __restrict__ obs, long obs_ld) {
+  __shared__ double T[F16M_IMAGE_LEN];
+  __shared__ SplitX X[kSplitPairs];
+  stage_image(T);
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int pair = wave >> 1;
+  const int i = blockIdx.x * kSplitAircraft + pair * 64 + lane;
+  const bool store = i < nac;
+  const int ia = store ? i : nac - 1;   // lanes past the batch shadow the last aircraft
+  if ((wave & 1) == 0)
+    split_flight<FCS_RATE>(st + ia, ld, S, store, obs ? obs + ia : nullptr, obs_ld, T, X[pair], lane);
+  else
+    split_systems<FCS_RATE>(st + ia, ld, act + 4L * ia, S, store, T, X[pair], lane);
 }
 
 // ------------------------------------------------------------------ IC seeding
@@ -193,14 +216,35 @@ __global__ __launch_bounds__(kBlock) void seed_kernel(const double* __restrict__
 }  // namespace f16
 
 // ------------------------------------------------------------------ C entry points
+static int fdm_step_args(double* states, long ld, const double* actions, int nac, int substeps,
+                         int fcs_rate, double* obs, long obs_ld) {
+  if (nac < 0 || substeps < 0 || ld < nac) return F16_EINVAL;
+  if (fcs_rate != 120 && fcs_rate != 60) return F16_ERATE;
+  if (nac == 0) return 1;
+  if (!states || !actions) return F16_EINVAL;
+  if (obs && obs_ld < nac) return F16_EINVAL;
+  return 0;
+}
+
 extern "C" int f16_fdm_step_batch(double* states, long ld, const double* actions, int nac,
                                   int substeps, int fcs_rate, double* obs, long obs_ld,
                                   void* stream) {
-  if (nac < 0 || substeps < 0 || ld < nac) return F16_EINVAL;
-  if (fcs_rate != 120 && fcs_rate != 60) return F16_ERATE;
-  if (nac == 0) return 0;
-  if (!states || !actions) return F16_EINVAL;
-  if (obs && obs_ld < nac) return F16_EINVAL;
+  const int rc = fdm_step_args(states, ld, actions, nac, substeps, fcs_rate, obs, obs_ld);
+  if (rc) return rc < 0 ? rc : 0;
+  const dim3 grid((nac + f16::kSplitAircraft - 1) / f16::kSplitAircraft), block(f16::kSplitBlock);
+  hipStream_t s = (hipStream_t)stream;
+  if (fcs_rate == 120)
+    hipLaunchKernelGGL(f16::fdm_step_split_kernel<120>, grid, block, 0, s, states, ld, actions, nac, substeps, obs, obs_ld);
+  else
+    hipLaunchKernelGGL(f16::fdm_step_split_kernel<60>, grid, block, 0, s, states, ld, actions, nac, substeps, obs, obs_ld);
+  return f16_last_error();
+}
+
+extern "C" int f16_fdm_step_batch_onelane(double* states, long ld, const double* actions,
+                                          int nac, int substeps, int fcs_rate, double* obs,
+                                          long obs_ld, void* stream) {
+  const int rc = fdm_step_args(states, ld, actions, nac, substeps, fcs_rate, obs, obs_ld);
+  if (rc) return rc < 0 ? rc : 0;
   const dim3 grid((nac + f16::kBlock - 1) / f16::kBlock), block(f16::kBlock);
   hipStream_t s = (hipStream_t)stream;
   if (fcs_rate == 120)

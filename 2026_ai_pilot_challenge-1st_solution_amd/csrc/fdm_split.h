@@ -1,0 +1,257 @@
+// fdm_split.h -- the batched F-16 step with each aircraft's substep spread over two cooperating
+// wavefronts of one workgroup.
+//
+// One lane per aircraft still, but every 64 aircraft get two wavefronts: the "flight" wave owns
+// the integrator (propagation, frames, body kinematics, aero build-up, forces, accelerations)
+// and the "systems" wave owns the mass, FCS, atmosphere, air data and engine.  The two run
+// concurrently on different SIMDs and trade what the other needs through LDS at three
+// workgroup barriers per substep:
+//
+//   phase 1  flight:  history pushes, propagate, frames, quaternion rate, gravity
+//            systems: mass properties, previous-frame FCS channels, pitch schedule
+//   -- X1: altitude, cos(theta)cos(phi), vg, p q r  |  mass/CG/inertia, aileron/rudder/LEF/flaperon
+//   phase 2  flight:  air-relative geometry (vt, alpha, beta), load factors, alpha/beta brackets
+//                     and their table values
+//            systems: atmosphere, pitch loop
+//   -- X2: vt, alpha, beta, n_y, n_z  |  rho, speed of sound, elevator
+//   phase 3  flight:  dynamic pressure, mach, mach/elevator brackets and values, the six sums
+//            systems: mach, calibrated airspeed, engine
+//   -- X3: thrust
+//   phase 4  flight:  forces, moments, accelerations, state update
+//            systems: fuel burn, previous-frame auxiliary values
+//
+// Every value is computed by the same component functions (fdm_device.h) with the same
+// operands as the one-lane kernel, so the two kernels agree bit for bit; this one halves the
+// instructions each wavefront issues and gives each the registers of its own half of the
+// state.  At 16,384 engagements the one-lane kernel has 512 wavefronts for 1,024 SIMDs; this
+// one fills them.
+#pragma once
+#include "fdm_device.h"
+
+namespace f16 {
+
+constexpr int kSplitPairs = 2;                      // wavefront pairs per workgroup
+constexpr int kSplitBlock = 128 * kSplitPairs;      // threads per workgroup
+constexpr int kSplitAircraft = 64 * kSplitPairs;    // aircraft per workgroup
+
+// LDS exchange fields, [pair][field][lane].
+enum SplitField : int {
+  // X1, flight -> systems
+  kXAlt, kXCtcp, kXVg, kXP, kXQ, kXR,
+  // X1, systems -> flight
+  kXMass, kXJ, kXJinv = kXJ + 6, kXRp = kXJinv + 6, kXCg = kXRp + 3,
+  kXAil = kXCg + 3, kXRud, kXLef, kXFlap,
+  // X2, flight -> systems
+  kXVt, kXAlpha, kXBeta, kXNpy, kXNpz,
+  // X2, systems -> flight
+  kXRho, kXSound, kXElev,
+  // X3, systems -> flight
+  kXThrust,
+  kSplitFields
+};
+
+typedef double SplitX[kSplitFields][64];
+
+// The flight wave of one pair.  `s`: the aircraft's state field 0 (fields `ld` apart); `store`:
+// whether this lane's aircraft exists (lanes past the batch shadow the last aircraft and store
+// nothing).  Issues exactly 3 barriers per substep, like split_systems.
+template <int FCS_RATE>
+__device__ __forceinline__ void split_flight(double* __restrict__ s, long ld, int S, bool store,
+                                             double* __restrict__ o, long obs_ld,
+                                             const double* __restrict__ T, SplitX& x, int lane) {
+#define F(k) s[(long)(k) * ld]
+  Aircraft a;
+#pragma unroll
+  for (int j = 0; j < 3; ++j) {
+    a.p[j] = F(F16S_POS + j); a.v[j] = F(F16S_VEL + j); a.wi[j] = F(F16S_PQRI + j);
+    a.ai[j] = F(F16S_UVWIDOT + j); a.wdi[j] = F(F16S_PQRIDOT + j);
+    a.vh1[j] = F(F16S_DIVEL + j); a.vh2[j] = F(F16S_DIVEL + 3 + j); a.ah1[j] = F(F16S_DUVW + j);
+    a.pba[j] = F(F16S_PBA + j); a.ppd[j] = F(F16S_PPQRIDOT + j); a.ppq[j] = F(F16S_PPQRI + j);
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) { a.q[j] = F(F16S_Q + j); a.qd[j] = F(F16S_QDOT + j); }
+  a.epa = F(F16S_EPA);
+  // fewer than three substeps keep older history entries, shifted down by S
+  if (store && S > 0 && S < 3) {
+    for (int k = 2; k >= S; --k) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) F(F16S_DQ + 4 * k + j) = F(F16S_DQ + 4 * (k - S) + j);
+#pragma unroll
+      for (int j = 0; j < 3; ++j) {
+        F(F16S_DPQRI + 3 * k + j) = F(F16S_DPQRI + 3 * (k - S) + j);
+        F(F16S_DIVEL + 3 * k + j) = F(F16S_DIVEL + 3 * (k - S) + j);
+        F(F16S_DUVW + 3 * k + j) = F(F16S_DUVW + 3 * (k - S) + j);
+      }
+    }
+  }
+  double euler[3] = {0.0, 0.0, 0.0}, mach = 0.0, alt = 0.0;
+  AuxGeo g;
+  Kin k;
+  for (int t = 0; t < S; ++t) {
+    const int slot = S - 1 - t;
+    // ---- phase 1
+    if (store && slot <= 2) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) F(F16S_DQ + 4 * slot + j) = a.qd[j];
+#pragma unroll
+      for (int j = 0; j < 3; ++j) {
+        F(F16S_DPQRI + 3 * slot + j) = a.wdi[j];
+        F(F16S_DIVEL + 3 * slot + j) = a.v[j];
+        F(F16S_DUVW + 3 * slot + j) = a.ai[j];
+      }
+    }
+    propagate(a);
+    frames(a, slot == 0 && o != nullptr, k, euler);
+    quat_rate(a);
+    double gi[3];
+    gravity(k, gi);
+    alt = k.radius - kSemiMajor;
+    const double vg = sqrt(k.vn * k.vn + k.ve * k.ve);
+    x[kXAlt][lane] = alt; x[kXCtcp][lane] = k.ctcp; x[kXVg][lane] = vg;
+    x[kXP][lane] = k.wpqr[0]; x[kXQ][lane] = k.wpqr[1]; x[kXR][lane] = k.wpqr[2];
+    __syncthreads();
+    // ---- phase 2
+    Mass mb;
+    mb.mass = x[kXMass][lane];
+#pragma unroll
+    for (int j = 0; j < 6; ++j) { mb.J[j] = x[kXJ + j][lane]; mb.Jinv[j] = x[kXJinv + j][lane]; }
+#pragma unroll
+    for (int j = 0; j < 3; ++j) { mb.rp[j] = x[kXRp + j][lane]; mb.cg[j] = x[kXCg + j][lane]; }
+    g = aux_geometry(k.uvw);
+    double npy, npz;
+    load_factors(a, mb.cg, npy, npz);
+    x[kXVt][lane] = g.vt; x[kXAlpha][lane] = g.alpha; x[kXBeta][lane] = g.beta;
+    x[kXNpy][lane] = npy; x[kXNpz][lane] = npz;
+    const double alpha = g.alpha, beta = g.beta;
+    F16_AERO_BRACKETS_AB;
+    F16_AERO_LOOKUPS_AB;
+    const double ail = x[kXAil][lane], rud = x[kXRud][lane];
+    const double lef = x[kXLef][lane], flap = x[kXFlap][lane];
+    __syncthreads();
+    // ---- phase 3
+    const double rho = x[kXRho][lane], sound = x[kXSound][lane], elev = x[kXElev][lane];
+    const double qbar = 0.5 * rho * g.vt2;
+    mach = g.vt / sound;
+    double ax[6];
+    {
+      double bi2vel, ci2vel;
+      aero_rates(g.vt, bi2vel, ci2vel);
+      constexpr double kclge = kCLge;
+      constexpr double gear = kGearPos<FCS_RATE>;
+      const double p = k.wpqr[0], q = k.wpqr[1], r = k.wpqr[2];
+      F16_AERO_BRACKETS_MACH;
+      F16_AERO_BRACKETS_ELEV;
+      F16_AERO_LOOKUPS_MACH;
+      F16_AERO_LOOKUPS_ELEV;
+      ax[0] = F16_AERO_DRAG_FREE + F16_AERO_DRAG_CTL;
+      ax[1] = F16_AERO_SIDE_FREE + F16_AERO_SIDE_CTL;
+      ax[2] = F16_AERO_LIFT_FREE + F16_AERO_LIFT_CTL;
+      ax[3] = F16_AERO_ROLL_FREE + F16_AERO_ROLL_CTL;
+      ax[4] = F16_AERO_PITCH_FREE + F16_AERO_PITCH_CTL;
+      ax[5] = F16_AERO_YAW_FREE + F16_AERO_YAW_CTL;
+    }
+    __syncthreads();
+    // ---- phase 4
+    const double thrust = x[kXThrust][lane];
+    double Fb[3], Mb[3];
+    forces_moments(ax, g, mb, thrust, Fb, Mb);
+    Accel ac;
+    accelerations(k, mb, Fb, Mb, gi, ac);
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+      a.ai[i] = ac.ai[i]; a.wdi[i] = ac.wdi[i]; a.pba[i] = ac.pba[i];
+      a.ppd[i] = ac.wdi[i]; a.ppq[i] = ac.ppq[i];
+    }
+  }
+  if (!store || S <= 0) return;
+#pragma unroll
+  for (int j = 0; j < 3; ++j) {
+    F(F16S_POS + j) = a.p[j]; F(F16S_VEL + j) = a.v[j]; F(F16S_PQRI + j) = a.wi[j];
+    F(F16S_UVWIDOT + j) = a.ai[j]; F(F16S_PQRIDOT + j) = a.wdi[j];
+    F(F16S_PBA + j) = a.pba[j]; F(F16S_PPQRIDOT + j) = a.ppd[j]; F(F16S_PPQRI + j) = a.ppq[j];
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) { F(F16S_Q + j) = a.q[j]; F(F16S_QDOT + j) = a.qd[j]; }
+  F(F16S_EPA) = a.epa;
+#undef F
+  if (o) {
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      o[(long)j * obs_ld] = a.p[j];
+      o[(long)(3 + j) * obs_ld] = a.v[j];
+      o[(long)(6 + j) * obs_ld] = euler[j];
+      o[(long)(9 + j) * obs_ld] = k.uvw[j];
+    }
+    o[12L * obs_ld] = g.alpha; o[13L * obs_ld] = g.beta; o[14L * obs_ld] = mach;
+    o[15L * obs_ld] = g.vt; o[16L * obs_ld] = alt;
+  }
+}
+
+// The systems wave of one pair: fuel, engine, FCS and previous-frame auxiliary state.
+// Issues exactly 3 barriers per substep, like split_flight.
+template <int FCS_RATE>
+__device__ __forceinline__ void split_systems(double* __restrict__ s, long ld,
+                                              const double* __restrict__ act4, int S, bool store,
+                                              const double* __restrict__ T, SplitX& x, int lane) {
+#define F(k) s[(long)(k) * ld]
+  Aircraft a;
+#pragma unroll
+  for (int j = 0; j < 3; ++j) { a.pid_ip[j] = F(F16S_PID + 3 * j); a.pid_io[j] = F(F16S_PID + 3 * j + 2); }
+#pragma unroll
+  for (int j = 0; j < 9; ++j) a.pa[j] = F(F16S_PAUX + j);
+  a.fuel = F(F16S_FUEL);
+  a.n1 = F(F16S_ENG); a.n2 = F(F16S_ENG + 1); a.n2n = F(F16S_ENG + 2); a.ff = F(F16S_ENG + 3);
+  a.k_tef = F(F16S_KIN); a.k_ail = F(F16S_KIN + 1); a.k_ele = F(F16S_KIN + 2); a.k_lef = F(F16S_KIN + 5);
+  const double c_ail = act4[0], c_ele = act4[1], c_rud = act4[2], c_thr = act4[3];
+  double k_rud = 0.0;
+  for (int t = 0; t < S; ++t) {
+    const int slot = S - 1 - t;
+    // ---- phase 1
+    if (store && slot == 0) {   // PID input_prev2 = input_prev before the final update
+#pragma unroll
+      for (int j = 0; j < 3; ++j) F(F16S_PID + 3 * j + 1) = a.pid_ip[j];
+    }
+    const Mass mb = mass_props(a.fuel);
+    FcsOut fc;
+    const double esch = fcs_prev_frame<FCS_RATE>(a, c_ail, c_ele, c_rud, T, fc);
+    k_rud = fc.k_rud;
+    x[kXMass][lane] = mb.mass;
+#pragma unroll
+    for (int j = 0; j < 6; ++j) { x[kXJ + j][lane] = mb.J[j]; x[kXJinv + j][lane] = mb.Jinv[j]; }
+#pragma unroll
+    for (int j = 0; j < 3; ++j) { x[kXRp + j][lane] = mb.rp[j]; x[kXCg + j][lane] = mb.cg[j]; }
+    x[kXAil][lane] = fc.ail; x[kXRud][lane] = fc.rud; x[kXLef][lane] = fc.lef; x[kXFlap][lane] = fc.flap;
+    __syncthreads();
+    // ---- phase 2
+    const double alt = x[kXAlt][lane], ctcp = x[kXCtcp][lane], vg = x[kXVg][lane];
+    const double p = x[kXP][lane], q = x[kXQ][lane], r = x[kXR][lane];
+    const Atmos at = isa(alt, T);
+    fcs_pitch<FCS_RATE>(a, esch, ctcp, fc);
+    x[kXRho][lane] = at.rho; x[kXSound][lane] = at.a; x[kXElev][lane] = fc.elev;
+    __syncthreads();
+    // ---- phase 3
+    const double vt = x[kXVt][lane], alpha = x[kXAlpha][lane];
+    const double npy = x[kXNpy][lane], npz = x[kXNpz][lane];
+    const double mach = vt / at.a;
+    const double vc = vc_knots(mach, at.P);
+    double burn;
+    x[kXThrust][lane] = engine(a, c_thr, at, mach, T, burn);
+    __syncthreads();
+    // ---- phase 4
+    a.fuel -= burn;
+    a.pa[0] = alpha; a.pa[1] = mach; a.pa[2] = vc; a.pa[3] = vg;
+    a.pa[4] = npy; a.pa[5] = npz; a.pa[6] = p; a.pa[7] = q; a.pa[8] = r;
+  }
+  if (!store || S <= 0) return;
+#pragma unroll
+  for (int j = 0; j < 3; ++j) { F(F16S_PID + 3 * j) = a.pid_ip[j]; F(F16S_PID + 3 * j + 2) = a.pid_io[j]; }
+#pragma unroll
+  for (int j = 0; j < 9; ++j) F(F16S_PAUX + j) = a.pa[j];
+  F(F16S_FUEL) = a.fuel;
+  F(F16S_ENG) = a.n1; F(F16S_ENG + 1) = a.n2; F(F16S_ENG + 2) = a.n2n; F(F16S_ENG + 3) = a.ff;
+  F(F16S_KIN) = a.k_tef; F(F16S_KIN + 1) = a.k_ail; F(F16S_KIN + 2) = a.k_ele;
+  F(F16S_KIN + 3) = k_rud; F(F16S_KIN + 4) = kGearPos<FCS_RATE>; F(F16S_KIN + 5) = a.k_lef;
+#undef F
+}
+
+}  // namespace f16

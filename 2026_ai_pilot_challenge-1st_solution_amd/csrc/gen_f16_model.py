@@ -450,31 +450,46 @@ def main():
         fh.write("\n".join(g) + "\n")
 
     # The speedbrake is never driven (its position is identically +0), so the four terms with
-    # that factor are exactly +-0 for every finite state and are omitted.  Every axis is split
-    # into the terms that involve no control-surface position, as a factor or as a table
-    # variable ("free": they need only the flow state), and the terms that do ("ctl"); each part is a left-to-right sum from 0 in XML
-    # order, and the axis is free + ctl.  Callers can evaluate the parts at different times
-    # (the free part before the FCS has run) and get the same bits.
+    # that factor are exactly +-0 for every finite state and are omitted.
+    # The build-up is emitted in three layers so that callers can evaluate it piecewise as its
+    # inputs become available and still get the same bits:
+    #   brackets  (one per shared grid), grouped by key: alpha/beta, mach, elevator;
+    #   lookups   lk_<term> = the term's table value, grouped by the brackets they need;
+    #   sums      per axis, FREE = terms with no control-surface position (as a factor or a
+    #             table variable), CTL = the others; each a left-to-right sum from 0 in XML
+    #             order of the term's factors times its lookup; axis = FREE + CTL.
     CTL = {"fcs/aileron-pos-rad", "fcs/elevator-pos-rad", "fcs/rudder-pos-rad",
            "fcs/lef-pos-rad", "fcs/flaperon-mix-rad"}
     SB = "fcs/speedbrake-pos-rad"
+    KEYGRP = {"aero/alpha-rad": "AB", "aero/beta-rad": "AB", "velocities/mach": "MACH",
+              "fcs/elevator-pos-rad": "ELEV"}
     d = []
     dw = d.append
+
+    def macro(name, stmts):
+        dw(f"#define {name} \\")
+        for i, st in enumerate(stmts):
+            dw(f"  {st}" + ("; \\" if i + 1 < len(stmts) else ""))
+        if not stmts:
+            dw("  do {} while (0)")
+
     dw("// f16_aero_gen.inc -- GENERATED by gen_f16_model.py; do not edit.")
-    dw("// The 40-function F-16 aero build-up as expression macros over names in scope: `T` (the")
-    dw("// model image), qbar alpha beta bi2vel ci2vel mach kclge p q r ail elev rud lef flap gear,")
-    dw("// and the brackets F16_AERO_BRACKETS declares (b1_<grid>, b2_<grid>).")
-    dw("// F16_AERO_<AXIS>_FREE sums the terms without a control-surface factor, F16_AERO_<AXIS>_CTL")
-    dw("// the terms with one; each is a left-to-right sum from 0 in XML order; axis = FREE + CTL.")
+    dw("// The 40-function F-16 aero build-up in three layers over names in scope (`T`, the model")
+    dw("// image; qbar alpha beta bi2vel ci2vel mach kclge p q r ail elev rud lef flap gear):")
+    dw("//   F16_AERO_BRACKETS_{AB,MACH,ELEV}: one bracket per shared grid (b1_<grid>, b2_<grid>),")
+    dw("//     keyed on alpha/beta, mach, elevator position;")
+    dw("//   F16_AERO_LOOKUPS_{AB,MACH,ELEV}: lk_<term> = the term's table value, by the brackets")
+    dw("//     it needs;")
+    dw("//   F16_AERO_<AXIS>_FREE / _CTL: the terms without / with a control-surface position, each")
+    dw("//     a left-to-right sum from 0 in XML order; the axis is FREE + CTL.")
     dw("// Terms with the speedbrake factor (identically 0) are omitted.")
-    brk = []
+    brk = {"AB": [], "MACH": [], "ELEV": []}
     for gr, var in sorted(used1.items(), key=lambda kv: kv[0][1]):
-        brk.append(f"const F16Br1 b1_{gr[0]} = F16_BR1({gr[0]}, {var_expr[var]})")
+        brk[KEYGRP[var]].append(f"const F16Br1 b1_{gr[0]} = F16_BR1({gr[0]}, {var_expr[var]})")
     for gr, var in sorted(used2.items(), key=lambda kv: kv[0][1]):
-        brk.append(f"const F16Br2 b2_{gr[0]} = F16_BR2({gr[0]}, {var_expr[var]})")
-    dw("#define F16_AERO_BRACKETS \\")
-    for i, b in enumerate(brk):
-        dw(f"  {b}" + ("; \\" if i + 1 < len(brk) else ""))
+        brk[KEYGRP[var]].append(f"const F16Br2 b2_{gr[0]} = F16_BR2({gr[0]}, {var_expr[var]})")
+    lks = {"AB": [], "MACH": [], "ELEV": []}
+    sums = {}
     for ai, ax in enumerate(AXES):
         parts_of = {"FREE": [], "CTL": []}
         for aj, short, f, rec in terms:
@@ -488,22 +503,33 @@ def main():
                 parts.append(fnum(const_of[pp]) if pp in const_of else var_expr[pp])
             if f["value"] is not None:
                 parts.append(fnum(f["value"]))
-            if rec is not None:
-                if rec["kind"] == 1:
-                    parts.append(f"f16_lerp1(T, F16M_T_AERO_{short}_OFF, b1_{rec['rg'][0]})")
-                else:
-                    parts.append(f"f16_lerp2(T, F16M_T_AERO_{short}_OFF, F16M_T_AERO_{short}_NC, "
-                                 f"b2_{rec['rg'][0]}, b2_{rec['cg'][0]})")
             uses = set(f["factors"])
             if rec is not None:
-                uses |= {rec["row_var"], rec.get("col_var")}
+                keys = [rec["row_var"]] + ([rec["col_var"]] if rec["kind"] == 2 else [])
+                uses |= set(keys)
+                grp = "ELEV" if "ELEV" in {KEYGRP[k] for k in keys} else (
+                    "MACH" if "MACH" in {KEYGRP[k] for k in keys} else "AB")
+                if rec["kind"] == 1:
+                    lk = f"f16_lerp1(T, F16M_T_AERO_{short}_OFF, b1_{rec['rg'][0]})"
+                else:
+                    lk = (f"f16_lerp2(T, F16M_T_AERO_{short}_OFF, F16M_T_AERO_{short}_NC, "
+                          f"b2_{rec['rg'][0]}, b2_{rec['cg'][0]})")
+                lks[grp].append(f"const double lk_{short} = {lk}")
+                parts.append(f"lk_{short}")
             kind = "CTL" if CTL & uses else "FREE"
             parts_of[kind].append((short, " * ".join(parts)))
+        sums[ax] = parts_of
+    for grp in ("AB", "MACH", "ELEV"):
+        macro(f"F16_AERO_BRACKETS_{grp}", brk[grp])
+    dw("#define F16_AERO_BRACKETS F16_AERO_BRACKETS_AB; F16_AERO_BRACKETS_MACH; F16_AERO_BRACKETS_ELEV")
+    for grp in ("AB", "MACH", "ELEV"):
+        macro(f"F16_AERO_LOOKUPS_{grp}", lks[grp])
+    dw("#define F16_AERO_LOOKUPS F16_AERO_LOOKUPS_AB; F16_AERO_LOOKUPS_MACH; F16_AERO_LOOKUPS_ELEV")
+    for ax in AXES:
         for kind in ("FREE", "CTL"):
-            lst = parts_of[kind]
             dw(f"#define F16_AERO_{ax}_{kind} ( \\")
             dw("  0.0 \\")
-            for short, expr in lst:
+            for short, expr in sums[ax][kind]:
                 dw(f"  + {expr} /* {short} */ \\")
             dw("  )")
     with open(os.path.join(args.out_dir, "f16_aero_gen.inc"), "w") as fh:

@@ -232,6 +232,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-rollout", action="store_true")
     ap.add_argument("--no-league", action="store_true")
+    ap.add_argument("--only", choices=["fdm", "env", "rollout", "league"], default=None,
+                    help="profiling aid: run only this section and print its own JSON line "
+                         "(not the contract line)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run 5 device-to-device copies of MIB MiB (rocprof counter "
                          "calibration: FETCH_SIZE/WRITE_SIZE of a copy of known size)")
@@ -255,6 +258,12 @@ def main():
     sys.path.insert(0, ROOT)
     pkg = importlib.import_module(PKG)
     icm = importlib.import_module(PKG + ".ic")
+    if args.only in ("env", "rollout", "league"):
+        part = {"env": lambda: env_step_bench(pkg, args.nenv, args.steps, args.warmup),
+                "rollout": lambda: rollout_bench(args.nenv),
+                "league": lambda: league_bench()}[args.only]()
+        print(json.dumps(part), flush=True)
+        return
 
     nenv, S = args.nenv, args.substeps
     nac = 2 * nenv
@@ -287,6 +296,10 @@ def main():
     if not bool(torch.isfinite(sim.states).all()):
         raise FloatingPointError("non-finite state after the timed steps")
 
+    if args.only == "fdm":
+        print(json.dumps({"workload": "fdm_tailchase_16k", "fdm_kernel_ms": kern_ms,
+                          "ms_per_step": ms_step}), flush=True)
+        return
     env_line = env_step_bench(pkg, nenv, args.steps, args.warmup)
     rollout_line = None if args.no_rollout else rollout_bench(nenv)
     league_line = None if args.no_league else league_bench()

@@ -25,6 +25,13 @@ extern "C" {
 int f16_fdm_step_batch(double* states, long ld, const double* actions, int nac, int substeps,
                        int fcs_rate, double* obs, long obs_ld, void* stream);
 
+/* The same step computed with one lane (one wavefront) per aircraft doing the whole substep.
+ * Results equal f16_fdm_step_batch bit for bit; f16_fdm_step_batch spreads each substep over
+ * two cooperating wavefronts.  Same arguments, contract and reference interface. */
+int f16_fdm_step_batch_onelane(double* states, long ld, const double* actions, int nac,
+                               int substeps, int fcs_rate, double* obs, long obs_ld,
+                               void* stream);
+
 /* Seed aircraft states from initial conditions on the device.
  * ic: (n, 10) rows [lat_deg, lon_deg, alt_ft, vt_fps, phi_deg, theta_deg, psi_deg, alpha_deg,
  *     beta_deg, fuel_lbs] (geodetic latitude, epa = 0, fuel-flow 0).

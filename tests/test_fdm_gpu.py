@@ -190,6 +190,40 @@ def test_independence_and_determinism(gpu):
     assert torch.equal(a.states[torch.as_tensor(perm, device=gpu)], c.states)
 
 
+@pytest.mark.parametrize("rate", [120, 60])
+@pytest.mark.parametrize("nenv,S,pad", [(4096, 6, 0), (77, 1, 0), (77, 2, 5), (1000, 3, 0),
+                                        (1, 6, 3), (300, 0, 0)])
+def test_split_kernel_equals_onelane(gpu, rate, nenv, S, pad):
+    """The production step spreads each substep over two wavefronts that trade values through
+    LDS; the one-lane kernel runs the same component functions in sequence.  They agree bit for
+    bit on states and outputs, for ragged batch sizes (lanes past the batch), short substep
+    counts (history shifting), a leading dimension larger than the batch, and S = 0."""
+    icm = import_pkg("ic")
+    L = import_pkg("_lib")
+    nac = 2 * nenv
+    ld = nac + pad
+    sim = _sim(nenv, rate, max(S, 1))
+    sim.seed_rows(torch.as_tensor(icm.sample_tailchase(nenv, seed=7), device=gpu))
+    bufs = []
+    for _ in range(2):
+        st = torch.zeros(101, ld, dtype=torch.float64, device=gpu)
+        st[:, :nac] = sim._state_soa
+        bufs.append((st, torch.zeros(17, ld, dtype=torch.float64, device=gpu)))
+    acts = icm.random_bin_actions(12, nac, seed=7)
+    fns = [L.lib().f16_fdm_step_batch, L.lib().f16_fdm_step_batch_onelane]
+    for d in range(12):
+        at = torch.as_tensor(acts[d], device=gpu).contiguous()
+        for fn, (st, ob) in zip(fns, bufs):
+            L.check(fn(L.ptr(st), ld, L.ptr(at), nac, S, rate, L.ptr(ob), ld,
+                       L.stream_handle(gpu)), "step")
+    (sa, oa), (sb, ob) = bufs
+    assert bool(torch.isfinite(sa).all())
+    assert torch.equal(sa, sb)
+    assert torch.equal(oa, ob)
+    if S == 0:
+        assert torch.equal(sa[:, :nac], sim._state_soa)
+
+
 def test_nonfinite_lane_is_isolated(gpu):
     g = oracle_lib.golden("seed_golden.npz")
     sim = _sim(4)
