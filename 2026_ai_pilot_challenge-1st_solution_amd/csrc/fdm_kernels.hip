@@ -16,8 +16,22 @@ __constant__ double c_image[F16M_IMAGE_LEN] = F16M_IMAGE_INIT;
 
 constexpr int kBlock = 256;
 
+// Copy the model image into LDS: every load of a thread is issued before its first store, so
+// the copy costs one memory latency rather than one per element.  NT = threads per block.
+template <int NT>
 __device__ __forceinline__ void stage_image(double* T) {
-  for (int i = threadIdx.x; i < F16M_IMAGE_LEN; i += blockDim.x) T[i] = c_image[i];
+  constexpr int kPer = (F16M_IMAGE_LEN + NT - 1) / NT;
+  double v[kPer];
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int i = threadIdx.x + j * NT;
+    v[j] = i < F16M_IMAGE_LEN ? c_image[i] : 0.0;
+  }
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int i = threadIdx.x + j * NT;
+    if (i < F16M_IMAGE_LEN) T[i] = v[j];
+  }
   __syncthreads();
 }
 
@@ -30,7 +44,7 @@ __global__ __launch_bounds__(kBlock) void fdm_step_kernel(double* __restrict__ s
                                                           int S, double* __restrict__ obs,
                                                           long obs_ld) {
   __shared__ double T[F16M_IMAGE_LEN];
-  stage_image(T);
+  stage_image<kBlock>(T);
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= nac) return;
   advance_aircraft<FCS_RATE>(st + i, ld, act + 4L * i, S, obs ? obs + i : nullptr, obs_ld, T);
@@ -45,7 +59,7 @@ __global__ __launch_bounds__(kSplitBlock) void fdm_step_split_kernel(
     double* __restrict__ obs, long obs_ld) {
   __shared__ double T[F16M_IMAGE_LEN];
   __shared__ SplitX X[kSplitPairs];
-  stage_image(T);
+  stage_image<kSplitBlock>(T);
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int pair = wave >> 1;
@@ -89,7 +103,7 @@ __global__ __launch_bounds__(kBlock) void seed_kernel(const double* __restrict__
                                                       double* __restrict__ st, long ld,
                                                       const long* __restrict__ rows) {
   __shared__ double T[F16M_IMAGE_LEN];
-  stage_image(T);
+  stage_image<kBlock>(T);
   const int r = blockIdx.x * blockDim.x + threadIdx.x;
   if (r >= n) return;
   const double* c = ic + (long)F16IC_N * r;

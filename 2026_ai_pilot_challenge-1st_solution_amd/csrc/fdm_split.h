@@ -7,18 +7,24 @@
 // concurrently on different SIMDs and trade what the other needs through LDS at three
 // workgroup barriers per substep:
 //
-//   phase 1  flight:  history pushes, propagate, frames, quaternion rate, gravity
-//            systems: mass properties, previous-frame FCS channels, pitch schedule
-//   -- X1: altitude, cos(theta)cos(phi), vg, p q r  |  mass/CG/inertia, aileron/rudder/LEF/flaperon
+//   phase 1  flight:  history pushes, propagate, frames
+//            systems: mass properties, previous-frame FCS channels, pitch schedule, Earth
+//                     position angle
+//   -- X1: altitude, cos(theta)cos(phi)  |  mass/CG/inertia, aileron/rudder/LEF/flaperon
 //   phase 2  flight:  air-relative geometry (vt, alpha, beta), load factors, alpha/beta brackets
 //                     and their table values
 //            systems: atmosphere, pitch loop
-//   -- X2: vt, alpha, beta, n_y, n_z  |  rho, speed of sound, elevator
-//   phase 3  flight:  dynamic pressure, mach, mach/elevator brackets and values, the six sums
-//            systems: mach, calibrated airspeed, engine
-//   -- X3: thrust
+//   -- X2: vt, alpha, beta, n_y, n_z  |  rho, pressure, speed of sound, elevator
+//   phase 3  flight:  dynamic pressure, mach, calibrated airspeed, mach/elevator brackets and
+//                     values, the six sums, quaternion rate, gravity, vg
+//            systems: mach, engine, sin/cos of the next substep's Earth position angle
+//   -- X3: calibrated airspeed, vg, p q r  |  thrust, sin/cos(epa)
 //   phase 4  flight:  forces, moments, accelerations, state update
 //            systems: fuel burn, previous-frame auxiliary values
+//
+// The phases are cut so that each side's share between two barriers is about equal (measured
+// with per-wavefront clock stamps); values only needed for the next substep's previous-frame
+// inputs travel at the last exchange.
 //
 // Every value is computed by the same component functions (fdm_device.h) with the same
 // operands as the one-lane kernel, so the two kernels agree bit for bit; this one halves the
@@ -37,16 +43,18 @@ constexpr int kSplitAircraft = 64 * kSplitPairs;    // aircraft per workgroup
 // LDS exchange fields, [pair][field][lane].
 enum SplitField : int {
   // X1, flight -> systems
-  kXAlt, kXCtcp, kXVg, kXP, kXQ, kXR,
+  kXAlt, kXCtcp,
   // X1, systems -> flight
   kXMass, kXJ, kXJinv = kXJ + 6, kXRp = kXJinv + 6, kXCg = kXRp + 3,
   kXAil = kXCg + 3, kXRud, kXLef, kXFlap,
   // X2, flight -> systems
   kXVt, kXAlpha, kXBeta, kXNpy, kXNpz,
   // X2, systems -> flight
-  kXRho, kXSound, kXElev,
+  kXRho, kXPres, kXSound, kXElev,
+  // X3, flight -> systems
+  kXVc, kXVg, kXP, kXQ, kXR,
   // X3, systems -> flight
-  kXThrust,
+  kXThrust, kXCe, kXSe,
   kSplitFields
 };
 
@@ -101,14 +109,18 @@ __device__ __forceinline__ void split_flight(double* __restrict__ s, long ld, in
       }
     }
     propagate(a);
-    frames(a, slot == 0 && o != nullptr, k, euler);
-    quat_rate(a);
-    double gi[3];
-    gravity(k, gi);
+    {   // sin/cos(epa): the systems wave evaluates them one substep ahead, off this chain
+      double ce, se;
+      if (t == 0) {
+        sincos(a.epa, &se, &ce);
+      } else {
+        ce = x[kXCe][lane];
+        se = x[kXSe][lane];
+      }
+      kinematics(a.p, a.v, a.q, a.wi, ce, se, slot == 0 && o != nullptr, k, euler);
+    }
     alt = k.radius - kSemiMajor;
-    const double vg = sqrt(k.vn * k.vn + k.ve * k.ve);
-    x[kXAlt][lane] = alt; x[kXCtcp][lane] = k.ctcp; x[kXVg][lane] = vg;
-    x[kXP][lane] = k.wpqr[0]; x[kXQ][lane] = k.wpqr[1]; x[kXR][lane] = k.wpqr[2];
+    x[kXAlt][lane] = alt; x[kXCtcp][lane] = k.ctcp;
     __syncthreads();
     // ---- phase 2
     Mass mb;
@@ -132,6 +144,12 @@ __device__ __forceinline__ void split_flight(double* __restrict__ s, long ld, in
     const double rho = x[kXRho][lane], sound = x[kXSound][lane], elev = x[kXElev][lane];
     const double qbar = 0.5 * rho * g.vt2;
     mach = g.vt / sound;
+    x[kXVc][lane] = vc_knots(mach, x[kXPres][lane]);
+    x[kXVg][lane] = sqrt(k.vn * k.vn + k.ve * k.ve);
+    x[kXP][lane] = k.wpqr[0]; x[kXQ][lane] = k.wpqr[1]; x[kXR][lane] = k.wpqr[2];
+    quat_rate(a);
+    double gi[3];
+    gravity(k, gi);
     double ax[6];
     {
       double bi2vel, ci2vel;
@@ -200,6 +218,7 @@ __device__ __forceinline__ void split_systems(double* __restrict__ s, long ld,
 #pragma unroll
   for (int j = 0; j < 9; ++j) a.pa[j] = F(F16S_PAUX + j);
   a.fuel = F(F16S_FUEL);
+  a.epa = F(F16S_EPA);   // tracked with the flight wave's increments; never stored here
   a.n1 = F(F16S_ENG); a.n2 = F(F16S_ENG + 1); a.n2n = F(F16S_ENG + 2); a.ff = F(F16S_ENG + 3);
   a.k_tef = F(F16S_KIN); a.k_ail = F(F16S_KIN + 1); a.k_ele = F(F16S_KIN + 2); a.k_lef = F(F16S_KIN + 5);
   const double c_ail = act4[0], c_ele = act4[1], c_rud = act4[2], c_thr = act4[3];
@@ -207,6 +226,7 @@ __device__ __forceinline__ void split_systems(double* __restrict__ s, long ld,
   for (int t = 0; t < S; ++t) {
     const int slot = S - 1 - t;
     // ---- phase 1
+    a.epa += kRot * kDt;        // the flight wave's propagate makes the same increment
     if (store && slot == 0) {   // PID input_prev2 = input_prev before the final update
 #pragma unroll
       for (int j = 0; j < 3; ++j) F(F16S_PID + 3 * j + 1) = a.pid_ip[j];
@@ -223,21 +243,28 @@ __device__ __forceinline__ void split_systems(double* __restrict__ s, long ld,
     x[kXAil][lane] = fc.ail; x[kXRud][lane] = fc.rud; x[kXLef][lane] = fc.lef; x[kXFlap][lane] = fc.flap;
     __syncthreads();
     // ---- phase 2
-    const double alt = x[kXAlt][lane], ctcp = x[kXCtcp][lane], vg = x[kXVg][lane];
-    const double p = x[kXP][lane], q = x[kXQ][lane], r = x[kXR][lane];
+    const double alt = x[kXAlt][lane], ctcp = x[kXCtcp][lane];
     const Atmos at = isa(alt, T);
     fcs_pitch<FCS_RATE>(a, esch, ctcp, fc);
-    x[kXRho][lane] = at.rho; x[kXSound][lane] = at.a; x[kXElev][lane] = fc.elev;
+    x[kXRho][lane] = at.rho; x[kXPres][lane] = at.P; x[kXSound][lane] = at.a;
+    x[kXElev][lane] = fc.elev;
     __syncthreads();
     // ---- phase 3
     const double vt = x[kXVt][lane], alpha = x[kXAlpha][lane];
     const double npy = x[kXNpy][lane], npz = x[kXNpz][lane];
     const double mach = vt / at.a;
-    const double vc = vc_knots(mach, at.P);
     double burn;
     x[kXThrust][lane] = engine(a, c_thr, at, mach, T, burn);
+    if (t + 1 < S) {
+      double sn, cn;
+      sincos(a.epa + kRot * kDt, &sn, &cn);
+      x[kXCe][lane] = cn;
+      x[kXSe][lane] = sn;
+    }
     __syncthreads();
     // ---- phase 4
+    const double vc = x[kXVc][lane], vg = x[kXVg][lane];
+    const double p = x[kXP][lane], q = x[kXQ][lane], r = x[kXR][lane];
     a.fuel -= burn;
     a.pa[0] = alpha; a.pa[1] = mach; a.pa[2] = vc; a.pa[3] = vg;
     a.pa[4] = npy; a.pa[5] = npz; a.pa[6] = p; a.pa[7] = q; a.pa[8] = r;
