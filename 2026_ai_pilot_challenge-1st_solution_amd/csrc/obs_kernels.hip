@@ -433,20 +433,57 @@ __device__ __forceinline__ void lane_build_obs(const Kin9& k, const Peer& p, con
   for (int i = 0; i < kActHist; ++i) put(o1, o2, vec_base(nvec) + i, r.act_hist[i * ld + a]);
 }
 
-// copy staged rows [0, n) of the tile to out[(a0 + row) * D ...], rows with keep[row] != 0 only
-// (keep == nullptr: all rows): row by row, the wave's lanes striding across the row in 8-byte
-// pieces (one contiguous 512-byte store per instruction)
+// Copy staged rows [0, n) of the tile to out[(a0 + row) * D ...]: row by row, the wave's lanes
+// striding across the row in 8-byte pieces (one contiguous 512-byte store per instruction).
+// Rows go to out1 where bit `row` of m1 is set and to out2 where bit `row` of m2 is set (wave-
+// uniform masks; out2 may be null).  Four rows' LDS reads are issued before their stores.
 template <int D>
-__device__ __forceinline__ void flush_rows(const float* S, long a0, int n,
-                                           const unsigned char* keep, float* __restrict__ out,
-                                           int lane) {
-  for (int r = 0; r < n; ++r) {
-    if (keep && !keep[r]) continue;                   // uniform across the wave
-    float* dst = out + (a0 + r) * D;
+__device__ __forceinline__ void flush_tile(const float* S, long a0, int n, uint64_t m1,
+                                           float* __restrict__ out1, uint64_t m2,
+                                           float* __restrict__ out2, int lane) {
+  constexpr int kPer = (D / 2 + kRowBlock - 1) / kRowBlock;   // 8-byte pieces per lane per row
+  if (!out2) m2 = 0;
+  const uint64_t any = m1 | m2;
+  for (int r0 = 0; r0 < n; r0 += 4) {
+    if (!((any >> r0) & 0xFull)) continue;                     // uniform
+    float2 v[4][kPer];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const float* src = S + (r0 + u) * kStagePitch;           // r0 + u < kRowBlock
+#pragma unroll
+      for (int q = 0; q < kPer; ++q) {
+        const int c = 2 * (lane + q * kRowBlock);
+        v[u][q] = c < D ? make_float2(src[c], src[c + 1]) : make_float2(0.0f, 0.0f);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int r = r0 + u;
+      if (r >= n) break;
+      const bool w1 = (m1 >> r) & 1, w2 = (m2 >> r) & 1;
+#pragma unroll
+      for (int q = 0; q < kPer; ++q) {
+        const int c = 2 * (lane + q * kRowBlock);
+        if (c < D) {
+          if (w1) *reinterpret_cast<float2*>(out1 + (a0 + r) * D + c) = v[u][q];
+          if (w2) *reinterpret_cast<float2*>(out2 + (a0 + r) * D + c) = v[u][q];
+        }
+      }
+    }
+  }
+}
+
+// The same for a sparse set of rows (autoreset rows): one row at a time, set bits only.
+template <int D>
+__device__ __forceinline__ void flush_sparse(const float* S, long a0, uint64_t m,
+                                             float* __restrict__ out, int lane) {
+  while (m) {
+    const int r = __builtin_ctzll(m);
+    m &= m - 1;
     const float* src = S + r * kStagePitch;
 #pragma unroll
     for (int c = 2 * lane; c < D; c += 2 * kRowBlock)
-      *reinterpret_cast<float2*>(dst + c) = make_float2(src[c], src[c + 1]);
+      *reinterpret_cast<float2*>(out + (a0 + r) * D + c) = make_float2(src[c], src[c + 1]);
   }
 }
 
@@ -503,7 +540,6 @@ __global__ __launch_bounds__(kRowBlock) void build_obs_kernel(
     const double* __restrict__ st, long ld, const unsigned char* __restrict__ mask, F16Recon r,
     Origin O, float* __restrict__ obs) {
   __shared__ float S[kRowBlock * kStagePitch];
-  __shared__ unsigned char keep[kRowBlock];
   const int lane = threadIdx.x;
   const long a0 = (long)blockIdx.x * kRowBlock, a = a0 + lane;
   const long nac = 2L * r.nenv;
@@ -520,9 +556,9 @@ __global__ __launch_bounds__(kRowBlock) void build_obs_kernel(
     const ObsIn in = load_obs_in(r, a, e);
     lane_build_obs(k, p, g, in, a, r, D, S + lane * kStagePitch, nullptr);
   }
-  keep[lane] = on ? 1 : 0;
+  const uint64_t keep = __ballot(on);
   __syncthreads();
-  flush_rows<D>(S, a0, n, keep, obs, lane);
+  flush_tile<D>(S, a0, n, keep, obs, 0, nullptr, lane);
 }
 
 template <int D>
@@ -530,7 +566,6 @@ __global__ __launch_bounds__(kRowBlock) void env_post_step_kernel(const F16EnvSt
                                                                    F16Recon r, F16RewardCfg c,
                                                                    Origin O) {
   __shared__ float S[kRowBlock * kStagePitch];
-  __shared__ unsigned char live[kRowBlock], fresh_row[kRowBlock];
   const int lane = threadIdx.x;
   const long a0 = (long)blockIdx.x * kRowBlock, a = a0 + lane;
   const long nac = 2L * r.nenv;
@@ -546,19 +581,30 @@ __global__ __launch_bounds__(kRowBlock) void env_post_step_kernel(const F16EnvSt
   Geo g;
   AdvOut o;
   if (on) {
+    // fields 0..14 (position .. fuel) feed the kinematics and the reward; they are read once
+    double f15[15];
+#pragma unroll
+    for (int f = 0; f < 15; ++f) f15[f] = st[f * ld + a];
     if (io.terminal_finite || io.finite_acc) {   // rl_env.py:545: every state value finite
+      // the other 86 fields with all their loads in flight together
       int fin = 1;
-      for (int f = 0; f < F16S_N; ++f) fin &= isfinite(st[f * ld + a]) ? 1 : 0;
+#pragma unroll
+      for (int f = 0; f < 15; ++f) fin &= isfinite(f15[f]) ? 1 : 0;
+      double v[F16S_N - 15];
+#pragma unroll
+      for (int j = 0; j < F16S_N - 15; ++j) v[j] = st[(15 + j) * ld + a];
+#pragma unroll
+      for (int j = 0; j < F16S_N - 15; ++j) fin &= isfinite(v[j]) ? 1 : 0;
       fin &= xchi(fin);
       if (!odd) {
         if (io.terminal_finite) io.terminal_finite[e] = (unsigned char)fin;
         if (io.finite_acc && !fin) io.finite_acc[e] = 0;
       }
     }
-    make_kin(st + a, ld, O, k);
+    make_kin(f15, 1, O, k);
     exchange(k, p);
     pair_geo(k, p, g);
-    o = lane_advance(k, p, g, a, e, io.actions, r, c, st[F16S_FUEL * ld + a]);
+    o = lane_advance(k, p, g, a, e, io.actions, r, c, f15[F16S_FUEL]);
     if (io.reward) io.reward[a] = o.reward;
     if (io.reward_f32) io.reward_f32[a] = (float)o.reward;
     d = o.term || o.trunc;
@@ -570,22 +616,20 @@ __global__ __launch_bounds__(kRowBlock) void env_post_step_kernel(const F16EnvSt
     }
     if (io.terminal_hp) io.terminal_hp[a] = o.obs.hp;
     if (io.terminal_alt_m) {
-      const double x = st[a], y = st[ld + a], z = st[2 * ld + a];
+      const double x = f15[0], y = f15[1], z = f15[2];
       io.terminal_alt_m[a] = (sqrt(x * x + y * y + z * z) - kSeaLevelRadiusFtT) * kFt2M;
     }
     // terminal observation (rl_env.py:552-554)
     lane_build_obs(k, p, g, o.obs, a, r, D, S + lane * kStagePitch, nullptr);
   }
-  live[lane] = (on && !d) ? 1 : 0;
-  fresh_row[lane] = (on && d) ? 1 : 0;
+  const uint64_t rows = __ballot(on), live = __ballot(on && !d), fresh = __ballot(on && d);
   __syncthreads();
   // every terminal row to terminal_obs; the live engagements' rows are also their observation
-  if (io.terminal_obs) {
-    flush_rows<D>(S, a0, n, nullptr, io.terminal_obs, lane);
-    flush_rows<D>(S, a0, n, live, io.obs, lane);
-  } else {
-    flush_rows<D>(S, a0, n, nullptr, io.obs, lane);
-  }
+  if (io.terminal_obs)
+    flush_tile<D>(S, a0, n, rows, io.terminal_obs, live, io.obs, lane);
+  else
+    flush_tile<D>(S, a0, n, rows, io.obs, 0, nullptr, lane);
+  if (!fresh) return;      // uniform: no autoreset in this wave
   __syncthreads();
   if (on && d) {           // autoreset from the initial-condition pool (rl_env.py:559-577)
     long pk;
@@ -643,7 +687,7 @@ __global__ __launch_bounds__(kRowBlock) void env_post_step_kernel(const F16EnvSt
     lane_build_obs(k2, p2, g2, fresh, a, r, D, S + lane * kStagePitch, nullptr);
   }
   __syncthreads();
-  flush_rows<D>(S, a0, n, fresh_row, io.obs, lane);
+  flush_sparse<D>(S, a0, fresh, io.obs, lane);
 }
 
 // rl_env.py:583-592 state9_flat: (nac, 9) float64 rows N/E/D m, roll/pitch/yaw deg, u/v/w m/s
