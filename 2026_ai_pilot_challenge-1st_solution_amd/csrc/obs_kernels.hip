@@ -132,42 +132,65 @@ struct AdvOut {
 
 // One decision of the reconstructor, termination and reward for this aircraft
 // (obs_reward.py:571-614 push_actions/advance, 747-819 compute_reward; rl_env.py:467-484).
+// Every reconstructor value the decision reads is loaded before anything is written back, so the
+// loads go out together.  With `row` set, the new action history is also written into the
+// aircraft's observation row at column `hist_col` (the observation built next reads it there).
 __device__ __forceinline__ AdvOut lane_advance(const Kin9& k, const Peer& p, const Geo& g, long a,
                                                long e, const double* __restrict__ act,
                                                const F16Recon& r, const F16RewardCfg& c,
-                                               double phys_fuel = 1.0) {
+                                               double phys_fuel = 1.0, float* row = nullptr,
+                                               int hist_col = 0) {
   const long ld = r.ld;
   AdvOut out;
-  // action history: roll by one decision, newest first
-  {
-    double h[16];
+  // ---- loads
+  double h[16];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) h[i] = r.act_hist[i * ld + a];
+  for (int i = 0; i < 16; ++i) h[i] = r.act_hist[i * ld + a];
+  double an[4];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) r.act_hist[(i + 4) * ld + a] = h[i];
+  for (int ch = 0; ch < 4; ++ch) an[ch] = act[4 * a + ch];
+  const double t_old = r.t_sec[e];
+  const double hp_before = r.hp[a];
+  const double fuel_before = r.fuel[a];
+  const bool prev_valid = r.prev_valid[a] != 0;
+  double patt[3], pvel[3] = {0.0, 0.0, 0.0};
 #pragma unroll
-    for (int ch = 0; ch < 4; ++ch) r.act_hist[ch * ld + a] = act[4 * a + ch];
+  for (int i = 0; i < 3; ++i) patt[i] = r.prev_att[i * ld + a];
+  if (r.accel) {
+#pragma unroll
+    for (int i = 0; i < 3; ++i) pvel[i] = r.prev_vel_ned[i * ld + a];
+  }
+  const bool pxv = r.prev_x_valid[a] != 0;
+  const double prev_x = r.prev_x[a];
+  const double prev_alt_log = r.prev_alt_log[a];
+  // ---- action history: roll by one decision, newest first
+#pragma unroll
+  for (int i = 0; i < 16; ++i) r.act_hist[(i + 4) * ld + a] = h[i];
+#pragma unroll
+  for (int ch = 0; ch < 4; ++ch) r.act_hist[ch * ld + a] = an[ch];
+  if (row) {
+#pragma unroll
+    for (int ch = 0; ch < 4; ++ch) row[hist_col + ch] = obs_value(an[ch]);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) row[hist_col + 4 + i] = obs_value(h[i]);
   }
   // damage exchanged inside the cones, rated at the time entering the decision
-  const double t_old = r.t_sec[e];
   const double dealt = damage_rate(g.dist * kM2FtObs, g.ata, t_old);
   const double taken = xch(dealt);
-  const double hp_before = r.hp[a];
   double hp = hp_before - taken * kDtStep;
   hp = hp < 0.0 ? 0.0 : hp;
   const double hp_loss = hp_before - hp;
   r.hp_loss[a] = hp_loss;
   r.hp[a] = hp;
   const double burn = kFuelBurn * (k.spd / kFuelRef);
-  double fuel = r.fuel[a] - burn * kDtStep;
+  double fuel = fuel_before - burn * kDtStep;
   fuel = fuel < 0.0 ? 0.0 : fuel;
   r.fuel[a] = fuel;
   // body rates from the attitude change since the previous decision
-  const bool prev_valid = r.prev_valid[a] != 0;
   double pqr[3] = {0.0, 0.0, 0.0};
   if (prev_valid) {
     Att P;
-    attitude_rpy(r.prev_att[a], r.prev_att[ld + a], r.prev_att[2 * ld + a], P);
+    attitude_rpy(patt[0], patt[1], patt[2], P);
     so3_rates(P.R, k.A.R, pqr);
   }
 #pragma unroll
@@ -179,7 +202,7 @@ __device__ __forceinline__ AdvOut lane_advance(const Kin9& k, const Peer& p, con
   if (r.accel) {   // 214-D lineage: NED acceleration from the velocity difference
 #pragma unroll
     for (int i = 0; i < 3; ++i) {
-      if (prev_valid) acc[i] = (k.vn[i] - r.prev_vel_ned[i * ld + a]) / kDtStep;
+      if (prev_valid) acc[i] = (k.vn[i] - pvel[i]) / kDtStep;
       r.accel[i * ld + a] = acc[i];
       r.prev_vel_ned[i * ld + a] = k.vn[i];
     }
@@ -204,10 +227,8 @@ __device__ __forceinline__ AdvOut lane_advance(const Kin9& k, const Peer& p, con
   const double G = clampd(s_own - s_opp, -1.0, 1.0);
   const double alt_log = altitude_log(alt_o);
   const double alt_log_t = xch(alt_log);
-  const bool pxv = r.prev_x_valid[a] != 0;
-  const double prev_x = r.prev_x[a];
   const double pxv_t = xch(pxv ? 1.0 : 0.0);
-  const double prev_alt_log_t = xch(r.prev_alt_log[a]);
+  const double prev_alt_log_t = xch(prev_alt_log);
   double r_shape;
   if (c.mode == 1) {
     r_shape = pxv_t != 0.0 ? (prev_alt_log_t - alt_log_t) * c.alt_hunt_coef : 0.0;
@@ -308,9 +329,11 @@ __device__ __forceinline__ void bank_of(const double R[3][3], const double F[3][
 
 // One observation row (obs_reward.py:617-723; 214-D: cuda_fdm/external_observation.cu).
 // Writes to o1 and, if non-null, o2.  All lanes of a pair must call it together.
+// hist: 0 = read the action history from the reconstructor, 1 = already in the row (written by
+// lane_advance), 2 = all zero (a row after an autoreset).
 __device__ __forceinline__ void lane_build_obs(const Kin9& k, const Peer& p, const Geo& g,
                                                const ObsIn& own, long a, const F16Recon& r,
-                                               int obs_dim, float* o1, float* o2) {
+                                               int obs_dim, float* o1, float* o2, int hist = 0) {
   const long ld = r.ld;
   const int nvec = obs_dim == 214 ? 9 : 7;
   // ---- vector block, frame by frame
@@ -429,44 +452,54 @@ __device__ __forceinline__ void lane_build_obs(const Kin9& k, const Peer& p, con
   put(o1, o2, j++, 2.0 * (pf_ata * pf_rng) - 1.0);
   put(o1, o2, j++, normz(own_alt, 0.0, 15000.0));
   put(o1, o2, j++, normz(tgt_alt, 0.0, 15000.0));
+  if (hist == 0) {
 #pragma unroll
-  for (int i = 0; i < kActHist; ++i) put(o1, o2, vec_base(nvec) + i, r.act_hist[i * ld + a]);
+    for (int i = 0; i < kActHist; ++i) put(o1, o2, vec_base(nvec) + i, r.act_hist[i * ld + a]);
+  } else if (hist == 2) {
+#pragma unroll
+    for (int i = 0; i < kActHist; ++i) put(o1, o2, vec_base(nvec) + i, 0.0);
+  }
 }
 
-// Copy staged rows [0, n) of the tile to out[(a0 + row) * D ...]: row by row, the wave's lanes
-// striding across the row in 8-byte pieces (one contiguous 512-byte store per instruction).
-// Rows go to out1 where bit `row` of m1 is set and to out2 where bit `row` of m2 is set (wave-
-// uniform masks; out2 may be null).  Four rows' LDS reads are issued before their stores.
+// Copy staged rows [0, n) of the tile to out[(a0 + row) * D ...].  Rows a0.. are one contiguous
+// range of the row-major matrix, so the tile is copied as a flat array: each lane moves W
+// consecutive floats of one row per step (W = 4 when D is a multiple of 4, else 2), 64 * W
+// contiguous floats per store instruction.  Rows go to out1 where bit `row` of m1 is set and to
+// out2 where bit `row` of m2 is set (wave-uniform masks; out2 may be null).  Four steps' LDS
+// reads are issued before their stores.
 template <int D>
 __device__ __forceinline__ void flush_tile(const float* S, long a0, int n, uint64_t m1,
                                            float* __restrict__ out1, uint64_t m2,
                                            float* __restrict__ out2, int lane) {
-  constexpr int kPer = (D / 2 + kRowBlock - 1) / kRowBlock;   // 8-byte pieces per lane per row
+  constexpr int W = (D % 4 == 0) ? 4 : 2;
   if (!out2) m2 = 0;
-  const uint64_t any = m1 | m2;
-  for (int r0 = 0; r0 < n; r0 += 4) {
-    if (!((any >> r0) & 0xFull)) continue;                     // uniform
-    float2 v[4][kPer];
+  const int total = n * D;                      // floats in the tile's valid rows
+  float* base1 = out1 + a0 * D;
+  float* base2 = out2 ? out2 + a0 * D : nullptr;
+  for (int f0 = 0; f0 < total; f0 += 4 * 64 * W) {
+    float v[4][W];
+    int fl[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const float* src = S + (r0 + u) * kStagePitch;           // r0 + u < kRowBlock
+      const int f = f0 + (u * 64 + lane) * W;
+      fl[u] = f;
+      const int row = f / D, col = f - row * D;
+      const float* src = S + (row < kRowBlock ? row : 0) * kStagePitch + col;
 #pragma unroll
-      for (int q = 0; q < kPer; ++q) {
-        const int c = 2 * (lane + q * kRowBlock);
-        v[u][q] = c < D ? make_float2(src[c], src[c + 1]) : make_float2(0.0f, 0.0f);
-      }
+      for (int w = 0; w < W; ++w) v[u][w] = src[w];
     }
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const int r = r0 + u;
-      if (r >= n) break;
-      const bool w1 = (m1 >> r) & 1, w2 = (m2 >> r) & 1;
-#pragma unroll
-      for (int q = 0; q < kPer; ++q) {
-        const int c = 2 * (lane + q * kRowBlock);
-        if (c < D) {
-          if (w1) *reinterpret_cast<float2*>(out1 + (a0 + r) * D + c) = v[u][q];
-          if (w2) *reinterpret_cast<float2*>(out2 + (a0 + r) * D + c) = v[u][q];
+      const int f = fl[u];
+      if (f < total) {
+        const int row = f / D;
+        if ((m1 >> row) & 1) {
+          if constexpr (W == 4) *reinterpret_cast<float4*>(base1 + f) = make_float4(v[u][0], v[u][1], v[u][2], v[u][3]);
+          else *reinterpret_cast<float2*>(base1 + f) = make_float2(v[u][0], v[u][1]);
+        }
+        if ((m2 >> row) & 1) {
+          if constexpr (W == 4) *reinterpret_cast<float4*>(base2 + f) = make_float4(v[u][0], v[u][1], v[u][2], v[u][3]);
+          else *reinterpret_cast<float2*>(base2 + f) = make_float2(v[u][0], v[u][1]);
         }
       }
     }
@@ -604,7 +637,8 @@ __global__ __launch_bounds__(kRowBlock) void env_post_step_kernel(const F16EnvSt
     make_kin(f15, 1, O, k);
     exchange(k, p);
     pair_geo(k, p, g);
-    o = lane_advance(k, p, g, a, e, io.actions, r, c, f15[F16S_FUEL]);
+    o = lane_advance(k, p, g, a, e, io.actions, r, c, f15[F16S_FUEL], S + lane * kStagePitch,
+                     vec_base(D == 214 ? 9 : 7));
     if (io.reward) io.reward[a] = o.reward;
     if (io.reward_f32) io.reward_f32[a] = (float)o.reward;
     d = o.term || o.trunc;
@@ -620,7 +654,7 @@ __global__ __launch_bounds__(kRowBlock) void env_post_step_kernel(const F16EnvSt
       io.terminal_alt_m[a] = (sqrt(x * x + y * y + z * z) - kSeaLevelRadiusFtT) * kFt2M;
     }
     // terminal observation (rl_env.py:552-554)
-    lane_build_obs(k, p, g, o.obs, a, r, D, S + lane * kStagePitch, nullptr);
+    lane_build_obs(k, p, g, o.obs, a, r, D, S + lane * kStagePitch, nullptr, 1);
   }
   const uint64_t rows = __ballot(on), live = __ballot(on && !d), fresh = __ballot(on && d);
   __syncthreads();
@@ -684,7 +718,7 @@ __global__ __launch_bounds__(kRowBlock) void env_post_step_kernel(const F16EnvSt
     ObsIn fresh;
     fresh.hp = 1.0; fresh.fuel = 1.0; fresh.dealt = 0.0; fresh.taken = 0.0; fresh.t = 0.0;
     for (int i = 0; i < 3; ++i) { fresh.pqr[i] = 0.0; fresh.accel[i] = 0.0; }
-    lane_build_obs(k2, p2, g2, fresh, a, r, D, S + lane * kStagePitch, nullptr);
+    lane_build_obs(k2, p2, g2, fresh, a, r, D, S + lane * kStagePitch, nullptr, 2);
   }
   __syncthreads();
   flush_sparse<D>(S, a0, fresh, io.obs, lane);
@@ -733,6 +767,11 @@ static int check_recon(const F16Recon* r, bool need_accel) {
   if ((r->accel == nullptr) != (r->prev_vel_ned == nullptr)) return F16_EINVAL;
   if (need_accel && !r->accel) return F16_EINVAL;
   return 0;
+}
+
+// Observation matrices are written 16 bytes (184-D) or 8 bytes (214-D) per lane and step.
+static bool rows_aligned(const float* p, int obs_dim) {
+  return ((uintptr_t)p & (obs_dim % 4 == 0 ? 15u : 7u)) == 0;
 }
 
 static int check_cfg(const F16RewardCfg* c) {
@@ -784,6 +823,7 @@ extern "C" int f16_obr_build_obs(const double* states, long ld, const unsigned c
   if (rc) return rc;
   if (rec->nenv == 0) return 0;
   if (!states || !obs || ld < 2L * rec->nenv) return F16_EINVAL;
+  if (!rows_aligned(obs, obs_dim)) return F16_EINVAL;
   if (obs_dim == 184)
     hipLaunchKernelGGL(build_obs_kernel<184>, grid_rows(rec->nenv), dim3(kRowBlock), 0,
                        (hipStream_t)stream, states, ld, env_mask, *rec, origin(), obs);
@@ -805,6 +845,9 @@ extern "C" int f16_env_post_step(const F16EnvStepIO* io, const F16Recon* rec,
       io->pool_size > 0xffffffffL || io->ld < 2L * rec->nenv || rec->ld != io->ld)
     return F16_EINVAL;
   if (io->opp_assign && (!io->opp_cdf || io->n_opp < 1)) return F16_EINVAL;
+  if (!rows_aligned(io->obs, io->obs_dim) ||
+      (io->terminal_obs && !rows_aligned(io->terminal_obs, io->obs_dim)))
+    return F16_EINVAL;
   if (io->obs_dim == 184)
     hipLaunchKernelGGL(env_post_step_kernel<184>, grid_rows(rec->nenv), dim3(kRowBlock), 0,
                        (hipStream_t)stream, *io, *rec, *cfg, origin());

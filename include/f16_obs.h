@@ -71,7 +71,8 @@ int f16_obr_init_reward(const double *states, long ld, const unsigned char *env_
 
 /* BatchObsReward.kernel_build_obs (obs_reward.py:454-469) and, for obs_dim 214, the external
  * 214-D observation (obs_reward.py:487-496, external_observation.cu): write the observation rows
- * of the engagements selected by env_mask (NULL = all).  214 needs rec->accel. */
+ * of the engagements selected by env_mask (NULL = all).  214 needs rec->accel.  obs must be
+ * 16-byte aligned for 184 and 8-byte aligned for 214 (as any tensor allocation is). */
 int f16_obr_build_obs(const double *states, long ld, const unsigned char *env_mask,
                       const F16Recon *rec, int obs_dim, float *obs, void *stream);
 
@@ -114,7 +115,7 @@ typedef struct F16EnvStepIO {
  * the reconstructor is reset, the reward state re-anchored and the observation rebuilt; live
  * engagements keep the terminal observation in `obs`.  A pick outside [0, pool_size) fills that
  * engagement's states with NaN so the error surfaces as a non-finite state instead of an
- * out-of-bounds read. */
+ * out-of-bounds read.  obs and terminal_obs: 16-byte aligned for 184, 8-byte for 214. */
 int f16_env_post_step(const F16EnvStepIO *io, const F16Recon *rec, const F16RewardCfg *cfg,
                       void *stream);
 
