@@ -32,7 +32,7 @@ PEAK_HBM_GBS = 8000.0
 REF_PUBLISHED_SUBSTEPS = 37.0e6
 
 
-def profiled_traffic(name="fdm_step_kernel_tailchase16k.md"):
+def profiled_traffic(name="fdm_step_split_kernel_tailchase16k.md"):
     """HBM bytes per launch measured by rocprofv3 FETCH_SIZE/WRITE_SIZE (copy-calibrated) and
     recorded in the kernel's profile summary; None when no summary is present."""
     path = os.path.join(ROOT, "profiles", name)
@@ -329,7 +329,7 @@ def main():
         "league": league_line,
         "roofline": {"bound": "valu", "achieved": achieved, "peak": PEAK_FP64_TFLOPS,
                      "unit": "TFLOP/s", "frac": achieved / PEAK_FP64_TFLOPS, "traffic": profiled_traffic(),
-                     "kernel": "fdm_step_kernel<120>", "kernel_ms": kern_ms,
+                     "kernel": "fdm_step_split_kernel<120>", "kernel_ms": kern_ms,
                      "flop_per_launch": flop_launch},
         "wall_s": wall,
     }
