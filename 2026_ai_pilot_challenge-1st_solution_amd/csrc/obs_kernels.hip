@@ -23,12 +23,13 @@
 namespace f16obs {
 
 constexpr int kObsBlock = 256;
-// Kernels that write observation rows run one wave per workgroup: each lane builds its row in a
-// wave-private LDS tile (odd pitch: lane-per-row stores hit distinct banks), then the wave copies
-// the tile out as consecutive 8-byte pieces -- its 64 rows are one contiguous range of the
-// row-major observation matrix, so the stores coalesce instead of striding by a row per lane.
+// Kernels that write observation rows run one wave per workgroup: each lane builds the vector
+// block of its row (the 114 or 144 columns the frames produce out of order) in a wave-private
+// LDS tile (odd pitch: lane-per-row stores hit distinct banks), then the wave copies the tile
+// out in consecutive 8-byte pieces; the rows' scalar block and action history are contiguous
+// and go out from registers.  The tile is 29 KB (184-D) or 37 KB (214-D), so four wavefronts
+// fit a CU's LDS.
 constexpr int kRowBlock = 64;
-constexpr int kStagePitch = 215;     // >= 214, odd
 constexpr double kFuelBurn = 8.0e-5;          // fuel proxy burn per second at 300 m/s
 constexpr double kFuelRef = 300.0;
 constexpr double kSeaLevelRadiusFtT = 20925646.32546;
@@ -127,19 +128,18 @@ __device__ __forceinline__ void lane_init_reward(const Kin9& k, const Peer& p, c
 struct AdvOut {
   double reward;
   bool term, trunc;
-  ObsIn obs;        // this aircraft's reconstructor values after the update
+  ObsIn obs;                // this aircraft's reconstructor values after the update
+  float hist[kActHist];     // the new action history as observation features
 };
 
 // One decision of the reconstructor, termination and reward for this aircraft
 // (obs_reward.py:571-614 push_actions/advance, 747-819 compute_reward; rl_env.py:467-484).
 // Every reconstructor value the decision reads is loaded before anything is written back, so the
-// loads go out together.  With `row` set, the new action history is also written into the
-// aircraft's observation row at column `hist_col` (the observation built next reads it there).
+// loads go out together.  The new action history is also returned as observation features.
 __device__ __forceinline__ AdvOut lane_advance(const Kin9& k, const Peer& p, const Geo& g, long a,
                                                long e, const double* __restrict__ act,
                                                const F16Recon& r, const F16RewardCfg& c,
-                                               double phys_fuel = 1.0, float* row = nullptr,
-                                               int hist_col = 0) {
+                                               double phys_fuel = 1.0) {
   const long ld = r.ld;
   AdvOut out;
   // ---- loads
@@ -168,12 +168,10 @@ __device__ __forceinline__ AdvOut lane_advance(const Kin9& k, const Peer& p, con
   for (int i = 0; i < 16; ++i) r.act_hist[(i + 4) * ld + a] = h[i];
 #pragma unroll
   for (int ch = 0; ch < 4; ++ch) r.act_hist[ch * ld + a] = an[ch];
-  if (row) {
 #pragma unroll
-    for (int ch = 0; ch < 4; ++ch) row[hist_col + ch] = obs_value(an[ch]);
+  for (int ch = 0; ch < 4; ++ch) out.hist[ch] = obs_value(an[ch]);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) row[hist_col + 4 + i] = obs_value(h[i]);
-  }
+  for (int i = 0; i < 16; ++i) out.hist[4 + i] = obs_value(h[i]);
   // damage exchanged inside the cones, rated at the time entering the decision
   const double dealt = damage_rate(g.dist * kM2FtObs, g.ata, t_old);
   const double taken = xch(dealt);
@@ -275,10 +273,58 @@ __device__ __forceinline__ double gauss_feat(double z) {      // e^{-z^2}
   return __builtin_amdgcn_exp2f(-(zf * zf) * 1.4426950408889634f);
 }
 
-__device__ __forceinline__ void put(float* o1, float* o2, int j, double v) {
-  const float f = obs_value(v);
-  o1[j] = f;
-  if (o2) o2[j] = f;
+// Where one observation row goes.  Rows are built lane-per-row in a wave-private LDS tile and
+// copied out coalesced by the wave (the frames produce the vector block's columns out of
+// order).  Two tile layouts:
+//   FULL:  the whole row is staged (pitch D | 1); the wave copies the tile as one flat array.
+//          Fastest while every wavefront of the launch is resident at once.
+//   !FULL: only the vector block, columns [50, D - 20), is staged (pitch (D - 70) | 1, 29 KB
+//          for 184-D, 37 KB for 214-D, so four wavefronts fit a CU's LDS); the scalar block
+//          and the action history, 50 + 20 contiguous floats, are stored by the lane straight
+//          from registers to `row_all` and, when set, `row_live` (rows of the output matrices,
+//          16-byte aligned for D = 184, 8-byte for D = 214).  Used for launches larger than
+//          the FULL tile lets the GPU hold.
+// `tile` = this lane's tile row, holding column tile_col0<FULL>() at tile[0].
+struct ObsOut {
+  float* tile;
+  float* row_all;
+  float* row_live;
+};
+
+constexpr int kVecCol0 = 50;                      // first vector-block column
+template <int D, bool FULL> constexpr int tile_pitch() { return FULL ? (D | 1) : ((D - 70) | 1); }
+template <bool FULL> constexpr int tile_col0() { return FULL ? 0 : kVecCol0; }
+
+// n consecutive floats of a row, from registers, at column C0: 16-byte stores where the row
+// layout allows (D and C0 multiples of 4), 8-byte otherwise.
+template <int D, int C0, int N>
+__device__ __forceinline__ void store_run(float* row, const float (&v)[N]) {
+  static_assert(N % 2 == 0 && C0 % 2 == 0, "even runs at even columns");
+  int i = 0;
+  if constexpr (D % 4 == 0 && C0 % 4 == 0) {
+#pragma unroll
+    for (; i + 4 <= N; i += 4)
+      *reinterpret_cast<float4*>(row + C0 + i) = make_float4(v[i], v[i + 1], v[i + 2], v[i + 3]);
+  }
+#pragma unroll
+  for (; i < N; i += 2) *reinterpret_cast<float2*>(row + C0 + i) = make_float2(v[i], v[i + 1]);
+}
+
+// A contiguous run of the row outside the vector block: into the tile (FULL) or to the rows.
+template <int D, bool FULL, int C0, int N>
+__device__ __forceinline__ void store_run2(const ObsOut& out, const float (&v)[N]) {
+  if constexpr (FULL) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) out.tile[C0 + i] = v[i];
+  } else {
+    store_run<D, C0, N>(out.row_all, v);
+    if (out.row_live) store_run<D, C0, N>(out.row_live, v);
+  }
+}
+
+template <bool FULL>
+__device__ __forceinline__ void put_vec(float* tile, int j, double v) {
+  tile[j - tile_col0<FULL>()] = obs_value(v);
 }
 
 enum VecKind { kRaw = 0, kVel = 1, kRate = 2, kAcc = 3 };
@@ -305,8 +351,8 @@ __device__ __forceinline__ double vec_feature(double x, int kind) {
 }
 
 // Frame f applied to every vector that uses it (frame-major, so only one frame is live at a time)
-template <int F>
-__device__ __forceinline__ void emit_frame(float* o1, float* o2, const double Fm[3][3],
+template <int F, bool FULL>
+__device__ __forceinline__ void emit_frame(float* vec, const double Fm[3][3],
                                            const double (&V)[9][3], int nvec) {
 #pragma unroll
   for (int s = 0; s < 9; ++s) {
@@ -314,7 +360,8 @@ __device__ __forceinline__ void emit_frame(float* o1, float* o2, const double Fm
     double comp[3];
     mv3(Fm, V[s], comp);
 #pragma unroll
-    for (int q = 0; q < 3; ++q) put(o1, o2, vec_col(s, F) + q, vec_feature(comp[q], kVecs[s].kind));
+    for (int q = 0; q < 3; ++q)
+      put_vec<FULL>(vec, vec_col(s, F) + q, vec_feature(comp[q], kVecs[s].kind));
   }
 }
 
@@ -327,15 +374,17 @@ __device__ __forceinline__ void bank_of(const double R[3][3], const double F[3][
   sc_atan2(y2, y1, s, co);                   // sin, cos of atan2(y2, y1)
 }
 
-// One observation row (obs_reward.py:617-723; 214-D: cuda_fdm/external_observation.cu).
-// Writes to o1 and, if non-null, o2.  All lanes of a pair must call it together.
-// hist: 0 = read the action history from the reconstructor, 1 = already in the row (written by
+// One observation row (obs_reward.py:617-723; 214-D: cuda_fdm/external_observation.cu) to
+// `out`.  All lanes of a pair must call it together.
+// hist: 0 = read the action history from the reconstructor, 1 = already stored (by
 // lane_advance), 2 = all zero (a row after an autoreset).
+template <int D, bool FULL>
 __device__ __forceinline__ void lane_build_obs(const Kin9& k, const Peer& p, const Geo& g,
                                                const ObsIn& own, long a, const F16Recon& r,
-                                               int obs_dim, float* o1, float* o2, int hist = 0) {
+                                               const ObsOut& out, int hist = 0) {
   const long ld = r.ld;
-  const int nvec = obs_dim == 214 ? 9 : 7;
+  constexpr int nvec = D == 214 ? 9 : 7;
+  float* o1 = out.tile;
   // ---- vector block, frame by frame
   double V[9][3];
   const bool los_ok = g.dist > 1e-6;
@@ -353,24 +402,24 @@ __device__ __forceinline__ void lane_build_obs(const Kin9& k, const Peer& p, con
   for (int i = 0; i < 3; ++i) { V[6][i] = xch(V[5][i]); V[8][i] = xch(own.accel[i]); }
   {
     const double I3[3][3] = {{1.0, 0.0, 0.0}, {0.0, 1.0, 0.0}, {0.0, 0.0, 1.0}};
-    emit_frame<0>(o1, o2, I3, V, nvec);
+    emit_frame<0, FULL>(o1, I3, V, nvec);
   }
-  emit_frame<1>(o1, o2, k.A.R, V, nvec);
-  emit_frame<2>(o1, o2, p.R, V, nvec);
+  emit_frame<1, FULL>(o1, k.A.R, V, nvec);
+  emit_frame<2, FULL>(o1, p.R, V, nvec);
   double bs, bc, tbs, tbc;
   {
     double Fm[3][3];
     dir_frame(k.vn, Fm);                                           // own motion frame
     bank_of(k.A.R, Fm, bs, bc);
-    emit_frame<3>(o1, o2, Fm, V, nvec);
+    emit_frame<3, FULL>(o1, Fm, V, nvec);
     tbs = xch(bs); tbc = xch(bc);
 #pragma unroll
     for (int i = 0; i < 3; ++i)
 #pragma unroll
       for (int q = 0; q < 3; ++q) Fm[i][q] = xch(Fm[i][q]);           // partner's motion frame
-    emit_frame<4>(o1, o2, Fm, V, nvec);
+    emit_frame<4, FULL>(o1, Fm, V, nvec);
     dir_frame(g.delta, Fm);                                        // line-of-sight frame
-    emit_frame<5>(o1, o2, Fm, V, nvec);
+    emit_frame<5, FULL>(o1, Fm, V, nvec);
   }
   // ---- scalars [0, 50)
   ObsIn tgt;
@@ -413,69 +462,70 @@ __device__ __forceinline__ void lane_build_obs(const Kin9& k, const Peer& p, con
   pf_ata = pf_ata < 0.0 ? 0.0 : pf_ata;
   double pf_rng = 1.0 - g.dist / 3000.0;
   pf_rng = pf_rng < 0.0 ? 0.0 : pf_rng;
+  float sc[kVecCol0];
   int j = 0;
-  put(o1, o2, j++, normz(k.spd, 0.0, 600.0));
-  put(o1, o2, j++, normz(p.spd, 0.0, 600.0));
-  put(o1, o2, j++, tanh_feat(aoa / 30.0));
-  put(o1, o2, j++, tanh_feat(ss / 15.0));
-  put(o1, o2, j++, tanh_feat((own_alt - kMinAltM) / 300.0));
-  put(o1, o2, j++, normz(-k.vn[2], -100.0, 100.0));
-  put(o1, o2, j++, normz(own.hp, 0.0, 1.0));
-  put(o1, o2, j++, normz(tgt.hp, 0.0, 1.0));
-  put(o1, o2, j++, own.hp - tgt.hp);
-  put(o1, o2, j++, e_adv / (fabs(e_adv) + 5000.0));
-  put(o1, o2, j++, normz(g.dist, 0.0, 2500.0));
-  put(o1, o2, j++, normz(closure, -1000.0, 1000.0));
-  put(o1, o2, j++, s_ata); put(o1, o2, j++, c_ata);
-  put(o1, o2, j++, s_aa); put(o1, o2, j++, c_aa);
-  put(o1, o2, j++, s_az); put(o1, o2, j++, c_az);
-  put(o1, o2, j++, s_el); put(o1, o2, j++, c_el);
-  put(o1, o2, j++, 2.0 * gauss_feat(g.ata / 3.0) - 1.0);
-  put(o1, o2, j++, tanh_feat((cone - fabs(g.ata)) / cc));
-  put(o1, o2, j++, 2.0 * gauss_feat(en_ata / 3.0) - 1.0);
-  put(o1, o2, j++, tanh_feat((cone - fabs(en_ata)) / cc));
-  put(o1, o2, j++, tanh_feat((g.dist - min_r) / span));
-  put(o1, o2, j++, tanh_feat((max_r - g.dist) / span));
-  put(o1, o2, j++, normz(t, 0.0, 200.0));
-  put(o1, o2, j++, k.A.sr); put(o1, o2, j++, k.A.cr);
-  put(o1, o2, j++, k.A.sp); put(o1, o2, j++, k.A.cp);
-  put(o1, o2, j++, k.A.sy); put(o1, o2, j++, k.A.cy);
-  put(o1, o2, j++, p.sr); put(o1, o2, j++, p.cr);
-  put(o1, o2, j++, p.sp); put(o1, o2, j++, p.cp);
-  put(o1, o2, j++, p.sy); put(o1, o2, j++, p.cy);
-  put(o1, o2, j++, bs); put(o1, o2, j++, bc);
-  put(o1, o2, j++, tbs); put(o1, o2, j++, tbc);
-  put(o1, o2, j++, normz(own.fuel, 0.0, 1.0));
-  put(o1, o2, j++, normz(tgt.fuel, 0.0, 1.0));
-  put(o1, o2, j++, clampd(2.0 * own.dealt - 1.0, -1.0, 1.0));
-  put(o1, o2, j++, clampd(2.0 * own.taken - 1.0, -1.0, 1.0));
-  put(o1, o2, j++, 2.0 * (pf_ata * pf_rng) - 1.0);
-  put(o1, o2, j++, normz(own_alt, 0.0, 15000.0));
-  put(o1, o2, j++, normz(tgt_alt, 0.0, 15000.0));
-  if (hist == 0) {
+  sc[j++] = obs_value(normz(k.spd, 0.0, 600.0));
+  sc[j++] = obs_value(normz(p.spd, 0.0, 600.0));
+  sc[j++] = obs_value(tanh_feat(aoa / 30.0));
+  sc[j++] = obs_value(tanh_feat(ss / 15.0));
+  sc[j++] = obs_value(tanh_feat((own_alt - kMinAltM) / 300.0));
+  sc[j++] = obs_value(normz(-k.vn[2], -100.0, 100.0));
+  sc[j++] = obs_value(normz(own.hp, 0.0, 1.0));
+  sc[j++] = obs_value(normz(tgt.hp, 0.0, 1.0));
+  sc[j++] = obs_value(own.hp - tgt.hp);
+  sc[j++] = obs_value(e_adv / (fabs(e_adv) + 5000.0));
+  sc[j++] = obs_value(normz(g.dist, 0.0, 2500.0));
+  sc[j++] = obs_value(normz(closure, -1000.0, 1000.0));
+  sc[j++] = obs_value(s_ata); sc[j++] = obs_value(c_ata);
+  sc[j++] = obs_value(s_aa); sc[j++] = obs_value(c_aa);
+  sc[j++] = obs_value(s_az); sc[j++] = obs_value(c_az);
+  sc[j++] = obs_value(s_el); sc[j++] = obs_value(c_el);
+  sc[j++] = obs_value(2.0 * gauss_feat(g.ata / 3.0) - 1.0);
+  sc[j++] = obs_value(tanh_feat((cone - fabs(g.ata)) / cc));
+  sc[j++] = obs_value(2.0 * gauss_feat(en_ata / 3.0) - 1.0);
+  sc[j++] = obs_value(tanh_feat((cone - fabs(en_ata)) / cc));
+  sc[j++] = obs_value(tanh_feat((g.dist - min_r) / span));
+  sc[j++] = obs_value(tanh_feat((max_r - g.dist) / span));
+  sc[j++] = obs_value(normz(t, 0.0, 200.0));
+  sc[j++] = obs_value(k.A.sr); sc[j++] = obs_value(k.A.cr);
+  sc[j++] = obs_value(k.A.sp); sc[j++] = obs_value(k.A.cp);
+  sc[j++] = obs_value(k.A.sy); sc[j++] = obs_value(k.A.cy);
+  sc[j++] = obs_value(p.sr); sc[j++] = obs_value(p.cr);
+  sc[j++] = obs_value(p.sp); sc[j++] = obs_value(p.cp);
+  sc[j++] = obs_value(p.sy); sc[j++] = obs_value(p.cy);
+  sc[j++] = obs_value(bs); sc[j++] = obs_value(bc);
+  sc[j++] = obs_value(tbs); sc[j++] = obs_value(tbc);
+  sc[j++] = obs_value(normz(own.fuel, 0.0, 1.0));
+  sc[j++] = obs_value(normz(tgt.fuel, 0.0, 1.0));
+  sc[j++] = obs_value(clampd(2.0 * own.dealt - 1.0, -1.0, 1.0));
+  sc[j++] = obs_value(clampd(2.0 * own.taken - 1.0, -1.0, 1.0));
+  sc[j++] = obs_value(2.0 * (pf_ata * pf_rng) - 1.0);
+  sc[j++] = obs_value(normz(own_alt, 0.0, 15000.0));
+  sc[j++] = obs_value(normz(tgt_alt, 0.0, 15000.0));
+  store_run2<D, FULL, 0, kVecCol0>(out, sc);
+  if (hist != 1) {
+    float h[kActHist];
 #pragma unroll
-    for (int i = 0; i < kActHist; ++i) put(o1, o2, vec_base(nvec) + i, r.act_hist[i * ld + a]);
-  } else if (hist == 2) {
-#pragma unroll
-    for (int i = 0; i < kActHist; ++i) put(o1, o2, vec_base(nvec) + i, 0.0);
+    for (int i = 0; i < kActHist; ++i) h[i] = hist == 0 ? obs_value(r.act_hist[i * ld + a]) : 0.0f;
+    store_run2<D, FULL, vec_base(nvec), kActHist>(out, h);
   }
 }
 
-// Copy staged rows [0, n) of the tile to out[(a0 + row) * D ...].  Rows a0.. are one contiguous
-// range of the row-major matrix, so the tile is copied as a flat array: each lane moves W
-// consecutive floats of one row per step (W = 4 when D is a multiple of 4, else 2), 64 * W
-// contiguous floats per store instruction.  Rows go to out1 where bit `row` of m1 is set and to
-// out2 where bit `row` of m2 is set (wave-uniform masks; out2 may be null).  Four steps' LDS
-// reads are issued before their stores.
-template <int D>
+// Copy the staged tile rows [0, n) out: the tile is walked as a flat array of n * Wt floats
+// (Wt = D for FULL, D - 70 for the vector block), each lane moving W consecutive floats of one
+// row per step (W = 4 for FULL 184-D, whose rows are 16-byte aligned, else 2), so every store
+// instruction covers 64 * W consecutive floats of the destination (rows a0.. are contiguous
+// there when FULL; the vector-block segments are when !FULL).  Rows go to out1 where bit `row`
+// of m1 is set and to out2 where bit `row` of m2 is set (wave-uniform masks; out2 may be null).
+// Four steps' LDS reads are issued before their stores.
+template <int D, bool FULL>
 __device__ __forceinline__ void flush_tile(const float* S, long a0, int n, uint64_t m1,
                                            float* __restrict__ out1, uint64_t m2,
                                            float* __restrict__ out2, int lane) {
-  constexpr int W = (D % 4 == 0) ? 4 : 2;
+  constexpr int Wt = FULL ? D : D - 70, P = tile_pitch<D, FULL>(), C0 = tile_col0<FULL>();
+  constexpr int W = (FULL && D % 4 == 0) ? 4 : 2;
   if (!out2) m2 = 0;
-  const int total = n * D;                      // floats in the tile's valid rows
-  float* base1 = out1 + a0 * D;
-  float* base2 = out2 ? out2 + a0 * D : nullptr;
+  const int total = n * Wt;
   for (int f0 = 0; f0 < total; f0 += 4 * 64 * W) {
     float v[4][W];
     int fl[4];
@@ -483,8 +533,8 @@ __device__ __forceinline__ void flush_tile(const float* S, long a0, int n, uint6
     for (int u = 0; u < 4; ++u) {
       const int f = f0 + (u * 64 + lane) * W;
       fl[u] = f;
-      const int row = f / D, col = f - row * D;
-      const float* src = S + (row < kRowBlock ? row : 0) * kStagePitch + col;
+      const int row = f / Wt, col = f - row * Wt;
+      const float* src = S + (row < kRowBlock ? row : 0) * P + col;
 #pragma unroll
       for (int w = 0; w < W; ++w) v[u][w] = src[w];
     }
@@ -492,14 +542,16 @@ __device__ __forceinline__ void flush_tile(const float* S, long a0, int n, uint6
     for (int u = 0; u < 4; ++u) {
       const int f = fl[u];
       if (f < total) {
-        const int row = f / D;
-        if ((m1 >> row) & 1) {
-          if constexpr (W == 4) *reinterpret_cast<float4*>(base1 + f) = make_float4(v[u][0], v[u][1], v[u][2], v[u][3]);
-          else *reinterpret_cast<float2*>(base1 + f) = make_float2(v[u][0], v[u][1]);
-        }
-        if ((m2 >> row) & 1) {
-          if constexpr (W == 4) *reinterpret_cast<float4*>(base2 + f) = make_float4(v[u][0], v[u][1], v[u][2], v[u][3]);
-          else *reinterpret_cast<float2*>(base2 + f) = make_float2(v[u][0], v[u][1]);
+        const int row = f / Wt, col = f - row * Wt;
+        const long off = (a0 + row) * D + C0 + col;
+        if constexpr (W == 4) {
+          const float4 x = make_float4(v[u][0], v[u][1], v[u][2], v[u][3]);
+          if ((m1 >> row) & 1) *reinterpret_cast<float4*>(out1 + off) = x;
+          if ((m2 >> row) & 1) *reinterpret_cast<float4*>(out2 + off) = x;
+        } else {
+          const float2 x = make_float2(v[u][0], v[u][1]);
+          if ((m1 >> row) & 1) *reinterpret_cast<float2*>(out1 + off) = x;
+          if ((m2 >> row) & 1) *reinterpret_cast<float2*>(out2 + off) = x;
         }
       }
     }
@@ -507,16 +559,17 @@ __device__ __forceinline__ void flush_tile(const float* S, long a0, int n, uint6
 }
 
 // The same for a sparse set of rows (autoreset rows): one row at a time, set bits only.
-template <int D>
+template <int D, bool FULL>
 __device__ __forceinline__ void flush_sparse(const float* S, long a0, uint64_t m,
                                              float* __restrict__ out, int lane) {
+  constexpr int Wt = FULL ? D : D - 70, P = tile_pitch<D, FULL>(), C0 = tile_col0<FULL>();
   while (m) {
     const int r = __builtin_ctzll(m);
     m &= m - 1;
-    const float* src = S + r * kStagePitch;
+    const float* src = S + r * P;
 #pragma unroll
-    for (int c = 2 * lane; c < D; c += 2 * kRowBlock)
-      *reinterpret_cast<float2*>(out + (a0 + r) * D + c) = make_float2(src[c], src[c + 1]);
+    for (int c = 2 * lane; c < Wt; c += 2 * kRowBlock)
+      *reinterpret_cast<float2*>(out + (a0 + r) * D + C0 + c) = make_float2(src[c], src[c + 1]);
   }
 }
 
@@ -568,11 +621,11 @@ __global__ __launch_bounds__(kObsBlock) void init_reward_kernel(
   lane_init_reward(k, p, g, a, r.t_sec[e], r);
 }
 
-template <int D>
+template <int D, bool FULL>
 __global__ __launch_bounds__(kRowBlock) void build_obs_kernel(
     const double* __restrict__ st, long ld, const unsigned char* __restrict__ mask, F16Recon r,
     Origin O, float* __restrict__ obs) {
-  __shared__ float S[kRowBlock * kStagePitch];
+  __shared__ float S[kRowBlock * tile_pitch<D, FULL>()];
   const int lane = threadIdx.x;
   const long a0 = (long)blockIdx.x * kRowBlock, a = a0 + lane;
   const long nac = 2L * r.nenv;
@@ -587,18 +640,19 @@ __global__ __launch_bounds__(kRowBlock) void build_obs_kernel(
     Geo g;
     pair_geo(k, p, g);
     const ObsIn in = load_obs_in(r, a, e);
-    lane_build_obs(k, p, g, in, a, r, D, S + lane * kStagePitch, nullptr);
+    lane_build_obs<D, FULL>(k, p, g, in, a, r,
+                            ObsOut{S + lane * tile_pitch<D, FULL>(), obs + a * D, nullptr});
   }
   const uint64_t keep = __ballot(on);
   __syncthreads();
-  flush_tile<D>(S, a0, n, keep, obs, 0, nullptr, lane);
+  flush_tile<D, FULL>(S, a0, n, keep, obs, 0, nullptr, lane);
 }
 
-template <int D>
+template <int D, bool FULL>
 __global__ __launch_bounds__(kRowBlock) void env_post_step_kernel(const F16EnvStepIO io,
                                                                    F16Recon r, F16RewardCfg c,
                                                                    Origin O) {
-  __shared__ float S[kRowBlock * kStagePitch];
+  __shared__ float S[kRowBlock * tile_pitch<D, FULL>()];
   const int lane = threadIdx.x;
   const long a0 = (long)blockIdx.x * kRowBlock, a = a0 + lane;
   const long nac = 2L * r.nenv;
@@ -637,8 +691,7 @@ __global__ __launch_bounds__(kRowBlock) void env_post_step_kernel(const F16EnvSt
     make_kin(f15, 1, O, k);
     exchange(k, p);
     pair_geo(k, p, g);
-    o = lane_advance(k, p, g, a, e, io.actions, r, c, f15[F16S_FUEL], S + lane * kStagePitch,
-                     vec_base(D == 214 ? 9 : 7));
+    o = lane_advance(k, p, g, a, e, io.actions, r, c, f15[F16S_FUEL]);
     if (io.reward) io.reward[a] = o.reward;
     if (io.reward_f32) io.reward_f32[a] = (float)o.reward;
     d = o.term || o.trunc;
@@ -653,16 +706,20 @@ __global__ __launch_bounds__(kRowBlock) void env_post_step_kernel(const F16EnvSt
       const double x = f15[0], y = f15[1], z = f15[2];
       io.terminal_alt_m[a] = (sqrt(x * x + y * y + z * z) - kSeaLevelRadiusFtT) * kFt2M;
     }
-    // terminal observation (rl_env.py:552-554)
-    lane_build_obs(k, p, g, o.obs, a, r, D, S + lane * kStagePitch, nullptr, 1);
+    // terminal observation (rl_env.py:552-554): every row to terminal_obs (or to obs when
+    // there is none); the live engagements' rows are also their observation
+    const ObsOut out{S + lane * tile_pitch<D, FULL>(),
+                     (io.terminal_obs ? io.terminal_obs : io.obs) + a * D,
+                     (io.terminal_obs && !d) ? io.obs + a * D : nullptr};
+    store_run2<D, FULL, vec_base(D == 214 ? 9 : 7), kActHist>(out, o.hist);
+    lane_build_obs<D, FULL>(k, p, g, o.obs, a, r, out, 1);
   }
   const uint64_t rows = __ballot(on), live = __ballot(on && !d), fresh = __ballot(on && d);
   __syncthreads();
-  // every terminal row to terminal_obs; the live engagements' rows are also their observation
   if (io.terminal_obs)
-    flush_tile<D>(S, a0, n, rows, io.terminal_obs, live, io.obs, lane);
+    flush_tile<D, FULL>(S, a0, n, rows, io.terminal_obs, live, io.obs, lane);
   else
-    flush_tile<D>(S, a0, n, rows, io.obs, 0, nullptr, lane);
+    flush_tile<D, FULL>(S, a0, n, rows, io.obs, 0, nullptr, lane);
   if (!fresh) return;      // uniform: no autoreset in this wave
   __syncthreads();
   if (on && d) {           // autoreset from the initial-condition pool (rl_env.py:559-577)
@@ -718,10 +775,11 @@ __global__ __launch_bounds__(kRowBlock) void env_post_step_kernel(const F16EnvSt
     ObsIn fresh;
     fresh.hp = 1.0; fresh.fuel = 1.0; fresh.dealt = 0.0; fresh.taken = 0.0; fresh.t = 0.0;
     for (int i = 0; i < 3; ++i) { fresh.pqr[i] = 0.0; fresh.accel[i] = 0.0; }
-    lane_build_obs(k2, p2, g2, fresh, a, r, D, S + lane * kStagePitch, nullptr, 2);
+    lane_build_obs<D, FULL>(k2, p2, g2, fresh, a, r,
+                            ObsOut{S + lane * tile_pitch<D, FULL>(), io.obs + a * D, nullptr}, 2);
   }
   __syncthreads();
-  flush_sparse<D>(S, a0, fresh, io.obs, lane);
+  flush_sparse<D, FULL>(S, a0, fresh, io.obs, lane);
 }
 
 // rl_env.py:583-592 state9_flat: (nac, 9) float64 rows N/E/D m, roll/pitch/yaw deg, u/v/w m/s
@@ -774,6 +832,24 @@ static bool rows_aligned(const float* p, int obs_dim) {
   return ((uintptr_t)p & (obs_dim % 4 == 0 ? 15u : 7u)) == 0;
 }
 
+// Whether a row launch over nenv engagements keeps every wavefront resident at once with the
+// full-row tile (limited by LDS per CU); otherwise the vector-block tile is used, which lets
+// four wavefronts share a CU.
+static bool full_tile_resident(int nenv, int obs_dim) {
+  static int cus = 0, lds = 0;
+  if (cus == 0) {
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    (void)hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev);
+    if (cus <= 0) cus = 256;
+    if (lds <= 0) lds = 160 * 1024;
+  }
+  const long waves = (2L * nenv + kRowBlock - 1) / kRowBlock;
+  const long tile = (long)kRowBlock * (obs_dim | 1) * (long)sizeof(float);
+  return waves <= (long)(lds / tile) * cus;
+}
+
 static int check_cfg(const F16RewardCfg* c) {
   if (!c || c->mode < 0 || c->mode > 3) return F16_EINVAL;
   return 0;
@@ -824,12 +900,17 @@ extern "C" int f16_obr_build_obs(const double* states, long ld, const unsigned c
   if (rec->nenv == 0) return 0;
   if (!states || !obs || ld < 2L * rec->nenv) return F16_EINVAL;
   if (!rows_aligned(obs, obs_dim)) return F16_EINVAL;
-  if (obs_dim == 184)
-    hipLaunchKernelGGL(build_obs_kernel<184>, grid_rows(rec->nenv), dim3(kRowBlock), 0,
-                       (hipStream_t)stream, states, ld, env_mask, *rec, origin(), obs);
-  else
-    hipLaunchKernelGGL(build_obs_kernel<214>, grid_rows(rec->nenv), dim3(kRowBlock), 0,
-                       (hipStream_t)stream, states, ld, env_mask, *rec, origin(), obs);
+  const bool full = full_tile_resident(rec->nenv, obs_dim);
+  hipStream_t s = (hipStream_t)stream;
+#define F16_BUILD_OBS(D, FULL)                                                                  \
+  hipLaunchKernelGGL((build_obs_kernel<D, FULL>), grid_rows(rec->nenv), dim3(kRowBlock), 0, s,   \
+                     states, ld, env_mask, *rec, origin(), obs)
+  if (obs_dim == 184) {
+    if (full) F16_BUILD_OBS(184, true); else F16_BUILD_OBS(184, false);
+  } else {
+    if (full) F16_BUILD_OBS(214, true); else F16_BUILD_OBS(214, false);
+  }
+#undef F16_BUILD_OBS
   return f16_last_error();
 }
 
@@ -848,12 +929,17 @@ extern "C" int f16_env_post_step(const F16EnvStepIO* io, const F16Recon* rec,
   if (!rows_aligned(io->obs, io->obs_dim) ||
       (io->terminal_obs && !rows_aligned(io->terminal_obs, io->obs_dim)))
     return F16_EINVAL;
-  if (io->obs_dim == 184)
-    hipLaunchKernelGGL(env_post_step_kernel<184>, grid_rows(rec->nenv), dim3(kRowBlock), 0,
-                       (hipStream_t)stream, *io, *rec, *cfg, origin());
-  else
-    hipLaunchKernelGGL(env_post_step_kernel<214>, grid_rows(rec->nenv), dim3(kRowBlock), 0,
-                       (hipStream_t)stream, *io, *rec, *cfg, origin());
+  const bool full = full_tile_resident(rec->nenv, io->obs_dim);
+  hipStream_t s = (hipStream_t)stream;
+#define F16_POST_STEP(D, FULL)                                                                  \
+  hipLaunchKernelGGL((env_post_step_kernel<D, FULL>), grid_rows(rec->nenv), dim3(kRowBlock), 0,  \
+                     s, *io, *rec, *cfg, origin())
+  if (io->obs_dim == 184) {
+    if (full) F16_POST_STEP(184, true); else F16_POST_STEP(184, false);
+  } else {
+    if (full) F16_POST_STEP(214, true); else F16_POST_STEP(214, false);
+  }
+#undef F16_POST_STEP
   return f16_last_error();
 }
 

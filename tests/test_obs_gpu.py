@@ -210,9 +210,11 @@ def test_init_reward_masked(gpu, orc):
     _cmp_recon(obr, ob)
 
 
-def test_external_214_matches_oracle(gpu, orc):
-    """214-D variant: acceleration vectors spliced in before the action history."""
-    nenv = 512
+@pytest.mark.parametrize("nenv", [512, 17000, 26000])
+def test_external_214_matches_oracle(gpu, orc, nenv):
+    """214-D variant: acceleration vectors spliced in before the action history.  17,000
+    engagements build the 214-D rows through the vector-block tile and the 184-D rows through
+    the full-row tile; 26,000 build both through the vector-block tile."""
     sim = _random_states(gpu, nenv, 51)
     obr = _obr(nenv, ext=True)
     s9 = oracle_lib.ObrOracle(orc, nenv).state9(sim.states.cpu().numpy())
@@ -248,13 +250,13 @@ def test_state9_kernel(gpu, orc):
 
 
 # ------------------------------------------------------------------------ fused env step
-@pytest.mark.parametrize("obs_dim", [184, 214])
-def test_env_post_step_matches_reference_sequence(gpu, orc, obs_dim):
+@pytest.mark.parametrize("obs_dim,nenv", [(184, 1024), (214, 1024), (184, 26000), (214, 17000)])
+def test_env_post_step_matches_reference_sequence(gpu, orc, obs_dim, nenv):
     """f16_env_post_step against the reference's sequence (rl_env.py:540-580) replayed on the
     oracle: advance -> terminal obs -> pool autoreset -> reset_envs -> init_reward -> masked
-    build_obs."""
+    build_obs.  The large sizes exceed what the full-row staging tile keeps resident on an
+    MI355X (768 / 512 wavefronts), so they run the vector-block tile with direct row stores."""
     ext = obs_dim == 214
-    nenv = 1024
     sim = _random_states(gpu, nenv, 71)
     pool_sim = _random_states(gpu, 64, 72)
     pool = pool_sim.states.reshape(64, 2, 101).contiguous()
