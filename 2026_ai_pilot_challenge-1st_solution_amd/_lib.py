@@ -46,7 +46,7 @@ class F16EnvStepIO(ctypes.Structure):
                 ("reward", _vp), ("reward_f32", _vp), ("term", _vp), ("trunc", _vp),
                 ("done", _vp), ("done_f32", _vp), ("terminal_hp", _vp),
                 ("terminal_alt_m", _vp), ("terminal_finite", _vp), ("finite_acc", _vp),
-                ("opp_assign", _vp), ("opp_cdf", _vp), ("n_opp", _i)]
+                ("opp_assign", _vp), ("opp_cdf", _vp), ("n_opp", _i), ("step_base", _vp)]
 
 
 class F16PolicyGroup(ctypes.Structure):
@@ -63,7 +63,8 @@ class F16PolicyArgs(ctypes.Structure):
                 ("max_group_rows", _i), ("seed", ctypes.c_ulonglong),
                 ("step", ctypes.c_uint), ("salt", ctypes.c_uint), ("deterministic", _i),
                 ("grid", _vp), ("nobs_out", _vp), ("nobs_ld", _l), ("act_idx", _vp),
-                ("logp", _vp), ("value", _vp), ("env_actions", _vp), ("logits_out", _vp)]
+                ("logp", _vp), ("value", _vp), ("env_actions", _vp), ("logits_out", _vp),
+                ("step_base", _vp)]
 
 
 _RP, _CP = ctypes.POINTER(F16Recon), ctypes.POINTER(F16RewardCfg)

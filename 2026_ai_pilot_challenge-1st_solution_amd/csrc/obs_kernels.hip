@@ -658,6 +658,7 @@ __global__ __launch_bounds__(kRowBlock) void env_post_step_kernel(const F16EnvSt
   const long nac = 2L * r.nenv;
   const int n = (int)min((long)kRowBlock, nac - a0);
   const bool on = a < nac;                              // nac is even: pairs agree
+  const uint32_t step = io.step + (io.step_base ? *io.step_base : 0u);
   const long e = a >> 1;
   const int odd = (int)(a & 1);
   double* __restrict__ st = io.states;
@@ -727,7 +728,7 @@ __global__ __launch_bounds__(kRowBlock) void env_post_step_kernel(const F16EnvSt
     if (io.pick) {
       pk = io.pick[e];
     } else {
-      uint32_t ctr[4] = {(uint32_t)e, io.step, 0u, 0x5EED5EEDu};
+      uint32_t ctr[4] = {(uint32_t)e, step, 0u, 0x5EED5EEDu};
       f16rng::philox4x32_10(ctr, (uint32_t)io.seed, (uint32_t)(io.seed >> 32));
       pk = (long)(((uint64_t)ctr[0] * (uint64_t)io.pool_size) >> 32);
     }
@@ -744,7 +745,7 @@ __global__ __launch_bounds__(kRowBlock) void env_post_step_kernel(const F16EnvSt
     r.dealt[a] = 0.0; r.taken[a] = 0.0; r.hp_loss[a] = 0.0; r.prev_x[a] = 0.0;
     r.prev_alt_log[a] = 0.0;
     if (io.opp_assign && !odd) {                     // league: draw this engagement's opponent
-      uint32_t ctr[4] = {(uint32_t)e, io.step, 1u, 0x0FF0A55Eu};
+      uint32_t ctr[4] = {(uint32_t)e, step, 1u, 0x0FF0A55Eu};
       f16rng::philox4x32_10(ctr, (uint32_t)io.seed, (uint32_t)(io.seed >> 32));
       const float u = (float)(ctr[0] >> 8) * 0x1p-24f;
       int kk = io.n_opp - 1;

@@ -258,6 +258,7 @@ __global__ __launch_bounds__(kThreads, 2) void policy_kernel(const F16PolicyArgs
   __syncthreads();
 
   // ---- per (row, channel): softmax, draw, log-probability, control (waves 0-3)
+  const uint32_t step = p.step + (p.step_base ? *p.step_base : 0u);
   if (tid < kRows * kChan) {
     const int row = tid >> 2, ch = tid & 3;
     const float* l = Ls + row * kLPitch + ch * kBins;
@@ -276,7 +277,7 @@ __global__ __launch_bounds__(kThreads, 2) void policy_kernel(const F16PolicyArgs
     const long pr = (row < nr) ? (p.rows ? p.rows[li] : li) : 0;
     int idx = amax;
     if (!p.deterministic) {
-      uint32_t c[4] = {(uint32_t)pr, p.step, (uint32_t)ch, p.salt};
+      uint32_t c[4] = {(uint32_t)pr, step, (uint32_t)ch, p.salt};
       f16rng::philox4x32_10(c, (uint32_t)p.seed, (uint32_t)(p.seed >> 32));
       const float u = (float)(c[0] >> 8) * 0x1p-24f;
       const float target = u * s;

@@ -105,7 +105,13 @@ class MLPActorCritic(torch.nn.Module):
                         c[2].bias.float().cpu(), b3, c[4].weight.float().cpu().flatten(),
                         c[4].bias.float().cpu()])
         assert wf.numel() == NF
-        self._packed = (wbf.to(device).contiguous(), wf.to(device).contiguous())
+        old = self._packed
+        if old is not None and old[0].device == torch.device(device) and old[0].shape == wbf.shape:
+            # refresh in place: launches recorded in a HIP graph keep pointing at these blobs
+            old[0].copy_(wbf)
+            old[1].copy_(wf)
+        else:
+            self._packed = (wbf.to(device).contiguous(), wf.to(device).contiguous())
         return self._packed
 
     def packed(self):
@@ -176,11 +182,14 @@ class PolicyStep:
 
     def __call__(self, obs, groups, *, norm=None, rows=None, step=0, salt=0, deterministic=False,
                  nobs_out=None, act_idx=None, logp=None, value=None, env_actions=None,
-                 logits_out=None, group_offsets=None, max_group_rows=None, nphys=None):
+                 logits_out=None, group_offsets=None, max_group_rows=None, nphys=None,
+                 step_base=None):
         """groups: (net, row_begin, row_end) or (net, row_begin, row_end, norm) -- a per-network
         RunningNorm overrides `norm` for that network.  group_offsets: device int32 (ngroups+1)
         row boundaries computed on the device (f16_group_rows); then row_begin/row_end are
         ignored, max_group_rows bounds any group's size and nphys bounds the physical rows.
+        step_base: optional device int32 scalar added to `step` in the kernel (rollouts recorded
+        in a HIP graph advance it on the device between replays).
         nphys given with a row map skips the (host-synchronising) row-map validation: the caller
         guarantees 0 <= rows < nphys."""
         if obs.dtype != torch.float32 or obs.dim() != 2 or obs.shape[1] != self.obs_dim:
@@ -257,6 +266,10 @@ class PolicyStep:
             a.nobs_out, a.nobs_ld = nobs_out.data_ptr(), nobs_out.stride(0)
         p = lambda t: t.data_ptr() if t is not None else None
         a.act_idx, a.logp, a.value = p(act_idx), p(logp), p(value)
+        if step_base is not None:
+            if step_base.dtype != torch.int32 or not step_base.is_cuda:
+                raise ValueError("step_base must be a device int32 scalar")
+            a.step_base = step_base.data_ptr()
         a.env_actions, a.logits_out = p(env_actions), p(logits_out)
         rc = self._lib.f16_policy_step(ctypes.byref(a), _lib.stream_handle(self.device))
         _lib.check(rc, "f16_policy_step")

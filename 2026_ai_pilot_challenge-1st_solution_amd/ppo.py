@@ -50,6 +50,51 @@ def gae(rew, val, done, last_val, next_done, gamma=0.997, lam=0.95):
 POLICY_FLOP_PER_ROW = {d: 2 * (2 * 256 * d + 2 * 256 * 256 + 84 * 256 + 256) for d in (184, 214)}
 
 
+class _RolloutGraph:
+    """Records a collector's _run() once as a HIP graph (torch.cuda.CUDAGraph) and replays it.
+
+    The env's and the collector's draw counters become device int32 scalars that the recorded
+    launches read (step_base) and that the graph itself advances by T at its end; the host
+    counters (collector.global_step, env._post_steps) are kept equal to them.  The first
+    collect() runs eagerly so that every lazily allocated workspace exists before recording."""
+
+    def __init__(self, owner, device):
+        self.owner = owner
+        self.graph = None
+        self.warm = False
+        self.pol_base = torch.zeros((), dtype=torch.int32, device=device)
+        self.env_base = torch.zeros((), dtype=torch.int32, device=device)
+        self.out = None
+
+    def collect(self):
+        o, env, T = self.owner, self.owner.env, self.owner.T
+        if not self.warm:
+            out = o._run()
+            o.global_step += T
+            self.warm = True
+            return out
+        if self.graph is None:
+            for v in (o.global_step, env._post_steps):
+                if not 0 <= v < 2 ** 31 - 4 * T:
+                    raise OverflowError("draw counters beyond the int32 device counters")
+            self.pol_base.fill_(o.global_step)
+            self.env_base.fill_(env._post_steps)
+            p0 = env._post_steps
+            torch.cuda.synchronize(self.pol_base.device)
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                self.out = o._run(self.pol_base, self.env_base)
+                self.pol_base.add_(T)
+                self.env_base.add_(T)
+            env._post_steps = p0            # recording ran nothing
+            self.graph = g
+        self.graph.replay()
+        o.global_step += T
+        env._post_steps += T
+        adv, ret, stats = self.out
+        return adv, ret, dict(stats)
+
+
 class SelfPlayRollout:
     """Rollout collection with one policy on both aircraft of every engagement (BASELINE C4):
     the per-step sequence of PPOGPUTrainer.collect_rollout (research/competition_36500/runtime/
@@ -62,10 +107,17 @@ class SelfPlayRollout:
     Per step: f16_norm_update (3 small launches), f16_policy_step, the FDM decision and
     f16_env_post_step (which writes the float32 rewards and done flags straight into the
     buffers and draws autoreset pool rows itself); no host synchronisation.  stats=True adds the
-    reference's episode-return bookkeeping (a few small torch launches per step)."""
+    reference's episode-return bookkeeping (a few small torch launches per step).
+
+    graph=True records the whole rollout (T steps, bootstrap value, GAE) once as a HIP graph
+    and replays it: the first collect() runs eagerly (it allocates every workspace), the second
+    records and replays, later ones replay.  The draws' step counters then live on the device
+    and advance inside the graph, so the results equal the eager collector's bit for bit.  The
+    returned adv/ret are overwritten by the next collect(); weights refreshed with
+    net.pack() are picked up by the next replay.  (stats=False only.)"""
 
     def __init__(self, env, net, T=64, gamma=0.99, lam=0.95, seed=0, update_norm=True,
-                 stats=True):
+                 stats=True, graph=False):
         from .policy import PolicyStep, RunningNorm
         self.env, self.net, self.T = env, net, int(T)
         self.gamma, self.lam = float(gamma), float(lam)
@@ -90,6 +142,10 @@ class SelfPlayRollout:
         self.global_step = 0
         # When set to a list, collect() appends (start, end) events around each policy launch.
         self.policy_events = None
+        self._graph_mode = bool(graph)
+        if self._graph_mode and self.want_stats:
+            raise ValueError("graph=True needs stats=False")
+        self._graphs = _RolloutGraph(self, dev) if self._graph_mode else None
 
     def reset(self, **kw):
         obs = self.env.reset(**kw)
@@ -97,22 +153,23 @@ class SelfPlayRollout:
         self.next_done.zero_()
         return obs
 
-    def _policy(self, obs, **out):
+    def _policy(self, obs, step, step_base, **out):
         ev = self.policy_events
         if ev is not None:
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record()
-        self.policy(obs, [(self.net, 0, self.nac)], norm=self.norm, step=self.global_step, **out)
+        self.policy(obs, [(self.net, 0, self.nac)], norm=self.norm, step=step,
+                    step_base=step_base, **out)
         if ev is not None:
             e1.record()
             ev.append((e0, e1))
 
-    def collect(self):
-        """One rollout of T steps; returns (adv, ret) as (T, nenv, 2) and a stats dict."""
-        if self.next_obs is None:
-            raise RuntimeError("call reset() first")
+    def _run(self, pol_base=None, env_base=None):
+        """The rollout's launches.  With the bases (device counters) the draws' step counters
+        are base + t instead of the host counters."""
         env, T = self.env, self.T
         dev = self.device
+        g0 = 0 if pol_base is not None else self.global_step
         self.finite_acc.fill_(1)
         self.b_done[0].copy_(self.next_done)
         if self.want_stats:
@@ -122,24 +179,36 @@ class SelfPlayRollout:
             obs = self.next_obs
             if self.update_norm:
                 self.norm.update(obs)
-            self._policy(obs, nobs_out=self.b_obs[t], act_idx=self.b_act[t], logp=self.b_logp[t],
-                         value=self.b_val[t], env_actions=env.sim.actions)
+            self._policy(obs, g0 + t, pol_base, nobs_out=self.b_obs[t], act_idx=self.b_act[t],
+                         logp=self.b_logp[t], value=self.b_val[t], env_actions=env.sim.actions)
             done_t = self.b_done[t + 1] if t + 1 < T else self.next_done
-            self.next_obs = env.step_rollout(self.b_rew[t], done_t, self.finite_acc)
+            self.next_obs = env.step_rollout(self.b_rew[t], done_t, self.finite_acc,
+                                             step_base=env_base, step=t)
             if self.want_stats:
                 d2 = done_t.repeat_interleave(2)
                 self.ep_ret += self.b_rew[t]
                 ret_sum += (self.ep_ret * d2).sum()
                 ep_count += done_t.sum()
                 self.ep_ret *= 1.0 - d2
-            self.global_step += 1
-        self._policy(self.next_obs, value=self.last_val)
+        self._policy(self.next_obs, g0 + T, pol_base, value=self.last_val)
         shape = (T, self.nenv, 2)
         adv, ret = gae(self.b_rew.view(shape), self.b_val.view(shape), self.b_done,
                        self.last_val.view(self.nenv, 2), self.next_done, self.gamma, self.lam)
-        stats = {"trajectory_finite": self.finite_acc.all()}
+        stats = {}
         if self.want_stats:
             stats.update(ret_sum=ret_sum, ep_count=ep_count)
+        return adv, ret, stats
+
+    def collect(self):
+        """One rollout of T steps; returns (adv, ret) as (T, nenv, 2) and a stats dict."""
+        if self.next_obs is None:
+            raise RuntimeError("call reset() first")
+        if self._graph_mode:
+            adv, ret, stats = self._graphs.collect()
+        else:
+            adv, ret, stats = self._run()
+            self.global_step += self.T
+        stats["trajectory_finite"] = self.finite_acc.all()
         return adv, ret, stats
 
 
@@ -162,10 +231,13 @@ class LeagueRollout:
     Per step: f16_norm_update over the learner's rows, f16_policy_step for the learner,
     f16_group_rows + one grouped f16_policy_step for all opponents, the FDM decision,
     f16_env_post_step (rewards, termination incl. optional fuel exhaustion, autoreset and the
-    opponent redraw), and a strided copy of the learner's rewards."""
+    opponent redraw), and a strided copy of the learner's rewards.
+
+    graph=True records the rollout as a HIP graph as SelfPlayRollout does (same results bit for
+    bit; adv/ret overwritten by the next collect())."""
 
     def __init__(self, env, net, opponents, T=128, gamma=0.99, lam=0.95, seed=0,
-                 update_norm=True, opp_weights=None, opp_norms=None):
+                 update_norm=True, opp_weights=None, opp_norms=None, graph=False):
         from .policy import PolicyStep, RunningNorm
         if len(opponents) < 1 or len(opponents) > 16:
             raise ValueError("1..16 opponent networks")
@@ -210,6 +282,8 @@ class LeagueRollout:
         # When set to lists, collect() appends (start, end) events around the policy launches.
         self.policy_events = None
         self.opp_events = None
+        self._graph_mode = bool(graph)
+        self._graphs = _RolloutGraph(self, dev) if self._graph_mode else None
 
     def reset(self, **kw):
         """Reset the env and draw every engagement's opponent from the weights (seeded)."""
@@ -232,7 +306,7 @@ class LeagueRollout:
         events.append((e0, e1))
         return out
 
-    def _opponents(self, obs):
+    def _opponents(self, obs, step, step_base):
         rc = self._lib.f16_group_rows(_lib.ptr(self.env.opp_assign), self.nenv,
                                       len(self.opponents), 2, 1, _lib.ptr(self.opp_rows),
                                       _lib.ptr(self.opp_offsets), _lib.ptr(self._group_work),
@@ -240,14 +314,13 @@ class LeagueRollout:
         _lib.check(rc, "f16_group_rows")
         groups = [(net, None, None, nrm) for net, nrm in zip(self.opponents, self.opp_norms)]
         self.policy(obs, groups, rows=self.opp_rows, group_offsets=self.opp_offsets,
-                    max_group_rows=self.nenv, nphys=self.nac, step=self.global_step, salt=1,
-                    env_actions=self.env.sim.actions)
+                    max_group_rows=self.nenv, nphys=self.nac, step=step, salt=1,
+                    env_actions=self.env.sim.actions, step_base=step_base)
 
-    def collect(self):
-        """One rollout of T steps; returns (adv, ret) as (T, nenv) and a stats dict."""
-        if self.next_obs is None:
-            raise RuntimeError("call reset() first")
+    def _run(self, pol_base=None, env_base=None):
+        """The rollout's launches (see SelfPlayRollout._run for the device counters)."""
         env, T = self.env, self.T
+        g0 = 0 if pol_base is not None else self.global_step
         self.finite_acc.fill_(1)
         self.b_done[0].copy_(self.next_done)
         for t in range(T):
@@ -256,17 +329,29 @@ class LeagueRollout:
                 self.norm.update(obs, rows=self.main_rows)
             self._timed(self.policy_events, lambda: self.policy(
                 obs, [(self.net, 0, self.nenv)], norm=self.norm, rows=self.main_rows,
-                nphys=self.nac, step=self.global_step, salt=0, nobs_out=self.b_obs[t],
+                nphys=self.nac, step=g0 + t, salt=0, nobs_out=self.b_obs[t],
                 act_idx=self.b_act[t], logp=self.b_logp[t], value=self.b_val[t],
-                env_actions=env.sim.actions))
-            self._timed(self.opp_events, lambda: self._opponents(obs))
+                env_actions=env.sim.actions, step_base=pol_base))
+            self._timed(self.opp_events, lambda: self._opponents(obs, g0 + t, pol_base))
             done_t = self.b_done[t + 1] if t + 1 < T else self.next_done
-            self.next_obs = env.step_rollout(self.rew_all, done_t, self.finite_acc)
+            self.next_obs = env.step_rollout(self.rew_all, done_t, self.finite_acc,
+                                             step_base=env_base, step=t)
             self.b_rew[t].copy_(self.rew_all[0::2])
-            self.global_step += 1
         self.policy(self.next_obs, [(self.net, 0, self.nenv)], norm=self.norm,
-                    rows=self.main_rows, nphys=self.nac, step=self.global_step,
-                    value=self.last_val)
+                    rows=self.main_rows, nphys=self.nac, step=g0 + T, value=self.last_val,
+                    step_base=pol_base)
         adv, ret = gae(self.b_rew, self.b_val, self.b_done, self.last_val, self.next_done,
                        self.gamma, self.lam)
-        return adv, ret, {"trajectory_finite": self.finite_acc.all()}
+        return adv, ret, {}
+
+    def collect(self):
+        """One rollout of T steps; returns (adv, ret) as (T, nenv) and a stats dict."""
+        if self.next_obs is None:
+            raise RuntimeError("call reset() first")
+        if self._graph_mode:
+            adv, ret, stats = self._graphs.collect()
+        else:
+            adv, ret, stats = self._run()
+            self.global_step += self.T
+        stats["trajectory_finite"] = self.finite_acc.all()
+        return adv, ret, stats

@@ -145,19 +145,26 @@ PEAK_BF16_TFLOPS = 2500.0
 def rollout_bench(nenv, T=64, reps=2):
     """BASELINE C4: nenv engagements x T-step self-play rollout (FDM + fused obs/reward + norm
     update + fused bf16 actor/critic with Philox draw) then GAE (gamma 0.99, lambda 0.95) over
-    [T, nenv, 2].  Weights N(0, 0.02), draw seed 0."""
+    [T, nenv, 2].  Weights N(0, 0.02), draw seed 0.  The collector records the rollout as a HIP
+    graph and replays it (its results equal the eager collector's bit for bit); a separate eager
+    rollout with events around the policy launches gives the policy kernel's time."""
     import torch
     env_mod = importlib.import_module(PKG + ".rl_env")
     pol = importlib.import_module(PKG + ".policy")
     ppo = importlib.import_module(PKG + ".ppo")
-    env = env_mod.GpuDogfightVecEnv(nenv, seed=0)
-    net = pol.MLPActorCritic(184, init="normal", init_std=0.02,
-                             generator=torch.Generator().manual_seed(0)).to("cuda")
-    ro = ppo.SelfPlayRollout(env, net, T=T, gamma=0.99, lam=0.95, seed=0, stats=False)
-    ro.reset(stagger=False)
-    ro.collect()                                    # warm-up rollout
+
+    def make(graph):
+        env = env_mod.GpuDogfightVecEnv(nenv, seed=0)
+        net = pol.MLPActorCritic(184, init="normal", init_std=0.02,
+                                 generator=torch.Generator().manual_seed(0)).to("cuda")
+        ro = ppo.SelfPlayRollout(env, net, T=T, gamma=0.99, lam=0.95, seed=0, stats=False,
+                                 graph=graph)
+        ro.reset(stagger=False)
+        return ro
+    ro = make(True)
+    ro.collect()                                    # eager warm-up (allocations)
+    ro.collect()                                    # records the graph, replays it
     torch.cuda.synchronize()
-    ro.policy_events = []
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
     for _ in range(reps):
@@ -167,11 +174,20 @@ def rollout_bench(nenv, T=64, reps=2):
     if not bool(stats["trajectory_finite"]) or not bool(torch.isfinite(adv).all()):
         raise FloatingPointError("non-finite rollout")
     ms = e0.elapsed_time(e1) / reps
-    pol_ms = float(np.mean([a.elapsed_time(b) for a, b in ro.policy_events]))
-    ro.policy_events = None
+    del ro
+    eager = make(False)
+    eager.collect()
+    torch.cuda.synchronize()
+    eager.policy_events = []
+    t0 = time.perf_counter()
+    eager.collect()
+    torch.cuda.synchronize()
+    eager_ms = (time.perf_counter() - t0) * 1e3
+    pol_ms = float(np.mean([a.elapsed_time(b) for a, b in eager.policy_events]))
     flop = ppo.POLICY_FLOP_PER_ROW[184] * 2 * nenv
     return {"workload": "selfplay_rollout_16k_T64", "engagements": nenv, "T": T,
-            "ms_per_rollout": ms, "transitions_per_s": nenv * T / (ms * 1e-3),
+            "hip_graph": True, "ms_per_rollout": ms, "eager_ms_per_rollout": eager_ms,
+            "transitions_per_s": nenv * T / (ms * 1e-3),
             "aircraft_transitions_per_s": 2 * nenv * T / (ms * 1e-3),
             "policy_kernel_ms": pol_ms,
             "policy_mfma": {"kernel": "policy_kernel<192>", "flop_per_launch": flop,
@@ -185,21 +201,26 @@ def league_bench(nenv=65536, T=128, nopp=8, reps=2):
     learner (plane 0) and 8 frozen random-init opponents (plane 1, bf16 N(0, 0.02)) assigned per
     engagement from Zipf(1.1) weights, evaluated as one grouped launch; fuel exhaustion and
     ground-collision (hard deck) terminations, autoreset with opponent redraw inside the step
-    kernel; GAE over [T, nenv]."""
+    kernel; GAE over [T, nenv].  Recorded as a HIP graph and replayed; one eager rollout with
+    events gives the per-kernel times."""
     import torch
     env_mod = importlib.import_module(PKG + ".rl_env")
     pol = importlib.import_module(PKG + ".policy")
     ppo = importlib.import_module(PKG + ".ppo")
-    env = env_mod.GpuDogfightVecEnv(nenv, seed=0, obs_dim=214, fuel_exhaustion=True,
-                                    fuel_lbs_range=(100.0, 3000.0))
-    mk = lambda s: pol.MLPActorCritic(214, init="normal", init_std=0.02,
-                                      generator=torch.Generator().manual_seed(s)).to("cuda")
-    net, opps = mk(0), [mk(100 + k) for k in range(nopp)]
-    ro = ppo.LeagueRollout(env, net, opps, T=T, gamma=0.99, lam=0.95, seed=0)
-    ro.reset(stagger=False)
+
+    def make(graph):
+        env = env_mod.GpuDogfightVecEnv(nenv, seed=0, obs_dim=214, fuel_exhaustion=True,
+                                        fuel_lbs_range=(100.0, 3000.0))
+        mk = lambda s: pol.MLPActorCritic(214, init="normal", init_std=0.02,
+                                          generator=torch.Generator().manual_seed(s)).to("cuda")
+        net, opps = mk(0), [mk(100 + k) for k in range(nopp)]
+        ro = ppo.LeagueRollout(env, net, opps, T=T, gamma=0.99, lam=0.95, seed=0, graph=graph)
+        ro.reset(stagger=False)
+        return ro
+    ro = make(True)
+    ro.collect()
     ro.collect()
     torch.cuda.synchronize()
-    ro.policy_events, ro.opp_events, env.kernel_events, env.sim.kernel_events = [], [], [], []
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
     for _ in range(reps):
@@ -209,15 +230,23 @@ def league_bench(nenv=65536, T=128, nopp=8, reps=2):
     if not bool(stats["trajectory_finite"]) or not bool(torch.isfinite(adv).all()):
         raise FloatingPointError("non-finite league rollout")
     ms = e0.elapsed_time(e1) / reps
+    done = float(ro.b_done[1:].sum().item() + ro.next_done.sum().item())
+    del ro
+    eager = make(False)
+    eager.collect()
+    torch.cuda.synchronize()
+    env = eager.env
+    eager.policy_events, eager.opp_events, env.kernel_events, env.sim.kernel_events = [], [], [], []
+    eager.collect()
+    torch.cuda.synchronize()
     avg = lambda ev: float(np.mean([a.elapsed_time(b) for a, b in ev]))
     out = {"workload": "league_rollout_64k_T128_214d_8opp", "engagements": nenv, "T": T,
-           "opponents": nopp, "opponent_weights": "zipf(1.1)", "ms_per_rollout": ms,
-           "transitions_per_s": nenv * T / (ms * 1e-3),
+           "opponents": nopp, "opponent_weights": "zipf(1.1)", "hip_graph": True,
+           "ms_per_rollout": ms, "transitions_per_s": nenv * T / (ms * 1e-3),
            "aircraft_transitions_per_s": 2 * nenv * T / (ms * 1e-3),
-           "learner_policy_ms": avg(ro.policy_events), "opponents_policy_ms": avg(ro.opp_events),
+           "learner_policy_ms": avg(eager.policy_events), "opponents_policy_ms": avg(eager.opp_events),
            "fdm_kernel_ms": avg(env.sim.kernel_events), "post_kernel_ms": avg(env.kernel_events),
-           "episodes_done_per_rollout": float(ro.b_done[1:].sum().item() + ro.next_done.sum().item())}
-    ro.policy_events = ro.opp_events = env.kernel_events = env.sim.kernel_events = None
+           "episodes_done_per_rollout": done}
     return out
 
 

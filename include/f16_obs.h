@@ -106,6 +106,8 @@ typedef struct F16EnvStepIO {
                                     word 0 with counter (e, step, 1, 0x0FF0A55E); or NULL */
     const float *opp_cdf;        /* (n_opp) cumulative opponent weights, last = 1 */
     int n_opp;
+    const unsigned int *step_base;   /* device counter added to `step` when non-NULL (captured
+                                        rollouts): the counters above use *step_base + step */
 } F16EnvStepIO;
 
 /* GpuDogfightVecEnv.step after the physics launch (research/competition_36500/runtime/

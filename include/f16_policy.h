@@ -59,6 +59,9 @@ typedef struct F16PolicyArgs {
     float *value;           /* (logical) critic value, or NULL */
     double *env_actions;    /* (physical, 4) float64 controls [ail, ele, rud, thr], or NULL */
     float *logits_out;      /* (logical, 84) actor logits, or NULL */
+    const unsigned int *step_base;  /* device counter added to `step` when non-NULL, so a
+                                       captured (HIP graph) rollout advances its draws on the
+                                       device: counter word 1 = *step_base + step */
 } F16PolicyArgs;
 
 /* One policy step for every logical row: optional RunningNorm.normalize with clip

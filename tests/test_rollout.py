@@ -25,13 +25,13 @@ _spec.loader.exec_module(GO)
 pytestmark = pytest.mark.gpu
 
 
-def _collector(gpu, nenv=256, T=12, seed=3):
+def _collector(gpu, nenv=256, T=12, seed=3, **kw):
     E = import_pkg("rl_env").GpuDogfightVecEnv
     P = import_pkg("policy")
     R = import_pkg("ppo")
     env = E(nenv, seed=seed, ic_pool_size=64)
     net = P.MLPActorCritic(184, init="normal", generator=torch.Generator().manual_seed(seed)).to(gpu)
-    ro = R.SelfPlayRollout(env, net, T=T, gamma=0.99, lam=0.95, seed=0)
+    ro = R.SelfPlayRollout(env, net, T=T, gamma=0.99, lam=0.95, seed=0, **kw)
     ro.reset(stagger=True, max_stagger_steps=8)
     return ro
 
@@ -71,3 +71,57 @@ def test_rollout_deterministic(gpu):
     for name in ("b_obs", "b_act", "b_logp", "b_rew", "b_val", "b_done"):
         assert torch.equal(getattr(a, name), getattr(b, name)), name
     assert torch.equal(ra[0], rb[0]) and torch.equal(ra[1], rb[1])
+
+
+BUFFERS = ("b_obs", "b_act", "b_logp", "b_rew", "b_val", "b_done", "last_val", "next_done",
+           "finite_acc")
+
+
+def _same_rollouts(a, b, n=4, refresh_at=2):
+    """n rollouts of the eager collector `a` and the graph collector `b`, with host work and
+    synchronisation between replays; every buffer, the GAE outputs and the env state agree bit
+    for bit after each one.  Before rollout `refresh_at` both networks' weights change and are
+    re-packed (the graph picks up the refreshed blobs)."""
+    for r in range(n):
+        if r == refresh_at:
+            for ro in (a, b):
+                with torch.no_grad():
+                    for prm in ro.net.parameters():
+                        prm.mul_(0.9)
+                ro.net.pack()
+        ra, rb = a.collect(), b.collect()
+        torch.cuda.synchronize()
+        x = torch.arange(1000, device=a.device).sum().item()      # eager work between replays
+        assert x == 499500
+        for name in BUFFERS:
+            assert torch.equal(getattr(a, name), getattr(b, name)), (r, name)
+        assert torch.equal(ra[0], rb[0]) and torch.equal(ra[1], rb[1]), r
+        assert bool(ra[2]["trajectory_finite"]) == bool(rb[2]["trajectory_finite"])
+        assert torch.equal(a.env.sim._state_soa, b.env.sim._state_soa), r
+        assert a.global_step == b.global_step and a.env._post_steps == b.env._post_steps
+
+
+def test_graph_rollout_equals_eager(gpu):
+    """SelfPlayRollout(graph=True) records the rollout once as a HIP graph and replays it; its
+    draws' counters advance on the device.  Four rollouts match the eager collector's."""
+    a = _collector(gpu, nenv=512, T=8, stats=False)
+    b = _collector(gpu, nenv=512, T=8, stats=False, graph=True)
+    _same_rollouts(a, b)
+
+
+def test_graph_league_rollout_equals_eager(gpu):
+    E = import_pkg("rl_env").GpuDogfightVecEnv
+    P = import_pkg("policy")
+    R = import_pkg("ppo")
+
+    def make(graph):
+        env = E(256, seed=5, obs_dim=214, ic_pool_size=64, fuel_exhaustion=True,
+                fuel_lbs_range=(0.0, 3.0))
+        mk = lambda s: P.MLPActorCritic(214, init="normal",
+                                        generator=torch.Generator().manual_seed(s)).to(gpu)
+        ro = R.LeagueRollout(env, mk(1), [mk(60 + k) for k in range(3)], T=6, seed=0, graph=graph)
+        ro.reset(stagger=False)
+        return ro
+    a, b = make(False), make(True)
+    _same_rollouts(a, b)
+    assert a.b_done.sum().item() > 0          # autoresets and opponent redraws happened
