@@ -399,7 +399,7 @@ __global__ void norm_count_kernel(float* __restrict__ count, int nrows) {
 static int norm_blocks(int nrows) { return (nrows + kNormRowsPerBlock - 1) / kNormRowsPerBlock; }
 
 // ---- stable counting sort of items by group (one workgroup; per-thread contiguous chunks)
-constexpr int kGroupThreads = 1024;
+constexpr int kGroupThreads = 256;
 constexpr int kGroupWaves = kGroupThreads / 64;
 
 // exclusive prefix of v over the workgroup's threads (in thread order) and the total
@@ -428,7 +428,7 @@ __device__ __forceinline__ int block_exclusive_scan(int v, int* wave_sum, int& t
 // Three passes over blocks of kGroupItems items: (A) per-block group counts, (B) one small
 // scan giving each (block, group) its output base -- groups in order, blocks in order within a
 // group -- and the group offsets, (C) per-block stable scatter.  Deterministic, no atomics.
-constexpr int kGroupItems = 4096;                 // items per block: 4 per thread
+constexpr int kGroupItems = 1024;                 // items per block: 4 per thread
 
 __device__ __forceinline__ void block_counts(const int* __restrict__ assign, int n, int ngroups,
                                              int i0, int (&c)[F16_POLICY_MAX_GROUPS], int& j0,
@@ -457,19 +457,43 @@ __global__ __launch_bounds__(kGroupThreads) void group_count_kernel(
   }
 }
 
-__global__ void group_base_kernel(int* __restrict__ counts, int nblocks, int ngroups,
-                                  int* __restrict__ offsets) {
-  if (threadIdx.x != 0) return;
-  int s = 0;
-  for (int g = 0; g < ngroups; ++g) {
-    offsets[g] = s;
-    for (int b = 0; b < nblocks; ++b) {            // counts become bases in place
-      const int v = counts[b * F16_POLICY_MAX_GROUPS + g];
-      counts[b * F16_POLICY_MAX_GROUPS + g] = s;
-      s += v;
+// Exclusive scan of the counts in (group, block) order -- groups in order, blocks in order
+// within a group -- written back in place as the (block, group) output bases, with the group
+// offsets.  One workgroup; thread t owns a contiguous run of that order, its loads all in flight.
+constexpr int kBasePer = 16;                      // (group, block) entries per thread per pass
+
+__global__ __launch_bounds__(kGroupThreads) void group_base_kernel(
+    int* __restrict__ counts, int nblocks, int ngroups, int* __restrict__ offsets) {
+  __shared__ int wave_sum[kGroupWaves];
+  const int total_n = nblocks * ngroups;
+  int carry = 0;
+  for (int base0 = 0; base0 < total_n; base0 += kGroupThreads * kBasePer) {   // uniform
+    const int k0 = base0 + threadIdx.x * kBasePer;
+    int v[kBasePer], sum = 0;
+#pragma unroll
+    for (int j = 0; j < kBasePer; ++j) {
+      const int k = k0 + j, g = k / max(nblocks, 1), b = k - g * nblocks;
+      v[j] = k < total_n ? counts[b * F16_POLICY_MAX_GROUPS + g] : 0;
+      sum += v[j];
     }
+    int total;
+    int run = carry + block_exclusive_scan(sum, wave_sum, total);
+#pragma unroll
+    for (int j = 0; j < kBasePer; ++j) {
+      const int k = k0 + j, g = k / max(nblocks, 1), b = k - g * nblocks;
+      if (k < total_n) {
+        if (b == 0) offsets[g] = run;
+        counts[b * F16_POLICY_MAX_GROUPS + g] = run;
+      }
+      run += v[j];
+    }
+    carry += total;
   }
-  offsets[ngroups] = s;
+  if (threadIdx.x == 0) {
+    if (nblocks == 0)
+      for (int g = 0; g < ngroups; ++g) offsets[g] = 0;
+    offsets[ngroups] = carry;
+  }
 }
 
 __global__ __launch_bounds__(kGroupThreads) void group_scatter_kernel(
@@ -512,7 +536,7 @@ extern "C" int f16_group_rows(const int* assign, int n, int ngroups, int stride,
   if (nb > 0)
     hipLaunchKernelGGL(group_count_kernel, dim3(nb), dim3(kGroupThreads), 0, s, assign, n,
                        ngroups, counts);
-  hipLaunchKernelGGL(group_base_kernel, dim3(1), dim3(64), 0, s, counts, nb, ngroups,
+  hipLaunchKernelGGL(group_base_kernel, dim3(1), dim3(kGroupThreads), 0, s, counts, nb, ngroups,
                      group_offsets);
   if (nb > 0)
     hipLaunchKernelGGL(group_scatter_kernel, dim3(nb), dim3(kGroupThreads), 0, s, assign, n,

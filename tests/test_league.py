@@ -29,7 +29,8 @@ def test_zipf_weights():
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("n,ng", [(65536, 8), (70001, 5), (1000, 3), (5, 16), (0, 2)])
+@pytest.mark.parametrize("n,ng", [(65536, 8), (70001, 5), (1000, 3), (5, 16), (0, 2),
+                                  (1000003, 16)])
 def test_group_rows_is_stable_sort(gpu, n, ng):
     L = import_pkg("_lib")
     rng = np.random.default_rng(n + ng)
