@@ -328,51 +328,79 @@ __global__ __launch_bounds__(kThreads, 2) void policy_kernel(const F16PolicyArgs
   }
 }
 
-// ---- RunningNorm.update: column partial sums over 32-row slabs (every load of a slab in flight
-// at once), a per-column fixed-order tree merge (deterministic), and the count update last.
-constexpr int kNormThreads = 256;
-constexpr int kNormRowsPerBlock = 32;
+// ---- RunningNorm.update in two launches.
+// (1) norm_partial_kernel: each block sums 128 rows per column in fp64 (four row phases of 32
+//     rows, every load of a phase in flight, phases combined in a fixed order) and writes one
+//     (sum, sum of squares) per column; block 0 also snapshots the running count into the
+//     workspace and advances it by nrows (the merge reads the snapshot, so no block of the
+//     merge can see the new count).
+// (2) norm_merge_kernel: one block per column; thread t sums partials t, t + 256, ... in order
+//     (all of a thread's loads in flight), then a fixed tree, then the reference's float32
+//     parallel-variance merge.  Deterministic, no atomics.
+constexpr int kNormCols = 256;                   // >= obs_dim
+constexpr int kNormPhases = 4;
+constexpr int kNormRowsPerPhase = 32;
+constexpr int kNormRowsPerBlock = kNormPhases * kNormRowsPerPhase;
+constexpr int kNormChunk = 32;
+constexpr int kMergeThreads = 256;
 
-__global__ __launch_bounds__(kNormThreads) void norm_partial_kernel(
+__global__ __launch_bounds__(kNormCols * kNormPhases) void norm_partial_kernel(
     const float* __restrict__ obs, long ld, const int* __restrict__ rows, int nrows, int dim,
-    double* __restrict__ work) {
-  const int c = threadIdx.x;
+    double* __restrict__ work, float* __restrict__ count, float* __restrict__ count_snap) {
+  __shared__ double ss[kNormPhases][kNormCols], sq[kNormPhases][kNormCols];
+  const int c = threadIdx.x % kNormCols, ph = threadIdx.x / kNormCols;
   const int b = blockIdx.x;
-  if (c >= dim) return;
-  const int i0 = b * kNormRowsPerBlock;
-  float x[kNormRowsPerBlock];
-#pragma unroll
-  for (int i = 0; i < kNormRowsPerBlock; ++i) {
-    const int ri = i0 + i;
-    x[i] = 0.0f;
-    if (ri < nrows) x[i] = obs[(rows ? (long)rows[ri] : (long)ri) * ld + c];
-  }
   double s = 0.0, q = 0.0;
+  if (c < dim) {
+    const int i0 = b * kNormRowsPerBlock + ph * kNormRowsPerPhase;
 #pragma unroll
-  for (int i = 0; i < kNormRowsPerBlock; ++i) {
-    const double v = x[i];
-    s += v;
-    q += v * v;
+    for (int k0 = 0; k0 < kNormRowsPerPhase; k0 += kNormChunk) {
+      float x[kNormChunk];
+#pragma unroll
+      for (int i = 0; i < kNormChunk; ++i) {
+        const int ri = i0 + k0 + i;
+        x[i] = 0.0f;
+        if (ri < nrows) x[i] = obs[(rows ? (long)rows[ri] : (long)ri) * ld + c];
+      }
+#pragma unroll
+      for (int i = 0; i < kNormChunk; ++i) {
+        const double v = x[i];
+        s += v;
+        q += v * v;
+      }
+    }
   }
-  work[(long)b * 2 * dim + c] = s;
-  work[(long)b * 2 * dim + dim + c] = q;
+  ss[ph][c] = s;
+  sq[ph][c] = q;
+  __syncthreads();
+  if (ph == 0 && c < dim) {
+    double S = ss[0][c], Q = sq[0][c];
+#pragma unroll
+    for (int k = 1; k < kNormPhases; ++k) { S += ss[k][c]; Q += sq[k][c]; }
+    work[(long)b * 2 * dim + c] = S;
+    work[(long)b * 2 * dim + dim + c] = Q;
+  }
+  if (b == 0 && threadIdx.x == 0) {
+    const float cnt = *count;
+    *count_snap = cnt;
+    *count = cnt + (float)nrows;
+  }
 }
 
-// one block per column: thread t sums partials t, t + 256, ... in order, then a fixed tree
-__global__ __launch_bounds__(kNormThreads) void norm_merge_kernel(
+__global__ __launch_bounds__(kMergeThreads) void norm_merge_kernel(
     const double* __restrict__ work, int nblocks, int nrows, int dim, float* __restrict__ mean,
-    float* __restrict__ var, const float* __restrict__ count) {
-  __shared__ double ss[kNormThreads], sq[kNormThreads];
+    float* __restrict__ var, const float* __restrict__ count_snap) {
+  __shared__ double ss[kMergeThreads], sq[kMergeThreads];
   const int c = blockIdx.x, t = threadIdx.x;
   double s = 0.0, q = 0.0;
-  for (int b = t; b < nblocks; b += kNormThreads) {
+  for (int b = t; b < nblocks; b += kMergeThreads) {
     s += work[(long)b * 2 * dim + c];
     q += work[(long)b * 2 * dim + dim + c];
   }
   ss[t] = s;
   sq[t] = q;
   __syncthreads();
-  for (int w = kNormThreads / 2; w > 0; w >>= 1) {
+  for (int w = kMergeThreads / 2; w > 0; w >>= 1) {
     if (t < w) { ss[t] += ss[t + w]; sq[t] += sq[t + w]; }
     __syncthreads();
   }
@@ -380,7 +408,7 @@ __global__ __launch_bounds__(kNormThreads) void norm_merge_kernel(
     const double mu = ss[0] / nrows;
     double v = sq[0] / nrows - mu * mu;
     v = v < 0.0 ? 0.0 : v;
-    const float cnt = *count;
+    const float cnt = *count_snap;
     const float b_mean = (float)mu, b_var = (float)v, b_count = (float)nrows;
     const float delta = b_mean - mean[c];
     const float tot = cnt + b_count;
@@ -390,10 +418,6 @@ __global__ __launch_bounds__(kNormThreads) void norm_merge_kernel(
     const float M2 = m_a + m_b + (delta * delta) * (cnt * b_count / tot);
     var[c] = M2 / tot;
   }
-}
-
-__global__ void norm_count_kernel(float* __restrict__ count, int nrows) {
-  if (threadIdx.x == 0) *count = *count + (float)nrows;
 }
 
 static int norm_blocks(int nrows) { return (nrows + kNormRowsPerBlock - 1) / kNormRowsPerBlock; }
@@ -584,20 +608,22 @@ extern "C" int f16_abi_struct_sizes(long* out, int n) {
 
 extern "C" long f16_norm_workspace_bytes(int nrows, int obs_dim) {
   if (nrows < 0 || obs_dim < 0) return -1;
-  return (long)norm_blocks(nrows) * 2 * obs_dim * (long)sizeof(double);
+  return (long)norm_blocks(nrows) * 2 * obs_dim * (long)sizeof(double) + (long)sizeof(double);
 }
 
 extern "C" int f16_norm_update(const float* obs, long obs_ld, const int* rows, int nrows,
                                int obs_dim, float* mean, float* var, float* count, void* work,
                                void* stream) {
-  if (nrows < 0 || obs_dim < 1 || obs_dim > kNormThreads || obs_ld < obs_dim) return F16_EINVAL;
+  if (nrows < 0 || obs_dim < 1 || obs_dim > kNormCols || obs_ld < obs_dim) return F16_EINVAL;
   if (nrows == 0) return 0;
   if (!obs || !mean || !var || !count || !work) return F16_EINVAL;
   const int nb = norm_blocks(nrows);
-  hipLaunchKernelGGL(norm_partial_kernel, dim3(nb), dim3(kNormThreads), 0, (hipStream_t)stream,
-                     obs, obs_ld, rows, nrows, obs_dim, (double*)work);
-  hipLaunchKernelGGL(norm_merge_kernel, dim3(obs_dim), dim3(kNormThreads), 0, (hipStream_t)stream,
-                     (const double*)work, nb, nrows, obs_dim, mean, var, count);
-  hipLaunchKernelGGL(norm_count_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream, count, nrows);
+  double* partial = static_cast<double*>(work);
+  float* snap = reinterpret_cast<float*>(partial + (long)nb * 2 * obs_dim);
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL(norm_partial_kernel, dim3(nb), dim3(kNormCols * kNormPhases), 0, s, obs,
+                     obs_ld, rows, nrows, obs_dim, partial, count, snap);
+  hipLaunchKernelGGL(norm_merge_kernel, dim3(obs_dim), dim3(kMergeThreads), 0, s,
+                     (const double*)partial, nb, nrows, obs_dim, mean, var, snap);
   return f16_last_error();
 }
