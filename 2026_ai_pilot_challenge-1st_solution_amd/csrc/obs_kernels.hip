@@ -648,6 +648,70 @@ __global__ __launch_bounds__(kRowBlock) void build_obs_kernel(
   flush_tile<D, FULL>(S, a0, n, keep, obs, 0, nullptr, lane);
 }
 
+// Autoreset of this lane's aircraft from the initial-condition pool (rl_env.py:559-577): state
+// rows copied in (NaN for a pick outside the pool), reconstructor reset, league opponent redraw,
+// and the new state's kinematics, partner exchange, geometry and re-anchored reward state.
+// Both lanes of an engagement call it together.
+__device__ __forceinline__ void lane_autoreset(const F16EnvStepIO& io, const F16Recon& r,
+                                               const Origin& O, long a, long e, int odd,
+                                               uint32_t step, Kin9& k2, Peer& p2, Geo& g2) {
+  double* __restrict__ st = io.states;
+  const long ld = io.ld;
+  long pk;
+  if (io.pick) {
+    pk = io.pick[e];
+  } else {
+    uint32_t ctr[4] = {(uint32_t)e, step, 0u, 0x5EED5EEDu};
+    f16rng::philox4x32_10(ctr, (uint32_t)io.seed, (uint32_t)(io.seed >> 32));
+    pk = (long)(((uint64_t)ctr[0] * (uint64_t)io.pool_size) >> 32);
+  }
+  const bool ok = pk >= 0 && pk < io.pool_size;
+  const double* src = io.ic_pool + (ok ? pk * 2 + odd : 0) * F16S_N;
+  const double qnan = __builtin_nan("");
+  if (ok) {
+    for (int f = 0; f < F16S_N; ++f) st[f * ld + a] = src[f];
+  } else {
+    for (int f = 0; f < F16S_N; ++f) st[f * ld + a] = qnan;
+  }
+  r.hp[a] = 1.0; r.fuel[a] = 1.0;
+  r.prev_valid[a] = 0; r.prev_x_valid[a] = 0;
+  r.dealt[a] = 0.0; r.taken[a] = 0.0; r.hp_loss[a] = 0.0; r.prev_x[a] = 0.0;
+  r.prev_alt_log[a] = 0.0;
+  if (io.opp_assign && !odd) {                     // league: draw this engagement's opponent
+    uint32_t ctr[4] = {(uint32_t)e, step, 1u, 0x0FF0A55Eu};
+    f16rng::philox4x32_10(ctr, (uint32_t)io.seed, (uint32_t)(io.seed >> 32));
+    const float u = (float)(ctr[0] >> 8) * 0x1p-24f;
+    int kk = io.n_opp - 1;
+    for (int q = io.n_opp - 1; q >= 0; --q)
+      if (io.opp_cdf[q] > u) kk = q;
+    io.opp_assign[e] = kk;
+  }
+  for (int i = 0; i < 3; ++i) {
+    r.prev_att[i * r.ld + a] = 0.0;
+    r.pqr[i * r.ld + a] = 0.0;
+    if (r.accel) { r.accel[i * r.ld + a] = 0.0; r.prev_vel_ned[i * r.ld + a] = 0.0; }
+  }
+  for (int i = 0; i < kActHist; ++i) r.act_hist[i * r.ld + a] = 0.0;
+  if (!odd) r.t_sec[e] = 0.0;
+  if (ok) {
+    make_kin(src, 1, O, k2);
+  } else {
+    const double nan14[14] = {qnan, qnan, qnan, qnan, qnan, qnan, qnan,
+                              qnan, qnan, qnan, qnan, qnan, qnan, qnan};   // fields 0..13
+    make_kin(nan14, 1, O, k2);
+  }
+  exchange(k2, p2);
+  pair_geo(k2, p2, g2);
+  lane_init_reward(k2, p2, g2, a, 0.0, r);
+}
+
+__device__ __forceinline__ ObsIn fresh_obs_in() {
+  ObsIn f;
+  f.hp = 1.0; f.fuel = 1.0; f.dealt = 0.0; f.taken = 0.0; f.t = 0.0;
+  for (int i = 0; i < 3; ++i) { f.pqr[i] = 0.0; f.accel[i] = 0.0; }
+  return f;
+}
+
 template <int D, bool FULL>
 __global__ __launch_bounds__(kRowBlock) void env_post_step_kernel(const F16EnvStepIO io,
                                                                    F16Recon r, F16RewardCfg c,
@@ -663,6 +727,8 @@ __global__ __launch_bounds__(kRowBlock) void env_post_step_kernel(const F16EnvSt
   const int odd = (int)(a & 1);
   double* __restrict__ st = io.states;
   const long ld = io.ld;
+  constexpr int kHistCol = vec_base(D == 214 ? 9 : 7);
+  float* tile = S + lane * tile_pitch<D, FULL>();
   bool d = false;
   Kin9 k;
   Peer p;
@@ -707,77 +773,45 @@ __global__ __launch_bounds__(kRowBlock) void env_post_step_kernel(const F16EnvSt
       const double x = f15[0], y = f15[1], z = f15[2];
       io.terminal_alt_m[a] = (sqrt(x * x + y * y + z * z) - kSeaLevelRadiusFtT) * kFt2M;
     }
-    // terminal observation (rl_env.py:552-554): every row to terminal_obs (or to obs when
-    // there is none); the live engagements' rows are also their observation
-    const ObsOut out{S + lane * tile_pitch<D, FULL>(),
-                     (io.terminal_obs ? io.terminal_obs : io.obs) + a * D,
-                     (io.terminal_obs && !d) ? io.obs + a * D : nullptr};
-    store_run2<D, FULL, vec_base(D == 214 ? 9 : 7), kActHist>(out, o.hist);
+  }
+  if (!io.terminal_obs) {
+    // Nobody asks for the finished engagements' terminal rows, so every row is built once:
+    // from the step's state for live engagements, from the autoreset state for finished ones.
+    if (on && d) {
+      lane_autoreset(io, r, O, a, e, odd, step, k, p, g);
+      o.obs = fresh_obs_in();
+#pragma unroll
+      for (int i = 0; i < kActHist; ++i) o.hist[i] = 0.0f;
+    }
+    if (on) {
+      const ObsOut out{tile, io.obs + a * D, nullptr};
+      store_run2<D, FULL, kHistCol, kActHist>(out, o.hist);
+      lane_build_obs<D, FULL>(k, p, g, o.obs, a, r, out, 1);
+    }
+    const uint64_t rows = __ballot(on);
+    __syncthreads();
+    flush_tile<D, FULL>(S, a0, n, rows, io.obs, 0, nullptr, lane);
+    return;
+  }
+  if (on) {
+    // terminal observation (rl_env.py:552-554): every row to terminal_obs; the live
+    // engagements' rows are also their observation
+    const ObsOut out{tile, io.terminal_obs + a * D, d ? nullptr : io.obs + a * D};
+    store_run2<D, FULL, kHistCol, kActHist>(out, o.hist);
     lane_build_obs<D, FULL>(k, p, g, o.obs, a, r, out, 1);
   }
   const uint64_t rows = __ballot(on), live = __ballot(on && !d), fresh = __ballot(on && d);
   __syncthreads();
-  if (io.terminal_obs)
-    flush_tile<D, FULL>(S, a0, n, rows, io.terminal_obs, live, io.obs, lane);
-  else
-    flush_tile<D, FULL>(S, a0, n, rows, io.obs, 0, nullptr, lane);
+  flush_tile<D, FULL>(S, a0, n, rows, io.terminal_obs, live, io.obs, lane);
   if (!fresh) return;      // uniform: no autoreset in this wave
   __syncthreads();
-  if (on && d) {           // autoreset from the initial-condition pool (rl_env.py:559-577)
-    long pk;
-    if (io.pick) {
-      pk = io.pick[e];
-    } else {
-      uint32_t ctr[4] = {(uint32_t)e, step, 0u, 0x5EED5EEDu};
-      f16rng::philox4x32_10(ctr, (uint32_t)io.seed, (uint32_t)(io.seed >> 32));
-      pk = (long)(((uint64_t)ctr[0] * (uint64_t)io.pool_size) >> 32);
-    }
-    const bool ok = pk >= 0 && pk < io.pool_size;
-    const double* src = io.ic_pool + (ok ? pk * 2 + odd : 0) * F16S_N;
-    const double qnan = __builtin_nan("");
-    if (ok) {
-      for (int f = 0; f < F16S_N; ++f) st[f * ld + a] = src[f];
-    } else {
-      for (int f = 0; f < F16S_N; ++f) st[f * ld + a] = qnan;
-    }
-    r.hp[a] = 1.0; r.fuel[a] = 1.0;
-    r.prev_valid[a] = 0; r.prev_x_valid[a] = 0;
-    r.dealt[a] = 0.0; r.taken[a] = 0.0; r.hp_loss[a] = 0.0; r.prev_x[a] = 0.0;
-    r.prev_alt_log[a] = 0.0;
-    if (io.opp_assign && !odd) {                     // league: draw this engagement's opponent
-      uint32_t ctr[4] = {(uint32_t)e, step, 1u, 0x0FF0A55Eu};
-      f16rng::philox4x32_10(ctr, (uint32_t)io.seed, (uint32_t)(io.seed >> 32));
-      const float u = (float)(ctr[0] >> 8) * 0x1p-24f;
-      int kk = io.n_opp - 1;
-      for (int q = io.n_opp - 1; q >= 0; --q)
-        if (io.opp_cdf[q] > u) kk = q;
-      io.opp_assign[e] = kk;
-    }
-    for (int i = 0; i < 3; ++i) {
-      r.prev_att[i * r.ld + a] = 0.0;
-      r.pqr[i * r.ld + a] = 0.0;
-      if (r.accel) { r.accel[i * r.ld + a] = 0.0; r.prev_vel_ned[i * r.ld + a] = 0.0; }
-    }
-    for (int i = 0; i < kActHist; ++i) r.act_hist[i * r.ld + a] = 0.0;
-    if (!odd) r.t_sec[e] = 0.0;
+  if (on && d) {
     Kin9 k2;
-    if (ok) {
-      make_kin(src, 1, O, k2);
-    } else {
-      const double nan14[14] = {qnan, qnan, qnan, qnan, qnan, qnan, qnan,
-                                qnan, qnan, qnan, qnan, qnan, qnan, qnan};   // fields 0..13
-      make_kin(nan14, 1, O, k2);
-    }
     Peer p2;
-    exchange(k2, p2);
     Geo g2;
-    pair_geo(k2, p2, g2);
-    lane_init_reward(k2, p2, g2, a, 0.0, r);
-    ObsIn fresh;
-    fresh.hp = 1.0; fresh.fuel = 1.0; fresh.dealt = 0.0; fresh.taken = 0.0; fresh.t = 0.0;
-    for (int i = 0; i < 3; ++i) { fresh.pqr[i] = 0.0; fresh.accel[i] = 0.0; }
-    lane_build_obs<D, FULL>(k2, p2, g2, fresh, a, r,
-                            ObsOut{S + lane * tile_pitch<D, FULL>(), io.obs + a * D, nullptr}, 2);
+    lane_autoreset(io, r, O, a, e, odd, step, k2, p2, g2);
+    lane_build_obs<D, FULL>(k2, p2, g2, fresh_obs_in(), a, r,
+                            ObsOut{tile, io.obs + a * D, nullptr}, 2);
   }
   __syncthreads();
   flush_sparse<D, FULL>(S, a0, fresh, io.obs, lane);
