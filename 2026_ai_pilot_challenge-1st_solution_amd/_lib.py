@@ -1,5 +1,5 @@
-"""ctypes binding of libf16hip.so (C ABI declared in include/f16_fdm.h, include/f16_obs.h and
-include/f16_policy.h).
+"""ctypes binding of libf16hip.so (C ABI declared in include/f16_fdm.h, include/f16_obs.h,
+include/f16_policy.h and include/f16_ppo.h).
 
 torch is imported first so that the process's HIP runtime is torch's; the library then binds
 to that same runtime (libamdhip64.so.7) and launches on torch's streams.  There is no CPU
@@ -67,6 +67,23 @@ class F16PolicyArgs(ctypes.Structure):
                 ("step_base", _vp)]
 
 
+class F16PPOArgs(ctypes.Structure):
+    """include/f16_ppo.h F16PPOArgs."""
+    _fields_ = [("obs", _vp), ("obs_ld", _l), ("obs_dim", _i), ("act", _vp), ("old_logp", _vp),
+                ("adv", _vp), ("ret", _vp), ("count", _l), ("idx", _vp), ("mb_rows", _i),
+                ("clip_coef", ctypes.c_float), ("ent_coef", ctypes.c_float),
+                ("vf_coef", ctypes.c_float), ("norm_adv", _i), ("wbf", _vp), ("wf", _vp),
+                ("wT", _vp), ("grad", _vp), ("stats", _vp), ("work", _vp)]
+
+
+class F16AdamArgs(ctypes.Structure):
+    """include/f16_ppo.h F16AdamArgs."""
+    _fields_ = [("obs_dim", _i), ("param", _vp), ("exp_avg", _vp), ("exp_avg_sq", _vp),
+                ("grad", _vp), ("max_grad_norm", ctypes.c_float), ("actor_lr", _d),
+                ("critic_lr", _d), ("beta1", _d), ("beta2", _d), ("eps", _d), ("step", _i),
+                ("grad_norms", _vp), ("wbf", _vp), ("wf", _vp), ("wT", _vp), ("work", _vp)]
+
+
 _RP, _CP = ctypes.POINTER(F16Recon), ctypes.POINTER(F16RewardCfg)
 _SIGNATURES = {
     "f16_fdm_step_batch": (_i, [_vp, _l, _vp, _i, _i, _i, _vp, _l, _vp]),
@@ -86,6 +103,11 @@ _SIGNATURES = {
     "f16_group_rows": (_i, [_vp, _i, _i, _i, _i, _vp, _vp, _vp, _vp]),
     "f16_group_workspace_bytes": (_l, [_i]),
     "f16_norm_update": (_i, [_vp, _l, _vp, _i, _i, _vp, _vp, _vp, _vp, _vp]),
+    "f16_ppo_param_counts": (_i, [_i, ctypes.POINTER(_l)]),
+    "f16_ppo_workspace_bytes": (_l, [_i, _i]),
+    "f16_ppo_grad": (_i, [ctypes.POINTER(F16PPOArgs), _vp]),
+    "f16_ppo_adam_step": (_i, [ctypes.POINTER(F16AdamArgs), _vp]),
+    "f16_ppo_pack": (_i, [_vp, _i, _vp, _vp, _vp, _vp]),
 }
 
 _lib = None

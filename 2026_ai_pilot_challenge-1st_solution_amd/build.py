@@ -16,7 +16,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 ROOT = os.path.dirname(HERE)
 LIB = os.path.join(HERE, "libf16hip.so")
-SOURCES = ["fdm_kernels.hip", "gae_kernel.hip", "obs_kernels.hip", "policy_kernels.hip"]
+SOURCES = ["fdm_kernels.hip", "gae_kernel.hip", "obs_kernels.hip", "policy_kernels.hip",
+           "ppo_kernels.hip"]
 ARCH = os.environ.get("F16_OFFLOAD_ARCH", "gfx950")
 
 

@@ -18,123 +18,12 @@
 
 #include "f16_capi_common.h"
 #include "f16_policy.h"
+#include "f16_ppo.h"
 #include "philox.h"
+#include "policy_mfma.h"
 #include "sample_math.h"
 
 namespace f16pol {
-
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-
-constexpr int kRows = 64;               // observation rows per workgroup
-constexpr int kWaves = 8;
-constexpr int kThreads = 64 * kWaves;
-constexpr int kHid = F16_POLICY_HID;    // 256
-constexpr int kHPitch = kHid + 8;       // bf16 per LDS row of one network's hidden activations
-constexpr int kBins = F16_POLICY_BINS;  // 21
-constexpr int kChan = F16_POLICY_CHANNELS;
-constexpr int kLogits = kBins * kChan;  // 84
-constexpr int kLogitsPad = 96;
-constexpr int kLPitch = 100;            // f32 per LDS row of logits (16-byte rows)
-constexpr int kPrefetch = 3;            // weight K-slices in flight ahead of the MFMAs
-
-// offsets (elements) inside the packed blobs
-template <int KP>
-struct Blob {
-  static constexpr long W1 = 0;
-  static constexpr long W1C = (long)kHid * KP;     // critic rows of W1
-  static constexpr long W2A = 2L * kHid * KP;
-  static constexpr long W2C = W2A + (long)kHid * kHid;
-  static constexpr long W3A = W2C + (long)kHid * kHid;
-  static constexpr long NBF = W3A + (long)kLogitsPad * kHid;
-};
-constexpr int kB1 = 0, kB2A = 512, kB2C = 768, kB3A = 1024, kW3C = 1120, kB3C = 1376;
-static_assert(kB3C + 1 == F16_POLICY_NF, "f32 blob layout");
-
-// tanh for the bf16 hidden activations: sign(x) (1 - t) / (1 + t), t = e^{-2|x|}, from the
-// hardware exp2 and reciprocal (~1 ulp each).  Near 0 the subtraction cancels, but the absolute
-// error stays below 2.5e-7 everywhere, far inside the bf16 rounding step the result is stored with.
-__device__ __forceinline__ float tanh_act(float x) {
-  const float t = __builtin_amdgcn_exp2f(fabsf(x) * -2.8853900817779268f);
-  return copysignf((1.0f - t) * __builtin_amdgcn_rcpf(1.0f + t), x);
-}
-
-__device__ __forceinline__ f32x16 mfma(const bf16x8& a, const bf16x8& b, const f32x16& c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
-}
-
-// acc[r] += W(units u0..u0+31, global [unit][K]) x A(rows 32r.., LDS [row][pitch])^T over K.
-// Units are the MFMA rows, observation rows the MFMA columns: element e of a tile's result held
-// by `lane` is unit 8(e/4) + 4(lane/32) + e%4, row lane%32.  Weights run kPrefetch K-slices
-// ahead, the LDS activation fragments one slice ahead.
-template <int NR, int K>
-__device__ __forceinline__ void gemm_t(f32x16 (&acc)[NR], const __bf16* __restrict__ Wg, int u0,
-                                       const __bf16* __restrict__ As, int a_pitch, int a_col0,
-                                       int lane) {
-  const int lr = lane & 31, lk = (lane >> 5) * 8;
-  constexpr int NK = K / 16;
-  const __bf16* wp = Wg + (long)(u0 + lr) * K + lk;
-  const __bf16* ap = As + lr * a_pitch + a_col0 + lk;
-  bf16x8 w[kPrefetch + 1];
-#pragma unroll
-  for (int q = 0; q < kPrefetch; ++q) w[q] = *reinterpret_cast<const bf16x8*>(wp + 16 * q);
-  bf16x8 a[NR], an[NR];
-#pragma unroll
-  for (int r = 0; r < NR; ++r) a[r] = *reinterpret_cast<const bf16x8*>(ap + 32 * r * a_pitch);
-#pragma unroll
-  for (int s = 0; s < NK; ++s) {
-    if (s + kPrefetch < NK) w[(s + kPrefetch) % (kPrefetch + 1)] =
-        *reinterpret_cast<const bf16x8*>(wp + 16 * (s + kPrefetch));
-    if (s + 1 < NK) {
-#pragma unroll
-      for (int r = 0; r < NR; ++r)
-        an[r] = *reinterpret_cast<const bf16x8*>(ap + 32 * r * a_pitch + 16 * (s + 1));
-    }
-#pragma unroll
-    for (int r = 0; r < NR; ++r) acc[r] = mfma(w[s % (kPrefetch + 1)], a[r], acc[r]);
-#pragma unroll
-    for (int r = 0; r < NR; ++r) a[r] = an[r];
-  }
-}
-
-// accumulators start at the layer's bias: element e of a tile is unit u0 + 8(e/4) + 4(lane/32) + e%4
-template <int NR>
-__device__ __forceinline__ void init_bias(f32x16 (&acc)[NR], const float* __restrict__ bias, int u0,
-                                          int lane) {
-  const int lh = (lane >> 5) * 4;
-#pragma unroll
-  for (int g = 0; g < 4; ++g) {
-    const float4 b = *reinterpret_cast<const float4*>(bias + u0 + 8 * g + lh);
-#pragma unroll
-    for (int r = 0; r < NR; ++r) {
-      acc[r][4 * g + 0] = b.x;
-      acc[r][4 * g + 1] = b.y;
-      acc[r][4 * g + 2] = b.z;
-      acc[r][4 * g + 3] = b.w;
-    }
-  }
-}
-
-// tanh, rounded to bf16, 4 consecutive units per 8-byte LDS store at Hs[row][unit]
-template <int NR>
-__device__ __forceinline__ void store_tanh(const f32x16 (&acc)[NR], __bf16* Hs, int u0, int lane) {
-  const int lr = lane & 31, lh = (lane >> 5) * 4;
-#pragma unroll
-  for (int g = 0; g < 4; ++g) {
-    const int unit = u0 + 8 * g + lh;
-#pragma unroll
-    for (int r = 0; r < NR; ++r) {
-      bf16x4 v;
-      v[0] = (__bf16)tanh_act(acc[r][4 * g + 0]);
-      v[1] = (__bf16)tanh_act(acc[r][4 * g + 1]);
-      v[2] = (__bf16)tanh_act(acc[r][4 * g + 2]);
-      v[3] = (__bf16)tanh_act(acc[r][4 * g + 3]);
-      *reinterpret_cast<bf16x4*>(Hs + (32 * r + lr) * kHPitch + unit) = v;
-    }
-  }
-}
 
 // One network's two tanh layers for the workgroup's 64 rows: X (LDS) -> Hs -> Hs.  Wave w owns
 // units [32w, 32w + 32) of each layer.
@@ -600,9 +489,10 @@ extern "C" int f16_policy_step(const F16PolicyArgs* a, void* stream) {
 }
 
 extern "C" int f16_abi_struct_sizes(long* out, int n) {
-  const long sizes[4] = {(long)sizeof(F16PolicyGroup), (long)sizeof(F16PolicyArgs), 0, 0};
+  const long sizes[4] = {(long)sizeof(F16PolicyGroup), (long)sizeof(F16PolicyArgs),
+                         (long)sizeof(F16PPOArgs), (long)sizeof(F16AdamArgs)};
   if (!out || n < 2) return F16_EINVAL;
-  for (int i = 0; i < 2; ++i) out[i] = sizes[i];
+  for (int i = 0; i < n && i < 4; ++i) out[i] = sizes[i];
   return 0;
 }
 

@@ -1,0 +1,901 @@
+// ppo_kernels.hip -- the PPO update of the discrete actor-critic MLP on gfx950.
+//
+// One minibatch (f16_ppo_grad) is six launches:
+//   adv_stats_kernel   minibatch advantage mean and sample std (fp64 sums, one workgroup);
+//   ppo_fused_kernel   per 64 gathered rows: forward of both networks, the loss head (softmax,
+//                      log-probability, entropy, ratio, clipped surrogate, value error) and the
+//                      backward chain down to the first hidden layer, all with the rows'
+//                      activations held in LDS.  The layer inputs and output gradients every
+//                      weight gradient needs leave unit-major ([feature][row], bf16), so the
+//                      reduction over rows reads them as contiguous MFMA fragments;
+//   wgrad_kernel       every weight gradient dW = dY^T X as one split-K launch: 128 x 128 output
+//                      tiles of all four products, rows in chunks, 32-row stages double-buffered
+//                      through LDS, fp32 partials per chunk (bias gradients are the row sums of
+//                      dY, taken while staging);
+//   colsum_kernel x2   the partials summed in a fixed order (deterministic, no atomics);
+//   stats_kernel       the minibatch means.
+// The optimizer step (f16_ppo_adam_step) is three: per-block squared-norm partials, the clipped
+// Adam update (every block re-reduces the norm partials in the same order), and the repack of
+// the bf16 blobs the rollout and the next minibatch read.
+//
+// The forward runs the same tiles, the same K order and the same epilogue as the rollout kernel
+// (policy_mfma.h), and the log-probability is formed with the same expression sequence, so at
+// unchanged weights the update's log-probability equals the rollout's bit for bit (ratio 1).
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+#include <stdint.h>
+
+#include <algorithm>
+
+#include "f16_capi_common.h"
+#include "f16_policy.h"
+#include "f16_ppo.h"
+#include "policy_mfma.h"
+#include "sample_math.h"
+
+namespace f16ppo {
+
+using namespace f16pol;
+
+constexpr int kZPitch = kLogitsPad + 8;          // bf16 per LDS row of logit gradients
+constexpr int kStatCols = 8;                     // fused-kernel partial row: 8 sums,
+constexpr int kPartCols = kStatCols + kHid + 1 + 7;   // dw3c [256], db3c, pad to 272
+constexpr long kWT3 = 0, kWT2A = 256L * 96, kWT2C = kWT2A + 65536;
+
+// ---- flat parameter offsets (f16_ppo.h)
+struct Flat {
+  long D;
+  __host__ __device__ long a_w1() const { return 0; }
+  __host__ __device__ long a_b1() const { return 256 * D; }
+  __host__ __device__ long a_w2() const { return 256 * D + 256; }
+  __host__ __device__ long a_b2() const { return 256 * D + 65792; }
+  __host__ __device__ long a_w3() const { return 256 * D + 66048; }
+  __host__ __device__ long a_b3() const { return 256 * D + 87552; }
+  __host__ __device__ long na() const { return 256 * D + 87636; }
+  __host__ __device__ long c_w1() const { return na(); }
+  __host__ __device__ long c_b1() const { return na() + 256 * D; }
+  __host__ __device__ long c_w2() const { return na() + 256 * D + 256; }
+  __host__ __device__ long c_b2() const { return na() + 256 * D + 65792; }
+  __host__ __device__ long c_w3() const { return na() + 256 * D + 66048; }
+  __host__ __device__ long c_b3() const { return na() + 256 * D + 66304; }
+  __host__ __device__ long n() const { return na() + 256 * D + 66305; }
+};
+
+// ---- workspace layout; the fixed-size parts come first, so the optimizer's scratch does not
+// move with the minibatch size
+constexpr int kAdvThreads = 1024;
+constexpr int kNormBlockElems = 4096;            // flat elements per squared-norm block
+constexpr int kWChunkTarget = 1024;              // aim for about this many wgrad workgroups
+constexpr int kMaxChunks = 64;                   // > kWChunkTarget / (fewest tiles, 18)
+
+__host__ __device__ inline long align256(long x) { return (x + 255) & ~255L; }
+
+struct Work {
+  float* advs;          // [8]: mean, std, statistics sums
+  double* normp;        // [nblk][2] squared-norm partials
+  __bf16 *xt, *h1t, *h2t, *dh1t, *dh2t, *dzt;   // unit-major, leading dimension ld
+  float* fpart;         // [nwg][kPartCols]
+  float* wpart;         // [nchunk][nflat - 257]
+  long ld;              // rows, rounded up to 64
+  int nwg, nchunk, chunk_rows;
+  long bytes;
+};
+
+inline int norm_blocks(long n) { return (int)((n + kNormBlockElems - 1) / kNormBlockElems); }
+
+inline int wgrad_tiles(int kp) { return 4 * ((kp + 127) / 128) + 4 + 4 + 2; }
+
+inline Work layout(int obs_dim, long mb_rows, void* base) {
+  Work w{};
+  const int kp = (obs_dim + 31) / 32 * 32;
+  const Flat F{obs_dim};
+  w.ld = (mb_rows + 63) / 64 * 64;
+  w.nwg = (int)(w.ld / 64);
+  const int tiles = wgrad_tiles(kp);
+  // chunks of 32-row stages: enough workgroups to fill the chip, at least 8 stages each
+  long chunks = (kWChunkTarget + tiles - 1) / tiles;
+  long cr = (w.ld + chunks - 1) / chunks;
+  cr = (cr + 31) / 32 * 32;
+  if (cr < 256) cr = 256;
+  w.chunk_rows = (int)cr;
+  w.nchunk = (int)((w.ld + cr - 1) / cr);
+  // partial rows are allocated for min(ceil(ld / 256), kMaxChunks) chunks: never fewer than
+  // nchunk (cr >= 256, nchunk <= chunks) and non-decreasing in ld, so a workspace sized for a
+  // minibatch serves every smaller one
+  const long cap = std::min((w.ld + 255) / 256, (long)kMaxChunks);
+  char* p = static_cast<char*>(base);
+  long off = 0;
+  auto take = [&](long bytes) { char* q = p ? p + off : nullptr; off += align256(bytes); return q; };
+  w.advs = reinterpret_cast<float*>(take(64));
+  w.normp = reinterpret_cast<double*>(take((long)norm_blocks(F.n()) * 2 * sizeof(double)));
+  w.xt = reinterpret_cast<__bf16*>(take((long)kp * w.ld * 2));
+  w.h1t = reinterpret_cast<__bf16*>(take(512L * w.ld * 2));
+  w.h2t = reinterpret_cast<__bf16*>(take(512L * w.ld * 2));
+  w.dh1t = reinterpret_cast<__bf16*>(take(512L * w.ld * 2));
+  w.dh2t = reinterpret_cast<__bf16*>(take(512L * w.ld * 2));
+  w.dzt = reinterpret_cast<__bf16*>(take((long)kLogitsPad * w.ld * 2));
+  w.fpart = reinterpret_cast<float*>(take((long)w.nwg * kPartCols * 4));
+  w.wpart = reinterpret_cast<float*>(take(cap * (F.n() - 257) * 4));
+  w.bytes = off;
+  return w;
+}
+
+// ---- minibatch advantage mean and sample standard deviation (ppo_gpu.py:2077-2078)
+__global__ __launch_bounds__(kAdvThreads) void adv_stats_kernel(const float* __restrict__ adv,
+                                                                 const long long* __restrict__ idx,
+                                                                 int n, long count, float* advs) {
+  __shared__ double red[kAdvThreads];
+  const int t = threadIdx.x;
+  double s = 0.0;
+  for (int i = t; i < n; i += kAdvThreads) {
+    const long long p = idx[i];
+    if (p >= 0 && p < count) s += (double)adv[p];
+  }
+  red[t] = s;
+  __syncthreads();
+  for (int w = kAdvThreads / 2; w > 0; w >>= 1) {
+    if (t < w) red[t] += red[t + w];
+    __syncthreads();
+  }
+  const double mean = red[0] / n;
+  __syncthreads();
+  double q = 0.0;
+  for (int i = t; i < n; i += kAdvThreads) {
+    const long long p = idx[i];
+    if (p >= 0 && p < count) {
+      const double d = (double)adv[p] - mean;
+      q += d * d;
+    }
+  }
+  red[t] = q;
+  __syncthreads();
+  for (int w = kAdvThreads / 2; w > 0; w >>= 1) {
+    if (t < w) red[t] += red[t + w];
+    __syncthreads();
+  }
+  if (t == 0) {
+    advs[0] = (float)mean;
+    advs[1] = n > 1 ? (float)sqrt(red[0] / (n - 1)) : 0.0f;
+  }
+}
+
+// ---- fused forward / loss / backward of 64 gathered rows
+
+// LDS [row][pitch] tile -> unit-major global dst[f][m0 + row], 8 rows per 16-byte store
+__device__ __forceinline__ void write_t(const __bf16* S, int pitch, int nfeat, __bf16* dst,
+                                        long ld, long m0, int tid) {
+  for (int it = tid; it < nfeat * 8; it += kThreads) {
+    const int f = it >> 3, g = it & 7;
+    bf16x8 v;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = S[(8 * g + i) * pitch + f];
+    *reinterpret_cast<bf16x8*>(dst + (long)f * ld + m0 + 8 * g) = v;
+  }
+}
+
+// tanh epilogue: bf16 activation to LDS Hs[row][unit] and to unit-major dst[unit][m0 + row]
+template <int NR>
+__device__ __forceinline__ void store_tanh_t(const f32x16 (&acc)[NR], __bf16* Hs, int u0,
+                                             __bf16* dst, long ld, long m0, int lane) {
+  const int lr = lane & 31, lh = (lane >> 5) * 4;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const int unit = u0 + 8 * g + lh;
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      bf16x4 v;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[j] = (__bf16)tanh_act(acc[r][4 * g + j]);
+      const int row = 32 * r + lr;
+      *reinterpret_cast<bf16x4*>(Hs + row * kHPitch + unit) = v;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) dst[(long)(unit + j) * ld + m0 + row] = v[j];
+    }
+  }
+}
+
+// backward epilogue: d = acc * (1 - h^2) with h the layer's bf16 activation at Hs[row][unit];
+// rounded to bf16, to unit-major dst and, when Out is non-null, to Out[row][unit]
+template <int NR>
+__device__ __forceinline__ void store_dtanh_t(const f32x16 (&acc)[NR], const __bf16* Hs,
+                                              __bf16* Out, int u0, __bf16* dst, long ld, long m0,
+                                              int lane) {
+  const int lr = lane & 31, lh = (lane >> 5) * 4;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const int unit = u0 + 8 * g + lh;
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      const int row = 32 * r + lr;
+      const bf16x4 h = *reinterpret_cast<const bf16x4*>(Hs + row * kHPitch + unit);
+      bf16x4 v;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float hv = (float)h[j];
+        v[j] = (__bf16)(acc[r][4 * g + j] * (1.0f - hv * hv));
+      }
+      if (Out) *reinterpret_cast<bf16x4*>(Out + row * kHPitch + unit) = v;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) dst[(long)(unit + j) * ld + m0 + row] = v[j];
+    }
+  }
+}
+
+template <int NR>
+__device__ __forceinline__ void zero_acc(f32x16 (&acc)[NR]) {
+#pragma unroll
+  for (int r = 0; r < NR; ++r)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[r][e] = 0.0f;
+}
+
+template <int KP>
+__global__ __launch_bounds__(kThreads, 1) void ppo_fused_kernel(const F16PPOArgs a, const Work w) {
+  constexpr int XP = KP + 8;
+  constexpr int D = KP == 192 ? 184 : 214;
+  __shared__ __align__(16) __bf16 Xs[kRows * XP];
+  __shared__ __align__(16) __bf16 H1s[kRows * kHPitch];
+  __shared__ __align__(16) __bf16 H2s[kRows * kHPitch];
+  __shared__ __align__(16) float Ls[kRows * kLPitch];     // logits, then (bf16) their gradients
+  __shared__ float rowf[kRows][8];
+  __shared__ long long rowp[kRows];
+  __bf16* Zs = reinterpret_cast<__bf16*>(Ls);
+  static_assert(kRows * kZPitch * 2 <= kRows * kLPitch * 4, "logit gradients overlay the logits");
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const long m0 = (long)blockIdx.x * kRows;
+  const int nr = (int)min((long)kRows, (long)a.mb_rows - m0);
+  const long ld = w.ld;
+  const __bf16* wbf = static_cast<const __bf16*>(a.wbf);
+  const __bf16* wT = static_cast<const __bf16*>(a.wT);
+  const float* wf = a.wf;
+  const float inv_mb = 1.0f / (float)a.mb_rows;
+
+  if (tid < kRows) {
+    long long p = 0;
+    float bad = 0.0f;
+    if (tid < nr) {
+      p = a.idx[m0 + tid];
+      if (p < 0 || p >= a.count) { bad = 1.0f; p = -1; }
+    } else {
+      p = -1;
+    }
+    rowp[tid] = p;                 // -1: no row (past the minibatch or a bad index)
+    rowf[tid][7] = bad;
+  }
+  __syncthreads();
+
+  // ---- gathered rows (already normalised at collection), rounded to bf16
+  {
+    constexpr int half = D / 2;
+    constexpr int kPer = (kRows * half + kThreads - 1) / kThreads;
+    float2 x[kPer];
+#pragma unroll
+    for (int q = 0; q < kPer; ++q) {
+      const int it = tid + q * kThreads;
+      const int r = it / half, c = it - r * half;
+      x[q] = make_float2(0.0f, 0.0f);
+      if (r < kRows && rowp[r] >= 0)
+        x[q] = *reinterpret_cast<const float2*>(a.obs + rowp[r] * a.obs_ld + 2 * c);
+    }
+#pragma unroll
+    for (int q = 0; q < kPer; ++q) {
+      const int it = tid + q * kThreads;
+      const int r = it / half, c = it - r * half;
+      if (r < kRows) {
+        bf16x2 b;
+        b[0] = (__bf16)x[q].x;
+        b[1] = (__bf16)x[q].y;
+        *reinterpret_cast<bf16x2*>(Xs + r * XP + 2 * c) = b;
+      }
+    }
+    for (int it = tid; it < kRows * (KP - D); it += kThreads) {
+      const int r = it / (KP - D);
+      Xs[r * XP + D + (it - r * (KP - D))] = (__bf16)0.0f;
+    }
+  }
+  __syncthreads();
+  write_t(Xs, XP, KP, w.xt, ld, m0, tid);
+
+  // ---- actor forward
+  {
+    f32x16 acc[2];
+    init_bias(acc, wf + kB1, 32 * wave, lane);
+    gemm_t<2, KP>(acc, wbf + Blob<KP>::W1, 32 * wave, Xs, XP, 0, lane);
+    store_tanh_t(acc, H1s, 32 * wave, w.h1t, ld, m0, lane);
+  }
+  __syncthreads();
+  {
+    f32x16 acc[2];
+    init_bias(acc, wf + kB2A, 32 * wave, lane);
+    gemm_t<2, kHid>(acc, wbf + Blob<KP>::W2A, 32 * wave, H1s, kHPitch, 0, lane);
+    store_tanh_t(acc, H2s, 32 * wave, w.h2t, ld, m0, lane);
+  }
+  __syncthreads();
+  if (wave < 6) {
+    const int ut = wave % 3, rt = wave / 3;
+    f32x16 acc[1];
+    init_bias(acc, wf + kB3A, 32 * ut, lane);
+    gemm_t<1, kHid>(acc, wbf + Blob<KP>::W3A, 32 * ut, H2s + 32 * rt * kHPitch, kHPitch, 0, lane);
+    const int row = 32 * rt + (lane & 31);
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int unit = 32 * ut + 8 * g + (lane >> 5) * 4;
+      *reinterpret_cast<float4*>(Ls + row * kLPitch + unit) =
+          make_float4(acc[0][4 * g + 0], acc[0][4 * g + 1], acc[0][4 * g + 2], acc[0][4 * g + 3]);
+    }
+  }
+  __syncthreads();
+
+  // ---- loss head, one lane per (row, channel) (ppo_gpu.py:2065-2090; model.py:207-219)
+  float dz[kBins];
+  if (tid < kRows * kChan) {
+    const int row = tid >> 2, ch = tid & 3;
+    const long long pr = rowp[row];
+    const bool valid = pr >= 0;
+    const float* l = Ls + row * kLPitch + ch * kBins;
+    float lg[kBins];
+#pragma unroll
+    for (int k = 0; k < kBins; ++k) lg[k] = l[k];
+    float m = lg[0];
+#pragma unroll
+    for (int k = 1; k < kBins; ++k)
+      if (lg[k] > m) m = lg[k];
+    float e[kBins], s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kBins; ++k) { e[k] = f16rng::exp_nonpos(lg[k] - m); s += e[k]; }
+    const long long act = valid ? a.act[pr * kChan + ch] : -1;
+    const float lse = logf(s);
+    float lp = 0.0f, hc = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kBins; ++k) {
+      const float lpk = (lg[k] - m) - lse;
+      if (k == act) lp = lpk;
+      hc -= (e[k] / s) * lpk;
+    }
+    lp += __shfl_xor(lp, 1);                // the rollout kernel's summation order
+    lp += __shfl_xor(lp, 2);
+    float ent = hc + __shfl_xor(hc, 1);
+    ent += __shfl_xor(ent, 2);
+    float gcoef = 0.0f, pl = 0.0f, kl = 0.0f, cf = 0.0f;
+    if (valid) {
+      const float logr = lp - a.old_logp[pr];
+      const float ratio = expf(logr);
+      float A = a.adv[pr];
+      if (a.norm_adv && a.mb_rows > 1) A = (A - w.advs[0]) / (w.advs[1] + 1e-8f);
+      const float lo = (float)(1.0 - (double)a.clip_coef), hi = (float)(1.0 + (double)a.clip_coef);
+      const float rc = ratio < lo ? lo : (ratio > hi ? hi : ratio);
+      const float pg1 = -A * ratio, pg2 = -A * rc;
+      const float inr = (ratio >= lo && ratio <= hi) ? 1.0f : 0.0f;
+      // d max(pg1, pg2) / d ratio; torch.max of two tensors shares a tie evenly
+      float dr;
+      if (pg1 > pg2) dr = -A;
+      else if (pg1 < pg2) dr = -A * inr;
+      else dr = 0.5f * -A + 0.5f * (-A * inr);
+      gcoef = dr * ratio * inv_mb;
+      pl = pg1 > pg2 ? pg1 : pg2;
+      kl = (ratio - 1.0f) - logr;
+      cf = fabsf(ratio - 1.0f) > a.clip_coef ? 1.0f : 0.0f;
+    }
+    const float ec = a.ent_coef * inv_mb;
+#pragma unroll
+    for (int k = 0; k < kBins; ++k) {
+      const float pk = e[k] / s;
+      const float lpk = (lg[k] - m) - lse;
+      const float oh = k == act ? 1.0f : 0.0f;
+      dz[k] = valid ? gcoef * (oh - pk) + ec * pk * (lpk + hc) : 0.0f;
+    }
+    if (ch == 0) {
+      rowf[row][0] = pl;
+      rowf[row][1] = valid ? ent : 0.0f;
+      rowf[row][2] = kl;
+      rowf[row][3] = cf;
+    }
+  }
+  __syncthreads();                            // every logit is read
+  if (tid < kRows * kChan) {
+    const int row = tid >> 2, ch = tid & 3;
+#pragma unroll
+    for (int k = 0; k < kBins; ++k) Zs[row * kZPitch + ch * kBins + k] = (__bf16)dz[k];
+    if (ch == 3) {
+#pragma unroll
+      for (int k = kLogits; k < kLogitsPad; ++k) Zs[row * kZPitch + k] = (__bf16)0.0f;
+    }
+  }
+  __syncthreads();
+  write_t(Zs, kZPitch, kLogitsPad, w.dzt, ld, m0, tid);
+
+  // ---- actor backward: dH2 = (dZ W3) (1 - H2^2) in place of H2, dH1 = (dH2 W2) (1 - H1^2)
+  {
+    f32x16 acc[2];
+    zero_acc(acc);
+    gemm_t<2, kLogitsPad>(acc, wT + kWT3, 32 * wave, Zs, kZPitch, 0, lane);
+    store_dtanh_t(acc, H2s, H2s, 32 * wave, w.dh2t, ld, m0, lane);
+  }
+  __syncthreads();
+  {
+    f32x16 acc[2];
+    zero_acc(acc);
+    gemm_t<2, kHid>(acc, wT + kWT2A, 32 * wave, H2s, kHPitch, 0, lane);
+    store_dtanh_t(acc, H1s, nullptr, 32 * wave, w.dh1t, ld, m0, lane);
+  }
+  __syncthreads();
+
+  // ---- critic forward
+  {
+    f32x16 acc[2];
+    init_bias(acc, wf + kB1 + kHid, 32 * wave, lane);
+    gemm_t<2, KP>(acc, wbf + Blob<KP>::W1C, 32 * wave, Xs, XP, 0, lane);
+    store_tanh_t(acc, H1s, 32 * wave, w.h1t + kHid * ld, ld, m0, lane);
+  }
+  __syncthreads();
+  {
+    f32x16 acc[2];
+    init_bias(acc, wf + kB2C, 32 * wave, lane);
+    gemm_t<2, kHid>(acc, wbf + Blob<KP>::W2C, 32 * wave, H1s, kHPitch, 0, lane);
+    store_tanh_t(acc, H2s, 32 * wave, w.h2t + kHid * ld, ld, m0, lane);
+  }
+  __syncthreads();
+  const float* w3 = wf + kW3C;
+  if (wave == 0) {                            // value (the rollout kernel's dot product)
+    const int row = lane;
+    float s = 0.0f;
+#pragma unroll 4
+    for (int k0 = 0; k0 < kHid; k0 += 8) {
+      const bf16x8 h = *reinterpret_cast<const bf16x8*>(H2s + row * kHPitch + k0);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) s += (float)h[q] * w3[k0 + q];
+    }
+    const long long pr = rowp[row];
+    float dv = 0.0f, se = 0.0f;
+    if (pr >= 0) {
+      const float err = (s + wf[kB3C]) - a.ret[pr];
+      se = err * err;
+      dv = a.vf_coef * err * inv_mb;        // d(vf_coef 0.5 mean(err^2)) / dv
+    }
+    rowf[row][4] = dv;
+    rowf[row][5] = se;
+  }
+  __syncthreads();
+  // per-workgroup partials: statistics, dw3c = sum dv h2, db3c = sum dv (rows in order)
+  {
+    float* part = w.fpart + (long)blockIdx.x * kPartCols;
+    if (tid < kHid) {
+      float s = 0.0f;
+      for (int r = 0; r < kRows; ++r) s += rowf[r][4] * (float)H2s[r * kHPitch + tid];
+      part[kStatCols + tid] = s;
+    } else if (tid < kHid + 8) {
+      const int c = tid - kHid;               // 0 pl, 1 ent, 2 kl, 3 cf, 4 dv (db3c), 5 se, 7 bad
+      float s = 0.0f;
+      if (c != 6)
+        for (int r = 0; r < kRows; ++r) s += rowf[r][c];
+      if (c == 4) part[kStatCols + kHid] = s;
+      else part[c] = s;
+    }
+    if (tid == kHid + 8) part[4] = 0.0f;
+    if (tid == kHid + 9) part[6] = 0.0f;
+  }
+  __syncthreads();                            // H2s is read
+  // dH2c = dv w3c (1 - H2c^2), in place and unit-major; lanes run over rows (coalesced stores)
+  for (int it = tid; it < kRows * kHid; it += kThreads) {
+    const int n = it >> 6, row = it & 63;
+    const float h = (float)H2s[row * kHPitch + n];
+    const __bf16 d = (__bf16)(rowf[row][4] * w3[n] * (1.0f - h * h));
+    H2s[row * kHPitch + n] = d;
+    w.dh2t[(long)(kHid + n) * ld + m0 + row] = d;
+  }
+  __syncthreads();
+  {
+    f32x16 acc[2];
+    zero_acc(acc);
+    gemm_t<2, kHid>(acc, wT + kWT2C, 32 * wave, H2s, kHPitch, 0, lane);
+    store_dtanh_t(acc, H1s, nullptr, 32 * wave, w.dh1t + kHid * ld, ld, m0, lane);
+  }
+}
+
+// ---- weight gradients: C[a][b] = sum over rows of A[a][row] B[b][row], split over row chunks
+constexpr int kWT = 128;                  // output tile side
+constexpr int kWK = 32;                   // rows per stage
+constexpr int kWPitch = kWK + 8;          // bf16 per LDS feature row (16-byte reads spread over banks)
+constexpr int kWThreads = 256;
+
+struct WJob {
+  const __bf16* A;
+  const __bf16* B;
+  int nA, nB;          // features present in the buffers (loads beyond read as zero)
+  int vA, vB;          // features that are parameters
+  long wbase[2];       // flat index of W[0][0] for a < 256 and for a >= 256
+  long bbase[2];       // flat index of the bias of a < 256 / a >= 256
+  int wld;             // flat row length of W
+};
+
+struct WJobs {
+  WJob job[4];
+  unsigned char tj[24], ta[24], tb[24];
+  int ntiles;
+};
+
+__global__ __launch_bounds__(kWThreads, 2) void wgrad_kernel(const WJobs J, long ld, long mp,
+                                                             int chunk_rows, float* __restrict__ wpart,
+                                                             long pld) {
+  __shared__ __align__(16) __bf16 As[2][kWT * kWPitch];
+  __shared__ __align__(16) __bf16 Bs[2][kWT * kWPitch];
+  const int tile = blockIdx.x, c = blockIdx.y;
+  const WJob& jb = J.job[J.tj[tile]];
+  const int fa0 = kWT * J.ta[tile], fb0 = kWT * J.tb[tile];
+  const bool bias = J.tb[tile] == 0;
+  const long k0 = (long)c * chunk_rows;
+  const long k1 = min(k0 + chunk_rows, mp);
+  const int nst = k1 > k0 ? (int)((k1 - k0) / kWK) : 0;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wa = wave & 1, wb = wave >> 1;
+  const int part = tid & 3;                   // 8-row piece of a feature's 32 rows
+  bf16x8 ra[2], rb[2];
+  float bsum[2] = {0.0f, 0.0f};
+  const bf16x8 zero8 = {};
+  auto load = [&](int st) {
+    const long k = k0 + (long)st * kWK + 8 * part;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int f = (tid >> 2) + 64 * q;
+      ra[q] = fa0 + f < jb.nA ? *reinterpret_cast<const bf16x8*>(jb.A + (long)(fa0 + f) * ld + k)
+                              : zero8;
+      rb[q] = fb0 + f < jb.nB ? *reinterpret_cast<const bf16x8*>(jb.B + (long)(fb0 + f) * ld + k)
+                              : zero8;
+    }
+  };
+  auto stage = [&](int buf) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int f = (tid >> 2) + 64 * q;
+      *reinterpret_cast<bf16x8*>(&As[buf][f * kWPitch + 8 * part]) = ra[q];
+      *reinterpret_cast<bf16x8*>(&Bs[buf][f * kWPitch + 8 * part]) = rb[q];
+      if (bias) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) bsum[q] += (float)ra[q][i];
+      }
+    }
+  };
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+  if (nst > 0) {
+    load(0);
+    stage(0);
+  }
+  __syncthreads();
+  const int lr = lane & 31, lk = (lane >> 5) * 8;
+  for (int st = 0; st < nst; ++st) {
+    const int buf = st & 1;
+    if (st + 1 < nst) load(st + 1);
+#pragma unroll
+    for (int kk = 0; kk < kWK / 16; ++kk) {
+      bf16x8 af[2], bfg[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        af[i] = *reinterpret_cast<const bf16x8*>(&As[buf][(64 * wa + 32 * i + lr) * kWPitch +
+                                                          16 * kk + lk]);
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        bfg[j] = *reinterpret_cast<const bf16x8*>(&Bs[buf][(64 * wb + 32 * j + lr) * kWPitch +
+                                                           16 * kk + lk]);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = mfma(af[i], bfg[j], acc[i][j]);
+    }
+    if (st + 1 < nst) stage(buf ^ 1);
+    __syncthreads();
+  }
+  float* out = wpart + (long)c * pld;
+  // element e of acc[i][j]: a = fa0 + 64wa + 32i + 8(e/4) + 4(lane/32) + e%4, b = fb0 + 64wb + 32j + lane%32
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int b = fb0 + 64 * wb + 32 * j + lr;
+      if (b >= jb.vB) continue;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int aa = fa0 + 64 * wa + 32 * i + 8 * (e >> 2) + (lane >> 5) * 4 + (e & 3);
+        if (aa < jb.vA)
+          out[jb.wbase[aa >> 8] + (long)(aa & 255) * jb.wld + b] = acc[i][j][e];
+      }
+    }
+  if (bias) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      float s = bsum[q];
+      s += __shfl_xor(s, 1);
+      s += __shfl_xor(s, 2);
+      const int aa = fa0 + (tid >> 2) + 64 * q;
+      if (part == 0 && aa < jb.vA) out[jb.bbase[aa >> 8] + (aa & 255)] = s;
+    }
+  }
+}
+
+// out[c] = sum over r of part[r * ld + c], rows in a fixed order: PH row phases per column
+template <int PH>
+__global__ __launch_bounds__(64 * PH) void colsum_kernel(const float* __restrict__ part, int nrows,
+                                                         long ld, long ncols,
+                                                         float* __restrict__ out) {
+  __shared__ float s[PH][64];
+  const int t = threadIdx.x & 63, ph = threadIdx.x >> 6;
+  const long c = (long)blockIdx.x * 64 + t;
+  float acc = 0.0f;
+  if (c < ncols)
+    for (int r = ph; r < nrows; r += PH) acc += part[(long)r * ld + c];
+  s[ph][t] = acc;
+  __syncthreads();
+  if (ph == 0 && c < ncols) {
+    float v = s[0][t];
+#pragma unroll
+    for (int k = 1; k < PH; ++k) v += s[k][t];
+    out[c] = v;
+  }
+}
+
+// minibatch means (ppo_gpu.py:2080-2081, 2098, 2107-2108)
+__global__ void stats_kernel(const float* __restrict__ sums, const float* __restrict__ advs,
+                             int n, float* __restrict__ stats) {
+  if (threadIdx.x != 0) return;
+  const float fn = (float)n;
+  stats[F16_PPO_STAT_POLICY_LOSS] = sums[0] / fn;
+  stats[F16_PPO_STAT_ENTROPY] = sums[1] / fn;
+  stats[F16_PPO_STAT_APPROX_KL] = sums[2] / fn;
+  stats[F16_PPO_STAT_CLIPFRAC] = sums[3] / fn;
+  stats[F16_PPO_STAT_VALUE_LOSS] = 0.5f * (sums[5] / fn);
+  stats[F16_PPO_STAT_ADV_MEAN] = advs[0];
+  stats[F16_PPO_STAT_ADV_STD] = advs[1];
+  stats[7] = sums[7];
+}
+
+// ---- clip_grad_norm_ + Adam
+__global__ __launch_bounds__(256) void sumsq_kernel(const float* __restrict__ g, long n, long na,
+                                                    double* __restrict__ normp) {
+  __shared__ double sa[256], sc[256];
+  const long b0 = (long)blockIdx.x * kNormBlockElems;
+  double xa = 0.0, xc = 0.0;
+  for (int i = threadIdx.x; i < kNormBlockElems; i += 256) {
+    const long k = b0 + i;
+    if (k < n) {
+      const double v = g[k];
+      if (k < na) xa += v * v;
+      else xc += v * v;
+    }
+  }
+  sa[threadIdx.x] = xa;
+  sc[threadIdx.x] = xc;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if (threadIdx.x < w) { sa[threadIdx.x] += sa[threadIdx.x + w]; sc[threadIdx.x] += sc[threadIdx.x + w]; }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) { normp[2L * blockIdx.x] = sa[0]; normp[2L * blockIdx.x + 1] = sc[0]; }
+}
+
+struct AdamScalars {
+  float lr_step[2];        // -lr / (1 - beta1^t), actor / critic
+  float bc2_sqrt;          // sqrt(1 - beta2^t)
+  float one_m_b1, b2, one_m_b2, eps, max_norm;
+};
+
+__global__ __launch_bounds__(256) void adam_kernel(float* __restrict__ p, float* __restrict__ m,
+                                                   float* __restrict__ v, float* __restrict__ g,
+                                                   long n, long na, const double* __restrict__ normp,
+                                                   int nblk, const AdamScalars S,
+                                                   float* __restrict__ norms_out) {
+  __shared__ double sa[256], sc[256];
+  __shared__ float clip[2];
+  double xa = 0.0, xc = 0.0;
+  for (int b = threadIdx.x; b < nblk; b += 256) { xa += normp[2L * b]; xc += normp[2L * b + 1]; }
+  sa[threadIdx.x] = xa;
+  sc[threadIdx.x] = xc;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if (threadIdx.x < w) { sa[threadIdx.x] += sa[threadIdx.x + w]; sc[threadIdx.x] += sc[threadIdx.x + w]; }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    const float tn[2] = {(float)sqrt(sa[0]), (float)sqrt(sc[0])};
+    for (int k = 0; k < 2; ++k) {
+      float cc = S.max_norm / (tn[k] + 1e-6f);
+      clip[k] = cc > 1.0f ? 1.0f : cc;
+    }
+    if (blockIdx.x == 0 && norms_out) { norms_out[0] = tn[0]; norms_out[1] = tn[1]; }
+  }
+  __syncthreads();
+  const long k = (long)blockIdx.x * 256 + threadIdx.x;
+  if (k >= n) return;
+  const int net = k < na ? 0 : 1;
+  const float gk = g[k] * clip[net];
+  g[k] = gk;
+  float mk = m[k], vk = v[k];
+  mk = mk + S.one_m_b1 * (gk - mk);            // exp_avg.lerp_(grad, 1 - beta1)
+  vk = vk * S.b2;                              // exp_avg_sq.mul_(beta2)
+  vk = vk + S.one_m_b2 * gk * gk;              //   .addcmul_(grad, grad, 1 - beta2)
+  const float denom = sqrtf(vk) / S.bc2_sqrt + S.eps;
+  p[k] = p[k] + S.lr_step[net] * (mk / denom); // param.addcdiv_(exp_avg, denom, -step_size)
+  m[k] = mk;
+  v[k] = vk;
+}
+
+// ---- blobs from the flat master parameters
+template <int KP>
+__global__ __launch_bounds__(256) void pack_kernel(const float* __restrict__ P,
+                                                   __bf16* __restrict__ wbf, float* __restrict__ wf,
+                                                   __bf16* __restrict__ wT) {
+  constexpr int D = KP == 192 ? 184 : 214;
+  const Flat F{D};
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  constexpr long nbf = Blob<KP>::NBF;
+  if (i < nbf) {
+    float x = 0.0f;
+    if (i < Blob<KP>::W2A) {
+      const long r = i / KP, c = i - r * KP;
+      if (c < D) x = r < kHid ? P[F.a_w1() + r * D + c] : P[F.c_w1() + (r - kHid) * D + c];
+    } else if (i < Blob<KP>::W2C) {
+      x = P[F.a_w2() + (i - Blob<KP>::W2A)];
+    } else if (i < Blob<KP>::W3A) {
+      x = P[F.c_w2() + (i - Blob<KP>::W2C)];
+    } else {
+      const long j = i - Blob<KP>::W3A;
+      if (j < (long)kLogits * kHid) x = P[F.a_w3() + j];
+    }
+    if (wbf) wbf[i] = (__bf16)x;
+    return;
+  }
+  long j = i - nbf;
+  if (j < F16_POLICY_NF) {
+    float x = 0.0f;
+    if (j < kB2A) x = j < kHid ? P[F.a_b1() + j] : P[F.c_b1() + j - kHid];
+    else if (j < kB2C) x = P[F.a_b2() + j - kB2A];
+    else if (j < kB3A) x = P[F.c_b2() + j - kB2C];
+    else if (j < kW3C) x = j - kB3A < kLogits ? P[F.a_b3() + j - kB3A] : 0.0f;
+    else if (j < kB3C) x = P[F.c_w3() + j - kW3C];
+    else x = P[F.c_b3()];
+    if (wf) wf[j] = x;
+    return;
+  }
+  j -= F16_POLICY_NF;
+  if (j < F16_PPO_WT_ELEMS && wT) {
+    float x = 0.0f;
+    if (j < kWT2A) {
+      const long nn = j / kLogitsPad, kk = j - nn * kLogitsPad;
+      if (kk < kLogits) x = P[F.a_w3() + kk * kHid + nn];
+    } else if (j < kWT2C) {
+      const long q = j - kWT2A, nn = q / kHid, kk = q - nn * kHid;
+      x = P[F.a_w2() + kk * kHid + nn];
+    } else {
+      const long q = j - kWT2C, nn = q / kHid, kk = q - nn * kHid;
+      x = P[F.c_w2() + kk * kHid + nn];
+    }
+    wT[j] = (__bf16)x;
+  }
+}
+
+template <int KP>
+int launch_pack(const float* param, void* wbf, float* wf, void* wT, hipStream_t s) {
+  const long total = Blob<KP>::NBF + F16_POLICY_NF + F16_PPO_WT_ELEMS;
+  hipLaunchKernelGGL(pack_kernel<KP>, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
+                     param, static_cast<__bf16*>(wbf), wf, static_cast<__bf16*>(wT));
+  return f16_last_error();
+}
+
+}  // namespace f16ppo
+
+using namespace f16ppo;
+
+extern "C" int f16_ppo_param_counts(int obs_dim, long* out2) {
+  if (!out2 || (obs_dim != 184 && obs_dim != 214)) return F16_EINVAL;
+  const Flat F{obs_dim};
+  out2[0] = F.na();
+  out2[1] = F.n() - F.na();
+  return 0;
+}
+
+extern "C" long f16_ppo_workspace_bytes(int obs_dim, int mb_rows) {
+  if ((obs_dim != 184 && obs_dim != 214) || mb_rows < 1) return -1;
+  return layout(obs_dim, mb_rows, nullptr).bytes;
+}
+
+extern "C" int f16_ppo_grad(const F16PPOArgs* a, void* stream) {
+  if (!a || (a->obs_dim != 184 && a->obs_dim != 214)) return F16_EINVAL;
+  if (a->mb_rows < 1 || a->count < 1 || a->obs_ld < a->obs_dim) return F16_EINVAL;
+  if (!a->obs || !a->act || !a->old_logp || !a->adv || !a->ret || !a->idx) return F16_EINVAL;
+  if (!a->wbf || !a->wf || !a->wT || !a->grad || !a->stats || !a->work) return F16_EINVAL;
+  if (((uintptr_t)a->wbf & 15) || ((uintptr_t)a->wT & 15) || ((uintptr_t)a->work & 255))
+    return F16_EINVAL;
+  if ((a->obs_ld & 1) || ((uintptr_t)a->obs & 7)) return F16_EINVAL;   // rows move as float2
+  const int D = a->obs_dim, kp = (D + 31) / 32 * 32;
+  const Flat F{D};
+  const Work w = layout(D, a->mb_rows, a->work);
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL(adv_stats_kernel, dim3(1), dim3(kAdvThreads), 0, s, a->adv, a->idx,
+                     a->mb_rows, a->count, w.advs);
+  if (kp == 192)
+    hipLaunchKernelGGL(ppo_fused_kernel<192>, dim3(w.nwg), dim3(kThreads), 0, s, *a, w);
+  else
+    hipLaunchKernelGGL(ppo_fused_kernel<224>, dim3(w.nwg), dim3(kThreads), 0, s, *a, w);
+  // the four weight-gradient products and their tiles
+  WJobs J{};
+  const long na = F.na();
+  J.job[0] = WJob{w.dh1t, w.xt, 512, kp, 512, D, {F.a_w1(), F.c_w1()}, {F.a_b1(), F.c_b1()}, D};
+  J.job[1] = WJob{w.dh2t, w.h1t, 256, 256, 256, 256, {F.a_w2(), F.a_w2()}, {F.a_b2(), F.a_b2()}, 256};
+  J.job[2] = WJob{w.dh2t + 256L * w.ld, w.h1t + 256L * w.ld, 256, 256, 256, 256,
+                  {F.c_w2(), F.c_w2()}, {F.c_b2(), F.c_b2()}, 256};
+  J.job[3] = WJob{w.dzt, w.h2t, kLogitsPad, 256, kLogits, 256, {F.a_w3(), F.a_w3()},
+                  {F.a_b3(), F.a_b3()}, 256};
+  (void)na;
+  int nt = 0;
+  const int ntA[4] = {4, 2, 2, 1}, ntB[4] = {(kp + 127) / 128, 2, 2, 2};
+  for (int j = 0; j < 4; ++j)
+    for (int ta = 0; ta < ntA[j]; ++ta)
+      for (int tb = 0; tb < ntB[j]; ++tb) {
+        J.tj[nt] = (unsigned char)j;
+        J.ta[nt] = (unsigned char)ta;
+        J.tb[nt] = (unsigned char)tb;
+        ++nt;
+      }
+  J.ntiles = nt;
+  const long pld = F.n() - 257;          // every flat parameter but the critic's value head
+  hipLaunchKernelGGL(wgrad_kernel, dim3(nt, w.nchunk), dim3(kWThreads), 0, s, J, w.ld, w.ld,
+                     w.chunk_rows, w.wpart, pld);
+  hipLaunchKernelGGL(colsum_kernel<4>, dim3((unsigned)((pld + 63) / 64)), dim3(256), 0, s,
+                     (const float*)w.wpart, w.nchunk, pld, pld, a->grad);
+  hipLaunchKernelGGL(colsum_kernel<16>, dim3((unsigned)((kHid + 1 + 63) / 64)), dim3(1024), 0, s,
+                     (const float*)(w.fpart + kStatCols), w.nwg, (long)kPartCols, (long)(kHid + 1),
+                     a->grad + F.c_w3());
+  hipLaunchKernelGGL(colsum_kernel<16>, dim3(1), dim3(1024), 0, s, (const float*)w.fpart, w.nwg,
+                     (long)kPartCols, (long)kStatCols, w.advs + 8);
+  hipLaunchKernelGGL(stats_kernel, dim3(1), dim3(64), 0, s, (const float*)(w.advs + 8),
+                     (const float*)w.advs, a->mb_rows, a->stats);
+  return f16_last_error();
+}
+
+extern "C" int f16_ppo_adam_step(const F16AdamArgs* a, void* stream) {
+  if (!a || (a->obs_dim != 184 && a->obs_dim != 214) || a->step < 1) return F16_EINVAL;
+  if (!a->param || !a->exp_avg || !a->exp_avg_sq || !a->grad || !a->work) return F16_EINVAL;
+  if (((uintptr_t)a->work & 255) || (a->wbf && ((uintptr_t)a->wbf & 15))) return F16_EINVAL;
+  if ((a->wbf == nullptr) != (a->wf == nullptr)) return F16_EINVAL;
+  const Flat F{a->obs_dim};
+  const Work w = layout(a->obs_dim, 1, a->work);
+  const long n = F.n();
+  const int nblk = norm_blocks(n);
+  AdamScalars S;
+  const double t = (double)a->step;
+  const double bc1 = 1.0 - pow(a->beta1, t), bc2 = 1.0 - pow(a->beta2, t);
+  S.lr_step[0] = (float)(-(a->actor_lr / bc1));
+  S.lr_step[1] = (float)(-(a->critic_lr / bc1));
+  S.bc2_sqrt = (float)sqrt(bc2);
+  S.one_m_b1 = (float)(1.0 - a->beta1);
+  S.b2 = (float)a->beta2;
+  S.one_m_b2 = (float)(1.0 - a->beta2);
+  S.eps = (float)a->eps;
+  S.max_norm = a->max_grad_norm;
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL(sumsq_kernel, dim3(nblk), dim3(256), 0, s, (const float*)a->grad, n, F.na(),
+                     w.normp);
+  hipLaunchKernelGGL(adam_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a->param,
+                     a->exp_avg, a->exp_avg_sq, a->grad, n, F.na(), (const double*)w.normp, nblk, S,
+                     a->grad_norms);
+  int rc = f16_last_error();
+  if (rc || (!a->wbf && !a->wT)) return rc;
+  return a->obs_dim == 184 ? launch_pack<192>(a->param, a->wbf, a->wf, a->wT, s)
+                           : launch_pack<224>(a->param, a->wbf, a->wf, a->wT, s);
+}
+
+extern "C" int f16_ppo_pack(const float* param, int obs_dim, void* wbf, float* wf, void* wT,
+                            void* stream) {
+  if (!param || (obs_dim != 184 && obs_dim != 214)) return F16_EINVAL;
+  if ((wbf == nullptr) != (wf == nullptr) || (!wbf && !wT)) return F16_EINVAL;
+  if ((wbf && ((uintptr_t)wbf & 15)) || (wT && ((uintptr_t)wT & 15))) return F16_EINVAL;
+  hipStream_t s = (hipStream_t)stream;
+  return obs_dim == 184 ? launch_pack<192>(param, wbf, wf, wT, s)
+                        : launch_pack<224>(param, wbf, wf, wT, s);
+}

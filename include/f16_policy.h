@@ -83,8 +83,9 @@ long f16_group_workspace_bytes(int n);
 int f16_group_rows(const int *assign, int n, int ngroups, int stride, int offset, int *rows,
                    int *group_offsets, void *work, void *stream);
 
-/* sizeof(F16PolicyGroup), sizeof(F16PolicyArgs) as compiled into the library (out[0..1]), so
- * that a binding can check its struct layout; no counterpart in the reference. */
+/* sizeof(F16PolicyGroup), sizeof(F16PolicyArgs), and with n >= 4 sizeof(F16PPOArgs),
+ * sizeof(F16AdamArgs) (f16_ppo.h) as compiled into the library (out[0..n)), so that a binding
+ * can check its struct layouts; no counterpart in the reference. */
 int f16_abi_struct_sizes(long *out, int n);
 
 /* RunningNorm.update (cuda_fdm/ppo_gpu.py:194-207) from the batch of `nrows` physical rows

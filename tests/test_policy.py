@@ -105,10 +105,12 @@ def test_sampler_closed_forms(orc):
 
 def test_library_struct_layout(pkg):
     L = import_pkg("_lib")
-    out = (ctypes.c_long * 2)()
-    L.check(L.lib().f16_abi_struct_sizes(out, 2), "f16_abi_struct_sizes")
+    out = (ctypes.c_long * 4)()
+    L.check(L.lib().f16_abi_struct_sizes(out, 4), "f16_abi_struct_sizes")
     assert out[0] == ctypes.sizeof(L.F16PolicyGroup)
     assert out[1] == ctypes.sizeof(L.F16PolicyArgs)
+    assert out[2] == ctypes.sizeof(L.F16PPOArgs)
+    assert out[3] == ctypes.sizeof(L.F16AdamArgs)
 
 
 def test_pack_layout():

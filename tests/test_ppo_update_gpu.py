@@ -1,0 +1,252 @@
+"""PPO update on the GPU (f16_ppo_grad / f16_ppo_adam_step / f16_ppo_pack through the C ABI)
+against the CPU oracle (oracle/ppo_oracle.py): minibatch gradients and statistics against the
+bf16-mirrored restatement, the optimizer against torch.optim.Adam + clip_grad_norm_, whole
+updates against the reference's epoch/minibatch loop, the repacked blobs against policy.pack, and
+the first minibatch of a real rollout at ratio 1."""
+import importlib.util
+import math
+import os
+from types import SimpleNamespace
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import ROOT, import_pkg
+
+_spec = importlib.util.spec_from_file_location("ppo_oracle", os.path.join(ROOT, "oracle", "ppo_oracle.py"))
+P = importlib.util.module_from_spec(_spec)
+_spec.loader.exec_module(P)
+
+pytestmark = pytest.mark.gpu
+
+
+def make_net(D, seed=0):
+    pol = import_pkg("policy")
+    torch.manual_seed(seed)
+    return pol.MLPActorCritic(D)                 # orthogonal(sqrt 2) init, model.py:86-90
+
+
+def flat_of(net):
+    U = import_pkg("ppo_update")
+    return torch.cat([p.detach().reshape(-1).float().cpu() for p in U.net_parameters(net)])
+
+
+def fake_rollout(flat, D, T, rows, seed=1, logp_noise=0.15):
+    """Rollout-shaped buffers: normalised observations, drawn bins, collection log-probabilities
+    near the current policy's (bf16-mirrored forward) so ratios straddle the clip range."""
+    g = torch.Generator().manual_seed(seed)
+    M = T * rows
+    obs = (torch.randn(M, D, generator=g) * 1.3).clamp(-10, 10)
+    act = torch.randint(0, P.BINS, (M, P.CH), generator=g)
+    _, st = P.mirror_minibatch(flat, D, obs, act, torch.zeros(M), torch.zeros(M), torch.zeros(M),
+                               norm_adv=False, bf16=True)
+    logp = st["new_logp"] + logp_noise * torch.randn(M, generator=g)
+    adv = torch.randn(M, generator=g) * 2.0 + 0.3
+    ret = torch.randn(M, generator=g)
+    val = torch.randn(M, generator=g)
+    rew = torch.randn(M, generator=g)
+    ro = SimpleNamespace(b_obs=obs.view(T, rows, D), b_act=act.view(T, rows, 4),
+                         b_logp=logp.view(T, rows), b_val=val.view(T, rows),
+                         b_rew=rew.view(T, rows))
+    return ro, adv.view(T, rows), ret.view(T, rows)
+
+
+def to_dev(ro, dev):
+    return SimpleNamespace(**{k: v.to(dev).contiguous() for k, v in vars(ro).items()})
+
+
+def rel_err(a, b):
+    return float((a - b).norm() / max(float(b.norm()), 1e-30))
+
+
+def check_grads(g_gpu, g_ref, D, tol):
+    """Per parameter tensor: relative 2-norm error below tol."""
+    ga, gc = P.unflatten(g_gpu, D)
+    ra, rc = P.unflatten(g_ref, D)
+    worst = 0.0
+    for tag, x, y in (("actor", ga, ra), ("critic", gc, rc)):
+        for k in x:
+            e = rel_err(x[k], y[k])
+            worst = max(worst, e)
+            assert e < tol, (tag, k, e)
+    print(f"  worst per-tensor relative gradient error {worst:.2e}", flush=True)
+
+
+def test_pack_matches_policy_pack(gpu):
+    U = import_pkg("ppo_update")
+    for D in (184, 214):
+        net = make_net(D, seed=3).to(gpu)
+        wbf_ref, wf_ref = (t.clone() for t in net.pack(gpu))
+        up = U.PPOUpdater(net)                   # packs from the flat master copy
+        assert torch.equal(up.wbf, wbf_ref) and torch.equal(up.wf, wf_ref)
+        a, c = net.actor_logits, net.critic
+        wT = up.wT.float().cpu()
+        W3T = wT[:256 * 96].view(256, 96)
+        assert torch.equal(W3T[:, :84], a[4].weight.detach().cpu().t().to(torch.bfloat16).float())
+        assert (W3T[:, 84:] == 0).all()
+        W2aT = wT[256 * 96:256 * 96 + 65536].view(256, 256)
+        W2cT = wT[256 * 96 + 65536:].view(256, 256)
+        assert torch.equal(W2aT, a[2].weight.detach().cpu().t().to(torch.bfloat16).float())
+        assert torch.equal(W2cT, c[2].weight.detach().cpu().t().to(torch.bfloat16).float())
+
+
+@pytest.mark.parametrize("D,mb,ent_coef,norm_adv", [(184, 300, 0.0, True), (214, 300, 0.01, True),
+                                                    (184, 64, 0.01, False), (214, 1, 0.0, True),
+                                                    (184, 2500, 0.0, True)])
+def test_minibatch_grad_matches_oracle(gpu, D, mb, ent_coef, norm_adv):
+    U = import_pkg("ppo_update")
+    print(f"minibatch grad D={D} mb={mb} ent={ent_coef} norm_adv={norm_adv}", flush=True)
+    net = make_net(D, seed=D + mb)
+    flat = flat_of(net)
+    T, rows = 5, 600
+    ro, adv, ret = fake_rollout(flat, D, T, rows, seed=mb)
+    up = U.PPOUpdater(net.to(gpu), U.UpdateConfig(ent_coef=ent_coef, norm_adv=norm_adv))
+    idx = torch.randperm(T * rows, generator=torch.Generator().manual_seed(7))[:mb]
+    d = to_dev(ro, gpu)
+    obs, act, logp = d.b_obs.flatten(0, 1), d.b_act.flatten(0, 1), d.b_logp.flatten()
+    advd, retd = adv.reshape(-1).to(gpu), ret.reshape(-1).to(gpu)
+    up.minibatch_grad(obs, act, logp, advd, retd, idx.to(gpu))
+    stats = up.stats[0].cpu()
+    g_gpu = up.grad.cpu()
+    o = ro.b_obs.flatten(0, 1)[idx]
+    g_ref, st = P.mirror_minibatch(flat, D, o, ro.b_act.flatten(0, 1)[idx],
+                                   ro.b_logp.flatten()[idx], adv.reshape(-1)[idx],
+                                   ret.reshape(-1)[idx], ent_coef=ent_coef, norm_adv=norm_adv)
+    assert torch.isfinite(g_gpu).all()
+    check_grads(g_gpu, g_ref, D, tol=3e-3)
+    U_ = U
+    for k, j in (("pl", U_.STAT_PL), ("vl", U_.STAT_VL), ("ent", U_.STAT_ENT), ("kl", U_.STAT_KL)):
+        assert math.isclose(float(stats[j]), st[k], rel_tol=2e-3, abs_tol=2e-5), (k, float(stats[j]), st[k])
+    # the clip fraction counts rows: at most a few rows at the clip edge may flip
+    assert abs(float(stats[U_.STAT_CF]) - st["cf"]) <= 2.0 / mb + 1e-7
+    a_sel = adv.reshape(-1)[idx].double()
+    assert math.isclose(float(stats[U_.STAT_ADV_MEAN]), float(a_sel.mean()), rel_tol=1e-5, abs_tol=1e-6)
+    if mb > 1:
+        assert math.isclose(float(stats[U_.STAT_ADV_STD]), float(a_sel.std()), rel_tol=1e-5)
+    assert float(stats[U_.STAT_BAD]) == 0.0
+
+
+def test_out_of_range_indices_are_counted_not_read(gpu):
+    U = import_pkg("ppo_update")
+    D = 184
+    net = make_net(D, seed=11)
+    flat = flat_of(net)
+    ro, adv, ret = fake_rollout(flat, D, 2, 100, seed=4)
+    up = U.PPOUpdater(net.to(gpu))
+    d = to_dev(ro, gpu)
+    idx = torch.tensor([3, -5, 17, 200, 250, 199], dtype=torch.int64, device=gpu)   # count 200
+    up.minibatch_grad(d.b_obs.flatten(0, 1), d.b_act.flatten(0, 1), d.b_logp.flatten(),
+                      adv.reshape(-1).to(gpu), ret.reshape(-1).to(gpu), idx)
+    assert float(up.stats[0, U.STAT_BAD]) == 3.0
+    assert torch.isfinite(up.grad).all()
+
+
+def test_optimizer_step_matches_torch_adam(gpu):
+    U = import_pkg("ppo_update")
+    D = 214
+    net = make_net(D, seed=5)
+    flat = flat_of(net)
+    up = U.PPOUpdater(net.to(gpu), U.UpdateConfig(lr=3e-4, critic_lr=1e-3))
+    ref = P.ReferenceOptim(flat, D, lr=3e-4, critic_lr=1e-3, max_grad_norm=0.5)
+    gen = torch.Generator().manual_seed(9)
+    for step in range(4):
+        g = torch.randn(flat.numel(), generator=gen) * (1e-3 if step % 2 else 3e-2)
+        up.grad.copy_(g.to(gpu))
+        up.optimizer_step()
+        na, nc = ref.step(g)
+        p_gpu = up.flat.cpu()
+        p_ref = ref.params()
+        assert torch.allclose(p_gpu, p_ref, rtol=1e-6, atol=1e-8), float((p_gpu - p_ref).abs().max())
+        gn = up.grad_norms.cpu()
+        assert math.isclose(float(gn[0]), na, rel_tol=1e-5)
+        assert math.isclose(float(gn[1]), nc, rel_tol=1e-5)
+    # the rollout blobs follow the master parameters
+    wbf, wf = up.wbf.clone(), up.wf.clone()
+    net.pack(gpu)
+    assert torch.equal(net.packed()[0], wbf) and torch.equal(net.packed()[1], wf)
+
+
+def test_update_matches_reference_loop(gpu):
+    """Two epochs of four minibatches (ragged last) with fixed permutations: final parameters,
+    statistics and norms against the reference loop with the mirrored gradients."""
+    U = import_pkg("ppo_update")
+    D = 184
+    net = make_net(D, seed=21)
+    flat = flat_of(net)
+    T, rows = 4, 130
+    ro, adv, ret = fake_rollout(flat, D, T, rows, seed=22, logp_noise=0.05)
+    count = T * rows
+    gen = torch.Generator().manual_seed(23)
+    perms = [torch.randperm(count, generator=gen) for _ in range(2)]
+    cfg = U.UpdateConfig(update_epochs=2, num_minibatches=4, target_kl=None)
+    up = U.PPOUpdater(net.to(gpu), cfg)
+    res = up.update(to_dev(ro, gpu), adv.to(gpu), ret.to(gpu), perms=perms)
+    mb = (count + 3) // 4
+    p_ref, rr = P.reference_update(flat, D, ro.b_obs.flatten(0, 1), ro.b_act.flatten(0, 1),
+                                   ro.b_logp.flatten(), adv.reshape(-1), ret.reshape(-1), perms,
+                                   mb, target_kl=None)
+    assert res["optimizer_steps"] == rr["optimizer_steps"] == 8
+    assert res["epochs"] == 2 and not res["early"]
+    p_gpu = up.flat.cpu()
+    diff = (p_gpu - p_ref).abs()
+    moved = (p_ref - flat).abs()
+    print("update: max |dp| %.3g, median %.3g; mean step %.3g" %
+          (float(diff.max()), float(diff.median()), float(moved.mean())), flush=True)
+    # Adam makes each coordinate's step the ratio of its moments, so a coordinate-wise relative
+    # gradient difference e (bf16 rounding flips and accumulation order, ~1e-3) moves it by about
+    # e * lr per step, and an element near zero can change sign: bound the worst by the steps'
+    # total, the typical coordinate by 1 % of one step, and the far tail by its share
+    lr, steps = cfg.lr, 8
+    far = float((diff > 0.05 * lr).float().mean())
+    print("  share of coordinates off by more than 5 %% of a step: %.2e" % far, flush=True)
+    assert float(diff.max()) <= 2 * lr * steps
+    assert far < 2e-3
+    assert float(diff.median()) < 1e-2 * lr
+    for k in ("pl", "vl", "ent"):
+        assert math.isclose(float(res[k]), rr[k], rel_tol=5e-3, abs_tol=5e-5), k
+    assert math.isclose(float(res["kl"]), rr["kl"], rel_tol=5e-2, abs_tol=2e-5)
+    assert math.isclose(float(res["actor_grad_norm"]), rr["actor_grad_norm"], rel_tol=5e-3)
+    assert math.isclose(float(res["critic_grad_norm"]), rr["critic_grad_norm"], rel_tol=5e-3)
+
+
+def test_early_stop_and_refusals(gpu):
+    U = import_pkg("ppo_update")
+    D = 184
+    net = make_net(D, seed=31)
+    flat = flat_of(net)
+    ro, adv, ret = fake_rollout(flat, D, 2, 64, seed=32, logp_noise=0.5)
+    up = U.PPOUpdater(net.to(gpu), U.UpdateConfig(target_kl=1e-6, num_minibatches=2))
+    res = up.update(to_dev(ro, gpu), adv.to(gpu), ret.to(gpu))
+    assert res["early"] and res["epochs"] == 1 and res["optimizer_steps"] == 2
+    bad = to_dev(ro, gpu)
+    bad.b_obs[0, 3, 5] = float("nan")
+    with pytest.raises(FloatingPointError):
+        up.update(bad, adv.to(gpu), ret.to(gpu))
+    with pytest.raises(ValueError):
+        up.update(to_dev(ro, gpu), adv[:1].to(gpu), ret.to(gpu))
+
+
+def test_first_minibatch_of_a_rollout_has_ratio_one(gpu):
+    """At the collection weights the update's log-probability equals the rollout kernel's bit
+    for bit: every ratio is exactly 1, so the approximate KL and the clip fraction are 0."""
+    ppo = import_pkg("ppo")
+    U = import_pkg("ppo_update")
+    rl = import_pkg("rl_env")
+    env = rl.GpuDogfightVecEnv(64, seed=0, ic_pool_size=64)
+    net = make_net(184, seed=41).to(gpu)
+    ro = ppo.SelfPlayRollout(env, net, T=8, seed=3, stats=False)
+    ro.reset(stagger=True, max_stagger_steps=8)
+    adv, ret, _ = ro.collect()
+    up = U.PPOUpdater(net)
+    count = ro.b_obs.shape[0] * ro.b_obs.shape[1]
+    idx = torch.arange(count, device=gpu)
+    up.minibatch_grad(ro.b_obs.flatten(0, 1), ro.b_act.flatten(0, 1), ro.b_logp.flatten(),
+                      adv.reshape(-1), ret.reshape(-1), idx)
+    st = up.stats[0].cpu()
+    assert float(st[U.STAT_KL]) == 0.0 and float(st[U.STAT_CF]) == 0.0
+    # a full update then trains: the next rollout runs on the new weights
+    res = up.update(ro, adv, ret)
+    assert res["optimizer_steps"] >= 8
+    adv2, ret2, _ = ro.collect()
+    assert torch.isfinite(adv2).all()
