@@ -52,35 +52,44 @@ __device__ __forceinline__ f32x16 mfma(const bf16x8& a, const bf16x8& b, const f
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
-// acc[r] += W(units u0..u0+31, global [unit][K]) x A(rows 32r.., LDS [row][pitch])^T over K.
-// Units are the MFMA rows, observation rows the MFMA columns: element e of a tile's result held
-// by `lane` is unit 8(e/4) + 4(lane/32) + e%4, row lane%32.  Weights run kPrefetch K-slices
-// ahead, the LDS activation fragments one slice ahead.
-template <int NR, int K>
+// Weight matrices [N][K] are stored fragment-major: one 512-element block per (32-unit tile t,
+// 16-wide K-slice s), blocks in (t, s) order, holding lane l's 8 operand values at [8l, 8l + 8)
+// -- unit 32t + l%32, K columns 16s + 8(l/32) .. +8 -- so a wavefront's fragment load is 1 KB
+// contiguous (8 whole cache lines instead of 32 partial ones).
+
+// acc[r] += W(units u0..u0+31, fragment-major [units][K]) x A(rows 32r.., LDS [row][pitch])^T
+// over K (u0 a multiple of 32).  Units are the MFMA rows, observation rows the MFMA columns:
+// element e of a tile's result held by `lane` is unit 8(e/4) + 4(lane/32) + e%4, row lane%32.
+// Weights run PF K-slices ahead (at most K/16 - 1), the LDS activation fragments one slice ahead.
+template <int NR, int K, int PF = kPrefetch, bool PIN = true>
 __device__ __forceinline__ void gemm_t(f32x16 (&acc)[NR], const __bf16* __restrict__ Wg, int u0,
                                        const __bf16* __restrict__ As, int a_pitch, int a_col0,
                                        int lane) {
+  constexpr int PD = PF < K / 16 ? PF : K / 16 - 1;     // prefetch distance
   const int lr = lane & 31, lk = (lane >> 5) * 8;
   constexpr int NK = K / 16;
-  const __bf16* wp = Wg + (long)(u0 + lr) * K + lk;
+  const __bf16* wp = Wg + (long)(u0 >> 5) * (K / 16) * 512 + lane * 8;
   const __bf16* ap = As + lr * a_pitch + a_col0 + lk;
-  bf16x8 w[kPrefetch + 1];
+  bf16x8 w[PD + 1];
 #pragma unroll
-  for (int q = 0; q < kPrefetch; ++q) w[q] = *reinterpret_cast<const bf16x8*>(wp + 16 * q);
+  for (int q = 0; q < PD; ++q) w[q] = *reinterpret_cast<const bf16x8*>(wp + 512 * q);
   bf16x8 a[NR], an[NR];
 #pragma unroll
   for (int r = 0; r < NR; ++r) a[r] = *reinterpret_cast<const bf16x8*>(ap + 32 * r * a_pitch);
 #pragma unroll
   for (int s = 0; s < NK; ++s) {
-    if (s + kPrefetch < NK) w[(s + kPrefetch) % (kPrefetch + 1)] =
-        *reinterpret_cast<const bf16x8*>(wp + 16 * (s + kPrefetch));
+    if (s + PD < NK) w[(s + PD) % (PD + 1)] =
+        *reinterpret_cast<const bf16x8*>(wp + 512 * (s + PD));
     if (s + 1 < NK) {
 #pragma unroll
       for (int r = 0; r < NR; ++r)
         an[r] = *reinterpret_cast<const bf16x8*>(ap + 32 * r * a_pitch + 16 * (s + 1));
     }
+    // keep the loads above ahead of this slice's MFMAs: left alone, the scheduler sinks each
+    // weight load next to its use and waits out a full L2 round trip every other slice
+    if constexpr (PIN) __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int r = 0; r < NR; ++r) acc[r] = mfma(w[s % (kPrefetch + 1)], a[r], acc[r]);
+    for (int r = 0; r < NR; ++r) acc[r] = mfma(w[s % (PD + 1)], a[r], acc[r]);
 #pragma unroll
     for (int r = 0; r < NR; ++r) a[r] = an[r];
   }

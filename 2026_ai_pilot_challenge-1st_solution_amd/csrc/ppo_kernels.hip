@@ -1,7 +1,7 @@
 // ppo_kernels.hip -- the PPO update of the discrete actor-critic MLP on gfx950.
 //
-// One minibatch (f16_ppo_grad) is six launches:
-//   adv_stats_kernel   minibatch advantage mean and sample std (fp64 sums, one workgroup);
+// One minibatch (f16_ppo_grad) is nine launches:
+//   adv_partial/final  minibatch advantage mean and sample std (shifted fp64 sums, two levels);
 //   ppo_fused_kernel   per 64 gathered rows: forward of both networks, the loss head (softmax,
 //                      log-probability, entropy, ratio, clipped surrogate, value error) and the
 //                      backward chain down to the first hidden layer, all with the rows'
@@ -12,7 +12,7 @@
 //                      tiles of all four products, rows in chunks, 32-row stages double-buffered
 //                      through LDS, fp32 partials per chunk (bias gradients are the row sums of
 //                      dY, taken while staging);
-//   colsum_kernel x2   the partials summed in a fixed order (deterministic, no atomics);
+//   colsum kernels     the partials summed in a fixed order (deterministic, no atomics);
 //   stats_kernel       the minibatch means.
 // The optimizer step (f16_ppo_adam_step) is three: per-block squared-norm partials, the clipped
 // Adam update (every block re-reduces the norm partials in the same order), and the repack of
@@ -39,6 +39,12 @@ namespace f16ppo {
 using namespace f16pol;
 
 constexpr int kZPitch = kLogitsPad + 8;          // bf16 per LDS row of logit gradients
+#ifndef F16_PPO_PREFETCH
+#define F16_PPO_PREFETCH 6
+#endif
+// weight K-slices in flight in the fused kernel: it runs one workgroup (two waves per SIMD) per CU,
+// so each wave keeps more of its weight stream in flight than the rollout kernel does
+constexpr int kFusedPrefetch = F16_PPO_PREFETCH;
 constexpr int kStatCols = 8;                     // fused-kernel partial row: 8 sums,
 constexpr int kPartCols = kStatCols + kHid + 1 + 7;   // dw3c [256], db3c, pad to 272
 constexpr long kWT3 = 0, kWT2A = 256L * 96, kWT2C = kWT2A + 65536;
@@ -64,7 +70,8 @@ struct Flat {
 
 // ---- workspace layout; the fixed-size parts come first, so the optimizer's scratch does not
 // move with the minibatch size
-constexpr int kAdvThreads = 1024;
+constexpr int kAdvThreads = 256;
+constexpr int kAdvPer = 8;                       // rows per thread of the advantage partials
 constexpr int kNormBlockElems = 4096;            // flat elements per squared-norm block
 constexpr int kWChunkTarget = 1024;              // aim for about this many wgrad workgroups
 constexpr int kMaxChunks = 64;                   // > kWChunkTarget / (fewest tiles, 18)
@@ -76,11 +83,16 @@ struct Work {
   double* normp;        // [nblk][2] squared-norm partials
   __bf16 *xt, *h1t, *h2t, *dh1t, *dh2t, *dzt;   // unit-major, leading dimension ld
   float* fpart;         // [nwg][kPartCols]
+  double* advp;         // [nadv][2] advantage partial sums
+  float* fmid;          // [ceil(nwg / kColRows)][kPartCols] first level of the fpart sums
   float* wpart;         // [nchunk][nflat - 257]
   long ld;              // rows, rounded up to 64
-  int nwg, nchunk, chunk_rows;
+  int nwg, nchunk, chunk_rows, nadv;
   long bytes;
 };
+
+constexpr int kColRows = 64;                     // rows per block of the two-level column sum
+inline long kColGroups(long nrows) { return (nrows + kColRows - 1) / kColRows; }
 
 inline int norm_blocks(long n) { return (int)((n + kNormBlockElems - 1) / kNormBlockElems); }
 
@@ -116,47 +128,74 @@ inline Work layout(int obs_dim, long mb_rows, void* base) {
   w.dh2t = reinterpret_cast<__bf16*>(take(512L * w.ld * 2));
   w.dzt = reinterpret_cast<__bf16*>(take((long)kLogitsPad * w.ld * 2));
   w.fpart = reinterpret_cast<float*>(take((long)w.nwg * kPartCols * 4));
+  w.nadv = (int)((w.ld + kAdvThreads * kAdvPer - 1) / (kAdvThreads * kAdvPer));
+  w.advp = reinterpret_cast<double*>(take((long)w.nadv * 2 * sizeof(double)));
+  w.fmid = reinterpret_cast<float*>(take((long)kColGroups(w.nwg) * kPartCols * 4));
   w.wpart = reinterpret_cast<float*>(take(cap * (F.n() - 257) * 4));
   w.bytes = off;
   return w;
 }
 
-// ---- minibatch advantage mean and sample standard deviation (ppo_gpu.py:2077-2078)
-__global__ __launch_bounds__(kAdvThreads) void adv_stats_kernel(const float* __restrict__ adv,
-                                                                 const long long* __restrict__ idx,
-                                                                 int n, long count, float* advs) {
-  __shared__ double red[kAdvThreads];
+// ---- minibatch advantage mean and sample standard deviation (ppo_gpu.py:2077-2078): each block
+// sums (x - K) and (x - K)^2 in fp64 over its rows, K the minibatch's first advantage (shifting
+// keeps the one-pass variance exact to fp64 rounding for any mean); one block merges the partials
+// in a fixed order.
+__global__ __launch_bounds__(kAdvThreads) void adv_partial_kernel(const float* __restrict__ adv,
+                                                                  const long long* __restrict__ idx,
+                                                                  int n, long count,
+                                                                  double* __restrict__ part) {
+  __shared__ double rs[kAdvThreads], rq[kAdvThreads];
   const int t = threadIdx.x;
-  double s = 0.0;
-  for (int i = t; i < n; i += kAdvThreads) {
-    const long long p = idx[i];
-    if (p >= 0 && p < count) s += (double)adv[p];
-  }
-  red[t] = s;
-  __syncthreads();
-  for (int w = kAdvThreads / 2; w > 0; w >>= 1) {
-    if (t < w) red[t] += red[t + w];
-    __syncthreads();
-  }
-  const double mean = red[0] / n;
-  __syncthreads();
-  double q = 0.0;
-  for (int i = t; i < n; i += kAdvThreads) {
-    const long long p = idx[i];
-    if (p >= 0 && p < count) {
-      const double d = (double)adv[p] - mean;
-      q += d * d;
+  const long long p0 = idx[0];
+  const double K = (p0 >= 0 && p0 < count) ? (double)adv[p0] : 0.0;
+  double s = 0.0, q = 0.0;
+  const int i = blockIdx.x * kAdvThreads * kAdvPer + t;
+#pragma unroll
+  for (int k = 0; k < kAdvPer; ++k) {
+    const int ii = i + k * kAdvThreads;
+    if (ii < n) {
+      const long long p = idx[ii];
+      if (p >= 0 && p < count) {
+        const double d = (double)adv[p] - K;
+        s += d;
+        q += d * d;
+      }
     }
   }
-  red[t] = q;
+  rs[t] = s;
+  rq[t] = q;
   __syncthreads();
   for (int w = kAdvThreads / 2; w > 0; w >>= 1) {
-    if (t < w) red[t] += red[t + w];
+    if (t < w) { rs[t] += rs[t + w]; rq[t] += rq[t + w]; }
+    __syncthreads();
+  }
+  if (t == 0) { part[2L * blockIdx.x] = rs[0]; part[2L * blockIdx.x + 1] = rq[0]; }
+}
+
+__global__ __launch_bounds__(kAdvThreads) void adv_final_kernel(const float* __restrict__ adv,
+                                                                const long long* __restrict__ idx,
+                                                                int n, long count, int nblk,
+                                                                const double* __restrict__ part,
+                                                                float* advs) {
+  __shared__ double rs[kAdvThreads], rq[kAdvThreads];
+  const int t = threadIdx.x;
+  double s = 0.0, q = 0.0;
+  for (int b = t; b < nblk; b += kAdvThreads) { s += part[2L * b]; q += part[2L * b + 1]; }
+  rs[t] = s;
+  rq[t] = q;
+  __syncthreads();
+  for (int w = kAdvThreads / 2; w > 0; w >>= 1) {
+    if (t < w) { rs[t] += rs[t + w]; rq[t] += rq[t + w]; }
     __syncthreads();
   }
   if (t == 0) {
-    advs[0] = (float)mean;
-    advs[1] = n > 1 ? (float)sqrt(red[0] / (n - 1)) : 0.0f;
+    const long long p0 = idx[0];
+    const double K = (p0 >= 0 && p0 < count) ? (double)adv[p0] : 0.0;
+    const double ms = rs[0] / n;                       // mean of the shifted values
+    double var = n > 1 ? (rq[0] - rs[0] * ms) / (n - 1) : 0.0;
+    var = var < 0.0 ? 0.0 : var;
+    advs[0] = (float)(K + ms);
+    advs[1] = (float)sqrt(var);
   }
 }
 
@@ -302,14 +341,14 @@ __global__ __launch_bounds__(kThreads, 1) void ppo_fused_kernel(const F16PPOArgs
   {
     f32x16 acc[2];
     init_bias(acc, wf + kB1, 32 * wave, lane);
-    gemm_t<2, KP>(acc, wbf + Blob<KP>::W1, 32 * wave, Xs, XP, 0, lane);
+    gemm_t<2, KP, kFusedPrefetch>(acc, wbf + Blob<KP>::W1, 32 * wave, Xs, XP, 0, lane);
     store_tanh_t(acc, H1s, 32 * wave, w.h1t, ld, m0, lane);
   }
   __syncthreads();
   {
     f32x16 acc[2];
     init_bias(acc, wf + kB2A, 32 * wave, lane);
-    gemm_t<2, kHid>(acc, wbf + Blob<KP>::W2A, 32 * wave, H1s, kHPitch, 0, lane);
+    gemm_t<2, kHid, kFusedPrefetch>(acc, wbf + Blob<KP>::W2A, 32 * wave, H1s, kHPitch, 0, lane);
     store_tanh_t(acc, H2s, 32 * wave, w.h2t, ld, m0, lane);
   }
   __syncthreads();
@@ -317,7 +356,7 @@ __global__ __launch_bounds__(kThreads, 1) void ppo_fused_kernel(const F16PPOArgs
     const int ut = wave % 3, rt = wave / 3;
     f32x16 acc[1];
     init_bias(acc, wf + kB3A, 32 * ut, lane);
-    gemm_t<1, kHid>(acc, wbf + Blob<KP>::W3A, 32 * ut, H2s + 32 * rt * kHPitch, kHPitch, 0, lane);
+    gemm_t<1, kHid, kFusedPrefetch>(acc, wbf + Blob<KP>::W3A, 32 * ut, H2s + 32 * rt * kHPitch, kHPitch, 0, lane);
     const int row = 32 * rt + (lane & 31);
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
@@ -410,14 +449,14 @@ __global__ __launch_bounds__(kThreads, 1) void ppo_fused_kernel(const F16PPOArgs
   {
     f32x16 acc[2];
     zero_acc(acc);
-    gemm_t<2, kLogitsPad>(acc, wT + kWT3, 32 * wave, Zs, kZPitch, 0, lane);
+    gemm_t<2, kLogitsPad, kFusedPrefetch>(acc, wT + kWT3, 32 * wave, Zs, kZPitch, 0, lane);
     store_dtanh_t(acc, H2s, H2s, 32 * wave, w.dh2t, ld, m0, lane);
   }
   __syncthreads();
   {
     f32x16 acc[2];
     zero_acc(acc);
-    gemm_t<2, kHid>(acc, wT + kWT2A, 32 * wave, H2s, kHPitch, 0, lane);
+    gemm_t<2, kHid, kFusedPrefetch>(acc, wT + kWT2A, 32 * wave, H2s, kHPitch, 0, lane);
     store_dtanh_t(acc, H1s, nullptr, 32 * wave, w.dh1t, ld, m0, lane);
   }
   __syncthreads();
@@ -426,14 +465,14 @@ __global__ __launch_bounds__(kThreads, 1) void ppo_fused_kernel(const F16PPOArgs
   {
     f32x16 acc[2];
     init_bias(acc, wf + kB1 + kHid, 32 * wave, lane);
-    gemm_t<2, KP>(acc, wbf + Blob<KP>::W1C, 32 * wave, Xs, XP, 0, lane);
+    gemm_t<2, KP, kFusedPrefetch>(acc, wbf + Blob<KP>::W1C, 32 * wave, Xs, XP, 0, lane);
     store_tanh_t(acc, H1s, 32 * wave, w.h1t + kHid * ld, ld, m0, lane);
   }
   __syncthreads();
   {
     f32x16 acc[2];
     init_bias(acc, wf + kB2C, 32 * wave, lane);
-    gemm_t<2, kHid>(acc, wbf + Blob<KP>::W2C, 32 * wave, H1s, kHPitch, 0, lane);
+    gemm_t<2, kHid, kFusedPrefetch>(acc, wbf + Blob<KP>::W2C, 32 * wave, H1s, kHPitch, 0, lane);
     store_tanh_t(acc, H2s, 32 * wave, w.h2t + kHid * ld, ld, m0, lane);
   }
   __syncthreads();
@@ -489,7 +528,7 @@ __global__ __launch_bounds__(kThreads, 1) void ppo_fused_kernel(const F16PPOArgs
   {
     f32x16 acc[2];
     zero_acc(acc);
-    gemm_t<2, kHid>(acc, wT + kWT2C, 32 * wave, H2s, kHPitch, 0, lane);
+    gemm_t<2, kHid, kFusedPrefetch>(acc, wT + kWT2C, 32 * wave, H2s, kHPitch, 0, lane);
     store_dtanh_t(acc, H1s, nullptr, 32 * wave, w.dh1t + kHid * ld, ld, m0, lane);
   }
 }
@@ -640,6 +679,23 @@ __global__ __launch_bounds__(64 * PH) void colsum_kernel(const float* __restrict
   }
 }
 
+// first level over the fused kernel's partial rows: block (x, y) sums rows [64y, 64y + 64) of
+// columns [64x, 64x + 64) (4 phases of 16 rows, combined in order)
+__global__ __launch_bounds__(256) void colsum_group_kernel(const float* __restrict__ part, int nrows,
+                                                           float* __restrict__ mid) {
+  __shared__ float sm[4][64];
+  const int t = threadIdx.x & 63, ph = threadIdx.x >> 6;
+  const int c = blockIdx.x * 64 + t;
+  const int r0 = blockIdx.y * kColRows;
+  float acc = 0.0f;
+  if (c < kPartCols)
+    for (int r = r0 + ph; r < min(r0 + kColRows, nrows); r += 4) acc += part[(long)r * kPartCols + c];
+  sm[ph][t] = acc;
+  __syncthreads();
+  if (ph == 0 && c < kPartCols)
+    mid[(long)blockIdx.y * kPartCols + c] = (sm[0][t] + sm[1][t]) + (sm[2][t] + sm[3][t]);
+}
+
 // minibatch means (ppo_gpu.py:2080-2081, 2098, 2107-2108)
 __global__ void stats_kernel(const float* __restrict__ sums, const float* __restrict__ advs,
                              int n, float* __restrict__ stats) {
@@ -735,17 +791,26 @@ __global__ __launch_bounds__(256) void pack_kernel(const float* __restrict__ P,
   const long i = (long)blockIdx.x * 256 + threadIdx.x;
   constexpr long nbf = Blob<KP>::NBF;
   if (i < nbf) {
+    // fragment-major blocks: element q of a matrix [N][K] is (n, k) of block q / 512
+    auto unfrag = [](long q, long K, long& n, long& k) {
+      const long blk = q >> 9, r = q & 511, l = r >> 3;
+      n = (blk / (K >> 4)) * 32 + (l & 31);
+      k = (blk % (K >> 4)) * 16 + (l >> 5) * 8 + (r & 7);
+    };
     float x = 0.0f;
+    long n, k;
     if (i < Blob<KP>::W2A) {
-      const long r = i / KP, c = i - r * KP;
-      if (c < D) x = r < kHid ? P[F.a_w1() + r * D + c] : P[F.c_w1() + (r - kHid) * D + c];
+      unfrag(i, KP, n, k);
+      if (k < D) x = n < kHid ? P[F.a_w1() + n * D + k] : P[F.c_w1() + (n - kHid) * D + k];
     } else if (i < Blob<KP>::W2C) {
-      x = P[F.a_w2() + (i - Blob<KP>::W2A)];
+      unfrag(i - Blob<KP>::W2A, kHid, n, k);
+      x = P[F.a_w2() + n * kHid + k];
     } else if (i < Blob<KP>::W3A) {
-      x = P[F.c_w2() + (i - Blob<KP>::W2C)];
+      unfrag(i - Blob<KP>::W2C, kHid, n, k);
+      x = P[F.c_w2() + n * kHid + k];
     } else {
-      const long j = i - Blob<KP>::W3A;
-      if (j < (long)kLogits * kHid) x = P[F.a_w3() + j];
+      unfrag(i - Blob<KP>::W3A, kHid, n, k);
+      if (n < kLogits) x = P[F.a_w3() + n * kHid + k];
     }
     if (wbf) wbf[i] = (__bf16)x;
     return;
@@ -764,15 +829,18 @@ __global__ __launch_bounds__(256) void pack_kernel(const float* __restrict__ P,
   }
   j -= F16_POLICY_NF;
   if (j < F16_PPO_WT_ELEMS && wT) {
+    // transposed matrices, fragment-major: W3a^T [256][96], W2a^T and W2c^T [256][256]
+    const long base = j < kWT2A ? 0 : (j < kWT2C ? kWT2A : kWT2C);
+    const long K = j < kWT2A ? kLogitsPad : kHid;
+    const long q = j - base, blk = q >> 9, r = q & 511, l = r >> 3;
+    const long nn = (blk / (K >> 4)) * 32 + (l & 31);
+    const long kk = (blk % (K >> 4)) * 16 + (l >> 5) * 8 + (r & 7);
     float x = 0.0f;
     if (j < kWT2A) {
-      const long nn = j / kLogitsPad, kk = j - nn * kLogitsPad;
       if (kk < kLogits) x = P[F.a_w3() + kk * kHid + nn];
     } else if (j < kWT2C) {
-      const long q = j - kWT2A, nn = q / kHid, kk = q - nn * kHid;
       x = P[F.a_w2() + kk * kHid + nn];
     } else {
-      const long q = j - kWT2C, nn = q / kHid, kk = q - nn * kHid;
       x = P[F.c_w2() + kk * kHid + nn];
     }
     wT[j] = (__bf16)x;
@@ -816,8 +884,10 @@ extern "C" int f16_ppo_grad(const F16PPOArgs* a, void* stream) {
   const Flat F{D};
   const Work w = layout(D, a->mb_rows, a->work);
   hipStream_t s = (hipStream_t)stream;
-  hipLaunchKernelGGL(adv_stats_kernel, dim3(1), dim3(kAdvThreads), 0, s, a->adv, a->idx,
-                     a->mb_rows, a->count, w.advs);
+  hipLaunchKernelGGL(adv_partial_kernel, dim3(w.nadv), dim3(kAdvThreads), 0, s, a->adv, a->idx,
+                     a->mb_rows, a->count, w.advp);
+  hipLaunchKernelGGL(adv_final_kernel, dim3(1), dim3(kAdvThreads), 0, s, a->adv, a->idx,
+                     a->mb_rows, a->count, w.nadv, (const double*)w.advp, w.advs);
   if (kp == 192)
     hipLaunchKernelGGL(ppo_fused_kernel<192>, dim3(w.nwg), dim3(kThreads), 0, s, *a, w);
   else
@@ -848,10 +918,14 @@ extern "C" int f16_ppo_grad(const F16PPOArgs* a, void* stream) {
                      w.chunk_rows, w.wpart, pld);
   hipLaunchKernelGGL(colsum_kernel<4>, dim3((unsigned)((pld + 63) / 64)), dim3(256), 0, s,
                      (const float*)w.wpart, w.nchunk, pld, pld, a->grad);
-  hipLaunchKernelGGL(colsum_kernel<16>, dim3((unsigned)((kHid + 1 + 63) / 64)), dim3(1024), 0, s,
-                     (const float*)(w.fpart + kStatCols), w.nwg, (long)kPartCols, (long)(kHid + 1),
+  // the per-workgroup partials (statistics, dw3c, db3c): groups of kColRows rows, then the groups
+  const int ng = (int)kColGroups(w.nwg);
+  hipLaunchKernelGGL(colsum_group_kernel, dim3((kPartCols + 63) / 64, ng), dim3(256), 0, s,
+                     (const float*)w.fpart, w.nwg, w.fmid);
+  hipLaunchKernelGGL(colsum_kernel<4>, dim3((unsigned)((kHid + 1 + 63) / 64)), dim3(256), 0, s,
+                     (const float*)(w.fmid + kStatCols), ng, (long)kPartCols, (long)(kHid + 1),
                      a->grad + F.c_w3());
-  hipLaunchKernelGGL(colsum_kernel<16>, dim3(1), dim3(1024), 0, s, (const float*)w.fpart, w.nwg,
+  hipLaunchKernelGGL(colsum_kernel<4>, dim3(1), dim3(256), 0, s, (const float*)w.fmid, ng,
                      (long)kPartCols, (long)kStatCols, w.advs + 8);
   hipLaunchKernelGGL(stats_kernel, dim3(1), dim3(64), 0, s, (const float*)(w.advs + 8),
                      (const float*)w.advs, a->mb_rows, a->stats);

@@ -43,6 +43,20 @@ def kpad(obs_dim):
     return (int(obs_dim) + 31) // 32 * 32
 
 
+def frag_major(w):
+    """(N, K) matrix -> the kernels' fragment-major order (N % 32 == 0, K % 16 == 0): one 512-element
+    block per (32-row tile, 16-column slice), element (n, k) of a block at lane
+    32 ((k % 16) // 8) + n % 32, position k % 8 -- the bf16x8 operand lane l of a
+    32x32x16 MFMA reads, so each wavefront's load of one block is 1 KB contiguous."""
+    N, K = w.shape
+    return w.reshape(N // 32, 32, K // 16, 2, 8).permute(0, 2, 3, 1, 4).reshape(-1)
+
+
+def frag_unmajor(v, N, K):
+    """Inverse of frag_major: flat blocks -> (N, K)."""
+    return v.reshape(N // 32, K // 16, 2, 32, 8).permute(0, 3, 1, 2, 4).reshape(N, K)
+
+
 def _mlp(in_dim, hidden, out_dim):
     layers, last = [], in_dim
     for h in hidden:
@@ -97,8 +111,8 @@ class MLPActorCritic(torch.nn.Module):
         w1[HIDDEN:, :self.obs_dim] = c[0].weight.float().cpu()
         w3 = torch.zeros(LOGITS_PAD, HIDDEN)
         w3[:self.act_dim * self.num_bins] = a[4].weight.float().cpu()
-        wbf = torch.cat([w1.flatten(), a[2].weight.float().cpu().flatten(),
-                         c[2].weight.float().cpu().flatten(), w3.flatten()]).to(torch.bfloat16)
+        wbf = torch.cat([frag_major(w1), frag_major(a[2].weight.float().cpu()),
+                         frag_major(c[2].weight.float().cpu()), frag_major(w3)]).to(torch.bfloat16)
         b3 = torch.zeros(LOGITS_PAD)
         b3[:self.act_dim * self.num_bins] = a[4].bias.float().cpu()
         wf = torch.cat([a[0].bias.float().cpu(), c[0].bias.float().cpu(), a[2].bias.float().cpu(),

@@ -196,6 +196,65 @@ def rollout_bench(nenv, T=64, reps=2):
                             "frac": flop / (pol_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS}}
 
 
+def update_bench(nenv, T=64, reps=2):
+    """The PPO update after a BASELINE C4 rollout (PPOGPUTrainer.update, ppo_gpu.py:2019-2145):
+    both aircraft's transitions (T x 2 nenv), the reference's PPOConfig (clip 0.2, 8 minibatches,
+    Adam 3e-4 / eps 1e-5, max grad norm 0.5) with all 4 epochs (no KL early stop, so every run
+    does the same work).  Per minibatch: f16_ppo_grad (forward, loss, backward, weight gradients)
+    and f16_ppo_adam_step (clip + Adam + blob repack)."""
+    import torch
+    env_mod = importlib.import_module(PKG + ".rl_env")
+    pol = importlib.import_module(PKG + ".policy")
+    ppo = importlib.import_module(PKG + ".ppo")
+    U = importlib.import_module(PKG + ".ppo_update")
+    env = env_mod.GpuDogfightVecEnv(nenv, seed=0)
+    net = pol.MLPActorCritic(184, init="normal", init_std=0.02,
+                             generator=torch.Generator().manual_seed(0)).to("cuda")
+    ro = ppo.SelfPlayRollout(env, net, T=T, gamma=0.99, lam=0.95, seed=0, stats=False)
+    ro.reset(stagger=False)
+    adv, ret, _ = ro.collect()
+    up = U.PPOUpdater(net, U.UpdateConfig(target_kl=None), seed=0)
+    up.update(ro, adv, ret)                         # warm-up (workspace allocation)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        res = up.update(ro, adv, ret)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    # one epoch with events around each call
+    obs, act = ro.b_obs.flatten(0, 1), ro.b_act.flatten(0, 1)
+    logp, a, r = ro.b_logp.flatten(), adv.reshape(-1), ret.reshape(-1)
+    count = obs.shape[0]
+    mb = (count + 7) // 8
+    perm = torch.randperm(count, device="cuda")
+    ev = []
+    for s in range(0, count, mb):
+        t = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        t[0].record()
+        up.minibatch_grad(obs, act, logp, a, r, perm[s:s + mb], up.stats[0])
+        t[1].record()
+        up.optimizer_step()
+        t[2].record()
+        ev.append(t)
+    torch.cuda.synchronize()
+    grad_ms = float(np.mean([x[0].elapsed_time(x[1]) for x in ev]))
+    adam_ms = float(np.mean([x[1].elapsed_time(x[2]) for x in ev]))
+    flop_mb = U.update_flop_per_row(184) * mb
+    if not bool(torch.isfinite(up.flat).all()):
+        raise FloatingPointError("non-finite parameters after the update")
+    return {"workload": "ppo_update_selfplay_16k_T64", "transitions": count, "epochs": res["epochs"],
+            "minibatches": (count + mb - 1) // mb, "minibatch_rows": mb, "ms_per_update": ms,
+            "transitions_per_s": count * res["epochs"] / (ms * 1e-3),
+            "minibatch_grad_ms": grad_ms, "optimizer_step_ms": adam_ms,
+            "mfma": {"what": "f16_ppo_grad (all its launches)", "flop_per_minibatch": flop_mb,
+                     "achieved_TFLOPs": flop_mb / (grad_ms * 1e-3) / 1e12,
+                     "peak_TFLOPs": PEAK_BF16_TFLOPS,
+                     "frac": flop_mb / (grad_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS},
+            "stats": {k: float(res[k]) for k in ("pl", "vl", "ent", "kl", "cf", "ev")}}
+
+
 def league_bench(nenv=65536, T=128, nopp=8, reps=2):
     """BASELINE C5: nenv engagements x T-step league rollout with the 214-D observation: the
     learner (plane 0) and 8 frozen random-init opponents (plane 1, bf16 N(0, 0.02)) assigned per
@@ -261,7 +320,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-rollout", action="store_true")
     ap.add_argument("--no-league", action="store_true")
-    ap.add_argument("--only", choices=["fdm", "env", "rollout", "league"], default=None,
+    ap.add_argument("--no-update", action="store_true")
+    ap.add_argument("--only", choices=["fdm", "env", "rollout", "league", "update"], default=None,
                     help="profiling aid: run only this section and print its own JSON line "
                          "(not the contract line)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -287,10 +347,11 @@ def main():
     sys.path.insert(0, ROOT)
     pkg = importlib.import_module(PKG)
     icm = importlib.import_module(PKG + ".ic")
-    if args.only in ("env", "rollout", "league"):
+    if args.only in ("env", "rollout", "league", "update"):
         part = {"env": lambda: env_step_bench(pkg, args.nenv, args.steps, args.warmup),
                 "rollout": lambda: rollout_bench(args.nenv),
-                "league": lambda: league_bench()}[args.only]()
+                "league": lambda: league_bench(),
+                "update": lambda: update_bench(args.nenv)}[args.only]()
         print(json.dumps(part), flush=True)
         return
 
@@ -332,6 +393,7 @@ def main():
     env_line = env_step_bench(pkg, nenv, args.steps, args.warmup)
     rollout_line = None if args.no_rollout else rollout_bench(nenv)
     league_line = None if args.no_league else league_bench()
+    update_line = None if args.no_update else update_bench(nenv)
 
     value = nac * S / (ms_step * 1e-3)
     flop_launch = FLOP_PER_SUBSTEP * nac * S
@@ -356,6 +418,7 @@ def main():
         "env_step": env_line,
         "rollout": rollout_line,
         "league": league_line,
+        "ppo_update": update_line,
         "roofline": {"bound": "valu", "achieved": achieved, "peak": PEAK_FP64_TFLOPS,
                      "unit": "TFLOP/s", "frac": achieved / PEAK_FP64_TFLOPS, "traffic": profiled_traffic(),
                      "kernel": "fdm_step_split_kernel<120>", "kernel_ms": kern_ms,

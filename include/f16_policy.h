@@ -14,7 +14,9 @@ extern "C" {
 
 /* Packed network of the reference's MLPDiscreteActorCritic with hidden (256, 256), tanh
  * (research/competition_36500/runtime/claude_code/model.py:162-205; BASELINE C4/C5 sizes).
- * bf16 part, row-major [out][in] with the input width padded to kp = round_up(obs_dim, 32):
+ * bf16 part, each matrix [out][in] (input width padded to kp = round_up(obs_dim, 32)) stored
+ * fragment-major: blocks of 512 elements in (32-row tile t, 16-column slice s) order, element
+ * (32t + l%32, 16s + 8(l/32) + i) of block (t, s) at 8l + i (l < 64, i < 8):
  *   W1 [512][kp]   actor layer-1 rows 0..255, critic layer-1 rows 256..511 (pad columns 0)
  *   W2a [256][256] actor layer 2,  W2c [256][256] critic layer 2
  *   W3a [96][256]  actor logits head, rows 84..95 zero

@@ -23,7 +23,7 @@ extern "C" {
 int f16_ppo_param_counts(int obs_dim, long *out2);
 
 /* Transposed bf16 blob the backward pass reads (elements): W3a^T [256][96] (columns 84..95
- * zero), W2a^T [256][256], W2c^T [256][256]. */
+ * zero), W2a^T [256][256], W2c^T [256][256], each fragment-major like the f16_policy.h blob. */
 #define F16_PPO_WT_ELEMS (256 * 96 + 2 * 256 * 256)
 
 /* Device scratch for f16_ppo_grad over minibatches of up to mb_rows rows. */

@@ -113,6 +113,21 @@ def test_library_struct_layout(pkg):
     assert out[3] == ctypes.sizeof(L.F16AdamArgs)
 
 
+def test_frag_major_blocks():
+    """Block (t, s) of a fragment-major matrix holds, at lane l, row 32t + l%32 and columns
+    16s + 8(l/32) .. +8: the 32x32x16 MFMA operand of lane l."""
+    import torch
+    P = import_pkg("policy")
+    N, K = 64, 48
+    w = torch.arange(N * K, dtype=torch.float64).view(N, K)
+    f = P.frag_major(w)
+    assert torch.equal(P.frag_unmajor(f, N, K), w)
+    t, s = 1, 2
+    blk = f[(t * (K // 16) + s) * 512:(t * (K // 16) + s + 1) * 512].view(64, 8)
+    for l in (0, 5, 31, 32, 63):
+        assert torch.equal(blk[l], w[32 * t + l % 32, 16 * s + 8 * (l // 32):16 * s + 8 * (l // 32) + 8])
+
+
 def test_pack_layout():
     import torch
     P = import_pkg("policy")
@@ -120,13 +135,15 @@ def test_pack_layout():
     wbf, wf = net.pack(device="cpu")
     kp = 192
     w = wbf.float()
-    W1 = w[:512 * kp].view(512, kp)
+    W1 = P.frag_unmajor(w[:512 * kp], 512, kp)
     a, c = net.actor_logits, net.critic
     assert torch.equal(W1[:256, :184], a[0].weight.to(torch.bfloat16).float())
     assert torch.equal(W1[256:, :184], c[0].weight.to(torch.bfloat16).float())
     assert (W1[:, 184:] == 0).all()
     off = 512 * kp + 2 * 256 * 256
-    W3 = w[off:off + 96 * 256].view(96, 256)
+    assert torch.equal(P.frag_unmajor(w[512 * kp:512 * kp + 65536], 256, 256),
+                       a[2].weight.to(torch.bfloat16).float())
+    W3 = P.frag_unmajor(w[off:off + 96 * 256], 96, 256)
     assert torch.equal(W3[:84], a[4].weight.to(torch.bfloat16).float()) and (W3[84:] == 0).all()
     assert wf.numel() == 1377 and torch.equal(wf[1120:1376], c[4].weight.flatten())
 

@@ -81,12 +81,13 @@ def test_pack_matches_policy_pack(gpu):
         up = U.PPOUpdater(net)                   # packs from the flat master copy
         assert torch.equal(up.wbf, wbf_ref) and torch.equal(up.wf, wf_ref)
         a, c = net.actor_logits, net.critic
+        pol = import_pkg("policy")
         wT = up.wT.float().cpu()
-        W3T = wT[:256 * 96].view(256, 96)
+        W3T = pol.frag_unmajor(wT[:256 * 96], 256, 96)
         assert torch.equal(W3T[:, :84], a[4].weight.detach().cpu().t().to(torch.bfloat16).float())
         assert (W3T[:, 84:] == 0).all()
-        W2aT = wT[256 * 96:256 * 96 + 65536].view(256, 256)
-        W2cT = wT[256 * 96 + 65536:].view(256, 256)
+        W2aT = pol.frag_unmajor(wT[256 * 96:256 * 96 + 65536], 256, 256)
+        W2cT = pol.frag_unmajor(wT[256 * 96 + 65536:], 256, 256)
         assert torch.equal(W2aT, a[2].weight.detach().cpu().t().to(torch.bfloat16).float())
         assert torch.equal(W2cT, c[2].weight.detach().cpu().t().to(torch.bfloat16).float())
 
