@@ -61,7 +61,10 @@ __device__ __forceinline__ f32x16 mfma(const bf16x8& a, const bf16x8& b, const f
 // over K (u0 a multiple of 32).  Units are the MFMA rows, observation rows the MFMA columns:
 // element e of a tile's result held by `lane` is unit 8(e/4) + 4(lane/32) + e%4, row lane%32.
 // Weights run PF K-slices ahead (at most K/16 - 1), the LDS activation fragments one slice ahead.
-template <int NR, int K, int PF = kPrefetch, bool PIN = true>
+#ifndef F16_GEMM_PIN
+#define F16_GEMM_PIN 1
+#endif
+template <int NR, int K, int PF = kPrefetch, bool PIN = (F16_GEMM_PIN != 0)>
 __device__ __forceinline__ void gemm_t(f32x16 (&acc)[NR], const __bf16* __restrict__ Wg, int u0,
                                        const __bf16* __restrict__ As, int a_pitch, int a_col0,
                                        int lane) {

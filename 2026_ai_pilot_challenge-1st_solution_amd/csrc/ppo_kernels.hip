@@ -2,7 +2,8 @@
 //
 // One minibatch (f16_ppo_grad) is nine launches:
 //   adv_partial/final  minibatch advantage mean and sample std (shifted fp64 sums, two levels);
-//   ppo_fused_kernel   per 64 gathered rows: forward of both networks, the loss head (softmax,
+//   ppo_fused_kernel   per 64 gathered rows (persistent, one workgroup per CU, the next tile's
+//                      rows in flight during the current one): forward of both networks, the loss head (softmax,
 //                      log-probability, entropy, ratio, clipped surrogate, value error) and the
 //                      backward chain down to the first hidden layer, all with the rows'
 //                      activations held in LDS.  The layer inputs and output gradients every
@@ -39,12 +40,6 @@ namespace f16ppo {
 using namespace f16pol;
 
 constexpr int kZPitch = kLogitsPad + 8;          // bf16 per LDS row of logit gradients
-#ifndef F16_PPO_PREFETCH
-#define F16_PPO_PREFETCH 6
-#endif
-// weight K-slices in flight in the fused kernel: it runs one workgroup (two waves per SIMD) per CU,
-// so each wave keeps more of its weight stream in flight than the rollout kernel does
-constexpr int kFusedPrefetch = F16_PPO_PREFETCH;
 constexpr int kStatCols = 8;                     // fused-kernel partial row: 8 sums,
 constexpr int kPartCols = kStatCols + kHid + 1 + 7;   // dw3c [256], db3c, pad to 272
 constexpr long kWT3 = 0, kWT2A = 256L * 96, kWT2C = kWT2A + 65536;
@@ -82,6 +77,8 @@ struct Work {
   float* advs;          // [8]: mean, std, statistics sums
   double* normp;        // [nblk][2] squared-norm partials
   __bf16 *xt, *h1t, *h2t, *dh1t, *dh2t, *dzt;   // unit-major, leading dimension ld
+                                                // (h2t: the actor's layer 2; the critic's
+                                                // enters only the value head, summed in-kernel)
   float* fpart;         // [nwg][kPartCols]
   double* advp;         // [nadv][2] advantage partial sums
   float* fmid;          // [ceil(nwg / kColRows)][kPartCols] first level of the fpart sums
@@ -123,7 +120,7 @@ inline Work layout(int obs_dim, long mb_rows, void* base) {
   w.normp = reinterpret_cast<double*>(take((long)norm_blocks(F.n()) * 2 * sizeof(double)));
   w.xt = reinterpret_cast<__bf16*>(take((long)kp * w.ld * 2));
   w.h1t = reinterpret_cast<__bf16*>(take(512L * w.ld * 2));
-  w.h2t = reinterpret_cast<__bf16*>(take(512L * w.ld * 2));
+  w.h2t = reinterpret_cast<__bf16*>(take(256L * w.ld * 2));   // actor layer 2 only
   w.dh1t = reinterpret_cast<__bf16*>(take(512L * w.ld * 2));
   w.dh2t = reinterpret_cast<__bf16*>(take(512L * w.ld * 2));
   w.dzt = reinterpret_cast<__bf16*>(take((long)kLogitsPad * w.ld * 2));
@@ -269,63 +266,88 @@ __device__ __forceinline__ void zero_acc(f32x16 (&acc)[NR]) {
     for (int e = 0; e < 16; ++e) acc[r][e] = 0.0f;
 }
 
+// rows of tile t: threads < 64 read the minibatch indices into rowpN (-1: past the minibatch or
+// a bad index, which is counted in badN and not read)
+__device__ __forceinline__ void fetch_rows(const F16PPOArgs& a, int t, long long* rowpN,
+                                           float* badN, int tid) {
+  if (tid < kRows) {
+    const long r = (long)t * kRows + tid;
+    long long p = -1;
+    float bad = 0.0f;
+    if (r < a.mb_rows) {
+      p = a.idx[r];
+      if (p < 0 || p >= a.count) { bad = 1.0f; p = -1; }
+    }
+    rowpN[tid] = p;
+    badN[tid] = bad;
+  }
+}
+
+// the rows listed in rowpN as float2 pairs, every load in flight at once
+template <int D, int kPer>
+__device__ __forceinline__ void issue_rows(const F16PPOArgs& a, const long long* rowpN,
+                                           float2 (&xr)[kPer], int tid) {
+  constexpr int half = D / 2;
+#pragma unroll
+  for (int q = 0; q < kPer; ++q) {
+    const int it = tid + q * kThreads;
+    const int r = it / half, c = it - r * half;
+    xr[q] = make_float2(0.0f, 0.0f);
+    if (r < kRows && rowpN[r] >= 0)
+      xr[q] = *reinterpret_cast<const float2*>(a.obs + rowpN[r] * a.obs_ld + 2 * c);
+  }
+}
+
+// The fused kernel is persistent: one workgroup per CU walks the minibatch's 64-row tiles, and
+// the next tile's gathered rows are loaded into registers during the current tile's matrix work.
 template <int KP>
 __global__ __launch_bounds__(kThreads, 1) void ppo_fused_kernel(const F16PPOArgs a, const Work w) {
   constexpr int XP = KP + 8;
   constexpr int D = KP == 192 ? 184 : 214;
+  constexpr int half = D / 2;                             // float2 per observation row
+  constexpr int kPer = (kRows * half + kThreads - 1) / kThreads;
   __shared__ __align__(16) __bf16 Xs[kRows * XP];
   __shared__ __align__(16) __bf16 H1s[kRows * kHPitch];
   __shared__ __align__(16) __bf16 H2s[kRows * kHPitch];
   __shared__ __align__(16) float Ls[kRows * kLPitch];     // logits, then (bf16) their gradients
   __shared__ float rowf[kRows][8];
-  __shared__ long long rowp[kRows];
+  __shared__ float vpart[kWaves][kRows];                  // per-wave partial critic values
+  __shared__ long long rowp[kRows], rowpN[kRows];
+  __shared__ float badN[kRows];
   __bf16* Zs = reinterpret_cast<__bf16*>(Ls);
   static_assert(kRows * kZPitch * 2 <= kRows * kLPitch * 4, "logit gradients overlay the logits");
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const long m0 = (long)blockIdx.x * kRows;
-  const int nr = (int)min((long)kRows, (long)a.mb_rows - m0);
   const long ld = w.ld;
   const __bf16* wbf = static_cast<const __bf16*>(a.wbf);
   const __bf16* wT = static_cast<const __bf16*>(a.wT);
   const float* wf = a.wf;
+  const float* w3 = wf + kW3C;
   const float inv_mb = 1.0f / (float)a.mb_rows;
 
-  if (tid < kRows) {
-    long long p = 0;
-    float bad = 0.0f;
-    if (tid < nr) {
-      p = a.idx[m0 + tid];
-      if (p < 0 || p >= a.count) { bad = 1.0f; p = -1; }
-    } else {
-      p = -1;
-    }
-    rowp[tid] = p;                 // -1: no row (past the minibatch or a bad index)
-    rowf[tid][7] = bad;
-  }
+  float2 xr[kPer];
+  int tile = blockIdx.x;
+  if (tile >= w.nwg) return;                               // uniform per workgroup
+  fetch_rows(a, tile, rowpN, badN, (int)threadIdx.x);
   __syncthreads();
-
-  // ---- gathered rows (already normalised at collection), rounded to bf16
-  {
-    constexpr int half = D / 2;
-    constexpr int kPer = (kRows * half + kThreads - 1) / kThreads;
-    float2 x[kPer];
-#pragma unroll
-    for (int q = 0; q < kPer; ++q) {
-      const int it = tid + q * kThreads;
-      const int r = it / half, c = it - r * half;
-      x[q] = make_float2(0.0f, 0.0f);
-      if (r < kRows && rowp[r] >= 0)
-        x[q] = *reinterpret_cast<const float2*>(a.obs + rowp[r] * a.obs_ld + 2 * c);
-    }
+  issue_rows<D, kPer>(a, rowpN, xr, (int)threadIdx.x);
+  for (; tile < w.nwg; tile += gridDim.x) {
+    // the thread index passes through an empty asm each tile, so the per-lane addresses below are
+    // formed inside the loop rather than hoisted out of it and held live (they would spill)
+    int tid = threadIdx.x;
+    asm volatile("" : "+v"(tid));
+    const int lane = tid & 63, wave = tid >> 6;
+    const int lr = lane & 31, lh = (lane >> 5) * 4;
+    const long m0 = (long)tile * kRows;
+    // ---- stage this tile's rows (normalised at collection), rounded to bf16
+    if (tid < kRows) { rowp[tid] = rowpN[tid]; rowf[tid][7] = badN[tid]; }
 #pragma unroll
     for (int q = 0; q < kPer; ++q) {
       const int it = tid + q * kThreads;
       const int r = it / half, c = it - r * half;
       if (r < kRows) {
         bf16x2 b;
-        b[0] = (__bf16)x[q].x;
-        b[1] = (__bf16)x[q].y;
+        b[0] = (__bf16)xr[q].x;
+        b[1] = (__bf16)xr[q].y;
         *reinterpret_cast<bf16x2*>(Xs + r * XP + 2 * c) = b;
       }
     }
@@ -333,203 +355,247 @@ __global__ __launch_bounds__(kThreads, 1) void ppo_fused_kernel(const F16PPOArgs
       const int r = it / (KP - D);
       Xs[r * XP + D + (it - r * (KP - D))] = (__bf16)0.0f;
     }
-  }
-  __syncthreads();
-  write_t(Xs, XP, KP, w.xt, ld, m0, tid);
+    __syncthreads();
+    const int next = tile + gridDim.x;
+    if (next < w.nwg) fetch_rows(a, next, rowpN, badN, tid);
+    write_t(Xs, XP, KP, w.xt, ld, m0, tid);
 
-  // ---- actor forward
-  {
-    f32x16 acc[2];
-    init_bias(acc, wf + kB1, 32 * wave, lane);
-    gemm_t<2, KP, kFusedPrefetch>(acc, wbf + Blob<KP>::W1, 32 * wave, Xs, XP, 0, lane);
-    store_tanh_t(acc, H1s, 32 * wave, w.h1t, ld, m0, lane);
-  }
-  __syncthreads();
-  {
-    f32x16 acc[2];
-    init_bias(acc, wf + kB2A, 32 * wave, lane);
-    gemm_t<2, kHid, kFusedPrefetch>(acc, wbf + Blob<KP>::W2A, 32 * wave, H1s, kHPitch, 0, lane);
-    store_tanh_t(acc, H2s, 32 * wave, w.h2t, ld, m0, lane);
-  }
-  __syncthreads();
-  if (wave < 6) {
-    const int ut = wave % 3, rt = wave / 3;
-    f32x16 acc[1];
-    init_bias(acc, wf + kB3A, 32 * ut, lane);
-    gemm_t<1, kHid, kFusedPrefetch>(acc, wbf + Blob<KP>::W3A, 32 * ut, H2s + 32 * rt * kHPitch, kHPitch, 0, lane);
-    const int row = 32 * rt + (lane & 31);
+    // ---- actor forward
+    {
+      f32x16 acc[2];
+      init_bias(acc, wf + kB1, 32 * wave, lane);
+      gemm_t<2, KP>(acc, wbf + Blob<KP>::W1, 32 * wave, Xs, XP, 0, lane);
+      store_tanh_t(acc, H1s, 32 * wave, w.h1t, ld, m0, lane);
+    }
+    __syncthreads();
+    {
+      f32x16 acc[2];
+      init_bias(acc, wf + kB2A, 32 * wave, lane);
+      gemm_t<2, kHid>(acc, wbf + Blob<KP>::W2A, 32 * wave, H1s, kHPitch, 0, lane);
+      store_tanh_t(acc, H2s, 32 * wave, w.h2t, ld, m0, lane);
+    }
+    __syncthreads();
+    if (wave < 6) {
+      const int ut = wave % 3, rt = wave / 3;
+      f32x16 acc[1];
+      init_bias(acc, wf + kB3A, 32 * ut, lane);
+      gemm_t<1, kHid>(acc, wbf + Blob<KP>::W3A, 32 * ut, H2s + 32 * rt * kHPitch, kHPitch, 0,
+                      lane);
+      const int row = 32 * rt + lr;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int unit = 32 * ut + 8 * g + lh;
+        *reinterpret_cast<float4*>(Ls + row * kLPitch + unit) =
+            make_float4(acc[0][4 * g + 0], acc[0][4 * g + 1], acc[0][4 * g + 2], acc[0][4 * g + 3]);
+      }
+    }
+    __syncthreads();
+
+    // ---- loss head, one lane per (row, channel) (ppo_gpu.py:2065-2090; model.py:207-219).
+    // Its per-row inputs are loaded first, then the next tile's rows: vmcnt retires loads in
+    // order, so the loss head waits only for its own loads and the gather lands during the loss
+    // head's arithmetic instead of stalling the next weight-fragment wait.
+    long long act = -1;
+    float old_lp = 0.0f, adv_r = 0.0f, ret_r = 0.0f;
+    if (tid < kRows * kChan) {
+      const long long pr = rowp[tid >> 2];
+      if (pr >= 0) {
+        act = a.act[pr * kChan + (tid & 3)];
+        old_lp = a.old_logp[pr];
+        adv_r = a.adv[pr];
+      }
+    }
+    if (tid < kRows && rowp[tid] >= 0) ret_r = a.ret[rowp[tid]];
+    if (next < w.nwg) issue_rows<D, kPer>(a, rowpN, xr, tid);   // lands while this tile computes
+    float dz[kBins];
+    if (tid < kRows * kChan) {
+      const int row = tid >> 2, ch = tid & 3;
+      const long long pr = rowp[row];
+      const bool valid = pr >= 0;
+      const float* l = Ls + row * kLPitch + ch * kBins;
+      float lg[kBins];
+#pragma unroll
+      for (int k = 0; k < kBins; ++k) lg[k] = l[k];
+      float m = lg[0];
+#pragma unroll
+      for (int k = 1; k < kBins; ++k)
+        if (lg[k] > m) m = lg[k];
+      float e[kBins], s = 0.0f;
+#pragma unroll
+      for (int k = 0; k < kBins; ++k) { e[k] = f16rng::exp_nonpos(lg[k] - m); s += e[k]; }
+      const float lse = logf(s), inv_s = 1.0f / s;
+      float lp = 0.0f, hc = 0.0f;
+#pragma unroll
+      for (int k = 0; k < kBins; ++k) {
+        const float lpk = (lg[k] - m) - lse;
+        if (k == act) lp = lpk;
+        hc -= (e[k] * inv_s) * lpk;
+      }
+      lp += __shfl_xor(lp, 1);              // the rollout kernel's summation order
+      lp += __shfl_xor(lp, 2);
+      float ent = hc + __shfl_xor(hc, 1);
+      ent += __shfl_xor(ent, 2);
+      float gcoef = 0.0f, pl = 0.0f, kl = 0.0f, cf = 0.0f;
+      if (valid) {
+        const float logr = lp - old_lp;
+        const float ratio = expf(logr);
+        float A = adv_r;
+        if (a.norm_adv && a.mb_rows > 1) A = (A - w.advs[0]) / (w.advs[1] + 1e-8f);
+        const float lo = (float)(1.0 - (double)a.clip_coef), hi = (float)(1.0 + (double)a.clip_coef);
+        const float rc = ratio < lo ? lo : (ratio > hi ? hi : ratio);
+        const float pg1 = -A * ratio, pg2 = -A * rc;
+        const float inr = (ratio >= lo && ratio <= hi) ? 1.0f : 0.0f;
+        // d max(pg1, pg2) / d ratio; torch.max of two tensors shares a tie evenly
+        float dr;
+        if (pg1 > pg2) dr = -A;
+        else if (pg1 < pg2) dr = -A * inr;
+        else dr = 0.5f * -A + 0.5f * (-A * inr);
+        gcoef = dr * ratio * inv_mb;
+        pl = pg1 > pg2 ? pg1 : pg2;
+        kl = (ratio - 1.0f) - logr;
+        cf = fabsf(ratio - 1.0f) > a.clip_coef ? 1.0f : 0.0f;
+      }
+      const float ec = a.ent_coef * inv_mb;
+#pragma unroll
+      for (int k = 0; k < kBins; ++k) {
+        const float pk = e[k] * inv_s;
+        const float lpk = (lg[k] - m) - lse;
+        const float oh = k == act ? 1.0f : 0.0f;
+        dz[k] = valid ? gcoef * (oh - pk) + ec * pk * (lpk + hc) : 0.0f;
+      }
+      if (ch == 0) {
+        rowf[row][0] = pl;
+        rowf[row][1] = valid ? ent : 0.0f;
+        rowf[row][2] = kl;
+        rowf[row][3] = cf;
+      }
+    }
+    __syncthreads();                          // every logit is read
+    if (tid < kRows * kChan) {
+      const int row = tid >> 2, ch = tid & 3;
+#pragma unroll
+      for (int k = 0; k < kBins; ++k) Zs[row * kZPitch + ch * kBins + k] = (__bf16)dz[k];
+      if (ch == 3) {
+#pragma unroll
+        for (int k = kLogits; k < kLogitsPad; ++k) Zs[row * kZPitch + k] = (__bf16)0.0f;
+      }
+    }
+    __syncthreads();
+    write_t(Zs, kZPitch, kLogitsPad, w.dzt, ld, m0, tid);
+
+    // ---- actor backward: dH2 = (dZ W3) (1 - H2^2) in place of H2, dH1 = (dH2 W2) (1 - H1^2)
+    {
+      f32x16 acc[2];
+      zero_acc(acc);
+      gemm_t<2, kLogitsPad>(acc, wT + kWT3, 32 * wave, Zs, kZPitch, 0, lane);
+      store_dtanh_t(acc, H2s, H2s, 32 * wave, w.dh2t, ld, m0, lane);
+    }
+    __syncthreads();
+    {
+      f32x16 acc[2];
+      zero_acc(acc);
+      gemm_t<2, kHid>(acc, wT + kWT2A, 32 * wave, H2s, kHPitch, 0, lane);
+      store_dtanh_t(acc, H1s, nullptr, 32 * wave, w.dh1t, ld, m0, lane);
+    }
+    __syncthreads();
+
+    // ---- critic forward; the value head is folded into the second layer's epilogue
+    {
+      f32x16 acc[2];
+      init_bias(acc, wf + kB1 + kHid, 32 * wave, lane);
+      gemm_t<2, KP>(acc, wbf + Blob<KP>::W1C, 32 * wave, Xs, XP, 0, lane);
+      store_tanh_t(acc, H1s, 32 * wave, w.h1t + kHid * ld, ld, m0, lane);
+    }
+    __syncthreads();
+    bf16x4 hc2[4][2];                          // this lane's critic layer-2 activations
+    {
+      f32x16 acc[2];
+      init_bias(acc, wf + kB2C, 32 * wave, lane);
+      gemm_t<2, kHid>(acc, wbf + Blob<KP>::W2C, 32 * wave, H1s, kHPitch, 0, lane);
+      float vp[2] = {0.0f, 0.0f};
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int unit = 32 * wave + 8 * g + lh;
+        const float4 w4 = *reinterpret_cast<const float4*>(w3 + unit);
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+          bf16x4 v;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) v[j] = (__bf16)tanh_act(acc[r][4 * g + j]);
+          hc2[g][r] = v;
+          *reinterpret_cast<bf16x4*>(H2s + (32 * r + lr) * kHPitch + unit) = v;
+          vp[r] += (float)v[0] * w4.x + (float)v[1] * w4.y + (float)v[2] * w4.z + (float)v[3] * w4.w;
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < 2; ++r) vp[r] += __shfl_xor(vp[r], 32);   // lanes l, l + 32: one row
+      if (lane < 32) { vpart[wave][lr] = vp[0]; vpart[wave][32 + lr] = vp[1]; }
+    }
+    __syncthreads();
+    if (tid < kRows) {                         // value, its error and d(loss)/dv per row
+      float v = vpart[0][tid];
+#pragma unroll
+      for (int q = 1; q < kWaves; ++q) v += vpart[q][tid];
+      const long long pr = rowp[tid];
+      float dv = 0.0f, se = 0.0f;
+      if (pr >= 0) {
+        const float err = (v + wf[kB3C]) - ret_r;
+        se = err * err;
+        dv = a.vf_coef * err * inv_mb;      // d(vf_coef 0.5 mean(err^2)) / dv
+      }
+      rowf[tid][4] = dv;
+      rowf[tid][5] = se;
+    }
+    __syncthreads();
+    // per-tile partials: statistics, dw3c = sum dv h2, db3c = sum dv (rows in order)
+    {
+      float* part = w.fpart + (long)tile * kPartCols;
+      if (tid < kHid) {
+        float s = 0.0f;
+        for (int r = 0; r < kRows; ++r) s += rowf[r][4] * (float)H2s[r * kHPitch + tid];
+        part[kStatCols + tid] = s;
+      } else if (tid < kHid + 8) {
+        const int c = tid - kHid;             // 0 pl, 1 ent, 2 kl, 3 cf, 4 dv (db3c), 5 se, 7 bad
+        float s = 0.0f;
+        if (c != 6)
+          for (int r = 0; r < kRows; ++r) s += rowf[r][c];
+        if (c == 4) {
+          part[kStatCols + kHid] = s;
+          part[4] = 0.0f;
+        } else {
+          part[c] = s;
+        }
+      }
+    }
+    __syncthreads();                          // H2s is read
+    // dH2c = dv w3c (1 - H2c^2) from the registers, in place and unit-major
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
-      const int unit = 32 * ut + 8 * g + (lane >> 5) * 4;
-      *reinterpret_cast<float4*>(Ls + row * kLPitch + unit) =
-          make_float4(acc[0][4 * g + 0], acc[0][4 * g + 1], acc[0][4 * g + 2], acc[0][4 * g + 3]);
-    }
-  }
-  __syncthreads();
-
-  // ---- loss head, one lane per (row, channel) (ppo_gpu.py:2065-2090; model.py:207-219)
-  float dz[kBins];
-  if (tid < kRows * kChan) {
-    const int row = tid >> 2, ch = tid & 3;
-    const long long pr = rowp[row];
-    const bool valid = pr >= 0;
-    const float* l = Ls + row * kLPitch + ch * kBins;
-    float lg[kBins];
+      const int unit = 32 * wave + 8 * g + lh;
 #pragma unroll
-    for (int k = 0; k < kBins; ++k) lg[k] = l[k];
-    float m = lg[0];
+      for (int r = 0; r < 2; ++r) {
+        const int row = 32 * r + lr;
+        const float dvr = rowf[row][4];
+        bf16x4 d;
 #pragma unroll
-    for (int k = 1; k < kBins; ++k)
-      if (lg[k] > m) m = lg[k];
-    float e[kBins], s = 0.0f;
+        for (int j = 0; j < 4; ++j) {
+          const float h = (float)hc2[g][r][j];
+          d[j] = (__bf16)(dvr * w3[unit + j] * (1.0f - h * h));
+        }
+        *reinterpret_cast<bf16x4*>(H2s + row * kHPitch + unit) = d;
 #pragma unroll
-    for (int k = 0; k < kBins; ++k) { e[k] = f16rng::exp_nonpos(lg[k] - m); s += e[k]; }
-    const long long act = valid ? a.act[pr * kChan + ch] : -1;
-    const float lse = logf(s);
-    float lp = 0.0f, hc = 0.0f;
-#pragma unroll
-    for (int k = 0; k < kBins; ++k) {
-      const float lpk = (lg[k] - m) - lse;
-      if (k == act) lp = lpk;
-      hc -= (e[k] / s) * lpk;
+        for (int j = 0; j < 4; ++j) w.dh2t[(long)(kHid + unit + j) * ld + m0 + row] = d[j];
+      }
     }
-    lp += __shfl_xor(lp, 1);                // the rollout kernel's summation order
-    lp += __shfl_xor(lp, 2);
-    float ent = hc + __shfl_xor(hc, 1);
-    ent += __shfl_xor(ent, 2);
-    float gcoef = 0.0f, pl = 0.0f, kl = 0.0f, cf = 0.0f;
-    if (valid) {
-      const float logr = lp - a.old_logp[pr];
-      const float ratio = expf(logr);
-      float A = a.adv[pr];
-      if (a.norm_adv && a.mb_rows > 1) A = (A - w.advs[0]) / (w.advs[1] + 1e-8f);
-      const float lo = (float)(1.0 - (double)a.clip_coef), hi = (float)(1.0 + (double)a.clip_coef);
-      const float rc = ratio < lo ? lo : (ratio > hi ? hi : ratio);
-      const float pg1 = -A * ratio, pg2 = -A * rc;
-      const float inr = (ratio >= lo && ratio <= hi) ? 1.0f : 0.0f;
-      // d max(pg1, pg2) / d ratio; torch.max of two tensors shares a tie evenly
-      float dr;
-      if (pg1 > pg2) dr = -A;
-      else if (pg1 < pg2) dr = -A * inr;
-      else dr = 0.5f * -A + 0.5f * (-A * inr);
-      gcoef = dr * ratio * inv_mb;
-      pl = pg1 > pg2 ? pg1 : pg2;
-      kl = (ratio - 1.0f) - logr;
-      cf = fabsf(ratio - 1.0f) > a.clip_coef ? 1.0f : 0.0f;
+    __syncthreads();
+    {
+      f32x16 acc[2];
+      zero_acc(acc);
+      gemm_t<2, kHid>(acc, wT + kWT2C, 32 * wave, H2s, kHPitch, 0, lane);
+      store_dtanh_t(acc, H1s, nullptr, 32 * wave, w.dh1t + kHid * ld, ld, m0, lane);
     }
-    const float ec = a.ent_coef * inv_mb;
-#pragma unroll
-    for (int k = 0; k < kBins; ++k) {
-      const float pk = e[k] / s;
-      const float lpk = (lg[k] - m) - lse;
-      const float oh = k == act ? 1.0f : 0.0f;
-      dz[k] = valid ? gcoef * (oh - pk) + ec * pk * (lpk + hc) : 0.0f;
-    }
-    if (ch == 0) {
-      rowf[row][0] = pl;
-      rowf[row][1] = valid ? ent : 0.0f;
-      rowf[row][2] = kl;
-      rowf[row][3] = cf;
-    }
-  }
-  __syncthreads();                            // every logit is read
-  if (tid < kRows * kChan) {
-    const int row = tid >> 2, ch = tid & 3;
-#pragma unroll
-    for (int k = 0; k < kBins; ++k) Zs[row * kZPitch + ch * kBins + k] = (__bf16)dz[k];
-    if (ch == 3) {
-#pragma unroll
-      for (int k = kLogits; k < kLogitsPad; ++k) Zs[row * kZPitch + k] = (__bf16)0.0f;
-    }
-  }
-  __syncthreads();
-  write_t(Zs, kZPitch, kLogitsPad, w.dzt, ld, m0, tid);
-
-  // ---- actor backward: dH2 = (dZ W3) (1 - H2^2) in place of H2, dH1 = (dH2 W2) (1 - H1^2)
-  {
-    f32x16 acc[2];
-    zero_acc(acc);
-    gemm_t<2, kLogitsPad, kFusedPrefetch>(acc, wT + kWT3, 32 * wave, Zs, kZPitch, 0, lane);
-    store_dtanh_t(acc, H2s, H2s, 32 * wave, w.dh2t, ld, m0, lane);
-  }
-  __syncthreads();
-  {
-    f32x16 acc[2];
-    zero_acc(acc);
-    gemm_t<2, kHid, kFusedPrefetch>(acc, wT + kWT2A, 32 * wave, H2s, kHPitch, 0, lane);
-    store_dtanh_t(acc, H1s, nullptr, 32 * wave, w.dh1t, ld, m0, lane);
-  }
-  __syncthreads();
-
-  // ---- critic forward
-  {
-    f32x16 acc[2];
-    init_bias(acc, wf + kB1 + kHid, 32 * wave, lane);
-    gemm_t<2, KP, kFusedPrefetch>(acc, wbf + Blob<KP>::W1C, 32 * wave, Xs, XP, 0, lane);
-    store_tanh_t(acc, H1s, 32 * wave, w.h1t + kHid * ld, ld, m0, lane);
-  }
-  __syncthreads();
-  {
-    f32x16 acc[2];
-    init_bias(acc, wf + kB2C, 32 * wave, lane);
-    gemm_t<2, kHid, kFusedPrefetch>(acc, wbf + Blob<KP>::W2C, 32 * wave, H1s, kHPitch, 0, lane);
-    store_tanh_t(acc, H2s, 32 * wave, w.h2t + kHid * ld, ld, m0, lane);
-  }
-  __syncthreads();
-  const float* w3 = wf + kW3C;
-  if (wave == 0) {                            // value (the rollout kernel's dot product)
-    const int row = lane;
-    float s = 0.0f;
-#pragma unroll 4
-    for (int k0 = 0; k0 < kHid; k0 += 8) {
-      const bf16x8 h = *reinterpret_cast<const bf16x8*>(H2s + row * kHPitch + k0);
-#pragma unroll
-      for (int q = 0; q < 8; ++q) s += (float)h[q] * w3[k0 + q];
-    }
-    const long long pr = rowp[row];
-    float dv = 0.0f, se = 0.0f;
-    if (pr >= 0) {
-      const float err = (s + wf[kB3C]) - a.ret[pr];
-      se = err * err;
-      dv = a.vf_coef * err * inv_mb;        // d(vf_coef 0.5 mean(err^2)) / dv
-    }
-    rowf[row][4] = dv;
-    rowf[row][5] = se;
-  }
-  __syncthreads();
-  // per-workgroup partials: statistics, dw3c = sum dv h2, db3c = sum dv (rows in order)
-  {
-    float* part = w.fpart + (long)blockIdx.x * kPartCols;
-    if (tid < kHid) {
-      float s = 0.0f;
-      for (int r = 0; r < kRows; ++r) s += rowf[r][4] * (float)H2s[r * kHPitch + tid];
-      part[kStatCols + tid] = s;
-    } else if (tid < kHid + 8) {
-      const int c = tid - kHid;               // 0 pl, 1 ent, 2 kl, 3 cf, 4 dv (db3c), 5 se, 7 bad
-      float s = 0.0f;
-      if (c != 6)
-        for (int r = 0; r < kRows; ++r) s += rowf[r][c];
-      if (c == 4) part[kStatCols + kHid] = s;
-      else part[c] = s;
-    }
-    if (tid == kHid + 8) part[4] = 0.0f;
-    if (tid == kHid + 9) part[6] = 0.0f;
-  }
-  __syncthreads();                            // H2s is read
-  // dH2c = dv w3c (1 - H2c^2), in place and unit-major; lanes run over rows (coalesced stores)
-  for (int it = tid; it < kRows * kHid; it += kThreads) {
-    const int n = it >> 6, row = it & 63;
-    const float h = (float)H2s[row * kHPitch + n];
-    const __bf16 d = (__bf16)(rowf[row][4] * w3[n] * (1.0f - h * h));
-    H2s[row * kHPitch + n] = d;
-    w.dh2t[(long)(kHid + n) * ld + m0 + row] = d;
-  }
-  __syncthreads();
-  {
-    f32x16 acc[2];
-    zero_acc(acc);
-    gemm_t<2, kHid, kFusedPrefetch>(acc, wT + kWT2C, 32 * wave, H2s, kHPitch, 0, lane);
-    store_dtanh_t(acc, H1s, nullptr, 32 * wave, w.dh1t + kHid * ld, ld, m0, lane);
+    // the next tile first writes Xs, rowp and rowf (read before the syncs above) and H1s only
+    // after its first barrier, so no barrier is needed here
   }
 }
 
@@ -859,6 +925,15 @@ int launch_pack(const float* param, void* wbf, float* wf, void* wT, hipStream_t 
 
 using namespace f16ppo;
 
+// compute units of the current device (the persistent fused kernel runs one workgroup on each)
+static int device_cus() {
+  int dev = 0, n = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1)
+    return 256;
+  return n;
+}
+
 extern "C" int f16_ppo_param_counts(int obs_dim, long* out2) {
   if (!out2 || (obs_dim != 184 && obs_dim != 214)) return F16_EINVAL;
   const Flat F{obs_dim};
@@ -888,10 +963,11 @@ extern "C" int f16_ppo_grad(const F16PPOArgs* a, void* stream) {
                      a->mb_rows, a->count, w.advp);
   hipLaunchKernelGGL(adv_final_kernel, dim3(1), dim3(kAdvThreads), 0, s, a->adv, a->idx,
                      a->mb_rows, a->count, w.nadv, (const double*)w.advp, w.advs);
+  const unsigned fgrid = (unsigned)std::min(w.nwg, device_cus());
   if (kp == 192)
-    hipLaunchKernelGGL(ppo_fused_kernel<192>, dim3(w.nwg), dim3(kThreads), 0, s, *a, w);
+    hipLaunchKernelGGL(ppo_fused_kernel<192>, dim3(fgrid), dim3(kThreads), 0, s, *a, w);
   else
-    hipLaunchKernelGGL(ppo_fused_kernel<224>, dim3(w.nwg), dim3(kThreads), 0, s, *a, w);
+    hipLaunchKernelGGL(ppo_fused_kernel<224>, dim3(fgrid), dim3(kThreads), 0, s, *a, w);
   // the four weight-gradient products and their tiles
   WJobs J{};
   const long na = F.na();
