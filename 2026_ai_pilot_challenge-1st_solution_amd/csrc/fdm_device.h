@@ -325,6 +325,18 @@ struct Kin {
   double ctcp;                // cos(theta) * cos(phi) of the local-NED Euler angles
 };
 
+// Ti2b from the ECI->body quaternion (quat_to_T, jsb_frames.py): rows are the body axes in ECI.
+// A pure function of q, so a caller may recompute it instead of keeping it live.
+F16_HD void body_dcm(const double q[4], double B[3][3]) {
+  const double q0 = q[0], q1 = q[1], q2 = q[2], q3 = q[3];
+  const double q0q0 = q0 * q0, q1q1 = q1 * q1, q2q2 = q2 * q2, q3q3 = q3 * q3;
+  const double q0q1 = q0 * q1, q0q2 = q0 * q2, q0q3 = q0 * q3;
+  const double q1q2 = q1 * q2, q1q3 = q1 * q3, q2q3 = q2 * q3;
+  B[0][0] = q0q0 + q1q1 - q2q2 - q3q3; B[0][1] = 2.0 * (q1q2 + q0q3); B[0][2] = 2.0 * (q1q3 - q0q2);
+  B[1][0] = 2.0 * (q1q2 - q0q3); B[1][1] = q0q0 - q1q1 + q2q2 - q3q3; B[1][2] = 2.0 * (q2q3 + q0q1);
+  B[2][0] = 2.0 * (q1q3 + q0q2); B[2][1] = 2.0 * (q2q3 - q0q1); B[2][2] = q0q0 - q1q1 - q2q2 + q3q3;
+}
+
 // `want_euler` (wave-uniform) also produces the Euler angles (mat_to_euler,
 // jsb_frames.py:140-163) for the output row; the FCS only needs cos(theta)cos(phi), which is
 // formed from the DCM without the inverse trigonometry.
@@ -351,15 +363,7 @@ F16_HD void kinematics(const double p[3], const double v[3], const double q[4],
   const double N[3] = {ce * n0 - se * n1, se * n0 + ce * n1, cLat};
   const double E[2] = {ce * (-sLon) - se * cLon, se * (-sLon) + ce * cLon};
   const double D[3] = {ce * d0 - se * d1, se * d0 + ce * d1, -sLat};
-  {
-    const double q0 = q[0], q1 = q[1], q2 = q[2], q3 = q[3];
-    const double q0q0 = q0 * q0, q1q1 = q1 * q1, q2q2 = q2 * q2, q3q3 = q3 * q3;
-    const double q0q1 = q0 * q1, q0q2 = q0 * q2, q0q3 = q0 * q3;
-    const double q1q2 = q1 * q2, q1q3 = q1 * q3, q2q3 = q2 * q3;
-    k.B[0][0] = q0q0 + q1q1 - q2q2 - q3q3; k.B[0][1] = 2.0 * (q1q2 + q0q3); k.B[0][2] = 2.0 * (q1q3 - q0q2);
-    k.B[1][0] = 2.0 * (q1q2 - q0q3); k.B[1][1] = q0q0 - q1q1 + q2q2 - q3q3; k.B[1][2] = 2.0 * (q2q3 + q0q1);
-    k.B[2][0] = 2.0 * (q1q3 + q0q2); k.B[2][1] = 2.0 * (q2q3 - q0q1); k.B[2][2] = q0q0 - q1q1 - q2q2 + q3q3;
-  }
+  body_dcm(q, k.B);
   // Tl2b[i][j] = body_i . local_j
   double L[3][3];
 #pragma unroll
@@ -616,11 +620,11 @@ F16_HD void gravity(const Kin& k, double gi[3]) {
 // ---- accelerations (jsb_accel.py:10-31) ----
 struct Accel { double ai[3], wdi[3], pba[3], ppq[3]; };   // vUVWidot, vPQRidot, vBodyAccel, vPQRi
 
-F16_HD void accelerations(const Kin& k, const Mass& mb, const double F[3], const double M[3],
-                          const double gi[3], Accel& o) {
+F16_HD void accelerations(const double B[3][3], const double wpqr[3], const Mass& mb,
+                          const double F[3], const double M[3], const double gi[3], Accel& o) {
   double wq[3];   // vPQRi re-formed from vPQR, as the reference's accelerations do
 #pragma unroll
-  for (int i = 0; i < 3; ++i) wq[i] = k.wpqr[i] + k.B[i][2] * kRot;
+  for (int i = 0; i < 3; ++i) wq[i] = wpqr[i] + B[i][2] * kRot;
   const double* J = mb.J;
   const double Jw0 = J[0] * wq[0] + J[3] * wq[1] + J[4] * wq[2];
   const double Jw1 = J[3] * wq[0] + J[1] * wq[1] + J[5] * wq[2];
@@ -637,7 +641,7 @@ F16_HD void accelerations(const Kin& k, const Mass& mb, const double F[3], const
   for (int i = 0; i < 3; ++i) o.pba[i] = F[i] * sm;
 #pragma unroll
   for (int i = 0; i < 3; ++i) {
-    o.ai[i] = (k.B[0][i] * o.pba[0] + k.B[1][i] * o.pba[1] + k.B[2][i] * o.pba[2]) + gi[i];
+    o.ai[i] = (B[0][i] * o.pba[0] + B[1][i] * o.pba[1] + B[2][i] * o.pba[2]) + gi[i];
     o.ppq[i] = wq[i];
   }
 }
@@ -723,18 +727,22 @@ F16_HD void force_path(Aircraft& a, double c_ail, double c_ele, double c_rud,
     const double ail = fc.ail, elev = fc.elev, rud = fc.rud, lef = fc.lef, flap = fc.flap;
     F16_AERO_BRACKETS;
     F16_AERO_LOOKUPS;
-    ax[0] = F16_AERO_DRAG_FREE + F16_AERO_DRAG_CTL;
-    ax[1] = F16_AERO_SIDE_FREE + F16_AERO_SIDE_CTL;
-    ax[2] = F16_AERO_LIFT_FREE + F16_AERO_LIFT_CTL;
-    ax[3] = F16_AERO_ROLL_FREE + F16_AERO_ROLL_CTL;
-    ax[4] = F16_AERO_PITCH_FREE + F16_AERO_PITCH_CTL;
-    ax[5] = F16_AERO_YAW_FREE + F16_AERO_YAW_CTL;
+    // each axis as SCALE * (EARLY + LATE), the EARLY sums rounded first exactly as the split
+    // kernel forms them a phase ahead
+    const double e0 = F16_AERO_DRAG_EARLY, e1 = F16_AERO_SIDE_EARLY, e2 = F16_AERO_LIFT_EARLY;
+    const double e3 = F16_AERO_ROLL_EARLY, e4 = F16_AERO_PITCH_EARLY, e5 = F16_AERO_YAW_EARLY;
+    ax[0] = F16_AERO_DRAG_SCALE * (e0 + F16_AERO_DRAG_LATE);
+    ax[1] = F16_AERO_SIDE_SCALE * (e1 + F16_AERO_SIDE_LATE);
+    ax[2] = F16_AERO_LIFT_SCALE * (e2 + F16_AERO_LIFT_LATE);
+    ax[3] = F16_AERO_ROLL_SCALE * (e3 + F16_AERO_ROLL_LATE);
+    ax[4] = F16_AERO_PITCH_SCALE * (e4 + F16_AERO_PITCH_LATE);
+    ax[5] = F16_AERO_YAW_SCALE * (e5 + F16_AERO_YAW_LATE);
   }
   double F[3], M[3], gi[3];
   forces_moments(ax, g, mb, thrust, F, M);
   gravity(k, gi);
   Accel ac;
-  accelerations(k, mb, F, M, gi, ac);
+  accelerations(k.B, k.wpqr, mb, F, M, gi, ac);
 #pragma unroll
   for (int i = 0; i < 3; ++i) {
     o.ai[i] = ac.ai[i]; o.wdi[i] = ac.wdi[i]; o.pba[i] = ac.pba[i]; o.ppq[i] = ac.ppq[i];

@@ -11,12 +11,12 @@
 //            systems: mass properties, previous-frame FCS channels, pitch schedule, Earth
 //                     position angle
 //   -- X1: altitude, cos(theta)cos(phi)  |  mass/CG/inertia, aileron/rudder/LEF/flaperon
-//   phase 2  flight:  air-relative geometry (vt, alpha, beta), load factors, alpha/beta brackets
-//                     and their table values
+//   phase 2  flight:  air-relative geometry (vt, alpha, beta), load factors, alpha/beta brackets,
+//                     their table values and the alpha/beta-only part of each axis sum
 //            systems: atmosphere, pitch loop
 //   -- X2: vt, alpha, beta, n_y, n_z  |  rho, pressure, speed of sound, elevator
 //   phase 3  flight:  dynamic pressure, mach, calibrated airspeed, mach/elevator brackets and
-//                     values, the six sums, quaternion rate, gravity, vg
+//                     values, the six axes, quaternion rate, gravity, vg
 //            systems: mach, engine, sin/cos of the next substep's Earth position angle
 //   -- X3: calibrated airspeed, vg, p q r  |  thrust, sin/cos(epa)
 //   phase 4  flight:  forces, moments, accelerations, state update
@@ -135,10 +135,21 @@ __device__ __forceinline__ void split_flight(double* __restrict__ s, long ld, in
     x[kXVt][lane] = g.vt; x[kXAlpha][lane] = g.alpha; x[kXBeta][lane] = g.beta;
     x[kXNpy][lane] = npy; x[kXNpz][lane] = npz;
     const double alpha = g.alpha, beta = g.beta;
-    F16_AERO_BRACKETS_AB;
-    F16_AERO_LOOKUPS_AB;
     const double ail = x[kXAil][lane], rud = x[kXRud][lane];
-    const double lef = x[kXLef][lane], flap = x[kXFlap][lane];
+    double early[6];      // the alpha/beta-only part of each axis, so its 18 table values die here
+    {
+      const double lef = x[kXLef][lane], flap = x[kXFlap][lane];
+      double bi2vel, ci2vel;
+      aero_rates(g.vt, bi2vel, ci2vel);
+      constexpr double kclge = kCLge;
+      constexpr double gear = kGearPos<FCS_RATE>;
+      const double p = k.wpqr[0], q = k.wpqr[1], r = k.wpqr[2];
+      F16_AERO_BRACKETS_AB;
+      F16_AERO_LOOKUPS_AB;
+      early[0] = F16_AERO_DRAG_EARLY; early[1] = F16_AERO_SIDE_EARLY;
+      early[2] = F16_AERO_LIFT_EARLY; early[3] = F16_AERO_ROLL_EARLY;
+      early[4] = F16_AERO_PITCH_EARLY; early[5] = F16_AERO_YAW_EARLY;
+    }
     __syncthreads();
     // ---- phase 3
     const double rho = x[kXRho][lane], sound = x[kXSound][lane], elev = x[kXElev][lane];
@@ -152,21 +163,18 @@ __device__ __forceinline__ void split_flight(double* __restrict__ s, long ld, in
     gravity(k, gi);
     double ax[6];
     {
-      double bi2vel, ci2vel;
-      aero_rates(g.vt, bi2vel, ci2vel);
       constexpr double kclge = kCLge;
-      constexpr double gear = kGearPos<FCS_RATE>;
-      const double p = k.wpqr[0], q = k.wpqr[1], r = k.wpqr[2];
+      const F16Br2 b2_G9_ALPHA = F16_BR2(G9_ALPHA, alpha);   // the elevator tables' alpha bracket
       F16_AERO_BRACKETS_MACH;
       F16_AERO_BRACKETS_ELEV;
       F16_AERO_LOOKUPS_MACH;
       F16_AERO_LOOKUPS_ELEV;
-      ax[0] = F16_AERO_DRAG_FREE + F16_AERO_DRAG_CTL;
-      ax[1] = F16_AERO_SIDE_FREE + F16_AERO_SIDE_CTL;
-      ax[2] = F16_AERO_LIFT_FREE + F16_AERO_LIFT_CTL;
-      ax[3] = F16_AERO_ROLL_FREE + F16_AERO_ROLL_CTL;
-      ax[4] = F16_AERO_PITCH_FREE + F16_AERO_PITCH_CTL;
-      ax[5] = F16_AERO_YAW_FREE + F16_AERO_YAW_CTL;
+      ax[0] = F16_AERO_DRAG_SCALE * (early[0] + F16_AERO_DRAG_LATE);
+      ax[1] = F16_AERO_SIDE_SCALE * (early[1] + F16_AERO_SIDE_LATE);
+      ax[2] = F16_AERO_LIFT_SCALE * (early[2] + F16_AERO_LIFT_LATE);
+      ax[3] = F16_AERO_ROLL_SCALE * (early[3] + F16_AERO_ROLL_LATE);
+      ax[4] = F16_AERO_PITCH_SCALE * (early[4] + F16_AERO_PITCH_LATE);
+      ax[5] = F16_AERO_YAW_SCALE * (early[5] + F16_AERO_YAW_LATE);
     }
     __syncthreads();
     // ---- phase 4
@@ -174,7 +182,11 @@ __device__ __forceinline__ void split_flight(double* __restrict__ s, long ld, in
     double Fb[3], Mb[3];
     forces_moments(ax, g, mb, thrust, Fb, Mb);
     Accel ac;
-    accelerations(k, mb, Fb, Mb, gi, ac);
+    {
+      double B[3][3];   // recomputed from the quaternion rather than held since phase 1
+      body_dcm(a.q, B);
+      accelerations(B, k.wpqr, mb, Fb, Mb, gi, ac);
+    }
 #pragma unroll
     for (int i = 0; i < 3; ++i) {
       a.ai[i] = ac.ai[i]; a.wdi[i] = ac.wdi[i]; a.pba[i] = ac.pba[i];

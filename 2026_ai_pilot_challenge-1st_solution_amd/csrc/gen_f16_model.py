@@ -481,7 +481,10 @@ def main():
     dw("//   F16_AERO_LOOKUPS_{AB,MACH,ELEV}: lk_<term> = the term's table value, by the brackets")
     dw("//     it needs;")
     dw("//   F16_AERO_<AXIS>_FREE / _CTL: the terms without / with a control-surface position, each")
-    dw("//     a left-to-right sum from 0 in XML order; the axis is FREE + CTL.")
+    dw("//     a left-to-right sum from 0 in XML order; the axis is FREE + CTL;")
+    dw("//   F16_AERO_<AXIS>_SCALE, _EARLY, _LATE: the axis as SCALE * (EARLY + LATE), SCALE the")
+    dw("//     factors every term starts with, EARLY the rest of the alpha/beta-only terms, LATE the")
+    dw("//     terms that need mach or the elevator position (each a sum in XML order).")
     dw("// Terms with the speedbrake factor (identically 0) are omitted.")
     brk = {"AB": [], "MACH": [], "ELEV": []}
     for gr, var in sorted(used1.items(), key=lambda kv: kv[0][1]):
@@ -490,6 +493,41 @@ def main():
         brk[KEYGRP[var]].append(f"const F16Br2 b2_{gr[0]} = F16_BR2({gr[0]}, {var_expr[var]})")
     lks = {"AB": [], "MACH": [], "ELEV": []}
     sums = {}
+    # Every term of an axis starts with the same factors -- qbar, the wing area and, for the
+    # moments, the span or chord -- so the axis is also evaluated as SCALE * (EARLY + LATE):
+    # EARLY sums the rest of each term whose table is keyed on alpha/beta only and whose factors
+    # are all known once the air-relative geometry, the body rates and the aileron/rudder/LEF/
+    # flaperon positions are (XML order), LATE the terms that need mach or the elevator.  Callers
+    # that split the substep evaluate EARLY before the mach and elevator exist.
+    PREFIX_OK = {"aero/qbar-psf", "metrics/Sw-sqft", "metrics/bw-ft", "metrics/cbarw-ft"}
+    LATE_VARS = {"velocities/mach", "fcs/elevator-pos-rad"}
+    split = {}
+    for ai, ax in enumerate(AXES):
+        prefix = None
+        early, late = [], []
+        for aj, short, f, rec in terms:
+            if aj != ai or SB in f["factors"]:
+                continue
+            fs = list(f["factors"])
+            npre = 0
+            while npre < len(fs) and fs[npre] in PREFIX_OK:
+                npre += 1
+            pre = tuple(fs[:npre])
+            if prefix is None:
+                prefix = pre
+            if pre != prefix:
+                raise SystemExit(f"{ax}: term {short} does not share the axis prefix {prefix}")
+            rest = [fnum(const_of[pp]) if pp in const_of else var_expr[pp] for pp in fs[npre:]]
+            if f["value"] is not None:
+                rest.append(fnum(f["value"]))
+            keys = []
+            if rec is not None:
+                keys = [rec["row_var"]] + ([rec["col_var"]] if rec["kind"] == 2 else [])
+                rest.append(f"lk_{short}")
+            is_late = bool(LATE_VARS & (set(fs) | set(keys)))
+            (late if is_late else early).append((short, " * ".join(rest) if rest else "1.0"))
+        scale = " * ".join(fnum(const_of[pp]) if pp in const_of else var_expr[pp] for pp in prefix)
+        split[ax] = (scale, early, late)
     for ai, ax in enumerate(AXES):
         parts_of = {"FREE": [], "CTL": []}
         for aj, short, f, rec in terms:
@@ -530,6 +568,15 @@ def main():
             dw(f"#define F16_AERO_{ax}_{kind} ( \\")
             dw("  0.0 \\")
             for short, expr in sums[ax][kind]:
+                dw(f"  + {expr} /* {short} */ \\")
+            dw("  )")
+    for ax in AXES:
+        scale, early, late = split[ax]
+        dw(f"#define F16_AERO_{ax}_SCALE ({scale})")
+        for kind, lst in (("EARLY", early), ("LATE", late)):
+            dw(f"#define F16_AERO_{ax}_{kind} ( \\")
+            dw("  0.0 \\")
+            for short, expr in lst:
                 dw(f"  + {expr} /* {short} */ \\")
             dw("  )")
     with open(os.path.join(args.out_dir, "f16_aero_gen.inc"), "w") as fh:
