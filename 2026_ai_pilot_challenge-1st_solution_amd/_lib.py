@@ -26,7 +26,7 @@ class F16Recon(ctypes.Structure):
                 ("prev_valid", _vp), ("pqr", _vp), ("dealt", _vp), ("taken", _vp),
                 ("hp_loss", _vp), ("act_hist", _vp), ("prev_x", _vp), ("prev_x_valid", _vp),
                 ("prev_alt_log", _vp), ("prev_vel_ned", _vp), ("accel", _vp), ("ld", _l),
-                ("nenv", _i)]
+                ("nenv", _i), ("aux", _vp)]
 
 
 class F16RewardCfg(ctypes.Structure):
@@ -97,6 +97,7 @@ _SIGNATURES = {
     "f16_obr_build_obs": (_i, [_vp, _l, _vp, _RP, _i, _vp, _vp]),
     "f16_env_post_step": (_i, [ctypes.POINTER(F16EnvStepIO), _RP, _CP, _vp]),
     "f16_state9": (_i, [_vp, _l, _i, _vp, _vp]),
+    "f16_future_labels": (_i, [_vp, _vp, _i, _i, _d, _vp, _vp, _vp]),
     "f16_policy_step": (_i, [ctypes.POINTER(F16PolicyArgs), _vp]),
     "f16_norm_workspace_bytes": (_l, [_i, _i]),
     "f16_abi_struct_sizes": (_i, [ctypes.POINTER(_l), _i]),

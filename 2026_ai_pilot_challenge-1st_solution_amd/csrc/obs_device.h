@@ -36,6 +36,7 @@ constexpr double kTimeTol = 1.0e-8;
 constexpr double kAltLogScale = 304.8;
 constexpr double kAltLogFloor = 1e-4;
 constexpr int kActHist = 20;                        // 5 steps x 4 channels, newest first
+constexpr int kAuxDim = 21;                         // future-aux features per engagement
 
 // Official origin (37.240778 N, 131.869556 E, 0 m) in ECEF metres, its trigonometry, and the
 // WGS84 polar radius b = a sqrt(1 - e^2) and second eccentricity ep2 = (a^2 - b^2) / b^2 of the

@@ -621,6 +621,24 @@ __global__ __launch_bounds__(kObsBlock) void init_reward_kernel(
   lane_init_reward(k, p, g, a, r.t_sec[e], r);
 }
 
+// Future-aux training features of plane 0 (R/cuda_fdm/gen/obs_kernel.cu:348-355; the layout of
+// R/cuda_fdm/future_aux.py:1-7), fp64: own NED position [m] and NED velocity [m/s], the
+// partner's, own NED-to-body rotation row-major.  Written with the row that becomes the
+// engagement's observation.
+__device__ __forceinline__ void store_aux(const Kin9& k, const Peer& p, const F16Recon& r, long a) {
+  if (!r.aux || (a & 1)) return;
+  double* o = r.aux + (a >> 1) * kAuxDim;
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    o[i] = k.s9[i];
+    o[3 + i] = k.vn[i];
+    o[6 + i] = p.s9[i];
+    o[9 + i] = p.vn[i];
+#pragma unroll
+    for (int j = 0; j < 3; ++j) o[12 + 3 * i + j] = k.A.R[i][j];
+  }
+}
+
 template <int D, bool FULL>
 __global__ __launch_bounds__(kRowBlock) void build_obs_kernel(
     const double* __restrict__ st, long ld, const unsigned char* __restrict__ mask, F16Recon r,
@@ -642,6 +660,7 @@ __global__ __launch_bounds__(kRowBlock) void build_obs_kernel(
     const ObsIn in = load_obs_in(r, a, e);
     lane_build_obs<D, FULL>(k, p, g, in, a, r,
                             ObsOut{S + lane * tile_pitch<D, FULL>(), obs + a * D, nullptr});
+    store_aux(k, p, r, a);
   }
   const uint64_t keep = __ballot(on);
   __syncthreads();
@@ -787,6 +806,7 @@ __global__ __launch_bounds__(kRowBlock) void env_post_step_kernel(const F16EnvSt
       const ObsOut out{tile, io.obs + a * D, nullptr};
       store_run2<D, FULL, kHistCol, kActHist>(out, o.hist);
       lane_build_obs<D, FULL>(k, p, g, o.obs, a, r, out, 1);
+      store_aux(k, p, r, a);
     }
     const uint64_t rows = __ballot(on);
     __syncthreads();
@@ -799,6 +819,7 @@ __global__ __launch_bounds__(kRowBlock) void env_post_step_kernel(const F16EnvSt
     const ObsOut out{tile, io.terminal_obs + a * D, d ? nullptr : io.obs + a * D};
     store_run2<D, FULL, kHistCol, kActHist>(out, o.hist);
     lane_build_obs<D, FULL>(k, p, g, o.obs, a, r, out, 1);
+    if (!d) store_aux(k, p, r, a);
   }
   const uint64_t rows = __ballot(on), live = __ballot(on && !d), fresh = __ballot(on && d);
   __syncthreads();
@@ -812,6 +833,7 @@ __global__ __launch_bounds__(kRowBlock) void env_post_step_kernel(const F16EnvSt
     lane_autoreset(io, r, O, a, e, odd, step, k2, p2, g2);
     lane_build_obs<D, FULL>(k2, p2, g2, fresh_obs_in(), a, r,
                             ObsOut{tile, io.obs + a * D, nullptr}, 2);
+    store_aux(k2, p2, r, a);
   }
   __syncthreads();
   flush_sparse<D, FULL>(S, a0, fresh, io.obs, lane);
@@ -984,5 +1006,61 @@ extern "C" int f16_state9(const double* states, long ld, int nac, double* s9, vo
   if (!states || !s9) return F16_EINVAL;
   hipLaunchKernelGGL(state9_kernel, dim3((unsigned)((nac + kObsBlock - 1) / kObsBlock)),
                      dim3(kObsBlock), 0, (hipStream_t)stream, states, ld, nac, origin(), s9);
+  return f16_last_error();
+}
+
+// ---- build_future_labels (R/cuda_fdm/future_aux.py:29-55): one lane per engagement walks the
+// rollout; episode ids are the running count of episode starts, a horizon is valid when no
+// start falls in (t, t + h].
+namespace f16obs {
+constexpr int kAuxOppH = 5, kAuxSelfH = 10;
+constexpr double kAuxPosScaleM = 100.0;
+
+__global__ __launch_bounds__(256) void future_labels_kernel(const double* __restrict__ f,
+                                                            const float* __restrict__ starts,
+                                                            int T, int nenv, double dt,
+                                                            float* __restrict__ labels,
+                                                            unsigned char* __restrict__ mask) {
+  const long e = (long)blockIdx.x * 256 + threadIdx.x;
+  if (e >= nenv) return;
+  long eid_t = 0;                                  // episode id at t (starts[0..t] counted)
+  for (int t = 0; t < T; ++t) {
+    eid_t += (long)starts[(long)t * nenv + e];     // torch: episode_starts.to(int64).cumsum(0)
+    const double* ft = f + ((long)t * nenv + e) * kAuxDim;
+    for (int slot = 0; slot < 2; ++slot) {
+      const int h = slot == 0 ? kAuxOppH : kAuxSelfH;
+      const int pos = slot == 0 ? 6 : 0, vel = slot == 0 ? 9 : 3;
+      float out[3] = {0.0f, 0.0f, 0.0f};
+      unsigned char ok = 0;
+      if (t + h < T) {
+        long eid_h = eid_t;
+        for (int s2 = t + 1; s2 <= t + h; ++s2) eid_h += (long)starts[(long)s2 * nenv + e];
+        if (eid_h == eid_t) {
+          const double* fh = f + ((long)(t + h) * nenv + e) * kAuxDim;
+          double res[3];
+          for (int i = 0; i < 3; ++i)
+            res[i] = (fh[pos + i] - ft[pos + i]) - ft[vel + i] * ((double)h * dt);
+          for (int i = 0; i < 3; ++i) {
+            const double* R = ft + 12 + 3 * i;
+            out[i] = (float)((R[0] * res[0] + R[1] * res[1] + R[2] * res[2]) / kAuxPosScaleM);
+          }
+          ok = 1;
+        }
+      }
+      float* L = labels + ((long)t * nenv + e) * 6 + 3 * slot;
+      for (int i = 0; i < 3; ++i) L[i] = out[i];
+      mask[((long)t * nenv + e) * 2 + slot] = ok;
+    }
+  }
+}
+}  // namespace f16obs
+
+extern "C" int f16_future_labels(const double* features, const float* starts, int T, int nenv,
+                                 double dt, float* labels, unsigned char* mask, void* stream) {
+  if (T < 0 || nenv < 0 || !(dt > 0.0)) return F16_EINVAL;
+  if (T == 0 || nenv == 0) return 0;
+  if (!features || !starts || !labels || !mask) return F16_EINVAL;
+  hipLaunchKernelGGL(f16obs::future_labels_kernel, dim3((nenv + 255) / 256), dim3(256), 0,
+                     (hipStream_t)stream, features, starts, T, nenv, dt, labels, mask);
   return f16_last_error();
 }

@@ -18,6 +18,7 @@ import math
 import torch
 
 from . import _lib
+from .future_aux import AUX_FEATURE_DIM
 
 OBS_SIZE = 184
 OBS_SIZE_EXT = 214
@@ -134,7 +135,15 @@ class BatchObsReward:
         r.prev_alt_log = p(self.prev_alt_log)
         r.prev_vel_ned, r.accel = p(self._vel_soa), p(self._acc_soa)
         r.ld, r.nenv = self.nac, self.nenv
+        r.aux = p(self.aux_features)
         return r
+
+    def enable_aux_capture(self):
+        """Future-aux features (obs_reward.py:355-358): every observation launch also writes the
+        (nenv, 21) float64 features of plane 0 (training labels only, never observations)."""
+        if self.aux_features is None:
+            self.aux_features = torch.zeros(self.nenv, AUX_FEATURE_DIM, dtype=torch.float64,
+                                            device=self.device)
 
     def _check(self, t, shape, dtypes, label):
         """Validate the raw-pointer ABI before a launch can read memory (obs_reward.py:391-401)."""
@@ -246,7 +255,10 @@ class BatchObsReward:
 
     # ---- snapshot / capture / restore (obs_reward.py:536-556) ----
     def clone_state(self):
-        return {k: getattr(self, k).clone() for k in self._AC_KEYS + self._ENV_KEYS}
+        buf = {k: getattr(self, k).clone() for k in self._AC_KEYS + self._ENV_KEYS}
+        if self.aux_features is not None:
+            buf["aux_features"] = self.aux_features.clone()
+        return buf
 
     def capture_into(self, buf, env_mask):
         ac = env_mask.repeat_interleave(2)
@@ -254,10 +266,14 @@ class BatchObsReward:
             buf[k][ac] = getattr(self, k)[ac]
         for k in self._ENV_KEYS:
             buf[k][env_mask] = getattr(self, k)[env_mask]
+        if self.aux_features is not None:
+            buf["aux_features"][env_mask] = self.aux_features[env_mask]
 
     def restore(self, buf):
         for k in self._AC_KEYS + self._ENV_KEYS:
             getattr(self, k).copy_(buf[k])
+        if self.aux_features is not None:
+            self.aux_features.copy_(buf["aux_features"])
 
     def push_actions(self, actions_nac4):
         """Roll the action history by one decision, newest first (obs_reward.py:559-563)."""

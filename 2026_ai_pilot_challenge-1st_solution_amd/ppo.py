@@ -95,6 +95,27 @@ class _RolloutGraph:
         return adv, ret, dict(stats)
 
 
+def _aux_buffers(o, env, aux):
+    """aux=True: the future-aux buffers of collect_rollout (ppo_gpu.py:1194-1197) -- features of
+    plane 0 per step (T, nenv, 21) float64, labels (T, nenv, 6) float32 and mask (T, nenv, 2),
+    built after the rollout by f16_future_labels from the features and b_done."""
+    o.b_aux_features = o.b_aux_labels = o.b_aux_mask = None
+    if not aux:
+        return
+    env.enable_aux_capture()
+    ne, dev = env.nenv, env.device
+    o.b_aux_features = torch.zeros(o.T, ne, 21, dtype=torch.float64, device=dev)
+    o.b_aux_labels = torch.zeros(o.T, ne, 6, dtype=torch.float32, device=dev)
+    o._aux_mask_u8 = torch.zeros(o.T, ne, 2, dtype=torch.uint8, device=dev)
+    o.b_aux_mask = o._aux_mask_u8.view(torch.bool)
+
+
+def _aux_labels(o):
+    if o.b_aux_features is not None:            # ppo_gpu.py:1996-1999
+        from .future_aux import labels_into
+        labels_into(o.b_aux_features, o.b_done, o.env.obr.dt, o.b_aux_labels, o._aux_mask_u8)
+
+
 class SelfPlayRollout:
     """Rollout collection with one policy on both aircraft of every engagement (BASELINE C4):
     the per-step sequence of PPOGPUTrainer.collect_rollout (research/competition_36500/runtime/
@@ -117,7 +138,7 @@ class SelfPlayRollout:
     net.pack() are picked up by the next replay.  (stats=False only.)"""
 
     def __init__(self, env, net, T=64, gamma=0.99, lam=0.95, seed=0, update_norm=True,
-                 stats=True, graph=False):
+                 stats=True, graph=False, aux=False):
         from .policy import PolicyStep, RunningNorm
         self.env, self.net, self.T = env, net, int(T)
         self.gamma, self.lam = float(gamma), float(lam)
@@ -146,6 +167,7 @@ class SelfPlayRollout:
         if self._graph_mode and self.want_stats:
             raise ValueError("graph=True needs stats=False")
         self._graphs = _RolloutGraph(self, dev) if self._graph_mode else None
+        _aux_buffers(self, env, aux)
 
     def reset(self, **kw):
         obs = self.env.reset(**kw)
@@ -177,6 +199,8 @@ class SelfPlayRollout:
             ep_count = torch.zeros((), device=dev)
         for t in range(T):
             obs = self.next_obs
+            if self.b_aux_features is not None:       # features of s_t (ppo_gpu.py:1876-1879)
+                self.b_aux_features[t].copy_(env.obr.aux_features)
             if self.update_norm:
                 self.norm.update(obs)
             self._policy(obs, g0 + t, pol_base, nobs_out=self.b_obs[t], act_idx=self.b_act[t],
@@ -191,6 +215,7 @@ class SelfPlayRollout:
                 ep_count += done_t.sum()
                 self.ep_ret *= 1.0 - d2
         self._policy(self.next_obs, g0 + T, pol_base, value=self.last_val)
+        _aux_labels(self)
         shape = (T, self.nenv, 2)
         adv, ret = gae(self.b_rew.view(shape), self.b_val.view(shape), self.b_done,
                        self.last_val.view(self.nenv, 2), self.next_done, self.gamma, self.lam)
@@ -237,7 +262,7 @@ class LeagueRollout:
     bit; adv/ret overwritten by the next collect())."""
 
     def __init__(self, env, net, opponents, T=128, gamma=0.99, lam=0.95, seed=0,
-                 update_norm=True, opp_weights=None, opp_norms=None, graph=False):
+                 update_norm=True, opp_weights=None, opp_norms=None, graph=False, aux=False):
         from .policy import PolicyStep, RunningNorm
         if len(opponents) < 1 or len(opponents) > 16:
             raise ValueError("1..16 opponent networks")
@@ -284,6 +309,7 @@ class LeagueRollout:
         self.opp_events = None
         self._graph_mode = bool(graph)
         self._graphs = _RolloutGraph(self, dev) if self._graph_mode else None
+        _aux_buffers(self, env, aux)
 
     def reset(self, **kw):
         """Reset the env and draw every engagement's opponent from the weights (seeded)."""
@@ -325,6 +351,8 @@ class LeagueRollout:
         self.b_done[0].copy_(self.next_done)
         for t in range(T):
             obs = self.next_obs
+            if self.b_aux_features is not None:
+                self.b_aux_features[t].copy_(env.obr.aux_features)
             if self.update_norm:
                 self.norm.update(obs, rows=self.main_rows)
             self._timed(self.policy_events, lambda: self.policy(
@@ -340,6 +368,7 @@ class LeagueRollout:
         self.policy(self.next_obs, [(self.net, 0, self.nenv)], norm=self.norm,
                     rows=self.main_rows, nphys=self.nac, step=g0 + T, value=self.last_val,
                     step_base=pol_base)
+        _aux_labels(self)
         adv, ret = gae(self.b_rew, self.b_val, self.b_done, self.last_val, self.next_done,
                        self.gamma, self.lam)
         return adv, ret, {}

@@ -77,6 +77,12 @@ class GpuDogfightVecEnv:
         self._cfg, self._cfg_key = None, None
         self._post_steps = 0
 
+    def enable_aux_capture(self):
+        """Turn on the future-aux features (BatchObsReward.enable_aux_capture): every step and
+        reset then also writes obr.aux_features (nenv, 21) for the returned observations."""
+        self.obr.enable_aux_capture()
+        self._rec = self.obr._recon()
+
     # ---- initial conditions (rl_env.py:218-375) ----
     def _sample_pairs(self, npairs):
         return icm.contest_rows(self.rng, npairs, self.scenario_b_prob, self.fuel_lbs_range)

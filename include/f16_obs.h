@@ -39,6 +39,10 @@ typedef struct F16Recon {
     double *accel;         /* (3, ld)    214-D only (else NULL): NED acceleration [m/s^2]    */
     long ld;               /* column stride of the (k, ld) arrays, >= nac                   */
     int nenv;
+    double *aux;           /* (nenv, 21) future-aux features of plane 0, or NULL (off): own NED
+                              position [m] and velocity [m/s], the partner's, own NED-to-body
+                              rotation row-major -- written wherever a row becomes the
+                              engagement's observation (R/cuda_fdm/gen/obs_kernel.cu:348-355)  */
 } F16Recon;
 
 /* MY_REWARD_CONFIG scalars (claude_code/my_reward.py:45-103) and the kernel_advance options
@@ -126,6 +130,15 @@ int f16_env_post_step(const F16EnvStepIO *io, const F16Recon *rec, const F16Rewa
  * plane about the official origin of the point at the aircraft's geodetic latitude/longitude),
  * roll, pitch, yaw [deg], body u, v, w [m/s].  s9: (nac, 9) row-major float64. */
 int f16_state9(const double *states, long ld, int nac, double *s9, void *stream);
+
+/* build_future_labels (R/cuda_fdm/future_aux.py:29-55): from the (T, nenv, 21) features of a
+ * rollout and its (T, nenv) episode-start flags (the done flag entering each step; nonzero =
+ * start), labels (T, nenv, 6) float32 and mask (T, nenv, 2) bytes.  Slot 0: the partner 5 steps
+ * ahead, slot 1: own 10 steps ahead; each the position change minus the constant-velocity
+ * prediction (h * dt * velocity), rotated into the current own body frame, / 100 m; zero and
+ * masked when an episode starts within the horizon or the horizon leaves the rollout. */
+int f16_future_labels(const double *features, const float *starts, int T, int nenv, double dt,
+                      float *labels, unsigned char *mask, void *stream);
 
 #ifdef __cplusplus
 }
