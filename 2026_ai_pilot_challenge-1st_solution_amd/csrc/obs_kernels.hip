@@ -839,6 +839,24 @@ __global__ __launch_bounds__(kRowBlock) void env_post_step_kernel(const F16EnvSt
   flush_sparse<D, FULL>(S, a0, fresh, io.obs, lane);
 }
 
+// Masked autoreset without a step: engagements with mask[e] != 0 get an initial-condition pool
+// row (io.pick or the in-kernel Philox draw), the reconstructor reset and the reward state
+// re-anchored -- the departure reseeding of the staggered warm-up (rl_env.py:386-434) on the
+// device.  No observation is built (the warm-up builds them once at its end).
+__global__ __launch_bounds__(kRowBlock) void reseed_kernel(const F16EnvStepIO io, F16Recon r,
+                                                           const unsigned char* __restrict__ mask,
+                                                           Origin O) {
+  const long a = (long)blockIdx.x * kRowBlock + threadIdx.x;
+  const long nac = 2L * r.nenv;
+  const long e = a >> 1;
+  if (a >= nac || !mask[e]) return;              // pairs agree: the exchanges stay paired
+  const uint32_t step = io.step + (io.step_base ? *io.step_base : 0u);
+  Kin9 k;
+  Peer p;
+  Geo g;
+  lane_autoreset(io, r, O, a, e, (int)(a & 1), step, k, p, g);
+}
+
 // rl_env.py:583-592 state9_flat: (nac, 9) float64 rows N/E/D m, roll/pitch/yaw deg, u/v/w m/s
 __global__ __launch_bounds__(kObsBlock) void state9_kernel(const double* __restrict__ st, long ld,
                                                             int nac, Origin O,
@@ -997,6 +1015,21 @@ extern "C" int f16_env_post_step(const F16EnvStepIO* io, const F16Recon* rec,
     if (full) F16_POST_STEP(214, true); else F16_POST_STEP(214, false);
   }
 #undef F16_POST_STEP
+  return f16_last_error();
+}
+
+extern "C" int f16_env_reseed(const F16EnvStepIO* io, const F16Recon* rec,
+                              const unsigned char* mask, void* stream) {
+  if (!io || !mask) return F16_EINVAL;
+  int rc = check_recon(rec, io->obs_dim == 214);
+  if (rc) return rc;
+  if (rec->nenv == 0) return 0;
+  if (!io->states || !io->ic_pool || io->pool_size < 1 || io->pool_size > 0xffffffffL ||
+      io->ld < 2L * rec->nenv || rec->ld != io->ld)
+    return F16_EINVAL;
+  if (io->opp_assign && (!io->opp_cdf || io->n_opp < 1)) return F16_EINVAL;
+  hipLaunchKernelGGL(reseed_kernel, grid_rows(rec->nenv), dim3(kRowBlock), 0, (hipStream_t)stream,
+                     *io, *rec, mask, origin());
   return f16_last_error();
 }
 

@@ -119,12 +119,11 @@ CONTEST_DIST_HEADON_FT = 5539.0 / FT2M
 CONTEST_FUEL_LBS = 3000.0
 
 
-def contest_pair(rng, scenario_b_prob=0.0, alt_ft=None, speed=None, side_swap=None,
-                 scenario_b=None, head_swap=None, dist_ft=None, fuel_range=None):
-    """One engagement's (own, target) IC rows from the contest distribution, drawing from the
-    numpy Generator in the reference's order (rl_env.py:218-250): altitude, speed, side swap,
-    scenario B, then heading swap and 3-9 distance.  Scenario A puts the two aircraft abeam on
-    the north axis with opposite east/west headings; B is head-on."""
+def _contest_draw(rng, scenario_b_prob=0.0, alt_ft=None, speed=None, side_swap=None,
+                  scenario_b=None, head_swap=None, dist_ft=None, fuel_range=None):
+    """One engagement's draws, in the reference's order (rl_env.py:218-250): altitude, speed,
+    side swap, scenario B, then heading swap and 3-9 distance (scenario A only), then the optional
+    per-aircraft fuel.  Returns (own_n, tgt_n, d, speed_fps, own_hdg, tgt_hdg, fuel0, fuel1)."""
     alt_ft = float(rng.uniform(*CONTEST_ALT_FT) if alt_ft is None else alt_ft)
     speed = float(rng.uniform(*CONTEST_SPEED_MPS) if speed is None else speed)
     side_swap = bool(rng.integers(0, 2) if side_swap is None else side_swap)
@@ -134,25 +133,48 @@ def contest_pair(rng, scenario_b_prob=0.0, alt_ft=None, speed=None, side_swap=No
         own_hdg, tgt_hdg = (0.0, 180.0) if side_swap else (180.0, 0.0)
     else:
         head_swap = bool(rng.integers(0, 2) if head_swap is None else head_swap)
-        dist_ft = float(rng.choice(np.asarray(CONTEST_DIST_A_FT)) if dist_ft is None else dist_ft)
+        # rng.integers(0, 3) consumes the Generator's stream exactly as rng.choice of a 3-element
+        # array does (the reference's call), at a seventh of the cost
+        dist_ft = float(CONTEST_DIST_A_FT[int(rng.integers(0, 3))] if dist_ft is None else dist_ft)
         half = 0.5 * dist_ft * FT2M
         own_hdg, tgt_hdg = (270.0, 90.0) if head_swap else (90.0, 270.0)
     own_n = CONTEST_CENTER_N + (-half if side_swap else half)
     tgt_n = CONTEST_CENTER_N + (half if side_swap else -half)
-    d = -alt_ft * FT2M
-    la, lo, h = ned_to_geodetic(np.array([own_n, tgt_n]), np.array([CONTEST_CENTER_E] * 2),
-                                np.array([d, d]))
     # fuel_range (lb): per-aircraft fuel drawn after the reference's draws (league workload with
     # fuel exhaustion); None keeps the contest's 3000 lb
     f = (rng.uniform(*fuel_range, size=2) if fuel_range is not None
          else (CONTEST_FUEL_LBS, CONTEST_FUEL_LBS))
-    return [ic_row(la[0], lo[0], h[0], speed * M2FT, own_hdg, float(f[0])),
-            ic_row(la[1], lo[1], h[1], speed * M2FT, tgt_hdg, float(f[1]))]
+    return (own_n, tgt_n, -alt_ft * FT2M, speed * M2FT, own_hdg, tgt_hdg, float(f[0]),
+            float(f[1]))
+
+
+def _rows_from_draws(dr):
+    """(P, 8) draws -> (2P, 10) IC rows; the geodetic conversion runs once over all aircraft."""
+    dr = np.asarray(dr, dtype=np.float64).reshape(-1, 8)
+    P = dr.shape[0]
+    n = np.stack([dr[:, 0], dr[:, 1]], axis=1).reshape(-1)
+    d = np.repeat(dr[:, 2], 2)
+    la, lo, h = ned_to_geodetic(n, np.full(2 * P, CONTEST_CENTER_E), d)
+    rows = np.zeros((2 * P, 10))
+    rows[:, 0], rows[:, 1], rows[:, 2] = la, lo, h
+    rows[:, 3] = np.repeat(dr[:, 3], 2)
+    rows[:, 6] = dr[:, 4:6].reshape(-1)
+    rows[:, 9] = dr[:, 6:8].reshape(-1)
+    return rows
+
+
+def contest_pair(rng, scenario_b_prob=0.0, **fixed):
+    """One engagement's (own, target) IC rows from the contest distribution (rl_env.py:218-250).
+    Scenario A puts the two aircraft abeam on the north axis with opposite east/west headings;
+    B is head-on.  Keyword arguments fix individual draws (alt_ft, speed, side_swap, scenario_b,
+    head_swap, dist_ft, fuel_range)."""
+    return [list(r) for r in _rows_from_draws([_contest_draw(rng, scenario_b_prob, **fixed)])]
 
 
 def contest_rows(rng, npairs, scenario_b_prob=0.0, fuel_range=None):
-    """(2*npairs, 10) IC rows, plane 0 = ownship, plane 1 = target."""
-    rows = []
-    for _ in range(npairs):
-        rows += contest_pair(rng, scenario_b_prob, fuel_range=fuel_range)
-    return np.asarray(rows, dtype=np.float64).reshape(-1, 10)
+    """(2*npairs, 10) IC rows, plane 0 = ownship, plane 1 = target: the per-engagement draws in
+    the reference's order, then one vectorised geodetic conversion."""
+    if npairs == 0:
+        return np.zeros((0, 10))
+    return _rows_from_draws([_contest_draw(rng, scenario_b_prob, fuel_range=fuel_range)
+                             for _ in range(npairs)])

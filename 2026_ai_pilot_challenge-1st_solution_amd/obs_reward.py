@@ -269,6 +269,16 @@ class BatchObsReward:
         if self.aux_features is not None:
             buf["aux_features"][env_mask] = self.aux_features[env_mask]
 
+    def capture_where(self, buf, env_mask):
+        """capture_into without host synchronisation: masked device copies (torch.where)."""
+        ac = env_mask.repeat_interleave(2)
+        keys = [(k, ac) for k in self._AC_KEYS] + [(k, env_mask) for k in self._ENV_KEYS]
+        if self.aux_features is not None:
+            keys.append(("aux_features", env_mask))
+        for k, mask in keys:
+            cur, dst = getattr(self, k), buf[k]
+            torch.where(mask.view(-1, *([1] * (cur.dim() - 1))), cur, dst, out=dst)
+
     def restore(self, buf):
         for k in self._AC_KEYS + self._ENV_KEYS:
             getattr(self, k).copy_(buf[k])

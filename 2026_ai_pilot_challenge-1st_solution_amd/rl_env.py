@@ -101,15 +101,6 @@ class GpuDogfightVecEnv:
         if self.ic_pool is None:
             self.ic_pool = self._initialize_physical_seeds(self._sample_pairs(self.ic_pool_size))
 
-    def _seed_envs(self, env_indices):
-        """Re-seed the given engagements with fresh contest ICs (no neutral tick, rl_env.py:436-451)."""
-        if not len(env_indices):
-            return
-        rows = self._sample_pairs(len(env_indices))
-        ac = torch.tensor([[2 * e, 2 * e + 1] for e in env_indices], dtype=torch.int64,
-                          device=self.device).flatten()
-        self.sim.seed_rows(torch.as_tensor(rows, dtype=torch.float64, device=self.device), ac)
-
     # ---- reset (rl_env.py:362-434) ----
     def reset(self, stagger=True, max_stagger_steps=256, warmup_action_fn=None):
         """Fresh contest ICs for every engagement; with stagger, each engagement is advanced a
@@ -121,7 +112,9 @@ class GpuDogfightVecEnv:
         self.obr.reset_all()
         self.obr.kernel_init_reward_state(self.sim.states)
         if stagger and max_stagger_steps > 0:
-            self._staggered_warmup(max_stagger_steps, warmup_action_fn)
+            finite = self._staggered_warmup(max_stagger_steps, warmup_action_fn)
+            if not bool(finite):               # the warm-up's one host check
+                raise FloatingPointError("non-finite physical trajectory during staggered initialization")
         return self._build_obs_all()
 
     def _build_obs_all(self, env_mask=None):
@@ -135,55 +128,62 @@ class GpuDogfightVecEnv:
         return a
 
     def _staggered_warmup(self, max_steps, action_fn):
-        """rl_env.py:386-434: advance engagement e by p_e ~ U[0, max_steps) valid decisions,
-        re-seeding any that depart first, and capture physics + reconstructor at that phase."""
-        targ = torch.tensor(self.rng.integers(0, max_steps, size=self.nenv), device=self.device)
-        age = torch.zeros(self.nenv, dtype=torch.long, device=self.device)
+        """rl_env.py:386-434 on the device: engagement e is advanced p_e ~ U[0, max_steps) valid
+        decisions; an engagement that departs (below 100 m or non-finite) before its phase is
+        re-seeded from the initial-condition pool (f16_env_reseed: pool row, reconstructor reset,
+        re-anchored reward) and counts again; at its phase its physics and reconstructor are
+        captured.  Nothing inside the loop synchronises with the host: every branch of the
+        reference's loop is a masked device update and the loop runs its max_steps bound.
+        Returns the device flag "every uncaptured trajectory stayed finite"."""
+        self._ensure_ic_pool()
+        ne, dev = self.nenv, self.device
+        targ = torch.as_tensor(self.rng.integers(0, max_steps, size=ne)).pin_memory()
+        targ = targ.to(dev, non_blocking=True)
+        age = torch.zeros(ne, dtype=torch.long, device=dev)
         captured_mask = targ == 0
         captured = self.sim.states.clone()
         obr_buf = self.obr.clone_state()
-        warm_finite = torch.ones((), dtype=torch.bool, device=self.device)
-        for _ in range(max_steps):
+        warm_finite = torch.ones((), dtype=torch.bool, device=dev)
+        mask_u8 = torch.empty(ne, dtype=torch.uint8, device=dev)
+        for k in range(max_steps):
             if action_fn is None:
                 a = self._random_actions()
             else:
                 a = action_fn(self._build_obs_all().reshape(self.nac, self.OBS_SIZE))
                 a = torch.as_tensor(a, dtype=torch.float64, device=self.device).reshape(self.nac, 4)
             self.sim.step(a, substeps=self.substeps, want_obs=False)
-            fin = torch.isfinite(self.sim.states).reshape(self.nenv, -1).all(dim=1)
+            fin = torch.isfinite(self.sim.states).reshape(ne, -1).all(dim=1)
             warm_finite.logical_and_((fin | captured_mask).all())
             # push + advance (the kernel's reward side effects are re-anchored after capture)
             self.obr.kernel_advance(self.sim.states, a, cfg=self.reward_cfg,
                                     min_alt=self.min_altitude_m, max_time=self.max_engage_time_s,
                                     reward_mode=self.reward_mode, alt_hunt_coef=self.alt_hunt_coef)
             dep = self._departed_envs(self.state9_flat()) & (~captured_mask)
-            if bool(dep.any()):
-                self._seed_envs(torch.nonzero(dep).flatten().tolist())
-                self.obr.reset_envs(dep)
-                self.obr.kernel_init_reward_state(self.sim.states, dep)
-                age[dep] = 0
-            age = age + (~captured_mask).long()
+            mask_u8.copy_(dep)
+            self._reseed(mask_u8, 0x80000000 | k)
+            age = torch.where(dep, torch.zeros_like(age), age) + (~captured_mask).long()
             hit = (~captured_mask) & (age == targ)
-            if bool(hit.any()):
-                hac = hit.repeat_interleave(2)
-                captured[hac] = self.sim.states[hac]
-                self.obr.capture_into(obr_buf, hit)
-                captured_mask |= hit
-            if bool(captured_mask.all()):
-                break
-        if not bool(captured_mask.all()):
-            rest = ~captured_mask
-            self._seed_envs(torch.nonzero(rest).flatten().tolist())
-            self.obr.reset_envs(rest)
-            self.obr.kernel_init_reward_state(self.sim.states, rest)
-            rac = rest.repeat_interleave(2)
-            captured[rac] = self.sim.states[rac]
-            self.obr.capture_into(obr_buf, rest)
-        if not bool(warm_finite):
-            raise FloatingPointError("non-finite physical trajectory during staggered initialization")
+            captured = torch.where(hit.repeat_interleave(2)[:, None], self.sim.states, captured)
+            self.obr.capture_where(obr_buf, hit)
+            captured_mask = captured_mask | hit
+        rest = ~captured_mask                      # departed too late to reach their phase
+        mask_u8.copy_(rest)
+        self._reseed(mask_u8, 0x80000000 | max_steps)
+        captured = torch.where(rest.repeat_interleave(2)[:, None], self.sim.states, captured)
+        self.obr.capture_where(obr_buf, rest)
         self.sim.states.copy_(captured)
         self.obr.restore(obr_buf)
         self.obr.kernel_init_reward_state(self.sim.states)
+        return warm_finite
+
+    def _reseed(self, mask_u8, step):
+        """f16_env_reseed over the engagements with mask_u8 set (pool draws keyed by `step`)."""
+        io = self._io(None)
+        io.step = step & 0xffffffff
+        io.opp_assign = None
+        rc = self.obr._lib.f16_env_reseed(_lib.ctypes.byref(io), _lib.ctypes.byref(self._rec),
+                                          mask_u8.data_ptr(), _lib.stream_handle(self.device))
+        _lib.check(rc, "f16_env_reseed")
 
     def _departed_envs(self, s9_flat=None, floor_m=100.0):
         s9 = (self.state9() if s9_flat is None else s9_flat.view(self.nenv, 2, 9))

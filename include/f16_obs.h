@@ -122,6 +122,14 @@ typedef struct F16EnvStepIO {
  * engagements keep the terminal observation in `obs`.  A pick outside [0, pool_size) fills that
  * engagement's states with NaN so the error surfaces as a non-finite state instead of an
  * out-of-bounds read.  obs and terminal_obs: 16-byte aligned for 184, 8-byte for 214. */
+/* The autoreset half of f16_env_post_step alone, for the engagements with mask[e] != 0
+ * ((nenv) bytes): pool row (io->pick or the Philox draw at io->step), reconstructor reset,
+ * re-anchored reward state (and, with io->opp_assign, an opponent redraw); no observation.  The
+ * device-side replacement of the staggered warm-up's host re-seeding (R/cuda_fdm/rl_env.py:
+ * 386-434).  Reads io->states, ld, ic_pool, pool_size, pick, seed, step, step_base, obs_dim. */
+int f16_env_reseed(const F16EnvStepIO *io, const F16Recon *rec, const unsigned char *mask,
+                   void *stream);
+
 int f16_env_post_step(const F16EnvStepIO *io, const F16Recon *rec, const F16RewardCfg *cfg,
                       void *stream);
 

@@ -40,3 +40,44 @@ def test_samplers_shapes_and_ranges():
     t = icm.sample_tailchase(8, seed=1)
     assert (t[0::2, 6] == t[1::2, 6]).all()           # shared heading
     assert (t[:, 9] == 6972.0).all()
+
+
+def _pairwise_contest(rng, npairs, scenario_b_prob, fuel_range):
+    """The reference's per-engagement draws (rl_env.py:218-250, rng.choice for the 3-9 distance)
+    converted one engagement at a time."""
+    icm = import_pkg("ic")
+    rows = []
+    for _ in range(npairs):
+        alt = rng.uniform(2000.0, 30000.0)
+        spd = rng.uniform(200.0, 300.0)
+        side = bool(rng.integers(0, 2))
+        b = rng.random() < scenario_b_prob
+        if b:
+            half, hdg = 0.5 * 5539.0, ((0.0, 180.0) if side else (180.0, 0.0))
+        else:
+            head = bool(rng.integers(0, 2))
+            half = 0.5 * float(rng.choice(np.asarray([2000.0, 2500.0, 3000.0]))) * 0.3048
+            hdg = (270.0, 90.0) if head else (90.0, 270.0)
+        fuel = rng.uniform(*fuel_range, size=2) if fuel_range else (3000.0, 3000.0)
+        for k, sgn in ((0, -1.0 if side else 1.0), (1, 1.0 if side else -1.0)):
+            la, lo, h = icm.ned_to_geodetic(3500.0 + sgn * half, 0.0, -alt * 0.3048)
+            rows.append([la, lo, h, spd / 0.3048, 0, 0, hdg[k], 0, 0, fuel[k]])
+    return np.asarray(rows, dtype=np.float64)
+
+
+def test_contest_rows_match_pairwise_draws():
+    """The batched sampler (per-engagement draws, one vectorised geodetic conversion) gives the
+    rows of drawing and converting engagement by engagement with the reference's calls, from the
+    same Generator state, and leaves the Generator where the pairwise draws leave it."""
+    icm = import_pkg("ic")
+    for kw in (dict(scenario_b_prob=0.0, fuel_range=None), dict(scenario_b_prob=0.35, fuel_range=None),
+               dict(scenario_b_prob=0.0, fuel_range=(1500.0, 3000.0))):
+        r1, r2 = np.random.default_rng(7), np.random.default_rng(7)
+        a = icm.contest_rows(r1, 300, **kw)
+        b = _pairwise_contest(r2, 300, **kw)
+        np.testing.assert_allclose(a, b, rtol=0, atol=1e-9)
+        assert r1.random() == r2.random()
+    # scenario A: abeam on the north axis, east/west headings, 3-9 separations
+    a = icm.contest_rows(np.random.default_rng(1), 200)
+    assert set(np.unique(a[:, 6])) <= {90.0, 270.0} and (a[0::2, 6] != a[1::2, 6]).all()
+    assert icm.contest_rows(np.random.default_rng(1), 0).shape == (0, 10)

@@ -414,6 +414,33 @@ def test_vec_env_contract(gpu):
                                   env.sim.states[64:].cpu().numpy())
 
 
+def test_staggered_warmup_is_device_resident(gpu):
+    """The staggered warm-up (rl_env.py:386-434) runs without one host synchronisation (torch's
+    sync debug mode would raise), captures every engagement at a whole number of decisions below
+    the bound (the engagement clock restarts with each re-seed), and leaves every aircraft finite
+    and above the 100 m departure floor."""
+    E = import_pkg("rl_env").GpuDogfightVecEnv
+    env = E(512, seed=11, ic_pool_size=64)
+    env.reset(stagger=False)
+    env._ensure_ic_pool()                  # built once per environment, before any warm-up
+    torch.cuda.synchronize()
+    steps = 24
+    torch.cuda.set_sync_debug_mode("error")
+    try:
+        finite = env._staggered_warmup(steps, None)
+    finally:
+        torch.cuda.set_sync_debug_mode(0)
+    assert bool(finite)
+    t = env.obr.t_sec.cpu().numpy()
+    k = np.round(t / env.obr.dt)
+    np.testing.assert_allclose(t, k * env.obr.dt, atol=1e-9)
+    assert k.min() >= 0 and k.max() < steps and len(np.unique(k)) > steps // 2
+    s9 = env.state9().cpu().numpy()
+    assert np.isfinite(s9).all() and (-s9[:, :, 2] > 100.0).all()
+    obs = env._build_obs_all()
+    assert torch.isfinite(obs).all()
+
+
 def test_obs_argument_errors(gpu):
     obr = _obr(8)
     st = torch.zeros(16, 101, dtype=torch.float64, device=gpu)
