@@ -17,6 +17,7 @@
 #include <hip/hip_runtime.h>
 
 #include "f16_model_gen.h"
+#include "fdm_math.h"
 #include "f16_state.h"
 
 // Every model function is host+device so the identical algorithm can also be built for the CPU
@@ -204,7 +205,7 @@ F16_HD Atmos isa(double h, const double* T) {
   constexpr double temps[9] = F16M_ATM_TMP_INIT;
   constexpr double dbrk[9] = F16M_ATM_DBRK_INIT;
   Atmos o;
-  const double gp = (h * kER) / (kER + h);
+  const double gp = fm_div(h * kER, kER + h);
   if (gp >= 0.0) {
     const F16Br1 b = F16_BR1(F16M_TG_ISA_TEMP_R, gp);
     o.T = f16_lerp1(T, F16M_T_ISA_TEMP_OFF, b);
@@ -220,20 +221,20 @@ F16_HD Atmos isa(double h, const double* T) {
   const double* lb = T + F16M_ATM_LAYER_OFF + F16M_ATM_LAYER_STRIDE * b;
   const double dH = gp - lb[0];
   const double kb = lb[2];
-  const double lg = log(1.0 + kb * dH);
-  o.P = lb[1] * exp(lb[3] * (kb != 0.0 ? lg : dH));
-  o.rho = o.P / (F16M_RENG * o.T);
-  o.a = sqrt(F16M_GAMMA_R * o.T);
+  const double lg = fm_log(1.0 + kb * dH);
+  o.P = lb[1] * fm_exp(lb[3] * (kb != 0.0 ? lg : dH));
+  o.rho = fm_div(o.P, F16M_RENG * o.T);
+  o.a = fm_sqrt(F16M_GAMMA_R * o.T);
   o.sigma = o.rho * (1.0 / F16M_RHO_SL);
   // density altitude: first d with rho >= dbrk[d+1]; pow(rho / rb, x) is exp(x log(rho / rb))
   int d = 0;
 #pragma unroll
   for (int i = 1; i < 8; ++i) d += !(o.rho >= dbrk[i]);
   const double* ld = T + F16M_ATM_LAYER_OFF + F16M_ATM_LAYER_STRIDE * d;
-  const double lr = log(o.rho * ld[5]);
+  const double lr = fm_log(o.rho * ld[5]);
   const double xd = ld[6];
-  const double da = ld[4] + ld[7] * (xd != 0.0 ? exp(xd * lr) - 1.0 : lr);
-  o.densalt = (da * kER) / (kER - da);
+  const double da = ld[4] + ld[7] * (xd != 0.0 ? fm_exp(xd * lr) - 1.0 : lr);
+  o.densalt = fm_div(da * kER, kER - da);
   return o;
 }
 
@@ -261,7 +262,7 @@ F16_HD Mass mass_props(double fuel) {
   Mass o;
   const double t = fuel / 2.0;
   const double weight = ew + (t + t) + pw;
-  const double iw = 1.0 / weight;
+  const double iw = fm_rcp(weight);
 #pragma unroll
   for (int i = 0; i < 3; ++i)
     o.cg[i] = (ew * bcg[i] + pw * pl[i] + t * t0l[i] + t * t1l[i]) * iw;
@@ -276,7 +277,7 @@ F16_HD Mass mass_props(double fuel) {
   const double Ixx = mJ[0][0], Iyy = mJ[1][1], Izz = mJ[2][2];
   const double Ixy = -mJ[0][1], Ixz = -mJ[0][2], Iyz = -mJ[1][2];
   double k1 = Iyy * Izz - Iyz * Iyz, k2 = Iyz * Ixz + Ixy * Izz, k3 = Ixy * Iyz + Iyy * Ixz;
-  const double den = 1.0 / (Ixx * k1 - Ixy * k2 - Ixz * k3);
+  const double den = fm_rcp(Ixx * k1 - Ixy * k2 - Ixz * k3);
   k1 *= den; k2 *= den; k3 *= den;
   o.Jinv[0] = k1; o.Jinv[1] = (Izz * Ixx - Ixz * Ixz) * den; o.Jinv[2] = (Ixx * Iyy - Ixy * Ixy) * den;
   o.Jinv[3] = k2; o.Jinv[4] = k3; o.Jinv[5] = (Ixy * Ixz + Iyz * Ixx) * den;
@@ -295,18 +296,18 @@ F16_HD double vcal_from_mach(double mach, double p) {
     pt = p;
   } else if (mach < 1.0) {
     const double m2 = 1.0 + 0.2 * mach * mach;   // m2^3.5 = m2^3 sqrt(m2)
-    pt = p * (m2 * m2 * m2 * sqrt(m2));
+    pt = p * (m2 * m2 * m2 * fm_sqrt(m2));
   } else {
     const double m2 = mach * mach, m7 = m2 * m2 * m2 * mach, d = 7.0 * m2 - 1.0;
-    pt = p * 166.92158009316827 * m7 / (d * d * sqrt(d));
+    pt = fm_div(p * 166.92158009316827 * m7, d * d * fm_sqrt(d));
   }
   const double qc = pt - p;
   const double A = qc * (1.0 / 2116.228) + 1.0;  // StdDaySLpressure (jsb_const.py:24)
-  double M = sqrt(5.0 * (exp(log(A) * (1.0 / 3.5)) - 1.0));
+  double M = fm_sqrt(5.0 * (fm_exp(fm_log(A) * (1.0 / 3.5)) - 1.0));
   if (M > 1.0) {
     for (int i = 0; i < 10; ++i) {
-      const double t = 1.0 - 1.0 / (7.0 * M * M);
-      M = 0.8812848543473311 * sqrt(A * (t * t * sqrt(t)));
+      const double t = 1.0 - fm_rcp(7.0 * M * M);
+      M = 0.8812848543473311 * fm_sqrt(A * (t * t * fm_sqrt(t)));
     }
   }
   return F16M_STD_SL_SOUNDSPEED * M;
@@ -349,11 +350,11 @@ F16_HD void kinematics(const double p[3], const double v[3], const double q[4],
   k.ey = ce * p[1] - se * p[0];
   k.ez = p[2];
   const double rxy2 = k.ex * k.ex + k.ey * k.ey;
-  k.radius = sqrt(rxy2 + k.ez * k.ez);
-  const double rxy = sqrt(rxy2);
+  k.radius = fm_sqrt(rxy2 + k.ez * k.ez);
+  const double rxy = fm_sqrt(rxy2);
   double sLon = 0.0, cLon = 1.0, sLat = 0.0, cLat = 1.0;
-  if (rxy != 0.0) { const double ir = 1.0 / rxy; sLon = k.ey * ir; cLon = k.ex * ir; }
-  k.irad = 1.0 / k.radius;
+  if (rxy != 0.0) { const double ir = fm_rcp(rxy); sLon = k.ey * ir; cLon = k.ex * ir; }
+  k.irad = fm_rcp(k.radius);
   if (k.radius != 0.0) { sLat = k.ez * k.irad; cLat = rxy * k.irad; }
   k.sLat = sLat;
   // local N, E, D axes in ECI (columns of Tl2i = Tec2i * Tl2ec; Tec2l rows from
@@ -386,8 +387,8 @@ F16_HD void kinematics(const double p[3], const double v[3], const double q[4],
   if (gimbal) {
     k.ctcp = 6.123233995736766e-17 * cos(atan2(-L[2][1], L[1][1]));   // cos(+-pi/2) in double
   } else {
-    const double h = sqrt(L[1][2] * L[1][2] + L[2][2] * L[2][2]);
-    k.ctcp = sqrt(1.0 - d6 * d6) * (h != 0.0 ? L[2][2] / h : 1.0);
+    const double h = fm_sqrt(L[1][2] * L[1][2] + L[2][2] * L[2][2]);
+    k.ctcp = fm_sqrt(1.0 - d6 * d6) * (h != 0.0 ? fm_div(L[2][2], h) : 1.0);
   }
   if (want_euler) {
     if (gimbal) {
@@ -501,15 +502,15 @@ F16_HD AuxGeo aux_geometry(const double uvw[3]) {
   const double u = uvw[0], v = uvw[1], w = uvw[2];
   const double muw = u * u + w * w;
   g.vt2 = muw + v * v;
-  g.vt = sqrt(g.vt2);
+  g.vt = fm_sqrt(g.vt2);
   g.alpha = 0.0; g.beta = 0.0; g.ca = 1.0; g.sa = 0.0; g.cb = 1.0; g.sb = 0.0;
   if (g.vt > 0.001) {
-    const double suw = sqrt(muw), ivt = 1.0 / g.vt;
+    const double suw = fm_sqrt(muw), ivt = fm_rcp(g.vt);
     g.beta = atan2(v, suw);
     g.cb = suw * ivt;
     g.sb = v * ivt;
     if (muw >= 1e-6) {
-      const double isuw = 1.0 / suw;
+      const double isuw = fm_rcp(suw);
       g.alpha = atan2(w, u);
       g.ca = u * isuw;
       g.sa = w * isuw;
@@ -551,7 +552,7 @@ F16_HD double engine(Aircraft& a, double c_thr, const Atmos& at, double mach,
   const double nx = a.n2n + 0.1;
   const double om = 1.0 - (nx < 1.0 ? nx : 1.0);
   const double den = 1.0 + 3.0 * (om * om * om) + (1.0 - at.sigma);
-  const double iden = 1.0 / den;
+  const double iden = fm_rcp(den);
   const double up = d_up * iden, n2dn = d_n2dn * iden, n1dn = d_n1dn * iden;
   a.n2 = seek(a.n2, F16M_ENG_IDLEN2 + thr * (F16M_ENG_MAXN2 - F16M_ENG_IDLEN2), up, n2dn);
   a.n1 = seek(a.n1, F16M_ENG_IDLEN1 + thr * (F16M_ENG_MAXN1 - F16M_ENG_IDLEN1), up, n1dn);
@@ -563,7 +564,7 @@ F16_HD double engine(Aircraft& a, double c_thr, const Atmos& at, double mach,
   const double mil = (F16M_ENG_MILTHRUST - idle) * f16_lerp2(T, F16M_T_ENG_MIL_OFF, F16M_T_ENG_MIL_NC, bm2, bd);
   double thrust = idle + mil * a.n2n * a.n2n;
   const double on = 1.0 - a.n2n;
-  const double tsfc = F16M_ENG_TSFC * sqrt(at.T * (1.0 / 389.7)) * (0.84 + on * on);
+  const double tsfc = F16M_ENG_TSFC * fm_sqrt(at.T * (1.0 / 389.7)) * (0.84 + on * on);
   a.ff = seek(a.ff, thrust * tsfc, 1000.0, 10000.0);
   a.ff = a.ff < F16M_IDLEFF ? F16M_IDLEFF : a.ff;
   if (aug > 0.0) {   // afterburner, AugMethod 2
@@ -579,7 +580,7 @@ F16_HD double engine(Aircraft& a, double c_thr, const Atmos& at, double mach,
 // ---- aerodynamics (jsb_aero.py:75-107): 40 coefficient functions ----
 F16_HD void aero_rates(double vt, double& bi2vel, double& ci2vel) {
   const double twovel = 2.0 * vt;
-  const double i2v = twovel != 0.0 ? 1.0 / twovel : 0.0;
+  const double i2v = twovel != 0.0 ? fm_rcp(twovel) : 0.0;
   bi2vel = F16M_BW * i2v;
   ci2vel = F16M_CBAR * i2v;
 }
@@ -636,7 +637,7 @@ F16_HD void accelerations(const double B[3][3], const double wpqr[3], const Mass
   o.wdi[0] = Ji[0] * m0 + Ji[3] * m1 + Ji[4] * m2;
   o.wdi[1] = Ji[3] * m0 + Ji[1] * m1 + Ji[5] * m2;
   o.wdi[2] = Ji[4] * m0 + Ji[5] * m1 + Ji[2] * m2;
-  const double sm = 1.0 / mb.mass;
+  const double sm = fm_rcp(mb.mass);
 #pragma unroll
   for (int i = 0; i < 3; ++i) o.pba[i] = F[i] * sm;
 #pragma unroll
@@ -652,9 +653,9 @@ F16_HD void propagate(Aircraft& a) {
   {
     double q0 = a.q[0] + kDt * a.qd[0], q1 = a.q[1] + kDt * a.qd[1];
     double q2 = a.q[2] + kDt * a.qd[2], q3 = a.q[3] + kDt * a.qd[3];
-    const double mag = sqrt(q0 * q0 + q1 * q1 + q2 * q2 + q3 * q3);
+    const double mag = fm_sqrt(q0 * q0 + q1 * q1 + q2 * q2 + q3 * q3);
     if (mag != 0.0) {
-      const double inv = 1.0 / mag;
+      const double inv = fm_rcp(mag);
       q0 = q0 * inv; q1 = q1 * inv; q2 = q2 * inv; q3 = q3 * inv;
     }
     a.q[0] = q0; a.q[1] = q1; a.q[2] = q2; a.q[3] = q3;
@@ -710,10 +711,10 @@ F16_HD void force_path(Aircraft& a, double c_ail, double c_ele, double c_rud,
   o.k_rud = fc.k_rud;
   const AuxGeo g = aux_geometry(k.uvw);
   const double qbar = 0.5 * at.rho * g.vt2;
-  const double mach = g.vt / at.a;
+  const double mach = fm_div(g.vt, at.a);
   load_factors(a, mb.cg, o.npy, o.npz);
   o.vc_kts = vc_knots(mach, at.P);
-  o.vg = sqrt(k.vn * k.vn + k.ve * k.ve);
+  o.vg = fm_sqrt(k.vn * k.vn + k.ve * k.ve);
   o.alpha = g.alpha; o.beta = g.beta; o.vt = g.vt; o.mach = mach; o.alt = alt;
   const double thrust = engine(a, c_thr, at, mach, T, o.fuel_burn);
   double ax[6];

@@ -14,11 +14,12 @@
 //   phase 2  flight:  air-relative geometry (vt, alpha, beta), load factors, alpha/beta brackets,
 //                     their table values and the alpha/beta-only part of each axis sum
 //            systems: atmosphere, pitch loop
-//   -- X2: vt, alpha, beta, n_y, n_z  |  rho, pressure, speed of sound, elevator
-//   phase 3  flight:  dynamic pressure, mach, calibrated airspeed, mach/elevator brackets and
-//                     values, the six axes, quaternion rate, gravity, vg
-//            systems: mach, engine, sin/cos of the next substep's Earth position angle
-//   -- X3: calibrated airspeed, vg, p q r  |  thrust, sin/cos(epa)
+//   -- X2: vt, alpha, beta, n_y, n_z  |  rho, speed of sound, elevator
+//   phase 3  flight:  dynamic pressure, mach, mach/elevator brackets and values, the six axes,
+//                     quaternion rate, gravity, vg
+//            systems: mach, calibrated airspeed, engine, sin/cos of the next substep's Earth
+//                     position angle
+//   -- X3: vg, p q r  |  thrust, sin/cos(epa)
 //   phase 4  flight:  forces, moments, accelerations, state update
 //            systems: fuel burn, previous-frame auxiliary values
 //
@@ -50,9 +51,9 @@ enum SplitField : int {
   // X2, flight -> systems
   kXVt, kXAlpha, kXBeta, kXNpy, kXNpz,
   // X2, systems -> flight
-  kXRho, kXPres, kXSound, kXElev,
+  kXRho, kXSound, kXElev,
   // X3, flight -> systems
-  kXVc, kXVg, kXP, kXQ, kXR,
+  kXVg, kXP, kXQ, kXR,
   // X3, systems -> flight
   kXThrust, kXCe, kXSe,
   kSplitFields
@@ -154,9 +155,8 @@ __device__ __forceinline__ void split_flight(double* __restrict__ s, long ld, in
     // ---- phase 3
     const double rho = x[kXRho][lane], sound = x[kXSound][lane], elev = x[kXElev][lane];
     const double qbar = 0.5 * rho * g.vt2;
-    mach = g.vt / sound;
-    x[kXVc][lane] = vc_knots(mach, x[kXPres][lane]);
-    x[kXVg][lane] = sqrt(k.vn * k.vn + k.ve * k.ve);
+    mach = fm_div(g.vt, sound);
+    x[kXVg][lane] = fm_sqrt(k.vn * k.vn + k.ve * k.ve);
     x[kXP][lane] = k.wpqr[0]; x[kXQ][lane] = k.wpqr[1]; x[kXR][lane] = k.wpqr[2];
     quat_rate(a);
     double gi[3];
@@ -258,13 +258,14 @@ __device__ __forceinline__ void split_systems(double* __restrict__ s, long ld,
     const double alt = x[kXAlt][lane], ctcp = x[kXCtcp][lane];
     const Atmos at = isa(alt, T);
     fcs_pitch<FCS_RATE>(a, esch, ctcp, fc);
-    x[kXRho][lane] = at.rho; x[kXPres][lane] = at.P; x[kXSound][lane] = at.a;
+    x[kXRho][lane] = at.rho; x[kXSound][lane] = at.a;
     x[kXElev][lane] = fc.elev;
     __syncthreads();
     // ---- phase 3
     const double vt = x[kXVt][lane], alpha = x[kXAlpha][lane];
     const double npy = x[kXNpy][lane], npz = x[kXNpz][lane];
-    const double mach = vt / at.a;
+    const double mach = fm_div(vt, at.a);
+    const double vc = vc_knots(mach, at.P);   // previous-frame input of the next substep's FCS
     double burn;
     x[kXThrust][lane] = engine(a, c_thr, at, mach, T, burn);
     if (t + 1 < S) {
@@ -275,7 +276,7 @@ __device__ __forceinline__ void split_systems(double* __restrict__ s, long ld,
     }
     __syncthreads();
     // ---- phase 4
-    const double vc = x[kXVc][lane], vg = x[kXVg][lane];
+    const double vg = x[kXVg][lane];
     const double p = x[kXP][lane], q = x[kXQ][lane], r = x[kXR][lane];
     a.fuel -= burn;
     a.pa[0] = alpha; a.pa[1] = mach; a.pa[2] = vc; a.pa[3] = vg;
