@@ -14,12 +14,19 @@
 #include <hip/hip_runtime.h>
 
 #include "f16_state.h"
+#include "fdm_math.h"
 
 #ifndef F16_HD
 #define F16_HD __host__ __device__ __forceinline__
 #endif
 
 namespace f16obs {
+
+using f16::fm_div;
+using f16::fm_exp;
+using f16::fm_log;
+using f16::fm_rcp;
+using f16::fm_sqrt;
 
 constexpr double kD2R = 3.141592653589793 / 180.0;
 constexpr double kR2D = 180.0 / 3.141592653589793;
@@ -44,7 +51,7 @@ constexpr int kAuxDim = 21;                         // future-aux features per e
 struct Origin { double ox, oy, oz, slat, clat, slon, clon, b, ep2; };
 
 F16_HD double clampd(double x, double lo, double hi) { return x < lo ? lo : (x > hi ? hi : x); }
-F16_HD double norm3(const double v[3]) { return sqrt(v[0] * v[0] + v[1] * v[1] + v[2] * v[2]); }
+F16_HD double norm3(const double v[3]) { return fm_sqrt(v[0] * v[0] + v[1] * v[1] + v[2] * v[2]); }
 F16_HD void mv3(const double A[3][3], const double v[3], double o[3]) {
   const double a = A[0][0] * v[0] + A[0][1] * v[1] + A[0][2] * v[2];
   const double b = A[1][0] * v[0] + A[1][1] * v[1] + A[1][2] * v[2];
@@ -76,8 +83,8 @@ F16_HD void att_from_trig(Att& A) {
 
 // sin and cos of atan2(y, x) without the angle (atan2(0, 0) = 0)
 F16_HD void sc_atan2(double y, double x, double& s, double& c) {
-  const double h = sqrt(x * x + y * y);
-  if (h > 0.0) { s = y / h; c = x / h; } else { s = 0.0; c = 1.0; }
+  const double h = fm_sqrt(x * x + y * y);
+  if (h > 0.0) { const double ih = fm_rcp(h); s = y * ih; c = x * ih; } else { s = 0.0; c = 1.0; }
 }
 
 // 101-double state (field k at st[k*ld]) -> N/E/D m (D = -MSL), roll/pitch/yaw deg, body u/v/w
@@ -95,8 +102,9 @@ F16_HD void state9(const double* st, long ld, const Origin& O, double s9[9], Att
   sincos(epa, &se, &ce);
   const double ex = ce * px + se * py, ey = -se * px + ce * py, ez = pz;
   const double rxy2 = ex * ex + ey * ey;
-  const double radius = sqrt(rxy2 + ez * ez), rxy = sqrt(rxy2);
-  const double sLat = ez / radius, cLat = rxy / radius, sLon = ey / rxy, cLon = ex / rxy;
+  const double radius = fm_sqrt(rxy2 + ez * ez), rxy = fm_sqrt(rxy2);
+  const double ir = fm_rcp(radius), irxy = fm_rcp(rxy);
+  const double sLat = ez * ir, cLat = rxy * ir, sLon = ey * irxy, cLon = ex * irxy;
   // local N/E/D axes in ECI (columns of Tl2i)
   const double n0 = -cLon * sLat, n1 = -sLon * sLat, d0 = -cLon * cLat, d1 = -sLon * cLat;
   const double N[3] = {ce * n0 - se * n1, se * n0 + ce * n1, cLat};
@@ -119,7 +127,7 @@ F16_HD void state9(const double* st, long ld, const Origin& O, double s9[9], Att
   psi = psi < 0.0 ? psi + 2.0 * 3.141592653589793 : psi;
   if (att) {
     att->sp = sp;
-    att->cp = sqrt((1.0 - sp) * (1.0 + sp));
+    att->cp = fm_sqrt((1.0 - sp) * (1.0 + sp));
     sc_atan2(L12, L22, att->sr, att->cr);
     sc_atan2(L01, L00, att->sy, att->cy);
     att_from_trig(*att);
@@ -131,12 +139,12 @@ F16_HD void state9(const double* st, long ld, const Origin& O, double s9[9], Att
   // Bowring ECEF -> geodetic latitude / longitude, then back to ECEF at MSL altitude
   const double exm = ex * kFt2M, eym = ey * kFt2M, ezm = ez * kFt2M;
   const double b = O.b, ep2 = O.ep2;
-  const double p = sqrt(exm * exm + eym * eym);
+  const double p = fm_sqrt(exm * exm + eym * eym);
   double sth, cth, slat, clat, slon, clon;
   sc_atan2(ezm * kWgsA, p * b, sth, cth);
   sc_atan2(ezm + ep2 * b * (sth * sth * sth), p - kWgsE2 * kWgsA * (cth * cth * cth), slat, clat);
   sc_atan2(eym, exm, slon, clon);
-  const double Nr = kWgsA / sqrt(1.0 - kWgsE2 * slat * slat);
+  const double Nr = fm_div(kWgsA, fm_sqrt(1.0 - kWgsE2 * slat * slat));
   const double dx = (Nr + alt_m) * clat * clon - O.ox, dy = (Nr + alt_m) * clat * slon - O.oy;
   const double dz = (Nr * (1.0 - kWgsE2) + alt_m) * slat - O.oz;
   s9[0] = -O.slat * O.clon * dx - O.slat * O.slon * dy + O.clat * dz;
@@ -156,7 +164,7 @@ F16_HD void attitude(const double s9[9], Att& A) {
 
 F16_HD void unit_or_self(const double v[3], double o[3]) {
   const double n = norm3(v);
-  if (n > 0.0) { o[0] = v[0] / n; o[1] = v[1] / n; o[2] = v[2] / n; }
+  if (n > 0.0) { const double in = fm_rcp(n); o[0] = v[0] * in; o[1] = v[1] * in; o[2] = v[2] * in; }
   else { o[0] = v[0]; o[1] = v[1]; o[2] = v[2]; }
 }
 
@@ -175,7 +183,8 @@ F16_HD void dir_frame(const double x[3], double F[3][3]) {
   const double nx = norm3(x);
   const bool ok = nx >= 1e-8;
   const double nxs = ok ? nx : 1.0;
-  const double xn[3] = {x[0] / nxs, x[1] / nxs, x[2] / nxs};
+  const double inx = fm_rcp(nxs);
+  const double xn[3] = {x[0] * inx, x[1] * inx, x[2] * inx};
   // projections of down, north, east off x; the first with norm >= 1e-6 is used
   const double zd[3] = {-xn[2] * xn[0], -xn[2] * xn[1], 1.0 - xn[2] * xn[2]};
   const double zn[3] = {1.0 - xn[0] * xn[0], -xn[0] * xn[1], -xn[0] * xn[2]};
@@ -185,13 +194,13 @@ F16_HD void dir_frame(const double x[3], double F[3][3]) {
 #pragma unroll
   for (int i = 0; i < 3; ++i) z[i] = use_d ? zd[i] : (use_n ? zn[i] : ze[i]);
   double n = norm3(z);
-  n = n > 1e-300 ? n : 1e-300;
-  z[0] /= n; z[1] /= n; z[2] /= n;
+  n = fm_rcp(n > 1e-300 ? n : 1e-300);
+  z[0] *= n; z[1] *= n; z[2] *= n;
   double y[3];
   cross3(z, xn, y);
   n = norm3(y);
-  n = n > 1e-300 ? n : 1e-300;
-  y[0] /= n; y[1] /= n; y[2] /= n;
+  n = fm_rcp(n > 1e-300 ? n : 1e-300);
+  y[0] *= n; y[1] *= n; y[2] *= n;
   cross3(xn, y, z);
 #pragma unroll
   for (int i = 0; i < 3; ++i) {
@@ -209,23 +218,23 @@ F16_HD double normz(double x, double lo, double hi) {
 // three-tier cone damage rate, tier 1 first (obs_reward.py:206-218)
 F16_HD double damage_rate(double r_ft, double ata, double t) {
   const double a = fabs(ata);
-  if (r_ft >= 500.0 && r_ft <= 3000.0 && a < 1.0) return 1.0 * (3000.0 - r_ft) / (3000.0 - 500.0);
-  if (t >= 100.0 && r_ft >= 500.0 && r_ft <= 3500.0 && a < 2.0) return 0.3 * (3500.0 - r_ft) / (3500.0 - 500.0);
-  if (t >= 150.0 && r_ft >= 500.0 && r_ft <= 4000.0 && a < 3.0) return 0.1 * (4000.0 - r_ft) / (4000.0 - 500.0);
+  if (r_ft >= 500.0 && r_ft <= 3000.0 && a < 1.0) return 1.0 * (3000.0 - r_ft) * (1.0 / (3000.0 - 500.0));
+  if (t >= 100.0 && r_ft >= 500.0 && r_ft <= 3500.0 && a < 2.0) return 0.3 * (3500.0 - r_ft) * (1.0 / (3500.0 - 500.0));
+  if (t >= 150.0 && r_ft >= 500.0 && r_ft <= 4000.0 && a < 3.0) return 0.1 * (4000.0 - r_ft) * (1.0 / (4000.0 - 500.0));
   return 0.0;
 }
 
 F16_HD double smoothstep(double x, double e0, double e1) {
-  const double z = clampd((x - e0) / (e1 - e0), 0.0, 1.0);
+  const double z = clampd((x - e0) * (1.0 / (e1 - e0)), 0.0, 1.0);   // e0, e1: literals
   return z * z * (3.0 - 2.0 * z);
 }
 
 F16_HD void unit_fallback(const double v[3], const double fb[3], double o[3]) {
   const double n = norm3(v);
-  if (n >= 1e-9) { o[0] = v[0] / n; o[1] = v[1] / n; o[2] = v[2] / n; return; }
+  if (n >= 1e-9) { const double in = fm_rcp(n); o[0] = v[0] * in; o[1] = v[1] * in; o[2] = v[2] * in; return; }
   double fn = norm3(fb);
-  fn = fn > 1e-9 ? fn : 1e-9;
-  o[0] = fb[0] / fn; o[1] = fb[1] / fn; o[2] = fb[2] / fn;
+  fn = fm_rcp(fn > 1e-9 ? fn : 1e-9);
+  o[0] = fb[0] * fn; o[1] = fb[1] * fn; o[2] = fb[2] * fn;
 }
 
 F16_HD double align3(const double a[3], const double b[3]) {
@@ -243,12 +252,12 @@ F16_HD double final_safe_side(const double own[9], const double R[3][3], const d
                               const double tgt[9], const double tgt_v[3], double ata, double t) {
   const double ex[3] = {1.0, 0.0, 0.0};
   const double rel[3] = {tgt[0] - own[0], tgt[1] - own[1], tgt[2] - own[2]};
-  const double dist_m = norm3(rel), dist_ft = dist_m / kFt2M;
+  const double dist_m = norm3(rel), dist_ft = dist_m * (1.0 / kFt2M);
   double los[3];
   unit_fallback(rel, ex, los);
   const double fwd[3] = {R[0][0], R[0][1], R[0][2]};
   double spd = norm3(own_v);
-  const double tau = clampd(dist_m / (spd < 30.0 ? 30.0 : spd), 0.30, 1.50);
+  const double tau = clampd(fm_div(dist_m, spd < 30.0 ? 30.0 : spd), 0.30, 1.50);
   const double lv[3] = {tgt[0] + tgt_v[0] * tau - own[0], tgt[1] + tgt_v[1] * tau - own[1],
                         tgt[2] + tgt_v[2] * tau - own[2]};
   double lead[3], path[3];
@@ -259,22 +268,22 @@ F16_HD double final_safe_side(const double own[9], const double R[3][3], const d
   const double ss_ata = smoothstep(ata, 3.0, 8.0);
   const double w = smoothstep(dist_ft, 1000.0, 2500.0) * ss_ata;
   const double safe_lead = w * intercept + (1.0 - w) * direct;
-  const double broad = ata <= 30.0 ? 1.0 : clampd((180.0 - ata) / (180.0 - 30.0), 0.0, 1.0);
+  const double broad = ata <= 30.0 ? 1.0 : clampd((180.0 - ata) * (1.0 / (180.0 - 30.0)), 0.0, 1.0);
   const double range_gate = smoothstep(dist_ft, 600.0, 900.0) * (1.0 - smoothstep(dist_ft, 3200.0, 4300.0));
   const double closing = (own_v[0] - tgt_v[0]) * los[0] + (own_v[1] - tgt_v[1]) * los[1] +
                          (own_v[2] - tgt_v[2]) * los[2];
   const double mean_speed = 0.5 * (spd + norm3(tgt_v));
-  const double cr = closing / (mean_speed > 100.0 ? mean_speed : 100.0);
+  const double cr = fm_div(closing, mean_speed > 100.0 ? mean_speed : 100.0);
   const double desired = 0.20 * smoothstep(dist_ft, 2000.0, 4500.0) + (-0.12) * (1.0 - smoothstep(dist_ft, 650.0, 900.0));
-  const double zq = (cr - desired) / 0.15;
-  const double control = clampd((1.0 - ss_ata) * range_gate * exp(-0.5 * (zq * zq)), 0.0, 1.0);
+  const double zq = (cr - desired) * (1.0 / 0.15);
+  const double control = clampd((1.0 - ss_ata) * range_gate * fm_exp(-0.5 * (zq * zq)), 0.0, 1.0);
   const double fine = damage_rate(dist_ft, ata, t);
   return clampd(0.50 * broad + 0.20 * safe_lead + 0.20 * control + 0.10 * fine, 0.0, 1.0);
 }
 
 F16_HD double altitude_log(double alt_m) {
-  const double x = alt_m / kAltLogScale;
-  return log(x < kAltLogFloor ? kAltLogFloor : x);
+  const double x = alt_m * (1.0 / kAltLogScale);
+  return fm_log(x < kAltLogFloor ? kAltLogFloor : x);
 }
 
 // body rates from two attitudes: log_SO3(R_prev R_curr^T) / dt (obs_reward.py:169-186, 601-606)
@@ -285,10 +294,10 @@ F16_HD void so3_rates(const double Rp[3][3], const double Rc[3][3], double out[3
   const double tr = M[0][0] + M[1][1] + M[2][2];
   const double theta = acos(clampd((tr - 1.0) * 0.5, -1.0, 1.0));
   const double denom = 2.0 * sin(theta);
-  const double scale = (theta >= 1e-8 && fabs(denom) >= 1e-8) ? theta / denom : 0.0;
-  out[0] = (M[2][1] - M[1][2]) * scale / kDtStep;
-  out[1] = (M[0][2] - M[2][0]) * scale / kDtStep;
-  out[2] = (M[1][0] - M[0][1]) * scale / kDtStep;
+  const double scale = (theta >= 1e-8 && fabs(denom) >= 1e-8) ? fm_div(theta, denom) : 0.0;
+  out[0] = (M[2][1] - M[1][2]) * scale * (1.0 / kDtStep);
+  out[1] = (M[0][2] - M[2][0]) * scale * (1.0 / kDtStep);
+  out[2] = (M[1][0] - M[0][1]) * scale * (1.0 / kDtStep);
 }
 
 F16_HD float obs_value(double v) {

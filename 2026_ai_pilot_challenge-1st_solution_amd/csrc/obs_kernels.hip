@@ -180,7 +180,7 @@ __device__ __forceinline__ AdvOut lane_advance(const Kin9& k, const Peer& p, con
   const double hp_loss = hp_before - hp;
   r.hp_loss[a] = hp_loss;
   r.hp[a] = hp;
-  const double burn = kFuelBurn * (k.spd / kFuelRef);
+  const double burn = kFuelBurn * (k.spd * (1.0 / kFuelRef));
   double fuel = fuel_before - burn * kDtStep;
   fuel = fuel < 0.0 ? 0.0 : fuel;
   r.fuel[a] = fuel;
@@ -200,7 +200,7 @@ __device__ __forceinline__ AdvOut lane_advance(const Kin9& k, const Peer& p, con
   if (r.accel) {   // 214-D lineage: NED acceleration from the velocity difference
 #pragma unroll
     for (int i = 0; i < 3; ++i) {
-      if (prev_valid) acc[i] = (k.vn[i] - pvel[i]) / kDtStep;
+      if (prev_valid) acc[i] = (k.vn[i] - pvel[i]) * (1.0 / kDtStep);
       r.accel[i * ld + a] = acc[i];
       r.prev_vel_ned[i * ld + a] = k.vn[i];
     }
@@ -388,10 +388,11 @@ __device__ __forceinline__ void lane_build_obs(const Kin9& k, const Peer& p, con
   // ---- vector block, frame by frame
   double V[9][3];
   const bool los_ok = g.dist > 1e-6;
+  const double idist = fm_rcp(los_ok ? g.dist : 1.0);
 #pragma unroll
   for (int i = 0; i < 3; ++i) {
     V[0][i] = i == 2 ? 1.0 : 0.0;                                  // gravity direction
-    V[1][i] = los_ok ? g.delta[i] / g.dist : 0.0;                 // line of sight
+    V[1][i] = los_ok ? g.delta[i] * idist : 0.0;                  // line of sight
     V[2][i] = k.vn[i];
     V[3][i] = p.vn[i];
     V[4][i] = p.vn[i] - k.vn[i];
@@ -438,19 +439,19 @@ __device__ __forceinline__ void lane_build_obs(const Kin9& k, const Peer& p, con
   const double sgn = pt1 > 0.0 ? 1.0 : (pt1 < 0.0 ? -1.0 : (pt2 >= 0.0 ? 1.0 : -1.0));
   const double cb0 = clampd(g.b[0], -1.0, 1.0), cpb0 = clampd(-pb[0], -1.0, 1.0);
   const double cb2 = clampd(g.b[2], -1.0, 1.0);
-  const double s_ata = sqrt((1.0 - cb0) * (1.0 + cb0)), c_ata = cb0;
-  const double s_aa = sgn * sqrt((1.0 - cpb0) * (1.0 + cpb0)), c_aa = cpb0;
+  const double s_ata = fm_sqrt((1.0 - cb0) * (1.0 + cb0)), c_ata = cb0;
+  const double s_aa = sgn * fm_sqrt((1.0 - cpb0) * (1.0 + cpb0)), c_aa = cpb0;
   double s_az, c_az;
   sc_atan2(g.b[1], g.b[0], s_az, c_az);
-  const double s_el = -cb2, c_el = sqrt((1.0 - cb2) * (1.0 + cb2));
+  const double s_el = -cb2, c_el = fm_sqrt((1.0 - cb2) * (1.0 + cb2));
   const double u = k.s9[6], v = k.s9[7], w = k.s9[8];
   double aoa = 0.0, ss = 0.0;
   if (!(k.spd < 1.0)) {
     aoa = atan2(w, u) * kR2D;
-    ss = atan2(v, sqrt(u * u + w * w)) * kR2D;
+    ss = atan2(v, fm_sqrt(u * u + w * w)) * kR2D;
   }
-  const double e_adv = (own_alt + k.spd * k.spd / (2.0 * kGacc)) -
-                       (tgt_alt + p.spd * p.spd / (2.0 * kGacc));
+  const double e_adv = (own_alt + k.spd * k.spd * (1.0 / (2.0 * kGacc))) -
+                       (tgt_alt + p.spd * p.spd * (1.0 / (2.0 * kGacc)));
   const double t = own.t;
   const double cone = t >= 150.0 ? 3.0 : (t >= 100.0 ? 2.0 : 1.0);
   const double maxr_ft = t >= 150.0 ? 4000.0 : (t >= 100.0 ? 3500.0 : 3000.0);
@@ -458,34 +459,35 @@ __device__ __forceinline__ void lane_build_obs(const Kin9& k, const Peer& p, con
   const double min_r = 500.0 * kFt2M, max_r = maxr_ft * kFt2M;
   double span = max_r - min_r;
   span = span < 1e-6 ? 1e-6 : span;
-  double pf_ata = 1.0 - fabs(g.ata) / 30.0;
+  double pf_ata = 1.0 - fabs(g.ata) * (1.0 / 30.0);
   pf_ata = pf_ata < 0.0 ? 0.0 : pf_ata;
-  double pf_rng = 1.0 - g.dist / 3000.0;
+  double pf_rng = 1.0 - g.dist * (1.0 / 3000.0);
   pf_rng = pf_rng < 0.0 ? 0.0 : pf_rng;
   float sc[kVecCol0];
   int j = 0;
   sc[j++] = obs_value(normz(k.spd, 0.0, 600.0));
   sc[j++] = obs_value(normz(p.spd, 0.0, 600.0));
-  sc[j++] = obs_value(tanh_feat(aoa / 30.0));
-  sc[j++] = obs_value(tanh_feat(ss / 15.0));
-  sc[j++] = obs_value(tanh_feat((own_alt - kMinAltM) / 300.0));
+  sc[j++] = obs_value(tanh_feat(aoa * (1.0 / 30.0)));
+  sc[j++] = obs_value(tanh_feat(ss * (1.0 / 15.0)));
+  sc[j++] = obs_value(tanh_feat((own_alt - kMinAltM) * (1.0 / 300.0)));
   sc[j++] = obs_value(normz(-k.vn[2], -100.0, 100.0));
   sc[j++] = obs_value(normz(own.hp, 0.0, 1.0));
   sc[j++] = obs_value(normz(tgt.hp, 0.0, 1.0));
   sc[j++] = obs_value(own.hp - tgt.hp);
-  sc[j++] = obs_value(e_adv / (fabs(e_adv) + 5000.0));
+  sc[j++] = obs_value(fm_div(e_adv, fabs(e_adv) + 5000.0));
   sc[j++] = obs_value(normz(g.dist, 0.0, 2500.0));
   sc[j++] = obs_value(normz(closure, -1000.0, 1000.0));
   sc[j++] = obs_value(s_ata); sc[j++] = obs_value(c_ata);
   sc[j++] = obs_value(s_aa); sc[j++] = obs_value(c_aa);
   sc[j++] = obs_value(s_az); sc[j++] = obs_value(c_az);
   sc[j++] = obs_value(s_el); sc[j++] = obs_value(c_el);
-  sc[j++] = obs_value(2.0 * gauss_feat(g.ata / 3.0) - 1.0);
-  sc[j++] = obs_value(tanh_feat((cone - fabs(g.ata)) / cc));
-  sc[j++] = obs_value(2.0 * gauss_feat(en_ata / 3.0) - 1.0);
-  sc[j++] = obs_value(tanh_feat((cone - fabs(en_ata)) / cc));
-  sc[j++] = obs_value(tanh_feat((g.dist - min_r) / span));
-  sc[j++] = obs_value(tanh_feat((max_r - g.dist) / span));
+  const double icc = fm_rcp(cc), ispan = fm_rcp(span);
+  sc[j++] = obs_value(2.0 * gauss_feat(g.ata * (1.0 / 3.0)) - 1.0);
+  sc[j++] = obs_value(tanh_feat((cone - fabs(g.ata)) * icc));
+  sc[j++] = obs_value(2.0 * gauss_feat(en_ata * (1.0 / 3.0)) - 1.0);
+  sc[j++] = obs_value(tanh_feat((cone - fabs(en_ata)) * icc));
+  sc[j++] = obs_value(tanh_feat((g.dist - min_r) * ispan));
+  sc[j++] = obs_value(tanh_feat((max_r - g.dist) * ispan));
   sc[j++] = obs_value(normz(t, 0.0, 200.0));
   sc[j++] = obs_value(k.A.sr); sc[j++] = obs_value(k.A.cr);
   sc[j++] = obs_value(k.A.sp); sc[j++] = obs_value(k.A.cp);
@@ -790,7 +792,7 @@ __global__ __launch_bounds__(kRowBlock) void env_post_step_kernel(const F16EnvSt
     if (io.terminal_hp) io.terminal_hp[a] = o.obs.hp;
     if (io.terminal_alt_m) {
       const double x = f15[0], y = f15[1], z = f15[2];
-      io.terminal_alt_m[a] = (sqrt(x * x + y * y + z * z) - kSeaLevelRadiusFtT) * kFt2M;
+      io.terminal_alt_m[a] = (fm_sqrt(x * x + y * y + z * z) - kSeaLevelRadiusFtT) * kFt2M;
     }
   }
   if (!io.terminal_obs) {
