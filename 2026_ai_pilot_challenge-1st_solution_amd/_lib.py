@@ -96,6 +96,7 @@ _SIGNATURES = {
     "f16_obr_init_reward": (_i, [_vp, _l, _vp, _RP, _vp]),
     "f16_obr_build_obs": (_i, [_vp, _l, _vp, _RP, _i, _vp, _vp]),
     "f16_env_post_step": (_i, [ctypes.POINTER(F16EnvStepIO), _RP, _CP, _vp]),
+    "f16_env_post_step_onewave": (_i, [ctypes.POINTER(F16EnvStepIO), _RP, _CP, _vp]),
     "f16_env_reseed": (_i, [ctypes.POINTER(F16EnvStepIO), _RP, _vp, _vp]),
     "f16_state9": (_i, [_vp, _l, _i, _vp, _vp]),
     "f16_future_labels": (_i, [_vp, _vp, _i, _i, _d, _vp, _vp, _vp]),

@@ -374,18 +374,18 @@ __device__ __forceinline__ void bank_of(const double R[3][3], const double F[3][
   sc_atan2(y2, y1, s, co);                   // sin, cos of atan2(y2, y1)
 }
 
-// One observation row (obs_reward.py:617-723; 214-D: cuda_fdm/external_observation.cu) to
-// `out`.  All lanes of a pair must call it together.
-// hist: 0 = read the action history from the reconstructor, 1 = already stored (by
-// lane_advance), 2 = all zero (a row after an autoreset).
+// The observation row (obs_reward.py:617-723; 214-D: cuda_fdm/external_observation.cu) in two
+// parts that read the same inputs: the vector block, columns [50, D - 20), into the tile, and
+// the scalar block [0, 50) with the action history.  All lanes of a pair call each part
+// together.  The scalar block needs the bank of the own and partner body y axes about their
+// motion frames; the vector block forms the own motion frame anyway and hands them over in
+// `bank` (bs, bc, tbs, tbc) when given one.
 template <int D, bool FULL>
-__device__ __forceinline__ void lane_build_obs(const Kin9& k, const Peer& p, const Geo& g,
-                                               const ObsIn& own, long a, const F16Recon& r,
-                                               const ObsOut& out, int hist = 0) {
-  const long ld = r.ld;
+__device__ __forceinline__ void obs_vector_block(const Kin9& k, const Peer& p, const Geo& g,
+                                                 const ObsIn& own, const ObsOut& out,
+                                                 double* bank) {
   constexpr int nvec = D == 214 ? 9 : 7;
   float* o1 = out.tile;
-  // ---- vector block, frame by frame
   double V[9][3];
   const bool los_ok = g.dist > 1e-6;
   const double idist = fm_rcp(los_ok ? g.dist : 1.0);
@@ -407,21 +407,46 @@ __device__ __forceinline__ void lane_build_obs(const Kin9& k, const Peer& p, con
   }
   emit_frame<1, FULL>(o1, k.A.R, V, nvec);
   emit_frame<2, FULL>(o1, p.R, V, nvec);
-  double bs, bc, tbs, tbc;
-  {
-    double Fm[3][3];
-    dir_frame(k.vn, Fm);                                           // own motion frame
-    bank_of(k.A.R, Fm, bs, bc);
-    emit_frame<3, FULL>(o1, Fm, V, nvec);
-    tbs = xch(bs); tbc = xch(bc);
-#pragma unroll
-    for (int i = 0; i < 3; ++i)
-#pragma unroll
-      for (int q = 0; q < 3; ++q) Fm[i][q] = xch(Fm[i][q]);           // partner's motion frame
-    emit_frame<4, FULL>(o1, Fm, V, nvec);
-    dir_frame(g.delta, Fm);                                        // line-of-sight frame
-    emit_frame<5, FULL>(o1, Fm, V, nvec);
+  double Fm[3][3];
+  dir_frame(k.vn, Fm);                                             // own motion frame
+  if (bank) {
+    bank_of(k.A.R, Fm, bank[0], bank[1]);
+    bank[2] = xch(bank[0]); bank[3] = xch(bank[1]);
   }
+  emit_frame<3, FULL>(o1, Fm, V, nvec);
+#pragma unroll
+  for (int i = 0; i < 3; ++i)
+#pragma unroll
+    for (int q = 0; q < 3; ++q) Fm[i][q] = xch(Fm[i][q]);             // partner's motion frame
+  emit_frame<4, FULL>(o1, Fm, V, nvec);
+  dir_frame(g.delta, Fm);                                          // line-of-sight frame
+  emit_frame<5, FULL>(o1, Fm, V, nvec);
+}
+
+// hist: 0 = read the action history from the reconstructor, 1 = already stored (by
+// lane_advance), 2 = all zero (a row after an autoreset).  `bank`: the vector block's bank
+// values, or null to form them here.
+template <int D, bool FULL>
+__device__ __forceinline__ void obs_scalar_block(const Kin9& k, const Peer& p, const Geo& g,
+                                                 const ObsIn& own, long a, const F16Recon& r,
+                                                 const ObsOut& out, int hist,
+                                                 const double* bank) {
+  const long ld = r.ld;
+  constexpr int nvec = D == 214 ? 9 : 7;
+  double bs, bc, tbs, tbc;
+  if (bank) {
+    bs = bank[0]; bc = bank[1]; tbs = bank[2]; tbc = bank[3];
+  } else {
+    double Fm[3][3];
+    dir_frame(k.vn, Fm);
+    bank_of(k.A.R, Fm, bs, bc);
+    tbs = xch(bs); tbc = xch(bc);
+  }
+  const bool los_ok = g.dist > 1e-6;
+  const double idist = fm_rcp(los_ok ? g.dist : 1.0);
+  double V1[3];
+#pragma unroll
+  for (int i = 0; i < 3; ++i) V1[i] = los_ok ? g.delta[i] * idist : 0.0;
   // ---- scalars [0, 50)
   ObsIn tgt;
   tgt.hp = xch(own.hp); tgt.fuel = xch(own.fuel);
@@ -430,8 +455,8 @@ __device__ __forceinline__ void lane_build_obs(const Kin9& k, const Peer& p, con
   for (int i = 0; i < 3; ++i) pb[i] = xch(g.b[i]);
   const double en_ata = xch(g.ata);
   const double own_alt = -k.s9[2], tgt_alt = -p.s9[2];
-  const double closure = (k.vn[0] - p.vn[0]) * V[1][0] + (k.vn[1] - p.vn[1]) * V[1][1] +
-                         (k.vn[2] - p.vn[2]) * V[1][2];
+  const double closure = (k.vn[0] - p.vn[0]) * V1[0] + (k.vn[1] - p.vn[1]) * V1[1] +
+                         (k.vn[2] - p.vn[2]) * V1[2];
   // sines and cosines of the line-of-sight angles straight from the unit vectors they are
   // acos'd/atan2'd/asin'd from: ATA = acos(b0); aspect = +-acos(-pb0), signed by the partner's
   // body y; azimuth = atan2(b1, b0); elevation = -asin(b2)
@@ -513,27 +538,38 @@ __device__ __forceinline__ void lane_build_obs(const Kin9& k, const Peer& p, con
   }
 }
 
+// One observation row to `out` (both blocks).  All lanes of a pair must call it together.
+template <int D, bool FULL>
+__device__ __forceinline__ void lane_build_obs(const Kin9& k, const Peer& p, const Geo& g,
+                                               const ObsIn& own, long a, const F16Recon& r,
+                                               const ObsOut& out, int hist = 0) {
+  double bank[4];
+  obs_vector_block<D, FULL>(k, p, g, own, out, bank);
+  obs_scalar_block<D, FULL>(k, p, g, own, a, r, out, hist, bank);
+}
+
 // Copy the staged tile rows [0, n) out: the tile is walked as a flat array of n * Wt floats
 // (Wt = D for FULL, D - 70 for the vector block), each lane moving W consecutive floats of one
 // row per step (W = 4 for FULL 184-D, whose rows are 16-byte aligned, else 2), so every store
 // instruction covers 64 * W consecutive floats of the destination (rows a0.. are contiguous
 // there when FULL; the vector-block segments are when !FULL).  Rows go to out1 where bit `row`
 // of m1 is set and to out2 where bit `row` of m2 is set (wave-uniform masks; out2 may be null).
-// Four steps' LDS reads are issued before their stores.
-template <int D, bool FULL>
+// Four steps' LDS reads are issued before their stores.  NT threads (tid = 0..NT-1) share the
+// copy.
+template <int D, bool FULL, int NT = kRowBlock>
 __device__ __forceinline__ void flush_tile(const float* S, long a0, int n, uint64_t m1,
                                            float* __restrict__ out1, uint64_t m2,
-                                           float* __restrict__ out2, int lane) {
+                                           float* __restrict__ out2, int tid) {
   constexpr int Wt = FULL ? D : D - 70, P = tile_pitch<D, FULL>(), C0 = tile_col0<FULL>();
   constexpr int W = (FULL && D % 4 == 0) ? 4 : 2;
   if (!out2) m2 = 0;
   const int total = n * Wt;
-  for (int f0 = 0; f0 < total; f0 += 4 * 64 * W) {
+  for (int f0 = 0; f0 < total; f0 += 4 * NT * W) {
     float v[4][W];
     int fl[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const int f = f0 + (u * 64 + lane) * W;
+      const int f = f0 + (u * NT + tid) * W;
       fl[u] = f;
       const int row = f / Wt, col = f - row * Wt;
       const float* src = S + (row < kRowBlock ? row : 0) * P + col;
@@ -841,6 +877,144 @@ __global__ __launch_bounds__(kRowBlock) void env_post_step_kernel(const F16EnvSt
   flush_sparse<D, FULL>(S, a0, fresh, io.obs, lane);
 }
 
+// env_post_step with each group of 64 aircraft spread over two wavefronts of one workgroup, so
+// a 16k-engagement step fills every SIMD instead of half of them.  Wave 0 (advance role) makes
+// the reward, termination and reconstructor update, the row's scalar block and action history,
+// the aux features and the autoreset rows; wave 1 (vector role) builds the vector block, the
+// larger share of a row's arithmetic.  Both evaluate the kinematics and pair geometry (a few
+// percent of the work) rather than trade them.  The vector role needs the body rates (and,
+// 214-D, the NED acceleration) that the reconstructor update produces: it forms them from the
+// previous attitude and velocity, read before the first barrier (after it the advance role
+// overwrites them), with lane_advance's expressions, so they are bit-identical.  Rows of
+// finished engagements are rebuilt from their autoreset state by the advance role after the
+// flush, as the single-wave kernel's terminal path does; without terminal_obs their first
+// build is not stored.  Results equal env_post_step_kernel's bit for bit.
+template <int D, bool FULL>
+__global__ __launch_bounds__(2 * kRowBlock) void env_post_step_split_kernel(
+    const F16EnvStepIO io, F16Recon r, F16RewardCfg c, Origin O) {
+  __shared__ float S[kRowBlock * tile_pitch<D, FULL>()];
+  __shared__ uint64_t sh_mask[2];   // live and finished rows, from the advance role
+  const int lane = threadIdx.x & 63;
+  const int role = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const long a0 = (long)blockIdx.x * kRowBlock, a = a0 + lane;
+  const long nac = 2L * r.nenv;
+  const int n = (int)min((long)kRowBlock, nac - a0);
+  const bool on = a < nac;                              // nac is even: pairs agree
+  const long e = a >> 1;
+  const int odd = (int)(a & 1);
+  const double* __restrict__ st = io.states;
+  const long ld = io.ld;
+  constexpr int kHistCol = vec_base(D == 214 ? 9 : 7);
+  float* tile = S + lane * tile_pitch<D, FULL>();
+  float* const first_out = io.terminal_obs ? io.terminal_obs : io.obs;
+  Kin9 k;
+  Peer p;
+  Geo g;
+  double f15[15];
+  if (role == 0) {
+    bool d = false;
+    if (on) {
+#pragma unroll
+      for (int f = 0; f < 15; ++f) f15[f] = st[f * ld + a];
+      if (io.terminal_finite || io.finite_acc) {   // rl_env.py:545: every state value finite
+        int fin = 1;
+#pragma unroll
+        for (int f = 0; f < 15; ++f) fin &= isfinite(f15[f]) ? 1 : 0;
+        double v[F16S_N - 15];
+#pragma unroll
+        for (int j = 0; j < F16S_N - 15; ++j) v[j] = st[(15 + j) * ld + a];
+#pragma unroll
+        for (int j = 0; j < F16S_N - 15; ++j) fin &= isfinite(v[j]) ? 1 : 0;
+        fin &= xchi(fin);
+        if (!odd) {
+          if (io.terminal_finite) io.terminal_finite[e] = (unsigned char)fin;
+          if (io.finite_acc && !fin) io.finite_acc[e] = 0;
+        }
+      }
+      make_kin(f15, 1, O, k);
+      exchange(k, p);
+      pair_geo(k, p, g);
+    }
+    __syncthreads();   // the vector role has read the previous attitude and velocity
+    if (on) {
+      const AdvOut o = lane_advance(k, p, g, a, e, io.actions, r, c, f15[F16S_FUEL]);
+      if (io.reward) io.reward[a] = o.reward;
+      if (io.reward_f32) io.reward_f32[a] = (float)o.reward;
+      d = o.term || o.trunc;
+      if (!odd) {
+        if (io.term) io.term[e] = o.term;
+        if (io.trunc) io.trunc[e] = o.trunc;
+        if (io.done) io.done[e] = d;
+        if (io.done_f32) io.done_f32[e] = d ? 1.0f : 0.0f;
+      }
+      if (io.terminal_hp) io.terminal_hp[a] = o.obs.hp;
+      if (io.terminal_alt_m) {
+        const double x = f15[0], y = f15[1], z = f15[2];
+        io.terminal_alt_m[a] = (fm_sqrt(x * x + y * y + z * z) - kSeaLevelRadiusFtT) * kFt2M;
+      }
+      const ObsOut out{tile, first_out + a * D,
+                       (io.terminal_obs && !d) ? io.obs + a * D : nullptr};
+      store_run2<D, FULL, kHistCol, kActHist>(out, o.hist);
+      obs_scalar_block<D, FULL>(k, p, g, o.obs, a, r, out, 1, nullptr);
+      if (!d) store_aux(k, p, r, a);
+    }
+    const uint64_t live = __ballot(on && !d), fresh = __ballot(on && d);
+    if (lane == 0) { sh_mask[0] = live; sh_mask[1] = fresh; }
+  } else {
+    bool prev_valid = false;
+    double patt[3] = {0.0, 0.0, 0.0}, pvel[3] = {0.0, 0.0, 0.0};
+    if (on) {
+#pragma unroll
+      for (int f = 0; f < 15; ++f) f15[f] = st[f * ld + a];
+      make_kin(f15, 1, O, k);
+      exchange(k, p);
+      pair_geo(k, p, g);
+      prev_valid = r.prev_valid[a] != 0;
+#pragma unroll
+      for (int i = 0; i < 3; ++i) patt[i] = r.prev_att[i * r.ld + a];
+      if (r.accel) {
+#pragma unroll
+        for (int i = 0; i < 3; ++i) pvel[i] = r.prev_vel_ned[i * r.ld + a];
+      }
+    }
+    __syncthreads();   // the advance role may now update the reconstructor
+    if (on) {
+      ObsIn own = fresh_obs_in();   // only pqr and accel are read by the vector block
+      if (prev_valid) {             // lane_advance's body rates and acceleration
+        Att P;
+        attitude_rpy(patt[0], patt[1], patt[2], P);
+        so3_rates(P.R, k.A.R, own.pqr);
+      }
+      if (r.accel) {
+#pragma unroll
+        for (int i = 0; i < 3; ++i)
+          if (prev_valid) own.accel[i] = (k.vn[i] - pvel[i]) * (1.0 / kDtStep);
+      }
+      obs_vector_block<D, FULL>(k, p, g, own, ObsOut{tile, nullptr, nullptr}, nullptr);
+    }
+  }
+  __syncthreads();   // the tile holds every row; the masks are published
+  const uint64_t rows = __ballot(on), live = sh_mask[0], fresh = sh_mask[1];
+  if (io.terminal_obs)
+    flush_tile<D, FULL, 2 * kRowBlock>(S, a0, n, rows, io.terminal_obs, live, io.obs, threadIdx.x);
+  else
+    flush_tile<D, FULL, 2 * kRowBlock>(S, a0, n, live, io.obs, 0, nullptr, threadIdx.x);
+  if (!fresh) return;      // uniform over the workgroup: no autoreset among these rows
+  __syncthreads();
+  if (role == 0 && ((fresh >> lane) & 1)) {
+    const uint32_t step = io.step + (io.step_base ? *io.step_base : 0u);
+    Kin9 k2;
+    Peer p2;
+    Geo g2;
+    lane_autoreset(io, r, O, a, e, odd, step, k2, p2, g2);
+    lane_build_obs<D, FULL>(k2, p2, g2, fresh_obs_in(), a, r,
+                            ObsOut{tile, io.obs + a * D, nullptr}, 2);
+    store_aux(k2, p2, r, a);
+  }
+  __syncthreads();
+  if (role == 0) flush_sparse<D, FULL>(S, a0, fresh, io.obs, lane);
+}
+
 // Masked autoreset without a step: engagements with mask[e] != 0 get an initial-condition pool
 // row (io.pick or the in-kernel Philox draw), the reconstructor reset and the reward state
 // re-anchored -- the departure reseeding of the staggered warm-up (rl_env.py:386-434) on the
@@ -991,8 +1165,8 @@ extern "C" int f16_obr_build_obs(const double* states, long ld, const unsigned c
   return f16_last_error();
 }
 
-extern "C" int f16_env_post_step(const F16EnvStepIO* io, const F16Recon* rec,
-                                 const F16RewardCfg* cfg, void* stream) {
+static int post_step(const F16EnvStepIO* io, const F16Recon* rec, const F16RewardCfg* cfg,
+                     void* stream, bool split) {
   if (!io) return F16_EINVAL;
   if (io->obs_dim != 184 && io->obs_dim != 214) return F16_EINVAL;
   int rc = check_recon(rec, io->obs_dim == 214);
@@ -1009,8 +1183,14 @@ extern "C" int f16_env_post_step(const F16EnvStepIO* io, const F16Recon* rec,
   const bool full = full_tile_resident(rec->nenv, io->obs_dim);
   hipStream_t s = (hipStream_t)stream;
 #define F16_POST_STEP(D, FULL)                                                                  \
-  hipLaunchKernelGGL((env_post_step_kernel<D, FULL>), grid_rows(rec->nenv), dim3(kRowBlock), 0,  \
-                     s, *io, *rec, *cfg, origin())
+  do {                                                                                          \
+    if (split)                                                                                  \
+      hipLaunchKernelGGL((env_post_step_split_kernel<D, FULL>), grid_rows(rec->nenv),           \
+                         dim3(2 * kRowBlock), 0, s, *io, *rec, *cfg, origin());                 \
+    else                                                                                        \
+      hipLaunchKernelGGL((env_post_step_kernel<D, FULL>), grid_rows(rec->nenv), dim3(kRowBlock), \
+                         0, s, *io, *rec, *cfg, origin());                                      \
+  } while (0)
   if (io->obs_dim == 184) {
     if (full) F16_POST_STEP(184, true); else F16_POST_STEP(184, false);
   } else {
@@ -1018,6 +1198,16 @@ extern "C" int f16_env_post_step(const F16EnvStepIO* io, const F16Recon* rec,
   }
 #undef F16_POST_STEP
   return f16_last_error();
+}
+
+extern "C" int f16_env_post_step(const F16EnvStepIO* io, const F16Recon* rec,
+                                 const F16RewardCfg* cfg, void* stream) {
+  return post_step(io, rec, cfg, stream, true);
+}
+
+extern "C" int f16_env_post_step_onewave(const F16EnvStepIO* io, const F16Recon* rec,
+                                         const F16RewardCfg* cfg, void* stream) {
+  return post_step(io, rec, cfg, stream, false);
 }
 
 extern "C" int f16_env_reseed(const F16EnvStepIO* io, const F16Recon* rec,

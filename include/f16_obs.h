@@ -133,6 +133,12 @@ int f16_env_reseed(const F16EnvStepIO *io, const F16Recon *rec, const unsigned c
 int f16_env_post_step(const F16EnvStepIO *io, const F16Recon *rec, const F16RewardCfg *cfg,
                       void *stream);
 
+/* The same step with one wavefront per 64 aircraft instead of two (f16_env_post_step spreads
+ * each group's row build over an advance wave and a vector-block wave); results are identical
+ * bit for bit.  Kept as the cross-check of the two-wave kernel. */
+int f16_env_post_step_onewave(const F16EnvStepIO *io, const F16Recon *rec,
+                              const F16RewardCfg *cfg, void *stream);
+
 /* GpuDogfightVecEnv.state9_flat (cuda_fdm/rl_env.py:583-592 with kinematics_state and
  * ned_from_ecef_altasl, :88-163): per aircraft N, E, D [m] (D = -MSL altitude; N/E the tangent
  * plane about the official origin of the point at the aircraft's geodetic latitude/longitude),

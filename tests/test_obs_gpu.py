@@ -328,6 +328,70 @@ def test_env_post_step_matches_reference_sequence(gpu, orc, obs_dim, nenv):
     assert done_o.any() and (~done_o).any()
 
 
+@pytest.mark.parametrize("obs_dim,nenv,terminal", [
+    (184, 1024, True), (184, 1024, False), (214, 1024, True), (214, 1024, False),
+    (184, 26000, True), (184, 26000, False), (214, 17000, True)])
+def test_env_post_step_two_wave_equals_one_wave(gpu, obs_dim, nenv, terminal):
+    """f16_env_post_step (an advance wave and a vector-block wave per 64 aircraft) against
+    f16_env_post_step_onewave on identical inputs: every output, state row, reconstructor value
+    and aux feature bit for bit, with finished engagements (autoreset rows), with and without
+    terminal observations, with the full-row tile (1024) and the vector-block tile (26000 /
+    17000 engagements exceed what the full-row tile keeps resident)."""
+    ext = obs_dim == 214
+    sim = _random_states(gpu, nenv, 171)
+    pool = _random_states(gpu, 64, 172).states.reshape(64, 2, 101).contiguous()
+    obr = _obr(nenv, ext)
+    obr.enable_aux_capture()
+    _random_recon(gpu, obr, 173)
+    act = np.random.default_rng(174).uniform(-1, 1, (2 * nenv, 4))
+    sim.actions.copy_(torch.as_tensor(act, device=gpu))
+    pick = torch.as_tensor(np.random.default_rng(175).integers(0, 64, nenv), device=gpu)
+    L = import_pkg("_lib")
+    R = import_pkg("obs_reward")
+    c = R.reward_cfg_struct(R.MY_REWARD_CONFIG, 304.8, 200.0, 0, 5.0)
+    st0, rec0 = sim._state_soa.clone(), obr.clone_state()
+    n = 2 * nenv
+    results = []
+    for fn in ("f16_env_post_step_onewave", "f16_env_post_step"):
+        sim._state_soa.copy_(st0)
+        obr.restore(rec0)
+        out = {"obs": torch.full((n, obs_dim), -7.0, dtype=torch.float32, device=gpu),
+               "tobs": torch.full((n, obs_dim), -9.0, dtype=torch.float32, device=gpu),
+               "rew": torch.zeros(n, dtype=torch.float64, device=gpu),
+               "rew32": torch.zeros(n, dtype=torch.float32, device=gpu),
+               "thp": torch.zeros(n, dtype=torch.float64, device=gpu),
+               "talt": torch.zeros(n, dtype=torch.float64, device=gpu),
+               "dn32": torch.zeros(nenv, dtype=torch.float32, device=gpu),
+               "facc": torch.ones(nenv, dtype=torch.uint8, device=gpu)}
+        for k in ("te", "tr", "dn", "fin"):
+            out[k] = torch.zeros(nenv, dtype=torch.uint8, device=gpu)
+        rec = obr._recon()
+        io = L.F16EnvStepIO(states=sim._state_soa.data_ptr(), ld=sim.nac,
+                            actions=sim.actions.data_ptr(), ic_pool=pool.data_ptr(),
+                            pool_size=64, pick=pick.data_ptr(), obs_dim=obs_dim,
+                            obs=out["obs"].data_ptr(),
+                            terminal_obs=out["tobs"].data_ptr() if terminal else None,
+                            reward=out["rew"].data_ptr(), reward_f32=out["rew32"].data_ptr(),
+                            term=out["te"].data_ptr(), trunc=out["tr"].data_ptr(),
+                            done=out["dn"].data_ptr(), done_f32=out["dn32"].data_ptr(),
+                            terminal_hp=out["thp"].data_ptr(),
+                            terminal_alt_m=out["talt"].data_ptr(),
+                            terminal_finite=out["fin"].data_ptr(), finite_acc=out["facc"].data_ptr())
+        L.check(getattr(L.lib(), fn)(L.ctypes.byref(io), L.ctypes.byref(rec), L.ctypes.byref(c),
+                                     L.stream_handle(gpu)), fn)
+        torch.cuda.synchronize()
+        snap = {k: v.cpu().numpy() for k, v in out.items()}
+        snap["states"] = sim._state_soa.cpu().numpy()
+        snap.update({"recon_" + k: v.cpu().numpy() for k, v in obr.clone_state().items()})
+        results.append(snap)
+    one, two = results
+    assert one.keys() == two.keys()
+    for k in one:
+        np.testing.assert_array_equal(two[k], one[k], err_msg=k)
+    done = one["dn"].astype(bool)
+    assert done.any() and (~done).any()
+
+
 def test_env_post_step_bad_pick_poisons_state(gpu):
     """A pool index out of range never reads out of bounds: the engagement becomes NaN."""
     nenv = 4
