@@ -30,6 +30,9 @@ constexpr int kObsBlock = 256;
 // and go out from registers.  The tile is 29 KB (184-D) or 37 KB (214-D), so four wavefronts
 // fit a CU's LDS.
 constexpr int kRowBlock = 64;
+// The two-wave post-physics step runs two groups of 64 aircraft per workgroup.
+constexpr int kPostGroups = 2;
+constexpr int kPostSplitBlock = 2 * kRowBlock * kPostGroups;
 constexpr double kFuelBurn = 8.0e-5;          // fuel proxy burn per second at 300 m/s
 constexpr double kFuelRef = 300.0;
 constexpr double kSeaLevelRadiusFtT = 20925646.32546;
@@ -877,8 +880,9 @@ __global__ __launch_bounds__(kRowBlock) void env_post_step_kernel(const F16EnvSt
   flush_sparse<D, FULL>(S, a0, fresh, io.obs, lane);
 }
 
-// env_post_step with each group of 64 aircraft spread over two wavefronts of one workgroup, so
-// a 16k-engagement step fills every SIMD instead of half of them.  Wave 0 (advance role) makes
+// env_post_step with each group of 64 aircraft spread over two wavefronts, two groups per
+// 256-thread workgroup (the hardware then places its four wavefronts on the CU's four SIMDs),
+// so a 16k-engagement step fills every SIMD instead of half of them.  Wave 0 (advance role) makes
 // the reward, termination and reconstructor update, the row's scalar block and action history,
 // the aux features and the autoreset rows; wave 1 (vector role) builds the vector block, the
 // larger share of a row's arithmetic.  Both evaluate the kinematics and pair geometry (a few
@@ -890,15 +894,18 @@ __global__ __launch_bounds__(kRowBlock) void env_post_step_kernel(const F16EnvSt
 // flush, as the single-wave kernel's terminal path does; without terminal_obs their first
 // build is not stored.  Results equal env_post_step_kernel's bit for bit.
 template <int D, bool FULL>
-__global__ __launch_bounds__(2 * kRowBlock) void env_post_step_split_kernel(
+__global__ __launch_bounds__(kPostSplitBlock) void env_post_step_split_kernel(
     const F16EnvStepIO io, F16Recon r, F16RewardCfg c, Origin O) {
-  __shared__ float S[kRowBlock * tile_pitch<D, FULL>()];
-  __shared__ uint64_t sh_mask[2];   // live and finished rows, from the advance role
+  __shared__ float S_all[kPostGroups][kRowBlock * tile_pitch<D, FULL>()];
+  __shared__ uint64_t sh_mask[kPostGroups][2];   // live and finished rows, from the advance role
   const int lane = threadIdx.x & 63;
-  const int role = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-  const long a0 = (long)blockIdx.x * kRowBlock, a = a0 + lane;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int grp = wave >> 1, role = wave & 1;
+  const int gtid = (int)(threadIdx.x & (2 * kRowBlock - 1));   // thread index within the group
+  float* const S = S_all[grp];
+  const long a0 = ((long)blockIdx.x * kPostGroups + grp) * kRowBlock, a = a0 + lane;
   const long nac = 2L * r.nenv;
-  const int n = (int)min((long)kRowBlock, nac - a0);
+  const int n = (int)max(0L, min((long)kRowBlock, nac - a0));
   const bool on = a < nac;                              // nac is even: pairs agree
   const long e = a >> 1;
   const int odd = (int)(a & 1);
@@ -959,7 +966,7 @@ __global__ __launch_bounds__(2 * kRowBlock) void env_post_step_split_kernel(
       if (!d) store_aux(k, p, r, a);
     }
     const uint64_t live = __ballot(on && !d), fresh = __ballot(on && d);
-    if (lane == 0) { sh_mask[0] = live; sh_mask[1] = fresh; }
+    if (lane == 0) { sh_mask[grp][0] = live; sh_mask[grp][1] = fresh; }
   } else {
     bool prev_valid = false;
     double patt[3] = {0.0, 0.0, 0.0}, pvel[3] = {0.0, 0.0, 0.0};
@@ -994,12 +1001,15 @@ __global__ __launch_bounds__(2 * kRowBlock) void env_post_step_split_kernel(
     }
   }
   __syncthreads();   // the tile holds every row; the masks are published
-  const uint64_t rows = __ballot(on), live = sh_mask[0], fresh = sh_mask[1];
+  const uint64_t rows = __ballot(on), live = sh_mask[grp][0], fresh = sh_mask[grp][1];
   if (io.terminal_obs)
-    flush_tile<D, FULL, 2 * kRowBlock>(S, a0, n, rows, io.terminal_obs, live, io.obs, threadIdx.x);
+    flush_tile<D, FULL, 2 * kRowBlock>(S, a0, n, rows, io.terminal_obs, live, io.obs, gtid);
   else
-    flush_tile<D, FULL, 2 * kRowBlock>(S, a0, n, live, io.obs, 0, nullptr, threadIdx.x);
-  if (!fresh) return;      // uniform over the workgroup: no autoreset among these rows
+    flush_tile<D, FULL, 2 * kRowBlock>(S, a0, n, live, io.obs, 0, nullptr, gtid);
+  bool any_fresh = false;   // uniform over the workgroup, so every thread meets the same barriers
+#pragma unroll
+  for (int q = 0; q < kPostGroups; ++q) any_fresh |= sh_mask[q][1] != 0;
+  if (!any_fresh) return;
   __syncthreads();
   if (role == 0 && ((fresh >> lane) & 1)) {
     const uint32_t step = io.step + (io.step_base ? *io.step_base : 0u);
@@ -1083,10 +1093,10 @@ static bool rows_aligned(const float* p, int obs_dim) {
   return ((uintptr_t)p & (obs_dim % 4 == 0 ? 15u : 7u)) == 0;
 }
 
-// Whether a row launch over nenv engagements keeps every wavefront resident at once with the
+// Whether a row launch over nenv engagements keeps every workgroup resident at once with the
 // full-row tile (limited by LDS per CU); otherwise the vector-block tile is used, which lets
-// four wavefronts share a CU.
-static bool full_tile_resident(int nenv, int obs_dim) {
+// four wavefronts share a CU.  `groups`: 64-row tiles per workgroup.
+static bool full_tile_resident(int nenv, int obs_dim, int groups = 1) {
   static int cus = 0, lds = 0;
   if (cus == 0) {
     int dev = 0;
@@ -1096,9 +1106,10 @@ static bool full_tile_resident(int nenv, int obs_dim) {
     if (cus <= 0) cus = 256;
     if (lds <= 0) lds = 160 * 1024;
   }
-  const long waves = (2L * nenv + kRowBlock - 1) / kRowBlock;
-  const long tile = (long)kRowBlock * (obs_dim | 1) * (long)sizeof(float);
-  return waves <= (long)(lds / tile) * cus;
+  const long rows = (long)kRowBlock * groups;
+  const long blocks = (2L * nenv + rows - 1) / rows;
+  const long tile = rows * (obs_dim | 1) * (long)sizeof(float);
+  return blocks <= (long)(lds / tile) * cus;
 }
 
 static int check_cfg(const F16RewardCfg* c) {
@@ -1112,6 +1123,11 @@ static dim3 grid_for(int nenv) {
 
 static dim3 grid_rows(int nenv) {
   return dim3((unsigned)((2L * nenv + kRowBlock - 1) / kRowBlock));
+}
+
+static dim3 grid_groups(int nenv) {
+  constexpr long rows = (long)kRowBlock * kPostGroups;
+  return dim3((unsigned)((2L * nenv + rows - 1) / rows));
 }
 
 }  // namespace f16obs
@@ -1180,13 +1196,13 @@ static int post_step(const F16EnvStepIO* io, const F16Recon* rec, const F16Rewar
   if (!rows_aligned(io->obs, io->obs_dim) ||
       (io->terminal_obs && !rows_aligned(io->terminal_obs, io->obs_dim)))
     return F16_EINVAL;
-  const bool full = full_tile_resident(rec->nenv, io->obs_dim);
+  const bool full = full_tile_resident(rec->nenv, io->obs_dim, split ? kPostGroups : 1);
   hipStream_t s = (hipStream_t)stream;
 #define F16_POST_STEP(D, FULL)                                                                  \
   do {                                                                                          \
     if (split)                                                                                  \
-      hipLaunchKernelGGL((env_post_step_split_kernel<D, FULL>), grid_rows(rec->nenv),           \
-                         dim3(2 * kRowBlock), 0, s, *io, *rec, *cfg, origin());                 \
+      hipLaunchKernelGGL((env_post_step_split_kernel<D, FULL>), grid_groups(rec->nenv),         \
+                         dim3(kPostSplitBlock), 0, s, *io, *rec, *cfg, origin());               \
     else                                                                                        \
       hipLaunchKernelGGL((env_post_step_kernel<D, FULL>), grid_rows(rec->nenv), dim3(kRowBlock), \
                          0, s, *io, *rec, *cfg, origin());                                      \
