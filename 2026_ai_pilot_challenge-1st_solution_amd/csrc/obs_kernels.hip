@@ -600,16 +600,16 @@ __device__ __forceinline__ void flush_tile(const float* S, long a0, int n, uint6
 }
 
 // The same for a sparse set of rows (autoreset rows): one row at a time, set bits only.
-template <int D, bool FULL>
+template <int D, bool FULL, int NT = kRowBlock>
 __device__ __forceinline__ void flush_sparse(const float* S, long a0, uint64_t m,
-                                             float* __restrict__ out, int lane) {
+                                             float* __restrict__ out, int tid) {
   constexpr int Wt = FULL ? D : D - 70, P = tile_pitch<D, FULL>(), C0 = tile_col0<FULL>();
   while (m) {
     const int r = __builtin_ctzll(m);
     m &= m - 1;
     const float* src = S + r * P;
 #pragma unroll
-    for (int c = 2 * lane; c < Wt; c += 2 * kRowBlock)
+    for (int c = 2 * tid; c < Wt; c += 2 * NT)
       *reinterpret_cast<float2*>(out + (a0 + r) * D + C0 + c) = make_float2(src[c], src[c + 1]);
   }
 }
@@ -712,11 +712,9 @@ __global__ __launch_bounds__(kRowBlock) void build_obs_kernel(
 // rows copied in (NaN for a pick outside the pool), reconstructor reset, league opponent redraw,
 // and the new state's kinematics, partner exchange, geometry and re-anchored reward state.
 // Both lanes of an engagement call it together.
-__device__ __forceinline__ void lane_autoreset(const F16EnvStepIO& io, const F16Recon& r,
-                                               const Origin& O, long a, long e, int odd,
-                                               uint32_t step, Kin9& k2, Peer& p2, Geo& g2) {
-  double* __restrict__ st = io.states;
-  const long ld = io.ld;
+// The pool pair engagement e restarts from: io.pick[e], or floor(pool_size x0 / 2^32) of
+// Philox4x32-10 with key = seed and counter = (e, step, 0, 0x5EED5EED).  -1 when out of range.
+__device__ __forceinline__ long pool_pick(const F16EnvStepIO& io, long e, uint32_t step) {
   long pk;
   if (io.pick) {
     pk = io.pick[e];
@@ -725,7 +723,29 @@ __device__ __forceinline__ void lane_autoreset(const F16EnvStepIO& io, const F16
     f16rng::philox4x32_10(ctr, (uint32_t)io.seed, (uint32_t)(io.seed >> 32));
     pk = (long)(((uint64_t)ctr[0] * (uint64_t)io.pool_size) >> 32);
   }
-  const bool ok = pk >= 0 && pk < io.pool_size;
+  return (pk >= 0 && pk < io.pool_size) ? pk : -1;
+}
+
+// The kinematics of the pool row an autoreset copies in (NaN kinematics for a bad pick).
+__device__ __forceinline__ void pool_kin(const F16EnvStepIO& io, const Origin& O, long pk,
+                                         int odd, Kin9& k2) {
+  if (pk >= 0) {
+    make_kin(io.ic_pool + (pk * 2 + odd) * F16S_N, 1, O, k2);
+  } else {
+    const double qnan = __builtin_nan("");
+    const double nan14[14] = {qnan, qnan, qnan, qnan, qnan, qnan, qnan,
+                              qnan, qnan, qnan, qnan, qnan, qnan, qnan};   // fields 0..13
+    make_kin(nan14, 1, O, k2);
+  }
+}
+
+__device__ __forceinline__ void lane_autoreset(const F16EnvStepIO& io, const F16Recon& r,
+                                               const Origin& O, long a, long e, int odd,
+                                               uint32_t step, Kin9& k2, Peer& p2, Geo& g2) {
+  double* __restrict__ st = io.states;
+  const long ld = io.ld;
+  const long pk = pool_pick(io, e, step);
+  const bool ok = pk >= 0;
   const double* src = io.ic_pool + (ok ? pk * 2 + odd : 0) * F16S_N;
   const double qnan = __builtin_nan("");
   if (ok) {
@@ -753,13 +773,7 @@ __device__ __forceinline__ void lane_autoreset(const F16EnvStepIO& io, const F16
   }
   for (int i = 0; i < kActHist; ++i) r.act_hist[i * r.ld + a] = 0.0;
   if (!odd) r.t_sec[e] = 0.0;
-  if (ok) {
-    make_kin(src, 1, O, k2);
-  } else {
-    const double nan14[14] = {qnan, qnan, qnan, qnan, qnan, qnan, qnan,
-                              qnan, qnan, qnan, qnan, qnan, qnan, qnan};   // fields 0..13
-    make_kin(nan14, 1, O, k2);
-  }
+  pool_kin(io, O, pk, odd, k2);
   exchange(k2, p2);
   pair_geo(k2, p2, g2);
   lane_init_reward(k2, p2, g2, a, 0.0, r);
@@ -1011,18 +1025,29 @@ __global__ __launch_bounds__(kPostSplitBlock) void env_post_step_split_kernel(
   for (int q = 0; q < kPostGroups; ++q) any_fresh |= sh_mask[q][1] != 0;
   if (!any_fresh) return;
   __syncthreads();
-  if (role == 0 && ((fresh >> lane) & 1)) {
+  // Rows of finished engagements, again split: the advance role restarts them from the pool
+  // (state rows, reconstructor, reward anchor) and writes the scalar block; the vector role
+  // forms the same pool row's kinematics from the pool itself and writes the vector block.
+  if ((fresh >> lane) & 1) {
     const uint32_t step = io.step + (io.step_base ? *io.step_base : 0u);
     Kin9 k2;
     Peer p2;
     Geo g2;
-    lane_autoreset(io, r, O, a, e, odd, step, k2, p2, g2);
-    lane_build_obs<D, FULL>(k2, p2, g2, fresh_obs_in(), a, r,
-                            ObsOut{tile, io.obs + a * D, nullptr}, 2);
-    store_aux(k2, p2, r, a);
+    if (role == 0) {
+      lane_autoreset(io, r, O, a, e, odd, step, k2, p2, g2);
+      obs_scalar_block<D, FULL>(k2, p2, g2, fresh_obs_in(), a, r,
+                                ObsOut{tile, io.obs + a * D, nullptr}, 2, nullptr);
+      store_aux(k2, p2, r, a);
+    } else {
+      pool_kin(io, O, pool_pick(io, e, step), odd, k2);
+      exchange(k2, p2);
+      pair_geo(k2, p2, g2);
+      obs_vector_block<D, FULL>(k2, p2, g2, fresh_obs_in(), ObsOut{tile, nullptr, nullptr},
+                                nullptr);
+    }
   }
   __syncthreads();
-  if (role == 0) flush_sparse<D, FULL>(S, a0, fresh, io.obs, lane);
+  flush_sparse<D, FULL, 2 * kRowBlock>(S, a0, fresh, io.obs, gtid);
 }
 
 // Masked autoreset without a step: engagements with mask[e] != 0 get an initial-condition pool
