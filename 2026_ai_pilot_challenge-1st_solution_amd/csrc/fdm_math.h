@@ -11,7 +11,9 @@
 //   fm_div   a * fm_rcp(b), then one residual step q += r (a - b q)            (~0.5 ulp;
 //            identical to IEEE division on 1M random normal operands)
 //   fm_sqrt  Goldschmidt: g = x y, h = y / 2, one coupled step, then one residual step
-//            g += h (x - g g)                                                  (~0.5 ulp)
+//            g += h (x - g g)                       (~0.5 ulp for normal x; a subnormal x loses
+//            relative accuracy, to ~1e-14, as the residual g g underflows -- the model's square
+//            roots are of sums of squares of physical quantities, nowhere near that range)
 //   fm_exp   Cody-Waite reduction x = k ln2 + r, |r| <= ln2 / 2, Taylor series of degree 13
 //            (truncation < 5e-18 relative) evaluated by Estrin's scheme, scaled by 2^k
 //   fm_log   x = 2^k m, m in [sqrt(1/2), sqrt(2)); log m = 2 atanh(s), s = (m - 1) / (m + 1),
