@@ -56,8 +56,15 @@ enum SplitField : int {
   kXVg, kXP, kXQ, kXR,
   // X3, systems -> flight
   kXThrust, kXCe, kXSe,
-  kSplitFields
+  // the mass block again: substep t's mass properties live in block t & 1 (below)
+  kXMass2, kSplitFields = kXMass2 + (kXAil - kXMass)
 };
+
+// Mass properties are written by the systems wave in its first phase and read by the flight
+// wave in its second (CG) and fourth (forces, accelerations) phases; the next substep's first
+// phase overlaps this substep's fourth, so consecutive substeps use alternate blocks and the
+// flight wave does not hold the 19 values across its aero phases.
+__device__ __forceinline__ int mass_block(int t) { return (t & 1) ? kXMass2 - kXMass : 0; }
 
 typedef double SplitX[kSplitFields][64];
 
@@ -124,15 +131,13 @@ __device__ __forceinline__ void split_flight(double* __restrict__ s, long ld, in
     x[kXAlt][lane] = alt; x[kXCtcp][lane] = k.ctcp;
     __syncthreads();
     // ---- phase 2
-    Mass mb;
-    mb.mass = x[kXMass][lane];
-#pragma unroll
-    for (int j = 0; j < 6; ++j) { mb.J[j] = x[kXJ + j][lane]; mb.Jinv[j] = x[kXJinv + j][lane]; }
-#pragma unroll
-    for (int j = 0; j < 3; ++j) { mb.rp[j] = x[kXRp + j][lane]; mb.cg[j] = x[kXCg + j][lane]; }
+    const int mo = mass_block(t);
     g = aux_geometry(k.uvw);
     double npy, npz;
-    load_factors(a, mb.cg, npy, npz);
+    {
+      const double cg[3] = {x[mo + kXCg][lane], x[mo + kXCg + 1][lane], x[mo + kXCg + 2][lane]};
+      load_factors(a, cg, npy, npz);
+    }
     x[kXVt][lane] = g.vt; x[kXAlpha][lane] = g.alpha; x[kXBeta][lane] = g.beta;
     x[kXNpy][lane] = npy; x[kXNpz][lane] = npz;
     const double alpha = g.alpha, beta = g.beta;
@@ -179,6 +184,12 @@ __device__ __forceinline__ void split_flight(double* __restrict__ s, long ld, in
     __syncthreads();
     // ---- phase 4
     const double thrust = x[kXThrust][lane];
+    Mass mb;
+    mb.mass = x[mo + kXMass][lane];
+#pragma unroll
+    for (int j = 0; j < 6; ++j) { mb.J[j] = x[mo + kXJ + j][lane]; mb.Jinv[j] = x[mo + kXJinv + j][lane]; }
+#pragma unroll
+    for (int j = 0; j < 3; ++j) { mb.rp[j] = x[mo + kXRp + j][lane]; mb.cg[j] = x[mo + kXCg + j][lane]; }
     double Fb[3], Mb[3];
     forces_moments(ax, g, mb, thrust, Fb, Mb);
     Accel ac;
@@ -247,11 +258,12 @@ __device__ __forceinline__ void split_systems(double* __restrict__ s, long ld,
     FcsOut fc;
     const double esch = fcs_prev_frame<FCS_RATE>(a, c_ail, c_ele, c_rud, T, fc);
     k_rud = fc.k_rud;
-    x[kXMass][lane] = mb.mass;
+    const int mo = mass_block(t);
+    x[mo + kXMass][lane] = mb.mass;
 #pragma unroll
-    for (int j = 0; j < 6; ++j) { x[kXJ + j][lane] = mb.J[j]; x[kXJinv + j][lane] = mb.Jinv[j]; }
+    for (int j = 0; j < 6; ++j) { x[mo + kXJ + j][lane] = mb.J[j]; x[mo + kXJinv + j][lane] = mb.Jinv[j]; }
 #pragma unroll
-    for (int j = 0; j < 3; ++j) { x[kXRp + j][lane] = mb.rp[j]; x[kXCg + j][lane] = mb.cg[j]; }
+    for (int j = 0; j < 3; ++j) { x[mo + kXRp + j][lane] = mb.rp[j]; x[mo + kXCg + j][lane] = mb.cg[j]; }
     x[kXAil][lane] = fc.ail; x[kXRud][lane] = fc.rud; x[kXLef][lane] = fc.lef; x[kXFlap][lane] = fc.flap;
     __syncthreads();
     // ---- phase 2
