@@ -46,7 +46,8 @@ class F16EnvStepIO(ctypes.Structure):
                 ("reward", _vp), ("reward_f32", _vp), ("term", _vp), ("trunc", _vp),
                 ("done", _vp), ("done_f32", _vp), ("terminal_hp", _vp),
                 ("terminal_alt_m", _vp), ("terminal_finite", _vp), ("finite_acc", _vp),
-                ("opp_assign", _vp), ("opp_cdf", _vp), ("n_opp", _i), ("step_base", _vp)]
+                ("opp_assign", _vp), ("opp_cdf", _vp), ("n_opp", _i), ("step_base", _vp),
+                ("norm_partial", _vp), ("norm_count", _vp), ("norm_count_snap", _vp)]
 
 
 class F16PolicyGroup(ctypes.Structure):
@@ -97,6 +98,7 @@ _SIGNATURES = {
     "f16_obr_build_obs": (_i, [_vp, _l, _vp, _RP, _i, _vp, _vp]),
     "f16_env_post_step": (_i, [ctypes.POINTER(F16EnvStepIO), _RP, _CP, _vp]),
     "f16_env_post_step_onewave": (_i, [ctypes.POINTER(F16EnvStepIO), _RP, _CP, _vp]),
+    "f16_env_post_step_norm_fusable": (_i, [_i, _i]),
     "f16_env_reseed": (_i, [ctypes.POINTER(F16EnvStepIO), _RP, _vp, _vp]),
     "f16_state9": (_i, [_vp, _l, _i, _vp, _vp]),
     "f16_future_labels": (_i, [_vp, _vp, _i, _i, _d, _vp, _vp, _vp]),
@@ -106,6 +108,7 @@ _SIGNATURES = {
     "f16_group_rows": (_i, [_vp, _i, _i, _i, _i, _vp, _vp, _vp, _vp]),
     "f16_group_workspace_bytes": (_l, [_i]),
     "f16_norm_update": (_i, [_vp, _l, _vp, _i, _i, _vp, _vp, _vp, _vp, _vp]),
+    "f16_norm_merge": (_i, [_i, _i, _vp, _vp, _vp, _vp]),
     "f16_ppo_param_counts": (_i, [_i, ctypes.POINTER(_l)]),
     "f16_ppo_workspace_bytes": (_l, [_i, _i]),
     "f16_ppo_grad": (_i, [ctypes.POINTER(F16PPOArgs), _vp]),

@@ -894,6 +894,44 @@ __global__ __launch_bounds__(kRowBlock) void env_post_step_kernel(const F16EnvSt
   flush_sparse<D, FULL>(S, a0, fresh, io.obs, lane);
 }
 
+// RunningNorm partial sums of a workgroup's 128 new observation rows straight from the full-row
+// staging tiles, in norm_partial_kernel's order (policy_kernels.hip): block b = this workgroup,
+// four 32-row phases each summed row by row in fp64 (rows past the batch add 0), the phases
+// then added in order; block 0 also snapshots and advances the running count.  The results
+// equal a norm_partial_kernel launch over the same rows bit for bit.
+template <int D>
+__device__ __forceinline__ void norm_partials_from_tiles(const float* S_all, double* sh,
+                                                         long a_blk, long nac, long b,
+                                                         const F16EnvStepIO& io, int tid) {
+  constexpr int P = tile_pitch<D, true>(), kTile = kRowBlock * P;
+  for (int idx = tid; idx < 4 * D; idx += kPostSplitBlock) {
+    const int ph = idx / D, c = idx - ph * D;
+    const float* src = S_all + (ph >> 1) * kTile + ((ph & 1) * 32) * P + c;
+    const long r0 = a_blk + ph * 32;
+    double sum = 0.0, sq = 0.0;
+    for (int i = 0; i < 32; ++i) {
+      const double v = (r0 + i < nac) ? (double)src[i * P] : 0.0;
+      sum += v;
+      sq += v * v;
+    }
+    sh[(ph * 2) * D + c] = sum;
+    sh[(ph * 2 + 1) * D + c] = sq;
+  }
+  __syncthreads();
+  for (int c = tid; c < D; c += kPostSplitBlock) {
+    double sum = sh[c], sq = sh[D + c];
+#pragma unroll
+    for (int ph = 1; ph < 4; ++ph) { sum += sh[(ph * 2) * D + c]; sq += sh[(ph * 2 + 1) * D + c]; }
+    io.norm_partial[b * 2 * D + c] = sum;
+    io.norm_partial[b * 2 * D + D + c] = sq;
+  }
+  if (b == 0 && tid == 0) {
+    const float cnt = *io.norm_count;
+    *io.norm_count_snap = cnt;
+    *io.norm_count = cnt + (float)nac;
+  }
+}
+
 // env_post_step with each group of 64 aircraft spread over two wavefronts, two groups per
 // 256-thread workgroup (the hardware then places its four wavefronts on the CU's four SIMDs),
 // so a 16k-engagement step fills every SIMD instead of half of them.  Wave 0 (advance role) makes
@@ -912,6 +950,7 @@ __global__ __launch_bounds__(kPostSplitBlock) void env_post_step_split_kernel(
     const F16EnvStepIO io, F16Recon r, F16RewardCfg c, Origin O) {
   __shared__ float S_all[kPostGroups][kRowBlock * tile_pitch<D, FULL>()];
   __shared__ uint64_t sh_mask[kPostGroups][2];   // live and finished rows, from the advance role
+  __shared__ double sh_norm[FULL ? 8 * D : 1];     // RunningNorm partials per phase (full tile)
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int grp = wave >> 1, role = wave & 1;
@@ -1023,7 +1062,14 @@ __global__ __launch_bounds__(kPostSplitBlock) void env_post_step_split_kernel(
   bool any_fresh = false;   // uniform over the workgroup, so every thread meets the same barriers
 #pragma unroll
   for (int q = 0; q < kPostGroups; ++q) any_fresh |= sh_mask[q][1] != 0;
-  if (!any_fresh) return;
+  if (!any_fresh) {
+    if constexpr (FULL) {
+      if (io.norm_partial)
+        norm_partials_from_tiles<D>(&S_all[0][0], sh_norm, (long)blockIdx.x * 2 * kRowBlock, nac,
+                                    blockIdx.x, io, threadIdx.x);
+    }
+    return;
+  }
   __syncthreads();
   // Rows of finished engagements, again split: the advance role restarts them from the pool
   // (state rows, reconstructor, reward anchor) and writes the scalar block; the vector role
@@ -1048,6 +1094,11 @@ __global__ __launch_bounds__(kPostSplitBlock) void env_post_step_split_kernel(
   }
   __syncthreads();
   flush_sparse<D, FULL, 2 * kRowBlock>(S, a0, fresh, io.obs, gtid);
+  if constexpr (FULL) {   // the tiles now hold every new row, the rebuilt ones included
+    if (io.norm_partial)
+      norm_partials_from_tiles<D>(&S_all[0][0], sh_norm, (long)blockIdx.x * 2 * kRowBlock, nac,
+                                  blockIdx.x, io, threadIdx.x);
+  }
 }
 
 // Masked autoreset without a step: engagements with mask[e] != 0 get an initial-condition pool
@@ -1222,6 +1273,8 @@ static int post_step(const F16EnvStepIO* io, const F16Recon* rec, const F16Rewar
       (io->terminal_obs && !rows_aligned(io->terminal_obs, io->obs_dim)))
     return F16_EINVAL;
   const bool full = full_tile_resident(rec->nenv, io->obs_dim, split ? kPostGroups : 1);
+  if (io->norm_partial && (!split || !full || !io->norm_count || !io->norm_count_snap))
+    return F16_EINVAL;
   hipStream_t s = (hipStream_t)stream;
 #define F16_POST_STEP(D, FULL)                                                                  \
   do {                                                                                          \
@@ -1244,6 +1297,11 @@ static int post_step(const F16EnvStepIO* io, const F16Recon* rec, const F16Rewar
 extern "C" int f16_env_post_step(const F16EnvStepIO* io, const F16Recon* rec,
                                  const F16RewardCfg* cfg, void* stream) {
   return post_step(io, rec, cfg, stream, true);
+}
+
+extern "C" int f16_env_post_step_norm_fusable(int nenv, int obs_dim) {
+  if (nenv < 1 || (obs_dim != 184 && obs_dim != 214)) return 0;
+  return full_tile_resident(nenv, obs_dim, kPostGroups) ? 1 : 0;
 }
 
 extern "C" int f16_env_post_step_onewave(const F16EnvStepIO* io, const F16Recon* rec,

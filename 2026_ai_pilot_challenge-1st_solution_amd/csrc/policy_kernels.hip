@@ -501,6 +501,19 @@ extern "C" long f16_norm_workspace_bytes(int nrows, int obs_dim) {
   return (long)norm_blocks(nrows) * 2 * obs_dim * (long)sizeof(double) + (long)sizeof(double);
 }
 
+extern "C" int f16_norm_merge(int nrows, int obs_dim, float* mean, float* var, void* work,
+                              void* stream) {
+  if (nrows < 0 || obs_dim < 1 || obs_dim > kNormCols) return F16_EINVAL;
+  if (nrows == 0) return 0;
+  if (!mean || !var || !work) return F16_EINVAL;
+  const int nb = norm_blocks(nrows);
+  const double* partial = static_cast<const double*>(work);
+  const float* snap = reinterpret_cast<const float*>(partial + (long)nb * 2 * obs_dim);
+  hipLaunchKernelGGL(norm_merge_kernel, dim3(obs_dim), dim3(kMergeThreads), 0,
+                     (hipStream_t)stream, partial, nb, nrows, obs_dim, mean, var, snap);
+  return f16_last_error();
+}
+
 extern "C" int f16_norm_update(const float* obs, long obs_ld, const int* rows, int nrows,
                                int obs_dim, float* mean, float* var, float* count, void* work,
                                void* stream) {

@@ -147,6 +147,31 @@ class RunningNorm:
         self.eps = float(eps)
         self._work = None
 
+    def _workspace(self, n):
+        need = _lib.lib().f16_norm_workspace_bytes(n, self.dim)
+        if self._work is None or self._work.numel() < need:
+            self._work = torch.empty(max(need, 8), dtype=torch.uint8, device=self.device)
+        return self._work
+
+    def fused_partials(self, io, n):
+        """Point an F16EnvStepIO's norm fields at this normaliser's workspace, so the
+        post-physics step writes the partial sums of its n new observation rows; `merge(n)`
+        then completes update() of those rows."""
+        w = self._workspace(n)
+        nb = (n + 127) // 128
+        io.norm_partial = w.data_ptr()
+        io.norm_count = self.count.data_ptr()
+        io.norm_count_snap = w.data_ptr() + nb * 2 * self.dim * 8   # the workspace's last slot
+
+    @torch.no_grad()
+    def merge(self, n):
+        """The second half of update(): fold the partial sums already in the workspace (written
+        by a post-physics step with fused_partials) into mean/var."""
+        L = _lib.lib()
+        rc = L.f16_norm_merge(n, self.dim, _lib.ptr(self.mean), _lib.ptr(self.var),
+                              _lib.ptr(self._workspace(n)), _lib.stream_handle(self.device))
+        _lib.check(rc, "f16_norm_merge")
+
     @torch.no_grad()
     def update(self, x, rows=None):
         """x: (N, dim) float32 CUDA rows (or the rows listed in `rows`, int32)."""
@@ -156,9 +181,7 @@ class RunningNorm:
             x = x.contiguous()
         n = x.shape[0] if rows is None else rows.numel()
         L = _lib.lib()
-        need = L.f16_norm_workspace_bytes(n, self.dim)
-        if self._work is None or self._work.numel() < need:
-            self._work = torch.empty(max(need, 8), dtype=torch.uint8, device=self.device)
+        self._workspace(n)
         rc = L.f16_norm_update(_lib.ptr(x), x.stride(0), _lib.ptr(rows), n, self.dim,
                                _lib.ptr(self.mean), _lib.ptr(self.var), _lib.ptr(self.count),
                                _lib.ptr(self._work), _lib.stream_handle(self.device))

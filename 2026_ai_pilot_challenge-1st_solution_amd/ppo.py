@@ -138,11 +138,14 @@ class SelfPlayRollout:
     net.pack() are picked up by the next replay.  (stats=False only.)"""
 
     def __init__(self, env, net, T=64, gamma=0.99, lam=0.95, seed=0, update_norm=True,
-                 stats=True, graph=False, aux=False):
+                 stats=True, graph=False, aux=False, fuse_norm=True):
         from .policy import PolicyStep, RunningNorm
         self.env, self.net, self.T = env, net, int(T)
         self.gamma, self.lam = float(gamma), float(lam)
         self.update_norm, self.want_stats = bool(update_norm), bool(stats)
+        # the post-physics launch of step t also forms the RunningNorm partial sums of the rows
+        # step t + 1 normalises, which then needs only the merge (identical statistics)
+        self.fuse_norm = bool(fuse_norm) and self.update_norm and env.norm_fusable()
         D, nac, ne, dev = env.OBS_SIZE, env.nac, env.nenv, env.device
         self.D, self.nac, self.nenv, self.device = D, nac, ne, dev
         self.norm = RunningNorm(D, dev)
@@ -202,12 +205,16 @@ class SelfPlayRollout:
             if self.b_aux_features is not None:       # features of s_t (ppo_gpu.py:1876-1879)
                 self.b_aux_features[t].copy_(env.obr.aux_features)
             if self.update_norm:
-                self.norm.update(obs)
+                if self.fuse_norm and t > 0:
+                    self.norm.merge(self.nac)     # partials from step t - 1's post-physics launch
+                else:
+                    self.norm.update(obs)
             self._policy(obs, g0 + t, pol_base, nobs_out=self.b_obs[t], act_idx=self.b_act[t],
                          logp=self.b_logp[t], value=self.b_val[t], env_actions=env.sim.actions)
             done_t = self.b_done[t + 1] if t + 1 < T else self.next_done
+            fused = self.norm if (self.fuse_norm and t + 1 < T) else None
             self.next_obs = env.step_rollout(self.b_rew[t], done_t, self.finite_acc,
-                                             step_base=env_base, step=t)
+                                             step_base=env_base, step=t, norm=fused)
             if self.want_stats:
                 d2 = done_t.repeat_interleave(2)
                 self.ep_ret += self.b_rew[t]

@@ -306,14 +306,20 @@ class GpuDogfightVecEnv:
                 "terminal_state_finite": fin}
         return self._obs.view(ne, 2, self.OBS_SIZE), reward.view(ne, 2), done, info
 
-    def step_rollout(self, reward_f32, done_f32, finite_acc, step_base=None, step=0):
+    def norm_fusable(self):
+        """Whether step_rollout can also form the RunningNorm partial sums of its new rows."""
+        return bool(self.obr._lib.f16_env_post_step_norm_fusable(self.nenv, self.OBS_SIZE))
+
+    def step_rollout(self, reward_f32, done_f32, finite_acc, step_base=None, step=0, norm=None):
         """The rollout collector's step: the controls already sit in sim.actions (written by the
         policy kernel); one FDM launch and one post-physics launch that writes the float32
         rewards (nac,) and done flags (nenv,) straight into the caller's buffers and clears
         finite_acc (nenv,) bytes of engagements whose state went non-finite.  Autoreset pool rows
         are drawn inside the kernel (Philox keyed by the env seed and a per-env step counter).
         step_base (device int32 scalar) + step replaces the env's host step counter in the
-        kernel's draws: a rollout recorded in a HIP graph advances step_base on the device."""
+        kernel's draws: a rollout recorded in a HIP graph advances step_base on the device.
+        norm (a RunningNorm, only where norm_fusable()): the launch also writes the partial sums
+        of the new observation rows into its workspace, for norm.merge(nac)."""
         self._ensure_ic_pool()
         self.sim.step(self.sim.actions, substeps=self.substeps, want_obs=False)
         io = self._io(None)
@@ -321,6 +327,8 @@ class GpuDogfightVecEnv:
             io.step, io.step_base = int(step) & 0xffffffff, step_base.data_ptr()
         io.reward_f32, io.done_f32 = reward_f32.data_ptr(), done_f32.data_ptr()
         io.finite_acc = finite_acc.data_ptr()
+        if norm is not None:
+            norm.fused_partials(io, self.nac)
         self._post(io)
         return self._obs.view(self.nac, self.OBS_SIZE)
 

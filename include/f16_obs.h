@@ -112,6 +112,14 @@ typedef struct F16EnvStepIO {
     int n_opp;
     const unsigned int *step_base;   /* device counter added to `step` when non-NULL (captured
                                         rollouts): the counters above use *step_base + step */
+    double *norm_partial;        /* RunningNorm partial sums of the new `obs` rows, in the
+                                    f16_norm_update workspace layout (per 128-row block: obs_dim
+                                    sums, then obs_dim sums of squares), so that f16_norm_merge
+                                    completes RunningNorm.update(obs) -- or NULL.  Only where
+                                    f16_env_post_step_norm_fusable(nenv, obs_dim) is 1. */
+    float *norm_count;           /* with norm_partial: the running count, advanced by nac */
+    float *norm_count_snap;      /* with norm_partial: the count before this update (the
+                                    workspace's last element, as f16_norm_update keeps it) */
 } F16EnvStepIO;
 
 /* GpuDogfightVecEnv.step after the physics launch (research/competition_36500/runtime/
@@ -132,6 +140,11 @@ int f16_env_reseed(const F16EnvStepIO *io, const F16Recon *rec, const unsigned c
 
 int f16_env_post_step(const F16EnvStepIO *io, const F16Recon *rec, const F16RewardCfg *cfg,
                       void *stream);
+
+/* 1 when f16_env_post_step over nenv engagements can also produce the RunningNorm partial sums
+ * of its new observation rows (io->norm_partial): every row's block sits whole in one
+ * workgroup's staging tile.  0 otherwise (the caller then runs f16_norm_update). */
+int f16_env_post_step_norm_fusable(int nenv, int obs_dim);
 
 /* The same step with one wavefront per 64 aircraft instead of two (f16_env_post_step spreads
  * each group's row build over an advance wave and a vector-block wave); results are identical

@@ -98,6 +98,12 @@ long f16_norm_workspace_bytes(int nrows, int obs_dim);
 int f16_norm_update(const float *obs, long obs_ld, const int *rows, int nrows, int obs_dim,
                     float *mean, float *var, float *count, void *work, void *stream);
 
+/* The second half of f16_norm_update alone: merge the per-block partial sums already in `work`
+ * (written by a launch that formed them, e.g. f16_env_post_step with io->norm_partial) into
+ * mean/var with the count snapshot kept at the workspace's end.  f16_norm_update(obs, ...) and
+ * (partials of the same rows) + f16_norm_merge give identical statistics. */
+int f16_norm_merge(int nrows, int obs_dim, float *mean, float *var, void *work, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -25,11 +25,11 @@ _spec.loader.exec_module(GO)
 pytestmark = pytest.mark.gpu
 
 
-def _collector(gpu, nenv=256, T=12, seed=3, **kw):
+def _collector(gpu, nenv=256, T=12, seed=3, env_kw=None, **kw):
     E = import_pkg("rl_env").GpuDogfightVecEnv
     P = import_pkg("policy")
     R = import_pkg("ppo")
-    env = E(nenv, seed=seed, ic_pool_size=64)
+    env = E(nenv, seed=seed, ic_pool_size=64, **(env_kw or {}))
     net = P.MLPActorCritic(184, init="normal", generator=torch.Generator().manual_seed(seed)).to(gpu)
     ro = R.SelfPlayRollout(env, net, T=T, gamma=0.99, lam=0.95, seed=0, **kw)
     ro.reset(stagger=True, max_stagger_steps=8)
@@ -125,3 +125,26 @@ def test_graph_league_rollout_equals_eager(gpu):
     a, b = make(False), make(True)
     _same_rollouts(a, b)
     assert a.b_done.sum().item() > 0          # autoresets and opponent redraws happened
+
+
+@pytest.mark.parametrize("nenv,graph", [(200, False), (512, True)])
+def test_fused_norm_partials_equal_separate_update(gpu, nenv, graph):
+    """The post-physics launch forming the RunningNorm partial sums of the rows the next step
+    normalises (then only the merge runs) gives the same statistics and buffers, bit for bit, as
+    a separate f16_norm_update per step: over three rollouts with autoresets, a ragged last
+    128-row block (nenv 200) and the fused collector recorded as a HIP graph."""
+    short = {"max_engage_time_s": 1.5}          # every engagement ends within 15 decisions
+    a = _collector(gpu, nenv=nenv, T=8, stats=False, fuse_norm=False, env_kw=short)
+    b = _collector(gpu, nenv=nenv, T=8, stats=False, graph=graph, fuse_norm=True, env_kw=short)
+    assert not a.fuse_norm and b.fuse_norm
+    done = 0.0
+    for r in range(3):
+        ra, rb = a.collect(), b.collect()
+        torch.cuda.synchronize()
+        for name in BUFFERS:
+            assert torch.equal(getattr(a, name), getattr(b, name)), (r, name)
+        assert torch.equal(ra[0], rb[0]) and torch.equal(ra[1], rb[1]), r
+        for name in ("mean", "var", "count"):
+            assert torch.equal(getattr(a.norm, name), getattr(b.norm, name)), (r, name)
+        done += a.b_done.sum().item()
+    assert done > 0                            # rows rebuilt from the pool were in the sums
