@@ -13,13 +13,13 @@
 //   -- X1: altitude, cos(theta)cos(phi)  |  mass/CG/inertia, aileron/rudder/LEF/flaperon
 //   phase 2  flight:  air-relative geometry (vt, alpha, beta), load factors, alpha/beta brackets,
 //                     their table values and the alpha/beta-only part of each axis sum
-//            systems: atmosphere, pitch loop
+//            systems: atmosphere, pitch loop, sin/cos of the next substep's Earth position angle
 //   -- X2: vt, alpha, beta, n_y, n_z  |  rho, speed of sound, elevator
 //   phase 3  flight:  dynamic pressure, mach, mach/elevator brackets and values, the six axes,
 //                     quaternion rate, gravity, vg
-//            systems: mach, calibrated airspeed, engine, sin/cos of the next substep's Earth
-//                     position angle
-//   -- X3: vg, p q r  |  thrust, sin/cos(epa)
+//            systems: mach, calibrated airspeed, engine
+//   -- X3: vg, p q r  |  thrust (the next substep's sin/cos(epa), written in phase 2, are read
+//          by the flight wave after this exchange)
 //   phase 4  flight:  forces, moments, accelerations, state update
 //            systems: fuel burn, previous-frame auxiliary values
 //
@@ -272,6 +272,14 @@ __device__ __forceinline__ void split_systems(double* __restrict__ s, long ld,
     fcs_pitch<FCS_RATE>(a, esch, ctcp, fc);
     x[kXRho][lane] = at.rho; x[kXSound][lane] = at.a;
     x[kXElev][lane] = fc.elev;
+    // the next substep's sin/cos(epa): read by the flight wave in that substep's first phase,
+    // after this substep's third exchange; formed here, where this wave has slack
+    if (t + 1 < S) {
+      double sn, cn;
+      sincos(a.epa + kRot * kDt, &sn, &cn);
+      x[kXCe][lane] = cn;
+      x[kXSe][lane] = sn;
+    }
     __syncthreads();
     // ---- phase 3
     const double vt = x[kXVt][lane], alpha = x[kXAlpha][lane];
@@ -280,12 +288,6 @@ __device__ __forceinline__ void split_systems(double* __restrict__ s, long ld,
     const double vc = vc_knots(mach, at.P);   // previous-frame input of the next substep's FCS
     double burn;
     x[kXThrust][lane] = engine(a, c_thr, at, mach, T, burn);
-    if (t + 1 < S) {
-      double sn, cn;
-      sincos(a.epa + kRot * kDt, &sn, &cn);
-      x[kXCe][lane] = cn;
-      x[kXSe][lane] = sn;
-    }
     __syncthreads();
     // ---- phase 4
     const double vg = x[kXVg][lane];
