@@ -68,8 +68,9 @@ struct Flat {
 constexpr int kAdvThreads = 256;
 constexpr int kAdvPer = 8;                       // rows per thread of the advantage partials
 constexpr int kNormBlockElems = 4096;            // flat elements per squared-norm block
-constexpr int kWChunkTarget = 1024;              // aim for about this many wgrad workgroups
-constexpr int kMaxChunks = 64;                   // > kWChunkTarget / (fewest tiles, 18)
+constexpr int kWgradSlots = 768;                 // resident wgrad workgroups when the device
+                                                 // cannot be asked (3 per CU x 256 CUs)
+constexpr int kMaxChunks = 64;                   // bound on the chunks the partials hold
 
 __host__ __device__ inline long align256(long x) { return (x + 255) & ~255L; }
 
@@ -95,15 +96,16 @@ inline int norm_blocks(long n) { return (int)((n + kNormBlockElems - 1) / kNormB
 
 inline int wgrad_tiles(int kp) { return 4 * ((kp + 127) / 128) + 4 + 4 + 2; }
 
-inline Work layout(int obs_dim, long mb_rows, void* base) {
+inline Work layout(int obs_dim, long mb_rows, void* base, int wg_slots = kWgradSlots) {
   Work w{};
   const int kp = (obs_dim + 31) / 32 * 32;
   const Flat F{obs_dim};
   w.ld = (mb_rows + 63) / 64 * 64;
   w.nwg = (int)(w.ld / 64);
   const int tiles = wgrad_tiles(kp);
-  // chunks of 32-row stages: enough workgroups to fill the chip, at least 8 stages each
-  long chunks = (kWChunkTarget + tiles - 1) / tiles;
+  // chunks of 32-row stages: one workgroup per resident slot (a grid a little above a
+  // multiple of the slots leaves a mostly idle last round), at least 8 stages each
+  long chunks = std::max(1, std::min(wg_slots / tiles, kMaxChunks));
   long cr = (w.ld + chunks - 1) / chunks;
   cr = (cr + 31) / 32 * 32;
   if (cr < 256) cr = 256;
@@ -934,6 +936,20 @@ static int device_cus() {
   return n;
 }
 
+// Resident wgrad workgroups: compute units x the kernel's occupancy (3 per CU on MI355X: 142
+// VGPRs, 40 KB LDS), asked once per process.
+static int wgrad_slots() {
+  static int slots = 0;
+  if (slots == 0) {
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, wgrad_kernel, kWThreads, 0) !=
+            hipSuccess || per_cu < 1)
+      per_cu = 3;
+    slots = per_cu * device_cus();
+  }
+  return slots;
+}
+
 extern "C" int f16_ppo_param_counts(int obs_dim, long* out2) {
   if (!out2 || (obs_dim != 184 && obs_dim != 214)) return F16_EINVAL;
   const Flat F{obs_dim};
@@ -957,7 +973,7 @@ extern "C" int f16_ppo_grad(const F16PPOArgs* a, void* stream) {
   if ((a->obs_ld & 1) || ((uintptr_t)a->obs & 7)) return F16_EINVAL;   // rows move as float2
   const int D = a->obs_dim, kp = (D + 31) / 32 * 32;
   const Flat F{D};
-  const Work w = layout(D, a->mb_rows, a->work);
+  const Work w = layout(D, a->mb_rows, a->work, wgrad_slots());
   hipStream_t s = (hipStream_t)stream;
   hipLaunchKernelGGL(adv_partial_kernel, dim3(w.nadv), dim3(kAdvThreads), 0, s, a->adv, a->idx,
                      a->mb_rows, a->count, w.advp);
