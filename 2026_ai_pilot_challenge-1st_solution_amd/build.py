@@ -1,7 +1,8 @@
 """Build the HIP library (libf16hip.so) in-tree for gfx950.
 
-Compiled with hipcc straight from csrc/; no torch extension machinery, no JIT cache: the .so
-sits next to this file so that it travels with the repository snapshot to the GPU box.
+Compiled with hipcc straight from csrc/ (one object per source under _build/, linked into one
+shared library); no torch extension machinery, no JIT cache: the .so sits next to this file so
+that it travels with the repository snapshot to the GPU box.
 
 Flags:
   -ffp-contract=off    keep every add and multiply separately rounded (parity with the
@@ -28,21 +29,38 @@ def hipcc():
     raise RuntimeError("hipcc not found")
 
 
-def build(verbose=False):
-    """Compile every HIP source into libf16hip.so (always recompiles)."""
-    srcs = [os.path.join(CSRC, s) for s in SOURCES]
-    tmp = LIB + ".tmp"
-    cmd = [hipcc(), f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
+def _compile(src, obj, verbose):
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-c",
            "-ffp-contract=off", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-           "-I", os.path.join(ROOT, "include"), "-I", CSRC, "-o", tmp] + srcs
+           "-I", os.path.join(ROOT, "include"), "-I", CSRC, "-o", obj, src]
     if verbose:
         cmd.append("-Rpass-analysis=kernel-resource-usage")
-    p = subprocess.run(cmd, capture_output=True, text=True)
+    return subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True)
+
+
+def build(verbose=False):
+    """Compile every HIP source (one hipcc process per source, in parallel) and link them
+    into libf16hip.so (always recompiles)."""
+    objdir = os.path.join(HERE, "_build")
+    os.makedirs(objdir, exist_ok=True)
+    objs = [os.path.join(objdir, os.path.splitext(s)[0] + ".o") for s in SOURCES]
+    procs = [_compile(os.path.join(CSRC, s), o, verbose) for s, o in zip(SOURCES, objs)]
+    failed = False
+    for s, p in zip(SOURCES, procs):
+        out, err = p.communicate()
+        if p.returncode != 0:
+            sys.stderr.write(out + err)
+            failed = True
+        elif verbose:
+            sys.stderr.write("\n".join(l for l in err.splitlines() if "remark" in l) + "\n")
+    if failed:
+        raise RuntimeError("hipcc failed building libf16hip.so")
+    tmp = LIB + ".tmp"
+    p = subprocess.run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp] + objs,
+                       capture_output=True, text=True)
     if p.returncode != 0:
         sys.stderr.write(p.stdout + p.stderr)
-        raise RuntimeError("hipcc failed building libf16hip.so")
-    if verbose:
-        sys.stderr.write("\n".join(l for l in p.stderr.splitlines() if "remark" in l) + "\n")
+        raise RuntimeError("hipcc failed linking libf16hip.so")
     os.replace(tmp, LIB)
     return LIB
 

@@ -203,6 +203,7 @@ __global__ __launch_bounds__(kBlock) void seed_kernel(const double* __restrict__
     qd[3] = 0.5 * (-q[2] * p + q[1] * qq + q[0] * rr);
   }
   const long a = rows ? rows[r] : r;
+  if (a < 0 || a >= ld) return;            // a column outside the (101, ld) buffer: no write
   double* __restrict__ o = st + a;
 #define F(kk) o[(long)(kk) * ld]
   for (int j = 0; j < 3; ++j) {
@@ -283,17 +284,30 @@ extern "C" int f16_seed_batch(const double* ic, int n, int fcs_rate, double* sta
   return f16_last_error();
 }
 
-// Register/LDS/scratch footprint of the step kernel (the reference's profile_kernel.py reads the
-// same attributes from the CUDA driver).  out = {vgprs/regs per thread, lds bytes, scratch bytes,
-// max threads per block}.
-extern "C" int f16_fdm_kernel_info(int fcs_rate, int* out4) {
+// Register/LDS/scratch footprint of the step kernel that f16_fdm_step_batch launches (the
+// two-wave split kernel; the reference's profile_kernel.py reads the same attributes from the
+// CUDA driver).  out = {vgprs/regs per thread, lds bytes, scratch bytes, max threads per block}.
+static int kernel_info(const void* fn, int* out4) {
+  if (!out4) return F16_EINVAL;
   hipFuncAttributes at;
-  hipError_t e = fcs_rate == 60 ? hipFuncGetAttributes(&at, (const void*)f16::fdm_step_kernel<60>)
-                                : hipFuncGetAttributes(&at, (const void*)f16::fdm_step_kernel<120>);
+  hipError_t e = hipFuncGetAttributes(&at, fn);
   if (e != hipSuccess) return -(1000 + (int)e);
   out4[0] = at.numRegs;
   out4[1] = (int)at.sharedSizeBytes;
   out4[2] = (int)at.localSizeBytes;
   out4[3] = at.maxThreadsPerBlock;
   return 0;
+}
+
+extern "C" int f16_fdm_kernel_info(int fcs_rate, int* out4) {
+  if (fcs_rate != 120 && fcs_rate != 60) return F16_ERATE;
+  return kernel_info(fcs_rate == 60 ? (const void*)f16::fdm_step_split_kernel<60>
+                                    : (const void*)f16::fdm_step_split_kernel<120>, out4);
+}
+
+// The same for the one-lane kernel behind f16_fdm_step_batch_onelane.
+extern "C" int f16_fdm_kernel_info_onelane(int fcs_rate, int* out4) {
+  if (fcs_rate != 120 && fcs_rate != 60) return F16_ERATE;
+  return kernel_info(fcs_rate == 60 ? (const void*)f16::fdm_step_kernel<60>
+                                    : (const void*)f16::fdm_step_kernel<120>, out4);
 }

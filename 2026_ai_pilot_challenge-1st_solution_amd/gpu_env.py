@@ -70,9 +70,15 @@ class GpuDogfight:
 
     @property
     def kern(self):
-        """Kernel footprint {regs, lds, scratch, max_threads} (reference attribute: the kernel)."""
+        """Footprint {regs, lds, scratch, max_threads} of the kernel `step` launches (reference
+        attribute: the kernel object, cuda_fdm/gpu_env.py:49-55)."""
+        return self.kernel_info(onelane=False)
+
+    def kernel_info(self, onelane=False):
+        """Footprint of the split kernel (default) or of the one-lane kernel."""
         out = (_lib.ctypes.c_int * 4)()
-        _lib.check(self._lib.f16_fdm_kernel_info(self.fcs_rate, out), "f16_fdm_kernel_info")
+        fn = self._lib.f16_fdm_kernel_info_onelane if onelane else self._lib.f16_fdm_kernel_info
+        _lib.check(fn(self.fcs_rate, out), "f16_fdm_kernel_info")
         return dict(regs=out[0], lds=out[1], scratch=out[2], max_threads=out[3])
 
     # ---- reset (cuda_fdm/gpu_env.py:64-92) ----
@@ -110,6 +116,8 @@ class GpuDogfight:
             rows = rows.to(device=self.device, dtype=torch.int64).contiguous()
             if rows.shape != (n,):
                 raise ValueError("rows must be (n,)")
+            if n and not bool(((rows >= 0) & (rows < self.nac)).all()):   # one host sync
+                raise IndexError(f"rows must lie in [0, {self.nac})")
         elif n != self.nac:
             raise ValueError("without rows, n must equal nac")
         rc = self._lib.f16_seed_batch(_lib.ptr(ic), n, self.fcs_rate, _lib.ptr(self._state_soa),

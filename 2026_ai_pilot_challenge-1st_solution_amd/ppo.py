@@ -54,9 +54,11 @@ class _RolloutGraph:
     """Records a collector's _run() once as a HIP graph (torch.cuda.CUDAGraph) and replays it.
 
     The env's and the collector's draw counters become device int32 scalars that the recorded
-    launches read (step_base) and that the graph itself advances by T at its end; the host
-    counters (collector.global_step, env._post_steps) are kept equal to them.  The first
-    collect() runs eagerly so that every lazily allocated workspace exists before recording."""
+    launches read (step_base) and that the graph itself advances by T at its end.  Before every
+    replay they are refilled from the host counters (collector.global_step, env._post_steps), so
+    env steps taken outside the graph between two replays (an evaluation on the same env) move
+    the next replay's draws on exactly as they move an eager collect's.  The first collect()
+    runs eagerly so that every lazily allocated workspace exists before recording."""
 
     def __init__(self, owner, device):
         self.owner = owner
@@ -73,12 +75,10 @@ class _RolloutGraph:
             o.global_step += T
             self.warm = True
             return out
+        for v in (o.global_step, env._post_steps):
+            if not 0 <= v < 2 ** 31 - 4 * T:
+                raise OverflowError("draw counters beyond the int32 device counters")
         if self.graph is None:
-            for v in (o.global_step, env._post_steps):
-                if not 0 <= v < 2 ** 31 - 4 * T:
-                    raise OverflowError("draw counters beyond the int32 device counters")
-            self.pol_base.fill_(o.global_step)
-            self.env_base.fill_(env._post_steps)
             p0 = env._post_steps
             torch.cuda.synchronize(self.pol_base.device)
             g = torch.cuda.CUDAGraph()
@@ -88,6 +88,9 @@ class _RolloutGraph:
                 self.env_base.add_(T)
             env._post_steps = p0            # recording ran nothing
             self.graph = g
+        # small fills on the stream, outside the graph: the replay reads the host's counters
+        self.pol_base.fill_(o.global_step)
+        self.env_base.fill_(env._post_steps)
         self.graph.replay()
         o.global_step += T
         env._post_steps += T

@@ -36,14 +36,20 @@ int f16_fdm_step_batch_onelane(double* states, long ld, const double* actions, i
  * ic: (n, 10) rows [lat_deg, lon_deg, alt_ft, vt_fps, phi_deg, theta_deg, psi_deg, alpha_deg,
  *     beta_deg, fuel_lbs] (geodetic latitude, epa = 0, fuel-flow 0).
  * rows (optional): (n,) int64 target aircraft index per IC row; NULL seeds rows 0..n-1.
+ *     A row index outside [0, ld) is skipped (nothing written); callers validate first.
  * Replaces the host-side build_seed_vector (cuda_fdm/ic.py:117-138) used by
  * GpuDogfight.reset_ic (cuda_fdm/gpu_env.py:78-92) and the env's IC pools. */
 int f16_seed_batch(const double* ic, int n, int fcs_rate, double* states, long ld,
                    const long* rows, void* stream);
 
 /* Host pointer out4 <- {registers per lane, static LDS bytes, scratch bytes per lane,
- * max threads per block} of the step kernel (cf. cuda_fdm/tests/profile_kernel.py:23-33). */
+ * max threads per block} of the kernel f16_fdm_step_batch launches (the two-wave split kernel;
+ * cf. cuda_fdm/tests/profile_kernel.py:23-33).  NULL out4 -> F16_EINVAL. */
 int f16_fdm_kernel_info(int fcs_rate, int* out4);
+
+/* The same footprint for the one-lane kernel behind f16_fdm_step_batch_onelane
+ * (cuda_fdm/tests/profile_kernel.py:23-33 reads one kernel; this build has two). */
+int f16_fdm_kernel_info_onelane(int fcs_rate, int* out4);
 
 /* Generalized advantage estimation over a rollout buffer (fp32).
  * rew, val, adv, ret: (T, nenv*nagents) time-major, column = env*nagents + agent;

@@ -154,13 +154,90 @@ def child(ref_root, inp_path, out_path):
     np.savez_compressed(out_path, **out)
 
 
+def child_root214(ref_root, inp_path, out_path):
+    """The root lineage's CPU torch path (cuda_fdm/obs_reward.py, 214-D observation): advance
+    forms the NED-velocity step difference (cuda_fdm/obs_reward.py:569-575) and build_obs writes
+    it through the 10 accel (vector, frame) pairs (:702-712; layout claude_code/my_observation.py
+    VECTOR_SPECS).  Same scripted states and resets as the 184-D golden; reward mode 0 only
+    (the reconstructor and the observation do not depend on the mode)."""
+    for p in (os.path.join(ref_root, "src"), ref_root):
+        sys.path.insert(0, p)
+    import torch
+    from cuda_fdm import obs_reward as OR          # reference, build container only
+    from cuda_fdm import rl_env as RE
+    from dogfight.envs.termination import time_limit_reached
+    assert OR.OBS_SIZE == 214
+    inp = dict(np.load(inp_path))
+    cfg = dict(OR.RW.MY_REWARD_CONFIG)
+
+    def state9(st):
+        ecef_m, euler, vuvw, alt_ft = RE.kinematics_state(torch.as_tensor(st))
+        n, e, d = RE.ned_from_ecef_altasl(ecef_m, alt_ft * RE.FT2M)
+        return torch.cat([torch.stack([n, e, d], 1), euler * RE.R2D, vuvw * RE.FT2M], 1)
+
+    nenv = inp["reset"].shape[1]
+    obr = OR.BatchObsReward(nenv, device="cpu", enable_kernel=False)
+    obr.hp.copy_(torch.as_tensor(inp["hp0"]))
+    obr.t_sec.copy_(torch.as_tensor(inp["t0"]))
+    obr.initialize_reward_state(state9(inp["states"][0]), None, cfg)
+    rec = {k: [] for k in ("obs", "accel", "prev_vel_ned", "reward", "term", "trunc",
+                           "obs_reset", "accel_reset", "prev_vel_ned_reset")}
+    for k in range(inp["actions"].shape[0]):
+        obr.push_actions(torch.as_tensor(inp["actions"][k]))
+        s9 = state9(inp["states"][k])
+        obr.advance(s9)
+        s9v = s9.view(nenv, 2, 9)
+        fin = torch.isfinite(s9v).all(dim=2)
+        hp = obr.hp.view(nenv, 2)
+        term = ((-s9v[:, :, 2] < RE.HARD_DECK_M).any(1) | (hp <= 0.0).any(1) | (~fin).any(1))
+        trunc = time_limit_reached(obr.t_sec, 200.0) & (~term)
+        r = obr.compute_reward(s9, term, cfg, trunc, reward_mode=0, alt_hunt_coef=5.0)
+        for key, val in (("obs", obr.build_obs(s9)), ("accel", obr.accel),
+                         ("prev_vel_ned", obr.prev_vel_ned), ("reward", r), ("term", term),
+                         ("trunc", trunc)):
+            rec[key].append(val.clone().numpy())
+        mask = torch.as_tensor(inp["reset"][k])
+        s9r = state9(inp["states_reset"][k])
+        if bool(mask.any()):
+            obr.reset_envs(mask)
+            obr.initialize_reward_state(s9r, mask, cfg)
+        rec["obs_reset"].append(obr.build_obs(s9r).numpy())
+        rec["accel_reset"].append(obr.accel.clone().numpy())
+        rec["prev_vel_ned_reset"].append(obr.prev_vel_ned.clone().numpy())
+    np.savez_compressed(out_path, **{f"a214_{k}": np.array(v) for k, v in rec.items()})
+
+
+def main_root214(ref):
+    """Write obs214_golden.npz from the inputs stored in obs_golden.npz."""
+    g = dict(np.load(os.path.join(HERE, "obs_golden.npz")))
+    inp = {k[3:]: v for k, v in g.items() if k.startswith("in_")}
+    with tempfile.TemporaryDirectory() as td:
+        ip, op = os.path.join(td, "in.npz"), os.path.join(td, "out.npz")
+        np.savez(ip, **inp)
+        subprocess.run([sys.executable, __file__, "--ref", ref, "--child-root214", ip, op],
+                       check=True)
+        res = dict(np.load(op))
+    np.savez_compressed(os.path.join(HERE, "obs214_golden.npz"), **res)
+    print("wrote obs214_golden.npz", len(res), "arrays",
+          os.path.getsize(os.path.join(HERE, "obs214_golden.npz")) // 1024, "KiB")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--ref", default="/root/reference")
     ap.add_argument("--child", nargs=2)
+    ap.add_argument("--child-root214", nargs=2)
+    ap.add_argument("--root214", action="store_true",
+                    help="write obs214_golden.npz (root lineage, 214-D) from obs_golden's inputs")
     a = ap.parse_args()
     if a.child:
         child(a.ref, *a.child)
+        return
+    if a.child_root214:
+        child_root214(a.ref, *a.child_root214)
+        return
+    if a.root214:
+        main_root214(a.ref)
         return
     inp = make_inputs()
     with tempfile.TemporaryDirectory() as td:

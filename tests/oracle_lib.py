@@ -235,3 +235,39 @@ class ObrOracle:
         self.L.orc_obr_build_obs(ctypes.byref(s), _p(s9), obs_dim,
                                  None if m is None else m.ctypes.data, obs.ctypes.data)
         return obs
+
+
+# ------------------------------------------------------------------ drift envelope (BASELINE C1)
+# 8 replicas of C1 (seeds 0-7): 64 head-on engagements each, 600 decisions of i.i.d. 21-bin
+# actions, FCS at 120 Hz.  tests/golden/make_drift_envelope.py writes the reference pair's
+# divergence curve on exactly these inputs.
+DRIFT_REPLICAS, DRIFT_NENV, DRIFT_NDEC = 8, 64, 600
+DRIFT_QUANTILES = (0.5, 0.75, 0.9, 1.0)
+# the stated bound: every quantile of the divergence at decision d <= DRIFT_K x the reference
+# pair's same quantile anywhere in decisions d .. d + DRIFT_LAG (floored at DRIFT_FLOOR_FT)
+DRIFT_K, DRIFT_LAG, DRIFT_FLOOR_FT = 30.0, 50, 1e-6
+EARTH_RADIUS_FT = 20925646.32546
+
+
+def c1_replicas(icm):
+    """IC rows (1024, 10) and actions (600, 1024, 4) of the 8 C1 replicas."""
+    ic = np.concatenate([icm.sample_headon(DRIFT_NENV, seed=s) for s in range(DRIFT_REPLICAS)])
+    acts = np.concatenate([icm.random_bin_actions(DRIFT_NDEC, 2 * DRIFT_NENV, seed=s)
+                           for s in range(DRIFT_REPLICAS)], axis=1)
+    return ic, acts
+
+
+def altitude_m(states):
+    return (np.linalg.norm(states[:, 0:3], axis=1) - EARTH_RADIUS_FT) * 0.3048
+
+
+def drift_quantiles(a, b, alive):
+    """DRIFT_QUANTILES of |ECI position a - b| (ft) over the aircraft in `alive`."""
+    div = np.linalg.norm(a[:, 0:3] - b[:, 0:3], axis=1)[alive]
+    return np.array([np.quantile(div, q) if div.size else 0.0 for q in DRIFT_QUANTILES])
+
+
+def drift_envelope(env, d):
+    """The bound at decision index d (0-based) for each quantile, from the fixture."""
+    ref = env["pos_ft"]
+    return DRIFT_K * np.maximum(DRIFT_FLOOR_FT, ref[d:min(d + DRIFT_LAG, len(ref) - 1) + 1].max(0))

@@ -50,6 +50,39 @@ def test_seed_scatter_rows(gpu):
     assert (got[[0, 2, 3, 4, 6, 7]] == 7.0).all()
 
 
+def test_seed_rows_out_of_range(gpu):
+    """An aircraft index outside the batch is refused on the host (IndexError), and the kernel's
+    own bound skips it when the C ABI is called directly: only the in-range row is written."""
+    g = oracle_lib.golden("seed_golden.npz")
+    sim = _sim(2)
+    sim.states.fill_(7.0)
+    ic = torch.as_tensor(g["ic"][:3], device=gpu)
+    for bad in ([0, 4, 1], [-1, 0, 1]):
+        with pytest.raises(IndexError):
+            sim.seed_rows(ic, torch.tensor(bad, device=gpu))
+    assert (sim.states == 7.0).all()
+    L = import_pkg("_lib")
+    rows = torch.tensor([-1, 4, 2], dtype=torch.int64, device=gpu)   # ld = nac = 4
+    rc = L.lib().f16_seed_batch(L.ptr(ic), 3, 120, L.ptr(sim._state_soa), 4, L.ptr(rows),
+                                L.stream_handle())
+    assert rc == 0
+    got = sim.states.cpu().numpy()
+    assert oracle_lib.rel_err(got[[2]], g["seed_120"][2:3]).max() < STEP_TOL
+    assert (got[[0, 1, 3]] == 7.0).all()
+
+
+def test_kernel_info_reports_the_launched_kernel(gpu):
+    """kern describes the split kernel f16_fdm_step_batch launches; the one-lane kernel's
+    footprint is its own entry point; a NULL output is refused."""
+    sim = _sim(2)
+    split, one = sim.kern, sim.kernel_info(onelane=True)
+    assert split["max_threads"] >= 256 and split["scratch"] == 0
+    assert split != one
+    L = import_pkg("_lib")
+    assert L.lib().f16_fdm_kernel_info(120, None) == L.F16_EINVAL
+    assert L.lib().f16_fdm_kernel_info(100, None) == L.F16_ERATE
+
+
 @pytest.mark.parametrize("rate", [120, 60])
 def test_one_decision_matches_oracle(gpu, orc, rate):
     g = oracle_lib.golden("seed_golden.npz")
@@ -92,61 +125,84 @@ def test_zero_substeps_is_noop(gpu):
 
 
 def test_c2_per_step_parity_along_trajectory(gpu, orc):
-    """BASELINE C2: 4,096 tail-chase engagements, random held 21-bin actions; every decision is
-    compared against the CPU model on a 64-engagement subset, stepped from the GPU's own state."""
+    """BASELINE C2 at its stated length: 4,096 tail-chase engagements, 1,000 decisions of random
+    held 21-bin actions; every decision is compared against the CPU model on a 64-engagement
+    subset, stepped from the GPU's own state.  Aircraft above the 304.8 m hard deck: <= 1e-10
+    per state variable.  C2 has no termination, so by decision ~700 some aircraft have flown
+    kilometres underground, where the atmosphere is extrapolated far below its base layer and
+    the dynamic pressure exceeds anything the model's tables describe; there the step amplifies
+    last-ulp differences of the exp/log forms (measured worst 6.4e-9 at -7.8 km) and the bound
+    is 1e-8.  Non-finite aircraft must be non-finite on both sides."""
     icm = import_pkg("ic")
     nenv = 4096
     sim = _sim(nenv)
     sim.seed_rows(torch.as_tensor(icm.sample_tailchase(nenv, seed=2), device=gpu))
-    ndec = 150
+    ndec = 1000
     acts = icm.random_bin_actions(ndec, 2 * nenv, seed=2)
     sub = np.arange(0, 2 * nenv, 2 * nenv // 128)          # 128 aircraft = 64 engagements
     sub = np.sort(np.concatenate([sub[sub % 2 == 0], sub[sub % 2 == 0] + 1]))[:128]
-    worst = 0.0
+    idx = torch.as_tensor(sub, device=gpu)
+    worst, worst_deep, compared = 0.0, 0.0, 0
     for d in range(ndec):
-        before = np.ascontiguousarray(sim.states[torch.as_tensor(sub, device=gpu)].cpu().numpy())
+        before = np.ascontiguousarray(sim.states[idx].cpu().numpy())
+        above = (np.linalg.norm(before[:, 0:3], axis=1) - 20925646.32546) * 0.3048 > 304.8
         sim.step(torch.as_tensor(acts[d], device=gpu), want_obs=False)
-        orc.step(before, acts[d][sub], 6)
-        after = sim.states[torch.as_tensor(sub, device=gpu)].cpu().numpy()
-        worst = max(worst, oracle_lib.rel_err(after, before).max())
+        orc.step(before, acts[d][sub], 6, want_obs=False)
+        after = sim.states[idx].cpu().numpy()
+        fin = np.isfinite(before).all(1)
+        np.testing.assert_array_equal(np.isfinite(after).all(1), fin, err_msg=str(d))
+        up, deep = fin & above, fin & ~above
+        if up.any():
+            worst = max(worst, oracle_lib.rel_err(after[up], before[up]).max())
+            compared += int(up.sum())
+        if deep.any():
+            worst_deep = max(worst_deep, oracle_lib.rel_err(after[deep], before[deep]).max())
     assert worst < STEP_TOL
-    assert bool(torch.isfinite(sim.states).all())
+    assert worst_deep < 1e-8
+    assert compared > 0.4 * ndec * len(sub)       # measured 46 %: many aircraft crash
 
 
 def test_trajectory_drift_bound(gpu, orc):
-    """BASELINE C1 plumbing run: 64 head-on engagements, 600 decisions of random 21-bin actions,
-    FDM + FCS only (no termination, so aircraft fly through the ground), free-running on GPU
-    and CPU.  Random full-deflection manoeuvring amplifies last-ulp differences exponentially
-    (e-folding every ~6 decisions); the reference's own C model (fdm.cuh) and its Python model
-    diverge from each other the same way.  Stated drift bound, for aircraft still above the
-    304.8 m hard deck:
-      * decisions 1-50 (5 s):  relative error per state variable <= 1e-6;
-      * decisions 1-100 (10 s): ECI position difference <= 1e-2 ft;
-      * decision 600: the count of non-finite aircraft (flown into the ground) within 4 of the
-        CPU model's."""
+    """BASELINE C1 plumbing run, 8 replicas (seeds 0-7, 1,024 aircraft): 600 decisions of random
+    21-bin actions, FDM + FCS only (no termination: aircraft fly into the ground), free-running
+    on the GPU and on the CPU restatement from the same seeded states.
+
+    Random full-deflection manoeuvring amplifies last-ulp differences exponentially, and the
+    reference's own C model (fdm.cuh) and its Python model drift apart the same way; their
+    divergence on these inputs is the committed curve tests/golden/drift_envelope.npz.  Stated
+    bound, over aircraft above the 304.8 m hard deck:
+      * every decision, 1-600: one decision of the CPU model from the GPU's previous state
+        matches the GPU's next state within 1e-10 relative per state variable (the drift is
+        the amplification of per-step differences no larger than that);
+      * decisions 1-50: free-running relative error per state variable <= 1e-6;
+      * every 10th decision through 600: each of the 50/75/90/100 % quantiles of the ECI
+        position divergence <= 30 x the reference pair's same quantile anywhere within the
+        next 50 decisions (floored at 1e-6 ft).  Measured worst multiples 3.7 / 16.7 / 9.6 /
+        20.2; the CPU test test_drift_envelope_rejects_planted_drift shows that a per-decision
+        error of 1e-13 relative in the velocities already breaks it."""
     icm = import_pkg("ic")
-    nenv = 64
-    sim = _sim(nenv)
-    sim.seed_rows(torch.as_tensor(icm.sample_headon(nenv, seed=0), device=gpu))
+    ic, acts = oracle_lib.c1_replicas(icm)
+    env = oracle_lib.golden("drift_envelope.npz")
+    sim = _sim(len(ic) // 2)
+    sim.seed_rows(torch.as_tensor(ic, device=gpu))
     st = np.ascontiguousarray(sim.states.cpu().numpy())
-    acts = icm.random_bin_actions(600, 2 * nenv, seed=0)
-    alive = np.ones(2 * nenv, bool)
-    for d in range(600):
+    alive = np.ones(len(ic), bool)
+    for d in range(oracle_lib.DRIFT_NDEC):
+        prev = np.ascontiguousarray(sim.states.cpu().numpy())
         sim.step(torch.as_tensor(acts[d], device=gpu), want_obs=False)
         orc.step(st, acts[d], 6, want_obs=False)
-        if d >= 100 and d < 599:
-            continue
         g = sim.states.cpu().numpy()
-        alt_m = (np.linalg.norm(st[:, 0:3], axis=1) - 20925646.32546) * 0.3048
-        alive &= alt_m > 304.8
+        orc.step(prev, acts[d], 6, want_obs=False)            # the shadow step
+        up = (oracle_lib.altitude_m(g) > 304.8) & np.isfinite(prev).all(1)
+        assert oracle_lib.rel_err(g[up], prev[up]).max() <= STEP_TOL, d
+        alive &= oracle_lib.altitude_m(st) > 304.8
         if d < 50:
             assert oracle_lib.rel_err(g[alive], st[alive]).max() <= 1e-6, d
-        if d < 100:
-            assert np.abs(g[alive, 0:3] - st[alive, 0:3]).max() <= 1e-2, d
-    g = sim.states.cpu().numpy()
-    bad_gpu = int((~np.isfinite(g).all(1)).sum())
-    bad_cpu = int((~np.isfinite(st).all(1)).sum())
-    assert abs(bad_gpu - bad_cpu) <= 4
+        if d % 10 == 9:
+            q = oracle_lib.drift_quantiles(g, st, alive)
+            bound = oracle_lib.drift_envelope(env, d)
+            assert (q <= bound).all(), (d + 1, q, bound)
+    assert alive.sum() > 100                                  # the tail still has a sample
 
 
 def test_state_view_contract(gpu, orc):

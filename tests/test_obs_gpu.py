@@ -234,6 +234,43 @@ def test_external_214_matches_oracle(gpu, orc, nenv):
     np.testing.assert_array_equal(obs184[:, 164:], obs[:, 194:])
 
 
+def test_golden_replay_214_matches_root_reference(gpu):
+    """The scripted sequence through the GPU's 214-D path against the root lineage's own torch
+    path (cuda_fdm/obs_reward.py advance :544-582, build_obs :585-721; golden written by
+    tests/golden/make_obs_golden.py --root214): observation, acceleration and the previous NED
+    velocity after every decision and after the masked resets."""
+    g = oracle_lib.golden("obs_golden.npz")
+    a = oracle_lib.golden("obs214_golden.npz")
+    nenv = g["in_reset"].shape[1]
+    obr = _obr(nenv, ext=True)
+    obr.hp.copy_(torch.as_tensor(g["in_hp0"], device=gpu))
+    obr.t_sec.copy_(torch.as_tensor(g["in_t0"], device=gpu))
+    obr.kernel_init_reward_state(_soa(gpu, g["in_states"][0]))
+    c = lambda t: t.detach().cpu().numpy().astype(np.float64)
+    for k in range(g["in_actions"].shape[0]):
+        st = _soa(gpu, g["in_states"][k])
+        act = torch.as_tensor(g["in_actions"][k], device=gpu)
+        r, te, tr = obr.kernel_advance(st, act)
+        obs = obr.build_external_obs(st).cpu().numpy()
+        assert np.abs(obs - a["a214_obs"][k]).max() <= OBS_TOL, (k, "obs")
+        assert np.abs(c(obr.external_accel) - a["a214_accel"][k]).max() <= VAL_TOL * 100, k
+        assert np.abs(c(obr.external_previous_velocity)
+                      - a["a214_prev_vel_ned"][k]).max() <= VAL_TOL * 300, k
+        assert np.abs(c(r) - a["a214_reward"][k]).max() <= VAL_TOL, (k, "reward")
+        np.testing.assert_array_equal(te.cpu().numpy().astype(bool), a["a214_term"][k])
+        np.testing.assert_array_equal(tr.cpu().numpy().astype(bool), a["a214_trunc"][k])
+        if g["in_reset"][k].any():
+            mask = torch.as_tensor(g["in_reset"][k], device=gpu)
+            str_ = _soa(gpu, g["in_states_reset"][k])
+            obr.reset_envs(mask)
+            obr.kernel_init_reward_state(str_, mask)
+            obs = obr.build_external_obs(str_).cpu().numpy()
+            assert np.abs(obs - a["a214_obs_reset"][k]).max() <= OBS_TOL, (k, "obs_reset")
+            acc = c(obr.external_accel)
+            assert np.abs(acc - a["a214_accel_reset"][k]).max() <= VAL_TOL * 100, k
+            assert np.all(acc[np.repeat(g["in_reset"][k], 2)] == 0.0), k
+
+
 def test_state9_kernel(gpu, orc):
     nenv = 256
     sim = _random_states(gpu, nenv, 61)

@@ -118,3 +118,128 @@ def test_damage_rate_tiers(orc):
     assert abs(ob.hp[1] - (1.0 - rate * 0.1)) < 1e-15
     assert ob.hp[0] == 1.0                     # plane 1 looks away (ATA 180)
     assert abs(ob.dealt[0] - rate) < 1e-15 and abs(ob.taken[1] - rate) < 1e-15
+
+
+# ------------------------------------------------------------------ 214-D acceleration block
+ACC0 = 164          # 214-D: own accel x 5 frames at [164:179], target accel x 5 at [179:194]
+
+
+@pytest.fixture(scope="module")
+def gold214():
+    return oracle_lib.golden("obs214_golden.npz")
+
+
+def test_obs214_oracle_matches_root_reference(orc, gold, gold214):
+    """The oracle's 214-D path against the root lineage's own CPU torch path
+    (cuda_fdm/obs_reward.py BatchObsReward(device="cpu", enable_kernel=False): advance's NED
+    velocity difference at :569-575 and build_obs's accel columns at :702-712), driven by
+    tests/golden/make_obs_golden.py --root214 on the 184-D golden's scripted states."""
+    g, a = gold, gold214
+    nenv = g["in_reset"].shape[1]
+    ob = oracle_lib.ObrOracle(orc, nenv, accel=True)
+    ob.hp[:] = g["in_hp0"]
+    ob.t_sec[:] = g["in_t0"]
+    ob.init_reward(ob.state9(g["in_states"][0]))
+    for k in range(g["in_actions"].shape[0]):
+        s9 = ob.state9(g["in_states"][k])
+        r, te, tr = ob.step(s9, g["in_actions"][k])
+        obs = ob.build_obs(s9, obs_dim=214)
+        assert np.abs(obs.astype(np.float64) - a["a214_obs"][k]).max() <= 1e-6, k
+        assert np.abs(ob.accel - a["a214_accel"][k]).max() <= 1e-9, k
+        assert np.abs(ob.prev_vel_ned - a["a214_prev_vel_ned"][k]).max() <= 1e-9, k
+        assert np.abs(r - a["a214_reward"][k]).max() <= 1e-10, k
+        np.testing.assert_array_equal(te, a["a214_term"][k])
+        np.testing.assert_array_equal(tr, a["a214_trunc"][k])
+        m = g["in_reset"][k]
+        s9r = ob.state9(g["in_states_reset"][k])
+        if m.any():
+            ob.reset_envs(m)
+            ob.init_reward(s9r, m)
+        obs = ob.build_obs(s9r, obs_dim=214)
+        assert np.abs(obs.astype(np.float64) - a["a214_obs_reset"][k]).max() <= 1e-6, k
+        assert np.abs(ob.accel - a["a214_accel_reset"][k]).max() <= 1e-9, k
+        assert np.abs(ob.prev_vel_ned - a["a214_prev_vel_ned_reset"][k]).max() <= 1e-9, k
+
+
+def test_obs214_golden_is_the_184_layout_plus_accel(gold, gold214):
+    """The root lineage's 214-D row is the 184-D row with the acceleration block spliced in
+    before the action history (claude_code/my_observation.py VECTOR_SPECS: own_accel and
+    tgt_accel appended after tgt_omega), and its reward under the default configuration equals
+    the 184-D lineage's; the golden must also hold non-zero accelerations to pin anything."""
+    a, g = gold214, gold
+    np.testing.assert_array_equal(a["a214_obs"][..., :ACC0], g["m0_obs"][..., :ACC0])
+    np.testing.assert_array_equal(a["a214_obs"][..., ACC0 + 30:], g["m0_obs"][..., ACC0:])
+    np.testing.assert_array_equal(a["a214_reward"], g["m0_reward"])
+    assert np.all(a["a214_accel"][0] == 0.0)               # first decision: no previous velocity
+    assert np.abs(a["a214_accel"][1:]).max() > 5.0
+    reset_rows = np.repeat(g["in_reset"], 2, axis=1)       # masked resets zero the block
+    assert np.all(a["a214_accel_reset"][reset_rows] == 0.0)
+
+
+def _level_s9(north, east, alt, roll, pitch, yaw, u, v=0.0, w=0.0):
+    return np.array([north, east, -alt, roll, pitch, yaw, u, v, w], np.float64)
+
+
+def test_accel_closed_forms(orc):
+    """Closed forms of the acceleration features, independent of the restatement's formula:
+    (1) constant NED velocity -> zero acceleration in every frame; (2) a body velocity change
+    dv with a known attitude gives R_b2n dv / dt, with R_b2n from scipy's intrinsic Z-Y-X
+    (yaw, pitch, roll) rotation, the aerospace convention; (3) every frame is orthonormal, so
+    each of the 5 frame projections keeps the vector's norm; (4) the target block of one plane
+    is the own block of its partner; (5) the first decision after a reset is zero."""
+    from scipy.spatial.transform import Rotation
+    dt = 0.1
+    rng = np.random.default_rng(3)
+    ob = oracle_lib.ObrOracle(orc, 1, accel=True)
+    att = [(25.0, 10.0, 70.0), (-40.0, -15.0, 200.0)]
+    vb0 = [np.array([220.0, 4.0, 9.0]), np.array([180.0, -6.0, 3.0])]
+
+    def s9_of(vb, att_, pos_shift):
+        rows = []
+        for i in range(2):
+            r, p, y = att_[i]
+            rows.append(_level_s9(3500.0 + 900.0 * i + pos_shift, 200.0 * i, 5000.0 + 50 * i,
+                                  r, p, y, *vb[i]))
+        return np.array(rows)
+
+    s9a = s9_of(vb0, att, 0.0)
+    ob.init_reward(s9a)
+    ob.step(s9a, np.zeros((2, 4)))
+    assert np.all(ob.accel == 0.0)                         # (5): prev_valid was 0
+    obs = ob.build_obs(s9a, obs_dim=214)
+    assert np.all(obs[:, ACC0:ACC0 + 30] == 0.0)
+    # (1) same attitude and body velocity, aircraft moved: velocity in NED unchanged
+    s9b = s9_of(vb0, att, 25.0)
+    ob.step(s9b, np.zeros((2, 4)))
+    np.testing.assert_allclose(ob.accel, 0.0, atol=1e-10)
+    # (2) a body velocity change and a new attitude
+    att2 = [(26.0, 10.5, 71.0), (-39.0, -14.5, 201.0)]
+    vb1 = [vb0[0] + rng.normal(0, 2.0, 3), vb0[1] + rng.normal(0, 2.0, 3)]
+    s9c = s9_of(vb1, att2, 50.0)
+    ob.step(s9c, np.zeros((2, 4)))
+    for i in range(2):
+        Rn0 = Rotation.from_euler("ZYX", att[i][::-1], degrees=True).as_matrix()
+        Rn1 = Rotation.from_euler("ZYX", att2[i][::-1], degrees=True).as_matrix()
+        want = (Rn1 @ vb1[i] - Rn0 @ vb0[i]) / dt
+        np.testing.assert_allclose(ob.accel[i], want, rtol=1e-9, atol=1e-9)
+        assert np.linalg.norm(want) < 150.0                # no clamp below
+    obs = ob.build_obs(s9c, obs_dim=214).astype(np.float64)
+    for i in range(2):
+        own = obs[i, ACC0:ACC0 + 15].reshape(5, 3) * 150.0     # normalize(x, -150, 150) = x/150
+        np.testing.assert_allclose(own[0], ob.accel[i], rtol=0, atol=150.0 * 2e-7)  # world
+        np.testing.assert_allclose(np.linalg.norm(own, axis=1), np.linalg.norm(ob.accel[i]),
+                                   rtol=1e-5)                                     # (3)
+        # body frame = R_n2b a
+        Rn1 = Rotation.from_euler("ZYX", att2[i][::-1], degrees=True).as_matrix()
+        np.testing.assert_allclose(own[1], Rn1.T @ ob.accel[i], rtol=0, atol=150.0 * 2e-7)
+        # (4) the partner's target block: world, mybody(own body), oppbody, myvel, los of the
+        # partner hold this plane's acceleration
+        tgt = obs[i ^ 1, ACC0 + 15:ACC0 + 30].reshape(5, 3) * 150.0
+        np.testing.assert_allclose(tgt[0], ob.accel[i], rtol=0, atol=150.0 * 2e-7)
+        np.testing.assert_allclose(tgt[2], Rn1.T @ ob.accel[i], rtol=0, atol=150.0 * 2e-7)
+        np.testing.assert_allclose(np.linalg.norm(tgt, axis=1), np.linalg.norm(ob.accel[i]),
+                                   rtol=1e-5)
+    # (5) a masked reset zeroes the block and its history
+    ob.reset_envs(np.array([True]))
+    ob.step(s9c, np.zeros((2, 4)))
+    assert np.all(ob.accel == 0.0)

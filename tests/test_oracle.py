@@ -5,6 +5,7 @@ order; a dropped term) fails it: closed forms and textbook formulas, invariants,
 small tables, values printed in the reference's own generated header, golden vectors written
 from the reference's Python, and the reference's own host-compiled C model (oracle/_ref)."""
 import ast
+import importlib
 import math
 import os
 import re
@@ -352,3 +353,41 @@ def test_substep_count_equivalence(orc):
     for _ in range(6):
         orc.step(b, act, 1)
     assert np.array_equal(a, b)
+
+
+# ------------------------------------------------------------------ drift envelope (C1)
+def test_drift_envelope_fixture_shape():
+    """The reference pair's curve (tests/golden/make_drift_envelope.py): quantiles ordered,
+    the survivor count non-increasing, and the pair bit-identical over the first 50 decisions
+    (fdm.cuh and the Python model round differently only in a few expressions)."""
+    env = oracle_lib.golden("drift_envelope.npz")
+    q = env["pos_ft"]
+    assert q.shape == (oracle_lib.DRIFT_NDEC, len(oracle_lib.DRIFT_QUANTILES))
+    assert (np.diff(q, axis=1) >= 0).all()
+    assert (np.diff(env["alive"]) <= 0).all() and env["alive"][0] == 1024
+    assert (q[:50] == 0).all() and q[-1, -1] > 0
+
+
+def test_drift_envelope_rejects_planted_drift(orc):
+    """The GPU drift bound has power: the CPU model against itself with the velocities of every
+    aircraft perturbed by 1e-13 relative (normal, per decision) breaks the envelope well inside
+    the 600 decisions, while the unperturbed pair never does."""
+    icm = importlib.import_module("2026_ai_pilot_challenge-1st_solution_amd.ic")
+    ic, acts = oracle_lib.c1_replicas(icm)
+    env = oracle_lib.golden("drift_envelope.npz")
+    a = orc.seed(ic, 120)
+    b, c = a.copy(), a.copy()
+    alive = np.ones(len(a), bool)
+    rng = np.random.default_rng(0)
+    broke = None
+    for d in range(200):
+        for x in (a, b, c):
+            orc.step(x, acts[d], 6, want_obs=False)
+        b[:, 3:6] *= 1.0 + 1e-13 * rng.standard_normal((len(b), 3))
+        alive &= oracle_lib.altitude_m(a) > 304.8
+        if d % 10 == 9:
+            bound = oracle_lib.drift_envelope(env, d)
+            assert (oracle_lib.drift_quantiles(a, c, alive) <= bound).all()
+            if broke is None and (oracle_lib.drift_quantiles(a, b, alive) > bound).any():
+                broke = d + 1
+    assert broke is not None and broke <= 150, broke

@@ -77,12 +77,20 @@ BUFFERS = ("b_obs", "b_act", "b_logp", "b_rew", "b_val", "b_done", "last_val", "
            "finite_acc")
 
 
-def _same_rollouts(a, b, n=4, refresh_at=2):
+def _same_rollouts(a, b, n=4, refresh_at=2, outside_at=None):
     """n rollouts of the eager collector `a` and the graph collector `b`, with host work and
     synchronisation between replays; every buffer, the GAE outputs and the env state agree bit
     for bit after each one.  Before rollout `refresh_at` both networks' weights change and are
-    re-packed (the graph picks up the refreshed blobs)."""
+    re-packed (the graph picks up the refreshed blobs).  Before rollout `outside_at` both envs
+    take three steps outside the collectors (an evaluation on the same env), which advance the
+    envs' draw counters on the host only; the next replay must continue from them."""
     for r in range(n):
+        if r == outside_at:
+            act = torch.zeros(a.env.nac, 4, dtype=torch.float64, device=a.device)
+            act[:, 3] = 0.7
+            for ro in (a, b):
+                for _ in range(3):
+                    ro.env.step(act)
         if r == refresh_at:
             for ro in (a, b):
                 with torch.no_grad():
@@ -107,6 +115,15 @@ def test_graph_rollout_equals_eager(gpu):
     a = _collector(gpu, nenv=512, T=8, stats=False)
     b = _collector(gpu, nenv=512, T=8, stats=False, graph=True)
     _same_rollouts(a, b)
+
+
+def test_graph_rollout_after_outside_env_steps(gpu):
+    """Env steps taken between two replays (outside the graph) move the replay's draw counters
+    on as they move the eager collector's: the device counters are refilled from the host's
+    before every replay."""
+    a = _collector(gpu, nenv=256, T=6, stats=False)
+    b = _collector(gpu, nenv=256, T=6, stats=False, graph=True)
+    _same_rollouts(a, b, n=4, refresh_at=None, outside_at=3)
 
 
 def test_graph_league_rollout_equals_eager(gpu):
