@@ -110,6 +110,8 @@ _SIGNATURES = {
     "f16_group_workspace_bytes": (_l, [_i]),
     "f16_norm_update": (_i, [_vp, _l, _vp, _i, _i, _vp, _vp, _vp, _vp, _vp]),
     "f16_norm_merge": (_i, [_i, _i, _vp, _vp, _vp, _vp]),
+    "f16_norm_noalloc_max_bytes": (_l, []),
+    "f16_norm_update_noalloc": (_i, [_vp, _l, _vp, _i, _i, _vp, _vp, _vp, _vp]),
     "f16_ppo_param_counts": (_i, [_i, ctypes.POINTER(_l)]),
     "f16_ppo_workspace_bytes": (_l, [_i, _i]),
     "f16_ppo_grad": (_i, [ctypes.POINTER(F16PPOArgs), _vp]),

@@ -16,6 +16,8 @@
 
 #include <stdint.h>
 
+#include <mutex>
+
 #include "f16_capi_common.h"
 #include "f16_policy.h"
 #include "f16_ppo.h"
@@ -529,4 +531,56 @@ extern "C" int f16_norm_update(const float* obs, long obs_ld, const int* rows, i
   hipLaunchKernelGGL(norm_merge_kernel, dim3(obs_dim), dim3(kMergeThreads), 0, s,
                      (const double*)partial, nb, nrows, obs_dim, mean, var, snap);
   return f16_last_error();
+}
+
+// ------------------------------------------------------------------ allocation-free norm update
+// f16_norm_update with its workspace in a fixed device array instead of a caller buffer, for
+// callers that cannot allocate.  `scratch` is a file-scope __device__ array: the code object
+// holds one copy of it on every GPU it is loaded on, kept until the process ends.  Host code
+// never passes the symbol itself (on the host it names a stand-in, not device memory): the
+// device address is looked up once per device with hipGetSymbolAddress and kept in
+// g_scratch_dev[], and only that address reaches kernels.  Both kernels write every workspace
+// value they later read (per-block partial sums of every column, the count snapshot), so the
+// array needs no clearing between calls.  Calls that overlap on one GPU share the array and
+// race.
+constexpr long kNoAllocScratchBytes = 8l << 20;          // 8 MiB per GPU
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_dev[kMaxDevices];   // device address of `scratch` on each device, or null
+
+// The device address of `scratch` on the current device, looked up on the first call there.
+int scratch_address(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return -(1000 + (int)e);
+  if (dev < 0 || dev >= kMaxDevices) return F16_EINVAL;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return -(1000 + (int)e);
+    if (!p) return F16_EINVAL;
+    g_scratch_dev[dev] = p;
+  }
+  *out = g_scratch_dev[dev];
+  return 0;
+}
+}  // namespace
+
+extern "C" long f16_norm_noalloc_max_bytes(void) { return kNoAllocScratchBytes; }
+
+extern "C" int f16_norm_update_noalloc(const float* obs, long obs_ld, const int* rows, int nrows,
+                                       int obs_dim, float* mean, float* var, float* count,
+                                       void* stream) {
+  if (nrows < 0 || obs_dim < 1 || obs_dim > kNormCols || obs_ld < obs_dim) return F16_EINVAL;
+  if (nrows == 0) return 0;
+  if (!obs || !mean || !var || !count) return F16_EINVAL;
+  if (f16_norm_workspace_bytes(nrows, obs_dim) > kNoAllocScratchBytes) return F16_ETOOBIG;
+  void* work = nullptr;
+  const int rc = scratch_address(&work);
+  if (rc) return rc;
+  return f16_norm_update(obs, obs_ld, rows, nrows, obs_dim, mean, var, count, work, stream);
 }

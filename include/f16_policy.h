@@ -98,6 +98,18 @@ long f16_norm_workspace_bytes(int nrows, int obs_dim);
 int f16_norm_update(const float *obs, long obs_ld, const int *rows, int nrows, int obs_dim,
                     float *mean, float *var, float *count, void *work, void *stream);
 
+/* f16_norm_update without a workspace argument, for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * No counterpart in the reference.  The partial sums live in a fixed 8 MiB device array of the
+ * library (one per GPU, held until the process ends; f16_norm_noalloc_max_bytes() returns its
+ * size): a batch whose f16_norm_workspace_bytes(nrows, obs_dim) exceeds it is rejected with
+ * F16_ETOOBIG (262,144 rows of 214 columns fit).  Calls no allocating routine.  Every call on
+ * one GPU shares the array, so calls that overlap on one GPU (two streams, two host threads)
+ * race; calls ordered on one stream do not.  Results equal f16_norm_update's bit for bit. */
+long f16_norm_noalloc_max_bytes(void);
+int f16_norm_update_noalloc(const float *obs, long obs_ld, const int *rows, int nrows,
+                            int obs_dim, float *mean, float *var, float *count, void *stream);
+
 /* The second half of f16_norm_update alone: merge the per-block partial sums already in `work`
  * (written by a launch that formed them, e.g. f16_env_post_step with io->norm_partial) into
  * mean/var with the count snapshot kept at the workspace's end.  f16_norm_update(obs, ...) and
