@@ -47,7 +47,8 @@ class F16EnvStepIO(ctypes.Structure):
                 ("done", _vp), ("done_f32", _vp), ("terminal_hp", _vp),
                 ("terminal_alt_m", _vp), ("terminal_finite", _vp), ("finite_acc", _vp),
                 ("opp_assign", _vp), ("opp_cdf", _vp), ("n_opp", _i), ("step_base", _vp),
-                ("norm_partial", _vp), ("norm_count", _vp), ("norm_count_snap", _vp)]
+                ("norm_partial", _vp), ("norm_count", _vp), ("norm_count_snap", _vp),
+                ("state_finite", _vp)]
 
 
 class F16PolicyGroup(ctypes.Structure):
@@ -88,6 +89,7 @@ class F16AdamArgs(ctypes.Structure):
 _RP, _CP = ctypes.POINTER(F16Recon), ctypes.POINTER(F16RewardCfg)
 _SIGNATURES = {
     "f16_fdm_step_batch": (_i, [_vp, _l, _vp, _i, _i, _i, _vp, _l, _vp]),
+    "f16_fdm_step_batch_finite": (_i, [_vp, _l, _vp, _i, _i, _i, _vp, _l, _vp, _vp]),
     "f16_fdm_step_batch_onelane": (_i, [_vp, _l, _vp, _i, _i, _i, _vp, _l, _vp]),
     "f16_seed_batch": (_i, [_vp, _i, _i, _vp, _l, _vp, _vp]),
     "f16_fdm_kernel_info": (_i, [_i, ctypes.POINTER(_i)]),

@@ -53,10 +53,11 @@ __global__ __launch_bounds__(kBlock) void fdm_step_kernel(double* __restrict__ s
 // Two wavefronts per 64 aircraft (fdm_split.h): even waves fly, odd waves run the systems.
 // The role is wave-uniform (a scalar branch), so each role's loop issues its own barriers and
 // the two loops' barrier counts match (3 per substep each).
+// `fin` (optional, S >= 1): per aircraft, 1 if all 101 state values after the call are finite.
 template <int FCS_RATE>
 __global__ __launch_bounds__(kSplitBlock) void fdm_step_split_kernel(
     double* __restrict__ st, long ld, const double* __restrict__ act, int nac, int S,
-    double* __restrict__ obs, long obs_ld) {
+    double* __restrict__ obs, long obs_ld, unsigned char* __restrict__ fin) {
   __shared__ double T[F16M_IMAGE_LEN];
   __shared__ SplitX X[kSplitPairs];
   stage_image<kSplitBlock>(T);
@@ -67,9 +68,11 @@ __global__ __launch_bounds__(kSplitBlock) void fdm_step_split_kernel(
   const bool store = i < nac;
   const int ia = store ? i : nac - 1;   // lanes past the batch shadow the last aircraft
   if ((wave & 1) == 0)
-    split_flight<FCS_RATE>(st + ia, ld, S, store, obs ? obs + ia : nullptr, obs_ld, T, X[pair], lane);
+    split_flight<FCS_RATE>(st + ia, ld, S, store, obs ? obs + ia : nullptr, obs_ld, T, X[pair],
+                           lane, fin != nullptr);
   else
-    split_systems<FCS_RATE>(st + ia, ld, act + 4L * ia, S, store, T, X[pair], lane);
+    split_systems<FCS_RATE>(st + ia, ld, act + 4L * ia, S, store, T, X[pair], lane,
+                            fin ? fin + ia : nullptr);
 }
 
 // ------------------------------------------------------------------ IC seeding
@@ -241,18 +244,33 @@ static int fdm_step_args(double* states, long ld, const double* actions, int nac
   return 0;
 }
 
+static int fdm_step_split(double* states, long ld, const double* actions, int nac, int substeps,
+                          int fcs_rate, double* obs, long obs_ld, unsigned char* fin,
+                          void* stream) {
+  const dim3 grid((nac + f16::kSplitAircraft - 1) / f16::kSplitAircraft), block(f16::kSplitBlock);
+  hipStream_t s = (hipStream_t)stream;
+  if (fcs_rate == 120)
+    hipLaunchKernelGGL(f16::fdm_step_split_kernel<120>, grid, block, 0, s, states, ld, actions, nac, substeps, obs, obs_ld, fin);
+  else
+    hipLaunchKernelGGL(f16::fdm_step_split_kernel<60>, grid, block, 0, s, states, ld, actions, nac, substeps, obs, obs_ld, fin);
+  return f16_last_error();
+}
+
 extern "C" int f16_fdm_step_batch(double* states, long ld, const double* actions, int nac,
                                   int substeps, int fcs_rate, double* obs, long obs_ld,
                                   void* stream) {
   const int rc = fdm_step_args(states, ld, actions, nac, substeps, fcs_rate, obs, obs_ld);
   if (rc) return rc < 0 ? rc : 0;
-  const dim3 grid((nac + f16::kSplitAircraft - 1) / f16::kSplitAircraft), block(f16::kSplitBlock);
-  hipStream_t s = (hipStream_t)stream;
-  if (fcs_rate == 120)
-    hipLaunchKernelGGL(f16::fdm_step_split_kernel<120>, grid, block, 0, s, states, ld, actions, nac, substeps, obs, obs_ld);
-  else
-    hipLaunchKernelGGL(f16::fdm_step_split_kernel<60>, grid, block, 0, s, states, ld, actions, nac, substeps, obs, obs_ld);
-  return f16_last_error();
+  return fdm_step_split(states, ld, actions, nac, substeps, fcs_rate, obs, obs_ld, nullptr, stream);
+}
+
+extern "C" int f16_fdm_step_batch_finite(double* states, long ld, const double* actions, int nac,
+                                         int substeps, int fcs_rate, double* obs, long obs_ld,
+                                         unsigned char* finite, void* stream) {
+  if (substeps < 1 || !finite) return F16_EINVAL;
+  const int rc = fdm_step_args(states, ld, actions, nac, substeps, fcs_rate, obs, obs_ld);
+  if (rc) return rc < 0 ? rc : 0;
+  return fdm_step_split(states, ld, actions, nac, substeps, fcs_rate, obs, obs_ld, finite, stream);
 }
 
 extern "C" int f16_fdm_step_batch_onelane(double* states, long ld, const double* actions,

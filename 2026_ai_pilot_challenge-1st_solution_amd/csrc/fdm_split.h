@@ -57,7 +57,9 @@ enum SplitField : int {
   // X3, systems -> flight
   kXThrust, kXCe, kXSe,
   // the mass block again: substep t's mass properties live in block t & 1 (below)
-  kXMass2, kSplitFields = kXMass2 + (kXAil - kXMass)
+  kXMass2, kXFin = kXMass2 + (kXAil - kXMass),
+  // after the last substep, flight -> systems: every value the flight wave wrote is finite
+  kSplitFields
 };
 
 // Mass properties are written by the systems wave in its first phase and read by the flight
@@ -68,13 +70,26 @@ __device__ __forceinline__ int mass_block(int t) { return (t & 1) ? kXMass2 - kX
 
 typedef double SplitX[kSplitFields][64];
 
+// Finite-flag accumulator: the largest IEEE exponent field seen (high word & 0x7ff00000); every
+// value was finite iff the result is below 0x7ff00000.  Two 32-bit VALU operations per value,
+// no lane masks.
+__device__ __forceinline__ unsigned fin_acc(unsigned m, double x) {
+  const unsigned hi = (unsigned)((unsigned long long)__double_as_longlong(x) >> 32);
+  return max(m, hi & 0x7ff00000u);
+}
+constexpr unsigned kFinInf = 0x7ff00000u;
+
 // The flight wave of one pair.  `s`: the aircraft's state field 0 (fields `ld` apart); `store`:
 // whether this lane's aircraft exists (lanes past the batch shadow the last aircraft and store
 // nothing).  Issues exactly 3 barriers per substep, like split_systems.
+// With `fin` set, the wave also reports through x[kXFin] whether every state value it wrote
+// (or, for S < 3, shifted) is finite, after one more workgroup barrier that split_systems
+// matches.
 template <int FCS_RATE>
 __device__ __forceinline__ void split_flight(double* __restrict__ s, long ld, int S, bool store,
                                              double* __restrict__ o, long obs_ld,
-                                             const double* __restrict__ T, SplitX& x, int lane) {
+                                             const double* __restrict__ T, SplitX& x, int lane,
+                                             bool fin) {
 #define F(k) s[(long)(k) * ld]
   Aircraft a;
 #pragma unroll
@@ -87,16 +102,28 @@ __device__ __forceinline__ void split_flight(double* __restrict__ s, long ld, in
 #pragma unroll
   for (int j = 0; j < 4; ++j) { a.q[j] = F(F16S_Q + j); a.qd[j] = F(F16S_QDOT + j); }
   a.epa = F(F16S_EPA);
+  // Finite flag: the history values this call writes inside the substep loop are the qd, wdi,
+  // v, ai each following substep integrates by plain sums (q += dt qd, wi += dt wdi, AB2/AB3 on
+  // ai and v, no clamps), so a non-finite one leaves a non-finite q, wi, v or p at the end; only
+  // the older entries shifted down when S < 3 need their own test.
+  unsigned hist_m = 0u;
   // fewer than three substeps keep older history entries, shifted down by S
   if (store && S > 0 && S < 3) {
     for (int k = 2; k >= S; --k) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) F(F16S_DQ + 4 * k + j) = F(F16S_DQ + 4 * (k - S) + j);
+      for (int j = 0; j < 4; ++j) {
+        const double h = F(F16S_DQ + 4 * (k - S) + j);
+        hist_m = fin_acc(hist_m, h);
+        F(F16S_DQ + 4 * k + j) = h;
+      }
 #pragma unroll
       for (int j = 0; j < 3; ++j) {
-        F(F16S_DPQRI + 3 * k + j) = F(F16S_DPQRI + 3 * (k - S) + j);
-        F(F16S_DIVEL + 3 * k + j) = F(F16S_DIVEL + 3 * (k - S) + j);
-        F(F16S_DUVW + 3 * k + j) = F(F16S_DUVW + 3 * (k - S) + j);
+        const double h1 = F(F16S_DPQRI + 3 * (k - S) + j), h2 = F(F16S_DIVEL + 3 * (k - S) + j);
+        const double h3 = F(F16S_DUVW + 3 * (k - S) + j);
+        hist_m = fin_acc(fin_acc(fin_acc(hist_m, h1), h2), h3);
+        F(F16S_DPQRI + 3 * k + j) = h1;
+        F(F16S_DIVEL + 3 * k + j) = h2;
+        F(F16S_DUVW + 3 * k + j) = h3;
       }
     }
   }
@@ -204,36 +231,52 @@ __device__ __forceinline__ void split_flight(double* __restrict__ s, long ld, in
       a.ppd[i] = ac.wdi[i]; a.ppq[i] = ac.ppq[i];
     }
   }
-  if (!store || S <= 0) return;
-#pragma unroll
-  for (int j = 0; j < 3; ++j) {
-    F(F16S_POS + j) = a.p[j]; F(F16S_VEL + j) = a.v[j]; F(F16S_PQRI + j) = a.wi[j];
-    F(F16S_UVWIDOT + j) = a.ai[j]; F(F16S_PQRIDOT + j) = a.wdi[j];
-    F(F16S_PBA + j) = a.pba[j]; F(F16S_PPQRIDOT + j) = a.ppd[j]; F(F16S_PPQRI + j) = a.ppq[j];
-  }
-#pragma unroll
-  for (int j = 0; j < 4; ++j) { F(F16S_Q + j) = a.q[j]; F(F16S_QDOT + j) = a.qd[j]; }
-  F(F16S_EPA) = a.epa;
-#undef F
-  if (o) {
+  if (store && S > 0) {
 #pragma unroll
     for (int j = 0; j < 3; ++j) {
-      o[(long)j * obs_ld] = a.p[j];
-      o[(long)(3 + j) * obs_ld] = a.v[j];
-      o[(long)(6 + j) * obs_ld] = euler[j];
-      o[(long)(9 + j) * obs_ld] = k.uvw[j];
+      F(F16S_POS + j) = a.p[j]; F(F16S_VEL + j) = a.v[j]; F(F16S_PQRI + j) = a.wi[j];
+      F(F16S_UVWIDOT + j) = a.ai[j]; F(F16S_PQRIDOT + j) = a.wdi[j];
+      F(F16S_PBA + j) = a.pba[j]; F(F16S_PPQRIDOT + j) = a.ppd[j]; F(F16S_PPQRI + j) = a.ppq[j];
     }
-    o[12L * obs_ld] = g.alpha; o[13L * obs_ld] = g.beta; o[14L * obs_ld] = mach;
-    o[15L * obs_ld] = g.vt; o[16L * obs_ld] = alt;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) { F(F16S_Q + j) = a.q[j]; F(F16S_QDOT + j) = a.qd[j]; }
+    F(F16S_EPA) = a.epa;
+    if (o) {
+#pragma unroll
+      for (int j = 0; j < 3; ++j) {
+        o[(long)j * obs_ld] = a.p[j];
+        o[(long)(3 + j) * obs_ld] = a.v[j];
+        o[(long)(6 + j) * obs_ld] = euler[j];
+        o[(long)(9 + j) * obs_ld] = k.uvw[j];
+      }
+      o[12L * obs_ld] = g.alpha; o[13L * obs_ld] = g.beta; o[14L * obs_ld] = mach;
+      o[15L * obs_ld] = g.vt; o[16L * obs_ld] = alt;
+    }
+  }
+#undef F
+  if (fin) {   // every flight-side value stored above (the loop's history: see hist_m)
+    unsigned m = fin_acc(hist_m, a.epa);
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      m = fin_acc(fin_acc(fin_acc(fin_acc(m, a.p[j]), a.v[j]), a.wi[j]), a.ai[j]);
+      m = fin_acc(fin_acc(fin_acc(fin_acc(m, a.wdi[j]), a.pba[j]), a.ppd[j]), a.ppq[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) m = fin_acc(fin_acc(m, a.q[j]), a.qd[j]);
+    x[kXFin][lane] = m < kFinInf ? 1.0 : 0.0;
+    __syncthreads();
   }
 }
 
 // The systems wave of one pair: fuel, engine, FCS and previous-frame auxiliary state.
 // Issues exactly 3 barriers per substep, like split_flight.
+// With `fin` non-null, fin[0] <- 1 if every one of the aircraft's 101 state values after the
+// call is finite, else 0 (the flight wave's share arrives through x[kXFin]).
 template <int FCS_RATE>
 __device__ __forceinline__ void split_systems(double* __restrict__ s, long ld,
                                               const double* __restrict__ act4, int S, bool store,
-                                              const double* __restrict__ T, SplitX& x, int lane) {
+                                              const double* __restrict__ T, SplitX& x, int lane,
+                                              unsigned char* __restrict__ fin) {
 #define F(k) s[(long)(k) * ld]
   Aircraft a;
 #pragma unroll
@@ -246,13 +289,17 @@ __device__ __forceinline__ void split_systems(double* __restrict__ s, long ld,
   a.k_tef = F(F16S_KIN); a.k_ail = F(F16S_KIN + 1); a.k_ele = F(F16S_KIN + 2); a.k_lef = F(F16S_KIN + 5);
   const double c_ail = act4[0], c_ele = act4[1], c_rud = act4[2], c_thr = act4[3];
   double k_rud = 0.0;
+  unsigned ip2_m = 0u;   // finite-flag accumulator of the PID input_prev2 values written below
   for (int t = 0; t < S; ++t) {
     const int slot = S - 1 - t;
     // ---- phase 1
     a.epa += kRot * kDt;        // the flight wave's propagate makes the same increment
     if (store && slot == 0) {   // PID input_prev2 = input_prev before the final update
 #pragma unroll
-      for (int j = 0; j < 3; ++j) F(F16S_PID + 3 * j + 1) = a.pid_ip[j];
+      for (int j = 0; j < 3; ++j) {
+        F(F16S_PID + 3 * j + 1) = a.pid_ip[j];
+        ip2_m = fin_acc(ip2_m, a.pid_ip[j]);
+      }
     }
     const Mass mb = mass_props(a.fuel);
     FcsOut fc;
@@ -296,16 +343,28 @@ __device__ __forceinline__ void split_systems(double* __restrict__ s, long ld,
     a.pa[0] = alpha; a.pa[1] = mach; a.pa[2] = vc; a.pa[3] = vg;
     a.pa[4] = npy; a.pa[5] = npz; a.pa[6] = p; a.pa[7] = q; a.pa[8] = r;
   }
-  if (!store || S <= 0) return;
+  if (store && S > 0) {
 #pragma unroll
-  for (int j = 0; j < 3; ++j) { F(F16S_PID + 3 * j) = a.pid_ip[j]; F(F16S_PID + 3 * j + 2) = a.pid_io[j]; }
+    for (int j = 0; j < 3; ++j) { F(F16S_PID + 3 * j) = a.pid_ip[j]; F(F16S_PID + 3 * j + 2) = a.pid_io[j]; }
 #pragma unroll
-  for (int j = 0; j < 9; ++j) F(F16S_PAUX + j) = a.pa[j];
-  F(F16S_FUEL) = a.fuel;
-  F(F16S_ENG) = a.n1; F(F16S_ENG + 1) = a.n2; F(F16S_ENG + 2) = a.n2n; F(F16S_ENG + 3) = a.ff;
-  F(F16S_KIN) = a.k_tef; F(F16S_KIN + 1) = a.k_ail; F(F16S_KIN + 2) = a.k_ele;
-  F(F16S_KIN + 3) = k_rud; F(F16S_KIN + 4) = kGearPos<FCS_RATE>; F(F16S_KIN + 5) = a.k_lef;
+    for (int j = 0; j < 9; ++j) F(F16S_PAUX + j) = a.pa[j];
+    F(F16S_FUEL) = a.fuel;
+    F(F16S_ENG) = a.n1; F(F16S_ENG + 1) = a.n2; F(F16S_ENG + 2) = a.n2n; F(F16S_ENG + 3) = a.ff;
+    F(F16S_KIN) = a.k_tef; F(F16S_KIN + 1) = a.k_ail; F(F16S_KIN + 2) = a.k_ele;
+    F(F16S_KIN + 3) = k_rud; F(F16S_KIN + 4) = kGearPos<FCS_RATE>; F(F16S_KIN + 5) = a.k_lef;
+  }
 #undef F
+  if (fin) {   // every systems-side value stored above, then the flight wave's share
+    unsigned m = fin_acc(fin_acc(fin_acc(fin_acc(ip2_m, a.fuel), a.n1), a.n2), a.n2n);
+    m = fin_acc(fin_acc(fin_acc(fin_acc(m, a.ff), a.k_tef), a.k_ail), a.k_ele);
+    m = fin_acc(fin_acc(m, k_rud), a.k_lef);
+#pragma unroll
+    for (int j = 0; j < 3; ++j) m = fin_acc(fin_acc(m, a.pid_ip[j]), a.pid_io[j]);
+#pragma unroll
+    for (int j = 0; j < 9; ++j) m = fin_acc(m, a.pa[j]);
+    __syncthreads();
+    if (store) fin[0] = (m < kFinInf && x[kXFin][lane] != 0.0) ? 1 : 0;
+  }
 }
 
 }  // namespace f16

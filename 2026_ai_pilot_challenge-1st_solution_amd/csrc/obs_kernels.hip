@@ -814,15 +814,19 @@ __global__ __launch_bounds__(kRowBlock) void env_post_step_kernel(const F16EnvSt
 #pragma unroll
     for (int f = 0; f < 15; ++f) f15[f] = st[f * ld + a];
     if (io.terminal_finite || io.finite_acc) {   // rl_env.py:545: every state value finite
-      // the other 86 fields with all their loads in flight together
       int fin = 1;
+      if (io.state_finite) {                      // formed by the physics launch
+        fin = io.state_finite[a] ? 1 : 0;
+      } else {
+        // the other 86 fields with all their loads in flight together
 #pragma unroll
-      for (int f = 0; f < 15; ++f) fin &= isfinite(f15[f]) ? 1 : 0;
-      double v[F16S_N - 15];
+        for (int f = 0; f < 15; ++f) fin &= isfinite(f15[f]) ? 1 : 0;
+        double v[F16S_N - 15];
 #pragma unroll
-      for (int j = 0; j < F16S_N - 15; ++j) v[j] = st[(15 + j) * ld + a];
+        for (int j = 0; j < F16S_N - 15; ++j) v[j] = st[(15 + j) * ld + a];
 #pragma unroll
-      for (int j = 0; j < F16S_N - 15; ++j) fin &= isfinite(v[j]) ? 1 : 0;
+        for (int j = 0; j < F16S_N - 15; ++j) fin &= isfinite(v[j]) ? 1 : 0;
+      }
       fin &= xchi(fin);
       if (!odd) {
         if (io.terminal_finite) io.terminal_finite[e] = (unsigned char)fin;
@@ -978,13 +982,17 @@ __global__ __launch_bounds__(kPostSplitBlock) void env_post_step_split_kernel(
       for (int f = 0; f < 15; ++f) f15[f] = st[f * ld + a];
       if (io.terminal_finite || io.finite_acc) {   // rl_env.py:545: every state value finite
         int fin = 1;
+        if (io.state_finite) {                      // formed by the physics launch
+          fin = io.state_finite[a] ? 1 : 0;
+        } else {
 #pragma unroll
-        for (int f = 0; f < 15; ++f) fin &= isfinite(f15[f]) ? 1 : 0;
-        double v[F16S_N - 15];
+          for (int f = 0; f < 15; ++f) fin &= isfinite(f15[f]) ? 1 : 0;
+          double v[F16S_N - 15];
 #pragma unroll
-        for (int j = 0; j < F16S_N - 15; ++j) v[j] = st[(15 + j) * ld + a];
+          for (int j = 0; j < F16S_N - 15; ++j) v[j] = st[(15 + j) * ld + a];
 #pragma unroll
-        for (int j = 0; j < F16S_N - 15; ++j) fin &= isfinite(v[j]) ? 1 : 0;
+          for (int j = 0; j < F16S_N - 15; ++j) fin &= isfinite(v[j]) ? 1 : 0;
+        }
         fin &= xchi(fin);
         if (!odd) {
           if (io.terminal_finite) io.terminal_finite[e] = (unsigned char)fin;

@@ -125,10 +125,18 @@ class GpuDogfight:
         _lib.check(rc, "f16_seed_batch")
 
     # ---- step (cuda_fdm/gpu_env.py:95-106) ----
-    def step(self, actions, substeps=None, want_obs=True):
+    def step(self, actions, substeps=None, want_obs=True, finite_out=None):
         """actions (nac,4) or (nenv,ppe,4) [aileron, elevator, rudder, throttle] -> obs view
-        (nenv, ppe, 17).  want_obs=False skips the 17-value output write."""
+        (nenv, ppe, 17).  want_obs=False skips the 17-value output write.  finite_out: an
+        optional (nac,) uint8/bool device tensor that receives, per aircraft, whether all 101
+        state values after the step are finite (f16_fdm_step_batch_finite; substeps >= 1)."""
         ss = self.substeps if substeps is None else int(substeps)
+        if finite_out is not None:
+            if (finite_out.dtype not in (torch.uint8, torch.bool) or finite_out.numel() != self.nac
+                    or not finite_out.is_contiguous() or finite_out.device != self.states.device):
+                raise ValueError("finite_out must be a contiguous (nac,) uint8/bool device tensor")
+            if ss < 1:
+                raise ValueError("finite_out needs substeps >= 1")
         a = torch.as_tensor(actions, dtype=torch.float64, device=self.device).reshape(self.nac, 4)
         if a.data_ptr() != self.actions.data_ptr():
             self.actions.copy_(a)
@@ -136,10 +144,16 @@ class GpuDogfight:
         if ev is not None:
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record()
-        rc = self._lib.f16_fdm_step_batch(
-            _lib.ptr(self._state_soa), self.nac, _lib.ptr(self.actions), self.nac, ss,
-            self.fcs_rate, _lib.ptr(self._obs_soa) if want_obs else None, self.nac,
-            _lib.stream_handle(self.device))
+        obs_p = _lib.ptr(self._obs_soa) if want_obs else None
+        if finite_out is None:
+            rc = self._lib.f16_fdm_step_batch(
+                _lib.ptr(self._state_soa), self.nac, _lib.ptr(self.actions), self.nac, ss,
+                self.fcs_rate, obs_p, self.nac, _lib.stream_handle(self.device))
+        else:
+            rc = self._lib.f16_fdm_step_batch_finite(
+                _lib.ptr(self._state_soa), self.nac, _lib.ptr(self.actions), self.nac, ss,
+                self.fcs_rate, obs_p, self.nac, _lib.ptr(finite_out),
+                _lib.stream_handle(self.device))
         if ev is not None:
             e1.record()
             ev.append((e0, e1))

@@ -76,6 +76,11 @@ class GpuDogfightVecEnv:
         self._rec = self.obr._recon()
         self._cfg, self._cfg_key = None, None
         self._post_steps = 0
+        # per-aircraft "all 101 state values finite" flags, written by the physics launch from
+        # registers and read by the post-physics launch instead of the state (rl_env.py:545);
+        # fused_finite=False makes the post-physics launch read the state and test it itself
+        self._state_fin = torch.empty(n, dtype=torch.uint8, device=dev)
+        self.fused_finite = True
 
     def enable_aux_capture(self):
         """Turn on the future-aux features (BatchObsReward.enable_aux_capture): every step and
@@ -277,7 +282,8 @@ class GpuDogfightVecEnv:
         terminal_obs=False skips the terminal-observation copy (info["terminal_obs"] is None)."""
         a = self._to_nac4(actions)
         self._ensure_ic_pool()
-        self.sim.step(a, substeps=self.substeps, want_obs=False)
+        state_fin = self._state_fin if self.fused_finite and self.substeps >= 1 else None
+        self.sim.step(a, substeps=self.substeps, want_obs=False, finite_out=state_fin)
         if reset_indices is None:
             pick = torch.randint(0, self.ic_pool_size, (self.nenv,), device=self.device,
                                  generator=self.torch_gen)
@@ -295,6 +301,7 @@ class GpuDogfightVecEnv:
         term, trunc, done, fin = (torch.empty(ne, dtype=torch.bool, device=dev) for _ in range(4))
         io = self._io(pick)
         p = lambda t: t.data_ptr() if t is not None else None
+        io.state_finite = p(state_fin)
         io.terminal_obs, io.reward = p(tobs), p(reward)
         io.term, io.trunc, io.done, io.terminal_finite = p(term), p(trunc), p(done), p(fin)
         io.terminal_hp, io.terminal_alt_m = p(terminal_hp), p(terminal_alt)
@@ -321,8 +328,11 @@ class GpuDogfightVecEnv:
         norm (a RunningNorm, only where norm_fusable()): the launch also writes the partial sums
         of the new observation rows into its workspace, for norm.merge(nac)."""
         self._ensure_ic_pool()
-        self.sim.step(self.sim.actions, substeps=self.substeps, want_obs=False)
+        state_fin = self._state_fin if self.fused_finite and self.substeps >= 1 else None
+        self.sim.step(self.sim.actions, substeps=self.substeps, want_obs=False,
+                      finite_out=state_fin)
         io = self._io(None)
+        io.state_finite = state_fin.data_ptr() if state_fin is not None else None
         if step_base is not None:
             io.step, io.step_base = int(step) & 0xffffffff, step_base.data_ptr()
         io.reward_f32, io.done_f32 = reward_f32.data_ptr(), done_f32.data_ptr()

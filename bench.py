@@ -44,30 +44,73 @@ def profiled_traffic(name="fdm_step_split_kernel_tailchase16k.md"):
     return None
 
 
-def cpu_baseline(states0_aos, actions_host, substeps, cpu_seconds):
-    """Time the reference's own C model (oracle/_ref, fdm.cuh built from its sources) on the
-    host cores; fall back to the C restatement (oracle/liborc.so).  Bounded sample."""
+def _host_info():
+    """CPU model, sockets and the compiler/flags the CPU paths were built with."""
+    model, sockets = "unknown", set()
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name") and model == "unknown":
+                model = line.split(":", 1)[1].strip()
+            elif line.startswith("physical id"):
+                sockets.add(line.split(":", 1)[1].strip())
+    except OSError:
+        pass
+    try:
+        import subprocess
+        cc = subprocess.run(["gcc", "--version"], capture_output=True, text=True).stdout
+        cc = cc.splitlines()[0] if cc else "gcc (unknown)"
+    except OSError:
+        cc = "gcc (unknown)"
+    flags = "unknown"
+    for line in open(os.path.join(ROOT, "oracle", "Makefile")):
+        if line.startswith("CFLAGS"):
+            flags = line.split("=", 1)[1].strip()
+    return {"cpu_model": model, "sockets": max(1, len(sockets)), "compiler": cc,
+            "flags": flags, "host_threads": len(os.sched_getaffinity(0))}
+
+
+def _fdm_runner(fcs_rate, substeps):
+    """The reference's own C model (oracle/_ref, fdm.cuh built from its sources) for the host;
+    the C restatement (oracle/liborc.so) where that is absent."""
     D = ctypes.POINTER(ctypes.c_double)
-    ref = os.path.join(ROOT, "oracle", "_ref", "libf16ref_120.so")
+    ref = os.path.join(ROOT, "oracle", "_ref", f"libf16ref_{fcs_rate}.so")
     if os.path.exists(ref):
-        L = ctypes.CDLL(ref)
-        fn = L.ref_fdm_rollout
+        fn = ctypes.CDLL(ref).ref_fdm_rollout
         fn.argtypes = [D, D, ctypes.c_long, ctypes.c_int, ctypes.c_int, ctypes.c_int]
-        kind = "reference"
+        return "reference", lambda st, act, nac, ndec, nth: fn(
+            st.ctypes.data_as(D), act.ctypes.data_as(D), nac, ndec, substeps, nth)
+    fn = ctypes.CDLL(os.path.join(ROOT, "oracle", "liborc.so")).orc_fdm_rollout
+    fn.argtypes = [D, D, ctypes.c_long, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int]
+    return "port", lambda st, act, nac, ndec, nth: fn(
+        st.ctypes.data_as(D), act.ctypes.data_as(D), nac, ndec, substeps, fcs_rate, nth)
 
-        def run(st, act, nac, ndec, nth):
-            fn(st.ctypes.data_as(D), act.ctypes.data_as(D), nac, ndec, substeps, nth)
-    else:
-        L = ctypes.CDLL(os.path.join(ROOT, "oracle", "liborc.so"))
-        fn = L.orc_fdm_rollout
-        fn.argtypes = [D, D, ctypes.c_long, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int]
-        kind = "port"
 
-        def run(st, act, nac, ndec, nth):
-            fn(st.ctypes.data_as(D), act.ctypes.data_as(D), nac, ndec, substeps, 120, nth)
+def _threads_run(fns):
+    """Run the callables on host threads (ctypes calls release the GIL)."""
+    import threading
+    ts = [threading.Thread(target=f) for f in fns]
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join()
+
+
+def cpu_baseline(states0_aos, actions_host, substeps, cpu_seconds, icm):
+    """The reference path on the host cores, bounded samples (each stated in its entry):
+      value: the FDM (16k tail-chase, the GPU's timed decisions cycled for ~cpu_seconds) with
+             the reference's own C model on every host thread, plus a 1-thread figure;
+      c1_full: BASELINE C1 end to end (64 head-on engagements, 600 decisions, 120 Hz FCS);
+      obs_reward_c3: advance + reward + termination + the 184-D observation (the C restatement
+             of BatchObsReward, oracle/obs_oracle.c) over 32,768 aircraft, every host thread;
+      gae_c4: the reference's GAE recurrence (oracle/gae_oracle.py, numpy float32) over
+             [64, 16384, 2];
+      env_transitions_per_s: one env decision at 16k engagements = FDM (60 Hz FCS lineage) +
+             obs/reward, both on every host thread."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_lib
+    kind, run = _fdm_runner(120, substeps)
     cores = len(os.sched_getaffinity(0))
     nac = states0_aos.shape[0]
-    # the same decisions as the GPU's timed steps, cycled until ~cpu_seconds of wall time
     st = states0_aos.copy()
     acts = np.ascontiguousarray(actions_host)
     ndec = 0
@@ -78,40 +121,106 @@ def cpu_baseline(states0_aos, actions_host, substeps, cpu_seconds):
         dt = time.perf_counter() - t0
         if dt >= cpu_seconds:
             break
-    # single-thread figure on a slice
     n1 = min(nac, 256)
     st1 = np.ascontiguousarray(states0_aos[:n1])
     a1 = np.ascontiguousarray(actions_host[:1, :n1])
     t1 = time.perf_counter()
     run(st1, a1, n1, 1, 1)
     dt1 = time.perf_counter() - t1
-    return {"value": nac * substeps * ndec / dt, "unit": "aircraft-substeps/s", "cores": cores,
-            "kind": kind,
-            "sample": f"{nac} aircraft x {ndec} decisions x {substeps} substeps, fp64, OpenMP "
-                      f"over aircraft on {cores} host threads ({dt:.1f} s)",
-            "single_thread": n1 * substeps / dt1}
+    out = {"value": nac * substeps * ndec / dt, "unit": "aircraft-substeps/s", "cores": cores,
+           "kind": kind,
+           "sample": f"{nac} aircraft x {ndec} decisions x {substeps} substeps, fp64, OpenMP "
+                     f"over aircraft on {cores} host threads ({dt:.1f} s)",
+           "single_thread": n1 * substeps / dt1}
+    out.update(_host_info())
+    orc = oracle_lib.load()
+    # C1 in full: 128 aircraft x 600 decisions, seeded by the C restatement
+    c1_ic = icm.sample_headon(64, seed=0)
+    c1 = orc.seed(c1_ic, 120)
+    c1_act = np.ascontiguousarray(icm.random_bin_actions(600, 128, seed=0))
+    t0 = time.perf_counter()
+    run(c1, c1_act, 128, 600, cores)
+    dt = time.perf_counter() - t0
+    out["c1_full"] = {"value": 128 * 600 * substeps / dt, "unit": "aircraft-substeps/s",
+                      "seconds": dt, "cores": cores,
+                      "sample": "C1: 128 aircraft x 600 decisions x 6 substeps, fp64"}
+    # obs / reward on the 32,768 bench aircraft (16k engagements), one oracle per host thread
+    nenv = nac // 2
+    K = max(1, min(cores, 64))
+    while nenv % K:
+        K -= 1
+    per = nenv // K
+    s_all = np.ascontiguousarray(states0_aos)
+    obs_parts = []
+    for k in range(K):
+        ob = oracle_lib.ObrOracle(orc, per)
+        sub = np.ascontiguousarray(s_all[2 * per * k:2 * per * (k + 1)])
+        obs_parts.append((ob, sub, np.ascontiguousarray(actions_host[0, 2 * per * k:2 * per * (k + 1)])))
+
+    obs_parts[0][0].state9(obs_parts[0][1][:2])                # one-time init, one thread
+
+    def obs_decision():
+        _threads_run([lambda ob=ob, sub=sub, a=a: (lambda s9: (ob.step(s9, a), ob.build_obs(s9)))(
+            ob.state9(sub)) for ob, sub, a in obs_parts])
+    obs_decision()                                              # anchors prev state
+    reps, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < 3.0:
+        obs_decision()
+        reps += 1
+    obs_dt = (time.perf_counter() - t0) / reps
+    out["obs_reward_c3"] = {"value": nac / obs_dt, "unit": "aircraft/s", "cores": K,
+                            "ms_per_decision": obs_dt * 1e3, "kind": "port",
+                            "sample": f"{nac} aircraft (16k engagements) x {reps} decisions: "
+                                      "state9 + advance/reward/termination + 184-D observation"}
+    # GAE over [64, 16384, 2] float32 (numpy, one thread)
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("gae_oracle", os.path.join(ROOT, "oracle", "gae_oracle.py"))
+    GO = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(GO)
+    rng = np.random.default_rng(0)
+    T = 64
+    rew = rng.standard_normal((T, nac)).astype(np.float32)
+    val = rng.standard_normal((T, nac)).astype(np.float32)
+    done = (rng.random((T, nenv)) < 0.01).astype(np.float32)
+    lv = rng.standard_normal(nac).astype(np.float32)
+    nd = np.zeros(nenv, np.float32)
+    t0 = time.perf_counter()
+    GO.gae_f32(rew, val, done, lv, nd, 0.99, 0.95, nagents=2)
+    gdt = time.perf_counter() - t0
+    out["gae_c4"] = {"value": T * nac / gdt, "unit": "elements/s", "cores": 1, "kind": "port",
+                     "ms": gdt * 1e3, "sample": "[64, 16384, 2] float32, numpy"}
+    # one env decision on the host: FDM (60 Hz lineage) + obs/reward, every thread
+    kind60, run60 = _fdm_runner(60, substeps)
+    st60 = states0_aos.copy()
+    a60 = np.ascontiguousarray(actions_host[:1])
+    t0 = time.perf_counter()
+    for _ in range(3):
+        run60(st60, a60, nac, 1, cores)
+    fdm_dt = (time.perf_counter() - t0) / 3
+    out["env_transitions_per_s"] = nenv / (fdm_dt + obs_dt)
+    out["env_step_sample"] = (f"{nenv} engagements: FDM decision ({kind60} C model, 60 Hz FCS, "
+                              f"{fdm_dt * 1e3:.1f} ms) + obs/reward ({obs_dt * 1e3:.1f} ms), "
+                              f"{cores} host threads")
+    return out
 
 
-# Algorithmic HBM bytes of one aircraft in the fused post-physics kernel: reads 11 state doubles
-# + reconstructor (hp, fuel, prev_att 3, pqr-free, act_hist 16, prev_x, prev_alt_log, flags, t)
-# + actions 4; writes reconstructor (hp, hp_loss, fuel, pqr 3, prev_att 3, act_hist 20, dealt,
-# taken, prev_x, prev_alt_log, flags, t) + reward + terminal and live observations (2 x 184 f32)
-# + terminal HP/altitude + the 101 state doubles read for the finite flag.
-POST_BYTES_PER_AIRCRAFT = (11 + 101 + 4 + 27) * 8 + 2 + (34 + 3) * 8 + 2 * 184 * 4 + 4
+# Algorithmic HBM bytes of one aircraft in the fused post-physics kernel: reads the 15 state
+# doubles position..fuel (kinematics, reward, fuel) + the physics launch's finite flag (1 byte)
+# + actions 4 + reconstructor (hp, fuel, prev_att 3, act_hist 16, prev_x, prev_alt_log, flags,
+# t, ...: 27); writes reconstructor (hp, hp_loss, fuel, pqr 3, prev_att 3, act_hist 20, dealt,
+# taken, prev_x, prev_alt_log, flags, t) + reward + terminal and live observations (2 x 184
+# f32) + terminal HP/altitude.  Without the flag (F16EnvStepIO.state_finite NULL) the launch
+# reads the other 86 state doubles instead of the byte.
+POST_BYTES_PER_AIRCRAFT = (15 + 4 + 27) * 8 + 1 + 2 + (34 + 3) * 8 + 2 * 184 * 4 + 4
+POST_BYTES_SCAN_EXTRA = 86 * 8 - 1
+# reference's published full env step at 16,384 envs: 10.3 ms (RTX 3070 Ti,
+# cuda_fdm/README.md:225) = 1.59 M env transitions/s
+REF_PUBLISHED_ENV_TRANSITIONS = 16384 / 10.3e-3
+STAGGER_STEPS = 2000          # = the 200 s engagement limit: episode clocks spread over it
 
 
-def env_step_bench(pkg, nenv, steps, warmup):
-    """Full environment transitions: GpuDogfightVecEnv.step = FDM decision (6 substeps, FCS 60 Hz)
-    + the fused post-physics kernel (advance, reward, termination, terminal observation, pool
-    autoreset, new observation), contest ICs, random 4-channel actions resident on the device."""
+def _env_timed(env, acts, warmup, steps):
     import torch
-    env_mod = importlib.import_module(PKG + ".rl_env")
-    env = env_mod.GpuDogfightVecEnv(nenv, seed=0)
-    env.reset(stagger=False)
-    g = torch.Generator(device="cuda").manual_seed(0)
-    acts = torch.rand(warmup + steps, 2 * nenv, 4, generator=g, device="cuda",
-                      dtype=torch.float64) * 2 - 1
-    acts[..., 3] = (acts[..., 3] + 1) / 2
     for k in range(warmup):
         env.step(acts[k])
     torch.cuda.synchronize()
@@ -124,25 +233,79 @@ def env_step_bench(pkg, nenv, steps, warmup):
         dones.append(done)
     e1.record()
     torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / steps
-    done_total = torch.stack(dones).sum()
-    # kernel times from a second, instrumented pass (events around each launch)
+    return e0.elapsed_time(e1) / steps, int(torch.stack(dones).sum().item())
+
+
+def _env_kernel_ms(env, acts, warmup, n):
+    """Mean FDM and post-physics launch times from a pass with events around each launch."""
+    import torch
     env.kernel_events, env.sim.kernel_events = [], []
-    for k in range(min(steps, 20)):
+    for k in range(n):
         env.step(acts[warmup + k])
     torch.cuda.synchronize()
     post_ms = float(np.mean([a.elapsed_time(b) for a, b in env.kernel_events]))
     fdm_ms = float(np.mean([a.elapsed_time(b) for a, b in env.sim.kernel_events]))
     env.kernel_events = env.sim.kernel_events = None
+    return fdm_ms, post_ms
+
+
+def env_step_bench(pkg, nenv, steps, warmup, scan_finite=False):
+    """Full environment transitions: GpuDogfightVecEnv.step = FDM decision (6 substeps, FCS 60 Hz)
+    + the fused post-physics kernel (advance, reward, termination, terminal observation, pool
+    autoreset, new observation), contest ICs with the staggered reset spread over the whole
+    200 s engagement (so timeouts and deaths autoreset engagements inside the timed loop),
+    random 4-channel actions resident on the device.  The physics launch hands the post-physics
+    launch its per-aircraft finite flags; the same steps are timed again with the post-physics
+    launch re-reading the state for them (A/B in one process).  scan_finite: time only that
+    variant (profiling aid)."""
+    import torch
+    env_mod = importlib.import_module(PKG + ".rl_env")
+    env = env_mod.GpuDogfightVecEnv(nenv, seed=0)
+    env.reset(stagger=True, max_stagger_steps=STAGGER_STEPS)
+    g = torch.Generator(device="cuda").manual_seed(0)
+    acts = torch.rand(warmup + steps, 2 * nenv, 4, generator=g, device="cuda",
+                      dtype=torch.float64) * 2 - 1
+    acts[..., 3] = (acts[..., 3] + 1) / 2
+    snap_states = env.sim.states.clone()
+    snap_obr = env.obr.clone_state()
     post_bytes = POST_BYTES_PER_AIRCRAFT * 2 * nenv
-    return {"workload": "contest_env_step_16k", "engagements": nenv, "obs_dim": 184,
-            "substeps": env.substeps, "fcs_rate_hz": env.sim.fcs_rate,
-            "transitions_per_s": nenv / (ms * 1e-3), "ms_per_step": ms,
-            "fdm_kernel_ms": fdm_ms, "post_kernel_ms": post_ms,
-            "episodes_done": int(done_total.item()),
-            "post_kernel": {"kernel": "env_post_step_kernel", "algorithmic_bytes": post_bytes,
-                            "achieved_GBs": post_bytes / (post_ms * 1e-3) / 1e9,
-                            "hbm_frac": post_bytes / (post_ms * 1e-3) / 1e9 / PEAK_HBM_GBS}}
+    runs = {True: [], False: []}
+    # alternating order (A B B A): whichever variant runs first after the warm-up pays for it
+    order = (False, False) if scan_finite else (True, False, False, True)
+    for fused in order:
+        env.fused_finite = fused
+        env.sim.states.copy_(snap_states)        # both variants step the same engagements
+        env.obr.restore(snap_obr)
+        ms, done = _env_timed(env, acts, warmup, steps)
+        fdm_ms, post_ms = _env_kernel_ms(env, acts, warmup, min(steps, 20))
+        runs[fused].append((ms, done, fdm_ms, post_ms))
+    env.fused_finite = True
+    res = {}
+    for fused, r in runs.items():
+        if not r:
+            continue
+        ms, done, fdm_ms, post_ms = (float(np.mean([x[i] for x in r])) for i in range(4))
+        b = post_bytes + (0 if fused else POST_BYTES_SCAN_EXTRA * 2 * nenv)
+        res[fused] = {"ms_per_step": ms, "episodes_done": int(round(done)),
+                      "fdm_kernel_ms": fdm_ms, "post_kernel_ms": post_ms, "algorithmic_bytes": b,
+                      "achieved_GBs": b / (post_ms * 1e-3) / 1e9,
+                      "hbm_frac": b / (post_ms * 1e-3) / 1e9 / PEAK_HBM_GBS}
+    main = res[False] if scan_finite else res[True]
+    out = {"workload": "contest_env_step_16k", "engagements": nenv, "obs_dim": 184,
+           "substeps": env.substeps, "fcs_rate_hz": env.sim.fcs_rate,
+           "reset": f"stagger over {STAGGER_STEPS} decisions", "finite_flags": not scan_finite,
+           "transitions_per_s": nenv / (main["ms_per_step"] * 1e-3),
+           "ms_per_step": main["ms_per_step"], "fdm_kernel_ms": main["fdm_kernel_ms"],
+           "post_kernel_ms": main["post_kernel_ms"], "episodes_done": main["episodes_done"],
+           "vs_published": nenv / (main["ms_per_step"] * 1e-3) / REF_PUBLISHED_ENV_TRANSITIONS,
+           "post_kernel": {"kernel": "env_post_step_split_kernel<184,true>",
+                           "algorithmic_bytes": main["algorithmic_bytes"],
+                           "achieved_GBs": main["achieved_GBs"], "hbm_frac": main["hbm_frac"]}}
+    if not scan_finite:
+        out["state_scan_ab"] = {"what": "post-physics launch re-reading the 86 other state doubles "
+                                        "for the finite flag instead of the physics launch's flag",
+                                **res[False]}
+    return out
 
 
 PEAK_BF16_TFLOPS = 2500.0
@@ -165,7 +328,7 @@ def rollout_bench(nenv, T=64, reps=2):
                                  generator=torch.Generator().manual_seed(0)).to("cuda")
         ro = ppo.SelfPlayRollout(env, net, T=T, gamma=0.99, lam=0.95, seed=0, stats=False,
                                  graph=graph)
-        ro.reset(stagger=False)
+        ro.reset(stagger=True, max_stagger_steps=STAGGER_STEPS)
         return ro
     ro = make(True)
     ro.collect()                                    # eager warm-up (allocations)
@@ -180,6 +343,7 @@ def rollout_bench(nenv, T=64, reps=2):
     if not bool(stats["trajectory_finite"]) or not bool(torch.isfinite(adv).all()):
         raise FloatingPointError("non-finite rollout")
     ms = e0.elapsed_time(e1) / reps
+    done = float(ro.b_done[1:].sum().item() + ro.next_done.sum().item())
     del ro
     eager = make(False)
     eager.collect()
@@ -192,6 +356,8 @@ def rollout_bench(nenv, T=64, reps=2):
     pol_ms = float(np.mean([a.elapsed_time(b) for a, b in eager.policy_events]))
     flop = ppo.POLICY_FLOP_PER_ROW[184] * 2 * nenv
     return {"workload": "selfplay_rollout_16k_T64", "engagements": nenv, "T": T,
+            "reset": f"stagger over {STAGGER_STEPS} decisions",
+            "episodes_done_per_rollout": done,
             "hip_graph": True, "ms_per_rollout": ms, "eager_ms_per_rollout": eager_ms,
             "transitions_per_s": nenv * T / (ms * 1e-3),
             "aircraft_transitions_per_s": 2 * nenv * T / (ms * 1e-3),
@@ -327,6 +493,9 @@ def main():
     ap.add_argument("--no-rollout", action="store_true")
     ap.add_argument("--no-league", action="store_true")
     ap.add_argument("--no-update", action="store_true")
+    ap.add_argument("--scan-finite", action="store_true",
+                    help="with --only env: time only the post-physics launch that re-reads the "
+                         "state for the finite flags (profiling aid)")
     ap.add_argument("--only", choices=["fdm", "env", "rollout", "league", "update"], default=None,
                     help="profiling aid: run only this section and print its own JSON line "
                          "(not the contract line)")
@@ -354,7 +523,8 @@ def main():
     pkg = importlib.import_module(PKG)
     icm = importlib.import_module(PKG + ".ic")
     if args.only in ("env", "rollout", "league", "update"):
-        part = {"env": lambda: env_step_bench(pkg, args.nenv, args.steps, args.warmup),
+        part = {"env": lambda: env_step_bench(pkg, args.nenv, args.steps, args.warmup,
+                                              scan_finite=args.scan_finite),
                 "rollout": lambda: rollout_bench(args.nenv),
                 "league": lambda: league_bench(),
                 "update": lambda: update_bench(args.nenv)}[args.only]()
@@ -432,7 +602,8 @@ def main():
         "wall_s": wall,
     }
     if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(states0, acts_host[args.warmup:], S, args.cpu_seconds)
+        line["cpu_baseline"] = cpu_baseline(states0, acts_host[args.warmup:], S, args.cpu_seconds,
+                                            icm)
     print(json.dumps(line), flush=True)
 
 

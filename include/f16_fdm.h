@@ -25,6 +25,15 @@ extern "C" {
 int f16_fdm_step_batch(double* states, long ld, const double* actions, int nac, int substeps,
                        int fcs_rate, double* obs, long obs_ld, void* stream);
 
+/* f16_fdm_step_batch that also writes finite[a] = 1 if all 101 state values of aircraft a
+ * after the step are finite, else 0 ((nac) bytes), formed from the values the kernel holds in
+ * registers as it stores them -- the flag GpuDogfightVecEnv.step computes over `states` after
+ * the physics (R/cuda_fdm/rl_env.py:545), without reading the state back.  substeps >= 1.
+ * The env step hands it to f16_env_post_step as F16EnvStepIO.state_finite. */
+int f16_fdm_step_batch_finite(double* states, long ld, const double* actions, int nac,
+                              int substeps, int fcs_rate, double* obs, long obs_ld,
+                              unsigned char* finite, void* stream);
+
 /* The same step computed with one lane (one wavefront) per aircraft doing the whole substep.
  * Results equal f16_fdm_step_batch bit for bit; f16_fdm_step_batch spreads each substep over
  * two cooperating wavefronts.  Same arguments, contract and reference interface. */

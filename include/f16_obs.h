@@ -120,6 +120,10 @@ typedef struct F16EnvStepIO {
     float *norm_count;           /* with norm_partial: the running count, advanced by nac */
     float *norm_count_snap;      /* with norm_partial: the count before this update (the
                                     workspace's last element, as f16_norm_update keeps it) */
+    const unsigned char *state_finite;  /* (nac) per aircraft, 1 if all 101 state values are
+                                    finite, as f16_fdm_step_batch_finite wrote them for these
+                                    states -- or NULL: the kernel reads the 86 fields beyond the
+                                    15 it needs anyway and tests them itself */
 } F16EnvStepIO;
 
 /* GpuDogfightVecEnv.step after the physics launch (research/competition_36500/runtime/

@@ -378,6 +378,13 @@ typedef struct {
 enum { C_OWNW, C_DMG, C_SHAPE, C_WIN, C_LOSS, C_TWIN, C_TLOSS, C_TDRAW };
 static const double DT_STEP = 6.0 / 60.0;   /* STEP_RATIO / SIM_HZ */
 
+/* orc_state9 over n aircraft rows of 101 doubles (row-major (n, 101) -> (n, 9)). */
+void orc_state9_batch(const double *st, long n, double *s9)
+{
+    obs_init();
+    for (long i = 0; i < n; ++i) orc_state9(st + 101 * i, s9 + 9 * i);
+}
+
 void orc_obr_reset_envs(OrcObr *o, const unsigned char *mask)
 {   /* reset_all / reset_envs (obs_reward.py:517-541) */
     for (long e = 0; e < o->nenv; e++) {

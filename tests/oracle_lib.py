@@ -182,6 +182,7 @@ class ObrOracle:
         self.accel = np.zeros((n, 3)) if accel else None
         L = self.L
         L.orc_state9.argtypes = [D, D]
+        L.orc_state9_batch.argtypes = [D, _l, D]
         L.orc_obr_reset_envs.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
         L.orc_obr_init_reward.argtypes = [ctypes.c_void_p, D, ctypes.c_void_p]
         L.orc_obr_step.argtypes = [ctypes.c_void_p, D, D, D, ctypes.c_int, ctypes.c_double,
@@ -199,10 +200,9 @@ class ObrOracle:
         return s
 
     def state9(self, states):
-        states = np.ascontiguousarray(states, dtype=np.float64)
+        states = np.ascontiguousarray(states, dtype=np.float64).reshape(-1, 101)
         out = np.zeros((states.shape[0], 9))
-        for i in range(states.shape[0]):
-            self.L.orc_state9(_p(np.ascontiguousarray(states[i])), _p(out[i]))
+        self.L.orc_state9_batch(_p(states), states.shape[0], _p(out))
         return out
 
     def reset_envs(self, mask=None):

@@ -290,6 +290,43 @@ def test_nonfinite_lane_is_isolated(gpu):
     assert not fin[3] and fin[[0, 1, 2, 4, 5, 6, 7]].all()
 
 
+# fields poisoned below: position, fuel, the quaternion-rate history (oldest slot, never read),
+# velocity and acceleration histories, previous-frame body rates, previous-frame auxiliary
+# values, engine, kinematic surface outputs, PID input_prev2 (never read) and PID output
+POISON_FIELDS = (0, 14, 33, 50, 60, 70, 75, 83, 88, 93, 100)
+
+
+@pytest.mark.parametrize("S", [1, 2, 3, 6])
+@pytest.mark.parametrize("rate", [120, 60])
+def test_finite_flags_from_registers(gpu, S, rate):
+    """f16_fdm_step_batch_finite: the per-aircraft flag equals "all 101 state values finite"
+    of the states it leaves (what the env step tests, R/cuda_fdm/rl_env.py:545), for NaN or
+    infinity planted in fields the step reads, overwrites or only shifts (S < 3), on a ragged
+    batch; and the states are the plain entry point's bit for bit."""
+    g = oracle_lib.golden("seed_golden.npz")
+    nenv = 75                                                # 150 aircraft: a ragged workgroup
+    base = np.tile(np.ascontiguousarray(g[f"seed_{rate}"]), (3, 1))[:2 * nenv]
+    bad = {}
+    for i, f in enumerate(POISON_FIELDS):
+        bad[7 + 11 * i] = (f, np.inf if i % 3 == 1 else np.nan)
+    for a, (f, v) in bad.items():
+        base[a, f] = v
+    act = torch.as_tensor(_rand_actions(np.random.default_rng(S), 2 * nenv), device=gpu)
+    a_sim, b_sim = _sim(nenv, rate), _sim(nenv, rate)
+    for sim in (a_sim, b_sim):
+        sim.load_seed(torch.as_tensor(base))
+    fin = torch.full((2 * nenv,), 7, dtype=torch.uint8, device=gpu)
+    for _ in range(2):
+        a_sim.step(act, substeps=S, want_obs=False)
+        b_sim.step(act, substeps=S, want_obs=False, finite_out=fin)
+        assert torch.equal(a_sim._state_soa.view(torch.int64), b_sim._state_soa.view(torch.int64))
+        want = torch.isfinite(b_sim.states).all(dim=1)
+        assert torch.equal(fin.bool(), want)
+        assert set(fin.unique().tolist()) == {0, 1}
+    with pytest.raises(ValueError):
+        b_sim.step(act, substeps=0, finite_out=fin)
+
+
 def test_argument_errors(gpu):
     pkg = import_pkg()
     with pytest.raises(ValueError):

@@ -429,6 +429,45 @@ def test_env_post_step_two_wave_equals_one_wave(gpu, obs_dim, nenv, terminal):
     assert done.any() and (~done).any()
 
 
+@pytest.mark.parametrize("obs_dim", [184, 214])
+def test_env_step_fused_finite_equals_state_scan(gpu, obs_dim):
+    """GpuDogfightVecEnv.step with the physics launch's finite flags (F16EnvStepIO.state_finite)
+    against the post-physics launch testing the 101 state values itself: every output, the
+    reconstructor and the states agree bit for bit over several steps, with NaN and infinity
+    planted in some engagements' states (terminal_state_finite false, autoreset)."""
+    E = import_pkg("rl_env").GpuDogfightVecEnv
+    envs = [E(300, seed=4, ic_pool_size=64, obs_dim=obs_dim) for _ in range(2)]
+    envs[1].fused_finite = False
+    for env in envs:
+        env.reset(stagger=False)
+    rng = np.random.default_rng(5)
+    for k in range(4):
+        act = torch.as_tensor(rng.uniform(-1, 1, (600, 4)), device=gpu)
+        pick = torch.as_tensor(rng.integers(0, 64, 300), device=gpu)
+        outs = []
+        for env in envs:
+            if k == 1:
+                env.sim.states[17, 5] = float("nan")
+                env.sim.states[40, 88] = float("inf")
+                env.sim.states[301, 100] = float("nan")
+            outs.append(env.step(act, reset_indices=pick))
+        (oa, ra, da, ia), (ob, rb, db, ib) = outs
+        bits = lambda t: t.contiguous().view(torch.int32 if t.element_size() == 4 else
+                                             torch.int64 if t.element_size() == 8 else torch.uint8)
+        same = lambda x, y: torch.equal(bits(x), bits(y))       # NaN-safe, bit for bit
+        assert same(oa, ob) and same(ra, rb) and same(da, db), k
+        for key in ia:
+            assert same(ia[key], ib[key]), (k, key)
+        assert same(envs[0].sim._state_soa, envs[1].sim._state_soa), k
+        assert same(envs[0].obr.hp, envs[1].obr.hp)
+        if k == 1:
+            bad = (~ia["terminal_state_finite"]).nonzero().flatten().tolist()
+            assert bad == [8, 20, 150], bad
+            # termination tests the state9 row (rl_env.py:467-484): a NaN velocity terminates;
+            # an infinite actuator state or PID integrator is clamped before it reaches state9
+            assert bool(da[8])
+
+
 def test_env_post_step_bad_pick_poisons_state(gpu):
     """A pool index out of range never reads out of bounds: the engagement becomes NaN."""
     nenv = 4
