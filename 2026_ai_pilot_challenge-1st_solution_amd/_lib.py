@@ -48,7 +48,8 @@ class F16EnvStepIO(ctypes.Structure):
                 ("terminal_alt_m", _vp), ("terminal_finite", _vp), ("finite_acc", _vp),
                 ("opp_assign", _vp), ("opp_cdf", _vp), ("n_opp", _i), ("step_base", _vp),
                 ("norm_partial", _vp), ("norm_count", _vp), ("norm_count_snap", _vp),
-                ("state_finite", _vp)]
+                ("state_finite", _vp), ("pool_obs", _vp), ("pool_prev_x", _vp),
+                ("pool_prev_alt_log", _vp), ("pool_aux", _vp)]
 
 
 class F16PolicyGroup(ctypes.Structure):

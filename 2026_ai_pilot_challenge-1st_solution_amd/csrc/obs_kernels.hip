@@ -739,16 +739,18 @@ __device__ __forceinline__ void pool_kin(const F16EnvStepIO& io, const Origin& O
   }
 }
 
-__device__ __forceinline__ void lane_autoreset(const F16EnvStepIO& io, const F16Recon& r,
-                                               const Origin& O, long a, long e, int odd,
-                                               uint32_t step, Kin9& k2, Peer& p2, Geo& g2) {
+// The part of an autoreset that does not depend on the new state's geometry: state rows from
+// pool row pk (NaN rows for pk < 0), reconstructor reset, league opponent redraw.
+__device__ __forceinline__ void lane_reset_rows(const F16EnvStepIO& io, const F16Recon& r,
+                                                long a, long e, int odd, uint32_t step, long pk,
+                                                bool copy_state = true) {
   double* __restrict__ st = io.states;
   const long ld = io.ld;
-  const long pk = pool_pick(io, e, step);
   const bool ok = pk >= 0;
   const double* src = io.ic_pool + (ok ? pk * 2 + odd : 0) * F16S_N;
   const double qnan = __builtin_nan("");
-  if (ok) {
+  if (!copy_state) {
+  } else if (ok) {
     for (int f = 0; f < F16S_N; ++f) st[f * ld + a] = src[f];
   } else {
     for (int f = 0; f < F16S_N; ++f) st[f * ld + a] = qnan;
@@ -773,10 +775,84 @@ __device__ __forceinline__ void lane_autoreset(const F16EnvStepIO& io, const F16
   }
   for (int i = 0; i < kActHist; ++i) r.act_hist[i * r.ld + a] = 0.0;
   if (!odd) r.t_sec[e] = 0.0;
+}
+
+__device__ __forceinline__ void lane_autoreset(const F16EnvStepIO& io, const F16Recon& r,
+                                               const Origin& O, long a, long e, int odd,
+                                               uint32_t step, Kin9& k2, Peer& p2, Geo& g2) {
+  const long pk = pool_pick(io, e, step);
+  lane_reset_rows(io, r, a, e, odd, step, pk);
   pool_kin(io, O, pk, odd, k2);
   exchange(k2, p2);
   pair_geo(k2, p2, g2);
   lane_init_reward(k2, p2, g2, a, 0.0, r);
+}
+
+// An autoreset from pool row pk >= 0 with the row's re-anchored reward state and aux features
+// taken from the pool tables (io.pool_obs set); the state and observation rows are copied
+// separately, by the whole group (copy_pool_rows).
+__device__ __forceinline__ void lane_autoreset_cached(const F16EnvStepIO& io, const F16Recon& r,
+                                                      long a, long e, int odd, uint32_t step,
+                                                      long pk) {
+  lane_reset_rows(io, r, a, e, odd, step, pk, false);
+  r.prev_x[a] = io.pool_prev_x[pk * 2 + odd];
+  r.prev_x_valid[a] = 1;
+  r.prev_alt_log[a] = io.pool_prev_alt_log[pk * 2 + odd];
+  if (r.aux && !odd) {
+    double* o = r.aux + e * kAuxDim;
+    const double* src = io.pool_aux + pk * kAuxDim;
+#pragma unroll
+    for (int i = 0; i < kAuxDim; ++i) o[i] = src[i];
+  }
+}
+
+// The index of the k-th set bit of m (k < popcount(m)).
+__device__ __forceinline__ int nth_set_bit(uint64_t m, int k) {
+  for (int j = 0; j < k; ++j) m &= m - 1;
+  return __builtin_ctzll(m);
+}
+
+// State and observation rows of cached autoresets: row r of the group (bit r of m) restarts
+// from pool aircraft pick[r] (= 2 pool row + plane).  Every thread of the group takes part: the
+// 101 state doubles of all such rows are loaded together (contiguous in the pool) and stored
+// into the structure-of-arrays states, then each observation row is copied in 8-byte pieces
+// (coalesced).  With the full-row tile the observation rows also go into it, for the
+// RunningNorm partial sums that read the tile.
+template <int D, bool FULL, int NT>
+__device__ __forceinline__ void copy_pool_rows(float* S, long a0, uint64_t m,
+                                               const long* pick, const F16EnvStepIO& io,
+                                               const float* __restrict__ pool_obs,
+                                               float* __restrict__ out, int tid) {
+  constexpr int P = tile_pitch<D, FULL>(), kU = 4;
+  {
+    const int total = __popcll(m) * F16S_N;      // item i: field i % 101 of the (i / 101)-th row
+    for (int i0 = tid; i0 < total; i0 += kU * NT) {
+      double v[kU];
+      int row[kU];
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        const int i = i0 + u * NT;
+        row[u] = i < total ? nth_set_bit(m, i / F16S_N) : 0;
+        v[u] = i < total ? io.ic_pool[pick[row[u]] * F16S_N + i % F16S_N] : 0.0;
+      }
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        const int i = i0 + u * NT;
+        if (i < total) io.states[(long)(i % F16S_N) * io.ld + a0 + row[u]] = v[u];
+      }
+    }
+  }
+  while (m) {
+    const int r = __builtin_ctzll(m);
+    m &= m - 1;
+    const float* src = pool_obs + pick[r] * D;
+#pragma unroll
+    for (int c = 2 * tid; c < D; c += 2 * NT) {
+      const float2 x = *reinterpret_cast<const float2*>(src + c);
+      *reinterpret_cast<float2*>(out + (a0 + r) * D + c) = x;
+      if constexpr (FULL) { S[r * P + c] = x.x; S[r * P + c + 1] = x.y; }
+    }
+  }
 }
 
 __device__ __forceinline__ ObsIn fresh_obs_in() {
@@ -953,7 +1029,8 @@ template <int D, bool FULL>
 __global__ __launch_bounds__(kPostSplitBlock) void env_post_step_split_kernel(
     const F16EnvStepIO io, F16Recon r, F16RewardCfg c, Origin O) {
   __shared__ float S_all[kPostGroups][kRowBlock * tile_pitch<D, FULL>()];
-  __shared__ uint64_t sh_mask[kPostGroups][2];   // live and finished rows, from the advance role
+  __shared__ uint64_t sh_mask[kPostGroups][3];   // live, finished and pool-table finished rows
+  __shared__ long sh_pick[kPostGroups][kRowBlock]; // pool table row of each pool-table autoreset
   __shared__ double sh_norm[FULL ? 8 * D : 1];     // RunningNorm partials per phase (full tile)
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -1079,11 +1156,22 @@ __global__ __launch_bounds__(kPostSplitBlock) void env_post_step_split_kernel(
     return;
   }
   __syncthreads();
-  // Rows of finished engagements, again split: the advance role restarts them from the pool
-  // (state rows, reconstructor, reward anchor) and writes the scalar block; the vector role
-  // forms the same pool row's kinematics from the pool itself and writes the vector block.
-  if ((fresh >> lane) & 1) {
-    const uint32_t step = io.step + (io.step_base ? *io.step_base : 0u);
+  // Rows of finished engagements.  With the pool tables (io.pool_obs) the advance role restarts
+  // them from the pool row with its cached reward anchors and aux features, and the group
+  // copies the row's cached observation.  Otherwise (and for a pick outside the pool), split
+  // again: the advance role restarts them from the pool (state rows, reconstructor, reward
+  // anchor) and writes the scalar block; the vector role forms the same pool row's kinematics
+  // from the pool itself and writes the vector block.
+  const uint32_t step = io.step + (io.step_base ? *io.step_base : 0u);
+  const bool mine = (fresh >> lane) & 1;
+  const long pk = mine && io.pool_obs ? pool_pick(io, e, step) : -1;
+  const bool cached = pk >= 0;
+  const uint64_t from_table = __ballot(cached);    // the same in both roles
+  if (mine && cached && role == 0) {
+    lane_autoreset_cached(io, r, a, e, odd, step, pk);
+    sh_pick[grp][lane] = pk * 2 + odd;
+  }
+  if (mine && !cached) {
     Kin9 k2;
     Peer p2;
     Geo g2;
@@ -1101,11 +1189,16 @@ __global__ __launch_bounds__(kPostSplitBlock) void env_post_step_split_kernel(
     }
   }
   __syncthreads();
-  flush_sparse<D, FULL, 2 * kRowBlock>(S, a0, fresh, io.obs, gtid);
+  flush_sparse<D, FULL, 2 * kRowBlock>(S, a0, fresh & ~from_table, io.obs, gtid);
+  if (from_table)
+    copy_pool_rows<D, FULL, 2 * kRowBlock>(S, a0, from_table, sh_pick[grp], io, io.pool_obs,
+                                           io.obs, gtid);
   if constexpr (FULL) {   // the tiles now hold every new row, the rebuilt ones included
-    if (io.norm_partial)
+    if (io.norm_partial) {
+      __syncthreads();     // (workgroup-uniform) the copied rows have landed in the tiles
       norm_partials_from_tiles<D>(&S_all[0][0], sh_norm, (long)blockIdx.x * 2 * kRowBlock, nac,
                                   blockIdx.x, io, threadIdx.x);
+    }
   }
 }
 

@@ -81,6 +81,12 @@ class GpuDogfightVecEnv:
         # fused_finite=False makes the post-physics launch read the state and test it itself
         self._state_fin = torch.empty(n, dtype=torch.uint8, device=dev)
         self.fused_finite = True
+        # per pool row, what an autoreset from it produces (observation, reward anchors, aux
+        # features), so the post-physics launch copies instead of rebuilding; pool_tables=False
+        # makes it rebuild them
+        self.pool_tables = True
+        self._pool_key = None
+        self._pool_buf = None
 
     def enable_aux_capture(self):
         """Turn on the future-aux features (BatchObsReward.enable_aux_capture): every step and
@@ -238,6 +244,43 @@ class GpuDogfightVecEnv:
         a = torch.as_tensor(actions, dtype=torch.float64, device=self.device)
         return a.reshape(self.nac, 4)
 
+    def _pool_table_ptrs(self):
+        """Device tables of what an autoreset from each pool row produces: the observation
+        (2 rows), the re-anchored geometry advantage and log altitude, plane 0's aux features.
+        Built by the reference's own reset sequence on the pool's states (reset_envs ->
+        init_reward -> build_obs, rl_env.py:559-577) through the same kernels, so a copied row
+        equals a rebuilt one bit for bit; rebuilt when the pool tensor, its contents (torch's
+        version counter), the observation width or aux capture change.  The tables live in
+        persistent buffers, so a recorded HIP graph keeps reading the current ones."""
+        pool = self.ic_pool
+        aux = self.obr.aux_features is not None
+        key = (pool.data_ptr(), tuple(pool.shape), pool._version, self.OBS_SIZE, aux)
+        if self._pool_key != key:
+            P, D = pool.shape[0], self.OBS_SIZE
+            t = BatchObsReward(P, device=self.device)
+            if D == OBS_SIZE_EXT:
+                t.enable_external_observations()
+            if aux:
+                t.enable_aux_capture()
+            states = pool.reshape(2 * P, STATE_N)
+            t.kernel_init_reward_state(states)
+            buf = self._pool_buf
+            if buf is None or buf["obs"].shape != (2 * P, D):
+                buf = {"obs": torch.empty(2 * P, D, dtype=torch.float32, device=self.device),
+                       "prev_x": torch.empty(2 * P, dtype=torch.float64, device=self.device),
+                       "alt": torch.empty(2 * P, dtype=torch.float64, device=self.device),
+                       "aux": torch.zeros(P, 21, dtype=torch.float64, device=self.device)}
+                self._pool_buf = buf
+            t._build(states, None, D, buf["obs"])
+            buf["prev_x"].copy_(t.prev_x)
+            buf["alt"].copy_(t.prev_alt_log)
+            if aux:
+                buf["aux"].copy_(t.aux_features)
+            self._pool_key = key
+        b = self._pool_buf
+        return (b["obs"].data_ptr(), b["prev_x"].data_ptr(), b["alt"].data_ptr(),
+                b["aux"].data_ptr())
+
     def _io(self, pick):
         """F16EnvStepIO with the env's persistent pointers; per-call outputs set by the caller."""
         io = _lib.F16EnvStepIO()
@@ -250,6 +293,9 @@ class GpuDogfightVecEnv:
         if self.opp_assign is not None:
             io.opp_assign, io.opp_cdf = self.opp_assign.data_ptr(), self.opp_cdf.data_ptr()
             io.n_opp = self.opp_cdf.numel()
+        if self.pool_tables:
+            io.pool_obs, io.pool_prev_x, io.pool_prev_alt_log, io.pool_aux = \
+                self._pool_table_ptrs()
         return io
 
     def _post(self, io):

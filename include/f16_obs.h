@@ -124,6 +124,13 @@ typedef struct F16EnvStepIO {
                                     finite, as f16_fdm_step_batch_finite wrote them for these
                                     states -- or NULL: the kernel reads the 86 fields beyond the
                                     15 it needs anyway and tests them itself */
+    const float *pool_obs;       /* (pool_size, 2, obs_dim): each pool row's observation after an
+                                    autoreset (what reset_envs + init_reward + build_obs give
+                                    on that row, rl_env.py:559-577), or NULL: the kernel builds
+                                    them.  With pool_obs, also: */
+    const double *pool_prev_x;   /* (pool_size, 2) the re-anchored geometry advantage */
+    const double *pool_prev_alt_log;  /* (pool_size, 2) the re-anchored log altitude */
+    const double *pool_aux;      /* (pool_size, 21) plane 0's aux features (used when rec->aux) */
 } F16EnvStepIO;
 
 /* GpuDogfightVecEnv.step after the physics launch (research/competition_36500/runtime/
@@ -144,6 +151,10 @@ int f16_env_reseed(const F16EnvStepIO *io, const F16Recon *rec, const unsigned c
 
 int f16_env_post_step(const F16EnvStepIO *io, const F16Recon *rec, const F16RewardCfg *cfg,
                       void *stream);
+/* With io->pool_obs set, an autoreset copies the pool row's observation, anchors and aux
+ * features from those tables instead of rebuilding them (a pick outside the pool still builds
+ * its NaN row); the tables must describe io->ic_pool at this obs_dim.  f16_env_post_step_onewave
+ * ignores them and always builds, so the two entry points cross-check the tables. */
 
 /* 1 when f16_env_post_step over nenv engagements can also produce the RunningNorm partial sums
  * of its new observation rows (io->norm_partial): every row's block sits whole in one

@@ -468,6 +468,46 @@ def test_env_step_fused_finite_equals_state_scan(gpu, obs_dim):
             assert bool(da[8])
 
 
+@pytest.mark.parametrize("obs_dim,nenv", [(184, 300), (214, 300), (184, 20000)])
+def test_env_step_pool_tables_equal_rebuild(gpu, obs_dim, nenv):
+    """Autoresets that copy each pool row's observation, reward anchors and aux features from
+    the env's pool tables (F16EnvStepIO.pool_obs) against autoresets that rebuild them: every
+    output, the reconstructor, the aux features and the states agree bit for bit over steps
+    with many autoresets (a 1.2 s engagement limit on staggered clocks), including a pick
+    outside the pool (its NaN row is still built).  20,000 engagements exercise the
+    vector-block tile layout."""
+    E = import_pkg("rl_env").GpuDogfightVecEnv
+    envs = [E(nenv, seed=9, ic_pool_size=64, obs_dim=obs_dim, max_engage_time_s=1.2)
+            for _ in range(2)]
+    envs[1].pool_tables = False
+    for env in envs:
+        env.enable_aux_capture()
+        env.reset(stagger=True, max_stagger_steps=12)
+    bits = lambda t: t.contiguous().view(torch.int32 if t.element_size() == 4 else
+                                         torch.int64 if t.element_size() == 8 else torch.uint8)
+    same = lambda x, y: torch.equal(bits(x), bits(y))       # NaN-safe, bit for bit
+    rng = np.random.default_rng(6)
+    resets = 0
+    for k in range(8):
+        act = torch.as_tensor(rng.uniform(-1, 1, (2 * nenv, 4)), device=gpu)
+        pick = rng.integers(0, 64, nenv)
+        if k == 3:
+            pick[5] = 64                                    # outside the pool: NaN row
+        pick = torch.as_tensor(pick, device=gpu)
+        outs = [env.step(act, reset_indices=pick) for env in envs]
+        (oa, ra, da, ia), (ob, rb, db, ib) = outs
+        assert same(oa, ob) and same(ra, rb) and same(da, db), k
+        for key in ia:
+            assert same(ia[key], ib[key]), (k, key)
+        assert same(envs[0].sim._state_soa, envs[1].sim._state_soa), k
+        for name in ("hp", "fuel", "prev_x", "prev_x_valid", "prev_alt_log", "t_sec",
+                     "aux_features", "_hist_soa", "_att_soa", "_pqr_soa"):
+            assert same(getattr(envs[0].obr, name), getattr(envs[1].obr, name)), (k, name)
+        resets += int(da.sum())
+    assert resets > nenv // 4, resets
+    assert envs[0]._pool_key is not None and envs[1]._pool_key is None
+
+
 def test_env_post_step_bad_pick_poisons_state(gpu):
     """A pool index out of range never reads out of bounds: the engagement becomes NaN."""
     nenv = 4
