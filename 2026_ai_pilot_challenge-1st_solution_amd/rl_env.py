@@ -86,6 +86,7 @@ class GpuDogfightVecEnv:
         # makes it rebuild them
         self.pool_tables = True
         self._pool_key = None
+        self._capture_terminal_obs = True     # step's default (step_training clears it)
         self._pool_buf = None
 
     def enable_aux_capture(self):
@@ -322,10 +323,29 @@ class GpuDogfightVecEnv:
             self._cfg_key = key
         return self._cfg
 
-    def step(self, actions, *, reset_indices=None, terminal_obs=True):
+    def step_training(self, actions):
+        """The root lineage's training-consumer step (cuda_fdm/rl_env.py:518-527): step() with
+        the terminal-observation copy turned off for this call (info["terminal_obs"] is None);
+        the instance default is restored even if the step raises."""
+        previous = getattr(self, "_capture_terminal_obs", True)
+        self._capture_terminal_obs = False
+        try:
+            return self.step(actions)
+        finally:
+            self._capture_terminal_obs = previous
+
+    def step(self, actions, *, reset_indices=None, terminal_obs=None, capture_terminal_obs=None):
         """actions (nenv,2,4) or (nac,4) [aileron, elevator, rudder, throttle].
         Returns (obs (nenv,2,D) f32, reward (nenv,2) f64, done (nenv,) bool, info).
-        terminal_obs=False skips the terminal-observation copy (info["terminal_obs"] is None)."""
+        capture_terminal_obs=False (root lineage, cuda_fdm/rl_env.py:529; `terminal_obs` is the
+        same switch) skips the terminal-observation copy: info["terminal_obs"] is None.  Unset,
+        the instance default `_capture_terminal_obs` (True) applies.  reset_indices: the 184-D
+        lineage's explicit pool rows per engagement (R/cuda_fdm/rl_env.py:499)."""
+        if capture_terminal_obs is None:
+            capture_terminal_obs = terminal_obs
+        if capture_terminal_obs is None:
+            capture_terminal_obs = getattr(self, "_capture_terminal_obs", True)
+        terminal_obs = bool(capture_terminal_obs)
         a = self._to_nac4(actions)
         self._ensure_ic_pool()
         state_fin = self._state_fin if self.fused_finite and self.substeps >= 1 else None

@@ -23,9 +23,19 @@ import numpy as np
 ROOT = os.path.dirname(os.path.abspath(__file__))
 PKG = "2026_ai_pilot_challenge-1st_solution_amd"
 
-# Algorithmic FP64 work of one aircraft-substep: static count of the reference's model
-# (adds, subs, muls, divs, sqrts and libm calls each 1), SURVEY 8(d): ~1.55 kFLOP.
-FLOP_PER_SUBSTEP = 1550.0
+# Algorithmic FP64 work of one aircraft-substep (adds, subs, muls, divs, sqrts and libm calls
+# each 1), counted by the operation-counting build of the CPU restatement on the headline
+# workload (tests/golden/fdm_flops.json, c2_tailchase); the reference model's static count is
+# 1,550.
+def _flop_per_substep(sample="c2_tailchase"):
+    path = os.path.join(ROOT, "tests", "golden", "fdm_flops.json")
+    try:
+        return float(json.load(open(path))["per_aircraft_substep"][sample]["flop"])
+    except (OSError, KeyError, ValueError):
+        return 1550.0
+
+
+FLOP_PER_SUBSTEP = _flop_per_substep()
 PEAK_FP64_TFLOPS = 78.6
 PEAK_HBM_GBS = 8000.0
 # reference's published GpuDogfight.step rate at 16k envs (RTX 3070 Ti, cuda_fdm/README.md:130)
@@ -598,7 +608,8 @@ def main():
         "roofline": {"bound": "valu", "achieved": achieved, "peak": PEAK_FP64_TFLOPS,
                      "unit": "TFLOP/s", "frac": achieved / PEAK_FP64_TFLOPS, "traffic": profiled_traffic(),
                      "kernel": "fdm_step_split_kernel<120>", "kernel_ms": kern_ms,
-                     "flop_per_launch": flop_launch},
+                     "flop_per_launch": flop_launch, "flop_per_substep": FLOP_PER_SUBSTEP,
+                     "flop_source": "op-counted CPU restatement, tests/golden/fdm_flops.json"},
         "wall_s": wall,
     }
     if not args.no_cpu:

@@ -508,6 +508,41 @@ def test_env_step_pool_tables_equal_rebuild(gpu, obs_dim, nenv):
     assert envs[0]._pool_key is not None and envs[1]._pool_key is None
 
 
+def test_step_training_and_capture_switch(gpu):
+    """The root lineage's surface (cuda_fdm/rl_env.py:518-529): step_training and
+    step(capture_terminal_obs=False) return the same observation, reward, done and info as a
+    capturing step, with info["terminal_obs"] None; the instance default survives a failing
+    step_training."""
+    E = import_pkg("rl_env").GpuDogfightVecEnv
+    envs = [E(200, seed=3, ic_pool_size=32, max_engage_time_s=0.5) for _ in range(3)]
+    for env in envs:
+        env.reset(stagger=True, max_stagger_steps=5)
+    rng = np.random.default_rng(2)
+    for k in range(6):
+        act = torch.as_tensor(rng.uniform(-1, 1, (400, 4)), device=gpu)
+        pick = torch.as_tensor(rng.integers(0, 32, 200), device=gpu)
+        torch.manual_seed(k)
+        a = envs[0].step(act, reset_indices=pick)
+        b = envs[1].step(act, reset_indices=pick, capture_terminal_obs=False)
+        c = envs[2].step(act, reset_indices=pick, terminal_obs=False)
+        assert a[3]["terminal_obs"] is not None
+        assert b[3]["terminal_obs"] is None and c[3]["terminal_obs"] is None
+        for x, y in ((a, b), (a, c)):
+            for i in range(3):
+                assert torch.equal(x[i], y[i]), (k, i)
+            for key in x[3]:
+                if key != "terminal_obs":
+                    assert torch.equal(x[3][key], y[3][key]), (k, key)
+    # step_training draws its own pool picks (torch.randint on the env's generator)
+    env = envs[2]
+    out = env.step_training(torch.zeros(400, 4, dtype=torch.float64, device=gpu))
+    assert out[3]["terminal_obs"] is None and env._capture_terminal_obs
+    with pytest.raises((ValueError, RuntimeError)):
+        env.step_training(torch.zeros(3, 4, dtype=torch.float64, device=gpu))
+    assert env._capture_terminal_obs is True
+    assert env.step(torch.zeros(400, 4, dtype=torch.float64, device=gpu))[3]["terminal_obs"] is not None
+
+
 def test_env_post_step_bad_pick_poisons_state(gpu):
     """A pool index out of range never reads out of bounds: the engagement becomes NaN."""
     nenv = 4

@@ -6,6 +6,7 @@ small tables, values printed in the reference's own generated header, golden vec
 from the reference's Python, and the reference's own host-compiled C model (oracle/_ref)."""
 import ast
 import importlib
+import importlib.util
 import math
 import os
 import re
@@ -391,3 +392,30 @@ def test_drift_envelope_rejects_planted_drift(orc):
             if broke is None and (oracle_lib.drift_quantiles(a, b, alive) > bound).any():
                 broke = d + 1
     assert broke is not None and broke <= 150, broke
+
+
+# ------------------------------------------------------------------ FLOP-count fixture
+def test_flop_fixture_reproduces():
+    """tests/golden/fdm_flops.json (bench.py's algorithmic FLOPs per aircraft-substep) is what the
+    counting build of the restatement (oracle/opcount.hpp) tallies on its samples; that build
+    steps the aircraft bit for bit like the plain restatement, so it counts the restatement's
+    own operations; and the counts sit within 2 % of the reference model's static count
+    (1,550: 114 divisions, ~11 square roots, ~18 libm calls)."""
+    import json
+    spec = importlib.util.spec_from_file_location(
+        "make_flops_golden", os.path.join(ROOT, "tests", "golden", "make_flops_golden.py"))
+    M = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(M)
+    icm = importlib.import_module("2026_ai_pilot_challenge-1st_solution_amd.ic")
+    orc, lib = M.load_counter()
+    fix = json.load(open(os.path.join(ROOT, "tests", "golden", "fdm_flops.json")))
+    for name, (ic, act, rate) in M.samples(icm).items():
+        per, st = M.count(orc, lib, ic, act, rate)
+        want = fix["per_aircraft_substep"][name]
+        for k in M.KEYS + ("flop",):
+            assert abs(per[k] - want[k]) <= 1e-6 * max(1.0, want[k]), (name, k)
+        assert per["aircraft_substeps"] == want["aircraft_substeps"]
+        plain = orc.seed(ic, rate)
+        orc.rollout(plain, np.ascontiguousarray(act), 6, rate)
+        assert np.array_equal(st, plain, equal_nan=True), name    # crashed rows: NaN signs vary
+        assert abs(per["flop"] / 1550.0 - 1.0) < 0.02, (name, per["flop"])
