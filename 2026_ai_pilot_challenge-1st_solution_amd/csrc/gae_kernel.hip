@@ -20,8 +20,34 @@
 
 namespace f16 {
 
-constexpr int kGaeBlock = 256;
-constexpr int kGaeChunk = 8;   // time steps whose loads are issued together
+// 64-thread workgroups: at BASELINE C4 ([64, 16384, 2] = 32,768 columns) that is 512
+// workgroups, two per CU, so every CU streams (256-thread workgroups left half of them idle).
+constexpr int kGaeBlock = 64;
+// Time steps per chunk.  Chunks are double-buffered: the next chunk's loads are issued before
+// the current chunk's recurrence runs, so at T = 64 all of a column's loads are in flight at
+// once and each lane waits out one memory latency instead of one per chunk.
+constexpr int kGaeChunk = 32;
+
+struct GaeChunk {
+  float r[kGaeChunk], v[kGaeChunk], d[kGaeChunk];
+};
+
+// Steps t_hi, t_hi - 1, ..., t_hi - kGaeChunk + 1 of column c (steps below 0 are not read).
+__device__ __forceinline__ void gae_load(GaeChunk& x, const float* __restrict__ rew,
+                                         const float* __restrict__ val,
+                                         const float* __restrict__ done, int t_hi, int ncol,
+                                         int nenv, int c, int e) {
+#pragma unroll
+  for (int k = 0; k < kGaeChunk; ++k) {
+    const int t = t_hi - k;
+    if (t >= 0) {
+      const long i = (long)t * ncol + c;
+      x.r[k] = rew[i];
+      x.v[k] = val[i];
+      x.d[k] = done[(long)t * nenv + e];
+    }
+  }
+}
 
 __global__ __launch_bounds__(kGaeBlock) void gae_kernel(
     const float* __restrict__ rew, const float* __restrict__ val, const float* __restrict__ done,
@@ -35,39 +61,24 @@ __global__ __launch_bounds__(kGaeBlock) void gae_kernel(
   float a_next = 0.0f;
   float v_next = last_val[c];
   float nnt = 1.0f - next_done[e];
-  int t = T - 1;
-  // chunks of kGaeChunk steps: issue all loads of the chunk, then the dependent recurrence
-  for (; t >= kGaeChunk - 1; t -= kGaeChunk) {
-    float r[kGaeChunk], v[kGaeChunk], d[kGaeChunk];
+  GaeChunk cur, nxt;
+  gae_load(cur, rew, val, done, T - 1, ncol, nenv, c, e);
+  for (int t = T - 1; t >= 0; t -= kGaeChunk) {
+    if (t - kGaeChunk >= 0) gae_load(nxt, rew, val, done, t - kGaeChunk, ncol, nenv, c, e);
 #pragma unroll
     for (int k = 0; k < kGaeChunk; ++k) {
-      const long i = (long)(t - k) * ncol + c;
-      r[k] = rew[i];
-      v[k] = val[i];
-      d[k] = done[(long)(t - k) * nenv + e];
+      if (t - k >= 0) {
+        const float g = gamma * v_next;
+        const float delta = (cur.r[k] + g * nnt) - cur.v[k];
+        a_next = delta + (gamma_lambda * nnt) * a_next;
+        const long i = (long)(t - k) * ncol + c;
+        adv[i] = a_next;
+        ret[i] = a_next + cur.v[k];
+        v_next = cur.v[k];
+        nnt = 1.0f - cur.d[k];
+      }
     }
-#pragma unroll
-    for (int k = 0; k < kGaeChunk; ++k) {
-      const float g = gamma * v_next;
-      const float delta = (r[k] + g * nnt) - v[k];
-      a_next = delta + (gamma_lambda * nnt) * a_next;
-      const long i = (long)(t - k) * ncol + c;
-      adv[i] = a_next;
-      ret[i] = a_next + v[k];
-      v_next = v[k];
-      nnt = 1.0f - d[k];
-    }
-  }
-  for (; t >= 0; --t) {
-    const long i = (long)t * ncol + c;
-    const float rr = rew[i], vv = val[i];
-    const float g = gamma * v_next;
-    const float delta = (rr + g * nnt) - vv;
-    a_next = delta + (gamma_lambda * nnt) * a_next;
-    adv[i] = a_next;
-    ret[i] = a_next + vv;
-    v_next = vv;
-    nnt = 1.0f - done[(long)t * nenv + e];
+    cur = nxt;
   }
 }
 
