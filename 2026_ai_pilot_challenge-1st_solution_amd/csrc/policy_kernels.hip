@@ -27,43 +27,52 @@
 
 namespace f16pol {
 
-// One network's two tanh layers for the workgroup's 64 rows: X (LDS) -> Hs -> Hs.  Wave w owns
-// units [32w, 32w + 32) of each layer.
-template <int KP>
+// One network's two tanh layers for the workgroup's 32 NR rows: X (LDS) -> Hs -> Hs.  Wave w
+// owns units [32w, 32w + 32) of each layer; every weight fragment it streams feeds NR MFMAs.
+template <int KP, int NR>
 __device__ __forceinline__ void hidden_layers(const __bf16* Xs, __bf16* Hs, const __bf16* W1,
                                               const float* b1, const __bf16* W2, const float* b2,
                                               int wave, int lane) {
   constexpr int XP = KP + 8;
   {
-    f32x16 acc[2];
+    f32x16 acc[NR];
     init_bias(acc, b1, 32 * wave, lane);
-    gemm_t<2, KP>(acc, W1, 32 * wave, Xs, XP, 0, lane);
+    gemm_t<NR, KP>(acc, W1, 32 * wave, Xs, XP, 0, lane);
     store_tanh(acc, Hs, 32 * wave, lane);
   }
   __syncthreads();
-  f32x16 acc[2];
+  f32x16 acc[NR];
   init_bias(acc, b2, 32 * wave, lane);
-  gemm_t<2, kHid>(acc, W2, 32 * wave, Hs, kHPitch, 0, lane);
+  gemm_t<NR, kHid>(acc, W2, 32 * wave, Hs, kHPitch, 0, lane);
   __syncthreads();                                    // every wave has read layer 1
   store_tanh(acc, Hs, 32 * wave, lane);
   __syncthreads();
 }
 
-template <int KP>
-__global__ __launch_bounds__(kThreads, 2) void policy_kernel(const F16PolicyArgs p) {
+// RB observation rows per 8-wave workgroup (64 or 128).  128 rows halve the weight bytes each row
+// costs the CU's vector-memory path (every wave streams its 32-unit slice of every layer once
+// per workgroup) and give each weight fragment 4 MFMAs instead of 2, but the workgroup then
+// holds the whole CU's LDS share (one per CU) and measured slower on MI355X (32,768 rows:
+// 43.3 us against 39.8 us with 64 rows, two workgroups per CU), so the launch uses 64.  Each
+// row's arithmetic is the same for both sizes.
+constexpr int kPolicyRows = 64;
+template <int KP, int RB>
+__global__ __launch_bounds__(kThreads, RB == 64 ? 2 : 1) void policy_kernel(const F16PolicyArgs p) {
   constexpr int XP = KP + 8;
-  static_assert(kRows * kLPitch * 4 <= kRows * kHPitch * 2, "logits reuse the hidden rows' LDS");
-  __shared__ __align__(16) __bf16 Xs[kRows * XP];
-  __shared__ __align__(16) __bf16 Hs[kRows * kHPitch];
+  constexpr int NR = RB / 32;                          // 32-row MFMA tiles per wave and layer
+  constexpr int NRH = RB / 64;                         // row tiles per wave of the logits head
+  static_assert(RB * kLPitch * 4 <= RB * kHPitch * 2, "logits reuse the hidden rows' LDS");
+  __shared__ __align__(16) __bf16 Xs[RB * XP];
+  __shared__ __align__(16) __bf16 Hs[RB * kHPitch];
   __shared__ float col_mean[KP], col_sd[KP];
   const int gi = blockIdx.y;
   if (gi >= p.ngroups) return;
   const F16PolicyGroup G = p.group[gi];
   const int gb = p.group_offsets ? p.group_offsets[gi] : G.row_begin;
   const int ge = p.group_offsets ? p.group_offsets[gi + 1] : G.row_end;
-  const int r0 = gb + blockIdx.x * kRows;
+  const int r0 = gb + blockIdx.x * RB;
   if (r0 >= ge) return;                               // uniform per workgroup
-  const int nr = min(kRows, ge - r0);
+  const int nr = min(RB, ge - r0);
   const float* g_mean = G.mean ? G.mean : p.mean;
   const float* g_var = G.mean ? G.var : p.var;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -71,16 +80,12 @@ __global__ __launch_bounds__(kThreads, 2) void policy_kernel(const F16PolicyArgs
   const float* wf = G.wf;
   constexpr int D = KP == 192 ? 184 : 214;              // observation width of this kernel
 
-  // ---- normalise (RunningNorm.normalize, ppo_gpu.py:210-214) and stage bf16 rows in LDS
-  if (tid < KP) {
-    const bool on = g_mean && tid < D;
-    col_mean[tid] = on ? g_mean[tid] : 0.0f;
-    col_sd[tid] = on ? sqrtf(g_var[tid] + p.eps) : 1.0f;
-  }
-  __syncthreads();
+  // ---- normalise (RunningNorm.normalize, ppo_gpu.py:210-214) and stage bf16 rows in LDS.
+  // The rows' loads go out first, then the statistics' (and the barrier that publishes them),
+  // so both memory latencies overlap.
   {
     constexpr int half = D / 2;                       // float2 per row
-    constexpr int kPer = (kRows * (KP / 2) + kThreads - 1) / kThreads;
+    constexpr int kPer = (RB * (KP / 2) + kThreads - 1) / kThreads;
     float2 x[kPer];
 #pragma unroll
     for (int q = 0; q < kPer; ++q) {                   // issue every load before using any
@@ -93,11 +98,17 @@ __global__ __launch_bounds__(kThreads, 2) void policy_kernel(const F16PolicyArgs
         x[q] = *reinterpret_cast<const float2*>(p.obs + pr * p.obs_ld + 2 * c);
       }
     }
+    if (tid < KP) {
+      const bool on = g_mean && tid < D;
+      col_mean[tid] = on ? g_mean[tid] : 0.0f;
+      col_sd[tid] = on ? sqrtf(g_var[tid] + p.eps) : 1.0f;
+    }
+    __syncthreads();
 #pragma unroll
     for (int q = 0; q < kPer; ++q) {
       const int idx = tid + q * kThreads;
       const int r = idx / half, c = idx - r * half;
-      if (r < kRows) {
+      if (r < RB) {
         float v0 = x[q].x, v1 = x[q].y;
         if (r < nr) {
           if (g_mean) {
@@ -116,33 +127,37 @@ __global__ __launch_bounds__(kThreads, 2) void policy_kernel(const F16PolicyArgs
         *reinterpret_cast<bf16x2*>(Xs + r * XP + 2 * c) = b;
       }
     }
-    for (int idx = tid; idx < kRows * (KP - D); idx += kThreads) {   // zero the K padding
+    for (int idx = tid; idx < RB * (KP - D); idx += kThreads) {   // zero the K padding
       const int r = idx / (KP - D);
       Xs[r * XP + D + (idx - r * (KP - D))] = (__bf16)0.0f;
     }
   }
   __syncthreads();
 
-  // ---- actor: two tanh layers, then the logits head on waves 0-5 (32 units x 32 rows each)
-  hidden_layers<KP>(Xs, Hs, wbf + Blob<KP>::W1, wf + kB1, wbf + Blob<KP>::W2A, wf + kB2A, wave,
-                    lane);
+  // ---- actor: two tanh layers, then the logits head on waves 0-5 (32 units x 32 NRH rows each)
+  hidden_layers<KP, NR>(Xs, Hs, wbf + Blob<KP>::W1, wf + kB1, wbf + Blob<KP>::W2A, wf + kB2A,
+                        wave, lane);
   float* Ls = reinterpret_cast<float*>(Hs);
   {
-    const int ut = wave % 3, rt = wave / 3;
-    f32x16 acc[1];
+    const int ut = wave % 3, rt = (wave / 3) * NRH;
+    f32x16 acc[NRH];
     if (wave < 6) {
       init_bias(acc, wf + kB3A, 32 * ut, lane);
-      gemm_t<1, kHid>(acc, wbf + Blob<KP>::W3A, 32 * ut, Hs + 32 * rt * kHPitch, kHPitch, 0,
-                      lane);
+      gemm_t<NRH, kHid>(acc, wbf + Blob<KP>::W3A, 32 * ut, Hs + 32 * rt * kHPitch, kHPitch, 0,
+                        lane);
     }
     __syncthreads();                                  // every wave has read actor layer 2
     if (wave < 6) {
-      const int row = 32 * rt + (lane & 31);
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int unit = 32 * ut + 8 * g + (lane >> 5) * 4;
-        *reinterpret_cast<float4*>(Ls + row * kLPitch + unit) =
-            make_float4(acc[0][4 * g + 0], acc[0][4 * g + 1], acc[0][4 * g + 2], acc[0][4 * g + 3]);
+      for (int r = 0; r < NRH; ++r) {
+        const int row = 32 * (rt + r) + (lane & 31);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int unit = 32 * ut + 8 * g + (lane >> 5) * 4;
+          *reinterpret_cast<float4*>(Ls + row * kLPitch + unit) =
+              make_float4(acc[r][4 * g + 0], acc[r][4 * g + 1], acc[r][4 * g + 2],
+                          acc[r][4 * g + 3]);
+        }
       }
     }
   }
@@ -150,7 +165,7 @@ __global__ __launch_bounds__(kThreads, 2) void policy_kernel(const F16PolicyArgs
 
   // ---- per (row, channel): softmax, draw, log-probability, control (waves 0-3)
   const uint32_t step = p.step + (p.step_base ? *p.step_base : 0u);
-  if (tid < kRows * kChan) {
+  if (tid < RB * kChan) {
     const int row = tid >> 2, ch = tid & 3;
     const float* l = Ls + row * kLPitch + ch * kBins;
     float lg[kBins];
@@ -202,11 +217,12 @@ __global__ __launch_bounds__(kThreads, 2) void policy_kernel(const F16PolicyArgs
   }
   __syncthreads();                                    // the logits are consumed
 
-  // ---- critic: two tanh layers, then the value dot products (one row per lane of wave 0)
-  hidden_layers<KP>(Xs, Hs, wbf + Blob<KP>::W1C, wf + kB1 + kHid, wbf + Blob<KP>::W2C,
-                    wf + kB2C, wave, lane);
-  if (wave == 0) {
-    const int row = lane;
+  // ---- critic: two tanh layers, then the value dot products (one row per lane of waves
+  // 0 .. RB/64 - 1)
+  hidden_layers<KP, NR>(Xs, Hs, wbf + Blob<KP>::W1C, wf + kB1 + kHid, wbf + Blob<KP>::W2C,
+                        wf + kB2C, wave, lane);
+  if (wave < RB / 64) {
+    const int row = 64 * wave + lane;
     const float* w3 = wf + kW3C;
     float s = 0.0f;
 #pragma unroll 4
@@ -480,13 +496,13 @@ extern "C" int f16_policy_step(const F16PolicyArgs* a, void* stream) {
     max_rows = a->max_group_rows;
   }
   if (max_rows == 0) return 0;
-  const dim3 grid((unsigned)((max_rows + kRows - 1) / kRows), (unsigned)a->ngroups), block(kThreads);
   if (a->obs_ld % 2 || ((uintptr_t)a->obs & 7) || (a->nobs_out && (a->nobs_ld % 2 || ((uintptr_t)a->nobs_out & 7))))
     return F16_EINVAL;                                   // rows are moved as float2
-  if (a->obs_dim == 184)
-    hipLaunchKernelGGL(policy_kernel<192>, grid, block, 0, (hipStream_t)stream, *a);
-  else
-    hipLaunchKernelGGL(policy_kernel<224>, grid, block, 0, (hipStream_t)stream, *a);
+  constexpr int rb = kPolicyRows;
+  const dim3 grid((unsigned)((max_rows + rb - 1) / rb), (unsigned)a->ngroups), block(kThreads);
+  hipStream_t s = (hipStream_t)stream;
+  if (a->obs_dim == 184) hipLaunchKernelGGL((policy_kernel<192, rb>), grid, block, 0, s, *a);
+  else hipLaunchKernelGGL((policy_kernel<224, rb>), grid, block, 0, s, *a);
   return f16_last_error();
 }
 
