@@ -259,19 +259,23 @@ def _env_kernel_ms(env, acts, warmup, n):
     return fdm_ms, post_ms
 
 
-def env_step_bench(pkg, nenv, steps, warmup, scan_finite=False):
+def env_step_bench(pkg, nenv, steps, warmup, scan_finite=False, ab=True, stagger=True,
+                   pool_tables=True):
     """Full environment transitions: GpuDogfightVecEnv.step = FDM decision (6 substeps, FCS 60 Hz)
     + the fused post-physics kernel (advance, reward, termination, terminal observation, pool
     autoreset, new observation), contest ICs with the staggered reset spread over the whole
     200 s engagement (so timeouts and deaths autoreset engagements inside the timed loop),
     random 4-channel actions resident on the device.  The physics launch hands the post-physics
     launch its per-aircraft finite flags; the same steps are timed again with the post-physics
-    launch re-reading the state for them (A/B in one process).  scan_finite: time only that
-    variant (profiling aid)."""
+    launch re-reading the state for them (A/B in one process).  ab=False: time only one variant,
+    the flag hand-off, or with scan_finite the re-reading launch; stagger=False starts every
+    engagement at t = 0 (no autoresets in the window); pool_tables=False rebuilds autoreset rows
+    instead of copying them (profiling aids)."""
     import torch
     env_mod = importlib.import_module(PKG + ".rl_env")
     env = env_mod.GpuDogfightVecEnv(nenv, seed=0)
-    env.reset(stagger=True, max_stagger_steps=STAGGER_STEPS)
+    env.pool_tables = pool_tables
+    env.reset(stagger=stagger, max_stagger_steps=STAGGER_STEPS)
     g = torch.Generator(device="cuda").manual_seed(0)
     acts = torch.rand(warmup + steps, 2 * nenv, 4, generator=g, device="cuda",
                       dtype=torch.float64) * 2 - 1
@@ -281,7 +285,10 @@ def env_step_bench(pkg, nenv, steps, warmup, scan_finite=False):
     post_bytes = POST_BYTES_PER_AIRCRAFT * 2 * nenv
     runs = {True: [], False: []}
     # alternating order (A B B A): whichever variant runs first after the warm-up pays for it
-    order = (False, False) if scan_finite else (True, False, False, True)
+    if not ab:
+        order = (False,) if scan_finite else (True,)
+    else:
+        order = (True, False, False, True)
     for fused in order:
         env.fused_finite = fused
         env.sim.states.copy_(snap_states)        # both variants step the same engagements
@@ -300,10 +307,11 @@ def env_step_bench(pkg, nenv, steps, warmup, scan_finite=False):
                       "fdm_kernel_ms": fdm_ms, "post_kernel_ms": post_ms, "algorithmic_bytes": b,
                       "achieved_GBs": b / (post_ms * 1e-3) / 1e9,
                       "hbm_frac": b / (post_ms * 1e-3) / 1e9 / PEAK_HBM_GBS}
-    main = res[False] if scan_finite else res[True]
+    main = res[False] if (scan_finite and not ab) else res[True]
     out = {"workload": "contest_env_step_16k", "engagements": nenv, "obs_dim": 184,
            "substeps": env.substeps, "fcs_rate_hz": env.sim.fcs_rate,
-           "reset": f"stagger over {STAGGER_STEPS} decisions", "finite_flags": not scan_finite,
+           "reset": f"stagger over {STAGGER_STEPS} decisions" if stagger else "no stagger",
+           "pool_tables": pool_tables, "finite_flags": not (scan_finite and not ab),
            "transitions_per_s": nenv / (main["ms_per_step"] * 1e-3),
            "ms_per_step": main["ms_per_step"], "fdm_kernel_ms": main["fdm_kernel_ms"],
            "post_kernel_ms": main["post_kernel_ms"], "episodes_done": main["episodes_done"],
@@ -311,7 +319,7 @@ def env_step_bench(pkg, nenv, steps, warmup, scan_finite=False):
            "post_kernel": {"kernel": "env_post_step_split_kernel<184,true>",
                            "algorithmic_bytes": main["algorithmic_bytes"],
                            "achieved_GBs": main["achieved_GBs"], "hbm_frac": main["hbm_frac"]}}
-    if not scan_finite:
+    if ab:
         out["state_scan_ab"] = {"what": "post-physics launch re-reading the 86 other state doubles "
                                         "for the finite flag instead of the physics launch's flag",
                                 **res[False]}
@@ -506,6 +514,11 @@ def main():
     ap.add_argument("--scan-finite", action="store_true",
                     help="with --only env: time only the post-physics launch that re-reads the "
                          "state for the finite flags (profiling aid)")
+    ap.add_argument("--no-stagger", action="store_true",
+                    help="with --only env: every engagement starts at t = 0 (profiling aid)")
+    ap.add_argument("--rebuild-resets", action="store_true",
+                    help="with --only env: autoresets rebuild their rows instead of copying the "
+                         "pool tables (profiling aid)")
     ap.add_argument("--only", choices=["fdm", "env", "rollout", "league", "update"], default=None,
                     help="profiling aid: run only this section and print its own JSON line "
                          "(not the contract line)")
@@ -534,7 +547,9 @@ def main():
     icm = importlib.import_module(PKG + ".ic")
     if args.only in ("env", "rollout", "league", "update"):
         part = {"env": lambda: env_step_bench(pkg, args.nenv, args.steps, args.warmup,
-                                              scan_finite=args.scan_finite),
+                                              scan_finite=args.scan_finite, ab=False,
+                                              stagger=not args.no_stagger,
+                                              pool_tables=not args.rebuild_resets),
                 "rollout": lambda: rollout_bench(args.nenv),
                 "league": lambda: league_bench(),
                 "update": lambda: update_bench(args.nenv)}[args.only]()
