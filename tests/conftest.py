@@ -47,3 +47,27 @@ def gpu():
         pytest.fail("GPU test collected on a host without a HIP device")
     import torch
     return torch.device("cuda")
+
+
+# Measured worst errors of the parity tests, printed beside their bounds at the end of the run.
+_WORST = []
+
+
+@pytest.fixture(scope="session")
+def worst():
+    """worst(name, value, bound): record a test's measured worst error against its bound."""
+    def rec(name, value, bound):
+        _WORST.append((name, float(value), float(bound)))
+    return rec
+
+
+def pytest_terminal_summary(terminalreporter):
+    if not _WORST:
+        return
+    terminalreporter.section("measured worst errors (value / bound)")
+    best = {}
+    for name, v, b in _WORST:
+        if name not in best or v > best[name][0]:
+            best[name] = (v, b)
+    for name, (v, b) in best.items():
+        terminalreporter.write_line(f"{name}: {v:.3e} / {b:.1e}")

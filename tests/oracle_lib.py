@@ -152,6 +152,14 @@ def rel_err(got, want, floor_frac=1e-3):
     return np.abs(got - want) / den
 
 
+
+def raw_rel_err(got, want):
+    """|got - want| / |want| with no floor (entries whose reference value is exactly zero report
+    the absolute difference): the per-variable figure before rel_err's scale floor."""
+    got = np.asarray(got, dtype=np.float64); want = np.asarray(want, dtype=np.float64)
+    d = np.abs(got - want)
+    return np.where(want != 0, d / np.where(want != 0, np.abs(want), 1.0), d)
+
 # ------------------------------------------------------------------ observation / reward oracle
 class _OrcObrStruct(ctypes.Structure):
     _fields_ = [("nenv", ctypes.c_long)] + [

@@ -31,7 +31,7 @@ def _bin_actions(rng, n):
 
 
 @pytest.mark.parametrize("obs_dim,nenv,ndec", [(184, 16384, 24), (214, 4096, 20)])
-def test_env_step_chain_matches_oracle(gpu, orc, obs_dim, nenv, ndec):
+def test_env_step_chain_matches_oracle(gpu, orc, obs_dim, nenv, ndec, worst):
     E = import_pkg("rl_env").GpuDogfightVecEnv
     env = E(nenv, seed=5, ic_pool_size=256, obs_dim=obs_dim, max_engage_time_s=12.0)
     env.reset(stagger=True, max_stagger_steps=128)
@@ -70,6 +70,12 @@ def test_env_step_chain_matches_oracle(gpu, orc, obs_dim, nenv, ndec):
         # physics: live rows per step, autoreset rows exactly the pool's
         got = env.sim.states.cpu().numpy()
         live = ~rows
+        e_obs = np.abs(obs.reshape(n, obs_dim).cpu().numpy() - obs_o).max()
+        worst(f"env chain {obs_dim}, state rel_err", oracle_lib.rel_err(got[live], st1[live]).max(),
+              1e-10)
+        worst(f"env chain {obs_dim}, reward |err|", np.abs(rew.reshape(n).cpu().numpy() - r_o).max(),
+              VAL_TOL)
+        worst(f"env chain {obs_dim}, observation |err|", e_obs, OBS_TOL)
         assert oracle_lib.rel_err(got[live], st1[live]).max() <= 1e-10, d
         np.testing.assert_array_equal(got[rows], st2[rows], err_msg=str(d))
         # observation, terminal observation, reward, reconstructor

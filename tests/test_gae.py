@@ -61,10 +61,15 @@ def test_gpu_boundary_known_answer(gpu):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("T,nenv,nag", [(64, 16384, 2), (13, 1000, 1), (1, 7, 2), (9, 33, 3)])
+@pytest.mark.parametrize("T,nenv,nag", [(64, 16384, 2), (13, 1000, 1), (1, 7, 2), (9, 33, 3),
+                                         (16, 100, 2), (17, 65, 2), (128, 4096, 2),
+                                         (256, 300, 2), (257, 70, 2), (300, 129, 1),
+                                         (20, 32768, 2)])
 def test_gpu_bit_exact(gpu, T, nenv, nag):
-    """BASELINE C4 shape [64, 16384] x 2 agents plus ragged shapes; bit-exact vs the fp32
-    restatement, within 1e-6 of the float64 recurrence."""
+    """BASELINE C4 shape [64, 16384] x 2 agents plus ragged shapes (partial segments and
+    column blocks, one to sixteen 16-step segments; past 256 steps or from 65,536 columns on,
+    the chunked kernel);
+    bit-exact vs the fp32 restatement, within 1e-5 of the float64 recurrence."""
     import torch
     ppo = import_pkg("ppo")
     rng = np.random.default_rng(T * 7 + nenv)

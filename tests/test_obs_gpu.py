@@ -72,7 +72,7 @@ def _soa(gpu, states_aos):
 
 # ------------------------------------------------------------------------ golden replay
 @pytest.mark.parametrize("mode", [0, 1, 2, 3])
-def test_golden_replay_matches_reference(gpu, mode):
+def test_golden_replay_matches_reference(gpu, mode, worst):
     """The scripted reference sequence (damage, hard deck, HP death, timeout, masked resets)
     through the GPU kernels against the reference's own outputs."""
     g = oracle_lib.golden("obs_golden.npz")
@@ -87,6 +87,9 @@ def test_golden_replay_matches_reference(gpu, mode):
         act = torch.as_tensor(g["in_actions"][k], device=gpu)
         r, te, tr = obr.kernel_advance(st, act, reward_mode=mode)
         obs = obr.kernel_build_obs(st).cpu().numpy()
+        worst("golden replay 184, reward |err|", np.abs(r.cpu().numpy() - key("reward")[k]).max(),
+              VAL_TOL)
+        worst("golden replay 184, observation |err|", np.abs(obs - g["m0_obs"][k]).max(), OBS_TOL)
         assert np.abs(r.cpu().numpy() - key("reward")[k]).max() <= VAL_TOL, (k, "reward")
         np.testing.assert_array_equal(te.cpu().numpy().astype(bool), g["m0_term"][k].astype(bool))
         np.testing.assert_array_equal(tr.cpu().numpy().astype(bool), g["m0_trunc"][k].astype(bool))
@@ -234,7 +237,7 @@ def test_external_214_matches_oracle(gpu, orc, nenv):
     np.testing.assert_array_equal(obs184[:, 164:], obs[:, 194:])
 
 
-def test_golden_replay_214_matches_root_reference(gpu):
+def test_golden_replay_214_matches_root_reference(gpu, worst):
     """The scripted sequence through the GPU's 214-D path against the root lineage's own torch
     path (cuda_fdm/obs_reward.py advance :544-582, build_obs :585-721; golden written by
     tests/golden/make_obs_golden.py --root214): observation, acceleration and the previous NED
@@ -252,6 +255,9 @@ def test_golden_replay_214_matches_root_reference(gpu):
         act = torch.as_tensor(g["in_actions"][k], device=gpu)
         r, te, tr = obr.kernel_advance(st, act)
         obs = obr.build_external_obs(st).cpu().numpy()
+        worst("golden replay 214, observation |err|", np.abs(obs - a["a214_obs"][k]).max(), OBS_TOL)
+        worst("golden replay 214, acceleration |err| m/s2",
+              np.abs(c(obr.external_accel) - a["a214_accel"][k]).max(), VAL_TOL * 100)
         assert np.abs(obs - a["a214_obs"][k]).max() <= OBS_TOL, (k, "obs")
         assert np.abs(c(obr.external_accel) - a["a214_accel"][k]).max() <= VAL_TOL * 100, k
         assert np.abs(c(obr.external_previous_velocity)

@@ -185,7 +185,7 @@ def _setup(gpu, obs_dim, n, seed, init="normal"):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("obs_dim,init", [(184, "normal"), (184, "orthogonal"), (214, "normal")])
-def test_policy_step_matches_reference(gpu, orc, obs_dim, init):
+def test_policy_step_matches_reference(gpu, orc, obs_dim, init, worst):
     import torch
     n = 4096 + 37                                            # a ragged last tile
     P, net, obs, norm = _setup(gpu, obs_dim, n, 1, init)
@@ -208,9 +208,12 @@ def test_policy_step_matches_reference(gpu, orc, obs_dim, init):
     ref_l, ref_v = _ref_forward(net.cpu(), got_n)
     got_l, got_v = logits.cpu().numpy(), val.cpu().numpy()
     # one bf16 flip of a hidden activation moves a logit by ~2^-8 |w|: scale by the spread
-    for got, ref in ((got_l, ref_l), (got_v, ref_v)):
+    for name, got, ref in (("logits", got_l, ref_l), ("values", got_v, ref_v)):
         scale = max(1.0, float(np.std(ref)))
         err = np.abs(got - ref)
+        worst(f"policy {name} |err| / max(1, std) ({obs_dim})", err.max() / scale, 5e-3)
+        worst(f"policy {name} 99% quantile / max(1, std) ({obs_dim})",
+              np.quantile(err, 0.99) / scale, 1e-4)
         assert err.max() < 5e-3 * scale
         assert np.quantile(err, 0.99) < 1e-4 * scale
     # draw: exact against the checker on the kernel's logits
