@@ -9,8 +9,8 @@
 //                      activations held in LDS.  The layer inputs and output gradients every
 //                      weight gradient needs leave unit-major ([feature][row], bf16), so the
 //                      reduction over rows reads them as contiguous MFMA fragments;
-//   wgrad_kernel       every weight gradient dW = dY^T X as one split-K launch: 128 x 128 output
-//                      tiles of all four products, rows in chunks, 32-row stages double-buffered
+//   wgrad_kernel       every weight gradient dW = dY^T X as one split-K launch: 256 x 256 output
+//                      tiles of all four products, rows in chunks, 64-row stages double-buffered
 //                      through LDS, fp32 partials per chunk (bias gradients are the row sums of
 //                      dY, taken while staging);
 //   colsum kernels     the partials summed in a fixed order (deterministic, no atomics);
@@ -68,8 +68,8 @@ struct Flat {
 constexpr int kAdvThreads = 256;
 constexpr int kAdvPer = 8;                       // rows per thread of the advantage partials
 constexpr int kNormBlockElems = 4096;            // flat elements per squared-norm block
-constexpr int kWgradSlots = 768;                 // resident wgrad workgroups when the device
-                                                 // cannot be asked (3 per CU x 256 CUs)
+constexpr int kWgradSlots = 256;                 // resident wgrad workgroups when the device
+                                                 // cannot be asked (1 per CU x 256 CUs)
 constexpr int kMaxChunks = 64;                   // bound on the chunks the partials hold
 
 __host__ __device__ inline long align256(long x) { return (x + 255) & ~255L; }
@@ -94,7 +94,7 @@ inline long kColGroups(long nrows) { return (nrows + kColRows - 1) / kColRows; }
 
 inline int norm_blocks(long n) { return (int)((n + kNormBlockElems - 1) / kNormBlockElems); }
 
-inline int wgrad_tiles(int kp) { return 4 * ((kp + 127) / 128) + 4 + 4 + 2; }
+inline int wgrad_tiles(int kp) { return 2 * ((kp + 255) / 256) + 1 + 1 + 1; }
 
 inline Work layout(int obs_dim, long mb_rows, void* base, int wg_slots = kWgradSlots) {
   Work w{};
@@ -103,11 +103,11 @@ inline Work layout(int obs_dim, long mb_rows, void* base, int wg_slots = kWgradS
   w.ld = (mb_rows + 63) / 64 * 64;
   w.nwg = (int)(w.ld / 64);
   const int tiles = wgrad_tiles(kp);
-  // chunks of 32-row stages: one workgroup per resident slot (a grid a little above a
-  // multiple of the slots leaves a mostly idle last round), at least 8 stages each
+  // chunks of 64-row stages: one workgroup per resident slot (a grid a little above a
+  // multiple of the slots leaves a mostly idle last round), at least 4 stages each
   long chunks = std::max(1, std::min(wg_slots / tiles, kMaxChunks));
   long cr = (w.ld + chunks - 1) / chunks;
-  cr = (cr + 31) / 32 * 32;
+  cr = (cr + 63) / 64 * 64;
   if (cr < 256) cr = 256;
   w.chunk_rows = (int)cr;
   w.nchunk = (int)((w.ld + cr - 1) / cr);
@@ -601,11 +601,17 @@ __global__ __launch_bounds__(kThreads, 1) void ppo_fused_kernel(const F16PPOArgs
   }
 }
 
-// ---- weight gradients: C[a][b] = sum over rows of A[a][row] B[b][row], split over row chunks
-constexpr int kWT = 128;                  // output tile side
-constexpr int kWK = 32;                   // rows per stage
-constexpr int kWPitch = kWK + 8;          // bf16 per LDS feature row (16-byte reads spread over banks)
-constexpr int kWThreads = 256;
+// ---- weight gradients: C[a][b] = sum over rows of A[a][row] B[b][row], split over row chunks.
+// Output tiles are 256 x 256, so each product's operands are read once per row chunk (the
+// first layer's input twice, beside the two 256-unit halves of dH1): the kernel streams ~4.5 KB
+// per minibatch row against 4.2 KB of distinct operands.  Eight waves, 2 (A halves of 128) x 4
+// (B quarters of 64), each accumulating a 128 x 64 block as 4 x 2 MFMA 32x32 tiles; 64-row
+// stages double-buffered through LDS (147 KB), one workgroup per CU.
+constexpr int kWT = 256;                  // output tile side
+constexpr int kWK = 64;                   // rows per stage
+constexpr int kWPitch = kWK + 8;          // bf16 per LDS feature row (16-byte aligned, spread over banks)
+constexpr int kWThreads = 512;
+constexpr int kWPieces = kWT * kWK / 8 / kWThreads;   // 16-byte pieces per thread per operand
 
 struct WJob {
   const __bf16* A;
@@ -619,11 +625,11 @@ struct WJob {
 
 struct WJobs {
   WJob job[4];
-  unsigned char tj[24], ta[24], tb[24];
+  unsigned char tj[8], ta[8], tb[8];
   int ntiles;
 };
 
-__global__ __launch_bounds__(kWThreads, 2) void wgrad_kernel(const WJobs J, long ld, long mp,
+__global__ __launch_bounds__(kWThreads, 1) void wgrad_kernel(const WJobs J, long ld, long mp,
                                                              int chunk_rows, float* __restrict__ wpart,
                                                              long pld) {
   __shared__ __align__(16) __bf16 As[2][kWT * kWPitch];
@@ -635,17 +641,20 @@ __global__ __launch_bounds__(kWThreads, 2) void wgrad_kernel(const WJobs J, long
   const long k0 = (long)c * chunk_rows;
   const long k1 = min(k0 + chunk_rows, mp);
   const int nst = k1 > k0 ? (int)((k1 - k0) / kWK) : 0;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wa = wave & 1, wb = wave >> 1;
-  const int part = tid & 3;                   // 8-row piece of a feature's 32 rows
-  bf16x8 ra[2], rb[2];
-  float bsum[2] = {0.0f, 0.0f};
+  const int part = tid & 7;                   // 8-row piece of a feature's 64 rows
+  bf16x8 ra[kWPieces], rb[kWPieces];
+  float bsum[kWPieces];
+#pragma unroll
+  for (int q = 0; q < kWPieces; ++q) bsum[q] = 0.0f;
   const bf16x8 zero8 = {};
   auto load = [&](int st) {
     const long k = k0 + (long)st * kWK + 8 * part;
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const int f = (tid >> 2) + 64 * q;
+    for (int q = 0; q < kWPieces; ++q) {
+      const int f = (tid >> 3) + (kWThreads / 8) * q;
       ra[q] = fa0 + f < jb.nA ? *reinterpret_cast<const bf16x8*>(jb.A + (long)(fa0 + f) * ld + k)
                               : zero8;
       rb[q] = fb0 + f < jb.nB ? *reinterpret_cast<const bf16x8*>(jb.B + (long)(fb0 + f) * ld + k)
@@ -654,8 +663,8 @@ __global__ __launch_bounds__(kWThreads, 2) void wgrad_kernel(const WJobs J, long
   };
   auto stage = [&](int buf) {
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const int f = (tid >> 2) + 64 * q;
+    for (int q = 0; q < kWPieces; ++q) {
+      const int f = (tid >> 3) + (kWThreads / 8) * q;
       *reinterpret_cast<bf16x8*>(&As[buf][f * kWPitch + 8 * part]) = ra[q];
       *reinterpret_cast<bf16x8*>(&Bs[buf][f * kWPitch + 8 * part]) = rb[q];
       if (bias) {
@@ -664,9 +673,15 @@ __global__ __launch_bounds__(kWThreads, 2) void wgrad_kernel(const WJobs J, long
       }
     }
   };
-  f32x16 acc[2][2];
+  // MFMA blocks holding parameters or present features: wave-uniform
+  bool liveA[4], liveB[2];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < 4; ++i) liveA[i] = fa0 + 128 * wa + 32 * i < jb.nA;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) liveB[j] = fb0 + 64 * wb + 32 * j < jb.nB;
+  f32x16 acc[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -682,45 +697,47 @@ __global__ __launch_bounds__(kWThreads, 2) void wgrad_kernel(const WJobs J, long
     if (st + 1 < nst) load(st + 1);
 #pragma unroll
     for (int kk = 0; kk < kWK / 16; ++kk) {
-      bf16x8 af[2], bfg[2];
+      bf16x8 af[4], bfg[2];
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
-        af[i] = *reinterpret_cast<const bf16x8*>(&As[buf][(64 * wa + 32 * i + lr) * kWPitch +
+      for (int i = 0; i < 4; ++i)
+        af[i] = *reinterpret_cast<const bf16x8*>(&As[buf][(128 * wa + 32 * i + lr) * kWPitch +
                                                           16 * kk + lk]);
 #pragma unroll
       for (int j = 0; j < 2; ++j)
         bfg[j] = *reinterpret_cast<const bf16x8*>(&Bs[buf][(64 * wb + 32 * j + lr) * kWPitch +
                                                            16 * kk + lk]);
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = mfma(af[i], bfg[j], acc[i][j]);
+        for (int j = 0; j < 2; ++j)
+          if (liveA[i] && liveB[j]) acc[i][j] = mfma(af[i], bfg[j], acc[i][j]);
     }
     if (st + 1 < nst) stage(buf ^ 1);
     __syncthreads();
   }
   float* out = wpart + (long)c * pld;
-  // element e of acc[i][j]: a = fa0 + 64wa + 32i + 8(e/4) + 4(lane/32) + e%4, b = fb0 + 64wb + 32j + lane%32
+  // element e of acc[i][j]: a = fa0 + 128wa + 32i + 8(e/4) + 4(lane/32) + e%4, b = fb0 + 64wb + 32j + lane%32
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int b = fb0 + 64 * wb + 32 * j + lr;
       if (b >= jb.vB) continue;
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        const int aa = fa0 + 64 * wa + 32 * i + 8 * (e >> 2) + (lane >> 5) * 4 + (e & 3);
+        const int aa = fa0 + 128 * wa + 32 * i + 8 * (e >> 2) + (lane >> 5) * 4 + (e & 3);
         if (aa < jb.vA)
           out[jb.wbase[aa >> 8] + (long)(aa & 255) * jb.wld + b] = acc[i][j][e];
       }
     }
   if (bias) {
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
+    for (int q = 0; q < kWPieces; ++q) {
       float s = bsum[q];
       s += __shfl_xor(s, 1);
       s += __shfl_xor(s, 2);
-      const int aa = fa0 + (tid >> 2) + 64 * q;
+      s += __shfl_xor(s, 4);
+      const int aa = fa0 + (tid >> 3) + (kWThreads / 8) * q;
       if (part == 0 && aa < jb.vA) out[jb.bbase[aa >> 8] + (aa & 255)] = s;
     }
   }
@@ -936,15 +953,15 @@ static int device_cus() {
   return n;
 }
 
-// Resident wgrad workgroups: compute units x the kernel's occupancy (3 per CU on MI355X: 142
-// VGPRs, 40 KB LDS), asked once per process.
+// Resident wgrad workgroups: compute units x the kernel's occupancy (1 per CU on MI355X: 147 KB
+// LDS), asked once per process.
 static int wgrad_slots() {
   static int slots = 0;
   if (slots == 0) {
     int per_cu = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, wgrad_kernel, kWThreads, 0) !=
             hipSuccess || per_cu < 1)
-      per_cu = 3;
+      per_cu = 1;
     slots = per_cu * device_cus();
   }
   return slots;
@@ -995,7 +1012,7 @@ extern "C" int f16_ppo_grad(const F16PPOArgs* a, void* stream) {
                   {F.a_b3(), F.a_b3()}, 256};
   (void)na;
   int nt = 0;
-  const int ntA[4] = {4, 2, 2, 1}, ntB[4] = {(kp + 127) / 128, 2, 2, 2};
+  const int ntA[4] = {2, 1, 1, 1}, ntB[4] = {(kp + 255) / 256, 1, 1, 1};
   for (int j = 0; j < 4; ++j)
     for (int ta = 0; ta < ntA[j]; ++ta)
       for (int tb = 0; tb < ntB[j]; ++tb) {
