@@ -15,6 +15,7 @@ import torch
 import oracle_lib
 from conftest import ROOT, import_pkg
 from test_policy import oracle_sample, philox
+from test_rollout import _check_against_reference
 
 _spec = importlib.util.spec_from_file_location("gae_oracle", os.path.join(ROOT, "oracle", "gae_oracle.py"))
 GO = importlib.util.module_from_spec(_spec)
@@ -164,11 +165,11 @@ def test_league_rollout_buffers(gpu, orc):
     P = import_pkg("policy")
     R = import_pkg("ppo")
     E = import_pkg("rl_env").GpuDogfightVecEnv
-    nenv, T = 256, 8
+    nenv, T = 1024, 8
     env = E(nenv, seed=5, obs_dim=214, ic_pool_size=64, fuel_exhaustion=True,
             fuel_lbs_range=(0.0, 3.0))
     net = P.MLPActorCritic(214, init="normal", generator=torch.Generator().manual_seed(1)).to(gpu)
-    opps = _nets(P, 3, 214, gpu, 60)
+    opps = _nets(P, 8, 214, gpu, 60)                 # BASELINE C5's eight opponent networks
     ro = R.LeagueRollout(env, net, opps, T=T, seed=0)
     ro.reset(stagger=False)
     a0 = env.opp_assign.clone()
@@ -183,6 +184,7 @@ def test_league_rollout_buffers(gpu, orc):
         v = torch.empty(nenv, dtype=torch.float32, device=gpu)
         step(ro.b_obs[t], [(net, 0, nenv)], norm=None, logits_out=lg, value=v)
         assert torch.equal(v, ro.b_val[t]), t
+        _check_against_reference(net, ro.b_obs[t], lg, ro.b_val[t])
         idx, lp = oracle_sample(orc, lg.cpu().numpy(), rows, seed=0, step=g0 + t)
         np.testing.assert_array_equal(ro.b_act[t].cpu().numpy(), idx)
     ref_adv, ref_ret = GO.gae_f32(ro.b_rew.cpu().numpy(), ro.b_val.cpu().numpy(),
@@ -194,6 +196,50 @@ def test_league_rollout_buffers(gpu, orc):
     done_any = ro.b_done[1:].sum().item() + ro.next_done.sum().item()
     assert done_any > 0
     assert not torch.equal(a0, env.opp_assign)
+    assert len(np.unique(env.opp_assign.cpu().numpy())) == 8   # every opponent network has rows
     acts = env.sim.actions.cpu().numpy()
     grid = P.make_action_grid(21).double().numpy()
     assert np.isin(acts[1::2, :3], grid).all()           # opponents' controls are grid values
+
+
+@pytest.mark.gpu
+def test_full_c5_league_rollout(gpu, orc):
+    """BASELINE C5 at its stated size: 65,536 engagements x 128 steps, 214-D, eight opponent
+    networks drawn from Zipf(1.1) weights, fuel exhaustion (the bench's fuel range) so
+    engagements end and their opponents are redrawn inside the window.  GAE of the whole buffer
+    bit-exact against the float32 checker; on a 1,024-engagement sample of every 16th step, the
+    learner's stored values and the logits of its stored observations against the float64
+    reference evaluation and its stored draws against the draw checker; every opponent network
+    has engagements."""
+    P = import_pkg("policy")
+    R = import_pkg("ppo")
+    E = import_pkg("rl_env").GpuDogfightVecEnv
+    nenv, T = 65536, 128
+    env = E(nenv, seed=0, obs_dim=214, fuel_exhaustion=True, fuel_lbs_range=(100.0, 3000.0))
+    mk = lambda s: P.MLPActorCritic(214, init="normal", init_std=0.02,
+                                    generator=torch.Generator().manual_seed(s)).to(gpu)
+    net, opps = mk(0), [mk(100 + k) for k in range(8)]
+    ro = R.LeagueRollout(env, net, opps, T=T, seed=0)
+    ro.reset(stagger=False)
+    g0 = ro.global_step
+    adv, ret, stats = ro.collect()
+    torch.cuda.synchronize()
+    assert bool(stats["trajectory_finite"])
+    assert float(ro.b_done[1:].sum()) + float(ro.next_done.sum()) > 0
+    assert len(np.unique(env.opp_assign.cpu().numpy())) == 8
+    ref_adv, ref_ret = GO.gae_f32(ro.b_rew.cpu().numpy(), ro.b_val.cpu().numpy(),
+                                  ro.b_done.cpu().numpy(), ro.last_val.cpu().numpy(),
+                                  ro.next_done.cpu().numpy(), 0.99, 0.95)
+    np.testing.assert_array_equal(adv.cpu().numpy(), ref_adv)
+    np.testing.assert_array_equal(ret.cpu().numpy(), ref_ret)
+    step = P.PolicyStep(214, device=gpu, seed=0)
+    sample = np.sort(np.random.default_rng(8).choice(nenv, 1024, replace=False))
+    st = torch.as_tensor(sample, device=gpu)
+    for t in range(0, T, 16):
+        lg = torch.empty(nenv, 84, dtype=torch.float32, device=gpu)
+        v = torch.empty(nenv, dtype=torch.float32, device=gpu)
+        step(ro.b_obs[t], [(net, 0, nenv)], norm=None, logits_out=lg, value=v)
+        assert torch.equal(v[st], ro.b_val[t][st]), t
+        _check_against_reference(net, ro.b_obs[t], lg, ro.b_val[t], st)
+        idx, _ = oracle_sample(orc, lg[st].cpu().numpy(), 2 * sample, seed=0, step=g0 + t)
+        np.testing.assert_array_equal(ro.b_act[t][st].cpu().numpy(), idx)

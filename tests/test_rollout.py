@@ -16,7 +16,7 @@ import pytest
 import torch
 
 from conftest import ROOT, import_pkg
-from test_policy import oracle_sample
+from test_policy import _ref_forward, oracle_sample
 
 _spec = importlib.util.spec_from_file_location("gae_oracle", os.path.join(ROOT, "oracle", "gae_oracle.py"))
 GO = importlib.util.module_from_spec(_spec)
@@ -36,6 +36,20 @@ def _collector(gpu, nenv=256, T=12, seed=3, env_kw=None, **kw):
     return ro
 
 
+def _check_against_reference(net, nobs, logits, value, rows=None):
+    """Logits and values of stored rows against the float64 evaluation of the same network with
+    the kernel's bf16 roundings (the policy test's tolerance: 5e-3 x max(1, std), 99 % within
+    1e-4 x that scale)."""
+    x = nobs.cpu().numpy() if rows is None else nobs[rows].cpu().numpy()
+    ref_l, ref_v = _ref_forward(net, x)
+    for got, ref in ((logits, ref_l), (value, ref_v)):
+        got = got.cpu().numpy() if rows is None else got[rows].cpu().numpy()
+        scale = max(1.0, float(np.std(ref)))
+        err = np.abs(got - ref)
+        assert err.max() < 5e-3 * scale
+        assert np.quantile(err, 0.99) < 1e-4 * scale
+
+
 def test_rollout_buffers_consistent(gpu, orc):
     ro = _collector(gpu)
     T, nac, nenv = ro.T, ro.nac, ro.nenv
@@ -50,6 +64,7 @@ def test_rollout_buffers_consistent(gpu, orc):
         v = torch.empty(nac, dtype=torch.float32, device=gpu)
         step(ro.b_obs[t], [(ro.net, 0, nac)], norm=None, logits_out=lg, value=v)
         assert torch.equal(v, ro.b_val[t]), t
+        _check_against_reference(ro.net, ro.b_obs[t], lg, ro.b_val[t])
         idx, lp = oracle_sample(orc, lg.cpu().numpy(), np.arange(nac), seed=0, step=g0 + t)
         np.testing.assert_array_equal(ro.b_act[t].cpu().numpy(), idx)
         assert np.abs(ro.b_logp[t].cpu().numpy() - lp).max() < 1e-5
@@ -165,3 +180,38 @@ def test_fused_norm_partials_equal_separate_update(gpu, nenv, graph):
             assert torch.equal(getattr(a.norm, name), getattr(b.norm, name)), (r, name)
         done += a.b_done.sum().item()
     assert done > 0                            # rows rebuilt from the pool were in the sums
+
+
+def test_full_c4_rollout(gpu, orc):
+    """BASELINE C4 at its stated size: 16,384 engagements x 64 steps, the episode clocks
+    staggered over the 200 s limit so engagements end inside the window.  GAE of the whole
+    buffer bit-exact against the float32 checker; on a 1,024-row sample of every 8th step, the
+    stored values and the logits of the stored observations against the float64 reference
+    evaluation and the stored draws against the draw checker."""
+    ro = _collector(gpu, nenv=16384, T=64, seed=11)
+    ro.reset(stagger=True, max_stagger_steps=2000)
+    T, nac = ro.T, ro.nac
+    g0 = ro.global_step
+    adv, ret, stats = ro.collect()
+    torch.cuda.synchronize()
+    assert bool(stats["trajectory_finite"])
+    assert float(ro.b_done[1:].sum()) + float(ro.next_done.sum()) > 0     # autoresets happened
+    ref_adv, ref_ret = GO.gae_f32(ro.b_rew.cpu().numpy(), ro.b_val.cpu().numpy(),
+                                  ro.b_done.cpu().numpy(), ro.last_val.cpu().numpy(),
+                                  ro.next_done.cpu().numpy(), 0.99, 0.95, nagents=2)
+    np.testing.assert_array_equal(adv.reshape(T, nac).cpu().numpy(), ref_adv)
+    np.testing.assert_array_equal(ret.reshape(T, nac).cpu().numpy(), ref_ret)
+    P = import_pkg("policy")
+    step = P.PolicyStep(184, device=gpu, seed=0)
+    rows = np.sort(np.random.default_rng(7).choice(nac, 1024, replace=False))
+    rows_t = torch.as_tensor(rows, device=gpu)
+    for t in range(0, T, 8):
+        lg = torch.empty(nac, 84, dtype=torch.float32, device=gpu)
+        v = torch.empty(nac, dtype=torch.float32, device=gpu)
+        step(ro.b_obs[t], [(ro.net, 0, nac)], norm=None, logits_out=lg, value=v)
+        assert torch.equal(v[rows_t], ro.b_val[t][rows_t]), t
+        _check_against_reference(ro.net, ro.b_obs[t], lg, ro.b_val[t], rows_t)
+        idx, lp = oracle_sample(orc, lg[rows_t].cpu().numpy(), rows, seed=0, step=g0 + t)
+        np.testing.assert_array_equal(ro.b_act[t][rows_t].cpu().numpy(), idx)
+        assert np.abs(ro.b_logp[t][rows_t].cpu().numpy() - lp).max() < 1e-5
+    assert float(ro.b_obs.abs().max()) <= 10.0
