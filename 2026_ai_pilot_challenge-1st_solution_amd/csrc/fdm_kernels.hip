@@ -57,7 +57,8 @@ __global__ __launch_bounds__(kBlock) void fdm_step_kernel(double* __restrict__ s
 template <int FCS_RATE>
 __global__ __launch_bounds__(kSplitBlock) void fdm_step_split_kernel(
     double* __restrict__ st, long ld, const double* __restrict__ act, int nac, int S,
-    double* __restrict__ obs, long obs_ld, unsigned char* __restrict__ fin) {
+    double* __restrict__ obs, long obs_ld, unsigned char* __restrict__ fin,
+    double* __restrict__ act_keep) {
   __shared__ double T[F16M_IMAGE_LEN];
   __shared__ SplitX X[kSplitPairs];
   stage_image<kSplitBlock>(T);
@@ -72,7 +73,7 @@ __global__ __launch_bounds__(kSplitBlock) void fdm_step_split_kernel(
                            lane, fin != nullptr);
   else
     split_systems<FCS_RATE>(st + ia, ld, act + 4L * ia, S, store, T, X[pair], lane,
-                            fin ? fin + ia : nullptr);
+                            fin ? fin + ia : nullptr, act_keep ? act_keep + 4L * ia : nullptr);
 }
 
 // ------------------------------------------------------------------ IC seeding
@@ -246,13 +247,13 @@ static int fdm_step_args(double* states, long ld, const double* actions, int nac
 
 static int fdm_step_split(double* states, long ld, const double* actions, int nac, int substeps,
                           int fcs_rate, double* obs, long obs_ld, unsigned char* fin,
-                          void* stream) {
+                          void* stream, double* keep = nullptr) {
   const dim3 grid((nac + f16::kSplitAircraft - 1) / f16::kSplitAircraft), block(f16::kSplitBlock);
   hipStream_t s = (hipStream_t)stream;
   if (fcs_rate == 120)
-    hipLaunchKernelGGL(f16::fdm_step_split_kernel<120>, grid, block, 0, s, states, ld, actions, nac, substeps, obs, obs_ld, fin);
+    hipLaunchKernelGGL(f16::fdm_step_split_kernel<120>, grid, block, 0, s, states, ld, actions, nac, substeps, obs, obs_ld, fin, keep);
   else
-    hipLaunchKernelGGL(f16::fdm_step_split_kernel<60>, grid, block, 0, s, states, ld, actions, nac, substeps, obs, obs_ld, fin);
+    hipLaunchKernelGGL(f16::fdm_step_split_kernel<60>, grid, block, 0, s, states, ld, actions, nac, substeps, obs, obs_ld, fin, keep);
   return f16_last_error();
 }
 
@@ -271,6 +272,21 @@ extern "C" int f16_fdm_step_batch_finite(double* states, long ld, const double* 
   const int rc = fdm_step_args(states, ld, actions, nac, substeps, fcs_rate, obs, obs_ld);
   if (rc) return rc < 0 ? rc : 0;
   return fdm_step_split(states, ld, actions, nac, substeps, fcs_rate, obs, obs_ld, finite, stream);
+}
+
+extern "C" int f16_fdm_step_batch_keep(double* states, long ld, const double* actions,
+                                       double* actions_keep, int nac, int substeps, int fcs_rate,
+                                       double* obs, long obs_ld, unsigned char* finite,
+                                       void* stream) {
+  if (!actions_keep || (finite && substeps < 1)) return F16_EINVAL;
+  const int rc = fdm_step_args(states, ld, actions, nac, substeps, fcs_rate, obs, obs_ld);
+  if (rc) return rc < 0 ? rc : 0;
+  // the kernel reads `actions` and writes `actions_keep` as separate arrays
+  const uintptr_t a0 = (uintptr_t)actions, k0 = (uintptr_t)actions_keep;
+  const uintptr_t bytes = (uintptr_t)nac * 4 * sizeof(double);
+  if (a0 < k0 + bytes && k0 < a0 + bytes) return F16_EINVAL;
+  return fdm_step_split(states, ld, actions, nac, substeps, fcs_rate, obs, obs_ld, finite, stream,
+                        actions_keep);
 }
 
 extern "C" int f16_fdm_step_batch_onelane(double* states, long ld, const double* actions,

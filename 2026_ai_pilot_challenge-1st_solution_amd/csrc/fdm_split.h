@@ -271,12 +271,14 @@ __device__ __forceinline__ void split_flight(double* __restrict__ s, long ld, in
 // The systems wave of one pair: fuel, engine, FCS and previous-frame auxiliary state.
 // Issues exactly 3 barriers per substep, like split_flight.
 // With `fin` non-null, fin[0] <- 1 if every one of the aircraft's 101 state values after the
-// call is finite, else 0 (the flight wave's share arrives through x[kXFin]).
+// call is finite, else 0 (the flight wave's share arrives through x[kXFin]).  With `keep`
+// non-null, the aircraft's four actions are also written to keep[0..3].
 template <int FCS_RATE>
 __device__ __forceinline__ void split_systems(double* __restrict__ s, long ld,
                                               const double* __restrict__ act4, int S, bool store,
                                               const double* __restrict__ T, SplitX& x, int lane,
-                                              unsigned char* __restrict__ fin) {
+                                              unsigned char* __restrict__ fin,
+                                              double* __restrict__ keep) {
 #define F(k) s[(long)(k) * ld]
   Aircraft a;
 #pragma unroll
@@ -288,6 +290,7 @@ __device__ __forceinline__ void split_systems(double* __restrict__ s, long ld,
   a.n1 = F(F16S_ENG); a.n2 = F(F16S_ENG + 1); a.n2n = F(F16S_ENG + 2); a.ff = F(F16S_ENG + 3);
   a.k_tef = F(F16S_KIN); a.k_ail = F(F16S_KIN + 1); a.k_ele = F(F16S_KIN + 2); a.k_lef = F(F16S_KIN + 5);
   const double c_ail = act4[0], c_ele = act4[1], c_rud = act4[2], c_thr = act4[3];
+  if (keep && store) { keep[0] = c_ail; keep[1] = c_ele; keep[2] = c_rud; keep[3] = c_thr; }
   double k_rud = 0.0;
   unsigned ip2_m = 0u;   // finite-flag accumulator of the PID input_prev2 values written below
   for (int t = 0; t < S; ++t) {

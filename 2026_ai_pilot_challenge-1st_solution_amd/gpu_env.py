@@ -138,14 +138,24 @@ class GpuDogfight:
             if ss < 1:
                 raise ValueError("finite_out needs substeps >= 1")
         a = torch.as_tensor(actions, dtype=torch.float64, device=self.device).reshape(self.nac, 4)
-        if a.data_ptr() != self.actions.data_ptr():
+        # the reference copies the actions into self.actions before its launch; a separate
+        # contiguous device tensor is read by the launch itself, which also writes the copy
+        keep = (a.is_contiguous() and a.untyped_storage().data_ptr()
+                != self.actions.untyped_storage().data_ptr())
+        if not keep and a.data_ptr() != self.actions.data_ptr():
             self.actions.copy_(a)
         ev = self.kernel_events
         if ev is not None:
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record()
         obs_p = _lib.ptr(self._obs_soa) if want_obs else None
-        if finite_out is None:
+        if keep:
+            rc = self._lib.f16_fdm_step_batch_keep(
+                _lib.ptr(self._state_soa), self.nac, _lib.ptr(a), _lib.ptr(self.actions),
+                self.nac, ss, self.fcs_rate, obs_p, self.nac,
+                _lib.ptr(finite_out) if finite_out is not None else None,
+                _lib.stream_handle(self.device))
+        elif finite_out is None:
             rc = self._lib.f16_fdm_step_batch(
                 _lib.ptr(self._state_soa), self.nac, _lib.ptr(self.actions), self.nac, ss,
                 self.fcs_rate, obs_p, self.nac, _lib.stream_handle(self.device))

@@ -34,6 +34,15 @@ int f16_fdm_step_batch_finite(double* states, long ld, const double* actions, in
                               int substeps, int fcs_rate, double* obs, long obs_ld,
                               unsigned char* finite, void* stream);
 
+/* GpuDogfight.step in one launch: f16_fdm_step_batch (finite NULL) or
+ * f16_fdm_step_batch_finite (finite non-NULL, substeps >= 1) that also copies the (nac, 4)
+ * actions it reads into actions_keep -- the reference step's `self.actions.copy_(a)` before
+ * its launch (cuda_fdm/gpu_env.py:98-99), folded into the kernel.  actions_keep must not
+ * overlap actions (F16_EINVAL).  Written for every aircraft, also when substeps is 0. */
+int f16_fdm_step_batch_keep(double* states, long ld, const double* actions,
+                            double* actions_keep, int nac, int substeps, int fcs_rate,
+                            double* obs, long obs_ld, unsigned char* finite, void* stream);
+
 /* The same step computed with one lane (one wavefront) per aircraft doing the whole substep.
  * Results equal f16_fdm_step_batch bit for bit; f16_fdm_step_batch spreads each substep over
  * two cooperating wavefronts.  Same arguments, contract and reference interface. */

@@ -335,6 +335,43 @@ def test_finite_flags_from_registers(gpu, S, rate):
         b_sim.step(act, substeps=0, finite_out=fin)
 
 
+@pytest.mark.parametrize("S,with_fin", [(6, False), (6, True), (0, False), (2, True)])
+def test_step_keeps_actions(gpu, S, with_fin):
+    """GpuDogfight.step with a separate device tensor runs f16_fdm_step_batch_keep: one launch
+    that also leaves the actions in sim.actions, as the reference's copy before its launch
+    does (cuda_fdm/gpu_env.py:98-99).  Same states, flags and obs bit for bit as copying
+    first and launching f16_fdm_step_batch(_finite) on sim.actions; ragged batch."""
+    g = oracle_lib.golden("seed_golden.npz")
+    st = torch.as_tensor(np.ascontiguousarray(g["seed_120"][:50]))
+    act = torch.as_tensor(_rand_actions(np.random.default_rng(S), 50), device=gpu)
+    a_sim, b_sim = _sim(25), _sim(25)
+    for sim in (a_sim, b_sim):
+        sim.load_seed(st)
+        sim.actions.fill_(7.0)
+    fa = torch.zeros(50, dtype=torch.uint8, device=gpu) if with_fin else None
+    fb = torch.zeros(50, dtype=torch.uint8, device=gpu) if with_fin else None
+    oa = a_sim.step(act, substeps=S, finite_out=fa).clone()          # fused copy
+    b_sim.actions.copy_(act)
+    ob = b_sim.step(b_sim.actions, substeps=S, finite_out=fb).clone()  # the buffer itself
+    torch.cuda.synchronize()
+    assert torch.equal(a_sim.actions.view(torch.int64), act.view(torch.int64))
+    assert torch.equal(a_sim._state_soa.view(torch.int64), b_sim._state_soa.view(torch.int64))
+    assert torch.equal(oa.view(torch.int64), ob.view(torch.int64))
+    if with_fin:
+        assert torch.equal(fa, fb)
+    L = import_pkg("_lib")
+    lib, p, st_p = L.lib(), L.ptr, L.ptr(a_sim._state_soa)
+    rc = lib.f16_fdm_step_batch_keep(st_p, 50, p(act), p(act[10:]), 50, 6, 120, None, 50, None,
+                                     L.stream_handle())
+    assert rc == L.F16_EINVAL                                # overlapping copy target
+    rc = lib.f16_fdm_step_batch_keep(st_p, 50, p(act), None, 50, 6, 120, None, 50, None,
+                                     L.stream_handle())
+    assert rc == L.F16_EINVAL                                # no copy target
+    rc = lib.f16_fdm_step_batch_keep(st_p, 50, p(act), p(a_sim.actions), 50, 0, 120, None, 50,
+                                     p(fa) if with_fin else p(act), L.stream_handle())
+    assert rc == L.F16_EINVAL                                # finite flags need substeps >= 1
+
+
 def test_argument_errors(gpu):
     pkg = import_pkg()
     with pytest.raises(ValueError):
