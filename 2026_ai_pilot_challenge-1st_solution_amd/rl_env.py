@@ -351,8 +351,11 @@ class GpuDogfightVecEnv:
         state_fin = self._state_fin if self.fused_finite and self.substeps >= 1 else None
         self.sim.step(a, substeps=self.substeps, want_obs=False, finite_out=state_fin)
         if reset_indices is None:
-            pick = torch.randint(0, self.ic_pool_size, (self.nenv,), device=self.device,
-                                 generator=self.torch_gen)
+            # the pool row of each finished engagement is drawn inside the post-physics launch
+            # (uniform over the pool: Philox keyed by the env seed, the step count and the
+            # engagement), the reference's torch.randint draw (R/cuda_fdm/rl_env.py:534-535) without
+            # a launch of its own
+            pick = None
         else:
             if (reset_indices.shape != (self.nenv,) or reset_indices.dtype != torch.long
                     or reset_indices.device != self.sim.states.device):

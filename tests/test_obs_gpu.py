@@ -539,7 +539,7 @@ def test_step_training_and_capture_switch(gpu):
             for key in x[3]:
                 if key != "terminal_obs":
                     assert torch.equal(x[3][key], y[3][key]), (k, key)
-    # step_training draws its own pool picks (torch.randint on the env's generator)
+    # step_training draws its own pool picks (inside the post-physics launch)
     env = envs[2]
     out = env.step_training(torch.zeros(400, 4, dtype=torch.float64, device=gpu))
     assert out[3]["terminal_obs"] is None and env._capture_terminal_obs
