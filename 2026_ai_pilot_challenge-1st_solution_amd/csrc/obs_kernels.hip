@@ -1054,10 +1054,6 @@ __global__ __launch_bounds__(kPostSplitBlock) void env_post_step_split_kernel(
   double f15[15];
   if (role == 0) {
     bool d = false;
-    // Only the vector role's reads of the previous attitude and velocity must precede the
-    // barrier below (this role overwrites them after it); the advance role issues its loads
-    // before the barrier and does its own arithmetic after it, so the vector role, which has
-    // the longer share, starts its work as soon as both roles' loads have landed.
     int fin = 1;
     const bool want_fin = on && (io.terminal_finite || io.finite_acc);
     if (on) {
@@ -1065,27 +1061,40 @@ __global__ __launch_bounds__(kPostSplitBlock) void env_post_step_split_kernel(
       for (int f = 0; f < 15; ++f) f15[f] = st[f * ld + a];
       if (want_fin && io.state_finite) fin = io.state_finite[a] ? 1 : 0;   // the physics launch's
     }
+    // the finite flag, kinematics and pair geometry of this role
+    auto front = [&]() {
+      if (want_fin) {                               // rl_env.py:545: every state value finite
+        if (!io.state_finite) {
+#pragma unroll
+          for (int f = 0; f < 15; ++f) fin &= isfinite(f15[f]) ? 1 : 0;
+          double v[F16S_N - 15];
+#pragma unroll
+          for (int j = 0; j < F16S_N - 15; ++j) v[j] = st[(15 + j) * ld + a];
+#pragma unroll
+          for (int j = 0; j < F16S_N - 15; ++j) fin &= isfinite(v[j]) ? 1 : 0;
+        }
+        fin &= xchi(fin);
+        if (!odd) {
+          if (io.terminal_finite) io.terminal_finite[e] = (unsigned char)fin;
+          if (io.finite_acc && !fin) io.finite_acc[e] = 0;
+        }
+      }
+      if (on) {
+        make_kin(f15, 1, O, k);
+        exchange(k, p);
+        pair_geo(k, p, g);
+      }
+    };
+    // Only the vector role's reads of the previous attitude and velocity must precede the
+    // barrier below (this role overwrites them after it).  With the full-row tile (one
+    // workgroup per CU anyway) this role does its own arithmetic after the barrier, so the
+    // vector role, which has the longer share, starts as soon as both roles' loads have landed
+    // (3 % shorter launch at 16k engagements); with the vector-block tile, before it, which
+    // keeps the register count within two workgroups per CU.
+    if constexpr (!FULL) front();
     __syncthreads();   // the vector role has read the previous attitude and velocity
-    if (want_fin) {                                // rl_env.py:545: every state value finite
-      if (!io.state_finite) {
-#pragma unroll
-        for (int f = 0; f < 15; ++f) fin &= isfinite(f15[f]) ? 1 : 0;
-        double v[F16S_N - 15];
-#pragma unroll
-        for (int j = 0; j < F16S_N - 15; ++j) v[j] = st[(15 + j) * ld + a];
-#pragma unroll
-        for (int j = 0; j < F16S_N - 15; ++j) fin &= isfinite(v[j]) ? 1 : 0;
-      }
-      fin &= xchi(fin);
-      if (!odd) {
-        if (io.terminal_finite) io.terminal_finite[e] = (unsigned char)fin;
-        if (io.finite_acc && !fin) io.finite_acc[e] = 0;
-      }
-    }
+    if constexpr (FULL) front();
     if (on) {
-      make_kin(f15, 1, O, k);
-      exchange(k, p);
-      pair_geo(k, p, g);
       const AdvOut o = lane_advance(k, p, g, a, e, io.actions, r, c, f15[F16S_FUEL]);
       if (io.reward) io.reward[a] = o.reward;
       if (io.reward_f32) io.reward_f32[a] = (float)o.reward;

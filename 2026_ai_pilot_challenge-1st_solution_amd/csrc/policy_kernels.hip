@@ -215,10 +215,12 @@ __global__ __launch_bounds__(kThreads, RB == 64 ? 2 : 1) void policy_kernel(cons
       }
     }
   }
-  __syncthreads();                                    // the logits are consumed
-
   // ---- critic: two tanh layers, then the value dot products (one row per lane of waves
-  // 0 .. RB/64 - 1)
+  // 0 .. RB/64 - 1).  Only when values are asked for (p.value is the same for every workgroup
+  // of the launch): a league's opponent networks act but are not trained, and their launch
+  // skips it.
+  if (!p.value) return;
+  __syncthreads();                                    // the logits are consumed
   hidden_layers<KP, NR>(Xs, Hs, wbf + Blob<KP>::W1C, wf + kB1 + kHid, wbf + Blob<KP>::W2C,
                         wf + kB2C, wave, lane);
   if (wave < RB / 64) {
@@ -231,7 +233,7 @@ __global__ __launch_bounds__(kThreads, RB == 64 ? 2 : 1) void policy_kernel(cons
 #pragma unroll
       for (int q = 0; q < 8; ++q) s += (float)h[q] * w3[k0 + q];
     }
-    if (row < nr && p.value) p.value[r0 + row] = s + wf[kB3C];
+    if (row < nr) p.value[r0 + row] = s + wf[kB3C];
   }
 }
 

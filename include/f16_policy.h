@@ -58,7 +58,7 @@ typedef struct F16PolicyArgs {
     long nobs_ld;
     long long *act_idx;     /* (logical, 4) sampled bins, or NULL */
     float *logp;            /* (logical) summed log-probability of the sampled bins, or NULL */
-    float *value;           /* (logical) critic value, or NULL */
+    float *value;           /* (logical) critic value, or NULL (the critic is then skipped) */
     double *env_actions;    /* (physical, 4) float64 controls [ail, ele, rud, thr], or NULL */
     float *logits_out;      /* (logical, 84) actor logits, or NULL */
     const unsigned int *step_base;  /* device counter added to `step` when non-NULL, so a
