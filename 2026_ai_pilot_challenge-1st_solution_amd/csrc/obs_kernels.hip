@@ -751,7 +751,16 @@ __device__ __forceinline__ void lane_reset_rows(const F16EnvStepIO& io, const F1
   const double qnan = __builtin_nan("");
   if (!copy_state) {
   } else if (ok) {
-    for (int f = 0; f < F16S_N; ++f) st[f * ld + a] = src[f];
+    // loads of a chunk before its stores: copied element by element, each load waited for the
+    // store before it (the compiler cannot rule out the pool and the state overlapping)
+    for (int f0 = 0; f0 < F16S_N; f0 += 17) {
+      double v[17];
+#pragma unroll
+      for (int f = 0; f < 17; ++f) v[f] = f0 + f < F16S_N ? src[f0 + f] : 0.0;
+#pragma unroll
+      for (int f = 0; f < 17; ++f)
+        if (f0 + f < F16S_N) st[(f0 + f) * ld + a] = v[f];
+    }
   } else {
     for (int f = 0; f < F16S_N; ++f) st[f * ld + a] = qnan;
   }
@@ -794,15 +803,25 @@ __device__ __forceinline__ void lane_autoreset(const F16EnvStepIO& io, const F16
 __device__ __forceinline__ void lane_autoreset_cached(const F16EnvStepIO& io, const F16Recon& r,
                                                       long a, long e, int odd, uint32_t step,
                                                       long pk) {
-  lane_reset_rows(io, r, a, e, odd, step, pk, false);
-  r.prev_x[a] = io.pool_prev_x[pk * 2 + odd];
-  r.prev_x_valid[a] = 1;
-  r.prev_alt_log[a] = io.pool_prev_alt_log[pk * 2 + odd];
-  if (r.aux && !odd) {
-    double* o = r.aux + e * kAuxDim;
+  // every pool-table load before the first store (a load after a store to memory the compiler
+  // cannot prove distinct waits for the data of every earlier load)
+  const double px = io.pool_prev_x[pk * 2 + odd];
+  const double pal = io.pool_prev_alt_log[pk * 2 + odd];
+  const bool aux = r.aux && !odd;
+  double v[kAuxDim];
+  if (aux) {
     const double* src = io.pool_aux + pk * kAuxDim;
 #pragma unroll
-    for (int i = 0; i < kAuxDim; ++i) o[i] = src[i];
+    for (int i = 0; i < kAuxDim; ++i) v[i] = src[i];
+  }
+  lane_reset_rows(io, r, a, e, odd, step, pk, false);
+  r.prev_x[a] = px;
+  r.prev_x_valid[a] = 1;
+  r.prev_alt_log[a] = pal;
+  if (aux) {
+    double* o = r.aux + e * kAuxDim;
+#pragma unroll
+    for (int i = 0; i < kAuxDim; ++i) o[i] = v[i];
   }
 }
 

@@ -57,7 +57,9 @@ __device__ __forceinline__ void hidden_layers(const __bf16* Xs, __bf16* Hs, cons
 // row's arithmetic is the same for both sizes.
 constexpr int kPolicyRows = 64;
 template <int KP, int RB>
-__global__ __launch_bounds__(kThreads, RB == 64 ? 2 : 1) void policy_kernel(const F16PolicyArgs p) {
+// (HIP's second bound is waves per SIMD: two 8-wave workgroups per CU are four per SIMD, which
+// caps the registers at 128.)
+__global__ __launch_bounds__(kThreads, RB == 64 ? 4 : 2) void policy_kernel(const F16PolicyArgs p) {
   constexpr int XP = KP + 8;
   constexpr int NR = RB / 32;                          // 32-row MFMA tiles per wave and layer
   constexpr int NRH = RB / 64;                         // row tiles per wave of the logits head
@@ -83,20 +85,28 @@ __global__ __launch_bounds__(kThreads, RB == 64 ? 2 : 1) void policy_kernel(cons
   // ---- normalise (RunningNorm.normalize, ppo_gpu.py:210-214) and stage bf16 rows in LDS.
   // The rows' loads go out first, then the statistics' (and the barrier that publishes them),
   // so both memory latencies overlap.
+  constexpr int half = D / 2;                         // float2 per row
+  constexpr int kPer = (RB * (KP / 2) + kThreads - 1) / kThreads;
   {
-    constexpr int half = D / 2;                       // float2 per row
-    constexpr int kPer = (RB * (KP / 2) + kThreads - 1) / kThreads;
     float2 x[kPer];
+    // Physical rows first, then every observation load, unconditionally (items of rows past
+    // nr read row nr - 1 and are dropped below).  Choosing the row or skipping the load inside
+    // the load loop made the compiler wait for every outstanding load (vmcnt(0)) at each branch
+    // join, which serialised the staging.
+    long pr[kPer];
+    if (p.rows) {
+#pragma unroll
+      for (int q = 0; q < kPer; ++q)
+        pr[q] = p.rows[r0 + min((tid + q * kThreads) / half, nr - 1)];
+    } else {
+#pragma unroll
+      for (int q = 0; q < kPer; ++q) pr[q] = r0 + min((tid + q * kThreads) / half, nr - 1);
+    }
 #pragma unroll
     for (int q = 0; q < kPer; ++q) {                   // issue every load before using any
       const int idx = tid + q * kThreads;
-      const int r = idx / half, c = idx - r * half;
-      x[q] = make_float2(0.0f, 0.0f);
-      if (r < nr) {
-        const int li = r0 + r;
-        const long pr = p.rows ? p.rows[li] : li;
-        x[q] = *reinterpret_cast<const float2*>(p.obs + pr * p.obs_ld + 2 * c);
-      }
+      const int c = idx - (idx / half) * half;
+      x[q] = *reinterpret_cast<const float2*>(p.obs + pr[q] * p.obs_ld + 2 * c);
     }
     if (tid < KP) {
       const bool on = g_mean && tid < D;
@@ -109,8 +119,10 @@ __global__ __launch_bounds__(kThreads, RB == 64 ? 2 : 1) void policy_kernel(cons
       const int idx = tid + q * kThreads;
       const int r = idx / half, c = idx - r * half;
       if (r < RB) {
-        float v0 = x[q].x, v1 = x[q].y;
+        float v0 = 0.0f, v1 = 0.0f;
         if (r < nr) {
+          v0 = x[q].x;
+          v1 = x[q].y;
           if (g_mean) {
             v0 = (v0 - col_mean[2 * c]) / col_sd[2 * c];
             v1 = (v1 - col_mean[2 * c + 1]) / col_sd[2 * c + 1];
@@ -264,16 +276,23 @@ __global__ __launch_bounds__(kNormCols * kNormPhases) void norm_partial_kernel(
     const int i0 = b * kNormRowsPerBlock + ph * kNormRowsPerPhase;
 #pragma unroll
     for (int k0 = 0; k0 < kNormRowsPerPhase; k0 += kNormChunk) {
+      // row indices first, then every load unconditionally (rows past nrows read row nrows - 1
+      // and add 0): a choice or a skip inside the load loop made the compiler wait for all
+      // outstanding loads at each branch join, one load at a time
+      long src[kNormChunk];
+      if (rows) {
+#pragma unroll
+        for (int i = 0; i < kNormChunk; ++i) src[i] = rows[min(i0 + k0 + i, nrows - 1)];
+      } else {
+#pragma unroll
+        for (int i = 0; i < kNormChunk; ++i) src[i] = min(i0 + k0 + i, nrows - 1);
+      }
       float x[kNormChunk];
 #pragma unroll
-      for (int i = 0; i < kNormChunk; ++i) {
-        const int ri = i0 + k0 + i;
-        x[i] = 0.0f;
-        if (ri < nrows) x[i] = obs[(rows ? (long)rows[ri] : (long)ri) * ld + c];
-      }
+      for (int i = 0; i < kNormChunk; ++i) x[i] = obs[src[i] * ld + c];
 #pragma unroll
       for (int i = 0; i < kNormChunk; ++i) {
-        const double v = x[i];
+        const double v = (i0 + k0 + i < nrows) ? (double)x[i] : 0.0;
         s += v;
         q += v * v;
       }

@@ -149,13 +149,20 @@ __global__ __launch_bounds__(kAdvThreads) void adv_partial_kernel(const float* _
   const double K = (p0 >= 0 && p0 < count) ? (double)adv[p0] : 0.0;
   double s = 0.0, q = 0.0;
   const int i = blockIdx.x * kAdvThreads * kAdvPer + t;
+  // every index load, then every value load, unconditionally (out-of-range items read element
+  // 0 and are not summed): loads chosen or skipped inside the summing loop were issued one at a
+  // time, each waiting out the previous ones
+  long long p[kAdvPer];
 #pragma unroll
-  for (int k = 0; k < kAdvPer; ++k) {
-    const int ii = i + k * kAdvThreads;
-    if (ii < n) {
-      const long long p = idx[ii];
-      if (p >= 0 && p < count) {
-        const double d = (double)adv[p] - K;
+  for (int k = 0; k < kAdvPer; ++k) p[k] = idx[min(i + k * kAdvThreads, n - 1)];
+  if (count > 0) {
+    float v[kAdvPer];
+#pragma unroll
+    for (int k = 0; k < kAdvPer; ++k) v[k] = adv[(p[k] >= 0 && p[k] < count) ? p[k] : 0];
+#pragma unroll
+    for (int k = 0; k < kAdvPer; ++k) {
+      if (i + k * kAdvThreads < n && p[k] >= 0 && p[k] < count) {
+        const double d = (double)v[k] - K;
         s += d;
         q += d * d;
       }
@@ -515,10 +522,14 @@ __global__ __launch_bounds__(kThreads, 1) void ppo_fused_kernel(const F16PPOArgs
       init_bias(acc, wf + kB2C, 32 * wave, lane);
       gemm_t<2, kHid>(acc, wbf + Blob<KP>::W2C, 32 * wave, H1s, kHPitch, 0, lane);
       float vp[2] = {0.0f, 0.0f};
+      float4 w4s[4];                           // all four head loads in flight at once
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        w4s[g] = *reinterpret_cast<const float4*>(w3 + 32 * wave + 8 * g + lh);
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int unit = 32 * wave + 8 * g + lh;
-        const float4 w4 = *reinterpret_cast<const float4*>(w3 + unit);
+        const float4 w4 = w4s[g];
 #pragma unroll
         for (int r = 0; r < 2; ++r) {
           bf16x4 v;

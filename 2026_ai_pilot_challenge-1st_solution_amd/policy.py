@@ -87,7 +87,8 @@ class MLPActorCritic(torch.nn.Module):
             for mod in self.modules():
                 if isinstance(mod, torch.nn.Linear):
                     if init == "orthogonal":       # model.py:86-90 _init_weights
-                        torch.nn.init.orthogonal_(mod.weight, gain=float(np.sqrt(2)))
+                        torch.nn.init.orthogonal_(mod.weight, gain=float(np.sqrt(2)),
+                                                  generator=generator)
                     elif init == "normal":         # BASELINE C4/C5: N(0, 0.02)
                         mod.weight.normal_(0.0, float(init_std), generator=generator)
                     else:

@@ -148,6 +148,23 @@ def test_pack_layout():
     assert wf.numel() == 1377 and torch.equal(wf[1120:1376], c[4].weight.flatten())
 
 
+@pytest.mark.parametrize("init", ["normal", "orthogonal"])
+def test_init_draws_only_from_the_generator(init):
+    """A seeded generator fixes every weight, whatever the global RNG did before (parity
+    tests build their networks this way, so their inputs must not depend on test order)."""
+    import torch
+    P = import_pkg("policy")
+    nets = []
+    for glob in (1, 2):
+        torch.manual_seed(glob)
+        nets.append(P.MLPActorCritic(184, init=init, generator=torch.Generator().manual_seed(5)))
+    for p, q in zip(nets[0].parameters(), nets[1].parameters()):
+        assert torch.equal(p, q)
+    if init == "orthogonal":                       # gain sqrt(2): W W^T = 2 I on the short side
+        w = nets[0].actor_logits[2].weight.double()
+        assert torch.allclose(w @ w.T, 2 * torch.eye(256, dtype=torch.float64), atol=1e-5)
+
+
 # ------------------------------------------------------------------------ GPU
 def _bf(x):
     import torch
@@ -232,7 +249,8 @@ def test_policy_groups_and_row_maps(gpu, orc):
     n = 3000
     P, net0, obs, norm = _setup(gpu, 184, n, 2)
     net1 = P.MLPActorCritic(184, init="normal", generator=torch.Generator().manual_seed(3)).to(gpu)
-    net2 = P.MLPActorCritic(184, init="orthogonal").to(gpu)
+    net2 = P.MLPActorCritic(184, init="orthogonal",
+                            generator=torch.Generator().manual_seed(4)).to(gpu)
     perm = np.random.default_rng(4).permutation(n).astype(np.int32)
     rows = torch.as_tensor(perm, device=gpu)
     bounds = [(net0, 0, 1000), (net1, 1000, 1001), (net2, 1001, n)]
