@@ -27,190 +27,348 @@
 
 namespace f16pol {
 
-// One network's two tanh layers for the workgroup's 32 NR rows: X (LDS) -> Hs -> Hs.  Wave w
-// owns units [32w, 32w + 32) of each layer; every weight fragment it streams feeds NR MFMAs.
-template <int KP, int NR>
-__device__ __forceinline__ void hidden_layers(const __bf16* Xs, __bf16* Hs, const __bf16* W1,
-                                              const float* b1, const __bf16* W2, const float* b2,
-                                              int wave, int lane) {
-  constexpr int XP = KP + 8;
-  {
-    f32x16 acc[NR];
-    init_bias(acc, b1, 32 * wave, lane);
-    gemm_t<NR, KP>(acc, W1, 32 * wave, Xs, XP, 0, lane);
-    store_tanh(acc, Hs, 32 * wave, lane);
+// acc += W x A^T exactly as gemm_t forms it (the same K slices in the same order, so the sums are
+// bit-identical), with another layer's epilogue spread over the slices: epilogue step j (of 8)
+// follows the MFMAs of slice j * NK / 8.  A wave's matrix products and its vector epilogue then
+// interleave instead of alternating, and the SIMD keeps both pipes busy.
+template <int NR, int K, class Epi>
+__device__ __forceinline__ void gemm_epi(f32x16 (&acc)[NR], const __bf16* __restrict__ Wg, int u0,
+                                         const __bf16* __restrict__ As, int a_pitch, int lane,
+                                         Epi&& epi) {
+  constexpr int PD = 2;                               // weight slices in flight ahead
+  constexpr int NK = K / 16;
+  const int lr = lane & 31, lk = (lane >> 5) * 8;
+  const __bf16* wp = Wg + (long)(u0 >> 5) * (K / 16) * 512 + lane * 8;
+  const __bf16* ap = As + lr * a_pitch + lk;
+  bf16x8 w[PD + 1];
+#pragma unroll
+  for (int q = 0; q < PD; ++q) w[q] = *reinterpret_cast<const bf16x8*>(wp + 512 * q);
+  // one activation fragment per row tile: the next slice's is read right after this slice's
+  // MFMAs take theirs, and the epilogue step between covers the LDS latency
+  bf16x8 a[NR];
+#pragma unroll
+  for (int r = 0; r < NR; ++r) a[r] = *reinterpret_cast<const bf16x8*>(ap + 32 * r * a_pitch);
+#pragma unroll
+  for (int s = 0; s < NK; ++s) {
+    if (s + PD < NK) w[(s + PD) % (PD + 1)] =
+        *reinterpret_cast<const bf16x8*>(wp + 512 * (s + PD));
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int r = 0; r < NR; ++r) acc[r] = mfma(w[s % (PD + 1)], a[r], acc[r]);
+    if (s + 1 < NK) {
+#pragma unroll
+      for (int r = 0; r < NR; ++r)
+        a[r] = *reinterpret_cast<const bf16x8*>(ap + 32 * r * a_pitch + 16 * (s + 1));
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if ((j * NK) / 8 == s) epi(j);
   }
-  __syncthreads();
-  f32x16 acc[NR];
-  init_bias(acc, b2, 32 * wave, lane);
-  gemm_t<NR, kHid>(acc, W2, 32 * wave, Hs, kHPitch, 0, lane);
-  __syncthreads();                                    // every wave has read layer 1
-  store_tanh(acc, Hs, 32 * wave, lane);
-  __syncthreads();
 }
 
-// RB observation rows per 8-wave workgroup (64 or 128).  128 rows halve the weight bytes each row
-// costs the CU's vector-memory path (every wave streams its 32-unit slice of every layer once
-// per workgroup) and give each weight fragment 4 MFMAs instead of 2, but the workgroup then
-// holds the whole CU's LDS share (one per CU) and measured slower on MI355X (32,768 rows:
-// 43.3 us against 39.8 us with 64 rows, two workgroups per CU), so the launch uses 64.  Each
-// row's arithmetic is the same for both sizes.
-constexpr int kPolicyRows = 64;
-template <int KP, int RB>
-// (HIP's second bound is waves per SIMD: two 8-wave workgroups per CU are four per SIMD, which
-// caps the registers at 128.)
-__global__ __launch_bounds__(kThreads, RB == 64 ? 4 : 2) void policy_kernel(const F16PolicyArgs p) {
-  constexpr int XP = KP + 8;
-  constexpr int NR = RB / 32;                          // 32-row MFMA tiles per wave and layer
-  constexpr int NRH = RB / 64;                         // row tiles per wave of the logits head
-  static_assert(RB * kLPitch * 4 <= RB * kHPitch * 2, "logits reuse the hidden rows' LDS");
-  __shared__ __align__(16) __bf16 Xs[RB * XP];
-  __shared__ __align__(16) __bf16 Hs[RB * kHPitch];
-  __shared__ float col_mean[KP], col_sd[KP];
+// Epilogue step j of a hidden layer (two 32-row tiles): tanh of 4 consecutive units of one row,
+// rounded to bf16, one 8-byte LDS store at E[row][unit].  Steps 0..7 cover the 32 x 64 block.
+struct TanhEpi {
+  const f32x16* acc;
+  __bf16* E;
+  int u0, lane;
+  __device__ __forceinline__ void operator()(int j) const {
+    const int g = j >> 1, r = j & 1;
+    const int unit = u0 + 8 * g + (lane >> 5) * 4;
+    bf16x4 v;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = (__bf16)tanh_act(acc[r][4 * g + i]);
+    *reinterpret_cast<bf16x4*>(E + (32 * r + (lane & 31)) * kHPitch + unit) = v;
+  }
+};
+
+// Epilogue step j of the critic's layer 2: the same tanh and bf16 rounding, then the value
+// head's products for those 4 units summed into this lane's row partial vp[r].
+struct ValueEpi {
+  const f32x16* acc;
+  const float4* w3;      // the head weights of this lane's units, group g at w3[g]
+  float* vp;
+  __device__ __forceinline__ void operator()(int j) const {
+    const int g = j >> 1, r = j & 1;
+    float s = vp[r];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float h = (float)(__bf16)tanh_act(acc[r][4 * g + i]);
+      s += h * w3[g][i];
+    }
+    vp[r] = s;
+  }
+};
+
+// threadIdx.x % 64 through an empty asm, so the compiler derives lane values where they are used
+// instead of holding them in registers across phases.
+__device__ __forceinline__ int fresh_lane() {
+  int t = (int)threadIdx.x;
+  asm volatile("" : "+v"(t));
+  return t & 63;
+}
+
+// Row staging: VW floats per load (4 where the rows allow 16-byte access), NC vectors per row,
+// RP rows per pass of the 512 threads, NP passes for the 64 rows.  Each thread keeps one vector
+// column for every pass, so its normalisation statistics are read once.
+template <int D, int VW>
+struct Stage {
+  static constexpr int NC = D / VW;
+  static constexpr int RP = kThreads / NC;
+  static constexpr int NP = (kRows + RP - 1) / RP;
+};
+
+// One policy workgroup: 64 observation rows, 8 waves.  Wave w owns units [32w, 32w + 32) of
+// every hidden layer of both networks (two 32-row MFMA tiles each).  LDS: A holds the
+// normalised rows, then the critic's layer-1 activations; B the actor's layer-1, then layer-2
+// activations, then the logits.  Phases (barriers between them):
+//   1  actor layer 1 products                       (reads A)
+//   2  critic layer 1 products + actor layer 1 tanh (reads A, writes B)
+//   3  actor layer 2 products  + critic layer 1 tanh (reads B, writes A)
+//   4  critic layer 2 products + actor layer 2 tanh (reads A, writes B)
+//   5  logits products (waves 0-5) + critic layer 2 tanh and value partials (reads B)
+//   6  logits to LDS; 7 draws (waves 0-3) beside the value sums (wave 4).
+// Without values asked for (a league's opponents), the critic's work is skipped.  The actor's
+// arithmetic is the PPO update's forward (policy_mfma.h), operation for operation.
+// (HIP's second launch bound is waves per SIMD: two 8-wave workgroups per CU are four per SIMD,
+// which caps the registers at 128.)
+template <int KP, int VW>
+__global__ __launch_bounds__(kThreads, 4) void policy_kernel(const F16PolicyArgs p) {
+  static_assert(kRows * kLPitch * 4 <= kRows * kHPitch * 2, "logits reuse B");
+  static_assert(KP <= kHPitch, "rows fit A");
+  __shared__ __align__(16) __bf16 As[kRows * kHPitch];
+  __shared__ __align__(16) __bf16 Bs[kRows * kHPitch];
+  __shared__ __align__(16) float col_mean[KP], col_sd[KP];
+  __shared__ float vpart[kWaves][kRows];
   const int gi = blockIdx.y;
   if (gi >= p.ngroups) return;
   const F16PolicyGroup G = p.group[gi];
-  const int gb = p.group_offsets ? p.group_offsets[gi] : G.row_begin;
-  const int ge = p.group_offsets ? p.group_offsets[gi + 1] : G.row_end;
-  const int r0 = gb + blockIdx.x * RB;
+  // the group's row range is uniform: kept in scalar registers (a vector load would hold it,
+  // and everything derived from it, in vector registers for the whole kernel)
+  const int gb = __builtin_amdgcn_readfirstlane(p.group_offsets ? p.group_offsets[gi] : G.row_begin);
+  const int ge =
+      __builtin_amdgcn_readfirstlane(p.group_offsets ? p.group_offsets[gi + 1] : G.row_end);
+  const int r0 = gb + blockIdx.x * kRows;
   if (r0 >= ge) return;                               // uniform per workgroup
-  const int nr = min(RB, ge - r0);
+  const int nr = min(kRows, ge - r0);
   const float* g_mean = G.mean ? G.mean : p.mean;
   const float* g_var = G.mean ? G.var : p.var;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: a scalar register
   const __bf16* wbf = static_cast<const __bf16*>(G.wbf);
   const float* wf = G.wf;
   constexpr int D = KP == 192 ? 184 : 214;              // observation width of this kernel
+  const bool critic = p.value != nullptr;             // the same for every workgroup
+  const int u0 = 32 * wave;
 
-  // ---- normalise (RunningNorm.normalize, ppo_gpu.py:210-214) and stage bf16 rows in LDS.
-  // The rows' loads go out first, then the statistics' (and the barrier that publishes them),
-  // so both memory latencies overlap.
-  constexpr int half = D / 2;                         // float2 per row
-  constexpr int kPer = (RB * (KP / 2) + kThreads - 1) / kThreads;
+  // ---- normalise (RunningNorm.normalize, ppo_gpu.py:210-214) and stage bf16 rows in A.
+  // Row indices, then every row load (unconditional: items of rows past nr read row nr - 1 and
+  // are dropped; a choice or skip inside the load loop made the compiler wait for all
+  // outstanding loads at each branch join), then the statistics and their barrier, so both
+  // latencies overlap.
+  using S = Stage<D, VW>;
+  typedef float vec __attribute__((ext_vector_type(VW)));
+  vec x[S::NP];                                       // the rows, raw then normalised
   {
-    float2 x[kPer];
-    // Physical rows first, then every observation load, unconditionally (items of rows past
-    // nr read row nr - 1 and are dropped below).  Choosing the row or skipping the load inside
-    // the load loop made the compiler wait for every outstanding load (vmcnt(0)) at each branch
-    // join, which serialised the staging.
-    long pr[kPer];
+    const int cv = tid % S::NC, rb = tid / S::NC;     // vector column, first row
+    const bool act = rb < S::RP;                      // threads past RP * NC only load
+    long pr[S::NP];
     if (p.rows) {
 #pragma unroll
-      for (int q = 0; q < kPer; ++q)
-        pr[q] = p.rows[r0 + min((tid + q * kThreads) / half, nr - 1)];
+      for (int q = 0; q < S::NP; ++q) pr[q] = p.rows[r0 + min(rb + S::RP * q, nr - 1)];
     } else {
 #pragma unroll
-      for (int q = 0; q < kPer; ++q) pr[q] = r0 + min((tid + q * kThreads) / half, nr - 1);
+      for (int q = 0; q < S::NP; ++q) pr[q] = r0 + min(rb + S::RP * q, nr - 1);
     }
 #pragma unroll
-    for (int q = 0; q < kPer; ++q) {                   // issue every load before using any
-      const int idx = tid + q * kThreads;
-      const int c = idx - (idx / half) * half;
-      x[q] = *reinterpret_cast<const float2*>(p.obs + pr[q] * p.obs_ld + 2 * c);
-    }
+    for (int q = 0; q < S::NP; ++q)
+      x[q] = *reinterpret_cast<const vec*>(p.obs + pr[q] * p.obs_ld + VW * cv);
     if (tid < KP) {
       const bool on = g_mean && tid < D;
       col_mean[tid] = on ? g_mean[tid] : 0.0f;
       col_sd[tid] = on ? sqrtf(g_var[tid] + p.eps) : 1.0f;
     }
     __syncthreads();
+    if (act) {
+      const vec mu = *reinterpret_cast<const vec*>(col_mean + VW * cv);
+      const vec sd = *reinterpret_cast<const vec*>(col_sd + VW * cv);
 #pragma unroll
-    for (int q = 0; q < kPer; ++q) {
-      const int idx = tid + q * kThreads;
-      const int r = idx / half, c = idx - r * half;
-      if (r < RB) {
-        float v0 = 0.0f, v1 = 0.0f;
-        if (r < nr) {
-          v0 = x[q].x;
-          v1 = x[q].y;
-          if (g_mean) {
-            v0 = (v0 - col_mean[2 * c]) / col_sd[2 * c];
-            v1 = (v1 - col_mean[2 * c + 1]) / col_sd[2 * c + 1];
-            v0 = v0 < -p.clip ? -p.clip : (v0 > p.clip ? p.clip : v0);
-            v1 = v1 < -p.clip ? -p.clip : (v1 > p.clip ? p.clip : v1);
+      for (int q = 0; q < S::NP; ++q) {
+        const int r = rb + S::RP * q;
+        if (r < kRows) {
+          vec v = {};
+          if (r < nr) {
+            v = x[q];
+            if (g_mean) {
+#pragma unroll
+              for (int i = 0; i < VW; ++i) {
+                float t = (v[i] - mu[i]) / sd[i];
+                v[i] = t < -p.clip ? -p.clip : (t > p.clip ? p.clip : t);
+              }
+            }
           }
-          if (p.nobs_out)
-            *reinterpret_cast<float2*>(p.nobs_out + (long)(r0 + r) * p.nobs_ld + 2 * c) =
-                make_float2(v0, v1);
+          x[q] = v;
+          typedef __bf16 bvec __attribute__((ext_vector_type(VW)));
+          bvec b;
+#pragma unroll
+          for (int i = 0; i < VW; ++i) b[i] = (__bf16)v[i];
+          *reinterpret_cast<bvec*>(As + r * kHPitch + VW * cv) = b;
         }
-        bf16x2 b;
-        b[0] = (__bf16)v0;
-        b[1] = (__bf16)v1;
-        *reinterpret_cast<bf16x2*>(Xs + r * XP + 2 * c) = b;
       }
     }
-    for (int idx = tid; idx < RB * (KP - D); idx += kThreads) {   // zero the K padding
+    for (int idx = tid; idx < kRows * (KP - D); idx += kThreads) {   // zero the K padding
       const int r = idx / (KP - D);
-      Xs[r * XP + D + (idx - r * (KP - D))] = (__bf16)0.0f;
+      As[r * kHPitch + D + (idx - r * (KP - D))] = (__bf16)0.0f;
     }
   }
   __syncthreads();
 
-  // ---- actor: two tanh layers, then the logits head on waves 0-5 (32 units x 32 NRH rows each)
-  hidden_layers<KP, NR>(Xs, Hs, wbf + Blob<KP>::W1, wf + kB1, wbf + Blob<KP>::W2A, wf + kB2A,
-                        wave, lane);
-  float* Ls = reinterpret_cast<float*>(Hs);
+  // ---- phase 1: actor layer 1 products.  Every phase derives its lane values afresh
+  // (fresh_lane): held from one phase to the next they took registers the phases need.
+  f32x16 a1[2];
+  int ln = fresh_lane();
+  init_bias(a1, wf + kB1, u0, ln);
   {
-    const int ut = wave % 3, rt = (wave / 3) * NRH;
-    f32x16 acc[NRH];
-    if (wave < 6) {
-      init_bias(acc, wf + kB3A, 32 * ut, lane);
-      gemm_t<NRH, kHid>(acc, wbf + Blob<KP>::W3A, 32 * ut, Hs + 32 * rt * kHPitch, kHPitch, 0,
-                        lane);
-    }
-    __syncthreads();                                  // every wave has read actor layer 2
-    if (wave < 6) {
+    // the normalised rows leave for nobs_out during these products, not in the staging, where
+    // every workgroup's row reads are in flight at once
+    const int t = fresh_lane() + 64 * wave;
+    const int cv = t % S::NC, rb = t / S::NC;
+    auto store_rows = [&](int j) {
+      if (!p.nobs_out || rb >= S::RP) return;
 #pragma unroll
-      for (int r = 0; r < NRH; ++r) {
-        const int row = 32 * (rt + r) + (lane & 31);
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int unit = 32 * ut + 8 * g + (lane >> 5) * 4;
-          *reinterpret_cast<float4*>(Ls + row * kLPitch + unit) =
-              make_float4(acc[r][4 * g + 0], acc[r][4 * g + 1], acc[r][4 * g + 2],
-                          acc[r][4 * g + 3]);
-        }
+      for (int q = 0; q < S::NP; ++q) {
+        const int r = rb + S::RP * q;
+        if ((q * 8) / S::NP == j && r < nr)
+          *reinterpret_cast<vec*>(p.nobs_out + (long)(r0 + r) * p.nobs_ld + VW * cv) = x[q];
       }
+    };
+    gemm_epi<2, KP>(a1, wbf + Blob<KP>::W1, u0, As, kHPitch, ln, store_rows);
+  }
+  // ---- phase 2: critic layer 1 products, actor layer 1 tanh -> B
+  f32x16 c1[2];
+  ln = fresh_lane();
+  if (critic) {
+    init_bias(c1, wf + kB1 + kHid, u0, ln);
+    gemm_epi<2, KP>(c1, wbf + Blob<KP>::W1C, u0, As, kHPitch, ln, TanhEpi{a1, Bs, u0, ln});
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) TanhEpi{a1, Bs, u0, ln}(j);
+  }
+  __syncthreads();
+  // ---- phase 3: actor layer 2 products, critic layer 1 tanh -> A
+  f32x16 a2[2];
+  ln = fresh_lane();
+  init_bias(a2, wf + kB2A, u0, ln);
+  if (critic)
+    gemm_epi<2, kHid>(a2, wbf + Blob<KP>::W2A, u0, Bs, kHPitch, ln, TanhEpi{c1, As, u0, ln});
+  else
+    gemm_epi<2, kHid>(a2, wbf + Blob<KP>::W2A, u0, Bs, kHPitch, ln, [](int) {});
+  __syncthreads();
+  // ---- phase 4: critic layer 2 products, actor layer 2 tanh -> B
+  f32x16 c2[2];
+  ln = fresh_lane();
+  if (critic) {
+    init_bias(c2, wf + kB2C, u0, ln);
+    gemm_epi<2, kHid>(c2, wbf + Blob<KP>::W2C, u0, As, kHPitch, ln, TanhEpi{a2, Bs, u0, ln});
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) TanhEpi{a2, Bs, u0, ln}(j);
+  }
+  __syncthreads();
+  // ---- phase 5: the logits head on waves 0-5 (32 units x 32 rows each), beside the critic's
+  // layer-2 tanh and its value partials (this wave's 32 units of every row)
+  const int ut = wave % 3, rt = wave / 3;
+  f32x16 h[1];
+  ln = fresh_lane();
+  float vp[2] = {0.0f, 0.0f};
+  float4 w3[4];
+  if (critic) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+      w3[g] = *reinterpret_cast<const float4*>(wf + kW3C + u0 + 8 * g + (ln >> 5) * 4);
+  }
+  if (wave < 6) {
+    init_bias(h, wf + kB3A, 32 * ut, ln);
+    if (critic)
+      gemm_epi<1, kHid>(h, wbf + Blob<KP>::W3A, 32 * ut, Bs + 32 * rt * kHPitch, kHPitch, ln,
+                        ValueEpi{c2, w3, vp});
+    else
+      gemm_t<1, kHid>(h, wbf + Blob<KP>::W3A, 32 * ut, Bs + 32 * rt * kHPitch, kHPitch, 0, ln);
+  } else if (critic) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ValueEpi{c2, w3, vp}(j);
+  }
+  if (critic) {
+#pragma unroll
+    for (int r = 0; r < 2; ++r) vp[r] += __shfl_xor(vp[r], 32);   // lns l, l + 32: one row
+    if (ln < 32) { vpart[wave][ln] = vp[0]; vpart[wave][32 + ln] = vp[1]; }
+  }
+  __syncthreads();                                    // every wave has read actor layer 2
+  ln = fresh_lane();
+  float* Ls = reinterpret_cast<float*>(Bs);
+  if (wave < 6) {
+    const int row = 32 * rt + (ln & 31);
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int unit = 32 * ut + 8 * g + (ln >> 5) * 4;
+      *reinterpret_cast<float4*>(Ls + row * kLPitch + unit) =
+          make_float4(h[0][4 * g + 0], h[0][4 * g + 1], h[0][4 * g + 2], h[0][4 * g + 3]);
     }
   }
   __syncthreads();
+
+  // ---- value: the eight waves' partials in order, plus the bias (wave 4, beside the draws)
+  ln = fresh_lane();
+  if (critic && wave == 4) {
+    float v = vpart[0][ln];
+#pragma unroll
+    for (int q = 1; q < kWaves; ++q) v += vpart[q][ln];
+    if (ln < nr) p.value[r0 + ln] = v + wf[kB3C];
+  }
 
   // ---- per (row, channel): softmax, draw, log-probability, control (waves 0-3)
   const uint32_t step = p.step + (p.step_base ? *p.step_base : 0u);
-  if (tid < RB * kChan) {
+  if (tid < kRows * kChan) {
     const int row = tid >> 2, ch = tid & 3;
     const float* l = Ls + row * kLPitch + ch * kBins;
     float lg[kBins];
 #pragma unroll
     for (int k = 0; k < kBins; ++k) lg[k] = l[k];
     float m = lg[0];
-    int amax = 0;
 #pragma unroll
-    for (int k = 1; k < kBins; ++k)
-      if (lg[k] > m) { m = lg[k]; amax = k; }
+    for (int k = 1; k < kBins; ++k) m = fmaxf(m, lg[k]);
     float e[kBins], s = 0.0f;
 #pragma unroll
     for (int k = 0; k < kBins; ++k) { e[k] = f16rng::exp_nonpos(lg[k] - m); s += e[k]; }
     const int li = r0 + row;
     const long pr = (row < nr) ? (p.rows ? p.rows[li] : li) : 0;
-    int idx = amax;
+    int idx = 0;
     if (!p.deterministic) {
       uint32_t c[4] = {(uint32_t)pr, step, (uint32_t)ch, p.salt};
       f16rng::philox4x32_10(c, (uint32_t)p.seed, (uint32_t)(p.seed >> 32));
       const float u = (float)(c[0] >> 8) * 0x1p-24f;
       const float target = u * s;
+      // the first k with e_0 + ... + e_k > target (20 if none): the partial sums never
+      // decrease (every e_k is a finite value >= 0), so it is the count of the k whose sum
+      // is not above the target -- no early exit, no branch per bin
       float cum = 0.0f;
-      idx = kBins - 1;
+      int below = 0;
 #pragma unroll
       for (int k = 0; k < kBins; ++k) {
         cum += e[k];
-        if (cum > target) { idx = k; break; }
+        below += (cum > target) ? 0 : 1;
       }
-    }
-    float lp = 0.0f;
+      idx = min(below, kBins - 1);
+    } else {
 #pragma unroll
-    for (int k = 0; k < kBins; ++k)
-      if (k == idx) lp = (lg[k] - m) - logf(s);
+      for (int k = kBins - 1; k >= 0; --k)         // the first bin at the maximum (0 if none)
+        if (lg[k] == m) idx = k;
+    }
+    float lsel = lg[0];
+#pragma unroll
+    for (int k = 1; k < kBins; ++k)
+      if (k == idx) lsel = lg[k];
+    float lp = (lsel - m) - logf(s);
     lp += __shfl_xor(lp, 1);
     lp += __shfl_xor(lp, 2);
     if (row < nr) {
@@ -226,26 +384,6 @@ __global__ __launch_bounds__(kThreads, RB == 64 ? 4 : 2) void policy_kernel(cons
         for (int k = 0; k < kBins; ++k) p.logits_out[(long)li * kLogits + ch * kBins + k] = lg[k];
       }
     }
-  }
-  // ---- critic: two tanh layers, then the value dot products (one row per lane of waves
-  // 0 .. RB/64 - 1).  Only when values are asked for (p.value is the same for every workgroup
-  // of the launch): a league's opponent networks act but are not trained, and their launch
-  // skips it.
-  if (!p.value) return;
-  __syncthreads();                                    // the logits are consumed
-  hidden_layers<KP, NR>(Xs, Hs, wbf + Blob<KP>::W1C, wf + kB1 + kHid, wbf + Blob<KP>::W2C,
-                        wf + kB2C, wave, lane);
-  if (wave < RB / 64) {
-    const int row = 64 * wave + lane;
-    const float* w3 = wf + kW3C;
-    float s = 0.0f;
-#pragma unroll 4
-    for (int k0 = 0; k0 < kHid; k0 += 8) {
-      const bf16x8 h = *reinterpret_cast<const bf16x8*>(Hs + row * kHPitch + k0);
-#pragma unroll
-      for (int q = 0; q < 8; ++q) s += (float)h[q] * w3[k0 + q];
-    }
-    if (row < nr) p.value[r0 + row] = s + wf[kB3C];
   }
 }
 
@@ -518,12 +656,18 @@ extern "C" int f16_policy_step(const F16PolicyArgs* a, void* stream) {
   }
   if (max_rows == 0) return 0;
   if (a->obs_ld % 2 || ((uintptr_t)a->obs & 7) || (a->nobs_out && (a->nobs_ld % 2 || ((uintptr_t)a->nobs_out & 7))))
-    return F16_EINVAL;                                   // rows are moved as float2
-  constexpr int rb = kPolicyRows;
-  const dim3 grid((unsigned)((max_rows + rb - 1) / rb), (unsigned)a->ngroups), block(kThreads);
+    return F16_EINVAL;                                   // rows are moved as float2 at least
+  // float4 rows where every row start is 16-byte aligned (184 columns; 214 is not a multiple of 4)
+  const bool v4 = a->obs_dim == 184 && a->obs_ld % 4 == 0 && ((uintptr_t)a->obs & 15) == 0 &&
+                  (!a->nobs_out || (a->nobs_ld % 4 == 0 && ((uintptr_t)a->nobs_out & 15) == 0));
+  const dim3 grid((unsigned)((max_rows + kRows - 1) / kRows), (unsigned)a->ngroups), block(kThreads);
   hipStream_t s = (hipStream_t)stream;
-  if (a->obs_dim == 184) hipLaunchKernelGGL((policy_kernel<192, rb>), grid, block, 0, s, *a);
-  else hipLaunchKernelGGL((policy_kernel<224, rb>), grid, block, 0, s, *a);
+  if (a->obs_dim == 184) {
+    if (v4) hipLaunchKernelGGL((policy_kernel<192, 4>), grid, block, 0, s, *a);
+    else hipLaunchKernelGGL((policy_kernel<192, 2>), grid, block, 0, s, *a);
+  } else {
+    hipLaunchKernelGGL((policy_kernel<224, 2>), grid, block, 0, s, *a);
+  }
   return f16_last_error();
 }
 

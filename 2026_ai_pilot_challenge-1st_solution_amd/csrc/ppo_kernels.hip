@@ -427,8 +427,7 @@ __global__ __launch_bounds__(kThreads, 1) void ppo_fused_kernel(const F16PPOArgs
       for (int k = 0; k < kBins; ++k) lg[k] = l[k];
       float m = lg[0];
 #pragma unroll
-      for (int k = 1; k < kBins; ++k)
-        if (lg[k] > m) m = lg[k];
+      for (int k = 1; k < kBins; ++k) m = fmaxf(m, lg[k]);   // the rollout's maximum
       float e[kBins], s = 0.0f;
 #pragma unroll
       for (int k = 0; k < kBins; ++k) { e[k] = f16rng::exp_nonpos(lg[k] - m); s += e[k]; }

@@ -3,8 +3,10 @@
 // the same expression sequence (compiled without contraction).
 //
 // e^x for x <= 0: Cody-Waite reduction x = n ln2 + r with ln2 split into a 16-bit head (n * head
-// exact for |n| < 256) and a tail, |r| <= ln2/2; e^r by its degree-7 Taylor polynomial in Horner
-// form (truncation < 2e-8 relative); scaling by 2^n with ldexp.  Below -87, 0.
+// exact for |n| < 256) and a tail, |r| <= ln2/2, each step one fused multiply-add; e^r by its
+// degree-7 Taylor polynomial in Horner form, one fma per degree (truncation < 2e-8 relative);
+// scaling by 2^n with ldexp.  Below -87, 0.  fmaf is exactly rounded on every IEEE
+// implementation, so the sequence stays reproducible.
 #pragma once
 
 #include <math.h>
@@ -15,19 +17,19 @@
 
 namespace f16rng {
 
-F16_HD float exp_nonpos(float x) {
-  if (!(x >= -87.0f)) return 0.0f;
+F16_HD float exp_nonpos(float x0) {
+  const bool in = x0 >= -87.0f;                      // false below -87 and for NaN
+  const float x = in ? x0 : 0.0f;                    // selects, not a branch per call
   const float n = rintf(x * 1.44269504f);
-  const float r = (x - n * 0.693145751953125f) - n * 1.42860677e-6f;
-  float p = 1.0f / 5040.0f;
-  p = p * r + 1.0f / 720.0f;
-  p = p * r + 1.0f / 120.0f;
-  p = p * r + 1.0f / 24.0f;
-  p = p * r + 1.0f / 6.0f;
-  p = p * r + 0.5f;
-  p = p * r + 1.0f;
-  p = p * r + 1.0f;
-  return ldexpf(p, (int)n);
+  const float r = fmaf(-n, 1.42860677e-6f, fmaf(-n, 0.693145751953125f, x));
+  float p = fmaf(1.0f / 5040.0f, r, 1.0f / 720.0f);
+  p = fmaf(p, r, 1.0f / 120.0f);
+  p = fmaf(p, r, 1.0f / 24.0f);
+  p = fmaf(p, r, 1.0f / 6.0f);
+  p = fmaf(p, r, 0.5f);
+  p = fmaf(p, r, 1.0f);
+  p = fmaf(p, r, 1.0f);
+  return in ? ldexpf(p, (int)n) : 0.0f;
 }
 
 }  // namespace f16rng

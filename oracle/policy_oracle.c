@@ -7,7 +7,8 @@
  * 21 logits (research/competition_36500/runtime/claude_code/model.py:195-233,
  * cuda_fdm/ppo_gpu.py:266-276) with torch's generator; this build's draw is specified instead as
  * an inverse-CDF lookup at a Philox4x32-10 uniform (same distribution, its own stream):
- *   m = max_k l_k;  e_k = exp(l_k - m) (IEEE-only exp below);  s = sum_k e_k (k ascending)
+ *   m = max_k l_k (fmaxf, k ascending);  e_k = exp(l_k - m) (IEEE-only exp below);  s = sum_k e_k
+ *   (k ascending)
  *   x0 = Philox4x32-10(counter = (row, step, channel, salt), key = (seed_lo, seed_hi))[0]
  *   u = (x0 >> 8) 2^-24;  idx = first k with e_0 + ... + e_k > u s (else 20)
  *   logp = sum over channels of (l_idx - m) - log(s)
@@ -32,20 +33,20 @@ void orc_philox4x32_10(uint32_t ctr[4], uint32_t k0, uint32_t k1)
     }
 }
 
-/* e^x, x <= 0: Cody-Waite reduction with a 16-bit head of ln 2 and Taylor degree 7 */
+/* e^x, x <= 0: Cody-Waite reduction with a 16-bit head of ln 2 and Taylor degree 7, each step
+   one fused multiply-add (fmaf is exactly rounded, so the GPU's v_fma_f32 sequence matches) */
 static float exp_nonpos(float x)
 {
     if (!(x >= -87.0f)) return 0.0f;
     float n = rintf(x * 1.44269504f);
-    float r = (x - n * 0.693145751953125f) - n * 1.42860677e-6f;
-    float p = 1.0f / 5040.0f;
-    p = p * r + 1.0f / 720.0f;
-    p = p * r + 1.0f / 120.0f;
-    p = p * r + 1.0f / 24.0f;
-    p = p * r + 1.0f / 6.0f;
-    p = p * r + 0.5f;
-    p = p * r + 1.0f;
-    p = p * r + 1.0f;
+    float r = fmaf(-n, 1.42860677e-6f, fmaf(-n, 0.693145751953125f, x));
+    float p = fmaf(1.0f / 5040.0f, r, 1.0f / 720.0f);
+    p = fmaf(p, r, 1.0f / 120.0f);
+    p = fmaf(p, r, 1.0f / 24.0f);
+    p = fmaf(p, r, 1.0f / 6.0f);
+    p = fmaf(p, r, 0.5f);
+    p = fmaf(p, r, 1.0f);
+    p = fmaf(p, r, 1.0f);
     return ldexpf(p, (int)n);
 }
 
@@ -61,8 +62,9 @@ void orc_policy_sample(const float *logits, const long *rows, long n, uint64_t s
             const float *l = logits + i * 84 + ch * 21;
             float m = l[0];
             int amax = 0;
-            for (int k = 1; k < 21; k++)
-                if (l[k] > m) { m = l[k]; amax = k; }
+            for (int k = 1; k < 21; k++) m = fmaxf(m, l[k]);
+            for (int k = 20; k >= 0; k--)           /* the first bin at the maximum (0 if none) */
+                if (l[k] == m) amax = k;
             float e[21], s = 0.0f;
             for (int k = 0; k < 21; k++) { e[k] = exp_nonpos(l[k] - m); s += e[k]; }
             int idx = amax;
