@@ -1,17 +1,19 @@
 // policy_kernels.hip -- rollout policy step on gfx950: RunningNorm update and the fused
 // normalise -> actor/critic MLP (bf16 MFMA, fp32 accumulate) -> categorical draw -> controls.
 //
-// Policy workgroup: 64 observation rows, 8 waves; 59 KB of LDS, so two workgroups share a CU and
-// one's loads, matrix work and tanh epilogues overlap the other's.  The rows are loaded with
-// every load in flight at once, normalised with per-column statistics staged in LDS, rounded to
-// bf16 and kept in LDS.  Actor, then critic: each runs its two 256-unit tanh layers through one
-// LDS activation buffer, every wave owning 32 units (2 tiles of v_mfma_f32_32x32x16_bf16 with
-// units as the matrix rows, so a lane's results are 4 consecutive units of one observation row:
-// one 8-byte LDS store per 4 activations; row pitch width + 8, so 16-byte fragment reads of 16
-// consecutive rows hit 64 distinct banks).  The logits head (84 units padded to 96) runs on six
-// waves and its results overlay the activation buffer for the draw; the critic's value is one
-// 256-long dot product per row.  Weights stream from L2 three K-slices ahead (every workgroup
-// reads the same 0.55 MB).  Sampling is one lane per (row, channel).
+// Policy workgroup: 64 observation rows, 8 waves; 71 KB of LDS, so two workgroups share a CU.
+// The rows are loaded with every load in flight at once (float4 where the rows allow it, each
+// thread keeping one column), normalised with per-column statistics staged in LDS, rounded to
+// bf16 and kept in LDS.  Every wave owns 32 units of every hidden layer of both networks (2 tiles
+// of v_mfma_f32_32x32x16_bf16 with units as the matrix rows, so a lane's results are 4
+// consecutive units of one observation row: one 8-byte LDS store per 4 activations; row pitch
+// 264, so 16-byte fragment reads of 16 consecutive rows hit 64 distinct banks).  The two
+// networks' layers alternate so that one network's matrix products run beside the other's tanh
+// epilogue (the kernel is bound by the vector ALU, which the tanh fills).  The logits head (84
+// units padded to 96) runs on six waves and its results overlay an activation buffer for the
+// draw; the critic's value is summed from per-wave partials formed in its last epilogue.
+// Weights stream from L2 a few K-slices ahead (every workgroup reads the same 0.55 MB).
+// Sampling is one lane per (row, channel).
 #include <hip/hip_runtime.h>
 
 #include <stdint.h>

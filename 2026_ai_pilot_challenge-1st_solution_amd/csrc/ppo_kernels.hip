@@ -400,49 +400,71 @@ __global__ __launch_bounds__(kThreads, 1) void ppo_fused_kernel(const F16PPOArgs
     }
     __syncthreads();
 
-    // ---- loss head, one lane per (row, channel) (ppo_gpu.py:2065-2090; model.py:207-219).
+    // ---- loss head (ppo_gpu.py:2065-2090; model.py:207-219).
     // Its per-row inputs are loaded first, then the next tile's rows: vmcnt retires loads in
     // order, so the loss head waits only for its own loads and the gather lands during the loss
     // head's arithmetic instead of stalling the next weight-fragment wait.
+    // Two lanes per (row, channel) -- lanes 2i, 2i + 1 take bins 0-10 and 11-20 -- so all eight
+    // waves share the head.  The maximum (exact, order-free), the numerator sum in the rollout's
+    // order (the high half continues from the low half's partial), the chosen bin's
+    // log-probability and the channel sum are the rollout kernel's values bit for bit.
+    const int item = tid >> 1, hb = tid & 1;           // (row, channel) item, bin half
+    const int lrow = item >> 2, lch = item & 3;
+    const int k0 = hb ? 11 : 0;                        // this lane's bins: k0 .. k0 + nb - 1
+    constexpr int kHalf = 11;
+    const int nb = hb ? kBins - kHalf : kHalf;
     long long act = -1;
     float old_lp = 0.0f, adv_r = 0.0f, ret_r = 0.0f;
-    if (tid < kRows * kChan) {
-      const long long pr = rowp[tid >> 2];
+    {
+      const long long pr = rowp[lrow];
       if (pr >= 0) {
-        act = a.act[pr * kChan + (tid & 3)];
+        act = a.act[pr * kChan + lch];
         old_lp = a.old_logp[pr];
         adv_r = a.adv[pr];
       }
     }
     if (tid < kRows && rowp[tid] >= 0) ret_r = a.ret[rowp[tid]];
     if (next < w.nwg) issue_rows<D, kPer>(a, rowpN, xr, tid);   // lands while this tile computes
-    float dz[kBins];
-    if (tid < kRows * kChan) {
-      const int row = tid >> 2, ch = tid & 3;
-      const long long pr = rowp[row];
+    float dz[kHalf];
+    {
+      const long long pr = rowp[lrow];
       const bool valid = pr >= 0;
-      const float* l = Ls + row * kLPitch + ch * kBins;
-      float lg[kBins];
+      const float* l = Ls + lrow * kLPitch + lch * kBins + k0;
+      float lg[kHalf];
 #pragma unroll
-      for (int k = 0; k < kBins; ++k) lg[k] = l[k];
+      for (int k = 0; k < kHalf; ++k) lg[k] = k < nb ? l[k] : l[0];
       float m = lg[0];
 #pragma unroll
-      for (int k = 1; k < kBins; ++k) m = fmaxf(m, lg[k]);   // the rollout's maximum
-      float e[kBins], s = 0.0f;
+      for (int k = 1; k < kHalf; ++k) m = fmaxf(m, lg[k]);
+      m = fmaxf(m, __shfl_xor(m, 1));                 // the rollout's maximum (max is exact)
+      float e[kHalf], sp = 0.0f;
 #pragma unroll
-      for (int k = 0; k < kBins; ++k) { e[k] = f16rng::exp_nonpos(lg[k] - m); s += e[k]; }
+      for (int k = 0; k < kHalf; ++k) {
+        e[k] = k < nb ? f16rng::exp_nonpos(lg[k] - m) : 0.0f;
+        if (hb == 0) sp += e[k];                      // the low half's sum, bins in order
+      }
+      float s = __shfl_xor(sp, 1);                    // the high lane receives it and continues
+#pragma unroll
+      for (int k = 0; k < kHalf; ++k)
+        if (k < nb) s += e[k];
+      const float s_hi = __shfl_xor(s, 1);            // every lane takes part in the shuffle
+      s = hb ? s : s_hi;                              // (the low lane's value above is unused)
       const float lse = logf(s), inv_s = 1.0f / s;
       float lp = 0.0f, hc = 0.0f;
+      bool mine = false;
 #pragma unroll
-      for (int k = 0; k < kBins; ++k) {
+      for (int k = 0; k < kHalf; ++k) {
         const float lpk = (lg[k] - m) - lse;
-        if (k == act) lp = lpk;
-        hc -= (e[k] * inv_s) * lpk;
+        if (k < nb && k0 + k == act) { lp = lpk; mine = true; }
+        if (k < nb) hc -= (e[k] * inv_s) * lpk;
       }
-      lp += __shfl_xor(lp, 1);              // the rollout kernel's summation order
-      lp += __shfl_xor(lp, 2);
-      float ent = hc + __shfl_xor(hc, 1);
-      ent += __shfl_xor(ent, 2);
+      const float lpo = __shfl_xor(lp, 1);
+      lp = mine ? lp : lpo;
+      hc += __shfl_xor(hc, 1);
+      lp += __shfl_xor(lp, 2);                        // channels: the rollout kernel's order
+      lp += __shfl_xor(lp, 4);
+      float ent = hc + __shfl_xor(hc, 2);
+      ent += __shfl_xor(ent, 4);
       float gcoef = 0.0f, pl = 0.0f, kl = 0.0f, cf = 0.0f;
       if (valid) {
         const float logr = lp - old_lp;
@@ -465,28 +487,26 @@ __global__ __launch_bounds__(kThreads, 1) void ppo_fused_kernel(const F16PPOArgs
       }
       const float ec = a.ent_coef * inv_mb;
 #pragma unroll
-      for (int k = 0; k < kBins; ++k) {
+      for (int k = 0; k < kHalf; ++k) {
         const float pk = e[k] * inv_s;
         const float lpk = (lg[k] - m) - lse;
-        const float oh = k == act ? 1.0f : 0.0f;
+        const float oh = k0 + k == act ? 1.0f : 0.0f;
         dz[k] = valid ? gcoef * (oh - pk) + ec * pk * (lpk + hc) : 0.0f;
       }
-      if (ch == 0) {
-        rowf[row][0] = pl;
-        rowf[row][1] = valid ? ent : 0.0f;
-        rowf[row][2] = kl;
-        rowf[row][3] = cf;
+      if (lch == 0 && hb == 0) {
+        rowf[lrow][0] = pl;
+        rowf[lrow][1] = valid ? ent : 0.0f;
+        rowf[lrow][2] = kl;
+        rowf[lrow][3] = cf;
       }
     }
     __syncthreads();                          // every logit is read
-    if (tid < kRows * kChan) {
-      const int row = tid >> 2, ch = tid & 3;
 #pragma unroll
-      for (int k = 0; k < kBins; ++k) Zs[row * kZPitch + ch * kBins + k] = (__bf16)dz[k];
-      if (ch == 3) {
+    for (int k = 0; k < kHalf; ++k)
+      if (k < nb) Zs[lrow * kZPitch + lch * kBins + k0 + k] = (__bf16)dz[k];
+    if (lch == 3 && hb == 1) {
 #pragma unroll
-        for (int k = kLogits; k < kLogitsPad; ++k) Zs[row * kZPitch + k] = (__bf16)0.0f;
-      }
+      for (int k = kLogits; k < kLogitsPad; ++k) Zs[lrow * kZPitch + k] = (__bf16)0.0f;
     }
     __syncthreads();
     write_t(Zs, kZPitch, kLogitsPad, w.dzt, ld, m0, tid);
@@ -563,9 +583,12 @@ __global__ __launch_bounds__(kThreads, 1) void ppo_fused_kernel(const F16PPOArgs
     {
       float* part = w.fpart + (long)tile * kPartCols;
       if (tid < kHid) {
-        float s = 0.0f;
-        for (int r = 0; r < kRows; ++r) s += rowf[r][4] * (float)H2s[r * kHPitch + tid];
-        part[kStatCols + tid] = s;
+        // four interleaved row sums (rows r = q mod 4), then combined: four independent
+        // dependency chains instead of one 64 long
+        float s4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 16
+        for (int r = 0; r < kRows; ++r) s4[r & 3] += rowf[r][4] * (float)H2s[r * kHPitch + tid];
+        part[kStatCols + tid] = (s4[0] + s4[1]) + (s4[2] + s4[3]);
       } else if (tid < kHid + 8) {
         const int c = tid - kHid;             // 0 pl, 1 ent, 2 kl, 3 cf, 4 dv (db3c), 5 se, 7 bad
         float s = 0.0f;
