@@ -329,7 +329,7 @@ def env_step_bench(pkg, nenv, steps, warmup, scan_finite=False, ab=True, stagger
 PEAK_BF16_TFLOPS = 2500.0
 
 
-def rollout_bench(nenv, T=64, reps=2):
+def rollout_bench(nenv, T=64, reps=2, stagger=True):
     """BASELINE C4: nenv engagements x T-step self-play rollout (FDM + fused obs/reward + norm
     update + fused bf16 actor/critic with Philox draw) then GAE (gamma 0.99, lambda 0.95) over
     [T, nenv, 2].  Weights N(0, 0.02), draw seed 0.  The collector records the rollout as a HIP
@@ -346,7 +346,7 @@ def rollout_bench(nenv, T=64, reps=2):
                                  generator=torch.Generator().manual_seed(0)).to("cuda")
         ro = ppo.SelfPlayRollout(env, net, T=T, gamma=0.99, lam=0.95, seed=0, stats=False,
                                  graph=graph)
-        ro.reset(stagger=True, max_stagger_steps=STAGGER_STEPS)
+        ro.reset(stagger=stagger, max_stagger_steps=STAGGER_STEPS)
         return ro
     ro = make(True)
     ro.collect()                                    # eager warm-up (allocations)
@@ -374,7 +374,7 @@ def rollout_bench(nenv, T=64, reps=2):
     pol_ms = float(np.mean([a.elapsed_time(b) for a, b in eager.policy_events]))
     flop = ppo.POLICY_FLOP_PER_ROW[184] * 2 * nenv
     return {"workload": "selfplay_rollout_16k_T64", "engagements": nenv, "T": T,
-            "reset": f"stagger over {STAGGER_STEPS} decisions",
+            "reset": f"stagger over {STAGGER_STEPS} decisions" if stagger else "no stagger",
             "episodes_done_per_rollout": done,
             "hip_graph": True, "ms_per_rollout": ms, "eager_ms_per_rollout": eager_ms,
             "transitions_per_s": nenv * T / (ms * 1e-3),
@@ -515,7 +515,7 @@ def main():
                     help="with --only env: time only the post-physics launch that re-reads the "
                          "state for the finite flags (profiling aid)")
     ap.add_argument("--no-stagger", action="store_true",
-                    help="with --only env: every engagement starts at t = 0 (profiling aid)")
+                    help="with --only env or rollout: every engagement starts at t = 0 (profiling aid)")
     ap.add_argument("--rebuild-resets", action="store_true",
                     help="with --only env: autoresets rebuild their rows instead of copying the "
                          "pool tables (profiling aid)")
@@ -550,7 +550,7 @@ def main():
                                               scan_finite=args.scan_finite, ab=False,
                                               stagger=not args.no_stagger,
                                               pool_tables=not args.rebuild_resets),
-                "rollout": lambda: rollout_bench(args.nenv),
+                "rollout": lambda: rollout_bench(args.nenv, stagger=not args.no_stagger),
                 "league": lambda: league_bench(),
                 "update": lambda: update_bench(args.nenv)}[args.only]()
         print(json.dumps(part), flush=True)
