@@ -319,6 +319,9 @@ class LeagueRollout:
         self.opp_events = None
         self._graph_mode = bool(graph)
         self._graphs = _RolloutGraph(self, dev) if self._graph_mode else None
+        # the opponents' grouping and launch run on a second stream (default priority) beside
+        # the learner's normalisation and launch; both join before the env step
+        self._side = None
         _aux_buffers(self, env, aux)
 
     def reset(self, **kw):
@@ -359,10 +362,18 @@ class LeagueRollout:
         g0 = 0 if pol_base is not None else self.global_step
         self.finite_acc.fill_(1)
         self.b_done[0].copy_(self.next_done)
+        main = torch.cuda.current_stream(self.device)
+        if self._side is None:
+            self._side = torch.cuda.Stream(device=self.device)
         for t in range(T):
             obs = self.next_obs
             if self.b_aux_features is not None:
                 self.b_aux_features[t].copy_(env.obr.aux_features)
+            # plane 1 (grouping + the opponents' launch) beside plane 0 (normalisation + the
+            # learner's launch): they share only reads of obs and write disjoint action rows
+            self._side.wait_stream(main)
+            with torch.cuda.stream(self._side):
+                self._timed(self.opp_events, lambda: self._opponents(obs, g0 + t, pol_base))
             if self.update_norm:
                 self.norm.update(obs, rows=self.main_rows)
             self._timed(self.policy_events, lambda: self.policy(
@@ -370,7 +381,7 @@ class LeagueRollout:
                 nphys=self.nac, step=g0 + t, salt=0, nobs_out=self.b_obs[t],
                 act_idx=self.b_act[t], logp=self.b_logp[t], value=self.b_val[t],
                 env_actions=env.sim.actions, step_base=pol_base))
-            self._timed(self.opp_events, lambda: self._opponents(obs, g0 + t, pol_base))
+            main.wait_stream(self._side)
             done_t = self.b_done[t + 1] if t + 1 < T else self.next_done
             self.next_obs = env.step_rollout(self.rew_all, done_t, self.finite_acc,
                                              step_base=env_base, step=t)

@@ -495,7 +495,9 @@ def league_bench(nenv=65536, T=128, nopp=8, reps=2):
            "aircraft_transitions_per_s": 2 * nenv * T / (ms * 1e-3),
            "learner_policy_ms": avg(eager.policy_events), "opponents_policy_ms": avg(eager.opp_events),
            "fdm_kernel_ms": avg(env.sim.kernel_events), "post_kernel_ms": avg(env.kernel_events),
-           "episodes_done_per_rollout": done}
+           "episodes_done_per_rollout": done,
+           "streams": "opponents' grouping + launch on a second stream beside the learner's "
+                      "normalisation + launch (the policy times overlap)"}
     return out
 
 
