@@ -7,33 +7,13 @@
 #include <hip/hip_runtime.h>
 
 #include "fdm_advance.h"
+#include "fdm_image.h"
 #include "fdm_split.h"
 #include "f16_capi_common.h"
 
 namespace f16 {
 
-__constant__ double c_image[F16M_IMAGE_LEN] = F16M_IMAGE_INIT;
-
 constexpr int kBlock = 256;
-
-// Copy the model image into LDS: every load of a thread is issued before its first store, so
-// the copy costs one memory latency rather than one per element.  NT = threads per block.
-template <int NT>
-__device__ __forceinline__ void stage_image(double* T) {
-  constexpr int kPer = (F16M_IMAGE_LEN + NT - 1) / NT;
-  double v[kPer];
-#pragma unroll
-  for (int j = 0; j < kPer; ++j) {
-    const int i = threadIdx.x + j * NT;
-    v[j] = i < F16M_IMAGE_LEN ? c_image[i] : 0.0;
-  }
-#pragma unroll
-  for (int j = 0; j < kPer; ++j) {
-    const int i = threadIdx.x + j * NT;
-    if (i < F16M_IMAGE_LEN) T[i] = v[j];
-  }
-  __syncthreads();
-}
 
 // ------------------------------------------------------------------ batched substeps
 // One lane per aircraft; `S` substeps with the action held, state in registers throughout

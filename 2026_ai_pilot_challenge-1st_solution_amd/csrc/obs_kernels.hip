@@ -15,8 +15,11 @@
 #include <math.h>
 
 #include "f16_capi_common.h"
+#include "f16_fdm.h"
 #include "f16_obs.h"
 #include "f16_state.h"
+#include "fdm_image.h"
+#include "fdm_split.h"
 #include "obs_device.h"
 #include "philox.h"
 
@@ -1045,12 +1048,21 @@ __device__ __forceinline__ void norm_partials_from_tiles(const float* S_all, dou
 // flush, as the single-wave kernel's terminal path does; without terminal_obs their first
 // build is not stored.  Results equal env_post_step_kernel's bit for bit.
 template <int D, bool FULL>
-__global__ __launch_bounds__(kPostSplitBlock) void env_post_step_split_kernel(
-    const F16EnvStepIO io, F16Recon r, F16RewardCfg c, Origin O) {
-  __shared__ float S_all[kPostGroups][kRowBlock * tile_pitch<D, FULL>()];
-  __shared__ uint64_t sh_mask[kPostGroups][3];   // live, finished and pool-table finished rows
-  __shared__ long sh_pick[kPostGroups][kRowBlock]; // pool table row of each pool-table autoreset
-  __shared__ double sh_norm[FULL ? 8 * D : 1];     // RunningNorm partials per phase (full tile)
+struct PostSplitLds {
+  float S_all[kPostGroups][kRowBlock * tile_pitch<D, FULL>()];
+  uint64_t sh_mask[kPostGroups][3];    // live, finished and pool-table finished rows
+  long sh_pick[kPostGroups][kRowBlock];  // pool table row of each pool-table autoreset
+  double sh_norm[FULL ? 8 * D : 1];      // RunningNorm partials per phase (full tile)
+};
+
+template <int D, bool FULL>
+__device__ __forceinline__ void post_split_body(const F16EnvStepIO& io, const F16Recon& r,
+                                                const F16RewardCfg& c, const Origin& O,
+                                                PostSplitLds<D, FULL>& L) {
+  auto& S_all = L.S_all;
+  auto& sh_mask = L.sh_mask;
+  auto& sh_pick = L.sh_pick;
+  auto& sh_norm = L.sh_norm;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int grp = wave >> 1, role = wave & 1;
@@ -1234,6 +1246,61 @@ __global__ __launch_bounds__(kPostSplitBlock) void env_post_step_split_kernel(
   }
 }
 
+template <int D, bool FULL>
+__global__ __launch_bounds__(kPostSplitBlock) void env_post_step_split_kernel(
+    const F16EnvStepIO io, F16Recon r, F16RewardCfg c, Origin O) {
+  __shared__ PostSplitLds<D, FULL> L;
+  post_split_body<D, FULL>(io, r, c, O, L);
+}
+
+// A whole environment step in one launch, for batches whose rows fit the full-row tile: the
+// workgroup first runs the FDM substeps of its 128 aircraft as fdm_step_split_kernel does (two
+// wavefronts per 64 aircraft, model image and exchange fields in LDS), then, after a workgroup
+// barrier, the post-physics step of env_post_step_split_kernel over the same 128 aircraft (its
+// groups and roles are the FDM's pairs and roles: aircraft (2 blockIdx.x + wave / 2) * 64 + lane
+// in both).  Every value the post-physics step reads of the new states, the per-aircraft finite
+// flags and the kept actions was written by this workgroup before that barrier, which also makes
+// the two phases' LDS (a union) safe to reuse.  Results equal the two launches bit for bit; the
+// second launch's start-up, its wait for the last FDM workgroup and the write-back of the states
+// at the kernel boundary are saved.  `act`: the controls read by the physics (io.actions is
+// what the post-physics step reads, written from `act` when `act_keep` is set);
+// `state_finite`: (nac) bytes, written by the physics and read back as io.state_finite.
+template <int D>
+union EnvStepLds {
+  struct {
+    double T[F16M_IMAGE_LEN];
+    f16::SplitX X[f16::kSplitPairs];
+  } fdm;
+  PostSplitLds<D, true> post;
+};
+static_assert(f16::kSplitBlock == kPostSplitBlock && f16::kSplitAircraft == kPostGroups * kRowBlock,
+              "the FDM pairs and the post-physics groups must cover the same aircraft");
+
+template <int FCS_RATE, int D>
+__global__ __launch_bounds__(kPostSplitBlock) void env_step_fused_kernel(
+    const double* __restrict__ act, int S, double* __restrict__ act_keep,
+    unsigned char* __restrict__ state_finite, const F16EnvStepIO io, F16Recon r, F16RewardCfg c,
+    Origin O) {
+  __shared__ EnvStepLds<D> L;
+  f16::stage_image<kPostSplitBlock>(L.fdm.T);
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int pair = wave >> 1;
+  const int nac = 2 * r.nenv;
+  const int i = blockIdx.x * f16::kSplitAircraft + pair * 64 + lane;
+  const bool store = i < nac;
+  const int ia = store ? i : nac - 1;   // lanes past the batch shadow the last aircraft
+  if ((wave & 1) == 0)
+    f16::split_flight<FCS_RATE>(io.states + ia, io.ld, S, store, nullptr, 0, L.fdm.T,
+                                L.fdm.X[pair], lane, true);
+  else
+    f16::split_systems<FCS_RATE>(io.states + ia, io.ld, act + 4L * ia, S, store, L.fdm.T,
+                                 L.fdm.X[pair], lane, state_finite + ia,
+                                 act_keep ? act_keep + 4L * ia : nullptr);
+  __syncthreads();   // the new states, finite flags and actions are written; LDS is free
+  post_split_body<D, true>(io, r, c, O, L.post);
+}
+
 // Masked autoreset without a step: engagements with mask[e] != 0 get an initial-condition pool
 // row (io.pick or the in-kernel Philox draw), the reconstructor reset and the reward state
 // re-anchored -- the departure reseeding of the staggered warm-up (rl_env.py:386-434) on the
@@ -1390,14 +1457,16 @@ extern "C" int f16_obr_build_obs(const double* states, long ld, const unsigned c
   return f16_last_error();
 }
 
-static int post_step(const F16EnvStepIO* io, const F16Recon* rec, const F16RewardCfg* cfg,
-                     void* stream, bool split) {
+// Arguments of a post-physics step: 0 when valid, 1 when there is nothing to do (nenv == 0),
+// else the error code.  *full: whether the launch uses the full-row tile.
+static int post_step_args(const F16EnvStepIO* io, const F16Recon* rec, const F16RewardCfg* cfg,
+                          bool split, bool* full) {
   if (!io) return F16_EINVAL;
   if (io->obs_dim != 184 && io->obs_dim != 214) return F16_EINVAL;
   int rc = check_recon(rec, io->obs_dim == 214);
   if (rc) return rc;
   if ((rc = check_cfg(cfg))) return rc;
-  if (rec->nenv == 0) return 0;
+  if (rec->nenv == 0) return 1;
   if (!io->states || !io->actions || !io->obs || !io->ic_pool || io->pool_size < 1 ||
       io->pool_size > 0xffffffffL || io->ld < 2L * rec->nenv || rec->ld != io->ld)
     return F16_EINVAL;
@@ -1405,9 +1474,14 @@ static int post_step(const F16EnvStepIO* io, const F16Recon* rec, const F16Rewar
   if (!rows_aligned(io->obs, io->obs_dim) ||
       (io->terminal_obs && !rows_aligned(io->terminal_obs, io->obs_dim)))
     return F16_EINVAL;
-  const bool full = full_tile_resident(rec->nenv, io->obs_dim, split ? kPostGroups : 1);
-  if (io->norm_partial && (!split || !full || !io->norm_count || !io->norm_count_snap))
+  *full = full_tile_resident(rec->nenv, io->obs_dim, split ? kPostGroups : 1);
+  if (io->norm_partial && (!split || !*full || !io->norm_count || !io->norm_count_snap))
     return F16_EINVAL;
+  return 0;
+}
+
+static int post_step_launch(const F16EnvStepIO* io, const F16Recon* rec, const F16RewardCfg* cfg,
+                            void* stream, bool split, bool full) {
   hipStream_t s = (hipStream_t)stream;
 #define F16_POST_STEP(D, FULL)                                                                  \
   do {                                                                                          \
@@ -1427,9 +1501,58 @@ static int post_step(const F16EnvStepIO* io, const F16Recon* rec, const F16Rewar
   return f16_last_error();
 }
 
+static int post_step(const F16EnvStepIO* io, const F16Recon* rec, const F16RewardCfg* cfg,
+                     void* stream, bool split) {
+  bool full = false;
+  const int rc = post_step_args(io, rec, cfg, split, &full);
+  if (rc) return rc < 0 ? rc : 0;
+  return post_step_launch(io, rec, cfg, stream, split, full);
+}
+
 extern "C" int f16_env_post_step(const F16EnvStepIO* io, const F16Recon* rec,
                                  const F16RewardCfg* cfg, void* stream) {
   return post_step(io, rec, cfg, stream, true);
+}
+
+extern "C" int f16_env_step(const F16EnvStepIO* io, const F16Recon* rec, const F16RewardCfg* cfg,
+                            const double* actions, int substeps, int fcs_rate,
+                            unsigned char* state_finite, void* stream) {
+  if (!io || !state_finite || substeps < 1) return F16_EINVAL;
+  if (fcs_rate != 120 && fcs_rate != 60) return F16_ERATE;
+  F16EnvStepIO x = *io;
+  x.state_finite = state_finite;
+  bool full = false;
+  int rc = post_step_args(&x, rec, cfg, true, &full);
+  if (rc) return rc < 0 ? rc : 0;
+  if (2L * rec->nenv > 0x7fffffffL) return F16_EINVAL;
+  const int nac = 2 * rec->nenv;
+  const double* act = actions ? actions : io->actions;
+  double* keep = act != io->actions ? const_cast<double*>(io->actions) : nullptr;
+  if (keep) {   // the physics reads `actions` and writes io->actions as separate arrays
+    const uintptr_t a0 = (uintptr_t)act, k0 = (uintptr_t)keep;
+    const uintptr_t bytes = (uintptr_t)nac * 4 * sizeof(double);
+    if (a0 < k0 + bytes && k0 < a0 + bytes) return F16_EINVAL;
+  }
+  if (!full) {
+    rc = keep ? f16_fdm_step_batch_keep(x.states, x.ld, act, keep, nac, substeps, fcs_rate,
+                                        nullptr, 0, state_finite, stream)
+              : f16_fdm_step_batch_finite(x.states, x.ld, act, nac, substeps, fcs_rate, nullptr,
+                                          0, state_finite, stream);
+    if (rc) return rc;
+    return post_step_launch(&x, rec, cfg, stream, true, false);
+  }
+  hipStream_t s = (hipStream_t)stream;
+#define F16_ENV_STEP(R, D)                                                                      \
+  hipLaunchKernelGGL((env_step_fused_kernel<R, D>), grid_groups(rec->nenv),                      \
+                     dim3(kPostSplitBlock), 0, s, act, substeps, keep, state_finite, x, *rec,    \
+                     *cfg, origin())
+  if (fcs_rate == 120) {
+    if (x.obs_dim == 184) F16_ENV_STEP(120, 184); else F16_ENV_STEP(120, 214);
+  } else {
+    if (x.obs_dim == 184) F16_ENV_STEP(60, 184); else F16_ENV_STEP(60, 214);
+  }
+#undef F16_ENV_STEP
+  return f16_last_error();
 }
 
 extern "C" int f16_env_post_step_norm_fusable(int nenv, int obs_dim) {

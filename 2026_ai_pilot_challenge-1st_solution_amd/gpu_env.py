@@ -125,6 +125,19 @@ class GpuDogfight:
         _lib.check(rc, "f16_seed_batch")
 
     # ---- step (cuda_fdm/gpu_env.py:95-106) ----
+    def action_source(self, actions):
+        """The (nac, 4) float64 device tensor a step launch reads its controls from.  The
+        reference copies the actions into self.actions before its launch; a separate contiguous
+        device tensor is returned as is (the launch reads it and writes the copy itself),
+        anything else is copied into self.actions here and self.actions is returned."""
+        a = torch.as_tensor(actions, dtype=torch.float64, device=self.device).reshape(self.nac, 4)
+        if (a.is_contiguous() and a.untyped_storage().data_ptr()
+                != self.actions.untyped_storage().data_ptr()):
+            return a
+        if a.data_ptr() != self.actions.data_ptr():
+            self.actions.copy_(a)
+        return self.actions
+
     def step(self, actions, substeps=None, want_obs=True, finite_out=None):
         """actions (nac,4) or (nenv,ppe,4) [aileron, elevator, rudder, throttle] -> obs view
         (nenv, ppe, 17).  want_obs=False skips the 17-value output write.  finite_out: an
@@ -137,13 +150,8 @@ class GpuDogfight:
                 raise ValueError("finite_out must be a contiguous (nac,) uint8/bool device tensor")
             if ss < 1:
                 raise ValueError("finite_out needs substeps >= 1")
-        a = torch.as_tensor(actions, dtype=torch.float64, device=self.device).reshape(self.nac, 4)
-        # the reference copies the actions into self.actions before its launch; a separate
-        # contiguous device tensor is read by the launch itself, which also writes the copy
-        keep = (a.is_contiguous() and a.untyped_storage().data_ptr()
-                != self.actions.untyped_storage().data_ptr())
-        if not keep and a.data_ptr() != self.actions.data_ptr():
-            self.actions.copy_(a)
+        a = self.action_source(actions)
+        keep = a.data_ptr() != self.actions.data_ptr()
         ev = self.kernel_events
         if ev is not None:
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)

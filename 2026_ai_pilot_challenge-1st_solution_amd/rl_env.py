@@ -81,6 +81,9 @@ class GpuDogfightVecEnv:
         # fused_finite=False makes the post-physics launch read the state and test it itself
         self._state_fin = torch.empty(n, dtype=torch.uint8, device=dev)
         self.fused_finite = True
+        # physics and post-physics in one launch (f16_env_step) where the finite flags are on;
+        # fused_step=False issues sim.step and f16_env_post_step as two launches
+        self.fused_step = True
         # per pool row, what an autoreset from it produces (observation, reward anchors, aux
         # features), so the post-physics launch copies instead of rebuilding; pool_tables=False
         # makes it rebuild them
@@ -299,6 +302,33 @@ class GpuDogfightVecEnv:
                 self._pool_table_ptrs()
         return io
 
+    def _advance(self, io, actions, state_fin):
+        """The physics step of `actions` and the post-physics step `io` describes: one
+        f16_env_step launch with fused_step and the finite flags (state_fin) on (where the batch
+        exceeds one workgroup per CU it issues the two launches itself), else sim.step and
+        f16_env_post_step.  kernel_events, when a list, gets the one launch's (start, end)."""
+        if not (self.fused_step and state_fin is not None):
+            self.sim.step(actions, substeps=self.substeps, want_obs=False, finite_out=state_fin)
+            io.state_finite = state_fin.data_ptr() if state_fin is not None else None
+            self._post(io)
+            return
+        a = self.sim.action_source(actions)
+        io.state_finite = state_fin.data_ptr()
+        c = self._cfg_struct()
+        ev = self.kernel_events
+        if ev is not None:
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+        rc = self.obr._lib.f16_env_step(_lib.ctypes.byref(io), _lib.ctypes.byref(self._rec),
+                                        _lib.ctypes.byref(c), a.data_ptr(), self.substeps,
+                                        self.sim.fcs_rate, state_fin.data_ptr(),
+                                        _lib.stream_handle(self.device))
+        if ev is not None:
+            e1.record()
+            ev.append((e0, e1))
+        _lib.check(rc, "f16_env_step")
+        self._post_steps += 1
+
     def _post(self, io):
         c = self._cfg_struct()
         ev = self.kernel_events
@@ -349,7 +379,6 @@ class GpuDogfightVecEnv:
         a = self._to_nac4(actions)
         self._ensure_ic_pool()
         state_fin = self._state_fin if self.fused_finite and self.substeps >= 1 else None
-        self.sim.step(a, substeps=self.substeps, want_obs=False, finite_out=state_fin)
         if reset_indices is None:
             # the pool row of each finished engagement is drawn inside the post-physics launch
             # (uniform over the pool: Philox keyed by the env seed, the step count and the
@@ -370,11 +399,10 @@ class GpuDogfightVecEnv:
         term, trunc, done, fin = (torch.empty(ne, dtype=torch.bool, device=dev) for _ in range(4))
         io = self._io(pick)
         p = lambda t: t.data_ptr() if t is not None else None
-        io.state_finite = p(state_fin)
         io.terminal_obs, io.reward = p(tobs), p(reward)
         io.term, io.trunc, io.done, io.terminal_finite = p(term), p(trunc), p(done), p(fin)
         io.terminal_hp, io.terminal_alt_m = p(terminal_hp), p(terminal_alt)
-        self._post(io)
+        self._advance(io, a, state_fin)
         info = {"terminated": term, "truncated": trunc,
                 "terminal_obs": tobs.view(ne, 2, self.OBS_SIZE) if tobs is not None else None,
                 "terminal_hp": terminal_hp.view(ne, 2),
@@ -388,8 +416,8 @@ class GpuDogfightVecEnv:
 
     def step_rollout(self, reward_f32, done_f32, finite_acc, step_base=None, step=0, norm=None):
         """The rollout collector's step: the controls already sit in sim.actions (written by the
-        policy kernel); one FDM launch and one post-physics launch that writes the float32
-        rewards (nac,) and done flags (nenv,) straight into the caller's buffers and clears
+        policy kernel); the physics and the post-physics step (one launch, _advance) write the
+        float32 rewards (nac,) and done flags (nenv,) straight into the caller's buffers and clear
         finite_acc (nenv,) bytes of engagements whose state went non-finite.  Autoreset pool rows
         are drawn inside the kernel (Philox keyed by the env seed and a per-env step counter).
         step_base (device int32 scalar) + step replaces the env's host step counter in the
@@ -398,17 +426,14 @@ class GpuDogfightVecEnv:
         of the new observation rows into its workspace, for norm.merge(nac)."""
         self._ensure_ic_pool()
         state_fin = self._state_fin if self.fused_finite and self.substeps >= 1 else None
-        self.sim.step(self.sim.actions, substeps=self.substeps, want_obs=False,
-                      finite_out=state_fin)
         io = self._io(None)
-        io.state_finite = state_fin.data_ptr() if state_fin is not None else None
         if step_base is not None:
             io.step, io.step_base = int(step) & 0xffffffff, step_base.data_ptr()
         io.reward_f32, io.done_f32 = reward_f32.data_ptr(), done_f32.data_ptr()
         io.finite_acc = finite_acc.data_ptr()
         if norm is not None:
             norm.fused_partials(io, self.nac)
-        self._post(io)
+        self._advance(io, self.sim.actions, state_fin)
         return self._obs.view(self.nac, self.OBS_SIZE)
 
     # ---- state export (rl_env.py:583-592) ----

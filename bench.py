@@ -247,28 +247,36 @@ def _env_timed(env, acts, warmup, steps):
 
 
 def _env_kernel_ms(env, acts, warmup, n):
-    """Mean FDM and post-physics launch times from a pass with events around each launch."""
+    """Mean launch times from a pass with events around each launch: (FDM, post-physics) for
+    the two-launch step, (None, None) and the one launch's for f16_env_step's fused kernel."""
     import torch
     env.kernel_events, env.sim.kernel_events = [], []
     for k in range(n):
         env.step(acts[warmup + k])
     torch.cuda.synchronize()
-    post_ms = float(np.mean([a.elapsed_time(b) for a, b in env.kernel_events]))
-    fdm_ms = float(np.mean([a.elapsed_time(b) for a, b in env.sim.kernel_events]))
+    mean = lambda ev: float(np.mean([a.elapsed_time(b) for a, b in ev])) if ev else None
+    post, fdm = mean(env.kernel_events), mean(env.sim.kernel_events)
     env.kernel_events = env.sim.kernel_events = None
-    return fdm_ms, post_ms
+    return (fdm, post, None) if fdm is not None else (None, None, post)
+
+
+# env step variants: (fused_step, fused_finite)
+ENV_VARIANTS = {"one_launch": (True, True), "two_launch": (False, True),
+                "state_scan": (False, False)}
 
 
 def env_step_bench(pkg, nenv, steps, warmup, scan_finite=False, ab=True, stagger=True,
-                   pool_tables=True):
+                   pool_tables=True, two_launch=False):
     """Full environment transitions: GpuDogfightVecEnv.step = FDM decision (6 substeps, FCS 60 Hz)
-    + the fused post-physics kernel (advance, reward, termination, terminal observation, pool
+    + the fused post-physics step (advance, reward, termination, terminal observation, pool
     autoreset, new observation), contest ICs with the staggered reset spread over the whole
     200 s engagement (so timeouts and deaths autoreset engagements inside the timed loop),
-    random 4-channel actions resident on the device.  The physics launch hands the post-physics
-    launch its per-aircraft finite flags; the same steps are timed again with the post-physics
-    launch re-reading the state for them (A/B in one process).  ab=False: time only one variant,
-    the flag hand-off, or with scan_finite the re-reading launch; stagger=False starts every
+    random 4-channel actions resident on the device.  Three variants are timed on the same
+    steps (A/B in one process): f16_env_step's single launch (the default), the physics launch
+    and the post-physics launch separately (the physics launch's per-aircraft finite flags
+    handed over; each launch timed on its own), and the two launches with the post-physics
+    launch re-reading the state for the finite flag.  ab=False: time only one variant, the
+    single launch, or with two_launch / scan_finite that one; stagger=False starts every
     engagement at t = 0 (no autoresets in the window); pool_tables=False rebuilds autoreset rows
     instead of copying them (profiling aids)."""
     import torch
@@ -283,46 +291,62 @@ def env_step_bench(pkg, nenv, steps, warmup, scan_finite=False, ab=True, stagger
     snap_states = env.sim.states.clone()
     snap_obr = env.obr.clone_state()
     post_bytes = POST_BYTES_PER_AIRCRAFT * 2 * nenv
-    runs = {True: [], False: []}
-    # alternating order (A B B A): whichever variant runs first after the warm-up pays for it
-    if not ab:
-        order = (False,) if scan_finite else (True,)
+    if ab:
+        # mirrored order: whichever variant runs first after the warm-up pays for it
+        order = ("one_launch", "two_launch", "state_scan", "state_scan", "two_launch",
+                 "one_launch")
     else:
-        order = (True, False, False, True)
-    for fused in order:
-        env.fused_finite = fused
-        env.sim.states.copy_(snap_states)        # both variants step the same engagements
+        order = ("state_scan",) if scan_finite else ("two_launch",) if two_launch else \
+            ("one_launch",)
+    runs = {}
+    for name in order:
+        env.fused_step, env.fused_finite = ENV_VARIANTS[name]
+        env.sim.states.copy_(snap_states)        # every variant steps the same engagements
         env.obr.restore(snap_obr)
         ms, done = _env_timed(env, acts, warmup, steps)
-        fdm_ms, post_ms = _env_kernel_ms(env, acts, warmup, min(steps, 20))
-        runs[fused].append((ms, done, fdm_ms, post_ms))
-    env.fused_finite = True
+        runs.setdefault(name, []).append((ms, done) + _env_kernel_ms(env, acts, warmup,
+                                                                       min(steps, 20)))
+    env.fused_step, env.fused_finite = ENV_VARIANTS["one_launch"]
     res = {}
-    for fused, r in runs.items():
-        if not r:
-            continue
-        ms, done, fdm_ms, post_ms = (float(np.mean([x[i] for x in r])) for i in range(4))
-        b = post_bytes + (0 if fused else POST_BYTES_SCAN_EXTRA * 2 * nenv)
-        res[fused] = {"ms_per_step": ms, "episodes_done": int(round(done)),
-                      "fdm_kernel_ms": fdm_ms, "post_kernel_ms": post_ms, "algorithmic_bytes": b,
-                      "achieved_GBs": b / (post_ms * 1e-3) / 1e9,
-                      "hbm_frac": b / (post_ms * 1e-3) / 1e9 / PEAK_HBM_GBS}
-    main = res[False] if (scan_finite and not ab) else res[True]
+    for name, r in runs.items():
+        avg = lambda i: None if r[0][i] is None else float(np.mean([x[i] for x in r]))
+        ms, done, fdm_ms, post_ms, step_ms = (avg(i) for i in range(5))
+        res[name] = {"ms_per_step": ms, "episodes_done": int(round(done))}
+        if step_ms is not None:
+            res[name]["step_kernel_ms"] = step_ms
+        else:
+            b = post_bytes + (POST_BYTES_SCAN_EXTRA * 2 * nenv if name == "state_scan" else 0)
+            res[name].update({"fdm_kernel_ms": fdm_ms, "post_kernel_ms": post_ms,
+                              "algorithmic_bytes": b,
+                              "achieved_GBs": b / (post_ms * 1e-3) / 1e9,
+                              "hbm_frac": b / (post_ms * 1e-3) / 1e9 / PEAK_HBM_GBS})
+    main_name = order[0]
+    main = res[main_name]
     out = {"workload": "contest_env_step_16k", "engagements": nenv, "obs_dim": 184,
            "substeps": env.substeps, "fcs_rate_hz": env.sim.fcs_rate,
            "reset": f"stagger over {STAGGER_STEPS} decisions" if stagger else "no stagger",
-           "pool_tables": pool_tables, "finite_flags": not (scan_finite and not ab),
+           "pool_tables": pool_tables, "variant": main_name,
            "transitions_per_s": nenv / (main["ms_per_step"] * 1e-3),
-           "ms_per_step": main["ms_per_step"], "fdm_kernel_ms": main["fdm_kernel_ms"],
-           "post_kernel_ms": main["post_kernel_ms"], "episodes_done": main["episodes_done"],
-           "vs_published": nenv / (main["ms_per_step"] * 1e-3) / REF_PUBLISHED_ENV_TRANSITIONS,
-           "post_kernel": {"kernel": "env_post_step_split_kernel<184,true>",
-                           "algorithmic_bytes": main["algorithmic_bytes"],
-                           "achieved_GBs": main["achieved_GBs"], "hbm_frac": main["hbm_frac"]}}
+           "ms_per_step": main["ms_per_step"], "episodes_done": main["episodes_done"],
+           "vs_published": nenv / (main["ms_per_step"] * 1e-3) / REF_PUBLISHED_ENV_TRANSITIONS}
+    if "step_kernel_ms" in main:
+        out["step_kernel"] = {"kernel": "env_step_fused_kernel<60,184>",
+                              "kernel_ms": main["step_kernel_ms"]}
+    two = res.get("two_launch", res.get("state_scan"))
+    if two is not None:
+        out["fdm_kernel_ms"], out["post_kernel_ms"] = two["fdm_kernel_ms"], two["post_kernel_ms"]
+        out["post_kernel"] = {"kernel": "env_post_step_split_kernel<184,true>",
+                              "variant": "two_launch" if "two_launch" in res else "state_scan",
+                              "algorithmic_bytes": two["algorithmic_bytes"],
+                              "achieved_GBs": two["achieved_GBs"], "hbm_frac": two["hbm_frac"]}
     if ab:
-        out["state_scan_ab"] = {"what": "post-physics launch re-reading the 86 other state doubles "
-                                        "for the finite flag instead of the physics launch's flag",
-                                **res[False]}
+        out["two_launch_ab"] = {"what": "f16_fdm_step_batch_keep then f16_env_post_step (the "
+                                        "physics launch's finite flags handed over)",
+                                **res["two_launch"]}
+        out["state_scan_ab"] = {"what": "the two launches with the post-physics launch "
+                                        "re-reading the 86 other state doubles for the finite "
+                                        "flag instead of the physics launch's flag",
+                                **res["state_scan"]}
     return out
 
 
@@ -485,6 +509,9 @@ def league_bench(nenv=65536, T=128, nopp=8, reps=2):
     eager.collect()
     torch.cuda.synchronize()
     env = eager.env
+    # (65,536 engagements exceed the single-launch step's residency: f16_env_step issues the
+    # same two launches as fused_step=False, which lets the events time each of them)
+    env.fused_step = False
     eager.policy_events, eager.opp_events, env.kernel_events, env.sim.kernel_events = [], [], [], []
     eager.collect()
     torch.cuda.synchronize()
@@ -514,8 +541,11 @@ def main():
     ap.add_argument("--no-league", action="store_true")
     ap.add_argument("--no-update", action="store_true")
     ap.add_argument("--scan-finite", action="store_true",
-                    help="with --only env: time only the post-physics launch that re-reads the "
-                         "state for the finite flags (profiling aid)")
+                    help="with --only env: time only the two-launch step whose post-physics "
+                         "launch re-reads the state for the finite flags (profiling aid)")
+    ap.add_argument("--two-launch", action="store_true",
+                    help="with --only env: time only the two-launch step (physics launch, then "
+                         "post-physics launch; profiling aid)")
     ap.add_argument("--no-stagger", action="store_true",
                     help="with --only env or rollout: every engagement starts at t = 0 (profiling aid)")
     ap.add_argument("--rebuild-resets", action="store_true",
@@ -551,7 +581,8 @@ def main():
         part = {"env": lambda: env_step_bench(pkg, args.nenv, args.steps, args.warmup,
                                               scan_finite=args.scan_finite, ab=False,
                                               stagger=not args.no_stagger,
-                                              pool_tables=not args.rebuild_resets),
+                                              pool_tables=not args.rebuild_resets,
+                                              two_launch=args.two_launch),
                 "rollout": lambda: rollout_bench(args.nenv, stagger=not args.no_stagger),
                 "league": lambda: league_bench(),
                 "update": lambda: update_bench(args.nenv)}[args.only]()

@@ -141,6 +141,21 @@ typedef struct F16EnvStepIO {
  * engagements keep the terminal observation in `obs`.  A pick outside [0, pool_size) fills that
  * engagement's states with NaN so the error surfaces as a non-finite state instead of an
  * out-of-bounds read.  obs and terminal_obs: 16-byte aligned for 184, 8-byte for 214. */
+/* The whole GpuDogfightVecEnv.step after the action decode (research/competition_36500/
+ * runtime/cuda_fdm/rl_env.py:511-580): the physics step of f16_fdm_step_batch_keep (`actions`
+ * for `substeps` steps at fcs_rate; when `actions` is non-NULL and differs from io->actions, the
+ * launch also copies it into io->actions, which must not overlap it) followed by
+ * f16_env_post_step of `io`, with `state_finite` ((nac) bytes, required) carrying the physics'
+ * per-aircraft finite flags to the post-physics step (io->state_finite is ignored).  Where every
+ * workgroup of the post-physics step's full-row tile is resident at once (as
+ * f16_env_post_step_norm_fusable reports), one launch does both, each workgroup running the
+ * physics of its 128 aircraft and then their post-physics step; otherwise the two launches are
+ * issued.  Results equal the two entry points' bit for bit.  Every argument is checked before
+ * anything is launched. */
+int f16_env_step(const F16EnvStepIO *io, const F16Recon *rec, const F16RewardCfg *cfg,
+                 const double *actions, int substeps, int fcs_rate, unsigned char *state_finite,
+                 void *stream);
+
 /* The autoreset half of f16_env_post_step alone, for the engagements with mask[e] != 0
  * ((nenv) bytes): pool row (io->pick or the Philox draw at io->step), reconstructor reset,
  * re-anchored reward state (and, with io->opp_assign, an opponent redraw); no observation.  The

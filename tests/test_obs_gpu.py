@@ -514,6 +514,91 @@ def test_env_step_pool_tables_equal_rebuild(gpu, obs_dim, nenv):
     assert envs[0]._pool_key is not None and envs[1]._pool_key is None
 
 
+@pytest.mark.parametrize("obs_dim,nenv,fcs", [(184, 300, 60), (214, 300, 120), (184, 16384, 60),
+                                              (214, 16384, 120), (184, 20000, 60)])
+def test_env_step_one_launch_equals_two(gpu, obs_dim, nenv, fcs):
+    """f16_env_step (physics and post-physics step in one launch wherever the full-row tile is
+    resident: 300 engagements, whose last workgroup is partly filled, and 16,384; at 20,000 the
+    entry issues the two launches itself) against sim.step + f16_env_post_step: every output,
+    the states, the kept actions, the reconstructor and the aux features bit for bit over steps
+    with autoresets (staggered 1.2 s engagements), terminal observations on and off, a separate
+    action tensor (the launch copies it into sim.actions) and a non-contiguous one (copied
+    before the launch), NaN planted in a state and a pick outside the pool; then rollout steps
+    (step_rollout) with a device step counter and, where fusable, the RunningNorm partial sums
+    merged into the statistics."""
+    E = import_pkg("rl_env").GpuDogfightVecEnv
+    P = import_pkg("policy")
+    envs = [E(nenv, seed=11, ic_pool_size=64, obs_dim=obs_dim, max_engage_time_s=1.2,
+              fcs_rate=fcs) for _ in range(2)]
+    envs[1].fused_step = False
+    for env in envs:
+        env.enable_aux_capture()
+        env.reset(stagger=True, max_stagger_steps=12)
+    bits = lambda t: t.contiguous().view(torch.int32 if t.element_size() == 4 else
+                                         torch.int64 if t.element_size() == 8 else torch.uint8)
+    same = lambda x, y: torch.equal(bits(x), bits(y))       # NaN-safe, bit for bit
+    names = ("hp", "fuel", "prev_x", "prev_x_valid", "prev_alt_log", "t_sec", "aux_features",
+             "_hist_soa", "_att_soa", "_pqr_soa")
+    rng = np.random.default_rng(12)
+    resets = 0
+    for k in range(6):
+        act = rng.uniform(-1, 1, (2 * nenv, 4))
+        act_t = (torch.as_tensor(act.T.copy(), device=gpu).t() if k == 2 else
+                 torch.as_tensor(act, device=gpu))
+        pick = rng.integers(0, 64, nenv)
+        if k == 3:
+            pick[5] = 64                                    # outside the pool: NaN row
+        pick = torch.as_tensor(pick, device=gpu)
+        outs = []
+        for env in envs:
+            if k == 1:
+                env.sim.states[17, 5] = float("nan")
+            outs.append(env.step(act_t, reset_indices=pick if k % 2 == 1 else None,
+                                 capture_terminal_obs=k != 4))
+        (oa, ra, da, ia), (ob, rb, db, ib) = outs
+        assert same(oa, ob) and same(ra, rb) and same(da, db), k
+        for key in ia:
+            assert (ia[key] is None) == (ib[key] is None), (k, key)
+            assert ia[key] is None or same(ia[key], ib[key]), (k, key)
+        assert same(envs[0].sim._state_soa, envs[1].sim._state_soa), k
+        assert same(envs[0].sim.actions, envs[1].sim.actions), k
+        assert same(envs[0].sim.actions, torch.as_tensor(act, device=gpu)), k
+        for name in names:
+            assert same(getattr(envs[0].obr, name), getattr(envs[1].obr, name)), (k, name)
+        if k == 1:
+            assert not bool(ia["terminal_state_finite"][8])
+        resets += int(da.sum())
+    assert resets > nenv // 4, resets
+    nac = 2 * nenv
+    norms = [P.RunningNorm(obs_dim, gpu) for _ in envs]
+    bases = [torch.full((), 40, dtype=torch.int32, device=gpu) for _ in envs]
+    bufs = [{"rew": torch.zeros(nac, dtype=torch.float32, device=gpu),
+             "dn": torch.zeros(nenv, dtype=torch.float32, device=gpu),
+             "facc": torch.ones(nenv, dtype=torch.uint8, device=gpu)} for _ in envs]
+    fusable = envs[0].norm_fusable()
+    assert fusable == (nenv <= 16384)
+    for t in range(3):
+        act = torch.as_tensor(rng.uniform(-1, 1, (nac, 4)), device=gpu)
+        obs = []
+        for env, norm, base, b in zip(envs, norms, bases, bufs):
+            env.sim.actions.copy_(act)
+            obs.append(env.step_rollout(b["rew"], b["dn"], b["facc"], step_base=base, step=t,
+                                        norm=norm if fusable else None))
+            if fusable:
+                norm.merge(nac)
+        assert same(obs[0], obs[1]), t
+        for key in bufs[0]:
+            assert same(bufs[0][key], bufs[1][key]), (t, key)
+        assert same(envs[0].sim._state_soa, envs[1].sim._state_soa), t
+        for name in names:
+            assert same(getattr(envs[0].obr, name), getattr(envs[1].obr, name)), (t, name)
+        if fusable:
+            for f in ("mean", "var", "count"):
+                assert same(getattr(norms[0], f), getattr(norms[1], f)), (t, f)
+    if fusable:
+        assert float(norms[0].count) > 1.0
+
+
 def test_step_training_and_capture_switch(gpu):
     """The root lineage's surface (cuda_fdm/rl_env.py:518-529): step_training and
     step(capture_terminal_obs=False) return the same observation, reward, done and info as a
