@@ -63,7 +63,7 @@ class F16PolicyArgs(ctypes.Structure):
     _fields_ = [("obs", _vp), ("obs_ld", _l), ("obs_dim", _i), ("mean", _vp), ("var", _vp),
                 ("clip", ctypes.c_float), ("eps", ctypes.c_float), ("rows", _vp),
                 ("ngroups", _i), ("group", F16PolicyGroup * 16), ("group_offsets", _vp),
-                ("max_group_rows", _i), ("seed", ctypes.c_ulonglong),
+                ("max_group_rows", _i), ("total_group_rows", _i), ("seed", ctypes.c_ulonglong),
                 ("step", ctypes.c_uint), ("salt", ctypes.c_uint), ("deterministic", _i),
                 ("grid", _vp), ("nobs_out", _vp), ("nobs_ld", _l), ("act_idx", _vp),
                 ("logp", _vp), ("value", _vp), ("env_actions", _vp), ("logits_out", _vp),

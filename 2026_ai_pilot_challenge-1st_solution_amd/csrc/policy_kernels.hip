@@ -142,16 +142,39 @@ __global__ __launch_bounds__(kThreads, 4) void policy_kernel(const F16PolicyArgs
   __shared__ __align__(16) __bf16 Bs[kRows * kHPitch];
   __shared__ __align__(16) float col_mean[KP], col_sd[KP];
   __shared__ float vpart[kWaves][kRows];
-  const int gi = blockIdx.y;
-  if (gi >= p.ngroups) return;
+  // The workgroup's network and 64-row tile.  The row ranges are uniform: kept in scalar
+  // registers (a vector load would hold them, and everything derived from them, in vector
+  // registers for the whole kernel).
+  int gi, r0, ge;
+  if (p.total_group_rows > 0) {
+    // packed grid (device offsets): the groups' tiles in group order along x
+    int t = blockIdx.x;
+    gi = -1;
+    r0 = ge = 0;
+    for (int g = 0; g < p.ngroups; ++g) {
+      const int b = __builtin_amdgcn_readfirstlane(p.group_offsets[g]);
+      const int e = __builtin_amdgcn_readfirstlane(p.group_offsets[g + 1]);
+      const int nt = e > b ? (e - b + kRows - 1) / kRows : 0;
+      if (t < nt) {
+        gi = g;
+        r0 = b + t * kRows;
+        ge = e;
+        break;
+      }
+      t -= nt;
+    }
+    if (gi < 0) return;                               // past the last group's last tile
+  } else {
+    gi = blockIdx.y;
+    if (gi >= p.ngroups) return;
+    const int gb = __builtin_amdgcn_readfirstlane(p.group_offsets ? p.group_offsets[gi]
+                                                                  : p.group[gi].row_begin);
+    ge = __builtin_amdgcn_readfirstlane(p.group_offsets ? p.group_offsets[gi + 1]
+                                                        : p.group[gi].row_end);
+    r0 = gb + blockIdx.x * kRows;
+    if (r0 >= ge) return;                             // uniform per workgroup
+  }
   const F16PolicyGroup G = p.group[gi];
-  // the group's row range is uniform: kept in scalar registers (a vector load would hold it,
-  // and everything derived from it, in vector registers for the whole kernel)
-  const int gb = __builtin_amdgcn_readfirstlane(p.group_offsets ? p.group_offsets[gi] : G.row_begin);
-  const int ge =
-      __builtin_amdgcn_readfirstlane(p.group_offsets ? p.group_offsets[gi + 1] : G.row_end);
-  const int r0 = gb + blockIdx.x * kRows;
-  if (r0 >= ge) return;                               // uniform per workgroup
   const int nr = min(kRows, ge - r0);
   const float* g_mean = G.mean ? G.mean : p.mean;
   const float* g_var = G.mean ? G.var : p.var;
@@ -653,8 +676,10 @@ extern "C" int f16_policy_step(const F16PolicyArgs* a, void* stream) {
     }
   }
   if (a->group_offsets) {
-    if (a->max_group_rows < 0) return F16_EINVAL;
+    if (a->max_group_rows < 0 || a->total_group_rows < 0) return F16_EINVAL;
     max_rows = a->max_group_rows;
+  } else if (a->total_group_rows != 0) {
+    return F16_EINVAL;                                   // the packed grid needs device offsets
   }
   if (max_rows == 0) return 0;
   if (a->obs_ld % 2 || ((uintptr_t)a->obs & 7) || (a->nobs_out && (a->nobs_ld % 2 || ((uintptr_t)a->nobs_out & 7))))
@@ -662,7 +687,10 @@ extern "C" int f16_policy_step(const F16PolicyArgs* a, void* stream) {
   // float4 rows where every row start is 16-byte aligned (184 columns; 214 is not a multiple of 4)
   const bool v4 = a->obs_dim == 184 && a->obs_ld % 4 == 0 && ((uintptr_t)a->obs & 15) == 0 &&
                   (!a->nobs_out || (a->nobs_ld % 4 == 0 && ((uintptr_t)a->nobs_out & 15) == 0));
-  const dim3 grid((unsigned)((max_rows + kRows - 1) / kRows), (unsigned)a->ngroups), block(kThreads);
+  const dim3 grid = a->total_group_rows > 0
+      ? dim3((unsigned)((a->total_group_rows + kRows - 1) / kRows + a->ngroups), 1u)
+      : dim3((unsigned)((max_rows + kRows - 1) / kRows), (unsigned)a->ngroups);
+  const dim3 block(kThreads);
   hipStream_t s = (hipStream_t)stream;
   if (a->obs_dim == 184) {
     if (v4) hipLaunchKernelGGL((policy_kernel<192, 4>), grid, block, 0, s, *a);

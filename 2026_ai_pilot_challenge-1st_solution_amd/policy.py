@@ -221,11 +221,14 @@ class PolicyStep:
     def __call__(self, obs, groups, *, norm=None, rows=None, step=0, salt=0, deterministic=False,
                  nobs_out=None, act_idx=None, logp=None, value=None, env_actions=None,
                  logits_out=None, group_offsets=None, max_group_rows=None, nphys=None,
-                 step_base=None):
+                 step_base=None, packed=True):
         """groups: (net, row_begin, row_end) or (net, row_begin, row_end, norm) -- a per-network
         RunningNorm overrides `norm` for that network.  group_offsets: device int32 (ngroups+1)
         row boundaries computed on the device (f16_group_rows); then row_begin/row_end are
-        ignored, max_group_rows bounds any group's size and nphys bounds the physical rows.
+        ignored, max_group_rows bounds any group's size and nphys bounds the physical rows;
+        packed=True launches about len(rows) / 64 + ngroups workgroups, each taking the next
+        64-row tile of the groups in order, instead of ngroups x max_group_rows / 64 (same
+        results).
         step_base: optional device int32 scalar added to `step` in the kernel (rollouts recorded
         in a HIP graph advance it on the device between replays).
         nphys given with a row map skips the (host-synchronising) row-map validation: the caller
@@ -297,6 +300,7 @@ class PolicyStep:
             a.group[i].row_begin, a.group[i].row_end = int(b or 0), int(e or 0)
         if group_offsets is not None:
             a.group_offsets, a.max_group_rows = group_offsets.data_ptr(), int(max_group_rows)
+            a.total_group_rows = nlog if packed else 0
         a.seed, a.step, a.salt = self.seed, int(step) & 0xffffffff, int(salt) & 0xffffffff
         a.deterministic = int(bool(deterministic))
         a.grid = self.grid.data_ptr()

@@ -49,6 +49,10 @@ typedef struct F16PolicyArgs {
     const int *group_offsets;  /* device (ngroups + 1) row offsets: group g evaluates logical rows
                                   [offsets[g], offsets[g+1]); NULL = the groups' row_begin/end */
     int max_group_rows;     /* with group_offsets: upper bound of any group's row count */
+    int total_group_rows;   /* with group_offsets: upper bound of the groups' row counts summed,
+                               or 0.  When set, the launch packs every group's 64-row tiles into
+                               one grid dimension (about total / 64 + ngroups workgroups instead
+                               of ngroups x max_group_rows / 64) */
     unsigned long long seed;/* Philox4x32-10 key */
     unsigned int step;      /* counter word 1 (rollout step) */
     unsigned int salt;      /* counter word 3 (separates independent draws at one step) */

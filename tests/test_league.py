@@ -60,9 +60,11 @@ def _nets(P, k, dim, gpu, seed):
 
 
 @pytest.mark.gpu
-def test_grouped_launch_with_device_offsets(gpu, orc):
+@pytest.mark.parametrize("packed,empty", [(True, False), (False, False), (True, True)])
+def test_grouped_launch_with_device_offsets(gpu, orc, packed, empty):
     """One launch over rows grouped on the device equals one launch per network, each with its
-    own normalisation statistics."""
+    own normalisation statistics: with the groups' tiles packed into one grid dimension and with
+    one grid row per group, and with a group that gets no rows (empty=True: ids avoid group 2)."""
     P = import_pkg("policy")
     L = import_pkg("_lib")
     nenv, ng, D = 3000, 5, 214
@@ -75,7 +77,10 @@ def test_grouped_launch_with_device_offsets(gpu, orc):
         nm.var.copy_(torch.as_tensor(rng.uniform(0.5, 2.0, D).astype(np.float32)))
         norms.append(nm)
     obs = torch.as_tensor(rng.normal(0, 1, (2 * nenv, D)).astype(np.float32), device=gpu)
-    assign = torch.as_tensor(rng.integers(0, ng, nenv).astype(np.int32), device=gpu)
+    ids = rng.integers(0, ng, nenv).astype(np.int32)
+    if empty:
+        ids[ids == 2] = 3
+    assign = torch.as_tensor(ids, device=gpu)
     rows = torch.empty(nenv, dtype=torch.int32, device=gpu)
     offs = torch.empty(ng + 1, dtype=torch.int32, device=gpu)
     work = torch.empty(max(8, L.lib().f16_group_workspace_bytes(nenv)), dtype=torch.uint8,
@@ -87,10 +92,13 @@ def test_grouped_launch_with_device_offsets(gpu, orc):
     lg = torch.empty(nenv, 84, dtype=torch.float32, device=gpu)
     step(obs, [(n, None, None, nm) for n, nm in zip(nets, norms)], rows=rows,
          group_offsets=offs, max_group_rows=nenv, nphys=2 * nenv, step=3, salt=1,
-         env_actions=acts, logits_out=lg)
+         env_actions=acts, logits_out=lg, packed=packed)
     o = offs.cpu().numpy()
+    assert (o[3] - o[2] == 0) == empty
     r = rows.cpu().numpy()
     for g in range(ng):
+        if o[g + 1] == o[g]:
+            continue
         sub = obs[rows[o[g]:o[g + 1]].long()].contiguous()
         lg2 = torch.empty(o[g + 1] - o[g], 84, dtype=torch.float32, device=gpu)
         step(sub, [(nets[g], 0, o[g + 1] - o[g])], norm=norms[g], logits_out=lg2)
