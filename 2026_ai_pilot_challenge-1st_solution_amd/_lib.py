@@ -49,7 +49,7 @@ class F16EnvStepIO(ctypes.Structure):
                 ("opp_assign", _vp), ("opp_cdf", _vp), ("n_opp", _i), ("step_base", _vp),
                 ("norm_partial", _vp), ("norm_count", _vp), ("norm_count_snap", _vp),
                 ("state_finite", _vp), ("pool_obs", _vp), ("pool_prev_x", _vp),
-                ("pool_prev_alt_log", _vp), ("pool_aux", _vp)]
+                ("pool_prev_alt_log", _vp), ("pool_aux", _vp), ("reward0_f32", _vp)]
 
 
 class F16PolicyGroup(ctypes.Structure):

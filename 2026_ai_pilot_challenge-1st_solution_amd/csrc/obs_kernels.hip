@@ -939,6 +939,7 @@ __global__ __launch_bounds__(kRowBlock) void env_post_step_kernel(const F16EnvSt
     if (io.reward_f32) io.reward_f32[a] = (float)o.reward;
     d = o.term || o.trunc;
     if (!odd) {
+      if (io.reward0_f32) io.reward0_f32[e] = (float)o.reward;
       if (io.term) io.term[e] = o.term;
       if (io.trunc) io.trunc[e] = o.trunc;
       if (io.done) io.done[e] = d;
@@ -1131,6 +1132,7 @@ __device__ __forceinline__ void post_split_body(const F16EnvStepIO& io, const F1
       if (io.reward_f32) io.reward_f32[a] = (float)o.reward;
       d = o.term || o.trunc;
       if (!odd) {
+        if (io.reward0_f32) io.reward0_f32[e] = (float)o.reward;
         if (io.term) io.term[e] = o.term;
         if (io.trunc) io.trunc[e] = o.trunc;
         if (io.done) io.done[e] = d;

@@ -307,7 +307,6 @@ class LeagueRollout:
         self.b_rew = torch.empty(self.T, ne, dtype=f32, device=dev)
         self.b_val = torch.empty(self.T, ne, dtype=f32, device=dev)
         self.b_done = torch.empty(self.T, ne, dtype=f32, device=dev)
-        self.rew_all = torch.empty(nac, dtype=f32, device=dev)
         self.last_val = torch.empty(ne, dtype=f32, device=dev)
         self.next_obs = None
         self.next_done = torch.zeros(ne, dtype=f32, device=dev)
@@ -383,9 +382,9 @@ class LeagueRollout:
                 env_actions=env.sim.actions, step_base=pol_base))
             main.wait_stream(self._side)
             done_t = self.b_done[t + 1] if t + 1 < T else self.next_done
-            self.next_obs = env.step_rollout(self.rew_all, done_t, self.finite_acc,
-                                             step_base=env_base, step=t)
-            self.b_rew[t].copy_(self.rew_all[0::2])
+            self.next_obs = env.step_rollout(None, done_t, self.finite_acc,
+                                             step_base=env_base, step=t,
+                                             reward0_f32=self.b_rew[t])
         self.policy(self.next_obs, [(self.net, 0, self.nenv)], norm=self.norm,
                     rows=self.main_rows, nphys=self.nac, step=g0 + T, value=self.last_val,
                     step_base=pol_base)

@@ -414,7 +414,8 @@ class GpuDogfightVecEnv:
         """Whether step_rollout can also form the RunningNorm partial sums of its new rows."""
         return bool(self.obr._lib.f16_env_post_step_norm_fusable(self.nenv, self.OBS_SIZE))
 
-    def step_rollout(self, reward_f32, done_f32, finite_acc, step_base=None, step=0, norm=None):
+    def step_rollout(self, reward_f32, done_f32, finite_acc, step_base=None, step=0, norm=None,
+                     reward0_f32=None):
         """The rollout collector's step: the controls already sit in sim.actions (written by the
         policy kernel); the physics and the post-physics step (one launch, _advance) write the
         float32 rewards (nac,) and done flags (nenv,) straight into the caller's buffers and clear
@@ -423,13 +424,19 @@ class GpuDogfightVecEnv:
         step_base (device int32 scalar) + step replaces the env's host step counter in the
         kernel's draws: a rollout recorded in a HIP graph advances step_base on the device.
         norm (a RunningNorm, only where norm_fusable()): the launch also writes the partial sums
-        of the new observation rows into its workspace, for norm.merge(nac)."""
+        of the new observation rows into its workspace, for norm.merge(nac).  reward_f32 may be
+        None when reward0_f32 (nenv,) is given: the launch then writes only each engagement's
+        first aircraft's reward, straight into a learner-side buffer."""
         self._ensure_ic_pool()
         state_fin = self._state_fin if self.fused_finite and self.substeps >= 1 else None
         io = self._io(None)
         if step_base is not None:
             io.step, io.step_base = int(step) & 0xffffffff, step_base.data_ptr()
-        io.reward_f32, io.done_f32 = reward_f32.data_ptr(), done_f32.data_ptr()
+        if reward_f32 is None and reward0_f32 is None:
+            raise ValueError("step_rollout needs reward_f32 or reward0_f32")
+        io.reward_f32 = reward_f32.data_ptr() if reward_f32 is not None else None
+        io.reward0_f32 = reward0_f32.data_ptr() if reward0_f32 is not None else None
+        io.done_f32 = done_f32.data_ptr()
         io.finite_acc = finite_acc.data_ptr()
         if norm is not None:
             norm.fused_partials(io, self.nac)

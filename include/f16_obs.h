@@ -131,6 +131,8 @@ typedef struct F16EnvStepIO {
     const double *pool_prev_x;   /* (pool_size, 2) the re-anchored geometry advantage */
     const double *pool_prev_alt_log;  /* (pool_size, 2) the re-anchored log altitude */
     const double *pool_aux;      /* (pool_size, 21) plane 0's aux features (used when rec->aux) */
+    float *reward0_f32;          /* (nenv) the float32 reward of each engagement's first aircraft
+                                    (aircraft 2e), or NULL: a learner-side rollout buffer row */
 } F16EnvStepIO;
 
 /* GpuDogfightVecEnv.step after the physics launch (research/competition_36500/runtime/

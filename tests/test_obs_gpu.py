@@ -525,7 +525,7 @@ def test_env_step_one_launch_equals_two(gpu, obs_dim, nenv, fcs):
     action tensor (the launch copies it into sim.actions) and a non-contiguous one (copied
     before the launch), NaN planted in a state and a pick outside the pool; then rollout steps
     (step_rollout) with a device step counter and, where fusable, the RunningNorm partial sums
-    merged into the statistics."""
+    merged into the statistics, and plane 0's float32 rewards written alone (reward0_f32)."""
     E = import_pkg("rl_env").GpuDogfightVecEnv
     P = import_pkg("policy")
     envs = [E(nenv, seed=11, ic_pool_size=64, obs_dim=obs_dim, max_engage_time_s=1.2,
@@ -575,6 +575,7 @@ def test_env_step_one_launch_equals_two(gpu, obs_dim, nenv, fcs):
     bufs = [{"rew": torch.zeros(nac, dtype=torch.float32, device=gpu),
              "dn": torch.zeros(nenv, dtype=torch.float32, device=gpu),
              "facc": torch.ones(nenv, dtype=torch.uint8, device=gpu)} for _ in envs]
+    rew0 = torch.full((nenv,), -5.0, dtype=torch.float32, device=gpu)
     fusable = envs[0].norm_fusable()
     assert fusable == (nenv <= 16384)
     for t in range(3):
@@ -583,10 +584,12 @@ def test_env_step_one_launch_equals_two(gpu, obs_dim, nenv, fcs):
         for env, norm, base, b in zip(envs, norms, bases, bufs):
             env.sim.actions.copy_(act)
             obs.append(env.step_rollout(b["rew"], b["dn"], b["facc"], step_base=base, step=t,
-                                        norm=norm if fusable else None))
+                                        norm=norm if fusable else None,
+                                        reward0_f32=rew0 if env is envs[0] else None))
             if fusable:
                 norm.merge(nac)
         assert same(obs[0], obs[1]), t
+        assert same(rew0, bufs[1]["rew"][0::2]), t         # plane 0's rewards alone
         for key in bufs[0]:
             assert same(bufs[0][key], bufs[1][key]), (t, key)
         assert same(envs[0].sim._state_soa, envs[1].sim._state_soa), t
