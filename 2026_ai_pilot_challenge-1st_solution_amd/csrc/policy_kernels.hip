@@ -632,6 +632,64 @@ __global__ __launch_bounds__(kGroupThreads) void group_scatter_kernel(
   }
 }
 
+// Passes (B) and (C) in one launch for up to kBasedBlocks blocks: every block reads all blocks'
+// counts (a few KB) and forms its own output bases -- the same sums group_base_kernel forms --
+// before its scatter; block 0 also writes the group offsets.  One launch fewer per grouping.
+constexpr int kBasedBlocks = kGroupThreads;
+
+__global__ __launch_bounds__(kGroupThreads) void group_scatter_based_kernel(
+    const int* __restrict__ assign, int n, int ngroups, int stride, int offset,
+    const int* __restrict__ counts, int nblocks, int* __restrict__ rows,
+    int* __restrict__ offsets) {
+  __shared__ int cnt[F16_POLICY_MAX_GROUPS][kBasedBlocks];
+  __shared__ int before[F16_POLICY_MAX_GROUPS], total[F16_POLICY_MAX_GROUPS];
+  __shared__ int gbase[F16_POLICY_MAX_GROUPS];
+  __shared__ int wave_sum[kGroupWaves];
+  const int t = threadIdx.x;
+  if (t < nblocks) {
+#pragma unroll
+    for (int g = 0; g < F16_POLICY_MAX_GROUPS; ++g)
+      if (g < ngroups) cnt[g][t] = counts[t * F16_POLICY_MAX_GROUPS + g];
+  }
+  __syncthreads();
+  if (t < ngroups) {                                 // thread g: its group's sums over blocks
+    int bf = 0, tot = 0;
+    for (int b = 0; b < nblocks; ++b) {
+      const int v = cnt[t][b];
+      bf += b < (int)blockIdx.x ? v : 0;
+      tot += v;
+    }
+    before[t] = bf;
+    total[t] = tot;
+  }
+  __syncthreads();
+  if (t == 0) {                                       // groups in order
+    int off = 0;
+    for (int g = 0; g < ngroups; ++g) {
+      gbase[g] = off + before[g];
+      if (blockIdx.x == 0) offsets[g] = off;
+      off += total[g];
+    }
+    if (blockIdx.x == 0) offsets[ngroups] = off;
+  }
+  __syncthreads();
+  int c[F16_POLICY_MAX_GROUPS], j0, j1;
+  block_counts(assign, n, ngroups, blockIdx.x * kGroupItems, c, j0, j1);
+  int pos[F16_POLICY_MAX_GROUPS];
+#pragma unroll
+  for (int g = 0; g < F16_POLICY_MAX_GROUPS; ++g) {
+    if (g >= ngroups) { pos[g] = 0; continue; }    // uniform
+    int tot;
+    pos[g] = gbase[g] + block_exclusive_scan(c[g], wave_sum, tot);
+  }
+  for (int i = j0; i < j1; ++i) {
+    const int g = assign[i];
+#pragma unroll
+    for (int q = 0; q < F16_POLICY_MAX_GROUPS; ++q)
+      if (g == q && q < ngroups) rows[pos[q]++] = stride * i + offset;
+  }
+}
+
 }  // namespace f16pol
 
 using namespace f16pol;
@@ -651,6 +709,11 @@ extern "C" int f16_group_rows(const int* assign, int n, int ngroups, int stride,
   if (nb > 0)
     hipLaunchKernelGGL(group_count_kernel, dim3(nb), dim3(kGroupThreads), 0, s, assign, n,
                        ngroups, counts);
+  if (nb > 0 && nb <= kBasedBlocks) {               // up to 262,144 items: two launches
+    hipLaunchKernelGGL(group_scatter_based_kernel, dim3(nb), dim3(kGroupThreads), 0, s, assign,
+                       n, ngroups, stride, offset, counts, nb, rows, group_offsets);
+    return f16_last_error();
+  }
   hipLaunchKernelGGL(group_base_kernel, dim3(1), dim3(kGroupThreads), 0, s, counts, nb, ngroups,
                      group_offsets);
   if (nb > 0)
