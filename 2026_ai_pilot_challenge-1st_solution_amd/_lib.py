@@ -104,6 +104,7 @@ _SIGNATURES = {
     "f16_env_post_step": (_i, [ctypes.POINTER(F16EnvStepIO), _RP, _CP, _vp]),
     "f16_env_post_step_onewave": (_i, [ctypes.POINTER(F16EnvStepIO), _RP, _CP, _vp]),
     "f16_env_step": (_i, [ctypes.POINTER(F16EnvStepIO), _RP, _CP, _vp, _i, _i, _vp, _vp]),
+    "f16_env_step_tworole": (_i, [ctypes.POINTER(F16EnvStepIO), _RP, _CP, _vp, _i, _i, _vp, _vp]),
     "f16_env_post_step_norm_fusable": (_i, [_i, _i]),
     "f16_env_reseed": (_i, [ctypes.POINTER(F16EnvStepIO), _RP, _vp, _vp]),
     "f16_state9": (_i, [_vp, _l, _i, _vp, _vp]),

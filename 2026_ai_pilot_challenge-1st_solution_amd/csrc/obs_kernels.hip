@@ -19,6 +19,7 @@
 #include "f16_obs.h"
 #include "f16_state.h"
 #include "fdm_image.h"
+#include "fdm_quad.h"
 #include "fdm_split.h"
 #include "obs_device.h"
 #include "philox.h"
@@ -131,6 +132,24 @@ __device__ __forceinline__ void lane_init_reward(const Kin9& k, const Peer& p, c
   r.prev_alt_log[a] = altitude_log(-k.s9[2]);
 }
 
+// The decision's damage exchange, HP, fuel proxy and clock of this aircraft (lane_advance's
+// arithmetic, shared with the four-role step's scalar-block wave, which forms them from the
+// same loads instead of waiting for them).  Both lanes of a pair call it together (xch).
+struct HpFuel { double dealt, taken, hp, fuel, t; };
+__device__ __forceinline__ HpFuel advance_hp_fuel(const Kin9& k, const Geo& g, double hp_before,
+                                                  double fuel_before, double t_old) {
+  HpFuel o;
+  o.dealt = damage_rate(g.dist * kM2FtObs, g.ata, t_old);
+  o.taken = xch(o.dealt);
+  double hp = hp_before - o.taken * kDtStep;
+  o.hp = hp < 0.0 ? 0.0 : hp;
+  const double burn = kFuelBurn * (k.spd * (1.0 / kFuelRef));
+  double fuel = fuel_before - burn * kDtStep;
+  o.fuel = fuel < 0.0 ? 0.0 : fuel;
+  o.t = t_old + kDtStep;
+  return o;
+}
+
 struct AdvOut {
   double reward;
   bool term, trunc;
@@ -179,16 +198,11 @@ __device__ __forceinline__ AdvOut lane_advance(const Kin9& k, const Peer& p, con
 #pragma unroll
   for (int i = 0; i < 16; ++i) out.hist[4 + i] = obs_value(h[i]);
   // damage exchanged inside the cones, rated at the time entering the decision
-  const double dealt = damage_rate(g.dist * kM2FtObs, g.ata, t_old);
-  const double taken = xch(dealt);
-  double hp = hp_before - taken * kDtStep;
-  hp = hp < 0.0 ? 0.0 : hp;
+  const HpFuel hf = advance_hp_fuel(k, g, hp_before, fuel_before, t_old);
+  const double dealt = hf.dealt, taken = hf.taken, hp = hf.hp, fuel = hf.fuel;
   const double hp_loss = hp_before - hp;
   r.hp_loss[a] = hp_loss;
   r.hp[a] = hp;
-  const double burn = kFuelBurn * (k.spd * (1.0 / kFuelRef));
-  double fuel = fuel_before - burn * kDtStep;
-  fuel = fuel < 0.0 ? 0.0 : fuel;
   r.fuel[a] = fuel;
   // body rates from the attitude change since the previous decision
   double pqr[3] = {0.0, 0.0, 0.0};
@@ -214,7 +228,7 @@ __device__ __forceinline__ AdvOut lane_advance(const Kin9& k, const Peer& p, con
   r.prev_valid[a] = 1;
   r.dealt[a] = dealt;
   r.taken[a] = taken;
-  const double t_new = t_old + kDtStep;
+  const double t_new = hf.t;
   if (!(a & 1)) r.t_sec[e] = t_new;
   // termination (rl_env.py:467-484): hard deck, HP, non-finite; truncation at the time limit
   const double alt_o = -k.s9[2], alt_t = -p.s9[2];
@@ -385,11 +399,13 @@ __device__ __forceinline__ void bank_of(const double R[3][3], const double F[3][
 // the scalar block [0, 50) with the action history.  All lanes of a pair call each part
 // together.  The scalar block needs the bank of the own and partner body y axes about their
 // motion frames; the vector block forms the own motion frame anyway and hands them over in
-// `bank` (bs, bc, tbs, tbc) when given one.
-template <int D, bool FULL>
+// `bank` (bs, bc, tbs, tbc) when given one.  The vector block emits frames [F0, F1) of the six
+// (all of them by default; the four-role step gives two waves three frames each).
+template <int D, bool FULL, int F0 = 0, int F1 = 6>
 __device__ __forceinline__ void obs_vector_block(const Kin9& k, const Peer& p, const Geo& g,
                                                  const ObsIn& own, const ObsOut& out,
                                                  double* bank) {
+  static_assert(0 <= F0 && F0 < F1 && F1 <= 6, "frames [F0, F1) of the six");
   constexpr int nvec = D == 214 ? 9 : 7;
   float* o1 = out.tile;
   double V[9][3];
@@ -407,26 +423,32 @@ __device__ __forceinline__ void obs_vector_block(const Kin9& k, const Peer& p, c
   mtv3(k.A.R, own.pqr, V[5]);                                      // own body rates in NED
 #pragma unroll
   for (int i = 0; i < 3; ++i) { V[6][i] = xch(V[5][i]); V[8][i] = xch(own.accel[i]); }
-  {
+  if constexpr (F0 <= 0 && 0 < F1) {
     const double I3[3][3] = {{1.0, 0.0, 0.0}, {0.0, 1.0, 0.0}, {0.0, 0.0, 1.0}};
     emit_frame<0, FULL>(o1, I3, V, nvec);
   }
-  emit_frame<1, FULL>(o1, k.A.R, V, nvec);
-  emit_frame<2, FULL>(o1, p.R, V, nvec);
-  double Fm[3][3];
-  dir_frame(k.vn, Fm);                                             // own motion frame
-  if (bank) {
-    bank_of(k.A.R, Fm, bank[0], bank[1]);
-    bank[2] = xch(bank[0]); bank[3] = xch(bank[1]);
+  if constexpr (F0 <= 1 && 1 < F1) emit_frame<1, FULL>(o1, k.A.R, V, nvec);
+  if constexpr (F0 <= 2 && 2 < F1) emit_frame<2, FULL>(o1, p.R, V, nvec);
+  if constexpr (F1 > 3) {
+    double Fm[3][3];
+    dir_frame(k.vn, Fm);                                           // own motion frame
+    if (bank) {
+      bank_of(k.A.R, Fm, bank[0], bank[1]);
+      bank[2] = xch(bank[0]); bank[3] = xch(bank[1]);
+    }
+    if constexpr (F0 <= 3) emit_frame<3, FULL>(o1, Fm, V, nvec);
+    if constexpr (F0 <= 4 && 4 < F1) {
+#pragma unroll
+      for (int i = 0; i < 3; ++i)
+#pragma unroll
+        for (int q = 0; q < 3; ++q) Fm[i][q] = xch(Fm[i][q]);       // partner's motion frame
+      emit_frame<4, FULL>(o1, Fm, V, nvec);
+    }
+    if constexpr (F1 > 5) {
+      dir_frame(g.delta, Fm);                                      // line-of-sight frame
+      emit_frame<5, FULL>(o1, Fm, V, nvec);
+    }
   }
-  emit_frame<3, FULL>(o1, Fm, V, nvec);
-#pragma unroll
-  for (int i = 0; i < 3; ++i)
-#pragma unroll
-    for (int q = 0; q < 3; ++q) Fm[i][q] = xch(Fm[i][q]);             // partner's motion frame
-  emit_frame<4, FULL>(o1, Fm, V, nvec);
-  dir_frame(g.delta, Fm);                                          // line-of-sight frame
-  emit_frame<5, FULL>(o1, Fm, V, nvec);
 }
 
 // hist: 0 = read the action history from the reconstructor, 1 = already stored (by
@@ -1002,12 +1024,12 @@ __global__ __launch_bounds__(kRowBlock) void env_post_step_kernel(const F16EnvSt
 // four 32-row phases each summed row by row in fp64 (rows past the batch add 0), the phases
 // then added in order; block 0 also snapshots and advances the running count.  The results
 // equal a norm_partial_kernel launch over the same rows bit for bit.
-template <int D>
+template <int D, int NT = kPostSplitBlock>
 __device__ __forceinline__ void norm_partials_from_tiles(const float* S_all, double* sh,
                                                          long a_blk, long nac, long b,
                                                          const F16EnvStepIO& io, int tid) {
   constexpr int P = tile_pitch<D, true>(), kTile = kRowBlock * P;
-  for (int idx = tid; idx < 4 * D; idx += kPostSplitBlock) {
+  for (int idx = tid; idx < 4 * D; idx += NT) {
     const int ph = idx / D, c = idx - ph * D;
     const float* src = S_all + (ph >> 1) * kTile + ((ph & 1) * 32) * P + c;
     const long r0 = a_blk + ph * 32;
@@ -1021,7 +1043,7 @@ __device__ __forceinline__ void norm_partials_from_tiles(const float* S_all, dou
     sh[(ph * 2 + 1) * D + c] = sq;
   }
   __syncthreads();
-  for (int c = tid; c < D; c += kPostSplitBlock) {
+  for (int c = tid; c < D; c += NT) {
     double sum = sh[c], sq = sh[D + c];
 #pragma unroll
     for (int ph = 1; ph < 4; ++ph) { sum += sh[(ph * 2) * D + c]; sq += sh[(ph * 2 + 1) * D + c]; }
@@ -1255,6 +1277,207 @@ __global__ __launch_bounds__(kPostSplitBlock) void env_post_step_split_kernel(
   post_split_body<D, FULL>(io, r, c, O, L);
 }
 
+// The post-physics step of post_split_body (full-row tile) with each group of 64 aircraft on
+// four wavefronts instead of two, for the 512-thread one-launch step: role 0 advances (finite
+// flag, reward, termination, reconstructor update, action history, aux features), role 1 builds
+// the scalar block, roles 2 and 3 the vector block's frames 0-2 and 3-5.  Every role forms the
+// kinematics and pair geometry itself; role 1 forms the decision's HP, fuel proxy, damage and
+// clock from the same loads with lane_advance's own arithmetic (advance_hp_fuel), and roles 1-3
+// read what they need of the reconstructor before the first barrier, after which role 0
+// overwrites it.  Groups map roles to waves in opposite orders (a SIMD holds waves w and w + 4),
+// so each SIMD pairs the advance role with a vector role and the scalar role with the other.
+// Every barrier is at the top level, met by all 512 threads.  Results equal post_split_body's
+// bit for bit.
+constexpr int kQuadPostBlock = 4 * kRowBlock * kPostGroups;   // 512
+
+template <int D>
+__device__ __forceinline__ void post_quad_body(const F16EnvStepIO& io, const F16Recon& r,
+                                               const F16RewardCfg& c, const Origin& O,
+                                               PostSplitLds<D, true>& L) {
+  auto& S_all = L.S_all;
+  auto& sh_mask = L.sh_mask;
+  auto& sh_pick = L.sh_pick;
+  auto& sh_norm = L.sh_norm;
+  constexpr int NTG = 4 * kRowBlock;                    // threads per group
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int grp = wave >> 2;
+  const int role = grp == 0 ? (wave & 3) : 3 - (wave & 3);
+  const int gtid = (int)(threadIdx.x & (NTG - 1));
+  float* const S = S_all[grp];
+  const long a0 = ((long)blockIdx.x * kPostGroups + grp) * kRowBlock, a = a0 + lane;
+  const long nac = 2L * r.nenv;
+  const int n = (int)max(0L, min((long)kRowBlock, nac - a0));
+  const bool on = a < nac;                              // nac is even: pairs agree
+  const long e = a >> 1;
+  const int odd = (int)(a & 1);
+  const double* __restrict__ st = io.states;
+  const long ld = io.ld;
+  constexpr int kHistCol = vec_base(D == 214 ? 9 : 7);
+  float* tile = S + lane * tile_pitch<D, true>();
+  float* const first_out = io.terminal_obs ? io.terminal_obs : io.obs;
+  Kin9 k;
+  Peer p;
+  Geo g;
+  double f15[15];
+  // ---- reads every role needs before role 0 rewrites the reconstructor
+  bool prev_valid = false;
+  double patt[3] = {0.0, 0.0, 0.0}, pvel[3] = {0.0, 0.0, 0.0};
+  double hp_before = 0.0, fuel_before = 0.0, t_old = 0.0;
+  bool d = false;
+  int fin = 1;
+  const bool want_fin = role == 0 && on && (io.terminal_finite || io.finite_acc);
+  if (on) {
+#pragma unroll
+    for (int f = 0; f < 15; ++f) f15[f] = st[f * ld + a];
+    if (role == 0) {
+      if (want_fin && io.state_finite) fin = io.state_finite[a] ? 1 : 0;
+    } else {
+      prev_valid = r.prev_valid[a] != 0;
+#pragma unroll
+      for (int i = 0; i < 3; ++i) patt[i] = r.prev_att[i * r.ld + a];
+      if (role == 1) {
+        hp_before = r.hp[a];
+        fuel_before = r.fuel[a];
+        t_old = r.t_sec[e];
+      } else if (r.accel) {
+#pragma unroll
+        for (int i = 0; i < 3; ++i) pvel[i] = r.prev_vel_ned[i * r.ld + a];
+      }
+    }
+  }
+  __syncthreads();   // roles 1-3 have read the previous reconstructor values
+  if (role == 0) {
+    if (want_fin) {                                 // rl_env.py:545: every state value finite
+      if (!io.state_finite) {
+#pragma unroll
+        for (int f = 0; f < 15; ++f) fin &= isfinite(f15[f]) ? 1 : 0;
+        double v[F16S_N - 15];
+#pragma unroll
+        for (int j = 0; j < F16S_N - 15; ++j) v[j] = st[(15 + j) * ld + a];
+#pragma unroll
+        for (int j = 0; j < F16S_N - 15; ++j) fin &= isfinite(v[j]) ? 1 : 0;
+      }
+      fin &= xchi(fin);
+      if (!odd) {
+        if (io.terminal_finite) io.terminal_finite[e] = (unsigned char)fin;
+        if (io.finite_acc && !fin) io.finite_acc[e] = 0;
+      }
+    }
+  }
+  if (on) {
+    make_kin(f15, 1, O, k);
+    exchange(k, p);
+    pair_geo(k, p, g);
+  }
+  if (role == 0) {
+    if (on) {
+      const AdvOut o = lane_advance(k, p, g, a, e, io.actions, r, c, f15[F16S_FUEL]);
+      if (io.reward) io.reward[a] = o.reward;
+      if (io.reward_f32) io.reward_f32[a] = (float)o.reward;
+      d = o.term || o.trunc;
+      if (!odd) {
+        if (io.reward0_f32) io.reward0_f32[e] = (float)o.reward;
+        if (io.term) io.term[e] = o.term;
+        if (io.trunc) io.trunc[e] = o.trunc;
+        if (io.done) io.done[e] = d;
+        if (io.done_f32) io.done_f32[e] = d ? 1.0f : 0.0f;
+      }
+      if (io.terminal_hp) io.terminal_hp[a] = o.obs.hp;
+      if (io.terminal_alt_m) {
+        const double x = f15[0], y = f15[1], z = f15[2];
+        io.terminal_alt_m[a] = (fm_sqrt(x * x + y * y + z * z) - kSeaLevelRadiusFtT) * kFt2M;
+      }
+      const ObsOut out{tile, first_out + a * D, (io.terminal_obs && !d) ? io.obs + a * D : nullptr};
+      store_run2<D, true, kHistCol, kActHist>(out, o.hist);
+      if (!d) store_aux(k, p, r, a);
+    }
+    const uint64_t live = __ballot(on && !d), fresh = __ballot(on && d);
+    if (lane == 0) { sh_mask[grp][0] = live; sh_mask[grp][1] = fresh; }
+  } else if (on) {
+    ObsIn own = fresh_obs_in();
+    if (role == 1) {                                // what lane_advance forms, formed again
+      const HpFuel hf = advance_hp_fuel(k, g, hp_before, fuel_before, t_old);
+      own.hp = hf.hp; own.fuel = hf.fuel; own.dealt = hf.dealt; own.taken = hf.taken;
+      own.t = hf.t;
+      obs_scalar_block<D, true>(k, p, g, own, a, r, ObsOut{tile, nullptr, nullptr}, 1, nullptr);
+    } else {
+      if (prev_valid) {                             // lane_advance's body rates and acceleration
+        Att P;
+        attitude_rpy(patt[0], patt[1], patt[2], P);
+        so3_rates(P.R, k.A.R, own.pqr);
+      }
+      if (r.accel) {
+#pragma unroll
+        for (int i = 0; i < 3; ++i)
+          if (prev_valid) own.accel[i] = (k.vn[i] - pvel[i]) * (1.0 / kDtStep);
+      }
+      if (role == 2)
+        obs_vector_block<D, true, 0, 3>(k, p, g, own, ObsOut{tile, nullptr, nullptr}, nullptr);
+      else
+        obs_vector_block<D, true, 3, 6>(k, p, g, own, ObsOut{tile, nullptr, nullptr}, nullptr);
+    }
+  }
+  __syncthreads();   // the tile holds every row; the masks are published
+  const uint64_t rows = __ballot(on), live = sh_mask[grp][0], fresh = sh_mask[grp][1];
+  if (io.terminal_obs)
+    flush_tile<D, true, NTG>(S, a0, n, rows, io.terminal_obs, live, io.obs, gtid);
+  else
+    flush_tile<D, true, NTG>(S, a0, n, live, io.obs, 0, nullptr, gtid);
+  bool any_fresh = false;   // uniform over the workgroup, so every thread meets the same barriers
+#pragma unroll
+  for (int q = 0; q < kPostGroups; ++q) any_fresh |= sh_mask[q][1] != 0;
+  if (!any_fresh) {
+    if (io.norm_partial)
+      norm_partials_from_tiles<D, kQuadPostBlock>(&S_all[0][0], sh_norm,
+                                                  (long)blockIdx.x * 2 * kRowBlock, nac,
+                                                  blockIdx.x, io, threadIdx.x);
+    return;
+  }
+  __syncthreads();
+  // Rows of finished engagements: as post_split_body, the scalar block of a rebuilt row on
+  // role 1 and its vector block on roles 2 and 3, each from the pool row's kinematics.
+  const uint32_t step = io.step + (io.step_base ? *io.step_base : 0u);
+  const bool mine = (fresh >> lane) & 1;
+  const long pk = mine && io.pool_obs ? pool_pick(io, e, step) : -1;
+  const bool cached = pk >= 0;
+  const uint64_t from_table = __ballot(cached);    // the same in every role
+  if (mine && cached && role == 0) {
+    lane_autoreset_cached(io, r, a, e, odd, step, pk);
+    sh_pick[grp][lane] = pk * 2 + odd;
+  }
+  if (mine && !cached) {
+    Kin9 k2;
+    Peer p2;
+    Geo g2;
+    if (role == 0) {
+      lane_autoreset(io, r, O, a, e, odd, step, k2, p2, g2);
+      store_aux(k2, p2, r, a);
+    } else {
+      pool_kin(io, O, pool_pick(io, e, step), odd, k2);
+      exchange(k2, p2);
+      pair_geo(k2, p2, g2);
+      const ObsOut out{tile, nullptr, nullptr};
+      if (role == 1)
+        obs_scalar_block<D, true>(k2, p2, g2, fresh_obs_in(), a, r, out, 2, nullptr);
+      else if (role == 2)
+        obs_vector_block<D, true, 0, 3>(k2, p2, g2, fresh_obs_in(), out, nullptr);
+      else
+        obs_vector_block<D, true, 3, 6>(k2, p2, g2, fresh_obs_in(), out, nullptr);
+    }
+  }
+  __syncthreads();
+  flush_sparse<D, true, NTG>(S, a0, fresh & ~from_table, io.obs, gtid);
+  if (from_table)
+    copy_pool_rows<D, true, NTG>(S, a0, from_table, sh_pick[grp], io, io.pool_obs, io.obs, gtid);
+  if (io.norm_partial) {
+    __syncthreads();     // (workgroup-uniform) the copied rows have landed in the tiles
+    norm_partials_from_tiles<D, kQuadPostBlock>(&S_all[0][0], sh_norm,
+                                                (long)blockIdx.x * 2 * kRowBlock, nac,
+                                                blockIdx.x, io, threadIdx.x);
+  }
+}
+
 // A whole environment step in one launch, for batches whose rows fit the full-row tile: the
 // workgroup first runs the FDM substeps of its 128 aircraft as fdm_step_split_kernel does (two
 // wavefronts per 64 aircraft, model image and exchange fields in LDS), then, after a workgroup
@@ -1301,6 +1524,51 @@ __global__ __launch_bounds__(kPostSplitBlock) void env_step_fused_kernel(
                                  act_keep ? act_keep + 4L * ia : nullptr);
   __syncthreads();   // the new states, finite flags and actions are written; LDS is free
   post_split_body<D, true>(io, r, c, O, L.post);
+}
+
+// The same step on 512-thread workgroups: each 64 aircraft on four wavefronts in both phases
+// (fdm_quad.h's four physics roles, then post_quad_body's four post-physics roles), so that at
+// 16,384 engagements every SIMD holds two wavefronts instead of one.  Results equal
+// env_step_fused_kernel's bit for bit.
+template <int D>
+union EnvQuadLds {
+  struct {
+    double T[F16M_IMAGE_LEN];
+    f16::QuadX X[f16::kQuadGroups];
+  } fdm;
+  PostSplitLds<D, true> post;
+};
+static_assert(f16::kQuadBlock == kQuadPostBlock && f16::kQuadAircraft == kPostGroups * kRowBlock,
+              "the four-role physics groups and post-physics groups must cover the same aircraft");
+
+template <int FCS_RATE, int D>
+__global__ __launch_bounds__(kQuadPostBlock) void env_step_quad_kernel(
+    const double* __restrict__ act, int S, double* __restrict__ act_keep,
+    unsigned char* __restrict__ state_finite, const F16EnvStepIO io, F16Recon r, F16RewardCfg c,
+    Origin O) {
+  __shared__ EnvQuadLds<D> L;
+  f16::stage_image<kQuadPostBlock>(L.fdm.T);
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int grp = wave >> 2;
+  const int role = f16::quad_role(grp, wave & 3);
+  const int nac = 2 * r.nenv;
+  const int i = blockIdx.x * f16::kQuadAircraft + grp * 64 + lane;
+  const bool store = i < nac;
+  const int ia = store ? i : nac - 1;   // lanes past the batch shadow the last aircraft
+  double* const st = io.states + ia;
+  if (role == f16::kRoleKin)
+    f16::quad_kin<FCS_RATE>(st, io.ld, S, store, nullptr, 0, L.fdm.T, L.fdm.X[grp], lane, true);
+  else if (role == f16::kRoleAero)
+    f16::quad_aero<FCS_RATE>(S, L.fdm.T, L.fdm.X[grp], lane, true);
+  else if (role == f16::kRoleFcs)
+    f16::quad_fcs<FCS_RATE>(st, io.ld, act + 4L * ia, S, store, L.fdm.T, L.fdm.X[grp], lane, true,
+                            act_keep ? act_keep + 4L * ia : nullptr);
+  else
+    f16::quad_air<FCS_RATE>(st, io.ld, act + 4L * ia, S, store, L.fdm.T, L.fdm.X[grp], lane,
+                            state_finite + ia);
+  __syncthreads();   // the new states, finite flags and actions are written; LDS is free
+  post_quad_body<D>(io, r, c, O, L.post);
 }
 
 // Masked autoreset without a step: engagements with mask[e] != 0 get an initial-condition pool
@@ -1516,9 +1784,9 @@ extern "C" int f16_env_post_step(const F16EnvStepIO* io, const F16Recon* rec,
   return post_step(io, rec, cfg, stream, true);
 }
 
-extern "C" int f16_env_step(const F16EnvStepIO* io, const F16Recon* rec, const F16RewardCfg* cfg,
-                            const double* actions, int substeps, int fcs_rate,
-                            unsigned char* state_finite, void* stream) {
+static int env_step(const F16EnvStepIO* io, const F16Recon* rec, const F16RewardCfg* cfg,
+                    const double* actions, int substeps, int fcs_rate, unsigned char* state_finite,
+                    void* stream, bool quad) {
   if (!io || !state_finite || substeps < 1) return F16_EINVAL;
   if (fcs_rate != 120 && fcs_rate != 60) return F16_ERATE;
   F16EnvStepIO x = *io;
@@ -1545,9 +1813,16 @@ extern "C" int f16_env_step(const F16EnvStepIO* io, const F16Recon* rec, const F
   }
   hipStream_t s = (hipStream_t)stream;
 #define F16_ENV_STEP(R, D)                                                                      \
-  hipLaunchKernelGGL((env_step_fused_kernel<R, D>), grid_groups(rec->nenv),                      \
-                     dim3(kPostSplitBlock), 0, s, act, substeps, keep, state_finite, x, *rec,    \
-                     *cfg, origin())
+  do {                                                                                          \
+    if (quad)                                                                                   \
+      hipLaunchKernelGGL((env_step_quad_kernel<R, D>), grid_groups(rec->nenv),                  \
+                         dim3(kQuadPostBlock), 0, s, act, substeps, keep, state_finite, x, *rec,\
+                         *cfg, origin());                                                       \
+    else                                                                                        \
+      hipLaunchKernelGGL((env_step_fused_kernel<R, D>), grid_groups(rec->nenv),                 \
+                         dim3(kPostSplitBlock), 0, s, act, substeps, keep, state_finite, x,     \
+                         *rec, *cfg, origin());                                                 \
+  } while (0)
   if (fcs_rate == 120) {
     if (x.obs_dim == 184) F16_ENV_STEP(120, 184); else F16_ENV_STEP(120, 214);
   } else {
@@ -1555,6 +1830,18 @@ extern "C" int f16_env_step(const F16EnvStepIO* io, const F16Recon* rec, const F
   }
 #undef F16_ENV_STEP
   return f16_last_error();
+}
+
+extern "C" int f16_env_step(const F16EnvStepIO* io, const F16Recon* rec, const F16RewardCfg* cfg,
+                            const double* actions, int substeps, int fcs_rate,
+                            unsigned char* state_finite, void* stream) {
+  return env_step(io, rec, cfg, actions, substeps, fcs_rate, state_finite, stream, true);
+}
+
+extern "C" int f16_env_step_tworole(const F16EnvStepIO* io, const F16Recon* rec,
+                                    const F16RewardCfg* cfg, const double* actions, int substeps,
+                                    int fcs_rate, unsigned char* state_finite, void* stream) {
+  return env_step(io, rec, cfg, actions, substeps, fcs_rate, state_finite, stream, false);
 }
 
 extern "C" int f16_env_post_step_norm_fusable(int nenv, int obs_dim) {

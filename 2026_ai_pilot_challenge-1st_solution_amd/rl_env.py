@@ -84,6 +84,9 @@ class GpuDogfightVecEnv:
         # physics and post-physics in one launch (f16_env_step) where the finite flags are on;
         # fused_step=False issues sim.step and f16_env_post_step as two launches
         self.fused_step = True
+        # wavefronts per 64 aircraft in the one-launch step: 4 (f16_env_step) or 2
+        # (f16_env_step_tworole); the same results
+        self.step_roles = 4
         # per pool row, what an autoreset from it produces (observation, reward anchors, aux
         # features), so the post-physics launch copies instead of rebuilding; pool_tables=False
         # makes it rebuild them
@@ -319,10 +322,11 @@ class GpuDogfightVecEnv:
         if ev is not None:
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record()
-        rc = self.obr._lib.f16_env_step(_lib.ctypes.byref(io), _lib.ctypes.byref(self._rec),
-                                        _lib.ctypes.byref(c), a.data_ptr(), self.substeps,
-                                        self.sim.fcs_rate, state_fin.data_ptr(),
-                                        _lib.stream_handle(self.device))
+        fn = (self.obr._lib.f16_env_step_tworole if self.step_roles == 2 else
+              self.obr._lib.f16_env_step)
+        rc = fn(_lib.ctypes.byref(io), _lib.ctypes.byref(self._rec), _lib.ctypes.byref(c),
+                a.data_ptr(), self.substeps, self.sim.fcs_rate, state_fin.data_ptr(),
+                _lib.stream_handle(self.device))
         if ev is not None:
             e1.record()
             ev.append((e0, e1))

@@ -238,12 +238,14 @@ def _env_timed(env, acts, warmup, steps):
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     dones = []
     e0.record()
+    t0 = time.perf_counter()
     for k in range(steps):
         _, _, done, _ = env.step(acts[warmup + k])
         dones.append(done)
+    host = (time.perf_counter() - t0) * 1e3 / steps     # issue time of one step on the host
     e1.record()
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / steps, int(torch.stack(dones).sum().item())
+    return e0.elapsed_time(e1) / steps, int(torch.stack(dones).sum().item()), host
 
 
 def _env_kernel_ms(env, acts, warmup, n):
@@ -303,15 +305,16 @@ def env_step_bench(pkg, nenv, steps, warmup, scan_finite=False, ab=True, stagger
         env.fused_step, env.fused_finite = ENV_VARIANTS[name]
         env.sim.states.copy_(snap_states)        # every variant steps the same engagements
         env.obr.restore(snap_obr)
-        ms, done = _env_timed(env, acts, warmup, steps)
+        ms, done, host = _env_timed(env, acts, warmup, steps)
         runs.setdefault(name, []).append((ms, done) + _env_kernel_ms(env, acts, warmup,
-                                                                       min(steps, 20)))
+                                                                       min(steps, 20)) + (host,))
     env.fused_step, env.fused_finite = ENV_VARIANTS["one_launch"]
     res = {}
     for name, r in runs.items():
         avg = lambda i: None if r[0][i] is None else float(np.mean([x[i] for x in r]))
-        ms, done, fdm_ms, post_ms, step_ms = (avg(i) for i in range(5))
-        res[name] = {"ms_per_step": ms, "episodes_done": int(round(done))}
+        ms, done, fdm_ms, post_ms, step_ms, host = (avg(i) for i in range(6))
+        res[name] = {"ms_per_step": ms, "episodes_done": int(round(done)),
+                     "host_issue_ms_per_step": host}
         if step_ms is not None:
             res[name]["step_kernel_ms"] = step_ms
         else:
@@ -328,9 +331,10 @@ def env_step_bench(pkg, nenv, steps, warmup, scan_finite=False, ab=True, stagger
            "pool_tables": pool_tables, "variant": main_name,
            "transitions_per_s": nenv / (main["ms_per_step"] * 1e-3),
            "ms_per_step": main["ms_per_step"], "episodes_done": main["episodes_done"],
+           "host_issue_ms_per_step": main["host_issue_ms_per_step"],
            "vs_published": nenv / (main["ms_per_step"] * 1e-3) / REF_PUBLISHED_ENV_TRANSITIONS}
     if "step_kernel_ms" in main:
-        out["step_kernel"] = {"kernel": "env_step_fused_kernel<60,184>",
+        out["step_kernel"] = {"kernel": "env_step_quad_kernel<60,184>",
                               "kernel_ms": main["step_kernel_ms"]}
     two = res.get("two_launch", res.get("state_scan"))
     if two is not None:

@@ -150,13 +150,21 @@ typedef struct F16EnvStepIO {
  * f16_env_post_step of `io`, with `state_finite` ((nac) bytes, required) carrying the physics'
  * per-aircraft finite flags to the post-physics step (io->state_finite is ignored).  Where every
  * workgroup of the post-physics step's full-row tile is resident at once (as
- * f16_env_post_step_norm_fusable reports), one launch does both, each workgroup running the
- * physics of its 128 aircraft and then their post-physics step; otherwise the two launches are
- * issued.  Results equal the two entry points' bit for bit.  Every argument is checked before
+ * f16_env_post_step_norm_fusable reports), one launch does both: each 512-thread workgroup runs
+ * the physics of its 128 aircraft on four wavefronts per 64 aircraft, then their post-physics
+ * step, again on four (two wavefronts per SIMD at 16,384 engagements); otherwise the two launches
+ * are issued.  Results equal the two entry points' bit for bit.  Every argument is checked before
  * anything is launched. */
 int f16_env_step(const F16EnvStepIO *io, const F16Recon *rec, const F16RewardCfg *cfg,
                  const double *actions, int substeps, int fcs_rate, unsigned char *state_finite,
                  void *stream);
+
+/* The same step with two wavefronts per 64 aircraft in each phase (256-thread workgroups, one
+ * wavefront per SIMD at 16,384 engagements); same arguments, same results bit for bit.  Kept as
+ * the cross-check of f16_env_step's four-wavefront kernel. */
+int f16_env_step_tworole(const F16EnvStepIO *io, const F16Recon *rec, const F16RewardCfg *cfg,
+                         const double *actions, int substeps, int fcs_rate,
+                         unsigned char *state_finite, void *stream);
 
 /* The autoreset half of f16_env_post_step alone, for the engagements with mask[e] != 0
  * ((nenv) bytes): pool row (io->pick or the Philox draw at io->step), reconstructor reset,

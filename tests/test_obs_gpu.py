@@ -514,12 +514,15 @@ def test_env_step_pool_tables_equal_rebuild(gpu, obs_dim, nenv):
     assert envs[0]._pool_key is not None and envs[1]._pool_key is None
 
 
-@pytest.mark.parametrize("obs_dim,nenv,fcs", [(184, 300, 60), (214, 300, 120), (184, 16384, 60),
-                                              (214, 16384, 120), (184, 20000, 60)])
-def test_env_step_one_launch_equals_two(gpu, obs_dim, nenv, fcs):
+@pytest.mark.parametrize("obs_dim,nenv,fcs,roles", [
+    (184, 300, 60, 2), (214, 300, 120, 2), (184, 16384, 60, 2), (214, 16384, 120, 2),
+    (184, 20000, 60, 2), (184, 300, 60, 4), (214, 300, 120, 4), (184, 16384, 60, 4),
+    (214, 16384, 120, 4)])
+def test_env_step_one_launch_equals_two(gpu, obs_dim, nenv, fcs, roles):
     """f16_env_step (physics and post-physics step in one launch wherever the full-row tile is
     resident: 300 engagements, whose last workgroup is partly filled, and 16,384; at 20,000 the
-    entry issues the two launches itself) against sim.step + f16_env_post_step: every output,
+    entry issues the two launches itself), and f16_env_step_quad (roles=4: four wavefronts per
+    64 aircraft in both phases), against sim.step + f16_env_post_step: every output,
     the states, the kept actions, the reconstructor and the aux features bit for bit over steps
     with autoresets (staggered 1.2 s engagements), terminal observations on and off, a separate
     action tensor (the launch copies it into sim.actions) and a non-contiguous one (copied
@@ -531,6 +534,7 @@ def test_env_step_one_launch_equals_two(gpu, obs_dim, nenv, fcs):
     envs = [E(nenv, seed=11, ic_pool_size=64, obs_dim=obs_dim, max_engage_time_s=1.2,
               fcs_rate=fcs) for _ in range(2)]
     envs[1].fused_step = False
+    envs[0].step_roles = roles
     for env in envs:
         env.enable_aux_capture()
         env.reset(stagger=True, max_stagger_steps=12)
@@ -748,6 +752,48 @@ def test_staggered_warmup_is_device_resident(gpu):
     assert np.isfinite(s9).all() and (-s9[:, :, 2] > 100.0).all()
     obs = env._build_obs_all()
     assert torch.isfinite(obs).all()
+
+
+def test_env_step_argument_errors_launch_nothing(gpu):
+    """f16_env_step rejects a bad call before launching anything: no substeps, an FCS rate other
+    than 60/120, no finite-flag buffer, controls overlapping io.actions, RunningNorm partials past
+    the resident full-row tile (the two-launch case) -- the states and observations stay as they
+    were."""
+    E = import_pkg("rl_env").GpuDogfightVecEnv
+    L = import_pkg("_lib")
+    env = E(20000, seed=2, ic_pool_size=16)
+    env.reset(stagger=False)
+    env._ensure_ic_pool()
+    lib = L.lib()
+    st0, obs0 = env.sim._state_soa.clone(), env._obs.clone()
+    fin = torch.zeros(env.nac, dtype=torch.uint8, device=gpu)
+    act = torch.zeros(env.nac, 4, dtype=torch.float64, device=gpu)
+    work = torch.zeros(1 << 20, dtype=torch.float64, device=gpu)
+    cnt = torch.zeros(2, dtype=torch.float32, device=gpu)
+    c = env._cfg_struct()
+
+    def call(actions_ptr, substeps, rate, fin_ptr, norm=False):
+        io = env._io(None)
+        if norm:
+            io.norm_partial, io.norm_count = work.data_ptr(), cnt.data_ptr()
+            io.norm_count_snap = cnt.data_ptr() + 4
+        return lib.f16_env_step(L.ctypes.byref(io), L.ctypes.byref(env._rec), L.ctypes.byref(c),
+                                actions_ptr, substeps, rate, fin_ptr, L.stream_handle(gpu))
+
+    EINVAL, ERATE = -1, -2
+    assert call(act.data_ptr(), 0, 60, fin.data_ptr()) == EINVAL
+    assert call(act.data_ptr(), 6, 90, fin.data_ptr()) == ERATE
+    assert call(act.data_ptr(), 6, 60, None) == EINVAL
+    overlap = env.sim.actions.data_ptr() + 8 * 4 * 3           # 3 rows into io.actions
+    assert call(overlap, 6, 60, fin.data_ptr()) == EINVAL
+    assert not env.norm_fusable()
+    assert call(act.data_ptr(), 6, 60, fin.data_ptr(), norm=True) == EINVAL
+    torch.cuda.synchronize()
+    assert torch.equal(env.sim._state_soa, st0) and torch.equal(env._obs, obs0)
+    assert call(act.data_ptr(), 6, 60, fin.data_ptr()) == 0    # the same call, valid
+    torch.cuda.synchronize()
+    assert not torch.equal(env.sim._state_soa, st0)
+    assert torch.equal(env.sim.actions, act)                  # the controls were kept
 
 
 def test_obs_argument_errors(gpu):
