@@ -93,6 +93,7 @@ _SIGNATURES = {
     "f16_fdm_step_batch_finite": (_i, [_vp, _l, _vp, _i, _i, _i, _vp, _l, _vp, _vp]),
     "f16_fdm_step_batch_keep": (_i, [_vp, _l, _vp, _vp, _i, _i, _i, _vp, _l, _vp, _vp]),
     "f16_fdm_step_batch_onelane": (_i, [_vp, _l, _vp, _i, _i, _i, _vp, _l, _vp]),
+    "f16_fdm_step_batch_split": (_i, [_vp, _l, _vp, _i, _i, _i, _vp, _l, _vp]),
     "f16_seed_batch": (_i, [_vp, _i, _i, _vp, _l, _vp, _vp]),
     "f16_fdm_kernel_info": (_i, [_i, ctypes.POINTER(_i)]),
     "f16_fdm_kernel_info_onelane": (_i, [_i, ctypes.POINTER(_i)]),

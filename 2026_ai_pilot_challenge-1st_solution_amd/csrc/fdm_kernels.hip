@@ -8,6 +8,7 @@
 
 #include "fdm_advance.h"
 #include "fdm_image.h"
+#include "fdm_quad.h"
 #include "fdm_split.h"
 #include "f16_capi_common.h"
 
@@ -54,6 +55,39 @@ __global__ __launch_bounds__(kSplitBlock) void fdm_step_split_kernel(
   else
     split_systems<FCS_RATE>(st + ia, ld, act + 4L * ia, S, store, T, X[pair], lane,
                             fin ? fin + ia : nullptr, act_keep ? act_keep + 4L * ia : nullptr);
+}
+
+// The four-role form (fdm_quad.h): each 64 aircraft on four wavefronts, two groups per
+// 512-thread workgroup, so 16,384 engagements put two wavefronts on every SIMD (at most 256
+// registers each) where the two-wave kernel has one.  The same results bit for bit.  OBS: the
+// 17-value output is written (launched with OBS = false only: the output's pointer arithmetic
+// pushes the integrator role past 256 registers).
+template <int FCS_RATE, bool OBS>
+__global__ __launch_bounds__(kQuadBlock) void fdm_step_quad_kernel(
+    double* __restrict__ st, long ld, const double* __restrict__ act, int nac, int S,
+    double* __restrict__ obs, long obs_ld, unsigned char* __restrict__ fin,
+    double* __restrict__ act_keep) {
+  __shared__ double T[F16M_IMAGE_LEN];
+  __shared__ QuadX X[kQuadGroups];
+  stage_image<kQuadBlock>(T);
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int grp = wave >> 2;
+  const int role = quad_role(grp, wave & 3);
+  const int i = blockIdx.x * kQuadAircraft + grp * 64 + lane;
+  const bool store = i < nac;
+  const int ia = store ? i : nac - 1;   // lanes past the batch shadow the last aircraft
+  if (role == kRoleKin)
+    quad_kin<FCS_RATE>(st + ia, ld, S, store, OBS ? obs + ia : nullptr, obs_ld, T, X[grp], lane,
+                       fin != nullptr);
+  else if (role == kRoleAero)
+    quad_aero<FCS_RATE>(S, T, X[grp], lane, fin != nullptr);
+  else if (role == kRoleFcs)
+    quad_fcs<FCS_RATE>(st + ia, ld, act + 4L * ia, S, store, T, X[grp], lane, fin != nullptr,
+                       act_keep ? act_keep + 4L * ia : nullptr);
+  else
+    quad_air<FCS_RATE>(st + ia, ld, act + 4L * ia, S, store, T, X[grp], lane,
+                       fin ? fin + ia : nullptr);
 }
 
 // ------------------------------------------------------------------ IC seeding
@@ -227,9 +261,23 @@ static int fdm_step_args(double* states, long ld, const double* actions, int nac
 
 static int fdm_step_split(double* states, long ld, const double* actions, int nac, int substeps,
                           int fcs_rate, double* obs, long obs_ld, unsigned char* fin,
-                          void* stream, double* keep = nullptr) {
-  const dim3 grid((nac + f16::kSplitAircraft - 1) / f16::kSplitAircraft), block(f16::kSplitBlock);
+                          void* stream, double* keep = nullptr, bool quad = true) {
   hipStream_t s = (hipStream_t)stream;
+  // The four-wave kernel where the 17-value output is off (16k tail-chase engagements: 33.0 vs
+  // 36.9 us; 64k: 134 vs 145 us); with the output its integrator role spills past 256
+  // registers and is no faster (38.0 vs 38.2 us; 153 vs 149 us at 64k), so the two-wave kernel
+  // writes it.
+  if (quad && !obs) {
+    const dim3 grid((nac + f16::kQuadAircraft - 1) / f16::kQuadAircraft), block(f16::kQuadBlock);
+    if (fcs_rate == 120)
+      hipLaunchKernelGGL((f16::fdm_step_quad_kernel<120, false>), grid, block, 0, s, states, ld,
+                         actions, nac, substeps, obs, obs_ld, fin, keep);
+    else
+      hipLaunchKernelGGL((f16::fdm_step_quad_kernel<60, false>), grid, block, 0, s, states, ld,
+                         actions, nac, substeps, obs, obs_ld, fin, keep);
+    return f16_last_error();
+  }
+  const dim3 grid((nac + f16::kSplitAircraft - 1) / f16::kSplitAircraft), block(f16::kSplitBlock);
   if (fcs_rate == 120)
     hipLaunchKernelGGL(f16::fdm_step_split_kernel<120>, grid, block, 0, s, states, ld, actions, nac, substeps, obs, obs_ld, fin, keep);
   else
@@ -269,6 +317,15 @@ extern "C" int f16_fdm_step_batch_keep(double* states, long ld, const double* ac
                         actions_keep);
 }
 
+extern "C" int f16_fdm_step_batch_split(double* states, long ld, const double* actions, int nac,
+                                        int substeps, int fcs_rate, double* obs, long obs_ld,
+                                        void* stream) {
+  const int rc = fdm_step_args(states, ld, actions, nac, substeps, fcs_rate, obs, obs_ld);
+  if (rc) return rc < 0 ? rc : 0;
+  return fdm_step_split(states, ld, actions, nac, substeps, fcs_rate, obs, obs_ld, nullptr, stream,
+                        nullptr, false);
+}
+
 extern "C" int f16_fdm_step_batch_onelane(double* states, long ld, const double* actions,
                                           int nac, int substeps, int fcs_rate, double* obs,
                                           long obs_ld, void* stream) {
@@ -299,8 +356,8 @@ extern "C" int f16_seed_batch(const double* ic, int n, int fcs_rate, double* sta
 }
 
 // Register/LDS/scratch footprint of the step kernel that f16_fdm_step_batch launches (the
-// two-wave split kernel; the reference's profile_kernel.py reads the same attributes from the
-// CUDA driver).  out = {vgprs/regs per thread, lds bytes, scratch bytes, max threads per block}.
+// four-wave kernel without the 17-value output; the reference's profile_kernel.py reads the same
+// attributes from the CUDA driver).  out = {vgprs/regs per thread, lds bytes, scratch bytes, max threads per block}.
 static int kernel_info(const void* fn, int* out4) {
   if (!out4) return F16_EINVAL;
   hipFuncAttributes at;
@@ -315,8 +372,8 @@ static int kernel_info(const void* fn, int* out4) {
 
 extern "C" int f16_fdm_kernel_info(int fcs_rate, int* out4) {
   if (fcs_rate != 120 && fcs_rate != 60) return F16_ERATE;
-  return kernel_info(fcs_rate == 60 ? (const void*)f16::fdm_step_split_kernel<60>
-                                    : (const void*)f16::fdm_step_split_kernel<120>, out4);
+  return kernel_info(fcs_rate == 60 ? (const void*)f16::fdm_step_quad_kernel<60, false>
+                                    : (const void*)f16::fdm_step_quad_kernel<120, false>, out4);
 }
 
 // The same for the one-lane kernel behind f16_fdm_step_batch_onelane.

@@ -75,7 +75,7 @@ class GpuDogfight:
         return self.kernel_info(onelane=False)
 
     def kernel_info(self, onelane=False):
-        """Footprint of the split kernel (default) or of the one-lane kernel."""
+        """Footprint of the four-wave kernel `step` launches (default) or of the one-lane kernel."""
         out = (_lib.ctypes.c_int * 4)()
         fn = self._lib.f16_fdm_kernel_info_onelane if onelane else self._lib.f16_fdm_kernel_info
         _lib.check(fn(self.fcs_rate, out), "f16_fdm_kernel_info")

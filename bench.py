@@ -42,7 +42,7 @@ PEAK_HBM_GBS = 8000.0
 REF_PUBLISHED_SUBSTEPS = 37.0e6
 
 
-def profiled_traffic(name="fdm_step_split_kernel_tailchase16k.md"):
+def profiled_traffic(name="fdm_step_quad_kernel_tailchase16k.md"):
     """HBM bytes per launch measured by rocprofv3 FETCH_SIZE/WRITE_SIZE (copy-calibrated) and
     recorded in the kernel's profile summary; None when no summary is present."""
     path = os.path.join(ROOT, "profiles", name)
@@ -678,7 +678,7 @@ def main():
         "ppo_update": update_line,
         "roofline": {"bound": "valu", "achieved": achieved, "peak": PEAK_FP64_TFLOPS,
                      "unit": "TFLOP/s", "frac": achieved / PEAK_FP64_TFLOPS, "traffic": profiled_traffic(),
-                     "kernel": "fdm_step_split_kernel<120>", "kernel_ms": launch_ms,
+                     "kernel": "fdm_step_quad_kernel<120, false>", "kernel_ms": launch_ms,
                      "kernel_ms_source": "HIP events around the timed region / steps (one launch "
                                          "per step)",
                      "kernel_ms_per_launch_events": kern_ms,

@@ -72,11 +72,11 @@ def test_seed_rows_out_of_range(gpu):
 
 
 def test_kernel_info_reports_the_launched_kernel(gpu):
-    """kern describes the split kernel f16_fdm_step_batch launches; the one-lane kernel's
+    """kern describes the four-wave kernel f16_fdm_step_batch launches; the one-lane kernel's
     footprint is its own entry point; a NULL output is refused."""
     sim = _sim(2)
     split, one = sim.kern, sim.kernel_info(onelane=True)
-    assert split["max_threads"] >= 256 and split["scratch"] == 0
+    assert split["max_threads"] >= 512 and split["scratch"] == 0
     assert split != one
     L = import_pkg("_lib")
     assert L.lib().f16_fdm_kernel_info(120, None) == L.F16_EINVAL
@@ -258,10 +258,11 @@ def test_independence_and_determinism(gpu):
 @pytest.mark.parametrize("nenv,S,pad", [(4096, 6, 0), (77, 1, 0), (77, 2, 5), (1000, 3, 0),
                                         (1, 6, 3), (300, 0, 0)])
 def test_split_kernel_equals_onelane(gpu, rate, nenv, S, pad):
-    """The production step spreads each substep over two wavefronts that trade values through
-    LDS; the one-lane kernel runs the same component functions in sequence.  They agree bit for
-    bit on states and outputs, for ragged batch sizes (lanes past the batch), short substep
-    counts (history shifting), a leading dimension larger than the batch, and S = 0."""
+    """The production step spreads each substep over four wavefronts that trade values through
+    LDS, the two-wave kernel over two; the one-lane kernel runs the same component functions in
+    sequence.  All three agree bit for bit on states and outputs, for ragged batch sizes (lanes
+    past the batch), short substep counts (history shifting), a leading dimension larger than the
+    batch, and S = 0."""
     icm = import_pkg("ic")
     L = import_pkg("_lib")
     nac = 2 * nenv
@@ -269,21 +270,25 @@ def test_split_kernel_equals_onelane(gpu, rate, nenv, S, pad):
     sim = _sim(nenv, rate, max(S, 1))
     sim.seed_rows(torch.as_tensor(icm.sample_tailchase(nenv, seed=7), device=gpu))
     bufs = []
-    for _ in range(2):
+    for _ in range(4):
         st = torch.zeros(101, ld, dtype=torch.float64, device=gpu)
         st[:, :nac] = sim._state_soa
         bufs.append((st, torch.zeros(17, ld, dtype=torch.float64, device=gpu)))
     acts = icm.random_bin_actions(12, nac, seed=7)
-    fns = [L.lib().f16_fdm_step_batch, L.lib().f16_fdm_step_batch_onelane]
+    # f16_fdm_step_batch launches the four-wave kernel without the 17-value output and the
+    # two-wave kernel with it
+    lib = L.lib()
+    fns = [(lib.f16_fdm_step_batch, True), (lib.f16_fdm_step_batch_onelane, True),
+           (lib.f16_fdm_step_batch_split, True), (lib.f16_fdm_step_batch, False)]
     for d in range(12):
         at = torch.as_tensor(acts[d], device=gpu).contiguous()
-        for fn, (st, ob) in zip(fns, bufs):
-            L.check(fn(L.ptr(st), ld, L.ptr(at), nac, S, rate, L.ptr(ob), ld,
-                       L.stream_handle(gpu)), "step")
-    (sa, oa), (sb, ob) = bufs
+        for (fn, want_obs), (st, ob) in zip(fns, bufs):
+            L.check(fn(L.ptr(st), ld, L.ptr(at), nac, S, rate, L.ptr(ob) if want_obs else None,
+                       ld, L.stream_handle(gpu)), "step")
+    (sa, oa), (sb, ob), (sc, oc), (sd, _) = bufs
     assert bool(torch.isfinite(sa).all())
-    assert torch.equal(sa, sb)
-    assert torch.equal(oa, ob)
+    assert torch.equal(sa, sb) and torch.equal(sa, sc) and torch.equal(sa, sd)
+    assert torch.equal(oa, ob) and torch.equal(oa, oc)
     if S == 0:
         assert torch.equal(sa[:, :nac], sim._state_soa)
 
