@@ -517,7 +517,7 @@ def test_env_step_pool_tables_equal_rebuild(gpu, obs_dim, nenv):
 @pytest.mark.parametrize("obs_dim,nenv,fcs,roles", [
     (184, 300, 60, 2), (214, 300, 120, 2), (184, 16384, 60, 2), (214, 16384, 120, 2),
     (184, 20000, 60, 2), (184, 300, 60, 4), (214, 300, 120, 4), (184, 16384, 60, 4),
-    (214, 16384, 120, 4)])
+    (214, 16384, 120, 4), (184, 20, 60, 4), (214, 33, 120, 4)])
 def test_env_step_one_launch_equals_two(gpu, obs_dim, nenv, fcs, roles):
     """f16_env_step (physics and post-physics step in one launch wherever the full-row tile is
     resident: 300 engagements, whose last workgroup is partly filled, and 16,384; at 20,000 the
@@ -572,7 +572,7 @@ def test_env_step_one_launch_equals_two(gpu, obs_dim, nenv, fcs, roles):
         if k == 1:
             assert not bool(ia["terminal_state_finite"][8])
         resets += int(da.sum())
-    assert resets > nenv // 4, resets
+    assert resets > nenv // 4 or nenv < 100, resets
     nac = 2 * nenv
     norms = [P.RunningNorm(obs_dim, gpu) for _ in envs]
     bases = [torch.full((), 40, dtype=torch.int32, device=gpu) for _ in envs]
