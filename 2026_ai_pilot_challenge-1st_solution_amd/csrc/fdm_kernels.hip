@@ -60,8 +60,7 @@ __global__ __launch_bounds__(kSplitBlock) void fdm_step_split_kernel(
 // The four-role form (fdm_quad.h): each 64 aircraft on four wavefronts, two groups per
 // 512-thread workgroup, so 16,384 engagements put two wavefronts on every SIMD (at most 256
 // registers each) where the two-wave kernel has one.  The same results bit for bit.  OBS: the
-// 17-value output is written (launched with OBS = false only: the output's pointer arithmetic
-// pushes the integrator role past 256 registers).
+// 17-value output is written (its own instantiation: 255 registers with it, 225 without).
 template <int FCS_RATE, bool OBS>
 __global__ __launch_bounds__(kQuadBlock) void fdm_step_quad_kernel(
     double* __restrict__ st, long ld, const double* __restrict__ act, int nac, int S,
@@ -263,18 +262,19 @@ static int fdm_step_split(double* states, long ld, const double* actions, int na
                           int fcs_rate, double* obs, long obs_ld, unsigned char* fin,
                           void* stream, double* keep = nullptr, bool quad = true) {
   hipStream_t s = (hipStream_t)stream;
-  // The four-wave kernel where the 17-value output is off (16k tail-chase engagements: 33.0 vs
-  // 36.9 us; 64k: 134 vs 145 us); with the output its integrator role spills past 256
-  // registers and is no faster (38.0 vs 38.2 us; 153 vs 149 us at 64k), so the two-wave kernel
-  // writes it.
-  if (quad && !obs) {
+  // The four-wave kernel (16k tail-chase engagements: 32.8 vs 36.7 us without the 17-value
+  // output, 36.3 vs 37.8 us with it; 64k: 133 vs 144 us, 142 vs 147 us).
+  if (quad) {
     const dim3 grid((nac + f16::kQuadAircraft - 1) / f16::kQuadAircraft), block(f16::kQuadBlock);
-    if (fcs_rate == 120)
-      hipLaunchKernelGGL((f16::fdm_step_quad_kernel<120, false>), grid, block, 0, s, states, ld,
-                         actions, nac, substeps, obs, obs_ld, fin, keep);
-    else
-      hipLaunchKernelGGL((f16::fdm_step_quad_kernel<60, false>), grid, block, 0, s, states, ld,
-                         actions, nac, substeps, obs, obs_ld, fin, keep);
+#define F16_QUAD(R, O)                                                                          \
+  hipLaunchKernelGGL((f16::fdm_step_quad_kernel<R, O>), grid, block, 0, s, states, ld, actions, \
+                     nac, substeps, obs, obs_ld, fin, keep)
+    if (fcs_rate == 120) {
+      if (obs) F16_QUAD(120, true); else F16_QUAD(120, false);
+    } else {
+      if (obs) F16_QUAD(60, true); else F16_QUAD(60, false);
+    }
+#undef F16_QUAD
     return f16_last_error();
   }
   const dim3 grid((nac + f16::kSplitAircraft - 1) / f16::kSplitAircraft), block(f16::kSplitBlock);

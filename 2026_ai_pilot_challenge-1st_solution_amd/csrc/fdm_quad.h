@@ -80,7 +80,7 @@ typedef double QuadX[kQuadFields][64];
 // value it stores through x[kQFinKin] after one more barrier.
 template <int FCS_RATE>
 __device__ __forceinline__ void quad_kin(double* __restrict__ s, long ld, int S, bool store,
-                                         double* __restrict__ o, long obs_ld,
+                                         double* __restrict__ out_base, long obs_ld,
                                          const double* __restrict__ T, QuadX& x, int lane,
                                          bool fin) {
 #define F(k) s[(long)(k) * ld]
@@ -116,7 +116,7 @@ __device__ __forceinline__ void quad_kin(double* __restrict__ s, long ld, int S,
       }
     }
   }
-  const bool out = o != nullptr && store;   // the 17-value output, written where formed
+  const bool out = out_base != nullptr && store;   // the 17-value output, written where formed
   double uvw[3] = {0.0, 0.0, 0.0}, wpqr[3] = {0.0, 0.0, 0.0};
   AuxGeo g;
   double gi[3] = {0.0, 0.0, 0.0};
@@ -151,9 +151,13 @@ __device__ __forceinline__ void quad_kin(double* __restrict__ s, long ld, int S,
         se = x[kQSe][lane];
       }
       double euler[3];
-      kinematics(a.p, a.v, a.q, a.wi, ce, se, slot == 0 && o != nullptr, k, euler);
+      kinematics(a.p, a.v, a.q, a.wi, ce, se, slot == 0 && out_base != nullptr, k, euler);
       const double alt = k.radius - kSemiMajor;
       if (slot == 0 && out) {   // p and v are final here: phase D does not change them
+        // the output's addresses are formed here from a pointer the compiler cannot see
+        // through, not hoisted above the loop (17 of them, 2 registers each)
+        double* o = out_base;
+        asm volatile("" : "+v"(o));
 #pragma unroll
         for (int j = 0; j < 3; ++j) {
           o[(long)j * obs_ld] = a.p[j];
@@ -175,7 +179,11 @@ __device__ __forceinline__ void quad_kin(double* __restrict__ s, long ld, int S,
     __syncthreads();
     // ---- phase B
     g = aux_geometry(uvw);
-    if (slot == 0 && out) { o[12L * obs_ld] = g.alpha; o[13L * obs_ld] = g.beta; o[15L * obs_ld] = g.vt; }
+    if (slot == 0 && out) {
+      double* o = out_base;
+      asm volatile("" : "+v"(o));
+      o[12L * obs_ld] = g.alpha; o[13L * obs_ld] = g.beta; o[15L * obs_ld] = g.vt;
+    }
     double npy, npz;
     {
       const double cg[3] = {x[mo + kQCg][lane], x[mo + kQCg + 1][lane], x[mo + kQCg + 2][lane]};
@@ -189,7 +197,11 @@ __device__ __forceinline__ void quad_kin(double* __restrict__ s, long ld, int S,
     __syncthreads();
     // ---- phase C
     {
-      if (slot == 0 && out) o[14L * obs_ld] = fm_div(g.vt, x[kQSound][lane]);
+      if (slot == 0 && out) {
+        double* o = out_base;
+        asm volatile("" : "+v"(o));
+        o[14L * obs_ld] = fm_div(g.vt, x[kQSound][lane]);
+      }
       x[kQVg][lane] = fm_sqrt(vn * vn + ve * ve);
       quat_rate(a);
       gravity(kg, gi);

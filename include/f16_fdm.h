@@ -45,9 +45,8 @@ int f16_fdm_step_batch_keep(double* states, long ld, const double* actions,
 
 /* The same step with each substep of 64 aircraft spread over two cooperating wavefronts (flight
  * and systems) instead of the four of f16_fdm_step_batch (integrator, aero build-up, FCS, mass /
- * atmosphere / engine; f16_fdm_step_batch itself uses the two-wave kernel when obs is given).
- * Results equal f16_fdm_step_batch bit for bit; kept as its cross-check.  Same arguments,
- * contract and reference interface. */
+ * atmosphere / engine).  Results equal f16_fdm_step_batch bit for bit; kept as its
+ * cross-check.  Same arguments, contract and reference interface. */
 int f16_fdm_step_batch_split(double* states, long ld, const double* actions, int nac,
                              int substeps, int fcs_rate, double* obs, long obs_ld, void* stream);
 

@@ -275,8 +275,7 @@ def test_split_kernel_equals_onelane(gpu, rate, nenv, S, pad):
         st[:, :nac] = sim._state_soa
         bufs.append((st, torch.zeros(17, ld, dtype=torch.float64, device=gpu)))
     acts = icm.random_bin_actions(12, nac, seed=7)
-    # f16_fdm_step_batch launches the four-wave kernel without the 17-value output and the
-    # two-wave kernel with it
+    # f16_fdm_step_batch launches the four-wave kernel, with and without the 17-value output
     lib = L.lib()
     fns = [(lib.f16_fdm_step_batch, True), (lib.f16_fdm_step_batch_onelane, True),
            (lib.f16_fdm_step_batch_split, True), (lib.f16_fdm_step_batch, False)]
