@@ -140,7 +140,7 @@ __global__ __launch_bounds__(kThreads, 4) void policy_kernel(const F16PolicyArgs
   static_assert(KP <= kHPitch, "rows fit A");
   __shared__ __align__(16) __bf16 As[kRows * kHPitch];
   __shared__ __align__(16) __bf16 Bs[kRows * kHPitch];
-  __shared__ __align__(16) float col_mean[KP], col_sd[KP];
+  __shared__ __align__(16) float col_mean[KP], col_sd[KP], col_rcp[KP];
   __shared__ float vpart[kWaves][kRows];
   // The workgroup's network and 64-row tile.  The row ranges are uniform: kept in scalar
   // registers (a vector load would hold them, and everything derived from them, in vector
@@ -211,12 +211,15 @@ __global__ __launch_bounds__(kThreads, 4) void policy_kernel(const F16PolicyArgs
     if (tid < KP) {
       const bool on = g_mean && tid < D;
       col_mean[tid] = on ? g_mean[tid] : 0.0f;
-      col_sd[tid] = on ? sqrtf(g_var[tid] + p.eps) : 1.0f;
+      const float sd = on ? sqrtf(g_var[tid] + p.eps) : 1.0f;
+      col_sd[tid] = sd;
+      col_rcp[tid] = 1.0f / sd;                       // correctly rounded (IEEE division)
     }
     __syncthreads();
     if (act) {
       const vec mu = *reinterpret_cast<const vec*>(col_mean + VW * cv);
       const vec sd = *reinterpret_cast<const vec*>(col_sd + VW * cv);
+      const vec rc = *reinterpret_cast<const vec*>(col_rcp + VW * cv);
 #pragma unroll
       for (int q = 0; q < S::NP; ++q) {
         const int r = rb + S::RP * q;
@@ -227,7 +230,13 @@ __global__ __launch_bounds__(kThreads, 4) void policy_kernel(const F16PolicyArgs
             if (g_mean) {
 #pragma unroll
               for (int i = 0; i < VW; ++i) {
-                float t = (v[i] - mu[i]) / sd[i];
+                // (v - mu) / sd as the correctly rounded quotient from the correctly rounded
+                // reciprocal: q0 = d rc, the exact residual d - q0 sd by one fma, one fma
+                // correction (Markstein), three operations in place of the division sequence
+                const float d = v[i] - mu[i];
+                const float q0 = d * rc[i];
+                const float e = __builtin_fmaf(-q0, sd[i], d);
+                const float t = __builtin_fmaf(e, rc[i], q0);
                 v[i] = t < -p.clip ? -p.clip : (t > p.clip ? p.clip : t);
               }
             }
