@@ -223,6 +223,10 @@ def cpu_baseline(states0_aos, actions_host, substeps, cpu_seconds, icm):
 # reads the other 86 state doubles instead of the byte.
 POST_BYTES_PER_AIRCRAFT = (15 + 4 + 27) * 8 + 1 + 2 + (34 + 3) * 8 + 2 * 184 * 4 + 4
 POST_BYTES_SCAN_EXTRA = 86 * 8 - 1
+# The one-launch step (f16_env_step): the physics' bytes (66 state doubles read, 101 written,
+# 4 actions read) and the post-physics step's, less the 15 state doubles the post-physics phase
+# reads back from L2 (the same workgroup stored them)
+STEP_BYTES_PER_AIRCRAFT = (66 + 101 + 4) * 8 + POST_BYTES_PER_AIRCRAFT - 15 * 8
 # reference's published full env step at 16,384 envs: 10.3 ms (RTX 3070 Ti,
 # cuda_fdm/README.md:225) = 1.59 M env transitions/s
 REF_PUBLISHED_ENV_TRANSITIONS = 16384 / 10.3e-3
@@ -334,8 +338,12 @@ def env_step_bench(pkg, nenv, steps, warmup, scan_finite=False, ab=True, stagger
            "host_issue_ms_per_step": main["host_issue_ms_per_step"],
            "vs_published": nenv / (main["ms_per_step"] * 1e-3) / REF_PUBLISHED_ENV_TRANSITIONS}
     if "step_kernel_ms" in main:
+        sb = STEP_BYTES_PER_AIRCRAFT * 2 * nenv
         out["step_kernel"] = {"kernel": "env_step_quad_kernel<60,184>",
-                              "kernel_ms": main["step_kernel_ms"]}
+                              "kernel_ms": main["step_kernel_ms"], "algorithmic_bytes": sb,
+                              "achieved_GBs": sb / (main["step_kernel_ms"] * 1e-3) / 1e9,
+                              "hbm_frac": sb / (main["step_kernel_ms"] * 1e-3) / 1e9 /
+                              PEAK_HBM_GBS}
     two = res.get("two_launch", res.get("state_scan"))
     if two is not None:
         out["fdm_kernel_ms"], out["post_kernel_ms"] = two["fdm_kernel_ms"], two["post_kernel_ms"]
