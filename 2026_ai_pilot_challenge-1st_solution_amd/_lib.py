@@ -4,6 +4,10 @@ include/f16_policy.h and include/f16_ppo.h).
 torch is imported first so that the process's HIP runtime is torch's; the library then binds
 to that same runtime (libamdhip64.so.7) and launches on torch's streams.  There is no CPU
 fallback: if the library is missing or fails to load, every call raises.
+
+Stream contract (cuda_fdm/tests/cuda_rt.py:107-139): each launch goes to the caller's current
+stream with no synchronisation; data readiness across streams is the caller's (wait_stream), and
+the tensors a launch touches are marked with `record` so their memory outlives the launch.
 """
 import ctypes
 import os
@@ -169,3 +173,51 @@ def ptr(t):
 
 def stream_handle(device=None):
     return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def launch_stream(device=None):
+    """(stream, C handle) of the caller's current stream on `device`: every launch of this
+    library goes there, and `record` marks its tensors as used on the same stream."""
+    s = torch.cuda.current_stream(device)
+    return s, ctypes.c_void_p(s.cuda_stream)
+
+
+def record(stream, tensors):
+    """The reference's lifetime contract (cuda_fdm/tests/cuda_rt.py:134-136): every tensor a
+    launch reads or writes, temporaries included, is marked as used on the launch's stream
+    (Tensor.record_stream), so torch's caching allocator does not hand its memory to another
+    stream's allocation before that stream has passed the launch -- the case of a tensor
+    allocated on one stream, handed to a launch on another and then dropped by its owner.
+
+    The allocator keeps a block's recorded streams until the block is freed, so a record is
+    made once per (tensor object, storage address, stream): a persistent buffer is recorded on
+    its first launch on a stream, a fresh tensor on each call.  torch itself ignores a record
+    on the stream the tensor was allocated on."""
+    key = stream.cuda_stream
+    for t in tensors:
+        if t is None:
+            continue
+        tag = (key, t.data_ptr())
+        seen = getattr(t, "_f16_streams", None)
+        if seen is None:
+            seen = set()
+            t._f16_streams = seen
+        elif tag in seen:
+            continue
+        t.record_stream(stream)
+        seen.add(tag)
+
+
+def record_owned(owner, stream, tensors):
+    """record() for the buffers an object holds across launches (a simulator's state, a
+    reconstructor's vectors): skipped while the stream and every buffer object are those of the
+    owner's previous record.  The owner keeps these objects alive, and the allocator keeps a
+    block's recorded streams until the block is freed, so the earlier record still holds; a
+    replaced buffer (a new object) or another stream records again."""
+    prev = owner.__dict__.get("_f16_owned")
+    key = stream.cuda_stream
+    if (prev is not None and prev[0] == key and len(prev[1]) == len(tensors)
+            and all(a is b for a, b in zip(prev[1], tensors))):
+        return
+    record(stream, tensors)
+    owner._f16_owned = (key, tensors)

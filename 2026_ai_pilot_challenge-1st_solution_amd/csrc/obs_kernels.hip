@@ -1503,8 +1503,8 @@ static_assert(f16::kSplitBlock == kPostSplitBlock && f16::kSplitAircraft == kPos
 
 template <int FCS_RATE, int D>
 __global__ __launch_bounds__(kPostSplitBlock) void env_step_fused_kernel(
-    const double* __restrict__ act, int S, double* __restrict__ act_keep,
-    unsigned char* __restrict__ state_finite, const F16EnvStepIO io, F16Recon r, F16RewardCfg c,
+    const double* __restrict__ act, int S, double* act_keep,
+    unsigned char* state_finite, const F16EnvStepIO io, F16Recon r, F16RewardCfg c,
     Origin O) {
   __shared__ EnvStepLds<D> L;
   f16::stage_image<kPostSplitBlock>(L.fdm.T);
@@ -1543,8 +1543,8 @@ static_assert(f16::kQuadBlock == kQuadPostBlock && f16::kQuadAircraft == kPostGr
 
 template <int FCS_RATE, int D>
 __global__ __launch_bounds__(kQuadPostBlock) void env_step_quad_kernel(
-    const double* __restrict__ act, int S, double* __restrict__ act_keep,
-    unsigned char* __restrict__ state_finite, const F16EnvStepIO io, F16Recon r, F16RewardCfg c,
+    const double* __restrict__ act, int S, double* act_keep,
+    unsigned char* state_finite, const F16EnvStepIO io, F16Recon r, F16RewardCfg c,
     Origin O) {
   __shared__ EnvQuadLds<D> L;
   f16::stage_image<kQuadPostBlock>(L.fdm.T);

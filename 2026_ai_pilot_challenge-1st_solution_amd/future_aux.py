@@ -46,6 +46,8 @@ def labels_into(features, episode_starts, dt, labels, mask_u8):
                                 episode_starts.is_contiguous()) else \
         episode_starts.to(device=dev, dtype=torch.float32).contiguous()
     T, nenv = f.shape[:2]
+    stream, h = _lib.launch_stream(dev)
     rc = _lib.lib().f16_future_labels(_lib.ptr(f), _lib.ptr(starts), T, nenv, float(dt),
-                                      _lib.ptr(labels), _lib.ptr(mask_u8), _lib.stream_handle(dev))
+                                      _lib.ptr(labels), _lib.ptr(mask_u8), h)
+    _lib.record(stream, (f, starts, labels, mask_u8))
     _lib.check(rc, "f16_future_labels")

@@ -81,6 +81,10 @@ class GpuDogfight:
         _lib.check(fn(self.fcs_rate, out), "f16_fdm_kernel_info")
         return dict(regs=out[0], lds=out[1], scratch=out[2], max_threads=out[3])
 
+    def _buffers(self):
+        """The device buffers every launch of this simulator touches."""
+        return (self._state_soa, self.actions, self._obs_soa)
+
     # ---- reset (cuda_fdm/gpu_env.py:64-92) ----
     def load_seed(self, seed):
         """seed: (101,), (ppe,101), (nac,101) or (nenv,ppe,101); numpy or torch."""
@@ -120,8 +124,11 @@ class GpuDogfight:
                 raise IndexError(f"rows must lie in [0, {self.nac})")
         elif n != self.nac:
             raise ValueError("without rows, n must equal nac")
+        stream, h = _lib.launch_stream(self.device)
         rc = self._lib.f16_seed_batch(_lib.ptr(ic), n, self.fcs_rate, _lib.ptr(self._state_soa),
-                                      self.nac, _lib.ptr(rows), _lib.stream_handle(self.device))
+                                      self.nac, _lib.ptr(rows), h)
+        _lib.record(stream, (ic, rows))
+        _lib.record_owned(self, stream, self._buffers())
         _lib.check(rc, "f16_seed_batch")
 
     # ---- step (cuda_fdm/gpu_env.py:95-106) ----
@@ -157,24 +164,25 @@ class GpuDogfight:
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record()
         obs_p = _lib.ptr(self._obs_soa) if want_obs else None
+        stream, h = _lib.launch_stream(self.device)
         if keep:
             rc = self._lib.f16_fdm_step_batch_keep(
                 _lib.ptr(self._state_soa), self.nac, _lib.ptr(a), _lib.ptr(self.actions),
                 self.nac, ss, self.fcs_rate, obs_p, self.nac,
-                _lib.ptr(finite_out) if finite_out is not None else None,
-                _lib.stream_handle(self.device))
+                _lib.ptr(finite_out) if finite_out is not None else None, h)
         elif finite_out is None:
             rc = self._lib.f16_fdm_step_batch(
                 _lib.ptr(self._state_soa), self.nac, _lib.ptr(self.actions), self.nac, ss,
-                self.fcs_rate, obs_p, self.nac, _lib.stream_handle(self.device))
+                self.fcs_rate, obs_p, self.nac, h)
         else:
             rc = self._lib.f16_fdm_step_batch_finite(
                 _lib.ptr(self._state_soa), self.nac, _lib.ptr(self.actions), self.nac, ss,
-                self.fcs_rate, obs_p, self.nac, _lib.ptr(finite_out),
-                _lib.stream_handle(self.device))
+                self.fcs_rate, obs_p, self.nac, _lib.ptr(finite_out), h)
         if ev is not None:
             e1.record()
             ev.append((e0, e1))
+        _lib.record_owned(self, stream, self._buffers())
+        _lib.record(stream, (a if keep else None, finite_out))
         _lib.check(rc, "f16_fdm_step_batch")
         return self.obs.view(self.nenv, self.ppe, OBS_N)
 

@@ -160,8 +160,12 @@ class BatchObsReward:
             return None
         return self._check(mask, (self.nenv,), (torch.bool, torch.uint8), "environment mask")
 
-    def _stream(self):
-        return _lib.stream_handle(self.device)
+    def _recon_tensors(self):
+        """The reconstructor buffers an F16Recon points at (for the launch-stream record)."""
+        return (self.hp, self.fuel, self.t_sec, self._att_soa, self.prev_valid, self._pqr_soa,
+                self.last_dmg_dealt, self.last_dmg_taken, self.hp_loss, self._hist_soa,
+                self.prev_x, self.prev_x_valid, self.prev_alt_log, self._vel_soa, self._acc_soa,
+                self.aux_features, self.obs_buf, self.reward_buf, self.term_buf, self.trunc_buf)
 
     # ---- kernels (obs_reward.py:410-469) ----
     def kernel_advance(self, states, actions, cfg=None, min_alt=304.8, max_time=200.0,
@@ -174,10 +178,12 @@ class BatchObsReward:
         ac = self._check(actions, (self.nac, 4), (torch.float64,), "actions")
         c = reward_cfg_struct(cfg, min_alt, max_time, mode, alt_hunt_coef)
         rec = self._recon()
+        stream, h = _lib.launch_stream(self.device)
         rc = self._lib.f16_obr_advance(_lib.ptr(st), ld, _lib.ptr(ac), _lib.ctypes.byref(rec),
                                        _lib.ctypes.byref(c), _lib.ptr(self.reward_buf),
-                                       _lib.ptr(self.term_buf), _lib.ptr(self.trunc_buf),
-                                       self._stream())
+                                       _lib.ptr(self.term_buf), _lib.ptr(self.trunc_buf), h)
+        _lib.record(stream, (st, ac))
+        _lib.record_owned(self, stream, self._recon_tensors())
         _lib.check(rc, "f16_obr_advance")
         return self.reward_buf, self.term_buf, self.trunc_buf
 
@@ -186,8 +192,11 @@ class BatchObsReward:
         st, ld = soa_states(states, self.nac)
         m = self._mask(env_mask)
         rec = self._recon()
+        stream, h = _lib.launch_stream(self.device)
         rc = self._lib.f16_obr_init_reward(_lib.ptr(st), ld, _lib.ptr(m), _lib.ctypes.byref(rec),
-                                           self._stream())
+                                           h)
+        _lib.record(stream, (st, m))
+        _lib.record_owned(self, stream, self._recon_tensors())
         _lib.check(rc, "f16_obr_init_reward")
 
     def kernel_build_obs(self, states, env_mask=None):
@@ -198,8 +207,11 @@ class BatchObsReward:
         st, ld = soa_states(states, self.nac)
         m = self._mask(env_mask)
         rec = self._recon()
+        stream, h = _lib.launch_stream(self.device)
         rc = self._lib.f16_obr_build_obs(_lib.ptr(st), ld, _lib.ptr(m), _lib.ctypes.byref(rec),
-                                         dim, _lib.ptr(out), self._stream())
+                                         dim, _lib.ptr(out), h)
+        _lib.record(stream, (st, m, out))
+        _lib.record_owned(self, stream, self._recon_tensors())
         _lib.check(rc, "f16_obr_build_obs")
         return out
 

@@ -169,8 +169,10 @@ class RunningNorm:
         """The second half of update(): fold the partial sums already in the workspace (written
         by a post-physics step with fused_partials) into mean/var."""
         L = _lib.lib()
+        stream, h = _lib.launch_stream(self.device)
         rc = L.f16_norm_merge(n, self.dim, _lib.ptr(self.mean), _lib.ptr(self.var),
-                              _lib.ptr(self._workspace(n)), _lib.stream_handle(self.device))
+                              _lib.ptr(self._workspace(n)), h)
+        _lib.record_owned(self, stream, (self.mean, self.var, self.count, self._work))
         _lib.check(rc, "f16_norm_merge")
 
     @torch.no_grad()
@@ -183,9 +185,12 @@ class RunningNorm:
         n = x.shape[0] if rows is None else rows.numel()
         L = _lib.lib()
         self._workspace(n)
+        stream, h = _lib.launch_stream(self.device)
         rc = L.f16_norm_update(_lib.ptr(x), x.stride(0), _lib.ptr(rows), n, self.dim,
                                _lib.ptr(self.mean), _lib.ptr(self.var), _lib.ptr(self.count),
-                               _lib.ptr(self._work), _lib.stream_handle(self.device))
+                               _lib.ptr(self._work), h)
+        _lib.record_owned(self, stream, (self.mean, self.var, self.count, self._work))
+        _lib.record(stream, (x, rows))
         _lib.check(rc, "f16_norm_update")
 
     @torch.no_grad()
@@ -313,6 +318,12 @@ class PolicyStep:
                 raise ValueError("step_base must be a device int32 scalar")
             a.step_base = step_base.data_ptr()
         a.env_actions, a.logits_out = p(env_actions), p(logits_out)
-        rc = self._lib.f16_policy_step(ctypes.byref(a), _lib.stream_handle(self.device))
+        stream, h = _lib.launch_stream(self.device)
+        rc = self._lib.f16_policy_step(ctypes.byref(a), h)
+        _lib.record(stream, (obs, rows, group_offsets, nobs_out, act_idx, logp, value,
+                             env_actions, logits_out, step_base, self.grid)
+                    + (() if norm is None else (norm.mean, norm.var))
+                    + tuple(t for wb in keep for t in wb)
+                    + tuple(t for g in groups if g[3] is not None for t in (g[3].mean, g[3].var)))
         _lib.check(rc, "f16_policy_step")
         return keep

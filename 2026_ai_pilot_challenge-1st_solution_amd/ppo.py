@@ -38,10 +38,11 @@ def gae(rew, val, done, last_val, next_done, gamma=0.997, lam=0.95):
     # gamma*lambda is formed in double then rounded once, as the reference's Python scalars are
     gl = float(torch.tensor(float(gamma) * float(lam), dtype=torch.float32))
     g = float(torch.tensor(float(gamma), dtype=torch.float32))
+    stream, h = _lib.launch_stream(dev)
     rc = _lib.lib().f16_gae(_lib.ptr(rew), _lib.ptr(val), _lib.ptr(done), _lib.ptr(last_val),
                             _lib.ptr(next_done), T, nenv, nag, _lib.ctypes.c_float(g),
-                            _lib.ctypes.c_float(gl), _lib.ptr(adv), _lib.ptr(ret),
-                            _lib.stream_handle(dev))
+                            _lib.ctypes.c_float(gl), _lib.ptr(adv), _lib.ptr(ret), h)
+    _lib.record(stream, (rew, val, done, last_val, next_done))
     _lib.check(rc, "f16_gae")
     return adv, ret
 
@@ -345,10 +346,12 @@ class LeagueRollout:
         return out
 
     def _opponents(self, obs, step, step_base):
+        stream, h = _lib.launch_stream(self.device)
         rc = self._lib.f16_group_rows(_lib.ptr(self.env.opp_assign), self.nenv,
                                       len(self.opponents), 2, 1, _lib.ptr(self.opp_rows),
-                                      _lib.ptr(self.opp_offsets), _lib.ptr(self._group_work),
-                                      _lib.stream_handle(self.device))
+                                      _lib.ptr(self.opp_offsets), _lib.ptr(self._group_work), h)
+        _lib.record_owned(self, stream, (self.env.opp_assign, self.opp_rows, self.opp_offsets,
+                                         self._group_work))
         _lib.check(rc, "f16_group_rows")
         groups = [(net, None, None, nrm) for net, nrm in zip(self.opponents, self.opp_norms)]
         self.policy(obs, groups, rows=self.opp_rows, group_offsets=self.opp_offsets,

@@ -103,10 +103,17 @@ class PPOUpdater:
     # ---- blobs
     def pack(self):
         """Rewrite the rollout blobs and the transposed blob from the master parameters."""
+        stream, h = _lib.launch_stream(self.device)
         rc = self._L.f16_ppo_pack(_lib.ptr(self.flat), self.D, _lib.ptr(self.wbf),
-                                  _lib.ptr(self.wf), _lib.ptr(self.wT),
-                                  _lib.stream_handle(self.device))
+                                  _lib.ptr(self.wf), _lib.ptr(self.wT), h)
+        _lib.record_owned(self, stream, self._buffers())
         _lib.check(rc, "f16_ppo_pack")
+
+    def _buffers(self):
+        """The updater's device buffers (master parameters, moments, gradients, blobs,
+        workspace, statistics) for the launch-stream record."""
+        return (self.flat, self.exp_avg, self.exp_avg_sq, self.grad, self.grad_norms, self.wT,
+                self.wbf, self.wf, getattr(self, "_work", None), getattr(self, "stats", None))
 
     def _workspace(self, mb_rows):
         if self._work is None or mb_rows > self._work_rows:
@@ -135,8 +142,11 @@ class PPOUpdater:
         a.wbf, a.wf, a.wT = _lib.ptr(self.wbf), _lib.ptr(self.wf), _lib.ptr(self.wT)
         a.grad, a.stats, a.work = _lib.ptr(self.grad), _lib.ptr(stats_row), \
             _lib.ptr(self._workspace(n))
-        _lib.check(self._L.f16_ppo_grad(ctypes.byref(a), _lib.stream_handle(self.device)),
-                   "f16_ppo_grad")
+        stream, h = _lib.launch_stream(self.device)
+        rc = self._L.f16_ppo_grad(ctypes.byref(a), h)
+        _lib.record_owned(self, stream, self._buffers())
+        _lib.record(stream, (obs, act, old_logp, adv, ret, idx, stats_row))
+        _lib.check(rc, "f16_ppo_grad")
 
     def optimizer_step(self):
         """clip_grad_norm_ + Adam on both networks, then the blobs (ppo_gpu.py:2088-2105)."""
@@ -154,8 +164,10 @@ class PPOUpdater:
         a.grad_norms = _lib.ptr(self.grad_norms)
         a.wbf, a.wf, a.wT = _lib.ptr(self.wbf), _lib.ptr(self.wf), _lib.ptr(self.wT)
         a.work = _lib.ptr(self._workspace(max(1, self._work_rows)))
-        _lib.check(self._L.f16_ppo_adam_step(ctypes.byref(a), _lib.stream_handle(self.device)),
-                   "f16_ppo_adam_step")
+        stream, h = _lib.launch_stream(self.device)
+        rc = self._L.f16_ppo_adam_step(ctypes.byref(a), h)
+        _lib.record_owned(self, stream, self._buffers())
+        _lib.check(rc, "f16_ppo_adam_step")
 
     # ---- the update (ppo_gpu.py:2019-2145)
     def update(self, rollout, adv, ret, perms=None):

@@ -92,8 +92,10 @@ class GpuDogfightVecEnv:
         # makes it rebuild them
         self.pool_tables = True
         self._pool_key = None
+        self._pool_src = None
         self._capture_terminal_obs = True     # step's default (step_training clears it)
         self._pool_buf = None
+        self._call_tensors = ()
 
     def enable_aux_capture(self):
         """Turn on the future-aux features (BatchObsReward.enable_aux_capture): every step and
@@ -199,9 +201,28 @@ class GpuDogfightVecEnv:
         io = self._io(None)
         io.step = step & 0xffffffff
         io.opp_assign = None
+        stream, h = _lib.launch_stream(self.device)
         rc = self.obr._lib.f16_env_reseed(_lib.ctypes.byref(io), _lib.ctypes.byref(self._rec),
-                                          mask_u8.data_ptr(), _lib.stream_handle(self.device))
+                                          mask_u8.data_ptr(), h)
+        self._record(stream, (mask_u8,))
         _lib.check(rc, "f16_env_reseed")
+
+    def _buffers(self):
+        """The env's own device buffers a step or reseed launch may touch (the simulator's and
+        the reconstructor's are recorded by their owners)."""
+        pb = self._pool_buf or {}
+        return (self._obs, self._state_fin, self.ic_pool, pb.get("obs"), pb.get("prev_x"),
+                pb.get("alt"), pb.get("aux"), self.opp_assign, self.opp_cdf)
+
+    def _record(self, stream, per_call):
+        """Mark every tensor a launch of this env touches as used on the launch stream
+        (cuda_fdm/tests/cuda_rt.py:134-136): the persistent buffers once per stream, `per_call`
+        (the caller's actions, picks and output buffers) on each call.  Outputs this env
+        allocates per call on the launch stream itself need no record."""
+        _lib.record_owned(self.sim, stream, self.sim._buffers())
+        _lib.record_owned(self.obr, stream, self.obr._recon_tensors())
+        _lib.record_owned(self, stream, self._buffers())
+        _lib.record(stream, per_call)
 
     def _departed_envs(self, s9_flat=None, floor_m=100.0):
         s9 = (self.state9() if s9_flat is None else s9_flat.view(self.nenv, 2, 9))
@@ -257,12 +278,15 @@ class GpuDogfightVecEnv:
         Built by the reference's own reset sequence on the pool's states (reset_envs ->
         init_reward -> build_obs, rl_env.py:559-577) through the same kernels, so a copied row
         equals a rebuilt one bit for bit; rebuilt when the pool tensor, its contents (torch's
-        version counter), the observation width or aux capture change.  The tables live in
-        persistent buffers, so a recorded HIP graph keeps reading the current ones."""
+        version counter), the observation width or aux capture change.  The tensor the tables
+        were built from is held (_pool_src) and compared by identity: a replaced pool
+        (`env.ic_pool = None` then a redraw, or a restored one) is a different object even
+        where the allocator gives it the old pool's address.  The tables live in persistent
+        buffers, so a recorded HIP graph keeps reading the current ones."""
         pool = self.ic_pool
         aux = self.obr.aux_features is not None
-        key = (pool.data_ptr(), tuple(pool.shape), pool._version, self.OBS_SIZE, aux)
-        if self._pool_key != key:
+        key = (tuple(pool.shape), pool._version, self.OBS_SIZE, aux)
+        if self._pool_src is not pool or self._pool_key != key:
             P, D = pool.shape[0], self.OBS_SIZE
             t = BatchObsReward(P, device=self.device)
             if D == OBS_SIZE_EXT:
@@ -283,7 +307,7 @@ class GpuDogfightVecEnv:
             buf["alt"].copy_(t.prev_alt_log)
             if aux:
                 buf["aux"].copy_(t.aux_features)
-            self._pool_key = key
+            self._pool_key, self._pool_src = key, pool
         b = self._pool_buf
         return (b["obs"].data_ptr(), b["prev_x"].data_ptr(), b["alt"].data_ptr(),
                 b["aux"].data_ptr())
@@ -324,12 +348,13 @@ class GpuDogfightVecEnv:
             e0.record()
         fn = (self.obr._lib.f16_env_step_tworole if self.step_roles == 2 else
               self.obr._lib.f16_env_step)
+        stream, h = _lib.launch_stream(self.device)
         rc = fn(_lib.ctypes.byref(io), _lib.ctypes.byref(self._rec), _lib.ctypes.byref(c),
-                a.data_ptr(), self.substeps, self.sim.fcs_rate, state_fin.data_ptr(),
-                _lib.stream_handle(self.device))
+                a.data_ptr(), self.substeps, self.sim.fcs_rate, state_fin.data_ptr(), h)
         if ev is not None:
             e1.record()
             ev.append((e0, e1))
+        self._record(stream, self._call_tensors + (a,))
         _lib.check(rc, "f16_env_step")
         self._post_steps += 1
 
@@ -339,11 +364,13 @@ class GpuDogfightVecEnv:
         if ev is not None:
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record()
+        stream, h = _lib.launch_stream(self.device)
         rc = self.obr._lib.f16_env_post_step(_lib.ctypes.byref(io), _lib.ctypes.byref(self._rec),
-                                             _lib.ctypes.byref(c), _lib.stream_handle(self.device))
+                                             _lib.ctypes.byref(c), h)
         if ev is not None:
             e1.record()
             ev.append((e0, e1))
+        self._record(stream, self._call_tensors)
         _lib.check(rc, "f16_env_post_step")
         self._post_steps += 1
 
@@ -402,6 +429,7 @@ class GpuDogfightVecEnv:
         terminal_alt = torch.empty(n, dtype=torch.float64, device=dev)
         term, trunc, done, fin = (torch.empty(ne, dtype=torch.bool, device=dev) for _ in range(4))
         io = self._io(pick)
+        self._call_tensors = (pick,)
         p = lambda t: t.data_ptr() if t is not None else None
         io.terminal_obs, io.reward = p(tobs), p(reward)
         io.term, io.trunc, io.done, io.terminal_finite = p(term), p(trunc), p(done), p(fin)
@@ -444,14 +472,18 @@ class GpuDogfightVecEnv:
         io.finite_acc = finite_acc.data_ptr()
         if norm is not None:
             norm.fused_partials(io, self.nac)
+        self._call_tensors = (reward_f32, reward0_f32, done_f32, finite_acc, step_base) + (
+            (norm._work, norm.count) if norm is not None else ())
         self._advance(io, self.sim.actions, state_fin)
         return self._obs.view(self.nac, self.OBS_SIZE)
 
     # ---- state export (rl_env.py:583-592) ----
     def state9_flat(self):
         out = torch.empty(self.nac, 9, dtype=torch.float64, device=self.device)
+        stream, h = _lib.launch_stream(self.device)
         rc = self.obr._lib.f16_state9(_lib.ptr(self.sim._state_soa), self.nac, self.nac,
-                                      _lib.ptr(out), _lib.stream_handle(self.device))
+                                      _lib.ptr(out), h)
+        _lib.record_owned(self.sim, stream, self.sim._buffers())
         _lib.check(rc, "f16_state9")
         return out
 

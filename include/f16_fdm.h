@@ -68,8 +68,9 @@ int f16_seed_batch(const double* ic, int n, int fcs_rate, double* states, long l
                    const long* rows, void* stream);
 
 /* Host pointer out4 <- {registers per lane, static LDS bytes, scratch bytes per lane,
- * max threads per block} of the kernel f16_fdm_step_batch launches (the two-wave split kernel;
- * cf. cuda_fdm/tests/profile_kernel.py:23-33).  NULL out4 -> F16_EINVAL. */
+ * max threads per block} of the kernel f16_fdm_step_batch launches: the four-wave kernel
+ * without the 17-value output (cf. cuda_fdm/tests/profile_kernel.py:23-33).  NULL out4 ->
+ * F16_EINVAL. */
 int f16_fdm_kernel_info(int fcs_rate, int* out4);
 
 /* The same footprint for the one-lane kernel behind f16_fdm_step_batch_onelane

@@ -514,6 +514,52 @@ def test_env_step_pool_tables_equal_rebuild(gpu, obs_dim, nenv):
     assert envs[0]._pool_key is not None and envs[1]._pool_key is None
 
 
+@pytest.mark.parametrize("obs_dim", [184, 214])
+def test_env_step_pool_tables_follow_pool_replacement(gpu, obs_dim):
+    """The pool tables follow the pool tensor itself, not its address: after
+    `env.ic_pool = None` (the reference's evaluation reset, search_eval.py:78, redraws the pool
+    on the next step) and after a restored pool of the same shape is assigned
+    (ppo_gpu.py:2909), autoresets with tables equal autoresets that rebuild their rows, bit for
+    bit, even when the caching allocator hands the new pool the freed pool's address."""
+    E = import_pkg("rl_env").GpuDogfightVecEnv
+    nenv = 200
+    envs = [E(nenv, seed=21, ic_pool_size=64, obs_dim=obs_dim, max_engage_time_s=1.2)
+            for _ in range(2)]
+    envs[1].pool_tables = False
+    for env in envs:
+        env.enable_aux_capture()
+        env.reset(stagger=True, max_stagger_steps=12)
+    bits = lambda t: t.contiguous().view(torch.int32 if t.element_size() == 4 else
+                                         torch.int64 if t.element_size() == 8 else torch.uint8)
+    same = lambda x, y: torch.equal(bits(x), bits(y))
+    donor = E(32, seed=77, ic_pool_size=64, obs_dim=obs_dim)
+    donor._ensure_ic_pool()
+    rng = np.random.default_rng(22)
+    resets = 0
+    for k in range(9):
+        if k == 3:
+            for env in envs:
+                env.ic_pool = None                  # redrawn (same draws in both) on this step
+        if k == 6:
+            for env in envs:
+                env.ic_pool = None
+            torch.cuda.synchronize()
+            for env in envs:                        # a restored pool of the same shape
+                env.ic_pool = donor.ic_pool.clone()
+        act = torch.as_tensor(rng.uniform(-1, 1, (2 * nenv, 4)), device=gpu)
+        pick = torch.as_tensor(rng.integers(0, 64, nenv), device=gpu)
+        (oa, ra, da, ia), (ob, rb, db, ib) = [env.step(act, reset_indices=pick) for env in envs]
+        assert same(oa, ob) and same(ra, rb) and same(da, db), k
+        for key in ia:
+            assert same(ia[key], ib[key]), (k, key)
+        assert same(envs[0].sim._state_soa, envs[1].sim._state_soa), k
+        for name in ("prev_x", "prev_alt_log", "aux_features"):
+            assert same(getattr(envs[0].obr, name), getattr(envs[1].obr, name)), (k, name)
+        assert envs[0]._pool_src is envs[0].ic_pool
+        resets += int(da.sum())
+    assert resets > nenv // 4, resets
+
+
 @pytest.mark.parametrize("obs_dim,nenv,fcs,roles", [
     (184, 300, 60, 2), (214, 300, 120, 2), (184, 16384, 60, 2), (214, 16384, 120, 2),
     (184, 20000, 60, 2), (184, 300, 60, 4), (214, 300, 120, 4), (184, 16384, 60, 4),
