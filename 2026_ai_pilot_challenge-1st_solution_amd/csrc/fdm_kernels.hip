@@ -57,23 +57,27 @@ __global__ __launch_bounds__(kSplitBlock) void fdm_step_split_kernel(
                             fin ? fin + ia : nullptr, act_keep ? act_keep + 4L * ia : nullptr);
 }
 
-// The four-role form (fdm_quad.h): each 64 aircraft on four wavefronts, two groups per
-// 512-thread workgroup, so 16,384 engagements put two wavefronts on every SIMD (at most 256
-// registers each) where the two-wave kernel has one.  The same results bit for bit.  OBS: the
-// 17-value output is written (its own instantiation: 255 registers with it, 225 without).
-template <int FCS_RATE, bool OBS>
-__global__ __launch_bounds__(kQuadBlock) void fdm_step_quad_kernel(
+// The four-role form (fdm_quad.h): each 64 aircraft on four wavefronts, G groups per
+// workgroup of 256 G threads.  G = 2: 16,384 engagements put two wavefronts on every SIMD (at
+// most 256 registers each) where the two-wave kernel has one, the two groups' roles paired on
+// each SIMD by quad_role.  G = 1: a batch too small to give every CU a two-group workgroup
+// spreads over twice as many CUs, one wavefront per SIMD (the two group orders alternate
+// between workgroups).  The same results bit for bit.  OBS: the 17-value output is written
+// (its own instantiation: 255 registers with it, 225 without).
+template <int FCS_RATE, bool OBS, int G>
+__global__ __launch_bounds__(256 * G) void fdm_step_quad_kernel(
     double* __restrict__ st, long ld, const double* __restrict__ act, int nac, int S,
     double* __restrict__ obs, long obs_ld, unsigned char* __restrict__ fin,
     double* __restrict__ act_keep) {
+  static_assert(G == 1 || G == kQuadGroups, "one or two 64-aircraft groups per workgroup");
   __shared__ double T[F16M_IMAGE_LEN];
-  __shared__ QuadX X[kQuadGroups];
-  stage_image<kQuadBlock>(T);
+  __shared__ QuadX X[G];
+  stage_image<256 * G>(T);
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int grp = wave >> 2;
-  const int role = quad_role(grp, wave & 3);
-  const int i = blockIdx.x * kQuadAircraft + grp * 64 + lane;
+  const int role = quad_role(G == 1 ? (int)(blockIdx.x & 1) : grp, wave & 3);
+  const int i = blockIdx.x * (64 * G) + grp * 64 + lane;
   const bool store = i < nac;
   const int ia = store ? i : nac - 1;   // lanes past the batch shadow the last aircraft
   if (role == kRoleKin)
@@ -258,22 +262,41 @@ static int fdm_step_args(double* states, long ld, const double* actions, int nac
   return 0;
 }
 
+// Compute units of the current device (cached per device).
+static int device_cus() {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cus[dev] <= 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      n = 256;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+
 static int fdm_step_split(double* states, long ld, const double* actions, int nac, int substeps,
                           int fcs_rate, double* obs, long obs_ld, unsigned char* fin,
                           void* stream, double* keep = nullptr, bool quad = true) {
   hipStream_t s = (hipStream_t)stream;
   // The four-wave kernel (16k tail-chase engagements: 32.8 vs 36.7 us without the 17-value
-  // output, 36.3 vs 37.8 us with it; 64k: 133 vs 144 us, 142 vs 147 us).
+  // output, 36.3 vs 37.8 us with it; 64k: 133 vs 144 us, 142 vs 147 us).  Two groups per
+  // workgroup once the batch gives every CU such a workgroup, else one group per workgroup.
   if (quad) {
-    const dim3 grid((nac + f16::kQuadAircraft - 1) / f16::kQuadAircraft), block(f16::kQuadBlock);
-#define F16_QUAD(R, O)                                                                          \
-  hipLaunchKernelGGL((f16::fdm_step_quad_kernel<R, O>), grid, block, 0, s, states, ld, actions, \
-                     nac, substeps, obs, obs_ld, fin, keep)
+    const bool two = (long)nac >= (long)f16::kQuadAircraft * device_cus();
+#define F16_QUAD(R, O, G)                                                                     \
+  hipLaunchKernelGGL((f16::fdm_step_quad_kernel<R, O, G>), dim3((nac + 64 * G - 1) / (64 * G)), \
+                     dim3(256 * G), 0, s, states, ld, actions, nac, substeps, obs, obs_ld, fin, \
+                     keep)
+#define F16_QUAD_G(R, O) do { if (two) F16_QUAD(R, O, 2); else F16_QUAD(R, O, 1); } while (0)
     if (fcs_rate == 120) {
-      if (obs) F16_QUAD(120, true); else F16_QUAD(120, false);
+      if (obs) F16_QUAD_G(120, true); else F16_QUAD_G(120, false);
     } else {
-      if (obs) F16_QUAD(60, true); else F16_QUAD(60, false);
+      if (obs) F16_QUAD_G(60, true); else F16_QUAD_G(60, false);
     }
+#undef F16_QUAD_G
 #undef F16_QUAD
     return f16_last_error();
   }
@@ -356,8 +379,9 @@ extern "C" int f16_seed_batch(const double* ic, int n, int fcs_rate, double* sta
 }
 
 // Register/LDS/scratch footprint of the step kernel that f16_fdm_step_batch launches (the
-// four-wave kernel without the 17-value output; the reference's profile_kernel.py reads the same
-// attributes from the CUDA driver).  out = {vgprs/regs per thread, lds bytes, scratch bytes, max threads per block}.
+// four-wave kernel without the 17-value output, two groups per workgroup, as at 16,384
+// engagements; the reference's profile_kernel.py reads the same attributes from the CUDA
+// driver).  out = {vgprs/regs per thread, lds bytes, scratch bytes, max threads per block}.
 static int kernel_info(const void* fn, int* out4) {
   if (!out4) return F16_EINVAL;
   hipFuncAttributes at;
@@ -372,8 +396,8 @@ static int kernel_info(const void* fn, int* out4) {
 
 extern "C" int f16_fdm_kernel_info(int fcs_rate, int* out4) {
   if (fcs_rate != 120 && fcs_rate != 60) return F16_ERATE;
-  return kernel_info(fcs_rate == 60 ? (const void*)f16::fdm_step_quad_kernel<60, false>
-                                    : (const void*)f16::fdm_step_quad_kernel<120, false>, out4);
+  return kernel_info(fcs_rate == 60 ? (const void*)f16::fdm_step_quad_kernel<60, false, 2>
+                                    : (const void*)f16::fdm_step_quad_kernel<120, false, 2>, out4);
 }
 
 // The same for the one-lane kernel behind f16_fdm_step_batch_onelane.

@@ -90,6 +90,34 @@ def sample_tailchase(nenv, seed=0, fuel_lbs=6972.0):
     return rows
 
 
+def sample_random_valid(nenv, seed=0, fuel_lbs=6972.0):
+    """BASELINE C3: a random valid state per aircraft -- position within +-20 km of the contest
+    centre (north and east; altitude 0.5-12 km, so every aircraft starts above the hard deck),
+    airspeed U[100, 350] m/s, any attitude (roll U[-180, 180], pitch U[-89, 89], heading
+    U[0, 360] deg: a uniformly random direction of the body axes' Euler parameterisation),
+    alpha U[-10, 40] and beta U[-25, 25] deg (inside the aero tables' breakpoints, so the
+    quaternion and velocity agree on them), fuel U[0.2, 1] of full.  Returns (2*nenv, 10) IC
+    rows; the device seeding (f16_seed_batch) turns them into consistent 101-value states."""
+    rng = np.random.default_rng(seed)
+    n = 2 * nenv
+    north = 3500.0 + rng.uniform(-20000.0, 20000.0, n)
+    east = rng.uniform(-20000.0, 20000.0, n)
+    alt = rng.uniform(500.0, 12000.0, n)
+    spd = rng.uniform(100.0, 350.0, n)
+    phi = rng.uniform(-180.0, 180.0, n)
+    theta = rng.uniform(-89.0, 89.0, n)
+    psi = rng.uniform(0.0, 360.0, n)
+    alpha = rng.uniform(-10.0, 40.0, n)
+    beta = rng.uniform(-25.0, 25.0, n)
+    fuel = rng.uniform(0.2, 1.0, n) * fuel_lbs
+    la, lo, h = ned_to_geodetic(north, east, -alt)
+    rows = np.zeros((n, 10))
+    rows[:, 0], rows[:, 1], rows[:, 2], rows[:, 3] = la, lo, h, spd * M2FT
+    rows[:, 4], rows[:, 5], rows[:, 6] = phi, theta, psi
+    rows[:, 7], rows[:, 8], rows[:, 9] = alpha, beta, fuel
+    return rows
+
+
 def action_grid(num_bins=21):
     """linspace(-1, 1, num_bins) (ppo_gpu.py:178-181)."""
     return np.linspace(-1.0, 1.0, num_bins)

@@ -36,10 +36,31 @@ def _flop_per_substep(sample="c2_tailchase"):
 
 
 FLOP_PER_SUBSTEP = _flop_per_substep()
+# Algorithmic HBM bytes of one aircraft per launch of the flight model: the 66 state doubles a
+# launch reads, the 101 it writes, and its 4 action doubles
+FDM_BYTES_PER_AIRCRAFT = (66 + 101 + 4) * 8
 PEAK_FP64_TFLOPS = 78.6
 PEAK_HBM_GBS = 8000.0
 # reference's published GpuDogfight.step rate at 16k envs (RTX 3070 Ti, cuda_fdm/README.md:130)
 REF_PUBLISHED_SUBSTEPS = 37.0e6
+
+
+def _regions(run, reps, reset=None):
+    """Time `run` (one region of GPU work on the current stream) `reps` times with HIP events
+    on that stream, `reset` (untimed) before each; returns the per-region milliseconds."""
+    import torch
+    out = []
+    for _ in range(reps):
+        if reset is not None:
+            reset()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        run()
+        e1.record()
+        torch.cuda.synchronize()
+        out.append(e0.elapsed_time(e1))
+    return out
 
 
 def profiled_traffic(name="fdm_step_quad_kernel_tailchase16k.md"):
@@ -131,17 +152,24 @@ def cpu_baseline(states0_aos, actions_host, substeps, cpu_seconds, icm):
         dt = time.perf_counter() - t0
         if dt >= cpu_seconds:
             break
-    n1 = min(nac, 256)
+    # one thread: the first 1,024 aircraft, decisions cycled for at least 2 s
+    n1 = min(nac, 1024)
     st1 = np.ascontiguousarray(states0_aos[:n1])
-    a1 = np.ascontiguousarray(actions_host[:1, :n1])
-    t1 = time.perf_counter()
-    run(st1, a1, n1, 1, 1)
-    dt1 = time.perf_counter() - t1
+    a1 = np.ascontiguousarray(actions_host[:, :n1])
+    nd1, t1 = 0, time.perf_counter()
+    while True:
+        run(st1, a1, n1, a1.shape[0], 1)
+        nd1 += a1.shape[0]
+        dt1 = time.perf_counter() - t1
+        if dt1 >= 2.0:
+            break
     out = {"value": nac * substeps * ndec / dt, "unit": "aircraft-substeps/s", "cores": cores,
            "kind": kind,
            "sample": f"{nac} aircraft x {ndec} decisions x {substeps} substeps, fp64, OpenMP "
                      f"over aircraft on {cores} host threads ({dt:.1f} s)",
-           "single_thread": n1 * substeps / dt1}
+           "single_thread": n1 * substeps * nd1 / dt1,
+           "single_thread_sample": f"{n1} aircraft x {nd1} decisions x {substeps} substeps on "
+                                   f"one thread ({dt1:.1f} s)"}
     out.update(_host_info())
     orc = oracle_lib.load()
     # C1 in full: 128 aircraft x 600 decisions, seeded by the C restatement
@@ -227,6 +255,10 @@ POST_BYTES_SCAN_EXTRA = 86 * 8 - 1
 # 4 actions read) and the post-physics step's, less the 15 state doubles the post-physics phase
 # reads back from L2 (the same workgroup stored them)
 STEP_BYTES_PER_AIRCRAFT = (66 + 101 + 4) * 8 + POST_BYTES_PER_AIRCRAFT - 15 * 8
+# The 214-D post-physics launch of the league rollout: the 184-D bytes, 30 more float32
+# columns in each of the two observation rows, the previous NED velocity read and it and the
+# acceleration written (9 doubles), and the opponent draw's id written on autoreset (ignored)
+POST_BYTES_214_PER_AIRCRAFT = POST_BYTES_PER_AIRCRAFT + 2 * 30 * 4 + 9 * 8
 # reference's published full env step at 16,384 envs: 10.3 ms (RTX 3070 Ti,
 # cuda_fdm/README.md:225) = 1.59 M env transitions/s
 REF_PUBLISHED_ENV_TRANSITIONS = 16384 / 10.3e-3
@@ -272,7 +304,7 @@ ENV_VARIANTS = {"one_launch": (True, True), "two_launch": (False, True),
 
 
 def env_step_bench(pkg, nenv, steps, warmup, scan_finite=False, ab=True, stagger=True,
-                   pool_tables=True, two_launch=False):
+                   pool_tables=True, two_launch=False, reps=5):
     """Full environment transitions: GpuDogfightVecEnv.step = FDM decision (6 substeps, FCS 60 Hz)
     + the fused post-physics step (advance, reward, termination, terminal observation, pool
     autoreset, new observation), contest ICs with the staggered reset spread over the whole
@@ -296,29 +328,33 @@ def env_step_bench(pkg, nenv, steps, warmup, scan_finite=False, ab=True, stagger
     acts[..., 3] = (acts[..., 3] + 1) / 2
     snap_states = env.sim.states.clone()
     snap_obr = env.obr.clone_state()
+    snap_steps = env._post_steps
     post_bytes = POST_BYTES_PER_AIRCRAFT * 2 * nenv
     if ab:
-        # mirrored order: whichever variant runs first after the warm-up pays for it
+        # mirrored order: whichever variant runs first after the warm-up pays for it; the
+        # default variant then runs to `reps` regions in all
         order = ("one_launch", "two_launch", "state_scan", "state_scan", "two_launch",
-                 "one_launch")
+                 "one_launch") + ("one_launch",) * max(0, reps - 2)
     else:
-        order = ("state_scan",) if scan_finite else ("two_launch",) if two_launch else \
-            ("one_launch",)
+        order = (("state_scan",) if scan_finite else ("two_launch",) if two_launch else
+                 ("one_launch",)) * reps
     runs = {}
     for name in order:
         env.fused_step, env.fused_finite = ENV_VARIANTS[name]
         env.sim.states.copy_(snap_states)        # every variant steps the same engagements
         env.obr.restore(snap_obr)
+        env._post_steps = snap_steps
         ms, done, host = _env_timed(env, acts, warmup, steps)
         runs.setdefault(name, []).append((ms, done) + _env_kernel_ms(env, acts, warmup,
                                                                        min(steps, 20)) + (host,))
     env.fused_step, env.fused_finite = ENV_VARIANTS["one_launch"]
     res = {}
     for name, r in runs.items():
-        avg = lambda i: None if r[0][i] is None else float(np.mean([x[i] for x in r]))
-        ms, done, fdm_ms, post_ms, step_ms, host = (avg(i) for i in range(6))
+        med = lambda i: None if r[0][i] is None else float(np.median([x[i] for x in r]))
+        ms, done, fdm_ms, post_ms, step_ms, host = (med(i) for i in range(6))
         res[name] = {"ms_per_step": ms, "episodes_done": int(round(done)),
-                     "host_issue_ms_per_step": host}
+                     "host_issue_ms_per_step": host, "regions": len(r),
+                     "ms_per_step_regions": [x[0] for x in r]}
         if step_ms is not None:
             res[name]["step_kernel_ms"] = step_ms
         else:
@@ -365,7 +401,73 @@ def env_step_bench(pkg, nenv, steps, warmup, scan_finite=False, ab=True, stagger
 PEAK_BF16_TFLOPS = 2500.0
 
 
-def rollout_bench(nenv, T=64, reps=2, stagger=True):
+def obs_reward_c3_bench(nenv=16384, steps=50, reps=5):
+    """BASELINE C3, the fused observation/reward kernel alone: 16,384 engagements whose
+    aircraft hold random valid states (ic.sample_random_valid: +-20 km, 100-350 m/s, any
+    attitude, alpha/beta inside the tables, fuel U[0.2, 1]), a fresh reconstructor anchored on
+    them, random actions.  The timed launch is f16_env_post_step without a physics launch
+    before it: advance (action history, damage, HP, fuel, body rates, time), reward and
+    termination for both aircraft, terminal and new 184-D observations and autoreset from the
+    IC pool; with no physics launch to hand over the finite flags, it tests the state itself
+    (reads all 101 doubles).  `steps` launches per region on the same states (regions start
+    from the same reconstructor), median of `reps` regions."""
+    import torch
+    env_mod = importlib.import_module(PKG + ".rl_env")
+    icm = importlib.import_module(PKG + ".ic")
+    env = env_mod.GpuDogfightVecEnv(nenv, seed=0)
+    env.reset(stagger=False)
+    env.sim.seed_rows(torch.as_tensor(icm.sample_random_valid(nenv, seed=3), device="cuda"))
+    env.obr.reset_all()
+    env.obr.kernel_init_reward_state(env.sim.states)
+    env._ensure_ic_pool()
+    nac = env.nac
+    g = torch.Generator(device="cuda").manual_seed(3)
+    a = torch.rand(nac, 4, generator=g, device="cuda", dtype=torch.float64) * 2 - 1
+    a[:, 3] = (a[:, 3] + 1) / 2
+    env.sim.actions.copy_(a)
+    snap, snap_obr, snap_steps = env.sim.states.clone(), env.obr.clone_state(), env._post_steps
+    f64, b = dict(dtype=torch.float64, device="cuda"), dict(dtype=torch.bool, device="cuda")
+    reward, thp, talt = (torch.empty(nac, **f64) for _ in range(3))
+    tobs = torch.empty(nac, 184, dtype=torch.float32, device="cuda")
+    term, trunc, done, fin = (torch.empty(nenv, **b) for _ in range(4))
+    io = env._io(None)
+    io.reward, io.terminal_obs = reward.data_ptr(), tobs.data_ptr()
+    io.terminal_hp, io.terminal_alt_m = thp.data_ptr(), talt.data_ptr()
+    io.term, io.trunc, io.done, io.terminal_finite = (t.data_ptr() for t in (term, trunc, done, fin))
+    io.state_finite = None
+    env._call_tensors = ()
+
+    def run():
+        for _ in range(steps):
+            env._post(io)
+
+    def reset():
+        env.sim.states.copy_(snap)
+        env.obr.restore(snap_obr)
+        env._post_steps = snap_steps
+    reset()
+    run()                                              # warm-up
+    ms = _regions(run, reps, reset)
+    reset()
+    env.kernel_events = []
+    run()
+    torch.cuda.synchronize()
+    kms = float(np.median([x.elapsed_time(y) for x, y in env.kernel_events]))
+    env.kernel_events = None
+    done_n = int(done.sum().item())
+    m = float(np.median(ms)) / steps
+    byt = (POST_BYTES_PER_AIRCRAFT + POST_BYTES_SCAN_EXTRA) * nac
+    return {"workload": "obs_reward_c3_random_16k", "engagements": nenv, "obs_dim": 184,
+            "kernel": "env_post_step_split_kernel<184,true>", "launches_per_region": steps,
+            "regions": reps, "ms_per_launch": m, "ms_per_launch_regions": [x / steps for x in ms],
+            "kernel_ms_per_launch_events": kms,
+            "engagements_per_s": nenv / (m * 1e-3), "aircraft_per_s": nac / (m * 1e-3),
+            "algorithmic_bytes": byt, "achieved_GBs": byt / (m * 1e-3) / 1e9,
+            "frac_hbm_peak": byt / (m * 1e-3) / 1e9 / PEAK_HBM_GBS,
+            "episodes_done_last_launch": done_n}
+
+
+def rollout_bench(nenv, T=64, reps=5, stagger=True):
     """BASELINE C4: nenv engagements x T-step self-play rollout (FDM + fused obs/reward + norm
     update + fused bf16 actor/critic with Philox draw) then GAE (gamma 0.99, lambda 0.95) over
     [T, nenv, 2].  Weights N(0, 0.02), draw seed 0.  The collector records the rollout as a HIP
@@ -387,16 +489,15 @@ def rollout_bench(nenv, T=64, reps=2, stagger=True):
     ro = make(True)
     ro.collect()                                    # eager warm-up (allocations)
     ro.collect()                                    # records the graph, replays it
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(reps):
-        adv, ret, stats = ro.collect()
-    e1.record()
-    torch.cuda.synchronize()
+    res = {}
+
+    def one():
+        res["out"] = ro.collect()
+    regions = _regions(one, reps)
+    adv, ret, stats = res["out"]
     if not bool(stats["trajectory_finite"]) or not bool(torch.isfinite(adv).all()):
         raise FloatingPointError("non-finite rollout")
-    ms = e0.elapsed_time(e1) / reps
+    ms = float(np.median(regions))
     done = float(ro.b_done[1:].sum().item() + ro.next_done.sum().item())
     del ro
     eager = make(False)
@@ -412,7 +513,8 @@ def rollout_bench(nenv, T=64, reps=2, stagger=True):
     return {"workload": "selfplay_rollout_16k_T64", "engagements": nenv, "T": T,
             "reset": f"stagger over {STAGGER_STEPS} decisions" if stagger else "no stagger",
             "episodes_done_per_rollout": done,
-            "hip_graph": True, "ms_per_rollout": ms, "eager_ms_per_rollout": eager_ms,
+            "hip_graph": True, "ms_per_rollout": ms, "ms_per_rollout_regions": regions,
+            "eager_ms_per_rollout": eager_ms,
             "transitions_per_s": nenv * T / (ms * 1e-3),
             "aircraft_transitions_per_s": 2 * nenv * T / (ms * 1e-3),
             "policy_kernel_ms": pol_ms,
@@ -422,7 +524,7 @@ def rollout_bench(nenv, T=64, reps=2, stagger=True):
                             "frac": flop / (pol_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS}}
 
 
-def update_bench(nenv, T=64, reps=2):
+def update_bench(nenv, T=64, reps=5):
     """The PPO update after a BASELINE C4 rollout (PPOGPUTrainer.update, ppo_gpu.py:2019-2145):
     both aircraft's transitions (T x 2 nenv), the reference's PPOConfig (clip 0.2, 8 minibatches,
     Adam 3e-4 / eps 1e-5, max grad norm 0.5) with all 4 epochs (no KL early stop, so every run
@@ -441,14 +543,13 @@ def update_bench(nenv, T=64, reps=2):
     adv, ret, _ = ro.collect()
     up = U.PPOUpdater(net, U.UpdateConfig(target_kl=None), seed=0)
     up.update(ro, adv, ret)                         # warm-up (workspace allocation)
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(reps):
-        res = up.update(ro, adv, ret)
-    e1.record()
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / reps
+    hold = {}
+
+    def one():
+        hold["res"] = up.update(ro, adv, ret)
+    regions = _regions(one, reps)
+    res = hold["res"]
+    ms = float(np.median(regions))
     # one epoch with events around each call
     obs, act = ro.b_obs.flatten(0, 1), ro.b_act.flatten(0, 1)
     logp, a, r = ro.b_logp.flatten(), adv.reshape(-1), ret.reshape(-1)
@@ -472,6 +573,7 @@ def update_bench(nenv, T=64, reps=2):
         raise FloatingPointError("non-finite parameters after the update")
     return {"workload": "ppo_update_selfplay_16k_T64", "transitions": count, "epochs": res["epochs"],
             "minibatches": (count + mb - 1) // mb, "minibatch_rows": mb, "ms_per_update": ms,
+            "ms_per_update_regions": regions,
             "transitions_per_s": count * res["epochs"] / (ms * 1e-3),
             "minibatch_grad_ms": grad_ms, "optimizer_step_ms": adam_ms,
             "mfma": {"what": "f16_ppo_grad (all its launches)", "flop_per_minibatch": flop_mb,
@@ -481,7 +583,7 @@ def update_bench(nenv, T=64, reps=2):
             "stats": {k: float(res[k]) for k in ("pl", "vl", "ent", "kl", "cf", "ev")}}
 
 
-def league_bench(nenv=65536, T=128, nopp=8, reps=2):
+def league_bench(nenv=65536, T=128, nopp=8, reps=5):
     """BASELINE C5: nenv engagements x T-step league rollout with the 214-D observation: the
     learner (plane 0) and 8 frozen random-init opponents (plane 1, bf16 N(0, 0.02)) assigned per
     engagement from Zipf(1.1) weights, evaluated as one grouped launch; fuel exhaustion and
@@ -505,16 +607,15 @@ def league_bench(nenv=65536, T=128, nopp=8, reps=2):
     ro = make(True)
     ro.collect()
     ro.collect()
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(reps):
-        adv, ret, stats = ro.collect()
-    e1.record()
-    torch.cuda.synchronize()
+    res = {}
+
+    def one():
+        res["out"] = ro.collect()
+    regions = _regions(one, reps)
+    adv, ret, stats = res["out"]
     if not bool(stats["trajectory_finite"]) or not bool(torch.isfinite(adv).all()):
         raise FloatingPointError("non-finite league rollout")
-    ms = e0.elapsed_time(e1) / reps
+    ms = float(np.median(regions))
     done = float(ro.b_done[1:].sum().item() + ro.next_done.sum().item())
     del ro
     eager = make(False)
@@ -528,16 +629,128 @@ def league_bench(nenv=65536, T=128, nopp=8, reps=2):
     eager.collect()
     torch.cuda.synchronize()
     avg = lambda ev: float(np.mean([a.elapsed_time(b) for a, b in ev]))
+    nac = 2 * nenv
+    fdm_ms, post_ms = avg(env.sim.kernel_events), avg(env.kernel_events)
+    lp_ms, op_ms = avg(eager.policy_events), avg(eager.opp_events)
+    fdm_flop = _flop_per_substep("contest_60hz") * nac * env.substeps
+    post_b = POST_BYTES_214_PER_AIRCRAFT * nac
+    pol_flop = ppo.POLICY_FLOP_PER_ROW[214] * nenv
+    opp_flop = (ppo.POLICY_FLOP_PER_ROW[214] - 2 * (256 * 214 + 256 * 256 + 256)) * nenv
+    kernels = {
+        "fdm": {"kernel": "fdm_step_quad_kernel<60, false, 2>", "ms": fdm_ms,
+                "flop": fdm_flop, "achieved_TFLOPs": fdm_flop / (fdm_ms * 1e-3) / 1e12,
+                "frac_fp64_peak": fdm_flop / (fdm_ms * 1e-3) / 1e12 / PEAK_FP64_TFLOPS},
+        "post": {"kernel": "env_post_step_split_kernel<214, false>", "ms": post_ms,
+                 "algorithmic_bytes": post_b, "achieved_GBs": post_b / (post_ms * 1e-3) / 1e9,
+                 "frac_hbm_peak": post_b / (post_ms * 1e-3) / 1e9 / PEAK_HBM_GBS},
+        "learner_policy": {"kernel": "policy_kernel (actor + critic, plane 0)", "ms": lp_ms,
+                           "flop": pol_flop, "achieved_TFLOPs": pol_flop / (lp_ms * 1e-3) / 1e12,
+                           "frac_bf16_peak": pol_flop / (lp_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS},
+        "opponents_policy": {"kernel": "policy_kernel (8 grouped actors, plane 1)", "ms": op_ms,
+                             "flop": opp_flop,
+                             "achieved_TFLOPs": opp_flop / (op_ms * 1e-3) / 1e12,
+                             "frac_bf16_peak": opp_flop / (op_ms * 1e-3) / 1e12 /
+                             PEAK_BF16_TFLOPS}}
     out = {"workload": "league_rollout_64k_T128_214d_8opp", "engagements": nenv, "T": T,
            "opponents": nopp, "opponent_weights": "zipf(1.1)", "hip_graph": True,
-           "ms_per_rollout": ms, "transitions_per_s": nenv * T / (ms * 1e-3),
+           "ms_per_rollout": ms, "ms_per_rollout_regions": regions,
+           "transitions_per_s": nenv * T / (ms * 1e-3),
            "aircraft_transitions_per_s": 2 * nenv * T / (ms * 1e-3),
-           "learner_policy_ms": avg(eager.policy_events), "opponents_policy_ms": avg(eager.opp_events),
-           "fdm_kernel_ms": avg(env.sim.kernel_events), "post_kernel_ms": avg(env.kernel_events),
+           "learner_policy_ms": lp_ms, "opponents_policy_ms": op_ms,
+           "fdm_kernel_ms": fdm_ms, "post_kernel_ms": post_ms, "kernels": kernels,
            "episodes_done_per_rollout": done,
            "streams": "opponents' grouping + launch on a second stream beside the learner's "
                       "normalisation + launch (the policy times overlap)"}
     return out
+
+
+def fdm_section(pkg, icm, nenv, S, steps, warmup, reps, label, check_replay=True,
+                require_finite=True):
+    """The batched flight model alone: nenv tail-chase engagements (BASELINE configs[1]
+    initial conditions), random 21-bin actions held per decision, `steps` decisions of S
+    substeps per timed region, inputs resident in HBM.  Each region is timed `reps` times
+    (median reported):
+      graph  -- the `steps` GpuDogfight.step launches recorded once as a HIP graph and
+                replayed: one launch per step back to back, the kernel's own rate;
+      eager  -- the same steps as Python calls of GpuDogfight.step (each also validates its
+                arguments and records its tensors' stream use on the host).
+    A third pass with HIP events around each launch gives the launch duration on its own and
+    checks that it reproduces the eager region's states bit for bit.  Every region starts from
+    the same states (those after the warm-up decisions), so all regions time one trajectory."""
+    import torch
+    nac = 2 * nenv
+    sim = pkg.GpuDogfight(nenv, substeps=S, fcs_rate=120)
+    sim.seed_rows(torch.as_tensor(icm.sample_tailchase(nenv, seed=0), device="cuda"))
+    acts_host = icm.random_bin_actions(warmup + steps, nac, seed=0)
+    acts = torch.as_tensor(acts_host, device="cuda").contiguous()
+    torch.cuda.synchronize()
+    states0 = sim.states.cpu().numpy().copy()
+    for k in range(warmup):
+        sim.step(acts[k], want_obs=False)
+    torch.cuda.synchronize()
+    snap = sim.states.clone()
+
+    def eager():
+        for k in range(steps):
+            sim.step(acts[warmup + k], want_obs=False)
+
+    def reset():
+        sim.states.copy_(snap)
+    t0 = time.perf_counter()
+    eager_ms = _regions(eager, reps, reset)
+    wall = (time.perf_counter() - t0) / reps
+    nonfinite = int((~torch.isfinite(sim.states).all(1)).sum())
+    if require_finite and nonfinite:
+        raise FloatingPointError("non-finite state after the timed steps")
+    out = {"workload": label, "engagements": nenv, "aircraft": nac, "substeps_per_step": S,
+           "fcs_rate_hz": 120, "steps_per_region": steps, "regions": reps}
+    if check_replay:
+        # the launch on its own: one region again from the snapshot, events around each launch
+        sim.states.copy_(snap)
+        eager()
+        after = sim.states.clone()
+        sim.states.copy_(snap)
+        sim.kernel_events = []
+        eager()
+        torch.cuda.synchronize()
+        kev, sim.kernel_events = sim.kernel_events, None
+        if not torch.equal(sim.states.view(torch.int64), after.view(torch.int64)):
+            raise RuntimeError("the instrumented pass did not reproduce the timed steps")
+        out["kernel_ms_per_launch_events"] = float(np.median([a.elapsed_time(b) for a, b in kev]))
+    # the same steps recorded as a HIP graph
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(g, stream=side):
+            eager()
+    torch.cuda.current_stream().wait_stream(side)
+    graph_ms = _regions(g.replay, reps, reset)
+    end = sim.states.clone()
+    sim.states.copy_(snap)
+    eager()
+    if not torch.equal(sim.states.view(torch.int64), end.view(torch.int64)):
+        raise RuntimeError("the graph replay did not reproduce the eager steps")
+    del g
+    gm, em = float(np.median(graph_ms)) / steps, float(np.median(eager_ms)) / steps
+    flop = FLOP_PER_SUBSTEP * nac * S
+    out.update({
+        "nonfinite_aircraft_after_region": nonfinite,
+        "ms_per_step": gm, "aircraft_substeps_per_s": nac * S / (gm * 1e-3),
+        "graph_ms_per_step_regions": [x / steps for x in graph_ms],
+        "eager_ms_per_step": em, "eager_aircraft_substeps_per_s": nac * S / (em * 1e-3),
+        "eager_ms_per_step_regions": [x / steps for x in eager_ms],
+        "eager_host_ms_per_step": wall * 1e3 / steps,
+        "flop_per_launch": flop,
+        "achieved_TFLOPs": flop / (gm * 1e-3) / 1e12,
+        "frac_fp64_peak": flop / (gm * 1e-3) / 1e12 / PEAK_FP64_TFLOPS,
+        "algorithmic_bytes": FDM_BYTES_PER_AIRCRAFT * nac,
+        "achieved_GBs": FDM_BYTES_PER_AIRCRAFT * nac / (gm * 1e-3) / 1e9})
+    out["frac_hbm_peak"] = out["achieved_GBs"] / PEAK_HBM_GBS
+    out["_states0"] = states0
+    out["_acts_host"] = acts_host[warmup:]
+    return out
+
 
 
 def main():
@@ -545,6 +758,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--reps", type=int, default=5,
+                    help="timed regions per section; each section reports the median")
     ap.add_argument("--nenv", type=int, default=16384)
     ap.add_argument("--substeps", type=int, default=6)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -563,7 +778,8 @@ def main():
     ap.add_argument("--rebuild-resets", action="store_true",
                     help="with --only env: autoresets rebuild their rows instead of copying the "
                          "pool tables (profiling aid)")
-    ap.add_argument("--only", choices=["fdm", "env", "rollout", "league", "update"], default=None,
+    ap.add_argument("--only", choices=["fdm", "env", "c3", "rollout", "league", "update"],
+                    default=None,
                     help="profiling aid: run only this section and print its own JSON line "
                          "(not the contract line)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -589,78 +805,46 @@ def main():
     sys.path.insert(0, ROOT)
     pkg = importlib.import_module(PKG)
     icm = importlib.import_module(PKG + ".ic")
-    if args.only in ("env", "rollout", "league", "update"):
+    if args.only in ("env", "c3", "rollout", "league", "update"):
         part = {"env": lambda: env_step_bench(pkg, args.nenv, args.steps, args.warmup,
                                               scan_finite=args.scan_finite, ab=False,
                                               stagger=not args.no_stagger,
                                               pool_tables=not args.rebuild_resets,
-                                              two_launch=args.two_launch),
-                "rollout": lambda: rollout_bench(args.nenv, stagger=not args.no_stagger),
-                "league": lambda: league_bench(),
-                "update": lambda: update_bench(args.nenv)}[args.only]()
+                                              two_launch=args.two_launch, reps=args.reps),
+                "c3": lambda: obs_reward_c3_bench(args.nenv, args.steps, args.reps),
+                "rollout": lambda: rollout_bench(args.nenv, reps=args.reps,
+                                                 stagger=not args.no_stagger),
+                "league": lambda: league_bench(reps=args.reps),
+                "update": lambda: update_bench(args.nenv, reps=args.reps)}[args.only]()
         print(json.dumps(part), flush=True)
         return
 
     nenv, S = args.nenv, args.substeps
     nac = 2 * nenv
-    sim = pkg.GpuDogfight(nenv, substeps=S, fcs_rate=120)
-    ic = icm.sample_tailchase(nenv, seed=0)
-    sim.seed_rows(torch.as_tensor(ic, device="cuda"))
-    ndec = args.warmup + args.steps
-    acts_host = icm.random_bin_actions(ndec, nac, seed=0)
-    acts = torch.as_tensor(acts_host, device="cuda").contiguous()
-    torch.cuda.synchronize()
-    states0 = sim.states.cpu().numpy().copy()
-
-    for k in range(args.warmup):
-        sim.step(acts[k], want_obs=False)
-    torch.cuda.synchronize()
-    snap = sim.states.clone()
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    # the timed region: bare GpuDogfight.step calls (the reference's step: the actions copied
-    # into sim.actions, then the launch), nothing else recorded on the stream
-    t0 = time.perf_counter()
-    e0.record()
-    for k in range(args.steps):
-        sim.step(acts[args.warmup + k], want_obs=False)
-    e1.record()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    ms_step = e0.elapsed_time(e1) / args.steps
-    if not bool(torch.isfinite(sim.states).all()):
-        raise FloatingPointError("non-finite state after the timed steps")
-    # the kernel's own launch times: the same steps again from the same states, with HIP
-    # events around each launch on its stream
-    after = sim.states.clone()
-    sim.states.copy_(snap)
-    sim.kernel_events = []
-    for k in range(args.steps):
-        sim.step(acts[args.warmup + k], want_obs=False)
-    torch.cuda.synchronize()
-    kev, sim.kernel_events = sim.kernel_events, None
-    kern_ms = float(np.mean([s.elapsed_time(e) for s, e in kev]))
-    if not torch.equal(sim.states.view(torch.int64), after.view(torch.int64)):
-        raise RuntimeError("the instrumented pass did not reproduce the timed steps")
-
+    head = fdm_section(pkg, icm, nenv, S, args.steps, args.warmup, args.reps, "fdm_tailchase_16k")
+    states0, acts_host = head.pop("_states0"), head.pop("_acts_host")
     if args.only == "fdm":
-        print(json.dumps({"workload": "fdm_tailchase_16k", "fdm_kernel_ms": kern_ms,
-                          "ms_per_step": ms_step}), flush=True)
+        print(json.dumps(head), flush=True)
         return
-    env_line = env_step_bench(pkg, nenv, args.steps, args.warmup)
+    # the other named sizes of the flight model: BASELINE C2 (4,096 tail-chase engagements,
+    # its 1,000 decisions as one region) and C5's 65,536 engagements
+    sizes = {}
+    for ne, steps, label in ((4096, 1000, "fdm_c2_tailchase_4k_1000dec"),
+                             (65536, args.steps, "fdm_tailchase_64k")):
+        # C2 has no termination: over 1,000 decisions some aircraft fly into the ground and
+        # past the model's range (counted in nonfinite_aircraft_after_region)
+        r = fdm_section(pkg, icm, ne, S, steps, args.warmup, args.reps, label,
+                        check_replay=False, require_finite=ne != 4096)
+        r.pop("_states0"), r.pop("_acts_host")
+        sizes[label] = r
+    env_line = env_step_bench(pkg, nenv, args.steps, args.warmup, reps=args.reps)
+    c3_line = obs_reward_c3_bench(nenv, args.steps, args.reps)
     rollout_line = None if args.no_rollout else rollout_bench(nenv)
     league_line = None if args.no_league else league_bench()
     update_line = None if args.no_update else update_bench(nenv)
 
-    value = nac * S / (ms_step * 1e-3)
-    flop_launch = FLOP_PER_SUBSTEP * nac * S
-    # the timed region holds exactly one launch per step (GpuDogfight.step folds the actions
-    # copy into the launch), so its HIP events over the region / steps are the launch's average
-    # duration, gaps between launches included; the per-launch events of the second pass add
-    # their own records to each interval and are reported beside it
-    launch_ms = ms_step
-    achieved = flop_launch / (launch_ms * 1e-3) / 1e12
+    value = head["aircraft_substeps_per_s"]
+    ms_step = head["ms_per_step"]
     line = {
         "metric": "aircraft FDM substeps/s + env transitions/s at 16k engagements; % vector roofline",
         "value": value,
@@ -668,6 +852,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "regions": args.reps,
         "ms_per_step": ms_step,
         "higher_is_better": True,
         "scaling": "weak",
@@ -678,25 +863,31 @@ def main():
                    "substeps_per_step": S, "fcs_rate_hz": 120,
                    "actions": "i.i.d. uniform 21-bin per channel, held per decision",
                    "obs17": "not written (want_obs=False); the reference's kernel always "
-                            "writes the 17-value output"},
+                            "writes the 17-value output",
+                   "timing": f"median of {args.reps} regions of {args.steps} steps, the steps "
+                             "recorded once as a HIP graph and replayed (eager Python calls "
+                             "reported beside it in fdm)"},
+        "fdm": head,
+        "fdm_sizes": sizes,
         "env_transitions_per_s": env_line["transitions_per_s"],
         "env_step": env_line,
+        "obs_reward_c3": c3_line,
         "rollout": rollout_line,
         "league": league_line,
         "ppo_update": update_line,
-        "roofline": {"bound": "valu", "achieved": achieved, "peak": PEAK_FP64_TFLOPS,
-                     "unit": "TFLOP/s", "frac": achieved / PEAK_FP64_TFLOPS, "traffic": profiled_traffic(),
-                     "kernel": "fdm_step_quad_kernel<120, false>", "kernel_ms": launch_ms,
-                     "kernel_ms_source": "HIP events around the timed region / steps (one launch "
-                                         "per step)",
-                     "kernel_ms_per_launch_events": kern_ms,
-                     "flop_per_launch": flop_launch, "flop_per_substep": FLOP_PER_SUBSTEP,
+        "roofline": {"bound": "valu", "achieved": head["achieved_TFLOPs"],
+                     "peak": PEAK_FP64_TFLOPS, "unit": "TFLOP/s",
+                     "frac": head["frac_fp64_peak"], "traffic": profiled_traffic(),
+                     "kernel": "fdm_step_quad_kernel<120, false, 2>", "kernel_ms": ms_step,
+                     "kernel_ms_source": "HIP events around each graph replay of one launch per "
+                                         "step, / steps; median of the regions",
+                     "kernel_ms_per_launch_events": head.get("kernel_ms_per_launch_events"),
+                     "flop_per_launch": head["flop_per_launch"],
+                     "flop_per_substep": FLOP_PER_SUBSTEP,
                      "flop_source": "op-counted CPU restatement, tests/golden/fdm_flops.json"},
-        "wall_s": wall,
     }
     if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(states0, acts_host[args.warmup:], S, args.cpu_seconds,
-                                            icm)
+        line["cpu_baseline"] = cpu_baseline(states0, acts_host, S, args.cpu_seconds, icm)
     print(json.dumps(line), flush=True)
 
 

@@ -256,13 +256,14 @@ def test_independence_and_determinism(gpu):
 
 @pytest.mark.parametrize("rate", [120, 60])
 @pytest.mark.parametrize("nenv,S,pad", [(4096, 6, 0), (77, 1, 0), (77, 2, 5), (1000, 3, 0),
-                                        (1, 6, 3), (300, 0, 0)])
+                                        (1, 6, 3), (300, 0, 0), (16384, 6, 0), (16450, 2, 3)])
 def test_split_kernel_equals_onelane(gpu, rate, nenv, S, pad):
     """The production step spreads each substep over four wavefronts that trade values through
     LDS, the two-wave kernel over two; the one-lane kernel runs the same component functions in
     sequence.  All three agree bit for bit on states and outputs, for ragged batch sizes (lanes
     past the batch), short substep counts (history shifting), a leading dimension larger than the
-    batch, and S = 0."""
+    batch, and S = 0.  Up to 16,383 engagements the four-wave kernel runs one 64-aircraft group
+    per workgroup (more CUs than two-group workgroups would fill), from 16,384 two groups."""
     icm = import_pkg("ic")
     L = import_pkg("_lib")
     nac = 2 * nenv
