@@ -11,6 +11,14 @@
   unpickles through an allow-list (plain containers and torch tensors only), never arbitrary
   code.
 * ``checkpoint_to_bundle``: R/cuda_fdm/gpu_ckpt_to_bundle.py for the 184-D MLP checkpoint.
+* ``runtime_state`` / ``restore_runtime``: the trainer's runtime half of the checkpoint
+  (R/cuda_fdm/ppo_gpu.py:2859-2921 ``_runtime_state`` / ``_restore_runtime``): simulator states,
+  actions and 17-value output, the reconstructor, the IC pool, the env's generators and draw
+  counter, the collector's next observation/done, step counter and episode bookkeeping, the
+  league's opponent assignment, the updater's minibatch generator, and the process RNGs, so
+  that a run resumed from the checkpoint collects exactly what the uninterrupted run does.
+  ``save_checkpoint(..., runtime=collector)`` stores it under ``runtime``;
+  ``load_checkpoint(..., runtime=collector)`` restores it.
 """
 import gzip
 import io
@@ -20,6 +28,7 @@ import os
 import pickle
 from pathlib import Path
 
+import numpy as np
 import torch
 
 from . import policy as _policy
@@ -94,8 +103,112 @@ def _split_params(updater):
     return ps[:6], ps[6:]
 
 
-def save_checkpoint(path, updater, norm=None, global_step=0, iteration=0, extra=None):
-    """The learner's checkpoint (model, both Adam states, norm, counters, cfg)."""
+# ---- runtime state (R/cuda_fdm/ppo_gpu.py:2859-2921)
+def _rng_np_to_saved(state):
+    """np.random.get_state() as plain data (torch.load(weights_only=True) reads no numpy)."""
+    name, keys, pos, has_gauss, cached = state
+    return {"name": name, "keys": torch.as_tensor(np.asarray(keys, dtype=np.int64)),
+            "pos": int(pos), "has_gauss": int(has_gauss), "cached_gaussian": float(cached)}
+
+
+def _rng_np_from_saved(d):
+    return (d["name"], d["keys"].numpy().astype(np.uint32), int(d["pos"]), int(d["has_gauss"]),
+            float(d["cached_gaussian"]))
+
+
+def runtime_state(collector, updater=None):
+    """Everything a collector (SelfPlayRollout / LeagueRollout) and its env carry from one
+    rollout to the next, as plain CPU tensors and Python data (the reference's _runtime_state
+    plus what this build's device-side draws key on: the env's post-physics step counter and
+    the collector's step counter)."""
+    env, sim, obr = collector.env, collector.env.sim, collector.env.obr
+    cpu = lambda t: t.detach().cpu().clone()
+    st = {
+        "sim": {"states": cpu(sim.states), "obs": cpu(sim.obs), "actions": cpu(sim.actions)},
+        "obr": {k: cpu(v) for k, v in obr.clone_state().items()},
+        "env": {"obs": cpu(env._obs), "ic_pool": None if env.ic_pool is None else cpu(env.ic_pool),
+                "post_steps": int(env._post_steps), "seed": int(env.seed),
+                "rng": env.rng.bit_generator.state,
+                "torch_gen": env.torch_gen.get_state().cpu().clone(),
+                "reward_mode": int(env.reward_mode), "alt_hunt_coef": float(env.alt_hunt_coef),
+                "opp_assign": None if env.opp_assign is None else cpu(env.opp_assign),
+                "opp_cdf": None if env.opp_cdf is None else cpu(env.opp_cdf),
+                "obs_dim": int(env.OBS_SIZE), "nenv": int(env.nenv)},
+        "trainer": {"next_done": cpu(collector.next_done),
+                    "global_step": int(collector.global_step),
+                    "has_next_obs": collector.next_obs is not None,
+                    "norm": {k: cpu(v) for k, v in collector.norm.state_dict().items()}},
+        "numpy_rng": _rng_np_to_saved(np.random.get_state()),
+        "torch_rng": torch.get_rng_state(),
+        "cuda_rng": (torch.cuda.get_rng_state(env.device) if env.device.type == "cuda"
+                     else None)}
+    for name in ("ep_ret", "ep_len"):
+        if hasattr(collector, name):
+            st["trainer"][name] = cpu(getattr(collector, name))
+    if hasattr(collector, "opp_norms"):
+        st["trainer"]["opp_norms"] = [{k: cpu(v) for k, v in n.state_dict().items()}
+                                      for n in collector.opp_norms]
+    if updater is not None:
+        st["updater_gen"] = updater.gen.get_state().cpu().clone()
+    _require_finite({"sim": st["sim"], "obr": st["obr"]}, "runtime state")
+    return st
+
+
+def restore_runtime(collector, state, updater=None):
+    """Restore a runtime_state into a collector built with the same sizes (the reference's
+    _restore_runtime): every buffer is written in place, so launches recorded in a HIP graph
+    keep their addresses; the IC pool is replaced, which rebuilds its autoreset tables."""
+    env, sim, obr = collector.env, collector.env.sim, collector.env.obr
+    e = state["env"]
+    if e["nenv"] != env.nenv or e["obs_dim"] != env.OBS_SIZE:
+        raise ValueError("runtime environment count or observation width mismatch")
+    _require_finite({"sim": state["sim"], "obr": state["obr"]}, "restored runtime")
+    dev = env.device
+    sim.states.copy_(state["sim"]["states"])
+    sim.obs.copy_(state["sim"]["obs"])
+    sim.actions.copy_(state["sim"]["actions"])
+    if "external_accel" in state["obr"]:
+        obr.enable_external_observations()
+    if "aux_features" in state["obr"]:
+        env.enable_aux_capture()
+    obr.restore({k: v.to(dev) for k, v in state["obr"].items()})
+    env._obs.copy_(e["obs"])
+    env.ic_pool = None if e["ic_pool"] is None else e["ic_pool"].to(dev).contiguous()
+    env._post_steps = int(e["post_steps"])
+    env.seed = int(e["seed"])
+    env.rng.bit_generator.state = e["rng"]
+    env.torch_gen.set_state(e["torch_gen"])
+    from .obs_reward import validate_reward_mode
+    env.reward_mode = validate_reward_mode(e["reward_mode"], e["alt_hunt_coef"])
+    env.alt_hunt_coef = float(e["alt_hunt_coef"])
+    if e["opp_assign"] is not None:
+        if env.opp_assign is None or env.opp_assign.shape != e["opp_assign"].shape:
+            raise ValueError("runtime league assignment does not match the collector")
+        env.opp_assign.copy_(e["opp_assign"])
+        env.opp_cdf.copy_(e["opp_cdf"])
+    t = state["trainer"]
+    collector.next_done.copy_(t["next_done"])
+    collector.global_step = int(t["global_step"])
+    collector.next_obs = env._obs.view(env.nac, env.OBS_SIZE) if t["has_next_obs"] else None
+    collector.norm.load_state_dict({k: v.to(dev) for k, v in t["norm"].items()})
+    for name in ("ep_ret", "ep_len"):
+        if name in t and hasattr(collector, name):
+            getattr(collector, name).copy_(t[name])
+    if "opp_norms" in t and hasattr(collector, "opp_norms"):
+        for n, sd in zip(collector.opp_norms, t["opp_norms"]):
+            n.load_state_dict({k: v.to(dev) for k, v in sd.items()})
+    if updater is not None and "updater_gen" in state:
+        updater.gen.set_state(state["updater_gen"])
+    np.random.set_state(_rng_np_from_saved(state["numpy_rng"]))
+    torch.set_rng_state(state["torch_rng"])
+    if state.get("cuda_rng") is not None and env.device.type == "cuda":
+        torch.cuda.set_rng_state(state["cuda_rng"], env.device)
+
+
+def save_checkpoint(path, updater, norm=None, global_step=0, iteration=0, extra=None,
+                    runtime=None):
+    """The learner's checkpoint (model, both Adam states, norm, counters, cfg); with
+    `runtime` (a collector), also its runtime state under "runtime" (ppo_gpu.py:2845-2846)."""
     from dataclasses import asdict
     actor, critic = _split_params(updater)
     na = updater.na
@@ -112,6 +225,8 @@ def save_checkpoint(path, updater, norm=None, global_step=0, iteration=0, extra=
             "global_step": int(global_step), "iteration": int(iteration), "cfg": cfg}
     if extra:
         ckpt.update(extra)
+    if runtime is not None:
+        ckpt["runtime"] = runtime_state(runtime, updater)
     _require_finite({k: ckpt[k] for k in ("model", "actor_opt", "critic_opt", "norm")},
                     "checkpoint learner")
     path = Path(path)
@@ -122,10 +237,11 @@ def save_checkpoint(path, updater, norm=None, global_step=0, iteration=0, extra=
     return path
 
 
-def load_checkpoint(path, updater, norm=None):
+def load_checkpoint(path, updater, norm=None, runtime=None):
     """Restore a checkpoint written by save_checkpoint (or the reference's, when its extra entries
     are plain data): parameters (through the flat master copy), Adam moments and step count,
-    RunningNorm; returns the checkpoint dict."""
+    RunningNorm; with `runtime` (a collector of the same sizes) and a stored runtime state, the
+    collector, its env and the RNGs too.  Returns the checkpoint dict."""
     ckpt = torch.load(path, map_location="cpu", weights_only=True)
     _require_finite({k: ckpt.get(k) for k in ("model", "actor_opt", "critic_opt", "norm")},
                     "loaded checkpoint")
@@ -143,6 +259,10 @@ def load_checkpoint(path, updater, norm=None):
     updater.pack()
     if norm is not None and ckpt.get("norm") is not None:
         norm.load_state_dict({k: v.to(norm.device) for k, v in ckpt["norm"].items()})
+    if runtime is not None:
+        if ckpt.get("runtime") is None:
+            raise ValueError("checkpoint holds no runtime state")
+        restore_runtime(runtime, ckpt["runtime"], updater)
     return ckpt
 
 

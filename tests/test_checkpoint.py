@@ -143,3 +143,83 @@ def test_checkpoint_round_trip_and_torch_adam_resume(gpu, tmp_path):
     assert meta["obs_normalization"]["count"] == 777.0
     net3, _ = C.load_bundle(b)
     assert all(torch.equal(net3.state_dict()[k], v.cpu()) for k, v in ck["model"].items())
+
+
+def _collector(gpu, kind, env_seed, graph):
+    """A small collector of `kind` ("selfplay": BASELINE C4's shape; "league": C5's with the
+    214-D observation, fuel exhaustion and three frozen opponents) whose env and learner are
+    seeded by env_seed (the opponents are the league's fixed pool)."""
+    E, P, R = import_pkg("rl_env").GpuDogfightVecEnv, import_pkg("policy"), import_pkg("ppo")
+    mk = lambda d, s: P.MLPActorCritic(d, init="normal", init_std=0.05,
+                                        generator=torch.Generator().manual_seed(s)).to(gpu)
+    if kind == "selfplay":
+        env = E(200, seed=env_seed, ic_pool_size=64, max_engage_time_s=2.0)
+        return R.SelfPlayRollout(env, mk(184, env_seed), T=8, seed=0, stats=False, graph=graph)
+    env = E(200, seed=env_seed, ic_pool_size=64, max_engage_time_s=2.0, obs_dim=214,
+            fuel_exhaustion=True, fuel_lbs_range=(30.0, 3000.0))
+    return R.LeagueRollout(env, mk(214, env_seed), [mk(214, 90 + k) for k in range(3)], T=8,
+                           seed=0, graph=graph)
+
+
+def _bits(t):
+    return t.contiguous().view(torch.int32 if t.element_size() == 4 else
+                               torch.int64 if t.element_size() == 8 else torch.uint8)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("kind,graph", [("selfplay", False), ("selfplay", True),
+                                        ("league", False)])
+def test_runtime_resume_is_bit_identical(gpu, tmp_path, kind, graph):
+    """The checkpoint's runtime half (R/cuda_fdm/ppo_gpu.py:2859-2921): a run saved after two
+    collect + update iterations and resumed into a fresh env, network, updater and collector --
+    built with other seeds, so every value has to come from the file -- collects the next
+    rollout bit for bit as the uninterrupted run does: observations, actions, log-probabilities,
+    rewards, values, done flags, advantages, returns, and the simulator and reconstructor state
+    after it (autoresets from the restored IC pool and its rebuilt tables, fuel exhaustion and
+    opponent redraws included)."""
+    C, U = import_pkg("checkpoint"), import_pkg("ppo_update")
+    ro = _collector(gpu, kind, 5, graph)
+    up = U.PPOUpdater(ro.net, U.UpdateConfig(target_kl=None, update_epochs=1), seed=3)
+    ro.reset(stagger=True, max_stagger_steps=20)
+    for _ in range(2):
+        adv, ret, _ = ro.collect()
+        up.update(ro, adv, ret)
+    path = C.save_checkpoint(tmp_path / "run.pt", up, ro.norm, global_step=ro.global_step,
+                             iteration=2, runtime=ro)
+    adv, ret, _ = ro.collect()
+    want = {n: getattr(ro, n).clone() for n in ("b_obs", "b_act", "b_logp", "b_rew", "b_val",
+                                                "b_done", "next_done")}
+    want.update(adv=adv.clone(), ret=ret.clone(), states=ro.env.sim.states.clone(),
+                **{"obr_" + k: v for k, v in ro.env.obr.clone_state().items()})
+    done = float(want["b_done"].sum())
+
+    ro2 = _collector(gpu, kind, 17, graph)                  # other seeds everywhere
+    up2 = U.PPOUpdater(ro2.net, U.UpdateConfig(target_kl=None, update_epochs=1), seed=11)
+    ck = C.load_checkpoint(path, up2, ro2.norm, runtime=ro2)
+    assert ck["global_step"] == ro2.global_step == ro.global_step - ro.T
+    adv2, ret2, _ = ro2.collect()
+    got = {n: getattr(ro2, n) for n in ("b_obs", "b_act", "b_logp", "b_rew", "b_val", "b_done",
+                                        "next_done")}
+    got.update(adv=adv2, ret=ret2, states=ro2.env.sim.states,
+               **{"obr_" + k: v for k, v in ro2.env.obr.clone_state().items()})
+    assert set(got) == set(want)
+    for name in want:
+        assert torch.equal(_bits(got[name]), _bits(want[name])), name
+    assert done > 0                                          # autoresets inside the window
+    # the restored updater draws the same minibatch permutation
+    assert torch.equal(torch.randperm(64, device=gpu, generator=up2.gen),
+                       torch.randperm(64, device=gpu, generator=up.gen))
+
+
+def test_runtime_state_round_trips_through_weights_only_load(tmp_path):
+    """The runtime state is plain data: tensors, ints, floats, strings, dicts and lists only, so
+    torch.load(weights_only=True) reads it back (numpy's generator state included)."""
+    import numpy as np
+    C = import_pkg("checkpoint")
+    np.random.seed(12)
+    saved = C._rng_np_to_saved(np.random.get_state())
+    torch.save({"numpy_rng": saved}, tmp_path / "r.pt")
+    back = torch.load(tmp_path / "r.pt", weights_only=True)["numpy_rng"]
+    a = np.random.random(5)
+    np.random.set_state(C._rng_np_from_saved(back))
+    assert np.array_equal(np.random.random(5), a)
