@@ -821,7 +821,11 @@ def main():
 
     nenv, S = args.nenv, args.substeps
     nac = 2 * nenv
-    head = fdm_section(pkg, icm, nenv, S, args.steps, args.warmup, args.reps, "fdm_tailchase_16k")
+    # (long regions, as C2's 1,000 decisions, fly some aircraft past the model's range: counted,
+    # not an error)
+    head = fdm_section(pkg, icm, nenv, S, args.steps, args.warmup, args.reps,
+                       "fdm_tailchase_16k" if nenv == 16384 else f"fdm_tailchase_{nenv}",
+                       require_finite=args.steps <= 100)
     states0, acts_host = head.pop("_states0"), head.pop("_acts_host")
     if args.only == "fdm":
         print(json.dumps(head), flush=True)
