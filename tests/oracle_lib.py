@@ -153,6 +153,26 @@ def rel_err(got, want, floor_frac=1e-3):
 
 
 
+def scaled_abs_err(got, want):
+    """|got - want| / (largest |want| of the variable's group over the batch): the absolute
+    difference in units of its vector's magnitude (rel_err with floor_frac = 1 and no per-entry
+    denominator).  A component passing through zero -- an acceleration in level flight, a body
+    rate between manoeuvres -- is judged by the scale at which its vector is computed."""
+    return np.abs(np.asarray(got, dtype=np.float64) - np.asarray(want, dtype=np.float64)) / \
+        _group_scale(want)
+
+
+def _group_scale(want):
+    want = np.asarray(want, dtype=np.float64)
+    groups = {101: STATE_GROUPS, 17: OBS_GROUPS}.get(want.shape[-1])
+    if groups is None:
+        groups = [[k] for k in range(want.shape[-1])]
+    scale = np.zeros(want.shape[-1])
+    for g in groups:
+        scale[g] = np.max(np.abs(want[..., g])) if want.size else 0.0
+    return np.maximum(scale, 1e-300)
+
+
 def raw_rel_err(got, want):
     """|got - want| / |want| with no floor (entries whose reference value is exactly zero report
     the absolute difference): the per-variable figure before rel_err's scale floor."""
