@@ -331,9 +331,10 @@ class GpuDogfightVecEnv:
 
     def _advance(self, io, actions, state_fin):
         """The physics step of `actions` and the post-physics step `io` describes: one
-        f16_env_step launch with fused_step and the finite flags (state_fin) on (where the batch
-        exceeds one workgroup per CU it issues the two launches itself), else sim.step and
-        f16_env_post_step.  kernel_events, when a list, gets the one launch's (start, end)."""
+        f16_env_step launch with fused_step and the finite flags (state_fin) on (where the
+        batch exceeds what the full-row tile keeps resident it issues the two launches itself),
+        else sim.step and f16_env_post_step.  kernel_events, when a list, gets the one launch's
+        (start, end)."""
         if not (self.fused_step and state_fin is not None):
             self.sim.step(actions, substeps=self.substeps, want_obs=False, finite_out=state_fin)
             io.state_finite = state_fin.data_ptr() if state_fin is not None else None

@@ -563,12 +563,13 @@ def test_env_step_pool_tables_follow_pool_replacement(gpu, obs_dim):
 @pytest.mark.parametrize("obs_dim,nenv,fcs,roles", [
     (184, 300, 60, 2), (214, 300, 120, 2), (184, 16384, 60, 2), (214, 16384, 120, 2),
     (184, 20000, 60, 2), (184, 300, 60, 4), (214, 300, 120, 4), (184, 16384, 60, 4),
-    (214, 16384, 120, 4), (184, 20, 60, 4), (214, 33, 120, 4)])
+    (214, 16384, 120, 4), (184, 20, 60, 4), (214, 33, 120, 4), (184, 20000, 60, 4),
+    (214, 17000, 120, 4)])
 def test_env_step_one_launch_equals_two(gpu, obs_dim, nenv, fcs, roles):
     """f16_env_step (physics and post-physics step in one launch wherever the full-row tile is
-    resident: 300 engagements, whose last workgroup is partly filled, and 16,384; at 20,000 the
-    entry issues the two launches itself), and f16_env_step_quad (roles=4: four wavefronts per
-    64 aircraft in both phases), against sim.step + f16_env_post_step: every output,
+    resident: 300 engagements, whose last workgroup is partly filled, and 16,384; at 17,000 and
+    20,000 the entry issues the two launches itself), and roles=4: four wavefronts per 64
+    aircraft in both phases, against sim.step + f16_env_post_step: every output,
     the states, the kept actions, the reconstructor and the aux features bit for bit over steps
     with autoresets (staggered 1.2 s engagements), terminal observations on and off, a separate
     action tensor (the launch copies it into sim.actions) and a non-contiguous one (copied
