@@ -207,23 +207,100 @@ __global__ __launch_bounds__(kAdvThreads) void adv_final_kernel(const float* __r
 
 // ---- fused forward / loss / backward of 64 gathered rows
 
-// LDS [row][pitch] tile -> unit-major global dst[f][m0 + row], 8 rows per 16-byte store
-__device__ __forceinline__ void write_t(const __bf16* S, int pitch, int nfeat, __bf16* dst,
-                                        long ld, long m0, int tid) {
-  for (int it = tid; it < nfeat * 8; it += kThreads) {
-    const int f = it >> 3, g = it & 7;
-    bf16x8 v;
+// ---- cross-lane data movement by DPP (vector instructions, no LDS round trip)
+constexpr int kDppXor1 = 0xB1;          // quad_perm [1, 0, 3, 2]: lane ^ 1
+constexpr int kDppXor2 = 0x4E;          // quad_perm [2, 3, 0, 1]: lane ^ 2
+constexpr int kDppRor4 = 0x124;         // row_ror:4 within 16 lanes
+constexpr int kDppRor8 = 0x128;         // row_ror:8
+constexpr int kDppHalfMirror = 0x141;   // lane i <- lane 7 - i within 8 lanes (lane ^ 7)
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL,
+                                                               0xF, 0xF, true));
+}
+// Sum over the 32 lanes of a half-wave (lanes 0-31 and 32-63 separately), every lane getting
+// the sum: quad swaps and row rotations, then one exchange across the 16-lane rows.  The fixed
+// pattern fixes the summation order.
+__device__ __forceinline__ float sum32(float x) {
+  x += dpp<kDppXor1>(x);
+  x += dpp<kDppXor2>(x);
+  x += dpp<kDppRor4>(x);
+  x += dpp<kDppRor8>(x);
+  return x + __shfl_xor(x, 16);
+}
+// the same over all 64 lanes
+__device__ __forceinline__ float sum64(float x) {
+  x = sum32(x);
+  return x + __shfl_xor(x, 32);
+}
+
+constexpr int kBufWord3 = 0x00020000;   // gfx9 buffer descriptor word 3 (raw, 32-bit data format)
+constexpr int kMaxMinibatchRows = 1 << 24;
+
+// LDS [row][pitch] bf16 tile of 64 rows x NF features (NF a multiple of 32) -> unit-major global
+// dst[f][m0 + row], transposed by the matrix cores: D = A I over two 16-wide K slices, A the
+// tile's rows read as the usual activation operand (16-byte, bank-conflict-free) and I the
+// identity split over the slices, so result lane l holds feature l % 32 of rows
+// 32r + 8g + 4(l / 32) + 0..3 -- one 8-byte store per 4 rows.  Exact: each output is one
+// product x * 1 plus zero products.  Blocks of 32 features x 32 rows go round the waves.
+template <int NF>
+__device__ __forceinline__ void transpose_t(const __bf16* S, int pitch, __bf16* dst, long ld,
+                                            long m0, int wave, int lane) {
+  const int lr = lane & 31, kb = (lane >> 5) * 8;
+  bf16x8 i0, i1;                                  // identity fragments of the two K slices
 #pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = S[(8 * g + i) * pitch + f];
-    *reinterpret_cast<bf16x8*>(dst + (long)f * ld + m0 + 8 * g) = v;
+  for (int t = 0; t < 8; ++t) {
+    i0[t] = (__bf16)(kb + t == lr ? 1.0f : 0.0f);
+    i1[t] = (__bf16)(kb + t + 16 == lr ? 1.0f : 0.0f);
+  }
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc(dst + m0, 0, 0x7fffffff, kBufWord3);
+  const int lo = 2 * (lr * (int)ld + (lane >> 5) * 4);
+  for (int blk = wave; blk < (NF / 32) * 2; blk += kWaves) {
+    const int fb = blk >> 1, r = blk & 1;
+    const __bf16* ap = S + (32 * r + lr) * pitch + 32 * fb + kb;
+    const bf16x8 a0 = *reinterpret_cast<const bf16x8*>(ap);
+    const bf16x8 a1 = *reinterpret_cast<const bf16x8*>(ap + 16);
+    f32x16 acc = {};
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, i0, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, i1, acc, 0, 0, 0);
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      bf16x4 v;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = (__bf16)acc[4 * g + e];
+      typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+      __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, v), rs,
+                                            lo + 2 * (32 * r + 8 * g), 2 * 32 * fb * (int)ld, 0);
+    }
   }
 }
+
+// Unit-major stores of a 32-unit x 64-row block (unit u0 + 8g + lh + j, row 32r + lr) as buffer
+// stores: the block's origin dst + u0 ld + m0 is the (wave-uniform) buffer base, the (g, j)
+// offset 2 (8g + j) ld the scalar offset and the lane's 2 (lh ld + lr) + 64 r the vector
+// offset, so a store needs no vector address arithmetic.  The buffer's window is 2 GB from the
+// base (offsets below 72 ld bytes occur, so ld < 2^24 rows); u0 must be wave-uniform.
+struct UnitMajor {
+  __amdgpu_buffer_rsrc_t rsrc;
+  int ld2;              // bytes between consecutive features
+  int lane_off;         // 2 (lh ld + lr)
+  __device__ __forceinline__ UnitMajor(__bf16* dst, long ld, long m0, int u0, int lane)
+      : rsrc(__builtin_amdgcn_make_buffer_rsrc(dst + (long)u0 * ld + m0, 0, 0x7fffffff,
+                                               kBufWord3)),
+        ld2(2 * (int)ld), lane_off(2 * ((lane >> 5) * 4 * (int)ld + (lane & 31))) {}
+  __device__ __forceinline__ void put(int g, int r, int j, __bf16 v) const {
+    __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, v), rsrc,
+                                          lane_off + 64 * r, (8 * g + j) * ld2, 0);
+  }
+};
 
 // tanh epilogue: bf16 activation to LDS Hs[row][unit] and to unit-major dst[unit][m0 + row]
 template <int NR>
 __device__ __forceinline__ void store_tanh_t(const f32x16 (&acc)[NR], __bf16* Hs, int u0,
                                              __bf16* dst, long ld, long m0, int lane) {
   const int lr = lane & 31, lh = (lane >> 5) * 4;
+  const UnitMajor out(dst, ld, m0, u0, lane);
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
     const int unit = u0 + 8 * g + lh;
@@ -235,7 +312,7 @@ __device__ __forceinline__ void store_tanh_t(const f32x16 (&acc)[NR], __bf16* Hs
       const int row = 32 * r + lr;
       *reinterpret_cast<bf16x4*>(Hs + row * kHPitch + unit) = v;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) dst[(long)(unit + j) * ld + m0 + row] = v[j];
+      for (int j = 0; j < 4; ++j) out.put(g, r, j, v[j]);
     }
   }
 }
@@ -247,6 +324,7 @@ __device__ __forceinline__ void store_dtanh_t(const f32x16 (&acc)[NR], const __b
                                               __bf16* Out, int u0, __bf16* dst, long ld, long m0,
                                               int lane) {
   const int lr = lane & 31, lh = (lane >> 5) * 4;
+  const UnitMajor out(dst, ld, m0, u0, lane);
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
     const int unit = u0 + 8 * g + lh;
@@ -262,8 +340,76 @@ __device__ __forceinline__ void store_dtanh_t(const f32x16 (&acc)[NR], const __b
       }
       if (Out) *reinterpret_cast<bf16x4*>(Out + row * kHPitch + unit) = v;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) dst[(long)(unit + j) * ld + m0 + row] = v[j];
+      for (int j = 0; j < 4; ++j) out.put(g, r, j, v[j]);
     }
+  }
+}
+
+// A product's first weight fragments, loaded before the previous phase's epilogue.  vmcnt
+// retires loads and stores in issue order, so a weight load issued after that epilogue's global
+// stores could only be waited for behind all of them; these are issued ahead of the stores.
+template <int K>
+struct WPre {
+  static constexpr int PF = K / 16 < 4 ? K / 16 : 4;
+  bf16x8 w[PF];
+};
+template <int K>
+__device__ __forceinline__ void wprefetch(WPre<K>& p, const __bf16* __restrict__ Wg, int u0,
+                                          int lane) {
+  const __bf16* wp = Wg + (long)(u0 >> 5) * (K / 16) * 512 + lane * 8;
+#pragma unroll
+  for (int q = 0; q < WPre<K>::PF; ++q) p.w[q] = *reinterpret_cast<const bf16x8*>(wp + 512 * q);
+  __builtin_amdgcn_sched_barrier(0);     // issued here, not sunk towards the product
+}
+// init_bias from the biases staged in LDS (global loads there would wait behind the previous
+// epilogue's stores as well): element e of a tile is unit u0 + 8(e/4) + 4(lane/32) + e%4
+template <int NR>
+__device__ __forceinline__ void init_bias_lds(f32x16 (&acc)[NR], const float* bias, int u0,
+                                              int lane) {
+  const int lh = (lane >> 5) * 4;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const float4 b = *reinterpret_cast<const float4*>(bias + u0 + 8 * g + lh);
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      acc[r][4 * g + 0] = b.x;
+      acc[r][4 * g + 1] = b.y;
+      acc[r][4 * g + 2] = b.z;
+      acc[r][4 * g + 3] = b.w;
+    }
+  }
+}
+
+// gemm_t's product (the same slices in the same order, so the same sums) with the first
+// fragments taken from p; the rest stream PF slices ahead.
+template <int NR, int K>
+__device__ __forceinline__ void gemm_p(f32x16 (&acc)[NR], const WPre<K>& p,
+                                       const __bf16* __restrict__ Wg, int u0,
+                                       const __bf16* __restrict__ As, int a_pitch, int lane) {
+  constexpr int NK = K / 16, PF = WPre<K>::PF;
+  const int lr = lane & 31, lk = (lane >> 5) * 8;
+  const __bf16* wp = Wg + (long)(u0 >> 5) * (K / 16) * 512 + lane * 8;
+  const __bf16* ap = As + lr * a_pitch + lk;
+  bf16x8 w[PF + 1];
+#pragma unroll
+  for (int q = 0; q < PF; ++q) w[q] = p.w[q];
+  bf16x8 a[NR], an[NR];
+#pragma unroll
+  for (int r = 0; r < NR; ++r) a[r] = *reinterpret_cast<const bf16x8*>(ap + 32 * r * a_pitch);
+#pragma unroll
+  for (int s = 0; s < NK; ++s) {
+    if (s + PF < NK) w[(s + PF) % (PF + 1)] =
+        *reinterpret_cast<const bf16x8*>(wp + 512 * (s + PF));
+    if (s + 1 < NK) {
+#pragma unroll
+      for (int r = 0; r < NR; ++r)
+        an[r] = *reinterpret_cast<const bf16x8*>(ap + 32 * r * a_pitch + 16 * (s + 1));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int r = 0; r < NR; ++r) acc[r] = mfma(w[s % (PF + 1)], a[r], acc[r]);
+#pragma unroll
+    for (int r = 0; r < NR; ++r) a[r] = an[r];
   }
 }
 
@@ -275,17 +421,25 @@ __device__ __forceinline__ void zero_acc(f32x16 (&acc)[NR]) {
     for (int e = 0; e < 16; ++e) acc[r][e] = 0.0f;
 }
 
-// rows of tile t: threads < 64 read the minibatch indices into rowpN (-1: past the minibatch or
-// a bad index, which is counted in badN and not read)
-__device__ __forceinline__ void fetch_rows(const F16PPOArgs& a, int t, long long* rowpN,
-                                           float* badN, int tid) {
+// rows of tile t: threads < 64 read the minibatch indices (idx_load; kNoRow past the
+// minibatch), then idx_store puts them into rowpN (-1: past the minibatch or a bad index, which
+// is counted in badN and not read).  Split so that the load is waited for well after its issue.
+constexpr long long kNoRow = -(1LL << 62);
+__device__ __forceinline__ long long idx_load(const F16PPOArgs& a, int t, int tid) {
+  long long p = kNoRow;
+  const long r = (long)t * kRows + tid;
+  if (tid < kRows && r < a.mb_rows) p = a.idx[r];
+  return p;
+}
+__device__ __forceinline__ void idx_store(const F16PPOArgs& a, long long p, long long* rowpN,
+                                          float* badN, int tid) {
   if (tid < kRows) {
-    const long r = (long)t * kRows + tid;
-    long long p = -1;
     float bad = 0.0f;
-    if (r < a.mb_rows) {
-      p = a.idx[r];
-      if (p < 0 || p >= a.count) { bad = 1.0f; p = -1; }
+    if (p == kNoRow) {
+      p = -1;
+    } else if (p < 0 || p >= a.count) {
+      bad = 1.0f;
+      p = -1;
     }
     rowpN[tid] = p;
     badN[tid] = bad;
@@ -307,8 +461,29 @@ __device__ __forceinline__ void issue_rows(const F16PPOArgs& a, const long long*
   }
 }
 
+// The loss head's per-row inputs for thread tid of the rows listed in rp: the drawn bin of its
+// (row, channel) item (two lanes per item), the row's collection log-probability and advantage,
+// and for tid < 64 the return of row tid.  Rows with rp < 0 give act -1 and zeros.
+struct HeadIn {
+  long long act;
+  float old_lp, adv, ret;
+};
+__device__ __forceinline__ HeadIn gather_head(const F16PPOArgs& a, const long long* rp, int tid) {
+  HeadIn h{-1, 0.0f, 0.0f, 0.0f};
+  const int lrow = tid >> 3, lch = (tid >> 1) & 3;
+  const long long pr = rp[lrow];
+  if (pr >= 0) {
+    h.act = a.act[pr * kChan + lch];
+    h.old_lp = a.old_logp[pr];
+    h.adv = a.adv[pr];
+  }
+  if (tid < kRows && rp[tid] >= 0) h.ret = a.ret[rp[tid]];
+  return h;
+}
+
 // The fused kernel is persistent: one workgroup per CU walks the minibatch's 64-row tiles, and
-// the next tile's gathered rows are loaded into registers during the current tile's matrix work.
+// the next tile's gathered rows and loss-head inputs are loaded into registers during the
+// current tile's loss head, landing while it computes.
 template <int KP>
 __global__ __launch_bounds__(kThreads, 1) void ppo_fused_kernel(const F16PPOArgs a, const Work w) {
   constexpr int XP = KP + 8;
@@ -322,6 +497,7 @@ __global__ __launch_bounds__(kThreads, 1) void ppo_fused_kernel(const F16PPOArgs
   __shared__ float rowf[kRows][8];
   __shared__ float vpart[kWaves][kRows];                  // per-wave partial critic values
   __shared__ long long rowp[kRows], rowpN[kRows];
+  __shared__ __align__(16) float cst[kB3C];               // biases and the value head, wf[0, kB3C)
   __shared__ float badN[kRows];
   __bf16* Zs = reinterpret_cast<__bf16*>(Ls);
   static_assert(kRows * kZPitch * 2 <= kRows * kLPitch * 4, "logit gradients overlay the logits");
@@ -330,21 +506,32 @@ __global__ __launch_bounds__(kThreads, 1) void ppo_fused_kernel(const F16PPOArgs
   const __bf16* wbf = static_cast<const __bf16*>(a.wbf);
   const __bf16* wT = static_cast<const __bf16*>(a.wT);
   const float* wf = a.wf;
-  const float* w3 = wf + kW3C;
   const float inv_mb = 1.0f / (float)a.mb_rows;
+  // launch constants read once (scalar loads before any store of this kernel)
+  const float adv_mean = w.advs[0], adv_std = w.advs[1], b3c = wf[kB3C];
+  for (int i = threadIdx.x; i < kB3C / 4; i += kThreads)
+    reinterpret_cast<float4*>(cst)[i] = reinterpret_cast<const float4*>(wf)[i];
+  const float* w3s = cst + kW3C;
 
   float2 xr[kPer];
   int tile = blockIdx.x;
   if (tile >= w.nwg) return;                               // uniform per workgroup
-  fetch_rows(a, tile, rowpN, badN, (int)threadIdx.x);
+  idx_store(a, idx_load(a, tile, (int)threadIdx.x), rowpN, badN, (int)threadIdx.x);
   __syncthreads();
   issue_rows<D, kPer>(a, rowpN, xr, (int)threadIdx.x);
+  HeadIn hnext = gather_head(a, rowpN, (int)threadIdx.x);
+  WPre<KP> pa1;
+  wprefetch(pa1, wbf + Blob<KP>::W1, 32 * __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6),
+            (int)threadIdx.x & 63);
+  // every load above has landed before the loop, so the loop's own waits for the gathered rows
+  // count only the previous tile's loads (they retire by its last product's final wait)
+  __builtin_amdgcn_s_waitcnt(0x0F70);                     // vmcnt(0)
   for (; tile < w.nwg; tile += gridDim.x) {
     // the thread index passes through an empty asm each tile, so the per-lane addresses below are
     // formed inside the loop rather than hoisted out of it and held live (they would spill)
     int tid = threadIdx.x;
     asm volatile("" : "+v"(tid));
-    const int lane = tid & 63, wave = tid >> 6;
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lr = lane & 31, lh = (lane >> 5) * 4;
     const long m0 = (long)tile * kRows;
     // ---- stage this tile's rows (normalised at collection), rounded to bf16
@@ -366,29 +553,37 @@ __global__ __launch_bounds__(kThreads, 1) void ppo_fused_kernel(const F16PPOArgs
     }
     __syncthreads();
     const int next = tile + gridDim.x;
-    if (next < w.nwg) fetch_rows(a, next, rowpN, badN, tid);
-    write_t(Xs, XP, KP, w.xt, ld, m0, tid);
+    const long long pnext = next < w.nwg ? idx_load(a, next, tid) : kNoRow;
+    // the loss head's per-row inputs, gathered during the previous tile
+    const int item = tid >> 1, hb = tid & 1;           // (row, channel) item, bin half
+    const int lrow = item >> 2, lch = item & 3;
+    const HeadIn hin = hnext;
+    transpose_t<KP>(Xs, XP, w.xt, ld, m0, wave, lane);
 
     // ---- actor forward
+    WPre<kHid> pa2, pl3;
     {
       f32x16 acc[2];
-      init_bias(acc, wf + kB1, 32 * wave, lane);
-      gemm_t<2, KP>(acc, wbf + Blob<KP>::W1, 32 * wave, Xs, XP, 0, lane);
+      init_bias_lds(acc, cst + kB1, 32 * wave, lane);
+      gemm_p<2, KP>(acc, pa1, wbf + Blob<KP>::W1, 32 * wave, Xs, XP, lane);
+      wprefetch(pa2, wbf + Blob<KP>::W2A, 32 * wave, lane);
       store_tanh_t(acc, H1s, 32 * wave, w.h1t, ld, m0, lane);
     }
     __syncthreads();
     {
       f32x16 acc[2];
-      init_bias(acc, wf + kB2A, 32 * wave, lane);
-      gemm_t<2, kHid>(acc, wbf + Blob<KP>::W2A, 32 * wave, H1s, kHPitch, 0, lane);
+      init_bias_lds(acc, cst + kB2A, 32 * wave, lane);
+      gemm_p<2, kHid>(acc, pa2, wbf + Blob<KP>::W2A, 32 * wave, H1s, kHPitch, lane);
+      if (wave < 6) wprefetch(pl3, wbf + Blob<KP>::W3A, 32 * (wave % 3), lane);
       store_tanh_t(acc, H2s, 32 * wave, w.h2t, ld, m0, lane);
+      idx_store(a, pnext, rowpN, badN, tid);     // the next tile's rows, read after the barrier
     }
     __syncthreads();
     if (wave < 6) {
       const int ut = wave % 3, rt = wave / 3;
       f32x16 acc[1];
-      init_bias(acc, wf + kB3A, 32 * ut, lane);
-      gemm_t<1, kHid>(acc, wbf + Blob<KP>::W3A, 32 * ut, H2s + 32 * rt * kHPitch, kHPitch, 0,
+      init_bias_lds(acc, cst + kB3A, 32 * ut, lane);
+      gemm_p<1, kHid>(acc, pl3, wbf + Blob<KP>::W3A, 32 * ut, H2s + 32 * rt * kHPitch, kHPitch,
                       lane);
       const int row = 32 * rt + lr;
 #pragma unroll
@@ -401,30 +596,20 @@ __global__ __launch_bounds__(kThreads, 1) void ppo_fused_kernel(const F16PPOArgs
     __syncthreads();
 
     // ---- loss head (ppo_gpu.py:2065-2090; model.py:207-219).
-    // Its per-row inputs are loaded first, then the next tile's rows: vmcnt retires loads in
-    // order, so the loss head waits only for its own loads and the gather lands during the loss
-    // head's arithmetic instead of stalling the next weight-fragment wait.
+    // The next tile's rows are gathered from here on, landing while this tile computes.
     // Two lanes per (row, channel) -- lanes 2i, 2i + 1 take bins 0-10 and 11-20 -- so all eight
     // waves share the head.  The maximum (exact, order-free), the numerator sum in the rollout's
     // order (the high half continues from the low half's partial), the chosen bin's
     // log-probability and the channel sum are the rollout kernel's values bit for bit.
-    const int item = tid >> 1, hb = tid & 1;           // (row, channel) item, bin half
-    const int lrow = item >> 2, lch = item & 3;
     const int k0 = hb ? 11 : 0;                        // this lane's bins: k0 .. k0 + nb - 1
     constexpr int kHalf = 11;
     const int nb = hb ? kBins - kHalf : kHalf;
-    long long act = -1;
-    float old_lp = 0.0f, adv_r = 0.0f, ret_r = 0.0f;
-    {
-      const long long pr = rowp[lrow];
-      if (pr >= 0) {
-        act = a.act[pr * kChan + lch];
-        old_lp = a.old_logp[pr];
-        adv_r = a.adv[pr];
-      }
+    const long long act = hin.act;
+    const float old_lp = hin.old_lp, adv_r = hin.adv, ret_r = hin.ret;
+    if (next < w.nwg) {
+      issue_rows<D, kPer>(a, rowpN, xr, tid);
+      hnext = gather_head(a, rowpN, tid);
     }
-    if (tid < kRows && rowp[tid] >= 0) ret_r = a.ret[rowp[tid]];
-    if (next < w.nwg) issue_rows<D, kPer>(a, rowpN, xr, tid);   // lands while this tile computes
     float dz[kHalf];
     {
       const long long pr = rowp[lrow];
@@ -436,18 +621,18 @@ __global__ __launch_bounds__(kThreads, 1) void ppo_fused_kernel(const F16PPOArgs
       float m = lg[0];
 #pragma unroll
       for (int k = 1; k < kHalf; ++k) m = fmaxf(m, lg[k]);
-      m = fmaxf(m, __shfl_xor(m, 1));                 // the rollout's maximum (max is exact)
+      m = fmaxf(m, dpp<kDppXor1>(m));                 // the rollout's maximum (max is exact)
       float e[kHalf], sp = 0.0f;
 #pragma unroll
       for (int k = 0; k < kHalf; ++k) {
         e[k] = k < nb ? f16rng::exp_nonpos(lg[k] - m) : 0.0f;
         if (hb == 0) sp += e[k];                      // the low half's sum, bins in order
       }
-      float s = __shfl_xor(sp, 1);                    // the high lane receives it and continues
+      float s = dpp<kDppXor1>(sp);                    // the high lane receives it and continues
 #pragma unroll
       for (int k = 0; k < kHalf; ++k)
         if (k < nb) s += e[k];
-      const float s_hi = __shfl_xor(s, 1);            // every lane takes part in the shuffle
+      const float s_hi = dpp<kDppXor1>(s);            // every lane takes part in the exchange
       s = hb ? s : s_hi;                              // (the low lane's value above is unused)
       const float lse = logf(s), inv_s = 1.0f / s;
       float lp = 0.0f, hc = 0.0f;
@@ -458,19 +643,22 @@ __global__ __launch_bounds__(kThreads, 1) void ppo_fused_kernel(const F16PPOArgs
         if (k < nb && k0 + k == act) { lp = lpk; mine = true; }
         if (k < nb) hc -= (e[k] * inv_s) * lpk;
       }
-      const float lpo = __shfl_xor(lp, 1);
+      const float lpo = dpp<kDppXor1>(lp);
       lp = mine ? lp : lpo;
-      hc += __shfl_xor(hc, 1);
-      lp += __shfl_xor(lp, 2);                        // channels: the rollout kernel's order
-      lp += __shfl_xor(lp, 4);
-      float ent = hc + __shfl_xor(hc, 2);
-      ent += __shfl_xor(ent, 4);
+      hc += dpp<kDppXor1>(hc);
+      // channels (lane bits 1-2; both lanes of an item hold the same value): c + (c ^ 1), then
+      // plus the partner pair's sum -- lane ^ 7 holds (c ^ 3) + (c ^ 2) -- which equals the
+      // rollout kernel's (c + (c ^ 1)) + ((c ^ 2) + (c ^ 3)) bit for bit (commutative adds)
+      lp += dpp<kDppXor2>(lp);
+      lp += dpp<kDppHalfMirror>(lp);
+      float ent = hc + dpp<kDppXor2>(hc);
+      ent += dpp<kDppHalfMirror>(ent);
       float gcoef = 0.0f, pl = 0.0f, kl = 0.0f, cf = 0.0f;
       if (valid) {
         const float logr = lp - old_lp;
         const float ratio = expf(logr);
         float A = adv_r;
-        if (a.norm_adv && a.mb_rows > 1) A = (A - w.advs[0]) / (w.advs[1] + 1e-8f);
+        if (a.norm_adv && a.mb_rows > 1) A = (A - adv_mean) / (adv_std + 1e-8f);
         const float lo = (float)(1.0 - (double)a.clip_coef), hi = (float)(1.0 + (double)a.clip_coef);
         const float rc = ratio < lo ? lo : (ratio > hi ? hi : ratio);
         const float pg1 = -A * ratio, pg2 = -A * rc;
@@ -509,20 +697,26 @@ __global__ __launch_bounds__(kThreads, 1) void ppo_fused_kernel(const F16PPOArgs
       for (int k = kLogits; k < kLogitsPad; ++k) Zs[lrow * kZPitch + k] = (__bf16)0.0f;
     }
     __syncthreads();
-    write_t(Zs, kZPitch, kLogitsPad, w.dzt, ld, m0, tid);
+    WPre<kLogitsPad> pb3;
+    wprefetch(pb3, wT + kWT3, 32 * wave, lane);
+    transpose_t<kLogitsPad>(Zs, kZPitch, w.dzt, ld, m0, wave, lane);
 
     // ---- actor backward: dH2 = (dZ W3) (1 - H2^2) in place of H2, dH1 = (dH2 W2) (1 - H1^2)
+    WPre<kHid> pb2, pbc, pc2;
+    WPre<KP> pc1;
     {
       f32x16 acc[2];
       zero_acc(acc);
-      gemm_t<2, kLogitsPad>(acc, wT + kWT3, 32 * wave, Zs, kZPitch, 0, lane);
+      gemm_p<2, kLogitsPad>(acc, pb3, wT + kWT3, 32 * wave, Zs, kZPitch, lane);
+      wprefetch(pb2, wT + kWT2A, 32 * wave, lane);
       store_dtanh_t(acc, H2s, H2s, 32 * wave, w.dh2t, ld, m0, lane);
     }
     __syncthreads();
     {
       f32x16 acc[2];
       zero_acc(acc);
-      gemm_t<2, kHid>(acc, wT + kWT2A, 32 * wave, H2s, kHPitch, 0, lane);
+      gemm_p<2, kHid>(acc, pb2, wT + kWT2A, 32 * wave, H2s, kHPitch, lane);
+      wprefetch(pc1, wbf + Blob<KP>::W1C, 32 * wave, lane);
       store_dtanh_t(acc, H1s, nullptr, 32 * wave, w.dh1t, ld, m0, lane);
     }
     __syncthreads();
@@ -530,24 +724,24 @@ __global__ __launch_bounds__(kThreads, 1) void ppo_fused_kernel(const F16PPOArgs
     // ---- critic forward; the value head is folded into the second layer's epilogue
     {
       f32x16 acc[2];
-      init_bias(acc, wf + kB1 + kHid, 32 * wave, lane);
-      gemm_t<2, KP>(acc, wbf + Blob<KP>::W1C, 32 * wave, Xs, XP, 0, lane);
+      init_bias_lds(acc, cst + kB1 + kHid, 32 * wave, lane);
+      gemm_p<2, KP>(acc, pc1, wbf + Blob<KP>::W1C, 32 * wave, Xs, XP, lane);
+      wprefetch(pc2, wbf + Blob<KP>::W2C, 32 * wave, lane);
       store_tanh_t(acc, H1s, 32 * wave, w.h1t + kHid * ld, ld, m0, lane);
     }
     __syncthreads();
     bf16x4 hc2[4][2];                          // this lane's critic layer-2 activations
     {
       f32x16 acc[2];
-      init_bias(acc, wf + kB2C, 32 * wave, lane);
-      gemm_t<2, kHid>(acc, wbf + Blob<KP>::W2C, 32 * wave, H1s, kHPitch, 0, lane);
+      init_bias_lds(acc, cst + kB2C, 32 * wave, lane);
+      gemm_p<2, kHid>(acc, pc2, wbf + Blob<KP>::W2C, 32 * wave, H1s, kHPitch, lane);
       float vp[2] = {0.0f, 0.0f};
-      float4 w4s[4];                           // all four head loads in flight at once
+      float4 w4s[4];
 #pragma unroll
       for (int g = 0; g < 4; ++g)
-        w4s[g] = *reinterpret_cast<const float4*>(w3 + 32 * wave + 8 * g + lh);
+        w4s[g] = *reinterpret_cast<const float4*>(w3s + 32 * wave + 8 * g + lh);
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const int unit = 32 * wave + 8 * g + lh;
         const float4 w4 = w4s[g];
 #pragma unroll
         for (int r = 0; r < 2; ++r) {
@@ -555,7 +749,6 @@ __global__ __launch_bounds__(kThreads, 1) void ppo_fused_kernel(const F16PPOArgs
 #pragma unroll
           for (int j = 0; j < 4; ++j) v[j] = (__bf16)tanh_act(acc[r][4 * g + j]);
           hc2[g][r] = v;
-          *reinterpret_cast<bf16x4*>(H2s + (32 * r + lr) * kHPitch + unit) = v;
           vp[r] += (float)v[0] * w4.x + (float)v[1] * w4.y + (float)v[2] * w4.z + (float)v[3] * w4.w;
         }
       }
@@ -564,69 +757,69 @@ __global__ __launch_bounds__(kThreads, 1) void ppo_fused_kernel(const F16PPOArgs
       if (lane < 32) { vpart[wave][lr] = vp[0]; vpart[wave][32 + lr] = vp[1]; }
     }
     __syncthreads();
-    if (tid < kRows) {                         // value, its error and d(loss)/dv per row
+    if (tid < kRows) {      // wave 0, one lane per row: value, its error, d(loss)/dv; tile sums
       float v = vpart[0][tid];
 #pragma unroll
       for (int q = 1; q < kWaves; ++q) v += vpart[q][tid];
       const long long pr = rowp[tid];
       float dv = 0.0f, se = 0.0f;
       if (pr >= 0) {
-        const float err = (v + wf[kB3C]) - ret_r;
+        const float err = (v + b3c) - ret_r;
         se = err * err;
         dv = a.vf_coef * err * inv_mb;      // d(vf_coef 0.5 mean(err^2)) / dv
       }
       rowf[tid][4] = dv;
-      rowf[tid][5] = se;
-    }
-    __syncthreads();
-    // per-tile partials: statistics, dw3c = sum dv h2, db3c = sum dv (rows in order)
-    {
-      float* part = w.fpart + (long)tile * kPartCols;
-      if (tid < kHid) {
-        // four interleaved row sums (rows r = q mod 4), then combined: four independent
-        // dependency chains instead of one 64 long
-        float s4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll 16
-        for (int r = 0; r < kRows; ++r) s4[r & 3] += rowf[r][4] * (float)H2s[r * kHPitch + tid];
-        part[kStatCols + tid] = (s4[0] + s4[1]) + (s4[2] + s4[3]);
-      } else if (tid < kHid + 8) {
-        const int c = tid - kHid;             // 0 pl, 1 ent, 2 kl, 3 cf, 4 dv (db3c), 5 se, 7 bad
-        float s = 0.0f;
-        if (c != 6)
-          for (int r = 0; r < kRows; ++r) s += rowf[r][c];
-        if (c == 4) {
-          part[kStatCols + kHid] = s;
-          part[4] = 0.0f;
-        } else {
-          part[c] = s;
-        }
+      // the tile's sums over its rows: pl, ent, kl, cf, se, bad and db3c = sum dv
+      float st[7] = {rowf[tid][0], rowf[tid][1], rowf[tid][2], rowf[tid][3], se, rowf[tid][7], dv};
+#pragma unroll
+      for (int q = 0; q < 7; ++q) st[q] = sum64(st[q]);
+      if (tid == 0) {
+        float* part = w.fpart + (long)tile * kPartCols;
+        *reinterpret_cast<float4*>(part) = make_float4(st[0], st[1], st[2], st[3]);
+        *reinterpret_cast<float4*>(part + 4) = make_float4(0.0f, st[4], 0.0f, st[5]);
+        part[kStatCols + kHid] = st[6];
       }
     }
-    __syncthreads();                          // H2s is read
-    // dH2c = dv w3c (1 - H2c^2) from the registers, in place and unit-major
+    __syncthreads();
+    wprefetch(pbc, wT + kWT2C, 32 * wave, lane);
+    // dw3c = sum over rows of dv h2c (this lane's two rows, then the 32 lanes that share its
+    // units) and dH2c = dv w3c (1 - h2c^2), both from the registers; dH2c to H2s (no reader
+    // left since the actor's backward) and unit-major
+    {
+      const float dv0 = rowf[lr][4], dv1 = rowf[32 + lr][4];
+      const UnitMajor out(w.dh2t + kHid * ld, ld, m0, 32 * wave, lane);
+      float* part = w.fpart + (long)tile * kPartCols + kStatCols;
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int unit = 32 * wave + 8 * g + lh;
-#pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        const int row = 32 * r + lr;
-        const float dvr = rowf[row][4];
-        bf16x4 d;
+      for (int g = 0; g < 4; ++g) {
+        const int unit = 32 * wave + 8 * g + lh;
+        const float4 w4v = *reinterpret_cast<const float4*>(w3s + unit);
+        const float w4[4] = {w4v.x, w4v.y, w4v.z, w4v.w};
+        float sw[4];
+        bf16x4 d0, d1;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const float h = (float)hc2[g][r][j];
-          d[j] = (__bf16)(dvr * w3[unit + j] * (1.0f - h * h));
+          const float h0 = (float)hc2[g][0][j], h1 = (float)hc2[g][1][j];
+          sw[j] = sum32(dv0 * h0 + dv1 * h1);
+          d0[j] = (__bf16)(dv0 * w4[j] * (1.0f - h0 * h0));
+          d1[j] = (__bf16)(dv1 * w4[j] * (1.0f - h1 * h1));
         }
-        *reinterpret_cast<bf16x4*>(H2s + row * kHPitch + unit) = d;
+        *reinterpret_cast<bf16x4*>(H2s + lr * kHPitch + unit) = d0;
+        *reinterpret_cast<bf16x4*>(H2s + (32 + lr) * kHPitch + unit) = d1;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) w.dh2t[(long)(kHid + unit + j) * ld + m0 + row] = d[j];
+        for (int j = 0; j < 4; ++j) {
+          out.put(g, 0, j, d0[j]);
+          out.put(g, 1, j, d1[j]);
+        }
+        if ((lane & 31) == 0)
+          *reinterpret_cast<float4*>(part + unit) = make_float4(sw[0], sw[1], sw[2], sw[3]);
       }
     }
     __syncthreads();
     {
       f32x16 acc[2];
       zero_acc(acc);
-      gemm_t<2, kHid>(acc, wT + kWT2C, 32 * wave, H2s, kHPitch, 0, lane);
+      gemm_p<2, kHid>(acc, pbc, wT + kWT2C, 32 * wave, H2s, kHPitch, lane);
+      wprefetch(pa1, wbf + Blob<KP>::W1, 32 * wave, lane);    // the next tile's first product
       store_dtanh_t(acc, H1s, nullptr, 32 * wave, w.dh1t + kHid * ld, ld, m0, lane);
     }
     // the next tile first writes Xs, rowp and rowf (read before the syncs above) and H1s only
@@ -1009,13 +1202,14 @@ extern "C" int f16_ppo_param_counts(int obs_dim, long* out2) {
 }
 
 extern "C" long f16_ppo_workspace_bytes(int obs_dim, int mb_rows) {
-  if ((obs_dim != 184 && obs_dim != 214) || mb_rows < 1) return -1;
+  if ((obs_dim != 184 && obs_dim != 214) || mb_rows < 1 || mb_rows > kMaxMinibatchRows) return -1;
   return layout(obs_dim, mb_rows, nullptr).bytes;
 }
 
 extern "C" int f16_ppo_grad(const F16PPOArgs* a, void* stream) {
   if (!a || (a->obs_dim != 184 && a->obs_dim != 214)) return F16_EINVAL;
   if (a->mb_rows < 1 || a->count < 1 || a->obs_ld < a->obs_dim) return F16_EINVAL;
+  if (a->mb_rows > kMaxMinibatchRows) return F16_EINVAL;   // the unit-major stores' window
   if (!a->obs || !a->act || !a->old_logp || !a->adv || !a->ret || !a->idx) return F16_EINVAL;
   if (!a->wbf || !a->wf || !a->wT || !a->grad || !a->stats || !a->work) return F16_EINVAL;
   if (((uintptr_t)a->wbf & 15) || ((uintptr_t)a->wT & 15) || ((uintptr_t)a->work & 255))

@@ -26,7 +26,8 @@ int f16_ppo_param_counts(int obs_dim, long *out2);
  * zero), W2a^T [256][256], W2c^T [256][256], each fragment-major like the f16_policy.h blob. */
 #define F16_PPO_WT_ELEMS (256 * 96 + 2 * 256 * 256)
 
-/* Device scratch for f16_ppo_grad over minibatches of up to mb_rows rows. */
+/* Device scratch for f16_ppo_grad over minibatches of up to mb_rows rows (1 .. 2^24; -1
+ * beyond, and f16_ppo_grad returns F16_EINVAL for such a minibatch). */
 long f16_ppo_workspace_bytes(int obs_dim, int mb_rows);
 
 /* Per-minibatch statistics written by f16_ppo_grad (float32, means over the minibatch). */
