@@ -40,14 +40,15 @@ struct Blob {
 constexpr int kB1 = 0, kB2A = 512, kB2C = 768, kB3A = 1024, kW3C = 1120, kB3C = 1376;
 static_assert(kB3C + 1 == F16_POLICY_NF, "f32 blob layout");
 
-// tanh for the bf16 hidden activations: sign(x) (1 - t) / (1 + t), t = e^{-2|x|}, from the
-// hardware exp2 and reciprocal (~1 ulp each); r (1 - t) is one fma, r - t r, rounded once.
-// Near 0 the difference cancels, but the absolute error stays below 2.5e-7 everywhere, far
-// inside the bf16 rounding step the result is stored with.  Six instructions per activation.
+// tanh for the bf16 hidden activations: 2 / (1 + t) - 1, t = e^{-2x}, from the hardware exp2
+// and reciprocal (~1 ulp each) and one fma 2 r - 1.  Near 0 the difference cancels, but the
+// absolute error stays near 2e-7 everywhere (r = 1/2 to ~1e-7), far inside the bf16 rounding
+// step the result is stored with; t = inf below x = -44 gives r = 0, -1 exactly.  Five
+// instructions per activation, two of them transcendental.
 __device__ __forceinline__ float tanh_act(float x) {
-  const float t = __builtin_amdgcn_exp2f(fabsf(x) * -2.8853900817779268f);
+  const float t = __builtin_amdgcn_exp2f(x * -2.8853900817779268f);
   const float r = __builtin_amdgcn_rcpf(1.0f + t);
-  return copysignf(__builtin_fmaf(-t, r, r), x);
+  return __builtin_fmaf(2.0f, r, -1.0f);
 }
 
 __device__ __forceinline__ f32x16 mfma(const bf16x8& a, const bf16x8& b, const f32x16& c) {
