@@ -270,10 +270,17 @@ class LeagueRollout:
     opponent redraw), and a strided copy of the learner's rewards.
 
     graph=True records the rollout as a HIP graph as SelfPlayRollout does (same results bit for
-    bit; adv/ret overwritten by the next collect())."""
+    bit; adv/ret overwritten by the next collect()).
+
+    stats=True (eager only) adds collect_rollout's episode and match bookkeeping
+    (ppo_gpu.py:1940-1969): returns, lengths and completed episodes of the learner; wins,
+    losses and altitude losses from the terminal HP and altitude of both aircraft; and the
+    per-opponent win / loss / episode counts, each finished match credited to the opponent that
+    played it (the kernel redraws an autoreset engagement's opponent inside the step)."""
 
     def __init__(self, env, net, opponents, T=128, gamma=0.99, lam=0.95, seed=0,
-                 update_norm=True, opp_weights=None, opp_norms=None, graph=False, aux=False):
+                 update_norm=True, opp_weights=None, opp_norms=None, graph=False, aux=False,
+                 stats=False, opp_deterministic=False):
         from .policy import PolicyStep, RunningNorm
         if len(opponents) < 1 or len(opponents) > 16:
             raise ValueError("1..16 opponent networks")
@@ -318,7 +325,17 @@ class LeagueRollout:
         self.policy_events = None
         self.opp_events = None
         self._graph_mode = bool(graph)
+        self.want_stats = bool(stats)
+        self.opp_deterministic = bool(opp_deterministic)   # PPOGPUConfig.opp_sample = False
+        if self._graph_mode and self.want_stats:
+            raise ValueError("graph=True needs stats=False")
         self._graphs = _RolloutGraph(self, dev) if self._graph_mode else None
+        if self.want_stats:
+            self.min_alt = float(getattr(env, "min_altitude_m", 304.8))
+            self.ep_ret = torch.zeros(ne, dtype=f32, device=dev)
+            self.ep_len = torch.zeros(ne, dtype=f32, device=dev)
+            self._thp = torch.empty(nac, dtype=torch.float64, device=dev)
+            self._talt = torch.empty(nac, dtype=torch.float64, device=dev)
         # the opponents' grouping and launch run on a second stream (default priority) beside
         # the learner's normalisation and launch; both join before the env step
         self._side = None
@@ -333,6 +350,9 @@ class LeagueRollout:
         self.env.opp_assign.copy_(torch.as_tensor(ids, dtype=torch.int32))
         self.next_obs = obs.reshape(self.nac, self.D)
         self.next_done.zero_()
+        if self.want_stats:
+            self.ep_ret.zero_()
+            self.ep_len.zero_()
         return obs
 
     def _timed(self, events, fn):
@@ -356,7 +376,8 @@ class LeagueRollout:
         groups = [(net, None, None, nrm) for net, nrm in zip(self.opponents, self.opp_norms)]
         self.policy(obs, groups, rows=self.opp_rows, group_offsets=self.opp_offsets,
                     max_group_rows=self.nenv, nphys=self.nac, step=step, salt=1,
-                    env_actions=self.env.sim.actions, step_base=step_base)
+                    deterministic=self.opp_deterministic, env_actions=self.env.sim.actions,
+                    step_base=step_base)
 
     def _run(self, pol_base=None, env_base=None):
         """The rollout's launches (see SelfPlayRollout._run for the device counters)."""
@@ -367,6 +388,7 @@ class LeagueRollout:
         main = torch.cuda.current_stream(self.device)
         if self._side is None:
             self._side = torch.cuda.Stream(device=self.device)
+        st = self._stats_begin() if self.want_stats else None
         for t in range(T):
             obs = self.next_obs
             if self.b_aux_features is not None:
@@ -387,16 +409,59 @@ class LeagueRollout:
                 env_actions=env.sim.actions, step_base=pol_base))
             main.wait_stream(self._side)
             done_t = self.b_done[t + 1] if t + 1 < T else self.next_done
-            self.next_obs = env.step_rollout(None, done_t, self.finite_acc,
-                                             step_base=env_base, step=t,
-                                             reward0_f32=self.b_rew[t])
+            assign_t = env.opp_assign.clone() if st is not None else None
+            self.next_obs = env.step_rollout(
+                None, done_t, self.finite_acc, step_base=env_base, step=t,
+                reward0_f32=self.b_rew[t], terminal_hp=self._thp if st is not None else None,
+                terminal_alt_m=self._talt if st is not None else None)
+            if st is not None:
+                self._stats_step(st, self.b_rew[t], done_t, assign_t)
         self.policy(self.next_obs, [(self.net, 0, self.nenv)], norm=self.norm,
                     rows=self.main_rows, nphys=self.nac, step=g0 + T, value=self.last_val,
                     step_base=pol_base)
         _aux_labels(self)
         adv, ret = gae(self.b_rew, self.b_val, self.b_done, self.last_val, self.next_done,
                        self.gamma, self.lam)
-        return adv, ret, {}
+        return adv, ret, (st if st is not None else {})
+
+    def _stats_begin(self):
+        dev, P = self.device, len(self.opponents)
+        z = lambda: torch.zeros((), device=dev)
+        return {"ret_sum": z(), "len_sum": z(), "ep_count": z(), "win_sum": z(),
+                "loss_sum": z(), "alt_loss_sum": z(), "opponent_alt_loss_sum": z(),
+                "opponent_ids": torch.arange(P, device=dev),
+                "win_by_opp": torch.zeros(P, device=dev), "loss_by_opp": torch.zeros(P, device=dev),
+                "ep_by_opp": torch.zeros(P, device=dev)}
+
+    def _stats_step(self, st, rew, done, assign):
+        """One step of collect_rollout's bookkeeping (ppo_gpu.py:1940-1969) from the learner's
+        reward, the done flags, the terminal HP / altitude rows and the step's assignment."""
+        self.ep_ret += rew
+        self.ep_len += 1.0
+        st["ret_sum"] += (self.ep_ret * done).sum()
+        st["len_sum"] += (self.ep_len * done).sum()
+        st["ep_count"] += done.sum()
+        keep = 1.0 - done
+        self.ep_ret.mul_(keep)
+        self.ep_len.mul_(keep)
+        th = self._thp.view(self.nenv, 2)
+        ta = self._talt.view(self.nenv, 2)
+        own_alt_dead = ta[:, 0] < self.min_alt
+        own_dead = (th[:, 0] <= 0.0) | own_alt_dead
+        opp_dead = (th[:, 1] <= 0.0) | (ta[:, 1] < self.min_alt)
+        both_alive = ~own_dead & ~opp_dead
+        win = (opp_dead & ~own_dead) | (both_alive & (th[:, 0] > th[:, 1] + 1e-9))
+        loss = (own_dead & ~opp_dead) | (both_alive & (th[:, 0] < th[:, 1] - 1e-9))
+        done_b = done.bool()
+        dwin, dloss = (win & done_b).float(), (loss & done_b).float()
+        st["win_sum"] += dwin.sum()
+        st["loss_sum"] += dloss.sum()
+        st["alt_loss_sum"] += (loss & own_alt_dead & done_b).float().sum()
+        st["opponent_alt_loss_sum"] += (win & (ta[:, 1] < self.min_alt) & done_b).float().sum()
+        rows = assign.long()
+        st["win_by_opp"].scatter_add_(0, rows, dwin)
+        st["loss_by_opp"].scatter_add_(0, rows, dloss)
+        st["ep_by_opp"].scatter_add_(0, rows, done_b.float())
 
     def collect(self):
         """One rollout of T steps; returns (adv, ret) as (T, nenv) and a stats dict."""

@@ -448,7 +448,7 @@ class GpuDogfightVecEnv:
         return bool(self.obr._lib.f16_env_post_step_norm_fusable(self.nenv, self.OBS_SIZE))
 
     def step_rollout(self, reward_f32, done_f32, finite_acc, step_base=None, step=0, norm=None,
-                     reward0_f32=None):
+                     reward0_f32=None, terminal_hp=None, terminal_alt_m=None):
         """The rollout collector's step: the controls already sit in sim.actions (written by the
         policy kernel); the physics and the post-physics step (one launch, _advance) write the
         float32 rewards (nac,) and done flags (nenv,) straight into the caller's buffers and clear
@@ -459,7 +459,9 @@ class GpuDogfightVecEnv:
         norm (a RunningNorm, only where norm_fusable()): the launch also writes the partial sums
         of the new observation rows into its workspace, for norm.merge(nac).  reward_f32 may be
         None when reward0_f32 (nenv,) is given: the launch then writes only each engagement's
-        first aircraft's reward, straight into a learner-side buffer."""
+        first aircraft's reward, straight into a learner-side buffer.  terminal_hp and
+        terminal_alt_m (float64 (nac,), optional) receive step()'s info["terminal_hp"] and
+        info["terminal_alt_m"] rows."""
         self._ensure_ic_pool()
         state_fin = self._state_fin if self.fused_finite and self.substeps >= 1 else None
         io = self._io(None)
@@ -471,9 +473,19 @@ class GpuDogfightVecEnv:
         io.reward0_f32 = reward0_f32.data_ptr() if reward0_f32 is not None else None
         io.done_f32 = done_f32.data_ptr()
         io.finite_acc = finite_acc.data_ptr()
+        for t in (terminal_hp, terminal_alt_m):
+            if t is not None and (t.dtype != torch.float64 or t.numel() != self.nac or
+                                  not t.is_contiguous() or t.device != self._obs.device):
+                raise ValueError("terminal_hp / terminal_alt_m: contiguous float64 (nac,) on the "
+                                 "env's device")
+        if terminal_hp is not None:
+            io.terminal_hp = terminal_hp.data_ptr()
+        if terminal_alt_m is not None:
+            io.terminal_alt_m = terminal_alt_m.data_ptr()
         if norm is not None:
             norm.fused_partials(io, self.nac)
-        self._call_tensors = (reward_f32, reward0_f32, done_f32, finite_acc, step_base) + (
+        self._call_tensors = (reward_f32, reward0_f32, done_f32, finite_acc, step_base,
+                              terminal_hp, terminal_alt_m) + (
             (norm._work, norm.count) if norm is not None else ())
         self._advance(io, self.sim.actions, state_fin)
         return self._obs.view(self.nac, self.OBS_SIZE)
