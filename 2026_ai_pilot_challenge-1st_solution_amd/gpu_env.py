@@ -43,7 +43,7 @@ class GpuDogfight:
                  max_registers="auto", fcs_rate=120, device="cuda"):
         if precision != "fp64":
             raise ValueError("GpuDogfight on MI355X runs the validated fp64 model only "
-                             "(MI355X fp64 vector rate equals its fp32 rate)")
+                             "(precision='fp64')")
         if not torch.cuda.is_available():
             raise RuntimeError("GpuDogfight needs a HIP device")
         if fcs_rate not in (120, 60):
