@@ -831,10 +831,13 @@ def main():
         print(json.dumps(head), flush=True)
         return
     # the other named sizes of the flight model: BASELINE C2 (4,096 tail-chase engagements,
-    # its 1,000 decisions as one region) and C5's 65,536 engagements
+    # its 1,000 decisions as one region), C5's 65,536 engagements, and one GPU's share of C4
+    # on 8 and 2 GPUs (2,048 and 8,192 engagements: occupancy and tail effects)
     sizes = {}
     for ne, steps, label in ((4096, 1000, "fdm_c2_tailchase_4k_1000dec"),
-                             (65536, args.steps, "fdm_tailchase_64k")):
+                             (65536, args.steps, "fdm_tailchase_64k"),
+                             (2048, args.steps, "fdm_tailchase_2k"),
+                             (8192, args.steps, "fdm_tailchase_8k")):
         # C2 has no termination: over 1,000 decisions some aircraft fly into the ground and
         # past the model's range (counted in nonfinite_aircraft_after_region)
         r = fdm_section(pkg, icm, ne, S, steps, args.warmup, args.reps, label,
