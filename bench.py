@@ -1,6 +1,6 @@
 #!/usr/bin/env python3
-"""Benchmark of the batched F-16 step on one MI355X (see DESIGN.md for the workload and the
-roofline accounting).
+"""Benchmark of the batched F-16 step on one MI355X, with each kernel's roofline fraction
+(algorithmic FLOPs or bytes per launch over its measured duration) and a CPU baseline.
 
 A "step" is one decision of the batched flight model: every aircraft of 16,384 tail-chase
 engagements (32,768 aircraft) advances 6 substeps of 1/60 s with its random 21-bin action
@@ -798,7 +798,7 @@ def main():
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         sys.stderr.write("bench.py measures one GPU only: this build has no multi-GPU path "
-                         "(engagements shard with zero communication; see DESIGN.md).\n")
+                         "(engagements shard with zero communication).\n")
         sys.exit(2)
 
     import torch
