@@ -101,6 +101,8 @@ _SIGNATURES = {
     "f16_seed_batch": (_i, [_vp, _i, _i, _vp, _l, _vp, _vp]),
     "f16_fdm_kernel_info": (_i, [_i, ctypes.POINTER(_i)]),
     "f16_fdm_kernel_info_onelane": (_i, [_i, ctypes.POINTER(_i)]),
+    "f16_fdm_step_batch_f32": (_i, [_vp, _l, _vp, _i, _i, _i, _vp, _l, _vp]),
+    "f16_fdm_kernel_info_f32": (_i, [_i, ctypes.POINTER(_i)]),
     "f16_gae": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, ctypes.c_float, ctypes.c_float, _vp,
                      _vp, _vp]),
     "f16_obr_advance": (_i, [_vp, _l, _vp, _RP, _CP, _vp, _vp, _vp, _vp]),

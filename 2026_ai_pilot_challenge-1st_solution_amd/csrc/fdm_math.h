@@ -1,5 +1,6 @@
 // fdm_math.h -- short-latency fp64 division, reciprocal, square root, exp and log for the
-// dependency chains of the FDM kernels.
+// dependency chains of the FDM kernels, and the finite-flag accumulator (the FDM's
+// precision-specific primitives; fdm_math_f32.h holds the single-precision ones).
 //
 // Each FDM role runs one wavefront per SIMD, so nothing hides the latency of a dependent
 // operation: every division, square root or transcendental on a chain costs its full latency.
@@ -118,6 +119,15 @@ F16_DEV double fm_log(double x) {
   const double special = x == 0.0 ? -__builtin_inf() : (x == __builtin_inf() ? x : __builtin_nan(""));
   return (x > 0.0 && x < __builtin_inf()) ? y : special;
 }
+
+// Finite-flag accumulator: the largest IEEE exponent field seen (high word & 0x7ff00000); every
+// value was finite iff the result is below kFinInf.  Two 32-bit VALU operations per value, no
+// lane masks.
+F16_DEV unsigned fin_acc(unsigned m, double x) {
+  const unsigned hi = (unsigned)((unsigned long long)__double_as_longlong(x) >> 32);
+  return max(m, hi & 0x7ff00000u);
+}
+constexpr unsigned kFinInf = 0x7ff00000u;
 
 #undef F16_DEV
 

@@ -29,6 +29,7 @@
 // The two groups of a workgroup map their roles to waves in opposite orders, so each SIMD
 // (wave w and w + 4 of the workgroup) holds two roles that are busy in different phases.
 #pragma once
+#include "fdm_image.h"
 #include "fdm_split.h"
 
 namespace f16 {
@@ -442,6 +443,43 @@ __device__ __forceinline__ void quad_air(double* __restrict__ s, long ld,
     if (store)
       fin[0] = (m < kFinInf && x[kQFinKin][lane] != 0.0 && x[kQFinFcs][lane] != 0.0) ? 1 : 0;
   }
+}
+
+// ------------------------------------------------------------------ the kernel
+// The four-role form: each 64 aircraft on four wavefronts, G groups per
+// workgroup of 256 G threads.  G = 2: 16,384 engagements put two wavefronts on every SIMD (at
+// most 256 registers each) where the two-wave kernel has one, the two groups' roles paired on
+// each SIMD by quad_role.  G = 1: a batch too small to give every CU a two-group workgroup
+// spreads over twice as many CUs, one wavefront per SIMD (the two group orders alternate
+// between workgroups).  The same results bit for bit.  OBS: the 17-value output is written
+// (its own instantiation: 255 registers with it, 225 without).
+template <int FCS_RATE, bool OBS, int G>
+__global__ __launch_bounds__(256 * G) void fdm_step_quad_kernel(
+    double* __restrict__ st, long ld, const double* __restrict__ act, int nac, int S,
+    double* __restrict__ obs, long obs_ld, unsigned char* __restrict__ fin,
+    double* __restrict__ act_keep) {
+  static_assert(G == 1 || G == kQuadGroups, "one or two 64-aircraft groups per workgroup");
+  __shared__ double T[F16M_IMAGE_LEN];
+  __shared__ QuadX X[G];
+  stage_image<256 * G>(T);
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int grp = wave >> 2;
+  const int role = quad_role(G == 1 ? (int)(blockIdx.x & 1) : grp, wave & 3);
+  const int i = blockIdx.x * (64 * G) + grp * 64 + lane;
+  const bool store = i < nac;
+  const int ia = store ? i : nac - 1;   // lanes past the batch shadow the last aircraft
+  if (role == kRoleKin)
+    quad_kin<FCS_RATE>(st + ia, ld, S, store, OBS ? obs + ia : nullptr, obs_ld, T, X[grp], lane,
+                       fin != nullptr);
+  else if (role == kRoleAero)
+    quad_aero<FCS_RATE>(S, T, X[grp], lane, fin != nullptr);
+  else if (role == kRoleFcs)
+    quad_fcs<FCS_RATE>(st + ia, ld, act + 4L * ia, S, store, T, X[grp], lane, fin != nullptr,
+                       act_keep ? act_keep + 4L * ia : nullptr);
+  else
+    quad_air<FCS_RATE>(st + ia, ld, act + 4L * ia, S, store, T, X[grp], lane,
+                       fin ? fin + ia : nullptr);
 }
 
 }  // namespace f16

@@ -70,15 +70,6 @@ __device__ __forceinline__ int mass_block(int t) { return (t & 1) ? kXMass2 - kX
 
 typedef double SplitX[kSplitFields][64];
 
-// Finite-flag accumulator: the largest IEEE exponent field seen (high word & 0x7ff00000); every
-// value was finite iff the result is below 0x7ff00000.  Two 32-bit VALU operations per value,
-// no lane masks.
-__device__ __forceinline__ unsigned fin_acc(unsigned m, double x) {
-  const unsigned hi = (unsigned)((unsigned long long)__double_as_longlong(x) >> 32);
-  return max(m, hi & 0x7ff00000u);
-}
-constexpr unsigned kFinInf = 0x7ff00000u;
-
 // The flight wave of one pair.  `s`: the aircraft's state field 0 (fields `ld` apart); `store`:
 // whether this lane's aircraft exists (lanes past the batch shadow the last aircraft and store
 // nothing).  Issues exactly 3 barriers per substep, like split_systems.

@@ -7,7 +7,10 @@ methods).  Differences in mechanism, not in contract:
     while the kernel reads and writes coalesced columns;
   * the kernel is precompiled gfx950 code in libf16hip.so, launched through the C ABI on the
     caller's current stream (no JIT, no register-cap option);
-  * ``reset_ic`` seeds on the device (f16_seed_batch) instead of in host Python.
+  * ``reset_ic`` seeds on the device (f16_seed_batch) instead of in host Python;
+  * precision="fp32" runs f16_fdm_step_batch_f32, the same model generated in single precision
+    at build time (as the reference generates its fp32 kernel from the fp64 source); seeds are
+    computed in fp64 and rounded, as the reference's load_seed does.
 """
 import math
 
@@ -41,9 +44,8 @@ class GpuDogfight:
 
     def __init__(self, nenv, substeps=1, planes_per_env=2, block=128, precision="fp64",
                  max_registers="auto", fcs_rate=120, device="cuda"):
-        if precision != "fp64":
-            raise ValueError("GpuDogfight on MI355X runs the validated fp64 model only "
-                             "(precision='fp64')")
+        if precision not in ("fp64", "fp32"):
+            raise ValueError("precision must be 'fp64' or 'fp32'")
         if not torch.cuda.is_available():
             raise RuntimeError("GpuDogfight needs a HIP device")
         if fcs_rate not in (120, 60):
@@ -57,13 +59,13 @@ class GpuDogfight:
         self.precision = precision
         self.max_registers = max_registers  # accepted for compatibility (no JIT register cap)
         self.fcs_rate = int(fcs_rate)
-        self.dtype = torch.float64
+        self.dtype = torch.float32 if precision == "fp32" else torch.float64
         self._lib = _lib.lib()
-        self._state_soa = torch.zeros(STATE_N, self.nac, dtype=torch.float64, device=self.device)
-        self._obs_soa = torch.zeros(OBS_N, self.nac, dtype=torch.float64, device=self.device)
+        self._state_soa = torch.zeros(STATE_N, self.nac, dtype=self.dtype, device=self.device)
+        self._obs_soa = torch.zeros(OBS_N, self.nac, dtype=self.dtype, device=self.device)
         self.states = self._state_soa.t()      # (nac, 101) view of the SoA buffer
         self.obs = self._obs_soa.t()           # (nac, 17) view
-        self.actions = torch.zeros(self.nac, 4, dtype=torch.float64, device=self.device)
+        self.actions = torch.zeros(self.nac, 4, dtype=self.dtype, device=self.device)
         # When set to a list, every launch appends a (start, end) pair of timing events
         # recorded on the launch stream immediately around the kernel (bench/profiling).
         self.kernel_events = None
@@ -75,9 +77,13 @@ class GpuDogfight:
         return self.kernel_info(onelane=False)
 
     def kernel_info(self, onelane=False):
-        """Footprint of the four-wave kernel `step` launches (default) or of the one-lane kernel."""
+        """Footprint of the four-wave kernel `step` launches (default) or of the one-lane kernel;
+        with precision="fp32", of the single-precision kernel (one lane per aircraft)."""
         out = (_lib.ctypes.c_int * 4)()
-        fn = self._lib.f16_fdm_kernel_info_onelane if onelane else self._lib.f16_fdm_kernel_info
+        if self.precision == "fp32":
+            fn = self._lib.f16_fdm_kernel_info_f32
+        else:
+            fn = self._lib.f16_fdm_kernel_info_onelane if onelane else self._lib.f16_fdm_kernel_info
         _lib.check(fn(self.fcs_rate, out), "f16_fdm_kernel_info")
         return dict(regs=out[0], lds=out[1], scratch=out[2], max_threads=out[3])
 
@@ -124,21 +130,26 @@ class GpuDogfight:
                 raise IndexError(f"rows must lie in [0, {self.nac})")
         elif n != self.nac:
             raise ValueError("without rows, n must equal nac")
+        # fp32: seed an fp64 copy of the state (rows not seeded keep their values exactly) and
+        # round it back
+        soa = self._state_soa if self.precision == "fp64" else self._state_soa.double()
         stream, h = _lib.launch_stream(self.device)
-        rc = self._lib.f16_seed_batch(_lib.ptr(ic), n, self.fcs_rate, _lib.ptr(self._state_soa),
+        rc = self._lib.f16_seed_batch(_lib.ptr(ic), n, self.fcs_rate, _lib.ptr(soa),
                                       self.nac, _lib.ptr(rows), h)
-        _lib.record(stream, (ic, rows))
+        _lib.record(stream, (ic, rows, soa))
         _lib.record_owned(self, stream, self._buffers())
         _lib.check(rc, "f16_seed_batch")
+        if soa is not self._state_soa:
+            self._state_soa.copy_(soa)
 
     # ---- step (cuda_fdm/gpu_env.py:95-106) ----
     def action_source(self, actions):
-        """The (nac, 4) float64 device tensor a step launch reads its controls from.  The
+        """The (nac, 4) device tensor (self.dtype) a step launch reads its controls from.  The
         reference copies the actions into self.actions before its launch; a separate contiguous
         device tensor is returned as is (the launch reads it and writes the copy itself),
         anything else is copied into self.actions here and self.actions is returned."""
-        a = torch.as_tensor(actions, dtype=torch.float64, device=self.device).reshape(self.nac, 4)
-        if (a.is_contiguous() and a.untyped_storage().data_ptr()
+        a = torch.as_tensor(actions, dtype=self.dtype, device=self.device).reshape(self.nac, 4)
+        if self.precision == "fp64" and (a.is_contiguous() and a.untyped_storage().data_ptr()
                 != self.actions.untyped_storage().data_ptr()):
             return a
         if a.data_ptr() != self.actions.data_ptr():
@@ -149,8 +160,11 @@ class GpuDogfight:
         """actions (nac,4) or (nenv,ppe,4) [aileron, elevator, rudder, throttle] -> obs view
         (nenv, ppe, 17).  want_obs=False skips the 17-value output write.  finite_out: an
         optional (nac,) uint8/bool device tensor that receives, per aircraft, whether all 101
-        state values after the step are finite (f16_fdm_step_batch_finite; substeps >= 1)."""
+        state values after the step are finite (f16_fdm_step_batch_finite; substeps >= 1; fp64
+        only)."""
         ss = self.substeps if substeps is None else int(substeps)
+        if finite_out is not None and self.precision != "fp64":
+            raise ValueError("finite_out is available with precision='fp64' only")
         if finite_out is not None:
             if (finite_out.dtype not in (torch.uint8, torch.bool) or finite_out.numel() != self.nac
                     or not finite_out.is_contiguous() or finite_out.device != self.states.device):
@@ -165,7 +179,11 @@ class GpuDogfight:
             e0.record()
         obs_p = _lib.ptr(self._obs_soa) if want_obs else None
         stream, h = _lib.launch_stream(self.device)
-        if keep:
+        if self.precision == "fp32":
+            rc = self._lib.f16_fdm_step_batch_f32(
+                _lib.ptr(self._state_soa), self.nac, _lib.ptr(self.actions), self.nac, ss,
+                self.fcs_rate, obs_p, self.nac, h)
+        elif keep:
             rc = self._lib.f16_fdm_step_batch_keep(
                 _lib.ptr(self._state_soa), self.nac, _lib.ptr(a), _lib.ptr(self.actions),
                 self.nac, ss, self.fcs_rate, obs_p, self.nac,

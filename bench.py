@@ -36,10 +36,11 @@ def _flop_per_substep(sample="c2_tailchase"):
 
 
 FLOP_PER_SUBSTEP = _flop_per_substep()
-# Algorithmic HBM bytes of one aircraft per launch of the flight model: the 66 state doubles a
-# launch reads, the 101 it writes, and its 4 action doubles
+# Algorithmic HBM bytes of one aircraft per launch of the fp64 flight model: the 66 state doubles
+# a launch reads, the 101 it writes, and its 4 action doubles (half of it in the fp32 build)
 FDM_BYTES_PER_AIRCRAFT = (66 + 101 + 4) * 8
 PEAK_FP64_TFLOPS = 78.6
+PEAK_FP32_TFLOPS = 157.3
 PEAK_HBM_GBS = 8000.0
 # reference's published GpuDogfight.step rate at 16k envs (RTX 3070 Ti, cuda_fdm/README.md:130)
 REF_PUBLISHED_SUBSTEPS = 37.0e6
@@ -665,7 +666,7 @@ def league_bench(nenv=65536, T=128, nopp=8, reps=5):
 
 
 def fdm_section(pkg, icm, nenv, S, steps, warmup, reps, label, check_replay=True,
-                require_finite=True):
+                require_finite=True, precision="fp64"):
     """The batched flight model alone: nenv tail-chase engagements (BASELINE configs[1]
     initial conditions), random 21-bin actions held per decision, `steps` decisions of S
     substeps per timed region, inputs resident in HBM.  Each region is timed `reps` times
@@ -676,13 +677,15 @@ def fdm_section(pkg, icm, nenv, S, steps, warmup, reps, label, check_replay=True
                 arguments and records its tensors' stream use on the host).
     A third pass with HIP events around each launch gives the launch duration on its own and
     checks that it reproduces the eager region's states bit for bit.  Every region starts from
-    the same states (those after the warm-up decisions), so all regions time one trajectory."""
+    the same states (those after the warm-up decisions), so all regions time one trajectory.
+    precision="fp32": the single-precision build (its state, actions and bytes in float)."""
     import torch
     nac = 2 * nenv
-    sim = pkg.GpuDogfight(nenv, substeps=S, fcs_rate=120)
+    sim = pkg.GpuDogfight(nenv, substeps=S, fcs_rate=120, precision=precision)
+    bits = torch.int64 if precision == "fp64" else torch.int32
     sim.seed_rows(torch.as_tensor(icm.sample_tailchase(nenv, seed=0), device="cuda"))
     acts_host = icm.random_bin_actions(warmup + steps, nac, seed=0)
-    acts = torch.as_tensor(acts_host, device="cuda").contiguous()
+    acts = torch.as_tensor(acts_host, device="cuda", dtype=sim.dtype).contiguous()
     torch.cuda.synchronize()
     states0 = sim.states.cpu().numpy().copy()
     for k in range(warmup):
@@ -703,7 +706,8 @@ def fdm_section(pkg, icm, nenv, S, steps, warmup, reps, label, check_replay=True
     if require_finite and nonfinite:
         raise FloatingPointError("non-finite state after the timed steps")
     out = {"workload": label, "engagements": nenv, "aircraft": nac, "substeps_per_step": S,
-           "fcs_rate_hz": 120, "steps_per_region": steps, "regions": reps}
+           "fcs_rate_hz": 120, "steps_per_region": steps, "regions": reps,
+           "precision": precision}
     if check_replay:
         # the launch on its own: one region again from the snapshot, events around each launch
         sim.states.copy_(snap)
@@ -714,7 +718,7 @@ def fdm_section(pkg, icm, nenv, S, steps, warmup, reps, label, check_replay=True
         eager()
         torch.cuda.synchronize()
         kev, sim.kernel_events = sim.kernel_events, None
-        if not torch.equal(sim.states.view(torch.int64), after.view(torch.int64)):
+        if not torch.equal(sim.states.view(bits), after.view(bits)):
             raise RuntimeError("the instrumented pass did not reproduce the timed steps")
         out["kernel_ms_per_launch_events"] = float(np.median([a.elapsed_time(b) for a, b in kev]))
     # the same steps recorded as a HIP graph
@@ -729,11 +733,13 @@ def fdm_section(pkg, icm, nenv, S, steps, warmup, reps, label, check_replay=True
     end = sim.states.clone()
     sim.states.copy_(snap)
     eager()
-    if not torch.equal(sim.states.view(torch.int64), end.view(torch.int64)):
+    if not torch.equal(sim.states.view(bits), end.view(bits)):
         raise RuntimeError("the graph replay did not reproduce the eager steps")
     del g
     gm, em = float(np.median(graph_ms)) / steps, float(np.median(eager_ms)) / steps
     flop = FLOP_PER_SUBSTEP * nac * S
+    word = 8 if precision == "fp64" else 4
+    peak = PEAK_FP64_TFLOPS if precision == "fp64" else PEAK_FP32_TFLOPS
     out.update({
         "nonfinite_aircraft_after_region": nonfinite,
         "ms_per_step": gm, "aircraft_substeps_per_s": nac * S / (gm * 1e-3),
@@ -743,9 +749,9 @@ def fdm_section(pkg, icm, nenv, S, steps, warmup, reps, label, check_replay=True
         "eager_host_ms_per_step": wall * 1e3 / steps,
         "flop_per_launch": flop,
         "achieved_TFLOPs": flop / (gm * 1e-3) / 1e12,
-        "frac_fp64_peak": flop / (gm * 1e-3) / 1e12 / PEAK_FP64_TFLOPS,
-        "algorithmic_bytes": FDM_BYTES_PER_AIRCRAFT * nac,
-        "achieved_GBs": FDM_BYTES_PER_AIRCRAFT * nac / (gm * 1e-3) / 1e9})
+        f"frac_{precision}_peak": flop / (gm * 1e-3) / 1e12 / peak,
+        "algorithmic_bytes": FDM_BYTES_PER_AIRCRAFT // 8 * word * nac,
+        "achieved_GBs": FDM_BYTES_PER_AIRCRAFT // 8 * word * nac / (gm * 1e-3) / 1e9})
     out["frac_hbm_peak"] = out["achieved_GBs"] / PEAK_HBM_GBS
     out["_states0"] = states0
     out["_acts_host"] = acts_host[warmup:]
@@ -782,6 +788,8 @@ def main():
                     default=None,
                     help="profiling aid: run only this section and print its own JSON line "
                          "(not the contract line)")
+    ap.add_argument("--precision", choices=["fp64", "fp32"], default="fp64",
+                    help="with --only fdm: time this build of the flight model (profiling aid)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run 5 device-to-device copies of MIB MiB (rocprof counter "
                          "calibration: FETCH_SIZE/WRITE_SIZE of a copy of known size)")
@@ -823,9 +831,11 @@ def main():
     nac = 2 * nenv
     # (long regions, as C2's 1,000 decisions, fly some aircraft past the model's range: counted,
     # not an error)
+    prec = args.precision if args.only == "fdm" else "fp64"
     head = fdm_section(pkg, icm, nenv, S, args.steps, args.warmup, args.reps,
-                       "fdm_tailchase_16k" if nenv == 16384 else f"fdm_tailchase_{nenv}",
-                       require_finite=args.steps <= 100)
+                       ("fdm_tailchase_16k" if nenv == 16384 else f"fdm_tailchase_{nenv}")
+                       + ("_fp32" if prec == "fp32" else ""),
+                       require_finite=args.steps <= 100, precision=prec)
     states0, acts_host = head.pop("_states0"), head.pop("_acts_host")
     if args.only == "fdm":
         print(json.dumps(head), flush=True)
@@ -834,14 +844,17 @@ def main():
     # its 1,000 decisions as one region), C5's 65,536 engagements, and one GPU's share of C4
     # on 8 and 2 GPUs (2,048 and 8,192 engagements: occupancy and tail effects)
     sizes = {}
-    for ne, steps, label in ((4096, 1000, "fdm_c2_tailchase_4k_1000dec"),
-                             (65536, args.steps, "fdm_tailchase_64k"),
-                             (2048, args.steps, "fdm_tailchase_2k"),
-                             (8192, args.steps, "fdm_tailchase_8k")):
+    # and the single-precision build (GpuDogfight precision="fp32") at 16,384 and 65,536
+    for ne, steps, label, prec in ((4096, 1000, "fdm_c2_tailchase_4k_1000dec", "fp64"),
+                                   (65536, args.steps, "fdm_tailchase_64k", "fp64"),
+                                   (2048, args.steps, "fdm_tailchase_2k", "fp64"),
+                                   (8192, args.steps, "fdm_tailchase_8k", "fp64"),
+                                   (16384, args.steps, "fdm_tailchase_16k_fp32", "fp32"),
+                                   (65536, args.steps, "fdm_tailchase_64k_fp32", "fp32")):
         # C2 has no termination: over 1,000 decisions some aircraft fly into the ground and
         # past the model's range (counted in nonfinite_aircraft_after_region)
         r = fdm_section(pkg, icm, ne, S, steps, args.warmup, args.reps, label,
-                        check_replay=False, require_finite=ne != 4096)
+                        check_replay=False, require_finite=ne != 4096, precision=prec)
         r.pop("_states0"), r.pop("_acts_host")
         sizes[label] = r
     env_line = env_step_bench(pkg, nenv, args.steps, args.warmup, reps=args.reps)

@@ -77,6 +77,17 @@ int f16_fdm_kernel_info(int fcs_rate, int* out4);
  * (cuda_fdm/tests/profile_kernel.py:23-33 reads one kernel; this build has two). */
 int f16_fdm_kernel_info_onelane(int fcs_rate, int* out4);
 
+/* The step in single precision: GpuDogfight(precision="fp32") (cuda_fdm/gpu_env.py:33-58, whose
+ * kernel is the fp64 source with every double made float, cuda_fdm/tests/cuda_rt.py:150-160).
+ * states (101, ld) and obs (17, obs_ld) float, structure-of-arrays as above; actions (nac, 4)
+ * float.  The four-wave kernel of f16_fdm_step_batch, compiled from the same model source in
+ * float.  Same argument rules and return codes as f16_fdm_step_batch. */
+int f16_fdm_step_batch_f32(float* states, long ld, const float* actions, int nac, int substeps,
+                           int fcs_rate, float* obs, long obs_ld, void* stream);
+
+/* Footprint of the kernel behind f16_fdm_step_batch_f32, as f16_fdm_kernel_info. */
+int f16_fdm_kernel_info_f32(int fcs_rate, int* out4);
+
 /* Generalized advantage estimation over a rollout buffer (fp32).
  * rew, val, adv, ret: (T, nenv*nagents) time-major, column = env*nagents + agent;
  * done: (T, nenv), done[t] = done flag entering step t; last_val: (nenv*nagents);

@@ -6,6 +6,7 @@
 // steps are exercised from a start at least as bad as the hardware's.  Every result is compared
 // with an 80-bit long-double reference (glibc's expl/logl/sqrtl and exact long-double division)
 // in units of the double result's ulp.  Prints one line of maxima and the special-operand check.
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -20,6 +21,7 @@ static double emu_rsq(double x) { return (1.0 / std::sqrt(x)) * (1.0 - g_pert); 
 #define __builtin_amdgcn_rsq(x) emu_rsq(x)
 static long long __double_as_longlong(double d) { long long v; std::memcpy(&v, &d, 8); return v; }
 static double __longlong_as_double(long long v) { double d; std::memcpy(&d, &v, 8); return d; }
+using std::max;   // HIP's device max(unsigned, unsigned), used by fin_acc
 #include "fdm_math.h"
 
 using namespace f16;

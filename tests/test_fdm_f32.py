@@ -1,0 +1,204 @@
+"""GpuDogfight(precision="fp32"): the single-precision build of the batched F-16 step
+(cuda_fdm/gpu_env.py:33-58; the reference compiles its fp64 source with every double made float,
+cuda_fdm/tests/cuda_rt.py:150-160), and build.py's rewrite that produces it.
+
+There is no fp32 golden output to match bit for bit: the reference's fp32 kernel is a CUDA build
+whose roundings differ from any other compiler's.  Its documented accuracy is the bar
+(cuda_fdm/gpu_env.py:34-36: attitude, velocity and angle of attack at the level of the fp64
+model; the ECI position drifts by about 43 ft in 6 s, the resolution of float at Earth-centred
+coordinates of ~2.1e7 ft being 2 ft).  The tests compare the fp32 kernel with the fp64 CPU
+restatement (oracle/, itself pinned against the reference's golden vectors) from the same
+rounded states, with the bounds written in each test."""
+import os
+import re
+
+import numpy as np
+import pytest
+import torch
+
+import oracle_lib
+from conftest import import_pkg
+
+_LIT = r"(?<![\w.])(?:\d+\.\d*|\.\d+|\d+[eE][+-]?\d+)(?:[eE][+-]?\d+)?"
+_UNSUFFIXED = re.compile(_LIT + r"(?![\w.])")
+_SUFFIXED = re.compile(_LIT + r"[fF](?![\w.])")
+
+
+def test_single_precision_rewrite_known_cases():
+    """Each rule of the rewrite on a hand-written line, including what it must leave alone:
+    integers, identifiers with digits, already-suffixed literals, fm_* calls, member access."""
+    b = import_pkg("build")
+    src = ('constexpr double kDt = 1.0 / 60.0; double x = sqrt(a.b1) + fm_sqrt(y) * 2e-3 + .5 '
+           '+ 3.f + 10 + 1.5E+3 + x2.0; sincos(t, &s, &c); double e = exp(z) * M_PI;\n'
+           '#include "fdm_math.h"\nnamespace f16 {\n')
+    want = ('constexpr float kDt = 1.0f / 60.0f; float x = sqrtf(a.b1) + fm_sqrt(y) * 2e-3f + .5f '
+            '+ 3.f + 10 + 1.5E+3f + x2.0; sincosf(t, &s, &c); float e = expf(z) * ((float)M_PI);\n'
+            '#include "fdm_math_f32.h"\nnamespace f16f {\n')
+    assert b.single_precision(src) == want
+    with pytest.raises(RuntimeError):
+        b.single_precision("double y = f16::fm_sqrt(x);")
+
+
+def test_generated_headers_are_single_precision(tmp_path):
+    """The float copies of the model headers hold no double, no floating literal without its f
+    suffix (which would promote an expression back to fp64), no fp64 math header and no f16
+    namespace; the model tables keep their element count."""
+    b = import_pkg("build")
+    b.write_f32_headers(str(tmp_path))
+    for name in b.F32_HEADERS:
+        text = open(os.path.join(tmp_path, "f32", name)).read()
+        code = re.sub(r"//[^\n]*|/\*.*?\*/", "", text, flags=re.S)
+        assert not re.search(r"\bdouble\b", code), name
+        assert not _UNSUFFIXED.search(code), (name, _UNSUFFIXED.search(code))
+        assert '"fdm_math.h"' not in code and not re.search(r"\bnamespace f16\b", code), name
+    src = open(os.path.join(b.CSRC, "f16_model_gen.h")).read()
+    gen = open(os.path.join(tmp_path, "f32", "f16_model_gen.h")).read()
+    assert len(_SUFFIXED.findall(src)) == 0
+    assert len(_UNSUFFIXED.findall(gen)) == 0
+    assert len(_SUFFIXED.findall(gen)) == len(_UNSUFFIXED.findall(src)) > 1000
+
+
+def _fp32_sim(nenv, rate=120):
+    return import_pkg().GpuDogfight(nenv, substeps=6, fcs_rate=rate, precision="fp32")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("rate", [120, 60])
+def test_f32_seed_is_the_rounded_fp64_seed(gpu, rate):
+    """Seeds are computed in fp64 and rounded (as the reference's load_seed casts its fp64 seed
+    vector): equal bit for bit to the fp64 simulator's seed rounded to float."""
+    g = oracle_lib.golden("seed_golden.npz")
+    n = len(g["ic"])
+    s32, s64 = _fp32_sim(n // 2, rate), import_pkg().GpuDogfight(n // 2, fcs_rate=rate)
+    ic = torch.as_tensor(g["ic"], device=gpu)
+    s32.seed_rows(ic)
+    s64.seed_rows(ic)
+    assert s32.states.dtype == torch.float32
+    assert torch.equal(s32.states, s64.states.float())
+    s32.states.fill_(7.0)
+    s32.seed_rows(ic[:2], torch.tensor([3, 0], device=gpu))
+    assert torch.equal(s32.states[[3, 0]], s64.states[:2].float())
+    assert bool((s32.states[[1, 2]] == 7.0).all())
+
+
+# One-decision bounds against the fp64 oracle (absolute, in the quantity's unit, unless named
+# "scaled": |difference| / the largest |value| of its vector over the batch).  fp32 rounds each
+# operation to 6e-8 relative; the ECI position (~2.1e7 ft) is held to 2 ft, and what is
+# computed from it inherits that: the altitude (|r| - R, a difference of two ~2.1e7 ft numbers)
+# and through it the temperature, the speed of sound and the Mach number.
+# Measured worst (both FCS rates): position 5.1 ft, velocity 1.4e-3 ft/s, quaternion 9.9e-7,
+# body rates 8.5e-5, other state 1.9e-4 scaled, angles 2.7e-6 rad, Mach 2.2e-5, Vt 4.5e-4 ft/s,
+# altitude 6.2 ft.
+ONE_DECISION_BOUNDS = {
+    "position ft": 12.0,                 # 6 substeps x half a 2 ft float spacing per component
+    "velocity ft/s": 5e-3,
+    "quaternion": 4e-6,
+    "body rates rad/s": 4e-4,
+    "other state, scaled": 1e-3,         # accelerations, histories, previous-frame values
+    "output euler, alpha, beta rad": 1e-5,
+    "output mach": 1e-4,
+    "output Vt ft/s": 4e-3,
+    "output altitude ft": 16.0,
+}
+_ACTUATORS = list(range(86, 92))         # F16S_KIN: tef, aileron, elevator, rudder, gear, lef
+_OTHER = [k for k in range(13, 101) if k not in _ACTUATORS]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("rate", [120, 60])
+def test_f32_one_decision_against_fp64_oracle(gpu, orc, worst, rate):
+    """11 decisions (6 substeps each) of random 21-bin actions from the C1 replicas' seeded
+    states (1,024 aircraft); before each, the oracle takes the fp32 kernel's state (exactly, in
+    fp64) and steps it in fp64.  Bounds: ONE_DECISION_BOUNDS, and at most 1 % of aircraft
+    decisions with an actuator one step apart (a comparison of two nearly equal values that fp32
+    rounds the other way; measured 0.04 %).  The size of such a step is the actuator's rate
+    limit times the FCS period, not an fp32 rounding, and is not bounded here; that the steps
+    do not accumulate is test_f32_six_seconds_free_flight's bound on the trajectory."""
+    icm = import_pkg("ic")
+    ic, acts = oracle_lib.c1_replicas(icm)
+    sim = _fp32_sim(len(ic) // 2, rate)
+    sim.seed_rows(torch.as_tensor(ic, device=gpu))
+    meas = dict.fromkeys(ONE_DECISION_BOUNDS, 0.0)
+    flips = 0
+    for d in range(11):
+        prev = sim.states.double().cpu().numpy().copy()
+        obs = sim.step(torch.as_tensor(acts[d], device=gpu)).reshape(-1, 17).double().cpu().numpy()
+        got = sim.states.double().cpu().numpy()
+        want = prev.copy()
+        want_obs = orc.step(want, acts[d], 6, fcs_rate=rate)
+        assert np.isfinite(got).all()
+        ad, sc = np.abs(got - want), oracle_lib.scaled_abs_err(got, want)
+        od = np.abs(obs - want_obs)
+        od[:, 6:9] = np.minimum(od[:, 6:9], 2 * np.pi - od[:, 6:9])   # angles wrap at 2 pi
+        for key, v in (("position ft", np.linalg.norm(got[:, :3] - want[:, :3], axis=1).max()),
+                       ("velocity ft/s", np.linalg.norm(got[:, 3:6] - want[:, 3:6], axis=1).max()),
+                       ("quaternion", ad[:, 6:10].max()), ("body rates rad/s", ad[:, 10:13].max()),
+                       ("other state, scaled", sc[:, _OTHER].max()),
+                       ("output euler, alpha, beta rad", od[:, [6, 7, 8, 12, 13]].max()),
+                       ("output mach", od[:, 14].max()), ("output Vt ft/s", od[:, 15].max()),
+                       ("output altitude ft", od[:, 16].max())):
+            meas[key] = max(meas[key], float(v))
+        flips += int((sc[:, _ACTUATORS].max(1) > 1e-3).sum())
+    for key, b in ONE_DECISION_BOUNDS.items():
+        worst(f"f32 one decision {key} (rate {rate})", meas[key], b)
+    worst(f"f32 one decision actuator flips, share (rate {rate})", flips / (11 * len(ic)), 0.01)
+    assert all(meas[k] <= b for k, b in ONE_DECISION_BOUNDS.items()), meas
+    assert flips <= 0.01 * 11 * len(ic)
+
+
+@pytest.mark.gpu
+def test_f32_six_seconds_free_flight(gpu, orc, worst):
+    """60 decisions (6 s) free-running from the C1 replicas' seeded states with the stick
+    centred and throttle 0.8, fp32 kernel against the fp64 oracle from the same rounded start.
+    Bounds: ECI position median <= 150 ft and every aircraft <= 720 ft (2 ft, one float spacing,
+    per substep); velocity <= 1 ft/s; quaternion components <= 2.5e-4; Euler angles, alpha and
+    beta <= 6e-4 rad; true airspeed <= 1 ft/s.  Measured: position median 71 ft and max 217 ft
+    (the reference quotes ~43 ft in 6 s for its fp32 build), velocity 0.20 ft/s, quaternion
+    5.8e-5, angles 1.5e-4 rad, Vt 0.15 ft/s."""
+    icm = import_pkg("ic")
+    ic, _ = oracle_lib.c1_replicas(icm)
+    sim = _fp32_sim(len(ic) // 2)
+    sim.seed_rows(torch.as_tensor(ic, device=gpu))
+    st = sim.states.double().cpu().numpy().copy()
+    act = np.tile(np.array([0.0, 0.0, 0.0, 0.8]), (len(ic), 1))
+    act_t = torch.as_tensor(act, device=gpu)
+    for _ in range(60):
+        obs = sim.step(act_t)
+        want_obs = orc.step(st, act, 6)
+    got = sim.states.double().cpu().numpy()
+    obs = obs.reshape(-1, 17).double().cpu().numpy()
+    pos = np.linalg.norm(got[:, :3] - st[:, :3], axis=1)
+    vel = np.linalg.norm(got[:, 3:6] - st[:, 3:6], axis=1)
+    q = np.abs(got[:, 6:10] - st[:, 6:10]).max()
+    ang = np.abs(obs[:, [6, 7, 8, 12, 13]] - want_obs[:, [6, 7, 8, 12, 13]])
+    ang = np.minimum(ang, 2 * np.pi - ang).max()        # heading wraps at 2 pi
+    vt = np.abs(obs[:, 15] - want_obs[:, 15]).max()
+    for name, v, b in (("position median ft", np.median(pos), 150.0), ("position max ft",
+                       pos.max(), 720.0), ("velocity ft/s", vel.max(), 1.0),
+                       ("quaternion", q, 2.5e-4), ("angles rad", ang, 6e-4), ("Vt ft/s", vt, 1.0)):
+        worst(f"f32 6 s free flight {name}", v, b)
+        assert v <= b, (name, v, b)
+
+
+@pytest.mark.gpu
+def test_f32_argument_errors(gpu):
+    pkg = import_pkg()
+    L = import_pkg("_lib")
+    with pytest.raises(ValueError):
+        pkg.GpuDogfight(2, precision="fp16")
+    sim = _fp32_sim(2)
+    assert sim.dtype == torch.float32 and sim.kern["scratch"] == 0
+    with pytest.raises(ValueError):
+        sim.step(torch.zeros(4, 4, device=gpu), finite_out=torch.zeros(4, dtype=torch.uint8,
+                                                                       device=gpu))
+    lib, p, h = L.lib(), L.ptr, L.stream_handle()
+    assert lib.f16_fdm_step_batch_f32(p(sim._state_soa), 2, p(sim.actions), 4, 6, 120, None, 4,
+                                      h) == L.F16_EINVAL            # ld < nac
+    assert lib.f16_fdm_step_batch_f32(p(sim._state_soa), 4, p(sim.actions), 4, 6, 100, None, 4,
+                                      h) == L.F16_ERATE
+    assert lib.f16_fdm_step_batch_f32(p(sim._state_soa), 4, p(sim.actions), 4, 6, 120,
+                                      p(sim._obs_soa), 2, h) == L.F16_EINVAL   # obs_ld < nac
+    assert lib.f16_fdm_step_batch_f32(None, 0, None, 0, 6, 120, None, 0, h) == 0   # empty
+    before = sim.states.clone()
+    sim.step(torch.zeros(4, 4, device=gpu), substeps=0)
+    assert torch.equal(sim.states, before)

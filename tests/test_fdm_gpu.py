@@ -394,7 +394,7 @@ def test_argument_errors(gpu):
     with pytest.raises(ValueError):
         pkg.GpuDogfight(2, fcs_rate=100)
     with pytest.raises(ValueError):
-        pkg.GpuDogfight(2, precision="fp32")
+        pkg.GpuDogfight(2, precision="fp16")
     sim = _sim(2)
     with pytest.raises(ValueError):
         sim.seed_rows(torch.zeros(3, 9, dtype=torch.float64, device=gpu))
