@@ -1478,6 +1478,20 @@ __device__ __forceinline__ void post_quad_body(const F16EnvStepIO& io, const F16
   }
 }
 
+// post_quad_body on its own: the post-physics step of f16_env_post_step for batches whose rows
+// fit the full-row tile (512-thread workgroups, four wavefronts per 64 aircraft: at 16,384
+// engagements two wavefronts on every SIMD where env_post_step_split_kernel has one).  16,384
+// engagements of random valid states, the launch alone: 28.7 us against 33.1 us.  Giving
+// each role a quarter of the no-flags state scan (86 values that role 0 otherwise reads after
+// the first barrier) was measured at 33.4 us and not kept: the loads then sit before the barrier
+// on every role.
+template <int D>
+__global__ __launch_bounds__(kQuadPostBlock) void env_post_step_quad_kernel(
+    const F16EnvStepIO io, F16Recon r, F16RewardCfg c, Origin O) {
+  __shared__ PostSplitLds<D, true> L;
+  post_quad_body<D>(io, r, c, O, L);
+}
+
 // A whole environment step in one launch, for batches whose rows fit the full-row tile: the
 // workgroup first runs the FDM substeps of its 128 aircraft as fdm_step_split_kernel does (two
 // wavefronts per 64 aircraft, model image and exchange fields in LDS), then, after a workgroup
@@ -1755,8 +1769,11 @@ static int post_step_launch(const F16EnvStepIO* io, const F16Recon* rec, const F
   hipStream_t s = (hipStream_t)stream;
 #define F16_POST_STEP(D, FULL)                                                                  \
   do {                                                                                          \
-    if (split)                                                                                  \
-      hipLaunchKernelGGL((env_post_step_split_kernel<D, FULL>), grid_groups(rec->nenv),         \
+    if (split && FULL)                                                                          \
+      hipLaunchKernelGGL((env_post_step_quad_kernel<D>), grid_groups(rec->nenv),                \
+                         dim3(kQuadPostBlock), 0, s, *io, *rec, *cfg, origin());                \
+    else if (split)                                                                             \
+      hipLaunchKernelGGL((env_post_step_split_kernel<D, false>), grid_groups(rec->nenv),        \
                          dim3(kPostSplitBlock), 0, s, *io, *rec, *cfg, origin());               \
     else                                                                                        \
       hipLaunchKernelGGL((env_post_step_kernel<D, FULL>), grid_rows(rec->nenv), dim3(kRowBlock), \

@@ -384,7 +384,7 @@ def env_step_bench(pkg, nenv, steps, warmup, scan_finite=False, ab=True, stagger
     two = res.get("two_launch", res.get("state_scan"))
     if two is not None:
         out["fdm_kernel_ms"], out["post_kernel_ms"] = two["fdm_kernel_ms"], two["post_kernel_ms"]
-        out["post_kernel"] = {"kernel": "env_post_step_split_kernel<184,true>",
+        out["post_kernel"] = {"kernel": "env_post_step_quad_kernel<184>",
                               "variant": "two_launch" if "two_launch" in res else "state_scan",
                               "algorithmic_bytes": two["algorithmic_bytes"],
                               "achieved_GBs": two["achieved_GBs"], "hbm_frac": two["hbm_frac"]}
@@ -459,7 +459,7 @@ def obs_reward_c3_bench(nenv=16384, steps=50, reps=5):
     m = float(np.median(ms)) / steps
     byt = (POST_BYTES_PER_AIRCRAFT + POST_BYTES_SCAN_EXTRA) * nac
     return {"workload": "obs_reward_c3_random_16k", "engagements": nenv, "obs_dim": 184,
-            "kernel": "env_post_step_split_kernel<184,true>", "launches_per_region": steps,
+            "kernel": "env_post_step_quad_kernel<184>", "launches_per_region": steps,
             "regions": reps, "ms_per_launch": m, "ms_per_launch_regions": [x / steps for x in ms],
             "kernel_ms_per_launch_events": kms,
             "engagements_per_s": nenv / (m * 1e-3), "aircraft_per_s": nac / (m * 1e-3),

@@ -186,9 +186,11 @@ int f16_env_post_step(const F16EnvStepIO *io, const F16Recon *rec, const F16Rewa
  * workgroup's staging tile.  0 otherwise (the caller then runs f16_norm_update). */
 int f16_env_post_step_norm_fusable(int nenv, int obs_dim);
 
-/* The same step with one wavefront per 64 aircraft instead of two (f16_env_post_step spreads
- * each group's row build over an advance wave and a vector-block wave); results are identical
- * bit for bit.  Kept as the cross-check of the two-wave kernel. */
+/* The same step with one wavefront per 64 aircraft (f16_env_post_step spreads each group's
+ * row build over four wavefronts -- advance, scalar block, vector-block frames 0-2 and 3-5 --
+ * where the full-row tile is resident, as f16_env_post_step_norm_fusable reports, and over an
+ * advance wave and a vector-block wave otherwise); results are identical bit for bit.  Kept as
+ * the cross-check of the multi-wave kernels. */
 int f16_env_post_step_onewave(const F16EnvStepIO *io, const F16Recon *rec,
                               const F16RewardCfg *cfg, void *stream);
 
