@@ -58,6 +58,18 @@ def test_generated_headers_are_single_precision(tmp_path):
     assert len(_SUFFIXED.findall(gen)) == len(_UNSUFFIXED.findall(src)) > 1000
 
 
+def test_vec_env_refuses_fp32_before_the_simulator(monkeypatch):
+    """GpuDogfightVecEnv is fp64 only, as the reference's (R/cuda_fdm/rl_env.py:185-190; its
+    audit cuda_fdm/tests/kernel_contract_audit.py:167-172 checks that the refusal comes before
+    the simulator is constructed): no GPU needed, no simulator built."""
+    env = import_pkg("rl_env")
+    built = []
+    monkeypatch.setattr(env, "GpuDogfight", lambda *a, **k: built.append((a, k)))
+    with pytest.raises(ValueError, match="precision='fp64' only"):
+        env.GpuDogfightVecEnv(1, precision="fp32")
+    assert built == []
+
+
 def _fp32_sim(nenv, rate=120):
     return import_pkg().GpuDogfight(nenv, substeps=6, fcs_rate=rate, precision="fp32")
 
