@@ -3,9 +3,9 @@
 //
 // One lane per aircraft; every 64 aircraft get four wavefronts ("roles") of one 512-thread
 // workgroup (two such groups):
-//   kin   the integrator: propagation, frames, air-relative geometry, load factors, the roll and
-//         yaw axes of the aero build-up, gravity, forces, moments, accelerations;
-//   aero  air-relative geometry again (the same bits), the drag, side, lift and pitch axes;
+//   kin   the integrator: propagation, frames, air-relative geometry, load factors, gravity,
+//         forces, moments, accelerations;
+//   aero  air-relative geometry again (the same bits) and the six axes of the aero build-up;
 //   fcs   the flight control system and the previous-frame auxiliary values (with the
 //         calibrated airspeed they need);
 //   air   mass properties, atmosphere, sin/cos of the next substep's Earth angle, engine, fuel.
@@ -14,13 +14,12 @@
 //                 frames;  fcs: previous-frame FCS channels, pitch schedule;  air: mass
 //   -- X1: altitude, cos(theta)cos(phi), body velocity, body rates | aileron, rudder, LEF,
 //          flaperon | mass/CG/inertia (in the block of the substep's parity)
-//   phase B  kin: geometry, load factors, roll/yaw alpha-beta terms;  aero: geometry, the other
-//                 axes' alpha-beta terms;  fcs: pitch loop;  air: atmosphere, next sin/cos
+//   phase B  kin: geometry, load factors;  aero: geometry, the alpha-beta terms of the six
+//                 axes;  fcs: pitch loop;  air: atmosphere, next sin/cos
 //   -- X2: vt, alpha, n_y, n_z | elevator | rho, speed of sound, pressure, sin/cos
-//   phase C  kin: Mach/elevator terms of roll and yaw, quaternion rate, gravity, ground speed;
-//            aero: Mach/elevator terms of its axes;  fcs: Mach, calibrated airspeed;
-//            air: Mach, engine
-//   -- X3: drag, side, lift, pitch | thrust | ground speed
+//   phase C  kin: quaternion rate, gravity, ground speed;  aero: the Mach/elevator terms of the
+//            six axes;  fcs: Mach, calibrated airspeed;  air: Mach, engine
+//   -- X3: drag, side, lift, roll, pitch, yaw | thrust | ground speed
 // Every value is formed by the component functions of fdm_device.h with the operands the
 // one-lane kernel gives them, so all three kernels agree bit for bit.  An aero axis is summed
 // by one role in the generated order, and values a role reads from LDS after its writer's next
@@ -42,8 +41,8 @@ enum QuadRole : int { kRoleKin = 0, kRoleAero = 1, kRoleFcs = 2, kRoleAir = 3 };
 
 // role of wave w (0..3) of group g
 __device__ __forceinline__ int quad_role(int g, int w) {
-  // group 0: kin, fcs, aero, air; group 1: aero, air, kin, fcs  -> SIMD pairs (kin, aero),
-  // (fcs, air)
+  // group 0: kin, fcs, aero, air; group 1: air, aero, fcs, kin -> waves w and w + 4 share a
+  // SIMD, so the SIMD pairs are (kin, air) and (fcs, aero)
   constexpr int kOrder[2][4] = {{kRoleKin, kRoleFcs, kRoleAero, kRoleAir},
                                 {kRoleAir, kRoleAero, kRoleFcs, kRoleKin}};
   return kOrder[g][w];
@@ -267,7 +266,7 @@ __device__ __forceinline__ void quad_kin(double* __restrict__ s, long ld, int S,
   }
 }
 
-// ---- aero: the drag, side, lift and pitch axes.  Holds no state.
+// ---- aero: the six axes of the aero build-up.  Holds no state.
 template <int FCS_RATE>
 __device__ __forceinline__ void quad_aero(int S, const double* __restrict__ T, QuadX& x,
                                           int lane, bool fin) {
