@@ -159,6 +159,35 @@ def test_f32_one_decision_against_fp64_oracle(gpu, orc, worst, rate):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("S", [1, 2, 3, 7])
+def test_f32_substep_counts_ragged_batch(gpu, orc, S):
+    """37 engagements (a partial 64-aircraft group) for 1, 2, 3 and 7 substeps: the history
+    slots a step of fewer than three substeps shifts down are the previous slots bit for bit
+    (a copy), and the step is within the one-decision bounds of the fp64 oracle, the position
+    bound taken per substep (2 ft + one 2 ft float spacing each)."""
+    icm = import_pkg("ic")
+    ic, acts = oracle_lib.c1_replicas(icm)
+    sim = _fp32_sim(37)
+    sim.seed_rows(torch.as_tensor(ic[:74], device=gpu))
+    prev32 = sim.states.clone()
+    prev = prev32.double().cpu().numpy().copy()
+    act = acts[S, :74]
+    sim.step(torch.as_tensor(act, device=gpu), substeps=S)
+    got32 = sim.states.clone()
+    got = got32.double().cpu().numpy()
+    orc.step(prev, act, S)
+    assert np.isfinite(got).all()
+    for base, width in ((25, 4), (37, 3), (46, 3), (55, 3)):   # DQ, DPQRI, DIVEL, DUVW
+        for k in range(S, 3):
+            assert torch.equal(got32[:, base + width * k:base + width * (k + 1)],
+                               prev32[:, base + width * (k - S):base + width * (k - S + 1)])
+    assert np.linalg.norm(got[:, :3] - prev[:, :3], axis=1).max() <= 2.0 + 2.0 * S
+    sc = oracle_lib.scaled_abs_err(got, prev)
+    assert sc[:, _OTHER].max() <= ONE_DECISION_BOUNDS["other state, scaled"]
+    assert np.abs(got[:, 6:10] - prev[:, 6:10]).max() <= ONE_DECISION_BOUNDS["quaternion"]
+
+
+@pytest.mark.gpu
 def test_f32_six_seconds_free_flight(gpu, orc, worst):
     """60 decisions (6 s) free-running from the C1 replicas' seeded states with the stick
     centred and throttle 0.8, fp32 kernel against the fp64 oracle from the same rounded start.
