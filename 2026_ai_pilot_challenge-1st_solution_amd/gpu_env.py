@@ -78,7 +78,7 @@ class GpuDogfight:
 
     def kernel_info(self, onelane=False):
         """Footprint of the four-wave kernel `step` launches (default) or of the one-lane kernel;
-        with precision="fp32", of the single-precision kernel (one lane per aircraft)."""
+        with precision="fp32", of the single-precision four-wave kernel (`onelane` ignored)."""
         out = (_lib.ctypes.c_int * 4)()
         if self.precision == "fp32":
             fn = self._lib.f16_fdm_kernel_info_f32
