@@ -37,6 +37,8 @@ def test_single_precision_rewrite_known_cases():
     assert b.single_precision(src) == want
     with pytest.raises(RuntimeError):
         b.single_precision("double y = f16::fm_sqrt(x);")
+    with pytest.raises(RuntimeError):           # would stay double and promote its expression
+        b.single_precision("double y = 0x1.8p3 * x;")
 
 
 def test_generated_headers_are_single_precision(tmp_path):
