@@ -31,6 +31,7 @@ from pathlib import Path
 import numpy as np
 import torch
 
+from . import future_aux as _future_aux
 from . import policy as _policy
 
 WEIGHTS_FILENAME = "policy_weights.pkl.gz"
@@ -353,18 +354,21 @@ def checkpoint_to_bundle(ckpt_path, output_dir, observation_module="claude_code.
     _require_finite(ckpt["model"], "export.model")
     if ckpt.get("norm") is not None:
         _require_finite(ckpt["norm"], "export.normalization")
+    cfg = ckpt.get("cfg") or {}
+    # the auxiliary prediction heads teach the trunk and are never deployed: exactly their four
+    # tensors are dropped (gpu_ckpt_to_bundle.py:129-131); other unexpected keys still fail the
+    # strict load below
+    sd = _future_aux.inference_state_dict(ckpt["model"], enabled=bool(cfg.get("aux_pred", False)))
     if observation_module != "claude_code.my_observation":
         raise ValueError("bundle export supports only the 184D training observation contract")
-    sd = ckpt["model"]
     obs_dim = int(sd["actor_logits.0.weight"].shape[1])
     head = sd["actor_logits.4.weight"]
-    num_bins = int((ckpt.get("cfg") or {}).get("num_bins", head.shape[0] // 4))
+    num_bins = int(cfg.get("num_bins", head.shape[0] // 4))
     act_dim = head.shape[0] // num_bins
     if obs_dim != 184 or act_dim != 4:
         raise ValueError("the submission contract requires 184 observations and 4 controls")
     net = _policy.MLPActorCritic(obs_dim)
     net.load_state_dict(sd, strict=True)
-    cfg = ckpt.get("cfg") or {}
     return save_bundle(net, output_dir, obs_norm=obs_norm_from_checkpoint(ckpt.get("norm")),
                        extra_metadata={
                            "reward_module": reward_module,

@@ -17,6 +17,35 @@ AUX_DIM = 6
 AUX_OPP_H = 5
 AUX_SELF_H = 10
 AUX_POS_SCALE_M = 100.0
+# checkpoint metadata identifying this label construction (R/cuda_fdm/future_aux.py:16-17)
+AUX_PROTOCOL = "cuda_mlp_flat_finite_horizon_future_aux_diverse_h3_reset_v8"
+AUX_CONTRACT = "main_body_cv_residual_opp5_self10_scale100_v1"
+# the auxiliary prediction heads' tensors: trained, never deployed (R/cuda_fdm/future_aux.py:18-19)
+AUX_STATE_KEYS = frozenset(("actor_aux_head.weight", "actor_aux_head.bias",
+                            "critic_aux_head.weight", "critic_aux_head.bias"))
+
+
+def auxiliary_error(prediction, target, mask):
+    """Masked mean squared error of (rows, 6) predictions against the labels, with the (rows, 2)
+    per-horizon mask (R/cuda_fdm/future_aux.py:58-67): returns (mse, sse, count), sse and count
+    the per-horizon sums of squared errors and of masked elements (3 per unmasked horizon).
+    Non-finite predictions are not filtered: a NaN under a masked label still reaches the loss,
+    so a finite check downstream catches it."""
+    err = (prediction - target).reshape(-1, 2, 3)
+    per_h = (err * err).sum(-1)                     # (rows, 2) squared error per horizon
+    sse = (per_h * mask).sum(0)
+    count = mask.sum(0).to(sse.dtype) * 3.0
+    return sse.sum() / torch.clamp(count.sum(), min=1.0), sse, count
+
+
+def inference_state_dict(state_dict, enabled=False):
+    """The state_dict without the auxiliary heads (R/cuda_fdm/future_aux.py:70-75): with
+    `enabled` (the checkpoint was trained with them) exactly AUX_STATE_KEYS must be present, else
+    none of the heads' keys may be; any other combination raises ValueError."""
+    heads = {k for k in state_dict if k.startswith(("actor_aux_head.", "critic_aux_head."))}
+    if heads != (AUX_STATE_KEYS if enabled else frozenset()):
+        raise ValueError("checkpoint auxiliary metadata and prediction-head keys disagree")
+    return {k: v for k, v in state_dict.items() if k not in AUX_STATE_KEYS}
 
 
 @torch.no_grad()

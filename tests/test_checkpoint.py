@@ -57,6 +57,30 @@ def test_bundle_weights_round_trip(tmp_path):
     assert meta["model"]["type"] == "mlp_discrete_actor_critic"
 
 
+def test_bundle_export_drops_the_aux_heads(tmp_path):
+    """checkpoint_to_bundle on a checkpoint trained with the auxiliary heads (cfg aux_pred):
+    the bundle holds the policy's tensors only, equal to the checkpoint's, and says it was
+    trained with them; the same checkpoint claiming no aux training is refused."""
+    C, P, F = import_pkg("checkpoint"), import_pkg("policy"), import_pkg("future_aux")
+    torch.manual_seed(4)
+    sd = P.MLPActorCritic(184).state_dict()
+    heads = {"actor_aux_head.weight": torch.randn(6, 256), "actor_aux_head.bias": torch.randn(6),
+             "critic_aux_head.weight": torch.randn(6, 256), "critic_aux_head.bias": torch.randn(6)}
+    assert set(heads) == F.AUX_STATE_KEYS
+    ck = {"model": {**sd, **heads}, "cfg": {"aux_pred": True, "num_bins": 21},
+          "auxiliary_contract": F.AUX_CONTRACT, "iteration": 7}
+    torch.save(ck, tmp_path / "aux.pt")
+    C.checkpoint_to_bundle(tmp_path / "aux.pt", tmp_path / "bundle")
+    net, meta = C.load_bundle(tmp_path / "bundle")
+    assert list(net.state_dict()) == list(sd)
+    assert all(torch.equal(net.state_dict()[k], sd[k]) for k in sd)
+    assert meta["auxiliary_trained"] is True and meta["auxiliary_contract"] == F.AUX_CONTRACT
+    ck["cfg"]["aux_pred"] = False
+    torch.save(ck, tmp_path / "bad.pt")
+    with pytest.raises(ValueError, match="auxiliary"):
+        C.checkpoint_to_bundle(tmp_path / "bad.pt", tmp_path / "bundle2")
+
+
 def test_bundle_loader_refuses_code(tmp_path):
     C, P = import_pkg("checkpoint"), import_pkg("policy")
     C.save_bundle(P.MLPActorCritic(184), tmp_path)

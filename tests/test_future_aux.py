@@ -41,6 +41,41 @@ def trajectory(T, nenv, dt, rng):
     return f
 
 
+def test_auxiliary_error_known_case():
+    """Two rows, horizons (opponent, self): row 0 errs by (1, 2, 2) on the opponent horizon
+    (squared 9) and by 1 on one self component (1), row 1 by 3 on every component (27 each);
+    row 1's self horizon is masked.  sse = (9 + 27, 1), count = (6, 3), mse = 37 / 9.  A NaN
+    prediction under a masked label still poisons the mean."""
+    import torch
+    F = import_pkg("future_aux")
+    target = torch.zeros(2, 6, dtype=torch.float64)
+    pred = torch.tensor([[1.0, 2.0, 2.0, 0.0, 1.0, 0.0], [3.0] * 6], dtype=torch.float64)
+    mask = torch.tensor([[1.0, 1.0], [1.0, 0.0]], dtype=torch.float64)
+    mse, sse, count = F.auxiliary_error(pred, target, mask)
+    assert sse.tolist() == [36.0, 1.0] and count.tolist() == [6.0, 3.0]
+    assert float(mse) == 37.0 / 9.0
+    pred[1, 4] = float("nan")
+    assert math.isnan(float(F.auxiliary_error(pred, target, mask)[0]))
+    zero = F.auxiliary_error(pred[:0], target[:0], mask[:0])[0]
+    assert float(zero) == 0.0                   # no unmasked element: divided by 1, not 0
+
+
+def test_inference_state_dict_strips_exactly_the_aux_heads():
+    """The four auxiliary-head tensors are dropped when the checkpoint says it trained them;
+    present without that, absent with it, or one more head key all raise."""
+    import torch
+    F, P = import_pkg("future_aux"), import_pkg("policy")
+    base = P.MLPActorCritic(184).state_dict()
+    heads = {k: torch.zeros(1) for k in F.AUX_STATE_KEYS}
+    out = F.inference_state_dict({**base, **heads}, enabled=True)
+    assert list(out) == list(base)
+    assert F.inference_state_dict(base).keys() == base.keys()
+    for sd, enabled in (({**base, **heads}, False), (base, True),
+                        ({**base, **heads, "actor_aux_head.scale": torch.zeros(1)}, True)):
+        with pytest.raises(ValueError, match="auxiliary"):
+            F.inference_state_dict(sd, enabled=enabled)
+
+
 def test_oracle_closed_forms():
     rng = np.random.default_rng(0)
     T, nenv, dt = 24, 3, 0.1
