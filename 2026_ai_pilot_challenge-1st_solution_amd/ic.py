@@ -8,7 +8,10 @@
   same IC rows feed the GPU and the CPU restatement.
 * samplers for the BASELINE workloads (head-on and tail-chase engagements);
 * ``action_grid`` / ``bins_to_controls``: 21 bins on [-1, 1], throttle = 0.5 z + 0.5
-  (research/competition_36500/runtime/cuda_fdm/ppo_gpu.py:178-181, 361-370).
+  (research/competition_36500/runtime/cuda_fdm/ppo_gpu.py:178-181, 361-370);
+* ``build_seed_vector``: one IC's 101-value seed state under the reference's name and keywords,
+  computed by the device seeding kernel (the reference's host helpers geodetic_to_ecef,
+  ic_to_seedargs and _flatten_state are that kernel's steps, cuda_fdm/ic.py:18-114).
 """
 import math
 
@@ -46,6 +49,26 @@ def ned_to_geodetic(n, e, d, lat0=ORIGIN_LAT_DEG, lon0=ORIGIN_LON_DEG, h0=0.0):
         nn = WGS84_A_M / np.sqrt(1.0 - WGS84_E2 * s * s)
         lat = np.arctan2(z + WGS84_E2 * nn * s, p)
     return np.degrees(lat), np.degrees(lon), -d * M2FT
+
+
+def build_seed_vector(lat_deg, lon_deg, alt_ft, vt_fps, gamma_deg=0.0, phi_deg=0.0, psi_deg=0.0,
+                      theta_deg=0.0, alpha_deg=0.0, beta_deg=0.0, lat_type="geodetic",
+                      fuel_lbs=6000.0, throttle=0.8, fcs_rate=120, device="cuda"):
+    """The 101-value seed state of one initial condition (cuda_fdm/ic.py:117-138: the same
+    keywords in the same order), as a list of floats, computed on the device by f16_seed_batch
+    (no host model).  As in the reference, gamma_deg and throttle do not enter the seed (the
+    flight-path angle is not used by its ic_to_seedargs; the throwaway force path runs at 0.8
+    throttle).  fcs_rate: 120 for the root lineage, 60 for the 184-D one.  Only geodetic
+    latitude is supported (ValueError otherwise, before any device work)."""
+    if lat_type != "geodetic":
+        raise ValueError("only geodetic IC latitude is supported")
+    import torch
+    from .gpu_env import GpuDogfight
+    sim = GpuDogfight(1, planes_per_env=1, fcs_rate=fcs_rate, device=device)
+    row = [[lat_deg, lon_deg, alt_ft, vt_fps, phi_deg, theta_deg, psi_deg, alpha_deg, beta_deg,
+            fuel_lbs]]
+    sim.seed_rows(torch.tensor(row, dtype=torch.float64, device=sim.device))
+    return sim.states[0].tolist()
 
 
 def ic_row(lat_deg, lon_deg, alt_ft, vt_fps, psi_deg, fuel_lbs, phi_deg=0.0, theta_deg=0.0,

@@ -38,6 +38,23 @@ def test_seed_matches_golden(gpu, rate):
     assert oracle_lib.rel_err(got, g[f"seed_{rate}"]).max() < STEP_TOL
 
 
+def test_build_seed_vector_keywords(gpu):
+    """ic.build_seed_vector(**kwargs), the reference's per-IC entry (cuda_fdm/ic.py:117-138),
+    equals the seeding golden row for row (both FCS rates); gamma_deg and throttle do not
+    change the seed, as in the reference."""
+    icm = import_pkg("ic")
+    g = oracle_lib.golden("seed_golden.npz")
+    keys = import_pkg("gpu_env").IC_KEYS        # the golden's IC column order
+    for rate in (120, 60):
+        for i in (0, 3, len(g["ic"]) - 1):
+            kw = dict(zip(keys, (float(x) for x in g["ic"][i])))
+            got = np.array(icm.build_seed_vector(**kw, fcs_rate=rate))
+            assert oracle_lib.rel_err(got[None], g[f"seed_{rate}"][i:i + 1]).max() < STEP_TOL
+            alt = np.array(icm.build_seed_vector(**kw, gamma_deg=5.0, throttle=0.3,
+                                                 fcs_rate=rate))
+            assert np.array_equal(alt, got)
+
+
 def test_seed_scatter_rows(gpu):
     """rows= seeds chosen aircraft only (the autoreset path) and leaves the others untouched."""
     g = oracle_lib.golden("seed_golden.npz")

@@ -81,3 +81,12 @@ def test_contest_rows_match_pairwise_draws():
     a = icm.contest_rows(np.random.default_rng(1), 200)
     assert set(np.unique(a[:, 6])) <= {90.0, 270.0} and (a[0::2, 6] != a[1::2, 6]).all()
     assert icm.contest_rows(np.random.default_rng(1), 0).shape == (0, 10)
+
+
+def test_build_seed_vector_refuses_geocentric_before_device_work():
+    """The reference's keyword interface (cuda_fdm/ic.py:117-138); geocentric latitude is not
+    supported and is refused on the host, before any device call."""
+    import pytest
+    icm = import_pkg("ic")
+    with pytest.raises(ValueError, match="geodetic"):
+        icm.build_seed_vector(37.0, 131.0, 10000.0, 800.0, lat_type="geocentric")
