@@ -373,12 +373,14 @@ def test_env_post_step_matches_reference_sequence(gpu, orc, obs_dim, nenv):
 
 @pytest.mark.parametrize("obs_dim,nenv,terminal", [
     (184, 1024, True), (184, 1024, False), (214, 1024, True), (214, 1024, False),
+    (184, 300, True), (214, 33, False),
     (184, 26000, True), (184, 26000, False), (214, 17000, True)])
 def test_env_post_step_two_wave_equals_one_wave(gpu, obs_dim, nenv, terminal):
     """f16_env_post_step against f16_env_post_step_onewave on identical inputs: every output,
     state row, reconstructor value and aux feature bit for bit, with finished engagements
     (autoreset rows), with and without terminal observations, with the full-row tile (1024
-    engagements: four wavefronts per 64 aircraft) and the vector-block tile (26000 / 17000
+    engagements, and 300 and 33 whose last workgroup is partly filled: four wavefronts per 64
+    aircraft) and the vector-block tile (26000 / 17000
     engagements exceed what the full-row tile keeps resident: an advance wave and a vector-block
     wave per 64 aircraft)."""
     ext = obs_dim == 214
