@@ -109,7 +109,9 @@ def build():
 
 
 def load():
-    path = os.path.join(ORACLE, "liborc.so")
+    """The C restatement; F16_ORACLE_LIB names another build of it (the sanitizer build of
+    `make -C oracle sanitize`, run with its runtime preloaded)."""
+    path = os.environ.get("F16_ORACLE_LIB") or os.path.join(ORACLE, "liborc.so")
     if not os.path.exists(path):
         build()
     return Oracle(ctypes.CDLL(path))
