@@ -76,8 +76,8 @@ __device__ __forceinline__ int quad_mass_block(int t) { return (t & 1) ? kQMassB
 
 typedef double QuadX[kQuadFields][64];
 
-// ---- kin: the integrator and the roll/yaw axes.  `fin`: report the finite flag of every state
-// value it stores through x[kQFinKin] after one more barrier.
+// ---- kin: the integrator.  `fin`: report the finite flag of every state value it stores
+// through x[kQFinKin] after one more barrier.
 template <int FCS_RATE>
 __device__ __forceinline__ void quad_kin(double* __restrict__ s, long ld, int S, bool store,
                                          double* __restrict__ out_base, long obs_ld,
