@@ -26,7 +26,13 @@
 // phase could overwrite them are read early and held (the mass block alternates by parity).
 //
 // The two groups of a workgroup map their roles to waves in opposite orders, so each SIMD
-// (wave w and w + 4 of the workgroup) holds two roles that are busy in different phases.
+// (wave w and w + 4 of the workgroup) holds two roles that are busy in different phases: the
+// SIMD pairs are (kin, air) and (fcs, aero).  Within a pair, the role on the substep's critical
+// path in a phase runs at raised wave priority (s_setprio), so its instructions issue first
+// whenever both waves have one ready: kin in A, C and D (its forces-to-frames chain), air in B
+// and C (atmosphere, engine), aero in B and C (the build-up), fcs in A.  The same results;
+// 33.4 -> 32.2 us per step at 16k engagements.  Only with two groups per workgroup: with one,
+// a SIMD holds one wave and raised priorities made 4,096 engagements 5 % slower.
 #pragma once
 #include "fdm_image.h"
 #include "fdm_split.h"
@@ -74,11 +80,18 @@ constexpr int kQVh1 = kQPark, kQVh2 = kQPark + 3, kQAh1 = kQPark + 6, kQPba = kQ
               kQPpd = kQPark + 12, kQPpq = kQPark + 15;
 __device__ __forceinline__ int quad_mass_block(int t) { return (t & 1) ? kQMassB - kQMass : 0; }
 
+// Wave priority N for the rest of this phase, when priorities are in use (two groups per
+// workgroup: two waves per SIMD to arbitrate between).
+template <int N, bool P>
+__device__ __forceinline__ void quad_prio() {
+  if constexpr (P) __builtin_amdgcn_s_setprio(N);
+}
+
 typedef double QuadX[kQuadFields][64];
 
 // ---- kin: the integrator.  `fin`: report the finite flag of every state value it stores
 // through x[kQFinKin] after one more barrier.
-template <int FCS_RATE>
+template <int FCS_RATE, bool PRIO = false>
 __device__ __forceinline__ void quad_kin(double* __restrict__ s, long ld, int S, bool store,
                                          double* __restrict__ out_base, long obs_ld,
                                          const double* __restrict__ T, QuadX& x, int lane,
@@ -124,6 +137,7 @@ __device__ __forceinline__ void quad_kin(double* __restrict__ s, long ld, int S,
     const int slot = S - 1 - t;
     const int mo = quad_mass_block(t);
     // ---- phase A
+    quad_prio<3, PRIO>();
     if (store && slot <= 2) {
       double* h = s;                // the history addresses are formed here (see the stores
       asm volatile("" : "+v"(h));   // after the loop)
@@ -178,6 +192,7 @@ __device__ __forceinline__ void quad_kin(double* __restrict__ s, long ld, int S,
     }
     __syncthreads();
     // ---- phase B
+    quad_prio<0, PRIO>();
     g = aux_geometry(uvw);
     if (slot == 0 && out) {
       double* o = out_base;
@@ -196,6 +211,7 @@ __device__ __forceinline__ void quad_kin(double* __restrict__ s, long ld, int S,
     x[kQNpy][lane] = npy; x[kQNpz][lane] = npz;
     __syncthreads();
     // ---- phase C
+    quad_prio<3, PRIO>();
     {
       if (slot == 0 && out) {
         double* o = out_base;
@@ -208,6 +224,7 @@ __device__ __forceinline__ void quad_kin(double* __restrict__ s, long ld, int S,
     }
     __syncthreads();
     // ---- phase D
+    quad_prio<3, PRIO>();
     {
       const double ax[6] = {x[kQAx0][lane], x[kQAx1][lane], x[kQAx2][lane], x[kQAx3][lane],
                             x[kQAx4][lane], x[kQAx5][lane]};
@@ -237,6 +254,7 @@ __device__ __forceinline__ void quad_kin(double* __restrict__ s, long ld, int S,
   for (int j = 0; j < 3; ++j) {
     a.pba[j] = x[kQPba + j][lane]; a.ppd[j] = x[kQPpd + j][lane]; a.ppq[j] = x[kQPpq + j][lane];
   }
+  quad_prio<0, PRIO>();
   // the state's addresses are formed here, from a pointer the compiler cannot see through:
   // hoisted above the substep loop they would stay live across it, 2 registers each
   asm volatile("" : "+v"(s));
@@ -267,12 +285,13 @@ __device__ __forceinline__ void quad_kin(double* __restrict__ s, long ld, int S,
 }
 
 // ---- aero: the six axes of the aero build-up.  Holds no state.
-template <int FCS_RATE>
+template <int FCS_RATE, bool PRIO = false>
 __device__ __forceinline__ void quad_aero(int S, const double* __restrict__ T, QuadX& x,
                                           int lane, bool fin) {
   for (int t = 0; t < S; ++t) {
     __syncthreads();
     // ---- phase B
+    quad_prio<3, PRIO>();
     const double uvw[3] = {x[kQU][lane], x[kQV][lane], x[kQW][lane]};
     const AuxGeo g = aux_geometry(uvw);
     x[kQVt][lane] = g.vt; x[kQAlpha][lane] = g.alpha;
@@ -293,6 +312,7 @@ __device__ __forceinline__ void quad_aero(int S, const double* __restrict__ T, Q
     }
     __syncthreads();
     // ---- phase C
+    quad_prio<3, PRIO>();
     {
       const double rho = x[kQRho][lane], sound = x[kQSound][lane], elev = x[kQElev][lane];
       const double qbar = 0.5 * rho * g.vt2;
@@ -311,12 +331,13 @@ __device__ __forceinline__ void quad_aero(int S, const double* __restrict__ T, Q
       x[kQAx5][lane] = F16_AERO_YAW_SCALE * (e5 + F16_AERO_YAW_LATE);
     }
     __syncthreads();
+    quad_prio<0, PRIO>();
   }
   if (fin) __syncthreads();
 }
 
 // ---- fcs: the FCS channels and the previous-frame auxiliary values.
-template <int FCS_RATE>
+template <int FCS_RATE, bool PRIO = false>
 __device__ __forceinline__ void quad_fcs(double* __restrict__ s, long ld,
                                          const double* __restrict__ act4, int S, bool store,
                                          const double* __restrict__ T, QuadX& x, int lane,
@@ -335,6 +356,7 @@ __device__ __forceinline__ void quad_fcs(double* __restrict__ s, long ld,
   for (int t = 0; t < S; ++t) {
     const int slot = S - 1 - t;
     // ---- phase A
+    quad_prio<2, PRIO>();
     if (store && slot == 0) {   // PID input_prev2 = input_prev before the final update
 #pragma unroll
       for (int j = 0; j < 3; ++j) {
@@ -348,6 +370,7 @@ __device__ __forceinline__ void quad_fcs(double* __restrict__ s, long ld,
     x[kQAil][lane] = fc.ail; x[kQRud][lane] = fc.rud; x[kQLef][lane] = fc.lef; x[kQFlap][lane] = fc.flap;
     __syncthreads();
     // ---- phase B
+    quad_prio<0, PRIO>();
     const double p = x[kQP][lane], q = x[kQQ][lane], r = x[kQR][lane];
     fcs_pitch<FCS_RATE>(a, esch, x[kQCtcp][lane], fc);
     x[kQElev][lane] = fc.elev;
@@ -356,6 +379,7 @@ __device__ __forceinline__ void quad_fcs(double* __restrict__ s, long ld,
     a.pa[6] = p; a.pa[7] = q; a.pa[8] = r;
     __syncthreads();
     // ---- phase C
+    quad_prio<0, PRIO>();
     a.pa[4] = x[kQNpy][lane]; a.pa[5] = x[kQNpz][lane];
     a.pa[0] = x[kQAlpha][lane];
     const double mach = fm_div(x[kQVt][lane], x[kQSound][lane]);
@@ -363,6 +387,7 @@ __device__ __forceinline__ void quad_fcs(double* __restrict__ s, long ld,
     a.pa[2] = vc_knots(mach, x[kQPres][lane]);
     __syncthreads();
     // ---- phase D
+    quad_prio<0, PRIO>();
     a.pa[3] = x[kQVg][lane];
   }
   asm volatile("" : "+v"(s));   // as in quad_kin: the store addresses are formed here
@@ -389,7 +414,7 @@ __device__ __forceinline__ void quad_fcs(double* __restrict__ s, long ld,
 
 // ---- air: mass, atmosphere, engine and fuel.  With `fin` non-null, fin[0] <- 1 if all 101 state
 // values are finite (its own, and the kin and fcs roles' flags after the last barrier).
-template <int FCS_RATE>
+template <int FCS_RATE, bool PRIO = false>
 __device__ __forceinline__ void quad_air(double* __restrict__ s, long ld,
                                          const double* __restrict__ act4, int S, bool store,
                                          const double* __restrict__ T, QuadX& x, int lane,
@@ -403,6 +428,7 @@ __device__ __forceinline__ void quad_air(double* __restrict__ s, long ld,
   for (int t = 0; t < S; ++t) {
     const int mo = quad_mass_block(t);
     // ---- phase A
+    quad_prio<0, PRIO>();
     a.epa += kRot * kDt;   // the kin role's propagate makes the same increment
     const Mass mb = mass_props(a.fuel);
     x[mo + kQMass][lane] = mb.mass;
@@ -412,6 +438,7 @@ __device__ __forceinline__ void quad_air(double* __restrict__ s, long ld,
     for (int j = 0; j < 3; ++j) { x[mo + kQRp + j][lane] = mb.rp[j]; x[mo + kQCg + j][lane] = mb.cg[j]; }
     __syncthreads();
     // ---- phase B
+    quad_prio<3, PRIO>();
     const Atmos at = isa(x[kQAlt][lane], T);
     x[kQRho][lane] = at.rho; x[kQSound][lane] = at.a; x[kQPres][lane] = at.P;
     if (t + 1 < S) {
@@ -422,11 +449,13 @@ __device__ __forceinline__ void quad_air(double* __restrict__ s, long ld,
     }
     __syncthreads();
     // ---- phase C
+    quad_prio<3, PRIO>();
     const double mach = fm_div(x[kQVt][lane], at.a);
     double burn;
     x[kQThrust][lane] = engine(a, c_thr, at, mach, T, burn);
     __syncthreads();
     // ---- phase D
+    quad_prio<0, PRIO>();
     a.fuel -= burn;
   }
   asm volatile("" : "+v"(s));   // as in quad_kin
@@ -468,17 +497,18 @@ __global__ __launch_bounds__(256 * G) void fdm_step_quad_kernel(
   const int i = blockIdx.x * (64 * G) + grp * 64 + lane;
   const bool store = i < nac;
   const int ia = store ? i : nac - 1;   // lanes past the batch shadow the last aircraft
+  constexpr bool kPrio = G == kQuadGroups;   // two waves per SIMD to arbitrate between
   if (role == kRoleKin)
-    quad_kin<FCS_RATE>(st + ia, ld, S, store, OBS ? obs + ia : nullptr, obs_ld, T, X[grp], lane,
-                       fin != nullptr);
+    quad_kin<FCS_RATE, kPrio>(st + ia, ld, S, store, OBS ? obs + ia : nullptr, obs_ld, T, X[grp],
+                              lane, fin != nullptr);
   else if (role == kRoleAero)
-    quad_aero<FCS_RATE>(S, T, X[grp], lane, fin != nullptr);
+    quad_aero<FCS_RATE, kPrio>(S, T, X[grp], lane, fin != nullptr);
   else if (role == kRoleFcs)
-    quad_fcs<FCS_RATE>(st + ia, ld, act + 4L * ia, S, store, T, X[grp], lane, fin != nullptr,
-                       act_keep ? act_keep + 4L * ia : nullptr);
+    quad_fcs<FCS_RATE, kPrio>(st + ia, ld, act + 4L * ia, S, store, T, X[grp], lane,
+                              fin != nullptr, act_keep ? act_keep + 4L * ia : nullptr);
   else
-    quad_air<FCS_RATE>(st + ia, ld, act + 4L * ia, S, store, T, X[grp], lane,
-                       fin ? fin + ia : nullptr);
+    quad_air<FCS_RATE, kPrio>(st + ia, ld, act + 4L * ia, S, store, T, X[grp], lane,
+                              fin ? fin + ia : nullptr);
 }
 
 }  // namespace f16

@@ -1571,16 +1571,18 @@ __global__ __launch_bounds__(kQuadPostBlock) void env_step_quad_kernel(
   const bool store = i < nac;
   const int ia = store ? i : nac - 1;   // lanes past the batch shadow the last aircraft
   double* const st = io.states + ia;
+  // (two groups per workgroup: the physics roles run with their phase priorities, fdm_quad.h)
   if (role == f16::kRoleKin)
-    f16::quad_kin<FCS_RATE>(st, io.ld, S, store, nullptr, 0, L.fdm.T, L.fdm.X[grp], lane, true);
+    f16::quad_kin<FCS_RATE, true>(st, io.ld, S, store, nullptr, 0, L.fdm.T, L.fdm.X[grp], lane,
+                                  true);
   else if (role == f16::kRoleAero)
-    f16::quad_aero<FCS_RATE>(S, L.fdm.T, L.fdm.X[grp], lane, true);
+    f16::quad_aero<FCS_RATE, true>(S, L.fdm.T, L.fdm.X[grp], lane, true);
   else if (role == f16::kRoleFcs)
-    f16::quad_fcs<FCS_RATE>(st, io.ld, act + 4L * ia, S, store, L.fdm.T, L.fdm.X[grp], lane, true,
-                            act_keep ? act_keep + 4L * ia : nullptr);
+    f16::quad_fcs<FCS_RATE, true>(st, io.ld, act + 4L * ia, S, store, L.fdm.T, L.fdm.X[grp],
+                                  lane, true, act_keep ? act_keep + 4L * ia : nullptr);
   else
-    f16::quad_air<FCS_RATE>(st, io.ld, act + 4L * ia, S, store, L.fdm.T, L.fdm.X[grp], lane,
-                            state_finite + ia);
+    f16::quad_air<FCS_RATE, true>(st, io.ld, act + 4L * ia, S, store, L.fdm.T, L.fdm.X[grp],
+                                  lane, state_finite + ia);
   __syncthreads();   // the new states, finite flags and actions are written; LDS is free
   post_quad_body<D>(io, r, c, O, L.post);
 }
