@@ -56,6 +56,11 @@ class F16EnvStepIO(ctypes.Structure):
                 ("pool_prev_alt_log", _vp), ("pool_aux", _vp), ("reward0_f32", _vp)]
 
 
+class F16FiniteSpan(ctypes.Structure):
+    """include/f16_ppo.h F16FiniteSpan."""
+    _fields_ = [("ptr", _vp), ("n", _l), ("elem_bytes", _i)]
+
+
 class F16PolicyGroup(ctypes.Structure):
     """include/f16_policy.h F16PolicyGroup."""
     _fields_ = [("wbf", _vp), ("wf", _vp), ("mean", _vp), ("var", _vp), ("row_begin", _i),
@@ -130,6 +135,7 @@ _SIGNATURES = {
     "f16_ppo_grad": (_i, [ctypes.POINTER(F16PPOArgs), _vp]),
     "f16_ppo_adam_step": (_i, [ctypes.POINTER(F16AdamArgs), _vp]),
     "f16_ppo_pack": (_i, [_vp, _i, _vp, _vp, _vp, _vp]),
+    "f16_all_finite": (_i, [ctypes.POINTER(F16FiniteSpan), _i, _vp, _vp]),
 }
 
 _lib = None

@@ -1166,6 +1166,70 @@ int launch_pack(const float* param, void* wbf, float* wf, void* wT, hipStream_t 
   return f16_last_error();
 }
 
+// ---- the rollout's aggregate finite check
+// One pass over every span, 16-byte loads in the aligned body and single elements at the two
+// unaligned ends: the largest exponent field of the float32 words and of the float64 high
+// words (all ones only for inf and NaN), and whether any byte of a uint8 flag span is zero
+// (((w - 0x01010101) & ~w & 0x80808080) != 0 exactly when a byte of w is zero).
+struct FiniteSpans {
+  F16FiniteSpan s[F16_FINITE_MAX_SPANS];
+  int n;
+};
+constexpr int kFinBlock = 256;
+constexpr int kFinUnroll = 4;
+constexpr unsigned kExp32 = 0x7f800000u, kExp64 = 0x7ff00000u;
+
+struct FinAcc {
+  unsigned m32 = 0, m64 = 0, zero = 0;
+  __device__ __forceinline__ void word(unsigned w, int eb, bool high) {
+    if (eb == 4) m32 = max(m32, w & kExp32);
+    else if (eb == 8) { if (high) m64 = max(m64, w & kExp64); }
+    else zero |= (w - 0x01010101u) & ~w & 0x80808080u;
+  }
+  __device__ __forceinline__ void chunk(const uint4& q, int eb) {
+    word(q.x, eb, false); word(q.y, eb, true); word(q.z, eb, false); word(q.w, eb, true);
+  }
+  __device__ __forceinline__ void element(const unsigned char* e, int eb) {
+    if (eb == 4) m32 = max(m32, *reinterpret_cast<const unsigned*>(e) & kExp32);
+    else if (eb == 8) m64 = max(m64, *reinterpret_cast<const unsigned*>(e + 4) & kExp64);
+    else zero |= (*e == 0) ? 1u : 0u;
+  }
+};
+
+__global__ void finite_init_kernel(unsigned char* flag) { flag[0] = 1; }
+
+__global__ __launch_bounds__(kFinBlock) void finite_kernel(FiniteSpans S,
+                                                           unsigned char* __restrict__ flag) {
+  FinAcc acc;
+  const long gt = (long)blockIdx.x * kFinBlock + threadIdx.x;
+  const long G = (long)gridDim.x * kFinBlock;
+  for (int k = 0; k < S.n; ++k) {
+    const int eb = S.s[k].elem_bytes;
+    const uintptr_t p = (uintptr_t)S.s[k].ptr;
+    const uintptr_t end = p + (uintptr_t)S.s[k].n * (uintptr_t)eb;
+    const uintptr_t a = min((p + 15) & ~(uintptr_t)15, end);
+    const uintptr_t e = max(a, end & ~(uintptr_t)15);
+    const uint4* body = reinterpret_cast<const uint4*>(a);
+    const long nchunk = (long)((e - a) >> 4);
+    for (long c = gt; c < nchunk; c += kFinUnroll * G) {
+      uint4 q[kFinUnroll];
+#pragma unroll
+      for (int u = 0; u < kFinUnroll; ++u)
+        if (c + u * G < nchunk) q[u] = body[c + u * G];
+#pragma unroll
+      for (int u = 0; u < kFinUnroll; ++u)
+        if (c + u * G < nchunk) acc.chunk(q[u], eb);
+    }
+    // the ends: fewer than 16 bytes each, one element per thread of the first workgroup
+    if (gt < 16) {
+      const uintptr_t h = p + (uintptr_t)gt * eb, t = e + (uintptr_t)gt * eb;
+      if (h < a) acc.element(reinterpret_cast<const unsigned char*>(h), eb);
+      if (t < end) acc.element(reinterpret_cast<const unsigned char*>(t), eb);
+    }
+  }
+  if (acc.m32 == kExp32 || acc.m64 == kExp64 || acc.zero != 0) flag[0] = 0;
+}
+
 }  // namespace f16ppo
 
 using namespace f16ppo;
@@ -1308,4 +1372,31 @@ extern "C" int f16_ppo_pack(const float* param, int obs_dim, void* wbf, float* w
   hipStream_t s = (hipStream_t)stream;
   return obs_dim == 184 ? launch_pack<192>(param, wbf, wf, wT, s)
                         : launch_pack<224>(param, wbf, wf, wT, s);
+}
+
+extern "C" int f16_all_finite(const F16FiniteSpan* spans, int nspans, unsigned char* flag,
+                              void* stream) {
+  if (!flag || nspans < 0 || nspans > F16_FINITE_MAX_SPANS || (nspans > 0 && !spans))
+    return F16_EINVAL;
+  FiniteSpans S;
+  S.n = nspans;
+  long chunks = 0;
+  for (int k = 0; k < nspans; ++k) {
+    const F16FiniteSpan& sp = spans[k];
+    if (sp.n < 0 || (sp.elem_bytes != 1 && sp.elem_bytes != 4 && sp.elem_bytes != 8))
+      return F16_EINVAL;
+    if (sp.n > 0 && (!sp.ptr || ((uintptr_t)sp.ptr % (uintptr_t)sp.elem_bytes)))
+      return F16_EINVAL;
+    if (sp.n > (1L << 40) / sp.elem_bytes) return F16_EINVAL;
+    S.s[k] = sp;
+    chunks = std::max(chunks, sp.n * sp.elem_bytes / 16);
+  }
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL(finite_init_kernel, dim3(1), dim3(1), 0, s, flag);
+  // enough workgroups to keep every CU's loads in flight on the largest span, at most 8 per CU
+  const long per_block = (long)kFinBlock * kFinUnroll;
+  const long blocks = std::min<long>(std::max<long>(1, (chunks + per_block - 1) / per_block),
+                                     8L * device_cus());
+  hipLaunchKernelGGL(finite_kernel, dim3((unsigned)blocks), dim3(kFinBlock), 0, s, S, flag);
+  return f16_last_error();
 }

@@ -46,6 +46,37 @@ class UpdateConfig:
     norm_adv: bool = True
 
 
+def finite_flag(floats, flags=()):
+    """One device byte, 1 when every element of the float32/float64 tensors `floats` is finite
+    and every element of the uint8/bool tensors `flags` is nonzero, else 0: the reference's
+    torch.stack([...isfinite(x).all()...]).all() before an update (ppo_gpu.py:2000-2009) as one
+    read of each buffer (f16_all_finite), no host synchronisation."""
+    spans, keep = [], []
+    for xs, kinds in ((floats, (torch.float32, torch.float64)), (flags, (torch.uint8, torch.bool))):
+        for x in xs:
+            if x.dtype not in kinds:
+                raise TypeError(f"finite_flag: unsupported dtype {x.dtype}")
+            if not x.is_cuda:
+                raise ValueError("finite_flag: device tensors only")
+            x = x.contiguous()
+            keep.append(x)
+            spans.append((x.data_ptr(), x.numel(), x.element_size()))
+    if not keep:
+        raise ValueError("finite_flag: nothing to check")
+    if len(spans) > 16:
+        raise ValueError("finite_flag: at most 16 tensors")
+    dev = keep[0].device
+    if any(x.device != dev for x in keep):
+        raise ValueError("finite_flag: tensors on different devices")
+    arr = (_lib.F16FiniteSpan * len(spans))(*[_lib.F16FiniteSpan(p, n, e) for p, n, e in spans])
+    out = torch.empty(1, dtype=torch.uint8, device=dev)
+    stream, h = _lib.launch_stream(dev)
+    rc = _lib.lib().f16_all_finite(arr, len(spans), _lib.ptr(out), h)
+    _lib.record(stream, keep + [out])
+    _lib.check(rc, "f16_all_finite")
+    return out
+
+
 def param_counts(obs_dim):
     out = (ctypes.c_long * 2)()
     _lib.check(_lib.lib().f16_ppo_param_counts(int(obs_dim), out), "f16_ppo_param_counts")
@@ -185,9 +216,7 @@ class PPOUpdater:
         if obs.shape[1] != self.D:
             raise ValueError("observation width does not match the network")
         # one aggregate finite check before any gradient step (ppo_gpu.py:2000-2009)
-        checks = [torch.isfinite(x).all() for x in (obs, rollout.b_rew, b_val, old_logp,
-                                                    advantages, returns)]
-        if not bool(torch.stack(checks).all()):
+        if not bool(finite_flag((obs, rollout.b_rew, b_val, old_logp, advantages, returns))):
             raise FloatingPointError("non-finite physical trajectory or PPO rollout; update refused")
         obs, act = obs.contiguous(), act.contiguous()
         old_logp, advantages, returns = (x.contiguous().float() for x in

@@ -25,7 +25,7 @@ import torch
 
 from .policy import MLPActorCritic, RunningNorm
 from .ppo import LeagueRollout
-from .ppo_update import PPOUpdater, UpdateConfig
+from .ppo_update import PPOUpdater, UpdateConfig, finite_flag
 
 
 @dataclass
@@ -113,10 +113,9 @@ class PPOGPUTrainer:
         """One rollout of rollout_steps (ppo_gpu.py:1856-2017); see the module docstring."""
         ro = self._collector_for(opp_kind, frozen_opp, update_norm)
         adv, ret, stats = ro.collect()
-        checks = [stats["trajectory_finite"]]
-        checks += [torch.isfinite(x).all() for x in (ro.b_obs, ro.b_rew, ro.b_val, ro.b_logp,
-                                                     adv, ret)]
-        if not bool(torch.stack(checks).all()):
+        ok = finite_flag((ro.b_obs, ro.b_rew, ro.b_val, ro.b_logp, adv, ret),
+                         flags=(ro.finite_acc,))
+        if not bool(ok):
             raise FloatingPointError("non-finite physical trajectory or PPO rollout; update refused")
         self.global_step += self.cfg.rollout_steps * self.nenv
         del stats["trajectory_finite"]

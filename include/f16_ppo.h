@@ -101,6 +101,20 @@ int f16_ppo_adam_step(const F16AdamArgs *args, void *stream);
  * from flat master parameters; wT may be NULL. */
 int f16_ppo_pack(const float *param, int obs_dim, void *wbf, float *wf, void *wT, void *stream);
 
+/* The aggregate finite check before an update: one flag for the reference's
+ * torch.stack([trajectory_finite] + [torch.isfinite(x).all() for x in (b_obs, b_rew, b_val,
+ * b_logp, adv, ret)]).all() (R/cuda_fdm/ppo_gpu.py:2000-2009), read in one pass.  A span is n
+ * elements of elem_bytes at ptr (aligned to elem_bytes; n = 0 allowed): 4 = float32 and 8 =
+ * float64, each element finite (not inf, not NaN); 1 = uint8/bool flags, each nonzero.  *flag (one
+ * device byte) = 1 when every span holds, else 0.  Two launches (the flag set, then the scan). */
+#define F16_FINITE_MAX_SPANS 16
+typedef struct F16FiniteSpan {
+    const void *ptr;
+    long n;
+    int elem_bytes;
+} F16FiniteSpan;
+int f16_all_finite(const F16FiniteSpan *spans, int nspans, unsigned char *flag, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

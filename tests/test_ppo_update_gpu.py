@@ -251,3 +251,94 @@ def test_first_minibatch_of_a_rollout_has_ratio_one(gpu):
     assert res["optimizer_steps"] >= 8
     adv2, ret2, _ = ro.collect()
     assert torch.isfinite(adv2).all()
+
+
+def _isfinite_all(floats, flags=()):
+    ok = all(bool(torch.isfinite(x.cpu()).all()) for x in floats)
+    return ok and all(bool((x.cpu() != 0).all()) for x in flags)
+
+
+def test_finite_flag_matches_isfinite(gpu):
+    """f16_all_finite against torch.isfinite(x).all() / (flags != 0).all(): float32, float64 and
+    uint8/bool spans of sizes 0..several chunks, views starting off the 16-byte grid, one inf,
+    -inf or NaN (or one zero flag) planted at the head, in the 16-byte body or at the tail, and
+    the largest finite and subnormal values (finite)."""
+    U = import_pkg("ppo_update")
+    g = torch.Generator().manual_seed(3)
+    cases = 0
+    for dtype in (torch.float32, torch.float64, torch.uint8, torch.bool):
+        is_flag = dtype in (torch.uint8, torch.bool)
+        for n in (0, 1, 3, 5, 16, 17, 63, 1000, 4099, 1 << 20):
+            for off in (0, 1, 3):
+                if n == 0 and off:
+                    continue
+                if is_flag:
+                    base = torch.randint(1, 256, (n + off + 8,), generator=g).to(torch.uint8)
+                    base = base.bool() if dtype == torch.bool else base
+                else:
+                    base = torch.randn(n + off + 8, generator=g, dtype=torch.float64).to(dtype)
+                    if n > 2:
+                        fi = torch.finfo(dtype)
+                        base[off] = fi.max
+                        base[off + n - 1] = -fi.tiny / 4          # subnormal
+                base[off + n:] = 0 if is_flag else float("nan")  # outside the span
+                dev = base.cuda()
+                view = dev[off:off + n]
+                fl, fa = ((), (view,)) if is_flag else ((view,), ())
+                if n > 0:
+                    fl_extra = (torch.ones(7, device="cuda"),)
+                    assert _isfinite_all(fl, fa)
+                    assert bool(U.finite_flag(fl + fl_extra, fa)), (dtype, n, off)
+                cases += 1
+                for pos in sorted({0, n // 2, n - 1}) if n > 0 else ():
+                    for bad in ((0,) if is_flag else (float("inf"), -float("inf"), float("nan"))):
+                        planted = dev.clone()
+                        planted[off + pos] = bad
+                        pv = planted[off:off + n]
+                        fl2, fa2 = ((), (pv,)) if is_flag else ((pv,), ())
+                        got = bool(U.finite_flag(fl2 + (torch.ones(5, device="cuda"),), fa2))
+                        assert got is False and _isfinite_all(fl2, fa2) is False, (dtype, n, off, pos, bad)
+                        cases += 1
+    assert cases > 300
+    # several spans at once: the flag is the AND of all of them
+    a = torch.randn(1000, device="cuda")
+    b = torch.randn(333, device="cuda", dtype=torch.float64)
+    c = torch.ones(77, dtype=torch.uint8, device="cuda")
+    assert bool(U.finite_flag((a, b), (c,)))
+    b[200] = float("nan")
+    assert not bool(U.finite_flag((a, b), (c,)))
+
+
+def test_finite_flag_argument_checks(gpu):
+    """Refused before any launch: more than 16 spans, an element size other than 1, 4, 8, a
+    pointer off its element alignment, a negative count, no flag; and the Python wrapper's dtype,
+    device and count checks."""
+    U, L = import_pkg("ppo_update"), import_pkg("_lib")
+    lib = L.lib()
+    x = torch.zeros(64, device="cuda")
+    flag = torch.zeros(1, dtype=torch.uint8, device="cuda")
+    h = L.stream_handle()
+    S = L.F16FiniteSpan
+
+    def call(spans, flag_ptr=L.ptr(flag)):
+        arr = (S * max(1, len(spans)))(*spans)
+        return lib.f16_all_finite(arr, len(spans), flag_ptr, h)
+
+    ok = S(x.data_ptr(), 64, 4)
+    assert call([ok]) == 0
+    torch.cuda.synchronize()
+    assert int(flag.item()) == 1
+    assert call([ok] * 17) == L.F16_EINVAL
+    assert call([S(x.data_ptr(), 64, 2)]) == L.F16_EINVAL
+    assert call([S(x.data_ptr() + 2, 8, 4)]) == L.F16_EINVAL
+    assert call([S(x.data_ptr() + 4, 8, 8)]) == L.F16_EINVAL
+    assert call([S(x.data_ptr(), -1, 4)]) == L.F16_EINVAL
+    assert call([ok], flag_ptr=None) == L.F16_EINVAL
+    with pytest.raises(TypeError):
+        U.finite_flag((torch.zeros(4, dtype=torch.float16, device="cuda"),))
+    with pytest.raises(ValueError):
+        U.finite_flag((torch.zeros(4),))
+    with pytest.raises(ValueError):
+        U.finite_flag([x] * 17)
+    with pytest.raises(ValueError):
+        U.finite_flag(())
