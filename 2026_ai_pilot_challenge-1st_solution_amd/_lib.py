@@ -136,6 +136,7 @@ _SIGNATURES = {
     "f16_ppo_adam_step": (_i, [ctypes.POINTER(F16AdamArgs), _vp]),
     "f16_ppo_pack": (_i, [_vp, _i, _vp, _vp, _vp, _vp]),
     "f16_all_finite": (_i, [ctypes.POINTER(F16FiniteSpan), _i, _vp, _vp]),
+    "f16_permutation": (_i, [_vp, _l, _vp, _vp]),
 }
 
 _lib = None

@@ -32,6 +32,7 @@
 #include "f16_capi_common.h"
 #include "f16_policy.h"
 #include "f16_ppo.h"
+#include "philox.h"
 #include "policy_mfma.h"
 #include "sample_math.h"
 
@@ -1230,6 +1231,60 @@ __global__ __launch_bounds__(kFinBlock) void finite_kernel(FiniteSpans S,
   if (acc.m32 == kExp32 || acc.m64 == kExp64 || acc.zero != 0) flag[0] = 0;
 }
 
+// ---- the epoch's permutation of the transitions
+// perm[i] = the image of i under an eight-round balanced Feistel network on 2h bits (4^h the
+// smallest power of four >= n; round r maps (L, R) to (R, L ^ F(R ^ k_r)), F the low h bits of
+// MurmurHash3's 32-bit finaliser, the eight round keys k_r two Philox4x32-10 blocks of the 64-bit
+// key), applied again while the image lies outside [0, n) (cycle walking: the walk stays on i's
+// cycle of the network's bijection of [0, 4^h), so it ends, and the restriction is a bijection of
+// [0, n)).  Fewer than four network passes per element on average; with four rounds instead of
+// eight, the positions drawn for small n are measurably non-uniform.
+constexpr int kPermBlock = 256;
+constexpr int kPermRounds = 8;
+
+__device__ __forceinline__ uint32_t fmix32(uint32_t x) {
+  x ^= x >> 16;
+  x *= 0x85EBCA6Bu;
+  x ^= x >> 13;
+  x *= 0xC2B2AE35u;
+  x ^= x >> 16;
+  return x;
+}
+
+__device__ __forceinline__ uint64_t feistel(uint64_t x, int h, const uint32_t (&k)[kPermRounds]) {
+  const uint32_t mask = (1u << h) - 1u;
+  uint32_t L = (uint32_t)(x >> h), R = (uint32_t)x & mask;
+#pragma unroll
+  for (int r = 0; r < kPermRounds; ++r) {
+    const uint32_t nr = L ^ (fmix32(R ^ k[r]) & mask);
+    L = R;
+    R = nr;
+  }
+  return ((uint64_t)L << h) | R;
+}
+
+__global__ __launch_bounds__(kPermBlock) void permute_kernel(long long* __restrict__ perm,
+                                                             long n, int h,
+                                                             const unsigned long long* key) {
+  __shared__ uint32_t ks[kPermRounds];
+  if (threadIdx.x < kPermRounds / 4) {
+    const unsigned long long k = key[0];
+    uint32_t c[4] = {threadIdx.x, 0x243F6A88u, 0x85A308D3u, 0x13198A2Eu};
+    f16rng::philox4x32_10(c, (uint32_t)k, (uint32_t)(k >> 32));
+#pragma unroll
+    for (int j = 0; j < 4; ++j) ks[4 * threadIdx.x + j] = c[j];
+  }
+  __syncthreads();
+  const long i = (long)blockIdx.x * kPermBlock + threadIdx.x;
+  if (i >= n) return;
+  uint32_t k[kPermRounds];
+#pragma unroll
+  for (int r = 0; r < kPermRounds; ++r) k[r] = ks[r];
+  uint64_t x = feistel((uint64_t)i, h, k);
+  while (x >= (uint64_t)n) x = feistel(x, h, k);
+  perm[i] = (long long)x;
+}
+
 }  // namespace f16ppo
 
 using namespace f16ppo;
@@ -1398,5 +1453,15 @@ extern "C" int f16_all_finite(const F16FiniteSpan* spans, int nspans, unsigned c
   const long blocks = std::min<long>(std::max<long>(1, (chunks + per_block - 1) / per_block),
                                      8L * device_cus());
   hipLaunchKernelGGL(finite_kernel, dim3((unsigned)blocks), dim3(kFinBlock), 0, s, S, flag);
+  return f16_last_error();
+}
+
+extern "C" int f16_permutation(long long* perm, long n, const unsigned long long* key,
+                               void* stream) {
+  if (!perm || !key || n < 1 || n > (1L << 40)) return F16_EINVAL;
+  int h = 1;
+  while ((1L << (2 * h)) < n) ++h;
+  hipLaunchKernelGGL(permute_kernel, dim3((unsigned)((n + kPermBlock - 1) / kPermBlock)),
+                     dim3(kPermBlock), 0, (hipStream_t)stream, perm, n, h, key);
   return f16_last_error();
 }

@@ -10,8 +10,10 @@ Per minibatch two C-ABI calls:
   * f16_ppo_adam_step: clip_grad_norm_ of each network, torch.optim.Adam's update of the fp32
     master parameters, and the repack of the bf16 blobs the rollout kernel reads -- the next
     rollout (eager or a replayed HIP graph) sees the new weights with no host work.
-One host synchronisation per epoch (the KL early-stop test, as the reference's
-``float(last_kl)``) and one for the finite check before the update.
+Each epoch's shuffle is f16_permutation (a keyed Feistel permutation drawn on the device) in
+place of torch.randperm's sort of random keys, and the finite check before the update reads each
+buffer once (f16_all_finite).  One host synchronisation per epoch (the KL early-stop test, as the
+reference's ``float(last_kl)``) and one for the finite check.
 
 The master parameters are one flat fp32 buffer (actor_parameters() then critic_parameters());
 the network's torch parameters become views into it, so state_dict() keeps the reference's
@@ -200,6 +202,19 @@ class PPOUpdater:
         _lib.record_owned(self, stream, self._buffers())
         _lib.check(rc, "f16_ppo_adam_step")
 
+    def permutation(self, count):
+        """The epoch's shuffle, torch.randperm(count)'s role (ppo_gpu.py:2055): f16_permutation
+        keyed by a 62-bit word drawn on the device from the updater's generator, so the draw
+        needs no host synchronisation and a restored generator repeats it."""
+        key = torch.randint(0, 2 ** 62, (1,), dtype=torch.int64, device=self.device,
+                            generator=self.gen)
+        perm = torch.empty(int(count), dtype=torch.int64, device=self.device)
+        stream, h = _lib.launch_stream(self.device)
+        rc = self._L.f16_permutation(_lib.ptr(perm), int(count), _lib.ptr(key), h)
+        _lib.record(stream, (perm, key))
+        _lib.check(rc, "f16_permutation")
+        return perm
+
     # ---- the update (ppo_gpu.py:2019-2145)
     def update(self, rollout, adv, ret, perms=None):
         cfg, dev = self.cfg, self.device
@@ -232,7 +247,7 @@ class PPOUpdater:
             if perms is not None:
                 perm = perms[epoch].to(dev, torch.int64)
             else:
-                perm = torch.randperm(count, device=dev, generator=self.gen)
+                perm = self.permutation(count)
             for j, s in enumerate(range(0, count, mb_size)):
                 mb = perm[s:s + mb_size]
                 self.minibatch_grad(obs, act, old_logp, advantages, returns, mb, self.stats[j])

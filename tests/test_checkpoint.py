@@ -231,8 +231,7 @@ def test_runtime_resume_is_bit_identical(gpu, tmp_path, kind, graph):
         assert torch.equal(_bits(got[name]), _bits(want[name])), name
     assert done > 0                                          # autoresets inside the window
     # the restored updater draws the same minibatch permutation
-    assert torch.equal(torch.randperm(64, device=gpu, generator=up2.gen),
-                       torch.randperm(64, device=gpu, generator=up.gen))
+    assert torch.equal(up2.permutation(64), up.permutation(64))
 
 
 def test_runtime_state_round_trips_through_weights_only_load(tmp_path):

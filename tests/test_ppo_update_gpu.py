@@ -342,3 +342,47 @@ def test_finite_flag_argument_checks(gpu):
         U.finite_flag([x] * 17)
     with pytest.raises(ValueError):
         U.finite_flag(())
+
+
+def test_permutation_is_a_uniform_shuffle(gpu):
+    """f16_permutation: a permutation of 0..n-1 for n from 1 through non-powers of four and past
+    2^21; another key, another permutation; where each element of five lands over 2,000 keys is
+    uniform, and so is where each element of 17 lands (chi-square below the 0.1 % point
+    for n - 1 degrees of freedom; the same network with four rounds fails it); at 2^21 + 3
+    elements the mean displacement |perm[i] - i| / n is 1/3 and i and perm[i] are uncorrelated,
+    as for a uniformly random permutation."""
+    L = import_pkg("_lib")
+    lib = L.lib()
+    h = L.stream_handle()
+
+    def perm_of(n, key):
+        k = torch.tensor([key], dtype=torch.int64, device="cuda")
+        p = torch.empty(n, dtype=torch.int64, device="cuda")
+        assert lib.f16_permutation(L.ptr(p), n, L.ptr(k), h) == 0
+        return p
+
+    for n in (1, 2, 3, 4, 5, 16, 17, 1000, 65537, 1 << 21, (1 << 21) + 3):
+        p = perm_of(n, 12345 + n)
+        assert torch.equal(torch.sort(p).values, torch.arange(n, device="cuda")), n
+    assert not torch.equal(perm_of(1000, 1), perm_of(1000, 2))
+    assert torch.equal(perm_of(1000, 7), perm_of(1000, 7))
+    K = 2000
+    for n, bound in ((5, 18.47), (17, 39.25)):      # chi-square 0.1 % points, n - 1 dof
+        draws = torch.stack([perm_of(n, 1000 + k) for k in range(K)]).cpu()
+        for e in range(n):
+            pos = (draws == e).nonzero()[:, 1]
+            cnt = torch.bincount(pos, minlength=n).double()
+            chi2 = float(((cnt - K / n) ** 2 / (K / n)).sum())
+            assert chi2 < bound, (n, e, cnt.tolist())
+    n = (1 << 21) + 3
+    p = perm_of(n, 99).double()
+    i = torch.arange(n, device="cuda", dtype=torch.float64)
+    assert abs(float((p - i).abs().mean()) / n - 1 / 3) < 2e-3
+    corr = float(((p - p.mean()) * (i - i.mean())).mean() / (p.std() * i.std()))
+    assert abs(corr) < 3e-3
+    # argument checks (nothing launched)
+    k = torch.zeros(1, dtype=torch.int64, device="cuda")
+    out = torch.empty(4, dtype=torch.int64, device="cuda")
+    assert lib.f16_permutation(L.ptr(out), 0, L.ptr(k), h) == L.F16_EINVAL
+    assert lib.f16_permutation(None, 4, L.ptr(k), h) == L.F16_EINVAL
+    assert lib.f16_permutation(L.ptr(out), 4, None, h) == L.F16_EINVAL
