@@ -1,6 +1,6 @@
 // ppo_kernels.hip -- the PPO update of the discrete actor-critic MLP on gfx950.
 //
-// One minibatch (f16_ppo_grad) is nine launches:
+// One minibatch (f16_ppo_grad) is seven launches:
 //   adv_partial/final  minibatch advantage mean and sample std (shifted fp64 sums, two levels);
 //   ppo_fused_kernel   per 64 gathered rows (persistent, one workgroup per CU, the next tile's
 //                      rows in flight during the current one): forward of both networks, the loss head (softmax,
@@ -13,8 +13,9 @@
 //                      tiles of all four products, rows in chunks, 64-row stages double-buffered
 //                      through LDS, fp32 partials per chunk (bias gradients are the row sums of
 //                      dY, taken while staging);
-//   colsum kernels     the partials summed in a fixed order (deterministic, no atomics);
-//   stats_kernel       the minibatch means.
+//   colsum kernels     the partials summed in a fixed order (deterministic, no atomics): the
+//                      weight-gradient chunks, then the fused kernel's per-tile rows in two
+//                      levels, the second (colsum_tail_kernel) also forming the minibatch means.
 // The optimizer step (f16_ppo_adam_step) is three: per-block squared-norm partials, the clipped
 // Adam update (every block re-reduces the norm partials in the same order), and the repack of
 // the bf16 blobs the rollout and the next minibatch read.
@@ -1008,19 +1009,48 @@ __global__ __launch_bounds__(256) void colsum_group_kernel(const float* __restri
     mid[(long)blockIdx.y * kPartCols + c] = (sm[0][t] + sm[1][t]) + (sm[2][t] + sm[3][t]);
 }
 
-// minibatch means (ppo_gpu.py:2080-2081, 2098, 2107-2108)
-__global__ void stats_kernel(const float* __restrict__ sums, const float* __restrict__ advs,
-                             int n, float* __restrict__ stats) {
-  if (threadIdx.x != 0) return;
-  const float fn = (float)n;
-  stats[F16_PPO_STAT_POLICY_LOSS] = sums[0] / fn;
-  stats[F16_PPO_STAT_ENTROPY] = sums[1] / fn;
-  stats[F16_PPO_STAT_APPROX_KL] = sums[2] / fn;
-  stats[F16_PPO_STAT_CLIPFRAC] = sums[3] / fn;
-  stats[F16_PPO_STAT_VALUE_LOSS] = 0.5f * (sums[5] / fn);
-  stats[F16_PPO_STAT_ADV_MEAN] = advs[0];
-  stats[F16_PPO_STAT_ADV_STD] = advs[1];
-  stats[7] = sums[7];
+// second level over the first-level sums `mid` ([ng][kPartCols]): block x sums columns
+// [64x, 64x + 64) exactly as colsum_kernel<4> does (row phases r = ph (mod 4), combined in
+// order); the statistics columns [0, kStatCols) go to sums, dw3c and db3c to grad; block 0 then
+// forms the minibatch means from its statistics sums (ppo_gpu.py:2080-2081, 2098, 2107-2108).
+__global__ __launch_bounds__(256) void colsum_tail_kernel(const float* __restrict__ mid, int ng,
+                                                          float* __restrict__ sums,
+                                                          float* __restrict__ grad_w3c,
+                                                          const float* __restrict__ advs, int n,
+                                                          float* __restrict__ stats) {
+  __shared__ float sm[4][64];
+  const int t = threadIdx.x & 63, ph = threadIdx.x >> 6;
+  const int c = blockIdx.x * 64 + t;
+  constexpr int kCols = kStatCols + kHid + 1;
+  float acc = 0.0f;
+  if (c < kCols)
+    for (int r = ph; r < ng; r += 4) acc += mid[(long)r * kPartCols + c];
+  sm[ph][t] = acc;
+  __syncthreads();
+  if (ph == 0 && c < kCols) {
+    float v = sm[0][t];
+#pragma unroll
+    for (int k = 1; k < 4; ++k) v += sm[k][t];
+    if (c < kStatCols) {
+      sums[c] = v;
+      sm[0][t] = v;
+    } else {
+      grad_w3c[c - kStatCols] = v;
+    }
+  }
+  if (blockIdx.x != 0) return;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const float fn = (float)n;
+    stats[F16_PPO_STAT_POLICY_LOSS] = sm[0][0] / fn;
+    stats[F16_PPO_STAT_ENTROPY] = sm[0][1] / fn;
+    stats[F16_PPO_STAT_APPROX_KL] = sm[0][2] / fn;
+    stats[F16_PPO_STAT_CLIPFRAC] = sm[0][3] / fn;
+    stats[F16_PPO_STAT_VALUE_LOSS] = 0.5f * (sm[0][5] / fn);
+    stats[F16_PPO_STAT_ADV_MEAN] = advs[0];
+    stats[F16_PPO_STAT_ADV_STD] = advs[1];
+    stats[7] = sm[0][7];
+  }
 }
 
 // ---- clip_grad_norm_ + Adam
@@ -1377,12 +1407,8 @@ extern "C" int f16_ppo_grad(const F16PPOArgs* a, void* stream) {
   const int ng = (int)kColGroups(w.nwg);
   hipLaunchKernelGGL(colsum_group_kernel, dim3((kPartCols + 63) / 64, ng), dim3(256), 0, s,
                      (const float*)w.fpart, w.nwg, w.fmid);
-  hipLaunchKernelGGL(colsum_kernel<4>, dim3((unsigned)((kHid + 1 + 63) / 64)), dim3(256), 0, s,
-                     (const float*)(w.fmid + kStatCols), ng, (long)kPartCols, (long)(kHid + 1),
-                     a->grad + F.c_w3());
-  hipLaunchKernelGGL(colsum_kernel<4>, dim3(1), dim3(256), 0, s, (const float*)w.fmid, ng,
-                     (long)kPartCols, (long)kStatCols, w.advs + 8);
-  hipLaunchKernelGGL(stats_kernel, dim3(1), dim3(64), 0, s, (const float*)(w.advs + 8),
+  hipLaunchKernelGGL(colsum_tail_kernel, dim3((kStatCols + kHid + 1 + 63) / 64), dim3(256), 0, s,
+                     (const float*)w.fmid, ng, w.advs + 8, a->grad + F.c_w3(),
                      (const float*)w.advs, a->mb_rows, a->stats);
   return f16_last_error();
 }
