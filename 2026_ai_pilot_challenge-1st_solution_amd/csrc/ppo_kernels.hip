@@ -79,7 +79,8 @@ __host__ __device__ inline long align256(long x) { return (x + 255) & ~255L; }
 struct Work {
   float* advs;          // [8]: mean, std, statistics sums
   double* normp;        // [nblk][2] squared-norm partials
-  __bf16 *xt, *h1t, *h2t, *dh1t, *dh2t, *dzt;   // unit-major, leading dimension ld
+  __bf16 *xt, *h1t, *h2t, *dh1t, *dh2t, *dzt;   // unit-major in 64-row blocks (ublock); features
+                                                // kp, 512, 256, 512, 512, kLogitsPad
                                                 // (h2t: the actor's layer 2; the critic's
                                                 // enters only the value head, summed in-kernel)
   float* fpart;         // [nwg][kPartCols]
@@ -90,6 +91,16 @@ struct Work {
   int nwg, nchunk, chunk_rows, nadv;
   long bytes;
 };
+
+// The unit-major buffers are stored in 64-row blocks: feature f of row m of a buffer of NF
+// features at (m / 64) NF 64 + 64 f + m % 64, so each tile's output for one buffer is one
+// contiguous NF x 128-byte run and a weight-gradient stage (256 features x 64 rows) is one
+// contiguous 32 KB read, where a [feature][row] layout over the whole minibatch made every
+// 128-byte row segment its own DRAM page.  Within a block the feature stride is 64 elements.
+constexpr long kUBlock = 64;
+__host__ __device__ inline __bf16* ublock(__bf16* buf, long nf, long m0) {
+  return buf + (m0 / kUBlock) * nf * kUBlock;
+}
 
 constexpr int kColRows = 64;                     // rows per block of the two-level column sum
 inline long kColGroups(long nrows) { return (nrows + kColRows - 1) / kColRows; }
@@ -282,7 +293,8 @@ __device__ __forceinline__ void transpose_t(const __bf16* S, int pitch, __bf16* 
 // stores: the block's origin dst + u0 ld + m0 is the (wave-uniform) buffer base, the (g, j)
 // offset 2 (8g + j) ld the scalar offset and the lane's 2 (lh ld + lr) + 64 r the vector
 // offset, so a store needs no vector address arithmetic.  The buffer's window is 2 GB from the
-// base (offsets below 72 ld bytes occur, so ld < 2^24 rows); u0 must be wave-uniform.
+// base (offsets below 72 ld bytes occur; the kernels pass a 64-row block with ld = 64); u0 must
+// be wave-uniform.
 struct UnitMajor {
   __amdgpu_buffer_rsrc_t rsrc;
   int ld2;              // bytes between consecutive features
@@ -560,7 +572,7 @@ __global__ __launch_bounds__(kThreads, 1) void ppo_fused_kernel(const F16PPOArgs
     const int item = tid >> 1, hb = tid & 1;           // (row, channel) item, bin half
     const int lrow = item >> 2, lch = item & 3;
     const HeadIn hin = hnext;
-    transpose_t<KP>(Xs, XP, w.xt, ld, m0, wave, lane);
+    transpose_t<KP>(Xs, XP, ublock(w.xt, KP, m0), kUBlock, 0, wave, lane);
 
     // ---- actor forward
     WPre<kHid> pa2, pl3;
@@ -569,7 +581,7 @@ __global__ __launch_bounds__(kThreads, 1) void ppo_fused_kernel(const F16PPOArgs
       init_bias_lds(acc, cst + kB1, 32 * wave, lane);
       gemm_p<2, KP>(acc, pa1, wbf + Blob<KP>::W1, 32 * wave, Xs, XP, lane);
       wprefetch(pa2, wbf + Blob<KP>::W2A, 32 * wave, lane);
-      store_tanh_t(acc, H1s, 32 * wave, w.h1t, ld, m0, lane);
+      store_tanh_t(acc, H1s, 32 * wave, ublock(w.h1t, 2 * kHid, m0), kUBlock, 0, lane);
     }
     __syncthreads();
     {
@@ -577,7 +589,7 @@ __global__ __launch_bounds__(kThreads, 1) void ppo_fused_kernel(const F16PPOArgs
       init_bias_lds(acc, cst + kB2A, 32 * wave, lane);
       gemm_p<2, kHid>(acc, pa2, wbf + Blob<KP>::W2A, 32 * wave, H1s, kHPitch, lane);
       if (wave < 6) wprefetch(pl3, wbf + Blob<KP>::W3A, 32 * (wave % 3), lane);
-      store_tanh_t(acc, H2s, 32 * wave, w.h2t, ld, m0, lane);
+      store_tanh_t(acc, H2s, 32 * wave, ublock(w.h2t, kHid, m0), kUBlock, 0, lane);
       idx_store(a, pnext, rowpN, badN, tid);     // the next tile's rows, read after the barrier
     }
     __syncthreads();
@@ -701,7 +713,7 @@ __global__ __launch_bounds__(kThreads, 1) void ppo_fused_kernel(const F16PPOArgs
     __syncthreads();
     WPre<kLogitsPad> pb3;
     wprefetch(pb3, wT + kWT3, 32 * wave, lane);
-    transpose_t<kLogitsPad>(Zs, kZPitch, w.dzt, ld, m0, wave, lane);
+    transpose_t<kLogitsPad>(Zs, kZPitch, ublock(w.dzt, kLogitsPad, m0), kUBlock, 0, wave, lane);
 
     // ---- actor backward: dH2 = (dZ W3) (1 - H2^2) in place of H2, dH1 = (dH2 W2) (1 - H1^2)
     WPre<kHid> pb2, pbc, pc2;
@@ -711,7 +723,7 @@ __global__ __launch_bounds__(kThreads, 1) void ppo_fused_kernel(const F16PPOArgs
       zero_acc(acc);
       gemm_p<2, kLogitsPad>(acc, pb3, wT + kWT3, 32 * wave, Zs, kZPitch, lane);
       wprefetch(pb2, wT + kWT2A, 32 * wave, lane);
-      store_dtanh_t(acc, H2s, H2s, 32 * wave, w.dh2t, ld, m0, lane);
+      store_dtanh_t(acc, H2s, H2s, 32 * wave, ublock(w.dh2t, 2 * kHid, m0), kUBlock, 0, lane);
     }
     __syncthreads();
     {
@@ -719,7 +731,8 @@ __global__ __launch_bounds__(kThreads, 1) void ppo_fused_kernel(const F16PPOArgs
       zero_acc(acc);
       gemm_p<2, kHid>(acc, pb2, wT + kWT2A, 32 * wave, H2s, kHPitch, lane);
       wprefetch(pc1, wbf + Blob<KP>::W1C, 32 * wave, lane);
-      store_dtanh_t(acc, H1s, nullptr, 32 * wave, w.dh1t, ld, m0, lane);
+      store_dtanh_t(acc, H1s, nullptr, 32 * wave, ublock(w.dh1t, 2 * kHid, m0), kUBlock, 0,
+                    lane);
     }
     __syncthreads();
 
@@ -729,7 +742,8 @@ __global__ __launch_bounds__(kThreads, 1) void ppo_fused_kernel(const F16PPOArgs
       init_bias_lds(acc, cst + kB1 + kHid, 32 * wave, lane);
       gemm_p<2, KP>(acc, pc1, wbf + Blob<KP>::W1C, 32 * wave, Xs, XP, lane);
       wprefetch(pc2, wbf + Blob<KP>::W2C, 32 * wave, lane);
-      store_tanh_t(acc, H1s, 32 * wave, w.h1t + kHid * ld, ld, m0, lane);
+      store_tanh_t(acc, H1s, 32 * wave, ublock(w.h1t, 2 * kHid, m0) + kHid * kUBlock, kUBlock, 0,
+                   lane);
     }
     __syncthreads();
     bf16x4 hc2[4][2];                          // this lane's critic layer-2 activations
@@ -789,7 +803,8 @@ __global__ __launch_bounds__(kThreads, 1) void ppo_fused_kernel(const F16PPOArgs
     // left since the actor's backward) and unit-major
     {
       const float dv0 = rowf[lr][4], dv1 = rowf[32 + lr][4];
-      const UnitMajor out(w.dh2t + kHid * ld, ld, m0, 32 * wave, lane);
+      const UnitMajor out(ublock(w.dh2t, 2 * kHid, m0) + kHid * kUBlock, kUBlock, 0, 32 * wave,
+                          lane);
       float* part = w.fpart + (long)tile * kPartCols + kStatCols;
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
@@ -822,7 +837,8 @@ __global__ __launch_bounds__(kThreads, 1) void ppo_fused_kernel(const F16PPOArgs
       zero_acc(acc);
       gemm_p<2, kHid>(acc, pbc, wT + kWT2C, 32 * wave, H2s, kHPitch, lane);
       wprefetch(pa1, wbf + Blob<KP>::W1, 32 * wave, lane);    // the next tile's first product
-      store_dtanh_t(acc, H1s, nullptr, 32 * wave, w.dh1t + kHid * ld, ld, m0, lane);
+      store_dtanh_t(acc, H1s, nullptr, 32 * wave, ublock(w.dh1t, 2 * kHid, m0) + kHid * kUBlock,
+                    kUBlock, 0, lane);
     }
     // the next tile first writes Xs, rowp and rowf (read before the syncs above) and H1s only
     // after its first barrier, so no barrier is needed here
@@ -842,8 +858,9 @@ constexpr int kWThreads = 512;
 constexpr int kWPieces = kWT * kWK / 8 / kWThreads;   // 16-byte pieces per thread per operand
 
 struct WJob {
-  const __bf16* A;
+  const __bf16* A;     // feature 0 of row 0 in the 64-row block layout (ublock)
   const __bf16* B;
+  long sA, sB;         // elements between consecutive 64-row blocks: the buffer's features x 64
   int nA, nB;          // features present in the buffers (loads beyond read as zero)
   int vA, vB;          // features that are parameters
   long wbase[2];       // flat index of W[0][0] for a < 256 and for a >= 256
@@ -857,7 +874,9 @@ struct WJobs {
   int ntiles;
 };
 
-__global__ __launch_bounds__(kWThreads, 1) void wgrad_kernel(const WJobs J, long ld, long mp,
+static_assert(kWK == kUBlock, "a weight-gradient stage is one 64-row block of each operand");
+
+__global__ __launch_bounds__(kWThreads, 1) void wgrad_kernel(const WJobs J, long mp,
                                                              int chunk_rows, float* __restrict__ wpart,
                                                              long pld) {
   __shared__ __align__(16) __bf16 As[2][kWT * kWPitch];
@@ -879,13 +898,15 @@ __global__ __launch_bounds__(kWThreads, 1) void wgrad_kernel(const WJobs J, long
   for (int q = 0; q < kWPieces; ++q) bsum[q] = 0.0f;
   const bf16x8 zero8 = {};
   auto load = [&](int st) {
-    const long k = k0 + (long)st * kWK + 8 * part;
+    const long blk = k0 / kUBlock + st;         // kWK = 64: one block per stage
+    const __bf16* A = jb.A + blk * jb.sA + 8 * part;
+    const __bf16* B = jb.B + blk * jb.sB + 8 * part;
 #pragma unroll
     for (int q = 0; q < kWPieces; ++q) {
       const int f = (tid >> 3) + (kWThreads / 8) * q;
-      ra[q] = fa0 + f < jb.nA ? *reinterpret_cast<const bf16x8*>(jb.A + (long)(fa0 + f) * ld + k)
+      ra[q] = fa0 + f < jb.nA ? *reinterpret_cast<const bf16x8*>(A + (long)(fa0 + f) * kUBlock)
                               : zero8;
-      rb[q] = fb0 + f < jb.nB ? *reinterpret_cast<const bf16x8*>(jb.B + (long)(fb0 + f) * ld + k)
+      rb[q] = fb0 + f < jb.nB ? *reinterpret_cast<const bf16x8*>(B + (long)(fb0 + f) * kUBlock)
                               : zero8;
     }
   };
@@ -1358,7 +1379,7 @@ extern "C" long f16_ppo_workspace_bytes(int obs_dim, int mb_rows) {
 extern "C" int f16_ppo_grad(const F16PPOArgs* a, void* stream) {
   if (!a || (a->obs_dim != 184 && a->obs_dim != 214)) return F16_EINVAL;
   if (a->mb_rows < 1 || a->count < 1 || a->obs_ld < a->obs_dim) return F16_EINVAL;
-  if (a->mb_rows > kMaxMinibatchRows) return F16_EINVAL;   // the unit-major stores' window
+  if (a->mb_rows > kMaxMinibatchRows) return F16_EINVAL;   // bound on the minibatch size
   if (!a->obs || !a->act || !a->old_logp || !a->adv || !a->ret || !a->idx) return F16_EINVAL;
   if (!a->wbf || !a->wf || !a->wT || !a->grad || !a->stats || !a->work) return F16_EINVAL;
   if (((uintptr_t)a->wbf & 15) || ((uintptr_t)a->wT & 15) || ((uintptr_t)a->work & 255))
@@ -1380,11 +1401,15 @@ extern "C" int f16_ppo_grad(const F16PPOArgs* a, void* stream) {
   // the four weight-gradient products and their tiles
   WJobs J{};
   const long na = F.na();
-  J.job[0] = WJob{w.dh1t, w.xt, 512, kp, 512, D, {F.a_w1(), F.c_w1()}, {F.a_b1(), F.c_b1()}, D};
-  J.job[1] = WJob{w.dh2t, w.h1t, 256, 256, 256, 256, {F.a_w2(), F.a_w2()}, {F.a_b2(), F.a_b2()}, 256};
-  J.job[2] = WJob{w.dh2t + 256L * w.ld, w.h1t + 256L * w.ld, 256, 256, 256, 256,
+  constexpr long kB512 = 512 * kUBlock, kB256 = 256 * kUBlock;
+  J.job[0] = WJob{w.dh1t, w.xt, kB512, kp * kUBlock, 512, kp, 512, D, {F.a_w1(), F.c_w1()},
+                  {F.a_b1(), F.c_b1()}, D};
+  J.job[1] = WJob{w.dh2t, w.h1t, kB512, kB512, 256, 256, 256, 256, {F.a_w2(), F.a_w2()},
+                  {F.a_b2(), F.a_b2()}, 256};
+  J.job[2] = WJob{w.dh2t + kB256, w.h1t + kB256, kB512, kB512, 256, 256, 256, 256,
                   {F.c_w2(), F.c_w2()}, {F.c_b2(), F.c_b2()}, 256};
-  J.job[3] = WJob{w.dzt, w.h2t, kLogitsPad, 256, kLogits, 256, {F.a_w3(), F.a_w3()},
+  J.job[3] = WJob{w.dzt, w.h2t, kLogitsPad * kUBlock, kB256, kLogitsPad, 256, kLogits, 256,
+                  {F.a_w3(), F.a_w3()},
                   {F.a_b3(), F.a_b3()}, 256};
   (void)na;
   int nt = 0;
@@ -1399,7 +1424,7 @@ extern "C" int f16_ppo_grad(const F16PPOArgs* a, void* stream) {
       }
   J.ntiles = nt;
   const long pld = F.n() - 257;          // every flat parameter but the critic's value head
-  hipLaunchKernelGGL(wgrad_kernel, dim3(nt, w.nchunk), dim3(kWThreads), 0, s, J, w.ld, w.ld,
+  hipLaunchKernelGGL(wgrad_kernel, dim3(nt, w.nchunk), dim3(kWThreads), 0, s, J, w.ld,
                      w.chunk_rows, w.wpart, pld);
   hipLaunchKernelGGL(colsum_kernel<4>, dim3((unsigned)((pld + 63) / 64)), dim3(256), 0, s,
                      (const float*)w.wpart, w.nchunk, pld, pld, a->grad);
