@@ -85,7 +85,7 @@ class F16PPOArgs(ctypes.Structure):
                 ("adv", _vp), ("ret", _vp), ("count", _l), ("idx", _vp), ("mb_rows", _i),
                 ("clip_coef", ctypes.c_float), ("ent_coef", ctypes.c_float),
                 ("vf_coef", ctypes.c_float), ("norm_adv", _i), ("wbf", _vp), ("wf", _vp),
-                ("wT", _vp), ("grad", _vp), ("stats", _vp), ("work", _vp)]
+                ("wT", _vp), ("grad", _vp), ("stats", _vp), ("work", _vp), ("adv_stats", _vp)]
 
 
 class F16AdamArgs(ctypes.Structure):
@@ -137,6 +137,8 @@ _SIGNATURES = {
     "f16_ppo_pack": (_i, [_vp, _i, _vp, _vp, _vp, _vp]),
     "f16_all_finite": (_i, [ctypes.POINTER(F16FiniteSpan), _i, _vp, _vp]),
     "f16_permutation": (_i, [_vp, _l, _vp, _vp]),
+    "f16_ppo_adv_work_bytes": (_l, [_i, _i]),
+    "f16_ppo_adv_stats": (_i, [_vp, _vp, _l, _l, _i, _i, _vp, _vp, _vp]),
 }
 
 _lib = None

@@ -152,16 +152,15 @@ inline Work layout(int obs_dim, long mb_rows, void* base, int wg_slots = kWgradS
 // sums (x - K) and (x - K)^2 in fp64 over its rows, K the minibatch's first advantage (shifting
 // keeps the one-pass variance exact to fp64 rounding for any mean); one block merges the partials
 // in a fixed order.
-__global__ __launch_bounds__(kAdvThreads) void adv_partial_kernel(const float* __restrict__ adv,
-                                                                  const long long* __restrict__ idx,
-                                                                  int n, long count,
-                                                                  double* __restrict__ part) {
+__device__ __forceinline__ void adv_partial_body(const float* __restrict__ adv,
+                                                 const long long* __restrict__ idx, int n,
+                                                 long count, double* __restrict__ part, int blk) {
   __shared__ double rs[kAdvThreads], rq[kAdvThreads];
   const int t = threadIdx.x;
   const long long p0 = idx[0];
   const double K = (p0 >= 0 && p0 < count) ? (double)adv[p0] : 0.0;
   double s = 0.0, q = 0.0;
-  const int i = blockIdx.x * kAdvThreads * kAdvPer + t;
+  const int i = blk * kAdvThreads * kAdvPer + t;
   // every index load, then every value load, unconditionally (out-of-range items read element
   // 0 and are not summed): loads chosen or skipped inside the summing loop were issued one at a
   // time, each waiting out the previous ones
@@ -188,14 +187,20 @@ __global__ __launch_bounds__(kAdvThreads) void adv_partial_kernel(const float* _
     if (t < w) { rs[t] += rs[t + w]; rq[t] += rq[t + w]; }
     __syncthreads();
   }
-  if (t == 0) { part[2L * blockIdx.x] = rs[0]; part[2L * blockIdx.x + 1] = rq[0]; }
+  if (t == 0) { part[2L * blk] = rs[0]; part[2L * blk + 1] = rq[0]; }
 }
 
-__global__ __launch_bounds__(kAdvThreads) void adv_final_kernel(const float* __restrict__ adv,
-                                                                const long long* __restrict__ idx,
-                                                                int n, long count, int nblk,
-                                                                const double* __restrict__ part,
-                                                                float* advs) {
+__global__ __launch_bounds__(kAdvThreads) void adv_partial_kernel(const float* __restrict__ adv,
+                                                                  const long long* __restrict__ idx,
+                                                                  int n, long count,
+                                                                  double* __restrict__ part) {
+  adv_partial_body(adv, idx, n, count, part, blockIdx.x);
+}
+
+__device__ __forceinline__ void adv_final_body(const float* __restrict__ adv,
+                                               const long long* __restrict__ idx, int n,
+                                               long count, int nblk,
+                                               const double* __restrict__ part, float* advs) {
   __shared__ double rs[kAdvThreads], rq[kAdvThreads];
   const int t = threadIdx.x;
   double s = 0.0, q = 0.0;
@@ -216,6 +221,33 @@ __global__ __launch_bounds__(kAdvThreads) void adv_final_kernel(const float* __r
     advs[0] = (float)(K + ms);
     advs[1] = (float)sqrt(var);
   }
+}
+
+__global__ __launch_bounds__(kAdvThreads) void adv_final_kernel(const float* __restrict__ adv,
+                                                                const long long* __restrict__ idx,
+                                                                int n, long count, int nblk,
+                                                                const double* __restrict__ part,
+                                                                float* advs) {
+  adv_final_body(adv, idx, n, count, nblk, part, advs);
+}
+
+// The same for every minibatch of an epoch at once: minibatch j (blockIdx.y, then blockIdx.x of
+// the final level) is idx[j mb, min((j + 1) mb, total)), its partials at part + 2 nadv j and its
+// mean and std at out[2j], out[2j + 1] -- the values f16_ppo_grad forms for that minibatch alone.
+__global__ __launch_bounds__(kAdvThreads) void adv_partial_epoch_kernel(
+    const float* __restrict__ adv, const long long* __restrict__ idx, int mb, long total,
+    long count, int nadv, double* __restrict__ part) {
+  const long s0 = (long)blockIdx.y * mb;
+  adv_partial_body(adv, idx + s0, (int)min((long)mb, total - s0), count,
+                   part + 2L * nadv * blockIdx.y, blockIdx.x);
+}
+
+__global__ __launch_bounds__(kAdvThreads) void adv_final_epoch_kernel(
+    const float* __restrict__ adv, const long long* __restrict__ idx, int mb, long total,
+    long count, int nadv, const double* __restrict__ part, float* __restrict__ out) {
+  const long s0 = (long)blockIdx.x * mb;
+  adv_final_body(adv, idx + s0, (int)min((long)mb, total - s0), count, nadv,
+                 part + 2L * nadv * blockIdx.x, out + 2L * blockIdx.x);
 }
 
 // ---- fused forward / loss / backward of 64 gathered rows
@@ -522,7 +554,8 @@ __global__ __launch_bounds__(kThreads, 1) void ppo_fused_kernel(const F16PPOArgs
   const float* wf = a.wf;
   const float inv_mb = 1.0f / (float)a.mb_rows;
   // launch constants read once (scalar loads before any store of this kernel)
-  const float adv_mean = w.advs[0], adv_std = w.advs[1], b3c = wf[kB3C];
+  const float* const am = a.adv_stats ? a.adv_stats : w.advs;
+  const float adv_mean = am[0], adv_std = am[1], b3c = wf[kB3C];
   for (int i = threadIdx.x; i < kB3C / 4; i += kThreads)
     reinterpret_cast<float4*>(cst)[i] = reinterpret_cast<const float4*>(wf)[i];
   const float* w3s = cst + kW3C;
@@ -1389,10 +1422,12 @@ extern "C" int f16_ppo_grad(const F16PPOArgs* a, void* stream) {
   const Flat F{D};
   const Work w = layout(D, a->mb_rows, a->work, wgrad_slots());
   hipStream_t s = (hipStream_t)stream;
-  hipLaunchKernelGGL(adv_partial_kernel, dim3(w.nadv), dim3(kAdvThreads), 0, s, a->adv, a->idx,
-                     a->mb_rows, a->count, w.advp);
-  hipLaunchKernelGGL(adv_final_kernel, dim3(1), dim3(kAdvThreads), 0, s, a->adv, a->idx,
-                     a->mb_rows, a->count, w.nadv, (const double*)w.advp, w.advs);
+  if (!a->adv_stats) {   // else the epoch's f16_ppo_adv_stats formed them
+    hipLaunchKernelGGL(adv_partial_kernel, dim3(w.nadv), dim3(kAdvThreads), 0, s, a->adv, a->idx,
+                       a->mb_rows, a->count, w.advp);
+    hipLaunchKernelGGL(adv_final_kernel, dim3(1), dim3(kAdvThreads), 0, s, a->adv, a->idx,
+                       a->mb_rows, a->count, w.nadv, (const double*)w.advp, w.advs);
+  }
   const unsigned fgrid = (unsigned)std::min(w.nwg, device_cus());
   if (kp == 192)
     hipLaunchKernelGGL(ppo_fused_kernel<192>, dim3(fgrid), dim3(kThreads), 0, s, *a, w);
@@ -1434,7 +1469,7 @@ extern "C" int f16_ppo_grad(const F16PPOArgs* a, void* stream) {
                      (const float*)w.fpart, w.nwg, w.fmid);
   hipLaunchKernelGGL(colsum_tail_kernel, dim3((kStatCols + kHid + 1 + 63) / 64), dim3(256), 0, s,
                      (const float*)w.fmid, ng, w.advs + 8, a->grad + F.c_w3(),
-                     (const float*)w.advs, a->mb_rows, a->stats);
+                     a->adv_stats ? a->adv_stats : (const float*)w.advs, a->mb_rows, a->stats);
   return f16_last_error();
 }
 
@@ -1514,5 +1549,29 @@ extern "C" int f16_permutation(long long* perm, long n, const unsigned long long
   while ((1L << (2 * h)) < n) ++h;
   hipLaunchKernelGGL(permute_kernel, dim3((unsigned)((n + kPermBlock - 1) / kPermBlock)),
                      dim3(kPermBlock), 0, (hipStream_t)stream, perm, n, h, key);
+  return f16_last_error();
+}
+
+static inline int adv_blocks(int mb_rows) {
+  return (mb_rows + kAdvThreads * kAdvPer - 1) / (kAdvThreads * kAdvPer);
+}
+
+extern "C" long f16_ppo_adv_work_bytes(int mb_rows, int nmb) {
+  if (mb_rows < 1 || mb_rows > kMaxMinibatchRows || nmb < 1) return -1;
+  return (long)adv_blocks(mb_rows) * nmb * 2 * (long)sizeof(double);
+}
+
+extern "C" int f16_ppo_adv_stats(const float* adv, const long long* idx, long total, long count,
+                                 int mb_rows, int nmb, float* out, void* work, void* stream) {
+  if (!adv || !idx || !out || !work || total < 1 || count < 1) return F16_EINVAL;
+  if (mb_rows < 1 || mb_rows > kMaxMinibatchRows || nmb < 1 || nmb > 65535) return F16_EINVAL;
+  if ((long)(nmb - 1) * mb_rows >= total || (long)nmb * mb_rows < total) return F16_EINVAL;
+  if ((uintptr_t)work & 7) return F16_EINVAL;
+  const int nadv = adv_blocks(mb_rows);
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL(adv_partial_epoch_kernel, dim3(nadv, nmb), dim3(kAdvThreads), 0, s, adv,
+                     idx, mb_rows, total, count, nadv, static_cast<double*>(work));
+  hipLaunchKernelGGL(adv_final_epoch_kernel, dim3(nmb), dim3(kAdvThreads), 0, s, adv, idx,
+                     mb_rows, total, count, nadv, static_cast<const double*>(work), out);
   return f16_last_error();
 }

@@ -131,6 +131,7 @@ class PPOUpdater:
         self.gen.manual_seed(int(seed))
         self._work = None
         self._work_rows = 0
+        self._adv_work = None
         self.stats = torch.zeros(1, NSTATS, dtype=torch.float32, device=dev)
 
     # ---- blobs
@@ -158,9 +159,10 @@ class PPOUpdater:
         return self._work
 
     # ---- one minibatch
-    def minibatch_grad(self, obs, act, old_logp, adv, ret, idx, stats_row=None):
+    def minibatch_grad(self, obs, act, old_logp, adv, ret, idx, stats_row=None, adv_stats=None):
         """Loss gradients of the minibatch idx (int64 device indices into the flattened buffers)
-        into self.grad; statistics into stats_row (8 floats)."""
+        into self.grad; statistics into stats_row (8 floats).  adv_stats: the minibatch's
+        advantage mean and std (2 device floats, from epoch_adv_stats), or None to form them."""
         cfg = self.cfg
         n = int(idx.numel())
         if stats_row is None:
@@ -175,11 +177,32 @@ class PPOUpdater:
         a.wbf, a.wf, a.wT = _lib.ptr(self.wbf), _lib.ptr(self.wf), _lib.ptr(self.wT)
         a.grad, a.stats, a.work = _lib.ptr(self.grad), _lib.ptr(stats_row), \
             _lib.ptr(self._workspace(n))
+        a.adv_stats = _lib.ptr(adv_stats)
         stream, h = _lib.launch_stream(self.device)
         rc = self._L.f16_ppo_grad(ctypes.byref(a), h)
         _lib.record_owned(self, stream, self._buffers())
-        _lib.record(stream, (obs, act, old_logp, adv, ret, idx, stats_row))
+        _lib.record(stream, (obs, act, old_logp, adv, ret, idx, stats_row, adv_stats))
         _lib.check(rc, "f16_ppo_grad")
+
+    def epoch_adv_stats(self, adv, perm, mb_rows):
+        """(nmb, 2) device floats: every minibatch's advantage mean and sample std for the
+        epoch's permutation cut into mb_rows slices (f16_ppo_adv_stats: two launches per epoch
+        instead of two per minibatch; the same values f16_ppo_grad forms per minibatch)."""
+        total = int(perm.numel())
+        nmb = (total + mb_rows - 1) // mb_rows
+        nbytes = self._L.f16_ppo_adv_work_bytes(int(mb_rows), nmb)
+        if nbytes < 0:
+            raise ValueError("bad minibatch size")
+        if self._adv_work is None or self._adv_work.numel() < nbytes:
+            self._adv_work = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
+        out = torch.empty(nmb, 2, dtype=torch.float32, device=self.device)
+        stream, h = _lib.launch_stream(self.device)
+        rc = self._L.f16_ppo_adv_stats(_lib.ptr(adv), _lib.ptr(perm), total, int(adv.numel()),
+                                       int(mb_rows), nmb, _lib.ptr(out),
+                                       _lib.ptr(self._adv_work), h)
+        _lib.record(stream, (adv, perm, out, self._adv_work))
+        _lib.check(rc, "f16_ppo_adv_stats")
+        return out
 
     def optimizer_step(self):
         """clip_grad_norm_ + Adam on both networks, then the blobs (ppo_gpu.py:2088-2105)."""
@@ -248,9 +271,11 @@ class PPOUpdater:
                 perm = perms[epoch].to(dev, torch.int64)
             else:
                 perm = self.permutation(count)
+            adv_stats = self.epoch_adv_stats(advantages, perm, mb_size)
             for j, s in enumerate(range(0, count, mb_size)):
                 mb = perm[s:s + mb_size]
-                self.minibatch_grad(obs, act, old_logp, advantages, returns, mb, self.stats[j])
+                self.minibatch_grad(obs, act, old_logp, advantages, returns, mb, self.stats[j],
+                                    adv_stats=adv_stats[j])
                 self.optimizer_step()
                 steps += 1
             last_kl = self.stats[:nmb, STAT_KL].mean()

@@ -63,6 +63,8 @@ typedef struct F16PPOArgs {
     float *grad;                 /* flat (n_actor + n_critic) loss gradients, unclipped */
     float *stats;                /* F16_PPO_NSTATS floats */
     void *work;                  /* f16_ppo_workspace_bytes(obs_dim, >= mb_rows) */
+    const float *adv_stats;      /* optional: this minibatch's advantage mean and sample std
+                                    (2 floats, f16_ppo_adv_stats); NULL = formed here */
 } F16PPOArgs;
 
 /* One minibatch of PPOGPUTrainer.update (R/cuda_fdm/ppo_gpu.py:2059-2109): the actor loss
@@ -72,6 +74,15 @@ typedef struct F16PPOArgs {
  * respect to the flat parameters (the actor's through log_softmax, the critic's through the value
  * head); bf16 operands on MFMA, fp32 accumulation, deterministic reductions. */
 int f16_ppo_grad(const F16PPOArgs *args, void *stream);
+
+/* The advantage mean and sample std of every minibatch of an epoch, in two launches instead of
+ * two per minibatch: minibatch j is idx[j mb_rows .. min((j + 1) mb_rows, total)) (the epoch's
+ * permutation cut as PPOGPUTrainer.update cuts it, ppo_gpu.py:2055-2078), its mean and std at
+ * out[2j], out[2j + 1] (device), the same values f16_ppo_grad forms for it alone.  nmb must be
+ * ceil(total / mb_rows); work: f16_ppo_adv_work_bytes(mb_rows, nmb) device bytes. */
+long f16_ppo_adv_work_bytes(int mb_rows, int nmb);
+int f16_ppo_adv_stats(const float *adv, const long long *idx, long total, long count, int mb_rows,
+                      int nmb, float *out, void *work, void *stream);
 
 typedef struct F16AdamArgs {
     int obs_dim;

@@ -386,3 +386,48 @@ def test_permutation_is_a_uniform_shuffle(gpu):
     assert lib.f16_permutation(L.ptr(out), 0, L.ptr(k), h) == L.F16_EINVAL
     assert lib.f16_permutation(None, 4, L.ptr(k), h) == L.F16_EINVAL
     assert lib.f16_permutation(L.ptr(out), 4, None, h) == L.F16_EINVAL
+
+
+def test_epoch_advantage_stats_equal_per_minibatch(gpu):
+    """f16_ppo_adv_stats forms every minibatch's advantage mean and std of an epoch in two
+    launches: equal bit for bit to what f16_ppo_grad forms for each minibatch alone (a ragged
+    last minibatch, sizes across the 2,048-row partial blocks), and a minibatch gradient fed the
+    precomputed pair equals the one that forms it; the argument checks refuse a bad cut."""
+    U, L = import_pkg("ppo_update"), import_pkg("_lib")
+    D = 184
+    net = make_net(D, seed=11)
+    flat = flat_of(net)
+    T, rows = 7, 1000
+    ro, adv, ret = fake_rollout(flat, D, T, rows, seed=3)
+    up = U.PPOUpdater(net.to(gpu), U.UpdateConfig())
+    d = to_dev(ro, gpu)
+    obs, act, logp = d.b_obs.flatten(0, 1), d.b_act.flatten(0, 1), d.b_logp.flatten()
+    advd, retd = adv.reshape(-1).to(gpu), ret.reshape(-1).to(gpu)
+    count = T * rows
+    for mb in (2048, 2049, 1000, 333, count):
+        perm = torch.randperm(count, generator=torch.Generator().manual_seed(mb)).to(gpu)
+        st = up.epoch_adv_stats(advd, perm, mb)
+        nmb = (count + mb - 1) // mb
+        assert st.shape == (nmb, 2)
+        for j in sorted({0, nmb - 1}):
+            idx = perm[j * mb:(j + 1) * mb]
+            up.minibatch_grad(obs, act, logp, advd, retd, idx)
+            own = up.stats[0].clone()
+            g_own = up.grad.clone()
+            assert float(own[U.STAT_ADV_MEAN]) == float(st[j, 0]), (mb, j)
+            assert float(own[U.STAT_ADV_STD]) == float(st[j, 1]), (mb, j)
+            up.minibatch_grad(obs, act, logp, advd, retd, idx, adv_stats=st[j])
+            assert torch.equal(up.grad, g_own), (mb, j)
+            assert torch.equal(up.stats[0], own), (mb, j)
+    lib, h = L.lib(), L.stream_handle()
+    perm = torch.arange(count, device=gpu)
+    out = torch.empty(16, dtype=torch.float32, device=gpu)
+    work = torch.empty(1 << 20, dtype=torch.uint8, device=gpu)
+    args = lambda total, mb, nmb: lib.f16_ppo_adv_stats(L.ptr(advd), L.ptr(perm), total, count,
+                                                        mb, nmb, L.ptr(out), L.ptr(work), h)
+    assert args(count, 1000, 7) == 0
+    torch.cuda.synchronize()
+    assert args(count, 1000, 6) == L.F16_EINVAL      # too few minibatches for the cut
+    assert args(count, 1000, 8) == L.F16_EINVAL      # one minibatch past the end
+    assert args(0, 1000, 1) == L.F16_EINVAL
+    assert lib.f16_ppo_adv_work_bytes(0, 1) == -1
