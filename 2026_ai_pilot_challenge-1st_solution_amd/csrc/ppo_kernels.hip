@@ -1046,6 +1046,33 @@ __global__ __launch_bounds__(64 * PH) void colsum_kernel(const float* __restrict
   }
 }
 
+// colsum_kernel<4> four columns to a thread (16-byte loads and stores; ncols and ld multiples of
+// 4, part and out 16-byte aligned): every column summed in the same row order, the same bits
+__global__ __launch_bounds__(256) void colsum4_kernel(const float* __restrict__ part, int nrows,
+                                                      long ld, long ncols,
+                                                      float* __restrict__ out) {
+  __shared__ float4 s[4][64];
+  const int t = threadIdx.x & 63, ph = threadIdx.x >> 6;
+  const long c = 4 * ((long)blockIdx.x * 64 + t);
+  float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  if (c < ncols)
+    for (int r = ph; r < nrows; r += 4) {
+      const float4 v = *reinterpret_cast<const float4*>(part + (long)r * ld + c);
+      acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
+    }
+  s[ph][t] = acc;
+  __syncthreads();
+  if (ph == 0 && c < ncols) {
+    float4 v = s[0][t];
+#pragma unroll
+    for (int k = 1; k < 4; ++k) {
+      const float4 u = s[k][t];
+      v.x += u.x; v.y += u.y; v.z += u.z; v.w += u.w;
+    }
+    *reinterpret_cast<float4*>(out + c) = v;
+  }
+}
+
 // first level over the fused kernel's partial rows: block (x, y) sums rows [64y, 64y + 64) of
 // columns [64x, 64x + 64) (4 phases of 16 rows, combined in order)
 __global__ __launch_bounds__(256) void colsum_group_kernel(const float* __restrict__ part, int nrows,
@@ -1461,8 +1488,12 @@ extern "C" int f16_ppo_grad(const F16PPOArgs* a, void* stream) {
   const long pld = F.n() - 257;          // every flat parameter but the critic's value head
   hipLaunchKernelGGL(wgrad_kernel, dim3(nt, w.nchunk), dim3(kWThreads), 0, s, J, w.ld,
                      w.chunk_rows, w.wpart, pld);
-  hipLaunchKernelGGL(colsum_kernel<4>, dim3((unsigned)((pld + 63) / 64)), dim3(256), 0, s,
-                     (const float*)w.wpart, w.nchunk, pld, pld, a->grad);
+  if (pld % 4 == 0 && ((uintptr_t)a->grad & 15) == 0)
+    hipLaunchKernelGGL(colsum4_kernel, dim3((unsigned)((pld / 4 + 63) / 64)), dim3(256), 0, s,
+                       (const float*)w.wpart, w.nchunk, pld, pld, a->grad);
+  else
+    hipLaunchKernelGGL(colsum_kernel<4>, dim3((unsigned)((pld + 63) / 64)), dim3(256), 0, s,
+                       (const float*)w.wpart, w.nchunk, pld, pld, a->grad);
   // the per-workgroup partials (statistics, dw3c, db3c): groups of kColRows rows, then the groups
   const int ng = (int)kColGroups(w.nwg);
   hipLaunchKernelGGL(colsum_group_kernel, dim3((kPartCols + 63) / 64, ng), dim3(256), 0, s,
