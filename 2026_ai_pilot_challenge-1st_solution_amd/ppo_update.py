@@ -12,7 +12,8 @@ Per minibatch two C-ABI calls:
     rollout (eager or a replayed HIP graph) sees the new weights with no host work.
 Each epoch's shuffle is f16_permutation (a keyed Feistel permutation drawn on the device) in
 place of torch.randperm's sort of random keys, and the finite check before the update reads each
-buffer once (f16_all_finite).  One host synchronisation per epoch (the KL early-stop test, as the
+buffer once (f16_all_finite), on a second stream beside the first minibatch's gradient and tested
+before its optimizer step.  One host synchronisation per epoch (the KL early-stop test, as the
 reference's ``float(last_kl)``) and one for the finite check.
 
 The master parameters are one flat fp32 buffer (actor_parameters() then critic_parameters());
@@ -132,6 +133,7 @@ class PPOUpdater:
         self._work = None
         self._work_rows = 0
         self._adv_work = None
+        self._side = None                                  # the finite check's stream
         self.stats = torch.zeros(1, NSTATS, dtype=torch.float32, device=dev)
 
     # ---- blobs
@@ -253,9 +255,17 @@ class PPOUpdater:
             raise ValueError("advantage/return shape must match the rollout values")
         if obs.shape[1] != self.D:
             raise ValueError("observation width does not match the network")
-        # one aggregate finite check before any gradient step (ppo_gpu.py:2000-2009)
-        if not bool(finite_flag((obs, rollout.b_rew, b_val, old_logp, advantages, returns))):
-            raise FloatingPointError("non-finite physical trajectory or PPO rollout; update refused")
+        # one aggregate finite check before any optimizer step (ppo_gpu.py:2000-2009): read on
+        # a second stream beside the first minibatch's gradient launches, its flag copied to the
+        # host on that stream and tested before the first Adam step, so the parameters and the
+        # optimizer state are untouched when the update is refused
+        cur = torch.cuda.current_stream(dev)
+        if self._side is None:
+            self._side = torch.cuda.Stream(device=dev)   # default priority
+        self._side.wait_stream(cur)
+        with torch.cuda.stream(self._side):
+            ok = finite_flag((obs, rollout.b_rew, b_val, old_logp, advantages, returns))
+        checked = False
         obs, act = obs.contiguous(), act.contiguous()
         old_logp, advantages, returns = (x.contiguous().float() for x in
                                          (old_logp, advantages, returns))
@@ -276,6 +286,13 @@ class PPOUpdater:
                 mb = perm[s:s + mb_size]
                 self.minibatch_grad(obs, act, old_logp, advantages, returns, mb, self.stats[j],
                                     adv_stats=adv_stats[j])
+                if not checked:
+                    with torch.cuda.stream(self._side):
+                        finite = bool(ok.cpu())           # waits for the side stream only
+                    if not finite:
+                        raise FloatingPointError(
+                            "non-finite physical trajectory or PPO rollout; update refused")
+                    checked = True
                 self.optimizer_step()
                 steps += 1
             last_kl = self.stats[:nmb, STAT_KL].mean()

@@ -222,8 +222,14 @@ def test_early_stop_and_refusals(gpu):
     assert res["early"] and res["epochs"] == 1 and res["optimizer_steps"] == 2
     bad = to_dev(ro, gpu)
     bad.b_obs[0, 3, 5] = float("nan")
+    before = [t.clone() for t in (up.flat, up.exp_avg, up.exp_avg_sq)]
+    steps = up.steps
     with pytest.raises(FloatingPointError):
         up.update(bad, adv.to(gpu), ret.to(gpu))
+    # refused before any optimizer step: parameters, moments and the step count untouched
+    torch.cuda.synchronize()
+    assert all(torch.equal(x, y) for x, y in zip(before, (up.flat, up.exp_avg, up.exp_avg_sq)))
+    assert up.steps == steps
     with pytest.raises(ValueError):
         up.update(to_dev(ro, gpu), adv[:1].to(gpu), ret.to(gpu))
 
