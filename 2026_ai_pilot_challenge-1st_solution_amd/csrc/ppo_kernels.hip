@@ -1343,13 +1343,16 @@ __global__ __launch_bounds__(kFinBlock) void finite_kernel(FiniteSpans S,
 }
 
 // ---- the epoch's permutation of the transitions
-// perm[i] = the image of i under an eight-round balanced Feistel network on 2h bits (4^h the
-// smallest power of four >= n; round r maps (L, R) to (R, L ^ F(R ^ k_r)), F the low h bits of
+// perm[i] = the image of i under an eight-round Feistel network on la + lb bits (round r maps
+// (L, R), L of a bits and R of b, to (R, L ^ F(R ^ k_r)) and swaps a and b; F the low a bits of
 // MurmurHash3's 32-bit finaliser, the eight round keys k_r two Philox4x32-10 blocks of the 64-bit
 // key), applied again while the image lies outside [0, n) (cycle walking: the walk stays on i's
-// cycle of the network's bijection of [0, 4^h), so it ends, and the restriction is a bijection of
-// [0, n)).  Fewer than four network passes per element on average; with four rounds instead of
-// eight, the positions drawn for small n are measurably non-uniform.
+// cycle of the network's bijection of [0, 2^(la + lb)), so it ends, and the restriction is a
+// bijection of [0, n)).  Below 2^15 elements the halves are equal (la = lb = h, 4^h the smallest
+// power of four >= n: fewer than four passes per element on average; with four rounds instead of
+// eight the positions drawn for small n are measurably non-uniform); above, la + lb is the
+// smallest power of two >= n with halves of 8 bits or more: fewer than two passes on average and
+// one at a power of two (a wave waits for its longest walk, so the shorter walks count).
 constexpr int kPermBlock = 256;
 constexpr int kPermRounds = 8;
 
@@ -1362,20 +1365,24 @@ __device__ __forceinline__ uint32_t fmix32(uint32_t x) {
   return x;
 }
 
-__device__ __forceinline__ uint64_t feistel(uint64_t x, int h, const uint32_t (&k)[kPermRounds]) {
-  const uint32_t mask = (1u << h) - 1u;
-  uint32_t L = (uint32_t)(x >> h), R = (uint32_t)x & mask;
+__device__ __forceinline__ uint64_t feistel(uint64_t x, int la, int lb,
+                                            const uint32_t (&k)[kPermRounds]) {
+  int a = la, b = lb;
+  uint32_t L = (uint32_t)(x >> b), R = (uint32_t)x & ((1u << b) - 1u);
 #pragma unroll
-  for (int r = 0; r < kPermRounds; ++r) {
-    const uint32_t nr = L ^ (fmix32(R ^ k[r]) & mask);
+  for (int r = 0; r < kPermRounds; ++r) {   // an even count: a and b end as they began
+    const uint32_t nr = L ^ (fmix32(R ^ k[r]) & ((1u << a) - 1u));
     L = R;
     R = nr;
+    const int t = a;
+    a = b;
+    b = t;
   }
-  return ((uint64_t)L << h) | R;
+  return ((uint64_t)L << b) | R;
 }
 
 __global__ __launch_bounds__(kPermBlock) void permute_kernel(long long* __restrict__ perm,
-                                                             long n, int h,
+                                                             long n, int la, int lb,
                                                              const unsigned long long* key) {
   __shared__ uint32_t ks[kPermRounds];
   if (threadIdx.x < kPermRounds / 4) {
@@ -1391,8 +1398,8 @@ __global__ __launch_bounds__(kPermBlock) void permute_kernel(long long* __restri
   uint32_t k[kPermRounds];
 #pragma unroll
   for (int r = 0; r < kPermRounds; ++r) k[r] = ks[r];
-  uint64_t x = feistel((uint64_t)i, h, k);
-  while (x >= (uint64_t)n) x = feistel(x, h, k);
+  uint64_t x = feistel((uint64_t)i, la, lb, k);
+  while (x >= (uint64_t)n) x = feistel(x, la, lb, k);
   perm[i] = (long long)x;
 }
 
@@ -1576,10 +1583,19 @@ extern "C" int f16_all_finite(const F16FiniteSpan* spans, int nspans, unsigned c
 extern "C" int f16_permutation(long long* perm, long n, const unsigned long long* key,
                                void* stream) {
   if (!perm || !key || n < 1 || n > (1L << 40)) return F16_EINVAL;
-  int h = 1;
-  while ((1L << (2 * h)) < n) ++h;
+  int k = 1;
+  while ((1L << k) < n) ++k;
+  int la, lb;
+  if (k >= 16) {
+    la = k - k / 2;
+    lb = k / 2;
+  } else {
+    la = 1;
+    while ((1L << (2 * la)) < n) ++la;
+    lb = la;
+  }
   hipLaunchKernelGGL(permute_kernel, dim3((unsigned)((n + kPermBlock - 1) / kPermBlock)),
-                     dim3(kPermBlock), 0, (hipStream_t)stream, perm, n, h, key);
+                     dim3(kPermBlock), 0, (hipStream_t)stream, perm, n, la, lb, key);
   return f16_last_error();
 }
 

@@ -380,6 +380,13 @@ def test_permutation_is_a_uniform_shuffle(gpu):
             cnt = torch.bincount(pos, minlength=n).double()
             chi2 = float(((cnt - K / n) ** 2 / (K / n)).sum())
             assert chi2 < bound, (n, e, cnt.tolist())
+    # the unequal-halves network above 2^15 elements: where positions 0, 777 and n - 1 send
+    # their element over 400 keys, in 16 bins of the range (chi-square, 15 dof, 0.1 % point)
+    n = (1 << 16) + 3
+    draws = torch.stack([perm_of(n, 1000 + k)[[0, 777, n - 1]] for k in range(400)]).cpu()
+    for c in range(3):
+        cnt = torch.bincount(draws[:, c] * 16 // n, minlength=16).double()
+        assert float(((cnt - 25.0) ** 2 / 25.0).sum()) < 37.7, cnt.tolist()
     n = (1 << 21) + 3
     p = perm_of(n, 99).double()
     i = torch.arange(n, device="cuda", dtype=torch.float64)
