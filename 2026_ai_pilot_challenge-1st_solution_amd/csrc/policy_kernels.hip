@@ -147,8 +147,16 @@ __global__ __launch_bounds__(kThreads, 4) void policy_kernel(const F16PolicyArgs
   // registers for the whole kernel).
   int gi, r0, ge;
   if (p.total_group_rows > 0) {
-    // packed grid (device offsets): the groups' tiles in group order along x
-    int t = blockIdx.x;
+    // packed grid (device offsets): the groups' tiles in group order.  Workgroups go to the 8
+    // XCDs round robin (workgroup i to XCD i % 8), each XCD with its own L2, so workgroup i takes
+    // tile start(i % 8) + i / 8 of a split of the tiles into 8 contiguous runs: each XCD's L2
+    // then holds the weights of one or two of the networks rather than of all of them.
+    int t;
+    {
+      constexpr int kX = 8;
+      const int n = gridDim.x, q = n / kX, rem = n % kX, x = blockIdx.x % kX;
+      t = x * q + min(x, rem) + (int)(blockIdx.x / kX);
+    }
     gi = -1;
     r0 = ge = 0;
     for (int g = 0; g < p.ngroups; ++g) {
