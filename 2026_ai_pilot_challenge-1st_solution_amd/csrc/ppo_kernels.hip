@@ -901,10 +901,16 @@ struct WJob {
   int wld;             // flat row length of W
 };
 
+constexpr int kWMaxWG = 8 * kMaxChunks;   // tiles x chunks (at most 8 tiles)
+
 struct WJobs {
   WJob job[4];
   unsigned char tj[8], ta[8], tb[8];
   int ntiles;
+  // workgroup i computes tile wg[i] >> 6 of chunk wg[i] & 63.  Workgroups go to the 8 XCDs round
+  // robin (i to XCD i % 8): the two tiles that read the same layer-input rows (the two 256-unit
+  // halves of dH1 against X) are placed 8 apart, on one XCD, so the second reads them from its L2.
+  unsigned short wg[kWMaxWG];
 };
 
 static_assert(kWK == kUBlock, "a weight-gradient stage is one 64-row block of each operand");
@@ -914,7 +920,7 @@ __global__ __launch_bounds__(kWThreads, 1) void wgrad_kernel(const WJobs J, long
                                                              long pld) {
   __shared__ __align__(16) __bf16 As[2][kWT * kWPitch];
   __shared__ __align__(16) __bf16 Bs[2][kWT * kWPitch];
-  const int tile = blockIdx.x, c = blockIdx.y;
+  const int tile = J.wg[blockIdx.x] >> 6, c = J.wg[blockIdx.x] & 63;
   const WJob& jb = J.job[J.tj[tile]];
   const int fa0 = kWT * J.ta[tile], fb0 = kWT * J.tb[tile];
   const bool bias = J.tb[tile] == 0;
@@ -1492,8 +1498,32 @@ extern "C" int f16_ppo_grad(const F16PPOArgs* a, void* stream) {
         ++nt;
       }
   J.ntiles = nt;
+  {
+    // tiles 0 and 1 (job 0's A halves, one B) of chunk c at ids 16 (c / 8) + c % 8 and 8 more,
+    // the other tiles' work in the ids left, in tile-major order; where the last pair would not
+    // fit the grid (few chunks), id c nt + t runs tile t of chunk c
+    const int nwg = nt * w.nchunk;
+    const int last = 16 * ((w.nchunk - 1) / 8) + (w.nchunk - 1) % 8 + 8;
+    if (last < nwg) {
+      for (int i = 0; i < nwg; ++i) J.wg[i] = 0xffff;
+      for (int c = 0; c < w.nchunk; ++c) {
+        const int id0 = 16 * (c / 8) + c % 8;
+        J.wg[id0] = (unsigned short)c;
+        J.wg[id0 + 8] = (unsigned short)(64 + c);
+      }
+      int next = 0;
+      for (int t = 2; t < nt; ++t)
+        for (int c = 0; c < w.nchunk; ++c) {
+          while (J.wg[next] != 0xffff) ++next;   // exactly nwg - 2 nchunk free ids remain
+          J.wg[next] = (unsigned short)(t * 64 + c);
+        }
+    } else {
+      for (int c = 0; c < w.nchunk; ++c)
+        for (int t = 0; t < nt; ++t) J.wg[c * nt + t] = (unsigned short)(t * 64 + c);
+    }
+  }
   const long pld = F.n() - 257;          // every flat parameter but the critic's value head
-  hipLaunchKernelGGL(wgrad_kernel, dim3(nt, w.nchunk), dim3(kWThreads), 0, s, J, w.ld,
+  hipLaunchKernelGGL(wgrad_kernel, dim3(nt * w.nchunk), dim3(kWThreads), 0, s, J, w.ld,
                      w.chunk_rows, w.wpart, pld);
   if (pld % 4 == 0 && ((uintptr_t)a->grad & 15) == 0)
     hipLaunchKernelGGL(colsum4_kernel, dim3((unsigned)((pld / 4 + 63) / 64)), dim3(256), 0, s,
