@@ -1612,7 +1612,7 @@ extern "C" int f16_all_finite(const F16FiniteSpan* spans, int nspans, unsigned c
 
 extern "C" int f16_permutation(long long* perm, long n, const unsigned long long* key,
                                void* stream) {
-  if (!perm || !key || n < 1 || n > (1L << 40)) return F16_EINVAL;
+  if (!perm || !key || n < 1 || n > (1L << 31)) return F16_EINVAL;   // the grid's x extent
   int k = 1;
   while ((1L << k) < n) ++k;
   int la, lb;

@@ -131,7 +131,7 @@ int f16_all_finite(const F16FiniteSpan *spans, int nspans, unsigned char *flag, 
  * the 64-bit device word *key -- an eight-round Feistel network (MurmurHash3-finaliser round
  * functions, Philox4x32-10 round keys) with equal halves on the smallest power-of-four domain >= n
  * below 2^15 elements, unequal halves of 8 bits or more on the smallest power of two above,
- * cycle-walked into [0, n).  1 <= n <= 2^40. */
+ * cycle-walked into [0, n).  1 <= n <= 2^31. */
 int f16_permutation(long long *perm, long n, const unsigned long long *key, void *stream);
 
 #ifdef __cplusplus

@@ -397,6 +397,7 @@ def test_permutation_is_a_uniform_shuffle(gpu):
     k = torch.zeros(1, dtype=torch.int64, device="cuda")
     out = torch.empty(4, dtype=torch.int64, device="cuda")
     assert lib.f16_permutation(L.ptr(out), 0, L.ptr(k), h) == L.F16_EINVAL
+    assert lib.f16_permutation(L.ptr(out), (1 << 31) + 1, L.ptr(k), h) == L.F16_EINVAL
     assert lib.f16_permutation(None, 4, L.ptr(k), h) == L.F16_EINVAL
     assert lib.f16_permutation(L.ptr(out), 4, None, h) == L.F16_EINVAL
 
